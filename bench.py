@@ -1,0 +1,160 @@
+"""Decode throughput of the MI355X decode loop on the Llama-3-8B shape.
+
+Workload (default): Llama-3.1-8B-shaped decoder (32 layers, d_model 4096,
+32 query / 8 KV heads of 128, SwiGLU 14336, vocab 128256, RoPE theta 5e5),
+int4 group-32 weights generated on the device from a seed, a 4096-token
+fp16 paged KV context (16-token pages, shuffled block table) of N(0,1)
+values, greedy decode at batch 1.  One step = one decode_step (every
+layer, lm_head and argmax) of every sequence, as one HIP graph launch;
+W untimed warmup steps, then K timed steps, bracketed by device syncs.
+
+Also reported:
+  roofline      the dominant kernel (fused RMSNorm + gate/up int4 GEMV +
+                SwiGLU of one layer) timed with HIP events over back-to-back
+                launches on the library stream; achieved = its algorithmic
+                bytes / average duration, against 8 TB/s HBM peak.
+  attention     the fp16 paged attention kernel of one layer, same method.
+  cpu_baseline  the C oracle (OpenMP) on the host cores, on a bounded
+                sample: one 8B-shaped layer at 4096 context plus 1/8 of the
+                lm_head rows, scaled to a token (32 layers + full lm_head).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+                       [--kv fp16|tq --ctx C] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "nexus-inference-engine-_amd"
+for p in (str(ROOT), str(PKG)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "decode tok/s, Llama-3-8B-shape int4 bs1 ctx4K; GEMV/attn HBM GB/s % of peak"
+PEAK_HBM_GBS = 8000.0
+
+LLAMA8B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336,
+               vocab=128256, n_experts=0, top_k=0, batch=1, kv_kind=0, rope_theta=500000.0,
+               eps=1e-5, seed=0x5EED)
+
+
+def cpu_baseline(ctx_len: int, batch: int, kv_kind: int) -> dict:
+    """Time the oracle's decode step on a bounded sample and scale to a token."""
+    import numpy as np
+
+    import oracle
+    vocab_frac = 8
+    cfg = dict(LLAMA8B, n_layers=1, vocab=LLAMA8B["vocab"] // vocab_frac, batch=batch, kv_kind=kv_kind,
+               max_seq=((ctx_len + 16) // 16 + 1) * 16)
+    m = oracle.Model(**cfg)
+    m.fill_context(ctx_len, 4 if kv_kind else 0)
+    tok = np.zeros(batch, np.int32)
+    m.forward_timed(tok)  # warm caches
+    reps, tl, th = 3, 0.0, 0.0
+    for _ in range(reps):
+        _, a, b = m.forward_timed(tok)
+        tl += a
+        th += b
+    m.close()
+    t_token = LLAMA8B["n_layers"] * tl / reps + vocab_frac * th / reps
+    return {"value": round(batch / t_token, 4), "unit": "tok/s",
+            "cores": int(oracle.lib.nxo_num_threads()), "kind": "port",
+            "sample": (f"oracle decode step of one 8B-shaped layer at ctx {ctx_len} ({reps} reps) "
+                       f"+ lm_head rows 1/{vocab_frac}, scaled to 32 layers + full lm_head")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--kv", choices=["fp16", "tq"], default="fp16")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(--gpus must be 1).", file=sys.stderr)
+        return 2
+
+    import nexus_amd
+
+    kv_kind = 1 if args.kv == "tq" else 0
+    max_seq = ((args.ctx + args.warmup + args.steps + 16) // 16 + 1) * 16
+    cfg = dict(LLAMA8B, batch=args.batch, kv_kind=kv_kind, max_seq=max_seq)
+    ctx = nexus_amd.Context(0)
+    print(f"[bench] device {ctx.device_name()}; building 8B-shaped model "
+          f"(batch {args.batch}, ctx {args.ctx}, kv {args.kv})", file=sys.stderr, flush=True)
+    model = nexus_amd.Model(ctx, **cfg)
+    model.fill_context(args.ctx, 4 if kv_kind else 0)
+    if args.warmup > 0:
+        model.decode_untimed(args.warmup)
+    bytes_start = model.step_bytes()
+    ctx.sync()
+    t0 = time.perf_counter()
+    model.decode_untimed(args.steps)  # launches K step graphs and waits for them
+    ctx.sync()
+    t1 = time.perf_counter()
+    bytes_end = model.step_bytes()
+    elapsed = t1 - t0
+    tok_s = args.steps * args.batch / elapsed
+    step_bytes = 0.5 * (bytes_start + bytes_end)
+    print(f"[bench] {args.steps} steps in {elapsed * 1e3:.2f} ms; {step_bytes / 1e9:.3f} GB/step",
+          file=sys.stderr, flush=True)
+
+    ffn_ms, ffn_bytes = model.time_ffn_gemv(200)
+    att_ms, att_bytes = model.time_attention(200)
+    ffn_gbs = ffn_bytes / (ffn_ms * 1e-3) / 1e9
+    att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
+    model.close()
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4-g32 x fp16 -> fp32 accumulate",
+        "data": "synthetic (seeded device generator; random-init weights)",
+        "config": {
+            "workload": (f"llama-3.1-8b-shape int4-g32 greedy decode, batch {args.batch}, "
+                         f"ctx {args.ctx} {'fp16' if kv_kind == 0 else 'TurboQuant 3.5-bit'} paged KV"),
+            "batch": args.batch, "ctx": args.ctx, "layers": 32, "d_model": 4096, "ffn": 14336,
+            "vocab": 128256, "parallelism": "none (1 GPU)",
+        },
+        "hbm_GBps_end_to_end": round(step_bytes / (elapsed / args.steps) / 1e9, 1),
+        "roofline": {
+            "kernel": "fused RMSNorm + gate/up int4-g32 GEMV + SwiGLU (28672 x 4096)",
+            "bound": "hbm", "achieved": round(ffn_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "avg_us": round(ffn_ms * 1e3, 3), "bytes": int(ffn_bytes),
+        },
+        "attention": {
+            "kernel": "paged decode attention, one layer", "achieved": round(att_gbs, 1),
+            "frac": round(att_gbs / PEAK_HBM_GBS, 4), "avg_us": round(att_ms * 1e3, 3),
+            "bytes": int(att_bytes),
+        },
+        "roofline_end_to_end_frac": round(step_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
+    }
+    if not args.no_cpu:
+        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(args.ctx, args.batch, kv_kind)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

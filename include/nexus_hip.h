@@ -1,0 +1,260 @@
+/*
+ * nexus_hip.h -- C-ABI of the MI355X (gfx950) decode-loop library
+ * libnexus_hip.so.
+ *
+ * This is the drop-in boundary for the NEXUS per-token decode loop.  The
+ * reference's runner calls nexus::compute::ComputeDispatch
+ * (nexus/src/compute/compute_dispatch.h:22-323), which wraps MetalBackend
+ * (nexus/src/compute/metal/metal_backend.h:38-228).  Each entry point below
+ * names the reference member it replaces.
+ *
+ * Conventions (all entry points):
+ *   - return nx_status: NX_OK (0) or an error code; on error nothing is
+ *     zero-filled (the reference writes zeros on failure at
+ *     compute_dispatch.cpp:174-175, :220-223, :273-274; this library never
+ *     does) and nx_last_error() describes the failure;
+ *   - buffers are opaque nx_buf handles (the reference's uint64_t buffer_id,
+ *     metal_backend.h:41) owned by the context; every op checks that each
+ *     buffer exists and is large enough for the shapes given;
+ *   - every op is enqueued asynchronously on the context's one HIP stream, in
+ *     call order; nx_synchronize() / nx_download() wait for it;
+ *   - a context is single-threaded by contract, like the reference's global
+ *     ComputeDispatch (compute_dispatch.cpp:18-27).
+ *
+ * Formats:
+ *   int4-g32 weights: codes [N][Kp/2] bytes (Kp = ceil(K/32)*32), low nibble
+ *     = even k; scales fp16 [N][Kp/32]; value = (q - 8) * scale.  Columns
+ *     k >= K of a ragged last group hold q = 8.
+ *   fp16 paged KV: pools [num_blocks][hkv][16][head_dim] fp16;
+ *     block_table int32 [batch][max_blocks]; position p of sequence b lives
+ *     in block block_table[b][p/16], slot p%16.
+ *   TurboQuant paged KV (head_dim 128): codes4 [num_blocks][hkv][16][32] u8,
+ *     codes3 [num_blocks][hkv][16][24] u8, norms [num_blocks][hkv][16] fp16;
+ *     58 bytes per vector (see nx_tq_encode).
+ */
+#ifndef NEXUS_HIP_H
+#define NEXUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int nx_status;
+#define NX_OK 0
+#define NX_ERR_INVALID 1      /* bad argument, unknown buffer, size mismatch */
+#define NX_ERR_HIP 2          /* HIP runtime error */
+#define NX_ERR_OOM 3          /* device allocation failed */
+#define NX_ERR_UNSUPPORTED 4  /* shape or mode this build does not implement */
+#define NX_ERR_STATE 5        /* call out of order (e.g. token_end without begin) */
+#define NX_ERR_NO_DEVICE 6    /* no usable gfx950 device */
+#define NX_ERR_CAPACITY 7     /* sequence or cache capacity exhausted */
+
+typedef struct nx_ctx nx_ctx;
+typedef uint64_t nx_buf; /* 0 = none */
+
+/* ------------------------------------------------------------ lifecycle -- */
+/* ComputeDispatch::init_gpu (compute_dispatch.h:30, compute_dispatch.cpp:47-71) */
+nx_status nx_init(nx_ctx** out, int device);
+/* ComputeDispatch::~ComputeDispatch; frees every buffer of the context. */
+nx_status nx_destroy(nx_ctx* ctx);
+/* ComputeDispatch::has_gpu (compute_dispatch.h:33): 1 if a gfx950 device is visible. */
+int nx_has_gpu(void);
+/* ComputeDispatch::gpu_name (compute_dispatch.h:36) */
+nx_status nx_device_name(nx_ctx* ctx, char* buf, size_t n);
+/* Message of the last failed call on this context ("" if none). */
+const char* nx_last_error(nx_ctx* ctx);
+/* Message of the last nx_init failure (no context exists then). */
+const char* nx_init_error(void);
+
+/* --------------------------------------------------------------- memory -- */
+/* MetalBackend::alloc_shared_buffer / free_buffer (metal_backend.mm:760-768, :859-864).
+ * Device memory, zero-filled. */
+nx_status nx_alloc(nx_ctx* ctx, size_t bytes, nx_buf* out);
+nx_status nx_free(nx_ctx* ctx, nx_buf buf);
+/* ComputeDispatch::upload_to_gpu (compute_dispatch.h:227); replaces the UMA
+ * memcpy into a shared MTLBuffer (metal_backend.mm:836-850).  Synchronous. */
+nx_status nx_upload(nx_ctx* ctx, nx_buf dst, size_t dst_offset, const void* src, size_t bytes);
+/* ComputeDispatch::download_from_gpu (compute_dispatch.h:231); waits for the stream. */
+nx_status nx_download(nx_ctx* ctx, void* dst, nx_buf src, size_t src_offset, size_t bytes);
+/* The wrapped-pointer weight cache keyed by host pointer
+ * (compute_dispatch.h:311, compute_dispatch.cpp:148-154) and
+ * upload_small_buffer (compute_dispatch.h:117): the first call uploads
+ * `bytes` from `src` into a new device buffer remembered under `host_key`;
+ * later calls with the same key return that buffer without copying. */
+nx_status nx_weight_cache(nx_ctx* ctx, const void* host_key, const void* src, size_t bytes,
+                          nx_buf* out);
+/* ComputeDispatch::get_cached_buffer (compute_dispatch.h:299); NX_ERR_INVALID if absent. */
+nx_status nx_get_cached_buffer(nx_ctx* ctx, const void* host_key, nx_buf* out);
+/* ComputeDispatch::clear_buffer_cache (compute_dispatch.h:296): frees cached weights. */
+nx_status nx_clear_buffer_cache(nx_ctx* ctx);
+/* Size in bytes of a buffer of this context. */
+nx_status nx_buffer_size(nx_ctx* ctx, nx_buf buf, size_t* bytes);
+/* Wait for all work enqueued on the context's stream. */
+nx_status nx_synchronize(nx_ctx* ctx);
+
+/* ------------------------------------------------------------- batching -- */
+/* ComputeDispatch::begin_token / end_token (compute_dispatch.h:96-102,
+ * compute_dispatch.cpp:798-833).  Ops between the two are captured into one
+ * HIP graph; end_token launches it and waits.  When the captured sequence
+ * has the same shape as the previous token's, the instantiated graph is
+ * updated in place instead of re-instantiated. */
+nx_status nx_token_begin(nx_ctx* ctx);
+nx_status nx_token_end(nx_ctx* ctx);
+
+/* ------------------------------------------------------------------ ops -- */
+/* int4-g32 GEMV: y[b][n] = sum_k x[b][k] * (q[n][k] - 8) * s[n][k/32], fp32
+ * accumulation, y stored fp16.  x fp16 [batch][K].  batch 1..8.
+ * Replaces ComputeDispatch::gemm_int4 (compute_dispatch.h:57,
+ * compute_dispatch.cpp:142-176) -> MetalBackend::gemv_int4_nr8
+ * (metal_backend.mm:607-642), and gemv_int4 (compute_dispatch.h:48) whose
+ * grouped semantics it follows. */
+nx_status nx_gemv_int4_g32(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16,
+                           nx_buf y_f16, int N, int K, int batch);
+/* Same product with fp32 output; accumulate != 0 adds into y (the residual
+ * add of hybrid_model.cpp:1397-1400 fused).  Replaces gemm_int4_gpu
+ * (compute_dispatch.h:214) + gpu_residual_add (compute_dispatch.h:247). */
+nx_status nx_gemv_int4_g32_f32(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16,
+                               nx_buf y_f32, int N, int K, int batch, int accumulate);
+/* Unpack n int4 codes (low nibble first) to one byte each -- the bit-exact
+ * check hook for the GPU unpack (quant::dequant_int4, gptq.cpp:12-25). */
+nx_status nx_unpack_int4(nx_ctx* ctx, nx_buf packed, nx_buf codes_u8, size_t n);
+/* Device symmetric int4-g32 quantizer of w fp32 [N][K]: s = fp16(amax/7),
+ * q = clamp(roundf(w/s), -8, 7) + 8.  (Replaces the offline quant_int4,
+ * gptq.cpp:37-70, whose asymmetric output the GPU kernels never consumed.) */
+nx_status nx_quantize_int4_g32(nx_ctx* ctx, nx_buf w_f32, nx_buf wq, nx_buf scales_f16, int N,
+                               int K);
+/* RMSNorm: out = fp16((x * 1/sqrt(mean(x^2) + eps)) * w), x fp32 [batch][dim];
+ * w fp32 [dim] or 0 for ones.  ComputeDispatch::rmsnorm / gpu_rmsnorm
+ * (compute_dispatch.h:63, :241; compute::rms_norm gemm.cpp:96-114). */
+nx_status nx_rmsnorm(nx_ctx* ctx, nx_buf x_f32, nx_buf w_f32, nx_buf out_f16, int dim, float eps,
+                     int batch);
+/* RoPE in place on x fp32 [batch][heads][head_dim]: interleaved pairs,
+ * angle pos*theta^(-2i/hd) from the cos/sin tables fp32 [max_pos][hd/2].
+ * The reference has none (transformer.cpp:255). */
+nx_status nx_rope(nx_ctx* ctx, nx_buf x_f32, nx_buf positions_i32, nx_buf cos_tab, nx_buf sin_tab,
+                  int heads, int head_dim, int batch, int max_pos);
+/* SwiGLU: out = fp16(g / (1 + exp(-g)) * u), fp32 inputs [batch][n].
+ * ComputeDispatch::swiglu / gpu_swiglu (compute_dispatch.h:69, :236). */
+nx_status nx_swiglu(nx_ctx* ctx, nx_buf gate_f32, nx_buf up_f32, nx_buf out_f16, int n, int batch);
+/* out = a + b, fp32 [n].  ComputeDispatch::gpu_residual_add (compute_dispatch.h:247). */
+nx_status nx_residual_add(nx_ctx* ctx, nx_buf a, nx_buf b, nx_buf out, int n);
+/* Append one token's K/V (fp32 [batch][hkv][head_dim], converted to fp16
+ * round-to-nearest-even) at positions[b] through the block table.  The
+ * cache write of MetalBackend::attention_gpu (attention_gpu.metal:40-64) and
+ * of gqa_attention (hybrid_model.cpp:1460-1468, which truncates instead). */
+nx_status nx_kv_append_f16(nx_ctx* ctx, nx_buf k_f32, nx_buf v_f32, nx_buf kpool, nx_buf vpool,
+                           nx_buf block_table, nx_buf positions_i32, int batch, int hkv,
+                           int head_dim, int max_blocks, int num_blocks);
+/* Paged fp16 decode attention: out[b][h] = softmax(q.K^T / sqrt(hd)) V over
+ * positions [0, ctx_lens[b]), GQA kv head = h / (hq/hkv); q fp32
+ * [batch][hq][hd]; out fp16 [batch][hq][hd].  Replaces
+ * ComputeDispatch::attention_gpu / fused_attention (compute_dispatch.h:190,
+ * :198) and the CPU gqa_attention (hybrid_model.cpp:1447-1565). */
+nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q_f32, nx_buf kpool, nx_buf vpool,
+                                   nx_buf block_table, nx_buf ctx_lens_i32, nx_buf out_f16,
+                                   int batch, int hq, int hkv, int head_dim, int max_blocks,
+                                   int num_blocks);
+/* TurboQuant codebooks (Lloyd-Max for N(0,1/128), kv/turbo_quant.cpp:172-219)
+ * as computed by this library on the host: c4[16], b4[15], c3[8], b3[7]. */
+nx_status nx_tq_codebooks(float* c4, float* b4, float* c3, float* b3);
+/* TurboQuant encode of nvec vectors x fp32 [nvec][128]:
+ *   n = sqrt(canonical sum of squares); u = (sign .* x) * (1/n);
+ *   y = FWHT128(u) * float(1/sqrt(128)); code_i = first j with y_i < b[j]
+ *   (4-bit codebook for i < 64, 3-bit for i >= 64); codes packed LSB-first
+ *   (kv/turbo_quant.cpp:249-268); norm stored fp16.
+ * signs fp32 [128] of +-1.  Replaces TurboQuantKV::quantize
+ * (kv/turbo_quant.cpp:289-327) with a randomized Hadamard rotation. */
+nx_status nx_tq_encode(nx_ctx* ctx, nx_buf x_f32, nx_buf signs_f32, nx_buf codes4, nx_buf codes3,
+                       nx_buf norms_f16, int nvec);
+/* Append one token's K/V (fp32 [batch][hkv][128]) to TurboQuant pages. */
+nx_status nx_tq_append(nx_ctx* ctx, nx_buf k_f32, nx_buf v_f32, nx_buf ksigns, nx_buf vsigns,
+                       nx_buf kc4, nx_buf kc3, nx_buf kn, nx_buf vc4, nx_buf vc3, nx_buf vn,
+                       nx_buf block_table, nx_buf positions_i32, int batch, int hkv,
+                       int max_blocks, int num_blocks);
+/* Decode attention over TurboQuant pages (head_dim 128), scored in the
+ * rotated domain: score = n_t * <Pi q, c[code_t]> / sqrt(128), V summed in
+ * the rotated domain and rotated back once.  out fp16 [batch][hq][128]. */
+nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q_f32, nx_buf kc4, nx_buf kc3, nx_buf kn,
+                                  nx_buf vc4, nx_buf vc3, nx_buf vn, nx_buf ksigns, nx_buf vsigns,
+                                  nx_buf block_table, nx_buf ctx_lens_i32, nx_buf out_f16,
+                                  int batch, int hq, int hkv, int max_blocks, int num_blocks);
+/* MoE routing: softmax over E logits fp32 [batch][E], top-k by probability
+ * (ties: lower id), renormalized weights.  hybrid_model.cpp:1656-1694. */
+nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits_f32, nx_buf ids_i32, nx_buf weights_f32,
+                            int E, int k, int batch);
+/* Expert SwiGLU FFN for routed tokens: out[b] (+)= sum_j w[b][j] *
+ * W2_e(fp16(silu(W1_e x) * W3_e x)), e = ids[b][j].  Expert weights are
+ * int4-g32: w13 [E][2F][d] with gate/up rows interleaved (row 2f = gate f,
+ * 2f+1 = up f), s13 its scales; w2 [E][d][F], s2.  x fp16 [batch][d].
+ * ComputeDispatch::batched_moe_ffn (compute_dispatch.h:81,
+ * compute_dispatch.cpp:211-275; batched_expert_gemv.metal:47-160). */
+nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, nx_buf w2,
+                            nx_buf s2, nx_buf ids_i32, nx_buf weights_f32, nx_buf out_f32, int d,
+                            int F, int E, int k, int batch, int accumulate);
+/* Greedy sampling: first maximum of logits fp32 [batch][V]
+ * (hybrid_model.cpp:2027-2038). */
+nx_status nx_argmax(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int batch);
+
+/* ----------------------------------------------------------- the runner -- */
+/* A resident decoder driven by this library: the counterpart of
+ * HybridModel (hybrid_model.h, hybrid_model.cpp:319-774) for Llama-style
+ * dense and MoE models, with synthetic int4-g32 weights generated on the
+ * device from a seed (counter-based RNG shared with the test oracle). */
+typedef struct {
+    int n_layers, d_model, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    int n_experts, top_k;   /* n_experts == 0: dense SwiGLU */
+    int max_seq;            /* per sequence, multiple of 16 */
+    int batch;              /* sequences decoded together (1..8) */
+    int kv_kind;            /* 0 = fp16 pages, 1 = TurboQuant pages (head_dim 128) */
+    float rope_theta;
+    float eps;
+    uint64_t seed;
+} nx_model_config;
+
+typedef struct nx_model nx_model;
+
+/* HybridModel::create (hybrid_model.cpp:319-600): allocate and generate weights. */
+nx_status nx_model_create(nx_ctx* ctx, const nx_model_config* cfg, nx_model** out);
+nx_status nx_model_destroy(nx_model* m);
+/* HybridModel::prefill (hybrid_model.cpp:604-644): run prompt [batch][P]
+ * token by token; afterwards the greedy token of the last prompt position is
+ * pending as the next input and written to next_tokens [batch] (optional). */
+nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens);
+/* Fill positions [0, ctx) of every layer's cache with synthetic N(0,1) K/V
+ * (n_outlier channels per head scaled x10); the pending token of every
+ * sequence becomes a seeded start token. */
+nx_status nx_model_fill_context(nx_model* m, int ctx, int n_outlier);
+/* The pending (next input) token of every sequence, [batch]. */
+nx_status nx_model_pending(nx_model* m, int32_t* tokens);
+/* Engine::generate's loop (engine.cpp:155-173) of `steps` decode_step calls
+ * (hybrid_model.cpp:648-774) with the sampled token fed back: out_tokens
+ * [batch][steps] receives the greedy token produced by each step.  The
+ * whole step is one HIP graph launch; nothing is copied to the host between
+ * steps. */
+nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens);
+/* Logits fp32 [batch][V] of the last step. */
+nx_status nx_model_logits(nx_model* m, float* out);
+/* Current position of sequence b. */
+nx_status nx_model_position(nx_model* m, int b, int* pos);
+/* Algorithmic HBM bytes of one decode step at the current positions. */
+nx_status nx_model_step_bytes(nx_model* m, double* bytes);
+
+/* ---------------------------------------------------------- measurement -- */
+/* Average device duration (ms) of the dominant decode kernel -- the fused
+ * RMSNorm + gate/up int4 GEMV + SwiGLU of layer 0 -- over `iters`
+ * back-to-back launches on the model's buffers, timed with HIP events on the
+ * library stream; bytes = its algorithmic bytes per launch. */
+nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double* bytes);
+/* Same for a standalone nx_gemv_int4_g32 launch of shape N x K, batch. */
+nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16, nx_buf y_f16,
+                       int N, int K, int batch, int iters, double* avg_ms);
+/* Same for nx_attn_decode_paged_f16 (and _tq when kind = 1) with the given buffers. */
+nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

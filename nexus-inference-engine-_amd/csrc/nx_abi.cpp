@@ -1,0 +1,738 @@
+// C-ABI of the decode-loop library: context, buffer registry, weight cache,
+// token-level HIP graphs and the validated op entry points.  Every entry
+// point checks its buffers and shapes on the host before enqueueing a
+// kernel, and reports errors as status codes (never zero-filled outputs).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "nx_common.h"
+#include "nx_internal.h"
+#include "nx_kernels.h"
+
+using nx::fail;
+
+namespace {
+thread_local std::string g_init_error;
+
+bool device_is_gfx950(int dev) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return false;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+nx_status ensure_attn_ws(nx_ctx* ctx, size_t bytes, size_t ncounters) {
+    if (bytes <= ctx->attn_ws_bytes && ncounters <= ctx->attn_ncounters) return NX_OK;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "attention workspace must grow outside capture");
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (bytes > ctx->attn_ws_bytes) {
+        if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+        ctx->attn_ws = nullptr;
+        ctx->attn_ws_bytes = 0;
+        NX_HIP(ctx, hipMalloc(&ctx->attn_ws, bytes));
+        ctx->attn_ws_bytes = bytes;
+    }
+    if (ncounters > ctx->attn_ncounters) {
+        if (ctx->attn_counters) (void)hipFree(ctx->attn_counters);
+        ctx->attn_counters = nullptr;
+        ctx->attn_ncounters = 0;
+        NX_HIP(ctx, hipMalloc(&ctx->attn_counters, ncounters * sizeof(unsigned int)));
+        NX_HIP(ctx, hipMemset(ctx->attn_counters, 0, ncounters * sizeof(unsigned int)));
+        ctx->attn_ncounters = ncounters;
+    }
+    return NX_OK;
+}
+
+template <class T>
+T* dptr(nx_buf b) {
+    return reinterpret_cast<T*>(static_cast<uintptr_t>(b));
+}
+
+nx_status launched(nx_ctx* ctx, hipError_t e, const char* what) {
+    if (e != hipSuccess) return nx::hip_fail(ctx, e, what);
+    return NX_OK;
+}
+}  // namespace
+
+// ---------------------------------------------------------------- codebook --
+namespace nx {
+static float cb_normal_pdf(float x, float sigma) {
+    const float z = x / sigma;
+    return std::exp(-0.5f * z * z) / (sigma * std::sqrt(2.0f * static_cast<float>(M_PI)));
+}
+static float cb_normal_cdf(float x, float sigma) {
+    const float z = x / sigma;
+    return 0.5f * std::erfc(-z * static_cast<float>(M_SQRT1_2));
+}
+static float cb_conditional_mean(float a, float b, float sigma) {
+    const float pa = cb_normal_pdf(a, sigma), pb = cb_normal_pdf(b, sigma);
+    const float ca = cb_normal_cdf(a, sigma), cb = cb_normal_cdf(b, sigma);
+    const float denom = cb - ca;
+    if (denom < 1e-12f) return 0.5f * (a + b);
+    return sigma * sigma * (pa - pb) / denom;
+}
+void tq_codebook(int d, int bits, float* c, float* bnd) {
+    const int n = 1 << bits;
+    const float sigma = 1.0f / std::sqrt(static_cast<float>(d));
+    const float lo = -3.0f * sigma, hi = 3.0f * sigma;
+    for (int i = 0; i < n; ++i) c[i] = lo + (hi - lo) * (i + 0.5f) / n;
+    for (int iter = 0; iter < 100; ++iter) {
+        for (int i = 0; i < n - 1; ++i) bnd[i] = 0.5f * (c[i] + c[i + 1]);
+        float max_delta = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const float a = (i == 0) ? -10.0f * sigma : bnd[i - 1];
+            const float b = (i == n - 1) ? 10.0f * sigma : bnd[i];
+            const float nc = cb_conditional_mean(a, b, sigma);
+            const float delta = std::fabs(nc - c[i]);
+            if (delta > max_delta) max_delta = delta;
+            c[i] = nc;
+        }
+        if (max_delta < 1e-7f * sigma) break;
+    }
+    for (int i = 0; i < n - 1; ++i) bnd[i] = 0.5f * (c[i] + c[i + 1]);
+}
+}  // namespace nx
+
+extern "C" {
+
+// ---------------------------------------------------------------- lifecycle --
+int nx_has_gpu(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    for (int i = 0; i < n; ++i)
+        if (device_is_gfx950(i)) return 1;
+    return 0;
+}
+
+const char* nx_init_error(void) { return g_init_error.c_str(); }
+
+nx_status nx_init(nx_ctx** out, int device) {
+    if (!out) return NX_ERR_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) {
+        g_init_error = "no HIP device " + std::to_string(device);
+        return NX_ERR_NO_DEVICE;
+    }
+    if (!device_is_gfx950(device)) {
+        g_init_error = "device is not gfx950";
+        return NX_ERR_NO_DEVICE;
+    }
+    if (hipSetDevice(device) != hipSuccess) {
+        g_init_error = "hipSetDevice failed";
+        return NX_ERR_HIP;
+    }
+    nx_ctx* ctx = new nx_ctx();
+    ctx->device = device;
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess) {
+        g_init_error = "stream/event creation failed";
+        delete ctx;
+        return NX_ERR_HIP;
+    }
+    nx::tq_codebook(128, 4, ctx->c4, ctx->b4);
+    nx::tq_codebook(128, 3, ctx->c3, ctx->b3);
+    nx::tq_set_codebooks(ctx->c4, ctx->b4, ctx->c3, ctx->b3);
+    if (hipDeviceSynchronize() != hipSuccess) {
+        g_init_error = "device synchronize failed";
+        delete ctx;
+        return NX_ERR_HIP;
+    }
+    *out = ctx;
+    return NX_OK;
+}
+
+nx_status nx_destroy(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->token_exec) (void)hipGraphExecDestroy(ctx->token_exec);
+    for (auto& kv : ctx->bufs) (void)hipFree(reinterpret_cast<void*>(kv.first));
+    if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+    if (ctx->attn_counters) (void)hipFree(ctx->attn_counters);
+    (void)hipEventDestroy(ctx->ev0);
+    (void)hipEventDestroy(ctx->ev1);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return NX_OK;
+}
+
+nx_status nx_device_name(nx_ctx* ctx, char* buf, size_t n) {
+    if (!ctx || !buf || n == 0) return NX_ERR_INVALID;
+    hipDeviceProp_t p;
+    NX_HIP(ctx, hipGetDeviceProperties(&p, ctx->device));
+    std::snprintf(buf, n, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return NX_OK;
+}
+
+const char* nx_last_error(nx_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+// ------------------------------------------------------------------- memory --
+nx_status nx_alloc(nx_ctx* ctx, size_t bytes, nx_buf* out) {
+    if (!ctx || !out) return NX_ERR_INVALID;
+    if (bytes == 0) return fail(ctx, NX_ERR_INVALID, "nx_alloc: zero bytes");
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_alloc inside a token batch");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return nx::hip_fail(ctx, e, "hipMalloc");
+    e = hipMemsetAsync(p, 0, bytes, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return nx::hip_fail(ctx, e, "hipMemsetAsync");
+    }
+    ctx->bufs[reinterpret_cast<uint64_t>(p)] = bytes;
+    *out = reinterpret_cast<uint64_t>(p);
+    return NX_OK;
+}
+
+nx_status nx_free(nx_ctx* ctx, nx_buf b) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_free inside a token batch");
+    auto it = ctx->bufs.find(b);
+    if (it == ctx->bufs.end()) return fail(ctx, NX_ERR_INVALID, "nx_free: unknown buffer");
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    NX_HIP(ctx, hipFree(reinterpret_cast<void*>(b)));
+    ctx->bufs.erase(it);
+    for (auto w = ctx->wcache.begin(); w != ctx->wcache.end();)
+        w = (w->second == b) ? ctx->wcache.erase(w) : std::next(w);
+    return NX_OK;
+}
+
+nx_status nx_buffer_size(nx_ctx* ctx, nx_buf b, size_t* bytes) {
+    if (!ctx || !bytes) return NX_ERR_INVALID;
+    *bytes = nx::buf_size(ctx, b);
+    return *bytes ? NX_OK : fail(ctx, NX_ERR_INVALID, "unknown buffer");
+}
+
+nx_status nx_upload(nx_ctx* ctx, nx_buf dst, size_t off, const void* src, size_t bytes) {
+    if (!ctx || (!src && bytes)) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_upload inside a token batch");
+    NX_NEED(ctx, dst, off + bytes, "nx_upload dst");
+    if (bytes == 0) return NX_OK;
+    NX_HIP(ctx, hipMemcpyAsync(dptr<char>(dst) + off, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return NX_OK;
+}
+
+nx_status nx_download(nx_ctx* ctx, void* dst, nx_buf src, size_t off, size_t bytes) {
+    if (!ctx || (!dst && bytes)) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_download inside a token batch");
+    NX_NEED(ctx, src, off + bytes, "nx_download src");
+    if (bytes == 0) return NX_OK;
+    NX_HIP(ctx, hipMemcpyAsync(dst, dptr<char>(src) + off, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return NX_OK;
+}
+
+nx_status nx_weight_cache(nx_ctx* ctx, const void* key, const void* src, size_t bytes, nx_buf* out) {
+    if (!ctx || !key || !out) return NX_ERR_INVALID;
+    auto it = ctx->wcache.find(key);
+    if (it != ctx->wcache.end()) {
+        if (nx::buf_size(ctx, it->second) < bytes)
+            return fail(ctx, NX_ERR_INVALID, "nx_weight_cache: cached buffer smaller than request");
+        *out = it->second;
+        return NX_OK;
+    }
+    nx_buf b = 0;
+    nx_status s = nx_alloc(ctx, bytes, &b);
+    if (s != NX_OK) return s;
+    s = nx_upload(ctx, b, 0, src, bytes);
+    if (s != NX_OK) {
+        (void)nx_free(ctx, b);
+        return s;
+    }
+    ctx->wcache[key] = b;
+    *out = b;
+    return NX_OK;
+}
+
+nx_status nx_get_cached_buffer(nx_ctx* ctx, const void* key, nx_buf* out) {
+    if (!ctx || !out) return NX_ERR_INVALID;
+    auto it = ctx->wcache.find(key);
+    if (it == ctx->wcache.end()) return fail(ctx, NX_ERR_INVALID, "no cached buffer for key");
+    *out = it->second;
+    return NX_OK;
+}
+
+nx_status nx_clear_buffer_cache(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    std::vector<nx_buf> bs;
+    for (auto& kv : ctx->wcache) bs.push_back(kv.second);
+    ctx->wcache.clear();
+    for (nx_buf b : bs) {
+        nx_status s = nx_free(ctx, b);
+        if (s != NX_OK) return s;
+    }
+    return NX_OK;
+}
+
+nx_status nx_synchronize(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return NX_OK;
+}
+
+// ----------------------------------------------------------------- batching --
+nx_status nx_token_begin(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "token batch already open");
+    NX_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return NX_OK;
+}
+
+nx_status nx_token_end(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (!ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_token_end without nx_token_begin");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    NX_HIP(ctx, hipStreamEndCapture(ctx->stream, &g));
+    bool ok = false;
+    if (ctx->token_exec) {
+        hipGraphNode_t err_node = nullptr;
+        hipGraphExecUpdateResult res;
+        if (hipGraphExecUpdate(ctx->token_exec, g, &err_node, &res) == hipSuccess &&
+            res == hipGraphExecUpdateSuccess)
+            ok = true;
+        else {
+            (void)hipGetLastError();
+            (void)hipGraphExecDestroy(ctx->token_exec);
+            ctx->token_exec = nullptr;
+        }
+    }
+    if (!ok) {
+        hipError_t e = hipGraphInstantiate(&ctx->token_exec, g, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            ctx->token_exec = nullptr;
+            return nx::hip_fail(ctx, e, "hipGraphInstantiate");
+        }
+    }
+    (void)hipGraphDestroy(g);
+    NX_HIP(ctx, hipGraphLaunch(ctx->token_exec, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return NX_OK;
+}
+
+// ---------------------------------------------------------------------- ops --
+static nx_status gemv_common(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
+                             int batch, int out_bytes, const char* name, nx::GemvArgs& a) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (N <= 0 || K <= 0 || batch < 1 || batch > 8)
+        return fail(ctx, NX_ERR_INVALID, "%s: bad shape N=%d K=%d batch=%d", name, N, K, batch);
+    const int G = (K + 31) / 32;
+    if (G > 7 * 64) return fail(ctx, NX_ERR_UNSUPPORTED, "%s: K=%d above 14336", name, K);
+    NX_NEED(ctx, x, (size_t)batch * K * 2, "x");
+    NX_NEED(ctx, wq, (size_t)N * G * 16, "weights");
+    NX_NEED(ctx, sc, (size_t)N * G * 2, "scales");
+    NX_NEED(ctx, y, (size_t)batch * N * out_bytes, "y");
+    a = nx::GemvArgs{};
+    a.W = dptr<const uint8_t>(wq);
+    a.S = dptr<const uint16_t>(sc);
+    a.N = N;
+    a.K = K;
+    a.G = G;
+    a.batch = batch;
+    a.x16 = dptr<const uint16_t>(x);
+    a.ldx = K;
+    a.ldy = N;
+    return NX_OK;
+}
+
+nx_status nx_gemv_int4_g32(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
+                           int batch) {
+    nx::GemvArgs a;
+    nx_status s = gemv_common(ctx, x, wq, sc, y, N, K, batch, 2, "nx_gemv_int4_g32", a);
+    if (s != NX_OK) return s;
+    a.y16 = dptr<uint16_t>(y);
+    return launched(ctx, nx::gemv_launch(nx::X_F16, nx::E_F16, a, ctx->stream), "gemv");
+}
+
+nx_status nx_gemv_int4_g32_f32(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
+                               int batch, int accumulate) {
+    nx::GemvArgs a;
+    nx_status s = gemv_common(ctx, x, wq, sc, y, N, K, batch, 4, "nx_gemv_int4_g32_f32", a);
+    if (s != NX_OK) return s;
+    a.y32 = dptr<float>(y);
+    return launched(ctx, nx::gemv_launch(nx::X_F16, accumulate ? nx::E_ACC : nx::E_F32, a, ctx->stream),
+                    "gemv");
+}
+
+nx_status nx_unpack_int4(nx_ctx* ctx, nx_buf packed, nx_buf codes, size_t n) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (n % 2) return fail(ctx, NX_ERR_INVALID, "nx_unpack_int4: n must be even");
+    NX_NEED(ctx, packed, n / 2, "packed");
+    NX_NEED(ctx, codes, n, "codes");
+    return launched(ctx, nx::unpack_int4_launch(dptr<const uint8_t>(packed), dptr<uint8_t>(codes), n, ctx->stream),
+                    "unpack");
+}
+
+nx_status nx_quantize_int4_g32(nx_ctx* ctx, nx_buf w, nx_buf wq, nx_buf sc, int N, int K) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (N <= 0 || K <= 0) return fail(ctx, NX_ERR_INVALID, "nx_quantize_int4_g32: bad shape");
+    const int G = (K + 31) / 32;
+    NX_NEED(ctx, w, (size_t)N * K * 4, "w");
+    NX_NEED(ctx, wq, (size_t)N * G * 16, "codes");
+    NX_NEED(ctx, sc, (size_t)N * G * 2, "scales");
+    return launched(ctx, nx::quantize_int4_launch(dptr<const float>(w), dptr<uint8_t>(wq), dptr<uint16_t>(sc), N, K, ctx->stream),
+                    "quantize");
+}
+
+nx_status nx_rmsnorm(nx_ctx* ctx, nx_buf x, nx_buf w, nx_buf out, int dim, float eps, int batch) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (dim <= 0 || batch < 1) return fail(ctx, NX_ERR_INVALID, "nx_rmsnorm: bad shape");
+    NX_NEED(ctx, x, (size_t)batch * dim * 4, "x");
+    if (w) NX_NEED(ctx, w, (size_t)dim * 4, "w");
+    NX_NEED(ctx, out, (size_t)batch * dim * 2, "out");
+    return launched(ctx, nx::rmsnorm_launch(dptr<const float>(x), w ? dptr<const float>(w) : nullptr,
+                                            dptr<uint16_t>(out), dim, eps, batch, ctx->stream),
+                    "rmsnorm");
+}
+
+nx_status nx_rope(nx_ctx* ctx, nx_buf x, nx_buf pos, nx_buf cs, nx_buf sn, int heads, int hd,
+                  int batch, int max_pos) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (heads <= 0 || hd <= 0 || hd % 2 || batch < 1 || max_pos <= 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_rope: bad shape");
+    NX_NEED(ctx, x, (size_t)batch * heads * hd * 4, "x");
+    NX_NEED(ctx, pos, (size_t)batch * 4, "positions");
+    NX_NEED(ctx, cs, (size_t)max_pos * (hd / 2) * 4, "cos");
+    NX_NEED(ctx, sn, (size_t)max_pos * (hd / 2) * 4, "sin");
+    std::vector<int32_t> hp(batch);
+    // positions are validated against the tables on the host
+    NX_HIP(ctx, hipMemcpyAsync(hp.data(), dptr<void>(pos), (size_t)batch * 4, hipMemcpyDeviceToHost, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int b = 0; b < batch; ++b)
+        if (hp[b] < 0 || hp[b] >= max_pos) return fail(ctx, NX_ERR_INVALID, "nx_rope: position %d out of table", hp[b]);
+    return launched(ctx, nx::rope_launch(dptr<float>(x), dptr<const int32_t>(pos), dptr<const float>(cs),
+                                         dptr<const float>(sn), heads, hd, batch, ctx->stream),
+                    "rope");
+}
+
+nx_status nx_swiglu(nx_ctx* ctx, nx_buf g, nx_buf u, nx_buf out, int n, int batch) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (n <= 0 || batch < 1) return fail(ctx, NX_ERR_INVALID, "nx_swiglu: bad shape");
+    NX_NEED(ctx, g, (size_t)batch * n * 4, "gate");
+    NX_NEED(ctx, u, (size_t)batch * n * 4, "up");
+    NX_NEED(ctx, out, (size_t)batch * n * 2, "out");
+    return launched(ctx, nx::swiglu_launch(dptr<const float>(g), dptr<const float>(u), dptr<uint16_t>(out), n, batch, ctx->stream),
+                    "swiglu");
+}
+
+nx_status nx_residual_add(nx_ctx* ctx, nx_buf a, nx_buf b, nx_buf out, int n) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (n <= 0) return fail(ctx, NX_ERR_INVALID, "nx_residual_add: bad shape");
+    NX_NEED(ctx, a, (size_t)n * 4, "a");
+    NX_NEED(ctx, b, (size_t)n * 4, "b");
+    NX_NEED(ctx, out, (size_t)n * 4, "out");
+    return launched(ctx, nx::residual_add_launch(dptr<const float>(a), dptr<const float>(b), dptr<float>(out), n, ctx->stream),
+                    "residual_add");
+}
+
+// Host-side validation of a block table and per-sequence positions.
+static nx_status check_table(nx_ctx* ctx, nx_buf bt, nx_buf lens, int batch, int max_blocks,
+                             int num_blocks, bool lens_are_positions, const char* name) {
+    NX_NEED(ctx, bt, (size_t)batch * max_blocks * 4, "block_table");
+    NX_NEED(ctx, lens, (size_t)batch * 4, lens_are_positions ? "positions" : "ctx_lens");
+    std::vector<int32_t> t((size_t)batch * max_blocks), l(batch);
+    NX_HIP(ctx, hipMemcpyAsync(t.data(), dptr<void>(bt), t.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    NX_HIP(ctx, hipMemcpyAsync(l.data(), dptr<void>(lens), l.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int b = 0; b < batch; ++b) {
+        const int len = lens_are_positions ? l[b] + 1 : l[b];
+        if (len < 0 || len > max_blocks * nx::kPage)
+            return fail(ctx, NX_ERR_CAPACITY, "%s: sequence %d length %d exceeds %d", name, b, len, max_blocks * nx::kPage);
+        for (int p = 0; p < (len + nx::kPage - 1) / nx::kPage; ++p) {
+            const int blk = t[(size_t)b * max_blocks + p];
+            if (blk < 0 || blk >= num_blocks)
+                return fail(ctx, NX_ERR_INVALID, "%s: block %d of sequence %d out of pool", name, blk, b);
+        }
+    }
+    return NX_OK;
+}
+
+nx_status nx_kv_append_f16(nx_ctx* ctx, nx_buf k, nx_buf v, nx_buf kpool, nx_buf vpool, nx_buf bt,
+                           nx_buf pos, int batch, int hkv, int hd, int max_blocks, int num_blocks) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_kv_append_f16 validates positions on the host; not capturable");
+    if (batch < 1 || hkv <= 0 || hd <= 0 || max_blocks <= 0 || num_blocks <= 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_kv_append_f16: bad shape");
+    NX_NEED(ctx, k, (size_t)batch * hkv * hd * 4, "k");
+    NX_NEED(ctx, v, (size_t)batch * hkv * hd * 4, "v");
+    const size_t pool = (size_t)num_blocks * hkv * nx::kPage * hd * 2;
+    NX_NEED(ctx, kpool, pool, "kpool");
+    NX_NEED(ctx, vpool, pool, "vpool");
+    nx_status s = check_table(ctx, bt, pos, batch, max_blocks, num_blocks, true, "nx_kv_append_f16");
+    if (s != NX_OK) return s;
+    return launched(ctx, nx::kv_append_f16_launch(dptr<const float>(k), dptr<const float>(v), dptr<uint16_t>(kpool),
+                                                  dptr<uint16_t>(vpool), dptr<const int32_t>(bt), dptr<const int32_t>(pos),
+                                                  batch, hkv, hd, max_blocks, ctx->stream),
+                    "kv_append");
+}
+
+nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf vpool, nx_buf bt,
+                                   nx_buf lens, nx_buf out, int batch, int hq, int hkv, int hd,
+                                   int max_blocks, int num_blocks) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_attn_decode_paged_f16 validates the block table on the host; not capturable");
+    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || (hd != 64 && hd != 128) || max_blocks <= 0 ||
+        num_blocks <= 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_attn_decode_paged_f16: bad shape");
+    const int G = hq / hkv;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "nx_attn_decode_paged_f16: hq/hkv = %d", G);
+    NX_NEED(ctx, q, (size_t)batch * hq * hd * 4, "q");
+    const size_t pool = (size_t)num_blocks * hkv * nx::kPage * hd * 2;
+    NX_NEED(ctx, kpool, pool, "kpool");
+    NX_NEED(ctx, vpool, pool, "vpool");
+    NX_NEED(ctx, out, (size_t)batch * hq * hd * 2, "out");
+    nx_status s = check_table(ctx, bt, lens, batch, max_blocks, num_blocks, false, "nx_attn_decode_paged_f16");
+    if (s != NX_OK) return s;
+    const int max_ctx = max_blocks * nx::kPage;
+    s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, hd, max_ctx),
+                       nx::attn_counter_count(batch, hkv));
+    if (s != NX_OK) return s;
+    nx::AttnArgs a{};
+    a.q = dptr<const float>(q);
+    a.kpool = dptr<const uint16_t>(kpool);
+    a.vpool = dptr<const uint16_t>(vpool);
+    a.block_table = dptr<const int32_t>(bt);
+    a.ctx_lens = dptr<const int32_t>(lens);
+    a.out16 = dptr<uint16_t>(out);
+    a.batch = batch;
+    a.hq = hq;
+    a.hkv = hkv;
+    a.hd = hd;
+    a.max_blocks = max_blocks;
+    a.max_ctx = max_ctx;
+    a.part = static_cast<float*>(ctx->attn_ws);
+    a.counters = ctx->attn_counters;
+    return launched(ctx, nx::attn_f16_launch(a, ctx->stream), "attn_f16");
+}
+
+nx_status nx_tq_codebooks(float* c4, float* b4, float* c3, float* b3) {
+    if (!c4 || !b4 || !c3 || !b3) return NX_ERR_INVALID;
+    nx::tq_codebook(128, 4, c4, b4);
+    nx::tq_codebook(128, 3, c3, b3);
+    return NX_OK;
+}
+
+nx_status nx_tq_encode(nx_ctx* ctx, nx_buf x, nx_buf signs, nx_buf c4, nx_buf c3, nx_buf norms,
+                       int nvec) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (nvec <= 0) return fail(ctx, NX_ERR_INVALID, "nx_tq_encode: nvec must be positive");
+    NX_NEED(ctx, x, (size_t)nvec * 128 * 4, "x");
+    NX_NEED(ctx, signs, 128 * 4, "signs");
+    NX_NEED(ctx, c4, (size_t)nvec * 32, "codes4");
+    NX_NEED(ctx, c3, (size_t)nvec * 24, "codes3");
+    NX_NEED(ctx, norms, (size_t)nvec * 2, "norms");
+    return launched(ctx, nx::tq_encode_launch(dptr<const float>(x), nvec, dptr<const float>(signs), nullptr, nullptr,
+                                              dptr<uint8_t>(c4), dptr<uint8_t>(c3), dptr<uint16_t>(norms), nullptr,
+                                              ctx->stream),
+                    "tq_encode");
+}
+
+nx_status nx_tq_append(nx_ctx* ctx, nx_buf k, nx_buf v, nx_buf ksg, nx_buf vsg, nx_buf kc4,
+                       nx_buf kc3, nx_buf kn, nx_buf vc4, nx_buf vc3, nx_buf vn, nx_buf bt,
+                       nx_buf pos, int batch, int hkv, int max_blocks, int num_blocks) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_tq_append validates positions on the host; not capturable");
+    if (batch < 1 || hkv <= 0 || max_blocks <= 0 || num_blocks <= 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_tq_append: bad shape");
+    const size_t nv = (size_t)num_blocks * hkv * nx::kPage;
+    NX_NEED(ctx, k, (size_t)batch * hkv * 128 * 4, "k");
+    NX_NEED(ctx, v, (size_t)batch * hkv * 128 * 4, "v");
+    NX_NEED(ctx, ksg, 512, "ksigns");
+    NX_NEED(ctx, vsg, 512, "vsigns");
+    NX_NEED(ctx, kc4, nv * 32, "kc4");
+    NX_NEED(ctx, kc3, nv * 24, "kc3");
+    NX_NEED(ctx, kn, nv * 2, "kn");
+    NX_NEED(ctx, vc4, nv * 32, "vc4");
+    NX_NEED(ctx, vc3, nv * 24, "vc3");
+    NX_NEED(ctx, vn, nv * 2, "vn");
+    nx_status s = check_table(ctx, bt, pos, batch, max_blocks, num_blocks, true, "nx_tq_append");
+    if (s != NX_OK) return s;
+    // the append kernel reads K and V from one [batch][2][hkv*128] staging layout
+    const size_t stage = (size_t)batch * 2 * hkv * 128 * 4;
+    s = ensure_attn_ws(ctx, stage > ctx->attn_ws_bytes ? stage : ctx->attn_ws_bytes, ctx->attn_ncounters);
+    if (s != NX_OK) return s;
+    float* tmp = static_cast<float*>(ctx->attn_ws);
+    for (int b = 0; b < batch; ++b) {
+        NX_HIP(ctx, hipMemcpyAsync(tmp + ((size_t)b * 2 + 0) * hkv * 128, dptr<float>(k) + (size_t)b * hkv * 128,
+                                   (size_t)hkv * 128 * 4, hipMemcpyDeviceToDevice, ctx->stream));
+        NX_HIP(ctx, hipMemcpyAsync(tmp + ((size_t)b * 2 + 1) * hkv * 128, dptr<float>(v) + (size_t)b * hkv * 128,
+                                   (size_t)hkv * 128 * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    }
+    return launched(ctx, nx::tq_append_launch(tmp, batch, hkv, dptr<const float>(ksg), dptr<const float>(vsg), nullptr,
+                                              nullptr, dptr<uint8_t>(kc4), dptr<uint8_t>(kc3), dptr<uint16_t>(kn),
+                                              dptr<uint8_t>(vc4), dptr<uint8_t>(vc3), dptr<uint16_t>(vn),
+                                              dptr<const int32_t>(bt), dptr<const int32_t>(pos), max_blocks, ctx->stream),
+                    "tq_append");
+}
+
+nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q, nx_buf kc4, nx_buf kc3, nx_buf kn,
+                                  nx_buf vc4, nx_buf vc3, nx_buf vn, nx_buf ksg, nx_buf vsg,
+                                  nx_buf bt, nx_buf lens, nx_buf out, int batch, int hq, int hkv,
+                                  int max_blocks, int num_blocks) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_attn_decode_paged_tq validates the block table on the host; not capturable");
+    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || max_blocks <= 0 || num_blocks <= 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_attn_decode_paged_tq: bad shape");
+    const int G = hq / hkv;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "nx_attn_decode_paged_tq: hq/hkv = %d", G);
+    const size_t nv = (size_t)num_blocks * hkv * nx::kPage;
+    NX_NEED(ctx, q, (size_t)batch * hq * 128 * 4, "q");
+    NX_NEED(ctx, kc4, nv * 32, "kc4");
+    NX_NEED(ctx, kc3, nv * 24, "kc3");
+    NX_NEED(ctx, kn, nv * 2, "kn");
+    NX_NEED(ctx, vc4, nv * 32, "vc4");
+    NX_NEED(ctx, vc3, nv * 24, "vc3");
+    NX_NEED(ctx, vn, nv * 2, "vn");
+    NX_NEED(ctx, ksg, 512, "ksigns");
+    NX_NEED(ctx, vsg, 512, "vsigns");
+    NX_NEED(ctx, out, (size_t)batch * hq * 128 * 2, "out");
+    nx_status s = check_table(ctx, bt, lens, batch, max_blocks, num_blocks, false, "nx_attn_decode_paged_tq");
+    if (s != NX_OK) return s;
+    const int max_ctx = max_blocks * nx::kPage;
+    s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, 128, max_ctx), nx::attn_counter_count(batch, hkv));
+    if (s != NX_OK) return s;
+    nx::AttnArgs a{};
+    a.q = dptr<const float>(q);
+    a.kc4 = dptr<const uint8_t>(kc4);
+    a.kc3 = dptr<const uint8_t>(kc3);
+    a.kn = dptr<const uint16_t>(kn);
+    a.vc4 = dptr<const uint8_t>(vc4);
+    a.vc3 = dptr<const uint8_t>(vc3);
+    a.vn = dptr<const uint16_t>(vn);
+    a.ksign = dptr<const float>(ksg);
+    a.vsign = dptr<const float>(vsg);
+    a.block_table = dptr<const int32_t>(bt);
+    a.ctx_lens = dptr<const int32_t>(lens);
+    a.out16 = dptr<uint16_t>(out);
+    a.batch = batch;
+    a.hq = hq;
+    a.hkv = hkv;
+    a.hd = 128;
+    a.max_blocks = max_blocks;
+    a.max_ctx = max_ctx;
+    a.part = static_cast<float*>(ctx->attn_ws);
+    a.counters = ctx->attn_counters;
+    return launched(ctx, nx::attn_tq_launch(a, ctx->stream), "attn_tq");
+}
+
+nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits, nx_buf ids, nx_buf w, int E, int k, int batch) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (E < 1 || E > 64 || k < 1 || k > 8 || k > E || batch < 1 || batch > 64)
+        return fail(ctx, NX_ERR_INVALID, "nx_moe_route_topk: bad shape E=%d k=%d batch=%d", E, k, batch);
+    NX_NEED(ctx, logits, (size_t)batch * E * 4, "logits");
+    NX_NEED(ctx, ids, (size_t)batch * k * 4, "ids");
+    NX_NEED(ctx, w, (size_t)batch * k * 4, "weights");
+    // per-expert token lists live in the attention workspace
+    const size_t extra = ((size_t)E + (size_t)E * batch * k) * 4;
+    nx_status s = ensure_attn_ws(ctx, extra > ctx->attn_ws_bytes ? extra : ctx->attn_ws_bytes, ctx->attn_ncounters);
+    if (s != NX_OK) return s;
+    nx::MoeArgs a{};
+    a.logits = dptr<const float>(logits);
+    a.E = E;
+    a.k = k;
+    a.batch = batch;
+    a.ids = dptr<int32_t>(ids);
+    a.weights = dptr<float>(w);
+    a.expert_count = static_cast<int32_t*>(ctx->attn_ws);
+    a.expert_slots = a.expert_count + E;
+    return launched(ctx, nx::moe_route_launch(a, ctx->stream), "moe_route");
+}
+
+nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_buf w2, nx_buf s2,
+                            nx_buf ids, nx_buf w, nx_buf out, int d, int F, int E, int k, int batch,
+                            int accumulate) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_moe_expert_ffn validates expert ids on the host; not capturable");
+    if (d <= 0 || F <= 0 || E < 1 || E > 64 || k < 1 || k > 8 || k > E || batch < 1 || batch > 8)
+        return fail(ctx, NX_ERR_INVALID, "nx_moe_expert_ffn: bad shape");
+    const int Gd = (d + 31) / 32, Gf = (F + 31) / 32;
+    if (Gd > 448 || Gf > 448) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_moe_expert_ffn: K above 14336");
+    const int Fp = Gf * 32;
+    NX_NEED(ctx, x, (size_t)batch * d * 2, "x");
+    NX_NEED(ctx, w13, (size_t)E * 2 * F * Gd * 16, "w13");
+    NX_NEED(ctx, s13, (size_t)E * 2 * F * Gd * 2, "s13");
+    NX_NEED(ctx, w2, (size_t)E * d * Gf * 16, "w2");
+    NX_NEED(ctx, s2, (size_t)E * d * Gf * 2, "s2");
+    NX_NEED(ctx, ids, (size_t)batch * k * 4, "ids");
+    NX_NEED(ctx, w, (size_t)batch * k * 4, "weights");
+    NX_NEED(ctx, out, (size_t)batch * d * 4, "out");
+    std::vector<int32_t> hid((size_t)batch * k);
+    NX_HIP(ctx, hipMemcpyAsync(hid.data(), dptr<void>(ids), hid.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    std::vector<int32_t> count(E, 0), slots((size_t)E * batch * k, 0);
+    for (int b = 0; b < batch; ++b)
+        for (int j = 0; j < k; ++j) {
+            const int e = hid[(size_t)b * k + j];
+            if (e < 0 || e >= E) return fail(ctx, NX_ERR_INVALID, "nx_moe_expert_ffn: expert id %d out of range", e);
+            slots[(size_t)e * batch * k + count[e]++] = b * k + j;
+        }
+    // workspace: count[E] | slots[E*batch*k] | act16[batch*k][Fp] | y32[batch*k][d]
+    const size_t off_slots = (size_t)E * 4;
+    const size_t off_act = (off_slots + slots.size() * 4 + 255) / 256 * 256;
+    const size_t off_y = (off_act + (size_t)batch * k * Fp * 2 + 255) / 256 * 256;
+    const size_t total = off_y + (size_t)batch * k * d * 4;
+    nx_status s = ensure_attn_ws(ctx, total, ctx->attn_ncounters);
+    if (s != NX_OK) return s;
+    char* ws = static_cast<char*>(ctx->attn_ws);
+    NX_HIP(ctx, hipMemcpyAsync(ws, count.data(), count.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    NX_HIP(ctx, hipMemcpyAsync(ws + off_slots, slots.data(), slots.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    NX_HIP(ctx, hipMemsetAsync(ws + off_act, 0, (size_t)batch * k * Fp * 2, ctx->stream));
+    nx::MoeFfnArgs a{};
+    a.x16 = dptr<const uint16_t>(x);
+    a.ldx = d;
+    a.w13 = dptr<const uint8_t>(w13);
+    a.s13 = dptr<const uint16_t>(s13);
+    a.w2 = dptr<const uint8_t>(w2);
+    a.s2 = dptr<const uint16_t>(s2);
+    a.d = d;
+    a.F = F;
+    a.E = E;
+    a.k = k;
+    a.batch = batch;
+    a.expert_count = reinterpret_cast<const int32_t*>(ws);
+    a.expert_slots = reinterpret_cast<const int32_t*>(ws + off_slots);
+    a.weights = dptr<const float>(w);
+    a.act16 = reinterpret_cast<uint16_t*>(ws + off_act);
+    a.y32 = reinterpret_cast<float*>(ws + off_y);
+    a.out = dptr<float>(out);
+    a.accumulate = accumulate;
+    hipError_t e = nx::moe_gate_up_launch(a, ctx->stream);
+    if (e == hipSuccess) e = nx::moe_down_launch(a, ctx->stream);
+    if (e == hipSuccess) e = nx::moe_combine_launch(a, ctx->stream);
+    return launched(ctx, e, "moe_expert_ffn");
+}
+
+nx_status nx_argmax(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (V <= 0 || batch < 1) return fail(ctx, NX_ERR_INVALID, "nx_argmax: bad shape");
+    NX_NEED(ctx, logits, (size_t)batch * V * 4, "logits");
+    NX_NEED(ctx, out, (size_t)batch * 4, "out");
+    return launched(ctx, nx::argmax_launch(dptr<const float>(logits), dptr<int32_t>(out), V, batch, ctx->stream), "argmax");
+}
+
+nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
+                       int batch, int iters, double* avg_ms) {
+    if (!ctx || !avg_ms || iters < 1) return NX_ERR_INVALID;
+    nx_status s = nx_gemv_int4_g32(ctx, x, wq, sc, y, N, K, batch);  // warm-up and validation
+    if (s != NX_OK) return s;
+    NX_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
+    for (int i = 0; i < iters; ++i) {
+        s = nx_gemv_int4_g32(ctx, x, wq, sc, y, N, K, batch);
+        if (s != NX_OK) return s;
+    }
+    NX_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));
+    NX_HIP(ctx, hipEventSynchronize(ctx->ev1));
+    float ms = 0.0f;
+    NX_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+    *avg_ms = (double)ms / iters;
+    return NX_OK;
+}
+
+}  // extern "C"

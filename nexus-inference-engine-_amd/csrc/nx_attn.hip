@@ -1,0 +1,613 @@
+// Paged decode attention on gfx950 over fp16 pages and TurboQuant pages.
+//
+// Grid (split, kv head, sequence); 4 wavefronts per block.  A block owns a
+// contiguous range of 16-token pages of one kv head and serves the G = hq/hkv
+// query heads that share it, so every K/V byte is read once per step.
+// Within a wavefront lane l owns dims [l%16 * DPL, +DPL) of the tokens
+// l/16, l/16+4, l/16+8, l/16+12 of each page; a score is reduced over the 16
+// lanes of a DPP row.  Each DPP row keeps its own online-softmax state
+// (m, l, o); rows, wavefronts and then splits are merged with the usual
+// rescaling.  The last block of a (sequence, kv head) to finish -- found with
+// an atomic counter, no spinning -- merges all splits and writes fp16 output.
+//
+// TurboQuant pages are scored in the rotated domain: the block rotates q once
+// (q~ = H D q / sqrt(128)), scores are n_t * <q~, c[code_t]>, V is summed in the
+// rotated domain and rotated back (D H o~ / sqrt(128)) once after the merge.
+#include "nx_common.h"
+#include "nx_kernels.h"
+
+namespace nx {
+
+namespace {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kTargetBlocks = 512;
+
+struct SplitPlan {
+    int nsplit, pps;  // splits per (sequence, kv head), pages per split
+};
+
+SplitPlan plan_splits(int batch, int hkv, int max_ctx) {
+    const int pages = (max_ctx + kPage - 1) / kPage;
+    int nsplit = (kTargetBlocks + batch * hkv - 1) / (batch * hkv);
+    if (nsplit > pages) nsplit = pages;
+    if (nsplit < 1) nsplit = 1;
+    const int pps = (pages + nsplit - 1) / nsplit;
+    nsplit = (pages + pps - 1) / pps;
+    if (nsplit < 1) nsplit = 1;
+    return {nsplit, pps < 1 ? 1 : pps};
+}
+
+// Online-softmax state of one lane: G heads x DPL dims.
+template <int G, int DPL>
+struct State {
+    float m[G], l[G], o[G][DPL];
+};
+
+template <int G, int DPL>
+__device__ inline void state_init(State<G, DPL>& s) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        s.m[h] = -__builtin_inff();
+        s.l[h] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) s.o[h][d] = 0.0f;
+    }
+}
+
+// Fold four token scores (per head) and their value rows into the state.
+template <int G, int DPL>
+__device__ inline void state_update(State<G, DPL>& s, const float (&sc)[4][G],
+                                    const float (&v)[4][DPL]) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float mn = s.m[h];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mn = fmaxf(mn, sc[j][h]);
+        if (mn == -__builtin_inff()) continue;  // nothing valid yet
+        const float corr = __expf(s.m[h] - mn);
+        float p[4], psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            p[j] = __expf(sc[j][h] - mn);
+            psum += p[j];
+        }
+        s.l[h] = s.l[h] * corr + psum;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) {
+            float acc = s.o[h][d] * corr;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc = fmaf(p[j], v[j][d], acc);
+            s.o[h][d] = acc;
+        }
+        s.m[h] = mn;
+    }
+}
+
+// Merge the four DPP rows of a wavefront; results valid in lanes 48..63.
+template <int G, int DPL>
+__device__ inline void state_merge_rows(State<G, DPL>& s) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float M = s.m[h];
+        M = fmaxf(M, readlane_f(s.m[h], 0));
+        M = fmaxf(M, readlane_f(s.m[h], 16));
+        M = fmaxf(M, readlane_f(s.m[h], 32));
+        M = fmaxf(M, readlane_f(s.m[h], 48));
+        const float f = (M == -__builtin_inff()) ? 0.0f : __expf(s.m[h] - M);
+        s.l[h] = rows4_sum_to_row3(s.l[h] * f);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) s.o[h][d] = rows4_sum_to_row3(s.o[h][d] * f);
+        s.m[h] = M;
+    }
+}
+
+// Block-level merge of the wavefronts' states through LDS, then store the
+// split's partial [M[G], L[G], O[G][HD]] (or the final output if nsplit == 1).
+// Returns nothing; `part` points at this split's record.
+template <int G, int HD>
+__device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __restrict__ part,
+                                         float* lds) {
+    constexpr int DPL = HD / 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // lds layout per wave: m[G], l[G], o[G][HD]
+    constexpr int REC = G * (HD + 2);
+    float* my = lds + wave * REC;
+    if (lane >= 48) {
+        const int c = lane - 48;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            if (c == 0) {
+                my[h] = s.m[h];
+                my[G + h] = s.l[h];
+            }
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) my[2 * G + h * HD + c * DPL + d] = s.o[h][d];
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * HD + G; idx += kAttnThreads) {
+        if (idx < G * HD) {
+            const int h = idx / HD;
+            float M = -__builtin_inff();
+            for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, lds[w * REC + h]);
+            float O = 0.0f;
+            for (int w = 0; w < kAttnWaves; ++w) {
+                const float mw = lds[w * REC + h];
+                const float f = (M == -__builtin_inff()) ? 0.0f : __expf(mw - M);
+                O = fmaf(lds[w * REC + 2 * G + idx], f, O);
+            }
+            part[2 * G + idx] = O;
+        } else {
+            const int h = idx - G * HD;
+            float M = -__builtin_inff();
+            for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, lds[w * REC + h]);
+            float L = 0.0f;
+            for (int w = 0; w < kAttnWaves; ++w) {
+                const float f = (M == -__builtin_inff()) ? 0.0f : __expf(lds[w * REC + h] - M);
+                L = fmaf(lds[w * REC + G + h], f, L);
+            }
+            part[h] = M;
+            part[G + h] = L;
+        }
+    }
+}
+
+// Is this the last split block of its (sequence, kv head) to finish?
+__device__ inline bool arrive_last(unsigned int* counter, int nsplit, int* flag) {
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int prev = atomicAdd(counter, 1u);
+        *flag = (prev == (unsigned int)(nsplit - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    const bool last = *flag != 0;
+    if (last) __threadfence();
+    return last;
+}
+
+// Merge all split partials of (b, kvh) into o_merged[G][HD] / L (in LDS).
+template <int G, int HD>
+__device__ inline void merge_splits(const float* __restrict__ parts, int nsplit, float* out_o,
+                                    float* out_l) {
+    constexpr int REC = G * (HD + 2);
+    for (int idx = threadIdx.x; idx < G * HD + G; idx += kAttnThreads) {
+        const int h = idx < G * HD ? idx / HD : idx - G * HD;
+        float M = -__builtin_inff();
+        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, parts[(size_t)s * REC + h]);
+        float acc = 0.0f;
+        for (int s = 0; s < nsplit; ++s) {
+            const float* p = parts + (size_t)s * REC;
+            const float ms = p[h];
+            const float f = (M == -__builtin_inff()) ? 0.0f : __expf(ms - M);
+            const float val = idx < G * HD ? p[2 * G + idx] : p[G + h];
+            acc = fmaf(val, f, acc);
+        }
+        if (idx < G * HD)
+            out_o[idx] = acc;
+        else
+            out_l[h] = acc;
+    }
+}
+
+// ------------------------------------------------------------ fp16 pages --
+template <int G, int HD>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
+    constexpr int DPL = HD / 16;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, tg = lane >> 4;
+    __shared__ float lds[kAttnWaves * G * (HD + 2) + G * HD + G];
+    __shared__ int flag;
+
+    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float q[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d)
+            q[h][d] = a.q[((size_t)b * a.hq + kvh * G + h) * HD + c * DPL + d];
+
+    State<G, DPL> st;
+    state_init(st);
+    const int npages = (ctx + kPage - 1) / kPage;
+    const int p0 = split * pps;
+    const int p1 = min(p0 + pps, npages);
+    const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
+    for (int p = p0 + wave; p < p1; p += kAttnWaves) {
+        const int blk = bt[p];
+        const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
+        float kf[4][DPL], vf[4][DPL];
+        float sc[4][G];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = tg + 4 * j;
+            const bool valid = p * kPage + t < ctx;
+            const uint16_t* kp = a.kpool + base + (size_t)t * HD + c * DPL;
+            const uint16_t* vp = a.vpool + base + (size_t)t * HD + c * DPL;
+            if (DPL == 8) {
+                uint4 kr = valid ? *reinterpret_cast<const uint4*>(kp) : make_uint4(0, 0, 0, 0);
+                uint4 vr = valid ? *reinterpret_cast<const uint4*>(vp) : make_uint4(0, 0, 0, 0);
+                const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w}, vw[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kf[j][2 * i] = h2f_bits((uint16_t)(kw[i] & 0xFFFFu));
+                    kf[j][2 * i + 1] = h2f_bits((uint16_t)(kw[i] >> 16));
+                    vf[j][2 * i] = h2f_bits((uint16_t)(vw[i] & 0xFFFFu));
+                    vf[j][2 * i + 1] = h2f_bits((uint16_t)(vw[i] >> 16));
+                }
+            } else {
+                uint2 kr = valid ? *reinterpret_cast<const uint2*>(kp) : make_uint2(0, 0);
+                uint2 vr = valid ? *reinterpret_cast<const uint2*>(vp) : make_uint2(0, 0);
+                const uint32_t kw[2] = {kr.x, kr.y}, vw[2] = {vr.x, vr.y};
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    kf[j][2 * i] = h2f_bits((uint16_t)(kw[i] & 0xFFFFu));
+                    kf[j][2 * i + 1] = h2f_bits((uint16_t)(kw[i] >> 16));
+                    vf[j][2 * i] = h2f_bits((uint16_t)(vw[i] & 0xFFFFu));
+                    vf[j][2 * i + 1] = h2f_bits((uint16_t)(vw[i] >> 16));
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) dot = fmaf(q[h][d], kf[j][d], dot);
+                dot = row16_sum(dot) * scale;
+                sc[j][h] = valid ? dot : -__builtin_inff();
+            }
+        }
+        state_update(st, sc, vf);
+    }
+    state_merge_rows(st);
+
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * (G * (HD + 2));
+    block_merge_store<G, HD>(st, parts + (size_t)split * (G * (HD + 2)), lds);
+    if (!arrive_last(a.counters + (size_t)b * a.hkv + kvh, nsplit, &flag)) return;
+
+    float* mo = lds + kAttnWaves * G * (HD + 2);
+    float* ml = mo + G * HD;
+    merge_splits<G, HD>(parts, nsplit, mo, ml);
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads) {
+        const int h = idx / HD;
+        const float L = ml[h];
+        const float o = L > 0.0f ? mo[idx] / L : 0.0f;
+        a.out16[((size_t)b * a.hq + kvh * G) * HD + idx] = f2h_bits(o);
+    }
+    if (threadIdx.x == 0) a.counters[(size_t)b * a.hkv + kvh] = 0u;
+}
+
+// ------------------------------------------------------ TurboQuant pages --
+__constant__ float c_tq_c4[16];
+__constant__ float c_tq_b4[15];
+__constant__ float c_tq_c3[8];
+__constant__ float c_tq_b3[7];
+
+// In-LDS FWHT of G vectors of 128 (canonical butterfly network).
+template <int G>
+__device__ inline void lds_fwht(float* v) {
+    for (int h = 1; h < 128; h <<= 1) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < G * 64; t += kAttnThreads) {
+            const int g = t >> 6, k = t & 63;
+            const int j = ((k / h) * 2 * h) + (k % h);
+            const float x = v[g * 128 + j], y = v[g * 128 + j + h];
+            v[g * 128 + j] = x + y;
+            v[g * 128 + j + h] = x - y;
+        }
+    }
+    __syncthreads();
+}
+
+constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
+
+// Decode the 8 codebook values of coordinates [8c, 8c+8) of token record t.
+__device__ inline void tq_decode8(const uint8_t* __restrict__ c4, const uint8_t* __restrict__ c3,
+                                  int c, const float* lds_c4, const float* lds_c3, float (&out)[8]) {
+    if (c < 8) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(c4 + 4 * c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = lds_c4[(w >> (4 * i)) & 15u];
+    } else {
+        const uint8_t* p = c3 + 3 * (c - 8);
+        const uint32_t w = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = lds_c3[(w >> (3 * i)) & 7u];
+    }
+}
+
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
+    constexpr int HD = 128, DPL = 8;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, tg = lane >> 4;
+    __shared__ float lds[kAttnWaves * G * (HD + 2) + G * HD + G];
+    __shared__ float qrot[G * HD];
+    __shared__ float cb[24];
+    __shared__ int flag;
+
+    if (threadIdx.x < 16) cb[threadIdx.x] = c_tq_c4[threadIdx.x];
+    else if (threadIdx.x < 24) cb[threadIdx.x] = c_tq_c3[threadIdx.x - 16];
+    for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads)
+        qrot[idx] = a.ksign[idx % HD] * a.q[((size_t)b * a.hq + kvh * G) * HD + idx];
+    lds_fwht<G>(qrot);
+
+    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
+    float q[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) q[h][d] = qrot[h * HD + c * DPL + d];
+
+    State<G, DPL> st;
+    state_init(st);
+    const int npages = (ctx + kPage - 1) / kPage;
+    const int p0 = split * pps;
+    const int p1 = min(p0 + pps, npages);
+    const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
+    for (int p = p0 + wave; p < p1; p += kAttnWaves) {
+        const int blk = bt[p];
+        const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage;
+        float vf[4][DPL];
+        float sc[4][G];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = tg + 4 * j;
+            const bool valid = p * kPage + t < ctx;
+            float kf[DPL];
+            if (valid) {
+                tq_decode8(a.kc4 + (rec + t) * 32, a.kc3 + (rec + t) * 24, c, cb, cb + 16, kf);
+                tq_decode8(a.vc4 + (rec + t) * 32, a.vc3 + (rec + t) * 24, c, cb, cb + 16, vf[j]);
+                const float vn = h2f_bits(a.vn[rec + t]);
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) vf[j][d] *= vn;
+            } else {
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) kf[d] = vf[j][d] = 0.0f;
+            }
+            const float kn = valid ? h2f_bits(a.kn[rec + t]) : 0.0f;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) dot = fmaf(q[h][d], kf[d], dot);
+                dot = row16_sum(dot) * kn * scale;
+                sc[j][h] = valid ? dot : -__builtin_inff();
+            }
+        }
+        state_update(st, sc, vf);
+    }
+    state_merge_rows(st);
+
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * (G * (HD + 2));
+    block_merge_store<G, HD>(st, parts + (size_t)split * (G * (HD + 2)), lds);
+    if (!arrive_last(a.counters + (size_t)b * a.hkv + kvh, nsplit, &flag)) return;
+
+    float* mo = lds + kAttnWaves * G * (HD + 2);
+    float* ml = mo + G * HD;
+    merge_splits<G, HD>(parts, nsplit, mo, ml);
+    // rotate back: o = D_v H o~ / sqrt(128)
+    lds_fwht<G>(mo);
+    for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads) {
+        const int h = idx / HD;
+        const float L = ml[h];
+        const float o = L > 0.0f ? (mo[idx] * kTqScale * a.vsign[idx % HD]) / L : 0.0f;
+        a.out16[((size_t)b * a.hq + kvh * G) * HD + idx] = f2h_bits(o);
+    }
+    if (threadIdx.x == 0) a.counters[(size_t)b * a.hkv + kvh] = 0u;
+}
+
+// ----------------------------------------------------- TurboQuant encode --
+// One wavefront per vector; lane l holds coordinates l and l + 64.
+__device__ inline void tq_encode_wave(const float* __restrict__ x, const float* __restrict__ sign,
+                                      uint8_t* __restrict__ c4, uint8_t* __restrict__ c3,
+                                      uint16_t* __restrict__ norm, uint8_t* lds_codes) {
+    const int lane = threadIdx.x & 63;
+    const float x0 = x[lane], x1 = x[lane + 64];
+    const float a0 = x0 * x0;
+    const float a1 = x1 * x1;
+    float w = a0 + a1;
+    for (int s = 32; s >= 1; s >>= 1) {
+        const float o = __shfl_down(w, s, 64);
+        w = w + o;
+    }
+    const float ss = readlane_f(w, 0);
+    const float n = __fsqrt_rn(ss);
+    float u0 = 0.0f, u1 = 0.0f;
+    if (n > 1e-12f) {
+        const float inv = __fdiv_rn(1.0f, n);
+        u0 = (sign[lane] * x0) * inv;
+        u1 = (sign[lane + 64] * x1) * inv;
+    }
+    // FWHT: stages h = 1 .. 32 across lanes, h = 64 inside the lane.
+    for (int h = 1; h < 64; h <<= 1) {
+        const float p0 = __shfl_xor(u0, h, 64);
+        const float p1 = __shfl_xor(u1, h, 64);
+        if (lane & h) {
+            u0 = p0 - u0;
+            u1 = p1 - u1;
+        } else {
+            u0 = u0 + p0;
+            u1 = u1 + p1;
+        }
+    }
+    {
+        const float t0 = u0 + u1, t1 = u0 - u1;
+        u0 = t0;
+        u1 = t1;
+    }
+    const float y0 = u0 * kTqScale, y1 = u1 * kTqScale;
+    int q0 = 0, q1 = 0;
+#pragma unroll
+    for (int j = 0; j < 15; ++j) q0 += (y0 < c_tq_b4[j]) ? 0 : 1;
+#pragma unroll
+    for (int j = 0; j < 7; ++j) q1 += (y1 < c_tq_b3[j]) ? 0 : 1;
+    lds_codes[lane] = (uint8_t)q0;
+    lds_codes[lane + 64] = (uint8_t)q1;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 32) c4[lane] = (uint8_t)(lds_codes[2 * lane] | (lds_codes[2 * lane + 1] << 4));
+    if (lane < 24) {
+        const int g = lane / 3, r = lane % 3;
+        uint32_t bits = 0;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) bits |= (uint32_t)lds_codes[64 + 8 * g + m] << (3 * m);
+        c3[lane] = (uint8_t)(bits >> (8 * r));
+    }
+    if (lane == 0) *norm = f2h_bits(n);
+}
+
+__global__ __launch_bounds__(256) void k_tq_encode(const float* x, int nvec, const float* signs,
+                                                   uint8_t* c4, uint8_t* c3, uint16_t* norms,
+                                                   const int32_t* idx) {
+    __shared__ uint8_t codes[4][128];
+    const int wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * 4 + wave;
+    if (v >= nvec) return;
+    const int dst = idx ? idx[v] : v;
+    tq_encode_wave(x + (size_t)v * 128, signs, c4 + (size_t)dst * 32, c3 + (size_t)dst * 24,
+                   norms + dst, codes[wave]);
+}
+
+// Context rows [ctx][hkv][128] of sequence b -> pages.
+__global__ __launch_bounds__(256) void k_tq_encode_ctx(const float* x, int ctx, int hkv,
+                                                       const float* signs, uint8_t* c4,
+                                                       uint8_t* c3, uint16_t* norms,
+                                                       const int32_t* block_table, int max_blocks,
+                                                       int b) {
+    __shared__ uint8_t codes[4][128];
+    const int wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * 4 + wave;
+    if (v >= ctx * hkv) return;
+    const int t = v / hkv, h = v % hkv;
+    const int blk = block_table[(size_t)b * max_blocks + t / kPage];
+    const size_t dst = ((size_t)blk * hkv + h) * kPage + t % kPage;
+    tq_encode_wave(x + (size_t)v * 128, signs, c4 + dst * 32, c3 + dst * 24, norms + dst,
+                   codes[wave]);
+}
+
+// One token per sequence from kv_tmp [batch][2][hkv*128].
+__global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batch, int hkv,
+                                                   const float* ksign, const float* vsign,
+                                                   uint8_t* kc4, uint8_t* kc3, uint16_t* kn,
+                                                   uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                                                   const int32_t* block_table, const int32_t* pos,
+                                                   int max_blocks) {
+    __shared__ uint8_t codes[4][128];
+    const int wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * 4 + wave;  // (b, kv, h)
+    if (v >= batch * 2 * hkv) return;
+    const int b = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv;
+    const int p = pos[b];
+    const int blk = block_table[(size_t)b * max_blocks + p / kPage];
+    const size_t dst = ((size_t)blk * hkv + h) * kPage + p % kPage;
+    const float* src = kv_tmp + ((size_t)b * 2 + kv) * hkv * 128 + (size_t)h * 128;
+    if (kv == 0)
+        tq_encode_wave(src, ksign, kc4 + dst * 32, kc3 + dst * 24, kn + dst, codes[wave]);
+    else
+        tq_encode_wave(src, vsign, vc4 + dst * 32, vc3 + dst * 24, vn + dst, codes[wave]);
+}
+
+}  // namespace
+
+size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
+    const SplitPlan sp = plan_splits(batch, hkv, max_ctx);
+    const int G = hq / hkv;
+    return sizeof(float) * (size_t)batch * hkv * sp.nsplit * G * (hd + 2);
+}
+
+size_t attn_counter_count(int batch, int hkv) { return (size_t)batch * hkv; }
+
+hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
+    const SplitPlan sp = plan_splits(a.batch, a.hkv, a.max_ctx);
+    const dim3 grid(sp.nsplit, a.hkv, a.batch);
+    const int G = a.hq / a.hkv;
+#define NX_ATTN_CASE(GG, HH)                                                                   \
+    if (G == GG && a.hd == HH) {                                                               \
+        hipLaunchKernelGGL((k_attn_f16<GG, HH>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit, \
+                           sp.pps);                                                            \
+        return hipGetLastError();                                                              \
+    }
+    NX_ATTN_CASE(1, 64)
+    NX_ATTN_CASE(2, 64)
+    NX_ATTN_CASE(4, 64)
+    NX_ATTN_CASE(8, 64)
+    NX_ATTN_CASE(1, 128)
+    NX_ATTN_CASE(2, 128)
+    NX_ATTN_CASE(4, 128)
+    NX_ATTN_CASE(8, 128)
+#undef NX_ATTN_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st) {
+    const SplitPlan sp = plan_splits(a.batch, a.hkv, a.max_ctx);
+    const dim3 grid(sp.nsplit, a.hkv, a.batch);
+    const int G = a.hq / a.hkv;
+    if (a.hd != 128) return hipErrorInvalidValue;
+#define NX_ATTN_CASE(GG)                                                                      \
+    if (G == GG) {                                                                            \
+        hipLaunchKernelGGL((k_attn_tq<GG>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit,    \
+                           sp.pps);                                                           \
+        return hipGetLastError();                                                             \
+    }
+    NX_ATTN_CASE(1)
+    NX_ATTN_CASE(2)
+    NX_ATTN_CASE(4)
+    NX_ATTN_CASE(8)
+#undef NX_ATTN_CASE
+    return hipErrorInvalidValue;
+}
+
+void tq_set_codebooks(const float* c4, const float* b4, const float* c3, const float* b3) {
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_c4), c4, sizeof(float) * 16);
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_b4), b4, sizeof(float) * 15);
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_c3), c3, sizeof(float) * 8);
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_b3), b3, sizeof(float) * 7);
+}
+
+hipError_t tq_encode_launch(const float* x, int nvec, const float* signs, const float* b4,
+                            const float* b3, uint8_t* c4, uint8_t* c3, uint16_t* norms,
+                            const int32_t* idx, hipStream_t st) {
+    (void)b4;
+    (void)b3;
+    if (nvec <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tq_encode, dim3((nvec + 3) / 4), dim3(256), 0, st, x, nvec, signs, c4, c3,
+                       norms, idx);
+    return hipGetLastError();
+}
+
+hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* signs,
+                                const float* b4, const float* b3, uint8_t* c4, uint8_t* c3,
+                                uint16_t* norms, const int32_t* block_table, int max_blocks, int b,
+                                hipStream_t st) {
+    (void)b4;
+    (void)b3;
+    const int nvec = ctx * hkv;
+    if (nvec <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tq_encode_ctx, dim3((nvec + 3) / 4), dim3(256), 0, st, x, ctx, hkv, signs,
+                       c4, c3, norms, block_table, max_blocks, b);
+    return hipGetLastError();
+}
+
+hipError_t tq_append_launch(const float* kv_tmp, int batch, int hkv, const float* ksign,
+                            const float* vsign, const float* b4, const float* b3, uint8_t* kc4,
+                            uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                            const int32_t* block_table, const int32_t* pos, int max_blocks,
+                            hipStream_t st) {
+    (void)b4;
+    (void)b3;
+    const int nvec = batch * 2 * hkv;
+    hipLaunchKernelGGL(k_tq_append, dim3((nvec + 3) / 4), dim3(256), 0, st, kv_tmp, batch, hkv,
+                       ksign, vsign, kc4, kc3, kn, vc4, vc3, vn, block_table, pos, max_blocks);
+    return hipGetLastError();
+}
+
+}  // namespace nx

@@ -1,0 +1,74 @@
+// Internal host-side state shared by the C-ABI layer and the runner.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/nexus_hip.h"
+
+struct nx_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::map<uint64_t, size_t> bufs;                   // device address -> bytes
+    std::unordered_map<const void*, uint64_t> wcache;  // host key -> buffer
+    std::string err;
+    bool capturing = false;
+    hipGraphExec_t token_exec = nullptr;
+    // workspace of the standalone attention entry points
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    unsigned int* attn_counters = nullptr;
+    size_t attn_ncounters = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    float c4[16], b4[15], c3[8], b3[7];
+};
+
+namespace nx {
+
+inline nx_status fail(nx_ctx* ctx, nx_status code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    return code;
+}
+
+inline nx_status hip_fail(nx_ctx* ctx, hipError_t e, const char* what) {
+    return fail(ctx, e == hipErrorOutOfMemory ? NX_ERR_OOM : NX_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+// Size of a buffer of the context, 0 if it is not one.
+inline size_t buf_size(const nx_ctx* ctx, nx_buf b) {
+    auto it = ctx->bufs.find(b);
+    return it == ctx->bufs.end() ? 0 : it->second;
+}
+
+// Restatement of the Lloyd-Max codebook construction for N(0, 1/d)
+// (kv/turbo_quant.cpp:172-219), float arithmetic as in the reference.
+void tq_codebook(int d, int bits, float* centroids, float* boundaries);
+
+}  // namespace nx
+
+#define NX_HIP(ctx, expr)                                  \
+    do {                                                   \
+        hipError_t nx_e_ = (expr);                         \
+        if (nx_e_ != hipSuccess) return nx::hip_fail((ctx), nx_e_, #expr); \
+    } while (0)
+
+// Check that handle `b` names a buffer of at least `bytes` bytes.
+#define NX_NEED(ctx, b, bytes, name)                                                          \
+    do {                                                                                      \
+        size_t nx_sz_ = nx::buf_size((ctx), (b));                                             \
+        if (nx_sz_ == 0) return nx::fail((ctx), NX_ERR_INVALID, "%s: unknown buffer", name); \
+        if (nx_sz_ < (size_t)(bytes))                                                         \
+            return nx::fail((ctx), NX_ERR_INVALID, "%s: buffer has %zu bytes, needs %zu", name, \
+                            nx_sz_, (size_t)(bytes));                                         \
+    } while (0)

@@ -1,0 +1,186 @@
+// Host-side launchers of the gfx950 decode kernels.  All pointers are
+// device pointers; every launcher enqueues on `st` and returns the launch
+// status.  Shapes are validated by the callers (the C-ABI layer and the
+// runner) before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nx {
+
+// ----------------------------------------------------------------- GEMV --
+// Where the GEMV input x comes from.
+enum XSrc : int {
+    X_F16 = 0,      // x fp16 [batch][K] (row stride ldx elements)
+    X_RMSNORM = 1,  // x = fp16((h * 1/sqrt(mean(h^2)+eps)) * w), h fp32 [batch][K]
+};
+// What the GEMV does with each output row.
+enum Epi : int {
+    E_F16 = 0,      // y16[b][n] = y
+    E_F32 = 1,      // y32[b][n] = y
+    E_ACC = 2,      // y32[b][n] += y   (residual add)
+    E_QKV = 3,      // RoPE on q/k rows; q -> q32; k,v -> fp16 pages (or fp32 kv_tmp)
+    E_SWIGLU = 4,   // rows (2j, 2j+1) = (gate j, up j) -> act16[b][j] = fp16(silu(g)*u)
+    E_LOGITS = 5,   // y32[b][n] = y and running argmax into best[b]
+};
+
+struct GemvArgs {
+    const uint8_t* W;       // [N][G*16]
+    const uint16_t* S;      // [N][G]
+    int N, K, G;
+    int batch;
+    // input
+    const uint16_t* x16;    // X_F16
+    int ldx;                // elements between batch rows of x16 / h32
+    const float* h32;       // X_RMSNORM
+    const float* norm_w;    // X_RMSNORM (nullptr = ones)
+    float eps;
+    // outputs
+    uint16_t* y16;
+    float* y32;
+    int ldy;                // elements between batch rows of y
+    // E_QKV
+    float* q32;             // [batch][qdim]
+    int qdim, kvdim, hd, hkv;
+    const int32_t* pos;     // [batch] position of the token being processed
+    const float* cos_t;     // [max_pos][hd/2]
+    const float* sin_t;
+    uint16_t* kpool;        // fp16 pages (kv_kind 0)
+    uint16_t* vpool;
+    float* kv_tmp;          // [batch][2][kvdim] fp32 (kv_kind 1)
+    const int32_t* block_table;
+    int max_blocks;
+    // E_SWIGLU
+    uint16_t* act16;        // [batch][lda]
+    int lda;
+    // E_LOGITS
+    unsigned long long* best;  // [batch] packed (ordered value, ~index)
+};
+
+hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st);
+
+// ------------------------------------------------------------ attention --
+struct AttnArgs {
+    const float* q;            // [batch][hq][hd]
+    const uint16_t* kpool;     // fp16 pages
+    const uint16_t* vpool;
+    // TurboQuant pages (head_dim 128)
+    const uint8_t *kc4, *kc3, *vc4, *vc3;
+    const uint16_t *kn, *vn;
+    const float *ksign, *vsign;  // [128] of +-1
+    const int32_t* block_table;  // [batch][max_blocks]
+    const int32_t* ctx_lens;     // [batch] (nullptr: use pos[b] + 1)
+    const int32_t* pos;
+    uint16_t* out16;             // [batch][hq][hd]
+    int batch, hq, hkv, hd, max_blocks;
+    int max_ctx;                 // upper bound of ctx_lens (sizes the split grid)
+    // workspace
+    float* part;                 // partial (m, l, o) per split
+    unsigned int* counters;      // [batch][hkv], zero between launches
+};
+size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
+size_t attn_counter_count(int batch, int hkv);
+hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st);
+hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st);
+
+// ---------------------------------------------------------------- misc --
+hipError_t rmsnorm_launch(const float* x, const float* w, uint16_t* out, int dim, float eps,
+                          int batch, hipStream_t st);
+hipError_t rope_launch(float* x, const int32_t* pos, const float* cos_t, const float* sin_t,
+                       int heads, int hd, int batch, hipStream_t st);
+hipError_t swiglu_launch(const float* g, const float* u, uint16_t* out, int n, int batch,
+                         hipStream_t st);
+hipError_t residual_add_launch(const float* a, const float* b, float* out, int n, hipStream_t st);
+hipError_t kv_append_f16_launch(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
+                                const int32_t* block_table, const int32_t* pos, int batch,
+                                int hkv, int hd, int max_blocks, hipStream_t st);
+hipError_t argmax_launch(const float* logits, int32_t* out, int V, int batch, hipStream_t st);
+hipError_t unpack_int4_launch(const uint8_t* packed, uint8_t* codes, size_t n, hipStream_t st);
+hipError_t quantize_int4_launch(const float* w, uint8_t* codes, uint16_t* scales, int N, int K,
+                                hipStream_t st);
+// Synthetic weights: W[N][K] ~ normal(k) from stream (seed, tid), quantized
+// int4-g32 in one pass (bit-identical to quantizing the generated floats).
+// row_offset/rows_total place the matrix at row `row_offset` of a larger
+// allocation with `row_stride` rows between consecutive generated rows
+// (row_stride 2 interleaves gate/up).
+hipError_t gen_quant_launch(uint8_t* codes, uint16_t* scales, int N, int K, uint64_t seed,
+                            uint32_t tid, float k, int row_offset, int row_stride,
+                            hipStream_t st);
+hipError_t gen_f16_launch(uint16_t* out, size_t n, uint64_t seed, uint32_t tid, float k,
+                          hipStream_t st);
+// Synthetic fp16 context for layer L, positions [0, ctx) of every sequence.
+hipError_t gen_ctx_f16_launch(uint16_t* kpool, uint16_t* vpool, const int32_t* block_table,
+                              int max_blocks, int batch, int ctx, int hkv, int hd, int L,
+                              uint64_t seed, float k, const int32_t* outlier_ch, int n_outlier,
+                              hipStream_t st);
+// Synthetic raw K/V fp32 [ctx][hkv][hd] of (L, b, kv) into dst (for TurboQuant encode).
+hipError_t gen_ctx_raw_launch(float* dst, int ctx, int hkv, int hd, int L, int b, int kv,
+                              uint64_t seed, float k, const int32_t* outlier_ch, int n_outlier,
+                              hipStream_t st);
+
+// TurboQuant: encode nvec vectors (rows of x, stride 128) into the given
+// destinations; dst index of vector i is idx ? idx[i] : i.
+hipError_t tq_encode_launch(const float* x, int nvec, const float* signs, const float* b4,
+                            const float* b3, uint8_t* c4, uint8_t* c3, uint16_t* norms,
+                            const int32_t* idx, hipStream_t st);
+// Encode context rows [ctx][hkv][128] of sequence b into pages.
+hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* signs,
+                                const float* b4, const float* b3, uint8_t* c4, uint8_t* c3,
+                                uint16_t* norms, const int32_t* block_table, int max_blocks,
+                                int b, hipStream_t st);
+// Append one token per sequence from kv_tmp [batch][2][hkv*128].
+hipError_t tq_append_launch(const float* kv_tmp, int batch, int hkv, const float* ksign,
+                            const float* vsign, const float* b4, const float* b3, uint8_t* kc4,
+                            uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                            const int32_t* block_table, const int32_t* pos, int max_blocks,
+                            hipStream_t st);
+void tq_set_codebooks(const float* c4, const float* b4, const float* c3, const float* b3);
+
+// Step start: tok[b] = token decoded from best[b]; best[b] = 0; pos[b] += 1;
+// h[b] = fp32(embed[tok]).
+// The token consumed at new position p is recorded at out_tokens[b][p - base[b] - 1]
+// when that index is in [0, out_stride).
+hipError_t embed_launch(unsigned long long* best, int32_t* pos, const int32_t* base,
+                        int32_t* out_tokens, int out_stride, const uint16_t* embed, float* h,
+                        int d, int vocab, int batch, hipStream_t st);
+// Record the pending tokens (decoded from best) at out_tokens[b][pos[b] - base[b]].
+hipError_t finish_tokens_launch(const unsigned long long* best, const int32_t* pos,
+                                const int32_t* base, int32_t* out_tokens, int out_stride,
+                                int batch, hipStream_t st);
+
+// Make tokens[b] the pending token of sequence b (as if sampled).
+hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, int batch,
+                             hipStream_t st);
+
+// MoE
+struct MoeArgs {
+    const float* logits;        // [batch][E]
+    int E, k, batch;
+    int32_t* ids;               // [batch][k]
+    float* weights;             // [batch][k]
+    int32_t* expert_count;      // [E]
+    int32_t* expert_slots;      // [E][batch*k] : entries b*k + j
+};
+hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st);
+struct MoeFfnArgs {
+    const uint16_t* x16;        // [batch][ldx] normed hidden (fp16)
+    int ldx;
+    const uint8_t* w13;         // [E][2F][d/2]
+    const uint16_t* s13;        // [E][2F][d/32]
+    const uint8_t* w2;          // [E][d][Fp/2]
+    const uint16_t* s2;
+    int d, F, E, k, batch;
+    const int32_t* expert_count;
+    const int32_t* expert_slots;
+    const float* weights;       // [batch][k]
+    uint16_t* act16;            // [batch*k][Fp]
+    float* y32;                 // [batch*k][d]
+    float* out;                 // [batch][d]
+    int accumulate;
+};
+hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st);
+hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st);
+hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st);
+
+}  // namespace nx

@@ -1,0 +1,424 @@
+// Small decode-loop kernels on gfx950: standalone RMSNorm / RoPE / SwiGLU /
+// residual add / KV append / argmax, int4 unpack and quantize, the device
+// side of the synthetic generator, the step-start embedding kernel and MoE
+// routing.  None of these is on the HBM-heavy path; they favour simplicity.
+#include "nx_common.h"
+#include "nx_kernels.h"
+
+namespace nx {
+
+namespace {
+
+__device__ inline float block_sum256(float v, float* red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    const float t = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return t;
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* w, uint16_t* out,
+                                                 int dim, float eps) {
+    __shared__ float red[4];
+    const float* xb = x + (size_t)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += 256) ss += xb[i] * xb[i];
+    ss = block_sum256(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = threadIdx.x; i < dim; i += 256) {
+        const float v = xb[i] * inv;
+        out[(size_t)blockIdx.x * dim + i] = f2h_bits(w ? v * w[i] : v);
+    }
+}
+
+__global__ void k_rope(float* x, const int32_t* pos, const float* cos_t, const float* sin_t,
+                       int heads, int hd, int batch) {
+    const int half = hd / 2;
+    const int total = batch * heads * half;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int b = t / (heads * half), r = t % (heads * half);
+    const int h = r / half, i = r % half;
+    const int p = pos[b];
+    float* v = x + ((size_t)b * heads + h) * hd;
+    const float c = cos_t[(size_t)p * half + i], s = sin_t[(size_t)p * half + i];
+    const float a = v[2 * i], bb = v[2 * i + 1];
+    v[2 * i] = a * c - bb * s;
+    v[2 * i + 1] = a * s + bb * c;
+}
+
+__global__ void k_swiglu(const float* g, const float* u, uint16_t* out, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    out[i] = f2h_bits(gv / (1.0f + expf(-gv)) * u[i]);
+}
+
+__global__ void k_residual_add(const float* a, const float* b, float* out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+__global__ void k_kv_append_f16(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
+                                const int32_t* block_table, const int32_t* pos, int batch, int hkv,
+                                int hd, int max_blocks) {
+    const int total = batch * hkv * hd;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int b = t / (hkv * hd), r = t % (hkv * hd);
+    const int h = r / hd, d = r % hd;
+    const int p = pos[b];
+    const int blk = block_table[(size_t)b * max_blocks + p / kPage];
+    const size_t off = (((size_t)blk * hkv + h) * kPage + p % kPage) * hd + d;
+    kpool[off] = f2h_bits(k[(size_t)b * hkv * hd + r]);
+    vpool[off] = f2h_bits(v[(size_t)b * hkv * hd + r]);
+}
+
+__device__ inline unsigned long long pack_best(float v, int idx) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+__global__ __launch_bounds__(256) void k_argmax(const float* logits, int32_t* out, int V) {
+    __shared__ unsigned long long red[256];
+    const float* l = logits + (size_t)blockIdx.x * V;
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < V; i += 256) {
+        const unsigned long long k = pack_best(l[i], i);
+        if (k > best) best = k;
+    }
+    red[threadIdx.x] = best;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s && red[threadIdx.x + s] > red[threadIdx.x])
+            red[threadIdx.x] = red[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFull));
+}
+
+__global__ void k_unpack_int4(const uint8_t* packed, uint8_t* codes, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint8_t b = packed[i >> 1];
+    codes[i] = (i & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 0x0F);
+}
+
+// One thread per (row, group): s = fp16(amax/7); q = clamp(roundf(w/s), -8, 7) + 8.
+__device__ inline void quantize_group(const float (&w)[32], int valid, uint8_t* dst,
+                                      uint16_t* sdst) {
+    float amax = 0.0f;
+    for (int j = 0; j < valid; ++j) amax = fmaxf(amax, fabsf(w[j]));
+    const uint16_t s16 = f2h_bits(__fdiv_rn(amax, 7.0f));
+    const float s = h2f_bits(s16);
+    uint32_t words[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        int q = 8;
+        if (j < valid && s != 0.0f) {
+            int r = (int)roundf(__fdiv_rn(w[j], s));
+            r = r < -8 ? -8 : (r > 7 ? 7 : r);
+            q = r + 8;
+        }
+        words[j >> 3] |= (uint32_t)q << (4 * (j & 7));
+    }
+    *reinterpret_cast<uint4*>(dst) = make_uint4(words[0], words[1], words[2], words[3]);
+    *sdst = s16;
+}
+
+__global__ void k_quantize_int4(const float* w, uint8_t* codes, uint16_t* scales, int N, int K) {
+    const int G = (K + 31) / 32;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)N * G) return;
+    const int n = (int)(t / G), g = (int)(t % G);
+    const int k0 = g * 32, valid = min(32, K - k0);
+    float v[32];
+    for (int j = 0; j < 32; ++j) v[j] = j < valid ? w[(size_t)n * K + k0 + j] : 0.0f;
+    quantize_group(v, valid, codes + ((size_t)n * G + g) * 16, scales + (size_t)n * G + g);
+}
+
+__global__ void k_gen_quant(uint8_t* codes, uint16_t* scales, int N, int K, uint64_t key, float kf,
+                            int row_offset, int row_stride) {
+    const int G = (K + 31) / 32;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)N * G) return;
+    const int n = (int)(t / G), g = (int)(t % G);
+    const int k0 = g * 32, valid = min(32, K - k0);
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        v[j] = j < valid ? normal_from(rand_at(key, (uint64_t)n * K + k0 + j), kf) : 0.0f;
+    const size_t row = (size_t)row_offset + (size_t)n * row_stride;
+    quantize_group(v, valid, codes + (row * G + g) * 16, scales + row * G + g);
+}
+
+__global__ void k_gen_f16(uint16_t* out, size_t n, uint64_t key, float kf) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f2h_bits(normal_from(rand_at(key, i), kf));
+}
+
+__device__ inline float ctx_value(uint64_t key, size_t idx, float kf, const int32_t* och,
+                                  int n_outlier, int d) {
+    float v = normal_from(rand_at(key, idx), kf);
+    for (int j = 0; j < n_outlier; ++j)
+        if (och[j] == d) v *= 10.0f;
+    return v;
+}
+
+// Thread per (b, p, kv, h, d).
+__global__ void k_gen_ctx_f16(uint16_t* kpool, uint16_t* vpool, const int32_t* block_table,
+                              int max_blocks, int batch, int ctx, int hkv, int hd, int L,
+                              uint64_t seed, float kf, const int32_t* outlier_ch, int n_outlier) {
+    const size_t per_pos = (size_t)2 * hkv * hd;
+    const size_t total = (size_t)batch * ctx * per_pos;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int b = (int)(t / ((size_t)ctx * per_pos));
+    const size_t r = t % ((size_t)ctx * per_pos);
+    const int p = (int)(r / per_pos);
+    const int r2 = (int)(r % per_pos);
+    const int kv = r2 / (hkv * hd), i = r2 % (hkv * hd);
+    const int h = i / hd, d = i % hd;
+    const uint64_t key = stream_key(seed, tid_ctx(L, b, kv));
+    const float v = ctx_value(key, (size_t)p * hkv * hd + i, kf,
+                              outlier_ch + ((size_t)kv * hkv + h) * n_outlier, n_outlier, d);
+    const int blk = block_table[(size_t)b * max_blocks + p / kPage];
+    const size_t off = (((size_t)blk * hkv + h) * kPage + p % kPage) * hd + d;
+    (kv ? vpool : kpool)[off] = f2h_bits(v);
+}
+
+__global__ void k_gen_ctx_raw(float* dst, int ctx, int hkv, int hd, uint64_t key, float kf,
+                              const int32_t* outlier_ch, int n_outlier) {
+    const size_t total = (size_t)ctx * hkv * hd;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int i = (int)(t % ((size_t)hkv * hd));
+    const int h = i / hd, d = i % hd;
+    dst[t] = ctx_value(key, t, kf, outlier_ch + (size_t)h * n_outlier, n_outlier, d);
+}
+
+// Block per sequence.
+__global__ __launch_bounds__(256) void k_embed(unsigned long long* best, int32_t* pos,
+                                               const int32_t* base, int32_t* out_tokens,
+                                               int out_stride, const uint16_t* embed, float* h,
+                                               int d, int vocab) {
+    __shared__ int tok_s;
+    const int b = blockIdx.x;
+    if (threadIdx.x == 0) {
+        const unsigned long long k = best[b];
+        int tok = (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+        if (tok < 0 || tok >= vocab) tok = 0;  // never index outside the table
+        tok_s = tok;
+        best[b] = 0ull;
+        const int p = pos[b] + 1;
+        pos[b] = p;
+        const int idx = p - base[b] - 1;
+        if (out_tokens && idx >= 0 && idx < out_stride) out_tokens[(size_t)b * out_stride + idx] = tok;
+    }
+    __syncthreads();
+    const int tok = tok_s;
+    for (int i = threadIdx.x; i < d; i += 256)
+        h[(size_t)b * d + i] = h2f_bits(embed[(size_t)tok * d + i]);
+}
+
+__global__ void k_finish_tokens(const unsigned long long* best, const int32_t* pos,
+                                const int32_t* base, int32_t* out_tokens, int out_stride,
+                                int batch) {
+    const int b = threadIdx.x;
+    if (b >= batch) return;
+    const int idx = pos[b] - base[b];
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)(best[b] & 0xFFFFFFFFull));
+    if (idx >= 0 && idx < out_stride) out_tokens[(size_t)b * out_stride + idx] = tok;
+}
+
+__global__ void k_set_tokens(unsigned long long* best, const int32_t* tokens, int batch) {
+    const int b = threadIdx.x;
+    if (b < batch) best[b] = 0xFFFFFFFFull - (unsigned long long)(uint32_t)tokens[b];
+}
+
+// Single block: thread b routes sequence b; thread 0 then builds the
+// per-expert token lists in (b, j) order.
+__global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
+    const int b = threadIdx.x;
+    if (b < a.batch) {
+        const float* lg = a.logits + (size_t)b * a.E;
+        float p[64];
+        float mx = lg[0];
+        for (int e = 1; e < a.E; ++e) mx = fmaxf(mx, lg[e]);
+        float sum = 0.0f;
+        for (int e = 0; e < a.E; ++e) {
+            p[e] = expf(lg[e] - mx);
+            sum += p[e];
+        }
+        if (sum > 0.0f)
+            for (int e = 0; e < a.E; ++e) p[e] = p[e] / sum;
+        unsigned long long taken = 0ull;
+        int ids[8];
+        float active = 0.0f;
+        for (int j = 0; j < a.k; ++j) {
+            int best = -1;
+            for (int e = 0; e < a.E; ++e)
+                if (!((taken >> e) & 1ull) && (best < 0 || p[e] > p[best])) best = e;
+            taken |= 1ull << best;
+            ids[j] = best;
+            active += p[best];
+        }
+        for (int j = 0; j < a.k; ++j) {
+            a.ids[(size_t)b * a.k + j] = ids[j];
+            a.weights[(size_t)b * a.k + j] = active > 0.0f ? p[ids[j]] / active : 1.0f / (float)a.k;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int e = 0; e < a.E; ++e) a.expert_count[e] = 0;
+        for (int bb = 0; bb < a.batch; ++bb)
+            for (int j = 0; j < a.k; ++j) {
+                const int e = a.ids[(size_t)bb * a.k + j];
+                a.expert_slots[(size_t)e * a.batch * a.k + a.expert_count[e]] = bb * a.k + j;
+                a.expert_count[e] += 1;
+            }
+    }
+}
+
+__global__ void k_moe_combine(const float* y32, const float* weights, float* out, int d, int k,
+                              int batch, int accumulate) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= batch * d) return;
+    const int b = t / d, i = t % d;
+    float acc = 0.0f;
+    for (int j = 0; j < k; ++j) acc += weights[(size_t)b * k + j] * y32[((size_t)b * k + j) * d + i];
+    out[t] = accumulate ? out[t] + acc : acc;
+}
+
+inline dim3 grid1(size_t n, int threads) { return dim3((unsigned)((n + threads - 1) / threads)); }
+
+}  // namespace
+
+hipError_t rmsnorm_launch(const float* x, const float* w, uint16_t* out, int dim, float eps,
+                          int batch, hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(batch), dim3(256), 0, st, x, w, out, dim, eps);
+    return hipGetLastError();
+}
+
+hipError_t rope_launch(float* x, const int32_t* pos, const float* cos_t, const float* sin_t,
+                       int heads, int hd, int batch, hipStream_t st) {
+    const size_t n = (size_t)batch * heads * (hd / 2);
+    hipLaunchKernelGGL(k_rope, grid1(n, 256), dim3(256), 0, st, x, pos, cos_t, sin_t, heads, hd,
+                       batch);
+    return hipGetLastError();
+}
+
+hipError_t swiglu_launch(const float* g, const float* u, uint16_t* out, int n, int batch,
+                         hipStream_t st) {
+    const size_t total = (size_t)n * batch;
+    hipLaunchKernelGGL(k_swiglu, grid1(total, 256), dim3(256), 0, st, g, u, out, total);
+    return hipGetLastError();
+}
+
+hipError_t residual_add_launch(const float* a, const float* b, float* out, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_residual_add, grid1(n, 256), dim3(256), 0, st, a, b, out, n);
+    return hipGetLastError();
+}
+
+hipError_t kv_append_f16_launch(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
+                                const int32_t* block_table, const int32_t* pos, int batch,
+                                int hkv, int hd, int max_blocks, hipStream_t st) {
+    const size_t n = (size_t)batch * hkv * hd;
+    hipLaunchKernelGGL(k_kv_append_f16, grid1(n, 256), dim3(256), 0, st, k, v, kpool, vpool,
+                       block_table, pos, batch, hkv, hd, max_blocks);
+    return hipGetLastError();
+}
+
+hipError_t argmax_launch(const float* logits, int32_t* out, int V, int batch, hipStream_t st) {
+    hipLaunchKernelGGL(k_argmax, dim3(batch), dim3(256), 0, st, logits, out, V);
+    return hipGetLastError();
+}
+
+hipError_t unpack_int4_launch(const uint8_t* packed, uint8_t* codes, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_unpack_int4, grid1(n, 256), dim3(256), 0, st, packed, codes, n);
+    return hipGetLastError();
+}
+
+hipError_t quantize_int4_launch(const float* w, uint8_t* codes, uint16_t* scales, int N, int K,
+                                hipStream_t st) {
+    const size_t n = (size_t)N * ((K + 31) / 32);
+    hipLaunchKernelGGL(k_quantize_int4, grid1(n, 256), dim3(256), 0, st, w, codes, scales, N, K);
+    return hipGetLastError();
+}
+
+hipError_t gen_quant_launch(uint8_t* codes, uint16_t* scales, int N, int K, uint64_t seed,
+                            uint32_t tid, float k, int row_offset, int row_stride,
+                            hipStream_t st) {
+    const size_t n = (size_t)N * ((K + 31) / 32);
+    hipLaunchKernelGGL(k_gen_quant, grid1(n, 256), dim3(256), 0, st, codes, scales, N, K,
+                       stream_key(seed, tid), k, row_offset, row_stride);
+    return hipGetLastError();
+}
+
+hipError_t gen_f16_launch(uint16_t* out, size_t n, uint64_t seed, uint32_t tid, float k,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_gen_f16, grid1(n, 256), dim3(256), 0, st, out, n, stream_key(seed, tid), k);
+    return hipGetLastError();
+}
+
+hipError_t gen_ctx_f16_launch(uint16_t* kpool, uint16_t* vpool, const int32_t* block_table,
+                              int max_blocks, int batch, int ctx, int hkv, int hd, int L,
+                              uint64_t seed, float k, const int32_t* outlier_ch, int n_outlier,
+                              hipStream_t st) {
+    const size_t n = (size_t)batch * ctx * 2 * hkv * hd;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gen_ctx_f16, grid1(n, 256), dim3(256), 0, st, kpool, vpool, block_table,
+                       max_blocks, batch, ctx, hkv, hd, L, seed, k, outlier_ch, n_outlier);
+    return hipGetLastError();
+}
+
+hipError_t gen_ctx_raw_launch(float* dst, int ctx, int hkv, int hd, int L, int b, int kv,
+                              uint64_t seed, float k, const int32_t* outlier_ch, int n_outlier,
+                              hipStream_t st) {
+    const size_t n = (size_t)ctx * hkv * hd;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gen_ctx_raw, grid1(n, 256), dim3(256), 0, st, dst, ctx, hkv, hd,
+                       stream_key(seed, tid_ctx(L, b, kv)), k, outlier_ch, n_outlier);
+    return hipGetLastError();
+}
+
+hipError_t embed_launch(unsigned long long* best, int32_t* pos, const int32_t* base,
+                        int32_t* out_tokens, int out_stride, const uint16_t* embed, float* h,
+                        int d, int vocab, int batch, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed, dim3(batch), dim3(256), 0, st, best, pos, base, out_tokens,
+                       out_stride, embed, h, d, vocab);
+    return hipGetLastError();
+}
+
+hipError_t finish_tokens_launch(const unsigned long long* best, const int32_t* pos,
+                                const int32_t* base, int32_t* out_tokens, int out_stride,
+                                int batch, hipStream_t st) {
+    hipLaunchKernelGGL(k_finish_tokens, dim3(1), dim3(64), 0, st, best, pos, base, out_tokens,
+                       out_stride, batch);
+    return hipGetLastError();
+}
+
+hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, int batch,
+                             hipStream_t st) {
+    hipLaunchKernelGGL(k_set_tokens, dim3(1), dim3(64), 0, st, best, tokens, batch);
+    return hipGetLastError();
+}
+
+hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st) {
+    if (a.batch > 64 || a.E > 64 || a.k > 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st) {
+    const size_t n = (size_t)a.batch * a.d;
+    hipLaunchKernelGGL(k_moe_combine, grid1(n, 256), dim3(256), 0, st, a.y32, a.weights, a.out,
+                       a.d, a.k, a.batch, a.accumulate);
+    return hipGetLastError();
+}
+
+}  // namespace nx

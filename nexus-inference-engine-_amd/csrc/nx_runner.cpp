@@ -1,0 +1,762 @@
+// Resident decode runner: the MI355X counterpart of HybridModel
+// (nexus/src/model/hybrid_model.cpp:319-774) for Llama-style dense and MoE
+// decoders.  All weights live in HBM (generated on the device from the
+// seed), the KV cache is paged (16-token pages, shuffled block table), and
+// one decode step -- embedding of the pending token, every layer, the
+// lm_head and the greedy argmax -- is a single captured HIP graph whose
+// kernels read the positions and the pending token from device memory, so
+// consecutive steps run back to back with no host round trip.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "nx_common.h"
+#include "nx_internal.h"
+#include "nx_kernels.h"
+
+using nx::fail;
+
+namespace {
+
+struct Layer {
+    uint8_t* wqkv = nullptr;  // [qdim + 2 kvdim][Gd*16]  rows: q | k | v
+    uint16_t* sqkv = nullptr;
+    uint8_t* wo = nullptr;    // [d][Gq*16]
+    uint16_t* so = nullptr;
+    uint8_t* w13 = nullptr;   // dense [2F][Gd*16] (gate/up interleaved) or experts [E][2F][Gd*16]
+    uint16_t* s13 = nullptr;
+    uint8_t* w2 = nullptr;    // dense [d][Gf*16] or experts [E][d][Gf*16]
+    uint16_t* s2 = nullptr;
+    uint8_t* wr = nullptr;    // router [E][Gd*16]
+    uint16_t* sr = nullptr;
+    uint16_t *kpool = nullptr, *vpool = nullptr;
+    uint8_t *kc4 = nullptr, *kc3 = nullptr, *vc4 = nullptr, *vc3 = nullptr;
+    uint16_t *kn = nullptr, *vn = nullptr;
+    float *ksign = nullptr, *vsign = nullptr;
+    int32_t* moe_count = nullptr;  // [E]
+};
+
+size_t qbytes(size_t N, int K) { return N * (size_t)((K + 31) / 32) * 18; }
+
+}  // namespace
+
+struct nx_model {
+    nx_ctx* ctx = nullptr;
+    nx_model_config c{};
+    int qdim = 0, kvdim = 0, nqkv = 0, Gd = 0, Gq = 0, Gf = 0, Fp = 0;
+    std::vector<void*> allocs;
+    uint16_t* embed = nullptr;
+    uint8_t* lm_w = nullptr;
+    uint16_t* lm_s = nullptr;
+    std::vector<Layer> layers;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    int max_blocks = 0, n_blocks = 0;
+    int32_t* block_table = nullptr;
+    int32_t *pos = nullptr, *base = nullptr, *out_tokens = nullptr, *prompt = nullptr;
+    unsigned long long* best = nullptr;
+    int out_stride = 0;
+    float* h = nullptr;
+    float* q = nullptr;
+    uint16_t* att16 = nullptr;
+    uint16_t* act16 = nullptr;
+    float* logits = nullptr;
+    float* kv_tmp = nullptr;
+    uint16_t* xn16 = nullptr;
+    float* router_logits = nullptr;
+    int32_t* moe_ids = nullptr;
+    float* moe_w = nullptr;
+    int32_t* moe_slots = nullptr;
+    uint16_t* moe_act = nullptr;
+    float* moe_y = nullptr;
+    float* attn_part = nullptr;
+    unsigned int* attn_counters = nullptr;
+    int32_t* h_stage = nullptr;  // pinned host staging [batch]
+    int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
+    hipGraphExec_t exec = nullptr;
+    std::vector<int> hpos;       // host mirror of pos (last processed position)
+};
+
+namespace {
+
+template <class T>
+nx_status dalloc(nx_model* m, T** out, size_t count) {
+    void* p = nullptr;
+    const size_t bytes = count * sizeof(T) > 0 ? count * sizeof(T) : 16;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return nx::hip_fail(m->ctx, e, "hipMalloc (model)");
+    m->allocs.push_back(p);
+    e = hipMemsetAsync(p, 0, bytes, m->ctx->stream);
+    if (e != hipSuccess) return nx::hip_fail(m->ctx, e, "hipMemsetAsync (model)");
+    *out = static_cast<T*>(p);
+    return NX_OK;
+}
+
+#define NX_TRY(expr)                      \
+    do {                                  \
+        nx_status nx_s_ = (expr);         \
+        if (nx_s_ != NX_OK) return nx_s_; \
+    } while (0)
+#define NX_LAUNCH(m, expr)                                                       \
+    do {                                                                         \
+        hipError_t nx_e_ = (expr);                                               \
+        if (nx_e_ != hipSuccess) return nx::hip_fail((m)->ctx, nx_e_, #expr);    \
+    } while (0)
+
+void host_shuffle(std::vector<int32_t>& perm, int n, uint64_t seed, uint32_t tid) {
+    perm.resize(n);
+    for (int i = 0; i < n; ++i) perm[i] = i;
+    const uint64_t key = nx::stream_key(seed, tid);
+    for (int i = n - 1; i >= 1; --i) {
+        const int j = (int)(nx::rand_at(key, (uint64_t)i) % (uint64_t)(i + 1));
+        std::swap(perm[i], perm[j]);
+    }
+}
+
+nx_status generate_weights(nx_model* m) {
+    const nx_model_config& c = m->c;
+    hipStream_t st = m->ctx->stream;
+    const uint64_t seed = c.seed;
+    const float k02 = nx::normal_k(0.02);
+    const int d = c.d_model, F = c.ffn, E = c.n_experts;
+    NX_LAUNCH(m, nx::gen_f16_launch(m->embed, (size_t)c.vocab * d, seed, nx::kTidEmbed, k02, st));
+    NX_LAUNCH(m, nx::gen_quant_launch(m->lm_w, m->lm_s, c.vocab, d, seed, nx::kTidLmHead, k02, 0, 1, st));
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = m->layers[L];
+        NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->qdim, d, seed, nx::tid_layer(L, nx::W_Q), k02, 0, 1, st));
+        NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->kvdim, d, seed, nx::tid_layer(L, nx::W_K), k02, m->qdim, 1, st));
+        NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->kvdim, d, seed, nx::tid_layer(L, nx::W_V), k02,
+                                          m->qdim + m->kvdim, 1, st));
+        NX_LAUNCH(m, nx::gen_quant_launch(ly.wo, ly.so, d, m->qdim, seed, nx::tid_layer(L, nx::W_O), k02, 0, 1, st));
+        if (E == 0) {
+            NX_LAUNCH(m, nx::gen_quant_launch(ly.w13, ly.s13, F, d, seed, nx::tid_layer(L, nx::W_GATE), k02, 0, 2, st));
+            NX_LAUNCH(m, nx::gen_quant_launch(ly.w13, ly.s13, F, d, seed, nx::tid_layer(L, nx::W_UP), k02, 1, 2, st));
+            NX_LAUNCH(m, nx::gen_quant_launch(ly.w2, ly.s2, d, F, seed, nx::tid_layer(L, nx::W_DOWN), k02, 0, 1, st));
+        } else {
+            NX_LAUNCH(m, nx::gen_quant_launch(ly.wr, ly.sr, E, d, seed, nx::tid_layer(L, nx::W_ROUTER),
+                                              nx::normal_k(1.0 / std::sqrt((double)d)), 0, 1, st));
+            for (int e = 0; e < E; ++e) {
+                NX_LAUNCH(m, nx::gen_quant_launch(ly.w13, ly.s13, F, d, seed, nx::tid_expert(L, e, 0), k02, e * 2 * F, 2, st));
+                NX_LAUNCH(m, nx::gen_quant_launch(ly.w13, ly.s13, F, d, seed, nx::tid_expert(L, e, 1), k02, e * 2 * F + 1, 2, st));
+                NX_LAUNCH(m, nx::gen_quant_launch(ly.w2, ly.s2, d, F, seed, nx::tid_expert(L, e, 2), k02, e * d, 1, st));
+            }
+        }
+    }
+    return NX_OK;
+}
+
+// One decode step for every sequence, enqueued on the context stream.
+nx_status enqueue_step(nx_model* m) {
+    const nx_model_config& c = m->c;
+    hipStream_t st = m->ctx->stream;
+    const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts;
+    NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d, c.vocab, B, st));
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = m->layers[L];
+        // RMSNorm + QKV + RoPE + paged KV append
+        nx::GemvArgs a{};
+        a.W = ly.wqkv;
+        a.S = ly.sqkv;
+        a.N = m->nqkv;
+        a.K = d;
+        a.G = m->Gd;
+        a.batch = B;
+        a.h32 = m->h;
+        a.ldx = d;
+        a.eps = c.eps;
+        a.q32 = m->q;
+        a.qdim = m->qdim;
+        a.kvdim = m->kvdim;
+        a.hd = c.head_dim;
+        a.hkv = c.n_kv_heads;
+        a.pos = m->pos;
+        a.cos_t = m->rope_cos;
+        a.sin_t = m->rope_sin;
+        a.block_table = m->block_table;
+        a.max_blocks = m->max_blocks;
+        if (c.kv_kind == 0) {
+            a.kpool = ly.kpool;
+            a.vpool = ly.vpool;
+        } else {
+            a.kv_tmp = m->kv_tmp;
+        }
+        NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_QKV, a, st));
+        if (c.kv_kind == 1)
+            NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr, ly.kc4,
+                                              ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table, m->pos,
+                                              m->max_blocks, st));
+        // attention
+        nx::AttnArgs at{};
+        at.q = m->q;
+        at.kpool = ly.kpool;
+        at.vpool = ly.vpool;
+        at.kc4 = ly.kc4;
+        at.kc3 = ly.kc3;
+        at.vc4 = ly.vc4;
+        at.vc3 = ly.vc3;
+        at.kn = ly.kn;
+        at.vn = ly.vn;
+        at.ksign = ly.ksign;
+        at.vsign = ly.vsign;
+        at.block_table = m->block_table;
+        at.ctx_lens = nullptr;
+        at.pos = m->pos;
+        at.out16 = m->att16;
+        at.batch = B;
+        at.hq = c.n_heads;
+        at.hkv = c.n_kv_heads;
+        at.hd = c.head_dim;
+        at.max_blocks = m->max_blocks;
+        at.max_ctx = c.max_seq;
+        at.part = m->attn_part;
+        at.counters = m->attn_counters;
+        NX_LAUNCH(m, c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st));
+        // output projection + residual
+        nx::GemvArgs o{};
+        o.W = ly.wo;
+        o.S = ly.so;
+        o.N = d;
+        o.K = m->qdim;
+        o.G = m->Gq;
+        o.batch = B;
+        o.x16 = m->att16;
+        o.ldx = m->qdim;
+        o.y32 = m->h;
+        o.ldy = d;
+        NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, o, st));
+        if (E == 0) {
+            // RMSNorm + gate/up + SwiGLU, then down + residual
+            nx::GemvArgs f{};
+            f.W = ly.w13;
+            f.S = ly.s13;
+            f.N = 2 * F;
+            f.K = d;
+            f.G = m->Gd;
+            f.batch = B;
+            f.h32 = m->h;
+            f.ldx = d;
+            f.eps = c.eps;
+            f.act16 = m->act16;
+            f.lda = m->Fp;
+            NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
+            nx::GemvArgs dn{};
+            dn.W = ly.w2;
+            dn.S = ly.s2;
+            dn.N = d;
+            dn.K = F;
+            dn.G = m->Gf;
+            dn.batch = B;
+            dn.x16 = m->act16;
+            dn.ldx = m->Fp;
+            dn.y32 = m->h;
+            dn.ldy = d;
+            NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, dn, st));
+        } else {
+            NX_LAUNCH(m, nx::rmsnorm_launch(m->h, nullptr, m->xn16, d, c.eps, B, st));
+            nx::GemvArgs r{};
+            r.W = ly.wr;
+            r.S = ly.sr;
+            r.N = E;
+            r.K = d;
+            r.G = m->Gd;
+            r.batch = B;
+            r.x16 = m->xn16;
+            r.ldx = d;
+            r.y32 = m->router_logits;
+            r.ldy = E;
+            NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_F32, r, st));
+            nx::MoeArgs ma{};
+            ma.logits = m->router_logits;
+            ma.E = E;
+            ma.k = c.top_k;
+            ma.batch = B;
+            ma.ids = m->moe_ids;
+            ma.weights = m->moe_w;
+            ma.expert_count = ly.moe_count;
+            ma.expert_slots = m->moe_slots;
+            NX_LAUNCH(m, nx::moe_route_launch(ma, st));
+            nx::MoeFfnArgs mf{};
+            mf.x16 = m->xn16;
+            mf.ldx = d;
+            mf.w13 = ly.w13;
+            mf.s13 = ly.s13;
+            mf.w2 = ly.w2;
+            mf.s2 = ly.s2;
+            mf.d = d;
+            mf.F = F;
+            mf.E = E;
+            mf.k = c.top_k;
+            mf.batch = B;
+            mf.expert_count = ly.moe_count;
+            mf.expert_slots = m->moe_slots;
+            mf.weights = m->moe_w;
+            mf.act16 = m->moe_act;
+            mf.y32 = m->moe_y;
+            mf.out = m->h;
+            mf.accumulate = 1;
+            NX_LAUNCH(m, nx::moe_gate_up_launch(mf, st));
+            NX_LAUNCH(m, nx::moe_down_launch(mf, st));
+            NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+        }
+    }
+    // final RMSNorm + lm_head + greedy argmax
+    nx::GemvArgs lm{};
+    lm.W = m->lm_w;
+    lm.S = m->lm_s;
+    lm.N = c.vocab;
+    lm.K = d;
+    lm.G = m->Gd;
+    lm.batch = B;
+    lm.h32 = m->h;
+    lm.ldx = d;
+    lm.eps = c.eps;
+    lm.y32 = m->logits;
+    lm.ldy = c.vocab;
+    lm.best = m->best;
+    NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_LOGITS, lm, st));
+    return NX_OK;
+}
+
+nx_status ensure_graph(nx_model* m) {
+    if (m->exec) return NX_OK;
+    hipStream_t st = m->ctx->stream;
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    NX_HIP(m->ctx, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    nx_status s = enqueue_step(m);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(st, &g);
+    if (s != NX_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return s;
+    }
+    if (e != hipSuccess) return nx::hip_fail(m->ctx, e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        m->exec = nullptr;
+        return nx::hip_fail(m->ctx, e, "hipGraphInstantiate (decode step)");
+    }
+    return NX_OK;
+}
+
+nx_status free_model(nx_model* m) {
+    if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    for (void* p : m->allocs) (void)hipFree(p);
+    if (m->h_stage) (void)hipHostFree(m->h_stage);
+    if (m->h_out) (void)hipHostFree(m->h_out);
+    delete m;
+    return NX_OK;
+}
+
+nx_status create_impl(nx_model* m) {
+    const nx_model_config& c = m->c;
+    const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts, L = c.n_layers;
+    m->qdim = c.n_heads * c.head_dim;
+    m->kvdim = c.n_kv_heads * c.head_dim;
+    m->nqkv = m->qdim + 2 * m->kvdim;
+    m->Gd = (d + 31) / 32;
+    m->Gq = (m->qdim + 31) / 32;
+    m->Gf = (F + 31) / 32;
+    m->Fp = m->Gf * 32;
+    m->max_blocks = c.max_seq / nx::kPage;
+    m->n_blocks = m->max_blocks * B;
+    m->out_stride = c.max_seq;
+    m->layers.resize(L);
+    m->hpos.assign(B, -1);
+
+    NX_TRY(dalloc(m, &m->embed, (size_t)c.vocab * d));
+    NX_TRY(dalloc(m, &m->lm_w, (size_t)c.vocab * m->Gd * 16));
+    NX_TRY(dalloc(m, &m->lm_s, (size_t)c.vocab * m->Gd));
+    const size_t pool_elems = (size_t)m->n_blocks * c.n_kv_heads * nx::kPage * c.head_dim;
+    const size_t pool_vecs = (size_t)m->n_blocks * c.n_kv_heads * nx::kPage;
+    for (int l = 0; l < L; ++l) {
+        Layer& ly = m->layers[l];
+        NX_TRY(dalloc(m, &ly.wqkv, (size_t)m->nqkv * m->Gd * 16));
+        NX_TRY(dalloc(m, &ly.sqkv, (size_t)m->nqkv * m->Gd));
+        NX_TRY(dalloc(m, &ly.wo, (size_t)d * m->Gq * 16));
+        NX_TRY(dalloc(m, &ly.so, (size_t)d * m->Gq));
+        const size_t ne = E == 0 ? 1 : (size_t)E;
+        NX_TRY(dalloc(m, &ly.w13, ne * 2 * F * m->Gd * 16));
+        NX_TRY(dalloc(m, &ly.s13, ne * 2 * F * m->Gd));
+        NX_TRY(dalloc(m, &ly.w2, ne * d * m->Gf * 16));
+        NX_TRY(dalloc(m, &ly.s2, ne * d * m->Gf));
+        if (E > 0) {
+            NX_TRY(dalloc(m, &ly.wr, (size_t)E * m->Gd * 16));
+            NX_TRY(dalloc(m, &ly.sr, (size_t)E * m->Gd));
+            NX_TRY(dalloc(m, &ly.moe_count, (size_t)E));
+        }
+        if (c.kv_kind == 0) {
+            NX_TRY(dalloc(m, &ly.kpool, pool_elems));
+            NX_TRY(dalloc(m, &ly.vpool, pool_elems));
+        } else {
+            NX_TRY(dalloc(m, &ly.kc4, pool_vecs * 32));
+            NX_TRY(dalloc(m, &ly.kc3, pool_vecs * 24));
+            NX_TRY(dalloc(m, &ly.vc4, pool_vecs * 32));
+            NX_TRY(dalloc(m, &ly.vc3, pool_vecs * 24));
+            NX_TRY(dalloc(m, &ly.kn, pool_vecs));
+            NX_TRY(dalloc(m, &ly.vn, pool_vecs));
+        }
+        NX_TRY(dalloc(m, &ly.ksign, 128));
+        NX_TRY(dalloc(m, &ly.vsign, 128));
+        float sg[2][128];
+        for (int kv = 0; kv < 2; ++kv) {
+            const uint64_t key = nx::stream_key(c.seed, nx::tid_layer(l, kv ? nx::TQ_VSIGN : nx::TQ_KSIGN));
+            for (int i = 0; i < 128; ++i) sg[kv][i] = (nx::rand_at(key, (uint64_t)i) & 1u) ? -1.0f : 1.0f;
+        }
+        NX_HIP(m->ctx, hipMemcpyAsync(ly.ksign, sg[0], sizeof(sg[0]), hipMemcpyHostToDevice, m->ctx->stream));
+        NX_HIP(m->ctx, hipMemcpyAsync(ly.vsign, sg[1], sizeof(sg[1]), hipMemcpyHostToDevice, m->ctx->stream));
+        NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    }
+    // rope tables
+    {
+        const int half = c.head_dim / 2;
+        std::vector<float> cs((size_t)c.max_seq * half), sn((size_t)c.max_seq * half);
+        for (int p = 0; p < c.max_seq; ++p)
+            for (int i = 0; i < half; ++i) {
+                const double inv_freq = std::pow((double)c.rope_theta, -(2.0 * i) / (double)c.head_dim);
+                const double ang = (double)p * inv_freq;
+                cs[(size_t)p * half + i] = (float)std::cos(ang);
+                sn[(size_t)p * half + i] = (float)std::sin(ang);
+            }
+        NX_TRY(dalloc(m, &m->rope_cos, cs.size()));
+        NX_TRY(dalloc(m, &m->rope_sin, sn.size()));
+        NX_HIP(m->ctx, hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
+        NX_HIP(m->ctx, hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
+        NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    }
+    // block table: a seeded permutation of the pool, max_blocks per sequence
+    {
+        std::vector<int32_t> perm;
+        host_shuffle(perm, m->n_blocks, c.seed, nx::kTidShuffle);
+        NX_TRY(dalloc(m, &m->block_table, perm.size()));
+        NX_HIP(m->ctx, hipMemcpyAsync(m->block_table, perm.data(), perm.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
+        NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    }
+    NX_TRY(dalloc(m, &m->pos, B));
+    NX_TRY(dalloc(m, &m->base, B));
+    NX_TRY(dalloc(m, &m->best, B));
+    NX_TRY(dalloc(m, &m->out_tokens, (size_t)B * m->out_stride));
+    NX_TRY(dalloc(m, &m->prompt, (size_t)B * c.max_seq));
+    NX_TRY(dalloc(m, &m->h, (size_t)B * d));
+    NX_TRY(dalloc(m, &m->q, (size_t)B * m->qdim));
+    NX_TRY(dalloc(m, &m->att16, (size_t)B * m->qdim));
+    NX_TRY(dalloc(m, &m->act16, (size_t)B * m->Fp));
+    NX_TRY(dalloc(m, &m->logits, (size_t)B * c.vocab));
+    NX_TRY(dalloc(m, &m->kv_tmp, (size_t)B * 2 * m->kvdim));
+    NX_TRY(dalloc(m, &m->xn16, (size_t)B * d));
+    if (E > 0) {
+        NX_TRY(dalloc(m, &m->router_logits, (size_t)B * E));
+        NX_TRY(dalloc(m, &m->moe_ids, (size_t)B * c.top_k));
+        NX_TRY(dalloc(m, &m->moe_w, (size_t)B * c.top_k));
+        NX_TRY(dalloc(m, &m->moe_slots, (size_t)E * B * c.top_k));
+        NX_TRY(dalloc(m, &m->moe_act, (size_t)B * c.top_k * m->Fp));
+        NX_TRY(dalloc(m, &m->moe_y, (size_t)B * c.top_k * d));
+    }
+    NX_TRY(dalloc(m, &m->attn_part,
+                  nx::attn_workspace_bytes(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq) / 4 + 1));
+    NX_TRY(dalloc(m, &m->attn_counters, nx::attn_counter_count(B, c.n_kv_heads)));
+    {
+        std::vector<int32_t> minus1(B, -1);
+        NX_HIP(m->ctx, hipMemcpyAsync(m->pos, minus1.data(), (size_t)B * 4, hipMemcpyHostToDevice, m->ctx->stream));
+        NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    }
+    NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_stage, sizeof(int32_t) * B, hipHostMallocDefault));
+    NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_out, sizeof(int32_t) * (size_t)B * m->out_stride, hipHostMallocDefault));
+    NX_TRY(generate_weights(m));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return NX_OK;
+}
+
+nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
+    if (c.n_layers < 1 || c.d_model < 32 || c.n_heads < 1 || c.n_kv_heads < 1 || c.n_heads % c.n_kv_heads ||
+        c.ffn < 2 || c.vocab < 2 || c.max_seq < nx::kPage || c.max_seq % nx::kPage || c.batch < 1 || c.batch > 8 ||
+        (c.kv_kind != 0 && c.kv_kind != 1) || c.eps <= 0.0f || c.rope_theta <= 0.0f)
+        return fail(ctx, NX_ERR_INVALID, "nx_model_create: invalid configuration");
+    const int G = c.n_heads / c.n_kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return fail(ctx, NX_ERR_UNSUPPORTED, "hq/hkv must be 1, 2, 4 or 8");
+    if (c.head_dim != 64 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+    if (c.kv_kind == 1 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
+    if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
+    if (c.d_model > 14336 || c.ffn > 14336 || c.n_heads * c.head_dim > 14336)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "GEMV K above 14336");
+    if (c.n_experts < 0 || c.n_experts > 64 || (c.n_experts > 0 && (c.top_k < 1 || c.top_k > 8 || c.top_k > c.n_experts)))
+        return fail(ctx, NX_ERR_INVALID, "invalid expert configuration");
+    return NX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+nx_status nx_model_create(nx_ctx* ctx, const nx_model_config* cfg, nx_model** out) {
+    if (!ctx || !cfg || !out) return NX_ERR_INVALID;
+    *out = nullptr;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_model_create inside a token batch");
+    NX_TRY(check_config(ctx, *cfg));
+    nx_model* m = new nx_model();
+    m->ctx = ctx;
+    m->c = *cfg;
+    nx_status s = create_impl(m);
+    if (s != NX_OK) {
+        free_model(m);
+        return s;
+    }
+    *out = m;
+    return NX_OK;
+}
+
+nx_status nx_model_destroy(nx_model* m) {
+    if (!m) return NX_ERR_INVALID;
+    return free_model(m);
+}
+
+nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens) {
+    if (!m || !prompt || P < 1) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    const int B = c.batch;
+    for (int b = 0; b < B; ++b) {
+        if (m->hpos[b] + P >= c.max_seq) return fail(m->ctx, NX_ERR_CAPACITY, "prefill exceeds max_seq");
+        for (int i = 0; i < P; ++i)
+            if (prompt[(size_t)b * P + i] < 0 || prompt[(size_t)b * P + i] >= c.vocab)
+                return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
+    }
+    NX_TRY(ensure_graph(m));
+    hipStream_t st = m->ctx->stream;
+    // token-major copy of the prompt: prompt_dev[i][b]
+    std::vector<int32_t> tm((size_t)P * B);
+    for (int b = 0; b < B; ++b)
+        for (int i = 0; i < P; ++i) tm[(size_t)i * B + b] = prompt[(size_t)b * P + i];
+    NX_HIP(m->ctx, hipMemcpyAsync(m->prompt, tm.data(), tm.size() * 4, hipMemcpyHostToDevice, st));
+    // nothing is recorded while prefilling
+    for (int b = 0; b < B; ++b) m->h_stage[b] = 1 << 30;
+    NX_HIP(m->ctx, hipMemcpyAsync(m->base, m->h_stage, (size_t)B * 4, hipMemcpyHostToDevice, st));
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    for (int i = 0; i < P; ++i) {
+        NX_LAUNCH(m, nx::set_tokens_launch(m->best, m->prompt + (size_t)i * B, B, st));
+        NX_HIP(m->ctx, hipGraphLaunch(m->exec, st));
+    }
+    std::vector<unsigned long long> best(B);
+    NX_HIP(m->ctx, hipMemcpyAsync(best.data(), m->best, (size_t)B * 8, hipMemcpyDeviceToHost, st));
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    for (int b = 0; b < B; ++b) {
+        m->hpos[b] += P;
+        if (next_tokens) next_tokens[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)(best[b] & 0xFFFFFFFFull));
+    }
+    return NX_OK;
+}
+
+nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
+    if (!m) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    if (ctx_len < 1 || ctx_len >= c.max_seq) return fail(m->ctx, NX_ERR_CAPACITY, "context must leave room in max_seq");
+    if (n_outlier < 0 || n_outlier > 16 || n_outlier > c.head_dim) return fail(m->ctx, NX_ERR_INVALID, "n_outlier out of range");
+    hipStream_t st = m->ctx->stream;
+    const int hkv = c.n_kv_heads, hd = c.head_dim, B = c.batch;
+    const float k1 = nx::normal_k(1.0);
+    int32_t* och = nullptr;
+    NX_TRY(dalloc(m, &och, (size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1)));
+    float* raw = nullptr;
+    if (c.kv_kind == 1) NX_TRY(dalloc(m, &raw, (size_t)ctx_len * hkv * hd));
+    std::vector<int32_t> ho((size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1));
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = m->layers[L];
+        for (int kv = 0; kv < 2; ++kv)
+            for (int h = 0; h < hkv; ++h) {
+                std::vector<int32_t> perm;
+                host_shuffle(perm, hd, c.seed, nx::tid_outlier(L, kv, h));
+                for (int j = 0; j < n_outlier; ++j) ho[((size_t)kv * hkv + h) * n_outlier + j] = perm[j];
+            }
+        NX_HIP(m->ctx, hipMemcpyAsync(och, ho.data(), ho.size() * 4, hipMemcpyHostToDevice, st));
+        if (c.kv_kind == 0) {
+            NX_LAUNCH(m, nx::gen_ctx_f16_launch(ly.kpool, ly.vpool, m->block_table, m->max_blocks, B, ctx_len, hkv, hd, L,
+                                                c.seed, k1, och, n_outlier, st));
+        } else {
+            for (int b = 0; b < B; ++b)
+                for (int kv = 0; kv < 2; ++kv) {
+                    NX_LAUNCH(m, nx::gen_ctx_raw_launch(raw, ctx_len, hkv, hd, L, b, kv, c.seed, k1,
+                                                        och + (size_t)kv * hkv * n_outlier, n_outlier, st));
+                    NX_LAUNCH(m, nx::tq_encode_ctx_launch(raw, ctx_len, hkv, kv ? ly.vsign : ly.ksign, nullptr, nullptr,
+                                                          kv ? ly.vc4 : ly.kc4, kv ? ly.vc3 : ly.kc3, kv ? ly.vn : ly.kn,
+                                                          m->block_table, m->max_blocks, b, st));
+                }
+        }
+        NX_HIP(m->ctx, hipStreamSynchronize(st));
+    }
+    // positions and the seeded start tokens
+    std::vector<int32_t> p(B, ctx_len - 1), start(B);
+    const uint64_t key = nx::stream_key(c.seed, nx::kTidStart);
+    for (int b = 0; b < B; ++b) start[b] = (int32_t)(nx::rand_at(key, (uint64_t)b) % (uint64_t)c.vocab);
+    NX_HIP(m->ctx, hipMemcpyAsync(m->pos, p.data(), (size_t)B * 4, hipMemcpyHostToDevice, st));
+    NX_HIP(m->ctx, hipMemcpyAsync(m->prompt, start.data(), (size_t)B * 4, hipMemcpyHostToDevice, st));
+    NX_LAUNCH(m, nx::set_tokens_launch(m->best, m->prompt, B, st));
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    for (int b = 0; b < B; ++b) m->hpos[b] = ctx_len - 1;
+    // the scratch buffers are released with the model; drop them now
+    for (void* ptr : {static_cast<void*>(och), static_cast<void*>(raw)}) {
+        if (!ptr) continue;
+        for (auto it = m->allocs.begin(); it != m->allocs.end(); ++it)
+            if (*it == ptr) {
+                (void)hipFree(ptr);
+                m->allocs.erase(it);
+                break;
+            }
+    }
+    return NX_OK;
+}
+
+nx_status nx_model_pending(nx_model* m, int32_t* tokens) {
+    if (!m || !tokens) return NX_ERR_INVALID;
+    std::vector<unsigned long long> best(m->c.batch);
+    NX_HIP(m->ctx, hipMemcpyAsync(best.data(), m->best, best.size() * 8, hipMemcpyDeviceToHost, m->ctx->stream));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    for (int b = 0; b < m->c.batch; ++b) tokens[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)(best[b] & 0xFFFFFFFFull));
+    return NX_OK;
+}
+
+nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
+    if (!m || steps < 1) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    const int B = c.batch;
+    for (int b = 0; b < B; ++b) {
+        if (m->hpos[b] < 0) return fail(m->ctx, NX_ERR_STATE, "decode before prefill or fill_context");
+        if (m->hpos[b] + steps >= c.max_seq) return fail(m->ctx, NX_ERR_CAPACITY, "decode exceeds max_seq");
+    }
+    if (steps > m->out_stride) return fail(m->ctx, NX_ERR_CAPACITY, "too many steps for one call");
+    NX_TRY(ensure_graph(m));
+    hipStream_t st = m->ctx->stream;
+    for (int b = 0; b < B; ++b) m->h_stage[b] = m->hpos[b] + 1;
+    NX_HIP(m->ctx, hipMemcpyAsync(m->base, m->h_stage, (size_t)B * 4, hipMemcpyHostToDevice, st));
+    for (int s = 0; s < steps; ++s) NX_HIP(m->ctx, hipGraphLaunch(m->exec, st));
+    NX_LAUNCH(m, nx::finish_tokens_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, B, st));
+    if (out_tokens)
+        NX_HIP(m->ctx, hipMemcpyAsync(m->h_out, m->out_tokens, (size_t)B * m->out_stride * 4, hipMemcpyDeviceToHost, st));
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    for (int b = 0; b < B; ++b) {
+        m->hpos[b] += steps;
+        if (out_tokens)
+            std::memcpy(out_tokens + (size_t)b * steps, m->h_out + (size_t)b * m->out_stride, (size_t)steps * 4);
+    }
+    return NX_OK;
+}
+
+nx_status nx_model_logits(nx_model* m, float* out) {
+    if (!m || !out) return NX_ERR_INVALID;
+    NX_HIP(m->ctx, hipMemcpyAsync(out, m->logits, (size_t)m->c.batch * m->c.vocab * 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return NX_OK;
+}
+
+nx_status nx_model_position(nx_model* m, int b, int* p) {
+    if (!m || !p || b < 0 || b >= m->c.batch) return NX_ERR_INVALID;
+    *p = m->hpos[b];
+    return NX_OK;
+}
+
+nx_status nx_model_step_bytes(nx_model* m, double* bytes) {
+    if (!m || !bytes) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    const int d = c.d_model, F = c.ffn, E = c.n_experts, B = c.batch;
+    double w = (double)qbytes(c.vocab, d);  // lm_head
+    for (int L = 0; L < c.n_layers; ++L) {
+        w += (double)qbytes(m->nqkv, d) + (double)qbytes(d, m->qdim);
+        if (E == 0) {
+            w += (double)qbytes(2 * (size_t)F, d) + (double)qbytes(d, F);
+        } else {
+            std::vector<int32_t> cnt(E, 0);
+            NX_HIP(m->ctx, hipMemcpy(cnt.data(), m->layers[L].moe_count, (size_t)E * 4, hipMemcpyDeviceToHost));
+            int active = 0;
+            for (int e = 0; e < E; ++e) active += cnt[e] > 0;
+            if (active == 0) active = c.top_k;  // before the first step
+            w += (double)qbytes(E, d) + active * ((double)qbytes(2 * (size_t)F, d) + (double)qbytes(d, F));
+        }
+    }
+    double kv = 0.0;
+    const double per_tok = c.kv_kind == 0 ? 2.0 * c.n_kv_heads * c.head_dim * 2 : 2.0 * c.n_kv_heads * 58;
+    for (int b = 0; b < B; ++b) kv += (double)(m->hpos[b] + 1) * per_tok;
+    *bytes = w + kv * c.n_layers;
+    return NX_OK;
+}
+
+nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double* bytes) {
+    if (!m || !avg_ms || iters < 1) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    if (c.n_experts != 0) return fail(m->ctx, NX_ERR_UNSUPPORTED, "dense models only");
+    hipStream_t st = m->ctx->stream;
+    Layer& ly = m->layers[0];
+    nx::GemvArgs f{};
+    f.W = ly.w13;
+    f.S = ly.s13;
+    f.N = 2 * c.ffn;
+    f.K = c.d_model;
+    f.G = m->Gd;
+    f.batch = c.batch;
+    f.h32 = m->h;
+    f.ldx = c.d_model;
+    f.eps = c.eps;
+    f.act16 = m->act16;
+    f.lda = m->Fp;
+    NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
+    NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
+    for (int i = 0; i < iters; ++i) NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
+    NX_HIP(m->ctx, hipEventRecord(m->ctx->ev1, st));
+    NX_HIP(m->ctx, hipEventSynchronize(m->ctx->ev1));
+    float ms = 0.0f;
+    NX_HIP(m->ctx, hipEventElapsedTime(&ms, m->ctx->ev0, m->ctx->ev1));
+    *avg_ms = (double)ms / iters;
+    if (bytes)
+        *bytes = (double)qbytes(2 * (size_t)c.ffn, c.d_model) +
+                 (double)c.batch * (4.0 * c.d_model + 2.0 * c.ffn);
+    return NX_OK;
+}
+
+nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double* bytes) {
+    if (!m || !avg_ms || iters < 1) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    for (int b = 0; b < c.batch; ++b)
+        if (m->hpos[b] < 0) return fail(m->ctx, NX_ERR_STATE, "no context to attend over");
+    hipStream_t st = m->ctx->stream;
+    Layer& ly = m->layers[0];
+    nx::AttnArgs at{};
+    at.q = m->q;
+    at.kpool = ly.kpool;
+    at.vpool = ly.vpool;
+    at.kc4 = ly.kc4;
+    at.kc3 = ly.kc3;
+    at.vc4 = ly.vc4;
+    at.vc3 = ly.vc3;
+    at.kn = ly.kn;
+    at.vn = ly.vn;
+    at.ksign = ly.ksign;
+    at.vsign = ly.vsign;
+    at.block_table = m->block_table;
+    at.pos = m->pos;
+    at.out16 = m->att16;
+    at.batch = c.batch;
+    at.hq = c.n_heads;
+    at.hkv = c.n_kv_heads;
+    at.hd = c.head_dim;
+    at.max_blocks = m->max_blocks;
+    at.max_ctx = c.max_seq;
+    at.part = m->attn_part;
+    at.counters = m->attn_counters;
+    auto launch = [&]() { return c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st); };
+    NX_LAUNCH(m, launch());
+    NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
+    for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch());
+    NX_HIP(m->ctx, hipEventRecord(m->ctx->ev1, st));
+    NX_HIP(m->ctx, hipEventSynchronize(m->ctx->ev1));
+    float ms = 0.0f;
+    NX_HIP(m->ctx, hipEventElapsedTime(&ms, m->ctx->ev0, m->ctx->ev1));
+    *avg_ms = (double)ms / iters;
+    if (bytes) {
+        const double per_tok = c.kv_kind == 0 ? 2.0 * c.n_kv_heads * c.head_dim * 2 : 2.0 * c.n_kv_heads * 58;
+        double kv = 0.0;
+        for (int b = 0; b < c.batch; ++b) kv += (double)(m->hpos[b] + 1) * per_tok;
+        *bytes = kv;
+    }
+    return NX_OK;
+}
+
+}  // extern "C"

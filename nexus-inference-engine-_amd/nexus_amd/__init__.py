@@ -1,0 +1,273 @@
+"""ctypes binding of libnexus_hip.so, the gfx950 decode-loop library.
+
+This mirrors the C-ABI in include/nexus_hip.h one to one.  Device memory is
+owned by a Context (nx_buf handles); numpy arrays are copied in and out with
+upload()/download().  There is no CPU fallback: if the library is missing or
+no gfx950 device is present, the constructors raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+ROOT = PKG_DIR.parent
+LIB_PATH = PKG_DIR / "libnexus_hip.so"
+HEADER = ROOT.parent / "include" / "nexus_hip.h"
+
+NX_OK = 0
+STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "OOM", 4: "UNSUPPORTED", 5: "STATE",
+          6: "NO_DEVICE", 7: "CAPACITY"}
+
+
+class NxError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"nx error {STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+def build(jobs: int = 8) -> None:
+    """Compile libnexus_hip.so for gfx950 in place."""
+    subprocess.run(["make", "-s", "-j", str(jobs), "-B", "-C", str(ROOT)], check=True)
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("d_model", C.c_int), ("n_heads", C.c_int),
+        ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
+        ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
+        ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
+        ("seed", C.c_uint64),
+    ]
+
+
+_B = C.c_uint64  # nx_buf
+_P = C.c_void_p
+_I = C.c_int
+_F = C.c_float
+_SIGS = {
+    "nx_init": (_I, [C.POINTER(_P), _I]),
+    "nx_destroy": (_I, [_P]),
+    "nx_has_gpu": (_I, []),
+    "nx_device_name": (_I, [_P, C.c_char_p, C.c_size_t]),
+    "nx_last_error": (C.c_char_p, [_P]),
+    "nx_init_error": (C.c_char_p, []),
+    "nx_alloc": (_I, [_P, C.c_size_t, C.POINTER(_B)]),
+    "nx_free": (_I, [_P, _B]),
+    "nx_upload": (_I, [_P, _B, C.c_size_t, _P, C.c_size_t]),
+    "nx_download": (_I, [_P, _P, _B, C.c_size_t, C.c_size_t]),
+    "nx_weight_cache": (_I, [_P, _P, _P, C.c_size_t, C.POINTER(_B)]),
+    "nx_get_cached_buffer": (_I, [_P, _P, C.POINTER(_B)]),
+    "nx_clear_buffer_cache": (_I, [_P]),
+    "nx_buffer_size": (_I, [_P, _B, C.POINTER(C.c_size_t)]),
+    "nx_synchronize": (_I, [_P]),
+    "nx_token_begin": (_I, [_P]),
+    "nx_token_end": (_I, [_P]),
+    "nx_gemv_int4_g32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I]),
+    "nx_gemv_int4_g32_f32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I]),
+    "nx_unpack_int4": (_I, [_P, _B, _B, C.c_size_t]),
+    "nx_quantize_int4_g32": (_I, [_P, _B, _B, _B, _I, _I]),
+    "nx_rmsnorm": (_I, [_P, _B, _B, _B, _I, _F, _I]),
+    "nx_rope": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I]),
+    "nx_swiglu": (_I, [_P, _B, _B, _B, _I, _I]),
+    "nx_residual_add": (_I, [_P, _B, _B, _B, _I]),
+    "nx_kv_append_f16": (_I, [_P, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I]),
+    "nx_attn_decode_paged_f16": (_I, [_P, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I, _I]),
+    "nx_tq_codebooks": (_I, [_P, _P, _P, _P]),
+    "nx_tq_encode": (_I, [_P, _B, _B, _B, _B, _B, _I]),
+    "nx_tq_append": (_I, [_P, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I]),
+    "nx_attn_decode_paged_tq": (_I, [_P, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _I, _I,
+                                     _I, _I, _I]),
+    "nx_moe_route_topk": (_I, [_P, _B, _B, _B, _I, _I, _I]),
+    "nx_moe_expert_ffn": (_I, [_P, _B, _B, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I, _I]),
+    "nx_argmax": (_I, [_P, _B, _B, _I, _I]),
+    "nx_model_create": (_I, [_P, C.POINTER(ModelConfig), C.POINTER(_P)]),
+    "nx_model_destroy": (_I, [_P]),
+    "nx_model_prefill": (_I, [_P, _P, _I, _P]),
+    "nx_model_fill_context": (_I, [_P, _I, _I]),
+    "nx_model_pending": (_I, [_P, _P]),
+    "nx_model_decode": (_I, [_P, _I, _P]),
+    "nx_model_logits": (_I, [_P, _P]),
+    "nx_model_position": (_I, [_P, _I, C.POINTER(_I)]),
+    "nx_model_step_bytes": (_I, [_P, C.POINTER(C.c_double)]),
+    "nx_model_time_ffn_gemv": (_I, [_P, _I, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "nx_time_gemv": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I, C.POINTER(C.c_double)]),
+    "nx_model_time_attention": (_I, [_P, _I, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libnexus_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with `make -C {ROOT}` "
+                "(there is no CPU fallback)")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def has_gpu() -> bool:
+    return bool(lib().nx_has_gpu())
+
+
+def tq_codebooks():
+    c4 = np.empty(16, np.float32)
+    b4 = np.empty(15, np.float32)
+    c3 = np.empty(8, np.float32)
+    b3 = np.empty(7, np.float32)
+    st = lib().nx_tq_codebooks(c4.ctypes.data, b4.ctypes.data, c3.ctypes.data, b3.ctypes.data)
+    if st != NX_OK:
+        raise NxError(st, "nx_tq_codebooks")
+    return c4, b4, c3, b3
+
+
+class Context:
+    """An nx_ctx on one gfx950 device."""
+
+    def __init__(self, device: int = 0):
+        L = lib()
+        h = C.c_void_p()
+        st = L.nx_init(C.byref(h), device)
+        if st != NX_OK:
+            raise NxError(st, L.nx_init_error().decode())
+        self.h = h
+        self.L = L
+        self._bufs: dict[int, tuple] = {}
+
+    # ------------------------------------------------------------ helpers --
+    def check(self, st: int, what: str = ""):
+        if st != NX_OK:
+            raise NxError(st, f"{what}: {self.L.nx_last_error(self.h).decode()}")
+
+    def close(self):
+        if self.h:
+            self.L.nx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def device_name(self) -> str:
+        buf = C.create_string_buffer(256)
+        self.check(self.L.nx_device_name(self.h, buf, 256), "nx_device_name")
+        return buf.value.decode()
+
+    def alloc(self, nbytes: int) -> int:
+        b = C.c_uint64()
+        self.check(self.L.nx_alloc(self.h, int(nbytes), C.byref(b)), "nx_alloc")
+        return b.value
+
+    def free(self, b: int):
+        self.check(self.L.nx_free(self.h, b), "nx_free")
+
+    def upload(self, arr: np.ndarray, buf: int | None = None) -> int:
+        a = np.ascontiguousarray(arr)
+        if buf is None:
+            buf = self.alloc(max(a.nbytes, 1))
+        self.check(self.L.nx_upload(self.h, buf, 0, a.ctypes.data, a.nbytes), "nx_upload")
+        return buf
+
+    def download(self, buf: int, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self.check(self.L.nx_download(self.h, out.ctypes.data, buf, 0, out.nbytes), "nx_download")
+        return out
+
+    def sync(self):
+        self.check(self.L.nx_synchronize(self.h), "nx_synchronize")
+
+    # ---------------------------------------------------------------- ops --
+    def gemv(self, x, wq, sc, y, N, K, batch=1):
+        self.check(self.L.nx_gemv_int4_g32(self.h, x, wq, sc, y, N, K, batch), "nx_gemv_int4_g32")
+
+    def gemv_f32(self, x, wq, sc, y, N, K, batch=1, accumulate=False):
+        self.check(self.L.nx_gemv_int4_g32_f32(self.h, x, wq, sc, y, N, K, batch, int(accumulate)),
+                   "nx_gemv_int4_g32_f32")
+
+
+class Model:
+    """An nx_model (the resident decode runner)."""
+
+    def __init__(self, ctx: Context, **cfg):
+        self.ctx = ctx
+        self.cfg = ModelConfig(**cfg)
+        h = C.c_void_p()
+        ctx.check(ctx.L.nx_model_create(ctx.h, C.byref(self.cfg), C.byref(h)), "nx_model_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.ctx.L.nx_model_destroy(self.h)
+            self.h = None
+
+    def prefill(self, prompt: np.ndarray) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.int32).reshape(self.cfg.batch, -1)
+        nxt = np.empty(self.cfg.batch, np.int32)
+        self.ctx.check(self.ctx.L.nx_model_prefill(self.h, p.ctypes.data, p.shape[1], nxt.ctypes.data),
+                       "nx_model_prefill")
+        return nxt
+
+    def fill_context(self, ctx_len: int, n_outlier: int = 0):
+        self.ctx.check(self.ctx.L.nx_model_fill_context(self.h, ctx_len, n_outlier),
+                       "nx_model_fill_context")
+
+    def pending(self) -> np.ndarray:
+        t = np.empty(self.cfg.batch, np.int32)
+        self.ctx.check(self.ctx.L.nx_model_pending(self.h, t.ctypes.data), "nx_model_pending")
+        return t
+
+    def decode(self, steps: int) -> np.ndarray:
+        out = np.empty((self.cfg.batch, steps), np.int32)
+        self.ctx.check(self.ctx.L.nx_model_decode(self.h, steps, out.ctypes.data), "nx_model_decode")
+        return out
+
+    def decode_untimed(self, steps: int):
+        self.ctx.check(self.ctx.L.nx_model_decode(self.h, steps, None), "nx_model_decode")
+
+    def logits(self) -> np.ndarray:
+        out = np.empty((self.cfg.batch, self.cfg.vocab), np.float32)
+        self.ctx.check(self.ctx.L.nx_model_logits(self.h, out.ctypes.data), "nx_model_logits")
+        return out
+
+    def position(self, b: int = 0) -> int:
+        p = C.c_int()
+        self.ctx.check(self.ctx.L.nx_model_position(self.h, b, C.byref(p)), "nx_model_position")
+        return p.value
+
+    def step_bytes(self) -> float:
+        v = C.c_double()
+        self.ctx.check(self.ctx.L.nx_model_step_bytes(self.h, C.byref(v)), "nx_model_step_bytes")
+        return v.value
+
+    def time_ffn_gemv(self, iters: int = 50):
+        ms, nb = C.c_double(), C.c_double()
+        self.ctx.check(self.ctx.L.nx_model_time_ffn_gemv(self.h, iters, C.byref(ms), C.byref(nb)),
+                       "nx_model_time_ffn_gemv")
+        return ms.value, nb.value
+
+    def time_attention(self, iters: int = 50):
+        ms, nb = C.c_double(), C.c_double()
+        self.ctx.check(self.ctx.L.nx_model_time_attention(self.h, iters, C.byref(ms), C.byref(nb)),
+                       "nx_model_time_attention")
+        return ms.value, nb.value

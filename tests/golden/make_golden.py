@@ -1,0 +1,136 @@
+"""Write the golden vectors of the decode-loop parity tests.
+
+Run in a container that has the reference sources (it builds the reference
+checker oracle/_ref/libnexus_ref.so from them with `make -C oracle ref`).
+Every expected output below is produced by the reference's own functions,
+compiled in place from the reference sources:
+
+  tq_codebook.npz    TurboQuantKV::build_codebook  (kv/turbo_quant.cpp:172-219), d=128, bits 3/4
+  tq_encode.npz      LloydMaxCodebook::encode      (kv/turbo_quant.cpp:19-32), incl. boundary ties
+  tq_pack.npz        TurboQuantKV::pack_codes      (kv/turbo_quant.cpp:249-268)
+  tq_quantize.npz    TurboQuantKV::quantize        (kv/turbo_quant.cpp:289-327), identity rotation
+  dequant_int4.npz   quant::dequant_int4           (quant/gptq.cpp:9-27), zero = 8
+  kv_fp16.npz        HybridKVCache::f32_to_f16 / f16_to_f32 (model/hybrid_model.h:123-140)
+  paged_gather.npz   PagedKVCache::insert_kv + get_keys/get_values (kv/paged_attention.cpp:81-230)
+  moe_route.npz      MoERouter::route              (model/moe_router.cpp:55-113), identity gate
+
+Usage: python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+sys.path.insert(0, str(ROOT))
+
+
+def main() -> None:
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle"), "ref"], check=True)
+    import oracle
+    R = oracle.ref()
+    assert R is not None, "reference checker did not build"
+    rng = np.random.default_rng(20261201)
+
+    # codebooks
+    cb = {}
+    for bits in (3, 4):
+        n = 1 << bits
+        c = np.empty(n, np.float32)
+        b = np.empty(n - 1, np.float32)
+        R.ref_tq_codebook(128, bits, c, b)
+        cb[f"c{bits}"] = c
+        cb[f"b{bits}"] = b
+    np.savez_compressed(HERE / "tq_codebook.npz", **cb)
+
+    # scalar encode rule, with values on and one ulp either side of every boundary
+    enc = {}
+    for bits in (3, 4):
+        b = cb[f"b{bits}"]
+        x = np.concatenate([
+            rng.normal(0, 1 / np.sqrt(128), 512).astype(np.float32),
+            b, np.nextafter(b, -np.inf), np.nextafter(b, np.inf),
+            np.array([0.0, -0.0, 1.0, -1.0, 3.4e38, -3.4e38], np.float32),
+        ]).astype(np.float32)
+        codes = np.empty(x.size, np.uint8)
+        R.ref_tq_encode_scalar(128, bits, x, x.size, codes)
+        enc[f"x{bits}"] = x
+        enc[f"code{bits}"] = codes
+    np.savez_compressed(HERE / "tq_encode.npz", **enc)
+
+    # bit packing
+    pk = {}
+    for bits in (3, 4):
+        for n in (8, 37, 64, 128):
+            codes = rng.integers(0, 1 << bits, n, dtype=np.uint8)
+            packed = np.zeros((n * bits + 7) // 8, np.uint8)
+            R.ref_pack_codes(packed, codes, n, bits)
+            pk[f"codes_{bits}_{n}"] = codes
+            pk[f"packed_{bits}_{n}"] = packed
+    np.savez_compressed(HERE / "tq_pack.npz", **pk)
+
+    # quantize with the identity rotation: norm, normalize, encode, pack
+    tq = {}
+    for bits in (3, 4):
+        x = rng.normal(0, 1, (6, 128)).astype(np.float32)
+        x[1] *= 1e-3
+        x[2, :4] *= 10
+        x[3] = 0.0
+        nbytes = (128 * bits + 7) // 8
+        packed = np.zeros(6 * nbytes, np.uint8)
+        norms = np.zeros(6, np.float32)
+        R.ref_tq_quantize_identity(128, bits, x, 6, packed, norms)
+        tq[f"x{bits}"] = x
+        tq[f"packed{bits}"] = packed
+        tq[f"norms{bits}"] = norms
+    np.savez_compressed(HERE / "tq_quantize.npz", **tq)
+
+    # grouped int4 dequant with zero = 8 and fp16-representable scales
+    n, gs = 256, 32
+    data = rng.integers(0, 256, n // 2, dtype=np.uint8)
+    scales = rng.uniform(1e-3, 0.05, n // gs).astype(np.float16).astype(np.float32)
+    zeros = np.full(n // gs, 8.0, np.float32)
+    out = np.empty(n, np.float32)
+    R.ref_dequant_int4(out, data, scales, zeros, n, gs)
+    np.savez_compressed(HERE / "dequant_int4.npz", data=data, scales=scales, zeros=zeros, out=out)
+
+    # reference fp16 KV conversions (truncating) on edge values
+    vals = np.concatenate([
+        rng.normal(0, 10, 256).astype(np.float32),
+        np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65520.0, 70000.0, 6.1e-5, 6.0e-5, 3e-8, 1e-10,
+                  np.inf, -np.inf, 1.0009765625, 1.00048828125, 2049.0], np.float32),
+    ]).astype(np.float32)
+    h = np.empty(vals.size, np.uint16)
+    R.ref_f32_to_f16_kv(vals, h, vals.size)
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    back = np.empty(65536, np.float32)
+    R.ref_f16_to_f32_kv(allh, back, 65536)
+    np.savez_compressed(HERE / "kv_fp16.npz", f32=vals, f16_trunc=h, f16_to_f32=back)
+
+    # paged gather
+    hkv, hd, npos = 2, 8, 37
+    k = rng.normal(0, 1, (npos, hkv * hd)).astype(np.float32)
+    v = rng.normal(0, 1, (npos, hkv * hd)).astype(np.float32)
+    ko = np.empty_like(k)
+    vo = np.empty_like(v)
+    R.ref_paged_gather(hkv, hd, 16, k, v, npos, ko, vo)
+    np.savez_compressed(HERE / "paged_gather.npz", k=k, v=v, k_out=ko, v_out=vo, hkv=hkv, hd=hd)
+
+    # MoE routing with an identity gate (logits = hidden exactly)
+    E, topk = 8, 2
+    hidden = rng.normal(0, 1, (16, E)).astype(np.float32)
+    gate = np.eye(E, dtype=np.float32)
+    ids = np.zeros((16, topk), np.int32)
+    w = np.zeros((16, topk), np.float32)
+    for i in range(16):
+        R.ref_moe_route(E, topk, E, gate, np.ascontiguousarray(hidden[i]), ids[i], w[i])
+    np.savez_compressed(HERE / "moe_route.npz", logits=hidden, ids=ids, weights=w, k=topk)
+    print("golden vectors written to", HERE)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,142 @@
+"""End-to-end decode-loop parity on the GPU: greedy token ids produced by the
+HIP runner (one HIP graph per step, token fed back on the device) must equal
+the oracle's on the same seeded model, prompt and context."""
+import numpy as np
+import pytest
+
+import nexus_amd
+import oracle
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=688, vocab=4096,
+            n_experts=0, top_k=0, max_seq=128, batch=1, kv_kind=0, rope_theta=10000.0, eps=1e-5,
+            seed=0x5EED)
+
+
+def run_both(ctx, cfg, P=16, n_new=64):
+    prompt = oracle.prompt_tokens(cfg["seed"], cfg["batch"], P, cfg["vocab"])
+    om = oracle.Model(**cfg)
+    want, margins = om.generate(prompt, n_new)
+    om.close()
+    gm = nexus_amd.Model(ctx, **cfg)
+    first = gm.prefill(prompt)
+    rest = gm.decode(n_new - 1)
+    got = np.concatenate([first[:, None], rest], axis=1)
+    assert gm.position(0) == P + n_new - 2
+    gm.close()
+    return got, want, margins
+
+
+def test_tiny_greedy_parity(ctx):
+    """The tiny Llama-style model: 16-token prompt, 64 greedy tokens."""
+    got, want, margins = run_both(ctx, TINY)
+    print("min top1-top2 margin", float(margins.min()))
+    assert np.array_equal(got, want)
+
+
+def test_tiny_greedy_parity_batch2(ctx):
+    cfg = dict(TINY, batch=2, seed=0xBEEF)
+    got, want, _ = run_both(ctx, cfg, P=9, n_new=24)
+    assert np.array_equal(got, want)
+
+
+def test_tiny_moe_greedy_parity(ctx):
+    cfg = dict(TINY, n_experts=4, top_k=2, seed=0x0E0E)
+    got, want, _ = run_both(ctx, cfg, P=8, n_new=24)
+    assert np.array_equal(got, want)
+
+
+def test_tiny_moe_greedy_parity_batch3(ctx):
+    cfg = dict(TINY, n_experts=8, top_k=2, batch=3, seed=0x0E0F)
+    got, want, _ = run_both(ctx, cfg, P=5, n_new=12)
+    assert np.array_equal(got, want)
+
+
+def test_tiny_turboquant_greedy_parity(ctx):
+    cfg = dict(TINY, n_heads=4, n_kv_heads=1, head_dim=128, kv_kind=1, seed=0x7777, d_model=512)
+    got, want, _ = run_both(ctx, cfg, P=12, n_new=24)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kv_kind,n_outlier", [(0, 0), (1, 4)])
+def test_filled_context_decode_parity(ctx, kv_kind, n_outlier):
+    cfg = dict(TINY, n_kv_heads=2, n_heads=4, head_dim=128, d_model=512, max_seq=512, batch=2,
+               kv_kind=kv_kind, seed=0xC0DE)
+    ctx_len, steps = 300, 10
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(ctx_len, n_outlier)
+    start = gm.pending()
+    got = gm.decode(steps)
+    glog = gm.logits()
+    gm.close()
+    om = oracle.Model(**cfg)
+    om.fill_context(ctx_len, n_outlier)
+    want_start = np.array([oracle.lib.nxo_rand_u64(cfg["seed"], 5, b) % cfg["vocab"] for b in range(2)], np.int32)
+    assert np.array_equal(start, want_start)
+    tok = start
+    want = []
+    for _ in range(steps):
+        logits = om.forward(tok)
+        tok = logits.argmax(axis=1).astype(np.int32)
+        want.append(tok)
+    om.close()
+    assert np.array_equal(got, np.stack(want, 1))
+    assert rel_err(glog, logits) < 1e-3
+
+
+LLAMA8B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336,
+               vocab=128256, n_experts=0, top_k=0, max_seq=4096 + 256, batch=1, kv_kind=0,
+               rope_theta=500000.0, eps=1e-5, seed=0x5EED)
+
+
+def test_8b_one_layer_full_shape_parity(ctx):
+    """Full Llama-3-8B layer and lm_head shapes (one layer) at 512 context."""
+    cfg = dict(LLAMA8B, n_layers=1, max_seq=1024)
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(512, 0)
+    got = gm.decode(3)
+    glog = gm.logits()
+    start = gm.pending()
+    gm.close()
+    om = oracle.Model(**cfg)
+    om.fill_context(512, 0)
+    tok = np.array([oracle.lib.nxo_rand_u64(cfg["seed"], 5, 0) % cfg["vocab"]], np.int32)
+    want = []
+    for _ in range(3):
+        logits = om.forward(tok)
+        tok = logits.argmax(axis=1).astype(np.int32)
+        want.append(tok)
+    om.close()
+    assert np.array_equal(got, np.stack(want, 1))
+    assert start[0] == want[-1][0]
+    assert rel_err(glog, logits) < 1e-3
+
+
+def test_8b_decode_properties(ctx):
+    """The full 32-layer 8B shape at 4096 context: deterministic, in range,
+    and the algorithmic bytes of a step match the closed form."""
+    gm = nexus_amd.Model(ctx, **LLAMA8B)
+    gm.fill_context(4096, 0)
+    bytes_at_4096 = gm.step_bytes()
+    # weights 4,221,370,368 B + fp16 KV of 4096 positions x 32 layers
+    assert abs(bytes_at_4096 - (4221370368 + 536870912)) < 1e6
+    a = gm.decode(6)
+    assert a.min() >= 0 and a.max() < LLAMA8B["vocab"]
+    assert np.all(np.isfinite(gm.logits()))
+    gm.close()
+    gm2 = nexus_amd.Model(ctx, **LLAMA8B)
+    gm2.fill_context(4096, 0)
+    b = gm2.decode(6)
+    gm2.close()
+    assert np.array_equal(a, b)
+
+
+def test_capacity_is_an_error(ctx):
+    gm = nexus_amd.Model(ctx, **dict(TINY, max_seq=32))
+    gm.prefill(np.arange(20, dtype=np.int32)[None, :])
+    with pytest.raises(nexus_amd.NxError) as e:
+        gm.decode(20)
+    assert e.value.code == 7
+    gm.close()

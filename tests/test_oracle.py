@@ -1,0 +1,528 @@
+"""CPU tests that pin the oracle before it is trusted as the checker.
+
+Each oracle function is checked against (a) golden vectors produced by the
+reference's own functions (tests/golden, see make_golden.py), (b) the live
+reference checker oracle/_ref when it is built, and/or (c) what mathematics
+fixes: published tables, closed forms and fp64 brute force.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+
+GOLD = Path(__file__).resolve().parent / "golden"
+L = oracle.lib
+
+
+def gold(name):
+    return np.load(GOLD / name)
+
+
+# ------------------------------------------------------------------- fp16 --
+def test_f32_to_f16_rne_matches_ieee():
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    edge = np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, 6.1035156e-05, 6.097555e-05,
+                     5.9604645e-08, 2.9802322e-08, 2.9802326e-08, 8.940697e-08, 1.0009766,
+                     1.0004883, -1.0004883, 2049.0, 2051.0], np.float32)
+    for v in (vals, edge, rng.normal(0, 1, 50000).astype(np.float32)):
+        got = oracle.f16_bits(v)
+        want = v.astype(np.float16).view(np.uint16)  # numpy rounds to nearest even
+        assert np.array_equal(got, want)
+
+
+def test_f16_to_f32_exact_all_values():
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = np.array([L.nxo_f16_to_f32(int(h)) for h in allh[::7]], np.float32)
+    want = allh[::7].view(np.float16).astype(np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+
+
+def test_reference_kv_conversion_golden():
+    g = gold("kv_fp16.npz")
+    got = np.array([L.nxo_f32_to_f16_trunc(float(v)) for v in g["f32"]], np.uint16)
+    assert np.array_equal(got, g["f16_trunc"])
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    back = np.array([L.nxo_f16_to_f32_ref(int(h)) for h in allh], np.float32)
+    ref = g["f16_to_f32"]
+    # NaN payloads do not survive the trip through a Python float; compare the rest bitwise
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(back), nan)
+    assert np.array_equal(back[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+# -------------------------------------------------------------------- RNG --
+def test_rng_determinism_and_moments():
+    a = oracle.gen_normal(1 << 20, 7, 123, 0.02)
+    b = oracle.gen_normal(1 << 20, 7, 123, 0.02)
+    c = oracle.gen_normal(1 << 20, 7, 124, 0.02)
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, c)
+    assert abs(a.mean()) < 1e-4
+    assert abs(a.std() / 0.02 - 1) < 3e-3
+    # Irwin-Hall(4): excess kurtosis -0.3, bounded support |z| <= sqrt(12)
+    z = a.astype(np.float64) / 0.02
+    kurt = np.mean(z**4) / np.mean(z**2) ** 2 - 3
+    assert abs(kurt + 0.3) < 0.02
+    assert np.max(np.abs(z)) <= np.sqrt(12) + 1e-3
+
+
+def test_gen_quant_rows_matches_full_generation():
+    K, N = 96, 40
+    w = oracle.gen_normal(N * K, 3, 9, 0.02).reshape(N, K)
+    codes, scales = oracle.quantize(w)
+    c2, s2 = oracle.gen_quant_rows(11, 17, K, 3, 9, 0.02)
+    assert np.array_equal(c2, codes[11:28])
+    assert np.array_equal(s2, scales[11:28])
+
+
+# -------------------------------------------------------------- int4 g32 --
+def test_dequant_int4_golden():
+    g = gold("dequant_int4.npz")
+    scales16 = g["scales"].astype(np.float16).view(np.uint16)
+    codes = np.ascontiguousarray(g["data"][None, :])
+    out = oracle.dequantize(codes, scales16[None, :], 1, 256)
+    assert np.array_equal(out[0].view(np.uint32), g["out"].view(np.uint32))
+
+
+def test_dequant_int4_live_reference():
+    R = oracle.ref()
+    if R is None:
+        pytest.skip("reference checker not built")
+    rng = np.random.default_rng(5)
+    data = rng.integers(0, 256, 512, dtype=np.uint8)
+    s16 = rng.uniform(1e-4, 1, 32).astype(np.float16)
+    out_ref = np.empty(1024, np.float32)
+    R.ref_dequant_int4(out_ref, data, s16.astype(np.float32), np.full(32, 8.0, np.float32), 1024, 32)
+    out = oracle.dequantize(data[None, :], s16.view(np.uint16)[None, :], 1, 1024)
+    assert np.array_equal(out[0].view(np.uint32), out_ref.view(np.uint32))
+
+
+def test_unpack_int4_all_bytes():
+    allb = np.arange(256, dtype=np.uint8)
+    codes = np.empty(512, np.uint8)
+    L.nxo_unpack_int4(allb, 512, codes)
+    assert np.array_equal(codes[0::2], allb & 15)
+    assert np.array_equal(codes[1::2], allb >> 4)
+
+
+@pytest.mark.parametrize("K", [32, 96, 688, 4096])
+def test_quantizer_invariants(K):
+    rng = np.random.default_rng(K)
+    N = 33
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    w[3] = 0.0
+    w[5, :7] = 0.5  # outliers in one group
+    codes, scales = oracle.quantize(w)
+    deq = oracle.dequantize(codes, scales, N, K)
+    s = scales.view(np.float16).astype(np.float32)
+    s_el = np.repeat(s, 32, axis=1)[:, :K]
+    assert np.all(np.abs(deq - w) <= s_el * 0.5000001 + 1e-12)
+    assert np.all(scales[3] == 0) and np.all(deq[3] == 0)
+    # codes of a ragged tail hold 8
+    G = (K + 31) // 32
+    if K % 32:
+        un = np.empty(G * 32 * N, np.uint8)
+        L.nxo_unpack_int4(np.ascontiguousarray(codes), un.size, un)
+        un = un.reshape(N, G * 32)
+        assert np.all(un[:, K:] == 8)
+
+
+@pytest.mark.parametrize("N,K,B", [(64, 96, 1), (256, 688, 2), (128, 4096, 3)])
+def test_gemv_vs_fp64(N, K, B):
+    rng = np.random.default_rng(N + K)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    codes, scales = oracle.quantize(w)
+    x = rng.normal(0, 1, (B, K)).astype(np.float16).astype(np.float32)
+    y = oracle.gemv(codes, scales, x, N, K)
+    deq = oracle.dequantize(codes, scales, N, K).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T
+    assert rel_err(y, want) < 1e-5
+
+
+# ------------------------------------------------------------ elementwise --
+def test_rmsnorm_vs_fp64():
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 3, 4096).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    out = np.empty_like(x)
+    L.nxo_rmsnorm(x, w.ctypes.data, 4096, 1e-5, out)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt(np.mean(xd**2) + 1e-5) * w
+    assert rel_err(out, want) < 1e-6
+
+
+def test_rope_is_complex_rotation():
+    hd, heads, pos, theta = 64, 3, 37, 10000.0
+    cos = np.empty((128, hd // 2), np.float32)
+    sin = np.empty((128, hd // 2), np.float32)
+    L.nxo_rope_table(128, hd, theta, cos, sin)
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, heads * hd).astype(np.float32)
+    y = x.copy()
+    L.nxo_rope(y, heads, hd, pos, cos, sin)
+    z = x.astype(np.float64).reshape(heads, hd // 2, 2)
+    zc = z[..., 0] + 1j * z[..., 1]
+    ang = pos * theta ** (-(2.0 * np.arange(hd // 2)) / hd)
+    r = zc * np.exp(1j * ang)
+    want = np.stack([r.real, r.imag], -1).reshape(-1)
+    assert rel_err(y, want) < 1e-6
+    # position 0 is the identity
+    y0 = x.copy()
+    L.nxo_rope(y0, heads, hd, 0, cos, sin)
+    assert np.array_equal(y0, x)
+
+
+def test_swiglu_vs_fp64():
+    rng = np.random.default_rng(4)
+    g = rng.normal(0, 3, 1000).astype(np.float32)
+    u = rng.normal(0, 1, 1000).astype(np.float32)
+    out = np.empty_like(g)
+    L.nxo_swiglu(g, u, 1000, out)
+    gd = g.astype(np.float64)
+    want = gd / (1 + np.exp(-gd)) * u
+    assert rel_err(out, want) < 1e-6
+
+
+def test_argmax_first_maximum():
+    v = np.array([1.0, 3.0, -2.0, 3.0, 0.5], np.float32)
+    assert L.nxo_argmax(v, 5) == 1
+
+
+# -------------------------------------------------------- paged attention --
+def _attn_fp64(q, K, V, hq, hkv, hd):
+    grp = hq // hkv
+    out = np.zeros((hq, hd))
+    for h in range(hq):
+        kvh = h // grp
+        s = K[:, kvh, :] @ q[h] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p @ V[:, kvh, :]
+    return out
+
+
+def _paged_setup(rng, B, hkv, hd, max_blocks, ctx_lens):
+    nblk = B * max_blocks
+    perm = np.empty(nblk, np.int32)
+    L.nxo_shuffle_perm(perm, nblk, 11, 7)
+    bt = np.ascontiguousarray(perm.reshape(B, max_blocks))
+    kpool = np.zeros(nblk * hkv * 16 * hd, np.uint16)
+    vpool = np.zeros_like(kpool)
+    raw = []
+    for b in range(B):
+        K = rng.normal(0, 1, (ctx_lens[b], hkv, hd)).astype(np.float32)
+        V = rng.normal(0, 1, (ctx_lens[b], hkv, hd)).astype(np.float32)
+        for p in range(ctx_lens[b]):
+            L.nxo_kv_append_f16(np.ascontiguousarray(K[p]), np.ascontiguousarray(V[p]), kpool, vpool,
+                                bt, max_blocks, b, p, hkv, hd)
+        raw.append((K, V))
+    return bt, kpool, vpool, raw
+
+
+@pytest.mark.parametrize("hq,hkv,hd", [(4, 2, 64), (8, 2, 128)])
+def test_paged_attention_vs_fp64(hq, hkv, hd):
+    rng = np.random.default_rng(hq * hd)
+    B, max_blocks = 3, 4
+    ctx = np.array([1, 17, 64], np.int32)
+    bt, kp, vp, raw = _paged_setup(rng, B, hkv, hd, max_blocks, ctx)
+    q = rng.normal(0, 1, (B, hq, hd)).astype(np.float32)
+    out = np.empty_like(q)
+    L.nxo_attn_decode_paged_f16(q, kp, vp, bt, max_blocks, ctx, B, hq, hkv, hd, out)
+    for b in range(B):
+        K, V = raw[b]
+        Kh = K.astype(np.float16).astype(np.float64)
+        Vh = V.astype(np.float16).astype(np.float64)
+        want = _attn_fp64(q[b].astype(np.float64), Kh, Vh, hq, hkv, hd)
+        assert rel_err(out[b], want) < 1e-5
+
+
+def test_paged_gather_golden_and_shuffle_invariance():
+    g = gold("paged_gather.npz")
+    hkv, hd = int(g["hkv"]), int(g["hd"])
+    # the reference gather returns positions in order: contiguous == input
+    assert np.array_equal(g["k_out"], g["k"]) and np.array_equal(g["v_out"], g["v"])
+    npos = g["k"].shape[0]
+    max_blocks = (npos + 15) // 16
+    for seed in (1, 2, 3):
+        perm = np.empty(max_blocks, np.int32)
+        L.nxo_shuffle_perm(perm, max_blocks, seed, 7)
+        kp = np.zeros(max_blocks * hkv * 16 * hd, np.uint16)
+        vp = np.zeros_like(kp)
+        for p in range(npos):
+            L.nxo_kv_append_f16(np.ascontiguousarray(g["k"][p]), np.ascontiguousarray(g["v"][p]),
+                                kp, vp, perm, max_blocks, 0, p, hkv, hd)
+        q = np.random.default_rng(seed).normal(0, 1, (1, 2 * hkv, hd)).astype(np.float32)
+        out = np.empty_like(q)
+        L.nxo_attn_decode_paged_f16(q, kp, vp, perm, max_blocks, np.array([npos], np.int32), 1,
+                                    2 * hkv, hkv, hd, out)
+        Kc = g["k_out"].astype(np.float16).astype(np.float32)
+        Vc = g["v_out"].astype(np.float16).astype(np.float32)
+        want = np.empty_like(q)
+        L.nxo_attn_decode_contig(np.ascontiguousarray(q[0]), np.ascontiguousarray(Kc),
+                                 np.ascontiguousarray(Vc), npos, 2 * hkv, hkv, hd, want[0])
+        assert np.array_equal(out, want)
+
+
+# ------------------------------------------------------------- TurboQuant --
+# Max (1960) Lloyd-Max quantizers for N(0, 1), output levels (positive half).
+MAX_8 = [0.2451, 0.7560, 1.3440, 2.1520]
+MAX_16 = [0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6181, 2.0690, 2.7326]
+
+
+def test_codebook_matches_reference_golden():
+    g = gold("tq_codebook.npz")
+    for bits in (3, 4):
+        c, b = oracle.codebook(bits)
+        assert np.array_equal(c.view(np.uint32), g[f"c{bits}"].view(np.uint32))
+        assert np.array_equal(b.view(np.uint32), g[f"b{bits}"].view(np.uint32))
+
+
+def test_codebook_live_reference():
+    R = oracle.ref()
+    if R is None:
+        pytest.skip("reference checker not built")
+    for d in (64, 128, 256):
+        for bits in (2, 3, 4):
+            n = 1 << bits
+            c, b = np.empty(n, np.float32), np.empty(n - 1, np.float32)
+            rc, rb = np.empty(n, np.float32), np.empty(n - 1, np.float32)
+            L.nxo_tq_codebook(d, bits, c, b)
+            R.ref_tq_codebook(d, bits, rc, rb)
+            assert np.array_equal(c.view(np.uint32), rc.view(np.uint32))
+            assert np.array_equal(b.view(np.uint32), rb.view(np.uint32))
+
+
+def test_codebook_is_lloyd_max_iteration():
+    """The codebook is the Lloyd-Max iteration for N(0, 1/128) run from a
+    uniform start in +-3 sigma with +-10 sigma tails for at most 100 steps
+    (it stops short of the fixed point, as the reference does); checked in
+    fp64 with scipy's normal pdf/cdf, and against Max's (1960) table."""
+    from scipy.stats import norm
+    sigma = 1 / np.sqrt(128)
+    for bits, table in ((3, MAX_8), (4, MAX_16)):
+        n = 1 << bits
+        c, b = oracle.codebook(bits)
+        c64 = c.astype(np.float64)
+        assert np.allclose(b, 0.5 * (c64[:-1] + c64[1:]), atol=1e-7)
+        cm = -3 * sigma + 6 * sigma * (np.arange(n) + 0.5) / n
+        for _ in range(100):
+            bd = 0.5 * (cm[:-1] + cm[1:])
+            edges = np.concatenate([[-10 * sigma], bd, [10 * sigma]])
+            new = sigma**2 * (norm.pdf(edges[:-1], scale=sigma) - norm.pdf(edges[1:], scale=sigma)) / (
+                norm.cdf(edges[1:], scale=sigma) - norm.cdf(edges[:-1], scale=sigma))
+            delta = np.max(np.abs(new - cm))
+            cm = new
+            if delta < 1e-7 * sigma:
+                break
+        assert np.allclose(c64, cm, atol=2e-6)
+        half = np.sort(np.abs(c64))[::2] * np.sqrt(128)
+        assert np.allclose(half, table, atol=2e-2)
+
+
+def test_encode_rule_golden():
+    g = gold("tq_encode.npz")
+    for bits in (3, 4):
+        _, b = oracle.codebook(bits)
+        got = np.array([L.nxo_tq_encode_scalar(float(x), b, 1 << bits) for x in g[f"x{bits}"]], np.uint8)
+        assert np.array_equal(got, g[f"code{bits}"])
+
+
+def test_pack_golden_and_roundtrip():
+    g = gold("tq_pack.npz")
+    for bits in (3, 4):
+        for n in (8, 37, 64, 128):
+            codes = g[f"codes_{bits}_{n}"]
+            packed = np.zeros((n * bits + 7) // 8, np.uint8)
+            L.nxo_pack_codes(packed, np.ascontiguousarray(codes), n, bits)
+            assert np.array_equal(packed, g[f"packed_{bits}_{n}"])
+            back = np.empty(n, np.uint8)
+            L.nxo_unpack_codes(back, packed, n, bits)
+            assert np.array_equal(back, codes)
+
+
+def test_quantize_composition_golden():
+    """norm -> normalize -> encode -> pack, as TurboQuantKV::quantize does it."""
+    g = gold("tq_quantize.npz")
+    for bits in (3, 4):
+        _, b = oracle.codebook(bits)
+        x = g[f"x{bits}"]
+        nbytes = (128 * bits + 7) // 8
+        for v in range(x.shape[0]):
+            nrm = g[f"norms{bits}"][v]
+            assert np.isclose(nrm, np.sqrt(np.sum(x[v].astype(np.float64) ** 2)), rtol=1e-6)
+            if nrm > 1e-12:
+                inv = np.float32(1.0) / np.float32(nrm)
+                y = (x[v] * inv).astype(np.float32)
+            else:
+                y = np.zeros(128, np.float32)
+            codes = np.array([L.nxo_tq_encode_scalar(float(t), b, 1 << bits) for t in y], np.uint8)
+            packed = np.zeros(nbytes, np.uint8)
+            L.nxo_pack_codes(packed, codes, 128, bits)
+            assert np.array_equal(packed, g[f"packed{bits}"][v * nbytes:(v + 1) * nbytes])
+
+
+def test_fwht_is_sylvester_hadamard():
+    from scipy.linalg import hadamard
+    H = hadamard(128).astype(np.float64)
+    u = np.random.default_rng(6).normal(0, 1, 128).astype(np.float32)
+    v = u.copy()
+    L.nxo_fwht128(v)
+    assert rel_err(v, H @ u.astype(np.float64)) < 1e-6
+    L.nxo_fwht128(v)  # H H = 128 I
+    assert rel_err(v / 128.0, u) < 1e-6
+
+
+def test_tq_sumsq_tree_is_exact_sum():
+    x = np.random.default_rng(7).normal(0, 1, 128).astype(np.float32)
+    assert np.isclose(L.nxo_tq_sumsq(x), np.sum(x.astype(np.float64) ** 2), rtol=1e-6)
+
+
+def test_tq_roundtrip_distortion():
+    rng = np.random.default_rng(8)
+    x = rng.normal(0, 1, (2000, 128)).astype(np.float32)
+    signs = oracle.tq_signs(5, 0x108)
+    k4, k3, nr, cu = oracle.tq_encode(x, signs)
+    xh = oracle.tq_decode(k4, k3, nr, signs)
+    err = np.sum((xh - x) ** 2, 1) / np.sum(x**2, 1)
+    # Gaussian Lloyd-Max distortion: 0.009497 (16 levels), 0.03454 (8 levels); average 0.0220
+    assert 0.018 < err.mean() < 0.026
+    # the codes index both halves correctly and the norm is stored in fp16
+    assert cu[:, :64].max() <= 15 and cu[:, 64:].max() <= 7
+    assert np.allclose(nr.view(np.float16).astype(np.float32), np.linalg.norm(x, axis=1), rtol=1e-3)
+    # zero vector -> norm 0, reconstruction 0
+    z = np.zeros((1, 128), np.float32)
+    zk4, zk3, znr, _ = oracle.tq_encode(z, signs)
+    assert znr[0] == 0 and np.all(oracle.tq_decode(zk4, zk3, znr, signs) == 0)
+
+
+def test_tq_rotated_domain_identity():
+    """<Pi q, c> * n == <q, n Pi^T c>: the score the GPU computes without inverse-rotating K."""
+    from scipy.linalg import hadamard
+    rng = np.random.default_rng(9)
+    signs = oracle.tq_signs(5, 0x108).astype(np.float64)
+    x = rng.normal(0, 1, (64, 128)).astype(np.float32)
+    k4, k3, nr, cu = oracle.tq_encode(x, signs.astype(np.float32))
+    khat = oracle.tq_decode(k4, k3, nr, signs.astype(np.float32)).astype(np.float64)
+    c4, _ = oracle.codebook(4)
+    c3, _ = oracle.codebook(3)
+    cvals = np.where(np.arange(128) < 64, c4[np.minimum(cu, 15)], c3[np.minimum(cu, 7)]).astype(np.float64)
+    H = hadamard(128).astype(np.float64) / np.sqrt(128)
+    q = rng.normal(0, 1, 128)
+    qrot = H @ (signs * q)
+    s_rot = (cvals @ qrot) * nr.view(np.float16).astype(np.float64)
+    s_dir = khat @ q
+    assert rel_err(s_rot, s_dir) < 1e-5
+
+
+def test_tq_attention_close_to_fp16_attention():
+    """Quantization error of 3.5-bit KV on attention output stays moderate."""
+    rng = np.random.default_rng(10)
+    hq, hkv, ctx = 4, 1, 48
+    K = rng.normal(0, 1, (ctx, hkv, 128)).astype(np.float32)
+    V = rng.normal(0, 1, (ctx, hkv, 128)).astype(np.float32)
+    q = rng.normal(0, 0.3, (1, hq, 128)).astype(np.float32)
+    ks, vs = oracle.tq_signs(1, 1), oracle.tq_signs(1, 2)
+    c4, b4 = oracle.codebook(4)
+    c3, b3 = oracle.codebook(3)
+    max_blocks = 3
+    bt = np.array([[2, 0, 1]], np.int32)
+    nv = max_blocks * hkv * 16
+    kc4, kc3, kn = np.zeros((nv, 32), np.uint8), np.zeros((nv, 24), np.uint8), np.zeros(nv, np.uint16)
+    vc4, vc3, vn = np.zeros_like(kc4), np.zeros_like(kc3), np.zeros_like(kn)
+    for p in range(ctx):
+        L.nxo_tq_append(np.ascontiguousarray(K[p]), np.ascontiguousarray(V[p]), hkv, ks, vs, b4, b3,
+                        kc4, kc3, kn, vc4, vc3, vn, bt, max_blocks, 0, p)
+    out = np.empty_like(q)
+    L.nxo_attn_decode_paged_tq(q, kc4, kc3, kn, vc4, vc3, vn, ks, vs, c4, c3, bt, max_blocks,
+                               np.array([ctx], np.int32), 1, hq, hkv, out)
+    want = _attn_fp64(q[0].astype(np.float64), K.astype(np.float64), V.astype(np.float64), hq, hkv, 128)
+    assert rel_err(out[0], want) < 0.25
+
+
+# -------------------------------------------------------------------- MoE --
+def test_moe_route_golden():
+    g = gold("moe_route.npz")
+    k = int(g["k"])
+    for i in range(g["logits"].shape[0]):
+        ids = np.empty(k, np.int32)
+        w = np.empty(k, np.float32)
+        L.nxo_moe_route(np.ascontiguousarray(g["logits"][i]), g["logits"].shape[1], k, ids, w)
+        assert np.array_equal(ids, g["ids"][i])
+        assert np.allclose(w, g["weights"][i], rtol=1e-6, atol=0)
+
+
+def test_moe_route_ties_pick_lower_id():
+    ids = np.empty(2, np.int32)
+    w = np.empty(2, np.float32)
+    L.nxo_moe_route(np.array([0.5, 1.0, 1.0, 1.0], np.float32), 4, 2, ids, w)
+    assert list(ids) == [1, 2] and np.allclose(w, 0.5)
+
+
+# ------------------------------------------------------------------ model --
+TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=688, vocab=4096,
+            n_experts=0, top_k=0, max_seq=128, batch=1, kv_kind=0, rope_theta=10000.0, eps=1e-5,
+            seed=0x5EED)
+
+
+def _deq(tid, N, K, sigma=0.02, seed=0x5EED):
+    c, s = oracle.gen_quant_rows(0, N, K, seed, tid, sigma)
+    return oracle.dequantize(c, s, N, K).astype(np.float64)
+
+
+def test_tiny_model_step_vs_fp64_composition():
+    """One forward step of the oracle model against an fp64 composition of
+    independently pinned pieces (dequant, fp64 matmul, closed-form norm /
+    RoPE / softmax / SwiGLU) in the reference layer order."""
+    m = oracle.Model(**TINY)
+    toks = [17, 999, 4000]
+    logits = [m.forward(np.array([t], np.int32))[0] for t in toks]
+    d, hq, hkv, hd, F, V = 256, 4, 2, 64, 688, 4096
+    emb = oracle.gen_normal(V * d, 0x5EED, 1, 0.02).reshape(V, d).astype(np.float16).astype(np.float64)
+    lid = lambda Li, kind: 0x100 * (Li + 1) + kind
+    W = [{k: _deq(lid(Li, i), n, kk) for k, i, n, kk in
+          (("q", 0, hq * hd, d), ("k", 1, hkv * hd, d), ("v", 2, hkv * hd, d), ("o", 3, d, hq * hd),
+           ("g", 4, F, d), ("u", 5, F, d), ("dn", 6, d, F))} for Li in range(2)]
+    lm = _deq(2, V, d)
+    f16r = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float64)
+    norm = lambda h: f16r(h / np.sqrt(np.mean(h**2) + 1e-5))
+    ang = lambda p: p * 10000.0 ** (-(2.0 * np.arange(hd // 2)) / hd)
+
+    def rope(x, p, heads):
+        z = x.reshape(heads, hd // 2, 2)
+        zc = (z[..., 0] + 1j * z[..., 1]) * np.exp(1j * ang(p))
+        return np.stack([zc.real, zc.imag], -1).reshape(-1)
+
+    cache = [([], []) for _ in range(2)]
+    for p, t in enumerate(toks):
+        h = emb[t].copy()
+        for Li in range(2):
+            w = W[Li]
+            xn = norm(h)
+            q, k, v = rope(w["q"] @ xn, p, hq), rope(w["k"] @ xn, p, hkv), w["v"] @ xn
+            cache[Li][0].append(f16r(k).reshape(hkv, hd))
+            cache[Li][1].append(f16r(v).reshape(hkv, hd))
+            att = _attn_fp64(q.reshape(hq, hd), np.array(cache[Li][0]), np.array(cache[Li][1]), hq, hkv, hd)
+            h = h + w["o"] @ f16r(att.reshape(-1))
+            xn = norm(h)
+            g, u = w["g"] @ xn, w["u"] @ xn
+            h = h + w["dn"] @ f16r(g / (1 + np.exp(-g)) * u)
+        want = lm @ norm(h)
+        assert rel_err(logits[p], want) < 1e-4
+    m.close()
+
+
+def test_tiny_model_generate_is_deterministic():
+    p = oracle.prompt_tokens(0x5EED, 1, 16, 4096)
+    a = oracle.Model(**TINY)
+    b = oracle.Model(**TINY)
+    ta, ma = a.generate(p, 8)
+    tb, _ = b.generate(p, 8)
+    assert np.array_equal(ta, tb)
+    assert np.all(ma >= 0)
