@@ -69,6 +69,29 @@ def cpu_baseline(ctx_len: int, batch: int, kv_kind: int) -> dict:
                        f"+ lm_head rows 1/{vocab_frac}, scaled to 32 layers + full lm_head")}
 
 
+GEMV_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+
+
+def gemv_microbench(ctx, batch: int = 1, iters: int = 100) -> list:
+    """Standalone int4-g32 GEMV (fp16 x, fp16 y) on the five 8B projection
+    shapes; bytes = N*K*0.5625 + batch*(2K + 2N), HIP-event timed."""
+    import ctypes as C
+    out = []
+    for N, K in GEMV_SHAPES:
+        G = (K + 31) // 32
+        w, s = ctx.alloc(N * G * 16), ctx.alloc(N * G * 2)
+        x, y = ctx.alloc(batch * K * 2), ctx.alloc(batch * N * 2)
+        ms = C.c_double()
+        ctx.check(ctx.L.nx_time_gemv(ctx.h, x, w, s, y, N, K, batch, iters, C.byref(ms)), "nx_time_gemv")
+        nbytes = N * K * 0.5625 + batch * (2 * K + 2 * N)
+        gbs = nbytes / (ms.value * 1e-3) / 1e9
+        out.append({"shape": f"{N}x{K}", "batch": batch, "us": round(ms.value * 1e3, 3),
+                    "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)})
+        for b in (w, s, x, y):
+            ctx.free(b)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,6 +137,7 @@ def main() -> int:
     ffn_gbs = ffn_bytes / (ffn_ms * 1e-3) / 1e9
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     model.close()
+    micro = gemv_microbench(ctx, args.batch)
     ctx.close()
 
     line = {
@@ -148,6 +172,7 @@ def main() -> int:
             "bytes": int(att_bytes),
         },
         "roofline_end_to_end_frac": round(step_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
+        "gemv_microbench": micro,
     }
     if not args.no_cpu:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)

@@ -5,7 +5,8 @@
 // query heads that share it, so every K/V byte is read once per step.
 // Within a wavefront lane l owns dims [l%16 * DPL, +DPL) of the tokens
 // l/16, l/16+4, l/16+8, l/16+12 of each page; a score is reduced over the 16
-// lanes of a DPP row.  Each DPP row keeps its own online-softmax state
+// lanes of a DPP row.  A wavefront issues the loads of two pages before it
+// computes either.  Each DPP row keeps its own online-softmax state
 // (m, l, o); rows, wavefronts and then splits are merged with the usual
 // rescaling.  The last block of a (sequence, kv head) to finish -- found with
 // an atomic counter, no spinning -- merges all splits and writes fp16 output.
@@ -22,7 +23,8 @@ namespace {
 
 constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * kWave;
-constexpr int kTargetBlocks = 512;
+constexpr int kTargetBlocks = 256;
+constexpr int kMaxSplits = 64;  // splits per (sequence, kv head)
 
 struct SplitPlan {
     int nsplit, pps;  // splits per (sequence, kv head), pages per split
@@ -31,6 +33,7 @@ struct SplitPlan {
 SplitPlan plan_splits(int batch, int hkv, int max_ctx) {
     const int pages = (max_ctx + kPage - 1) / kPage;
     int nsplit = (kTargetBlocks + batch * hkv - 1) / (batch * hkv);
+    if (nsplit > kMaxSplits) nsplit = kMaxSplits;
     if (nsplit > pages) nsplit = pages;
     if (nsplit < 1) nsplit = 1;
     const int pps = (pages + nsplit - 1) / nsplit;
@@ -38,6 +41,9 @@ SplitPlan plan_splits(int batch, int hkv, int max_ctx) {
     if (nsplit < 1) nsplit = 1;
     return {nsplit, pps < 1 ? 1 : pps};
 }
+
+// Split partial record, float offsets: O[G][HD] at 0, M[G], L[G], padded to 16 bytes.
+__host__ __device__ constexpr int rec_floats(int G, int HD) { return (G * HD + 2 * G + 3) / 4 * 4; }
 
 // Online-softmax state of one lane: G heads x DPL dims.
 template <int G, int DPL>
@@ -85,7 +91,15 @@ __device__ inline void state_update(State<G, DPL>& s, const float (&sc)[4][G],
     }
 }
 
-// Merge the four DPP rows of a wavefront; results valid in lanes 48..63.
+// Lane-wise sum over the four DPP rows (lanes i, i^16, i^32, i^48): every
+// lane ends with the total of its column, in a fixed order.
+__device__ inline float cols4_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Merge the four DPP rows of a wavefront; every row ends with the merged state.
 template <int G, int DPL>
 __device__ inline void state_merge_rows(State<G, DPL>& s) {
 #pragma unroll
@@ -96,60 +110,50 @@ __device__ inline void state_merge_rows(State<G, DPL>& s) {
         M = fmaxf(M, readlane_f(s.m[h], 32));
         M = fmaxf(M, readlane_f(s.m[h], 48));
         const float f = (M == -__builtin_inff()) ? 0.0f : __expf(s.m[h] - M);
-        s.l[h] = rows4_sum_to_row3(s.l[h] * f);
+        s.l[h] = cols4_sum(s.l[h] * f);
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) s.o[h][d] = rows4_sum_to_row3(s.o[h][d] * f);
+        for (int d = 0; d < DPL; ++d) s.o[h][d] = cols4_sum(s.o[h][d] * f);
         s.m[h] = M;
     }
 }
 
-// Block-level merge of the wavefronts' states through LDS, then store the
-// split's partial [M[G], L[G], O[G][HD]] (or the final output if nsplit == 1).
-// Returns nothing; `part` points at this split's record.
+// Block-level merge of the wavefronts' states through LDS (lds holds
+// kAttnWaves records), then store this split's record to `part`.
 template <int G, int HD>
 __device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __restrict__ part,
                                          float* lds) {
-    constexpr int DPL = HD / 16;
+    constexpr int DPL = HD / 16, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // lds layout per wave: m[G], l[G], o[G][HD]
-    constexpr int REC = G * (HD + 2);
     float* my = lds + wave * REC;
-    if (lane >= 48) {
-        const int c = lane - 48;
+    if (lane < 16) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            if (c == 0) {
-                my[h] = s.m[h];
-                my[G + h] = s.l[h];
+            if (lane == 0) {
+                my[MO + h] = s.m[h];
+                my[LO + h] = s.l[h];
             }
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) my[2 * G + h * HD + c * DPL + d] = s.o[h][d];
+            for (int d = 0; d < DPL; ++d) my[h * HD + lane * DPL + d] = s.o[h][d];
         }
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < G * HD + G; idx += kAttnThreads) {
-        if (idx < G * HD) {
-            const int h = idx / HD;
-            float M = -__builtin_inff();
-            for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, lds[w * REC + h]);
-            float O = 0.0f;
-            for (int w = 0; w < kAttnWaves; ++w) {
-                const float mw = lds[w * REC + h];
-                const float f = (M == -__builtin_inff()) ? 0.0f : __expf(mw - M);
-                O = fmaf(lds[w * REC + 2 * G + idx], f, O);
-            }
-            part[2 * G + idx] = O;
+        const bool is_o = idx < G * HD;
+        const int h = is_o ? idx / HD : idx - G * HD;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, lds[w * REC + MO + h]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float f = (M == -__builtin_inff()) ? 0.0f : __expf(lds[w * REC + MO + h] - M);
+            acc = fmaf(lds[w * REC + (is_o ? idx : LO + h)], f, acc);
+        }
+        if (is_o) {
+            part[idx] = acc;
         } else {
-            const int h = idx - G * HD;
-            float M = -__builtin_inff();
-            for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, lds[w * REC + h]);
-            float L = 0.0f;
-            for (int w = 0; w < kAttnWaves; ++w) {
-                const float f = (M == -__builtin_inff()) ? 0.0f : __expf(lds[w * REC + h] - M);
-                L = fmaf(lds[w * REC + G + h], f, L);
-            }
-            part[h] = M;
-            part[G + h] = L;
+            part[MO + h] = M;
+            part[LO + h] = acc;
         }
     }
 }
@@ -168,38 +172,123 @@ __device__ inline bool arrive_last(unsigned int* counter, int nsplit, int* flag)
     return last;
 }
 
-// Merge all split partials of (b, kvh) into o_merged[G][HD] / L (in LDS).
+// Merge all split records of (b, kvh) into out_o[G][HD] and out_l[G] (LDS).
+// fs: LDS scratch of kMaxSplits * G + G floats.  Split maxima and rescale
+// factors are computed once; the weighted sums then read float4s with the
+// loads of consecutive splits independent of each other.
 template <int G, int HD>
 __device__ inline void merge_splits(const float* __restrict__ parts, int nsplit, float* out_o,
-                                    float* out_l) {
-    constexpr int REC = G * (HD + 2);
-    for (int idx = threadIdx.x; idx < G * HD + G; idx += kAttnThreads) {
-        const int h = idx < G * HD ? idx / HD : idx - G * HD;
+                                    float* out_l, float* fs) {
+    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
+    float* Mh = fs + kMaxSplits * G;
+    for (int idx = threadIdx.x; idx < nsplit * G; idx += kAttnThreads)
+        fs[idx] = parts[(size_t)(idx / G) * REC + MO + idx % G];
+    __syncthreads();
+    if (threadIdx.x < G) {
         float M = -__builtin_inff();
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, parts[(size_t)s * REC + h]);
-        float acc = 0.0f;
-        for (int s = 0; s < nsplit; ++s) {
-            const float* p = parts + (size_t)s * REC;
-            const float ms = p[h];
-            const float f = (M == -__builtin_inff()) ? 0.0f : __expf(ms - M);
-            const float val = idx < G * HD ? p[2 * G + idx] : p[G + h];
-            acc = fmaf(val, f, acc);
-        }
-        if (idx < G * HD)
-            out_o[idx] = acc;
-        else
-            out_l[h] = acc;
+        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, fs[s * G + threadIdx.x]);
+        Mh[threadIdx.x] = M;
     }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nsplit * G; idx += kAttnThreads) {
+        const float M = Mh[idx % G];
+        fs[idx] = (M == -__builtin_inff()) ? 0.0f : __expf(fs[idx] - M);
+    }
+    __syncthreads();
+    constexpr int NQ = G * HD / 4;
+    for (int q = threadIdx.x; q < NQ + G; q += kAttnThreads) {
+        if (q < NQ) {
+            const int h = (4 * q) / HD;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 16
+            for (int s = 0; s < nsplit; ++s) {
+                const float4 v = *reinterpret_cast<const float4*>(parts + (size_t)s * REC + 4 * q);
+                const float f = fs[s * G + h];
+                acc.x = fmaf(v.x, f, acc.x);
+                acc.y = fmaf(v.y, f, acc.y);
+                acc.z = fmaf(v.z, f, acc.z);
+                acc.w = fmaf(v.w, f, acc.w);
+            }
+            *reinterpret_cast<float4*>(out_o + 4 * q) = acc;
+        } else {
+            const int h = q - NQ;
+            float acc = 0.0f;
+            for (int s = 0; s < nsplit; ++s) acc = fmaf(parts[(size_t)s * REC + LO + h], fs[s * G + h], acc);
+            out_l[h] = acc;
+        }
+    }
+    __syncthreads();
 }
 
 // ------------------------------------------------------------ fp16 pages --
+// Raw fp16 K/V of one page for one lane: 4 tokens x DPL halves each.
+template <int DPL>
+struct PageRaw {
+    uint32_t k[4][DPL / 2], v[4][DPL / 2];
+};
+
+template <int DPL>
+__device__ inline void load_page_f16(PageRaw<DPL>& r, const AttnArgs& a, int blk, int kvh, int p,
+                                     int ctx, int tg, int c) {
+    constexpr int HD = DPL * 16;
+    const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = tg + 4 * j;
+        const bool valid = p * kPage + t < ctx;
+        const uint16_t* kp = a.kpool + base + (size_t)t * HD + c * DPL;
+        const uint16_t* vp = a.vpool + base + (size_t)t * HD + c * DPL;
+        if (DPL == 8) {
+            const uint4 kr = valid ? *reinterpret_cast<const uint4*>(kp) : make_uint4(0, 0, 0, 0);
+            const uint4 vr = valid ? *reinterpret_cast<const uint4*>(vp) : make_uint4(0, 0, 0, 0);
+            r.k[j][0] = kr.x; r.k[j][1] = kr.y; r.k[j][2] = kr.z; r.k[j][3] = kr.w;
+            r.v[j][0] = vr.x; r.v[j][1] = vr.y; r.v[j][2] = vr.z; r.v[j][3] = vr.w;
+        } else {
+            const uint2 kr = valid ? *reinterpret_cast<const uint2*>(kp) : make_uint2(0, 0);
+            const uint2 vr = valid ? *reinterpret_cast<const uint2*>(vp) : make_uint2(0, 0);
+            r.k[j][0] = kr.x; r.k[j][1] = kr.y;
+            r.v[j][0] = vr.x; r.v[j][1] = vr.y;
+        }
+    }
+}
+
+template <int G, int DPL>
+__device__ inline void process_page_f16(State<G, DPL>& st, const PageRaw<DPL>& r,
+                                        const float (&q)[G][DPL], float scale, int p, int ctx,
+                                        int tg) {
+    float vf[4][DPL];
+    float sc[4][G];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool valid = p * kPage + tg + 4 * j < ctx;
+        float kf[DPL];
+#pragma unroll
+        for (int i = 0; i < DPL / 2; ++i) {
+            kf[2 * i] = h2f_bits((uint16_t)(r.k[j][i] & 0xFFFFu));
+            kf[2 * i + 1] = h2f_bits((uint16_t)(r.k[j][i] >> 16));
+            vf[j][2 * i] = h2f_bits((uint16_t)(r.v[j][i] & 0xFFFFu));
+            vf[j][2 * i + 1] = h2f_bits((uint16_t)(r.v[j][i] >> 16));
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) dot = fmaf(q[h][d], kf[d], dot);
+            dot = row16_sum(dot) * scale;
+            sc[j][h] = valid ? dot : -__builtin_inff();
+        }
+    }
+    state_update(st, sc, vf);
+}
+
 template <int G, int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
-    constexpr int DPL = HD / 16;
+    constexpr int DPL = HD / 16, REC = rec_floats(G, HD);
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, tg = lane >> 4;
-    __shared__ float lds[kAttnWaves * G * (HD + 2) + G * HD + G];
+    __shared__ __align__(16) float lds[kAttnWaves * REC + G * HD + G];
+    __shared__ float fsh[kMaxSplits * G + G];
     __shared__ int flag;
 
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
@@ -217,64 +306,25 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nspli
     const int p0 = split * pps;
     const int p1 = min(p0 + pps, npages);
     const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
-    for (int p = p0 + wave; p < p1; p += kAttnWaves) {
-        const int blk = bt[p];
-        const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
-        float kf[4][DPL], vf[4][DPL];
-        float sc[4][G];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = tg + 4 * j;
-            const bool valid = p * kPage + t < ctx;
-            const uint16_t* kp = a.kpool + base + (size_t)t * HD + c * DPL;
-            const uint16_t* vp = a.vpool + base + (size_t)t * HD + c * DPL;
-            if (DPL == 8) {
-                uint4 kr = valid ? *reinterpret_cast<const uint4*>(kp) : make_uint4(0, 0, 0, 0);
-                uint4 vr = valid ? *reinterpret_cast<const uint4*>(vp) : make_uint4(0, 0, 0, 0);
-                const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w}, vw[4] = {vr.x, vr.y, vr.z, vr.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    kf[j][2 * i] = h2f_bits((uint16_t)(kw[i] & 0xFFFFu));
-                    kf[j][2 * i + 1] = h2f_bits((uint16_t)(kw[i] >> 16));
-                    vf[j][2 * i] = h2f_bits((uint16_t)(vw[i] & 0xFFFFu));
-                    vf[j][2 * i + 1] = h2f_bits((uint16_t)(vw[i] >> 16));
-                }
-            } else {
-                uint2 kr = valid ? *reinterpret_cast<const uint2*>(kp) : make_uint2(0, 0);
-                uint2 vr = valid ? *reinterpret_cast<const uint2*>(vp) : make_uint2(0, 0);
-                const uint32_t kw[2] = {kr.x, kr.y}, vw[2] = {vr.x, vr.y};
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    kf[j][2 * i] = h2f_bits((uint16_t)(kw[i] & 0xFFFFu));
-                    kf[j][2 * i + 1] = h2f_bits((uint16_t)(kw[i] >> 16));
-                    vf[j][2 * i] = h2f_bits((uint16_t)(vw[i] & 0xFFFFu));
-                    vf[j][2 * i + 1] = h2f_bits((uint16_t)(vw[i] >> 16));
-                }
-            }
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float dot = 0.0f;
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) dot = fmaf(q[h][d], kf[j][d], dot);
-                dot = row16_sum(dot) * scale;
-                sc[j][h] = valid ? dot : -__builtin_inff();
-            }
-        }
-        state_update(st, sc, vf);
+    for (int p = p0 + wave; p < p1; p += 2 * kAttnWaves) {
+        const int pn = p + kAttnWaves;
+        PageRaw<DPL> r0, r1;
+        load_page_f16<DPL>(r0, a, bt[p], kvh, p, ctx, tg, c);
+        if (pn < p1) load_page_f16<DPL>(r1, a, bt[pn], kvh, pn, ctx, tg, c);
+        process_page_f16<G, DPL>(st, r0, q, scale, p, ctx, tg);
+        if (pn < p1) process_page_f16<G, DPL>(st, r1, q, scale, pn, ctx, tg);
     }
     state_merge_rows(st);
 
-    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * (G * (HD + 2));
-    block_merge_store<G, HD>(st, parts + (size_t)split * (G * (HD + 2)), lds);
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
+    block_merge_store<G, HD>(st, parts + (size_t)split * REC, lds);
     if (!arrive_last(a.counters + (size_t)b * a.hkv + kvh, nsplit, &flag)) return;
 
-    float* mo = lds + kAttnWaves * G * (HD + 2);
+    float* mo = lds + kAttnWaves * REC;
     float* ml = mo + G * HD;
-    merge_splits<G, HD>(parts, nsplit, mo, ml);
-    __syncthreads();
+    merge_splits<G, HD>(parts, nsplit, mo, ml, fsh);
     for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads) {
-        const int h = idx / HD;
-        const float L = ml[h];
+        const float L = ml[idx / HD];
         const float o = L > 0.0f ? mo[idx] / L : 0.0f;
         a.out16[((size_t)b * a.hq + kvh * G) * HD + idx] = f2h_bits(o);
     }
@@ -305,28 +355,87 @@ __device__ inline void lds_fwht(float* v) {
 
 constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
 
-// Decode the 8 codebook values of coordinates [8c, 8c+8) of token record t.
-__device__ inline void tq_decode8(const uint8_t* __restrict__ c4, const uint8_t* __restrict__ c3,
-                                  int c, const float* lds_c4, const float* lds_c3, float (&out)[8]) {
+// Raw codes of one page for one lane: 4 tokens x (8 codes of K and V, norms).
+struct TqRaw {
+    uint32_t k[4], v[4];
+    uint16_t kn[4], vn[4];
+};
+
+__device__ inline uint32_t tq_codes8(const uint8_t* __restrict__ c4, const uint8_t* __restrict__ c3,
+                                     int c) {
+    if (c < 8) return *reinterpret_cast<const uint32_t*>(c4 + 4 * c);
+    const uint8_t* p = c3 + 3 * (c - 8);
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16);
+}
+
+__device__ inline void load_page_tq(TqRaw& r, const AttnArgs& a, int blk, int kvh, int p, int ctx,
+                                    int tg, int c) {
+    const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = tg + 4 * j;
+        if (p * kPage + t < ctx) {
+            r.k[j] = tq_codes8(a.kc4 + (rec + t) * 32, a.kc3 + (rec + t) * 24, c);
+            r.v[j] = tq_codes8(a.vc4 + (rec + t) * 32, a.vc3 + (rec + t) * 24, c);
+            r.kn[j] = a.kn[rec + t];
+            r.vn[j] = a.vn[rec + t];
+        } else {
+            r.k[j] = r.v[j] = 0u;
+            r.kn[j] = r.vn[j] = 0;
+        }
+    }
+}
+
+// Codebook values of the 8 codes in w (4-bit lanes for c < 8, 3-bit otherwise).
+__device__ inline void tq_lookup8(uint32_t w, int c, const float* cb, float (&out)[8]) {
     if (c < 8) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(c4 + 4 * c);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = lds_c4[(w >> (4 * i)) & 15u];
+        for (int i = 0; i < 8; ++i) out[i] = cb[(w >> (4 * i)) & 15u];
     } else {
-        const uint8_t* p = c3 + 3 * (c - 8);
-        const uint32_t w = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = lds_c3[(w >> (3 * i)) & 7u];
+        for (int i = 0; i < 8; ++i) out[i] = cb[16 + ((w >> (3 * i)) & 7u)];
     }
 }
 
 template <int G>
+__device__ inline void process_page_tq(State<G, 8>& st, const TqRaw& r, const float (&q)[G][8],
+                                       float scale, int p, int ctx, int tg, int c, const float* cb) {
+    float vf[4][8];
+    float sc[4][G];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool valid = p * kPage + tg + 4 * j < ctx;
+        float kf[8];
+        tq_lookup8(r.k[j], c, cb, kf);
+        tq_lookup8(r.v[j], c, cb, vf[j]);
+        const float vn = h2f_bits(r.vn[j]);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) vf[j][d] *= vn;
+        const float kn = h2f_bits(r.kn[j]);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) dot = fmaf(q[h][d], kf[d], dot);
+            dot = row16_sum(dot) * kn * scale;
+            sc[j][h] = valid ? dot : -__builtin_inff();
+        }
+        if (!valid) {
+#pragma unroll
+            for (int d = 0; d < 8; ++d) vf[j][d] = 0.0f;
+        }
+    }
+    state_update(st, sc, vf);
+}
+
+template <int G>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
-    constexpr int HD = 128, DPL = 8;
+    constexpr int HD = 128, DPL = 8, REC = rec_floats(G, HD);
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, tg = lane >> 4;
-    __shared__ float lds[kAttnWaves * G * (HD + 2) + G * HD + G];
+    __shared__ __align__(16) float lds[kAttnWaves * REC + G * HD + G];
+    __shared__ float fsh[kMaxSplits * G + G];
     __shared__ float qrot[G * HD];
     __shared__ float cb[24];
     __shared__ int flag;
@@ -351,52 +460,27 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
     const int p0 = split * pps;
     const int p1 = min(p0 + pps, npages);
     const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
-    for (int p = p0 + wave; p < p1; p += kAttnWaves) {
-        const int blk = bt[p];
-        const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage;
-        float vf[4][DPL];
-        float sc[4][G];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = tg + 4 * j;
-            const bool valid = p * kPage + t < ctx;
-            float kf[DPL];
-            if (valid) {
-                tq_decode8(a.kc4 + (rec + t) * 32, a.kc3 + (rec + t) * 24, c, cb, cb + 16, kf);
-                tq_decode8(a.vc4 + (rec + t) * 32, a.vc3 + (rec + t) * 24, c, cb, cb + 16, vf[j]);
-                const float vn = h2f_bits(a.vn[rec + t]);
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) vf[j][d] *= vn;
-            } else {
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) kf[d] = vf[j][d] = 0.0f;
-            }
-            const float kn = valid ? h2f_bits(a.kn[rec + t]) : 0.0f;
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float dot = 0.0f;
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) dot = fmaf(q[h][d], kf[d], dot);
-                dot = row16_sum(dot) * kn * scale;
-                sc[j][h] = valid ? dot : -__builtin_inff();
-            }
-        }
-        state_update(st, sc, vf);
+    for (int p = p0 + wave; p < p1; p += 2 * kAttnWaves) {
+        const int pn = p + kAttnWaves;
+        TqRaw r0, r1;
+        load_page_tq(r0, a, bt[p], kvh, p, ctx, tg, c);
+        if (pn < p1) load_page_tq(r1, a, bt[pn], kvh, pn, ctx, tg, c);
+        process_page_tq<G>(st, r0, q, scale, p, ctx, tg, c, cb);
+        if (pn < p1) process_page_tq<G>(st, r1, q, scale, pn, ctx, tg, c, cb);
     }
     state_merge_rows(st);
 
-    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * (G * (HD + 2));
-    block_merge_store<G, HD>(st, parts + (size_t)split * (G * (HD + 2)), lds);
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
+    block_merge_store<G, HD>(st, parts + (size_t)split * REC, lds);
     if (!arrive_last(a.counters + (size_t)b * a.hkv + kvh, nsplit, &flag)) return;
 
-    float* mo = lds + kAttnWaves * G * (HD + 2);
+    float* mo = lds + kAttnWaves * REC;
     float* ml = mo + G * HD;
-    merge_splits<G, HD>(parts, nsplit, mo, ml);
+    merge_splits<G, HD>(parts, nsplit, mo, ml, fsh);
     // rotate back: o = D_v H o~ / sqrt(128)
     lds_fwht<G>(mo);
     for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads) {
-        const int h = idx / HD;
-        const float L = ml[h];
+        const float L = ml[idx / HD];
         const float o = L > 0.0f ? (mo[idx] * kTqScale * a.vsign[idx % HD]) / L : 0.0f;
         a.out16[((size_t)b * a.hq + kvh * G) * HD + idx] = f2h_bits(o);
     }
@@ -520,7 +604,7 @@ __global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batc
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
     const SplitPlan sp = plan_splits(batch, hkv, max_ctx);
     const int G = hq / hkv;
-    return sizeof(float) * (size_t)batch * hkv * sp.nsplit * G * (hd + 2);
+    return sizeof(float) * (size_t)batch * hkv * sp.nsplit * rec_floats(G, hd);
 }
 
 size_t attn_counter_count(int batch, int hkv) { return (size_t)batch * hkv; }

@@ -292,19 +292,138 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, const float (&
     }
 }
 
+constexpr int kB1MaxThreads = 512;
+
+// Block-cooperative staging of one x row into LDS in the pair layout:
+// sp[g*16 + 4d + j] = (x[32g+8d+j], x[32g+8d+j+4]) and s8[g] = 8 * sum of
+// group g.  Each thread converts 8-element chunks; for X_RMSNORM the block
+// first reduces sum(h^2) once, so the hidden state is read twice per block
+// rather than per wavefront.  Ends with a barrier.
+template <int XS>
+__device__ inline void stage_x(const GemvArgs& a, int b, uint32_t* sp, float* s8, float* red) {
+    const int K = a.K, nch = a.G * 4;
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    float inv = 1.0f;
+    const float* h = a.h32 + (size_t)b * a.ldx;
+    const uint16_t* x = a.x16 + (size_t)b * a.ldx;
+    if (XS == X_RMSNORM) {
+        float ss = 0.0f;
+        for (int c = tid; c < nch; c += nthr) {
+            const int k0 = 8 * c;
+            if (k0 + 8 <= K && ((reinterpret_cast<uintptr_t>(h + k0) & 15u) == 0)) {
+                const float4 v0 = *reinterpret_cast<const float4*>(h + k0);
+                const float4 v1 = *reinterpret_cast<const float4*>(h + k0 + 4);
+                ss += v0.x * v0.x;
+                ss += v0.y * v0.y;
+                ss += v0.z * v0.z;
+                ss += v0.w * v0.w;
+                ss += v1.x * v1.x;
+                ss += v1.y * v1.y;
+                ss += v1.z * v1.z;
+                ss += v1.w * v1.w;
+            } else {
+                for (int j = 0; j < 8; ++j)
+                    if (k0 + j < K) ss += h[k0 + j] * h[k0 + j];
+            }
+        }
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int w = 0; w < (nthr >> 6); ++w) tot += red[w];
+        inv = 1.0f / sqrtf(tot / (float)K + a.eps);
+    }
+    for (int c = tid; c < nch; c += nthr) {
+        const int k0 = 8 * c;
+        uint32_t X[4];
+        if (XS == X_F16) {
+            if (k0 + 8 <= K && ((reinterpret_cast<uintptr_t>(x + k0) & 15u) == 0)) {
+                const uint4 v = *reinterpret_cast<const uint4*>(x + k0);
+                X[0] = v.x;
+                X[1] = v.y;
+                X[2] = v.z;
+                X[3] = v.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t lo = k0 + 2 * j < K ? x[k0 + 2 * j] : 0u;
+                    const uint32_t hi = k0 + 2 * j + 1 < K ? x[k0 + 2 * j + 1] : 0u;
+                    X[j] = lo | (hi << 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t lo = 0, hi = 0;
+                const int k = k0 + 2 * j;
+                if (k < K) {
+                    const float v = h[k] * inv;
+                    lo = f2h_bits(a.norm_w ? v * a.norm_w[k] : v);
+                }
+                if (k + 1 < K) {
+                    const float v = h[k + 1] * inv;
+                    hi = f2h_bits(a.norm_w ? v * a.norm_w[k + 1] : v);
+                }
+                X[j] = lo | (hi << 16);
+            }
+        }
+        uint32_t* dst = sp + (c >> 2) * 16 + (c & 3) * 4;
+        dst[0] = __builtin_amdgcn_perm(X[2], X[0], 0x05040100u);
+        dst[1] = __builtin_amdgcn_perm(X[2], X[0], 0x07060302u);
+        dst[2] = __builtin_amdgcn_perm(X[3], X[1], 0x05040100u);
+        dst[3] = __builtin_amdgcn_perm(X[3], X[1], 0x07060302u);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s += h2f_bits((uint16_t)(X[j] & 0xFFFFu));
+            s += h2f_bits((uint16_t)(X[j] >> 16));
+        }
+        // the 4 chunks of a group sit in one DPP quad (nthr and nch are multiples of 4)
+        s += dpp<kQuadXor1>(s);
+        s += dpp<kQuadXor2>(s);
+        if ((c & 3) == 0) s8[c >> 2] = 8.0f * s;
+    }
+    __syncthreads();
+}
+
+template <int GPL>
+__device__ inline void load_pairs_lds(XPairs<GPL>& xp, const uint32_t* sp, const float* s8, int G,
+                                      int lane) {
+#pragma unroll
+    for (int i = 0; i < GPL; ++i) {
+        const int g = lane + kWave * i;
+        if (g < G) {
+            const uint4* src = reinterpret_cast<const uint4*>(sp + g * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = src[q];
+                xp.p[i][4 * q + 0] = v.x;
+                xp.p[i][4 * q + 1] = v.y;
+                xp.p[i][4 * q + 2] = v.z;
+                xp.p[i][4 * q + 3] = v.w;
+            }
+            xp.s8[i] = s8[g];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xp.p[i][j] = 0u;
+            xp.s8[i] = 0.0f;
+        }
+    }
+}
+
 // Batch 1.
 template <int GPL, int R, int XS, int EPI>
-__global__ __launch_bounds__(kBlockThreads) void k_gemv_b1(GemvArgs a) {
+__global__ __launch_bounds__(kB1MaxThreads) void k_gemv_b1(GemvArgs a) {
+    __shared__ uint32_t sp[kWave * GPL * 16];
+    __shared__ float s8[kWave * GPL];
+    __shared__ float red[kB1MaxThreads / kWave];
     const int lane = threadIdx.x & (kWave - 1);
-    const int wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const int nw = gridDim.x * kWavesPerBlock;
+    const int wpb = blockDim.x >> 6;
+    const int wid = blockIdx.x * wpb + (threadIdx.x >> 6);
+    const int nw = gridDim.x * wpb;
+    stage_x<XS>(a, 0, sp, s8, red);
     XPairs<GPL> xp;
-    if (XS == X_F16) {
-        load_x16<GPL>(xp, a.x16, a.K, a.G, lane);
-    } else {
-        const float inv = rms_inv<GPL>(a.h32, a.K, a.G, a.eps, lane);
-        load_x_norm<GPL>(xp, a.h32, a.norm_w, inv, a.K, a.G, lane);
-    }
+    load_pairs_lds<GPL>(xp, sp, s8, a.G, lane);
     float best_v = -__builtin_inff();
     int best_i = -1;
     for (int n0 = wid * R; n0 < a.N; n0 += nw * R) {
@@ -432,13 +551,21 @@ hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
 template <int GPL, int R, int XS, int EPI>
 hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
     const int tiles = (a.N + R - 1) / R;
+    if (a.batch == 1) {
+        // one wavefront per R-row tile; wavefronts per block chosen so the
+        // grid covers the 256 CUs, up to 8 per block (2 blocks of 8 per CU
+        // fit when the kernel stays under 128 VGPRs, 1 block otherwise)
+        int wpb = 1;
+        while (wpb < 8 && tiles >= 256 * wpb * 2) wpb *= 2;
+        int blocks = (tiles + wpb - 1) / wpb;
+        const int cap = GPL >= 7 ? 256 : 512;
+        if (wpb == 8 && blocks > cap) blocks = cap;
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, XS, EPI>), dim3(blocks), dim3(wpb * kWave), 0, st, a);
+        return hipGetLastError();
+    }
     int blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int cap = 1024;
-    if (blocks > cap) blocks = cap;
-    if (a.batch == 1)
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, XS, EPI>), dim3(blocks), dim3(kBlockThreads), 0, st, a);
-    else
-        hipLaunchKernelGGL((k_gemv_bn<GPL, R, XS, EPI>), dim3(blocks), dim3(kBlockThreads), 0, st, a);
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL((k_gemv_bn<GPL, R, XS, EPI>), dim3(blocks), dim3(kBlockThreads), 0, st, a);
     return hipGetLastError();
 }
 

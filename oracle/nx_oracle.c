@@ -804,8 +804,8 @@ static void ffn_moe(nxo_model* m, layer_t* ly, const float* xn, int B, float* ou
             gemv(&ly->ew3[e], xb, 1, m->u);
             nxo_swiglu(m->g, m->u, F, m->a);
             for (int i = 0; i < F; ++i) m->a[i] = round_f16(m->a[i]);
-            gemv(&ly->ew2[e], m->a, 1, m->dn);
-            for (int i = 0; i < d; ++i) ob[i] += w[j] * m->dn[i];
+            gemv(&ly->ew2[e], m->a, 1, m->acc);  /* expert output (out aliases m->dn) */
+            for (int i = 0; i < d; ++i) ob[i] += w[j] * m->acc[i];
         }
     }
 }

@@ -518,7 +518,65 @@ def test_tiny_model_step_vs_fp64_composition():
     m.close()
 
 
-def test_tiny_model_generate_is_deterministic():
+def test_tiny_moe_step_vs_fp64_composition():
+    """MoE FFN of the oracle model (hybrid_model.cpp:1656-1711 order: router
+    logits, softmax, top-k, renormalize, weighted sum of expert SwiGLUs)
+    against an fp64 composition, two steps on one sequence."""
+    cfg = dict(TINY, n_experts=4, top_k=2, seed=0x0E0E)
+    m = oracle.Model(**cfg)
+    toks = [5, 3000]
+    logits = [m.forward(np.array([t], np.int32))[0] for t in toks]
+    m.close()
+    seed, d, hq, hkv, hd, F, V, E = 0x0E0E, 256, 4, 2, 64, 688, 4096, 4
+    emb = oracle.gen_normal(V * d, seed, 1, 0.02).reshape(V, d).astype(np.float16).astype(np.float64)
+    lid = lambda Li, kind: 0x100 * (Li + 1) + kind
+    eid = lambda Li, e, w: 0x01000000 + 0x1000 * Li + 4 * e + w
+    W = []
+    for Li in range(2):
+        w = {k: _deq(lid(Li, i), n, kk, seed=seed) for k, i, n, kk in
+             (("q", 0, hq * hd, d), ("k", 1, hkv * hd, d), ("v", 2, hkv * hd, d), ("o", 3, d, hq * hd))}
+        w["r"] = _deq(lid(Li, 7), E, d, sigma=1 / np.sqrt(d), seed=seed)
+        w["e"] = [(_deq(eid(Li, e, 0), F, d, seed=seed), _deq(eid(Li, e, 1), F, d, seed=seed),
+                   _deq(eid(Li, e, 2), d, F, seed=seed)) for e in range(E)]
+        W.append(w)
+    lm = _deq(2, V, d, seed=seed)
+    f16r = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float64)
+    norm = lambda h: f16r(h / np.sqrt(np.mean(h**2) + 1e-5))
+    ang = lambda p: p * 10000.0 ** (-(2.0 * np.arange(hd // 2)) / hd)
+
+    def rope(x, p, heads):
+        z = x.reshape(heads, hd // 2, 2)
+        zc = (z[..., 0] + 1j * z[..., 1]) * np.exp(1j * ang(p))
+        return np.stack([zc.real, zc.imag], -1).reshape(-1)
+
+    cache = [([], []) for _ in range(2)]
+    for p, t in enumerate(toks):
+        h = emb[t].copy()
+        for Li in range(2):
+            w = W[Li]
+            xn = norm(h)
+            q, k, v = rope(w["q"] @ xn, p, hq), rope(w["k"] @ xn, p, hkv), w["v"] @ xn
+            cache[Li][0].append(f16r(k).reshape(hkv, hd))
+            cache[Li][1].append(f16r(v).reshape(hkv, hd))
+            att = _attn_fp64(q.reshape(hq, hd), np.array(cache[Li][0]), np.array(cache[Li][1]), hq, hkv, hd)
+            h = h + w["o"] @ f16r(att.reshape(-1))
+            xn = norm(h)
+            lg = w["r"] @ xn
+            pr = np.exp(lg - lg.max())
+            pr /= pr.sum()
+            top = np.argsort(-pr, kind="stable")[:2]
+            wts = pr[top] / pr[top].sum()
+            out = np.zeros(d)
+            for e, we in zip(top, wts):
+                g1, u1, d1 = w["e"][e]
+                g, u = g1 @ xn, u1 @ xn
+                out += we * (d1 @ f16r(g / (1 + np.exp(-g)) * u))
+            h = h + out
+        want = lm @ norm(h)
+        # fp16-rounded activations can land on the other side of a rounding
+        # boundary in fp32 vs fp64 (one fp16 ulp is 4.9e-4 relative)
+        assert rel_err(logits[p], want) < 5e-4
+
     p = oracle.prompt_tokens(0x5EED, 1, 16, 4096)
     a = oracle.Model(**TINY)
     b = oracle.Model(**TINY)
