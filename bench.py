@@ -72,22 +72,30 @@ def cpu_baseline(ctx_len: int, batch: int, kv_kind: int) -> dict:
 GEMV_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
 
 
-def gemv_microbench(ctx, batch: int = 1, iters: int = 100) -> list:
+def gemv_microbench(ctx, batch: int = 1, iters: int = 200) -> list:
     """Standalone int4-g32 GEMV (fp16 x, fp16 y) on the five 8B projection
-    shapes; bytes = N*K*0.5625 + batch*(2K + 2N), HIP-event timed."""
+    shapes; bytes = N*K*0.5625 + batch*(2K + 2N), HIP-event timed.  Each
+    shape rotates over enough weight copies (>= 768 MB in total) that every
+    launch reads its weights from HBM, not from the 256 MB last-level cache."""
     import ctypes as C
     out = []
     for N, K in GEMV_SHAPES:
         G = (K + 31) // 32
-        w, s = ctx.alloc(N * G * 16), ctx.alloc(N * G * 2)
+        wbytes = N * G * 18
+        ncopies = max(2, -(-(768 << 20) // wbytes))
+        ws = [ctx.alloc(N * G * 16) for _ in range(ncopies)]
+        ss = [ctx.alloc(N * G * 2) for _ in range(ncopies)]
         x, y = ctx.alloc(batch * K * 2), ctx.alloc(batch * N * 2)
+        warr = (C.c_uint64 * ncopies)(*ws)
+        sarr = (C.c_uint64 * ncopies)(*ss)
         ms = C.c_double()
-        ctx.check(ctx.L.nx_time_gemv(ctx.h, x, w, s, y, N, K, batch, iters, C.byref(ms)), "nx_time_gemv")
+        ctx.check(ctx.L.nx_time_gemv(ctx.h, x, warr, sarr, ncopies, y, N, K, batch, iters, C.byref(ms)),
+                  "nx_time_gemv")
         nbytes = N * K * 0.5625 + batch * (2 * K + 2 * N)
         gbs = nbytes / (ms.value * 1e-3) / 1e9
         out.append({"shape": f"{N}x{K}", "batch": batch, "us": round(ms.value * 1e3, 3),
                     "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)})
-        for b in (w, s, x, y):
+        for b in ws + ss + [x, y]:
             ctx.free(b)
     return out
 

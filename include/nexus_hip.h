@@ -244,14 +244,20 @@ nx_status nx_model_step_bytes(nx_model* m, double* bytes);
 
 /* ---------------------------------------------------------- measurement -- */
 /* Average device duration (ms) of the dominant decode kernel -- the fused
- * RMSNorm + gate/up int4 GEMV + SwiGLU of layer 0 -- over `iters`
- * back-to-back launches on the model's buffers, timed with HIP events on the
- * library stream; bytes = its algorithmic bytes per launch. */
+ * RMSNorm + gate/up int4 GEMV + SwiGLU -- over `iters` back-to-back launches
+ * on the model's buffers, launch i on layer i % n_layers (cold weights, as
+ * in a decode step), timed with HIP events on the library stream; bytes =
+ * its algorithmic bytes per launch. */
 nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double* bytes);
-/* Same for a standalone nx_gemv_int4_g32 launch of shape N x K, batch. */
-nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16, nx_buf y_f16,
-                       int N, int K, int batch, int iters, double* avg_ms);
-/* Same for nx_attn_decode_paged_f16 (and _tq when kind = 1) with the given buffers. */
+/* Same for standalone nx_gemv_int4_g32 launches of shape N x K, batch:
+ * launch i uses weight copy i % ncopies (wq[], scales_f16[]), so with enough
+ * copies every launch streams its weights from HBM rather than from the
+ * last-level cache. */
+nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x_f16, const nx_buf* wq, const nx_buf* scales_f16,
+                       int ncopies, nx_buf y_f16, int N, int K, int batch, int iters,
+                       double* avg_ms);
+/* Same for the paged attention of the model's cache kind (split and merge
+ * launches together), launch i over layer i % n_layers. */
 nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double* bytes);
 
 #ifdef __cplusplus

@@ -22,25 +22,15 @@ bool device_is_gfx950(int dev) {
     return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
 }
 
-nx_status ensure_attn_ws(nx_ctx* ctx, size_t bytes, size_t ncounters) {
-    if (bytes <= ctx->attn_ws_bytes && ncounters <= ctx->attn_ncounters) return NX_OK;
+nx_status ensure_attn_ws(nx_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->attn_ws_bytes) return NX_OK;
     if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "attention workspace must grow outside capture");
     NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (bytes > ctx->attn_ws_bytes) {
-        if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
-        ctx->attn_ws = nullptr;
-        ctx->attn_ws_bytes = 0;
-        NX_HIP(ctx, hipMalloc(&ctx->attn_ws, bytes));
-        ctx->attn_ws_bytes = bytes;
-    }
-    if (ncounters > ctx->attn_ncounters) {
-        if (ctx->attn_counters) (void)hipFree(ctx->attn_counters);
-        ctx->attn_counters = nullptr;
-        ctx->attn_ncounters = 0;
-        NX_HIP(ctx, hipMalloc(&ctx->attn_counters, ncounters * sizeof(unsigned int)));
-        NX_HIP(ctx, hipMemset(ctx->attn_counters, 0, ncounters * sizeof(unsigned int)));
-        ctx->attn_ncounters = ncounters;
-    }
+    if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+    ctx->attn_ws = nullptr;
+    ctx->attn_ws_bytes = 0;
+    NX_HIP(ctx, hipMalloc(&ctx->attn_ws, bytes));
+    ctx->attn_ws_bytes = bytes;
     return NX_OK;
 }
 
@@ -150,7 +140,6 @@ nx_status nx_destroy(nx_ctx* ctx) {
     if (ctx->token_exec) (void)hipGraphExecDestroy(ctx->token_exec);
     for (auto& kv : ctx->bufs) (void)hipFree(reinterpret_cast<void*>(kv.first));
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
-    if (ctx->attn_counters) (void)hipFree(ctx->attn_counters);
     (void)hipEventDestroy(ctx->ev0);
     (void)hipEventDestroy(ctx->ev1);
     (void)hipStreamDestroy(ctx->stream);
@@ -490,8 +479,8 @@ nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf v
     nx_status s = check_table(ctx, bt, lens, batch, max_blocks, num_blocks, false, "nx_attn_decode_paged_f16");
     if (s != NX_OK) return s;
     const int max_ctx = max_blocks * nx::kPage;
-    s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, hd, max_ctx),
-                       nx::attn_counter_count(batch, hkv));
+    if (max_ctx > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_blocks above the attention limit");
+    s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, hd, max_ctx));
     if (s != NX_OK) return s;
     nx::AttnArgs a{};
     a.q = dptr<const float>(q);
@@ -507,7 +496,6 @@ nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf v
     a.max_blocks = max_blocks;
     a.max_ctx = max_ctx;
     a.part = static_cast<float*>(ctx->attn_ws);
-    a.counters = ctx->attn_counters;
     return launched(ctx, nx::attn_f16_launch(a, ctx->stream), "attn_f16");
 }
 
@@ -555,7 +543,7 @@ nx_status nx_tq_append(nx_ctx* ctx, nx_buf k, nx_buf v, nx_buf ksg, nx_buf vsg, 
     if (s != NX_OK) return s;
     // the append kernel reads K and V from one [batch][2][hkv*128] staging layout
     const size_t stage = (size_t)batch * 2 * hkv * 128 * 4;
-    s = ensure_attn_ws(ctx, stage > ctx->attn_ws_bytes ? stage : ctx->attn_ws_bytes, ctx->attn_ncounters);
+    s = ensure_attn_ws(ctx, stage > ctx->attn_ws_bytes ? stage : ctx->attn_ws_bytes);
     if (s != NX_OK) return s;
     float* tmp = static_cast<float*>(ctx->attn_ws);
     for (int b = 0; b < batch; ++b) {
@@ -596,7 +584,8 @@ nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q, nx_buf kc4, nx_buf kc3,
     nx_status s = check_table(ctx, bt, lens, batch, max_blocks, num_blocks, false, "nx_attn_decode_paged_tq");
     if (s != NX_OK) return s;
     const int max_ctx = max_blocks * nx::kPage;
-    s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, 128, max_ctx), nx::attn_counter_count(batch, hkv));
+    if (max_ctx > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_blocks above the attention limit");
+    s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, 128, max_ctx));
     if (s != NX_OK) return s;
     nx::AttnArgs a{};
     a.q = dptr<const float>(q);
@@ -618,7 +607,6 @@ nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q, nx_buf kc4, nx_buf kc3,
     a.max_blocks = max_blocks;
     a.max_ctx = max_ctx;
     a.part = static_cast<float*>(ctx->attn_ws);
-    a.counters = ctx->attn_counters;
     return launched(ctx, nx::attn_tq_launch(a, ctx->stream), "attn_tq");
 }
 
@@ -631,7 +619,7 @@ nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits, nx_buf ids, nx_buf w, in
     NX_NEED(ctx, w, (size_t)batch * k * 4, "weights");
     // per-expert token lists live in the attention workspace
     const size_t extra = ((size_t)E + (size_t)E * batch * k) * 4;
-    nx_status s = ensure_attn_ws(ctx, extra > ctx->attn_ws_bytes ? extra : ctx->attn_ws_bytes, ctx->attn_ncounters);
+    nx_status s = ensure_attn_ws(ctx, extra > ctx->attn_ws_bytes ? extra : ctx->attn_ws_bytes);
     if (s != NX_OK) return s;
     nx::MoeArgs a{};
     a.logits = dptr<const float>(logits);
@@ -678,7 +666,7 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
     const size_t off_act = (off_slots + slots.size() * 4 + 255) / 256 * 256;
     const size_t off_y = (off_act + (size_t)batch * k * Fp * 2 + 255) / 256 * 256;
     const size_t total = off_y + (size_t)batch * k * d * 4;
-    nx_status s = ensure_attn_ws(ctx, total, ctx->attn_ncounters);
+    nx_status s = ensure_attn_ws(ctx, total);
     if (s != NX_OK) return s;
     char* ws = static_cast<char*>(ctx->attn_ws);
     NX_HIP(ctx, hipMemcpyAsync(ws, count.data(), count.size() * 4, hipMemcpyHostToDevice, ctx->stream));
@@ -717,14 +705,16 @@ nx_status nx_argmax(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch) {
     return launched(ctx, nx::argmax_launch(dptr<const float>(logits), dptr<int32_t>(out), V, batch, ctx->stream), "argmax");
 }
 
-nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
-                       int batch, int iters, double* avg_ms) {
-    if (!ctx || !avg_ms || iters < 1) return NX_ERR_INVALID;
-    nx_status s = nx_gemv_int4_g32(ctx, x, wq, sc, y, N, K, batch);  // warm-up and validation
-    if (s != NX_OK) return s;
+nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x, const nx_buf* wq, const nx_buf* sc, int ncopies,
+                       nx_buf y, int N, int K, int batch, int iters, double* avg_ms) {
+    if (!ctx || !avg_ms || !wq || !sc || ncopies < 1 || iters < 1) return NX_ERR_INVALID;
+    for (int c = 0; c < ncopies; ++c) {  // warm-up and validation of every copy
+        nx_status s = nx_gemv_int4_g32(ctx, x, wq[c], sc[c], y, N, K, batch);
+        if (s != NX_OK) return s;
+    }
     NX_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
     for (int i = 0; i < iters; ++i) {
-        s = nx_gemv_int4_g32(ctx, x, wq, sc, y, N, K, batch);
+        nx_status s = nx_gemv_int4_g32(ctx, x, wq[i % ncopies], sc[i % ncopies], y, N, K, batch);
         if (s != NX_OK) return s;
     }
     NX_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));

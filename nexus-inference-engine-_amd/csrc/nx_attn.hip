@@ -5,11 +5,15 @@
 // query heads that share it, so every K/V byte is read once per step.
 // Within a wavefront lane l owns dims [l%16 * DPL, +DPL) of the tokens
 // l/16, l/16+4, l/16+8, l/16+12 of each page; a score is reduced over the 16
-// lanes of a DPP row.  A wavefront issues the loads of two pages before it
-// computes either.  Each DPP row keeps its own online-softmax state
-// (m, l, o); rows, wavefronts and then splits are merged with the usual
-// rescaling.  The last block of a (sequence, kv head) to finish -- found with
-// an atomic counter, no spinning -- merges all splits and writes fp16 output.
+// lanes of a DPP row.  A block owns 8 pages (more for very long contexts);
+// each wavefront requests its block-table entries with q and then keeps two
+// pairs of pages in flight.  Each DPP row keeps its own online-softmax state
+// (m, l, o); rows and wavefronts are merged with the usual rescaling and the
+// block stores one split record.  A second small launch merges the split
+// records of each (sequence, kv head) and writes the fp16 output: a separate
+// launch costs less than handing the records across blocks inside one launch,
+// which on this multi-XCD part needs device-scope fences or several dependent
+// memory round trips.
 //
 // TurboQuant pages are scored in the rotated domain: the block rotates q once
 // (q~ = H D q / sqrt(128)), scores are n_t * <q~, c[code_t]>, V is summed in the
@@ -23,23 +27,27 @@ namespace {
 
 constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * kWave;
-constexpr int kTargetBlocks = 256;
 constexpr int kMaxSplits = 64;  // splits per (sequence, kv head)
 
 struct SplitPlan {
     int nsplit, pps;  // splits per (sequence, kv head), pages per split
 };
 
-SplitPlan plan_splits(int batch, int hkv, int max_ctx) {
+// A split is 8 pages (two per wavefront, all in flight at once) until
+// kMaxSplits splits per (sequence, kv head) are reached; longer contexts get
+// more pages per split.  A wavefront keeps its block-table entries one per
+// lane, which bounds a split at 4 * 64 pages: contexts up to
+// kMaxSplits * 256 pages (attn_max_ctx() tokens).
+constexpr int kPagesPerSplitMin = 2 * kAttnWaves;
+constexpr int kPagesPerSplitMax = kAttnWaves * kWave;
+
+SplitPlan plan_splits(int max_ctx) {
     const int pages = (max_ctx + kPage - 1) / kPage;
-    int nsplit = (kTargetBlocks + batch * hkv - 1) / (batch * hkv);
-    if (nsplit > kMaxSplits) nsplit = kMaxSplits;
-    if (nsplit > pages) nsplit = pages;
+    int pps = kPagesPerSplitMin;
+    if ((pages + pps - 1) / pps > kMaxSplits) pps = (pages + kMaxSplits - 1) / kMaxSplits;
+    int nsplit = (pages + pps - 1) / pps;
     if (nsplit < 1) nsplit = 1;
-    const int pps = (pages + nsplit - 1) / nsplit;
-    nsplit = (pages + pps - 1) / pps;
-    if (nsplit < 1) nsplit = 1;
-    return {nsplit, pps < 1 ? 1 : pps};
+    return {nsplit, pps};
 }
 
 // Split partial record, float offsets: O[G][HD] at 0, M[G], L[G], padded to 16 bytes.
@@ -158,68 +166,6 @@ __device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __re
     }
 }
 
-// Is this the last split block of its (sequence, kv head) to finish?
-__device__ inline bool arrive_last(unsigned int* counter, int nsplit, int* flag) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned int prev = atomicAdd(counter, 1u);
-        *flag = (prev == (unsigned int)(nsplit - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    const bool last = *flag != 0;
-    if (last) __threadfence();
-    return last;
-}
-
-// Merge all split records of (b, kvh) into out_o[G][HD] and out_l[G] (LDS).
-// fs: LDS scratch of kMaxSplits * G + G floats.  Split maxima and rescale
-// factors are computed once; the weighted sums then read float4s with the
-// loads of consecutive splits independent of each other.
-template <int G, int HD>
-__device__ inline void merge_splits(const float* __restrict__ parts, int nsplit, float* out_o,
-                                    float* out_l, float* fs) {
-    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    float* Mh = fs + kMaxSplits * G;
-    for (int idx = threadIdx.x; idx < nsplit * G; idx += kAttnThreads)
-        fs[idx] = parts[(size_t)(idx / G) * REC + MO + idx % G];
-    __syncthreads();
-    if (threadIdx.x < G) {
-        float M = -__builtin_inff();
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, fs[s * G + threadIdx.x]);
-        Mh[threadIdx.x] = M;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < nsplit * G; idx += kAttnThreads) {
-        const float M = Mh[idx % G];
-        fs[idx] = (M == -__builtin_inff()) ? 0.0f : __expf(fs[idx] - M);
-    }
-    __syncthreads();
-    constexpr int NQ = G * HD / 4;
-    for (int q = threadIdx.x; q < NQ + G; q += kAttnThreads) {
-        if (q < NQ) {
-            const int h = (4 * q) / HD;
-            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 16
-            for (int s = 0; s < nsplit; ++s) {
-                const float4 v = *reinterpret_cast<const float4*>(parts + (size_t)s * REC + 4 * q);
-                const float f = fs[s * G + h];
-                acc.x = fmaf(v.x, f, acc.x);
-                acc.y = fmaf(v.y, f, acc.y);
-                acc.z = fmaf(v.z, f, acc.z);
-                acc.w = fmaf(v.w, f, acc.w);
-            }
-            *reinterpret_cast<float4*>(out_o + 4 * q) = acc;
-        } else {
-            const int h = q - NQ;
-            float acc = 0.0f;
-            for (int s = 0; s < nsplit; ++s) acc = fmaf(parts[(size_t)s * REC + LO + h], fs[s * G + h], acc);
-            out_l[h] = acc;
-        }
-    }
-    __syncthreads();
-}
-
 // ------------------------------------------------------------ fp16 pages --
 // Raw fp16 K/V of one page for one lane: 4 tokens x DPL halves each.
 template <int DPL>
@@ -287,11 +233,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nspli
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, tg = lane >> 4;
-    __shared__ __align__(16) float lds[kAttnWaves * REC + G * HD + G];
-    __shared__ float fsh[kMaxSplits * G + G];
-    __shared__ int flag;
+    __shared__ __align__(16) float lds[kAttnWaves * REC];
 
+    // The context length, q and this wavefront's block-table entries (page
+    // p0 + wave + 4i in lane i) are requested together: one round trip.
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    const int p0 = split * pps;
+    const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
+    const int my_page = p0 + wave + kAttnWaves * lane;
+    const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
+                            ? a.block_table[(size_t)b * a.max_blocks + my_page]
+                            : 0;
     const float scale = 1.0f / sqrtf((float)HD);
     float q[G][DPL];
 #pragma unroll
@@ -303,32 +255,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nspli
     State<G, DPL> st;
     state_init(st);
     const int npages = (ctx + kPage - 1) / kPage;
-    const int p0 = split * pps;
     const int p1 = min(p0 + pps, npages);
-    const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
-    for (int p = p0 + wave; p < p1; p += 2 * kAttnWaves) {
-        const int pn = p + kAttnWaves;
-        PageRaw<DPL> r0, r1;
-        load_page_f16<DPL>(r0, a, bt[p], kvh, p, ctx, tg, c);
-        if (pn < p1) load_page_f16<DPL>(r1, a, bt[pn], kvh, pn, ctx, tg, c);
-        process_page_f16<G, DPL>(st, r0, q, scale, p, ctx, tg);
-        if (pn < p1) process_page_f16<G, DPL>(st, r1, q, scale, pn, ctx, tg);
+    // pages of this wavefront: p0 + wave + 4i for i < npw, two pairs in flight
+    const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
+#define NX_PAGE(i) (p0 + wave + kAttnWaves * (i))
+#define NX_LOAD(r, i) load_page_f16<DPL>(r, a, __builtin_amdgcn_readlane(bt_lane, (i)), kvh, NX_PAGE(i), ctx, tg, c)
+    PageRaw<DPL> a0, a1, b0, b1;
+    if (npw > 0) NX_LOAD(a0, 0);
+    if (npw > 1) NX_LOAD(a1, 1);
+    for (int i = 0; i < npw; i += 4) {
+        if (i + 2 < npw) NX_LOAD(b0, i + 2);
+        if (i + 3 < npw) NX_LOAD(b1, i + 3);
+        process_page_f16<G, DPL>(st, a0, q, scale, NX_PAGE(i), ctx, tg);
+        if (i + 1 < npw) process_page_f16<G, DPL>(st, a1, q, scale, NX_PAGE(i + 1), ctx, tg);
+        if (i + 2 >= npw) break;
+        if (i + 4 < npw) NX_LOAD(a0, i + 4);
+        if (i + 5 < npw) NX_LOAD(a1, i + 5);
+        process_page_f16<G, DPL>(st, b0, q, scale, NX_PAGE(i + 2), ctx, tg);
+        if (i + 3 < npw) process_page_f16<G, DPL>(st, b1, q, scale, NX_PAGE(i + 3), ctx, tg);
     }
+#undef NX_LOAD
+#undef NX_PAGE
     state_merge_rows(st);
 
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
     block_merge_store<G, HD>(st, parts + (size_t)split * REC, lds);
-    if (!arrive_last(a.counters + (size_t)b * a.hkv + kvh, nsplit, &flag)) return;
-
-    float* mo = lds + kAttnWaves * REC;
-    float* ml = mo + G * HD;
-    merge_splits<G, HD>(parts, nsplit, mo, ml, fsh);
-    for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads) {
-        const float L = ml[idx / HD];
-        const float o = L > 0.0f ? mo[idx] / L : 0.0f;
-        a.out16[((size_t)b * a.hq + kvh * G) * HD + idx] = f2h_bits(o);
-    }
-    if (threadIdx.x == 0) a.counters[(size_t)b * a.hkv + kvh] = 0u;
 }
 
 // ------------------------------------------------------ TurboQuant pages --
@@ -434,19 +385,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, tg = lane >> 4;
-    __shared__ __align__(16) float lds[kAttnWaves * REC + G * HD + G];
-    __shared__ float fsh[kMaxSplits * G + G];
+    __shared__ __align__(16) float lds[kAttnWaves * REC];
     __shared__ float qrot[G * HD];
     __shared__ float cb[24];
-    __shared__ int flag;
 
+    // context length and block-table entries first (see k_attn_f16)
+    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    const int p0 = split * pps;
+    const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
+    const int my_page = p0 + wave + kAttnWaves * lane;
+    const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
+                            ? a.block_table[(size_t)b * a.max_blocks + my_page]
+                            : 0;
     if (threadIdx.x < 16) cb[threadIdx.x] = c_tq_c4[threadIdx.x];
     else if (threadIdx.x < 24) cb[threadIdx.x] = c_tq_c3[threadIdx.x - 16];
     for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads)
         qrot[idx] = a.ksign[idx % HD] * a.q[((size_t)b * a.hq + kvh * G) * HD + idx];
     lds_fwht<G>(qrot);
 
-    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
     float q[G][DPL];
 #pragma unroll
@@ -457,34 +413,79 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
     State<G, DPL> st;
     state_init(st);
     const int npages = (ctx + kPage - 1) / kPage;
-    const int p0 = split * pps;
     const int p1 = min(p0 + pps, npages);
-    const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
-    for (int p = p0 + wave; p < p1; p += 2 * kAttnWaves) {
-        const int pn = p + kAttnWaves;
-        TqRaw r0, r1;
-        load_page_tq(r0, a, bt[p], kvh, p, ctx, tg, c);
-        if (pn < p1) load_page_tq(r1, a, bt[pn], kvh, pn, ctx, tg, c);
-        process_page_tq<G>(st, r0, q, scale, p, ctx, tg, c, cb);
-        if (pn < p1) process_page_tq<G>(st, r1, q, scale, pn, ctx, tg, c, cb);
+    const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
+#define NX_PAGE(i) (p0 + wave + kAttnWaves * (i))
+#define NX_LOAD(r, i) load_page_tq(r, a, __builtin_amdgcn_readlane(bt_lane, (i)), kvh, NX_PAGE(i), ctx, tg, c)
+    TqRaw a0, a1, b0, b1;
+    if (npw > 0) NX_LOAD(a0, 0);
+    if (npw > 1) NX_LOAD(a1, 1);
+    for (int i = 0; i < npw; i += 4) {
+        if (i + 2 < npw) NX_LOAD(b0, i + 2);
+        if (i + 3 < npw) NX_LOAD(b1, i + 3);
+        process_page_tq<G>(st, a0, q, scale, NX_PAGE(i), ctx, tg, c, cb);
+        if (i + 1 < npw) process_page_tq<G>(st, a1, q, scale, NX_PAGE(i + 1), ctx, tg, c, cb);
+        if (i + 2 >= npw) break;
+        if (i + 4 < npw) NX_LOAD(a0, i + 4);
+        if (i + 5 < npw) NX_LOAD(a1, i + 5);
+        process_page_tq<G>(st, b0, q, scale, NX_PAGE(i + 2), ctx, tg, c, cb);
+        if (i + 3 < npw) process_page_tq<G>(st, b1, q, scale, NX_PAGE(i + 3), ctx, tg, c, cb);
     }
+#undef NX_LOAD
+#undef NX_PAGE
     state_merge_rows(st);
 
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
     block_merge_store<G, HD>(st, parts + (size_t)split * REC, lds);
-    if (!arrive_last(a.counters + (size_t)b * a.hkv + kvh, nsplit, &flag)) return;
+}
 
-    float* mo = lds + kAttnWaves * REC;
-    float* ml = mo + G * HD;
-    merge_splits<G, HD>(parts, nsplit, mo, ml, fsh);
-    // rotate back: o = D_v H o~ / sqrt(128)
-    lds_fwht<G>(mo);
-    for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads) {
-        const float L = ml[idx / HD];
-        const float o = L > 0.0f ? (mo[idx] * kTqScale * a.vsign[idx % HD]) / L : 0.0f;
-        a.out16[((size_t)b * a.hq + kvh * G) * HD + idx] = f2h_bits(o);
+// Merge the split records of one query head: block (h, kv head, sequence),
+// one thread per dimension.  Every thread requests its nsplit partial sums
+// and the heads' split maxima / sums at once (one memory round trip), then
+// rescales and sums in split order.  TQ: the merged value sum is still in the
+// rotated domain and is rotated back once, o = D_v H o~ / sqrt(128).
+template <int G, int HD, bool TQ>
+__global__ __launch_bounds__(HD) void k_attn_merge(AttnArgs a, int nsplit) {
+    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
+    const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+    __shared__ float ms[kMaxSplits], ls[kMaxSplits];
+    __shared__ float ov[HD];
+    const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
+    float o[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) o[s] = s < nsplit ? parts[(size_t)s * REC + h * HD + t] : 0.0f;
+    for (int s = t; s < nsplit; s += HD) {
+        ms[s] = parts[(size_t)s * REC + MO + h];
+        ls[s] = parts[(size_t)s * REC + LO + h];
     }
-    if (threadIdx.x == 0) a.counters[(size_t)b * a.hkv + kvh] = 0u;
+    __syncthreads();
+    float M = -__builtin_inff();
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ms[s]);
+    float acc = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+        if (s < nsplit) {
+            const float f = (M == -__builtin_inff()) ? 0.0f : __expf(ms[s] - M);
+            acc = fmaf(o[s], f, acc);
+            L = fmaf(ls[s], f, L);
+        }
+    }
+    if (TQ) {
+        ov[t] = acc;
+        for (int hh = 1; hh < HD; hh <<= 1) {
+            __syncthreads();
+            if (t < HD / 2) {
+                const int j = ((t / hh) * 2 * hh) + (t % hh);
+                const float x = ov[j], y = ov[j + hh];
+                ov[j] = x + y;
+                ov[j + hh] = x - y;
+            }
+        }
+        __syncthreads();
+        acc = ov[t] * kTqScale * a.vsign[t];
+    }
+    const float out = L > 0.0f ? acc / L : 0.0f;
+    a.out16[((size_t)b * a.hq + kvh * G + h) * HD + t] = f2h_bits(out);
 }
 
 // ----------------------------------------------------- TurboQuant encode --
@@ -602,22 +603,24 @@ __global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batc
 }  // namespace
 
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
-    const SplitPlan sp = plan_splits(batch, hkv, max_ctx);
+    const SplitPlan sp = plan_splits(max_ctx);
     const int G = hq / hkv;
     return sizeof(float) * (size_t)batch * hkv * sp.nsplit * rec_floats(G, hd);
 }
 
-size_t attn_counter_count(int batch, int hkv) { return (size_t)batch * hkv; }
+int attn_max_ctx() { return kMaxSplits * kPagesPerSplitMax * kPage; }
 
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
-    const SplitPlan sp = plan_splits(a.batch, a.hkv, a.max_ctx);
-    const dim3 grid(sp.nsplit, a.hkv, a.batch);
+    const SplitPlan sp = plan_splits(a.max_ctx);
+    const dim3 grid(sp.nsplit, a.hkv, a.batch), mgrid(a.hq / a.hkv, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
-#define NX_ATTN_CASE(GG, HH)                                                                   \
-    if (G == GG && a.hd == HH) {                                                               \
-        hipLaunchKernelGGL((k_attn_f16<GG, HH>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit, \
-                           sp.pps);                                                            \
-        return hipGetLastError();                                                              \
+#define NX_ATTN_CASE(GG, HH)                                                                      \
+    if (G == GG && a.hd == HH) {                                                                  \
+        hipLaunchKernelGGL((k_attn_f16<GG, HH>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit,    \
+                           sp.pps);                                                               \
+        hipLaunchKernelGGL((k_attn_merge<GG, HH, false>), mgrid, dim3(HH), 0, st, a,              \
+                           sp.nsplit);                                                            \
+        return hipGetLastError();                                                                 \
     }
     NX_ATTN_CASE(1, 64)
     NX_ATTN_CASE(2, 64)
@@ -632,15 +635,17 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st) {
-    const SplitPlan sp = plan_splits(a.batch, a.hkv, a.max_ctx);
-    const dim3 grid(sp.nsplit, a.hkv, a.batch);
+    const SplitPlan sp = plan_splits(a.max_ctx);
+    const dim3 grid(sp.nsplit, a.hkv, a.batch), mgrid(a.hq / a.hkv, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
     if (a.hd != 128) return hipErrorInvalidValue;
-#define NX_ATTN_CASE(GG)                                                                      \
-    if (G == GG) {                                                                            \
-        hipLaunchKernelGGL((k_attn_tq<GG>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit,    \
-                           sp.pps);                                                           \
-        return hipGetLastError();                                                             \
+#define NX_ATTN_CASE(GG)                                                                          \
+    if (G == GG) {                                                                                \
+        hipLaunchKernelGGL((k_attn_tq<GG>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit,        \
+                           sp.pps);                                                               \
+        hipLaunchKernelGGL((k_attn_merge<GG, 128, true>), mgrid, dim3(128), 0, st, a,             \
+                           sp.nsplit);                                                            \
+        return hipGetLastError();                                                                 \
     }
     NX_ATTN_CASE(1)
     NX_ATTN_CASE(2)

@@ -7,8 +7,11 @@
 // (i < GPL).  Each lane keeps the x values of its groups in registers for
 // the whole launch, pre-paired for the nibble layout, so weights are the only
 // HBM stream: one 16-byte load (one group = 32 codes) plus one 2-byte scale
-// per lane per row, coalesced into 1 KiB per wave instruction.  R rows are
-// issued together to keep R*GPL loads in flight per lane.
+// per lane per row, coalesced into 1 KiB per wave instruction.  R rows form a
+// tile whose R*GPL loads are in flight together.  At batch 1 the grid is
+// persistent (8 wavefronts per CU), each wavefront streams a contiguous row
+// range with the next tile requested before the current one is reduced, and
+// the first tile is requested before the input is staged.
 //
 // Dequantisation without per-code conversion: the four masks
 //   A = w & 0x000F000F   (k0, k4)      B = w & 0x00F000F0   (k1, k5) * 16
@@ -23,7 +26,7 @@
 // handed to an epilogue: plain fp16/fp32 store, residual add, QKV with RoPE
 // and the paged KV append, SwiGLU of interleaved gate/up rows, or logits
 // with a running argmax.  The input is either fp16 x or the fused RMSNorm of
-// an fp32 hidden state, computed redundantly per wavefront.
+// an fp32 hidden state, computed once per block into LDS.
 #include "nx_common.h"
 #include "nx_kernels.h"
 
@@ -174,12 +177,14 @@ __device__ inline float group_dot(uint4 w, const uint32_t (&P)[16], float s8) {
 template <int GPL, int R>
 struct Tile {
     uint4 w[R][GPL];
-    float s[R][GPL];
+    uint16_t s[R][GPL];  // raw fp16 scales, converted at use so no wait is forced at load
 };
 
+// Load rows [n0, n0 + R) of the weight matrix; rows at or beyond `nlim`
+// (the end of this wavefront's row range) are not read and count as zero.
 template <int GPL, int R>
 __device__ inline void load_tile(Tile<GPL, R>& t, const uint8_t* __restrict__ W,
-                                 const uint16_t* __restrict__ S, int G, int N, int n0,
+                                 const uint16_t* __restrict__ S, int G, int nlim, int n0,
                                  int lane) {
     const size_t rowbytes = (size_t)G * 16;
 #pragma unroll
@@ -188,12 +193,12 @@ __device__ inline void load_tile(Tile<GPL, R>& t, const uint8_t* __restrict__ W,
 #pragma unroll
         for (int i = 0; i < GPL; ++i) {
             const int g = lane + kWave * i;
-            if (row < N && g < G) {
+            if (row < nlim && g < G) {
                 t.w[r][i] = *reinterpret_cast<const uint4*>(W + (size_t)row * rowbytes + 16 * (size_t)g);
-                t.s[r][i] = h2f_bits(S[(size_t)row * G + g]);
+                t.s[r][i] = S[(size_t)row * G + g];
             } else {
                 t.w[r][i] = make_uint4(0u, 0u, 0u, 0u);
-                t.s[r][i] = 0.0f;
+                t.s[r][i] = 0;
             }
         }
     }
@@ -205,7 +210,8 @@ __device__ inline void tile_dot(const Tile<GPL, R>& t, const XPairs<GPL>& xp, fl
     for (int r = 0; r < R; ++r) {
         float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < GPL; ++i) acc = fmaf(group_dot(t.w[r][i], xp.p[i], xp.s8[i]), t.s[r][i], acc);
+        for (int i = 0; i < GPL; ++i)
+            acc = fmaf(group_dot(t.w[r][i], xp.p[i], xp.s8[i]), h2f_bits(t.s[r][i]), acc);
         res[r] = wave_sum(acc);
     }
 }
@@ -216,21 +222,22 @@ __device__ inline unsigned long long pack_best(float v, int idx) {
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+// Rows at or beyond `nlim` are not stored.
 template <int EPI, int R>
-__device__ inline void epilogue(const GemvArgs& a, int b, int n0, const float (&res)[R],
+__device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, const float (&res)[R],
                                 float& best_v, int& best_i) {
     if (EPI == E_F16) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (n0 + r < a.N) a.y16[(size_t)b * a.ldy + n0 + r] = f2h_bits(res[r]);
+            if (n0 + r < nlim) a.y16[(size_t)b * a.ldy + n0 + r] = f2h_bits(res[r]);
     } else if (EPI == E_F32) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (n0 + r < a.N) a.y32[(size_t)b * a.ldy + n0 + r] = res[r];
+            if (n0 + r < nlim) a.y32[(size_t)b * a.ldy + n0 + r] = res[r];
     } else if (EPI == E_ACC) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (n0 + r < a.N) {
+            if (n0 + r < nlim) {
                 float* y = a.y32 + (size_t)b * a.ldy + n0 + r;
                 *y = *y + res[r];
             }
@@ -240,7 +247,7 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, const float (&
 #pragma unroll
         for (int r = 0; r < R; r += 2) {
             const int row = n0 + r;
-            if (row >= a.N) break;
+            if (row >= nlim) break;
             float v0 = res[r], v1 = res[r + 1];
             if (row < a.qdim + a.kvdim) {
                 const int i = (row % a.hd) >> 1;
@@ -275,14 +282,14 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, const float (&
 #pragma unroll
         for (int r = 0; r < R; r += 2) {
             const int row = n0 + r;
-            if (row >= a.N) break;
+            if (row >= nlim) break;
             const float g = res[r], u = res[r + 1];
             a.act16[(size_t)b * a.lda + (row >> 1)] = f2h_bits(g / (1.0f + expf(-g)) * u);
         }
     } else if (EPI == E_LOGITS) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (n0 + r < a.N) {
+            if (n0 + r < nlim) {
                 a.y32[(size_t)b * a.ldy + n0 + r] = res[r];
                 if (res[r] > best_v) {
                     best_v = res[r];
@@ -292,96 +299,143 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, const float (&
     }
 }
 
-constexpr int kB1MaxThreads = 512;
+// Eight consecutive inputs starting at k0 (zero beyond K).
+__device__ inline void load_h8(const float* __restrict__ h, int k0, int K, bool vec, float (&v)[8]) {
+    if (vec && k0 + 8 <= K) {
+        const float4 a = *reinterpret_cast<const float4*>(h + k0);
+        const float4 c = *reinterpret_cast<const float4*>(h + k0 + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = k0 + j < K ? h[k0 + j] : 0.0f;
+    }
+}
+__device__ inline void load_x8(const uint16_t* __restrict__ x, int k0, int K, bool vec, uint32_t (&X)[4]) {
+    if (vec && k0 + 8 <= K) {
+        const uint4 v = *reinterpret_cast<const uint4*>(x + k0);
+        X[0] = v.x; X[1] = v.y; X[2] = v.z; X[3] = v.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = k0 + 2 * j < K ? x[k0 + 2 * j] : 0u;
+            const uint32_t hi = k0 + 2 * j + 1 < K ? x[k0 + 2 * j + 1] : 0u;
+            X[j] = lo | (hi << 16);
+        }
+    }
+}
+
+// Store one 8-element chunk c (fp16 values X) in the pair layout and its
+// contribution to the group sum.
+__device__ inline void put_chunk(int c, const uint32_t (&X)[4], uint32_t* sp, float* s8) {
+    uint32_t* dst = sp + (c >> 2) * 16 + (c & 3) * 4;
+    dst[0] = __builtin_amdgcn_perm(X[2], X[0], 0x05040100u);
+    dst[1] = __builtin_amdgcn_perm(X[2], X[0], 0x07060302u);
+    dst[2] = __builtin_amdgcn_perm(X[3], X[1], 0x05040100u);
+    dst[3] = __builtin_amdgcn_perm(X[3], X[1], 0x07060302u);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        s += h2f_bits((uint16_t)(X[j] & 0xFFFFu));
+        s += h2f_bits((uint16_t)(X[j] >> 16));
+    }
+    // the 4 chunks of a group sit in one DPP quad (nthr and nch are multiples of 4)
+    s += dpp<kQuadXor1>(s);
+    s += dpp<kQuadXor2>(s);
+    if ((c & 3) == 0) s8[c >> 2] = 8.0f * s;
+}
+
+__device__ inline void norm_chunk(const float (&v)[8], const float* __restrict__ w, int k0, int K,
+                                  float inv, uint32_t (&X)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t lo = 0, hi = 0;
+        const int k = k0 + 2 * j;
+        if (k < K) {
+            const float t = v[2 * j] * inv;
+            lo = f2h_bits(w ? t * w[k] : t);
+        }
+        if (k + 1 < K) {
+            const float t = v[2 * j + 1] * inv;
+            hi = f2h_bits(w ? t * w[k + 1] : t);
+        }
+        X[j] = lo | (hi << 16);
+    }
+}
 
 // Block-cooperative staging of one x row into LDS in the pair layout:
 // sp[g*16 + 4d + j] = (x[32g+8d+j], x[32g+8d+j+4]) and s8[g] = 8 * sum of
-// group g.  Each thread converts 8-element chunks; for X_RMSNORM the block
-// first reduces sum(h^2) once, so the hidden state is read twice per block
-// rather than per wavefront.  Ends with a barrier.
+// group g.  Thread t handles the 8-element chunks t, t + nthr, ...; up to
+// kStageBatch chunks per thread are requested together, so a row of up to
+// kStageBatch * 8 * nthr elements costs one memory round trip, and for
+// X_RMSNORM the hidden state is kept in registers between the block's
+// sum(h^2) reduction and the conversion.  Ends with a barrier.
+constexpr int kStageBatch = 4;
+
 template <int XS>
 __device__ inline void stage_x(const GemvArgs& a, int b, uint32_t* sp, float* s8, float* red) {
     const int K = a.K, nch = a.G * 4;
     const int tid = threadIdx.x, nthr = blockDim.x;
-    float inv = 1.0f;
-    const float* h = a.h32 + (size_t)b * a.ldx;
-    const uint16_t* x = a.x16 + (size_t)b * a.ldx;
-    if (XS == X_RMSNORM) {
+    const int step = kStageBatch * nthr;
+    if (XS == X_F16) {
+        const uint16_t* x = a.x16 + (size_t)b * a.ldx;
+        const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (a.ldx & 7) == 0;
+        for (int c0 = tid; c0 < nch; c0 += step) {
+            uint32_t X[kStageBatch][4];
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j)
+                if (c0 + j * nthr < nch) load_x8(x, 8 * (c0 + j * nthr), K, vec, X[j]);
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j)
+                if (c0 + j * nthr < nch) put_chunk(c0 + j * nthr, X[j], sp, s8);
+        }
+    } else {
+        const float* h = a.h32 + (size_t)b * a.ldx;
+        const bool vec = (reinterpret_cast<uintptr_t>(h) & 15u) == 0 && (a.ldx & 3) == 0;
+        float v[kStageBatch][8];
         float ss = 0.0f;
-        for (int c = tid; c < nch; c += nthr) {
-            const int k0 = 8 * c;
-            if (k0 + 8 <= K && ((reinterpret_cast<uintptr_t>(h + k0) & 15u) == 0)) {
-                const float4 v0 = *reinterpret_cast<const float4*>(h + k0);
-                const float4 v1 = *reinterpret_cast<const float4*>(h + k0 + 4);
-                ss += v0.x * v0.x;
-                ss += v0.y * v0.y;
-                ss += v0.z * v0.z;
-                ss += v0.w * v0.w;
-                ss += v1.x * v1.x;
-                ss += v1.y * v1.y;
-                ss += v1.z * v1.z;
-                ss += v1.w * v1.w;
-            } else {
-                for (int j = 0; j < 8; ++j)
-                    if (k0 + j < K) ss += h[k0 + j] * h[k0 + j];
-            }
+        for (int c0 = tid; c0 < nch; c0 += step) {
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j)
+                if (c0 + j * nthr < nch) load_h8(h, 8 * (c0 + j * nthr), K, vec, v[j]);
+#pragma unroll
+            for (int j = 0; j < kStageBatch; ++j)
+                if (c0 + j * nthr < nch)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
         }
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         float tot = 0.0f;
         for (int w = 0; w < (nthr >> 6); ++w) tot += red[w];
-        inv = 1.0f / sqrtf(tot / (float)K + a.eps);
-    }
-    for (int c = tid; c < nch; c += nthr) {
-        const int k0 = 8 * c;
-        uint32_t X[4];
-        if (XS == X_F16) {
-            if (k0 + 8 <= K && ((reinterpret_cast<uintptr_t>(x + k0) & 15u) == 0)) {
-                const uint4 v = *reinterpret_cast<const uint4*>(x + k0);
-                X[0] = v.x;
-                X[1] = v.y;
-                X[2] = v.z;
-                X[3] = v.w;
-            } else {
+        const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
+        if (nch <= step) {  // the row is still in registers
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t lo = k0 + 2 * j < K ? x[k0 + 2 * j] : 0u;
-                    const uint32_t hi = k0 + 2 * j + 1 < K ? x[k0 + 2 * j + 1] : 0u;
-                    X[j] = lo | (hi << 16);
+            for (int j = 0; j < kStageBatch; ++j) {
+                const int c = tid + j * nthr;
+                if (c < nch) {
+                    uint32_t X[4];
+                    norm_chunk(v[j], a.norm_w, 8 * c, K, inv, X);
+                    put_chunk(c, X, sp, s8);
                 }
             }
         } else {
+            for (int c0 = tid; c0 < nch; c0 += step) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t lo = 0, hi = 0;
-                const int k = k0 + 2 * j;
-                if (k < K) {
-                    const float v = h[k] * inv;
-                    lo = f2h_bits(a.norm_w ? v * a.norm_w[k] : v);
+                for (int j = 0; j < kStageBatch; ++j)
+                    if (c0 + j * nthr < nch) load_h8(h, 8 * (c0 + j * nthr), K, vec, v[j]);
+#pragma unroll
+                for (int j = 0; j < kStageBatch; ++j) {
+                    const int c = c0 + j * nthr;
+                    if (c < nch) {
+                        uint32_t X[4];
+                        norm_chunk(v[j], a.norm_w, 8 * c, K, inv, X);
+                        put_chunk(c, X, sp, s8);
+                    }
                 }
-                if (k + 1 < K) {
-                    const float v = h[k + 1] * inv;
-                    hi = f2h_bits(a.norm_w ? v * a.norm_w[k + 1] : v);
-                }
-                X[j] = lo | (hi << 16);
             }
         }
-        uint32_t* dst = sp + (c >> 2) * 16 + (c & 3) * 4;
-        dst[0] = __builtin_amdgcn_perm(X[2], X[0], 0x05040100u);
-        dst[1] = __builtin_amdgcn_perm(X[2], X[0], 0x07060302u);
-        dst[2] = __builtin_amdgcn_perm(X[3], X[1], 0x05040100u);
-        dst[3] = __builtin_amdgcn_perm(X[3], X[1], 0x07060302u);
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            s += h2f_bits((uint16_t)(X[j] & 0xFFFFu));
-            s += h2f_bits((uint16_t)(X[j] >> 16));
-        }
-        // the 4 chunks of a group sit in one DPP quad (nthr and nch are multiples of 4)
-        s += dpp<kQuadXor1>(s);
-        s += dpp<kQuadXor2>(s);
-        if ((c & 3) == 0) s8[c >> 2] = 8.0f * s;
     }
     __syncthreads();
 }
@@ -411,27 +465,61 @@ __device__ inline void load_pairs_lds(XPairs<GPL>& xp, const uint32_t* sp, const
     }
 }
 
-// Batch 1.
-template <int GPL, int R, int XS, int EPI>
-__global__ __launch_bounds__(kB1MaxThreads) void k_gemv_b1(GemvArgs a) {
-    __shared__ uint32_t sp[kWave * GPL * 16];
+// Row range of wavefront `w` for batch 1: rows are dealt in pairs (a pair is
+// never split, so the RoPE and SwiGLU epilogues see both rows), `base` pairs
+// per wavefront plus one more for the first `extra` wavefronts.
+struct RowSplit {
+    int base, extra;
+};
+
+__device__ inline void wave_rows(const RowSplit& rs, int w, int N, int& r0, int& r1) {
+    const int u0 = w * rs.base + min(w, rs.extra);
+    const int nu = rs.base + (w < rs.extra ? 1 : 0);
+    r0 = min(2 * u0, N);
+    r1 = min(2 * (u0 + nu), N);
+}
+
+// Batch 1, persistent: every wavefront streams its own contiguous row range
+// as R-row tiles through a two-deep register pipeline (the next tile's loads
+// are in flight while the current one is reduced).  The first tile is
+// requested before x is staged, so the HBM stream starts with the kernel.
+template <int GPL, int R, int XS, int EPI, bool PIPE>
+__global__ __launch_bounds__(kBlockThreads) void k_gemv_b1(GemvArgs a, RowSplit rs) {
+    __shared__ __align__(16) uint32_t sp[kWave * GPL * 16];
     __shared__ float s8[kWave * GPL];
-    __shared__ float red[kB1MaxThreads / kWave];
+    __shared__ float red[kWavesPerBlock];
     const int lane = threadIdx.x & (kWave - 1);
-    const int wpb = blockDim.x >> 6;
-    const int wid = blockIdx.x * wpb + (threadIdx.x >> 6);
-    const int nw = gridDim.x * wpb;
-    stage_x<XS>(a, 0, sp, s8, red);
+    const int wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    int r0, r1;
+    wave_rows(rs, wid, a.N, r0, r1);
+    Tile<GPL, R> t0, t1;
+    if (r0 < r1) load_tile<GPL, R>(t0, a.W, a.S, a.G, r1, r0, lane);
+    if (PIPE && r0 + R < r1) load_tile<GPL, R>(t1, a.W, a.S, a.G, r1, r0 + R, lane);
+    stage_x<XS>(a, 0, sp, s8, red);  // block barrier: every wavefront takes part
+    if (r0 >= r1) return;
     XPairs<GPL> xp;
     load_pairs_lds<GPL>(xp, sp, s8, a.G, lane);
     float best_v = -__builtin_inff();
     int best_i = -1;
-    for (int n0 = wid * R; n0 < a.N; n0 += nw * R) {
-        Tile<GPL, R> t;
-        load_tile<GPL, R>(t, a.W, a.S, a.G, a.N, n0, lane);
-        float res[R];
-        tile_dot<GPL, R>(t, xp, res);
-        if (lane == 0) epilogue<EPI, R>(a, 0, n0, res, best_v, best_i);
+    float res[R];
+    if (PIPE) {
+        // t0 holds rows n0, t1 rows n0 + R; each buffer is refilled as soon
+        // as it has been reduced, so two tiles stay in flight
+        for (int n0 = r0; n0 < r1; n0 += 2 * R) {
+            tile_dot<GPL, R>(t0, xp, res);
+            if (lane == 0) epilogue<EPI, R>(a, 0, n0, r1, res, best_v, best_i);
+            if (n0 + 2 * R < r1) load_tile<GPL, R>(t0, a.W, a.S, a.G, r1, n0 + 2 * R, lane);
+            if (n0 + R >= r1) break;
+            tile_dot<GPL, R>(t1, xp, res);
+            if (lane == 0) epilogue<EPI, R>(a, 0, n0 + R, r1, res, best_v, best_i);
+            if (n0 + 3 * R < r1) load_tile<GPL, R>(t1, a.W, a.S, a.G, r1, n0 + 3 * R, lane);
+        }
+    } else {
+        for (int n0 = r0; n0 < r1; n0 += R) {
+            if (n0 != r0) load_tile<GPL, R>(t0, a.W, a.S, a.G, r1, n0, lane);
+            tile_dot<GPL, R>(t0, xp, res);
+            if (lane == 0) epilogue<EPI, R>(a, 0, n0, r1, res, best_v, best_i);
+        }
     }
     if (EPI == E_LOGITS && lane == 0 && best_i >= 0) atomicMax(&a.best[0], pack_best(best_v, best_i));
 }
@@ -464,7 +552,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_gemv_bn(GemvArgs a) {
                 load_x_norm<GPL>(xp, a.h32 + (size_t)b * a.ldx, a.norm_w, inv[b], a.K, a.G, lane);
             float res[R];
             tile_dot<GPL, R>(t, xp, res);
-            if (lane == 0) epilogue<EPI, R>(a, b, n0, res, best_v[b], best_i[b]);
+            if (lane == 0) epilogue<EPI, R>(a, b, n0, a.N, res, best_v[b], best_i[b]);
         }
     }
     if (EPI == E_LOGITS && lane == 0)
@@ -548,19 +636,39 @@ hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Wavefronts per CU of the batch-1 GEMV: two per SIMD.
+constexpr int kB1WavesPerCU = 8;
+
 template <int GPL, int R, int XS, int EPI>
 hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
     const int tiles = (a.N + R - 1) / R;
     if (a.batch == 1) {
-        // one wavefront per R-row tile; wavefronts per block chosen so the
-        // grid covers the 256 CUs, up to 8 per block (2 blocks of 8 per CU
-        // fit when the kernel stays under 128 VGPRs, 1 block otherwise)
-        int wpb = 1;
-        while (wpb < 8 && tiles >= 256 * wpb * 2) wpb *= 2;
-        int blocks = (tiles + wpb - 1) / wpb;
-        const int cap = GPL >= 7 ? 256 : 512;
-        if (wpb == 8 && blocks > cap) blocks = cap;
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, XS, EPI>), dim3(blocks), dim3(wpb * kWave), 0, st, a);
+        // a persistent grid of 8 wavefronts per CU, each with at least one
+        // full tile; row pairs are dealt out evenly
+        const int units = (a.N + 1) / 2;
+        const int min_units = R / 2;
+        int waves = device_cus() * kB1WavesPerCU;
+        const int maxw = (units + min_units - 1) / min_units;
+        if (waves > maxw) waves = maxw;
+        waves = (waves + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
+        const RowSplit rs{units / waves, units % waves};
+        constexpr bool kPipe = GPL <= 4;
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, XS, EPI, kPipe>), dim3(waves / kWavesPerBlock),
+                           dim3(kBlockThreads), 0, st, a, rs);
         return hipGetLastError();
     }
     int blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;

@@ -77,10 +77,11 @@ struct AttnArgs {
     int max_ctx;                 // upper bound of ctx_lens (sizes the split grid)
     // workspace
     float* part;                 // partial (m, l, o) per split
-    unsigned int* counters;      // [batch][hkv], zero between launches
 };
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
-size_t attn_counter_count(int batch, int hkv);
+// Longest context the attention kernels accept.
+int attn_max_ctx();
+// Each enqueues two launches: the split kernel and the merge of its records.
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st);
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st);
 

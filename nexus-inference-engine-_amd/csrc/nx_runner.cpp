@@ -71,7 +71,6 @@ struct nx_model {
     uint16_t* moe_act = nullptr;
     float* moe_y = nullptr;
     float* attn_part = nullptr;
-    unsigned int* attn_counters = nullptr;
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
     hipGraphExec_t exec = nullptr;
@@ -210,7 +209,6 @@ nx_status enqueue_step(nx_model* m) {
         at.max_blocks = m->max_blocks;
         at.max_ctx = c.max_seq;
         at.part = m->attn_part;
-        at.counters = m->attn_counters;
         NX_LAUNCH(m, c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st));
         // output projection + residual
         nx::GemvArgs o{};
@@ -456,7 +454,6 @@ nx_status create_impl(nx_model* m) {
     }
     NX_TRY(dalloc(m, &m->attn_part,
                   nx::attn_workspace_bytes(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq) / 4 + 1));
-    NX_TRY(dalloc(m, &m->attn_counters, nx::attn_counter_count(B, c.n_kv_heads)));
     {
         std::vector<int32_t> minus1(B, -1);
         NX_HIP(m->ctx, hipMemcpyAsync(m->pos, minus1.data(), (size_t)B * 4, hipMemcpyHostToDevice, m->ctx->stream));
@@ -479,6 +476,7 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.head_dim != 64 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
     if (c.kv_kind == 1 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
+    if (c.max_seq > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the attention limit");
     if (c.d_model > 14336 || c.ffn > 14336 || c.n_heads * c.head_dim > 14336)
         return fail(ctx, NX_ERR_UNSUPPORTED, "GEMV K above 14336");
     if (c.n_experts < 0 || c.n_experts > 64 || (c.n_experts > 0 && (c.top_k < 1 || c.top_k > 8 || c.top_k > c.n_experts)))
@@ -684,22 +682,28 @@ nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double*
     const nx_model_config& c = m->c;
     if (c.n_experts != 0) return fail(m->ctx, NX_ERR_UNSUPPORTED, "dense models only");
     hipStream_t st = m->ctx->stream;
-    Layer& ly = m->layers[0];
-    nx::GemvArgs f{};
-    f.W = ly.w13;
-    f.S = ly.s13;
-    f.N = 2 * c.ffn;
-    f.K = c.d_model;
-    f.G = m->Gd;
-    f.batch = c.batch;
-    f.h32 = m->h;
-    f.ldx = c.d_model;
-    f.eps = c.eps;
-    f.act16 = m->act16;
-    f.lda = m->Fp;
-    NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
+    // launch i uses layer i % n_layers, so consecutive launches stream
+    // different weights (every layer's gate/up, 2 GB at the 8B shape, is far
+    // larger than the last-level cache) as they do inside a decode step
+    auto launch = [&](int i) {
+        const Layer& ly = m->layers[i % c.n_layers];
+        nx::GemvArgs f{};
+        f.W = ly.w13;
+        f.S = ly.s13;
+        f.N = 2 * c.ffn;
+        f.K = c.d_model;
+        f.G = m->Gd;
+        f.batch = c.batch;
+        f.h32 = m->h;
+        f.ldx = c.d_model;
+        f.eps = c.eps;
+        f.act16 = m->act16;
+        f.lda = m->Fp;
+        return nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st);
+    };
+    for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
-    for (int i = 0; i < iters; ++i) NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
+    for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev1, st));
     NX_HIP(m->ctx, hipEventSynchronize(m->ctx->ev1));
     float ms = 0.0f;
@@ -717,34 +721,36 @@ nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double
     for (int b = 0; b < c.batch; ++b)
         if (m->hpos[b] < 0) return fail(m->ctx, NX_ERR_STATE, "no context to attend over");
     hipStream_t st = m->ctx->stream;
-    Layer& ly = m->layers[0];
-    nx::AttnArgs at{};
-    at.q = m->q;
-    at.kpool = ly.kpool;
-    at.vpool = ly.vpool;
-    at.kc4 = ly.kc4;
-    at.kc3 = ly.kc3;
-    at.vc4 = ly.vc4;
-    at.vc3 = ly.vc3;
-    at.kn = ly.kn;
-    at.vn = ly.vn;
-    at.ksign = ly.ksign;
-    at.vsign = ly.vsign;
-    at.block_table = m->block_table;
-    at.pos = m->pos;
-    at.out16 = m->att16;
-    at.batch = c.batch;
-    at.hq = c.n_heads;
-    at.hkv = c.n_kv_heads;
-    at.hd = c.head_dim;
-    at.max_blocks = m->max_blocks;
-    at.max_ctx = c.max_seq;
-    at.part = m->attn_part;
-    at.counters = m->attn_counters;
-    auto launch = [&]() { return c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st); };
-    NX_LAUNCH(m, launch());
+    // launch i attends over layer i % n_layers (a separate cache per layer)
+    auto launch = [&](int i) {
+        const Layer& ly = m->layers[i % c.n_layers];
+        nx::AttnArgs at{};
+        at.q = m->q;
+        at.kpool = ly.kpool;
+        at.vpool = ly.vpool;
+        at.kc4 = ly.kc4;
+        at.kc3 = ly.kc3;
+        at.vc4 = ly.vc4;
+        at.vc3 = ly.vc3;
+        at.kn = ly.kn;
+        at.vn = ly.vn;
+        at.ksign = ly.ksign;
+        at.vsign = ly.vsign;
+        at.block_table = m->block_table;
+        at.pos = m->pos;
+        at.out16 = m->att16;
+        at.batch = c.batch;
+        at.hq = c.n_heads;
+        at.hkv = c.n_kv_heads;
+        at.hd = c.head_dim;
+        at.max_blocks = m->max_blocks;
+        at.max_ctx = c.max_seq;
+        at.part = m->attn_part;
+        return c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st);
+    };
+    for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
-    for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch());
+    for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev1, st));
     NX_HIP(m->ctx, hipEventSynchronize(m->ctx->ev1));
     float ms = 0.0f;

@@ -95,7 +95,8 @@ _SIGS = {
     "nx_model_position": (_I, [_P, _I, C.POINTER(_I)]),
     "nx_model_step_bytes": (_I, [_P, C.POINTER(C.c_double)]),
     "nx_model_time_ffn_gemv": (_I, [_P, _I, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
-    "nx_time_gemv": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I, C.POINTER(C.c_double)]),
+    "nx_time_gemv": (_I, [_P, _B, C.POINTER(_B), C.POINTER(_B), _I, _B, _I, _I, _I, _I,
+                          C.POINTER(C.c_double)]),
     "nx_model_time_attention": (_I, [_P, _I, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
