@@ -69,6 +69,17 @@ def cpu_baseline(ctx_len: int, batch: int, kv_kind: int) -> dict:
                        f"+ lm_head rows 1/{vocab_frac}, scaled to 32 layers + full lm_head")}
 
 
+def measured_traffic(kind: str):
+    """HBM bytes per launch of `kind` ("ffn" / "attention") from the committed
+    rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE, calibrated on a copy
+    kernel); None when no summary is present."""
+    try:
+        with open(ROOT / "profiles" / "traffic.json") as f:
+            return int(json.load(f)["kernels"][kind]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 GEMV_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
 
 
@@ -109,11 +120,25 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--kv", choices=["fp16", "tq"], default="fp16")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-kernel", choices=["ffn", "attention"],
+                    help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only copy a 256 MiB buffer 16 times (counter calibration kernel)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(--gpus must be 1).", file=sys.stderr)
         return 2
+    if args.copy_calib:
+        import torch
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(16):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_per_launch_read": src.numel() * 4,
+                          "copy_calib_bytes_per_launch_write": dst.numel() * 4, "launches": 16}))
+        return 0
 
     import nexus_amd
 
@@ -125,6 +150,14 @@ def main() -> int:
           f"(batch {args.batch}, ctx {args.ctx}, kv {args.kv})", file=sys.stderr, flush=True)
     model = nexus_amd.Model(ctx, **cfg)
     model.fill_context(args.ctx, 4 if kv_kind else 0)
+    if args.profile_kernel:
+        model.decode_untimed(1)
+        ms, nb = (model.time_ffn_gemv if args.profile_kernel == "ffn" else model.time_attention)(64)
+        print(json.dumps({"kernel": args.profile_kernel, "avg_us": round(ms * 1e3, 3),
+                          "bytes": int(nb), "launches": 64 + LLAMA8B["n_layers"]}))
+        model.close()
+        ctx.close()
+        return 0
     if args.warmup > 0:
         model.decode_untimed(args.warmup)
     bytes_start = model.step_bytes()
@@ -171,13 +204,13 @@ def main() -> int:
         "roofline": {
             "kernel": "fused RMSNorm + gate/up int4-g32 GEMV + SwiGLU (28672 x 4096)",
             "bound": "hbm", "achieved": round(ffn_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic("ffn"),
             "avg_us": round(ffn_ms * 1e3, 3), "bytes": int(ffn_bytes),
         },
         "attention": {
             "kernel": "paged decode attention, one layer", "achieved": round(att_gbs, 1),
             "frac": round(att_gbs / PEAK_HBM_GBS, 4), "avg_us": round(att_ms * 1e3, 3),
-            "bytes": int(att_bytes),
+            "bytes": int(att_bytes), "traffic": measured_traffic("attention"),
         },
         "roofline_end_to_end_frac": round(step_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
         "gemv_microbench": micro,

@@ -56,13 +56,13 @@ typedef struct nx_ctx nx_ctx;
 typedef uint64_t nx_buf; /* 0 = none */
 
 /* ------------------------------------------------------------ lifecycle -- */
-/* ComputeDispatch::init_gpu (compute_dispatch.h:30, compute_dispatch.cpp:47-71) */
+/* ComputeDispatch::init_gpu (compute_dispatch.h:29, compute_dispatch.cpp:47-71) */
 nx_status nx_init(nx_ctx** out, int device);
 /* ComputeDispatch::~ComputeDispatch; frees every buffer of the context. */
 nx_status nx_destroy(nx_ctx* ctx);
-/* ComputeDispatch::has_gpu (compute_dispatch.h:33): 1 if a gfx950 device is visible. */
+/* ComputeDispatch::has_gpu (compute_dispatch.h:32): 1 if a gfx950 device is visible. */
 int nx_has_gpu(void);
-/* ComputeDispatch::gpu_name (compute_dispatch.h:36) */
+/* ComputeDispatch::gpu_name (compute_dispatch.h:35) */
 nx_status nx_device_name(nx_ctx* ctx, char* buf, size_t n);
 /* Message of the last failed call on this context ("" if none). */
 const char* nx_last_error(nx_ctx* ctx);
@@ -74,21 +74,21 @@ const char* nx_init_error(void);
  * Device memory, zero-filled. */
 nx_status nx_alloc(nx_ctx* ctx, size_t bytes, nx_buf* out);
 nx_status nx_free(nx_ctx* ctx, nx_buf buf);
-/* ComputeDispatch::upload_to_gpu (compute_dispatch.h:227); replaces the UMA
+/* ComputeDispatch::upload_to_gpu (compute_dispatch.h:203); replaces the UMA
  * memcpy into a shared MTLBuffer (metal_backend.mm:836-850).  Synchronous. */
 nx_status nx_upload(nx_ctx* ctx, nx_buf dst, size_t dst_offset, const void* src, size_t bytes);
-/* ComputeDispatch::download_from_gpu (compute_dispatch.h:231); waits for the stream. */
+/* ComputeDispatch::download_from_gpu (compute_dispatch.h:207); waits for the stream. */
 nx_status nx_download(nx_ctx* ctx, void* dst, nx_buf src, size_t src_offset, size_t bytes);
 /* The wrapped-pointer weight cache keyed by host pointer
  * (compute_dispatch.h:311, compute_dispatch.cpp:148-154) and
- * upload_small_buffer (compute_dispatch.h:117): the first call uploads
+ * upload_small_buffer (compute_dispatch.h:129): the first call uploads
  * `bytes` from `src` into a new device buffer remembered under `host_key`;
  * later calls with the same key return that buffer without copying. */
 nx_status nx_weight_cache(nx_ctx* ctx, const void* host_key, const void* src, size_t bytes,
                           nx_buf* out);
-/* ComputeDispatch::get_cached_buffer (compute_dispatch.h:299); NX_ERR_INVALID if absent. */
+/* ComputeDispatch::get_cached_buffer (compute_dispatch.h:273); NX_ERR_INVALID if absent. */
 nx_status nx_get_cached_buffer(nx_ctx* ctx, const void* host_key, nx_buf* out);
-/* ComputeDispatch::clear_buffer_cache (compute_dispatch.h:296): frees cached weights. */
+/* ComputeDispatch::clear_buffer_cache (compute_dispatch.h:270): frees cached weights. */
 nx_status nx_clear_buffer_cache(nx_ctx* ctx);
 /* Size in bytes of a buffer of this context. */
 nx_status nx_buffer_size(nx_ctx* ctx, nx_buf buf, size_t* bytes);
@@ -96,7 +96,7 @@ nx_status nx_buffer_size(nx_ctx* ctx, nx_buf buf, size_t* bytes);
 nx_status nx_synchronize(nx_ctx* ctx);
 
 /* ------------------------------------------------------------- batching -- */
-/* ComputeDispatch::begin_token / end_token (compute_dispatch.h:96-102,
+/* ComputeDispatch::begin_token / end_token (compute_dispatch.h:106-110,
  * compute_dispatch.cpp:798-833).  Ops between the two are captured into one
  * HIP graph; end_token launches it and waits.  When the captured sequence
  * has the same shape as the previous token's, the instantiated graph is
@@ -107,15 +107,15 @@ nx_status nx_token_end(nx_ctx* ctx);
 /* ------------------------------------------------------------------ ops -- */
 /* int4-g32 GEMV: y[b][n] = sum_k x[b][k] * (q[n][k] - 8) * s[n][k/32], fp32
  * accumulation, y stored fp16.  x fp16 [batch][K].  batch 1..8.
- * Replaces ComputeDispatch::gemm_int4 (compute_dispatch.h:57,
+ * Replaces ComputeDispatch::gemm_int4 (compute_dispatch.h:59,
  * compute_dispatch.cpp:142-176) -> MetalBackend::gemv_int4_nr8
- * (metal_backend.mm:607-642), and gemv_int4 (compute_dispatch.h:48) whose
+ * (metal_backend.mm:607-642), and gemv_int4 (compute_dispatch.h:47) whose
  * grouped semantics it follows. */
 nx_status nx_gemv_int4_g32(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16,
                            nx_buf y_f16, int N, int K, int batch);
 /* Same product with fp32 output; accumulate != 0 adds into y (the residual
  * add of hybrid_model.cpp:1397-1400 fused).  Replaces gemm_int4_gpu
- * (compute_dispatch.h:214) + gpu_residual_add (compute_dispatch.h:247). */
+ * (compute_dispatch.h:197) + gpu_residual_add (compute_dispatch.h:221). */
 nx_status nx_gemv_int4_g32_f32(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16,
                                nx_buf y_f32, int N, int K, int batch, int accumulate);
 /* Unpack n int4 codes (low nibble first) to one byte each -- the bit-exact
@@ -128,7 +128,7 @@ nx_status nx_quantize_int4_g32(nx_ctx* ctx, nx_buf w_f32, nx_buf wq, nx_buf scal
                                int K);
 /* RMSNorm: out = fp16((x * 1/sqrt(mean(x^2) + eps)) * w), x fp32 [batch][dim];
  * w fp32 [dim] or 0 for ones.  ComputeDispatch::rmsnorm / gpu_rmsnorm
- * (compute_dispatch.h:63, :241; compute::rms_norm gemm.cpp:96-114). */
+ * (compute_dispatch.h:66, :215; compute::rms_norm gemm.cpp:96-114). */
 nx_status nx_rmsnorm(nx_ctx* ctx, nx_buf x_f32, nx_buf w_f32, nx_buf out_f16, int dim, float eps,
                      int batch);
 /* RoPE in place on x fp32 [batch][heads][head_dim]: interleaved pairs,
@@ -137,9 +137,9 @@ nx_status nx_rmsnorm(nx_ctx* ctx, nx_buf x_f32, nx_buf w_f32, nx_buf out_f16, in
 nx_status nx_rope(nx_ctx* ctx, nx_buf x_f32, nx_buf positions_i32, nx_buf cos_tab, nx_buf sin_tab,
                   int heads, int head_dim, int batch, int max_pos);
 /* SwiGLU: out = fp16(g / (1 + exp(-g)) * u), fp32 inputs [batch][n].
- * ComputeDispatch::swiglu / gpu_swiglu (compute_dispatch.h:69, :236). */
+ * ComputeDispatch::swiglu / gpu_swiglu (compute_dispatch.h:72, :211). */
 nx_status nx_swiglu(nx_ctx* ctx, nx_buf gate_f32, nx_buf up_f32, nx_buf out_f16, int n, int batch);
-/* out = a + b, fp32 [n].  ComputeDispatch::gpu_residual_add (compute_dispatch.h:247). */
+/* out = a + b, fp32 [n].  ComputeDispatch::gpu_residual_add (compute_dispatch.h:221). */
 nx_status nx_residual_add(nx_ctx* ctx, nx_buf a, nx_buf b, nx_buf out, int n);
 /* Append one token's K/V (fp32 [batch][hkv][head_dim], converted to fp16
  * round-to-nearest-even) at positions[b] through the block table.  The
@@ -151,8 +151,8 @@ nx_status nx_kv_append_f16(nx_ctx* ctx, nx_buf k_f32, nx_buf v_f32, nx_buf kpool
 /* Paged fp16 decode attention: out[b][h] = softmax(q.K^T / sqrt(hd)) V over
  * positions [0, ctx_lens[b]), GQA kv head = h / (hq/hkv); q fp32
  * [batch][hq][hd]; out fp16 [batch][hq][hd].  Replaces
- * ComputeDispatch::attention_gpu / fused_attention (compute_dispatch.h:190,
- * :198) and the CPU gqa_attention (hybrid_model.cpp:1447-1565). */
+ * ComputeDispatch::attention_gpu / fused_attention (compute_dispatch.h:176,
+ * :187) and the CPU gqa_attention (hybrid_model.cpp:1447-1565). */
 nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q_f32, nx_buf kpool, nx_buf vpool,
                                    nx_buf block_table, nx_buf ctx_lens_i32, nx_buf out_f16,
                                    int batch, int hq, int hkv, int head_dim, int max_blocks,
@@ -189,7 +189,7 @@ nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits_f32, nx_buf ids_i32, nx_b
  * W2_e(fp16(silu(W1_e x) * W3_e x)), e = ids[b][j].  Expert weights are
  * int4-g32: w13 [E][2F][d] with gate/up rows interleaved (row 2f = gate f,
  * 2f+1 = up f), s13 its scales; w2 [E][d][F], s2.  x fp16 [batch][d].
- * ComputeDispatch::batched_moe_ffn (compute_dispatch.h:81,
+ * ComputeDispatch::batched_moe_ffn (compute_dispatch.h:84,
  * compute_dispatch.cpp:211-275; batched_expert_gemv.metal:47-160). */
 nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, nx_buf w2,
                             nx_buf s2, nx_buf ids_i32, nx_buf weights_f32, nx_buf out_f32, int d,
