@@ -25,7 +25,9 @@
  *   int4-g32 weights: codes [N][Kp/2] bytes (Kp = ceil(K/32)*32), low nibble
  *     = even k; scales fp16 [N][Kp/32]; value = (q - 8) * scale.  Columns
  *     k >= K of a ragged last group hold q = 8.
- *   fp16 paged KV: pools [num_blocks][hkv][16][head_dim] fp16;
+ *   fp16 paged KV: K pool [num_blocks][hkv][16][head_dim] fp16 (token-major),
+ *     V pool [num_blocks][hkv][head_dim][16] fp16 (dimension-major, so the
+ *     attention's value product reads it as a matrix-core operand);
  *     block_table int32 [batch][max_blocks]; position p of sequence b lives
  *     in block block_table[b][p/16], slot p%16.
  *   TurboQuant paged KV (head_dim 128): codes4 [num_blocks][hkv][16][32] u8,

@@ -125,25 +125,12 @@ __device__ inline void state_merge_rows(State<G, DPL>& s) {
     }
 }
 
-// Block-level merge of the wavefronts' states through LDS (lds holds
-// kAttnWaves records), then store this split's record to `part`.
+// Cross-wavefront merge of the block: lds holds one record per wavefront
+// (O[G][HD], M[G], L[G]); every wavefront has written its own before the
+// barrier.  The merged split record goes to `part`.
 template <int G, int HD>
-__device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __restrict__ part,
-                                         float* lds) {
-    constexpr int DPL = HD / 16, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* my = lds + wave * REC;
-    if (lane < 16) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            if (lane == 0) {
-                my[MO + h] = s.m[h];
-                my[LO + h] = s.l[h];
-            }
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) my[h * HD + lane * DPL + d] = s.o[h][d];
-        }
-    }
+__device__ inline void merge_waves_store(float* __restrict__ part, const float* lds) {
+    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     __syncthreads();
     for (int idx = threadIdx.x; idx < G * HD + G; idx += kAttnThreads) {
         const bool is_o = idx < G * HD;
@@ -166,73 +153,150 @@ __device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __re
     }
 }
 
-// ------------------------------------------------------------ fp16 pages --
-// Raw fp16 K/V of one page for one lane: 4 tokens x DPL halves each.
-template <int DPL>
-struct PageRaw {
-    uint32_t k[4][DPL / 2], v[4][DPL / 2];
-};
-
-template <int DPL>
-__device__ inline void load_page_f16(PageRaw<DPL>& r, const AttnArgs& a, int blk, int kvh, int p,
-                                     int ctx, int tg, int c) {
-    constexpr int HD = DPL * 16;
-    const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int t = tg + 4 * j;
-        const bool valid = p * kPage + t < ctx;
-        const uint16_t* kp = a.kpool + base + (size_t)t * HD + c * DPL;
-        const uint16_t* vp = a.vpool + base + (size_t)t * HD + c * DPL;
-        if (DPL == 8) {
-            const uint4 kr = valid ? *reinterpret_cast<const uint4*>(kp) : make_uint4(0, 0, 0, 0);
-            const uint4 vr = valid ? *reinterpret_cast<const uint4*>(vp) : make_uint4(0, 0, 0, 0);
-            r.k[j][0] = kr.x; r.k[j][1] = kr.y; r.k[j][2] = kr.z; r.k[j][3] = kr.w;
-            r.v[j][0] = vr.x; r.v[j][1] = vr.y; r.v[j][2] = vr.z; r.v[j][3] = vr.w;
-        } else {
-            const uint2 kr = valid ? *reinterpret_cast<const uint2*>(kp) : make_uint2(0, 0);
-            const uint2 vr = valid ? *reinterpret_cast<const uint2*>(vp) : make_uint2(0, 0);
-            r.k[j][0] = kr.x; r.k[j][1] = kr.y;
-            r.v[j][0] = vr.x; r.v[j][1] = vr.y;
-        }
-    }
-}
-
-template <int G, int DPL>
-__device__ inline void process_page_f16(State<G, DPL>& st, const PageRaw<DPL>& r,
-                                        const float (&q)[G][DPL], float scale, int p, int ctx,
-                                        int tg) {
-    float vf[4][DPL];
-    float sc[4][G];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const bool valid = p * kPage + tg + 4 * j < ctx;
-        float kf[DPL];
-#pragma unroll
-        for (int i = 0; i < DPL / 2; ++i) {
-            kf[2 * i] = h2f_bits((uint16_t)(r.k[j][i] & 0xFFFFu));
-            kf[2 * i + 1] = h2f_bits((uint16_t)(r.k[j][i] >> 16));
-            vf[j][2 * i] = h2f_bits((uint16_t)(r.v[j][i] & 0xFFFFu));
-            vf[j][2 * i + 1] = h2f_bits((uint16_t)(r.v[j][i] >> 16));
-        }
+// Block-level merge of the wavefronts' online-softmax states (row layout of
+// the TurboQuant kernel) through LDS, then store this split's record.
+template <int G, int HD>
+__device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __restrict__ part,
+                                         float* lds) {
+    constexpr int DPL = HD / 16, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* my = lds + wave * REC;
+    if (lane < 16) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            float dot = 0.0f;
+            if (lane == 0) {
+                my[MO + h] = s.m[h];
+                my[LO + h] = s.l[h];
+            }
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) dot = fmaf(q[h][d], kf[d], dot);
-            dot = row16_sum(dot) * scale;
-            sc[j][h] = valid ? dot : -__builtin_inff();
+            for (int d = 0; d < DPL; ++d) my[h * HD + lane * DPL + d] = s.o[h][d];
         }
     }
-    state_update(st, sc, vf);
+    merge_waves_store<G, HD>(part, lds);
 }
 
-template <int G, int HD>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
-    constexpr int DPL = HD / 16, REC = rec_floats(G, HD);
+// ------------------------------------------------------------ fp16 pages --
+// q.K^T and P.V run on the matrix cores (v_mfma_f32_16x16x32_f16, wave64):
+//   A operand (16 x 32): lane l holds row l%16, k = 8(l/16) .. +7
+//   B operand (32 x 16): lane l holds column l%16, k = 8(l/16) .. +7
+//   C (16 x 16 fp32):    lane l holds column l%16, rows 4(l/16) .. +3
+// Scores S = K q^T per page: M = the page's 16 tokens, N = query heads (G of
+// 16 columns used), K = head dims.  A K page row is read straight into the A
+// operand (16 bytes per lane per k-step).  q enters as fp16 hi + lo parts
+// (q = hi + lo to 2^-22), so the two products give the fp32 score; K is exact
+// fp16 and the products accumulate in fp32.
+// Values O = P V per page pair: M = heads, N = 16 dims per tile, K = the 32
+// tokens of two pages.  The token order of that K dimension is chosen so the
+// probabilities a lane needs are exactly the 8 scores it holds in the S
+// layout (k = 8g + j: page a token 4g + j for j < 4, page b token 4g + j - 4),
+// and V pages are stored dimension-major ([hd][16] per page), so the B
+// operand is two 8-byte reads per lane.  P enters as fp16 hi + lo as well.
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ inline h8_t as_h8(uint4 v) { return __builtin_bit_cast(h8_t, v); }
+
+template <int HD>
+struct PairRaw {
+    uint4 k[2][HD / 32];  // K of pages a, b: A operand per k-step
+    uint2 v[HD / 16][2];  // V of pages a, b: tokens 4g..4g+3 of dim 16 nt + l%16
+};
+
+// Load pages a and b of a pair; na / nb = valid tokens of each (0 = none).
+// Tokens at or beyond the valid count read as zero.
+template <int HD>
+__device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, int na, int blkb,
+                                 int nb, int kvh, int lane) {
+    const int g = lane >> 4, t = lane & 15;
+#pragma unroll
+    for (int pg = 0; pg < 2; ++pg) {
+        const int blk = pg ? blkb : blka, n = pg ? nb : na;
+        const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)
+            r.k[pg][s] = t < n ? *reinterpret_cast<const uint4*>(a.kpool + base + (size_t)t * HD + 32 * s + 8 * g)
+                               : make_uint4(0u, 0u, 0u, 0u);
+        const int valid = min(max(n - 4 * g, 0), 4);
+#pragma unroll
+        for (int nt = 0; nt < HD / 16; ++nt) {
+            uint2 w = make_uint2(0u, 0u);
+            if (valid > 0) {
+                w = *reinterpret_cast<const uint2*>(a.vpool + base + (size_t)(16 * nt + t) * kPage + 4 * g);
+                if (valid < 2) w.x &= 0xFFFFu;   // keep token 4g only
+                if (valid < 3) w.y = 0u;          // drop tokens 4g+2, 4g+3
+                else if (valid == 3) w.y &= 0xFFFFu;
+            }
+            r.v[nt][pg] = w;
+        }
+    }
+}
+
+// Fold one page pair into the wavefront's state: m (running max of head l%16),
+// lsum (this lane's share of the softmax denominator), O (C layout, rows =
+// heads 4(l/16) + i, columns = dims 16 nt + l%16).
+template <int HD>
+__device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 32],
+                                   const h8_t (&ql)[HD / 32], float scale, int na, int nb, float& m,
+                                   float& lsum, f4_t (&o)[HD / 16], int lane) {
+    const int g = lane >> 4;
+    f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), qh[s], sa, 0, 0, 0);
+        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), ql[s], sa, 0, 0, 0);
+        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), qh[s], sb, 0, 0, 0);
+        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), ql[s], sb, 0, 0, 0);
+    }
+    float p[8];
+    float mloc = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p[i] = 4 * g + i < na ? sa[i] * scale : -__builtin_inff();
+        p[4 + i] = 4 * g + i < nb ? sb[i] * scale : -__builtin_inff();
+        mloc = fmaxf(mloc, fmaxf(p[i], p[4 + i]));
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float mn = fmaxf(m, mloc);
+    const bool none = mn == -__builtin_inff();
+    const float corr = none ? 1.0f : __expf(m - mn);
+    float ps = 0.0f;
+    h8_t ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float e = none ? 0.0f : __expf(p[j] - mn);
+        ps += e;
+        ph[j] = (_Float16)e;
+        pl[j] = (_Float16)(e - (float)ph[j]);
+    }
+    lsum = lsum * corr + ps;
+    m = mn;
+    // rows of O in this lane are heads 4g + i; their rescale factors live in
+    // the lanes whose column is that head
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = __shfl(corr, 4 * g + i, 64);
+#pragma unroll
+    for (int nt = 0; nt < HD / 16; ++nt) {
+        f4_t acc = o[nt];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= c[i];
+        const h8_t vb = as_h8(make_uint4(r.v[nt][0].x, r.v[nt][0].y, r.v[nt][1].x, r.v[nt][1].y));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, acc, 0, 0, 0);
+        o[nt] = acc;
+    }
+}
+
+// PIPE: more than one page pair per wavefront (pps > 8), two pairs in
+// flight; otherwise the single pair is loaded up front and the kernel fits
+// two blocks per CU.
+template <int G, int HD, bool PIPE>
+__global__ __launch_bounds__(kAttnThreads, PIPE ? 1 : 2) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
+    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = lane & 15, tg = lane >> 4;
+    const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
 
     // The context length, q and this wavefront's block-table entries (page
@@ -244,42 +308,72 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_f16(AttnArgs a, int nspli
     const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
                             ? a.block_table[(size_t)b * a.max_blocks + my_page]
                             : 0;
+    // q as the B operand (column = head t, k = 8g + j of each 32-dim step)
+    h8_t qh[HD / 32], ql[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+        float x[8];
+        if (t < G) {
+            const float* src = a.q + ((size_t)b * a.hq + kvh * G + t) * HD + 32 * s + 8 * g;
+            const float4 x0 = *reinterpret_cast<const float4*>(src);
+            const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+            x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+            x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            qh[s][j] = (_Float16)x[j];
+            ql[s][j] = (_Float16)(x[j] - (float)qh[s][j]);
+        }
+    }
     const float scale = 1.0f / sqrtf((float)HD);
-    float q[G][DPL];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int d = 0; d < DPL; ++d)
-            q[h][d] = a.q[((size_t)b * a.hq + kvh * G + h) * HD + c * DPL + d];
 
-    State<G, DPL> st;
-    state_init(st);
     const int npages = (ctx + kPage - 1) / kPage;
     const int p1 = min(p0 + pps, npages);
-    // pages of this wavefront: p0 + wave + 4i for i < npw, two pairs in flight
+    // pages of this wavefront: p0 + wave + 4i for i < npw, taken in pairs
     const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
-#define NX_PAGE(i) (p0 + wave + kAttnWaves * (i))
-#define NX_LOAD(r, i) load_page_f16<DPL>(r, a, __builtin_amdgcn_readlane(bt_lane, (i)), kvh, NX_PAGE(i), ctx, tg, c)
-    PageRaw<DPL> a0, a1, b0, b1;
-    if (npw > 0) NX_LOAD(a0, 0);
-    if (npw > 1) NX_LOAD(a1, 1);
-    for (int i = 0; i < npw; i += 4) {
-        if (i + 2 < npw) NX_LOAD(b0, i + 2);
-        if (i + 3 < npw) NX_LOAD(b1, i + 3);
-        process_page_f16<G, DPL>(st, a0, q, scale, NX_PAGE(i), ctx, tg);
-        if (i + 1 < npw) process_page_f16<G, DPL>(st, a1, q, scale, NX_PAGE(i + 1), ctx, tg);
-        if (i + 2 >= npw) break;
-        if (i + 4 < npw) NX_LOAD(a0, i + 4);
-        if (i + 5 < npw) NX_LOAD(a1, i + 5);
-        process_page_f16<G, DPL>(st, b0, q, scale, NX_PAGE(i + 2), ctx, tg);
-        if (i + 3 < npw) process_page_f16<G, DPL>(st, b1, q, scale, NX_PAGE(i + 3), ctx, tg);
+    auto valid_of = [&](int i) { return i < npw ? min(ctx - (p0 + wave + kAttnWaves * i) * kPage, kPage) : 0; };
+    auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
+    float m = -__builtin_inff(), lsum = 0.0f;
+    f4_t o[HD / 16];
+#pragma unroll
+    for (int nt = 0; nt < HD / 16; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (PIPE) {
+        PairRaw<HD> ra, rb;
+        if (npw > 0) load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
+        for (int i = 0; i < npw; i += 4) {
+            if (i + 2 < npw)
+                load_pair<HD>(rb, a, blk_of(i + 2), valid_of(i + 2), blk_of(i + 3), valid_of(i + 3), kvh, lane);
+            pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
+            if (i + 2 >= npw) break;
+            if (i + 4 < npw)
+                load_pair<HD>(ra, a, blk_of(i + 4), valid_of(i + 4), blk_of(i + 5), valid_of(i + 5), kvh, lane);
+            pair_update<HD>(rb, qh, ql, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
+        }
+    } else if (npw > 0) {
+        PairRaw<HD> ra;
+        load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
+        pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
     }
-#undef NX_LOAD
-#undef NX_PAGE
-    state_merge_rows(st);
-
+    // the head's denominator: sum of the four lanes that share its column
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    // wavefront record into LDS: rows h = 4g + i < G of O, m / l of head t
+    float* my = lds + wave * REC;
+#pragma unroll
+    for (int nt = 0; nt < HD / 16; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * g + i < G) my[(4 * g + i) * HD + 16 * nt + t] = o[nt][i];
+    if (g == 0 && t < G) {
+        my[MO + t] = m;
+        my[LO + t] = lsum;
+    }
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    block_merge_store<G, HD>(st, parts + (size_t)split * REC, lds);
+    merge_waves_store<G, HD>(parts + (size_t)split * REC, lds);
 }
 
 // ------------------------------------------------------ TurboQuant pages --
@@ -614,10 +708,15 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     const SplitPlan sp = plan_splits(a.max_ctx);
     const dim3 grid(sp.nsplit, a.hkv, a.batch), mgrid(a.hq / a.hkv, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
+    const bool pipe = sp.pps > kPagesPerSplitMin;
 #define NX_ATTN_CASE(GG, HH)                                                                      \
     if (G == GG && a.hd == HH) {                                                                  \
-        hipLaunchKernelGGL((k_attn_f16<GG, HH>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit,    \
-                           sp.pps);                                                               \
+        if (pipe)                                                                                 \
+            hipLaunchKernelGGL((k_attn_f16<GG, HH, true>), grid, dim3(kAttnThreads), 0, st, a,     \
+                               sp.nsplit, sp.pps);                                                \
+        else                                                                                      \
+            hipLaunchKernelGGL((k_attn_f16<GG, HH, false>), grid, dim3(kAttnThreads), 0, st, a,    \
+                               sp.nsplit, sp.pps);                                                \
         hipLaunchKernelGGL((k_attn_merge<GG, HH, false>), mgrid, dim3(HH), 0, st, a,              \
                            sp.nsplit);                                                            \
         return hipGetLastError();                                                                 \

@@ -222,10 +222,21 @@ __device__ inline unsigned long long pack_best(float v, int idx) {
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
-// Rows at or beyond `nlim` are not stored.
+// Values the QKV epilogue needs, fetched before the tile is reduced so the
+// epilogue does not wait on memory: the position, RoPE cos/sin of each row
+// pair of the tile and the block of the page the new K/V go to.
+struct RopePre {
+    bool valid;
+    int p, blk;
+    float c[4], s[4];
+};
+
+// Rows at or beyond `nlim` are not stored.  The residual add (E_ACC) is a
+// no-return atomic add: each element has exactly one writer, so the sum is
+// the plain y + res, and the wavefront does not wait for a read of y.
 template <int EPI, int R>
 __device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, const float (&res)[R],
-                                float& best_v, int& best_i) {
+                                float& best_v, int& best_i, const RopePre* pre = nullptr) {
     if (EPI == E_F16) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -237,12 +248,12 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, cons
     } else if (EPI == E_ACC) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (n0 + r < nlim) {
-                float* y = a.y32 + (size_t)b * a.ldy + n0 + r;
-                *y = *y + res[r];
-            }
+            if (n0 + r < nlim)
+                __hip_atomic_fetch_add(a.y32 + (size_t)b * a.ldy + n0 + r, res[r], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
     } else if (EPI == E_QKV) {
-        const int p = a.pos[b];
+        const bool have = pre && pre->valid;
+        const int p = have ? pre->p : a.pos[b];
         const int half = a.hd >> 1;
 #pragma unroll
         for (int r = 0; r < R; r += 2) {
@@ -251,8 +262,8 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, cons
             float v0 = res[r], v1 = res[r + 1];
             if (row < a.qdim + a.kvdim) {
                 const int i = (row % a.hd) >> 1;
-                const float c = a.cos_t[(size_t)p * half + i];
-                const float s = a.sin_t[(size_t)p * half + i];
+                const float c = have ? pre->c[r / 2] : a.cos_t[(size_t)p * half + i];
+                const float s = have ? pre->s[r / 2] : a.sin_t[(size_t)p * half + i];
                 const float r0 = v0 * c - v1 * s;
                 const float r1 = v0 * s + v1 * c;
                 v0 = r0;
@@ -266,11 +277,15 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, cons
                 const int idx = row - a.qdim - kv * a.kvdim;
                 if (a.kpool) {
                     const int kvh = idx / a.hd, dd = idx % a.hd;
-                    const int blk = a.block_table[(size_t)b * a.max_blocks + p / kPage];
-                    uint16_t* pool = kv ? a.vpool : a.kpool;
-                    const size_t off = (((size_t)blk * a.hkv + kvh) * kPage + (p % kPage)) * a.hd + dd;
-                    pool[off] = f2h_bits(v0);
-                    pool[off + 1] = f2h_bits(v1);
+                    const int blk = have ? pre->blk : a.block_table[(size_t)b * a.max_blocks + p / kPage];
+                    const size_t page = ((size_t)blk * a.hkv + kvh) * kPage * a.hd;
+                    if (kv) {  // V pages are dimension-major: [hd][16]
+                        a.vpool[page + (size_t)dd * kPage + p % kPage] = f2h_bits(v0);
+                        a.vpool[page + (size_t)(dd + 1) * kPage + p % kPage] = f2h_bits(v1);
+                    } else {   // K pages are token-major: [16][hd]
+                        a.kpool[page + (size_t)(p % kPage) * a.hd + dd] = f2h_bits(v0);
+                        a.kpool[page + (size_t)(p % kPage) * a.hd + dd + 1] = f2h_bits(v1);
+                    }
                 } else {
                     float* dst = a.kv_tmp + ((size_t)b * 2 + kv) * a.kvdim + idx;
                     dst[0] = v0;
@@ -365,75 +380,66 @@ __device__ inline void norm_chunk(const float (&v)[8], const float* __restrict__
 
 // Block-cooperative staging of one x row into LDS in the pair layout:
 // sp[g*16 + 4d + j] = (x[32g+8d+j], x[32g+8d+j+4]) and s8[g] = 8 * sum of
-// group g.  Thread t handles the 8-element chunks t, t + nthr, ...; up to
-// kStageBatch chunks per thread are requested together, so a row of up to
-// kStageBatch * 8 * nthr elements costs one memory round trip, and for
-// X_RMSNORM the hidden state is kept in registers between the block's
-// sum(h^2) reduction and the conversion.  Ends with a barrier.
-constexpr int kStageBatch = 4;
+// group g.  Thread t of the 256 handles the 8-element chunks t, t + 256, ...
+// (at most CPT = GPL of them, as G * 4 <= 256 * GPL).  The staging is split
+// in two so the caller can request its weight tiles in between: the row is
+// requested first (stage_issue) and converted afterwards (stage_finish).
+// Loads complete in issue order, so waiting for the row then does not wait
+// for the weights, and a wavefront's first tile can be reduced as soon as it
+// arrives.  For X_RMSNORM the block reduces sum(h^2) once and converts from
+// the registers.  stage_finish ends with a barrier.
+template <int CPT, int XS>
+struct StageRegs {
+    float v[XS == X_RMSNORM ? CPT : 1][8];
+    uint32_t X[XS == X_F16 ? CPT : 1][4];
+};
 
-template <int XS>
-__device__ inline void stage_x(const GemvArgs& a, int b, uint32_t* sp, float* s8, float* red) {
-    const int K = a.K, nch = a.G * 4;
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const int step = kStageBatch * nthr;
+template <int CPT, int XS>
+__device__ inline void stage_issue(const GemvArgs& a, int b, StageRegs<CPT, XS>& r) {
+    const int K = a.K, nch = a.G * 4, tid = threadIdx.x;
     if (XS == X_F16) {
         const uint16_t* x = a.x16 + (size_t)b * a.ldx;
         const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (a.ldx & 7) == 0;
-        for (int c0 = tid; c0 < nch; c0 += step) {
-            uint32_t X[kStageBatch][4];
 #pragma unroll
-            for (int j = 0; j < kStageBatch; ++j)
-                if (c0 + j * nthr < nch) load_x8(x, 8 * (c0 + j * nthr), K, vec, X[j]);
-#pragma unroll
-            for (int j = 0; j < kStageBatch; ++j)
-                if (c0 + j * nthr < nch) put_chunk(c0 + j * nthr, X[j], sp, s8);
-        }
+        for (int j = 0; j < CPT; ++j)
+            if (tid + j * kBlockThreads < nch) load_x8(x, 8 * (tid + j * kBlockThreads), K, vec, r.X[j]);
     } else {
         const float* h = a.h32 + (size_t)b * a.ldx;
         const bool vec = (reinterpret_cast<uintptr_t>(h) & 15u) == 0 && (a.ldx & 3) == 0;
-        float v[kStageBatch][8];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+            if (tid + j * kBlockThreads < nch) load_h8(h, 8 * (tid + j * kBlockThreads), K, vec, r.v[j]);
+    }
+}
+
+template <int CPT, int XS>
+__device__ inline void stage_finish(const GemvArgs& a, StageRegs<CPT, XS>& r, uint32_t* sp,
+                                    float* s8, float* red) {
+    const int K = a.K, nch = a.G * 4, tid = threadIdx.x;
+    if (XS == X_F16) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+            if (tid + j * kBlockThreads < nch) put_chunk(tid + j * kBlockThreads, r.X[j], sp, s8);
+    } else {
         float ss = 0.0f;
-        for (int c0 = tid; c0 < nch; c0 += step) {
 #pragma unroll
-            for (int j = 0; j < kStageBatch; ++j)
-                if (c0 + j * nthr < nch) load_h8(h, 8 * (c0 + j * nthr), K, vec, v[j]);
+        for (int j = 0; j < CPT; ++j)
+            if (tid + j * kBlockThreads < nch)
 #pragma unroll
-            for (int j = 0; j < kStageBatch; ++j)
-                if (c0 + j * nthr < nch)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
-        }
+                for (int e = 0; e < 8; ++e) ss += r.v[j][e] * r.v[j][e];
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         float tot = 0.0f;
-        for (int w = 0; w < (nthr >> 6); ++w) tot += red[w];
+        for (int w = 0; w < kWavesPerBlock; ++w) tot += red[w];
         const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
-        if (nch <= step) {  // the row is still in registers
 #pragma unroll
-            for (int j = 0; j < kStageBatch; ++j) {
-                const int c = tid + j * nthr;
-                if (c < nch) {
-                    uint32_t X[4];
-                    norm_chunk(v[j], a.norm_w, 8 * c, K, inv, X);
-                    put_chunk(c, X, sp, s8);
-                }
-            }
-        } else {
-            for (int c0 = tid; c0 < nch; c0 += step) {
-#pragma unroll
-                for (int j = 0; j < kStageBatch; ++j)
-                    if (c0 + j * nthr < nch) load_h8(h, 8 * (c0 + j * nthr), K, vec, v[j]);
-#pragma unroll
-                for (int j = 0; j < kStageBatch; ++j) {
-                    const int c = c0 + j * nthr;
-                    if (c < nch) {
-                        uint32_t X[4];
-                        norm_chunk(v[j], a.norm_w, 8 * c, K, inv, X);
-                        put_chunk(c, X, sp, s8);
-                    }
-                }
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tid + j * kBlockThreads;
+            if (c < nch) {
+                uint32_t X[4];
+                norm_chunk(r.v[j], a.norm_w, 8 * c, K, inv, X);
+                put_chunk(c, X, sp, s8);
             }
         }
     }
@@ -479,12 +485,53 @@ __device__ inline void wave_rows(const RowSplit& rs, int w, int N, int& r0, int&
     r1 = min(2 * (u0 + nu), N);
 }
 
+// Tile product with x read from the LDS pair layout (used where holding x in
+// registers would cost GPL * 17 VGPRs and limit occupancy).
+template <int GPL, int R>
+__device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, const float* s8,
+                                    int G, int lane, float (&res)[R]) {
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GPL; ++i) {
+        const int g = lane + kWave * i;
+        uint32_t P[16];
+        float sx = 0.0f;
+        if (g < G) {
+            const uint4* src = reinterpret_cast<const uint4*>(sp + g * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = src[q];
+                P[4 * q + 0] = v.x;
+                P[4 * q + 1] = v.y;
+                P[4 * q + 2] = v.z;
+                P[4 * q + 3] = v.w;
+            }
+            sx = s8[g];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) P[j] = 0u;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            acc[r] = fmaf(group_dot(t.w[r][i], P, sx), h2f_bits(t.s[r][i]), acc[r]);
+        // keep the scheduler from hoisting the next groups' LDS reads (their
+        // registers would push the kernel below two wavefronts per SIMD)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) res[r] = wave_sum(acc[r]);
+}
+
 // Batch 1, persistent: every wavefront streams its own contiguous row range
-// as R-row tiles through a two-deep register pipeline (the next tile's loads
-// are in flight while the current one is reduced).  The first tile is
-// requested before x is staged, so the HBM stream starts with the kernel.
-template <int GPL, int R, int XS, int EPI, bool PIPE>
-__global__ __launch_bounds__(kBlockThreads) void k_gemv_b1(GemvArgs a, RowSplit rs) {
+// as R-row tiles through a ring of DEPTH register tiles.  A buffer is
+// refilled as soon as its tile has been reduced, so DEPTH - 1 tiles are in
+// flight while one is reduced, and the first DEPTH tiles are requested
+// before the input is staged, so the HBM stream starts with the kernel.
+// XLDS: x is read from LDS per group instead of being held in registers.
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI>
+__global__ __launch_bounds__(kBlockThreads, 2) void k_gemv_b1(GemvArgs a, RowSplit rs) {
     __shared__ __align__(16) uint32_t sp[kWave * GPL * 16];
     __shared__ float s8[kWave * GPL];
     __shared__ float red[kWavesPerBlock];
@@ -492,36 +539,72 @@ __global__ __launch_bounds__(kBlockThreads) void k_gemv_b1(GemvArgs a, RowSplit 
     const int wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     int r0, r1;
     wave_rows(rs, wid, a.N, r0, r1);
-    Tile<GPL, R> t0, t1;
-    if (r0 < r1) load_tile<GPL, R>(t0, a.W, a.S, a.G, r1, r0, lane);
-    if (PIPE && r0 + R < r1) load_tile<GPL, R>(t1, a.W, a.S, a.G, r1, r0 + R, lane);
-    stage_x<XS>(a, 0, sp, s8, red);  // block barrier: every wavefront takes part
-    if (r0 >= r1) return;
-    XPairs<GPL> xp;
-    load_pairs_lds<GPL>(xp, sp, s8, a.G, lane);
+    const int nt = r1 > r0 ? (r1 - r0 + R - 1) / R : 0;
+    // QKV: the position (a scalar load) first, the RoPE tables and the page
+    // block after the tiles; lane l holds the pair of rows r0 + 2l
+    const bool rope_pre = EPI == E_QKV && r1 - r0 <= 2 * kWave;
+    const int qp = EPI == E_QKV ? a.pos[0] : 0;
+    StageRegs<GPL, XS> sr;
+    stage_issue<GPL, XS>(a, 0, sr);
+    Tile<GPL, R> t[DEPTH];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j)
+        if (j < nt) load_tile<GPL, R>(t[j], a.W, a.S, a.G, r1, r0 + j * R, lane);
+    float qc = 0.0f, qs = 0.0f;
+    int qblk = 0;
+    if (EPI == E_QKV && rope_pre) {
+        const int row = r0 + 2 * lane;
+        if (row < r1 && row < a.qdim + a.kvdim) {
+            const int i = (row % a.hd) >> 1;
+            qc = a.cos_t[(size_t)qp * (a.hd >> 1) + i];
+            qs = a.sin_t[(size_t)qp * (a.hd >> 1) + i];
+        }
+        if (a.kpool) qblk = a.block_table[qp / kPage];
+    }
+    stage_finish<GPL, XS>(a, sr, sp, s8, red);  // block barrier: every wavefront takes part
     float best_v = -__builtin_inff();
     int best_i = -1;
-    float res[R];
-    if (PIPE) {
-        // t0 holds rows n0, t1 rows n0 + R; each buffer is refilled as soon
-        // as it has been reduced, so two tiles stay in flight
-        for (int n0 = r0; n0 < r1; n0 += 2 * R) {
-            tile_dot<GPL, R>(t0, xp, res);
-            if (lane == 0) epilogue<EPI, R>(a, 0, n0, r1, res, best_v, best_i);
-            if (n0 + 2 * R < r1) load_tile<GPL, R>(t0, a.W, a.S, a.G, r1, n0 + 2 * R, lane);
-            if (n0 + R >= r1) break;
-            tile_dot<GPL, R>(t1, xp, res);
-            if (lane == 0) epilogue<EPI, R>(a, 0, n0 + R, r1, res, best_v, best_i);
-            if (n0 + 3 * R < r1) load_tile<GPL, R>(t1, a.W, a.S, a.G, r1, n0 + 3 * R, lane);
-        }
-    } else {
-        for (int n0 = r0; n0 < r1; n0 += R) {
-            if (n0 != r0) load_tile<GPL, R>(t0, a.W, a.S, a.G, r1, n0, lane);
-            tile_dot<GPL, R>(t0, xp, res);
-            if (lane == 0) epilogue<EPI, R>(a, 0, n0, r1, res, best_v, best_i);
+    if (nt > 0) {
+        XPairs<XLDS ? 1 : GPL> xp;
+        if (!XLDS) load_pairs_lds<XLDS ? 1 : GPL>(xp, sp, s8, a.G, lane);
+        float res[R];
+        for (int i = 0; i < nt; i += DEPTH) {
+#pragma unroll
+            for (int j = 0; j < DEPTH; ++j) {
+                if (i + j >= nt) break;
+                if constexpr (XLDS)
+                    tile_dot_lds<GPL, R>(t[j], sp, s8, a.G, lane, res);
+                else
+                    tile_dot<GPL, R>(t[j], xp, res);
+                if (i + j + DEPTH < nt)
+                    load_tile<GPL, R>(t[j], a.W, a.S, a.G, r1, r0 + (i + j + DEPTH) * R, lane);
+                RopePre pre{};
+                if (EPI == E_QKV && rope_pre) {
+                    const int u0 = (i + j) * R / 2;  // first pair of the tile within the wave
+                    pre.valid = true;
+                    pre.p = qp;
+                    pre.blk = qblk;
+#pragma unroll
+                    for (int q = 0; q < (R + 1) / 2 && q < 4; ++q) {
+                        pre.c[q] = readlane_f(qc, min(u0 + q, kWave - 1));
+                        pre.s[q] = readlane_f(qs, min(u0 + q, kWave - 1));
+                    }
+                }
+                if (lane == 0) epilogue<EPI, R>(a, 0, r0 + (i + j) * R, r1, res, best_v, best_i, &pre);
+            }
         }
     }
-    if (EPI == E_LOGITS && lane == 0 && best_i >= 0) atomicMax(&a.best[0], pack_best(best_v, best_i));
+    if (EPI == E_LOGITS) {
+        // one atomic per block: the wavefronts' maxima meet in LDS first
+        __shared__ unsigned long long bk[kWavesPerBlock];
+        if (lane == 0) bk[threadIdx.x >> 6] = best_i >= 0 ? pack_best(best_v, best_i) : 0ull;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long m = 0ull;
+            for (int w = 0; w < kWavesPerBlock; ++w) m = bk[w] > m ? bk[w] : m;
+            if (m) atomicMax(&a.best[0], m);
+        }
+    }
 }
 
 // Batch 2..8: the weight tile is loaded once and applied to every row of x.
@@ -653,37 +736,53 @@ int device_cus() {
 // Wavefronts per CU of the batch-1 GEMV: two per SIMD.
 constexpr int kB1WavesPerCU = 8;
 
+// Batch 1: a persistent grid of kB1WavesPerCU wavefronts per CU, each with
+// at least one full tile; row pairs are dealt out evenly.
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI>
+hipError_t launch_b1(const GemvArgs& a, hipStream_t st, int waves_per_cu = kB1WavesPerCU) {
+    const int units = (a.N + 1) / 2;
+    const int min_units = (R + 1) / 2;
+    int waves = device_cus() * waves_per_cu;
+    const int maxw = (units + min_units - 1) / min_units;
+    if (waves > maxw) waves = maxw;
+    waves = (waves + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
+    const RowSplit rs{units / waves, units % waves};
+    hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI>), dim3(waves / kWavesPerBlock),
+                       dim3(kBlockThreads), 0, st, a, rs);
+    return hipGetLastError();
+}
+
+// Batch 2..8.
 template <int GPL, int R, int XS, int EPI>
-hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
+hipError_t launch_bn(const GemvArgs& a, hipStream_t st) {
     const int tiles = (a.N + R - 1) / R;
-    if (a.batch == 1) {
-        // a persistent grid of 8 wavefronts per CU, each with at least one
-        // full tile; row pairs are dealt out evenly
-        const int units = (a.N + 1) / 2;
-        const int min_units = R / 2;
-        int waves = device_cus() * kB1WavesPerCU;
-        const int maxw = (units + min_units - 1) / min_units;
-        if (waves > maxw) waves = maxw;
-        waves = (waves + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
-        const RowSplit rs{units / waves, units % waves};
-        constexpr bool kPipe = GPL <= 4;
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, XS, EPI, kPipe>), dim3(waves / kWavesPerBlock),
-                           dim3(kBlockThreads), 0, st, a, rs);
-        return hipGetLastError();
-    }
     int blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks > 1024) blocks = 1024;
     hipLaunchKernelGGL((k_gemv_bn<GPL, R, XS, EPI>), dim3(blocks), dim3(kBlockThreads), 0, st, a);
     return hipGetLastError();
 }
 
+// Tile shapes per groups-per-lane (K <= 64 * 32 * GPL), chosen by measuring
+// the 8B decode shapes on cold weights.  Batch 1, K = 4096: tiles of 2 rows
+// (a pair, as the RoPE and SwiGLU epilogues need) in a ring of 2 with 12
+// wavefronts per CU.  K = 14336 without paired rows: one row per tile with x
+// in registers.  Paired epilogues at GPL >= 4 keep x in LDS.
 template <int XS, int EPI>
 hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
     const int gpl = (a.G + kWave - 1) / kWave;
-    if (gpl <= 1) return launch_t<1, 4, XS, EPI>(a, st);
-    if (gpl <= 2) return launch_t<2, 4, XS, EPI>(a, st);
-    if (gpl <= 4) return launch_t<4, 2, XS, EPI>(a, st);
-    if (gpl <= 7) return launch_t<7, 2, XS, EPI>(a, st);
+    constexpr bool kPairs = EPI == E_QKV || EPI == E_SWIGLU;
+    if (a.batch == 1) {
+        if (gpl <= 1) return launch_b1<1, 4, 2, false, XS, EPI>(a, st);
+        if (gpl <= 2) return launch_b1<2, 2, 2, false, XS, EPI>(a, st, 12);
+        if (gpl <= 4) return launch_b1<4, 2, 2, true, XS, EPI>(a, st);
+        if (gpl > 7) return hipErrorInvalidValue;
+        if constexpr (kPairs) return launch_b1<7, 2, 2, true, XS, EPI>(a, st);
+        return launch_b1<7, 1, 1, false, XS, EPI>(a, st);
+    }
+    if (gpl <= 1) return launch_bn<1, 4, XS, EPI>(a, st);
+    if (gpl <= 2) return launch_bn<2, 4, XS, EPI>(a, st);
+    if (gpl <= 4) return launch_bn<4, 2, XS, EPI>(a, st);
+    if (gpl <= 7) return launch_bn<7, 2, XS, EPI>(a, st);
     return hipErrorInvalidValue;
 }
 

@@ -71,9 +71,9 @@ __global__ void k_kv_append_f16(const float* k, const float* v, uint16_t* kpool,
     const int h = r / hd, d = r % hd;
     const int p = pos[b];
     const int blk = block_table[(size_t)b * max_blocks + p / kPage];
-    const size_t off = (((size_t)blk * hkv + h) * kPage + p % kPage) * hd + d;
-    kpool[off] = f2h_bits(k[(size_t)b * hkv * hd + r]);
-    vpool[off] = f2h_bits(v[(size_t)b * hkv * hd + r]);
+    const size_t page = ((size_t)blk * hkv + h) * kPage * hd;
+    kpool[page + (size_t)(p % kPage) * hd + d] = f2h_bits(k[(size_t)b * hkv * hd + r]);
+    vpool[page + (size_t)d * kPage + p % kPage] = f2h_bits(v[(size_t)b * hkv * hd + r]);
 }
 
 __device__ inline unsigned long long pack_best(float v, int idx) {
@@ -186,8 +186,11 @@ __global__ void k_gen_ctx_f16(uint16_t* kpool, uint16_t* vpool, const int32_t* b
     const float v = ctx_value(key, (size_t)p * hkv * hd + i, kf,
                               outlier_ch + ((size_t)kv * hkv + h) * n_outlier, n_outlier, d);
     const int blk = block_table[(size_t)b * max_blocks + p / kPage];
-    const size_t off = (((size_t)blk * hkv + h) * kPage + p % kPage) * hd + d;
-    (kv ? vpool : kpool)[off] = f2h_bits(v);
+    const size_t page = ((size_t)blk * hkv + h) * kPage * hd;
+    if (kv)
+        vpool[page + (size_t)d * kPage + p % kPage] = f2h_bits(v);
+    else
+        kpool[page + (size_t)(p % kPage) * hd + d] = f2h_bits(v);
 }
 
 __global__ void k_gen_ctx_raw(float* dst, int ctx, int hkv, int hd, uint64_t key, float kf,

@@ -283,10 +283,10 @@ void nxo_kv_append_f16(const float* k, const float* v, uint16_t* kpool, uint16_t
     const int blk = block_table[(size_t)b * max_blocks + pos / NXO_PAGE];
     const int slot = pos % NXO_PAGE;
     for (int h = 0; h < hkv; ++h) {
-        const size_t base = (((size_t)blk * hkv + h) * NXO_PAGE + slot) * hd;
+        const size_t page = ((size_t)blk * hkv + h) * NXO_PAGE * hd;
         for (int d = 0; d < hd; ++d) {
-            kpool[base + d] = nxo_f32_to_f16(k[(size_t)h * hd + d]);
-            vpool[base + d] = nxo_f32_to_f16(v[(size_t)h * hd + d]);
+            kpool[page + (size_t)slot * hd + d] = nxo_f32_to_f16(k[(size_t)h * hd + d]);
+            vpool[page + (size_t)d * NXO_PAGE + slot] = nxo_f32_to_f16(v[(size_t)h * hd + d]);
         }
     }
 }
@@ -330,12 +330,16 @@ void nxo_attn_decode_contig(const float* q, const float* K, const float* V, int 
 }
 
 /* Gather one kv head of a paged pool into contiguous fp32 rows [ctx][hd]. */
+/* Gather positions [0, ctx) of kv head h into dst [ctx][hd]; token-major
+ * pages ([16][hd], K) or dimension-major pages ([hd][16], V). */
 static void gather_f16(const uint16_t* pool, const int32_t* bt, int ctx, int hkv, int h, int hd,
-                       float* dst) {
+                       int dim_major, float* dst) {
     for (int t = 0; t < ctx; ++t) {
-        const int blk = bt[t / NXO_PAGE];
-        const uint16_t* src = pool + (((size_t)blk * hkv + h) * NXO_PAGE + t % NXO_PAGE) * hd;
-        for (int d = 0; d < hd; ++d) dst[(size_t)t * hd + d] = nxo_f16_to_f32(src[d]);
+        const int blk = bt[t / NXO_PAGE], slot = t % NXO_PAGE;
+        const uint16_t* page = pool + ((size_t)blk * hkv + h) * NXO_PAGE * hd;
+        for (int d = 0; d < hd; ++d)
+            dst[(size_t)t * hd + d] =
+                nxo_f16_to_f32(dim_major ? page[(size_t)d * NXO_PAGE + slot] : page[(size_t)slot * hd + d]);
     }
 }
 
@@ -352,8 +356,8 @@ void nxo_attn_decode_paged_f16(const float* q, const uint16_t* kpool, const uint
             float* K = (float*)malloc(sizeof(float) * (size_t)(ctx > 0 ? ctx : 1) * hd);
             float* V = (float*)malloc(sizeof(float) * (size_t)(ctx > 0 ? ctx : 1) * hd);
             float* scores = (float*)malloc(sizeof(float) * (size_t)(ctx > 0 ? ctx : 1));
-            gather_f16(kpool, bt, ctx, hkv, kvh, hd, K);
-            gather_f16(vpool, bt, ctx, hkv, kvh, hd, V);
+            gather_f16(kpool, bt, ctx, hkv, kvh, hd, 0, K);
+            gather_f16(vpool, bt, ctx, hkv, kvh, hd, 1, V);
             for (int j = 0; j < grp; ++j) {
                 const int h = kvh * grp + j;
                 attend_head(q + ((size_t)b * hq + h) * hd, K, V, (size_t)hd, ctx, hd,

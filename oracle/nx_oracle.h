@@ -92,9 +92,11 @@ void nxo_swiglu(const float* g, const float* u, int n, float* out);
 int nxo_argmax(const float* v, int n);
 
 /* ----------------------------------------------------- paged attention -- */
-/* Page pool layout [num_blocks][hkv][16][hd] fp16; block_table [B][max_blocks];
- * position p of sequence b lives in block block_table[b][p/16], slot p%16
- * (the gather of kv/paged_attention.cpp:161-230 with 16-token pages).
+/* Page pools fp16: K [num_blocks][hkv][16][hd] (token-major), V
+ * [num_blocks][hkv][hd][16] (dimension-major, the layout the matrix-core
+ * attention reads); block_table [B][max_blocks]; position p of sequence b
+ * lives in block block_table[b][p/16], slot p%16 (the gather of
+ * kv/paged_attention.cpp:161-230 with 16-token pages).
  * Attention follows model/hybrid_model.cpp:1493-1550: scores q.k * 1/sqrt(hd),
  * max-subtracted expf softmax divided by the sum, then the V weighted sum;
  * GQA maps query head h to kv head h / (hq/hkv) (:1471, :1502). */

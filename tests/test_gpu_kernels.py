@@ -165,16 +165,16 @@ def _pools(rng, B, hkv, hd, lens, seed=7):
     perm = np.empty(nblk, np.int32)
     L.nxo_shuffle_perm(perm, nblk, seed, 7)
     bt = np.ascontiguousarray(perm.reshape(B, max_blocks))
-    kp = np.zeros((nblk, hkv, 16, hd), np.float16)
-    vp = np.zeros_like(kp)
+    kp = np.zeros((nblk, hkv, 16, hd), np.float16)  # K pages token-major
+    vp = np.zeros((nblk, hkv, hd, 16), np.float16)  # V pages dimension-major
     for b in range(B):
         n = lens[b]
         K = rng.normal(0, 1, (n, hkv, hd)).astype(np.float16)
         V = rng.normal(0, 1, (n, hkv, hd)).astype(np.float16)
-        p = np.arange(n)
-        blk = bt[b, p // 16]
-        kp[blk, :, p % 16, :] = K
-        vp[blk, :, p % 16, :] = V
+        for p in range(n):
+            blk = bt[b, p // 16]
+            kp[blk, :, p % 16, :] = K[p]
+            vp[blk, :, :, p % 16] = V[p]
     return max_blocks, nblk, bt, kp.view(np.uint16), vp.view(np.uint16)
 
 
