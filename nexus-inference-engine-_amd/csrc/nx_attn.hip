@@ -288,18 +288,17 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
     }
 }
 
-// PIPE: more than one page pair per wavefront (pps > 8), two pairs in
-// flight; otherwise the single pair is loaded up front and the kernel fits
-// two blocks per CU.
+// One split of one (kv head, sequence): 8 pages (more for very long
+// contexts) shared by the block's four wavefronts, two pages per wavefront
+// step.  PIPE: more than one page pair per wavefront, two pairs in flight.
 template <int G, int HD, bool PIPE>
-__global__ __launch_bounds__(kAttnThreads, PIPE ? 1 : 2) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
+__device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
 
-    // The context length, q and this wavefront's block-table entries (page
+    // The context length and this wavefront's block-table entries (page
     // p0 + wave + 4i in lane i) are requested together: one round trip.
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     const int p0 = split * pps;
@@ -353,10 +352,12 @@ __global__ __launch_bounds__(kAttnThreads, PIPE ? 1 : 2) void k_attn_f16(AttnArg
                 load_pair<HD>(ra, a, blk_of(i + 4), valid_of(i + 4), blk_of(i + 5), valid_of(i + 5), kvh, lane);
             pair_update<HD>(rb, qh, ql, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
         }
-    } else if (npw > 0) {
+    } else {
         PairRaw<HD> ra;
-        load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
-        pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
+        if (npw > 0) {
+            load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
+            pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
+        }
     }
     // the head's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);
@@ -374,6 +375,14 @@ __global__ __launch_bounds__(kAttnThreads, PIPE ? 1 : 2) void k_attn_f16(AttnArg
     }
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
     merge_waves_store<G, HD>(parts + (size_t)split * REC, lds);
+}
+
+// PIPE: more than one page pair per wavefront (pps > 8), two pairs in
+// flight; otherwise the single pair is loaded up front and the kernel fits
+// two blocks per CU.
+template <int G, int HD, bool PIPE>
+__global__ __launch_bounds__(kAttnThreads, PIPE ? 1 : 2) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
+    attn_f16_run<G, HD, PIPE>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // ------------------------------------------------------ TurboQuant pages --
@@ -534,37 +543,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
 }
 
 // Merge the split records of one query head: block (h, kv head, sequence),
-// one thread per dimension.  Every thread requests its nsplit partial sums
-// and the heads' split maxima / sums at once (one memory round trip), then
-// rescales and sums in split order.  TQ: the merged value sum is still in the
+// one thread per dimension.  Every thread requests its nsplit partial sums at
+// once, and lane s of every wavefront the maximum and denominator of split s
+// (nsplit <= 64), so the split weights exp(m_s - M) and the denominator come
+// from wavefront reductions with no LDS round trip; the weighted sum reads
+// each weight from its lane.  TQ: the merged value sum is still in the
 // rotated domain and is rotated back once, o = D_v H o~ / sqrt(128).
 template <int G, int HD, bool TQ>
 __global__ __launch_bounds__(HD) void k_attn_merge(AttnArgs a, int nsplit) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
+    static_assert(kMaxSplits <= kWave, "one split per lane");
     const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
-    __shared__ float ms[kMaxSplits], ls[kMaxSplits];
-    __shared__ float ov[HD];
+    const int lane = t & (kWave - 1);
     const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
     float o[kMaxSplits];
 #pragma unroll
     for (int s = 0; s < kMaxSplits; ++s) o[s] = s < nsplit ? parts[(size_t)s * REC + h * HD + t] : 0.0f;
-    for (int s = t; s < nsplit; s += HD) {
-        ms[s] = parts[(size_t)s * REC + MO + h];
-        ls[s] = parts[(size_t)s * REC + LO + h];
-    }
-    __syncthreads();
-    float M = -__builtin_inff();
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ms[s]);
-    float acc = 0.0f, L = 0.0f;
+    const float ms = lane < nsplit ? parts[(size_t)lane * REC + MO + h] : -__builtin_inff();
+    const float ls = lane < nsplit ? parts[(size_t)lane * REC + LO + h] : 0.0f;
+    const float M = wave_max(ms);
+    const float f = (lane >= nsplit || M == -__builtin_inff()) ? 0.0f : __expf(ms - M);
+    const float L = wave_sum(f * ls);
+    float acc = 0.0f;
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) {
-        if (s < nsplit) {
-            const float f = (M == -__builtin_inff()) ? 0.0f : __expf(ms[s] - M);
-            acc = fmaf(o[s], f, acc);
-            L = fmaf(ls[s], f, L);
-        }
-    }
+    for (int s = 0; s < kMaxSplits; ++s)
+        if (s < nsplit) acc = fmaf(o[s], readlane_f(f, s), acc);
     if (TQ) {
+        __shared__ float ov[HD];
         ov[t] = acc;
         for (int hh = 1; hh < HD; hh <<= 1) {
             __syncthreads();

@@ -9,9 +9,11 @@
 // HBM stream: one 16-byte load (one group = 32 codes) plus one 2-byte scale
 // per lane per row, coalesced into 1 KiB per wave instruction.  R rows form a
 // tile whose R*GPL loads are in flight together.  At batch 1 the grid is
-// persistent (8 wavefronts per CU), each wavefront streams a contiguous row
-// range with the next tile requested before the current one is reduced, and
-// the first tile is requested before the input is staged.
+// persistent (one block of 8 wavefronts per CU), each wavefront streams a
+// contiguous row range with the next tile requested before the current one
+// is reduced, and the first tiles are requested right after the input.  The
+// loads up to the first wait are straight-line code, so the wait for the
+// input counts the tile loads behind it instead of waiting for all of them.
 //
 // Dequantisation without per-code conversion: the four masks
 //   A = w & 0x000F000F   (k0, k4)      B = w & 0x00F000F0   (k1, k5) * 16
@@ -27,584 +29,19 @@
 // and the paged KV append, SwiGLU of interleaved gate/up rows, or logits
 // with a running argmax.  The input is either fp16 x or the fused RMSNorm of
 // an fp32 hidden state, computed once per block into LDS.
-#include "nx_common.h"
-#include "nx_kernels.h"
+#include "nx_gemv_dev.h"
 
 namespace nx {
 
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-constexpr int kBlockThreads = kWavesPerBlock * kWave;
+using namespace gv;
 
-template <int GPL>
-struct XPairs {
-    uint32_t p[GPL][16];  // fp16 pairs (x[8d+j], x[8d+j+4]) per group
-    float s8[GPL];        // 8 * sum of the group's x (fp32)
-};
-
-__device__ inline void build_pairs(const uint32_t (&X)[16], uint32_t (&P)[16]) {
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        P[4 * d + 0] = __builtin_amdgcn_perm(X[4 * d + 2], X[4 * d + 0], 0x05040100u);
-        P[4 * d + 1] = __builtin_amdgcn_perm(X[4 * d + 2], X[4 * d + 0], 0x07060302u);
-        P[4 * d + 2] = __builtin_amdgcn_perm(X[4 * d + 3], X[4 * d + 1], 0x05040100u);
-        P[4 * d + 3] = __builtin_amdgcn_perm(X[4 * d + 3], X[4 * d + 1], 0x07060302u);
-    }
-}
-
-__device__ inline float group_sum16(const uint32_t (&X)[16]) {
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        s += h2f_bits((uint16_t)(X[j] & 0xFFFFu));
-        s += h2f_bits((uint16_t)(X[j] >> 16));
-    }
-    return s;
-}
-
-// x fp16 row -> pair registers.  Elements k >= K read as 0.
-template <int GPL>
-__device__ inline void load_x16(XPairs<GPL>& xp, const uint16_t* __restrict__ x, int K, int G,
-                                int lane) {
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-        const int g = lane + kWave * i;
-        uint32_t X[16];
-        const uint16_t* src = x + 32 * g;
-        if (g < G && 32 * g + 32 <= K && ((reinterpret_cast<uintptr_t>(src) & 15u) == 0)) {
-            const uint4* s4 = reinterpret_cast<const uint4*>(src);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = s4[q];
-                X[4 * q + 0] = v.x;
-                X[4 * q + 1] = v.y;
-                X[4 * q + 2] = v.z;
-                X[4 * q + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int k = 32 * g + 2 * j;
-                const uint32_t lo = (g < G && k < K) ? src[2 * j] : 0u;
-                const uint32_t hi = (g < G && k + 1 < K) ? src[2 * j + 1] : 0u;
-                X[j] = lo | (hi << 16);
-            }
-        }
-        build_pairs(X, xp.p[i]);
-        xp.s8[i] = 8.0f * group_sum16(X);
-    }
-}
-
-// 1/sqrt(mean(h^2) + eps) of one fp32 row, wave-uniform.
-template <int GPL>
-__device__ inline float rms_inv(const float* __restrict__ h, int K, int G, float eps, int lane) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-        const int g = lane + kWave * i;
-        if (g < G) {
-            const float* src = h + 32 * g;
-            if (32 * g + 32 <= K && ((reinterpret_cast<uintptr_t>(src) & 15u) == 0)) {
-                const float4* s4 = reinterpret_cast<const float4*>(src);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const float4 v = s4[q];
-                    ss += v.x * v.x;
-                    ss += v.y * v.y;
-                    ss += v.z * v.z;
-                    ss += v.w * v.w;
-                }
-            } else {
-                for (int j = 0; j < 32; ++j)
-                    if (32 * g + j < K) ss += src[j] * src[j];
-            }
-        }
-    }
-    ss = wave_sum(ss);
-    return 1.0f / sqrtf(ss / (float)K + eps);
-}
-
-// x = fp16((h * inv) * w) -> pair registers.
-template <int GPL>
-__device__ inline void load_x_norm(XPairs<GPL>& xp, const float* __restrict__ h,
-                                   const float* __restrict__ w, float inv, int K, int G,
-                                   int lane) {
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-        const int g = lane + kWave * i;
-        uint32_t X[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int k = 32 * g + 2 * j;
-            uint32_t lo = 0, hi = 0;
-            if (g < G && k < K) {
-                const float v = h[k] * inv;
-                lo = f2h_bits(w ? v * w[k] : v);
-            }
-            if (g < G && k + 1 < K) {
-                const float v = h[k + 1] * inv;
-                hi = f2h_bits(w ? v * w[k + 1] : v);
-            }
-            X[j] = lo | (hi << 16);
-        }
-        build_pairs(X, xp.p[i]);
-        xp.s8[i] = 8.0f * group_sum16(X);
-    }
-}
-
-__device__ inline half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
-
-// sum_{k in group} (q_k - 8) x_k for one 16-byte group of codes.
-__device__ inline float group_dot(uint4 w, const uint32_t (&P)[16], float s8) {
-    float accA = 0.0f, accB = 0.0f;
-    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const uint32_t a = wd[d] & 0x000F000Fu;
-        const uint32_t b = wd[d] & 0x00F000F0u;
-        const uint32_t w8 = wd[d] >> 8;
-        const uint32_t c = w8 & 0x000F000Fu;
-        const uint32_t e = w8 & 0x00F000F0u;
-        accA = __builtin_amdgcn_fdot2(as_h2(a), as_h2(P[4 * d + 0]), accA, false);
-        accA = __builtin_amdgcn_fdot2(as_h2(c), as_h2(P[4 * d + 2]), accA, false);
-        accB = __builtin_amdgcn_fdot2(as_h2(b), as_h2(P[4 * d + 1]), accB, false);
-        accB = __builtin_amdgcn_fdot2(as_h2(e), as_h2(P[4 * d + 3]), accB, false);
-    }
-    return fmaf(accB, 0x1p20f, accA * 0x1p24f) - s8;
-}
-
-template <int GPL, int R>
-struct Tile {
-    uint4 w[R][GPL];
-    uint16_t s[R][GPL];  // raw fp16 scales, converted at use so no wait is forced at load
-};
-
-// Load rows [n0, n0 + R) of the weight matrix; rows at or beyond `nlim`
-// (the end of this wavefront's row range) are not read and count as zero.
-template <int GPL, int R>
-__device__ inline void load_tile(Tile<GPL, R>& t, const uint8_t* __restrict__ W,
-                                 const uint16_t* __restrict__ S, int G, int nlim, int n0,
-                                 int lane) {
-    const size_t rowbytes = (size_t)G * 16;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = n0 + r;
-#pragma unroll
-        for (int i = 0; i < GPL; ++i) {
-            const int g = lane + kWave * i;
-            if (row < nlim && g < G) {
-                t.w[r][i] = *reinterpret_cast<const uint4*>(W + (size_t)row * rowbytes + 16 * (size_t)g);
-                t.s[r][i] = S[(size_t)row * G + g];
-            } else {
-                t.w[r][i] = make_uint4(0u, 0u, 0u, 0u);
-                t.s[r][i] = 0;
-            }
-        }
-    }
-}
-
-template <int GPL, int R>
-__device__ inline void tile_dot(const Tile<GPL, R>& t, const XPairs<GPL>& xp, float (&res)[R]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < GPL; ++i)
-            acc = fmaf(group_dot(t.w[r][i], xp.p[i], xp.s8[i]), h2f_bits(t.s[r][i]), acc);
-        res[r] = wave_sum(acc);
-    }
-}
-
-__device__ inline unsigned long long pack_best(float v, int idx) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
-}
-
-// Values the QKV epilogue needs, fetched before the tile is reduced so the
-// epilogue does not wait on memory: the position, RoPE cos/sin of each row
-// pair of the tile and the block of the page the new K/V go to.
-struct RopePre {
-    bool valid;
-    int p, blk;
-    float c[4], s[4];
-};
-
-// Rows at or beyond `nlim` are not stored.  The residual add (E_ACC) is a
-// no-return atomic add: each element has exactly one writer, so the sum is
-// the plain y + res, and the wavefront does not wait for a read of y.
-template <int EPI, int R>
-__device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, const float (&res)[R],
-                                float& best_v, int& best_i, const RopePre* pre = nullptr) {
-    if (EPI == E_F16) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (n0 + r < nlim) a.y16[(size_t)b * a.ldy + n0 + r] = f2h_bits(res[r]);
-    } else if (EPI == E_F32) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (n0 + r < nlim) a.y32[(size_t)b * a.ldy + n0 + r] = res[r];
-    } else if (EPI == E_ACC) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (n0 + r < nlim)
-                __hip_atomic_fetch_add(a.y32 + (size_t)b * a.ldy + n0 + r, res[r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-    } else if (EPI == E_QKV) {
-        const bool have = pre && pre->valid;
-        const int p = have ? pre->p : a.pos[b];
-        const int half = a.hd >> 1;
-#pragma unroll
-        for (int r = 0; r < R; r += 2) {
-            const int row = n0 + r;
-            if (row >= nlim) break;
-            float v0 = res[r], v1 = res[r + 1];
-            if (row < a.qdim + a.kvdim) {
-                const int i = (row % a.hd) >> 1;
-                const float c = have ? pre->c[r / 2] : a.cos_t[(size_t)p * half + i];
-                const float s = have ? pre->s[r / 2] : a.sin_t[(size_t)p * half + i];
-                const float r0 = v0 * c - v1 * s;
-                const float r1 = v0 * s + v1 * c;
-                v0 = r0;
-                v1 = r1;
-            }
-            if (row < a.qdim) {
-                a.q32[(size_t)b * a.qdim + row] = v0;
-                a.q32[(size_t)b * a.qdim + row + 1] = v1;
-            } else {
-                const int kv = row < a.qdim + a.kvdim ? 0 : 1;
-                const int idx = row - a.qdim - kv * a.kvdim;
-                if (a.kpool) {
-                    const int kvh = idx / a.hd, dd = idx % a.hd;
-                    const int blk = have ? pre->blk : a.block_table[(size_t)b * a.max_blocks + p / kPage];
-                    const size_t page = ((size_t)blk * a.hkv + kvh) * kPage * a.hd;
-                    if (kv) {  // V pages are dimension-major: [hd][16]
-                        a.vpool[page + (size_t)dd * kPage + p % kPage] = f2h_bits(v0);
-                        a.vpool[page + (size_t)(dd + 1) * kPage + p % kPage] = f2h_bits(v1);
-                    } else {   // K pages are token-major: [16][hd]
-                        a.kpool[page + (size_t)(p % kPage) * a.hd + dd] = f2h_bits(v0);
-                        a.kpool[page + (size_t)(p % kPage) * a.hd + dd + 1] = f2h_bits(v1);
-                    }
-                } else {
-                    float* dst = a.kv_tmp + ((size_t)b * 2 + kv) * a.kvdim + idx;
-                    dst[0] = v0;
-                    dst[1] = v1;
-                }
-            }
-        }
-    } else if (EPI == E_SWIGLU) {
-#pragma unroll
-        for (int r = 0; r < R; r += 2) {
-            const int row = n0 + r;
-            if (row >= nlim) break;
-            const float g = res[r], u = res[r + 1];
-            a.act16[(size_t)b * a.lda + (row >> 1)] = f2h_bits(g / (1.0f + expf(-g)) * u);
-        }
-    } else if (EPI == E_LOGITS) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (n0 + r < nlim) {
-                a.y32[(size_t)b * a.ldy + n0 + r] = res[r];
-                if (res[r] > best_v) {
-                    best_v = res[r];
-                    best_i = n0 + r;
-                }
-            }
-    }
-}
-
-// Eight consecutive inputs starting at k0 (zero beyond K).
-__device__ inline void load_h8(const float* __restrict__ h, int k0, int K, bool vec, float (&v)[8]) {
-    if (vec && k0 + 8 <= K) {
-        const float4 a = *reinterpret_cast<const float4*>(h + k0);
-        const float4 c = *reinterpret_cast<const float4*>(h + k0 + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = k0 + j < K ? h[k0 + j] : 0.0f;
-    }
-}
-__device__ inline void load_x8(const uint16_t* __restrict__ x, int k0, int K, bool vec, uint32_t (&X)[4]) {
-    if (vec && k0 + 8 <= K) {
-        const uint4 v = *reinterpret_cast<const uint4*>(x + k0);
-        X[0] = v.x; X[1] = v.y; X[2] = v.z; X[3] = v.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t lo = k0 + 2 * j < K ? x[k0 + 2 * j] : 0u;
-            const uint32_t hi = k0 + 2 * j + 1 < K ? x[k0 + 2 * j + 1] : 0u;
-            X[j] = lo | (hi << 16);
-        }
-    }
-}
-
-// Store one 8-element chunk c (fp16 values X) in the pair layout and its
-// contribution to the group sum.
-__device__ inline void put_chunk(int c, const uint32_t (&X)[4], uint32_t* sp, float* s8) {
-    uint32_t* dst = sp + (c >> 2) * 16 + (c & 3) * 4;
-    dst[0] = __builtin_amdgcn_perm(X[2], X[0], 0x05040100u);
-    dst[1] = __builtin_amdgcn_perm(X[2], X[0], 0x07060302u);
-    dst[2] = __builtin_amdgcn_perm(X[3], X[1], 0x05040100u);
-    dst[3] = __builtin_amdgcn_perm(X[3], X[1], 0x07060302u);
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        s += h2f_bits((uint16_t)(X[j] & 0xFFFFu));
-        s += h2f_bits((uint16_t)(X[j] >> 16));
-    }
-    // the 4 chunks of a group sit in one DPP quad (nthr and nch are multiples of 4)
-    s += dpp<kQuadXor1>(s);
-    s += dpp<kQuadXor2>(s);
-    if ((c & 3) == 0) s8[c >> 2] = 8.0f * s;
-}
-
-__device__ inline void norm_chunk(const float (&v)[8], const float* __restrict__ w, int k0, int K,
-                                  float inv, uint32_t (&X)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint32_t lo = 0, hi = 0;
-        const int k = k0 + 2 * j;
-        if (k < K) {
-            const float t = v[2 * j] * inv;
-            lo = f2h_bits(w ? t * w[k] : t);
-        }
-        if (k + 1 < K) {
-            const float t = v[2 * j + 1] * inv;
-            hi = f2h_bits(w ? t * w[k + 1] : t);
-        }
-        X[j] = lo | (hi << 16);
-    }
-}
-
-// Block-cooperative staging of one x row into LDS in the pair layout:
-// sp[g*16 + 4d + j] = (x[32g+8d+j], x[32g+8d+j+4]) and s8[g] = 8 * sum of
-// group g.  Thread t of the 256 handles the 8-element chunks t, t + 256, ...
-// (at most CPT = GPL of them, as G * 4 <= 256 * GPL).  The staging is split
-// in two so the caller can request its weight tiles in between: the row is
-// requested first (stage_issue) and converted afterwards (stage_finish).
-// Loads complete in issue order, so waiting for the row then does not wait
-// for the weights, and a wavefront's first tile can be reduced as soon as it
-// arrives.  For X_RMSNORM the block reduces sum(h^2) once and converts from
-// the registers.  stage_finish ends with a barrier.
-template <int CPT, int XS>
-struct StageRegs {
-    float v[XS == X_RMSNORM ? CPT : 1][8];
-    uint32_t X[XS == X_F16 ? CPT : 1][4];
-};
-
-template <int CPT, int XS>
-__device__ inline void stage_issue(const GemvArgs& a, int b, StageRegs<CPT, XS>& r) {
-    const int K = a.K, nch = a.G * 4, tid = threadIdx.x;
-    if (XS == X_F16) {
-        const uint16_t* x = a.x16 + (size_t)b * a.ldx;
-        const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (a.ldx & 7) == 0;
-#pragma unroll
-        for (int j = 0; j < CPT; ++j)
-            if (tid + j * kBlockThreads < nch) load_x8(x, 8 * (tid + j * kBlockThreads), K, vec, r.X[j]);
-    } else {
-        const float* h = a.h32 + (size_t)b * a.ldx;
-        const bool vec = (reinterpret_cast<uintptr_t>(h) & 15u) == 0 && (a.ldx & 3) == 0;
-#pragma unroll
-        for (int j = 0; j < CPT; ++j)
-            if (tid + j * kBlockThreads < nch) load_h8(h, 8 * (tid + j * kBlockThreads), K, vec, r.v[j]);
-    }
-}
-
-template <int CPT, int XS>
-__device__ inline void stage_finish(const GemvArgs& a, StageRegs<CPT, XS>& r, uint32_t* sp,
-                                    float* s8, float* red) {
-    const int K = a.K, nch = a.G * 4, tid = threadIdx.x;
-    if (XS == X_F16) {
-#pragma unroll
-        for (int j = 0; j < CPT; ++j)
-            if (tid + j * kBlockThreads < nch) put_chunk(tid + j * kBlockThreads, r.X[j], sp, s8);
-    } else {
-        float ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPT; ++j)
-            if (tid + j * kBlockThreads < nch)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss += r.v[j][e] * r.v[j][e];
-        ss = wave_sum(ss);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int w = 0; w < kWavesPerBlock; ++w) tot += red[w];
-        const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = tid + j * kBlockThreads;
-            if (c < nch) {
-                uint32_t X[4];
-                norm_chunk(r.v[j], a.norm_w, 8 * c, K, inv, X);
-                put_chunk(c, X, sp, s8);
-            }
-        }
-    }
-    __syncthreads();
-}
-
-template <int GPL>
-__device__ inline void load_pairs_lds(XPairs<GPL>& xp, const uint32_t* sp, const float* s8, int G,
-                                      int lane) {
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-        const int g = lane + kWave * i;
-        if (g < G) {
-            const uint4* src = reinterpret_cast<const uint4*>(sp + g * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = src[q];
-                xp.p[i][4 * q + 0] = v.x;
-                xp.p[i][4 * q + 1] = v.y;
-                xp.p[i][4 * q + 2] = v.z;
-                xp.p[i][4 * q + 3] = v.w;
-            }
-            xp.s8[i] = s8[g];
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) xp.p[i][j] = 0u;
-            xp.s8[i] = 0.0f;
-        }
-    }
-}
-
-// Row range of wavefront `w` for batch 1: rows are dealt in pairs (a pair is
-// never split, so the RoPE and SwiGLU epilogues see both rows), `base` pairs
-// per wavefront plus one more for the first `extra` wavefronts.
-struct RowSplit {
-    int base, extra;
-};
-
-__device__ inline void wave_rows(const RowSplit& rs, int w, int N, int& r0, int& r1) {
-    const int u0 = w * rs.base + min(w, rs.extra);
-    const int nu = rs.base + (w < rs.extra ? 1 : 0);
-    r0 = min(2 * u0, N);
-    r1 = min(2 * (u0 + nu), N);
-}
-
-// Tile product with x read from the LDS pair layout (used where holding x in
-// registers would cost GPL * 17 VGPRs and limit occupancy).
-template <int GPL, int R>
-__device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, const float* s8,
-                                    int G, int lane, float (&res)[R]) {
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-        const int g = lane + kWave * i;
-        uint32_t P[16];
-        float sx = 0.0f;
-        if (g < G) {
-            const uint4* src = reinterpret_cast<const uint4*>(sp + g * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = src[q];
-                P[4 * q + 0] = v.x;
-                P[4 * q + 1] = v.y;
-                P[4 * q + 2] = v.z;
-                P[4 * q + 3] = v.w;
-            }
-            sx = s8[g];
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) P[j] = 0u;
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            acc[r] = fmaf(group_dot(t.w[r][i], P, sx), h2f_bits(t.s[r][i]), acc[r]);
-        // keep the scheduler from hoisting the next groups' LDS reads (their
-        // registers would push the kernel below two wavefronts per SIMD)
-        __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) res[r] = wave_sum(acc[r]);
-}
-
-// Batch 1, persistent: every wavefront streams its own contiguous row range
-// as R-row tiles through a ring of DEPTH register tiles.  A buffer is
-// refilled as soon as its tile has been reduced, so DEPTH - 1 tiles are in
-// flight while one is reduced, and the first DEPTH tiles are requested
-// before the input is staged, so the HBM stream starts with the kernel.
-// XLDS: x is read from LDS per group instead of being held in registers.
-template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI>
-__global__ __launch_bounds__(kBlockThreads, 2) void k_gemv_b1(GemvArgs a, RowSplit rs) {
-    __shared__ __align__(16) uint32_t sp[kWave * GPL * 16];
-    __shared__ float s8[kWave * GPL];
-    __shared__ float red[kWavesPerBlock];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    int r0, r1;
-    wave_rows(rs, wid, a.N, r0, r1);
-    const int nt = r1 > r0 ? (r1 - r0 + R - 1) / R : 0;
-    // QKV: the position (a scalar load) first, the RoPE tables and the page
-    // block after the tiles; lane l holds the pair of rows r0 + 2l
-    const bool rope_pre = EPI == E_QKV && r1 - r0 <= 2 * kWave;
-    const int qp = EPI == E_QKV ? a.pos[0] : 0;
-    StageRegs<GPL, XS> sr;
-    stage_issue<GPL, XS>(a, 0, sr);
-    Tile<GPL, R> t[DEPTH];
-#pragma unroll
-    for (int j = 0; j < DEPTH; ++j)
-        if (j < nt) load_tile<GPL, R>(t[j], a.W, a.S, a.G, r1, r0 + j * R, lane);
-    float qc = 0.0f, qs = 0.0f;
-    int qblk = 0;
-    if (EPI == E_QKV && rope_pre) {
-        const int row = r0 + 2 * lane;
-        if (row < r1 && row < a.qdim + a.kvdim) {
-            const int i = (row % a.hd) >> 1;
-            qc = a.cos_t[(size_t)qp * (a.hd >> 1) + i];
-            qs = a.sin_t[(size_t)qp * (a.hd >> 1) + i];
-        }
-        if (a.kpool) qblk = a.block_table[qp / kPage];
-    }
-    stage_finish<GPL, XS>(a, sr, sp, s8, red);  // block barrier: every wavefront takes part
-    float best_v = -__builtin_inff();
-    int best_i = -1;
-    if (nt > 0) {
-        XPairs<XLDS ? 1 : GPL> xp;
-        if (!XLDS) load_pairs_lds<XLDS ? 1 : GPL>(xp, sp, s8, a.G, lane);
-        float res[R];
-        for (int i = 0; i < nt; i += DEPTH) {
-#pragma unroll
-            for (int j = 0; j < DEPTH; ++j) {
-                if (i + j >= nt) break;
-                if constexpr (XLDS)
-                    tile_dot_lds<GPL, R>(t[j], sp, s8, a.G, lane, res);
-                else
-                    tile_dot<GPL, R>(t[j], xp, res);
-                if (i + j + DEPTH < nt)
-                    load_tile<GPL, R>(t[j], a.W, a.S, a.G, r1, r0 + (i + j + DEPTH) * R, lane);
-                RopePre pre{};
-                if (EPI == E_QKV && rope_pre) {
-                    const int u0 = (i + j) * R / 2;  // first pair of the tile within the wave
-                    pre.valid = true;
-                    pre.p = qp;
-                    pre.blk = qblk;
-#pragma unroll
-                    for (int q = 0; q < (R + 1) / 2 && q < 4; ++q) {
-                        pre.c[q] = readlane_f(qc, min(u0 + q, kWave - 1));
-                        pre.s[q] = readlane_f(qs, min(u0 + q, kWave - 1));
-                    }
-                }
-                if (lane == 0) epilogue<EPI, R>(a, 0, r0 + (i + j) * R, r1, res, best_v, best_i, &pre);
-            }
-        }
-    }
-    if (EPI == E_LOGITS) {
-        // one atomic per block: the wavefronts' maxima meet in LDS first
-        __shared__ unsigned long long bk[kWavesPerBlock];
-        if (lane == 0) bk[threadIdx.x >> 6] = best_i >= 0 ? pack_best(best_v, best_i) : 0ull;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned long long m = 0ull;
-            for (int w = 0; w < kWavesPerBlock; ++w) m = bk[w] > m ? bk[w] : m;
-            if (m) atomicMax(&a.best[0], m);
-        }
-    }
+// Batch 1 kernel: the whole grid runs one GEMV, one block of WPB
+// wavefronts per CU.
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB, bool XVEC>
+__global__ __launch_bounds__(WPB * kWave, 1) void k_gemv_b1(GemvArgs a, RowSplit rs) {
+    gemv_b1_run<GPL, R, DEPTH, XLDS, XS, EPI, WPB, XVEC>(a, rs, blockIdx.x);
 }
 
 // Batch 2..8: the weight tile is loaded once and applied to every row of x.
@@ -719,36 +156,21 @@ hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
-// Wavefronts per CU of the batch-1 GEMV: two per SIMD.
-constexpr int kB1WavesPerCU = 8;
-
-// Batch 1: a persistent grid of kB1WavesPerCU wavefronts per CU, each with
-// at least one full tile; row pairs are dealt out evenly.
-template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI>
-hipError_t launch_b1(const GemvArgs& a, hipStream_t st, int waves_per_cu = kB1WavesPerCU) {
-    const int units = (a.N + 1) / 2;
-    const int min_units = (R + 1) / 2;
-    int waves = device_cus() * waves_per_cu;
-    const int maxw = (units + min_units - 1) / min_units;
-    if (waves > maxw) waves = maxw;
-    waves = (waves + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
-    const RowSplit rs{units / waves, units % waves};
-    hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI>), dim3(waves / kWavesPerBlock),
-                       dim3(kBlockThreads), 0, st, a, rs);
+// Batch 1: a persistent grid of WPB wavefronts per CU in one block each
+// (see b1_plan).
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB = kB1WavesPerCU>
+hipError_t launch_b1(const GemvArgs& a, hipStream_t st) {
+    RowSplit rs;
+    const int blocks = b1_plan(a.N, R, WPB, rs, WPB);
+    // the branch-free input loads need whole 8-element chunks on 16 bytes
+    const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
+    const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    if (xvec)
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, true>), dim3(blocks), dim3(WPB * kWave),
+                           0, st, a, rs);
+    else
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, false>), dim3(blocks),
+                           dim3(WPB * kWave), 0, st, a, rs);
     return hipGetLastError();
 }
 
@@ -763,17 +185,22 @@ hipError_t launch_bn(const GemvArgs& a, hipStream_t st) {
 }
 
 // Tile shapes per groups-per-lane (K <= 64 * 32 * GPL), chosen by measuring
-// the 8B decode shapes on cold weights.  Batch 1, K = 4096: tiles of 2 rows
-// (a pair, as the RoPE and SwiGLU epilogues need) in a ring of 2 with 12
-// wavefronts per CU.  K = 14336 without paired rows: one row per tile with x
-// in registers.  Paired epilogues at GPL >= 4 keep x in LDS.
+// the 8B decode shapes on cold weights; batch 1 runs one block of 8
+// wavefronts per CU.  K = 4096: QKV in 4-row tiles, gate/up and lm_head in
+// 2-row tiles (a pair, as the SwiGLU epilogue needs) in a ring of 2, single
+// rows in a ring of 3 otherwise.  K = 14336 without paired rows: one row per
+// tile with x in registers.  Paired epilogues at GPL >= 4 keep x in LDS.
 template <int XS, int EPI>
 hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
     const int gpl = (a.G + kWave - 1) / kWave;
     constexpr bool kPairs = EPI == E_QKV || EPI == E_SWIGLU;
     if (a.batch == 1) {
         if (gpl <= 1) return launch_b1<1, 4, 2, false, XS, EPI>(a, st);
-        if (gpl <= 2) return launch_b1<2, 2, 2, false, XS, EPI>(a, st, 12);
+        if (gpl <= 2) {
+            if constexpr (EPI == E_QKV) return launch_b1<2, 4, 1, false, XS, EPI>(a, st);
+            if constexpr (EPI == E_SWIGLU || EPI == E_LOGITS) return launch_b1<2, 2, 2, false, XS, EPI>(a, st);
+            return launch_b1<2, 1, 3, false, XS, EPI>(a, st);
+        }
         if (gpl <= 4) return launch_b1<4, 2, 2, true, XS, EPI>(a, st);
         if (gpl > 7) return hipErrorInvalidValue;
         if constexpr (kPairs) return launch_b1<7, 2, 2, true, XS, EPI>(a, st);

@@ -73,7 +73,8 @@ struct nx_model {
     float* attn_part = nullptr;
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
-    hipGraphExec_t exec = nullptr;
+    hipGraphExec_t exec = nullptr;        // one decode step
+    hipGraphExec_t exec_multi = nullptr;  // kStepsPerGraph decode steps
     std::vector<int> hpos;       // host mirror of pos (last processed position)
 };
 
@@ -150,7 +151,8 @@ nx_status enqueue_step(nx_model* m) {
     const nx_model_config& c = m->c;
     hipStream_t st = m->ctx->stream;
     const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts;
-    NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d, c.vocab, B, st));
+    NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d,
+                                  c.vocab, B, st));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
         // RMSNorm + QKV + RoPE + paged KV append
@@ -316,12 +318,16 @@ nx_status enqueue_step(nx_model* m) {
     return NX_OK;
 }
 
-nx_status ensure_graph(nx_model* m) {
-    if (m->exec) return NX_OK;
+// Decode steps per multi-step graph: a graph launch has a fixed cost of a few
+// microseconds, paid once per kStepsPerGraph tokens in nx_model_decode.
+constexpr int kStepsPerGraph = 8;
+
+nx_status capture_steps(nx_model* m, int steps, hipGraphExec_t* out) {
     hipStream_t st = m->ctx->stream;
     NX_HIP(m->ctx, hipStreamSynchronize(st));
     NX_HIP(m->ctx, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    nx_status s = enqueue_step(m);
+    nx_status s = NX_OK;
+    for (int i = 0; i < steps && s == NX_OK; ++i) s = enqueue_step(m);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(st, &g);
     if (s != NX_OK) {
@@ -329,18 +335,25 @@ nx_status ensure_graph(nx_model* m) {
         return s;
     }
     if (e != hipSuccess) return nx::hip_fail(m->ctx, e, "hipStreamEndCapture");
-    e = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-        m->exec = nullptr;
+        *out = nullptr;
         return nx::hip_fail(m->ctx, e, "hipGraphInstantiate (decode step)");
     }
+    return NX_OK;
+}
+
+nx_status ensure_graph(nx_model* m) {
+    if (!m->exec) NX_TRY(capture_steps(m, 1, &m->exec));
+    if (!m->exec_multi) NX_TRY(capture_steps(m, kStepsPerGraph, &m->exec_multi));
     return NX_OK;
 }
 
 nx_status free_model(nx_model* m) {
     if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->exec_multi) (void)hipGraphExecDestroy(m->exec_multi);
     for (void* p : m->allocs) (void)hipFree(p);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
     if (m->h_out) (void)hipHostFree(m->h_out);
@@ -626,7 +639,9 @@ nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
     hipStream_t st = m->ctx->stream;
     for (int b = 0; b < B; ++b) m->h_stage[b] = m->hpos[b] + 1;
     NX_HIP(m->ctx, hipMemcpyAsync(m->base, m->h_stage, (size_t)B * 4, hipMemcpyHostToDevice, st));
-    for (int s = 0; s < steps; ++s) NX_HIP(m->ctx, hipGraphLaunch(m->exec, st));
+    int s = 0;
+    for (; s + kStepsPerGraph <= steps; s += kStepsPerGraph) NX_HIP(m->ctx, hipGraphLaunch(m->exec_multi, st));
+    for (; s < steps; ++s) NX_HIP(m->ctx, hipGraphLaunch(m->exec, st));
     NX_LAUNCH(m, nx::finish_tokens_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, B, st));
     if (out_tokens)
         NX_HIP(m->ctx, hipMemcpyAsync(m->h_out, m->out_tokens, (size_t)B * m->out_stride * 4, hipMemcpyDeviceToHost, st));
