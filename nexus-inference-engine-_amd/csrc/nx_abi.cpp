@@ -34,6 +34,21 @@ nx_status ensure_attn_ws(nx_ctx* ctx, size_t bytes) {
     return NX_OK;
 }
 
+// Split-completion counters of the fp16 attention: zeroed when allocated,
+// and every launch leaves them at zero.
+nx_status ensure_attn_counts(nx_ctx* ctx, size_t words) {
+    if (words <= ctx->attn_count_words) return NX_OK;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "attention counters must grow outside capture");
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->attn_counts) (void)hipFree(ctx->attn_counts);
+    ctx->attn_counts = nullptr;
+    ctx->attn_count_words = 0;
+    NX_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->attn_counts), words * sizeof(unsigned)));
+    NX_HIP(ctx, hipMemsetAsync(ctx->attn_counts, 0, words * sizeof(unsigned), ctx->stream));
+    ctx->attn_count_words = words;
+    return NX_OK;
+}
+
 template <class T>
 T* dptr(nx_buf b) {
     return reinterpret_cast<T*>(static_cast<uintptr_t>(b));
@@ -140,6 +155,7 @@ nx_status nx_destroy(nx_ctx* ctx) {
     if (ctx->token_exec) (void)hipGraphExecDestroy(ctx->token_exec);
     for (auto& kv : ctx->bufs) (void)hipFree(reinterpret_cast<void*>(kv.first));
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+    if (ctx->attn_counts) (void)hipFree(ctx->attn_counts);
     (void)hipEventDestroy(ctx->ev0);
     (void)hipEventDestroy(ctx->ev1);
     (void)hipStreamDestroy(ctx->stream);
@@ -482,7 +498,10 @@ nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf v
     if (max_ctx > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_blocks above the attention limit");
     s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, hq, hkv, hd, max_ctx));
     if (s != NX_OK) return s;
+    s = ensure_attn_counts(ctx, nx::attn_count_words(batch, hkv));
+    if (s != NX_OK) return s;
     nx::AttnArgs a{};
+    a.counts = ctx->attn_counts;
     a.q = dptr<const float>(q);
     a.kpool = dptr<const uint16_t>(kpool);
     a.vpool = dptr<const uint16_t>(vpool);

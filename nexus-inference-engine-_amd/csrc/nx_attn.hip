@@ -9,11 +9,11 @@
 // each wavefront requests its block-table entries with q and then keeps two
 // pairs of pages in flight.  Each DPP row keeps its own online-softmax state
 // (m, l, o); rows and wavefronts are merged with the usual rescaling and the
-// block stores one split record.  A second small launch merges the split
-// records of each (sequence, kv head) and writes the fp16 output: a separate
-// launch costs less than handing the records across blocks inside one launch,
-// which on this multi-XCD part needs device-scope fences or several dependent
-// memory round trips.
+// block stores one split record.  fp16 pages: the last block of a (sequence,
+// kv head) to count itself done merges its split records and writes the fp16
+// output; records and counters use agent-scope (cross-XCD coherent) relaxed
+// accesses, with each block's stores complete before it counts, and no
+// device-scope fence.  TurboQuant pages: a second small launch merges.
 //
 // TurboQuant pages are scored in the rotated domain: the block rotates q once
 // (q~ = H D q / sqrt(128)), scores are n_t * <q~, c[code_t]>, V is summed in the
@@ -52,6 +52,7 @@ SplitPlan plan_splits(int max_ctx) {
 
 // Split partial record, float offsets: O[G][HD] at 0, M[G], L[G], padded to 16 bytes.
 __host__ __device__ constexpr int rec_floats(int G, int HD) { return (G * HD + 2 * G + 3) / 4 * 4; }
+
 
 // Online-softmax state of one lane: G heads x DPL dims.
 template <int G, int DPL>
@@ -125,10 +126,19 @@ __device__ inline void state_merge_rows(State<G, DPL>& s) {
     }
 }
 
+// Agent-scope (coherent across XCDs) store and load of a split record word,
+// for records handed to the block that merges them within the same launch.
+__device__ inline void st_coh(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_coh(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Cross-wavefront merge of the block: lds holds one record per wavefront
 // (O[G][HD], M[G], L[G]); every wavefront has written its own before the
-// barrier.  The merged split record goes to `part`.
-template <int G, int HD>
+// barrier.  The merged split record goes to `part` (COH: agent-scope stores).
+template <int G, int HD, bool COH = false>
 __device__ inline void merge_waves_store(float* __restrict__ part, const float* lds) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     __syncthreads();
@@ -144,7 +154,14 @@ __device__ inline void merge_waves_store(float* __restrict__ part, const float* 
             const float f = (M == -__builtin_inff()) ? 0.0f : __expf(lds[w * REC + MO + h] - M);
             acc = fmaf(lds[w * REC + (is_o ? idx : LO + h)], f, acc);
         }
-        if (is_o) {
+        if (COH) {
+            if (is_o) {
+                st_coh(part + idx, acc);
+            } else {
+                st_coh(part + MO + h, M);
+                st_coh(part + LO + h, acc);
+            }
+        } else if (is_o) {
             part[idx] = acc;
         } else {
             part[MO + h] = M;
@@ -200,35 +217,40 @@ template <int HD>
 struct PairRaw {
     uint4 k[2][HD / 32];  // K of pages a, b: A operand per k-step
     uint2 v[HD / 16][2];  // V of pages a, b: tokens 4g..4g+3 of dim 16 nt + l%16
+    uint2 vmask[2];       // per page: bits of the V words that hold valid tokens
 };
 
 // Load pages a and b of a pair; na / nb = valid tokens of each (0 = none).
-// Tokens at or beyond the valid count read as zero.
+// Every load is issued unconditionally, because a branch or a select around a
+// load makes the compiler wait for that load at once and the page would
+// arrive one round trip per tile: page b with no valid token re-reads page a
+// (blka must be a valid block), K rows of tokens past the valid count are
+// left as loaded (their scores are masked in pair_update), and the V words
+// of those tokens are cleared with masks.
 template <int HD>
 __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, int na, int blkb,
                                  int nb, int kvh, int lane) {
     const int g = lane >> 4, t = lane & 15;
+    const int pb = nb > 0 ? blkb : blka;
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
-        const int blk = pg ? blkb : blka, n = pg ? nb : na;
+        const int blk = pg ? pb : blka, n = pg ? nb : na;
         const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
 #pragma unroll
         for (int s = 0; s < HD / 32; ++s)
-            r.k[pg][s] = t < n ? *reinterpret_cast<const uint4*>(a.kpool + base + (size_t)t * HD + 32 * s + 8 * g)
-                               : make_uint4(0u, 0u, 0u, 0u);
+            r.k[pg][s] = *reinterpret_cast<const uint4*>(a.kpool + base + (size_t)t * HD + 32 * s + 8 * g);
+        // tokens 4g .. 4g+3 of the V words: the first `valid` are kept
+        // (applied in pair_update, so that nothing here waits for the data)
         const int valid = min(max(n - 4 * g, 0), 4);
+        r.vmask[pg] = make_uint2((uint32_t)(0xFFFFFFFFull >> (16 * (2 - min(valid, 2)))),
+                                 (uint32_t)(0xFFFFFFFFull >> (16 * (2 - max(valid - 2, 0)))));
 #pragma unroll
-        for (int nt = 0; nt < HD / 16; ++nt) {
-            uint2 w = make_uint2(0u, 0u);
-            if (valid > 0) {
-                w = *reinterpret_cast<const uint2*>(a.vpool + base + (size_t)(16 * nt + t) * kPage + 4 * g);
-                if (valid < 2) w.x &= 0xFFFFu;   // keep token 4g only
-                if (valid < 3) w.y = 0u;          // drop tokens 4g+2, 4g+3
-                else if (valid == 3) w.y &= 0xFFFFu;
-            }
-            r.v[nt][pg] = w;
-        }
+        for (int nt = 0; nt < HD / 16; ++nt)
+            r.v[nt][pg] = *reinterpret_cast<const uint2*>(a.vpool + base + (size_t)(16 * nt + t) * kPage + 4 * g);
     }
+    // keep the V loads ahead of the first product (the scheduler would sink
+    // them below the wait for K, costing a second round trip)
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Fold one page pair into the wavefront's state: m (running max of head l%16),
@@ -281,16 +303,99 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
         f4_t acc = o[nt];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= c[i];
-        const h8_t vb = as_h8(make_uint4(r.v[nt][0].x, r.v[nt][0].y, r.v[nt][1].x, r.v[nt][1].y));
+        const h8_t vb = as_h8(make_uint4(r.v[nt][0].x & r.vmask[0].x, r.v[nt][0].y & r.vmask[0].y,
+                                         r.v[nt][1].x & r.vmask[1].x, r.v[nt][1].y & r.vmask[1].y));
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, acc, 0, 0, 0);
         o[nt] = acc;
     }
 }
 
+
+// Run by the last split block of a (sequence, kv head) to finish: merges the
+// nsplit records of its G query heads and writes the fp16 output.  The
+// records were stored by other blocks with agent-scope stores, each complete
+// before its block counted itself, so they are read with agent-scope (sc1)
+// loads.  Wavefront w computes the weights exp(m_s - M) / L of heads
+// w, w + 4, ... with lane s holding split s (nsplit <= 64).  Thread t then
+// owns float4 column t % NC of O (NC = G * HD / 4) for the splits
+// s = t / NC (mod NG), NG = 256 / NC; it requests all of them at once
+// (16-byte buffer loads with the sc1 bit, split index clamped, weight zero
+// past nsplit), and the NG partial sums meet in LDS.
+template <int G, int HD>
+__device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b) {
+    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
+    constexpr int NC = G * HD / 4, NG = kAttnThreads / NC;
+    constexpr int KMAX = (kMaxSplits + NG - 1) / NG, U = KMAX < 32 ? KMAX : 32;
+    constexpr int kSc1 = 16;  // cache-policy bit of the agent-scope load
+    static_assert(kMaxSplits <= kWave, "one split per lane");
+    static_assert(NC * NG == kAttnThreads, "float4 columns tile the block");
+    __shared__ float wgt[G * kMaxSplits];
+    __shared__ float4 acc4[kAttnThreads];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
+    const int c = tid % NC, sg = tid / NC, h = 4 * c / HD;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(parts), 0, nsplit * REC * 4, 0x00020000);
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    // the first batch of O columns is requested together with the split
+    // maxima and denominators: one round trip for both
+    f4v v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int sc = min(sg + u * NG, nsplit - 1);
+        v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (sc * REC + 4 * c) * 4, 0, kSc1);
+    }
+    for (int hh = wave; hh < G; hh += kAttnWaves) {
+        const bool ok = lane < nsplit;
+        const int sl = ok ? lane : nsplit - 1;
+        const float m = ld_coh(parts + (size_t)sl * REC + MO + hh);
+        const float l = ld_coh(parts + (size_t)sl * REC + LO + hh);
+        const float M = wave_max(m);
+        const float e = (ok && M != -__builtin_inff()) ? __expf(m - M) : 0.0f;
+        const float L = wave_sum(e * l);
+        wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : 0.0f;
+    }
+    f4v acc = {0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    for (int s0 = sg;;) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int sx = s0 + u * NG;
+            const float w = wgt[h * kMaxSplits + min(sx, kMaxSplits - 1)] * (sx < nsplit ? 1.0f : 0.0f);
+            acc += w * v[u];
+        }
+        s0 += NG * U;
+        if (s0 >= nsplit) break;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int sc = min(s0 + u * NG, nsplit - 1);
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (sc * REC + 4 * c) * 4, 0, kSc1);
+        }
+    }
+    acc4[tid] = make_float4(acc.x, acc.y, acc.z, acc.w);
+    __syncthreads();
+    if (tid < NC) {
+        float4 r = acc4[tid];
+        for (int gi = 1; gi < NG; ++gi) {
+            const float4 q = acc4[gi * NC + tid];
+            r.x += q.x;
+            r.y += q.y;
+            r.z += q.z;
+            r.w += q.w;
+        }
+        uint16_t* out = a.out16 + ((size_t)b * a.hq + (size_t)kvh * G) * HD + 4 * tid;
+        *reinterpret_cast<uint2*>(out) = make_uint2((uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16),
+                                                    (uint32_t)f2h_bits(r.z) | ((uint32_t)f2h_bits(r.w) << 16));
+    }
+}
+
 // One split of one (kv head, sequence): 8 pages (more for very long
 // contexts) shared by the block's four wavefronts, two pages per wavefront
 // step.  PIPE: more than one page pair per wavefront, two pairs in flight.
+// The block stores its record, counts itself in a.counts for its (sequence,
+// kv head), and the last of the nsplit blocks merges the records
+// (merge_last) and resets the counter to zero for the next launch.
 template <int G, int HD, bool PIPE>
 __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
@@ -307,25 +412,27 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
     const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
                             ? a.block_table[(size_t)b * a.max_blocks + my_page]
                             : 0;
-    // q as the B operand (column = head t, k = 8g + j of each 32-dim step)
+    // q as the B operand (column = head t, k = 8g + j of each 32-dim step).
+    // Columns t >= G repeat head G - 1 (loads without a branch, so all of q
+    // is requested at once); their scores and output rows are never used.
     h8_t qh[HD / 32], ql[HD / 32];
+    {
+        const float* qsrc = a.q + ((size_t)b * a.hq + kvh * G + min(t, G - 1)) * HD + 8 * g;
+        float4 x[HD / 32][2];
 #pragma unroll
-    for (int s = 0; s < HD / 32; ++s) {
-        float x[8];
-        if (t < G) {
-            const float* src = a.q + ((size_t)b * a.hq + kvh * G + t) * HD + 32 * s + 8 * g;
-            const float4 x0 = *reinterpret_cast<const float4*>(src);
-            const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
-            x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
-            x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+        for (int s = 0; s < HD / 32; ++s) {
+            x[s][0] = *reinterpret_cast<const float4*>(qsrc + 32 * s);
+            x[s][1] = *reinterpret_cast<const float4*>(qsrc + 32 * s + 4);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            qh[s][j] = (_Float16)x[j];
-            ql[s][j] = (_Float16)(x[j] - (float)qh[s][j]);
+        for (int s = 0; s < HD / 32; ++s) {
+            const float v[8] = {x[s][0].x, x[s][0].y, x[s][0].z, x[s][0].w,
+                                x[s][1].x, x[s][1].y, x[s][1].z, x[s][1].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                qh[s][j] = (_Float16)v[j];
+                ql[s][j] = (_Float16)(v[j] - (float)qh[s][j]);
+            }
         }
     }
     const float scale = 1.0f / sqrtf((float)HD);
@@ -374,7 +481,19 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
         my[LO + t] = lsum;
     }
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    merge_waves_store<G, HD>(parts + (size_t)split * REC, lds);
+    merge_waves_store<G, HD, true>(parts + (size_t)split * REC, lds);
+    // every thread's record stores are complete before the block counts itself
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int last;
+    if (threadIdx.x == 0) {
+        unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
+        const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == (unsigned)nsplit - 1u;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (last) merge_last<G, HD>(a, nsplit, kvh, b);
 }
 
 // PIPE: more than one page pair per wavefront (pps > 8), two pairs in
@@ -710,8 +829,9 @@ size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
 int attn_max_ctx() { return kMaxSplits * kPagesPerSplitMax * kPage; }
 
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
+    if (!a.counts || !a.part) return hipErrorInvalidValue;
     const SplitPlan sp = plan_splits(a.max_ctx);
-    const dim3 grid(sp.nsplit, a.hkv, a.batch), mgrid(a.hq / a.hkv, a.hkv, a.batch);
+    const dim3 grid(sp.nsplit, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
     const bool pipe = sp.pps > kPagesPerSplitMin;
 #define NX_ATTN_CASE(GG, HH)                                                                      \
@@ -722,8 +842,6 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
         else                                                                                      \
             hipLaunchKernelGGL((k_attn_f16<GG, HH, false>), grid, dim3(kAttnThreads), 0, st, a,    \
                                sp.nsplit, sp.pps);                                                \
-        hipLaunchKernelGGL((k_attn_merge<GG, HH, false>), mgrid, dim3(HH), 0, st, a,              \
-                           sp.nsplit);                                                            \
         return hipGetLastError();                                                                 \
     }
     NX_ATTN_CASE(1, 64)

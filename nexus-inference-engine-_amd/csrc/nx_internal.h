@@ -22,6 +22,8 @@ struct nx_ctx {
     // workspace of the standalone attention entry points
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    unsigned* attn_counts = nullptr;  // split-completion counters (zero between launches)
+    size_t attn_count_words = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float c4[16], b4[15], c3[8], b3[7];
 };

@@ -77,8 +77,14 @@ struct AttnArgs {
     int max_ctx;                 // upper bound of ctx_lens (sizes the split grid)
     // workspace
     float* part;                 // partial (m, l, o) per split
+    // fp16 pages: split-completion counter of each (sequence, kv head) at
+    // counts[(b * hkv + kvh) * kAttnCountStride]; zero before a launch, and
+    // the launch leaves them at zero
+    unsigned* counts;
 };
+constexpr int kAttnCountStride = 64;  // counters 256 bytes apart
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
+inline size_t attn_count_words(int batch, int hkv) { return (size_t)batch * hkv * kAttnCountStride; }
 // Longest context the attention kernels accept.
 int attn_max_ctx();
 // Each enqueues two launches: the split kernel and the merge of its records.

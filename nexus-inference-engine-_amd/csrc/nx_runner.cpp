@@ -71,6 +71,7 @@ struct nx_model {
     uint16_t* moe_act = nullptr;
     float* moe_y = nullptr;
     float* attn_part = nullptr;
+    unsigned* attn_counts = nullptr;  // split-completion counters of the fp16 attention
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
     hipGraphExec_t exec = nullptr;        // one decode step
@@ -211,6 +212,7 @@ nx_status enqueue_step(nx_model* m) {
         at.max_blocks = m->max_blocks;
         at.max_ctx = c.max_seq;
         at.part = m->attn_part;
+        at.counts = m->attn_counts;
         NX_LAUNCH(m, c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st));
         // output projection + residual
         nx::GemvArgs o{};
@@ -465,6 +467,7 @@ nx_status create_impl(nx_model* m) {
         NX_TRY(dalloc(m, &m->moe_act, (size_t)B * c.top_k * m->Fp));
         NX_TRY(dalloc(m, &m->moe_y, (size_t)B * c.top_k * d));
     }
+    NX_TRY(dalloc(m, &m->attn_counts, nx::attn_count_words(B, c.n_kv_heads)));
     NX_TRY(dalloc(m, &m->attn_part,
                   nx::attn_workspace_bytes(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq) / 4 + 1));
     {
@@ -761,6 +764,7 @@ nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double
         at.max_blocks = m->max_blocks;
         at.max_ctx = c.max_seq;
         at.part = m->attn_part;
+        at.counts = m->attn_counts;
         return c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st);
     };
     for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
