@@ -320,8 +320,8 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
 // w, w + 4, ... with lane s holding split s (nsplit <= 64).  Thread t then
 // owns float4 column t % NC of O (NC = G * HD / 4) for the splits
 // s = t / NC (mod NG), NG = 256 / NC; it requests all of them at once
-// (16-byte buffer loads with the sc1 bit, split index clamped, weight zero
-// past nsplit), and the NG partial sums meet in LDS.
+// (16-byte buffer loads with the sc1 bit, skipped past nsplit, where the
+// weight is zero), and the NG partial sums meet in LDS.
 template <int G, int HD>
 __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
@@ -340,11 +340,15 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
     typedef float f4v __attribute__((ext_vector_type(4)));
     // the first batch of O columns is requested together with the split
     // maxima and denominators: one round trip for both
+    // (s is uniform within a wavefront, as NC is a multiple of 64 or NG
+    // divides the wavefront evenly; every load is consumed only after all
+    // of them are issued)
     f4v v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int sc = min(sg + u * NG, nsplit - 1);
-        v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (sc * REC + 4 * c) * 4, 0, kSc1);
+        const int sx = sg + u * NG;
+        v[u] = sx < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(rs, (sx * REC + 4 * c) * 4, 0, kSc1)
+                           : f4v{0.f, 0.f, 0.f, 0.f};
     }
     for (int hh = wave; hh < G; hh += kAttnWaves) {
         const bool ok = lane < nsplit;
@@ -369,8 +373,9 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
         if (s0 >= nsplit) break;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int sc = min(s0 + u * NG, nsplit - 1);
-            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (sc * REC + 4 * c) * 4, 0, kSc1);
+            const int sx = s0 + u * NG;
+            v[u] = sx < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(rs, (sx * REC + 4 * c) * 4, 0, kSc1)
+                               : f4v{0.f, 0.f, 0.f, 0.f};
         }
     }
     acc4[tid] = make_float4(acc.x, acc.y, acc.z, acc.w);

@@ -223,8 +223,33 @@ __global__ __launch_bounds__(256) void k_embed(unsigned long long* best, int32_t
     }
     __syncthreads();
     const int tok = tok_s;
-    for (int i = threadIdx.x; i < d; i += 256)
-        h[(size_t)b * d + i] = h2f_bits(embed[(size_t)tok * d + i]);
+    const uint16_t* src = embed + (size_t)tok * d;
+    float* dst = h + (size_t)b * d;
+    if ((d & 7) == 0) {
+        // 16-byte chunks, both of a thread's loads in flight together
+        // (one round trip for a 4096-wide row)
+        const int nch = d / 8;
+        for (int c0 = threadIdx.x; c0 < nch; c0 += 512) {
+            const int c1 = c0 + 256 < nch ? c0 + 256 : c0;
+            const uint4 v0 = reinterpret_cast<const uint4*>(src)[c0];
+            const uint4 v1 = reinterpret_cast<const uint4*>(src)[c1];
+            const uint32_t w[2][4] = {{v0.x, v0.y, v0.z, v0.w}, {v1.x, v1.y, v1.z, v1.w}};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int c = j ? c0 + 256 : c0;
+                if (c >= nch) break;
+                float4 lo, hi;
+                lo.x = h2f_bits((uint16_t)(w[j][0] & 0xFFFFu)); lo.y = h2f_bits((uint16_t)(w[j][0] >> 16));
+                lo.z = h2f_bits((uint16_t)(w[j][1] & 0xFFFFu)); lo.w = h2f_bits((uint16_t)(w[j][1] >> 16));
+                hi.x = h2f_bits((uint16_t)(w[j][2] & 0xFFFFu)); hi.y = h2f_bits((uint16_t)(w[j][2] >> 16));
+                hi.z = h2f_bits((uint16_t)(w[j][3] & 0xFFFFu)); hi.w = h2f_bits((uint16_t)(w[j][3] >> 16));
+                reinterpret_cast<float4*>(dst)[2 * c] = lo;
+                reinterpret_cast<float4*>(dst)[2 * c + 1] = hi;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < d; i += 256) dst[i] = h2f_bits(src[i]);
+    }
 }
 
 __global__ void k_finish_tokens(const unsigned long long* best, const int32_t* pos,
