@@ -25,7 +25,7 @@ namespace nx {
 
 namespace {
 
-constexpr int kAttnWaves = 4;
+constexpr int kAttnWaves = 8;
 constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kMaxSplits = 64;  // splits per (sequence, kv head)
 
@@ -137,36 +137,52 @@ __device__ inline float ld_coh(const float* p) {
 
 // Cross-wavefront merge of the block: lds holds one record per wavefront
 // (O[G][HD], M[G], L[G]); every wavefront has written its own before the
-// barrier.  The merged split record goes to `part` (COH: agent-scope stores).
+// barrier.  The rescale factors exp(m_w - M) are computed once per (wavefront,
+// head) by the first G * kAttnWaves lanes of wavefront 0 (max and sum over
+// groups of kAttnWaves lanes), then every thread sums its O elements over the
+// wavefronts.  The merged split record goes to `part` (COH: agent-scope
+// stores).
 template <int G, int HD, bool COH = false>
 __device__ inline void merge_waves_store(float* __restrict__ part, const float* lds) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
+    static_assert(G * kAttnWaves <= kWave, "one lane of wavefront 0 per (wavefront, head)");
+    __shared__ float fw[kAttnWaves * G];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * HD + G; idx += kAttnThreads) {
-        const bool is_o = idx < G * HD;
-        const int h = is_o ? idx / HD : idx - G * HD;
-        float M = -__builtin_inff();
+    const int t = threadIdx.x;
+    if (t < kWave) {
+        const bool act = t < G * kAttnWaves;
+        const int h = act ? t / kAttnWaves : 0, w = t % kAttnWaves;
+        const float m = act ? lds[w * REC + MO + h] : -__builtin_inff();
+        float M = m;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, lds[w * REC + MO + h]);
+        for (int o = 1; o < kAttnWaves; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, kWave));
+        const float f = (M == -__builtin_inff()) ? 0.0f : __expf(m - M);
+        float L = act ? f * lds[w * REC + LO + h] : 0.0f;
+#pragma unroll
+        for (int o = 1; o < kAttnWaves; o <<= 1) L += __shfl_xor(L, o, kWave);
+        if (act) {
+            fw[w * G + h] = f;
+            if (w == 0) {
+                if (COH) {
+                    st_coh(part + MO + h, M);
+                    st_coh(part + LO + h, L);
+                } else {
+                    part[MO + h] = M;
+                    part[LO + h] = L;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = t; idx < G * HD; idx += kAttnThreads) {
+        const int h = idx / HD;
         float acc = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) {
-            const float f = (M == -__builtin_inff()) ? 0.0f : __expf(lds[w * REC + MO + h] - M);
-            acc = fmaf(lds[w * REC + (is_o ? idx : LO + h)], f, acc);
-        }
-        if (COH) {
-            if (is_o) {
-                st_coh(part + idx, acc);
-            } else {
-                st_coh(part + MO + h, M);
-                st_coh(part + LO + h, acc);
-            }
-        } else if (is_o) {
+        for (int w = 0; w < kAttnWaves; ++w) acc = fmaf(lds[w * REC + idx], fw[w * G + h], acc);
+        if (COH)
+            st_coh(part + idx, acc);
+        else
             part[idx] = acc;
-        } else {
-            part[MO + h] = M;
-            part[LO + h] = acc;
-        }
     }
 }
 
@@ -326,7 +342,7 @@ template <int G, int HD>
 __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     constexpr int NC = G * HD / 4, NG = kAttnThreads / NC;
-    constexpr int KMAX = (kMaxSplits + NG - 1) / NG, U = KMAX < 32 ? KMAX : 32;
+    constexpr int KMAX = (kMaxSplits + NG - 1) / NG, U = KMAX < 16 ? KMAX : 16;
     constexpr int kSc1 = 16;  // cache-policy bit of the agent-scope load
     static_assert(kMaxSplits <= kWave, "one split per lane");
     static_assert(NC * NG == kAttnThreads, "float4 columns tile the block");
@@ -505,7 +521,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
 // flight; otherwise the single pair is loaded up front and the kernel fits
 // two blocks per CU.
 template <int G, int HD, bool PIPE>
-__global__ __launch_bounds__(kAttnThreads, PIPE ? 1 : 2) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
+__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
     attn_f16_run<G, HD, PIPE>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
