@@ -39,45 +39,334 @@ using namespace gv;
 
 // Batch 1 kernel: the whole grid runs one GEMV, one block of WPB
 // wavefronts per CU.
-template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB, bool XVEC>
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB, bool XVEC, bool XFIRST>
 __global__ __launch_bounds__(WPB * kWave, 1) void k_gemv_b1(GemvArgs a, RowSplit rs) {
-    gemv_b1_run<GPL, R, DEPTH, XLDS, XS, EPI, WPB, XVEC>(a, rs, blockIdx.x);
+    gemv_b1_run<GPL, R, DEPTH, XLDS, XS, EPI, WPB, XVEC, XFIRST>(a, rs, blockIdx.x);
 }
 
-// Batch 2..8: the weight tile is loaded once and applied to every row of x.
-template <int GPL, int R, int XS, int EPI>
-__global__ __launch_bounds__(kBlockThreads) void k_gemv_bn(GemvArgs a) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const int nw = gridDim.x * kWavesPerBlock;
-    float inv[8];
-    if (XS == X_RMSNORM) {
-        for (int b = 0; b < a.batch; ++b)
-            inv[b] = rms_inv<GPL>(a.h32 + (size_t)b * a.ldx, a.K, a.G, a.eps, lane);
+// ---------------------------------------------------------- batch 2..8 --
+// The weights of 16 rows meet the batch's x on the matrix cores
+// (v_mfma_f32_16x16x32_f16, one 32-element group per product):
+//   A (16 x 32): lane l holds row l%16, k = 8(l/16) .. +7 of the group: its 4
+//      code bytes, split into low and high nibbles, give the fp16 values
+//      (q - 8) in the k order (0 2 4 6 1 3 5 7); a byte joined with 0x64 is
+//      1024 + q, exact in fp16;
+//   B (32 x 16): lane l holds batch column l%16 with the same k order (x is
+//      staged in LDS in that order; columns past the batch are never stored);
+//   C (16 x 16 fp32): lane l holds column l%16, rows 4(l/16) .. +3.
+// Each product is a group sum (exact int4 x fp16 products, fp32 sums), which
+// is scaled by its row's group scale and accumulated in fp32, as in the
+// batch-1 kernel.  A block of 8 wavefronts takes whole 16-row tiles and splits
+// each 4096-wide K stage among its wavefronts (16 groups each); x is staged in
+// LDS per stage (K = 14336 takes four stages, one tile per block), the
+// wavefronts' partial tiles meet in LDS, and the tile's epilogue runs in
+// wavefront (tile % 8).  Every load before a wait is unconditional (clamped
+// rows, groups and stage entries), so the compiler's waits count exactly.
+typedef _Float16 mh8_t __attribute__((ext_vector_type(8)));
+typedef float mf4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaThreads = kMfmaWaves * kWave;
+constexpr int kMfmaCols = 8;                       // batch rows held in LDS
+constexpr int kMfmaKC = 4096;                      // K per stage
+constexpr int kMfmaGC = kMfmaKC / 32;              // groups per stage
+constexpr int kMfmaGW = kMfmaGC / kMfmaWaves;      // groups per wavefront per stage
+constexpr int kMfmaEPT = kMfmaGC * 4 * kMfmaCols / kMfmaThreads;  // stage entries per thread
+
+__device__ inline mh8_t codes_to_h8(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu, k64 = 0x64646464u;
+    const uint4 r = make_uint4(__builtin_amdgcn_perm(k64, lo, 0x04010400u), __builtin_amdgcn_perm(k64, lo, 0x04030402u),
+                               __builtin_amdgcn_perm(k64, hi, 0x04010400u), __builtin_amdgcn_perm(k64, hi, 0x04030402u));
+    return __builtin_bit_cast(mh8_t, r) - (_Float16)1032.0f;
+}
+
+// Eight consecutive fp16 inputs (as 4 dwords) in the k order (0 2 4 6 1 3 5 7).
+__device__ inline uint4 perm_x8(const uint32_t (&X)[4]) {
+    return make_uint4(__builtin_amdgcn_perm(X[1], X[0], 0x05040100u), __builtin_amdgcn_perm(X[3], X[2], 0x05040100u),
+                      __builtin_amdgcn_perm(X[1], X[0], 0x07060302u), __builtin_amdgcn_perm(X[3], X[2], 0x07060302u));
+}
+
+// Stage x[b][k0 .. k0 + 32 gc) of every batch row into LDS: entry
+// (g * 4 + q) * kMfmaCols + b holds x[b][k0 + 32g + 8q + (0 2 4 6 1 3 5 7)].
+// XVEC: K % 8 == 0 and 16-byte aligned rows, one 16-byte load per entry (X_F16)
+// or two (X_RMSNORM); all loads of a thread are issued before any is used.
+// X_RMSNORM needs inv[b] = 1 / sqrt(mean(h_b^2) + eps).
+// NORM (X_RMSNORM, K in one stage): inv is computed here from the staged
+// values (sums of squares per batch row over the thread's entries, reduced
+// through LDS in red), so the input costs one round trip.
+template <int XS, bool XVEC, bool NORM = false>
+__device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs, float* inv,
+                                    float (*red)[kMfmaCols] = nullptr) {
+    const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
+    if (XVEC) {
+        uint32_t X[kMfmaEPT][4];
+        float V[XS == X_RMSNORM ? kMfmaEPT : 1][8];
+#pragma unroll
+        for (int j = 0; j < kMfmaEPT; ++j) {
+            const int e = min(tid + j * kMfmaThreads, ne - 1);
+            const int b = min(e % kMfmaCols, nb - 1), q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
+            const int kb = min(k0 + 32 * g + 8 * q, K - 8);
+            if (XS == X_F16) {
+                const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + (size_t)b * a.ldx + kb);
+                X[j][0] = v.x; X[j][1] = v.y; X[j][2] = v.z; X[j][3] = v.w;
+            } else {
+                const float4* src = reinterpret_cast<const float4*>(a.h32 + (size_t)b * a.ldx + kb);
+                const float4 u = src[0], w = src[1];
+                V[j][0] = u.x; V[j][1] = u.y; V[j][2] = u.z; V[j][3] = u.w;
+                V[j][4] = w.x; V[j][5] = w.y; V[j][6] = w.z; V[j][7] = w.w;
+            }
+        }
+        if (XS == X_RMSNORM && NORM) {
+            // a thread's entries all belong to batch row tid % kMfmaCols
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kMfmaEPT; ++j) {
+                const int e = tid + j * kMfmaThreads;
+                const int kb = k0 + 32 * (e / (4 * kMfmaCols)) + 8 * ((e / kMfmaCols) & 3);
+                if (e < ne && kb < K)
+#pragma unroll
+                    for (int h = 0; h < 8; ++h) ss = fmaf(V[j][h], V[j][h], ss);
+            }
+            // lanes with the same tid % kMfmaCols: a stride-8 sum within the wavefront
+            ss += __shfl_xor(ss, 8, kWave);
+            ss += __shfl_xor(ss, 16, kWave);
+            ss += __shfl_xor(ss, 32, kWave);
+            const int lane = tid & (kWave - 1), wave = tid >> 6;
+            if (lane < kMfmaCols) red[wave][lane] = ss;
+            __syncthreads();
+            if (tid < kMfmaCols) {
+                float t = 0.0f;
+                for (int w = 0; w < kMfmaWaves; ++w) t += red[w][tid];
+                inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int j = 0; j < kMfmaEPT; ++j) {
+            const int e = tid + j * kMfmaThreads;
+            if (e >= ne) break;
+            const int b = e % kMfmaCols, q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
+            const int kb = k0 + 32 * g + 8 * q;
+            if (b >= nb) continue;
+            if (XS == X_RMSNORM) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const int k = kb + 2 * h;
+                    const float t0 = V[j][2 * h] * inv[b], t1 = V[j][2 * h + 1] * inv[b];
+                    const uint32_t lo = k < K ? f2h_bits(a.norm_w ? t0 * a.norm_w[k] : t0) : 0u;
+                    const uint32_t hi = k + 1 < K ? f2h_bits(a.norm_w ? t1 * a.norm_w[k + 1] : t1) : 0u;
+                    X[j][h] = lo | (hi << 16);
+                }
+            } else if (kb >= K) {
+                X[j][0] = X[j][1] = X[j][2] = X[j][3] = 0u;
+            }
+            xs[e] = perm_x8(X[j]);
+        }
+        return;
     }
-    float best_v[8];
-    int best_i[8];
-    for (int b = 0; b < 8; ++b) {
-        best_v[b] = -__builtin_inff();
-        best_i[b] = -1;
+    for (int e = tid; e < ne; e += kMfmaThreads) {
+        const int b = e % kMfmaCols, q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
+        if (b >= nb) continue;
+        const int kb = k0 + 32 * g + 8 * q;
+        uint32_t X[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int k = kb + 2 * h;
+            uint32_t lo = 0, hi = 0;
+            if (XS == X_F16) {
+                if (k < K) lo = a.x16[(size_t)b * a.ldx + k];
+                if (k + 1 < K) hi = a.x16[(size_t)b * a.ldx + k + 1];
+            } else {
+                if (k < K) lo = f2h_bits(a.h32[(size_t)b * a.ldx + k] * inv[b] * (a.norm_w ? a.norm_w[k] : 1.0f));
+                if (k + 1 < K)
+                    hi = f2h_bits(a.h32[(size_t)b * a.ldx + k + 1] * inv[b] * (a.norm_w ? a.norm_w[k + 1] : 1.0f));
+            }
+            X[h] = lo | (hi << 16);
+        }
+        xs[e] = perm_x8(X);
     }
-    for (int n0 = wid * R; n0 < a.N; n0 += nw * R) {
-        Tile<GPL, R> t;
-        load_tile<GPL, R>(t, a.W, a.S, a.G, a.N, n0, lane);
-        for (int b = 0; b < a.batch; ++b) {
-            XPairs<GPL> xp;
-            if (XS == X_F16)
-                load_x16<GPL>(xp, a.x16 + (size_t)b * a.ldx, a.K, a.G, lane);
-            else
-                load_x_norm<GPL>(xp, a.h32 + (size_t)b * a.ldx, a.norm_w, inv[b], a.K, a.G, lane);
-            float res[R];
-            tile_dot<GPL, R>(t, xp, res);
-            if (lane == 0) epilogue<EPI, R>(a, b, n0, a.N, res, best_v[b], best_i[b]);
+}
+
+// The product of one group is one MFMA with the batch's x as A (row = batch
+// row, k-quad l/16 of lane l) and the weight codes as B (column = weight row
+// l%16, same k-quad), so lane l's accumulators hold weight row l%16 for batch
+// rows 4(l/16)..+3 and every lane needs one scale per group.
+//
+// One wavefront's share (groups [gs, ge) of the stage starting at group
+// gbase) of a 16-row tile, requested without branches.  SALIGN: G % 4 == 0,
+// so the scales of 4 consecutive groups are one 8-byte load.
+struct MfmaRegs {
+    uint32_t code[kMfmaGW];
+    uint32_t sc[kMfmaGW / 2];  // fp16 scale pairs (groups 2u, 2u+1) of the lane's weight row
+};
+
+template <bool SALIGN>
+__device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs, int ge, MfmaRegs& r) {
+    const int lane = threadIdx.x & (kWave - 1), c = lane & 15, kq = lane >> 4;
+    const int G = a.G;
+    const int gl = ge - 1;  // last group of the stage (ge == stage groups when the wavefront has none)
+    const size_t row = (size_t)min(row0 + c, a.N - 1);
+    const uint16_t* srow = a.S + row * G + gbase;
+    if (SALIGN) {
+#pragma unroll
+        for (int u4 = 0; u4 < kMfmaGW / 4; ++u4) {
+            const uint2 v = *reinterpret_cast<const uint2*>(srow + min(gs + 4 * u4, gl & ~3));
+            r.sc[2 * u4] = v.x;
+            r.sc[2 * u4 + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int u2 = 0; u2 < kMfmaGW / 2; ++u2)
+            r.sc[u2] = (uint32_t)srow[min(gs + 2 * u2, gl)] | ((uint32_t)srow[min(gs + 2 * u2 + 1, gl)] << 16);
+    }
+    const uint8_t* wrow = a.W + row * G * 16 + 4 * kq;
+#pragma unroll
+    for (int u = 0; u < kMfmaGW; ++u)
+        r.code[u] = *reinterpret_cast<const uint32_t*>(wrow + (size_t)(gbase + min(gs + u, gl)) * 16);
+}
+
+// The A operands (x of the batch) of the wavefront's groups, from LDS.
+__device__ inline void mfma_load_x(const uint4* xs, int gs, int ge, uint4 (&xv)[kMfmaGW]) {
+    const int lane = threadIdx.x & (kWave - 1), c = lane & 15, kq = lane >> 4;
+    const int gl = ge - 1;
+#pragma unroll
+    for (int u = 0; u < kMfmaGW; ++u) xv[u] = xs[(min(gs + u, gl) * 4 + kq) * kMfmaCols + (c & (kMfmaCols - 1))];
+}
+
+// Group sums of the wavefront's share, scaled and accumulated into acc
+// (fully unrolled, so the register arrays stay in registers; groups past ge
+// repeat a valid group with weight zero).
+__device__ inline void mfma_compute(const MfmaRegs& r, const uint4 (&xv)[kMfmaGW], int gs, int ge, mf4_t& acc) {
+#pragma unroll
+    for (int u = 0; u < kMfmaGW; ++u) {
+        const float on = gs + u < ge ? 1.0f : 0.0f;
+        const mf4_t z = {0.f, 0.f, 0.f, 0.f};
+        const mf4_t cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8_t, xv[u]),
+                                                               codes_to_h8(r.code[u]), z, 0, 0, 0);
+        const uint32_t pr = r.sc[u >> 1];
+        const float sv = h2f_bits((uint16_t)((u & 1) ? (pr >> 16) : (pr & 0xFFFFu))) * on;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(cg[i], sv, acc[i]);
+    }
+}
+
+template <int XS, int EPI, bool XVEC, bool SALIGN>
+__global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int tpb) {
+    __shared__ __align__(16) uint4 xs[kMfmaGC * 4 * kMfmaCols];
+    __shared__ __align__(16) float part[2][kMfmaWaves * 16 * 16];  // [wave][weight row][batch row]
+    __shared__ float inv[kMfmaCols];
+    __shared__ float red[kMfmaWaves][kMfmaCols];
+    __shared__ unsigned long long bk[kMfmaThreads];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int c = lane & 15, kq = lane >> 4;
+    const int N = a.N, K = a.K;
+    const int ntile = (N + 15) / 16, t0 = blockIdx.x * tpb, nt = min(tpb, ntile - t0);
+    if (nt <= 0) return;
+    const int nstage = (K + kMfmaKC - 1) / kMfmaKC;
+    if (XS == X_RMSNORM && XVEC && nstage == 1) {
+        mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red);
+    } else if (XS == X_RMSNORM) {
+        // sum of h^2 per batch row over all of K
+        float ss[kMfmaCols];
+#pragma unroll
+        for (int b = 0; b < kMfmaCols; ++b) ss[b] = 0.0f;
+        for (int k = tid; k < K; k += kMfmaThreads)
+#pragma unroll
+            for (int b = 0; b < kMfmaCols; ++b)
+                if (b < a.batch) {
+                    const float v = a.h32[(size_t)b * a.ldx + k];
+                    ss[b] = fmaf(v, v, ss[b]);
+                }
+#pragma unroll
+        for (int b = 0; b < kMfmaCols; ++b) {
+            const float t = wave_sum(ss[b]);
+            if (lane == 0) red[wave][b] = t;
+        }
+        __syncthreads();
+        if (tid < kMfmaCols) {
+            float t = 0.0f;
+            for (int w = 0; w < kMfmaWaves; ++w) t += red[w][tid];
+            inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
+        }
+        __syncthreads();
+    }
+    if (nstage == 1 && !(XS == X_RMSNORM && XVEC)) mfma_stage_x<XS, XVEC>(a, 0, (K + 31) / 32, xs, inv);
+    if (nstage == 1) __syncthreads();  // x staged
+    float best_v = -__builtin_inff();
+    int best_i = -1;
+    const int gs = wave * kMfmaGW;
+    // tile t: every wavefront stores its partial sums in part[t & 1]; after
+    // the barrier wavefront t % 8 adds them, lane (c, kq) taking batch row c
+    // and weight rows 4kq..+3, and runs the epilogue
+    auto finish = [&](int t, int row0, const mf4_t& acc) {
+        *reinterpret_cast<float4*>(&part[t & 1][(wave * 16 + c) * 16 + 4 * kq]) =
+            make_float4(acc[0], acc[1], acc[2], acc[3]);
+        __syncthreads();
+        if (wave == (t & (kMfmaWaves - 1)) && c < a.batch) {
+            float res[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int w = 0; w < kMfmaWaves; ++w)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) res[i] += part[t & 1][(w * 16 + 4 * kq + i) * 16 + c];
+            epilogue<EPI, 4>(a, c, row0 + 4 * kq, N, res, best_v, best_i);
+        }
+    };
+    if (nstage == 1) {
+        // x stays in registers for all tiles, and the next tile's codes and
+        // scales are requested before the current tile is computed (two
+        // register sets used alternately; the request after the block's last
+        // tile re-reads that tile)
+        const int ge = min((K + 31) / 32, gs + kMfmaGW);
+        const int rlast = (t0 + nt - 1) * 16;
+        uint4 xv[kMfmaGW];
+        mfma_load_x(xs, gs, ge, xv);
+        MfmaRegs ra, rb;
+        mfma_load<SALIGN>(a, t0 * 16, 0, gs, ge, ra);
+        for (int t = 0; t < nt; t += 2) {
+            const int row0 = (t0 + t) * 16;
+            mfma_load<SALIGN>(a, min(row0 + 16, rlast), 0, gs, ge, rb);
+            mf4_t acc = {0.f, 0.f, 0.f, 0.f};
+            mfma_compute(ra, xv, gs, ge, acc);
+            finish(t, row0, acc);
+            if (t + 1 < nt) {
+                mfma_load<SALIGN>(a, min(row0 + 32, rlast), 0, gs, ge, ra);
+                mf4_t acc2 = {0.f, 0.f, 0.f, 0.f};
+                mfma_compute(rb, xv, gs, ge, acc2);
+                finish(t + 1, row0 + 16, acc2);
+            }
+        }
+    } else {
+        // K in several stages: x restaged per stage
+        for (int t = 0; t < nt; ++t) {
+            const int row0 = (t0 + t) * 16;
+            mf4_t acc = {0.f, 0.f, 0.f, 0.f};
+            for (int st = 0; st < nstage; ++st) {
+                const int k0 = st * kMfmaKC, gc = (min(kMfmaKC, K - k0) + 31) / 32;
+                const int ge = min(gc, gs + kMfmaGW);
+                MfmaRegs rg;
+                mfma_load<SALIGN>(a, row0, k0 / 32, gs, ge, rg);
+                __syncthreads();  // the previous stage's readers are done
+                mfma_stage_x<XS, XVEC>(a, k0, gc, xs, inv);
+                __syncthreads();
+                uint4 xv[kMfmaGW];
+                mfma_load_x(xs, gs, ge, xv);
+                mfma_compute(rg, xv, gs, ge, acc);
+            }
+            finish(t, row0, acc);
         }
     }
-    if (EPI == E_LOGITS && lane == 0)
-        for (int b = 0; b < a.batch; ++b)
-            if (best_i[b] >= 0) atomicMax(&a.best[b], pack_best(best_v[b], best_i[b]));
+    if (EPI == E_LOGITS) {
+        bk[tid] = (c < a.batch && best_i >= 0) ? pack_best(best_v, best_i) : 0ull;
+        __syncthreads();
+        if (tid < a.batch) {
+            unsigned long long m = 0ull;
+            for (int w = 0; w < kMfmaWaves; ++w)
+                for (int q = 0; q < 4; ++q) {
+                    const unsigned long long v = bk[w * kWave + q * 16 + tid];
+                    m = v > m ? v : m;
+                }
+            if (m) atomicMax(&a.best[tid], m);
+        }
+    }
 }
 
 // MoE expert GEMV with gathered tokens: blockIdx.y is the expert; its rows
@@ -158,7 +447,7 @@ hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
 
 // Batch 1: a persistent grid of WPB wavefronts per CU in one block each
 // (see b1_plan).
-template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB = kB1WavesPerCU>
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB = kB1WavesPerCU, bool XFIRST = false>
 hipError_t launch_b1(const GemvArgs& a, hipStream_t st) {
     RowSplit rs;
     const int blocks = b1_plan(a.N, R, WPB, rs, WPB);
@@ -166,21 +455,32 @@ hipError_t launch_b1(const GemvArgs& a, hipStream_t st) {
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (xvec)
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, true>), dim3(blocks), dim3(WPB * kWave),
-                           0, st, a, rs);
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, true, XFIRST>), dim3(blocks),
+                           dim3(WPB * kWave), 0, st, a, rs);
     else
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, false>), dim3(blocks),
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, false, XFIRST>), dim3(blocks),
                            dim3(WPB * kWave), 0, st, a, rs);
     return hipGetLastError();
 }
 
-// Batch 2..8.
-template <int GPL, int R, int XS, int EPI>
-hipError_t launch_bn(const GemvArgs& a, hipStream_t st) {
-    const int tiles = (a.N + R - 1) / R;
-    int blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (blocks > 1024) blocks = 1024;
-    hipLaunchKernelGGL((k_gemv_bn<GPL, R, XS, EPI>), dim3(blocks), dim3(kBlockThreads), 0, st, a);
+// Batch 2..8 on the matrix cores: whole tiles per block, one tile per block
+// when K takes more than one stage.
+template <int XS, int EPI>
+hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
+    const int ntile = (a.N + 15) / 16, cus = device_cus();
+    const int tpb = a.K <= kMfmaKC ? (ntile + cus - 1) / cus : 1;
+    const int blocks = (ntile + tpb - 1) / tpb;
+    const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
+    const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                      a.ldx % (XS == X_F16 ? 8 : 4) == 0;
+    const bool salign = a.G % 4 == 0;
+#define NX_MFMA(XV, SA) \
+    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA>), dim3(blocks), dim3(kMfmaThreads), 0, st, a, tpb)
+    if (xvec && salign) NX_MFMA(true, true);
+    else if (xvec) NX_MFMA(true, false);
+    else if (salign) NX_MFMA(false, true);
+    else NX_MFMA(false, false);
+#undef NX_MFMA
     return hipGetLastError();
 }
 
@@ -206,11 +506,8 @@ hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
         if constexpr (kPairs) return launch_b1<7, 2, 2, true, XS, EPI>(a, st);
         return launch_b1<7, 1, 1, false, XS, EPI>(a, st);
     }
-    if (gpl <= 1) return launch_bn<1, 4, XS, EPI>(a, st);
-    if (gpl <= 2) return launch_bn<2, 4, XS, EPI>(a, st);
-    if (gpl <= 4) return launch_bn<4, 2, XS, EPI>(a, st);
-    if (gpl <= 7) return launch_bn<7, 2, XS, EPI>(a, st);
-    return hipErrorInvalidValue;
+    if (gpl > 7) return hipErrorInvalidValue;
+    return launch_mfma<XS, EPI>(a, st);
 }
 
 }  // namespace

@@ -569,7 +569,7 @@ __device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, c
 // XLDS: x is read from LDS per group instead of being held in registers.
 // `block` is the block's index within the grid.
 template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB = kWavesPerBlock,
-          bool XVEC = false>
+          bool XVEC = false, bool XFIRST = false>
 __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int block) {
     constexpr int NT = WPB * kWave, CPT = (4 * GPL + WPB - 1) / WPB;
     __shared__ __align__(16) uint32_t sp[kWave * GPL * 16];
@@ -592,8 +592,10 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     // of behind the first tiles of all the other wavefronts.
     if (WPB > kWavesPerBlock) __syncthreads();
     Tile<GPL, R> t[DEPTH];
+    if (!XFIRST) {
 #pragma unroll
-    for (int j = 0; j < DEPTH; ++j) load_tile_u<GPL, R>(t[j], a.W, a.S, a.G, r0, r1, r0 + j * R, lane);
+        for (int j = 0; j < DEPTH; ++j) load_tile_u<GPL, R>(t[j], a.W, a.S, a.G, r0, r1, r0 + j * R, lane);
+    }
     float qc = 0.0f, qs = 0.0f;
     int qblk = 0;
     if (EPI == E_QKV && rope_pre) {
@@ -606,6 +608,12 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
         if (a.kpool) qblk = a.block_table[qp / kPage];
     }
     stage_finish<CPT, XS, NT>(a, sr, sp, s8, red);  // block barrier: every wavefront takes part
+    // XFIRST: the first tiles are requested only once x is staged (x then
+    // arrives without weight traffic queued beside it)
+    if (XFIRST) {
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) load_tile_u<GPL, R>(t[j], a.W, a.S, a.G, r0, r1, r0 + j * R, lane);
+    }
     float best_v = -__builtin_inff();
     int best_i = -1;
     if (nt > 0) {
