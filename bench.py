@@ -18,8 +18,12 @@ Also reported:
                 sample: one 8B-shaped layer at 4096 context plus 1/8 of the
                 lm_head rows, scaled to a token (32 layers + full lm_head).
 
+Other workloads: --model mixtral-8x7b (top-2 of 8 experts of 14336, vocab
+32000; the roofline kernel is then the routed gate/up expert GEMV), --kv tq
+(TurboQuant pages), --batch, --ctx.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
-                       [--kv fp16|tq --ctx C] [--no-cpu]
+                       [--model llama-8b|mixtral-8x7b] [--kv fp16|tq --ctx C] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -42,15 +46,18 @@ PEAK_HBM_GBS = 8000.0
 LLAMA8B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336,
                vocab=128256, n_experts=0, top_k=0, batch=1, kv_kind=0, rope_theta=500000.0,
                eps=1e-5, seed=0x5EED)
+# Mixtral-8x7B shape: 8 SwiGLU experts of 14336, router top-2, vocab 32000
+MIXTRAL = dict(LLAMA8B, vocab=32000, n_experts=8, top_k=2, rope_theta=1000000.0)
+MODELS = {"llama-8b": LLAMA8B, "mixtral-8x7b": MIXTRAL}
 
 
-def cpu_baseline(ctx_len: int, batch: int, kv_kind: int) -> dict:
+def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int) -> dict:
     """Time the oracle's decode step on a bounded sample and scale to a token."""
     import numpy as np
 
     import oracle
     vocab_frac = 8
-    cfg = dict(LLAMA8B, n_layers=1, vocab=LLAMA8B["vocab"] // vocab_frac, batch=batch, kv_kind=kv_kind,
+    cfg = dict(base, n_layers=1, vocab=base["vocab"] // vocab_frac, batch=batch, kv_kind=kv_kind,
                max_seq=((ctx_len + 16) // 16 + 1) * 16)
     m = oracle.Model(**cfg)
     m.fill_context(ctx_len, 4 if kv_kind else 0)
@@ -62,11 +69,12 @@ def cpu_baseline(ctx_len: int, batch: int, kv_kind: int) -> dict:
         tl += a
         th += b
     m.close()
-    t_token = LLAMA8B["n_layers"] * tl / reps + vocab_frac * th / reps
+    t_token = base["n_layers"] * tl / reps + vocab_frac * th / reps
+    shape = "8B-shaped" if base["n_experts"] == 0 else "Mixtral-shaped (top-2 of 8 experts)"
     return {"value": round(batch / t_token, 4), "unit": "tok/s",
             "cores": int(oracle.lib.nxo_num_threads()), "kind": "port",
-            "sample": (f"oracle decode step of one 8B-shaped layer at ctx {ctx_len} ({reps} reps) "
-                       f"+ lm_head rows 1/{vocab_frac}, scaled to 32 layers + full lm_head")}
+            "sample": (f"oracle decode step of one {shape} layer at ctx {ctx_len} ({reps} reps) "
+                       f"+ lm_head rows 1/{vocab_frac}, scaled to {base['n_layers']} layers + full lm_head")}
 
 
 def measured_traffic(kind: str):
@@ -114,6 +122,7 @@ def gemv_microbench(ctx, batch: int = 1, iters: int = 200) -> list:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--model", choices=sorted(MODELS), default="llama-8b")
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--batch", type=int, default=1)
@@ -144,9 +153,11 @@ def main() -> int:
 
     kv_kind = 1 if args.kv == "tq" else 0
     max_seq = ((args.ctx + args.warmup + args.steps + 16) // 16 + 1) * 16
-    cfg = dict(LLAMA8B, batch=args.batch, kv_kind=kv_kind, max_seq=max_seq)
+    base = MODELS[args.model]
+    moe = base["n_experts"] > 0
+    cfg = dict(base, batch=args.batch, kv_kind=kv_kind, max_seq=max_seq)
     ctx = nexus_amd.Context(0)
-    print(f"[bench] device {ctx.device_name()}; building 8B-shaped model "
+    print(f"[bench] device {ctx.device_name()}; building {args.model}-shaped model "
           f"(batch {args.batch}, ctx {args.ctx}, kv {args.kv})", file=sys.stderr, flush=True)
     model = nexus_amd.Model(ctx, **cfg)
     model.fill_context(args.ctx, 4 if kv_kind else 0)
@@ -154,7 +165,7 @@ def main() -> int:
         model.decode_untimed(1)
         ms, nb = (model.time_ffn_gemv if args.profile_kernel == "ffn" else model.time_attention)(64)
         print(json.dumps({"kernel": args.profile_kernel, "avg_us": round(ms * 1e3, 3),
-                          "bytes": int(nb), "launches": 64 + LLAMA8B["n_layers"]}))
+                          "bytes": int(nb), "launches": 64 + base["n_layers"]}))
         model.close()
         ctx.close()
         return 0
@@ -178,8 +189,17 @@ def main() -> int:
     ffn_gbs = ffn_bytes / (ffn_ms * 1e-3) / 1e9
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     model.close()
-    micro = gemv_microbench(ctx, args.batch)
+    micro = gemv_microbench(ctx, args.batch) if not moe else None
     ctx.close()
+    kv_name = "fp16" if kv_kind == 0 else "TurboQuant 3.5-bit"
+    if moe:
+        workload = (f"mixtral-8x7b-shape int4-g32 greedy decode (top-2 of 8 experts), batch {args.batch}, "
+                    f"ctx {args.ctx} {kv_name} paged KV")
+        ffn_kernel = "routed gate/up int4-g32 expert GEMV + SwiGLU (active experts x 28672 x 4096)"
+    else:
+        workload = (f"llama-3.1-8b-shape int4-g32 greedy decode, batch {args.batch}, "
+                    f"ctx {args.ctx} {kv_name} paged KV")
+        ffn_kernel = "fused RMSNorm + gate/up int4-g32 GEMV + SwiGLU (28672 x 4096)"
 
     line = {
         "metric": METRIC,
@@ -195,29 +215,30 @@ def main() -> int:
         "dtype": "int4-g32 x fp16 -> fp32 accumulate",
         "data": "synthetic (seeded device generator; random-init weights)",
         "config": {
-            "workload": (f"llama-3.1-8b-shape int4-g32 greedy decode, batch {args.batch}, "
-                         f"ctx {args.ctx} {'fp16' if kv_kind == 0 else 'TurboQuant 3.5-bit'} paged KV"),
-            "batch": args.batch, "ctx": args.ctx, "layers": 32, "d_model": 4096, "ffn": 14336,
-            "vocab": 128256, "parallelism": "none (1 GPU)",
+            "workload": workload,
+            "batch": args.batch, "ctx": args.ctx, "layers": base["n_layers"], "d_model": base["d_model"],
+            "ffn": base["ffn"], "vocab": base["vocab"], "experts": base["n_experts"], "top_k": base["top_k"],
+            "parallelism": "none (1 GPU)",
         },
         "hbm_GBps_end_to_end": round(step_bytes / (elapsed / args.steps) / 1e9, 1),
         "roofline": {
-            "kernel": "fused RMSNorm + gate/up int4-g32 GEMV + SwiGLU (28672 x 4096)",
+            "kernel": ffn_kernel,
             "bound": "hbm", "achieved": round(ffn_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic("ffn"),
+            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": None if moe else measured_traffic("ffn"),
             "avg_us": round(ffn_ms * 1e3, 3), "bytes": int(ffn_bytes),
         },
         "attention": {
             "kernel": "paged decode attention, one layer", "achieved": round(att_gbs, 1),
             "frac": round(att_gbs / PEAK_HBM_GBS, 4), "avg_us": round(att_ms * 1e3, 3),
-            "bytes": int(att_bytes), "traffic": measured_traffic("attention"),
+            "bytes": int(att_bytes), "traffic": measured_traffic("attention") if kv_kind == 0 else None,
         },
         "roofline_end_to_end_frac": round(step_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
-        "gemv_microbench": micro,
     }
+    if micro is not None:
+        line["gemv_microbench"] = micro
     if not args.no_cpu:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(args.ctx, args.batch, kv_kind)
+        line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -191,6 +191,7 @@ nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits_f32, nx_buf ids_i32, nx_b
  * W2_e(fp16(silu(W1_e x) * W3_e x)), e = ids[b][j].  Expert weights are
  * int4-g32: w13 [E][2F][d] with gate/up rows interleaved (row 2f = gate f,
  * 2f+1 = up f), s13 its scales; w2 [E][d][F], s2.  x fp16 [batch][d].
+ * batch <= 8; at most 8 slots may name one expert (NX_ERR_INVALID).
  * ComputeDispatch::batched_moe_ffn (compute_dispatch.h:84,
  * compute_dispatch.cpp:211-275; batched_expert_gemv.metal:47-160). */
 nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, nx_buf w2,
@@ -249,7 +250,10 @@ nx_status nx_model_step_bytes(nx_model* m, double* bytes);
  * RMSNorm + gate/up int4 GEMV + SwiGLU -- over `iters` back-to-back launches
  * on the model's buffers, launch i on layer i % n_layers (cold weights, as
  * in a decode step), timed with HIP events on the library stream; bytes =
- * its algorithmic bytes per launch. */
+ * its algorithmic bytes per launch.  MoE models: the routed gate/up expert
+ * GEMV + SwiGLU with the last decode step's routing of the last layer (at
+ * least one step must have run; NX_ERR_STATE otherwise), bytes = the active
+ * experts' gate/up weights plus the gathered inputs and outputs. */
 nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double* bytes);
 /* Same for standalone nx_gemv_int4_g32 launches of shape N x K, batch:
  * launch i uses weight copy i % ncopies (wq[], scales_f16[]), so with enough

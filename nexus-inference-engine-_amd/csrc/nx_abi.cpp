@@ -673,23 +673,45 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
     std::vector<int32_t> hid((size_t)batch * k);
     NX_HIP(ctx, hipMemcpyAsync(hid.data(), dptr<void>(ids), hid.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
     NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    std::vector<int32_t> count(E, 0), slots((size_t)E * batch * k, 0);
+    // routing plan (the layout moe_route writes): the experts that hold slots
+    // in ascending order, each with its slots b * k + j and their tokens b
+    std::vector<int32_t> count(E, 0);
     for (int b = 0; b < batch; ++b)
         for (int j = 0; j < k; ++j) {
             const int e = hid[(size_t)b * k + j];
             if (e < 0 || e >= E) return fail(ctx, NX_ERR_INVALID, "nx_moe_expert_ffn: expert id %d out of range", e);
-            slots[(size_t)e * batch * k + count[e]++] = b * k + j;
+            if (++count[e] > nx::kMoePlanMaxSlots)
+                return fail(ctx, NX_ERR_INVALID, "nx_moe_expert_ffn: more than %d slots on expert %d",
+                            nx::kMoePlanMaxSlots, e);
         }
-    // workspace: count[E] | slots[E*batch*k] | act16[batch*k][Fp] | y32[batch*k][d]
-    const size_t off_slots = (size_t)E * 4;
-    const size_t off_act = (off_slots + slots.size() * 4 + 255) / 256 * 256;
+    const int rows = nx::moe_plan_rows(E, batch, k);
+    std::vector<int32_t> plan((size_t)rows * nx::kMoePlanInts, 0);
+    int r = 0;
+    for (int e = 0; e < E; ++e) {
+        if (count[e] == 0) continue;
+        if (r == rows) return fail(ctx, NX_ERR_INVALID, "nx_moe_expert_ffn: more active experts than slots");
+        int32_t* pl = plan.data() + (size_t)r * nx::kMoePlanInts;
+        pl[0] = e;
+        int n = 0;
+        for (int b = 0; b < batch; ++b)
+            for (int j = 0; j < k; ++j)
+                if (hid[(size_t)b * k + j] == e) {
+                    pl[8 + n] = b * k + j;
+                    pl[16 + n] = b;
+                    ++n;
+                }
+        pl[1] = n;
+        ++r;
+    }
+    for (; r < rows; ++r) plan[(size_t)r * nx::kMoePlanInts] = -1;
+    // workspace: plan | act16[batch*k][Fp] | y32[batch*k][d]
+    const size_t off_act = (plan.size() * 4 + 255) / 256 * 256;
     const size_t off_y = (off_act + (size_t)batch * k * Fp * 2 + 255) / 256 * 256;
     const size_t total = off_y + (size_t)batch * k * d * 4;
     nx_status s = ensure_attn_ws(ctx, total);
     if (s != NX_OK) return s;
     char* ws = static_cast<char*>(ctx->attn_ws);
-    NX_HIP(ctx, hipMemcpyAsync(ws, count.data(), count.size() * 4, hipMemcpyHostToDevice, ctx->stream));
-    NX_HIP(ctx, hipMemcpyAsync(ws + off_slots, slots.data(), slots.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    NX_HIP(ctx, hipMemcpyAsync(ws, plan.data(), plan.size() * 4, hipMemcpyHostToDevice, ctx->stream));
     NX_HIP(ctx, hipMemsetAsync(ws + off_act, 0, (size_t)batch * k * Fp * 2, ctx->stream));
     nx::MoeFfnArgs a{};
     a.x16 = dptr<const uint16_t>(x);
@@ -703,8 +725,7 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
     a.E = E;
     a.k = k;
     a.batch = batch;
-    a.expert_count = reinterpret_cast<const int32_t*>(ws);
-    a.expert_slots = reinterpret_cast<const int32_t*>(ws + off_slots);
+    a.plan = reinterpret_cast<const int32_t*>(ws);
     a.weights = dptr<const float>(w);
     a.act16 = reinterpret_cast<uint16_t*>(ws + off_act);
     a.y32 = reinterpret_cast<float*>(ws + off_y);

@@ -530,6 +530,7 @@ __constant__ float c_tq_c4[16];
 __constant__ float c_tq_b4[15];
 __constant__ float c_tq_c3[8];
 __constant__ float c_tq_b3[7];
+__constant__ float c_tq_cb[24];  // c_tq_c4 then c_tq_c3
 
 // In-LDS FWHT of G vectors of 128 (canonical butterfly network).
 template <int G>
@@ -549,63 +550,85 @@ __device__ inline void lds_fwht(float* v) {
 
 constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
 
-// Raw codes of one page for one lane: 4 tokens x (8 codes of K and V, norms).
+// One page for one lane (c = l%16, tg = l/16): the codes of dims [8c, 8c+8)
+// of tokens 4tg .. 4tg+3, for K and V, and those tokens' norms.  Lanes c < 8
+// hold 8 4-bit codes in one dword of the 32-byte record; lanes c >= 8 hold 8
+// 3-bit codes, the 3 bytes at 3(c-8) of the 24-byte record, which span at
+// most two dwords (w0, w1; joined with alignbyte once they have arrived).
 struct TqRaw {
-    uint32_t k[4], v[4];
-    uint16_t kn[4], vn[4];
+    uint32_t k0[4], k1[4], v0[4], v1[4];
+    uint2 kn, vn;  // fp16 norms of the 4 tokens
 };
 
-__device__ inline uint32_t tq_codes8(const uint8_t* __restrict__ c4, const uint8_t* __restrict__ c3,
-                                     int c) {
-    if (c < 8) return *reinterpret_cast<const uint32_t*>(c4 + 4 * c);
-    const uint8_t* p = c3 + 3 * (c - 8);
-    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16);
-}
+// Lane constants of the code layout: where the lane's first dword of a
+// token's K and V codes lies (record base plus byte offset), distance to the
+// second dword, record stride, and the decode parameters (byte shift, code
+// width, codebook offset).  Computed once, so that a page's addresses are one
+// multiply-add per lane.
+struct TqLane {
+    const uint8_t *kb, *vb;
+    int d1, stride, shift, bits, cbo;
+    __device__ TqLane(const AttnArgs& a, int c) {
+        const bool b4 = c < 8;
+        const int j = c - 8;
+        const int off = b4 ? 4 * c : 4 * ((3 * j) >> 2);
+        kb = (b4 ? a.kc4 : a.kc3) + off;
+        vb = (b4 ? a.vc4 : a.vc3) + off;
+        d1 = b4 ? 0 : 4 * (((3 * j + 2) >> 2) - ((3 * j) >> 2));
+        stride = b4 ? 32 : 24;
+        shift = b4 ? 0 : (3 * j) & 3;
+        bits = b4 ? 4 : 3;
+        cbo = b4 ? 0 : 16;
+    }
+};
 
-__device__ inline void load_page_tq(TqRaw& r, const AttnArgs& a, int blk, int kvh, int p, int ctx,
-                                    int tg, int c) {
-    const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage;
+// Every load is issued unconditionally (see load_pair): blk must be a valid
+// block; tokens past the context are masked when the page is processed.
+__device__ inline void load_page_tq(TqRaw& r, const AttnArgs& a, const TqLane& ln, int blk, int kvh,
+                                    int tg) {
+    const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage + 4 * tg;
+    const size_t cofs = rec * (size_t)ln.stride;
+    const uint8_t* kb = ln.kb + cofs;
+    const uint8_t* vb = ln.vb + cofs;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int t = tg + 4 * j;
-        if (p * kPage + t < ctx) {
-            r.k[j] = tq_codes8(a.kc4 + (rec + t) * 32, a.kc3 + (rec + t) * 24, c);
-            r.v[j] = tq_codes8(a.vc4 + (rec + t) * 32, a.vc3 + (rec + t) * 24, c);
-            r.kn[j] = a.kn[rec + t];
-            r.vn[j] = a.vn[rec + t];
-        } else {
-            r.k[j] = r.v[j] = 0u;
-            r.kn[j] = r.vn[j] = 0;
-        }
+        r.k0[j] = *reinterpret_cast<const uint32_t*>(kb + j * ln.stride);
+        r.k1[j] = *reinterpret_cast<const uint32_t*>(kb + j * ln.stride + ln.d1);
+        r.v0[j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride);
+        r.v1[j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride + ln.d1);
     }
+    r.kn = *reinterpret_cast<const uint2*>(a.kn + rec);
+    r.vn = *reinterpret_cast<const uint2*>(a.vn + rec);
 }
 
-// Codebook values of the 8 codes in w (4-bit lanes for c < 8, 3-bit otherwise).
-__device__ inline void tq_lookup8(uint32_t w, int c, const float* cb, float (&out)[8]) {
-    if (c < 8) {
+// Codebook values of the lane's 8 codes (cb: 16 4-bit levels, then 8 3-bit).
+__device__ inline void tq_lookup8(uint32_t w0, uint32_t w1, const TqLane& ln, const float* cb,
+                                  float (&out)[8]) {
+    const uint32_t w = __builtin_amdgcn_alignbyte(w1, w0, ln.shift);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = cb[(w >> (4 * i)) & 15u];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = cb[16 + ((w >> (3 * i)) & 7u)];
-    }
+    for (int i = 0; i < 8; ++i) out[i] = cb[ln.cbo + __builtin_amdgcn_ubfe(w, ln.bits * i, ln.bits)];
 }
 
+// n = valid tokens of the page (0..16).
 template <int G>
 __device__ inline void process_page_tq(State<G, 8>& st, const TqRaw& r, const float (&q)[G][8],
-                                       float scale, int p, int ctx, int tg, int c, const float* cb) {
+                                       float scale, int n, int tg, const TqLane& ln, const float* cb) {
     float vf[4][8];
     float sc[4][G];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const bool valid = p * kPage + tg + 4 * j < ctx;
+        const bool valid = 4 * tg + j < n;
+        const uint32_t nw = j < 2 ? r.kn.x : r.kn.y, vw = j < 2 ? r.vn.x : r.vn.y;
+        const uint32_t sh = 16 * (j & 1);
+        // the V norm of a token past the context is cleared (its bits may be
+        // anything), so its zero probability meets a finite value
+        const float vn = h2f_bits((uint16_t)((vw >> sh) & (valid ? 0xFFFFu : 0u)));
+        const float kn = h2f_bits((uint16_t)(nw >> sh));
         float kf[8];
-        tq_lookup8(r.k[j], c, cb, kf);
-        tq_lookup8(r.v[j], c, cb, vf[j]);
-        const float vn = h2f_bits(r.vn[j]);
+        tq_lookup8(r.k0[j], r.k1[j], ln, cb, kf);
+        tq_lookup8(r.v0[j], r.v1[j], ln, cb, vf[j]);
 #pragma unroll
         for (int d = 0; d < 8; ++d) vf[j][d] *= vn;
-        const float kn = h2f_bits(r.kn[j]);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             float dot = 0.0f;
@@ -613,10 +636,6 @@ __device__ inline void process_page_tq(State<G, 8>& st, const TqRaw& r, const fl
             for (int d = 0; d < 8; ++d) dot = fmaf(q[h][d], kf[d], dot);
             dot = row16_sum(dot) * kn * scale;
             sc[j][h] = valid ? dot : -__builtin_inff();
-        }
-        if (!valid) {
-#pragma unroll
-            for (int d = 0; d < 8; ++d) vf[j][d] = 0.0f;
         }
     }
     state_update(st, sc, vf);
@@ -626,13 +645,13 @@ template <int G>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
     constexpr int HD = 128, DPL = 8, REC = rec_floats(G, HD);
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, tg = lane >> 4;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
     __shared__ float qrot[G * HD];
     __shared__ float cb[24];
 
-    // context length and block-table entries first (see k_attn_f16)
+    // context length and block-table entries first (see attn_f16_run)
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
@@ -640,10 +659,35 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
     const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
                             ? a.block_table[(size_t)b * a.max_blocks + my_page]
                             : 0;
-    if (threadIdx.x < 16) cb[threadIdx.x] = c_tq_c4[threadIdx.x];
-    else if (threadIdx.x < 24) cb[threadIdx.x] = c_tq_c3[threadIdx.x - 16];
-    for (int idx = threadIdx.x; idx < G * HD; idx += kAttnThreads)
-        qrot[idx] = a.ksign[idx % HD] * a.q[((size_t)b * a.hq + kvh * G) * HD + idx];
+    const int npages = (ctx + kPage - 1) / kPage;
+    const int p1 = min(p0 + pps, npages);
+    const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
+    // page i of this wavefront; pages past npw re-read the last one (or the
+    // entry of lane 0, a valid block, when there is none) with no valid token
+    auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, max(npw - 1, 0))); };
+    auto valid_of = [&](int i) { return i < npw ? min(ctx - (p0 + wave + kAttnWaves * i) * kPage, kPage) : 0; };
+    const TqLane ln(a, c);
+    // q, the K signs and the codebook, one clamped load per value and thread,
+    // then the first two pages: every load is in flight before q is rotated
+    constexpr int QPT = (G * HD + kAttnThreads - 1) / kAttnThreads;
+    float qv[QPT], sv[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int idx = min((int)threadIdx.x + u * kAttnThreads, G * HD - 1);
+        qv[u] = a.q[((size_t)b * a.hq + kvh * G) * HD + idx];
+        sv[u] = a.ksign[idx % HD];
+    }
+    const float cbv = c_tq_cb[min((int)threadIdx.x, 23)];
+    TqRaw a0, a1, b0, b1;
+    load_page_tq(a0, a, ln, blk_of(0), kvh, tg);
+    load_page_tq(a1, a, ln, blk_of(1), kvh, tg);
+
+    if (threadIdx.x < 24) cb[threadIdx.x] = cbv;
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const int idx = threadIdx.x + u * kAttnThreads;
+        if (idx < G * HD) qrot[idx] = sv[u] * qv[u];
+    }
     lds_fwht<G>(qrot);
 
     const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
@@ -655,27 +699,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
 
     State<G, DPL> st;
     state_init(st);
-    const int npages = (ctx + kPage - 1) / kPage;
-    const int p1 = min(p0 + pps, npages);
-    const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
-#define NX_PAGE(i) (p0 + wave + kAttnWaves * (i))
-#define NX_LOAD(r, i) load_page_tq(r, a, __builtin_amdgcn_readlane(bt_lane, (i)), kvh, NX_PAGE(i), ctx, tg, c)
-    TqRaw a0, a1, b0, b1;
-    if (npw > 0) NX_LOAD(a0, 0);
-    if (npw > 1) NX_LOAD(a1, 1);
+    // two pairs of pages in flight; both pairs are requested on every pass
+    // (past the last page they re-read it), and only the processing of a
+    // pair with no page is skipped, a branch with no load in it
     for (int i = 0; i < npw; i += 4) {
-        if (i + 2 < npw) NX_LOAD(b0, i + 2);
-        if (i + 3 < npw) NX_LOAD(b1, i + 3);
-        process_page_tq<G>(st, a0, q, scale, NX_PAGE(i), ctx, tg, c, cb);
-        if (i + 1 < npw) process_page_tq<G>(st, a1, q, scale, NX_PAGE(i + 1), ctx, tg, c, cb);
-        if (i + 2 >= npw) break;
-        if (i + 4 < npw) NX_LOAD(a0, i + 4);
-        if (i + 5 < npw) NX_LOAD(a1, i + 5);
-        process_page_tq<G>(st, b0, q, scale, NX_PAGE(i + 2), ctx, tg, c, cb);
-        if (i + 3 < npw) process_page_tq<G>(st, b1, q, scale, NX_PAGE(i + 3), ctx, tg, c, cb);
+        load_page_tq(b0, a, ln, blk_of(i + 2), kvh, tg);
+        load_page_tq(b1, a, ln, blk_of(i + 3), kvh, tg);
+        process_page_tq<G>(st, a0, q, scale, valid_of(i), tg, ln, cb);
+        if (i + 1 < npw) process_page_tq<G>(st, a1, q, scale, valid_of(i + 1), tg, ln, cb);
+        load_page_tq(a0, a, ln, blk_of(i + 4), kvh, tg);
+        load_page_tq(a1, a, ln, blk_of(i + 5), kvh, tg);
+        if (i + 2 < npw) process_page_tq<G>(st, b0, q, scale, valid_of(i + 2), tg, ln, cb);
+        if (i + 3 < npw) process_page_tq<G>(st, b1, q, scale, valid_of(i + 3), tg, ln, cb);
     }
-#undef NX_LOAD
-#undef NX_PAGE
     state_merge_rows(st);
 
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
@@ -903,6 +939,8 @@ void tq_set_codebooks(const float* c4, const float* b4, const float* c3, const f
     (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_b4), b4, sizeof(float) * 15);
     (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_c3), c3, sizeof(float) * 8);
     (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_b3), b3, sizeof(float) * 7);
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_cb), c4, sizeof(float) * 16);
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(c_tq_cb), c3, sizeof(float) * 8, sizeof(float) * 16);
 }
 
 hipError_t tq_encode_launch(const float* x, int nvec, const float* signs, const float* b4,

@@ -39,9 +39,24 @@ using namespace gv;
 
 // Batch 1 kernel: the whole grid runs one GEMV, one block of WPB
 // wavefronts per CU.
-template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB, bool XVEC, bool XFIRST>
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB, bool XVEC, bool XFIRST, bool MOE = false>
 __global__ __launch_bounds__(WPB * kWave, 1) void k_gemv_b1(GemvArgs a, RowSplit rs) {
-    gemv_b1_run<GPL, R, DEPTH, XLDS, XS, EPI, WPB, XVEC, XFIRST>(a, rs, blockIdx.x);
+    if constexpr (MOE) {
+        // routed expert of grid row y, one token slot (batch 1)
+        const int32_t* pl = a.moe_plan + blockIdx.y * kMoePlanInts;
+        const int e = pl[0];
+        if (e < 0) return;
+        const int slot = pl[8], xr = a.moe_xslot ? slot : pl[16];
+        GemvArgs m = a;
+        m.W += (size_t)e * a.moe_wstride;
+        m.S += (size_t)e * a.moe_sstride;
+        m.x16 += (size_t)xr * a.ldx;
+        m.act16 += (size_t)slot * a.lda;
+        m.y32 += (size_t)slot * a.ldy;
+        gemv_b1_run<GPL, R, DEPTH, XLDS, XS, EPI, WPB, XVEC, XFIRST>(m, rs, blockIdx.x);
+    } else {
+        gemv_b1_run<GPL, R, DEPTH, XLDS, XS, EPI, WPB, XVEC, XFIRST>(a, rs, blockIdx.x);
+    }
 }
 
 // ---------------------------------------------------------- batch 2..8 --
@@ -96,7 +111,9 @@ __device__ inline uint4 perm_x8(const uint32_t (&X)[4]) {
 // through LDS in red), so the input costs one round trip.
 template <int XS, bool XVEC, bool NORM = false>
 __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs, float* inv,
-                                    float (*red)[kMfmaCols] = nullptr) {
+                                    float (*red)[kMfmaCols] = nullptr, int xrow = -1) {
+    // xrow >= 0: the x row of this thread's batch row (routed experts gather
+    // their tokens); a thread's entries all belong to batch row tid % 8
     const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
     if (XVEC) {
         uint32_t X[kMfmaEPT][4];
@@ -106,11 +123,12 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
             const int e = min(tid + j * kMfmaThreads, ne - 1);
             const int b = min(e % kMfmaCols, nb - 1), q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
             const int kb = min(k0 + 32 * g + 8 * q, K - 8);
+            const size_t xo = (size_t)(xrow >= 0 ? xrow : b) * a.ldx + kb;
             if (XS == X_F16) {
-                const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + (size_t)b * a.ldx + kb);
+                const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + xo);
                 X[j][0] = v.x; X[j][1] = v.y; X[j][2] = v.z; X[j][3] = v.w;
             } else {
-                const float4* src = reinterpret_cast<const float4*>(a.h32 + (size_t)b * a.ldx + kb);
+                const float4* src = reinterpret_cast<const float4*>(a.h32 + xo);
                 const float4 u = src[0], w = src[1];
                 V[j][0] = u.x; V[j][1] = u.y; V[j][2] = u.z; V[j][3] = u.w;
                 V[j][4] = w.x; V[j][5] = w.y; V[j][6] = w.z; V[j][7] = w.w;
@@ -168,18 +186,19 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
         const int b = e % kMfmaCols, q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
         if (b >= nb) continue;
         const int kb = k0 + 32 * g + 8 * q;
+        const size_t xo = (size_t)(xrow >= 0 ? xrow : b) * a.ldx;
         uint32_t X[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
             const int k = kb + 2 * h;
             uint32_t lo = 0, hi = 0;
             if (XS == X_F16) {
-                if (k < K) lo = a.x16[(size_t)b * a.ldx + k];
-                if (k + 1 < K) hi = a.x16[(size_t)b * a.ldx + k + 1];
+                if (k < K) lo = a.x16[xo + k];
+                if (k + 1 < K) hi = a.x16[xo + k + 1];
             } else {
-                if (k < K) lo = f2h_bits(a.h32[(size_t)b * a.ldx + k] * inv[b] * (a.norm_w ? a.norm_w[k] : 1.0f));
+                if (k < K) lo = f2h_bits(a.h32[xo + k] * inv[b] * (a.norm_w ? a.norm_w[k] : 1.0f));
                 if (k + 1 < K)
-                    hi = f2h_bits(a.h32[(size_t)b * a.ldx + k + 1] * inv[b] * (a.norm_w ? a.norm_w[k + 1] : 1.0f));
+                    hi = f2h_bits(a.h32[xo + k + 1] * inv[b] * (a.norm_w ? a.norm_w[k + 1] : 1.0f));
             }
             X[h] = lo | (hi << 16);
         }
@@ -250,8 +269,8 @@ __device__ inline void mfma_compute(const MfmaRegs& r, const uint4 (&xv)[kMfmaGW
     }
 }
 
-template <int XS, int EPI, bool XVEC, bool SALIGN>
-__global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int tpb) {
+template <int XS, int EPI, bool XVEC, bool SALIGN, bool MOE = false>
+__global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, int tpb) {
     __shared__ __align__(16) uint4 xs[kMfmaGC * 4 * kMfmaCols];
     __shared__ __align__(16) float part[2][kMfmaWaves * 16 * 16];  // [wave][weight row][batch row]
     __shared__ float inv[kMfmaCols];
@@ -259,12 +278,27 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int t
     __shared__ unsigned long long bk[kMfmaThreads];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
-    const int N = a.N, K = a.K;
+    const int N = args.N, K = args.K;
     const int ntile = (N + 15) / 16, t0 = blockIdx.x * tpb, nt = min(tpb, ntile - t0);
     if (nt <= 0) return;
+    static_assert(!MOE || XS == X_F16, "routed experts take fp16 x");
+    GemvArgs a = args;
+    // routed experts: grid row y's expert and its token slots; x row of this
+    // thread's batch row, output row of lane column c
+    int xrow = -1, yrow = c;
+    if constexpr (MOE) {
+        const int32_t* pl = args.moe_plan + blockIdx.y * kMoePlanInts;
+        const int e = pl[0];
+        if (e < 0) return;
+        a.batch = pl[1];
+        a.W += (size_t)e * args.moe_wstride;
+        a.S += (size_t)e * args.moe_sstride;
+        xrow = pl[(args.moe_xslot ? 8 : 16) + min(tid % kMfmaCols, a.batch - 1)];
+        yrow = pl[8 + min(c, kMoePlanMaxSlots - 1)];
+    }
     const int nstage = (K + kMfmaKC - 1) / kMfmaKC;
     if (XS == X_RMSNORM && XVEC && nstage == 1) {
-        mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red);
+        mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red, xrow);
     } else if (XS == X_RMSNORM) {
         // sum of h^2 per batch row over all of K
         float ss[kMfmaCols];
@@ -290,7 +324,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int t
         }
         __syncthreads();
     }
-    if (nstage == 1 && !(XS == X_RMSNORM && XVEC)) mfma_stage_x<XS, XVEC>(a, 0, (K + 31) / 32, xs, inv);
+    if (nstage == 1 && !(XS == X_RMSNORM && XVEC)) mfma_stage_x<XS, XVEC>(a, 0, (K + 31) / 32, xs, inv, nullptr, xrow);
     if (nstage == 1) __syncthreads();  // x staged
     float best_v = -__builtin_inff();
     int best_i = -1;
@@ -307,7 +341,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int t
             for (int w = 0; w < kMfmaWaves; ++w)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) res[i] += part[t & 1][(w * 16 + 4 * kq + i) * 16 + c];
-            epilogue<EPI, 4>(a, c, row0 + 4 * kq, N, res, best_v, best_i);
+            epilogue<EPI, 4>(a, yrow, row0 + 4 * kq, N, res, best_v, best_i);
         }
     };
     if (nstage == 1) {
@@ -345,7 +379,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int t
                 MfmaRegs rg;
                 mfma_load<SALIGN>(a, row0, k0 / 32, gs, ge, rg);
                 __syncthreads();  // the previous stage's readers are done
-                mfma_stage_x<XS, XVEC>(a, k0, gc, xs, inv);
+                mfma_stage_x<XS, XVEC>(a, k0, gc, xs, inv, nullptr, xrow);
                 __syncthreads();
                 uint4 xv[kMfmaGW];
                 mfma_load_x(xs, gs, ge, xv);
@@ -369,113 +403,41 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs a, int t
     }
 }
 
-// MoE expert GEMV with gathered tokens: blockIdx.y is the expert; its rows
-// are applied to every token slot routed to it (expert_slots), so each
-// active expert's weights are read once per step whatever the batch.
-//   GATEUP: rows (2f, 2f+1) = (gate f, up f) of w13[e]; x = x16 of the slot's
-//           sequence; act16[slot][f] = fp16(silu(g) * u).
-//   down:   rows of w2[e]; x = act16[slot]; y32[slot][n] = y.
-template <int GPL, int R, bool GATEUP>
-__global__ __launch_bounds__(kBlockThreads) void k_moe_gemv(MoeFfnArgs m) {
-    const int e = blockIdx.y;
-    const int ntok = m.expert_count[e];
-    if (ntok == 0) return;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wid = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    const int nw = gridDim.x * kWavesPerBlock;
-    const int Fp = (m.F + 31) / 32 * 32;
-    const int N = GATEUP ? 2 * m.F : m.d;
-    const int K = GATEUP ? m.d : m.F;
-    const int G = (K + 31) / 32;
-    const uint8_t* W = (GATEUP ? m.w13 : m.w2) + (size_t)e * N * G * 16;
-    const uint16_t* S = (GATEUP ? m.s13 : m.s2) + (size_t)e * N * G;
-    const int32_t* slots = m.expert_slots + (size_t)e * m.batch * m.k;
-    for (int n0 = wid * R; n0 < N; n0 += nw * R) {
-        Tile<GPL, R> t;
-        load_tile<GPL, R>(t, W, S, G, N, n0, lane);
-        for (int i = 0; i < ntok; ++i) {
-            const int slot = slots[i];
-            XPairs<GPL> xp;
-            if (GATEUP)
-                load_x16<GPL>(xp, m.x16 + (size_t)(slot / m.k) * m.ldx, K, G, lane);
-            else
-                load_x16<GPL>(xp, m.act16 + (size_t)slot * Fp, K, G, lane);
-            float res[R];
-            tile_dot<GPL, R>(t, xp, res);
-            if (lane == 0) {
-                if (GATEUP) {
-#pragma unroll
-                    for (int r = 0; r < R; r += 2) {
-                        const int row = n0 + r;
-                        if (row >= N) break;
-                        const float g = res[r], u = res[r + 1];
-                        m.act16[(size_t)slot * Fp + (row >> 1)] = f2h_bits(g / (1.0f + expf(-g)) * u);
-                    }
-                } else {
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        if (n0 + r < N) m.y32[(size_t)slot * m.d + n0 + r] = res[r];
-                }
-            }
-        }
-    }
-}
-
-template <bool GATEUP>
-hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
-    const int N = GATEUP ? 2 * m.F : m.d;
-    const int K = GATEUP ? m.d : m.F;
-    const int G = (K + 31) / 32;
-    const int gpl = (G + kWave - 1) / kWave;
-    auto blocks_for = [&](int R) {
-        int b = ((N + R - 1) / R + kWavesPerBlock - 1) / kWavesPerBlock;
-        return b > 512 ? 512 : b;
-    };
-    if (gpl <= 1) {
-        hipLaunchKernelGGL((k_moe_gemv<1, 4, GATEUP>), dim3(blocks_for(4), m.E), dim3(kBlockThreads), 0, st, m);
-    } else if (gpl <= 2) {
-        hipLaunchKernelGGL((k_moe_gemv<2, 4, GATEUP>), dim3(blocks_for(4), m.E), dim3(kBlockThreads), 0, st, m);
-    } else if (gpl <= 4) {
-        hipLaunchKernelGGL((k_moe_gemv<4, 2, GATEUP>), dim3(blocks_for(2), m.E), dim3(kBlockThreads), 0, st, m);
-    } else if (gpl <= 7) {
-        hipLaunchKernelGGL((k_moe_gemv<7, 2, GATEUP>), dim3(blocks_for(2), m.E), dim3(kBlockThreads), 0, st, m);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 // Batch 1: a persistent grid of WPB wavefronts per CU in one block each
 // (see b1_plan).
-template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB = kB1WavesPerCU, bool XFIRST = false>
-hipError_t launch_b1(const GemvArgs& a, hipStream_t st) {
+// MOE: ny grid rows of routed experts share the CUs.
+template <int GPL, int R, int DEPTH, bool XLDS, int XS, int EPI, int WPB = kB1WavesPerCU, bool XFIRST = false,
+          bool MOE = false>
+hipError_t launch_b1(const GemvArgs& a, hipStream_t st, int ny = 1) {
     RowSplit rs;
-    const int blocks = b1_plan(a.N, R, WPB, rs, WPB);
+    const int blocks = b1_plan(a.N, R, WPB, rs, WPB, ny);
     // the branch-free input loads need whole 8-element chunks on 16 bytes
+    // (for routed experts, every row of x as well)
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
-    const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (!MOE || a.ldx % 8 == 0);
     if (xvec)
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, true, XFIRST>), dim3(blocks),
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, true, XFIRST, MOE>), dim3(blocks, ny),
                            dim3(WPB * kWave), 0, st, a, rs);
     else
-        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, false, XFIRST>), dim3(blocks),
+        hipLaunchKernelGGL((k_gemv_b1<GPL, R, DEPTH, XLDS, XS, EPI, WPB, false, XFIRST, MOE>), dim3(blocks, ny),
                            dim3(WPB * kWave), 0, st, a, rs);
     return hipGetLastError();
 }
 
 // Batch 2..8 on the matrix cores: whole tiles per block, one tile per block
 // when K takes more than one stage.
-template <int XS, int EPI>
-hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
+// MOE: ny grid rows of routed experts share the CUs.
+template <int XS, int EPI, bool MOE = false>
+hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
     const int ntile = (a.N + 15) / 16, cus = device_cus();
-    const int tpb = a.K <= kMfmaKC ? (ntile + cus - 1) / cus : 1;
+    const int tpb = a.K <= kMfmaKC ? (ntile * ny + cus - 1) / cus : 1;
     const int blocks = (ntile + tpb - 1) / tpb;
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       a.ldx % (XS == X_F16 ? 8 : 4) == 0;
     const bool salign = a.G % 4 == 0;
 #define NX_MFMA(XV, SA) \
-    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA>), dim3(blocks), dim3(kMfmaThreads), 0, st, a, tpb)
+    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA, MOE>), dim3(blocks, ny), dim3(kMfmaThreads), 0, st, a, tpb)
     if (xvec && salign) NX_MFMA(true, true);
     else if (xvec) NX_MFMA(true, false);
     else if (salign) NX_MFMA(false, true);
@@ -530,6 +492,57 @@ hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st) {
         default: return hipErrorInvalidValue;
     }
 }
+
+namespace {
+
+// Routed expert GEMVs on the dense kernels: grid row y takes the y-th
+// active expert of the routing plan (rows without one exit at once), the
+// expert's weights and its gathered token rows.  Batch 1 (one slot per
+// expert) runs the batch-1 kernel, with the CUs shared by the possible
+// active experts; larger batches run the matrix-core kernel over each
+// expert's slots.
+//   gate/up: rows (2f, 2f+1) = (gate f, up f) of w13[e]; x = the token's
+//            x16 row; act16[slot][f] = fp16(silu(g) * u).
+//   down:    rows of w2[e]; x = act16[slot]; y32[slot][n] = y.
+template <bool GATEUP>
+hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
+    if (!m.plan || m.batch < 1 || m.batch > kMoePlanMaxSlots) return hipErrorInvalidValue;
+    const int N = GATEUP ? 2 * m.F : m.d, K = GATEUP ? m.d : m.F;
+    const int G = (K + 31) / 32, Fp = (m.F + 31) / 32 * 32;
+    GemvArgs a{};
+    a.W = GATEUP ? m.w13 : m.w2;
+    a.S = GATEUP ? m.s13 : m.s2;
+    a.N = N;
+    a.K = K;
+    a.G = G;
+    a.batch = m.batch;
+    a.x16 = GATEUP ? m.x16 : m.act16;
+    a.ldx = GATEUP ? m.ldx : Fp;
+    a.act16 = m.act16;
+    a.lda = Fp;
+    a.y32 = m.y32;
+    a.ldy = m.d;
+    a.moe_plan = m.plan;
+    a.moe_wstride = (size_t)N * G * 16;
+    a.moe_sstride = (size_t)N * G;
+    a.moe_xslot = GATEUP ? 0 : 1;
+    const int ny = moe_plan_rows(m.E, m.batch, m.k);
+    constexpr int EPI = GATEUP ? E_SWIGLU : E_F32;
+    const int gpl = (G + kWave - 1) / kWave;
+    if (gpl > 7) return hipErrorInvalidValue;
+    if (m.batch > 1) return launch_mfma<X_F16, EPI, true>(a, st, ny);
+    constexpr int W = kB1WavesPerCU;
+    if (gpl <= 1) return launch_b1<1, 4, 2, false, X_F16, EPI, W, false, true>(a, st, ny);
+    if (gpl <= 2) {
+        if constexpr (GATEUP) return launch_b1<2, 2, 2, false, X_F16, EPI, W, false, true>(a, st, ny);
+        return launch_b1<2, 1, 3, false, X_F16, EPI, W, false, true>(a, st, ny);
+    }
+    if (gpl <= 4) return launch_b1<4, 2, 2, true, X_F16, EPI, W, false, true>(a, st, ny);
+    if constexpr (GATEUP) return launch_b1<7, 2, 2, true, X_F16, EPI, W, false, true>(a, st, ny);
+    return launch_b1<7, 1, 1, false, X_F16, EPI, W, false, true>(a, st, ny);
+}
+
+}  // namespace
 
 hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st) { return moe_launch<true>(a, st); }
 hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st) { return moe_launch<false>(a, st); }

@@ -678,12 +678,12 @@ constexpr int kB1WavesPerCU = 8;
 
 // Grid of the batch-1 GEMV over N rows with R-row tiles: waves_per_cu
 // wavefronts per CU, each with at least one full tile, in blocks of wpb
-// wavefronts; row pairs are dealt out evenly (rs).  Returns the number of
-// blocks.
-inline int b1_plan(int N, int R, int waves_per_cu, RowSplit& rs, int wpb = kWavesPerBlock) {
+// wavefronts; row pairs are dealt out evenly (rs).  share > 1: that many
+// such grids (routed experts) divide the CUs.  Returns the number of blocks.
+inline int b1_plan(int N, int R, int waves_per_cu, RowSplit& rs, int wpb = kWavesPerBlock, int share = 1) {
     const int units = (N + 1) / 2;
     const int min_units = (R + 1) / 2;
-    int waves = device_cus() * waves_per_cu;
+    int waves = device_cus() * waves_per_cu / (share > 0 ? share : 1);
     const int maxw = (units + min_units - 1) / min_units;
     if (waves > maxw) waves = maxw;
     waves = (waves + wpb - 1) / wpb * wpb;

@@ -56,7 +56,23 @@ struct GemvArgs {
     int lda;
     // E_LOGITS
     unsigned long long* best;  // [batch] packed (ordered value, ~index)
+    // Routed experts (launched through moe_gate_up_launch / moe_down_launch):
+    // grid row y takes the active expert of moe_plan + y * kMoePlanInts; its
+    // weights are at W + e * moe_wstride and S + e * moe_sstride, and batch
+    // row i reads x row (moe_xslot ? slot i : token i) and writes output row
+    // slot i.
+    const int32_t* moe_plan;
+    size_t moe_wstride, moe_sstride;
+    int moe_xslot;
 };
+
+// Routing plan of one active expert (int32 words): [0] expert id (-1: no
+// expert for this grid row), [1] its number of token slots n (<= 8),
+// [8 + i] slot i (= b * k + j), [16 + i] token b of slot i, for i < n.
+constexpr int kMoePlanInts = 32;
+constexpr int kMoePlanMaxSlots = 8;
+// Plan rows a step needs: the most experts that can be active at once.
+__host__ __device__ inline int moe_plan_rows(int E, int batch, int k) { return E < batch * k ? E : batch * k; }
 
 hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st);
 
@@ -168,6 +184,7 @@ struct MoeArgs {
     float* weights;             // [batch][k]
     int32_t* expert_count;      // [E]
     int32_t* expert_slots;      // [E][batch*k] : entries b*k + j
+    int32_t* plan;              // [moe_plan_rows][kMoePlanInts] or nullptr (batch <= 8)
 };
 hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st);
 struct MoeFfnArgs {
@@ -178,8 +195,7 @@ struct MoeFfnArgs {
     const uint8_t* w2;          // [E][d][Fp/2]
     const uint16_t* s2;
     int d, F, E, k, batch;
-    const int32_t* expert_count;
-    const int32_t* expert_slots;
+    const int32_t* plan;        // [moe_plan_rows][kMoePlanInts]
     const float* weights;       // [batch][k]
     uint16_t* act16;            // [batch*k][Fp]
     float* y32;                 // [batch*k][d]

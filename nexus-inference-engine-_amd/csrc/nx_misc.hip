@@ -308,6 +308,26 @@ __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
                 a.expert_slots[(size_t)e * a.batch * a.k + a.expert_count[e]] = bb * a.k + j;
                 a.expert_count[e] += 1;
             }
+        // routing plan: the active experts in ascending order (a token's k
+        // experts are distinct, so an expert holds at most `batch` slots)
+        if (a.plan) {
+            const int rows = moe_plan_rows(a.E, a.batch, a.k);
+            int r = 0;
+            for (int e = 0; e < a.E && r < rows; ++e) {
+                const int n = a.expert_count[e];
+                if (n == 0) continue;
+                int32_t* pl = a.plan + (size_t)r * kMoePlanInts;
+                pl[0] = e;
+                pl[1] = n;
+                for (int i = 0; i < n; ++i) {
+                    const int slot = a.expert_slots[(size_t)e * a.batch * a.k + i];
+                    pl[8 + i] = slot;
+                    pl[16 + i] = slot / a.k;
+                }
+                ++r;
+            }
+            for (; r < rows; ++r) a.plan[(size_t)r * kMoePlanInts] = -1;
+        }
     }
 }
 
@@ -438,6 +458,7 @@ hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, in
 
 hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st) {
     if (a.batch > 64 || a.E > 64 || a.k > 8) return hipErrorInvalidValue;
+    if (a.plan && a.batch > kMoePlanMaxSlots) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
 }

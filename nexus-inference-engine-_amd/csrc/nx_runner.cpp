@@ -10,6 +10,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <vector>
 
 #include "nx_common.h"
@@ -68,6 +69,7 @@ struct nx_model {
     int32_t* moe_ids = nullptr;
     float* moe_w = nullptr;
     int32_t* moe_slots = nullptr;
+    int32_t* moe_plan = nullptr;   // [moe_plan_rows][kMoePlanInts]
     uint16_t* moe_act = nullptr;
     float* moe_y = nullptr;
     float* attn_part = nullptr;
@@ -277,6 +279,7 @@ nx_status enqueue_step(nx_model* m) {
             ma.weights = m->moe_w;
             ma.expert_count = ly.moe_count;
             ma.expert_slots = m->moe_slots;
+            ma.plan = m->moe_plan;
             NX_LAUNCH(m, nx::moe_route_launch(ma, st));
             nx::MoeFfnArgs mf{};
             mf.x16 = m->xn16;
@@ -290,8 +293,7 @@ nx_status enqueue_step(nx_model* m) {
             mf.E = E;
             mf.k = c.top_k;
             mf.batch = B;
-            mf.expert_count = ly.moe_count;
-            mf.expert_slots = m->moe_slots;
+            mf.plan = m->moe_plan;
             mf.weights = m->moe_w;
             mf.act16 = m->moe_act;
             mf.y32 = m->moe_y;
@@ -464,6 +466,7 @@ nx_status create_impl(nx_model* m) {
         NX_TRY(dalloc(m, &m->moe_ids, (size_t)B * c.top_k));
         NX_TRY(dalloc(m, &m->moe_w, (size_t)B * c.top_k));
         NX_TRY(dalloc(m, &m->moe_slots, (size_t)E * B * c.top_k));
+        NX_TRY(dalloc(m, &m->moe_plan, (size_t)nx::moe_plan_rows(E, B, c.top_k) * nx::kMoePlanInts));
         NX_TRY(dalloc(m, &m->moe_act, (size_t)B * c.top_k * m->Fp));
         NX_TRY(dalloc(m, &m->moe_y, (size_t)B * c.top_k * d));
     }
@@ -698,27 +701,68 @@ nx_status nx_model_step_bytes(nx_model* m, double* bytes) {
 nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double* bytes) {
     if (!m || !avg_ms || iters < 1) return NX_ERR_INVALID;
     const nx_model_config& c = m->c;
-    if (c.n_experts != 0) return fail(m->ctx, NX_ERR_UNSUPPORTED, "dense models only");
+    const int E = c.n_experts;
     hipStream_t st = m->ctx->stream;
     // launch i uses layer i % n_layers, so consecutive launches stream
     // different weights (every layer's gate/up, 2 GB at the 8B shape, is far
     // larger than the last-level cache) as they do inside a decode step
-    auto launch = [&](int i) {
-        const Layer& ly = m->layers[i % c.n_layers];
-        nx::GemvArgs f{};
-        f.W = ly.w13;
-        f.S = ly.s13;
-        f.N = 2 * c.ffn;
-        f.K = c.d_model;
-        f.G = m->Gd;
-        f.batch = c.batch;
-        f.h32 = m->h;
-        f.ldx = c.d_model;
-        f.eps = c.eps;
-        f.act16 = m->act16;
-        f.lda = m->Fp;
-        return nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st);
-    };
+    std::function<hipError_t(int)> launch;
+    double nbytes = 0.0;
+    if (E == 0) {
+        launch = [&](int i) {
+            const Layer& ly = m->layers[i % c.n_layers];
+            nx::GemvArgs f{};
+            f.W = ly.w13;
+            f.S = ly.s13;
+            f.N = 2 * c.ffn;
+            f.K = c.d_model;
+            f.G = m->Gd;
+            f.batch = c.batch;
+            f.h32 = m->h;
+            f.ldx = c.d_model;
+            f.eps = c.eps;
+            f.act16 = m->act16;
+            f.lda = m->Fp;
+            return nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st);
+        };
+        nbytes = (double)qbytes(2 * (size_t)c.ffn, c.d_model) + (double)c.batch * (4.0 * c.d_model + 2.0 * c.ffn);
+    } else {
+        // the routed gate/up expert GEMV with the routing of the last step's
+        // last layer (the routing plan is shared by the layers and holds that
+        // layer's routing), over the weights of layer i % n_layers
+        const Layer& last = m->layers[c.n_layers - 1];
+        std::vector<int32_t> cnt(E, 0);
+        NX_HIP(m->ctx, hipMemcpy(cnt.data(), last.moe_count, (size_t)E * 4, hipMemcpyDeviceToHost));
+        int active = 0, slots = 0;
+        for (int e = 0; e < E; ++e) {
+            active += cnt[e] > 0;
+            slots += cnt[e];
+        }
+        if (active == 0) return fail(m->ctx, NX_ERR_STATE, "no routed step to time (decode once first)");
+        launch = [&](int i) {
+            const Layer& ly = m->layers[i % c.n_layers];
+            nx::MoeFfnArgs mf{};
+            mf.x16 = m->xn16;
+            mf.ldx = c.d_model;
+            mf.w13 = ly.w13;
+            mf.s13 = ly.s13;
+            mf.w2 = ly.w2;
+            mf.s2 = ly.s2;
+            mf.d = c.d_model;
+            mf.F = c.ffn;
+            mf.E = E;
+            mf.k = c.top_k;
+            mf.batch = c.batch;
+            mf.plan = m->moe_plan;
+            mf.weights = m->moe_w;
+            mf.act16 = m->moe_act;
+            mf.y32 = m->moe_y;
+            mf.out = m->h;
+            mf.accumulate = 1;
+            return nx::moe_gate_up_launch(mf, st);
+        };
+        nbytes = active * (double)qbytes(2 * (size_t)c.ffn, c.d_model) + (double)slots * (2.0 * c.d_model + 2.0 * c.ffn);
+    }
     for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
     for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch(i));
@@ -727,9 +771,7 @@ nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double*
     float ms = 0.0f;
     NX_HIP(m->ctx, hipEventElapsedTime(&ms, m->ctx->ev0, m->ctx->ev1));
     *avg_ms = (double)ms / iters;
-    if (bytes)
-        *bytes = (double)qbytes(2 * (size_t)c.ffn, c.d_model) +
-                 (double)c.batch * (4.0 * c.d_model + 2.0 * c.ffn);
+    if (bytes) *bytes = nbytes;
     return NX_OK;
 }
 
