@@ -212,10 +212,14 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
 // rows 4(l/16)..+3 and every lane needs one scale per group.
 //
 // One wavefront's share (groups [gs, ge) of the stage starting at group
-// gbase) of a 16-row tile, requested without branches.  SALIGN: G % 4 == 0,
+// gbase) of a 16-row tile, requested without branches: lane (c, kq) loads the
+// whole 16-byte groups gs + 4u + kq (u < 4) of row c, so each request moves
+// 16 bytes per lane (64 contiguous bytes of each of the 16 rows); the MFMA
+// needs quarter kq of every group in lane row kq, which a 4 x 4 exchange
+// across the four 16-lane rows provides (quad_transpose).  SALIGN: G % 4 == 0,
 // so the scales of 4 consecutive groups are one 8-byte load.
 struct MfmaRegs {
-    uint32_t code[kMfmaGW];
+    uint4 code[kMfmaGW / 4];
     uint32_t sc[kMfmaGW / 2];  // fp16 scale pairs (groups 2u, 2u+1) of the lane's weight row
 };
 
@@ -238,10 +242,27 @@ __device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs,
         for (int u2 = 0; u2 < kMfmaGW / 2; ++u2)
             r.sc[u2] = (uint32_t)srow[min(gs + 2 * u2, gl)] | ((uint32_t)srow[min(gs + 2 * u2 + 1, gl)] << 16);
     }
-    const uint8_t* wrow = a.W + row * G * 16 + 4 * kq;
+    const uint8_t* wrow = a.W + row * G * 16;
 #pragma unroll
-    for (int u = 0; u < kMfmaGW; ++u)
-        r.code[u] = *reinterpret_cast<const uint32_t*>(wrow + (size_t)(gbase + min(gs + u, gl)) * 16);
+    for (int u4 = 0; u4 < kMfmaGW / 4; ++u4)
+        r.code[u4] = *reinterpret_cast<const uint4*>(wrow + (size_t)(gbase + min(gs + 4 * u4 + kq, gl)) * 16);
+}
+
+// 4 x 4 exchange across the 16-lane rows: on entry lane row r holds the four
+// quarters (q.x .. q.w) of group 4u + r; on exit register j holds, in lane
+// row r, quarter r of group 4u + j.  v_permlane32_swap exchanges the upper
+// half of its first operand with the lower half of its second, and
+// v_permlane16_swap the odd rows of the first with the even rows of the
+// second.
+__device__ inline void quad_transpose(const uint4& q, uint32_t (&o)[4]) {
+    const auto p02 = __builtin_amdgcn_permlane32_swap(q.x, q.z, false, false);
+    const auto p13 = __builtin_amdgcn_permlane32_swap(q.y, q.w, false, false);
+    const auto s01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+    const auto s23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+    o[0] = s01[0];
+    o[1] = s01[1];
+    o[2] = s23[0];
+    o[3] = s23[1];
 }
 
 // The A operands (x of the batch) of the wavefront's groups, from LDS.
@@ -256,12 +277,20 @@ __device__ inline void mfma_load_x(const uint4* xs, int gs, int ge, uint4 (&xv)[
 // (fully unrolled, so the register arrays stay in registers; groups past ge
 // repeat a valid group with weight zero).
 __device__ inline void mfma_compute(const MfmaRegs& r, const uint4 (&xv)[kMfmaGW], int gs, int ge, mf4_t& acc) {
+    uint32_t code[kMfmaGW];
+#pragma unroll
+    for (int u4 = 0; u4 < kMfmaGW / 4; ++u4) {
+        uint32_t o[4];
+        quad_transpose(r.code[u4], o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) code[4 * u4 + j] = o[j];
+    }
 #pragma unroll
     for (int u = 0; u < kMfmaGW; ++u) {
         const float on = gs + u < ge ? 1.0f : 0.0f;
         const mf4_t z = {0.f, 0.f, 0.f, 0.f};
         const mf4_t cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8_t, xv[u]),
-                                                               codes_to_h8(r.code[u]), z, 0, 0, 0);
+                                                               codes_to_h8(code[u]), z, 0, 0, 0);
         const uint32_t pr = r.sc[u >> 1];
         const float sv = h2f_bits((uint16_t)((u & 1) ? (pr >> 16) : (pr & 0xFFFFu))) * on;
 #pragma unroll
