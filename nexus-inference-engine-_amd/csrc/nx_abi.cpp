@@ -641,7 +641,7 @@ nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits, nx_buf ids, nx_buf w, in
     nx_status s = ensure_attn_ws(ctx, extra > ctx->attn_ws_bytes ? extra : ctx->attn_ws_bytes);
     if (s != NX_OK) return s;
     nx::MoeArgs a{};
-    a.logits = dptr<const float>(logits);
+    a.logits = dptr<float>(logits);
     a.E = E;
     a.k = k;
     a.batch = batch;

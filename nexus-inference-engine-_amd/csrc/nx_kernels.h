@@ -178,15 +178,30 @@ hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, in
 
 // MoE
 struct MoeArgs {
-    const float* logits;        // [batch][E]
+    float* logits;              // [batch][E] (read by moe_route_launch, written by moe_norm_route_launch)
     int E, k, batch;
     int32_t* ids;               // [batch][k]
     float* weights;             // [batch][k]
     int32_t* expert_count;      // [E]
     int32_t* expert_slots;      // [E][batch*k] : entries b*k + j
     int32_t* plan;              // [moe_plan_rows][kMoePlanInts] or nullptr (batch <= 8)
+    // moe_norm_route_launch: the block input h fp32 [batch][d] (RMSNorm with
+    // norm_w, nullptr = ones, and eps) to fp16 x16 [batch][d], and the router
+    // int4-g32 rows wr [E][G*16], sr [E][G] whose products with x16 are the
+    // logits it writes to `logits`
+    const float* h;
+    const float* norm_w;
+    float eps;
+    int d;
+    const uint8_t* wr;
+    const uint16_t* sr;
+    uint16_t* xn16;
 };
+// Routing from logits [batch][E].
 hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st);
+// RMSNorm + router GEMV + routing in one launch (shapes moe_norm_route_fits).
+bool moe_norm_route_fits(int d, int E, int k, int batch);
+hipError_t moe_norm_route_launch(const MoeArgs& a, hipStream_t st);
 struct MoeFfnArgs {
     const uint16_t* x16;        // [batch][ldx] normed hidden (fp16)
     int ldx;

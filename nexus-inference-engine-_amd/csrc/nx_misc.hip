@@ -267,68 +267,203 @@ __global__ void k_set_tokens(unsigned long long* best, const int32_t* tokens, in
     if (b < batch) best[b] = 0xFFFFFFFFull - (unsigned long long)(uint32_t)tokens[b];
 }
 
+// Routing of one sequence (hybrid_model.cpp:1656-1694): softmax over the E
+// logits, the k largest probabilities (ties: lower id), weights renormalized
+// over the chosen k.
+// ids, w: the k outputs; p: E floats of scratch (all in LDS).
+__device__ inline void route_row(const float* lg, int E, int k, int* ids, float* w, float* p) {
+    float mx = lg[0];
+    for (int e = 1; e < E; ++e) mx = fmaxf(mx, lg[e]);
+    float sum = 0.0f;
+    for (int e = 0; e < E; ++e) {
+        p[e] = expf(lg[e] - mx);
+        sum += p[e];
+    }
+    if (sum > 0.0f)
+        for (int e = 0; e < E; ++e) p[e] = p[e] / sum;
+    unsigned long long taken = 0ull;
+    float active = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        int best = -1;
+        for (int e = 0; e < E; ++e)
+            if (!((taken >> e) & 1ull) && (best < 0 || p[e] > p[best])) best = e;
+        taken |= 1ull << best;
+        ids[j] = best;
+        active += p[best];
+    }
+    for (int j = 0; j < k; ++j) w[j] = active > 0.0f ? p[ids[j]] / active : 1.0f / (float)k;
+}
+
+// Per-expert slot lists in (b, j) order and the routing plan (the active
+// experts in ascending order; a token's k experts are distinct, so an expert
+// holds at most `batch` slots), from the chosen ids [batch][k].  One thread;
+// cnt: E ints of scratch (LDS).
+__device__ inline void build_lists(const MoeArgs& a, const int32_t* ids, int* cnt) {
+    for (int e = 0; e < a.E; ++e) cnt[e] = 0;
+    for (int bb = 0; bb < a.batch; ++bb)
+        for (int j = 0; j < a.k; ++j) {
+            const int e = ids[bb * a.k + j];
+            a.expert_slots[(size_t)e * a.batch * a.k + cnt[e]] = bb * a.k + j;
+            cnt[e] += 1;
+        }
+    for (int e = 0; e < a.E; ++e) a.expert_count[e] = cnt[e];
+    if (!a.plan) return;
+    const int rows = moe_plan_rows(a.E, a.batch, a.k);
+    int r = 0;
+    for (int e = 0; e < a.E && r < rows; ++e) {
+        if (cnt[e] == 0) continue;
+        int32_t* pl = a.plan + (size_t)r * kMoePlanInts;
+        pl[0] = e;
+        pl[1] = cnt[e];
+        int n = 0;
+        for (int bb = 0; bb < a.batch; ++bb)
+            for (int j = 0; j < a.k; ++j)
+                if (ids[bb * a.k + j] == e) {
+                    pl[8 + n] = bb * a.k + j;
+                    pl[16 + n] = bb;
+                    ++n;
+                }
+        ++r;
+    }
+    for (; r < rows; ++r) a.plan[(size_t)r * kMoePlanInts] = -1;
+}
+
 // Single block: thread b routes sequence b; thread 0 then builds the
-// per-expert token lists in (b, j) order.
+// per-expert token lists and the routing plan.
 __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
     const int b = threadIdx.x;
+    __shared__ int32_t sid[64 * 8];
+    __shared__ float sp[64][64];
+    __shared__ int scnt[64];
+    __shared__ float sw[64 * 8];
     if (b < a.batch) {
-        const float* lg = a.logits + (size_t)b * a.E;
-        float p[64];
-        float mx = lg[0];
-        for (int e = 1; e < a.E; ++e) mx = fmaxf(mx, lg[e]);
-        float sum = 0.0f;
-        for (int e = 0; e < a.E; ++e) {
-            p[e] = expf(lg[e] - mx);
-            sum += p[e];
-        }
-        if (sum > 0.0f)
-            for (int e = 0; e < a.E; ++e) p[e] = p[e] / sum;
-        unsigned long long taken = 0ull;
-        int ids[8];
-        float active = 0.0f;
+        route_row(a.logits + (size_t)b * a.E, a.E, a.k, sid + b * a.k, sw + b * a.k, sp[b]);
         for (int j = 0; j < a.k; ++j) {
-            int best = -1;
-            for (int e = 0; e < a.E; ++e)
-                if (!((taken >> e) & 1ull) && (best < 0 || p[e] > p[best])) best = e;
-            taken |= 1ull << best;
-            ids[j] = best;
-            active += p[best];
-        }
-        for (int j = 0; j < a.k; ++j) {
-            a.ids[(size_t)b * a.k + j] = ids[j];
-            a.weights[(size_t)b * a.k + j] = active > 0.0f ? p[ids[j]] / active : 1.0f / (float)a.k;
+            a.ids[(size_t)b * a.k + j] = sid[b * a.k + j];
+            a.weights[(size_t)b * a.k + j] = sw[b * a.k + j];
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int e = 0; e < a.E; ++e) a.expert_count[e] = 0;
-        for (int bb = 0; bb < a.batch; ++bb)
-            for (int j = 0; j < a.k; ++j) {
-                const int e = a.ids[(size_t)bb * a.k + j];
-                a.expert_slots[(size_t)e * a.batch * a.k + a.expert_count[e]] = bb * a.k + j;
-                a.expert_count[e] += 1;
-            }
-        // routing plan: the active experts in ascending order (a token's k
-        // experts are distinct, so an expert holds at most `batch` slots)
-        if (a.plan) {
-            const int rows = moe_plan_rows(a.E, a.batch, a.k);
-            int r = 0;
-            for (int e = 0; e < a.E && r < rows; ++e) {
-                const int n = a.expert_count[e];
-                if (n == 0) continue;
-                int32_t* pl = a.plan + (size_t)r * kMoePlanInts;
-                pl[0] = e;
-                pl[1] = n;
-                for (int i = 0; i < n; ++i) {
-                    const int slot = a.expert_slots[(size_t)e * a.batch * a.k + i];
-                    pl[8 + i] = slot;
-                    pl[16 + i] = slot / a.k;
-                }
-                ++r;
-            }
-            for (; r < rows; ++r) a.plan[(size_t)r * kMoePlanInts] = -1;
+    if (threadIdx.x == 0) build_lists(a, sid, scnt);
+}
+
+// The MoE block's input and routing in one block of 1024 threads (batch <=
+// 8, E <= 16, d <= 4096): RMSNorm of h to fp16 x (xn16, also kept in LDS,
+// hybrid_model.cpp:1647-1655), the router logits from x (int4-g32 rows of
+// wr: wavefront e takes row e, its lanes the groups, so the sum order is
+// fixed), then k_moe_route's routing from LDS.  h and the router weights
+// are requested together up front; no step waits on a global load after
+// that.
+constexpr int kNrThreads = 1024;
+constexpr int kNrMaxElems = 32768;  // batch * d
+constexpr int kNrMaxE = kNrThreads / kWave;
+constexpr int kNrMaxG = 2 * kWave;  // d <= 4096
+template <int MAXB>
+__global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
+    constexpr int PER = kNrMaxElems / 8 * MAXB / kNrThreads, JG = kNrMaxG / kWave;
+    __shared__ __align__(16) uint16_t xs[kNrMaxElems];
+    __shared__ float red[kNrThreads / kWave][8];
+    __shared__ float inv[8];
+    __shared__ float lg[8 * kNrMaxE];
+    __shared__ int32_t sid[8 * 8];
+    __shared__ float sp[8][kNrMaxE];
+    __shared__ float sw[8 * 8];
+    __shared__ int scnt[kNrMaxE];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int d = a.d, B = a.batch, E = a.E, G = (d + 31) / 32, n = B * d;
+    float hv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) hv[j] = a.h[min(tid + kNrThreads * j, n - 1)];
+    const int er = min(wave, E - 1);
+    uint4 wc[JG];
+    uint16_t wsc[JG];
+#pragma unroll
+    for (int j = 0; j < JG; ++j) {
+        const int g = min(lane + kWave * j, G - 1);
+        wc[j] = *reinterpret_cast<const uint4*>(a.wr + ((size_t)er * G + g) * 16);
+        wsc[j] = a.sr[(size_t)er * G + g];
+    }
+    // sums of squares per batch row
+    float ss[MAXB];
+#pragma unroll
+    for (int bb = 0; bb < MAXB; ++bb) ss[bb] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int idx = tid + kNrThreads * j, b = idx / d;
+        const float v2 = idx < n ? hv[j] * hv[j] : 0.0f;
+#pragma unroll
+        for (int bb = 0; bb < MAXB; ++bb) ss[bb] += b == bb ? v2 : 0.0f;
+    }
+#pragma unroll
+    for (int bb = 0; bb < MAXB; ++bb) {
+        const float t = wave_sum(ss[bb]);
+        if (lane == 0) red[wave][bb] = t;
+    }
+    __syncthreads();
+    if (tid < B) {
+        float t = 0.0f;
+        for (int w = 0; w < kNrThreads / kWave; ++w) t += red[w][tid];
+        inv[tid] = 1.0f / sqrtf(t / (float)d + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int idx = tid + kNrThreads * j;
+        if (idx < n) {
+            const int b = idx / d, i = idx - b * d;
+            const float x = hv[j] * inv[b];
+            const uint16_t u = f2h_bits(a.norm_w ? x * a.norm_w[i] : x);
+            xs[idx] = u;
+            a.xn16[idx] = u;
         }
     }
+    __syncthreads();
+    // router logits: y[b][e] = sum_g s_g * sum_k (q_k - 8) x[b][32g + k]
+    if (wave < E) {
+        float acc[MAXB];
+#pragma unroll
+        for (int bb = 0; bb < MAXB; ++bb) acc[bb] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < JG; ++j) {
+            const int g = lane + kWave * j;
+            if (g < G) {
+                const uint32_t cw[4] = {wc[j].x, wc[j].y, wc[j].z, wc[j].w};
+                const float sg = h2f_bits(wsc[j]);
+#pragma unroll
+                for (int bb = 0; bb < MAXB; ++bb) {
+                    if (bb >= B) continue;
+                    // x pairs (2m, 2m+1) meet the low and high nibble of byte m
+                    const uint32_t* xr = reinterpret_cast<const uint32_t*>(xs + bb * d + 32 * g);
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int m = 0; m < 16; ++m) {
+                        const uint32_t byte = (cw[m >> 2] >> (8 * (m & 3))) & 0xFFu, xp = xr[m];
+                        dot = fmaf((float)(int)(byte & 15u) - 8.0f, h2f_bits((uint16_t)(xp & 0xFFFFu)), dot);
+                        dot = fmaf((float)(int)(byte >> 4) - 8.0f, h2f_bits((uint16_t)(xp >> 16)), dot);
+                    }
+                    acc[bb] = fmaf(dot, sg, acc[bb]);
+                }
+            }
+        }
+#pragma unroll
+        for (int bb = 0; bb < MAXB; ++bb) {
+            const float t = wave_sum(acc[bb]);
+            if (lane == 0 && bb < B) {
+                lg[bb * E + wave] = t;
+                a.logits[(size_t)bb * E + wave] = t;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < B) {
+        route_row(lg + tid * E, E, a.k, sid + tid * a.k, sw + tid * a.k, sp[tid]);
+        for (int j = 0; j < a.k; ++j) {
+            a.ids[(size_t)tid * a.k + j] = sid[tid * a.k + j];
+            a.weights[(size_t)tid * a.k + j] = sw[tid * a.k + j];
+        }
+    }
+    __syncthreads();
+    if (tid == 0) build_lists(a, sid, scnt);
 }
 
 __global__ void k_moe_combine(const float* y32, const float* weights, float* out, int d, int k,
@@ -453,6 +588,28 @@ hipError_t finish_tokens_launch(const unsigned long long* best, const int32_t* p
 hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, int batch,
                              hipStream_t st) {
     hipLaunchKernelGGL(k_set_tokens, dim3(1), dim3(64), 0, st, best, tokens, batch);
+    return hipGetLastError();
+}
+
+bool moe_norm_route_fits(int d, int E, int k, int batch) {
+    // batch rows of at most 4096 elements (kNrMaxElems / 8 per row in the
+    // register share of k_moe_norm_route<MAXB>)
+    // and whole 32-element groups (the router's last group reads no x past its row)
+    return batch >= 1 && batch <= 8 && E >= 1 && E <= kNrMaxE && k >= 1 && k <= 8 && k <= E && d >= 32 &&
+           d % 32 == 0 && d <= kNrMaxElems / 8 && d <= 32 * kNrMaxG;
+}
+
+hipError_t moe_norm_route_launch(const MoeArgs& a, hipStream_t st) {
+    if (!moe_norm_route_fits(a.d, a.E, a.k, a.batch) || !a.h || !a.wr || !a.sr || !a.xn16 || !a.logits)
+        return hipErrorInvalidValue;
+    if (a.batch == 1)
+        hipLaunchKernelGGL(k_moe_norm_route<1>, dim3(1), dim3(kNrThreads), 0, st, a);
+    else if (a.batch == 2)
+        hipLaunchKernelGGL(k_moe_norm_route<2>, dim3(1), dim3(kNrThreads), 0, st, a);
+    else if (a.batch <= 4)
+        hipLaunchKernelGGL(k_moe_norm_route<4>, dim3(1), dim3(kNrThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_moe_norm_route<8>, dim3(1), dim3(kNrThreads), 0, st, a);
     return hipGetLastError();
 }
 

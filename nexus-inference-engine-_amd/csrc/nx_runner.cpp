@@ -257,19 +257,6 @@ nx_status enqueue_step(nx_model* m) {
             dn.ldy = d;
             NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, dn, st));
         } else {
-            NX_LAUNCH(m, nx::rmsnorm_launch(m->h, nullptr, m->xn16, d, c.eps, B, st));
-            nx::GemvArgs r{};
-            r.W = ly.wr;
-            r.S = ly.sr;
-            r.N = E;
-            r.K = d;
-            r.G = m->Gd;
-            r.batch = B;
-            r.x16 = m->xn16;
-            r.ldx = d;
-            r.y32 = m->router_logits;
-            r.ldy = E;
-            NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_F32, r, st));
             nx::MoeArgs ma{};
             ma.logits = m->router_logits;
             ma.E = E;
@@ -280,7 +267,31 @@ nx_status enqueue_step(nx_model* m) {
             ma.expert_count = ly.moe_count;
             ma.expert_slots = m->moe_slots;
             ma.plan = m->moe_plan;
-            NX_LAUNCH(m, nx::moe_route_launch(ma, st));
+            if (nx::moe_norm_route_fits(d, E, c.top_k, B)) {
+                // RMSNorm, router and routing in one launch
+                ma.h = m->h;
+                ma.eps = c.eps;
+                ma.d = d;
+                ma.wr = ly.wr;
+                ma.sr = ly.sr;
+                ma.xn16 = m->xn16;
+                NX_LAUNCH(m, nx::moe_norm_route_launch(ma, st));
+            } else {
+                NX_LAUNCH(m, nx::rmsnorm_launch(m->h, nullptr, m->xn16, d, c.eps, B, st));
+                nx::GemvArgs r{};
+                r.W = ly.wr;
+                r.S = ly.sr;
+                r.N = E;
+                r.K = d;
+                r.G = m->Gd;
+                r.batch = B;
+                r.x16 = m->xn16;
+                r.ldx = d;
+                r.y32 = m->router_logits;
+                r.ldy = E;
+                NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_F32, r, st));
+                NX_LAUNCH(m, nx::moe_route_launch(ma, st));
+            }
             nx::MoeFfnArgs mf{};
             mf.x16 = m->xn16;
             mf.ldx = d;
