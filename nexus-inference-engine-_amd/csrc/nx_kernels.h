@@ -196,6 +196,7 @@ struct MoeArgs {
     const uint8_t* wr;
     const uint16_t* sr;
     uint16_t* xn16;
+    unsigned* counter;  // one word, zero before a launch (batch > 1); the launch leaves it at zero
 };
 // Routing from logits [batch][E].
 hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st);

@@ -347,113 +347,115 @@ __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
     if (threadIdx.x == 0) build_lists(a, sid, scnt);
 }
 
-// The MoE block's input and routing in one block of 1024 threads (batch <=
-// 8, E <= 16, d <= 4096): RMSNorm of h to fp16 x (xn16, also kept in LDS,
-// hybrid_model.cpp:1647-1655), the router logits from x (int4-g32 rows of
-// wr: wavefront e takes row e, its lanes the groups, so the sum order is
-// fixed), then k_moe_route's routing from LDS.  h and the router weights
-// are requested together up front; no step waits on a global load after
-// that.
-constexpr int kNrThreads = 1024;
-constexpr int kNrMaxElems = 32768;  // batch * d
-constexpr int kNrMaxE = kNrThreads / kWave;
-constexpr int kNrMaxG = 2 * kWave;  // d <= 4096
-template <int MAXB>
+// The MoE block's input and routing in one launch (batch <= 8, E <= 16,
+// d <= 4096, d % 32 == 0).  Block b takes sequence b: the RMSNorm of h[b] to
+// fp16 x (xn16[b], also kept in LDS; hybrid_model.cpp:1647-1655) and the
+// router logits of x (int4-g32 rows of wr: wavefront w takes rows w, w + 4,
+// ..., its lanes the groups, so every sum has a fixed order).  h and the
+// router rows are requested together up front.  Each block publishes its
+// logits with agent-scope stores, waits for them, and counts itself in
+// *counter; the last block resets the counter and routes every sequence
+// (k_moe_route's routing) from the published logits.
+constexpr int kNrThreads = 256;
+constexpr int kNrWaves = kNrThreads / kWave;
+constexpr int kNrMaxD = 4096;
+constexpr int kNrMaxE = 16;
+constexpr int kNrMaxG = kNrMaxD / 32;
 __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
-    constexpr int PER = kNrMaxElems / 8 * MAXB / kNrThreads, JG = kNrMaxG / kWave;
-    __shared__ __align__(16) uint16_t xs[kNrMaxElems];
-    __shared__ float red[kNrThreads / kWave][8];
-    __shared__ float inv[8];
+    constexpr int PER = kNrMaxD / kNrThreads, RW = kNrMaxE / kNrWaves, JG = kNrMaxG / kWave;
+    __shared__ __align__(16) uint16_t xs[kNrMaxD];  // pair-major: [pair m of the group][group g]
+    __shared__ float red[kNrWaves];
+    __shared__ float inv_s;
     __shared__ float lg[8 * kNrMaxE];
     __shared__ int32_t sid[8 * 8];
     __shared__ float sp[8][kNrMaxE];
     __shared__ float sw[8 * 8];
     __shared__ int scnt[kNrMaxE];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-    const int d = a.d, B = a.batch, E = a.E, G = (d + 31) / 32, n = B * d;
+    __shared__ int last;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6, b = blockIdx.x;
+    const int d = a.d, B = a.batch, E = a.E, G = d / 32;
+    const float* hb = a.h + (size_t)b * d;
     float hv[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) hv[j] = a.h[min(tid + kNrThreads * j, n - 1)];
-    const int er = min(wave, E - 1);
-    uint4 wc[JG];
-    uint16_t wsc[JG];
+    for (int j = 0; j < PER; ++j) hv[j] = hb[min(tid + kNrThreads * j, d - 1)];
+    uint4 wc[RW][JG];
+    uint16_t wsc[RW][JG];
 #pragma unroll
-    for (int j = 0; j < JG; ++j) {
-        const int g = min(lane + kWave * j, G - 1);
-        wc[j] = *reinterpret_cast<const uint4*>(a.wr + ((size_t)er * G + g) * 16);
-        wsc[j] = a.sr[(size_t)er * G + g];
-    }
-    // sums of squares per batch row
-    float ss[MAXB];
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
-    for (int bb = 0; bb < MAXB; ++bb) ss[bb] = 0.0f;
+        for (int j = 0; j < JG; ++j) {
+            const int e = min(wave + kNrWaves * r, E - 1), g = min(lane + kWave * j, G - 1);
+            wc[r][j] = *reinterpret_cast<const uint4*>(a.wr + ((size_t)e * G + g) * 16);
+            wsc[r][j] = a.sr[(size_t)e * G + g];
+        }
+    float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int idx = tid + kNrThreads * j, b = idx / d;
-        const float v2 = idx < n ? hv[j] * hv[j] : 0.0f;
-#pragma unroll
-        for (int bb = 0; bb < MAXB; ++bb) ss[bb] += b == bb ? v2 : 0.0f;
-    }
-#pragma unroll
-    for (int bb = 0; bb < MAXB; ++bb) {
-        const float t = wave_sum(ss[bb]);
-        if (lane == 0) red[wave][bb] = t;
-    }
+    for (int j = 0; j < PER; ++j) ss += tid + kNrThreads * j < d ? hv[j] * hv[j] : 0.0f;
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
     __syncthreads();
-    if (tid < B) {
+    if (tid == 0) {
         float t = 0.0f;
-        for (int w = 0; w < kNrThreads / kWave; ++w) t += red[w][tid];
-        inv[tid] = 1.0f / sqrtf(t / (float)d + a.eps);
+        for (int w = 0; w < kNrWaves; ++w) t += red[w];
+        inv_s = 1.0f / sqrtf(t / (float)d + a.eps);
     }
     __syncthreads();
+    const float inv = inv_s;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-        const int idx = tid + kNrThreads * j;
-        if (idx < n) {
-            const int b = idx / d, i = idx - b * d;
-            const float x = hv[j] * inv[b];
+        const int i = tid + kNrThreads * j;
+        if (i < d) {
+            const float x = hv[j] * inv;
             const uint16_t u = f2h_bits(a.norm_w ? x * a.norm_w[i] : x);
-            xs[idx] = u;
-            a.xn16[idx] = u;
+            // the router's lanes (consecutive groups) read consecutive words
+            xs[(((i >> 1) & 15) * G + (i >> 5)) * 2 + (i & 1)] = u;
+            a.xn16[(size_t)b * d + i] = u;
         }
     }
     __syncthreads();
-    // router logits: y[b][e] = sum_g s_g * sum_k (q_k - 8) x[b][32g + k]
-    if (wave < E) {
-        float acc[MAXB];
+    // router logits: y[e] = sum_g s_g * sum_k (q_k - 8) x[32g + k]
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(xs);
 #pragma unroll
-        for (int bb = 0; bb < MAXB; ++bb) acc[bb] = 0.0f;
+    for (int r = 0; r < RW; ++r) {
+        const int e = wave + kNrWaves * r;
+        if (e >= E) continue;
+        float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < JG; ++j) {
             const int g = lane + kWave * j;
             if (g < G) {
-                const uint32_t cw[4] = {wc[j].x, wc[j].y, wc[j].z, wc[j].w};
-                const float sg = h2f_bits(wsc[j]);
+                const uint32_t cw[4] = {wc[r][j].x, wc[r][j].y, wc[r][j].z, wc[r][j].w};
+                float dot = 0.0f;
 #pragma unroll
-                for (int bb = 0; bb < MAXB; ++bb) {
-                    if (bb >= B) continue;
-                    // x pairs (2m, 2m+1) meet the low and high nibble of byte m
-                    const uint32_t* xr = reinterpret_cast<const uint32_t*>(xs + bb * d + 32 * g);
-                    float dot = 0.0f;
-#pragma unroll
-                    for (int m = 0; m < 16; ++m) {
-                        const uint32_t byte = (cw[m >> 2] >> (8 * (m & 3))) & 0xFFu, xp = xr[m];
-                        dot = fmaf((float)(int)(byte & 15u) - 8.0f, h2f_bits((uint16_t)(xp & 0xFFFFu)), dot);
-                        dot = fmaf((float)(int)(byte >> 4) - 8.0f, h2f_bits((uint16_t)(xp >> 16)), dot);
-                    }
-                    acc[bb] = fmaf(dot, sg, acc[bb]);
+                for (int m = 0; m < 16; ++m) {
+                    // x pair (2m, 2m+1) meets the low and high nibble of byte m
+                    const uint32_t byte = (cw[m >> 2] >> (8 * (m & 3))) & 0xFFu, xp = xw[m * G + g];
+                    dot = fmaf((float)(int)(byte & 15u) - 8.0f, h2f_bits((uint16_t)(xp & 0xFFFFu)), dot);
+                    dot = fmaf((float)(int)(byte >> 4) - 8.0f, h2f_bits((uint16_t)(xp >> 16)), dot);
                 }
+                acc = fmaf(dot, h2f_bits(wsc[r][j]), acc);
             }
         }
-#pragma unroll
-        for (int bb = 0; bb < MAXB; ++bb) {
-            const float t = wave_sum(acc[bb]);
-            if (lane == 0 && bb < B) {
-                lg[bb * E + wave] = t;
-                a.logits[(size_t)bb * E + wave] = t;
-            }
-        }
+        acc = wave_sum(acc);
+        if (lane == 0)
+            __hip_atomic_store(a.logits + (size_t)b * E + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // this block's logits are stored before it counts itself
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        int l = 1;
+        if (B > 1) {
+            const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            l = prev == (unsigned)B - 1u;
+            if (l) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        last = l;
+    }
+    __syncthreads();
+    if (!last) return;
+    for (int idx = tid; idx < B * E; idx += kNrThreads)
+        lg[idx] = __hip_atomic_load(a.logits + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (tid < B) {
         route_row(lg + tid * E, E, a.k, sid + tid * a.k, sw + tid * a.k, sp[tid]);
@@ -592,24 +594,16 @@ hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, in
 }
 
 bool moe_norm_route_fits(int d, int E, int k, int batch) {
-    // batch rows of at most 4096 elements (kNrMaxElems / 8 per row in the
-    // register share of k_moe_norm_route<MAXB>)
-    // and whole 32-element groups (the router's last group reads no x past its row)
+    // whole 32-element groups, so the router's last group reads no x past its row
     return batch >= 1 && batch <= 8 && E >= 1 && E <= kNrMaxE && k >= 1 && k <= 8 && k <= E && d >= 32 &&
-           d % 32 == 0 && d <= kNrMaxElems / 8 && d <= 32 * kNrMaxG;
+           d % 32 == 0 && d <= kNrMaxD;
 }
 
 hipError_t moe_norm_route_launch(const MoeArgs& a, hipStream_t st) {
-    if (!moe_norm_route_fits(a.d, a.E, a.k, a.batch) || !a.h || !a.wr || !a.sr || !a.xn16 || !a.logits)
+    if (!moe_norm_route_fits(a.d, a.E, a.k, a.batch) || !a.h || !a.wr || !a.sr || !a.xn16 || !a.logits ||
+        (a.batch > 1 && !a.counter))
         return hipErrorInvalidValue;
-    if (a.batch == 1)
-        hipLaunchKernelGGL(k_moe_norm_route<1>, dim3(1), dim3(kNrThreads), 0, st, a);
-    else if (a.batch == 2)
-        hipLaunchKernelGGL(k_moe_norm_route<2>, dim3(1), dim3(kNrThreads), 0, st, a);
-    else if (a.batch <= 4)
-        hipLaunchKernelGGL(k_moe_norm_route<4>, dim3(1), dim3(kNrThreads), 0, st, a);
-    else
-        hipLaunchKernelGGL(k_moe_norm_route<8>, dim3(1), dim3(kNrThreads), 0, st, a);
+    hipLaunchKernelGGL(k_moe_norm_route, dim3(a.batch), dim3(kNrThreads), 0, st, a);
     return hipGetLastError();
 }
 

@@ -70,6 +70,7 @@ struct nx_model {
     float* moe_w = nullptr;
     int32_t* moe_slots = nullptr;
     int32_t* moe_plan = nullptr;   // [moe_plan_rows][kMoePlanInts]
+    unsigned* moe_counter = nullptr;  // arrival counter of the MoE routing launch (zero between launches)
     uint16_t* moe_act = nullptr;
     float* moe_y = nullptr;
     float* attn_part = nullptr;
@@ -275,6 +276,7 @@ nx_status enqueue_step(nx_model* m) {
                 ma.wr = ly.wr;
                 ma.sr = ly.sr;
                 ma.xn16 = m->xn16;
+                ma.counter = m->moe_counter;
                 NX_LAUNCH(m, nx::moe_norm_route_launch(ma, st));
             } else {
                 NX_LAUNCH(m, nx::rmsnorm_launch(m->h, nullptr, m->xn16, d, c.eps, B, st));
@@ -478,6 +480,7 @@ nx_status create_impl(nx_model* m) {
         NX_TRY(dalloc(m, &m->moe_w, (size_t)B * c.top_k));
         NX_TRY(dalloc(m, &m->moe_slots, (size_t)E * B * c.top_k));
         NX_TRY(dalloc(m, &m->moe_plan, (size_t)nx::moe_plan_rows(E, B, c.top_k) * nx::kMoePlanInts));
+        NX_TRY(dalloc(m, &m->moe_counter, 64));
         NX_TRY(dalloc(m, &m->moe_act, (size_t)B * c.top_k * m->Fp));
         NX_TRY(dalloc(m, &m->moe_y, (size_t)B * c.top_k * d));
     }
