@@ -350,13 +350,13 @@ __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
 // The MoE block's input and routing in one launch (batch <= 8, E <= 16,
 // d <= 4096, d % 32 == 0).  Block b takes sequence b: the RMSNorm of h[b] to
 // fp16 x (xn16[b], also kept in LDS; hybrid_model.cpp:1647-1655) and the
-// router logits of x (int4-g32 rows of wr: wavefront w takes rows w, w + 4,
+// router logits of x (int4-g32 rows of wr: wavefront w takes rows w, w + 16,
 // ..., its lanes the groups, so every sum has a fixed order).  h and the
 // router rows are requested together up front.  Each block publishes its
 // logits with agent-scope stores, waits for them, and counts itself in
 // *counter; the last block resets the counter and routes every sequence
 // (k_moe_route's routing) from the published logits.
-constexpr int kNrThreads = 256;
+constexpr int kNrThreads = 1024;
 constexpr int kNrWaves = kNrThreads / kWave;
 constexpr int kNrMaxD = 4096;
 constexpr int kNrMaxE = 16;
