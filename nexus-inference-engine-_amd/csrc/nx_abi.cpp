@@ -626,6 +626,9 @@ nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q, nx_buf kc4, nx_buf kc3,
     a.max_blocks = max_blocks;
     a.max_ctx = max_ctx;
     a.part = static_cast<float*>(ctx->attn_ws);
+    s = ensure_attn_counts(ctx, nx::attn_count_words(batch, hkv));
+    if (s != NX_OK) return s;
+    a.counts = ctx->attn_counts;
     return launched(ctx, nx::attn_tq_launch(a, ctx->stream), "attn_tq");
 }
 

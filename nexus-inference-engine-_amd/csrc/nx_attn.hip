@@ -1,23 +1,21 @@
 // Paged decode attention on gfx950 over fp16 pages and TurboQuant pages.
 //
-// Grid (split, kv head, sequence); 4 wavefronts per block.  A block owns a
+// Grid (split, kv head, sequence); 8 wavefronts per block.  A block owns a
 // contiguous range of 16-token pages of one kv head and serves the G = hq/hkv
-// query heads that share it, so every K/V byte is read once per step.
-// Within a wavefront lane l owns dims [l%16 * DPL, +DPL) of the tokens
-// l/16, l/16+4, l/16+8, l/16+12 of each page; a score is reduced over the 16
-// lanes of a DPP row.  A block owns 8 pages (more for very long contexts);
-// each wavefront requests its block-table entries with q and then keeps two
-// pairs of pages in flight.  Each DPP row keeps its own online-softmax state
-// (m, l, o); rows and wavefronts are merged with the usual rescaling and the
-// block stores one split record.  fp16 pages: the last block of a (sequence,
-// kv head) to count itself done merges its split records and writes the fp16
-// output; records and counters use agent-scope (cross-XCD coherent) relaxed
-// accesses, with each block's stores complete before it counts, and no
-// device-scope fence.  TurboQuant pages: a second small launch merges.
+// query heads that share it, so every K/V byte is read once per step.  Each
+// wavefront requests its block-table entries with q and then processes its
+// pages in pairs on the matrix cores (two pairs in flight when it has more
+// than one), keeping an online-softmax state per query head.  Wavefronts are
+// merged through LDS and the block stores one split record; the last block of
+// a (sequence, kv head) to count itself done merges the split records and
+// writes the fp16 output.  Records and counters use agent-scope (cross-XCD
+// coherent) relaxed accesses, with each block's stores complete before it
+// counts, and no device-scope fence.
 //
 // TurboQuant pages are scored in the rotated domain: the block rotates q once
-// (q~ = H D q / sqrt(128)), scores are n_t * <q~, c[code_t]>, V is summed in the
-// rotated domain and rotated back (D H o~ / sqrt(128)) once after the merge.
+// (q~ = H D q), scores are n_t * <q~, c[code_t]> / sqrt(128 * 128), V is summed
+// in the rotated domain and rotated back (D H o~ / sqrt(128)) by the merging
+// block.
 #include "nx_common.h"
 #include "nx_kernels.h"
 
@@ -53,78 +51,6 @@ SplitPlan plan_splits(int max_ctx) {
 // Split partial record, float offsets: O[G][HD] at 0, M[G], L[G], padded to 16 bytes.
 __host__ __device__ constexpr int rec_floats(int G, int HD) { return (G * HD + 2 * G + 3) / 4 * 4; }
 
-
-// Online-softmax state of one lane: G heads x DPL dims.
-template <int G, int DPL>
-struct State {
-    float m[G], l[G], o[G][DPL];
-};
-
-template <int G, int DPL>
-__device__ inline void state_init(State<G, DPL>& s) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        s.m[h] = -__builtin_inff();
-        s.l[h] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) s.o[h][d] = 0.0f;
-    }
-}
-
-// Fold four token scores (per head) and their value rows into the state.
-template <int G, int DPL>
-__device__ inline void state_update(State<G, DPL>& s, const float (&sc)[4][G],
-                                    const float (&v)[4][DPL]) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float mn = s.m[h];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) mn = fmaxf(mn, sc[j][h]);
-        if (mn == -__builtin_inff()) continue;  // nothing valid yet
-        const float corr = __expf(s.m[h] - mn);
-        float p[4], psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            p[j] = __expf(sc[j][h] - mn);
-            psum += p[j];
-        }
-        s.l[h] = s.l[h] * corr + psum;
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) {
-            float acc = s.o[h][d] * corr;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc = fmaf(p[j], v[j][d], acc);
-            s.o[h][d] = acc;
-        }
-        s.m[h] = mn;
-    }
-}
-
-// Lane-wise sum over the four DPP rows (lanes i, i^16, i^32, i^48): every
-// lane ends with the total of its column, in a fixed order.
-__device__ inline float cols4_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
-
-// Merge the four DPP rows of a wavefront; every row ends with the merged state.
-template <int G, int DPL>
-__device__ inline void state_merge_rows(State<G, DPL>& s) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float M = s.m[h];
-        M = fmaxf(M, readlane_f(s.m[h], 0));
-        M = fmaxf(M, readlane_f(s.m[h], 16));
-        M = fmaxf(M, readlane_f(s.m[h], 32));
-        M = fmaxf(M, readlane_f(s.m[h], 48));
-        const float f = (M == -__builtin_inff()) ? 0.0f : __expf(s.m[h] - M);
-        s.l[h] = cols4_sum(s.l[h] * f);
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) s.o[h][d] = cols4_sum(s.o[h][d] * f);
-        s.m[h] = M;
-    }
-}
 
 // Agent-scope (coherent across XCDs) store and load of a split record word,
 // for records handed to the block that merges them within the same launch.
@@ -184,28 +110,6 @@ __device__ inline void merge_waves_store(float* __restrict__ part, const float* 
         else
             part[idx] = acc;
     }
-}
-
-// Block-level merge of the wavefronts' online-softmax states (row layout of
-// the TurboQuant kernel) through LDS, then store this split's record.
-template <int G, int HD>
-__device__ inline void block_merge_store(const State<G, HD / 16>& s, float* __restrict__ part,
-                                         float* lds) {
-    constexpr int DPL = HD / 16, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* my = lds + wave * REC;
-    if (lane < 16) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            if (lane == 0) {
-                my[MO + h] = s.m[h];
-                my[LO + h] = s.l[h];
-            }
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) my[h * HD + lane * DPL + d] = s.o[h][d];
-        }
-    }
-    merge_waves_store<G, HD>(part, lds);
 }
 
 // ------------------------------------------------------------ fp16 pages --
@@ -328,6 +232,31 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
 }
 
 
+// ------------------------------------------------- TurboQuant constants --
+__constant__ float c_tq_c4[16];
+__constant__ float c_tq_b4[15];
+__constant__ float c_tq_c3[8];
+__constant__ float c_tq_b3[7];
+__constant__ float c_tq_cb[24];  // c_tq_c4 then c_tq_c3
+
+// In-LDS FWHT of G vectors of 128 (canonical butterfly network).
+template <int G>
+__device__ inline void lds_fwht(float* v) {
+    for (int h = 1; h < 128; h <<= 1) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < G * 64; t += kAttnThreads) {
+            const int g = t >> 6, k = t & 63;
+            const int j = ((k / h) * 2 * h) + (k % h);
+            const float x = v[g * 128 + j], y = v[g * 128 + j + h];
+            v[g * 128 + j] = x + y;
+            v[g * 128 + j + h] = x - y;
+        }
+    }
+    __syncthreads();
+}
+
+constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
+
 // Run by the last split block of a (sequence, kv head) to finish: merges the
 // nsplit records of its G query heads and writes the fp16 output.  The
 // records were stored by other blocks with agent-scope stores, each complete
@@ -338,7 +267,9 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
 // s = t / NC (mod NG), NG = 256 / NC; it requests all of them at once
 // (16-byte buffer loads with the sc1 bit, skipped past nsplit, where the
 // weight is zero), and the NG partial sums meet in LDS.
-template <int G, int HD>
+// TQ: the merged value sums are in the rotated domain; they are rotated
+// back (o = D_v H o~ / sqrt(128), an FWHT in LDS) before the fp16 output.
+template <int G, int HD, bool TQ = false>
 __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     constexpr int NC = G * HD / 4, NG = kAttnThreads / NC;
@@ -396,8 +327,9 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
     }
     acc4[tid] = make_float4(acc.x, acc.y, acc.z, acc.w);
     __syncthreads();
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < NC) {
-        float4 r = acc4[tid];
+        r = acc4[tid];
         for (int gi = 1; gi < NG; ++gi) {
             const float4 q = acc4[gi * NC + tid];
             r.x += q.x;
@@ -405,9 +337,19 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
             r.z += q.z;
             r.w += q.w;
         }
-        uint16_t* out = a.out16 + ((size_t)b * a.hq + (size_t)kvh * G) * HD + 4 * tid;
-        *reinterpret_cast<uint2*>(out) = make_uint2((uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16),
-                                                    (uint32_t)f2h_bits(r.z) | ((uint32_t)f2h_bits(r.w) << 16));
+    }
+    uint16_t* out = a.out16 + ((size_t)b * a.hq + (size_t)kvh * G) * HD;
+    if constexpr (TQ) {
+        static_assert(HD == 128, "TurboQuant vectors are 128 long");
+        __shared__ float ov[G * HD];
+        if (tid < NC) *reinterpret_cast<float4*>(&ov[4 * tid]) = r;
+        lds_fwht<G>(ov);
+        for (int idx = tid; idx < G * HD; idx += kAttnThreads)
+            out[idx] = f2h_bits(ov[idx] * kTqScale * a.vsign[idx % HD]);
+    } else if (tid < NC) {
+        *reinterpret_cast<uint2*>(out + 4 * tid) =
+            make_uint2((uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16),
+                       (uint32_t)f2h_bits(r.z) | ((uint32_t)f2h_bits(r.w) << 16));
     }
 }
 
@@ -526,54 +468,41 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int ns
 }
 
 // ------------------------------------------------------ TurboQuant pages --
-__constant__ float c_tq_c4[16];
-__constant__ float c_tq_b4[15];
-__constant__ float c_tq_c3[8];
-__constant__ float c_tq_b3[7];
-__constant__ float c_tq_cb[24];  // c_tq_c4 then c_tq_c3
 
-// In-LDS FWHT of G vectors of 128 (canonical butterfly network).
-template <int G>
-__device__ inline void lds_fwht(float* v) {
-    for (int h = 1; h < 128; h <<= 1) {
-        __syncthreads();
-        for (int t = threadIdx.x; t < G * 64; t += kAttnThreads) {
-            const int g = t >> 6, k = t & 63;
-            const int j = ((k / h) * 2 * h) + (k % h);
-            const float x = v[g * 128 + j], y = v[g * 128 + j + h];
-            v[g * 128 + j] = x + y;
-            v[g * 128 + j + h] = x - y;
-        }
-    }
-    __syncthreads();
-}
-
-constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
-
-// One page for one lane (c = l%16, tg = l/16): the codes of dims [8c, 8c+8)
-// of tokens 4tg .. 4tg+3, for K and V, and those tokens' norms.  Lanes c < 8
-// hold 8 4-bit codes in one dword of the 32-byte record; lanes c >= 8 hold 8
-// 3-bit codes, the 3 bytes at 3(c-8) of the 24-byte record, which span at
-// most two dwords (w0, w1; joined with alignbyte once they have arrived).
-struct TqRaw {
-    uint32_t k0[4], k1[4], v0[4], v1[4];
-    uint2 kn, vn;  // fp16 norms of the 4 tokens
+// TurboQuant pages on the matrix cores, in the layouts of the fp16 kernel
+// above.  Records are token-major (a 32-byte 4-bit part: dimensions 0..63 as
+// eight chunks of 8 codes, a 24-byte 3-bit part: dimensions 64..127 as eight
+// chunks of 3 bytes).  The assignment of dimensions to the k slots of the
+// score product and to the output columns of P.V is free, and is chosen so
+// that every operand a lane needs is one or two dwords of a record:
+//   scores S = K q~^T (A = K: row = token t = l%16, k slice g = l/16):
+//     k-step s < 2 takes 4-bit chunk 2g + s (dimensions 16g + 8s .. +7),
+//     s >= 2 the 3-bit chunk 2g + s - 2 (dimensions 64 + 16g + 8(s-2) .. +7);
+//     q~ (B, column = head) is staged in the same order;
+//   P.V (B = V: column n = l%16, k = the pair's tokens 8g + j, j < 4 from page
+//     a, j >= 4 from page b): tile nt holds code nt of chunk n of each token,
+//     so output column n of tile nt is dimension 8n + nt.
+// Codebook values enter as fp16 hi + lo (one LDS word holds both halves), q~
+// and P as hi + lo; three products give fp32-accurate sums.  The V norm is
+// folded into P, the K norm and the scale into the scores.
+struct TqPair {
+    uint2 k4[2], k3[2];           // pages a, b: 4-bit chunks (2g, 2g+1) of token l%16; the 8 bytes holding its 3-bit chunks (2g, 2g+1)
+    uint32_t v0[2][4], v1[2][4];  // pages a, b, tokens 4g + j: the dwords holding chunk l%16
+    uint2 kn[2], vn[2];           // pages a, b: fp16 norms of tokens 4g .. 4g+3
 };
 
-// Lane constants of the code layout: where the lane's first dword of a
-// token's K and V codes lies (record base plus byte offset), distance to the
-// second dword, record stride, and the decode parameters (byte shift, code
-// width, codebook offset).  Computed once, so that a page's addresses are one
-// multiply-add per lane.
+// Lane constants of the V operand (chunk n = l%16): where the chunk's first
+// dword lies in a token's record, the distance to the second, the record
+// stride, and the decode parameters (byte shift, code width, codebook
+// offset).  Chunks n < 8 are one dword of the 4-bit part; chunks n >= 8 are 3
+// bytes of the 3-bit part, at most two dwords.
 struct TqLane {
-    const uint8_t *kb, *vb;
+    const uint8_t* vb;
     int d1, stride, shift, bits, cbo;
-    __device__ TqLane(const AttnArgs& a, int c) {
-        const bool b4 = c < 8;
-        const int j = c - 8;
-        const int off = b4 ? 4 * c : 4 * ((3 * j) >> 2);
-        kb = (b4 ? a.kc4 : a.kc3) + off;
-        vb = (b4 ? a.vc4 : a.vc3) + off;
+    __device__ TqLane(const AttnArgs& a, int n) {
+        const bool b4 = n < 8;
+        const int j = n - 8;
+        vb = (b4 ? a.vc4 : a.vc3) + (b4 ? 4 * n : 4 * ((3 * j) >> 2));
         d1 = b4 ? 0 : 4 * (((3 * j + 2) >> 2) - ((3 * j) >> 2));
         stride = b4 ? 32 : 24;
         shift = b4 ? 0 : (3 * j) & 3;
@@ -582,76 +511,158 @@ struct TqLane {
     }
 };
 
-// Every load is issued unconditionally (see load_pair): blk must be a valid
-// block; tokens past the context are masked when the page is processed.
-__device__ inline void load_page_tq(TqRaw& r, const AttnArgs& a, const TqLane& ln, int blk, int kvh,
-                                    int tg) {
-    const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage + 4 * tg;
-    const size_t cofs = rec * (size_t)ln.stride;
-    const uint8_t* kb = ln.kb + cofs;
-    const uint8_t* vb = ln.vb + cofs;
+// Every load is unconditional (see load_pair): page b with no valid token
+// re-reads page a (blka is a valid block); tokens past the valid counts are
+// masked when the pair is processed.
+__device__ inline void tq_load_pair(TqPair& r, const AttnArgs& a, const TqLane& ln, int blka, int blkb,
+                                    int nb, int kvh, int lane) {
+    const int t = lane & 15, g = lane >> 4;
+    const int o3 = 4 * ((3 * g) >> 1);  // dword holding byte 6g of the 3-bit part
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        r.k0[j] = *reinterpret_cast<const uint32_t*>(kb + j * ln.stride);
-        r.k1[j] = *reinterpret_cast<const uint32_t*>(kb + j * ln.stride + ln.d1);
-        r.v0[j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride);
-        r.v1[j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride + ln.d1);
+    for (int pg = 0; pg < 2; ++pg) {
+        const int blk = pg && nb > 0 ? blkb : blka;
+        const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage;
+        r.k4[pg] = *reinterpret_cast<const uint2*>(a.kc4 + (rec + t) * 32 + 8 * g);
+        r.k3[pg] = *reinterpret_cast<const uint2*>(a.kc3 + (rec + t) * 24 + o3);
+        const uint8_t* vb = ln.vb + (rec + 4 * g) * (size_t)ln.stride;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.v0[pg][j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride);
+            r.v1[pg][j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride + ln.d1);
+        }
+        r.kn[pg] = *reinterpret_cast<const uint2*>(a.kn + rec + 4 * g);
+        r.vn[pg] = *reinterpret_cast<const uint2*>(a.vn + rec + 4 * g);
     }
-    r.kn = *reinterpret_cast<const uint2*>(a.kn + rec);
-    r.vn = *reinterpret_cast<const uint2*>(a.vn + rec);
+    __builtin_amdgcn_sched_barrier(0);
 }
 
-// Codebook values of the lane's 8 codes (cb: 16 4-bit levels, then 8 3-bit).
-__device__ inline void tq_lookup8(uint32_t w0, uint32_t w1, const TqLane& ln, const float* cb,
-                                  float (&out)[8]) {
-    const uint32_t w = __builtin_amdgcn_alignbyte(w1, w0, ln.shift);
+// fp16 hi and lo operands of 8 codes (width `bits`, from bit 0 of w) through
+// the LDS codebook (cbk[cbo + code] = hi | lo << 16).
+__device__ inline void tq_dequant8(uint32_t w, int bits, int cbo, const uint32_t* cbk, h8_t& hi, h8_t& lo) {
+    uint32_t e[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = cb[ln.cbo + __builtin_amdgcn_ubfe(w, ln.bits * i, ln.bits)];
+    for (int i = 0; i < 8; ++i) e[i] = cbk[cbo + __builtin_amdgcn_ubfe(w, bits * i, bits)];
+    uint4 h, l;
+    h.x = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
+    l.x = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
+    h.y = __builtin_amdgcn_perm(e[3], e[2], 0x05040100u);
+    l.y = __builtin_amdgcn_perm(e[3], e[2], 0x07060302u);
+    h.z = __builtin_amdgcn_perm(e[5], e[4], 0x05040100u);
+    l.z = __builtin_amdgcn_perm(e[5], e[4], 0x07060302u);
+    h.w = __builtin_amdgcn_perm(e[7], e[6], 0x05040100u);
+    l.w = __builtin_amdgcn_perm(e[7], e[6], 0x07060302u);
+    hi = as_h8(h);
+    lo = as_h8(l);
 }
 
-// n = valid tokens of the page (0..16).
-template <int G>
-__device__ inline void process_page_tq(State<G, 8>& st, const TqRaw& r, const float (&q)[G][8],
-                                       float scale, int n, int tg, const TqLane& ln, const float* cb) {
-    float vf[4][8];
-    float sc[4][G];
+// Fold one page pair into the wavefront's state (as pair_update: m and lsum
+// of head l%16, O in the C layout with rows = heads 4(l/16) + i, tile nt
+// column n = dimension 8n + nt).  na / nb: valid tokens of the two pages.
+__device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h8_t (&qh)[4], const h8_t (&ql)[4],
+                                      const uint32_t* cbk, float scale, int na, int nb, float& m, float& lsum,
+                                      f4_t (&o)[8], int lane) {
+    const int g = lane >> 4;
+    const int sh3 = 8 * ((6 * g) & 3);
+    f4_t sc[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const bool valid = 4 * tg + j < n;
-        const uint32_t nw = j < 2 ? r.kn.x : r.kn.y, vw = j < 2 ? r.vn.x : r.vn.y;
-        const uint32_t sh = 16 * (j & 1);
-        // the V norm of a token past the context is cleared (its bits may be
-        // anything), so its zero probability meets a finite value
-        const float vn = h2f_bits((uint16_t)((vw >> sh) & (valid ? 0xFFFFu : 0u)));
-        const float kn = h2f_bits((uint16_t)(nw >> sh));
-        float kf[8];
-        tq_lookup8(r.k0[j], r.k1[j], ln, cb, kf);
-        tq_lookup8(r.v0[j], r.v1[j], ln, cb, vf[j]);
+    for (int pg = 0; pg < 2; ++pg) {
+        const uint64_t w3 = ((uint64_t)r.k3[pg].y << 32 | r.k3[pg].x) >> sh3;
+        const uint32_t chunk[4] = {r.k4[pg].x, r.k4[pg].y, (uint32_t)w3 & 0xFFFFFFu, (uint32_t)(w3 >> 24) & 0xFFFFFFu};
+        f4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int d = 0; d < 8; ++d) vf[j][d] *= vn;
+        for (int s = 0; s < 4; ++s) {
+            h8_t kh, kl;
+            tq_dequant8(chunk[s], s < 2 ? 4 : 3, s < 2 ? 0 : 16, cbk, kh, kl);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], acc, 0, 0, 0);
+        }
+        sc[pg] = acc;
+    }
+    // scores of tokens 4g + i: K norm and scale; tokens past the valid counts
+    // get -inf, and their V norms are cleared (a zero probability then meets
+    // a finite value)
+    float p[8];
+    uint32_t vnb[8];
+    float mloc = -__builtin_inff();
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float dot = 0.0f;
+    for (int pg = 0; pg < 2; ++pg) {
+        const int n = pg ? nb : na;
 #pragma unroll
-            for (int d = 0; d < 8; ++d) dot = fmaf(q[h][d], kf[d], dot);
-            dot = row16_sum(dot) * kn * scale;
-            sc[j][h] = valid ? dot : -__builtin_inff();
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t kw = i < 2 ? r.kn[pg].x : r.kn[pg].y, vw = i < 2 ? r.vn[pg].x : r.vn[pg].y;
+            const bool valid = 4 * g + i < n;
+            const float kn = h2f_bits((uint16_t)(kw >> (16 * (i & 1))));
+            const float v = sc[pg][i] * kn * scale;
+            p[4 * pg + i] = valid ? v : -__builtin_inff();
+            vnb[4 * pg + i] = (vw >> (16 * (i & 1))) & (valid ? 0xFFFFu : 0u);
+            mloc = fmaxf(mloc, p[4 * pg + i]);
         }
     }
-    state_update(st, sc, vf);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float mn = fmaxf(m, mloc);
+    const bool none = mn == -__builtin_inff();
+    const float corr = none ? 1.0f : __expf(m - mn);
+    float ps = 0.0f;
+    h8_t ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float e = none ? 0.0f : __expf(p[j] - mn);
+        ps += e;
+        const float ev = e * h2f_bits((uint16_t)vnb[j]);
+        ph[j] = (_Float16)ev;
+        pl[j] = (_Float16)(ev - (float)ph[j]);
+    }
+    lsum = lsum * corr + ps;
+    m = mn;
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = __shfl(corr, 4 * g + i, 64);
+    // V chunk words of the 8 tokens (k = 8g + j)
+    uint32_t vw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        vw[j] = __builtin_amdgcn_alignbyte(r.v1[j >> 2][j & 3], r.v0[j >> 2][j & 3], ln.shift);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+        uint32_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = cbk[ln.cbo + __builtin_amdgcn_ubfe(vw[j], ln.bits * nt, ln.bits)];
+        uint4 h, l;
+        h.x = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
+        l.x = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
+        h.y = __builtin_amdgcn_perm(e[3], e[2], 0x05040100u);
+        l.y = __builtin_amdgcn_perm(e[3], e[2], 0x07060302u);
+        h.z = __builtin_amdgcn_perm(e[5], e[4], 0x05040100u);
+        l.z = __builtin_amdgcn_perm(e[5], e[4], 0x07060302u);
+        h.w = __builtin_amdgcn_perm(e[7], e[6], 0x05040100u);
+        l.w = __builtin_amdgcn_perm(e[7], e[6], 0x07060302u);
+        f4_t acc = o[nt];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= c[i];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, as_h8(h), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, as_h8(h), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, as_h8(l), acc, 0, 0, 0);
+        o[nt] = acc;
+    }
 }
 
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
-    constexpr int HD = 128, DPL = 8, REC = rec_floats(G, HD);
+// One split of one (kv head, sequence) over TurboQuant pages: the page
+// schedule of attn_f16_run (pairs, two in flight when a wavefront has more
+// than one), q rotated once per block (q~ = H D q in LDS); the last block
+// of the (sequence, kv head) merges the records and rotates the value sums
+// back (merge_last<G, 128, true>).
+template <int G, bool PIPE>
+__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
+    constexpr int HD = 128, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int c = lane & 15, tg = lane >> 4;
+    const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
     __shared__ float qrot[G * HD];
-    __shared__ float cb[24];
+    __shared__ uint32_t cbk[24];
 
-    // context length and block-table entries first (see attn_f16_run)
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
@@ -662,13 +673,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
     const int npages = (ctx + kPage - 1) / kPage;
     const int p1 = min(p0 + pps, npages);
     const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
-    // page i of this wavefront; pages past npw re-read the last one (or the
-    // entry of lane 0, a valid block, when there is none) with no valid token
-    auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, max(npw - 1, 0))); };
     auto valid_of = [&](int i) { return i < npw ? min(ctx - (p0 + wave + kAttnWaves * i) * kPage, kPage) : 0; };
-    const TqLane ln(a, c);
-    // q, the K signs and the codebook, one clamped load per value and thread,
-    // then the first two pages: every load is in flight before q is rotated
+    auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
+    const TqLane ln(a, t);
+
+    // q, the K signs and the codebook first (one clamped load per value and
+    // thread), then the first pair of pages: all in flight before q is rotated
     constexpr int QPT = (G * HD + kAttnThreads - 1) / kAttnThreads;
     float qv[QPT], sv[QPT];
 #pragma unroll
@@ -678,11 +688,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
         sv[u] = a.ksign[idx % HD];
     }
     const float cbv = c_tq_cb[min((int)threadIdx.x, 23)];
-    TqRaw a0, a1, b0, b1;
-    load_page_tq(a0, a, ln, blk_of(0), kvh, tg);
-    load_page_tq(a1, a, ln, blk_of(1), kvh, tg);
+    TqPair ra, rb;
+    tq_load_pair(ra, a, ln, blk_of(0), blk_of(1), valid_of(1), kvh, lane);
 
-    if (threadIdx.x < 24) cb[threadIdx.x] = cbv;
+    if (threadIdx.x < 24) {
+        const _Float16 hi = (_Float16)cbv;
+        const _Float16 lo = (_Float16)(cbv - (float)hi);
+        cbk[threadIdx.x] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+    }
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         const int idx = threadIdx.x + u * kAttnThreads;
@@ -690,77 +703,72 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_tq(AttnArgs a, int nsplit
     }
     lds_fwht<G>(qrot);
 
-    const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
-    float q[G][DPL];
+    // q~ as the B operand: column = head t (columns past G repeat head G-1),
+    // k-step s in the dimension order of the K operand
+    h8_t qh[4], ql[4];
+    {
+        const float* qr = qrot + min(t, G - 1) * HD;
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+        for (int s = 0; s < 4; ++s) {
+            const int d0 = (s < 2 ? 0 : 64) + 16 * g + 8 * (s & 1);
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) q[h][d] = qrot[h * HD + c * DPL + d];
-
-    State<G, DPL> st;
-    state_init(st);
-    // two pairs of pages in flight; both pairs are requested on every pass
-    // (past the last page they re-read it), and only the processing of a
-    // pair with no page is skipped, a branch with no load in it
-    for (int i = 0; i < npw; i += 4) {
-        load_page_tq(b0, a, ln, blk_of(i + 2), kvh, tg);
-        load_page_tq(b1, a, ln, blk_of(i + 3), kvh, tg);
-        process_page_tq<G>(st, a0, q, scale, valid_of(i), tg, ln, cb);
-        if (i + 1 < npw) process_page_tq<G>(st, a1, q, scale, valid_of(i + 1), tg, ln, cb);
-        load_page_tq(a0, a, ln, blk_of(i + 4), kvh, tg);
-        load_page_tq(a1, a, ln, blk_of(i + 5), kvh, tg);
-        if (i + 2 < npw) process_page_tq<G>(st, b0, q, scale, valid_of(i + 2), tg, ln, cb);
-        if (i + 3 < npw) process_page_tq<G>(st, b1, q, scale, valid_of(i + 3), tg, ln, cb);
-    }
-    state_merge_rows(st);
-
-    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    block_merge_store<G, HD>(st, parts + (size_t)split * REC, lds);
-}
-
-// Merge the split records of one query head: block (h, kv head, sequence),
-// one thread per dimension.  Every thread requests its nsplit partial sums at
-// once, and lane s of every wavefront the maximum and denominator of split s
-// (nsplit <= 64), so the split weights exp(m_s - M) and the denominator come
-// from wavefront reductions with no LDS round trip; the weighted sum reads
-// each weight from its lane.  TQ: the merged value sum is still in the
-// rotated domain and is rotated back once, o = D_v H o~ / sqrt(128).
-template <int G, int HD, bool TQ>
-__global__ __launch_bounds__(HD) void k_attn_merge(AttnArgs a, int nsplit) {
-    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    static_assert(kMaxSplits <= kWave, "one split per lane");
-    const int h = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
-    const int lane = t & (kWave - 1);
-    const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    float o[kMaxSplits];
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) o[s] = s < nsplit ? parts[(size_t)s * REC + h * HD + t] : 0.0f;
-    const float ms = lane < nsplit ? parts[(size_t)lane * REC + MO + h] : -__builtin_inff();
-    const float ls = lane < nsplit ? parts[(size_t)lane * REC + LO + h] : 0.0f;
-    const float M = wave_max(ms);
-    const float f = (lane >= nsplit || M == -__builtin_inff()) ? 0.0f : __expf(ms - M);
-    const float L = wave_sum(f * ls);
-    float acc = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s)
-        if (s < nsplit) acc = fmaf(o[s], readlane_f(f, s), acc);
-    if (TQ) {
-        __shared__ float ov[HD];
-        ov[t] = acc;
-        for (int hh = 1; hh < HD; hh <<= 1) {
-            __syncthreads();
-            if (t < HD / 2) {
-                const int j = ((t / hh) * 2 * hh) + (t % hh);
-                const float x = ov[j], y = ov[j + hh];
-                ov[j] = x + y;
-                ov[j + hh] = x - y;
+            for (int j = 0; j < 8; ++j) {
+                const float v = qr[d0 + j];
+                qh[s][j] = (_Float16)v;
+                ql[s][j] = (_Float16)(v - (float)qh[s][j]);
             }
         }
-        __syncthreads();
-        acc = ov[t] * kTqScale * a.vsign[t];
     }
-    const float out = L > 0.0f ? acc / L : 0.0f;
-    a.out16[((size_t)b * a.hq + kvh * G + h) * HD + t] = f2h_bits(out);
+    const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
+
+    float m = -__builtin_inff(), lsum = 0.0f;
+    f4_t o[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (PIPE) {
+        // the next pair is requested unconditionally (a pair past the
+        // wavefront's pages re-reads its first page and is not processed), so
+        // the wait for the current pair leaves the next one in flight
+        auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
+        for (int i = 0; i < npw; i += 4) {
+            tq_load_pair(rb, a, ln, blk_or0(i + 2), blk_or0(i + 3), valid_of(i + 3), kvh, lane);
+            tq_pair_update(ra, ln, qh, ql, cbk, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
+            if (i + 2 >= npw) break;
+            tq_load_pair(ra, a, ln, blk_or0(i + 4), blk_or0(i + 5), valid_of(i + 5), kvh, lane);
+            tq_pair_update(rb, ln, qh, ql, cbk, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
+        }
+    } else {
+        if (npw > 0) tq_pair_update(ra, ln, qh, ql, cbk, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
+    }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    // wavefront record: rows h = 4g + i < G of O (column t of tile nt is
+    // dimension 8t + nt), m / l of head t
+    float* my = lds + wave * REC;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * g + i < G) my[(4 * g + i) * HD + 8 * t + nt] = o[nt][i];
+    if (g == 0 && t < G) {
+        my[MO + t] = m;
+        my[LO + t] = lsum;
+    }
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
+    merge_waves_store<G, HD, true>(parts + (size_t)split * REC, lds);
+    // as attn_f16_run: the record is stored before the block counts itself;
+    // the last of the nsplit blocks merges, rotates back and resets the counter
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int last;
+    if (threadIdx.x == 0) {
+        unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
+        const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == (unsigned)nsplit - 1u;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (last) merge_last<G, HD, true>(a, nsplit, kvh, b);
 }
 
 // ----------------------------------------------------- TurboQuant encode --
@@ -913,17 +921,33 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     return hipErrorInvalidValue;
 }
 
+// TurboQuant splits: about one block per CU over all (kv head, sequence)
+// pairs (the pipelined kernel holds one 8-wavefront block per CU), never
+// more splits than plan_splits (which sizes the workspace).
+SplitPlan plan_splits_tq(int max_ctx, int hkv, int batch) {
+    const SplitPlan base = plan_splits(max_ctx);
+    const int pages = (max_ctx + kPage - 1) / kPage;
+    const int want = (device_cus() + hkv * batch - 1) / (hkv * batch);
+    int nsplit = min(base.nsplit, max(want, 1));
+    const int pps = min(max((pages + nsplit - 1) / nsplit, 1), kPagesPerSplitMax);
+    nsplit = max((pages + pps - 1) / pps, 1);
+    return {nsplit, pps};
+}
+
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st) {
-    const SplitPlan sp = plan_splits(a.max_ctx);
-    const dim3 grid(sp.nsplit, a.hkv, a.batch), mgrid(a.hq / a.hkv, a.hkv, a.batch);
+    if (!a.counts || !a.part) return hipErrorInvalidValue;
+    const SplitPlan sp = plan_splits_tq(a.max_ctx, a.hkv, a.batch);
+    const dim3 grid(sp.nsplit, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
     if (a.hd != 128) return hipErrorInvalidValue;
 #define NX_ATTN_CASE(GG)                                                                          \
     if (G == GG) {                                                                                \
-        hipLaunchKernelGGL((k_attn_tq<GG>), grid, dim3(kAttnThreads), 0, st, a, sp.nsplit,        \
-                           sp.pps);                                                               \
-        hipLaunchKernelGGL((k_attn_merge<GG, 128, true>), mgrid, dim3(128), 0, st, a,             \
-                           sp.nsplit);                                                            \
+        if (sp.pps > kPagesPerSplitMin)                                                           \
+            hipLaunchKernelGGL((k_attn_tq<GG, true>), grid, dim3(kAttnThreads), 0, st, a,          \
+                               sp.nsplit, sp.pps);                                                \
+        else                                                                                      \
+            hipLaunchKernelGGL((k_attn_tq<GG, false>), grid, dim3(kAttnThreads), 0, st, a,         \
+                               sp.nsplit, sp.pps);                                                \
         return hipGetLastError();                                                                 \
     }
     NX_ATTN_CASE(1)

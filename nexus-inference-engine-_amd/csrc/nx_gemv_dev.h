@@ -659,19 +659,6 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
 }
 
 
-// Compute units of the current device (cached per device).
-inline int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
 
 // Default wavefronts per CU of the batch-1 GEMV: two per SIMD.
 constexpr int kB1WavesPerCU = 8;
