@@ -411,15 +411,17 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
 #pragma unroll
     for (int nt = 0; nt < HD / 16; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
     if constexpr (PIPE) {
+        // every pair is requested unconditionally (a pair past the
+        // wavefront's pages re-reads its first page and is not processed), so
+        // the wait for the current pair leaves the next one in flight
+        auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
         PairRaw<HD> ra, rb;
-        if (npw > 0) load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
+        load_pair<HD>(ra, a, blk_or0(0), valid_of(0), blk_or0(1), valid_of(1), kvh, lane);
         for (int i = 0; i < npw; i += 4) {
-            if (i + 2 < npw)
-                load_pair<HD>(rb, a, blk_of(i + 2), valid_of(i + 2), blk_of(i + 3), valid_of(i + 3), kvh, lane);
+            load_pair<HD>(rb, a, blk_or0(i + 2), valid_of(i + 2), blk_or0(i + 3), valid_of(i + 3), kvh, lane);
             pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
             if (i + 2 >= npw) break;
-            if (i + 4 < npw)
-                load_pair<HD>(ra, a, blk_of(i + 4), valid_of(i + 4), blk_of(i + 5), valid_of(i + 5), kvh, lane);
+            load_pair<HD>(ra, a, blk_or0(i + 4), valid_of(i + 4), blk_or0(i + 5), valid_of(i + 5), kvh, lane);
             pair_update<HD>(rb, qh, ql, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
         }
     } else {
@@ -893,9 +895,31 @@ size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
 
 int attn_max_ctx() { return kMaxSplits * kPagesPerSplitMax * kPage; }
 
+// TurboQuant splits: about one block per CU over all (kv head, sequence)
+// pairs (the pipelined kernel holds one 8-wavefront block per CU), never
+// more splits than plan_splits (which sizes the workspace).
+SplitPlan plan_splits_tq(int max_ctx, int hkv, int batch) {
+    const SplitPlan base = plan_splits(max_ctx);
+    const int pages = (max_ctx + kPage - 1) / kPage;
+    const int want = (device_cus() + hkv * batch - 1) / (hkv * batch);
+    int nsplit = min(base.nsplit, max(want, 1));
+    const int pps = min(max((pages + nsplit - 1) / nsplit, 1), kPagesPerSplitMax);
+    nsplit = max((pages + pps - 1) / pps, 1);
+    return {nsplit, pps};
+}
+
+// fp16 splits: plan_splits, unless its grid would exceed one block per CU
+// (batched decode); then the TurboQuant plan's larger splits, so a single
+// round of blocks streams with two pairs in flight per wavefront.
+SplitPlan plan_splits_f16(int max_ctx, int hkv, int batch) {
+    const SplitPlan base = plan_splits(max_ctx);
+    if ((long)base.nsplit * hkv * batch <= device_cus()) return base;
+    return plan_splits_tq(max_ctx, hkv, batch);
+}
+
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     if (!a.counts || !a.part) return hipErrorInvalidValue;
-    const SplitPlan sp = plan_splits(a.max_ctx);
+    const SplitPlan sp = plan_splits_f16(a.max_ctx, a.hkv, a.batch);
     const dim3 grid(sp.nsplit, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
     const bool pipe = sp.pps > kPagesPerSplitMin;
@@ -919,19 +943,6 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     NX_ATTN_CASE(8, 128)
 #undef NX_ATTN_CASE
     return hipErrorInvalidValue;
-}
-
-// TurboQuant splits: about one block per CU over all (kv head, sequence)
-// pairs (the pipelined kernel holds one 8-wavefront block per CU), never
-// more splits than plan_splits (which sizes the workspace).
-SplitPlan plan_splits_tq(int max_ctx, int hkv, int batch) {
-    const SplitPlan base = plan_splits(max_ctx);
-    const int pages = (max_ctx + kPage - 1) / kPage;
-    const int want = (device_cus() + hkv * batch - 1) / (hkv * batch);
-    int nsplit = min(base.nsplit, max(want, 1));
-    const int pps = min(max((pages + nsplit - 1) / nsplit, 1), kPagesPerSplitMax);
-    nsplit = max((pages + pps - 1) / pps, 1);
-    return {nsplit, pps};
 }
 
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st) {
