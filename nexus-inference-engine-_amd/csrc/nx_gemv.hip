@@ -29,6 +29,8 @@
 // and the paged KV append, SwiGLU of interleaved gate/up rows, or logits
 // with a running argmax.  The input is either fp16 x or the fused RMSNorm of
 // an fp32 hidden state, computed once per block into LDS.
+#include <algorithm>
+
 #include "nx_gemv_dev.h"
 
 namespace nx {
@@ -223,29 +225,34 @@ struct MfmaRegs {
     uint32_t sc[kMfmaGW / 2];  // fp16 scale pairs (groups 2u, 2u+1) of the lane's weight row
 };
 
+// keep = 0: a request with no use (past the block's last tile); every lane
+// then reads the first 16 bytes of row min(row0, N-1) of the stage, one cache
+// line.
 template <bool SALIGN>
-__device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs, int ge, MfmaRegs& r) {
+__device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs, int ge, MfmaRegs& r,
+                                 int keep = 1) {
     const int lane = threadIdx.x & (kWave - 1), c = lane & 15, kq = lane >> 4;
     const int G = a.G;
     const int gl = ge - 1;  // last group of the stage (ge == stage groups when the wavefront has none)
-    const size_t row = (size_t)min(row0 + c, a.N - 1);
+    const size_t row = (size_t)min(row0 + c * keep, a.N - 1);
     const uint16_t* srow = a.S + row * G + gbase;
     if (SALIGN) {
 #pragma unroll
         for (int u4 = 0; u4 < kMfmaGW / 4; ++u4) {
-            const uint2 v = *reinterpret_cast<const uint2*>(srow + min(gs + 4 * u4, gl & ~3));
+            const uint2 v = *reinterpret_cast<const uint2*>(srow + min(gs + 4 * u4, gl & ~3) * keep);
             r.sc[2 * u4] = v.x;
             r.sc[2 * u4 + 1] = v.y;
         }
     } else {
 #pragma unroll
         for (int u2 = 0; u2 < kMfmaGW / 2; ++u2)
-            r.sc[u2] = (uint32_t)srow[min(gs + 2 * u2, gl)] | ((uint32_t)srow[min(gs + 2 * u2 + 1, gl)] << 16);
+            r.sc[u2] = (uint32_t)srow[min(gs + 2 * u2, gl) * keep] |
+                       ((uint32_t)srow[min(gs + 2 * u2 + 1, gl) * keep] << 16);
     }
-    const uint8_t* wrow = a.W + row * G * 16;
+    const uint8_t* wrow = a.W + row * G * 16 + (size_t)gbase * 16;
 #pragma unroll
     for (int u4 = 0; u4 < kMfmaGW / 4; ++u4)
-        r.code[u4] = *reinterpret_cast<const uint4*>(wrow + (size_t)(gbase + min(gs + 4 * u4 + kq, gl)) * 16);
+        r.code[u4] = *reinterpret_cast<const uint4*>(wrow + (size_t)(min(gs + 4 * u4 + kq, gl) * keep) * 16);
 }
 
 // 4 x 4 exchange across the 16-lane rows: on entry lane row r holds the four
@@ -299,16 +306,19 @@ __device__ inline void mfma_compute(const MfmaRegs& r, const uint4 (&xv)[kMfmaGW
 }
 
 template <int XS, int EPI, bool XVEC, bool SALIGN, bool MOE = false>
-__global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, int tpb) {
+__global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, int nb, int ks) {
     __shared__ __align__(16) uint4 xs[kMfmaGC * 4 * kMfmaCols];
-    __shared__ __align__(16) float part[2][kMfmaWaves * 16 * 16];  // [wave][weight row][batch row]
+    __shared__ __align__(16) float part[2][kMfmaWaves * 16 * kMfmaCols];  // [wave][weight row][batch row]
     __shared__ float inv[kMfmaCols];
     __shared__ float red[kMfmaWaves][kMfmaCols];
     __shared__ unsigned long long bk[kMfmaThreads];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
     const int N = args.N, K = args.K;
-    const int ntile = (N + 15) / 16, t0 = blockIdx.x * tpb, nt = min(tpb, ntile - t0);
+    // the nb blocks of a grid row share the tiles evenly: block x takes
+    // [x ntile / nb, (x + 1) ntile / nb), at most tpb tiles
+    const int ntile = (N + 15) / 16, tpb = (ntile + nb - 1) / nb;
+    const int t0 = (int)((long)blockIdx.x * ntile / nb), nt = (int)((long)(blockIdx.x + 1) * ntile / nb) - t0;
     if (nt <= 0) return;
     static_assert(!MOE || XS == X_F16, "routed experts take fp16 x");
     GemvArgs a = args;
@@ -362,41 +372,80 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     // the barrier wavefront t % 8 adds them, lane (c, kq) taking batch row c
     // and weight rows 4kq..+3, and runs the epilogue
     auto finish = [&](int t, int row0, const mf4_t& acc) {
-        *reinterpret_cast<float4*>(&part[t & 1][(wave * 16 + c) * 16 + 4 * kq]) =
-            make_float4(acc[0], acc[1], acc[2], acc[3]);
+        if (kq < 2)  // lanes kq >= 2 hold batch rows 8..15, which repeat 0..7
+            *reinterpret_cast<float4*>(&part[t & 1][(wave * 16 + c) * kMfmaCols + 4 * kq]) =
+                make_float4(acc[0], acc[1], acc[2], acc[3]);
         __syncthreads();
         if (wave == (t & (kMfmaWaves - 1)) && c < a.batch) {
             float res[4] = {0.f, 0.f, 0.f, 0.f};
             for (int w = 0; w < kMfmaWaves; ++w)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) res[i] += part[t & 1][(w * 16 + 4 * kq + i) * 16 + c];
+                for (int i = 0; i < 4; ++i) res[i] += part[t & 1][(w * 16 + 4 * kq + i) * kMfmaCols + c];
             epilogue<EPI, 4>(a, yrow, row0 + 4 * kq, N, res, best_v, best_i);
         }
     };
     if (nstage == 1) {
-        // x stays in registers for all tiles, and the next tile's codes and
-        // scales are requested before the current tile is computed (two
-        // register sets used alternately; the request after the block's last
-        // tile re-reads that tile)
-        const int ge = min((K + 31) / 32, gs + kMfmaGW);
-        const int rlast = (t0 + nt - 1) * 16;
-        uint4 xv[kMfmaGW];
-        mfma_load_x(xs, gs, ge, xv);
-        MfmaRegs ra, rb;
-        mfma_load<SALIGN>(a, t0 * 16, 0, gs, ge, ra);
-        for (int t = 0; t < nt; t += 2) {
-            const int row0 = (t0 + t) * 16;
-            mfma_load<SALIGN>(a, min(row0 + 16, rlast), 0, gs, ge, rb);
-            mf4_t acc = {0.f, 0.f, 0.f, 0.f};
-            mfma_compute(ra, xv, gs, ge, acc);
-            finish(t, row0, acc);
-            if (t + 1 < nt) {
-                mfma_load<SALIGN>(a, min(row0 + 32, rlast), 0, gs, ge, ra);
-                mf4_t acc2 = {0.f, 0.f, 0.f, 0.f};
-                mfma_compute(rb, xv, gs, ge, acc2);
-                finish(t + 1, row0 + 16, acc2);
+        // A tile is split over ks wavefronts along K (ks = 1 for large N).
+        // Wavefront (tsub, kslice) = (wave / ks, wave % ks) takes tiles
+        // t0 + tsub + (8 / ks) i and, of each, the groups of its K slice in
+        // passes of 16; it streams these (tile, pass) items with the next
+        // item requested before the current one is computed.  Only at a
+        // tile's end do the wavefronts meet: partial sums go to LDS and, after
+        // the barrier, wavefront kslice 0 of each tile adds them and runs the
+        // epilogue.  (A barrier per pass made every wavefront wait for the
+        // others' prefetched data, which a CU returns in request order.)
+        // The item loop takes whole pairs with no exit inside, so each
+        // request it carries across the back edge is consumed in the next
+        // pass and the compiler's waits stay exact.
+        const int G = a.G, wpt = kMfmaWaves / ks, kslice = wave % ks, tsub = wave / ks;
+        const int gps = ((G + ks - 1) / ks + kMfmaGW - 1) / kMfmaGW * kMfmaGW, npass = gps / kMfmaGW;
+        const int iters = (tpb + wpt - 1) / wpt, nitem = iters * npass;
+        auto item_tile = [&](int j) { return t0 + tsub + wpt * (j / npass); };
+        auto item_gs = [&](int j) { return kslice * gps + kMfmaGW * (j % npass); };
+        auto load_item = [&](int j, MfmaRegs& r) {
+            const int gs = item_gs(j), keep = j < nitem && item_tile(j) < t0 + nt ? 1 : 0;
+            mfma_load<SALIGN>(a, item_tile(j) * 16, 0, gs, min(G, gs + kMfmaGW), r, keep);
+        };
+        auto tile_end = [&](int j, const mf4_t& acc) {
+            const int slot = (j / npass) & 1, t = item_tile(j);
+            if (kq < 2)
+                *reinterpret_cast<float4*>(&part[slot][(wave * 16 + c) * kMfmaCols + 4 * kq]) =
+                    make_float4(acc[0], acc[1], acc[2], acc[3]);
+            __syncthreads();
+            if (kslice == 0 && c < a.batch && t < t0 + nt) {
+                float res[4] = {0.f, 0.f, 0.f, 0.f};
+                for (int s2 = 0; s2 < ks; ++s2)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        res[i] += part[slot][((tsub * ks + s2) * 16 + 4 * kq + i) * kMfmaCols + c];
+                epilogue<EPI, 4>(a, yrow, t * 16 + 4 * kq, N, res, best_v, best_i);
             }
+        };
+        mf4_t acc = {0.f, 0.f, 0.f, 0.f};
+        auto step = [&](int j, const MfmaRegs& r) {
+            const int gs = item_gs(j), ge = min(G, gs + kMfmaGW);
+            uint4 xv[kMfmaGW];
+            mfma_load_x(xs, min(gs, G - 1), ge, xv);
+            mfma_compute(r, xv, gs, ge, acc);
+            if (j % npass == npass - 1) {
+                tile_end(j, acc);
+                acc = mf4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        };
+        MfmaRegs ra, rb;
+        load_item(0, ra);
+        int j = 0;
+        for (; j + 1 < nitem; j += 2) {
+            load_item(j + 1, rb);
+            // the next item's requests stay ahead of this item's first use (the
+            // scheduler would otherwise hoist the use, which then waits for all)
+            __builtin_amdgcn_sched_barrier(0);
+            step(j, ra);
+            load_item(j + 2, ra);
+            __builtin_amdgcn_sched_barrier(0);
+            step(j + 1, rb);
         }
+        if (j < nitem) step(j, ra);
     } else {
         // K in several stages: x restaged per stage
         for (int t = 0; t < nt; ++t) {
@@ -453,20 +502,28 @@ hipError_t launch_b1(const GemvArgs& a, hipStream_t st, int ny = 1) {
     return hipGetLastError();
 }
 
-// Batch 2..8 on the matrix cores: whole tiles per block, one tile per block
-// when K takes more than one stage.
+// Batch 2..8 on the matrix cores.  One stage (K <= 4096): ks wavefronts per
+// tile, the fewest that still give every wavefront of one block per CU a
+// tile, and enough tiles per block for one round of blocks.  Several stages:
+// one tile per block.
 // MOE: ny grid rows of routed experts share the CUs.
 template <int XS, int EPI, bool MOE = false>
 hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
     const int ntile = (a.N + 15) / 16, cus = device_cus();
-    const int tpb = a.K <= kMfmaKC ? (ntile * ny + cus - 1) / cus : 1;
-    const int blocks = (ntile + tpb - 1) / tpb;
+    int blocks = ntile, ks = 1;
+    if (a.K <= kMfmaKC) {
+        // one round: the grid rows (experts) share the CUs, a block's tiles
+        // are an even share of its row's
+        blocks = std::max(1, std::min(ntile, (cus + ny - 1) / ny));
+        const int per_block = (ntile + blocks - 1) / blocks;
+        ks = per_block <= 1 ? 8 : per_block <= 2 ? 4 : per_block <= 4 ? 2 : 1;
+    }
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       a.ldx % (XS == X_F16 ? 8 : 4) == 0;
     const bool salign = a.G % 4 == 0;
 #define NX_MFMA(XV, SA) \
-    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA, MOE>), dim3(blocks, ny), dim3(kMfmaThreads), 0, st, a, tpb)
+    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA, MOE>), dim3(blocks, ny), dim3(kMfmaThreads), 0, st, a, blocks, ks)
     if (xvec && salign) NX_MFMA(true, true);
     else if (xvec) NX_MFMA(true, false);
     else if (salign) NX_MFMA(false, true);
