@@ -215,6 +215,8 @@ typedef struct {
     float rope_theta;
     float eps;
     uint64_t seed;
+    float norm_sigma;       /* RMSNorm weights: 0 = all 1.0, else 1 + N(0, norm_sigma)
+                               seeded per tensor (synthetic models) */
 } nx_model_config;
 
 typedef struct nx_model nx_model;

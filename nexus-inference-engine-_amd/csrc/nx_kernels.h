@@ -222,4 +222,13 @@ hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st);
 
+// XXH32 (seed 0) of byte ranges of one device buffer: range i is
+// [off, off + len) (off a multiple of 16); its hash goes to out[slot].
+struct HashRange {
+    uint64_t off;
+    uint32_t len;
+    uint32_t slot;
+};
+hipError_t xxh32_launch(const uint8_t* data, const HashRange* ranges, int n, uint32_t* out, hipStream_t st);
+
 }  // namespace nx

@@ -8,11 +8,14 @@
 // consecutive steps run back to back with no host round trip.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <functional>
+#include <string>
 #include <vector>
 
+#include "../../include/nexus_nxf.h"
 #include "nx_common.h"
 #include "nx_internal.h"
 #include "nx_kernels.h"
@@ -37,6 +40,8 @@ struct Layer {
     uint16_t *kn = nullptr, *vn = nullptr;
     float *ksign = nullptr, *vsign = nullptr;
     int32_t* moe_count = nullptr;  // [E]
+    float* norm_attn = nullptr;    // RMSNorm weights [d]; nullptr = 1.0
+    float* norm_ffn = nullptr;
 };
 
 size_t qbytes(size_t N, int K) { return N * (size_t)((K + 31) / 32) * 18; }
@@ -51,6 +56,7 @@ struct nx_model {
     uint16_t* embed = nullptr;
     uint8_t* lm_w = nullptr;
     uint16_t* lm_s = nullptr;
+    float* norm_final = nullptr;  // final RMSNorm weights [d]; nullptr = 1.0
     std::vector<Layer> layers;
     float *rope_cos = nullptr, *rope_sin = nullptr;
     int max_blocks = 0, n_blocks = 0;
@@ -126,8 +132,22 @@ nx_status generate_weights(nx_model* m) {
     const int d = c.d_model, F = c.ffn, E = c.n_experts;
     NX_LAUNCH(m, nx::gen_f16_launch(m->embed, (size_t)c.vocab * d, seed, nx::kTidEmbed, k02, st));
     NX_LAUNCH(m, nx::gen_quant_launch(m->lm_w, m->lm_s, c.vocab, d, seed, nx::kTidLmHead, k02, 0, 1, st));
+    // RMSNorm weights 1 + N(0, norm_sigma), generated on the host
+    auto gen_norm = [&](float* dst, uint32_t tid) -> nx_status {
+        if (!dst) return NX_OK;
+        std::vector<float> w((size_t)d);
+        const uint64_t key = nx::stream_key(seed, tid);
+        const float kn = nx::normal_k((double)c.norm_sigma);
+        for (int i = 0; i < d; ++i) w[(size_t)i] = 1.0f + nx::normal_from(nx::rand_at(key, (uint64_t)i), kn);
+        NX_HIP(m->ctx, hipMemcpyAsync(dst, w.data(), w.size() * 4, hipMemcpyHostToDevice, st));
+        NX_HIP(m->ctx, hipStreamSynchronize(st));  // w is released on return
+        return NX_OK;
+    };
+    NX_TRY(gen_norm(m->norm_final, nx::kTidFinalNorm));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
+        NX_TRY(gen_norm(ly.norm_attn, nx::tid_layer(L, nx::N_ATTN)));
+        NX_TRY(gen_norm(ly.norm_ffn, nx::tid_layer(L, nx::N_FFN)));
         NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->qdim, d, seed, nx::tid_layer(L, nx::W_Q), k02, 0, 1, st));
         NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->kvdim, d, seed, nx::tid_layer(L, nx::W_K), k02, m->qdim, 1, st));
         NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->kvdim, d, seed, nx::tid_layer(L, nx::W_V), k02,
@@ -170,6 +190,7 @@ nx_status enqueue_step(nx_model* m) {
         a.h32 = m->h;
         a.ldx = d;
         a.eps = c.eps;
+        a.norm_w = ly.norm_attn;
         a.q32 = m->q;
         a.qdim = m->qdim;
         a.kvdim = m->kvdim;
@@ -242,6 +263,7 @@ nx_status enqueue_step(nx_model* m) {
             f.h32 = m->h;
             f.ldx = d;
             f.eps = c.eps;
+            f.norm_w = ly.norm_ffn;
             f.act16 = m->act16;
             f.lda = m->Fp;
             NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
@@ -272,6 +294,7 @@ nx_status enqueue_step(nx_model* m) {
                 // RMSNorm, router and routing in one launch
                 ma.h = m->h;
                 ma.eps = c.eps;
+                ma.norm_w = ly.norm_ffn;
                 ma.d = d;
                 ma.wr = ly.wr;
                 ma.sr = ly.sr;
@@ -279,7 +302,7 @@ nx_status enqueue_step(nx_model* m) {
                 ma.counter = m->moe_counter;
                 NX_LAUNCH(m, nx::moe_norm_route_launch(ma, st));
             } else {
-                NX_LAUNCH(m, nx::rmsnorm_launch(m->h, nullptr, m->xn16, d, c.eps, B, st));
+                NX_LAUNCH(m, nx::rmsnorm_launch(m->h, ly.norm_ffn, m->xn16, d, c.eps, B, st));
                 nx::GemvArgs r{};
                 r.W = ly.wr;
                 r.S = ly.sr;
@@ -328,6 +351,7 @@ nx_status enqueue_step(nx_model* m) {
     lm.h32 = m->h;
     lm.ldx = d;
     lm.eps = c.eps;
+    lm.norm_w = m->norm_final;
     lm.y32 = m->logits;
     lm.ldy = c.vocab;
     lm.best = m->best;
@@ -378,7 +402,9 @@ nx_status free_model(nx_model* m) {
     return NX_OK;
 }
 
-nx_status create_impl(nx_model* m) {
+// Allocate the model; synthetic: generate the weights from the seed,
+// otherwise leave them for the loader (norm weights always allocated).
+nx_status create_impl(nx_model* m, bool synthetic) {
     const nx_model_config& c = m->c;
     const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts, L = c.n_layers;
     m->qdim = c.n_heads * c.head_dim;
@@ -397,6 +423,8 @@ nx_status create_impl(nx_model* m) {
     NX_TRY(dalloc(m, &m->embed, (size_t)c.vocab * d));
     NX_TRY(dalloc(m, &m->lm_w, (size_t)c.vocab * m->Gd * 16));
     NX_TRY(dalloc(m, &m->lm_s, (size_t)c.vocab * m->Gd));
+    const bool norms = !synthetic || c.norm_sigma != 0.0f;
+    if (norms) NX_TRY(dalloc(m, &m->norm_final, (size_t)d));
     const size_t pool_elems = (size_t)m->n_blocks * c.n_kv_heads * nx::kPage * c.head_dim;
     const size_t pool_vecs = (size_t)m->n_blocks * c.n_kv_heads * nx::kPage;
     for (int l = 0; l < L; ++l) {
@@ -410,6 +438,10 @@ nx_status create_impl(nx_model* m) {
         NX_TRY(dalloc(m, &ly.s13, ne * 2 * F * m->Gd));
         NX_TRY(dalloc(m, &ly.w2, ne * d * m->Gf * 16));
         NX_TRY(dalloc(m, &ly.s2, ne * d * m->Gf));
+        if (norms) {
+            NX_TRY(dalloc(m, &ly.norm_attn, (size_t)d));
+            NX_TRY(dalloc(m, &ly.norm_ffn, (size_t)d));
+        }
         if (E > 0) {
             NX_TRY(dalloc(m, &ly.wr, (size_t)E * m->Gd * 16));
             NX_TRY(dalloc(m, &ly.sr, (size_t)E * m->Gd));
@@ -494,7 +526,7 @@ nx_status create_impl(nx_model* m) {
     }
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_stage, sizeof(int32_t) * B, hipHostMallocDefault));
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_out, sizeof(int32_t) * (size_t)B * m->out_stride, hipHostMallocDefault));
-    NX_TRY(generate_weights(m));
+    if (synthetic) NX_TRY(generate_weights(m));
     NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     return NX_OK;
 }
@@ -502,7 +534,8 @@ nx_status create_impl(nx_model* m) {
 nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.n_layers < 1 || c.d_model < 32 || c.n_heads < 1 || c.n_kv_heads < 1 || c.n_heads % c.n_kv_heads ||
         c.ffn < 2 || c.vocab < 2 || c.max_seq < nx::kPage || c.max_seq % nx::kPage || c.batch < 1 || c.batch > 8 ||
-        (c.kv_kind != 0 && c.kv_kind != 1) || c.eps <= 0.0f || c.rope_theta <= 0.0f)
+        (c.kv_kind != 0 && c.kv_kind != 1) || c.eps <= 0.0f || c.rope_theta <= 0.0f ||
+        !(c.norm_sigma >= 0.0f && c.norm_sigma < 1e3f))
         return fail(ctx, NX_ERR_INVALID, "nx_model_create: invalid configuration");
     const int G = c.n_heads / c.n_kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return fail(ctx, NX_ERR_UNSUPPORTED, "hq/hkv must be 1, 2, 4 or 8");
@@ -529,7 +562,7 @@ nx_status nx_model_create(nx_ctx* ctx, const nx_model_config* cfg, nx_model** ou
     nx_model* m = new nx_model();
     m->ctx = ctx;
     m->c = *cfg;
-    nx_status s = create_impl(m);
+    nx_status s = create_impl(m, true);
     if (s != NX_OK) {
         free_model(m);
         return s;
@@ -735,6 +768,7 @@ nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double*
             f.h32 = m->h;
             f.ldx = c.d_model;
             f.eps = c.eps;
+            f.norm_w = ly.norm_ffn;
             f.act16 = m->act16;
             f.lda = m->Fp;
             return nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st);
@@ -837,6 +871,342 @@ nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double
         for (int b = 0; b < c.batch; ++b) kv += (double)(m->hpos[b] + 1) * per_tok;
         *bytes = kv;
     }
+    return NX_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------- NXF files --
+// Tensors of a model in an NXF file.  Matrix shapes follow the reference's
+// {in, out} convention (hybrid_model.cpp:366-391: wq.shape[1] is the q
+// width, output.weight.shape[1] the vocabulary, experts.w1 is {E, d, F});
+// the payload of the build's codecs holds `out` rows of `in` elements.  A
+// file row r lands on device row (r / R) * GS + (r % R) * S + O of the
+// runner's buffer, which interleaves gate and up rows and stacks q, k, v.
+namespace {
+
+struct RowMap {
+    size_t R, GS, S, O;
+    size_t dev(size_t r) const { return (r / R) * GS + (r % R) * S + O; }
+};
+
+struct NxfTensorSpec {
+    std::string name;
+    std::vector<int64_t> shape;
+    int dtype;          // NX_DTYPE_*
+    size_t rows;        // file rows
+    size_t row_bytes;   // codes (I4), fp16 (F16) or fp32 (F32) bytes per row
+    size_t srow_bytes;  // I4: scale bytes per row
+    uint8_t* w;         // device rows
+    uint16_t* s;        // I4: device scale rows
+    RowMap map;
+};
+
+std::vector<NxfTensorSpec> nxf_specs(nx_model* m) {
+    const nx_model_config& c = m->c;
+    const size_t d = (size_t)c.d_model, F = (size_t)c.ffn, E = (size_t)c.n_experts, V = (size_t)c.vocab;
+    const size_t qd = (size_t)m->qdim, kvd = (size_t)m->kvdim;
+    const size_t Gd = (size_t)m->Gd, Gq = (size_t)m->Gq, Gf = (size_t)m->Gf;
+    auto plain = [](size_t rows, size_t off = 0) { return RowMap{rows ? rows : 1, 0, 1, off}; };
+    std::vector<NxfTensorSpec> t;
+    auto i4 = [&](const std::string& name, std::vector<int64_t> shape, size_t rows, size_t G, uint8_t* w, uint16_t* sc,
+                  RowMap mp) {
+        t.push_back({name, std::move(shape), NX_DTYPE_I4, rows, G * 16, G * 2, w, sc, mp});
+    };
+    auto f32 = [&](const std::string& name, float* w) {
+        t.push_back({name, {(int64_t)d}, NX_DTYPE_F32, 1, d * 4, 0, reinterpret_cast<uint8_t*>(w), nullptr, plain(1)});
+    };
+    t.push_back({"tok_embeddings.weight", {(int64_t)d, (int64_t)V}, NX_DTYPE_F16, V, d * 2, 0,
+                 reinterpret_cast<uint8_t*>(m->embed), nullptr, plain(V)});
+    f32("norm.weight", m->norm_final);
+    i4("output.weight", {(int64_t)d, (int64_t)V}, V, Gd, m->lm_w, m->lm_s, plain(V));
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = m->layers[(size_t)L];
+        const std::string p = "layers." + std::to_string(L) + ".";
+        f32(p + "attention_norm.weight", ly.norm_attn);
+        f32(p + "ffn_norm.weight", ly.norm_ffn);
+        i4(p + "attention.wq.weight", {(int64_t)d, (int64_t)qd}, qd, Gd, ly.wqkv, ly.sqkv, plain(qd, 0));
+        i4(p + "attention.wk.weight", {(int64_t)d, (int64_t)kvd}, kvd, Gd, ly.wqkv, ly.sqkv, plain(kvd, qd));
+        i4(p + "attention.wv.weight", {(int64_t)d, (int64_t)kvd}, kvd, Gd, ly.wqkv, ly.sqkv, plain(kvd, qd + kvd));
+        i4(p + "attention.wo.weight", {(int64_t)qd, (int64_t)d}, d, Gq, ly.wo, ly.so, plain(d));
+        if (E == 0) {
+            i4(p + "feed_forward.w1.weight", {(int64_t)d, (int64_t)F}, F, Gd, ly.w13, ly.s13, RowMap{F, 0, 2, 0});
+            i4(p + "feed_forward.w3.weight", {(int64_t)d, (int64_t)F}, F, Gd, ly.w13, ly.s13, RowMap{F, 0, 2, 1});
+            i4(p + "feed_forward.w2.weight", {(int64_t)F, (int64_t)d}, d, Gf, ly.w2, ly.s2, plain(d));
+        } else {
+            i4(p + "feed_forward.gate.weight", {(int64_t)d, (int64_t)E}, E, Gd, ly.wr, ly.sr, plain(E));
+            i4(p + "feed_forward.experts.w1.weight", {(int64_t)E, (int64_t)d, (int64_t)F}, E * F, Gd, ly.w13, ly.s13,
+               RowMap{F, 2 * F, 2, 0});
+            i4(p + "feed_forward.experts.w3.weight", {(int64_t)E, (int64_t)d, (int64_t)F}, E * F, Gd, ly.w13, ly.s13,
+               RowMap{F, 2 * F, 2, 1});
+            i4(p + "feed_forward.experts.w2.weight", {(int64_t)E, (int64_t)F, (int64_t)d}, E * d, Gf, ly.w2, ly.s2,
+               RowMap{d, d, 1, 0});
+        }
+    }
+    return t;
+}
+
+// Copy file rows [r0, r0 + n) between a host/staging buffer (packed rows)
+// and the device rows of map, one strided copy per run of rows in the
+// same group.
+nx_status copy_rows(nx_ctx* ctx, uint8_t* dev_base, uint8_t* packed, size_t rb, const RowMap& mp, size_t r0, size_t n,
+                    hipMemcpyKind kind) {
+    size_t r = r0;
+    while (r < r0 + n) {
+        const size_t run = std::min(r0 + n - r, mp.R - r % mp.R);
+        uint8_t* dv = dev_base + mp.dev(r) * rb;
+        uint8_t* pk = packed + (r - r0) * rb;
+        if (kind == hipMemcpyDeviceToHost)
+            NX_HIP(ctx, hipMemcpy2DAsync(pk, rb, dv, mp.S * rb, rb, run, kind, ctx->stream));
+        else
+            NX_HIP(ctx, hipMemcpy2DAsync(dv, mp.S * rb, pk, rb, rb, run, kind, ctx->stream));
+        r += run;
+    }
+    return NX_OK;
+}
+
+nx_status nxf_fail(nx_ctx* ctx, nx_status s) { return fail(ctx, s, "%s", nx_nxf_error()); }
+
+// Whole rows per chunk, at most 64 KiB (one row if a row is larger).
+nx_status write_rows(nx_ctx* ctx, nx_nxf_writer* w, const uint8_t* host, size_t rows, size_t rb, int codec, int gs) {
+    const size_t per = std::max<size_t>(1, (64u << 10) / rb);
+    for (size_t r = 0; r < rows; r += per) {
+        const size_t n = std::min(per, rows - r);
+        nx_status s = nx_nxf_writer_add_chunk(w, host + r * rb, n * rb, codec, gs);
+        if (s != NX_OK) return nxf_fail(ctx, s);
+    }
+    return NX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+nx_status nx_model_save_nxf(nx_model* m, const char* path) {
+    if (!m || !path) return NX_ERR_INVALID;
+    nx_ctx* ctx = m->ctx;
+    const nx_model_config& c = m->c;
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    nx_nxf_writer* w = nullptr;
+    nx_status s = nx_nxf_writer_create(ctx, path, &w);
+    if (s != NX_OK) return nxf_fail(ctx, s);
+    nx_nxf_manifest man{};
+    snprintf(man.architecture, sizeof(man.architecture), "%s", c.n_experts ? "mixtral" : "llama");
+    snprintf(man.name, sizeof(man.name), "nexus-int4-g32");
+    man.num_layers = (uint32_t)c.n_layers;
+    man.hidden_dim = (uint32_t)c.d_model;
+    man.num_heads = (uint32_t)c.n_heads;
+    man.num_kv_heads = (uint32_t)c.n_kv_heads;
+    man.head_dim = (uint32_t)c.head_dim;
+    man.vocab_size = (uint32_t)c.vocab;
+    man.max_seq_len = (uint32_t)c.max_seq;
+    man.rope_theta = c.rope_theta;
+    man.rms_norm_eps = c.eps;
+    man.num_experts = (uint32_t)c.n_experts;
+    man.num_active_experts = (uint32_t)c.top_k;
+    man.default_codec = NX_CODEC_INT4;
+    man.default_group_size = 32;
+    nx_nxf_writer_set_manifest(w, &man);
+    std::vector<uint8_t> host;
+    for (const NxfTensorSpec& t : nxf_specs(m)) {
+        s = nx_nxf_writer_begin_tensor(w, t.name.c_str(), t.shape.data(), (int)t.shape.size(), t.dtype);
+        if (s != NX_OK) break;
+        host.resize(t.rows * t.row_bytes);
+        if (t.w) {
+            if ((s = copy_rows(ctx, t.w, host.data(), t.row_bytes, t.map, 0, t.rows, hipMemcpyDeviceToHost)) != NX_OK) break;
+            if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+                s = fail(ctx, NX_ERR_HIP, "nx_model_save_nxf: device copy failed");
+                break;
+            }
+        } else {  // RMSNorm weights of 1.0
+            for (size_t i = 0; i < t.row_bytes / 4; ++i) reinterpret_cast<float*>(host.data())[i] = 1.0f;
+        }
+        const int codec = t.dtype == NX_DTYPE_I4 ? NX_CODEC_INT4 : t.dtype == NX_DTYPE_F16 ? NX_CODEC_FP16 : NX_CODEC_FP32;
+        if ((s = write_rows(ctx, w, host.data(), t.rows, t.row_bytes, codec, t.dtype == NX_DTYPE_I4 ? 32 : 0)) != NX_OK) break;
+        if (t.dtype == NX_DTYPE_I4) {  // the fp16 scales: sidecar chunks of the same tensor
+            host.resize(t.rows * t.srow_bytes);
+            if ((s = copy_rows(ctx, reinterpret_cast<uint8_t*>(t.s), host.data(), t.srow_bytes, t.map, 0, t.rows,
+                               hipMemcpyDeviceToHost)) != NX_OK)
+                break;
+            if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+                s = fail(ctx, NX_ERR_HIP, "nx_model_save_nxf: device copy failed");
+                break;
+            }
+            if ((s = write_rows(ctx, w, host.data(), t.rows, t.srow_bytes, NX_CODEC_FP16, 32)) != NX_OK) break;
+        }
+        if ((s = nx_nxf_writer_end_tensor(w)) != NX_OK) {
+            s = nxf_fail(ctx, s);
+            break;
+        }
+    }
+    if (s != NX_OK) {
+        nx_nxf_writer_destroy(w);
+        return s;
+    }
+    s = nx_nxf_writer_finalize(w);
+    return s == NX_OK ? NX_OK : nxf_fail(ctx, s);
+}
+
+nx_status nx_model_load_nxf(nx_ctx* ctx, const char* path, const nx_model_config* run, nx_model** out) {
+    if (!ctx || !path || !run || !out) return NX_ERR_INVALID;
+    *out = nullptr;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_model_load_nxf inside a token batch");
+    nx_nxf* r = nullptr;
+    nx_status s = nx_nxf_open(path, &r);
+    if (s != NX_OK) return nxf_fail(ctx, s);
+    nx_model* m = nullptr;
+    uint8_t* host = nullptr;
+    uint8_t* dev = nullptr;
+    nx::HashRange* dranges = nullptr;
+    uint32_t* dhash = nullptr;
+    do {
+        nx_nxf_manifest man{};
+        nx_nxf_get_manifest(r, &man);
+        nx_model_config c = *run;
+        c.n_layers = (int)man.num_layers;
+        c.d_model = (int)man.hidden_dim;
+        c.n_heads = (int)man.num_heads;
+        c.n_kv_heads = (int)man.num_kv_heads;
+        c.head_dim = (int)man.head_dim;
+        c.vocab = (int)man.vocab_size;
+        c.n_experts = (int)man.num_experts;
+        c.top_k = (int)man.num_active_experts;
+        c.rope_theta = man.rope_theta;
+        c.eps = man.rms_norm_eps;
+        c.norm_sigma = 0.0f;
+        // the FFN width from the first layer's gate projection
+        int ti = -1;
+        nx_nxf_tensor info{};
+        nx_nxf_find(r, c.n_experts ? "layers.0.feed_forward.experts.w1.weight" : "layers.0.feed_forward.w1.weight", &ti);
+        if (ti < 0 || nx_nxf_tensor_at(r, ti, &info) != NX_OK || info.ndim < 2) {
+            s = fail(ctx, NX_ERR_INVALID, "nxf '%s': no FFN gate tensor in layer 0", path);
+            break;
+        }
+        c.ffn = (int)info.shape[info.ndim - 1];
+        if ((s = check_config(ctx, c)) != NX_OK) break;
+        m = new nx_model();
+        m->ctx = ctx;
+        m->c = c;
+        if ((s = create_impl(m, false)) != NX_OK) break;
+        const std::vector<NxfTensorSpec> specs = nxf_specs(m);
+        // staging large enough for the biggest tensor, chunks 256-byte aligned
+        size_t cap = 0, maxchunks = 0;
+        for (const NxfTensorSpec& t : specs) {
+            if (nx_nxf_find(r, t.name.c_str(), &ti) != NX_OK || ti < 0) {
+                s = fail(ctx, NX_ERR_INVALID, "nxf '%s': tensor '%s' is missing", path, t.name.c_str());
+                break;
+            }
+            nx_nxf_tensor_at(r, ti, &info);
+            bool same = info.ndim == (int)t.shape.size() && info.dtype == t.dtype;
+            for (int k = 0; same && k < info.ndim; ++k) same = info.shape[k] == t.shape[(size_t)k];
+            if (!same) {
+                s = fail(ctx, NX_ERR_INVALID, "nxf '%s': tensor '%s' has another shape or dtype than the manifest implies",
+                         path, t.name.c_str());
+                break;
+            }
+            size_t need = 0;
+            for (int k = 0; k < info.num_chunks; ++k) {
+                nx_nxf_chunk ch{};
+                nx_nxf_chunk_at(r, ti, k, &ch);
+                need += (ch.compressed_size + 255) / 256 * 256;
+            }
+            cap = std::max(cap, need);
+            maxchunks = std::max(maxchunks, (size_t)info.num_chunks);
+        }
+        if (s != NX_OK) break;
+        cap = std::max<size_t>(cap, 256);
+        if (hipHostMalloc(reinterpret_cast<void**>(&host), cap, hipHostMallocDefault) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&dev), cap) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&dranges), std::max<size_t>(maxchunks, 1) * sizeof(nx::HashRange)) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void**>(&dhash), std::max<size_t>(maxchunks, 1) * 4) != hipSuccess) {
+            s = fail(ctx, NX_ERR_OOM, "nx_model_load_nxf: staging of %zu bytes", cap);
+            break;
+        }
+        hipStream_t st = ctx->stream;
+        for (const NxfTensorSpec& t : specs) {
+            nx_nxf_find(r, t.name.c_str(), &ti);
+            nx_nxf_tensor_at(r, ti, &info);
+            std::vector<nx_nxf_chunk> ch((size_t)info.num_chunks);
+            std::vector<size_t> at(ch.size());
+            std::vector<nx::HashRange> rg;
+            size_t used = 0;
+            for (size_t k = 0; k < ch.size() && s == NX_OK; ++k) {
+                nx_nxf_chunk_at(r, ti, (int)k, &ch[k]);
+                at[k] = used;
+                if (nx_nxf_read_chunk(r, ti, (int)k, host + used) != NX_OK) s = nxf_fail(ctx, NX_ERR_IO);
+                rg.push_back(nx::HashRange{used, ch[k].compressed_size, (uint32_t)k});
+                used += (ch[k].compressed_size + 255) / 256 * 256;
+            }
+            if (s != NX_OK) break;
+            // verify every chunk on the device before any is used
+            std::stable_sort(rg.begin(), rg.end(), [](const nx::HashRange& a, const nx::HashRange& b) { return a.len > b.len; });
+            std::vector<uint32_t> got(ch.size());
+            if (!ch.empty() &&
+                (hipMemcpyAsync(dev, host, used, hipMemcpyHostToDevice, st) != hipSuccess ||
+                 hipMemcpyAsync(dranges, rg.data(), rg.size() * sizeof(nx::HashRange), hipMemcpyHostToDevice, st) !=
+                     hipSuccess ||
+                 nx::xxh32_launch(dev, dranges, (int)rg.size(), dhash, st) != hipSuccess ||
+                 hipMemcpyAsync(got.data(), dhash, got.size() * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+                 hipStreamSynchronize(st) != hipSuccess)) {
+                s = fail(ctx, NX_ERR_HIP, "nx_model_load_nxf: upload or hashing of '%s' failed", t.name.c_str());
+                break;
+            }
+            for (size_t k = 0; k < ch.size() && s == NX_OK; ++k)
+                if (got[k] != ch[k].checksum)
+                    s = fail(ctx, NX_ERR_CHECKSUM, "nxf '%s': checksum mismatch in chunk %zu of '%s' (stored %08x, data %08x)",
+                             path, k, t.name.c_str(), ch[k].checksum, got[k]);
+            if (s != NX_OK) break;
+            // place the rows: codes (or values) chunks first, then for I4 the
+            // fp16 scale chunks, each holding whole rows
+            const int vcodec = t.dtype == NX_DTYPE_I4 ? NX_CODEC_INT4 : t.dtype == NX_DTYPE_F16 ? NX_CODEC_FP16 : NX_CODEC_FP32;
+            size_t vrow = 0, srow = 0;
+            for (size_t k = 0; k < ch.size() && s == NX_OK; ++k) {
+                const bool is_scale = t.dtype == NX_DTYPE_I4 && ch[k].codec == NX_CODEC_FP16;
+                if (!is_scale && ch[k].codec != vcodec) {
+                    s = fail(ctx, NX_ERR_UNSUPPORTED, "nxf '%s': chunk %zu of '%s' has codec %u", path, k, t.name.c_str(),
+                             (unsigned)ch[k].codec);
+                    break;
+                }
+                if (t.dtype == NX_DTYPE_I4 && ch[k].group_size != 32) {
+                    s = fail(ctx, NX_ERR_UNSUPPORTED, "nxf '%s': chunk %zu of '%s' has group size %u (32 expected)", path,
+                             k, t.name.c_str(), (unsigned)ch[k].group_size);
+                    break;
+                }
+                const size_t rb = is_scale ? t.srow_bytes : t.row_bytes;
+                size_t& row = is_scale ? srow : vrow;
+                if (ch[k].compressed_size % rb || row + ch[k].compressed_size / rb > t.rows) {
+                    s = fail(ctx, NX_ERR_INVALID, "nxf '%s': chunk %zu of '%s' does not hold whole rows within the tensor",
+                             path, k, t.name.c_str());
+                    break;
+                }
+                const size_t n = ch[k].compressed_size / rb;
+                s = copy_rows(ctx, is_scale ? reinterpret_cast<uint8_t*>(t.s) : t.w, dev + at[k], rb, t.map, row, n,
+                              hipMemcpyDeviceToDevice);
+                row += n;
+            }
+            if (s != NX_OK) break;
+            if (vrow != t.rows || (t.dtype == NX_DTYPE_I4 && srow != t.rows)) {
+                s = fail(ctx, NX_ERR_INVALID, "nxf '%s': tensor '%s' holds %zu value and %zu scale rows of %zu", path,
+                         t.name.c_str(), vrow, srow, t.rows);
+                break;
+            }
+            if (hipStreamSynchronize(st) != hipSuccess) {  // the staging is reused by the next tensor
+                s = fail(ctx, NX_ERR_HIP, "nx_model_load_nxf: placing '%s' failed", t.name.c_str());
+                break;
+            }
+        }
+    } while (false);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (host) (void)hipHostFree(host);
+    if (dev) (void)hipFree(dev);
+    if (dranges) (void)hipFree(dranges);
+    if (dhash) (void)hipFree(dhash);
+    nx_nxf_close(r);
+    if (s != NX_OK) {
+        if (m) free_model(m);
+        return s;
+    }
+    *out = m;
     return NX_OK;
 }
 

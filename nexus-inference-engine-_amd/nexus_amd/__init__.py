@@ -18,10 +18,11 @@ PKG_DIR = Path(__file__).resolve().parent
 ROOT = PKG_DIR.parent
 LIB_PATH = PKG_DIR / "libnexus_hip.so"
 HEADER = ROOT.parent / "include" / "nexus_hip.h"
+HEADERS = sorted((ROOT.parent / "include").glob("*.h"))
 
 NX_OK = 0
 STATUS = {0: "OK", 1: "INVALID", 2: "HIP", 3: "OOM", 4: "UNSUPPORTED", 5: "STATE",
-          6: "NO_DEVICE", 7: "CAPACITY"}
+          6: "NO_DEVICE", 7: "CAPACITY", 8: "CHECKSUM", 9: "IO"}
 
 
 class NxError(RuntimeError):
@@ -41,8 +42,34 @@ class ModelConfig(C.Structure):
         ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
-        ("seed", C.c_uint64),
+        ("seed", C.c_uint64), ("norm_sigma", C.c_float),
     ]
+
+
+class NxfManifest(C.Structure):
+    """nx_nxf_manifest (ModelManifest, nexus/src/format/nxf.h:76-96)."""
+    _fields_ = [
+        ("architecture", C.c_char * 64), ("name", C.c_char * 128),
+        ("num_layers", C.c_uint32), ("hidden_dim", C.c_uint32), ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("vocab_size", C.c_uint32),
+        ("max_seq_len", C.c_uint32), ("rope_theta", C.c_float), ("rms_norm_eps", C.c_float),
+        ("num_experts", C.c_uint32), ("num_active_experts", C.c_uint32),
+        ("default_codec", C.c_uint8), ("default_group_size", C.c_uint8),
+    ]
+
+
+class NxfChunk(C.Structure):
+    """nx_nxf_chunk (ChunkDesc, nexus/src/format/nxf.h:42-50)."""
+    _fields_ = [("file_offset", C.c_uint64), ("compressed_size", C.c_uint32),
+                ("decompressed_size", C.c_uint32), ("checksum", C.c_uint32),
+                ("codec", C.c_uint8), ("group_size", C.c_uint8)]
+
+
+class NxfTensor(C.Structure):
+    """nx_nxf_tensor (TensorInfo, nexus/src/format/nxf.h:54-73)."""
+    _fields_ = [("name", C.c_char_p), ("ndim", C.c_int), ("shape", C.c_int64 * 8),
+                ("dtype", C.c_int), ("num_chunks", C.c_int),
+                ("compressed_bytes", C.c_uint64), ("decompressed_bytes", C.c_uint64)]
 
 
 _B = C.c_uint64  # nx_buf
@@ -98,6 +125,32 @@ _SIGS = {
     "nx_time_gemv": (_I, [_P, _B, C.POINTER(_B), C.POINTER(_B), _I, _B, _I, _I, _I, _I,
                           C.POINTER(C.c_double)]),
     "nx_model_time_attention": (_I, [_P, _I, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    # include/nexus_nxf.h
+    "nx_nxf_error": (C.c_char_p, []),
+    "nx_nxf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "nx_nxf_close": (_I, [_P]),
+    "nx_nxf_get_manifest": (_I, [_P, C.POINTER(NxfManifest)]),
+    "nx_nxf_num_tensors": (_I, [_P, C.POINTER(_I)]),
+    "nx_nxf_tensor_at": (_I, [_P, _I, C.POINTER(NxfTensor)]),
+    "nx_nxf_find": (_I, [_P, C.c_char_p, C.POINTER(_I)]),
+    "nx_nxf_chunk_at": (_I, [_P, _I, _I, C.POINTER(NxfChunk)]),
+    "nx_nxf_map_chunk": (_I, [_P, _I, _I, C.POINTER(_P)]),
+    "nx_nxf_unmap_chunk": (_I, [_P, _P]),
+    "nx_nxf_read_chunk": (_I, [_P, _I, _I, _P]),
+    "nx_nxf_verify": (_I, [_P, _P, C.POINTER(_I), C.POINTER(_I), C.POINTER(C.c_uint64)]),
+    "nx_nxf_writer_create": (_I, [_P, C.c_char_p, C.POINTER(_P)]),
+    "nx_nxf_writer_set_manifest": (_I, [_P, C.POINTER(NxfManifest)]),
+    "nx_nxf_writer_begin_tensor": (_I, [_P, C.c_char_p, C.POINTER(C.c_int64), _I, _I]),
+    "nx_nxf_writer_add_chunk": (_I, [_P, _P, C.c_size_t, _I, _I]),
+    "nx_nxf_writer_end_tensor": (_I, [_P]),
+    "nx_nxf_writer_finalize": (_I, [_P]),
+    "nx_nxf_writer_destroy": (_I, [_P]),
+    "nx_xxh32_chunks": (_I, [_P, _B, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), _I,
+                             C.POINTER(C.c_uint32)]),
+    "nx_time_xxh32": (_I, [_P, _B, C.c_size_t, C.c_uint32, _I, C.POINTER(C.c_double),
+                           C.POINTER(C.c_uint32)]),
+    "nx_model_save_nxf": (_I, [_P, C.c_char_p]),
+    "nx_model_load_nxf": (_I, [_P, C.c_char_p, C.POINTER(ModelConfig), C.POINTER(_P)]),
 }
 
 _lib = None
@@ -216,6 +269,36 @@ class Model:
         h = C.c_void_p()
         ctx.check(ctx.L.nx_model_create(ctx.h, C.byref(self.cfg), C.byref(h)), "nx_model_create")
         self.h = h
+
+    @classmethod
+    def load_nxf(cls, ctx: Context, path, batch=1, max_seq=128, kv_kind=0, seed=0x5EED) -> "Model":
+        """A model from an NXF file (nx_model_load_nxf): dimensions from the
+        file, every chunk verified on the GPU; batch, max_seq, kv_kind and
+        seed are the caller's."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        run = ModelConfig(batch=batch, max_seq=max_seq, kv_kind=kv_kind, seed=seed)
+        h = C.c_void_p()
+        ctx.check(ctx.L.nx_model_load_nxf(ctx.h, str(path).encode(), C.byref(run), C.byref(h)),
+                  "nx_model_load_nxf")
+        self.h = h
+        # the dimensions the library read from the file
+        from .nxf import NXFReader
+        r = NXFReader.open(path)
+        m = r.manifest()
+        w1 = r.get_tensor("layers.0.feed_forward.experts.w1.weight" if m.num_experts
+                          else "layers.0.feed_forward.w1.weight")
+        r.close()
+        self.cfg = ModelConfig(
+            n_layers=m.num_layers, d_model=m.hidden_dim, n_heads=m.num_heads,
+            n_kv_heads=m.num_kv_heads, head_dim=m.head_dim, ffn=w1.shape[-1], vocab=m.vocab_size,
+            n_experts=m.num_experts, top_k=m.num_active_experts, max_seq=max_seq, batch=batch,
+            kv_kind=kv_kind, rope_theta=m.rope_theta, eps=m.rms_norm_eps, seed=seed)
+        return self
+
+    def save_nxf(self, path):
+        """Write the model as an NXF file (nx_model_save_nxf)."""
+        self.ctx.check(self.ctx.L.nx_model_save_nxf(self.h, str(path).encode()), "nx_model_save_nxf")
 
     def close(self):
         if self.h:

@@ -31,7 +31,7 @@ class Cfg(C.Structure):
         ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
-        ("seed", C.c_uint64),
+        ("seed", C.c_uint64), ("norm_sigma", C.c_float),
     ]
 
 
@@ -65,6 +65,7 @@ def _load() -> C.CDLL:
         "nxo_dequant_int4_g32": (None, [_u8p, _u16p, C.c_int, C.c_int, _f32p]),
         "nxo_gemv_int4_g32": (None, [_u8p, _u16p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]),
         "nxo_rmsnorm": (None, [_f32p, C.c_void_p, C.c_int, C.c_float, _f32p]),
+        "nxo_xxh32": (C.c_uint32, [C.c_void_p, C.c_size_t, C.c_uint32]),
         "nxo_rope_table": (None, [C.c_int, C.c_int, C.c_double, _f32p, _f32p]),
         "nxo_rope": (None, [_f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]),
         "nxo_swiglu": (None, [_f32p, _f32p, C.c_int, _f32p]),
@@ -131,6 +132,12 @@ def ref():
         R.ref_moe_route.argtypes = [C.c_int, C.c_int, C.c_int, _f32p, _f32p, _i32p, _f32p]
         R.ref_f32_to_f16_kv.argtypes = [_f32p, _u16p, C.c_int]
         R.ref_f16_to_f32_kv.argtypes = [_u16p, _f32p, C.c_int]
+        R.ref_nxf_write.restype = C.c_int
+        R.ref_nxf_write.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]
+        R.ref_nxf_summary.restype = C.c_long
+        R.ref_nxf_summary.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+        R.ref_nxf_chunk_bytes.restype = C.c_long
+        R.ref_nxf_chunk_bytes.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_void_p, C.c_size_t]
         _ref_lib = R
     return _ref_lib
 

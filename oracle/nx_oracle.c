@@ -615,6 +615,7 @@ typedef struct {
     uint8_t *kc4, *kc3, *vc4, *vc3;          /* TurboQuant pages */
     uint16_t *kn, *vn;
     float ksign[NXO_TQ_D], vsign[NXO_TQ_D];
+    float *norm_attn, *norm_ffn;             /* RMSNorm weights, NULL = 1.0 */
 } layer_t;
 
 struct nxo_model {
@@ -623,6 +624,7 @@ struct nxo_model {
     uint16_t* embed;
     qmat lm;
     layer_t* layers;
+    float* norm_final;                       /* NULL = 1.0 */
     float *rope_cos, *rope_sin;
     int max_blocks, n_blocks;
     int32_t* block_table;
@@ -642,6 +644,15 @@ static void make_qmat(qmat* m, int N, int K, uint64_t seed, uint32_t tid, double
     nxo_gen_normal(w, (size_t)N * K, seed, tid, nxo_normal_k(sigma));
     nxo_quantize_int4_g32(w, N, K, m->codes, m->scales);
     free(w);
+}
+
+/* RMSNorm weights 1 + N(0, sigma) of one tensor id; NULL for sigma 0. */
+static float* make_norm(int d, uint64_t seed, uint32_t tid, double sigma) {
+    if (sigma == 0.0) return NULL;
+    float* w = (float*)malloc(sizeof(float) * (size_t)d);
+    nxo_gen_normal(w, (size_t)d, seed, tid, nxo_normal_k(sigma));
+    for (int i = 0; i < d; ++i) w[i] = 1.0f + w[i];
+    return w;
 }
 
 static void free_qmat(qmat* m) {
@@ -672,6 +683,7 @@ nxo_model* nxo_model_create(const nxo_cfg* cfg) {
         free(e);
     }
     make_qmat(&m->lm, c->vocab, d, seed, NXO_TID_LMHEAD, 0.02);
+    m->norm_final = make_norm(d, seed, NXO_TID_FINAL_NORM, c->norm_sigma);
     m->max_blocks = c->max_seq / NXO_PAGE;
     m->n_blocks = m->max_blocks * B;
     m->block_table = (int32_t*)malloc(sizeof(int32_t) * (size_t)m->n_blocks);
@@ -691,6 +703,8 @@ nxo_model* nxo_model_create(const nxo_cfg* cfg) {
         make_qmat(&ly->wk, m->kvdim, d, seed, NXO_TID_LAYER(L, NXO_W_K), 0.02);
         make_qmat(&ly->wv, m->kvdim, d, seed, NXO_TID_LAYER(L, NXO_W_V), 0.02);
         make_qmat(&ly->wo, d, m->qdim, seed, NXO_TID_LAYER(L, NXO_W_O), 0.02);
+        ly->norm_attn = make_norm(d, seed, NXO_TID_LAYER(L, NXO_N_ATTN), c->norm_sigma);
+        ly->norm_ffn = make_norm(d, seed, NXO_TID_LAYER(L, NXO_N_FFN), c->norm_sigma);
         if (c->n_experts == 0) {
             make_qmat(&ly->w1, c->ffn, d, seed, NXO_TID_LAYER(L, NXO_W_GATE), 0.02);
             make_qmat(&ly->w3, c->ffn, d, seed, NXO_TID_LAYER(L, NXO_W_UP), 0.02);
@@ -755,7 +769,9 @@ void nxo_model_free(nxo_model* m) {
         }
         free(ly->kpool); free(ly->vpool);
         free(ly->kc4); free(ly->kc3); free(ly->vc4); free(ly->vc3); free(ly->kn); free(ly->vn);
+        free(ly->norm_attn); free(ly->norm_ffn);
     }
+    free(m->norm_final);
     free(m->layers);
     free_qmat(&m->lm);
     free(m->embed); free(m->block_table); free(m->pos); free(m->rope_cos); free(m->rope_sin);
@@ -768,9 +784,9 @@ int nxo_model_position(const nxo_model* m, int b) { return m->pos[b]; }
 const int32_t* nxo_model_block_table(const nxo_model* m) { return m->block_table; }
 int nxo_model_max_blocks(const nxo_model* m) { return m->max_blocks; }
 
-/* x (fp32) -> fp16-rounded RMSNorm output (norm weights are 1.0). */
-static void norm_to_f16(const float* x, int d, float eps, float* out) {
-    nxo_rmsnorm(x, NULL, d, eps, out);
+/* x (fp32) -> fp16-rounded RMSNorm output with weights w (NULL = 1.0). */
+static void norm_to_f16(const float* x, const float* w, int d, float eps, float* out) {
+    nxo_rmsnorm(x, w, d, eps, out);
     for (int i = 0; i < d; ++i) out[i] = round_f16(out[i]);
 }
 
@@ -826,7 +842,7 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
     for (int b = 0; b < B; ++b) ctx[b] = m->pos[b] + 1;
     for (int L = 0; L < c->n_layers; ++L) {
         layer_t* ly = &m->layers[L];
-        for (int b = 0; b < B; ++b) norm_to_f16(m->h + (size_t)b * d, d, c->eps, m->xn + (size_t)b * d);
+        for (int b = 0; b < B; ++b) norm_to_f16(m->h + (size_t)b * d, ly->norm_attn, d, c->eps, m->xn + (size_t)b * d);
         gemv(&ly->wq, m->xn, B, m->q);
         gemv(&ly->wk, m->xn, B, m->k);
         gemv(&ly->wv, m->xn, B, m->v);
@@ -854,7 +870,7 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
         for (size_t i = 0; i < (size_t)B * m->qdim; ++i) m->att[i] = round_f16(m->att[i]);
         gemv(&ly->wo, m->att, B, m->tmp);
         for (size_t i = 0; i < (size_t)B * d; ++i) m->h[i] = m->h[i] + m->tmp[i];
-        for (int b = 0; b < B; ++b) norm_to_f16(m->h + (size_t)b * d, d, c->eps, m->xn + (size_t)b * d);
+        for (int b = 0; b < B; ++b) norm_to_f16(m->h + (size_t)b * d, ly->norm_ffn, d, c->eps, m->xn + (size_t)b * d);
         if (c->n_experts == 0)
             ffn_dense(m, ly, m->xn, B, m->dn);
         else
@@ -862,7 +878,7 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
         for (size_t i = 0; i < (size_t)B * d; ++i) m->h[i] = m->h[i] + m->dn[i];
     }
     const double t1 = now_s();
-    for (int b = 0; b < B; ++b) norm_to_f16(m->h + (size_t)b * d, d, c->eps, m->xn + (size_t)b * d);
+    for (int b = 0; b < B; ++b) norm_to_f16(m->h + (size_t)b * d, m->norm_final, d, c->eps, m->xn + (size_t)b * d);
     gemv(&m->lm, m->xn, B, logits ? logits : m->logits_r);
     const double t2 = now_s();
     for (int b = 0; b < B; ++b) m->pos[b] += 1;
@@ -964,4 +980,41 @@ void nxo_set_num_threads(int n) {
 #else
     (void)n;
 #endif
+}
+
+/* --------------------------------------------------------------- NXF ---- */
+/* XXH32 (format/nxf_writer.cpp:33-72): four lanes v1..v4 over 16-byte
+ * stripes, v = rotl(v + w * P2, 13) * P1; merge rotl(v1,1) + rotl(v2,7) +
+ * rotl(v3,12) + rotl(v4,18) (seed + P5 below 16 bytes); add the length;
+ * remaining 4-byte words h = rotl(h + w * P3, 17) * P4, bytes
+ * h = rotl(h + b * P5, 11) * P1; avalanche >>15 *P2 >>13 *P3 >>16. */
+static uint32_t xxh_rotl(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+static uint32_t xxh_le32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+uint32_t nxo_xxh32(const void* data, size_t len, uint32_t seed) {
+    const uint32_t P1 = 0x9E3779B1u, P2 = 0x85EBCA77u, P3 = 0xC2B2AE3Du, P4 = 0x27D4EB2Fu,
+                   P5 = 0x165667B1u;
+    const uint8_t* p = (const uint8_t*)data;
+    const size_t nstripe = len / 16;
+    uint32_t h;
+    if (nstripe > 0) {
+        uint32_t v[4] = {seed + P1 + P2, seed + P2, seed, seed - P1};
+        for (size_t s = 0; s < nstripe; ++s)
+            for (int l = 0; l < 4; ++l) v[l] = xxh_rotl(v[l] + xxh_le32(p + 16 * s + 4 * l) * P2, 13) * P1;
+        h = xxh_rotl(v[0], 1) + xxh_rotl(v[1], 7) + xxh_rotl(v[2], 12) + xxh_rotl(v[3], 18);
+    } else {
+        h = seed + P5;
+    }
+    h += (uint32_t)len;
+    size_t i = 16 * nstripe;
+    for (; i + 4 <= len; i += 4) h = xxh_rotl(h + xxh_le32(p + i) * P3, 17) * P4;
+    for (; i < len; ++i) h = xxh_rotl(h + (uint32_t)p[i] * P5, 11) * P1;
+    h ^= h >> 15;
+    h *= P2;
+    h ^= h >> 13;
+    h *= P3;
+    h ^= h >> 16;
+    return h;
 }

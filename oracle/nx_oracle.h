@@ -181,6 +181,7 @@ typedef struct {
     float rope_theta;
     float eps;
     uint64_t seed;
+    float norm_sigma;              /* RMSNorm weights: 0 = 1.0, else 1 + N(0, norm_sigma) */
 } nxo_cfg;
 
 typedef struct nxo_model nxo_model;
@@ -208,14 +209,22 @@ void nxo_model_forward_timed(nxo_model* m, const int32_t* tokens, float* logits,
 int nxo_num_threads(void);
 void nxo_set_num_threads(int n);
 
+/* ------------------------------------------------------------ NXF -- */
+/* XXH32 of a byte range (the published xxHash 32-bit algorithm): the chunk
+ * checksum of NXF files, format/nxf_writer.cpp:33-72 (stored by
+ * NXFWriter::add_chunk, :255) and format/nxf_reader.cpp:32-71. */
+uint32_t nxo_xxh32(const void* data, size_t len, uint32_t seed);
+
 /* Tensor ids of the synthetic model (shared with the device generator). */
 #define NXO_TID_EMBED        1u
 #define NXO_TID_LMHEAD       2u
 #define NXO_TID_PROMPT       4u
 #define NXO_TID_PAGE_SHUFFLE 7u
+#define NXO_TID_FINAL_NORM   3u
 #define NXO_TID_LAYER(L, kind) (0x100u * ((uint32_t)(L) + 1u) + (uint32_t)(kind))
 enum { NXO_W_Q = 0, NXO_W_K = 1, NXO_W_V = 2, NXO_W_O = 3, NXO_W_GATE = 4, NXO_W_UP = 5,
-       NXO_W_DOWN = 6, NXO_W_ROUTER = 7, NXO_TQ_KSIGN = 8, NXO_TQ_VSIGN = 9 };
+       NXO_W_DOWN = 6, NXO_W_ROUTER = 7, NXO_TQ_KSIGN = 8, NXO_TQ_VSIGN = 9, NXO_N_ATTN = 10,
+       NXO_N_FFN = 11 };
 /* expert e of layer L: NXO_TID_EXPERT(L, e, 0=gate,1=up,2=down) */
 #define NXO_TID_EXPERT(L, e, w) (0x01000000u + 0x1000u * (uint32_t)(L) + 4u * (uint32_t)(e) + (uint32_t)(w))
 /* synthetic context of sequence b, layer L, kv = 0 (K) / 1 (V) */

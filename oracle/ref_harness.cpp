@@ -5,6 +5,11 @@
 #include <cstring>
 #include <vector>
 
+#include <algorithm>
+#include <cstdio>
+#include <string>
+
+#include "format/nxf.h"
 #include "kv/paged_attention.h"
 #include "kv/turbo_quant.h"
 #include "model/hybrid_model.h"
@@ -87,5 +92,115 @@ int ref_moe_route(int E, int k, int d, const float* gate_w, const float* hidden,
         ++i;
     }
     return i;
+}
+
+// ------------------------------------------------------------------ NXF --
+// Manifest and tensors in plain C for the NXF entry points below.
+struct ref_manifest {
+    char architecture[64];
+    char name[128];
+    uint32_t num_layers, hidden_dim, num_heads, num_kv_heads, head_dim, vocab_size, max_seq_len;
+    float rope_theta, rms_norm_eps;
+    uint32_t num_experts, num_active_experts;
+    uint8_t default_codec, default_group_size;
+};
+struct ref_tensor {
+    const char* name;
+    int ndim;
+    const int64_t* shape;
+    int dtype;
+    int nchunks;
+    const void* const* data;
+    const uint64_t* sizes;
+    const int* codecs;
+    const int* groups;
+};
+
+// format/nxf_writer.cpp:197-338 (create, set_manifest, begin_tensor,
+// add_chunk, end_tensor, finalize)
+int ref_nxf_write(const char* path, const ref_manifest* rm, const ref_tensor* ts, int n) {
+    using namespace nexus::format;
+    auto w = NXFWriter::create(path);
+    if (!w) return 1;
+    ModelManifest m{};
+    m.architecture = rm->architecture;
+    m.name = rm->name;
+    m.num_layers = rm->num_layers;
+    m.hidden_dim = rm->hidden_dim;
+    m.num_heads = rm->num_heads;
+    m.num_kv_heads = rm->num_kv_heads;
+    m.head_dim = rm->head_dim;
+    m.vocab_size = rm->vocab_size;
+    m.max_seq_len = rm->max_seq_len;
+    m.rope_theta = rm->rope_theta;
+    m.rms_norm_eps = rm->rms_norm_eps;
+    m.num_experts = rm->num_experts;
+    m.num_active_experts = rm->num_active_experts;
+    m.default_codec = static_cast<nexus::Codec>(rm->default_codec);
+    m.default_group_size = rm->default_group_size;
+    w->set_manifest(m);
+    for (int i = 0; i < n; ++i) {
+        const ref_tensor& t = ts[i];
+        w->begin_tensor(t.name, std::vector<int64_t>(t.shape, t.shape + t.ndim), static_cast<nexus::DType>(t.dtype));
+        for (int c = 0; c < t.nchunks; ++c)
+            w->add_chunk(t.data[c], t.sizes[c], static_cast<nexus::Codec>(t.codecs[c]),
+                         static_cast<uint8_t>(t.groups[c]));
+        w->end_tensor();
+    }
+    w->finalize();
+    return 0;
+}
+
+// format/nxf_reader.cpp:192-235: open, manifest(), tensor_names() and
+// get_tensor(), printed as text: the manifest fields, then per tensor (by
+// name) its shape, dtype and chunk descriptors.  Returns the text length
+// (the text is cut at cap - 1 bytes), -1 if the reader refused the file.
+long ref_nxf_summary(const char* path, char* out, size_t cap) {
+    using namespace nexus::format;
+    auto r = NXFReader::open(path);
+    if (!r) return -1;
+    const ModelManifest& m = r->manifest();
+    std::string s;
+    char buf[512];
+    snprintf(buf, sizeof(buf), "manifest %s|%s|%u %u %u %u %u %u %u|%.9g %.9g|%u %u|%u %u\n", m.architecture.c_str(),
+             m.name.c_str(), m.num_layers, m.hidden_dim, m.num_heads, m.num_kv_heads, m.head_dim, m.vocab_size,
+             m.max_seq_len, (double)m.rope_theta, (double)m.rms_norm_eps, m.num_experts, m.num_active_experts,
+             (unsigned)m.default_codec, (unsigned)m.default_group_size);
+    s += buf;
+    auto names = r->tensor_names();
+    std::sort(names.begin(), names.end());
+    for (const auto& nm : names) {
+        const TensorInfo* t = r->get_tensor(nm);
+        s += "tensor " + nm + " shape";
+        for (int64_t d : t->shape) s += " " + std::to_string(d);
+        s += " dtype " + std::to_string((int)t->dtype) + "\n";
+        for (const ChunkDesc& c : t->chunks) {
+            snprintf(buf, sizeof(buf), "  chunk %llu %u %u %08x %u %u\n", (unsigned long long)c.file_offset,
+                     c.compressed_size, c.decompressed_size, c.checksum, (unsigned)c.codec, (unsigned)c.group_size);
+            s += buf;
+        }
+    }
+    if (cap > 0) {
+        const size_t k = std::min(cap - 1, s.size());
+        std::memcpy(out, s.data(), k);
+        out[k] = 0;
+    }
+    return (long)s.size();
+}
+
+// format/nxf_reader.cpp:237-258 (map_chunk): the stored bytes of chunk c of
+// tensor `name`; returns their count, -1 if absent.
+long ref_nxf_chunk_bytes(const char* path, const char* name, int c, uint8_t* out, size_t cap) {
+    using namespace nexus::format;
+    auto r = NXFReader::open(path);
+    if (!r) return -1;
+    const TensorInfo* t = r->get_tensor(name);
+    if (!t || c < 0 || c >= (int)t->chunks.size()) return -1;
+    const void* p = r->map_chunk(t->chunks[(size_t)c]);
+    if (!p) return -1;
+    const size_t n = t->chunks[(size_t)c].compressed_size;
+    std::memcpy(out, p, std::min(n, cap));
+    r->unmap_chunk(p);
+    return (long)n;
 }
 }

@@ -12,15 +12,19 @@ import oracle
 
 
 def declared_symbols():
-    text = nexus_amd.HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:nx_status|int|const char\s*\*)\s+(nx_\w+)\s*\(", text, flags=re.M)))
+    """Every entry point declared in include/*.h."""
+    syms = set()
+    for h in nexus_amd.HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        syms |= set(re.findall(r"^\s*(?:nx_status|int|const char\s*\*)\s+(nx_\w+)\s*\(", text, flags=re.M))
+    return sorted(syms)
 
 
 def test_header_declares_entry_points():
     syms = declared_symbols()
     for must in ("nx_init", "nx_gemv_int4_g32", "nx_attn_decode_paged_f16", "nx_attn_decode_paged_tq",
-                 "nx_tq_encode", "nx_moe_expert_ffn", "nx_model_decode", "nx_token_begin"):
+                 "nx_tq_encode", "nx_moe_expert_ffn", "nx_model_decode", "nx_token_begin",
+                 "nx_nxf_open", "nx_nxf_verify", "nx_xxh32_chunks", "nx_model_load_nxf"):
         assert must in syms
     assert len(syms) >= 40
 
