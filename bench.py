@@ -17,6 +17,9 @@ Also reported:
   cpu_baseline  the C oracle (OpenMP) on the host cores, on a bounded
                 sample: one 8B-shaped layer at 4096 context plus 1/8 of the
                 lm_head rows, scaled to a token (32 layers + full lm_head).
+  nxf_verify    XXH32 verification of NXF chunks on the GPU (k_xxh32): 4 GiB
+                (an 8B model's weight bytes) as 64 KiB chunks, HIP-event
+                timed, against the oracle's XXH32 on one host core.
 
 Other workloads: --model mixtral-8x7b (top-2 of 8 experts of 14336, vocab
 32000; the roofline kernel is then the routed gate/up expert GEMV), --kv tq
@@ -119,6 +122,36 @@ def gemv_microbench(ctx, batch: int = 1, iters: int = 200) -> list:
     return out
 
 
+def nxf_verify_bench(ctx, cpu: bool, nbytes: int = 4 << 30, chunk: int = 64 << 10, iters: int = 10) -> dict:
+    """GB/s of hashing nbytes of device memory as consecutive chunks (the
+    load-time verification of an NXF file's chunks); algorithmic bytes =
+    the chunk bytes, read once."""
+    from nexus_amd.nxf import time_xxh32
+    buf = ctx.alloc(nbytes)
+    ms, _ = time_xxh32(ctx, buf, nbytes, chunk, iters)
+    ctx.free(buf)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"kernel": "k_xxh32 (XXH32 of NXF chunks, 4 lanes per chunk)", "bytes": nbytes,
+           "chunk_bytes": chunk, "avg_us": round(ms * 1e3, 3), "achieved": round(gbs, 1),
+           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    if cpu:
+        import ctypes as C
+
+        import numpy as np
+
+        import oracle
+        sample = np.random.default_rng(0).integers(0, 256, 512 << 20, dtype=np.uint8)
+        ptr = sample.ctypes.data
+        t0 = time.perf_counter()
+        for off in range(0, sample.size, chunk):
+            oracle.lib.nxo_xxh32(C.c_void_p(ptr + off), chunk, 0)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(sample.size / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+                               "kind": "port", "sample": "512 MiB of random bytes as 64 KiB chunks, "
+                               "oracle XXH32 (nxo_xxh32) on one host core"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -129,7 +162,7 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--kv", choices=["fp16", "tq"], default="fp16")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--profile-kernel", choices=["ffn", "attention"],
+    ap.add_argument("--profile-kernel", choices=["ffn", "attention", "xxh32"],
                     help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy a 256 MiB buffer 16 times (counter calibration kernel)")
@@ -151,6 +184,12 @@ def main() -> int:
 
     import nexus_amd
 
+    if args.profile_kernel == "xxh32":
+        ctx = nexus_amd.Context(0)
+        r = nxf_verify_bench(ctx, False, iters=16)
+        print(json.dumps({"kernel": "xxh32", "avg_us": r["avg_us"], "bytes": r["bytes"], "launches": 17}))
+        ctx.close()
+        return 0
     kv_kind = 1 if args.kv == "tq" else 0
     max_seq = ((args.ctx + args.warmup + args.steps + 16) // 16 + 1) * 16
     base = MODELS[args.model]
@@ -190,6 +229,7 @@ def main() -> int:
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     model.close()
     micro = gemv_microbench(ctx, args.batch) if not moe else None
+    nxf = nxf_verify_bench(ctx, not args.no_cpu)
     ctx.close()
     kv_name = "fp16" if kv_kind == 0 else "TurboQuant 3.5-bit"
     if moe:
@@ -236,6 +276,7 @@ def main() -> int:
     }
     if micro is not None:
         line["gemv_microbench"] = micro
+    line["nxf_verify"] = nxf
     if not args.no_cpu:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind)
