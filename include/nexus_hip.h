@@ -123,6 +123,13 @@ nx_status nx_gemv_int4_g32_f32(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scal
 /* Unpack n int4 codes (low nibble first) to one byte each -- the bit-exact
  * check hook for the GPU unpack (quant::dequant_int4, gptq.cpp:12-25). */
 nx_status nx_unpack_int4(nx_ctx* ctx, nx_buf packed, nx_buf codes_u8, size_t n);
+/* GEMM of M rows: y[M][N] (fp32) = x[M][K] (fp16) . W^T, W int4-g32 as for
+ * the GEMV; accumulate != 0 adds into y.  The matrix-core kernel of the
+ * batched prefill: exact (q - 8) x products per group, scaled in fp32, as
+ * in the GEMV.  K must be a multiple of 8.  Replaces gemm_int4
+ * (compute_dispatch.h:59) with M activation rows. */
+nx_status nx_gemm_int4_g32(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16, nx_buf y_f32, int M, int N,
+                           int K, int accumulate);
 /* Device symmetric int4-g32 quantizer of w fp32 [N][K]: s = fp16(amax/7),
  * q = clamp(roundf(w/s), -8, 7) + 8.  (Replaces the offline quant_int4,
  * gptq.cpp:37-70, whose asymmetric output the GPU kernels never consumed.) */
@@ -228,6 +235,13 @@ nx_status nx_model_destroy(nx_model* m);
  * token by token; afterwards the greedy token of the last prompt position is
  * pending as the next input and written to next_tokens [batch] (optional). */
 nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens);
+/* Prefill mode: 1 (default) = batched -- for dense models with fp16 pages
+ * each sequence's prompt goes through every layer in chunks of up to 512
+ * tokens as int4-g32 GEMMs on the matrix cores, with causal attention over
+ * the pages; 0 = one decode step per prompt token (the reference's
+ * HybridModel::prefill loop, hybrid_model.cpp:604-644).  MoE and
+ * TurboQuant-page models always prefill one token per step. */
+nx_status nx_model_set_prefill(nx_model* m, int batched);
 /* Fill positions [0, ctx) of every layer's cache with synthetic N(0,1) K/V
  * (n_outlier channels per head scaled x10); the pending token of every
  * sequence becomes a seeded start token. */
@@ -267,6 +281,10 @@ nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x_f16, const nx_buf* wq, const nx_buf
 /* Same for the paged attention of the model's cache kind (split and merge
  * launches together), launch i over layer i % n_layers. */
 nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double* bytes);
+/* Average device time (ms) of nx_gemm_int4_g32 (no accumulate) over iters
+ * launches, HIP events on the library stream. */
+nx_status nx_time_gemm(nx_ctx* ctx, nx_buf x_f16, nx_buf wq, nx_buf scales_f16, nx_buf y_f32, int M, int N, int K,
+                       int iters, double* avg_ms);
 
 #ifdef __cplusplus
 }

@@ -364,6 +364,46 @@ nx_status nx_gemv_int4_g32_f32(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_b
                     "gemv");
 }
 
+nx_status nx_gemm_int4_g32(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int M, int N, int K,
+                           int accumulate) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (M < 1 || N < 1 || K < 8) return fail(ctx, NX_ERR_INVALID, "nx_gemm_int4_g32: bad shape");
+    if (K % 8) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_gemm_int4_g32: K must be a multiple of 8");
+    const int G = (K + 31) / 32;
+    NX_NEED(ctx, x, (size_t)M * K * 2, "x");
+    NX_NEED(ctx, wq, (size_t)N * G * 16, "codes");
+    NX_NEED(ctx, sc, (size_t)N * G * 2, "scales");
+    NX_NEED(ctx, y, (size_t)M * N * 4, "y");
+    nx::PfGemmArgs a{};
+    a.x = dptr<const uint16_t>(x);
+    a.ldx = K;
+    a.W = dptr<const uint8_t>(wq);
+    a.S = dptr<const uint16_t>(sc);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.G = G;
+    a.y32 = dptr<float>(y);
+    a.ldy = N;
+    return launched(ctx, nx::pf_gemm_launch(accumulate ? nx::PF_ACC : nx::PF_F32, a, ctx->stream), "gemm");
+}
+
+nx_status nx_time_gemm(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int M, int N, int K, int iters,
+                       double* avg_ms) {
+    if (!ctx || !avg_ms || iters < 1) return NX_ERR_INVALID;
+    nx_status s = nx_gemm_int4_g32(ctx, x, wq, sc, y, M, N, K, 0);  // validation and warm-up
+    if (s != NX_OK) return s;
+    NX_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
+    for (int i = 0; i < iters; ++i)
+        if ((s = nx_gemm_int4_g32(ctx, x, wq, sc, y, M, N, K, 0)) != NX_OK) return s;
+    NX_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));
+    NX_HIP(ctx, hipEventSynchronize(ctx->ev1));
+    float ms = 0.0f;
+    NX_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+    *avg_ms = (double)ms / iters;
+    return NX_OK;
+}
+
 nx_status nx_unpack_int4(nx_ctx* ctx, nx_buf packed, nx_buf codes, size_t n) {
     if (!ctx) return NX_ERR_INVALID;
     if (n % 2) return fail(ctx, NX_ERR_INVALID, "nx_unpack_int4: n must be even");

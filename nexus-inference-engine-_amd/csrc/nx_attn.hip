@@ -895,6 +895,12 @@ size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
 
 int attn_max_ctx() { return kMaxSplits * kPagesPerSplitMax * kPage; }
 
+SplitPlan plan_splits_f16(int max_ctx, int hkv, int batch);
+size_t attn_f16_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
+    const SplitPlan sp = plan_splits_f16(max_ctx, hkv, batch);
+    return sizeof(float) * (size_t)batch * hkv * sp.nsplit * rec_floats(hq / hkv, hd);
+}
+
 // TurboQuant splits: about one block per CU over all (kv head, sequence)
 // pairs (the pipelined kernel holds one 8-wavefront block per CU), never
 // more splits than plan_splits (which sizes the workspace).

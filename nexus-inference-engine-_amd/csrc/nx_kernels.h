@@ -100,6 +100,10 @@ struct AttnArgs {
 };
 constexpr int kAttnCountStride = 64;  // counters 256 bytes apart
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
+// Workspace of attn_f16_launch for exactly this (batch, max_ctx): the split
+// plan it launches, which has fewer splits than attn_workspace_bytes assumes
+// when batch x kv heads exceeds the CU count.
+size_t attn_f16_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
 inline size_t attn_count_words(int batch, int hkv) { return (size_t)batch * hkv * kAttnCountStride; }
 // Longest context the attention kernels accept.
 int attn_max_ctx();
@@ -221,6 +225,27 @@ struct MoeFfnArgs {
 hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st);
+
+// Batched prefill (nx_prefill.hip): int4-g32 GEMM Y = X W^T on the matrix
+// cores, X fp16 [M][ldx] (K and ldx multiples of 8, 16-byte aligned rows).
+enum { PF_F32 = 0, PF_ACC = 1, PF_SWIGLU = 2 };
+struct PfGemmArgs {
+    const uint16_t* x;
+    int ldx;
+    const uint8_t* W;    // codes [N][G*16]
+    const uint16_t* S;   // fp16 scales [N][G]
+    int M, N, K, G;
+    float* y32;          // PF_F32: y32[m][n] = y; PF_ACC: y32[m][n] += y
+    int ldy;
+    uint16_t* act16;     // PF_SWIGLU: rows 2f, 2f+1 = gate f, up f -> act16[m][f]
+    int lda;
+};
+hipError_t pf_gemm_launch(int epi, const PfGemmArgs& a, hipStream_t st);
+hipError_t pf_embed_launch(const int32_t* tokens, int P, const uint16_t* embed, float* h, int d, int vocab,
+                           hipStream_t st);
+hipError_t pf_rope_kv_launch(const float* qkv, int ld, int P, int p0, int qdim, int kvdim, int hd, int hkv,
+                             const float* cos_t, const float* sin_t, const int32_t* bt, uint16_t* kpool,
+                             uint16_t* vpool, float* q32, hipStream_t st);
 
 // XXH32 (seed 0) of byte ranges of one device buffer: range i is
 // [off, off + len) (off a multiple of 16); its hash goes to out[slot].

@@ -1,0 +1,236 @@
+// Batched prefill of a prompt: the reference runs a prompt one token at a
+// time through the decode layers (HybridModel::prefill,
+// nexus/src/model/hybrid_model.cpp:604-644); here a chunk of P prompt tokens
+// goes through each layer at once, so every projection is a GEMM
+// [P x K] x [K x N] on the matrix cores instead of P weight-streaming GEMVs.
+//
+// k_pf_gemm: Y = X W^T with X fp16 [M][ldx] (tokens) and W int4-g32 (codes
+// [N][G*16], fp16 scales [N][G]).  A block computes 128 tokens x 64 weight
+// rows; its four wavefronts take 64 x 32 each as 4 x 2 tiles of
+// v_mfma_f32_16x16x32_f16 (A = X: row = token; B = W: column = weight row;
+// one 32-k group per product).  Per stage of two groups the block stages X
+// in LDS in the k order (0 2 4 6 1 3 5 7) of each 8-k chunk -- the order in
+// which a code dword turns into fp16 with two byte permutes -- and the codes
+// and scales of its 64 rows; the next stage's loads are in flight while the
+// current one is multiplied.  A wavefront turns each B fragment into fp16
+// q - 8 once (exact) and uses it for its four token tiles; each group's
+// product goes to a zeroed accumulator and is added scaled by the group's
+// scale in fp32 (a lane's output column is one weight row, so one scale per
+// lane), the numerics of the decode GEMV.  Epilogues: fp32 store, fp32
+// accumulate (residual), SwiGLU of interleaved gate/up rows to fp16.
+#include "nx_common.h"
+#include "nx_kernels.h"
+
+namespace nx {
+namespace {
+
+typedef _Float16 ph8_t __attribute__((ext_vector_type(8)));
+typedef float pf4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kPfBM = 128, kPfBN = 64, kPfBK = 64, kPfThreads = 256;
+constexpr int kPfAStride = kPfBK + 8;  // fp16 per LDS row of X: 144 bytes, so 16 rows read conflict-free
+
+// Code dword (8 nibbles, low nibble = even k) -> fp16 (q - 8) in the k order
+// (0 2 4 6 1 3 5 7): each nibble byte joined with 0x64 is the fp16 1024 + q.
+__device__ inline ph8_t pf_codes_to_h8(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu, k64 = 0x64646464u;
+    const uint4 r = make_uint4(__builtin_amdgcn_perm(k64, lo, 0x04010400u), __builtin_amdgcn_perm(k64, lo, 0x04030402u),
+                               __builtin_amdgcn_perm(k64, hi, 0x04010400u), __builtin_amdgcn_perm(k64, hi, 0x04030402u));
+    return __builtin_bit_cast(ph8_t, r) - (_Float16)1032.0f;
+}
+
+// Eight fp16 of consecutive k (4 dwords) into the k order (0 2 4 6 1 3 5 7).
+__device__ inline uint4 pf_perm_x8(uint4 x) {
+    return make_uint4(__builtin_amdgcn_perm(x.y, x.x, 0x05040100u), __builtin_amdgcn_perm(x.w, x.z, 0x05040100u),
+                      __builtin_amdgcn_perm(x.y, x.x, 0x07060302u), __builtin_amdgcn_perm(x.w, x.z, 0x07060302u));
+}
+
+__device__ inline float lane_xor1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
+    __shared__ __align__(16) uint16_t As[2][kPfBM * kPfAStride];
+    __shared__ __align__(16) uint32_t Bs[2][kPfBN * 8];  // [row][group 0/1][4 dwords]
+    __shared__ uint32_t Ss[2][kPfBN];                    // [row]: scales of groups 0 (low) and 1 (high)
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int c = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * kPfBN, m0 = blockIdx.y * kPfBM;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int M = a.M, N = a.N, K = a.K, G = a.G;
+    const int nstage = (G + 1) / 2;
+
+    // global -> registers for stage s; every address is clamped into its
+    // tensor and out-of-range values are zeroed after the load
+    uint4 ra[4], rb = make_uint4(0, 0, 0, 0);
+    uint32_t rs = 0;
+    auto load = [&](int s) {
+        const int kb = s * kPfBK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ch = tid + kPfThreads * j, row = ch >> 3, k = kb + 8 * (ch & 7);
+            const int m = min(m0 + row, M - 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(a.x + (size_t)m * a.ldx + min(k, K - 8));
+            const bool ok = k < K && m0 + row < M;
+            ra[j] = ok ? v : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < 2 * kPfBN) {
+            const int n = min(n0 + (tid >> 1), N - 1), g = min(2 * s + (tid & 1), G - 1);
+            rb = *reinterpret_cast<const uint4*>(a.W + ((size_t)n * G + g) * 16);
+        }
+        if (tid < kPfBN) {
+            const int n = min(n0 + tid, N - 1);
+            const uint16_t* sr = a.S + (size_t)n * G;
+            rs = (uint32_t)sr[min(2 * s, G - 1)] | ((uint32_t)sr[min(2 * s + 1, G - 1)] << 16);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ch = tid + kPfThreads * j, row = ch >> 3;
+            *reinterpret_cast<uint4*>(&As[buf][row * kPfAStride + 8 * (ch & 7)]) = pf_perm_x8(ra[j]);
+        }
+        if (tid < 2 * kPfBN) *reinterpret_cast<uint4*>(&Bs[buf][(tid >> 1) * 8 + (tid & 1) * 4]) = rb;
+        if (tid < kPfBN) Ss[buf][tid] = rs;
+    };
+
+    pf4_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = pf4_t{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int s = 0; s < nstage; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < nstage) load(s + 1);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            ph8_t af[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                af[i] = __builtin_bit_cast(
+                    ph8_t, *reinterpret_cast<const uint4*>(&As[buf][(64 * wm + 16 * i + c) * kPfAStride + 32 * g + 8 * kq]));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int row = 32 * wn + 16 * j + c;
+                const ph8_t w = pf_codes_to_h8(Bs[buf][row * 8 + g * 4 + kq]);
+                const float sc = h2f_bits((uint16_t)(Ss[buf][row] >> (16 * g)));
+                const pf4_t z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const pf4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], w, z, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(p[r], sc, acc[i][j][r]);
+                }
+            }
+        }
+        if (s + 1 < nstage) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // tile (i, j): lane (c, kq) holds weight row n0 + 32 wn + 16 j + c for
+    // tokens m0 + 64 wm + 16 i + 4 kq + r, r < 4
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + 32 * wn + 16 * j + c;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 64 * wm + 16 * i + 4 * kq + r;
+                const float v = acc[i][j][r];
+                if (EPI == PF_SWIGLU) {
+                    const float u = lane_xor1(v);  // the up row n + 1 sits in lane c + 1
+                    if ((c & 1) == 0 && m < M && n + 1 < N)
+                        a.act16[(size_t)m * a.lda + (n >> 1)] = f2h_bits(v / (1.0f + expf(-v)) * u);
+                } else if (m < M && n < N) {
+                    float* y = a.y32 + (size_t)m * a.ldy + n;
+                    *y = EPI == PF_ACC ? *y + v : v;
+                }
+            }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_pf_embed(const int32_t* tokens, const uint16_t* embed, float* h, int d,
+                                                  int vocab) {
+    int tok = tokens[blockIdx.x];
+    if (tok < 0 || tok >= vocab) tok = 0;  // the host checked the prompt; never index outside the table
+    const uint16_t* src = embed + (size_t)tok * d;
+    float* dst = h + (size_t)blockIdx.x * d;
+    for (int i = threadIdx.x; i < d; i += 256) dst[i] = h2f_bits(src[i]);
+}
+
+// RoPE of the q and k rows of token t at position p0 + t (the rotation of
+// the decode QKV epilogue), q to q32 [P][qdim], k and v (fp16, RNE) into
+// the pages of the sequence (block table row bt).
+__global__ __launch_bounds__(256) void k_pf_rope_kv(const float* qkv, int ld, int P, int p0, int qdim, int kvdim,
+                                                    int hd, int hkv, const float* cos_t, const float* sin_t,
+                                                    const int32_t* bt, uint16_t* kpool, uint16_t* vpool, float* q32) {
+    const int npair = (qdim + 2 * kvdim) / 2;
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long)P * npair) return;
+    const int t = (int)(idx / npair), row = 2 * (int)(idx % npair), p = p0 + t, half = hd >> 1;
+    float v0 = qkv[(size_t)t * ld + row], v1 = qkv[(size_t)t * ld + row + 1];
+    if (row < qdim + kvdim) {
+        const int i = (row % hd) >> 1;
+        const float c = cos_t[(size_t)p * half + i], s = sin_t[(size_t)p * half + i];
+        const float r0 = v0 * c - v1 * s;
+        const float r1 = v0 * s + v1 * c;
+        v0 = r0;
+        v1 = r1;
+    }
+    if (row < qdim) {
+        q32[(size_t)t * qdim + row] = v0;
+        q32[(size_t)t * qdim + row + 1] = v1;
+        return;
+    }
+    const int kv = row < qdim + kvdim ? 0 : 1, j = row - qdim - kv * kvdim, kvh = j / hd, dd = j % hd;
+    const size_t page = ((size_t)bt[p / kPage] * hkv + kvh) * kPage * hd;
+    if (kv) {  // V pages are dimension-major [hd][16]
+        vpool[page + (size_t)dd * kPage + p % kPage] = f2h_bits(v0);
+        vpool[page + (size_t)(dd + 1) * kPage + p % kPage] = f2h_bits(v1);
+    } else {   // K pages are token-major [16][hd]
+        kpool[page + (size_t)(p % kPage) * hd + dd] = f2h_bits(v0);
+        kpool[page + (size_t)(p % kPage) * hd + dd + 1] = f2h_bits(v1);
+    }
+}
+
+}  // namespace
+
+hipError_t pf_gemm_launch(int epi, const PfGemmArgs& a, hipStream_t st) {
+    // 16-byte rows of x (K and ldx multiples of 8, aligned base), at least one
+    // full 8-k chunk
+    if (a.M < 1 || a.N < 1 || a.K < 8 || a.K % 8 || a.ldx % 8 || (reinterpret_cast<uintptr_t>(a.x) & 15) ||
+        a.G != (a.K + 31) / 32 || (epi == PF_SWIGLU && a.N % 2))
+        return hipErrorInvalidValue;
+    const dim3 grid((a.N + kPfBN - 1) / kPfBN, (a.M + kPfBM - 1) / kPfBM);
+    if (grid.y > 65535) return hipErrorInvalidValue;
+    switch (epi) {
+        case PF_F32: hipLaunchKernelGGL(k_pf_gemm<PF_F32>, grid, dim3(kPfThreads), 0, st, a); break;
+        case PF_ACC: hipLaunchKernelGGL(k_pf_gemm<PF_ACC>, grid, dim3(kPfThreads), 0, st, a); break;
+        case PF_SWIGLU: hipLaunchKernelGGL(k_pf_gemm<PF_SWIGLU>, grid, dim3(kPfThreads), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t pf_embed_launch(const int32_t* tokens, int P, const uint16_t* embed, float* h, int d, int vocab,
+                           hipStream_t st) {
+    hipLaunchKernelGGL(k_pf_embed, dim3(P), dim3(256), 0, st, tokens, embed, h, d, vocab);
+    return hipGetLastError();
+}
+
+hipError_t pf_rope_kv_launch(const float* qkv, int ld, int P, int p0, int qdim, int kvdim, int hd, int hkv,
+                             const float* cos_t, const float* sin_t, const int32_t* bt, uint16_t* kpool,
+                             uint16_t* vpool, float* q32, hipStream_t st) {
+    const long n = (long)P * ((qdim + 2 * kvdim) / 2);
+    hipLaunchKernelGGL(k_pf_rope_kv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, qkv, ld, P, p0, qdim, kvdim,
+                       hd, hkv, cos_t, sin_t, bt, kpool, vpool, q32);
+    return hipGetLastError();
+}
+
+}  // namespace nx

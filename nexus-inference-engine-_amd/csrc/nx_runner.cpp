@@ -86,6 +86,7 @@ struct nx_model {
     hipGraphExec_t exec = nullptr;        // one decode step
     hipGraphExec_t exec_multi = nullptr;  // kStepsPerGraph decode steps
     std::vector<int> hpos;       // host mirror of pos (last processed position)
+    int prefill_batched = 1;     // batched (GEMM) prefill where the model allows it
 };
 
 namespace {
@@ -576,6 +577,178 @@ nx_status nx_model_destroy(nx_model* m) {
     return free_model(m);
 }
 
+}  // extern "C"
+
+namespace {
+
+constexpr int kPrefillChunk = 512;  // prompt tokens per pass through the layers
+
+// Device scratch of one prefill call, released on every exit path.
+struct PrefillScratch {
+    std::vector<void*> p;
+    ~PrefillScratch() {
+        for (void* q : p) (void)hipFree(q);
+    }
+    template <class T>
+    hipError_t get(T** out, size_t count) {
+        void* q = nullptr;
+        hipError_t e = hipMalloc(&q, std::max<size_t>(count * sizeof(T), 16));
+        if (e == hipSuccess) p.push_back(q);
+        *out = static_cast<T*>(q);
+        return e;
+    }
+};
+
+// The prompt of sequence b (P tokens, at positions hpos[b] + 1 on) through
+// every layer, kPrefillChunk tokens at a time: RMSNorm rows, QKV GEMM, RoPE
+// and page writes, causal attention (the split kernel with one row per
+// query token, row t seeing positions <= its own), output projection and
+// FFN GEMMs with the residual accumulated in place.  Then the final RMSNorm,
+// lm_head and argmax of the last token leave its greedy successor pending,
+// as after P decode steps.  Dense models with fp16 pages.
+nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
+    const nx_model_config& c = m->c;
+    nx_ctx* ctx = m->ctx;
+    hipStream_t st = ctx->stream;
+    const int d = c.d_model, F = c.ffn, hq = c.n_heads, hkv = c.n_kv_heads, hd = c.head_dim;
+    const int C = std::min(P, kPrefillChunk), p0 = m->hpos[(size_t)b] + 1, MB = m->max_blocks;
+    const int pend = p0 + P;  // first position after the prompt
+    PrefillScratch sc;
+    int32_t *tok = nullptr, *lens = nullptr, *bt = nullptr;
+    float *h = nullptr, *qkv = nullptr, *q = nullptr, *part = nullptr;
+    uint16_t *x16 = nullptr, *att = nullptr, *act = nullptr;
+    unsigned* counts = nullptr;
+    const size_t ws = nx::attn_f16_workspace_bytes(C, hq, hkv, hd, pend);
+    const size_t cw = nx::attn_count_words(C, hkv);
+    if (sc.get(&tok, C) != hipSuccess || sc.get(&lens, C) != hipSuccess || sc.get(&bt, (size_t)C * MB) != hipSuccess ||
+        sc.get(&h, (size_t)C * d) != hipSuccess || sc.get(&qkv, (size_t)C * m->nqkv) != hipSuccess ||
+        sc.get(&q, (size_t)C * m->qdim) != hipSuccess || sc.get(&part, ws / sizeof(float) + 4) != hipSuccess ||
+        sc.get(&x16, (size_t)C * d) != hipSuccess || sc.get(&att, (size_t)C * m->qdim) != hipSuccess ||
+        sc.get(&act, (size_t)C * m->Fp) != hipSuccess || sc.get(&counts, cw) != hipSuccess)
+        return fail(ctx, NX_ERR_OOM, "prefill: scratch for %d tokens", C);
+    NX_HIP(ctx, hipMemsetAsync(counts, 0, cw * sizeof(unsigned), st));
+    // every query row of a chunk reads the sequence's block table
+    std::vector<int32_t> row((size_t)MB), rep((size_t)C * MB);
+    NX_HIP(ctx, hipMemcpyAsync(row.data(), m->block_table + (size_t)b * MB, (size_t)MB * 4, hipMemcpyDeviceToHost, st));
+    NX_HIP(ctx, hipStreamSynchronize(st));
+    for (int t = 0; t < C; ++t) std::copy(row.begin(), row.end(), rep.begin() + (size_t)t * MB);
+    NX_HIP(ctx, hipMemcpyAsync(bt, rep.data(), rep.size() * 4, hipMemcpyHostToDevice, st));
+    std::vector<int32_t> hl((size_t)C);
+    int last = 0;
+    for (int done = 0; done < P; done += C) {
+        const int n = std::min(C, P - done), pb = p0 + done;
+        for (int t = 0; t < n; ++t) hl[(size_t)t] = pb + t + 1;
+        NX_HIP(ctx, hipMemcpyAsync(tok, tokens + done, (size_t)n * 4, hipMemcpyHostToDevice, st));
+        NX_HIP(ctx, hipMemcpyAsync(lens, hl.data(), (size_t)n * 4, hipMemcpyHostToDevice, st));
+        NX_LAUNCH(m, nx::pf_embed_launch(tok, n, m->embed, h, d, c.vocab, st));
+        for (int L = 0; L < c.n_layers; ++L) {
+            Layer& ly = m->layers[(size_t)L];
+            NX_LAUNCH(m, nx::rmsnorm_launch(h, ly.norm_attn, x16, d, c.eps, n, st));
+            nx::PfGemmArgs g{};
+            g.x = x16;
+            g.ldx = d;
+            g.W = ly.wqkv;
+            g.S = ly.sqkv;
+            g.M = n;
+            g.N = m->nqkv;
+            g.K = d;
+            g.G = m->Gd;
+            g.y32 = qkv;
+            g.ldy = m->nqkv;
+            NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_F32, g, st));
+            NX_LAUNCH(m, nx::pf_rope_kv_launch(qkv, m->nqkv, n, pb, m->qdim, m->kvdim, hd, hkv, m->rope_cos, m->rope_sin,
+                                               m->block_table + (size_t)b * MB, ly.kpool, ly.vpool, q, st));
+            nx::AttnArgs at{};
+            at.q = q;
+            at.kpool = ly.kpool;
+            at.vpool = ly.vpool;
+            at.block_table = bt;
+            at.ctx_lens = lens;
+            at.out16 = att;
+            at.batch = n;
+            at.hq = hq;
+            at.hkv = hkv;
+            at.hd = hd;
+            at.max_blocks = MB;
+            at.max_ctx = pend;
+            at.part = part;
+            at.counts = counts;
+            NX_LAUNCH(m, nx::attn_f16_launch(at, st));
+            nx::PfGemmArgs o{};
+            o.x = att;
+            o.ldx = m->qdim;
+            o.W = ly.wo;
+            o.S = ly.so;
+            o.M = n;
+            o.N = d;
+            o.K = m->qdim;
+            o.G = m->Gq;
+            o.y32 = h;
+            o.ldy = d;
+            NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_ACC, o, st));
+            NX_LAUNCH(m, nx::rmsnorm_launch(h, ly.norm_ffn, x16, d, c.eps, n, st));
+            nx::PfGemmArgs f{};
+            f.x = x16;
+            f.ldx = d;
+            f.W = ly.w13;
+            f.S = ly.s13;
+            f.M = n;
+            f.N = 2 * F;
+            f.K = d;
+            f.G = m->Gd;
+            f.act16 = act;
+            f.lda = m->Fp;
+            NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_SWIGLU, f, st));
+            nx::PfGemmArgs dn{};
+            dn.x = act;
+            dn.ldx = m->Fp;
+            dn.W = ly.w2;
+            dn.S = ly.s2;
+            dn.M = n;
+            dn.N = d;
+            dn.K = F;
+            dn.G = m->Gf;
+            dn.y32 = h;
+            dn.ldy = d;
+            NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_ACC, dn, st));
+        }
+        last = n - 1;
+        NX_HIP(ctx, hipStreamSynchronize(st));  // the host staging of tokens and lengths is refilled next
+    }
+    // the last prompt token: final RMSNorm, lm_head and argmax into best[b]
+    NX_HIP(ctx, hipMemsetAsync(m->best + b, 0, sizeof(unsigned long long), st));
+    nx::GemvArgs lm{};
+    lm.W = m->lm_w;
+    lm.S = m->lm_s;
+    lm.N = c.vocab;
+    lm.K = d;
+    lm.G = m->Gd;
+    lm.batch = 1;
+    lm.h32 = h + (size_t)last * d;
+    lm.ldx = d;
+    lm.eps = c.eps;
+    lm.norm_w = m->norm_final;
+    lm.y32 = m->logits + (size_t)b * c.vocab;
+    lm.ldy = c.vocab;
+    lm.best = m->best + b;
+    NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_LOGITS, lm, st));
+    const int32_t plast = pend - 1;
+    NX_HIP(ctx, hipMemcpyAsync(m->pos + b, &plast, 4, hipMemcpyHostToDevice, st));
+    NX_HIP(ctx, hipStreamSynchronize(st));
+    m->hpos[(size_t)b] = plast;
+    return NX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+nx_status nx_model_set_prefill(nx_model* m, int batched) {
+    if (!m || (batched != 0 && batched != 1)) return NX_ERR_INVALID;
+    m->prefill_batched = batched;
+    return NX_OK;
+}
+
 nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens) {
     if (!m || !prompt || P < 1) return NX_ERR_INVALID;
     const nx_model_config& c = m->c;
@@ -585,6 +758,11 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
         for (int i = 0; i < P; ++i)
             if (prompt[(size_t)b * P + i] < 0 || prompt[(size_t)b * P + i] >= c.vocab)
                 return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
+    }
+    if (m->prefill_batched && c.n_experts == 0 && c.kv_kind == 0) {
+        for (int b = 0; b < B; ++b) NX_TRY(prefill_batched(m, b, prompt + (size_t)b * P, P));
+        if (next_tokens) NX_TRY(nx_model_pending(m, next_tokens));
+        return NX_OK;
     }
     NX_TRY(ensure_graph(m));
     hipStream_t st = m->ctx->stream;

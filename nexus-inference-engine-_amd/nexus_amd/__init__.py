@@ -97,6 +97,8 @@ _SIGS = {
     "nx_gemv_int4_g32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I]),
     "nx_gemv_int4_g32_f32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I]),
     "nx_unpack_int4": (_I, [_P, _B, _B, C.c_size_t]),
+    "nx_gemm_int4_g32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I]),
+    "nx_time_gemm": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I, C.POINTER(C.c_double)]),
     "nx_quantize_int4_g32": (_I, [_P, _B, _B, _B, _I, _I]),
     "nx_rmsnorm": (_I, [_P, _B, _B, _B, _I, _F, _I]),
     "nx_rope": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I]),
@@ -115,6 +117,7 @@ _SIGS = {
     "nx_model_create": (_I, [_P, C.POINTER(ModelConfig), C.POINTER(_P)]),
     "nx_model_destroy": (_I, [_P]),
     "nx_model_prefill": (_I, [_P, _P, _I, _P]),
+    "nx_model_set_prefill": (_I, [_P, _I]),
     "nx_model_fill_context": (_I, [_P, _I, _I]),
     "nx_model_pending": (_I, [_P, _P]),
     "nx_model_decode": (_I, [_P, _I, _P]),
@@ -255,6 +258,9 @@ class Context:
     def gemv(self, x, wq, sc, y, N, K, batch=1):
         self.check(self.L.nx_gemv_int4_g32(self.h, x, wq, sc, y, N, K, batch), "nx_gemv_int4_g32")
 
+    def gemm(self, x, wq, sc, y, M, N, K, accumulate=False):
+        self.check(self.L.nx_gemm_int4_g32(self.h, x, wq, sc, y, M, N, K, int(accumulate)), "nx_gemm_int4_g32")
+
     def gemv_f32(self, x, wq, sc, y, N, K, batch=1, accumulate=False):
         self.check(self.L.nx_gemv_int4_g32_f32(self.h, x, wq, sc, y, N, K, batch, int(accumulate)),
                    "nx_gemv_int4_g32_f32")
@@ -311,6 +317,10 @@ class Model:
         self.ctx.check(self.ctx.L.nx_model_prefill(self.h, p.ctypes.data, p.shape[1], nxt.ctypes.data),
                        "nx_model_prefill")
         return nxt
+
+    def set_prefill(self, batched: bool):
+        """Batched GEMM prefill (default) or one decode step per prompt token."""
+        self.ctx.check(self.ctx.L.nx_model_set_prefill(self.h, int(batched)), "nx_model_set_prefill")
 
     def fill_context(self, ctx_len: int, n_outlier: int = 0):
         self.ctx.check(self.ctx.L.nx_model_fill_context(self.h, ctx_len, n_outlier),
