@@ -176,10 +176,14 @@ __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, in
 // Fold one page pair into the wavefront's state: m (running max of head l%16),
 // lsum (this lane's share of the softmax denominator), O (C layout, rows =
 // heads 4(l/16) + i, columns = dims 16 nt + l%16).
-template <int HD>
+// CAUSAL (prefill): the columns are query tokens instead of heads; token
+// 4(l/16) + i of page a (b) is at position pos_a (pos_b) + 4(l/16) + i and
+// is masked for the query at position qpos (this lane's column) when later.
+template <int HD, bool CAUSAL = false>
 __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 32],
                                    const h8_t (&ql)[HD / 32], float scale, int na, int nb, float& m,
-                                   float& lsum, f4_t (&o)[HD / 16], int lane) {
+                                   float& lsum, f4_t (&o)[HD / 16], int lane, int pos_a = 0, int pos_b = 0,
+                                   int qpos = 0) {
     const int g = lane >> 4;
     f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -193,8 +197,10 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
     float mloc = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        p[i] = 4 * g + i < na ? sa[i] * scale : -__builtin_inff();
-        p[4 + i] = 4 * g + i < nb ? sb[i] * scale : -__builtin_inff();
+        const bool va = 4 * g + i < na && (!CAUSAL || pos_a + 4 * g + i <= qpos);
+        const bool vb = 4 * g + i < nb && (!CAUSAL || pos_b + 4 * g + i <= qpos);
+        p[i] = va ? sa[i] * scale : -__builtin_inff();
+        p[4 + i] = vb ? sb[i] * scale : -__builtin_inff();
         mloc = fmaxf(mloc, fmaxf(p[i], p[4 + i]));
     }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
@@ -885,7 +891,98 @@ __global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batc
         tq_encode_wave(src, vsign, vc4 + dst * 32, vc3 + dst * 24, vn + dst, codes[wave]);
 }
 
+// Causal prefill attention over fp16 pages: query rows t < P of one sequence
+// (positions p0 + t) attend to the positions <= their own.  A wavefront takes
+// 16 consecutive queries of one head as the columns of the decode layout
+// (S = K q^T per page, O = P V per page pair), a block the G heads of one kv
+// head for the same queries, whose page loads are the same addresses and
+// meet in the L1.  Each wavefront walks the page pairs up to its last
+// query's position; the scores get the causal mask per (token, query).
+// Blocks are numbered from the last query tile down, so the longest walks
+// start first.
+template <int G, int HD>
+__global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int P) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, t = lane & 15;
+    const int kvh = blockIdx.y, h = kvh * G + w;
+    const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16;
+    const int lastpos = p0 + min(q0 + 15, P - 1);
+    const int npages = lastpos / kPage + 1;
+    // q as the B operand: column t = query q0 + t (clamped: columns past the
+    // prompt repeat its last query and are not written), k = 8g + j
+    h8_t qh[HD / 32], ql[HD / 32];
+    {
+        const float* qsrc = a.q + ((size_t)min(q0 + t, P - 1) * a.hq + h) * HD + 8 * g;
+        float4 x[HD / 32][2];
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s) {
+            x[s][0] = *reinterpret_cast<const float4*>(qsrc + 32 * s);
+            x[s][1] = *reinterpret_cast<const float4*>(qsrc + 32 * s + 4);
+        }
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s) {
+            const float v[8] = {x[s][0].x, x[s][0].y, x[s][0].z, x[s][0].w,
+                                x[s][1].x, x[s][1].y, x[s][1].z, x[s][1].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                qh[s][j] = (_Float16)v[j];
+                ql[s][j] = (_Float16)(v[j] - (float)qh[s][j]);
+            }
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int qpos = p0 + min(q0 + t, P - 1);
+    float m = -__builtin_inff(), lsum = 0.0f;
+    f4_t o[HD / 16];
+#pragma unroll
+    for (int nt = 0; nt < HD / 16; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int pa = 0; pa < npages; pa += 2) {
+        const int pb = pa + 1;
+        const int na = min(max(lastpos + 1 - kPage * pa, 0), kPage);
+        const int nb = min(max(lastpos + 1 - kPage * pb, 0), kPage);
+        const int blka = a.block_table[pa];
+        const int blkb = pb < npages ? a.block_table[pb] : blka;
+        PairRaw<HD> r;
+        load_pair<HD>(r, a, blka, na, blkb, nb, kvh, lane);
+        pair_update<HD, true>(r, qh, ql, scale, na, nb, m, lsum, o, lane, kPage * pa, kPage * pb, qpos);
+    }
+    // the query's denominator: sum of the four lanes that share its column
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    // rows of O in this lane are queries 4g + i, their denominators in lanes 4g + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float L = __shfl(lsum, 4 * g + i, 64);
+        const int q = q0 + 4 * g + i;
+        if (q < P) {
+            uint16_t* out = a.out16 + ((size_t)q * a.hq + h) * HD + t;
+#pragma unroll
+            for (int nt = 0; nt < HD / 16; ++nt) out[16 * nt] = f2h_bits(o[nt][i] / L);
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st) {
+    if (P < 1 || p0 < 0 || !a.block_table) return hipErrorInvalidValue;
+    const dim3 grid((P + 15) / 16, a.hkv);
+    const int G = a.hq / a.hkv;
+#define NX_PF_ATTN_CASE(GG, HH)                                                                       \
+    if (G == GG && a.hd == HH) {                                                                      \
+        hipLaunchKernelGGL((k_attn_prefill<GG, HH>), grid, dim3(64 * GG), 0, st, a, p0, P);           \
+        return hipGetLastError();                                                                     \
+    }
+    NX_PF_ATTN_CASE(1, 64)
+    NX_PF_ATTN_CASE(2, 64)
+    NX_PF_ATTN_CASE(4, 64)
+    NX_PF_ATTN_CASE(8, 64)
+    NX_PF_ATTN_CASE(1, 128)
+    NX_PF_ATTN_CASE(2, 128)
+    NX_PF_ATTN_CASE(4, 128)
+    NX_PF_ATTN_CASE(8, 128)
+#undef NX_PF_ATTN_CASE
+    return hipErrorInvalidValue;
+}
 
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
     const SplitPlan sp = plan_splits(max_ctx);

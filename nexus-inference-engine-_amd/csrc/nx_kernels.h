@@ -110,6 +110,10 @@ int attn_max_ctx();
 // Each enqueues two launches: the split kernel and the merge of its records.
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st);
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st);
+// Causal prefill attention over fp16 pages: q rows t < P ([P][hq][hd]) of
+// one sequence at positions p0 + t, block_table = that sequence's row,
+// out16 [P][hq][hd]; row t attends to positions <= p0 + t.  No workspace.
+hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st);
 
 // ---------------------------------------------------------------- misc --
 hipError_t rmsnorm_launch(const float* x, const float* w, uint16_t* out, int dim, float eps,

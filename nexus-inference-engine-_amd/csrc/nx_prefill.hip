@@ -8,7 +8,7 @@
 // [N][G*16], fp16 scales [N][G]).  A block computes 128 tokens x 64 weight
 // rows; its four wavefronts take 64 x 32 each as 4 x 2 tiles of
 // v_mfma_f32_16x16x32_f16 (A = X: row = token; B = W: column = weight row;
-// one 32-k group per product).  Per stage of two groups the block stages X
+// one 32-k group per product).  Per stage of four groups the block stages X
 // in LDS in the k order (0 2 4 6 1 3 5 7) of each 8-k chunk -- the order in
 // which a code dword turns into fp16 with two byte permutes -- and the codes
 // and scales of its 64 rows; the next stage's loads are in flight while the
@@ -27,8 +27,11 @@ namespace {
 typedef _Float16 ph8_t __attribute__((ext_vector_type(8)));
 typedef float pf4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kPfBM = 128, kPfBN = 64, kPfBK = 64, kPfThreads = 256;
-constexpr int kPfAStride = kPfBK + 8;  // fp16 per LDS row of X: 144 bytes, so 16 rows read conflict-free
+constexpr int kPfBM = 128, kPfBN = 64, kPfBK = 128, kPfThreads = 256;
+constexpr int kPfGPS = kPfBK / 32;          // groups per stage
+constexpr int kPfAStride = kPfBK + 8;       // fp16 per LDS row of X: rows 4 banks apart, 16 rows read conflict-free
+constexpr int kPfAChunks = kPfBM * kPfBK / 8 / kPfThreads;  // 16-byte chunks of X per thread per stage
+static_assert(kPfBN * kPfGPS <= kPfThreads, "one code group and one scale per thread");
 
 // Code dword (8 nibbles, low nibble = even k) -> fp16 (q - 8) in the k order
 // (0 2 4 6 1 3 5 7): each nibble byte joined with 0x64 is the fp16 1024 + q.
@@ -52,47 +55,46 @@ __device__ inline float lane_xor1(float v) {
 template <int EPI>
 __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
     __shared__ __align__(16) uint16_t As[2][kPfBM * kPfAStride];
-    __shared__ __align__(16) uint32_t Bs[2][kPfBN * 8];  // [row][group 0/1][4 dwords]
-    __shared__ uint32_t Ss[2][kPfBN];                    // [row]: scales of groups 0 (low) and 1 (high)
+    __shared__ __align__(16) uint32_t Bs[2][kPfBN * kPfGPS * 4];  // [row][group][4 dwords]
+    __shared__ uint16_t Ss[2][kPfBN * kPfGPS];                    // [row][group]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
     const int n0 = blockIdx.x * kPfBN, m0 = blockIdx.y * kPfBM;
     const int wm = wave & 1, wn = wave >> 1;
     const int M = a.M, N = a.N, K = a.K, G = a.G;
-    const int nstage = (G + 1) / 2;
+    const int nstage = (G + kPfGPS - 1) / kPfGPS;
 
     // global -> registers for stage s; every address is clamped into its
     // tensor and out-of-range values are zeroed after the load
-    uint4 ra[4], rb = make_uint4(0, 0, 0, 0);
-    uint32_t rs = 0;
+    constexpr int CPR = kPfBK / 8;  // 16-byte chunks per row of the X tile
+    uint4 ra[kPfAChunks], rb = make_uint4(0, 0, 0, 0);
+    uint16_t rs = 0;
     auto load = [&](int s) {
         const int kb = s * kPfBK;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ch = tid + kPfThreads * j, row = ch >> 3, k = kb + 8 * (ch & 7);
+        for (int j = 0; j < kPfAChunks; ++j) {
+            const int ch = tid + kPfThreads * j, row = ch / CPR, k = kb + 8 * (ch % CPR);
             const int m = min(m0 + row, M - 1);
             const uint4 v = *reinterpret_cast<const uint4*>(a.x + (size_t)m * a.ldx + min(k, K - 8));
             const bool ok = k < K && m0 + row < M;
             ra[j] = ok ? v : make_uint4(0, 0, 0, 0);
         }
-        if (tid < 2 * kPfBN) {
-            const int n = min(n0 + (tid >> 1), N - 1), g = min(2 * s + (tid & 1), G - 1);
+        if (tid < kPfBN * kPfGPS) {
+            const int n = min(n0 + tid / kPfGPS, N - 1), g = min(kPfGPS * s + tid % kPfGPS, G - 1);
             rb = *reinterpret_cast<const uint4*>(a.W + ((size_t)n * G + g) * 16);
-        }
-        if (tid < kPfBN) {
-            const int n = min(n0 + tid, N - 1);
-            const uint16_t* sr = a.S + (size_t)n * G;
-            rs = (uint32_t)sr[min(2 * s, G - 1)] | ((uint32_t)sr[min(2 * s + 1, G - 1)] << 16);
+            rs = a.S[(size_t)n * G + g];
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ch = tid + kPfThreads * j, row = ch >> 3;
-            *reinterpret_cast<uint4*>(&As[buf][row * kPfAStride + 8 * (ch & 7)]) = pf_perm_x8(ra[j]);
+        for (int j = 0; j < kPfAChunks; ++j) {
+            const int ch = tid + kPfThreads * j, row = ch / CPR;
+            *reinterpret_cast<uint4*>(&As[buf][row * kPfAStride + 8 * (ch % CPR)]) = pf_perm_x8(ra[j]);
         }
-        if (tid < 2 * kPfBN) *reinterpret_cast<uint4*>(&Bs[buf][(tid >> 1) * 8 + (tid & 1) * 4]) = rb;
-        if (tid < kPfBN) Ss[buf][tid] = rs;
+        if (tid < kPfBN * kPfGPS) {
+            *reinterpret_cast<uint4*>(&Bs[buf][tid * 4]) = rb;  // row tid / GPS, group tid % GPS
+            Ss[buf][tid] = rs;
+        }
     };
 
     pf4_t acc[4][2];
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
         const int buf = s & 1;
         if (s + 1 < nstage) load(s + 1);
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
+        for (int g = 0; g < kPfGPS; ++g) {
             ph8_t af[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -117,8 +119,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int row = 32 * wn + 16 * j + c;
-                const ph8_t w = pf_codes_to_h8(Bs[buf][row * 8 + g * 4 + kq]);
-                const float sc = h2f_bits((uint16_t)(Ss[buf][row] >> (16 * g)));
+                const ph8_t w = pf_codes_to_h8(Bs[buf][(row * kPfGPS + g) * 4 + kq]);
+                const float sc = h2f_bits(Ss[buf][row * kPfGPS + g]);
                 const pf4_t z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {

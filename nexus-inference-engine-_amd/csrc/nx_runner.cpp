@@ -601,9 +601,9 @@ struct PrefillScratch {
 
 // The prompt of sequence b (P tokens, at positions hpos[b] + 1 on) through
 // every layer, kPrefillChunk tokens at a time: RMSNorm rows, QKV GEMM, RoPE
-// and page writes, causal attention (the split kernel with one row per
-// query token, row t seeing positions <= its own), output projection and
-// FFN GEMMs with the residual accumulated in place.  Then the final RMSNorm,
+// and page writes, causal attention over the pages (16 queries per
+// wavefront), output projection and FFN GEMMs with the residual accumulated
+// in place.  Then the final RMSNorm,
 // lm_head and argmax of the last token leave its greedy successor pending,
 // as after P decode steps.  Dense models with fp16 pages.
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
@@ -614,32 +614,18 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
     const int C = std::min(P, kPrefillChunk), p0 = m->hpos[(size_t)b] + 1, MB = m->max_blocks;
     const int pend = p0 + P;  // first position after the prompt
     PrefillScratch sc;
-    int32_t *tok = nullptr, *lens = nullptr, *bt = nullptr;
-    float *h = nullptr, *qkv = nullptr, *q = nullptr, *part = nullptr;
+    int32_t* tok = nullptr;
+    float *h = nullptr, *qkv = nullptr, *q = nullptr;
     uint16_t *x16 = nullptr, *att = nullptr, *act = nullptr;
-    unsigned* counts = nullptr;
-    const size_t ws = nx::attn_f16_workspace_bytes(C, hq, hkv, hd, pend);
-    const size_t cw = nx::attn_count_words(C, hkv);
-    if (sc.get(&tok, C) != hipSuccess || sc.get(&lens, C) != hipSuccess || sc.get(&bt, (size_t)C * MB) != hipSuccess ||
-        sc.get(&h, (size_t)C * d) != hipSuccess || sc.get(&qkv, (size_t)C * m->nqkv) != hipSuccess ||
-        sc.get(&q, (size_t)C * m->qdim) != hipSuccess || sc.get(&part, ws / sizeof(float) + 4) != hipSuccess ||
+    if (sc.get(&tok, C) != hipSuccess || sc.get(&h, (size_t)C * d) != hipSuccess ||
+        sc.get(&qkv, (size_t)C * m->nqkv) != hipSuccess || sc.get(&q, (size_t)C * m->qdim) != hipSuccess ||
         sc.get(&x16, (size_t)C * d) != hipSuccess || sc.get(&att, (size_t)C * m->qdim) != hipSuccess ||
-        sc.get(&act, (size_t)C * m->Fp) != hipSuccess || sc.get(&counts, cw) != hipSuccess)
+        sc.get(&act, (size_t)C * m->Fp) != hipSuccess)
         return fail(ctx, NX_ERR_OOM, "prefill: scratch for %d tokens", C);
-    NX_HIP(ctx, hipMemsetAsync(counts, 0, cw * sizeof(unsigned), st));
-    // every query row of a chunk reads the sequence's block table
-    std::vector<int32_t> row((size_t)MB), rep((size_t)C * MB);
-    NX_HIP(ctx, hipMemcpyAsync(row.data(), m->block_table + (size_t)b * MB, (size_t)MB * 4, hipMemcpyDeviceToHost, st));
-    NX_HIP(ctx, hipStreamSynchronize(st));
-    for (int t = 0; t < C; ++t) std::copy(row.begin(), row.end(), rep.begin() + (size_t)t * MB);
-    NX_HIP(ctx, hipMemcpyAsync(bt, rep.data(), rep.size() * 4, hipMemcpyHostToDevice, st));
-    std::vector<int32_t> hl((size_t)C);
     int last = 0;
     for (int done = 0; done < P; done += C) {
         const int n = std::min(C, P - done), pb = p0 + done;
-        for (int t = 0; t < n; ++t) hl[(size_t)t] = pb + t + 1;
         NX_HIP(ctx, hipMemcpyAsync(tok, tokens + done, (size_t)n * 4, hipMemcpyHostToDevice, st));
-        NX_HIP(ctx, hipMemcpyAsync(lens, hl.data(), (size_t)n * 4, hipMemcpyHostToDevice, st));
         NX_LAUNCH(m, nx::pf_embed_launch(tok, n, m->embed, h, d, c.vocab, st));
         for (int L = 0; L < c.n_layers; ++L) {
             Layer& ly = m->layers[(size_t)L];
@@ -662,18 +648,15 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             at.q = q;
             at.kpool = ly.kpool;
             at.vpool = ly.vpool;
-            at.block_table = bt;
-            at.ctx_lens = lens;
+            at.block_table = m->block_table + (size_t)b * MB;
             at.out16 = att;
-            at.batch = n;
+            at.batch = 1;
             at.hq = hq;
             at.hkv = hkv;
             at.hd = hd;
             at.max_blocks = MB;
             at.max_ctx = pend;
-            at.part = part;
-            at.counts = counts;
-            NX_LAUNCH(m, nx::attn_f16_launch(at, st));
+            NX_LAUNCH(m, nx::attn_prefill_launch(at, pb, n, st));
             nx::PfGemmArgs o{};
             o.x = att;
             o.ldx = m->qdim;
@@ -713,7 +696,7 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_ACC, dn, st));
         }
         last = n - 1;
-        NX_HIP(ctx, hipStreamSynchronize(st));  // the host staging of tokens and lengths is refilled next
+        NX_HIP(ctx, hipStreamSynchronize(st));  // the token staging is refilled next
     }
     // the last prompt token: final RMSNorm, lm_head and argmax into best[b]
     NX_HIP(ctx, hipMemsetAsync(m->best + b, 0, sizeof(unsigned long long), st));
