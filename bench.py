@@ -20,6 +20,10 @@ Also reported:
   nxf_verify    XXH32 verification of NXF chunks on the GPU (k_xxh32): 4 GiB
                 (an 8B model's weight bytes) as 64 KiB chunks, HIP-event
                 timed, against the oracle's XXH32 on one host core.
+  prefill       batched prefill of a 2048-token prompt on a fresh model of
+                the same shape (dense models), wall clock around the call;
+                its dominant kernel, the gate/up int4-g32 GEMM of a
+                512-token chunk, against the 2.5 PFLOP/s dense fp16 peak.
 
 Other workloads: --model mixtral-8x7b (top-2 of 8 experts of 14336, vocab
 32000; the roofline kernel is then the routed gate/up expert GEMV), --kv tq
@@ -152,6 +156,48 @@ def nxf_verify_bench(ctx, cpu: bool, nbytes: int = 4 << 30, chunk: int = 64 << 1
     return out
 
 
+PEAK_MFMA_TFLOPS = 2500.0  # dense fp16 matrix-core peak
+
+
+def prefill_bench(ctx, base: dict, P: int = 2048) -> dict:
+    """Batched prefill throughput of a P-token prompt (fresh model, positions
+    from 0) and the TFLOP/s of its gate/up GEMM at the 512-token chunk."""
+    import ctypes as C
+
+    import numpy as np
+
+    import nexus_amd
+    cfg = dict(base, batch=1, kv_kind=0, max_seq=((P + 64) // 16 + 1) * 16)
+    prompt = np.random.default_rng(1).integers(0, base["vocab"], (1, P), dtype=np.int32)
+    m = nexus_amd.Model(ctx, **cfg)
+    m.prefill(prompt[:, :64])  # first launches of every kernel
+    m.close()
+    m = nexus_amd.Model(ctx, **cfg)
+    ctx.sync()
+    t0 = time.perf_counter()
+    m.prefill(prompt)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    m.close()
+    d, F, L = base["d_model"], base["ffn"], base["n_layers"]
+    qkv = (base["n_heads"] + 2 * base["n_kv_heads"]) * base["head_dim"]
+    w_flops = 2.0 * P * L * d * (qkv + base["n_heads"] * base["head_dim"] + 3 * F)
+    att_flops = 4.0 * L * base["n_heads"] * base["head_dim"] * P * (P + 1) / 2
+    M, N, K = 512, 2 * F, d
+    G = (K + 31) // 32
+    bx, bw, bs, by = ctx.alloc(M * K * 2), ctx.alloc(N * G * 16), ctx.alloc(N * G * 2), ctx.alloc(M * N * 4)
+    ms = C.c_double()
+    ctx.check(ctx.L.nx_time_gemm(ctx.h, bx, bw, bs, by, M, N, K, 50, C.byref(ms)), "nx_time_gemm")
+    for b in (bx, bw, bs, by):
+        ctx.free(b)
+    tf = 2.0 * M * N * K / (ms.value * 1e-3) / 1e12
+    return {"tokens": P, "ms": round(dt * 1e3, 2), "tok_s": round(P / dt, 1),
+            "TFLOPs_end_to_end": round((w_flops + att_flops) / dt / 1e12, 1),
+            "roofline": {"kernel": f"k_pf_gemm int4-g32 GEMM, gate/up {N}x{K}, {M}-token chunk", "bound": "mfma",
+                         "achieved": round(tf, 1), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_MFMA_TFLOPS, 4), "avg_us": round(ms.value * 1e3, 2)}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +210,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-kernel", choices=["ffn", "attention", "xxh32"],
                     help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the batched prefill measurement (for rocprofv3)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy a 256 MiB buffer 16 times (counter calibration kernel)")
     args = ap.parse_args()
@@ -184,6 +232,11 @@ def main() -> int:
 
     import nexus_amd
 
+    if args.prefill_only:
+        ctx = nexus_amd.Context(0)
+        print(json.dumps({"prefill": prefill_bench(ctx, MODELS[args.model])}))
+        ctx.close()
+        return 0
     if args.profile_kernel == "xxh32":
         ctx = nexus_amd.Context(0)
         r = nxf_verify_bench(ctx, False, iters=16)
@@ -230,6 +283,7 @@ def main() -> int:
     model.close()
     micro = gemv_microbench(ctx, args.batch) if not moe else None
     nxf = nxf_verify_bench(ctx, not args.no_cpu)
+    pre = prefill_bench(ctx, base) if not moe else None
     ctx.close()
     kv_name = "fp16" if kv_kind == 0 else "TurboQuant 3.5-bit"
     if moe:
@@ -277,6 +331,8 @@ def main() -> int:
     if micro is not None:
         line["gemv_microbench"] = micro
     line["nxf_verify"] = nxf
+    if pre is not None:
+        line["prefill"] = pre
     if not args.no_cpu:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind)

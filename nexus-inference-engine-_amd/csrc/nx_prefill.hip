@@ -12,12 +12,16 @@
 // in LDS in the k order (0 2 4 6 1 3 5 7) of each 8-k chunk -- the order in
 // which a code dword turns into fp16 with two byte permutes -- and the codes
 // and scales of its 64 rows; the next stage's loads are in flight while the
-// current one is multiplied.  A wavefront turns each B fragment into fp16
-// q - 8 once (exact) and uses it for its four token tiles; each group's
-// product goes to a zeroed accumulator and is added scaled by the group's
-// scale in fp32 (a lane's output column is one weight row, so one scale per
-// lane), the numerics of the decode GEMV.  Epilogues: fp32 store, fp32
-// accumulate (residual), SwiGLU of interleaved gate/up rows to fp16.
+// current one is multiplied.
+// Exact scaling without per-group fp32 work: the group's fp16 scale s is
+// split into s_hi (its 7 leading significant bits) and s_lo = s - s_hi (the
+// 4 trailing bits), so (q - 8) s_hi and (q - 8) s_lo 2^10 are both exact in
+// fp16 (4-bit x 7-bit and 4-bit x 4-bit products).  They go to two
+// accumulators, combined once at the end as hi + lo 2^-10: the products are
+// exactly (q - 8) s x, summed in fp32 -- the numerics of the decode GEMV at
+// two matrix-core products per group and no vector work per output.
+// Epilogues: fp32 store, fp32 accumulate (residual), SwiGLU of interleaved
+// gate/up rows to fp16.
 #include "nx_common.h"
 #include "nx_kernels.h"
 
@@ -28,6 +32,7 @@ typedef _Float16 ph8_t __attribute__((ext_vector_type(8)));
 typedef float pf4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kPfBM = 128, kPfBN = 64, kPfBK = 128, kPfThreads = 256;
+constexpr int kPfXcds = 8;  // blocks are dealt to the XCDs round-robin by block index
 constexpr int kPfGPS = kPfBK / 32;          // groups per stage
 constexpr int kPfAStride = kPfBK + 8;       // fp16 per LDS row of X: rows 4 banks apart, 16 rows read conflict-free
 constexpr int kPfAChunks = kPfBM * kPfBK / 8 / kPfThreads;  // 16-byte chunks of X per thread per stage
@@ -59,7 +64,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
     __shared__ uint16_t Ss[2][kPfBN * kPfGPS];                    // [row][group]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
-    const int n0 = blockIdx.x * kPfBN, m0 = blockIdx.y * kPfBM;
+    // XCD-aware tile order: the blocks of XCD x (block index % 8 == x) take
+    // the column tiles [x nt / 8, (x + 1) nt / 8), all of one row tile before
+    // the next, so an X row tile is fetched into that XCD's L2 once and
+    // shared by the XCD's concurrent blocks
+    const int ntn = (a.N + kPfBN - 1) / kPfBN, ntm = (a.M + kPfBM - 1) / kPfBM;
+    const int xcd = (int)(blockIdx.x % kPfXcds), local = (int)(blockIdx.x / kPfXcds);
+    const int nb0 = xcd * ntn / kPfXcds, nn = (xcd + 1) * ntn / kPfXcds - nb0;
+    if (nn <= 0 || local >= nn * ntm) return;  // the block count is rounded up to 8 x the largest share
+    const int n0 = (nb0 + local % nn) * kPfBN, m0 = (local / nn) * kPfBM;
     const int wm = wave & 1, wn = wave >> 1;
     const int M = a.M, N = a.N, K = a.K, G = a.G;
     const int nstage = (G + kPfGPS - 1) / kPfGPS;
@@ -97,11 +110,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
         }
     };
 
-    pf4_t acc[4][2];
+    pf4_t acc[4][2], acl[4][2];  // (q - 8) s_hi x and (q - 8) s_lo 2^10 x
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = pf4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 2; ++j) acc[i][j] = acl[i][j] = pf4_t{0.f, 0.f, 0.f, 0.f};
 
     load(0);
     store(0);
@@ -120,13 +133,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
             for (int j = 0; j < 2; ++j) {
                 const int row = 32 * wn + 16 * j + c;
                 const ph8_t w = pf_codes_to_h8(Bs[buf][(row * kPfGPS + g) * 4 + kq]);
-                const float sc = h2f_bits(Ss[buf][row * kPfGPS + g]);
-                const pf4_t z = {0.f, 0.f, 0.f, 0.f};
+                const uint16_t sb = Ss[buf][row * kPfGPS + g];
+                const _Float16 shi = __builtin_bit_cast(_Float16, (uint16_t)(sb & 0xFFF0u));
+                const _Float16 slo = (__builtin_bit_cast(_Float16, sb) - shi) * (_Float16)1024.0f;
+                const ph8_t wh = w * shi, wl = w * slo;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const pf4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], w, z, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(p[r], sc, acc[i][j][r]);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], wh, acc[i][j], 0, 0, 0);
+                    acl[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], wl, acl[i][j], 0, 0, 0);
                 }
             }
         }
@@ -144,7 +158,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 64 * wm + 16 * i + 4 * kq + r;
-                const float v = acc[i][j][r];
+                const float v = fmaf(acl[i][j][r], 0.0009765625f, acc[i][j][r]);
                 if (EPI == PF_SWIGLU) {
                     const float u = lane_xor1(v);  // the up row n + 1 sits in lane c + 1
                     if ((c & 1) == 0 && m < M && n + 1 < N)
@@ -209,8 +223,11 @@ hipError_t pf_gemm_launch(int epi, const PfGemmArgs& a, hipStream_t st) {
     if (a.M < 1 || a.N < 1 || a.K < 8 || a.K % 8 || a.ldx % 8 || (reinterpret_cast<uintptr_t>(a.x) & 15) ||
         a.G != (a.K + 31) / 32 || (epi == PF_SWIGLU && a.N % 2))
         return hipErrorInvalidValue;
-    const dim3 grid((a.N + kPfBN - 1) / kPfBN, (a.M + kPfBM - 1) / kPfBM);
-    if (grid.y > 65535) return hipErrorInvalidValue;
+    const long ntn = (a.N + kPfBN - 1) / kPfBN, ntm = (a.M + kPfBM - 1) / kPfBM;
+    const long share = (ntn + kPfXcds - 1) / kPfXcds;  // largest column-tile share of an XCD
+    const long blocks = (long)kPfXcds * share * ntm;
+    if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks);
     switch (epi) {
         case PF_F32: hipLaunchKernelGGL(k_pf_gemm<PF_F32>, grid, dim3(kPfThreads), 0, st, a); break;
         case PF_ACC: hipLaunchKernelGGL(k_pf_gemm<PF_ACC>, grid, dim3(kPfThreads), 0, st, a); break;
