@@ -207,6 +207,16 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, n
 /* Greedy sampling: first maximum of logits fp32 [batch][V]
  * (hybrid_model.cpp:2027-2038). */
 nx_status nx_argmax(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int batch);
+/* HybridModel::Impl::sample_token (hybrid_model.cpp:2023-2099) on the device
+ * for each of `batch` rows of logits: temperature <= 0 is the greedy argmax;
+ * otherwise softmax of logits / T, top-k (0 = off, else at most 1024),
+ * top-p (< 1 needs top-k), renormalize, and the first index whose running
+ * sum reaches u * sum.  u comes from a fresh MT19937 seeded with `seed` at
+ * every call, as in the reference (std::uniform_real_distribution<float>
+ * as libstdc++ computes it); seed 0 draws from std::random_device.  Ties in
+ * the top-k and top-p orders keep the lower index. */
+nx_status nx_sample(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int batch, float temperature, int top_k,
+                    float top_p, uint64_t seed);
 
 /* ----------------------------------------------------------- the runner -- */
 /* A resident decoder driven by this library: the counterpart of
@@ -242,6 +252,13 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
  * HybridModel::prefill loop, hybrid_model.cpp:604-644).  MoE and
  * TurboQuant-page models always prefill one token per step. */
 nx_status nx_model_set_prefill(nx_model* m, int batched);
+/* Sampling of the decode loop (SamplingParams, core/config.h:60-66):
+ * temperature <= 0 = greedy (the default); otherwise every step samples
+ * with nx_sample's rules inside the step graph.  seed != 0: the draw of
+ * std::mt19937(seed), the same at every step as in the reference; seed 0:
+ * a counter-based draw keyed by (sequence, position) (the reference uses
+ * std::random_device). */
+nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float top_p, uint64_t seed);
 /* Fill positions [0, ctx) of every layer's cache with synthetic N(0,1) K/V
  * (n_outlier channels per head scaled x10); the pending token of every
  * sequence becomes a seeded start token. */

@@ -6,6 +6,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <random>
 
 #include "nx_common.h"
 #include "nx_internal.h"
@@ -59,6 +60,32 @@ nx_status launched(nx_ctx* ctx, hipError_t e, const char* what) {
     return NX_OK;
 }
 }  // namespace
+
+// ------------------------------------------------------------------ draw --
+namespace nx {
+// First output of MT19937 seeded with `seed` (the generator and seeding of
+// std::mt19937), as libstdc++'s uniform_real_distribution<float>(0, 1)
+// turns it into a float: x / 2^32 in float, 1 replaced by the largest float
+// below 1.  The reference draws from a fresh std::mt19937(seed) at every
+// sample_token call (hybrid_model.cpp:2089-2091); seed 0 means
+// std::random_device there and here.
+float sample_draw(uint64_t seed) {
+    uint32_t s32 = (uint32_t)seed;
+    if (seed == 0) s32 = std::random_device{}();
+    uint32_t mt[624];
+    mt[0] = s32;
+    for (uint32_t i = 1; i < 624; ++i) mt[i] = 1812433253u * (mt[i - 1] ^ (mt[i - 1] >> 30)) + i;
+    // the first output only needs the first twist step
+    const uint32_t y0 = (mt[0] & 0x80000000u) | (mt[1] & 0x7FFFFFFFu);
+    uint32_t y = mt[397] ^ (y0 >> 1) ^ ((y0 & 1u) ? 0x9908B0DFu : 0u);
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9D2C5680u;
+    y ^= (y << 15) & 0xEFC60000u;
+    y ^= y >> 18;
+    const float r = (float)y / 4294967296.0f;
+    return r >= 1.0f ? std::nextafter(1.0f, 0.0f) : r;
+}
+}  // namespace nx
 
 // ---------------------------------------------------------------- codebook --
 namespace nx {
@@ -778,6 +805,29 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
     if (e == hipSuccess) e = nx::moe_down_launch(a, ctx->stream);
     if (e == hipSuccess) e = nx::moe_combine_launch(a, ctx->stream);
     return launched(ctx, e, "moe_expert_ffn");
+}
+
+nx_status nx_sample(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch, float temperature, int top_k,
+                    float top_p, uint64_t seed) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (temperature <= 0.0f) return nx_argmax(ctx, logits, out, V, batch);
+    if (V <= 0 || batch < 1) return fail(ctx, NX_ERR_INVALID, "nx_sample: bad shape");
+    if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f) return fail(ctx, NX_ERR_INVALID, "nx_sample: bad parameters");
+    if (top_k > 1024 && top_k < V) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_sample: top_k above 1024");
+    if ((top_k == 0 || top_k >= V) && top_p < 1.0f)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "nx_sample: top_p < 1 needs top_k in (0, 1024]");
+    NX_NEED(ctx, logits, (size_t)batch * V * 4, "logits");
+    NX_NEED(ctx, out, (size_t)batch * 4, "out");
+    nx::SampleArgs a{};
+    a.logits = dptr<const float>(logits);
+    a.V = V;
+    a.ldl = V;
+    a.temperature = temperature;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.u_fixed = nx::sample_draw(seed);
+    a.out = dptr<int32_t>(out);
+    return launched(ctx, nx::sample_launch(a, batch, ctx->stream), "sample");
 }
 
 nx_status nx_argmax(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch) {

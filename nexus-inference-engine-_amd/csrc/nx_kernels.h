@@ -251,6 +251,28 @@ hipError_t pf_rope_kv_launch(const float* qkv, int ld, int P, int p0, int qdim, 
                              const float* cos_t, const float* sin_t, const int32_t* bt, uint16_t* kpool,
                              uint16_t* vpool, float* q32, hipStream_t st);
 
+// Sampling (nx_sample.hip): sample_token of hybrid_model.cpp:2023-2099 per
+// sequence; the draw is u_fixed when >= 0, else u[b], else a counter-based
+// draw keyed by (key, sequence, pos[b]).  Writes out[b] and/or
+// best[b] (the pending-token encoding read by the embedding kernel).
+struct SampleArgs {
+    const float* logits;  // [batch][ldl]
+    int V, ldl;
+    float temperature;    // > 0 (greedy is the argmax kernel)
+    int top_k;            // 0 or >= V: off; otherwise at most 1024
+    float top_p;          // (0, 1]; < 1 needs top-k
+    float u_fixed;
+    const float* u;       // [batch], or nullptr: draws keyed by (key, b, pos[b])
+    uint64_t key;
+    const int32_t* pos;
+    int32_t* out;
+    unsigned long long* best;
+};
+hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st);
+// The reference's draw for a seed: std::uniform_real_distribution<float>(0, 1)
+// of the first output of std::mt19937(seed) (seed 0: std::random_device).
+float sample_draw(uint64_t seed);
+
 // XXH32 (seed 0) of byte ranges of one device buffer: range i is
 // [off, off + len) (off a multiple of 16); its hash goes to out[slot].
 struct HashRange {

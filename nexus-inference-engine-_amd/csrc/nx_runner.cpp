@@ -87,6 +87,9 @@ struct nx_model {
     hipGraphExec_t exec_multi = nullptr;  // kStepsPerGraph decode steps
     std::vector<int> hpos;       // host mirror of pos (last processed position)
     int prefill_batched = 1;     // batched (GEMM) prefill where the model allows it
+    // sampling (temperature <= 0: greedy argmax of the lm_head epilogue)
+    float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
+    int top_k = 0;
 };
 
 namespace {
@@ -168,6 +171,24 @@ nx_status generate_weights(nx_model* m) {
             }
         }
     }
+    return NX_OK;
+}
+
+// Sampling of sequences [b0, b0 + nb) from the lm_head logits: the sampled
+// token replaces the argmax as the pending token.
+nx_status enqueue_sample(nx_model* m, int b0, int nb) {
+    nx::SampleArgs s{};
+    s.logits = m->logits + (size_t)b0 * m->c.vocab;
+    s.V = m->c.vocab;
+    s.ldl = m->c.vocab;
+    s.temperature = m->temperature;
+    s.top_k = m->top_k;
+    s.top_p = m->top_p;
+    s.u_fixed = m->u_fixed;
+    s.key = m->c.seed ^ 0x5A4D504C45ull;  // draws of seed 0, keyed by (sequence, position)
+    s.pos = m->pos + b0;
+    s.best = m->best + b0;
+    NX_LAUNCH(m, nx::sample_launch(s, nb, m->ctx->stream));
     return NX_OK;
 }
 
@@ -357,6 +378,7 @@ nx_status enqueue_step(nx_model* m) {
     lm.ldy = c.vocab;
     lm.best = m->best;
     NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_LOGITS, lm, st));
+    if (m->temperature > 0.0f) NX_TRY(enqueue_sample(m, 0, B));
     return NX_OK;
 }
 
@@ -716,6 +738,10 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
     lm.best = m->best + b;
     NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_LOGITS, lm, st));
     const int32_t plast = pend - 1;
+    if (m->temperature > 0.0f) {
+        NX_HIP(ctx, hipMemcpyAsync(m->pos + b, &plast, 4, hipMemcpyHostToDevice, st));  // the draw's key
+        NX_TRY(enqueue_sample(m, b, 1));
+    }
     NX_HIP(ctx, hipMemcpyAsync(m->pos + b, &plast, 4, hipMemcpyHostToDevice, st));
     NX_HIP(ctx, hipStreamSynchronize(st));
     m->hpos[(size_t)b] = plast;
@@ -725,6 +751,27 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
 }  // namespace
 
 extern "C" {
+
+nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float top_p, uint64_t seed) {
+    if (!m) return NX_ERR_INVALID;
+    const int V = m->c.vocab;
+    if (temperature > 0.0f) {
+        if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f) return fail(m->ctx, NX_ERR_INVALID, "sampling: bad parameters");
+        if (top_k > 1024 && top_k < V) return fail(m->ctx, NX_ERR_UNSUPPORTED, "sampling: top_k above 1024");
+        if ((top_k == 0 || top_k >= V) && top_p < 1.0f)
+            return fail(m->ctx, NX_ERR_UNSUPPORTED, "sampling: top_p < 1 needs top_k in (0, 1024]");
+    }
+    m->temperature = temperature > 0.0f ? temperature : 0.0f;
+    m->top_k = top_k;
+    m->top_p = top_p;
+    m->u_fixed = seed ? nx::sample_draw(seed) : -1.0f;
+    // the step graphs hold the sampling launch (or not): capture them again
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->exec_multi) (void)hipGraphExecDestroy(m->exec_multi);
+    m->exec = nullptr;
+    m->exec_multi = nullptr;
+    return NX_OK;
+}
 
 nx_status nx_model_set_prefill(nx_model* m, int batched) {
     if (!m || (batched != 0 && batched != 1)) return NX_ERR_INVALID;

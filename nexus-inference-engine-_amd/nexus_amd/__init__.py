@@ -114,6 +114,8 @@ _SIGS = {
     "nx_moe_route_topk": (_I, [_P, _B, _B, _B, _I, _I, _I]),
     "nx_moe_expert_ffn": (_I, [_P, _B, _B, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I, _I]),
     "nx_argmax": (_I, [_P, _B, _B, _I, _I]),
+    "nx_sample": (_I, [_P, _B, _B, _I, _I, _F, _I, _F, C.c_uint64]),
+    "nx_model_set_sampling": (_I, [_P, _F, _I, _F, C.c_uint64]),
     "nx_model_create": (_I, [_P, C.POINTER(ModelConfig), C.POINTER(_P)]),
     "nx_model_destroy": (_I, [_P]),
     "nx_model_prefill": (_I, [_P, _P, _I, _P]),
@@ -258,6 +260,9 @@ class Context:
     def gemv(self, x, wq, sc, y, N, K, batch=1):
         self.check(self.L.nx_gemv_int4_g32(self.h, x, wq, sc, y, N, K, batch), "nx_gemv_int4_g32")
 
+    def sample(self, logits, out, V, batch=1, temperature=0.7, top_k=40, top_p=0.9, seed=0):
+        self.check(self.L.nx_sample(self.h, logits, out, V, batch, temperature, top_k, top_p, seed), "nx_sample")
+
     def gemm(self, x, wq, sc, y, M, N, K, accumulate=False):
         self.check(self.L.nx_gemm_int4_g32(self.h, x, wq, sc, y, M, N, K, int(accumulate)), "nx_gemm_int4_g32")
 
@@ -317,6 +322,11 @@ class Model:
         self.ctx.check(self.ctx.L.nx_model_prefill(self.h, p.ctypes.data, p.shape[1], nxt.ctypes.data),
                        "nx_model_prefill")
         return nxt
+
+    def set_sampling(self, temperature=0.7, top_k=40, top_p=0.9, seed=0):
+        """SamplingParams of the decode loop; temperature <= 0 is greedy."""
+        self.ctx.check(self.ctx.L.nx_model_set_sampling(self.h, temperature, top_k, top_p, seed),
+                       "nx_model_set_sampling")
 
     def set_prefill(self, batched: bool):
         """Batched GEMM prefill (default) or one decode step per prompt token."""

@@ -66,6 +66,9 @@ def _load() -> C.CDLL:
         "nxo_gemv_int4_g32": (None, [_u8p, _u16p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]),
         "nxo_rmsnorm": (None, [_f32p, C.c_void_p, C.c_int, C.c_float, _f32p]),
         "nxo_xxh32": (C.c_uint32, [C.c_void_p, C.c_size_t, C.c_uint32]),
+        "nxo_mt19937": (None, [C.c_uint32, C.c_int, np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")]),
+        "nxo_canonical_f32": (C.c_float, [C.c_uint32]),
+        "nxo_sample": (C.c_int, [_f32p, C.c_int, C.c_float, C.c_int, C.c_float, C.c_float]),
         "nxo_rope_table": (None, [C.c_int, C.c_int, C.c_double, _f32p, _f32p]),
         "nxo_rope": (None, [_f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]),
         "nxo_swiglu": (None, [_f32p, _f32p, C.c_int, _f32p]),

@@ -1018,3 +1018,97 @@ uint32_t nxo_xxh32(const void* data, size_t len, uint32_t seed) {
     h ^= h >> 16;
     return h;
 }
+
+/* ------------------------------------------------------------ sampling ---- */
+void nxo_mt19937(uint32_t seed, int n, uint32_t* out) {
+    uint32_t mt[624];
+    mt[0] = seed;
+    for (int i = 1; i < 624; ++i) mt[i] = 1812433253u * (mt[i - 1] ^ (mt[i - 1] >> 30)) + (uint32_t)i;
+    int idx = 624;
+    for (int o = 0; o < n; ++o) {
+        if (idx >= 624) {
+            for (int i = 0; i < 624; ++i) {
+                const uint32_t y = (mt[i] & 0x80000000u) | (mt[(i + 1) % 624] & 0x7FFFFFFFu);
+                mt[i] = mt[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908B0DFu : 0u);
+            }
+            idx = 0;
+        }
+        uint32_t y = mt[idx++];
+        y ^= y >> 11;
+        y ^= (y << 7) & 0x9D2C5680u;
+        y ^= (y << 15) & 0xEFC60000u;
+        y ^= y >> 18;
+        out[o] = y;
+    }
+}
+
+float nxo_canonical_f32(uint32_t x) {
+    const float r = (float)x / 4294967296.0f;
+    return r >= 1.0f ? nextafterf(1.0f, 0.0f) : r;
+}
+
+/* descending by value, ties by ascending index */
+static const float* g_sort_vals;
+static int cmp_desc_idx(const void* a, const void* b) {
+    const int i = *(const int*)a, j = *(const int*)b;
+    const float x = g_sort_vals[i], y = g_sort_vals[j];
+    if (x > y) return -1;
+    if (x < y) return 1;
+    return i < j ? -1 : (i > j);
+}
+
+int nxo_sample(const float* logits, int V, float temperature, int top_k, float top_p, float u) {
+    if (temperature <= 0.0f) {
+        int best = 0;
+        for (int i = 1; i < V; ++i)
+            if (logits[i] > logits[best]) best = i;
+        return best;
+    }
+    float* probs = (float*)malloc(sizeof(float) * (size_t)V);
+    int* idx = (int*)malloc(sizeof(int) * (size_t)V);
+    float mx = logits[0];
+    for (int i = 1; i < V; ++i) mx = logits[i] > mx ? logits[i] : mx;
+    float sum = 0.0f;
+    for (int i = 0; i < V; ++i) {
+        probs[i] = expf((logits[i] - mx) / temperature);
+        sum += probs[i];
+    }
+    for (int i = 0; i < V; ++i) probs[i] /= sum;
+    g_sort_vals = probs;
+    if (top_k > 0 && top_k < V) {
+        for (int i = 0; i < V; ++i) idx[i] = i;
+        qsort(idx, (size_t)V, sizeof(int), cmp_desc_idx);
+        for (int i = top_k; i < V; ++i) probs[idx[i]] = 0.0f;
+    }
+    if (top_p < 1.0f) {
+        for (int i = 0; i < V; ++i) idx[i] = i;
+        qsort(idx, (size_t)V, sizeof(int), cmp_desc_idx);
+        float cum = 0.0f;
+        for (int i = 0; i < V; ++i) {
+            cum += probs[idx[i]];
+            if (cum > top_p) {
+                for (int j = i + 1; j < V; ++j) probs[idx[j]] = 0.0f;
+                break;
+            }
+        }
+    }
+    sum = 0.0f;
+    for (int i = 0; i < V; ++i) sum += probs[i];
+    int tok = V - 1;
+    if (sum <= 0.0f) {
+        tok = 0;
+    } else {
+        const float r = u * sum;
+        float cum = 0.0f;
+        for (int i = 0; i < V; ++i) {
+            cum += probs[i];
+            if (cum >= r) {
+                tok = i;
+                break;
+            }
+        }
+    }
+    free(probs);
+    free(idx);
+    return tok;
+}

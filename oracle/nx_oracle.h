@@ -209,6 +209,26 @@ void nxo_model_forward_timed(nxo_model* m, const int32_t* tokens, float* logits,
 int nxo_num_threads(void);
 void nxo_set_num_threads(int n);
 
+/* ------------------------------------------------------------ sampling -- */
+/* MT19937 (Matsumoto & Nishimura, the generator of std::mt19937): the first
+ * n 32-bit outputs after seeding with `seed` (the standard's seeding rule). */
+void nxo_mt19937(uint32_t seed, int n, uint32_t* out);
+/* std::uniform_real_distribution<float>(0, 1) applied to one 32-bit
+ * generator output x, as libstdc++ computes it (generate_canonical<float,24>
+ * with k = 1): float(x) / 2^32, values reaching 1 replaced by the largest
+ * float below 1. */
+float nxo_canonical_f32(uint32_t x);
+/* HybridModel::Impl::sample_token (model/hybrid_model.cpp:2023-2099) with the
+ * draw given as u in [0, 1) (the reference draws u from a fresh
+ * std::mt19937(seed) at every call): temperature <= 0 -> first maximum;
+ * else fp32 softmax of logits / T (sequential sums), top-k (top_k in
+ * (0, V)), top-p (top_p < 1: kept in descending order until the running
+ * sum exceeds top_p, that element included), renormalize, r = u * sum, and
+ * the first index whose running sum (index order) reaches r (V - 1 if
+ * none).  Ties in the sorts keep the lower index first (the reference's
+ * partial_sort / sort order for ties is unspecified). */
+int nxo_sample(const float* logits, int V, float temperature, int top_k, float top_p, float u);
+
 /* ------------------------------------------------------------ NXF -- */
 /* XXH32 of a byte range (the published xxHash 32-bit algorithm): the chunk
  * checksum of NXF files, format/nxf_writer.cpp:33-72 (stored by
