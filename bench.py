@@ -244,7 +244,8 @@ def main() -> int:
         ctx.close()
         return 0
     kv_kind = 1 if args.kv == "tq" else 0
-    max_seq = ((args.ctx + args.warmup + args.steps + 16) // 16 + 1) * 16
+    smp_steps = max(8, args.steps // 2)  # sampled decode steps after the greedy ones
+    max_seq = ((args.ctx + args.warmup + args.steps + smp_steps + 24) // 16 + 1) * 16
     base = MODELS[args.model]
     moe = base["n_experts"] > 0
     cfg = dict(base, batch=args.batch, kv_kind=kv_kind, max_seq=max_seq)
@@ -276,6 +277,29 @@ def main() -> int:
     print(f"[bench] {args.steps} steps in {elapsed * 1e3:.2f} ms; {step_bytes / 1e9:.3f} GB/step",
           file=sys.stderr, flush=True)
 
+    # the same decode with sampling in the step graph (SamplingParams defaults
+    # of core/config.h:60-66 with a fixed seed)
+    model.set_sampling(0.7, 40, 0.9, 42)
+    model.decode_untimed(2)
+    ctx.sync()
+    t0 = time.perf_counter()
+    model.decode_untimed(smp_steps)
+    ctx.sync()
+    smp_s = time.perf_counter() - t0
+    model.set_sampling(0.0, 0, 1.0, 0)
+    sampling = {"params": {"temperature": 0.7, "top_k": 40, "top_p": 0.9, "seed": 42}, "steps": smp_steps,
+                "tok_s": round(smp_steps * args.batch / smp_s, 2),
+                "ms_per_step": round(smp_s * 1e3 / smp_steps, 4),
+                "greedy_ms_per_step": round(elapsed * 1e3 / args.steps, 4)}
+    if not args.no_cpu:
+        import numpy as np
+
+        import oracle
+        lg = np.random.default_rng(2).standard_normal(base["vocab"]).astype(np.float32) * 3
+        t0 = time.perf_counter()
+        for _ in range(10):
+            oracle.lib.nxo_sample(lg, base["vocab"], 0.7, 40, 0.9, 0.5)
+        sampling["cpu_ms_per_sample"] = round((time.perf_counter() - t0) * 100, 3)
     ffn_ms, ffn_bytes = model.time_ffn_gemv(200)
     att_ms, att_bytes = model.time_attention(200)
     ffn_gbs = ffn_bytes / (ffn_ms * 1e-3) / 1e9
@@ -331,6 +355,7 @@ def main() -> int:
     if micro is not None:
         line["gemv_microbench"] = micro
     line["nxf_verify"] = nxf
+    line["sampling"] = sampling
     if pre is not None:
         line["prefill"] = pre
     if not args.no_cpu:

@@ -183,6 +183,7 @@ nx_status nx_destroy(nx_ctx* ctx) {
     for (auto& kv : ctx->bufs) (void)hipFree(reinterpret_cast<void*>(kv.first));
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
     if (ctx->attn_counts) (void)hipFree(ctx->attn_counts);
+    if (ctx->smp_ws) (void)hipFree(ctx->smp_ws);
     (void)hipEventDestroy(ctx->ev0);
     (void)hipEventDestroy(ctx->ev1);
     (void)hipStreamDestroy(ctx->stream);
@@ -818,7 +819,18 @@ nx_status nx_sample(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch, fl
         return fail(ctx, NX_ERR_UNSUPPORTED, "nx_sample: top_p < 1 needs top_k in (0, 1024]");
     NX_NEED(ctx, logits, (size_t)batch * V * 4, "logits");
     NX_NEED(ctx, out, (size_t)batch * 4, "out");
+    const size_t need = (size_t)batch * V;
+    if (need > ctx->smp_ws_floats) {
+        if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_sample: scratch must grow outside capture");
+        NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->smp_ws) (void)hipFree(ctx->smp_ws);
+        ctx->smp_ws = nullptr;
+        ctx->smp_ws_floats = 0;
+        NX_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->smp_ws), need * sizeof(float)));
+        ctx->smp_ws_floats = need;
+    }
     nx::SampleArgs a{};
+    a.scratch = ctx->smp_ws;
     a.logits = dptr<const float>(logits);
     a.V = V;
     a.ldl = V;

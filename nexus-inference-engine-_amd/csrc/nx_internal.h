@@ -25,6 +25,9 @@ struct nx_ctx {
     unsigned* attn_counts = nullptr;  // split-completion counters (zero between launches)
     size_t attn_count_words = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // scratch rows of nx_sample (grow-only)
+    float* smp_ws = nullptr;
+    size_t smp_ws_floats = 0;
     float c4[16], b4[15], c3[8], b3[7];
 };
 

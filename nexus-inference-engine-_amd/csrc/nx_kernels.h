@@ -267,6 +267,7 @@ struct SampleArgs {
     const int32_t* pos;
     int32_t* out;
     unsigned long long* best;
+    float* scratch;       // [batch][V] floats
 };
 hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st);
 // The reference's draw for a seed: std::uniform_real_distribution<float>(0, 1)

@@ -90,6 +90,7 @@ struct nx_model {
     // sampling (temperature <= 0: greedy argmax of the lm_head epilogue)
     float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
     int top_k = 0;
+    float* smp_scratch = nullptr;  // [batch][vocab], allocated when sampling is first set
 };
 
 namespace {
@@ -188,6 +189,7 @@ nx_status enqueue_sample(nx_model* m, int b0, int nb) {
     s.key = m->c.seed ^ 0x5A4D504C45ull;  // draws of seed 0, keyed by (sequence, position)
     s.pos = m->pos + b0;
     s.best = m->best + b0;
+    s.scratch = m->smp_scratch + (size_t)b0 * m->c.vocab;
     NX_LAUNCH(m, nx::sample_launch(s, nb, m->ctx->stream));
     return NX_OK;
 }
@@ -761,6 +763,7 @@ nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float
         if ((top_k == 0 || top_k >= V) && top_p < 1.0f)
             return fail(m->ctx, NX_ERR_UNSUPPORTED, "sampling: top_p < 1 needs top_k in (0, 1024]");
     }
+    if (temperature > 0.0f && !m->smp_scratch) NX_TRY(dalloc(m, &m->smp_scratch, (size_t)m->c.batch * V));
     m->temperature = temperature > 0.0f ? temperature : 0.0f;
     m->top_k = top_k;
     m->top_p = top_p;

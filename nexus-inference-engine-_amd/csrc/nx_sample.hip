@@ -3,21 +3,24 @@
 // top-k, top-p, renormalize, one uniform draw, the first vocabulary index
 // whose running sum reaches it -- so the logits never leave HBM.
 //
-// One block of 1024 threads per sequence; thread t owns the contiguous
-// vocabulary slice [t S, (t + 1) S), so block-wide prefix sums follow the
-// vocabulary order.  e_i = expf((l_i - max) / T) is recomputed from the
-// logits in every pass (no scratch).
+// One block of 1024 threads per sequence.  Wavefront w owns the contiguous
+// vocabulary chunk [w C, (w + 1) C) and walks it 64 consecutive entries at a
+// time (coalesced), so wavefront order then iteration order then lane order
+// is vocabulary order; ballots keep that order where it matters.
+// e_i = expf((l_i - max) / T) is computed once into a scratch row; later
+// passes read p_i = e_i / sum.
 //  - top-k (0 < k <= 1024, k < V): four 8-bit radix passes over the bits of
-//    e_i (positive floats order as their bits) find the k-th largest value;
+//    p_i (positive floats order as their bits) find the k-th largest value;
 //    ties at that value keep the lowest indices (the reference's
 //    partial_sort leaves their order unspecified).  The k survivors go to
 //    LDS in index order; top-p sorts them (bitonic, ties by index) and one
 //    lane takes the running sum in that order; the renormalization and the
 //    draw's scan run over the survivors in index order in one lane, the
 //    reference's own summation order.
-//  - no top-k (k == 0 or k >= V) with top_p = 1: the draw's scan is a
-//    block-wide prefix sum over the vocabulary (fp32 partial sums in a fixed
-//    order).  No top-k with top_p < 1 is refused by the launcher.
+//  - no top-k (k == 0 or k >= V) with top_p = 1: the draw's scan runs over
+//    the vocabulary in wavefront, iteration and lane order with fp32
+//    partial sums in a fixed order.  No top-k with top_p < 1 is refused by
+//    the launcher.
 // The softmax denominator is a fixed-order block sum; the reference's is a
 // sequential fp32 sum, so probabilities agree to rounding.
 #include "nx_common.h"
@@ -28,29 +31,38 @@ namespace {
 
 constexpr int kSmpThreads = 1024;
 constexpr int kSmpMaxK = 1024;
+constexpr int kSmpCand = 4096;  // top-k candidates held in LDS
+constexpr int kSmpThr = 8;      // candidate thresholds e >= exp(-D)
+__constant__ float c_smp_D[kSmpThr] = {24.0f, 16.0f, 12.0f, 8.0f, 5.0f, 3.0f, 2.0f, 1.0f};
 
-__device__ inline float smp_block_max(float v, float* red) {
+constexpr int kSmpWaves = kSmpThreads / 64;
+
+__device__ inline float smp_wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    if (l == 0) red[w] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float m = red[0];
-        for (int i = 1; i < kSmpThreads / 64; ++i) m = fmaxf(m, red[i]);
-        red[16] = m;
+    return v;
+}
+template <class T>
+__device__ inline T smp_wave_sum(T v) {
+    for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+    return v;
+}
+// inclusive prefix over the 64 lanes (Hillis-Steele, fixed order)
+__device__ inline float smp_wave_scan(float x) {
+    const int l = threadIdx.x & 63;
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(x, o, 64);
+        if (l >= o) x = x + y;
     }
-    __syncthreads();
-    const float r = red[16];
-    __syncthreads();
-    return r;
+    return x;
+}
+__device__ inline int popc_below(unsigned long long m, int l) {
+    return __popcll(m & ((1ull << l) - 1ull));
 }
 
-// Prefix sums of one value per thread, in thread order, with a fixed order
-// of additions (a Hillis-Steele scan in each wavefront, then the wavefront
-// totals in order).  Returns the exclusive prefix; *incl receives the
-// inclusive one and *total the sum.  A thread's inclusive prefix is the same
-// float as the next thread's exclusive prefix, so the intervals
-// [excl, incl] of consecutive threads meet exactly.
+// Prefix sums of one value per thread in thread order, fixed order of
+// additions (a Hillis-Steele scan per wavefront, then the wavefront totals
+// in order); wsum holds kSmpWaves + 1 entries.  Returns the exclusive
+// prefix; *incl the inclusive one, *total the sum.
 template <class T>
 __device__ inline T smp_block_scan(T v, T* wsum, T* incl, T* total) {
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -59,48 +71,107 @@ __device__ inline T smp_block_scan(T v, T* wsum, T* incl, T* total) {
         const T y = __shfl_up(x, o, 64);
         if (l >= o) x = x + y;
     }
-    const T xp = __shfl_up(x, 1, 64);  // the previous lane's inclusive sum
+    const T xp = __shfl_up(x, 1, 64);
     if (l == 63) wsum[w] = x;
     __syncthreads();
     if (threadIdx.x == 0) {
         T acc = T(0);
-        for (int i = 0; i < kSmpThreads / 64; ++i) {
-            const T s = wsum[i];
+        for (int i = 0; i < kSmpWaves; ++i) {
+            const T t = wsum[i];
             wsum[i] = acc;
-            acc = acc + s;
+            acc = acc + t;
         }
-        wsum[16] = acc;
+        wsum[kSmpWaves] = acc;
     }
     __syncthreads();
     const T ex = l == 0 ? wsum[w] : wsum[w] + xp;
     *incl = wsum[w] + x;
-    *total = wsum[16];
+    *total = wsum[kSmpWaves];
     __syncthreads();
     return ex;
 }
 
+// One pass of a wavefront over its chunk [c0, c1): kSmpU loads per lane are
+// requested before any is used (a block has only 16 wavefronts to hide the
+// memory latency with), then use(i0, valid, value) runs for the 64-entry
+// steps i0 in order (entry i0 + lane).  Indices past c1 load c1 - 1 and
+// are passed as not valid.
+constexpr int kSmpU = 16;
+template <class Load, class Use>
+__device__ inline void smp_pass(int c0, int c1, Load load, Use use) {
+    const int l = threadIdx.x & 63;
+    for (int base = c0; base < c1; base += 64 * kSmpU) {
+        float v[kSmpU];
+#pragma unroll
+        for (int u = 0; u < kSmpU; ++u) v[u] = load(min(base + 64 * u + l, c1 - 1));
+#pragma unroll
+        for (int u = 0; u < kSmpU; ++u) use(base + 64 * u, base + 64 * u + l < c1, v[u]);
+    }
+}
+
 __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
-    __shared__ float redf[17];
-    __shared__ float scanf_[17];
-    __shared__ int scani[17];
+    __shared__ float wf[kSmpWaves + 1];
+    __shared__ int wi[4][kSmpWaves + 1];
     __shared__ int hist[256];
-    __shared__ float cand_p[kSmpMaxK];
-    __shared__ int cand_i[kSmpMaxK];
-    __shared__ int sel_tok;
-    const int b = blockIdx.x, tid = threadIdx.x, V = a.V;
+    __shared__ int sel;
+    __shared__ float cand_p[kSmpCand];
+    __shared__ int cand_i[kSmpCand];
+    __shared__ int ord[kSmpCand];
+    __shared__ int tcnt[kSmpThr][kSmpWaves + 1];
+    const int b = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63, V = a.V;
     const float* lg = a.logits + (size_t)b * a.ldl;
-    const int S = (V + kSmpThreads - 1) / kSmpThreads, i0 = min(tid * S, V), i1 = min(i0 + S, V);
+    float* e = a.scratch + (size_t)b * V;
+    const int C = ((V + kSmpWaves - 1) / kSmpWaves + 63) / 64 * 64;
+    const int c0 = min(w * C, V), c1 = min(c0 + C, V);
     const float T = a.temperature;
 
+    // max, then e and its sum: per lane in order, wavefront tree, wavefronts in order
     float mx = -__builtin_inff();
-    for (int i = i0; i < i1; ++i) mx = fmaxf(mx, lg[i]);
-    mx = smp_block_max(mx, redf);
-    auto e_of = [&](int i) { return expf((lg[i] - mx) / T); };
-    // softmax denominator: per-thread sums in index order, then thread order
-    float part = 0.0f;
-    for (int i = i0; i < i1; ++i) part += e_of(i);
-    float sum_e = 0.0f, fin = 0.0f;
-    (void)smp_block_scan<float>(part, scanf_, &fin, &sum_e);
+    smp_pass(c0, c1, [&](int i) { return lg[i]; }, [&](int, bool ok, float v) { mx = ok ? fmaxf(mx, v) : mx; });
+    mx = smp_wave_max(mx);
+    if (l == 0) wf[w] = mx;
+    __syncthreads();
+    if (tid == 0) {
+        float m = wf[0];
+        for (int j = 1; j < kSmpWaves; ++j) m = fmaxf(m, wf[j]);
+        wf[kSmpWaves] = m;
+    }
+    __syncthreads();
+    mx = wf[kSmpWaves];
+    __syncthreads();
+    // e, its sum, and per wavefront the entries at or above each candidate
+    // threshold exp(-D)
+    float part = 0.0f, thr[kSmpThr];
+    int cnt[kSmpThr];
+#pragma unroll
+    for (int j = 0; j < kSmpThr; ++j) {
+        thr[j] = expf(-c_smp_D[j]);
+        cnt[j] = 0;
+    }
+    smp_pass(c0, c1, [&](int i) { return lg[i]; }, [&](int i0, bool ok, float x) {
+        if (!ok) return;
+        const float v = expf((x - mx) / T);
+        e[i0 + l] = v;
+        part += v;
+#pragma unroll
+        for (int j = 0; j < kSmpThr; ++j) cnt[j] += v >= thr[j];
+    });
+#pragma unroll
+    for (int j = 0; j < kSmpThr; ++j) {
+        const int c = smp_wave_sum(cnt[j]);
+        if (l == 0) tcnt[j][w] = c;
+    }
+    part = smp_wave_sum(part);
+    if (l == 0) wf[w] = part;
+    __syncthreads();  // also makes the e row visible to the block
+    if (tid == 0) {
+        float acc = 0.0f;
+        for (int j = 0; j < kSmpWaves; ++j) acc += wf[j];
+        wf[kSmpWaves] = acc;
+    }
+    __syncthreads();
+    const float sum_e = wf[kSmpWaves];
+    __syncthreads();
     // the draw: fixed, per sequence, or keyed by the sequence's position
     float u = a.u_fixed;
     if (u < 0.0f) {
@@ -113,18 +184,53 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
         }
     }
 
-    const bool topk = a.top_k > 0 && a.top_k < V;
-    if (topk) {
-        // the k-th largest e: radix select over its bits, 8 at a time
+    if (a.top_k > 0 && a.top_k < V) {
+        // candidates: the entries with e >= exp(-D) for the smallest D whose
+        // count is at least k (they hold the top k: p orders as e), if that
+        // count fits in LDS; otherwise a radix selection over all of p finds
+        // exactly k
+        if (tid == 0) {
+            int pick = -1;
+            for (int j = 0; j < kSmpThr; ++j) {
+                int tot = 0;
+                for (int q = 0; q < kSmpWaves; ++q) {
+                    const int c = tcnt[j][q];
+                    tcnt[j][q] = tot;  // exclusive prefix over wavefronts
+                    tot += c;
+                }
+                tcnt[j][kSmpWaves] = tot;
+                if (tot >= a.top_k) pick = tot <= kSmpCand ? j : -2;  // D decreasing: the last fitting one
+            }
+            wi[0][3] = pick;
+        }
+        __syncthreads();
+        int n = 0;
+        const int pick = wi[0][3];
+        if (pick >= 0) {
+            const float th = expf(-c_smp_D[pick]);
+            int orun = tcnt[pick][w];
+            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int i0, bool ok, float ev) {
+                const bool keep = ok && ev >= th;
+                const unsigned long long km = __ballot(keep);
+                if (keep) {
+                    const int at = orun + popc_below(km, l);
+                    cand_p[at] = ev / sum_e;
+                    cand_i[at] = i0 + l;
+                }
+                orun += __popcll(km);
+            });
+            n = tcnt[pick][kSmpWaves];
+        } else {
+        // the k-th largest p: radix select over its bits, 8 at a time
         uint32_t prefix = 0, pmask = 0;
         int need = a.top_k;  // still to take at or below the prefix
         for (int sh = 24; sh >= 0; sh -= 8) {
             for (int j = tid; j < 256; j += kSmpThreads) hist[j] = 0;
             __syncthreads();
-            for (int i = i0; i < i1; ++i) {
-                const uint32_t bits = __builtin_bit_cast(uint32_t, e_of(i) / sum_e);
-                if ((bits & pmask) == prefix) atomicAdd(&hist[(bits >> sh) & 0xFF], 1);
-            }
+            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+                const uint32_t bits = __builtin_bit_cast(uint32_t, ev / sum_e);
+                if (ok && (bits & pmask) == prefix) atomicAdd(&hist[(bits >> sh) & 0xFF], 1);
+            });
             __syncthreads();
             if (tid == 0) {
                 int bin = 255, above = 0;
@@ -132,47 +238,68 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
                     if (above + hist[bin] >= need) break;
                     above += hist[bin];
                 }
-                hist[0] = bin;      // reuse: chosen bin
-                scani[16] = above;  // elements in higher bins
+                wi[0][0] = bin;
+                wi[0][1] = above;
             }
             __syncthreads();
-            const int bin = hist[0];
-            need -= scani[16];
-            prefix |= (uint32_t)bin << sh;
+            prefix |= (uint32_t)wi[0][0] << sh;
             pmask |= 0xFFu << sh;
+            need -= wi[0][1];
             __syncthreads();
         }
-        // survivors: values above the k-th, and the first `need` ties by index
+        // per wavefront: values above the k-th and ties with it
         int nab = 0, ntie = 0;
-        for (int i = i0; i < i1; ++i) {
-            const uint32_t bits = __builtin_bit_cast(uint32_t, e_of(i) / sum_e);
-            nab += bits > prefix;
-            ntie += bits == prefix;
-        }
-        int tot = 0, iin = 0;
-        const int tie_ex = smp_block_scan<int>(ntie, scani, &iin, &tot);
-        int ntake = nab + max(0, min(ntie, need - tie_ex));
-        const int at = smp_block_scan<int>(ntake, scani, &iin, &tot);
-        int o = at, tr = tie_ex;
-        for (int i = i0; i < i1; ++i) {
-            const float p = e_of(i) / sum_e;
-            const uint32_t bits = __builtin_bit_cast(uint32_t, p);
-            bool keep = bits > prefix;
-            if (bits == prefix) keep = tr++ < need;
-            if (keep && o < kSmpMaxK) {
-                cand_p[o] = p;
-                cand_i[o] = i;
-                ++o;
-            }
+        smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+            const uint32_t bits = __builtin_bit_cast(uint32_t, ev / sum_e);
+            nab += ok && bits > prefix;
+            ntie += ok && bits == prefix;
+        });
+        nab = smp_wave_sum(nab);
+        ntie = smp_wave_sum(ntie);
+        if (l == 0) {
+            wi[1][w] = nab;
+            wi[2][w] = ntie;
         }
         __syncthreads();
-        const int n = min(tot, kSmpMaxK);
-        // top-p: descending order (ties by index) by a bitonic sort of
-        // positions 0..n-1 over the next power of two, padding sorting last
-        __shared__ int ord[kSmpMaxK];
+        if (tid == 0) {  // ties before each wavefront, and its first output slot
+            int tb = 0, ob = 0;
+            for (int j = 0; j < kSmpWaves; ++j) {
+                const int nt = wi[2][j];
+                wi[2][j] = tb;
+                wi[3][j] = ob;
+                ob += wi[1][j] + max(0, min(nt, need - tb));
+                tb += nt;
+            }
+            wi[0][2] = ob;  // survivors
+        }
+        __syncthreads();
+        // gather the survivors in index order
+        int trun = wi[2][w], orun = wi[3][w];
+        smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int i0, bool in, float ev) {
+            const float p = ev / sum_e;
+            const uint32_t bits = __builtin_bit_cast(uint32_t, p);
+            const bool tie = in && bits == prefix;
+            const unsigned long long tm = __ballot(tie);
+            const bool keep = in && (bits > prefix || (tie && trun + popc_below(tm, l) < need));
+            const unsigned long long km = __ballot(keep);
+            const int at = orun + popc_below(km, l);
+            if (keep && at < kSmpMaxK) {
+                cand_p[at] = p;
+                cand_i[at] = i0 + l;
+            }
+            trun += __popcll(tm);
+            orun += __popcll(km);
+        });
+        n = min(wi[0][2], kSmpMaxK);
+        }
+        __syncthreads();
+        // descending order of p (ties by index): a bitonic sort of positions
+        // 0..n-1 over the next power of two, padding sorting last; the first
+        // k are the top k, then top-p cuts along the same order
+        const int kk = min(a.top_k, n);
         int np2 = 1;
         while (np2 < n) np2 <<= 1;
-        if (a.top_p < 1.0f) {
+        if (n > kk || a.top_p < 1.0f) {
             for (int j = tid; j < np2; j += kSmpThreads) ord[j] = j;
             __syncthreads();
             auto before = [&](int x, int y) {  // x sorts before y
@@ -196,72 +323,117 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
                     __syncthreads();
                 }
             if (tid == 0) {
-                float cum = 0.0f;
-                int cut = n;
-                for (int j = 0; j < n; ++j) {
-                    cum += cand_p[ord[j]];
-                    if (cum > a.top_p) {
-                        cut = j + 1;
-                        break;
+                int cut = kk;
+                if (a.top_p < 1.0f) {
+                    float cum = 0.0f;
+                    for (int j = 0; j < kk; ++j) {
+                        cum += cand_p[ord[j]];
+                        if (cum > a.top_p) {
+                            cut = j + 1;
+                            break;
+                        }
                     }
                 }
                 for (int j = cut; j < n; ++j) cand_p[ord[j]] = 0.0f;
             }
             __syncthreads();
         }
+        // the kept entries (at most k) in index order, compacted in parallel
+        // (thread t holds candidates 4t .. 4t+3), then renormalized and drawn
+        // from by one lane in that order
+        int nk = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) nk += 4 * tid + q < n && cand_p[4 * tid + q] > 0.0f;
+        int ktot = 0, kin = 0;
+        const int kat = smp_block_scan<int>(nk, wi[1], &kin, &ktot);
+        {
+            int o = kat;
+            float kp[4];
+            int ki[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = 4 * tid + q;
+                kp[q] = j < n ? cand_p[j] : 0.0f;
+                ki[q] = j < n ? cand_i[j] : 0;
+            }
+            __syncthreads();  // the candidate arrays are rewritten in place
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (kp[q] > 0.0f) {
+                    cand_p[o] = kp[q];
+                    cand_i[o] = ki[q];
+                    ++o;
+                }
+        }
+        __syncthreads();
         if (tid == 0) {
-            // renormalize and draw over the survivors in index order
-            float s = 0.0f;
-            for (int j = 0; j < n; ++j) s += cand_p[j];
+            float sm = 0.0f;
+            for (int j = 0; j < ktot; ++j) sm += cand_p[j];
             int tok = V - 1;
-            if (s <= 0.0f) {
-                tok = 0;
+            const float r = u * sm;
+            if (sm <= 0.0f || r <= 0.0f) {
+                tok = 0;  // nothing kept, or the running sum reaches r = 0 at index 0
             } else {
-                const float r = u * s;
                 float cum = 0.0f;
-                if (r <= 0.0f) {
-                    tok = 0;  // the running sum reaches 0 at index 0
-                } else {
-                    for (int j = 0; j < n; ++j) {
-                        cum += cand_p[j];
-                        if (cum >= r) {
-                            tok = cand_i[j];
-                            break;
-                        }
+                for (int j = 0; j < ktot; ++j) {
+                    cum += cand_p[j];
+                    if (cum >= r) {
+                        tok = cand_i[j];
+                        break;
                     }
                 }
             }
-            sel_tok = tok;
+            sel = tok;
         }
         __syncthreads();
     } else {
-        // all V kept: r = u * (sum of p), scan in vocabulary order
-        float ps = 0.0f;
-        for (int i = i0; i < i1; ++i) ps += e_of(i) / sum_e;
-        float total = 0.0f, inc = 0.0f;
-        const float ex = smp_block_scan<float>(ps, scanf_, &inc, &total);
-        const float r = u * total;
-        if (tid == 0) sel_tok = r <= 0.0f ? 0 : V - 1;
+        // all V kept: running sums per wavefront (64-lane scans, iterations
+        // in order), wavefronts in order
+        float run = 0.0f;
+        smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+            const float x = smp_wave_scan(ok ? ev / sum_e : 0.0f);
+            run = run + __shfl(x, 63, 64);
+        });
+        if (l == 0) wf[w] = run;
         __syncthreads();
-        if (r > 0.0f && ex < r && inc >= r) {  // this slice holds the crossing (exactly one does)
-            float cum = ex;
-            int tok = -1, last = -1;
-            for (int i = i0; i < i1; ++i) {
-                const float p = e_of(i) / sum_e;
-                if (p > 0.0f) last = i;
-                cum += p;
-                if (cum >= r) {
-                    tok = i;
-                    break;
-                }
+        if (tid == 0) {
+            float acc = 0.0f;
+            for (int j = 0; j < kSmpWaves; ++j) {
+                const float t = wf[j];
+                wf[j] = acc;
+                acc = acc + t;
             }
-            sel_tok = tok >= 0 ? tok : (last >= 0 ? last : i0);
+            wf[kSmpWaves] = acc;
+            sel = -1;
         }
+        __syncthreads();
+        const float base = wf[w], next = w + 1 < kSmpWaves ? wf[w + 1] : wf[kSmpWaves];
+        const float r = u * wf[kSmpWaves];
+        if (r > 0.0f && base < r && next >= r) {  // this wavefront holds the crossing (exactly one does)
+            float rr = 0.0f;
+            int tok = -1, lastnz = -1;
+            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int i0, bool ok, float ev) {
+                if (tok >= 0) return;  // uniform: found in an earlier step
+                const float p = ok ? ev / sum_e : 0.0f;
+                const float x = smp_wave_scan(p);
+                const float it = __shfl(x, 63, 64);
+                const unsigned long long nz = __ballot(p > 0.0f);
+                if (base + (rr + it) >= r) {
+                    const unsigned long long hit = __ballot(base + (rr + x) >= r && p > 0.0f);
+                    tok = hit ? i0 + __ffsll((long long)hit) - 1 : (nz ? i0 + 63 - __clzll((long long)nz) : lastnz);
+                }
+                if (nz) lastnz = i0 + 63 - __clzll((long long)nz);
+                rr = rr + it;
+            });
+            if (l == 0) sel = tok >= 0 ? tok : (lastnz >= 0 ? lastnz : c0);
+        }
+        __syncthreads();
+        if (tid == 0 && sel < 0) sel = r <= 0.0f ? 0 : V - 1;
         __syncthreads();
     }
     if (tid == 0) {
-        if (a.out) a.out[b] = sel_tok;
-        if (a.best) a.best[b] = 0xFFFFFFFFull - (unsigned long long)(uint32_t)sel_tok;
+        if (a.out) a.out[b] = sel;
+        if (a.best) a.best[b] = 0xFFFFFFFFull - (unsigned long long)(uint32_t)sel;
     }
 }
 
@@ -270,7 +442,7 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
 hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st) {
     if (a.V < 1 || batch < 1 || a.temperature <= 0.0f || a.top_k < 0 || (a.top_k > kSmpMaxK && a.top_k < a.V) ||
         !(a.top_p > 0.0f) || ((a.top_k == 0 || a.top_k >= a.V) && a.top_p < 1.0f) ||
-        (a.u_fixed < 0.0f && !a.u && !a.pos))
+        (a.u_fixed < 0.0f && !a.u && !a.pos) || !a.scratch)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_sample, dim3(batch), dim3(kSmpThreads), 0, st, a);
     return hipGetLastError();

@@ -123,6 +123,28 @@ def test_gpu_sampler_matches_oracle(ctx, V, T, top_k, top_p):
 
 
 @pytest.mark.gpu
+def test_gpu_sampler_wide_top_k_uses_radix_selection(ctx):
+    """Flat logits (every entry within exp(-1) of the maximum, 32000 of them):
+    no candidate threshold fits the LDS buffer, so the radix selection over
+    all probabilities finds the top k; tokens equal the oracle's."""
+    V, B = 32000, 8
+    rng = np.random.default_rng(5)
+    logits = (rng.random((B, V)) * 0.5).astype(np.float32)
+    bl, bo = ctx.upload(logits), ctx.alloc(B * 4)
+    for k, tp in ((40, 0.9), (1024, 1.0), (3, 0.5)):
+        ctx.sample(bl, bo, V, B, 0.9, k, tp, 77)
+        got = ctx.download(bo, (B,), np.int32)
+        u = draw(77)
+        for b in range(B):
+            want = L.nxo_sample(np.ascontiguousarray(logits[b]), V, 0.9, k, tp, u)
+            _, margin = ref64(logits[b], 0.9, k, tp, u)
+            if margin > 1e-5:
+                assert got[b] == want, (k, tp, b, got[b], want)
+    ctx.free(bl)
+    ctx.free(bo)
+
+
+@pytest.mark.gpu
 def test_gpu_sampler_ties_and_edges(ctx):
     """Equal logits (ties at the k-th value keep the lowest indices), a
     one-hot row, and greedy through nx_sample."""
