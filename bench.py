@@ -58,14 +58,14 @@ MIXTRAL = dict(LLAMA8B, vocab=32000, n_experts=8, top_k=2, rope_theta=1000000.0)
 MODELS = {"llama-8b": LLAMA8B, "mixtral-8x7b": MIXTRAL}
 
 
-def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int) -> dict:
+def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window: int = 0) -> dict:
     """Time the oracle's decode step on a bounded sample and scale to a token."""
     import numpy as np
 
     import oracle
     vocab_frac = 8
     cfg = dict(base, n_layers=1, vocab=base["vocab"] // vocab_frac, batch=batch, kv_kind=kv_kind,
-               max_seq=((ctx_len + 16) // 16 + 1) * 16)
+               max_seq=((ctx_len + 16) // 16 + 1) * 16, hot_window=hot_window)
     m = oracle.Model(**cfg)
     m.fill_context(ctx_len, 4 if kv_kind else 0)
     tok = np.zeros(batch, np.int32)
@@ -159,6 +159,33 @@ def nxf_verify_bench(ctx, cpu: bool, nbytes: int = 4 << 30, chunk: int = 64 << 1
 PEAK_MFMA_TFLOPS = 2500.0  # dense fp16 matrix-core peak
 
 
+def tiering_bench(ctx, base: dict, ctx_len: int = 32768, hot_window: int = 4096, steps: int = 64) -> dict:
+    """One layer of the model's shape at a long context, with fp16,
+    TurboQuant and tiered pages: the attention pass (KV bytes it reads, its
+    time) and the time of a one-layer decode step (for tiered pages it
+    includes the device compressor, which encodes a page every 16 steps)."""
+    import nexus_amd
+    out = {"ctx": ctx_len, "hot_window": hot_window}
+    for name, kind in (("fp16", 0), ("tq", 1), ("tiered", 2)):
+        cfg = dict(base, n_layers=1, vocab=1024, batch=1, kv_kind=kind, max_seq=ctx_len + 16 * (steps // 16 + 2),
+                   hot_window=hot_window if kind == 2 else 0)
+        m = nexus_amd.Model(ctx, **cfg)
+        m.fill_context(ctx_len, 4 if kind else 0)
+        m.decode_untimed(2)
+        ctx.sync()
+        t0 = time.perf_counter()
+        m.decode_untimed(steps)
+        ctx.sync()
+        step_ms = (time.perf_counter() - t0) * 1e3 / steps
+        ms, nb = m.time_attention(200)
+        m.close()
+        gbs = nb / (ms * 1e-3) / 1e9
+        out[name] = {"attention_us": round(ms * 1e3, 2), "kv_bytes": int(nb), "GBps": round(gbs, 1),
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "step_ms_1layer": round(step_ms, 4)}
+    out["kv_bytes_vs_fp16"] = round(out["tiered"]["kv_bytes"] / out["fp16"]["kv_bytes"], 4)
+    return out
+
+
 def prefill_bench(ctx, base: dict, P: int = 2048) -> dict:
     """Batched prefill throughput of a P-token prompt (fresh model, positions
     from 0) and the TFLOP/s of its gate/up GEMM at the 512-token chunk."""
@@ -206,7 +233,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--ctx", type=int, default=4096)
-    ap.add_argument("--kv", choices=["fp16", "tq"], default="fp16")
+    ap.add_argument("--kv", choices=["fp16", "tq", "tiered"], default="fp16")
+    ap.add_argument("--hot-window", type=int, default=4096,
+                    help="tiered pages: positions kept fp16 (older pages TurboQuant)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-kernel", choices=["ffn", "attention", "xxh32"],
                     help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc)")
@@ -243,12 +272,13 @@ def main() -> int:
         print(json.dumps({"kernel": "xxh32", "avg_us": r["avg_us"], "bytes": r["bytes"], "launches": 17}))
         ctx.close()
         return 0
-    kv_kind = 1 if args.kv == "tq" else 0
+    kv_kind = {"fp16": 0, "tq": 1, "tiered": 2}[args.kv]
     smp_steps = max(8, args.steps // 2)  # sampled decode steps after the greedy ones
     max_seq = ((args.ctx + args.warmup + args.steps + smp_steps + 24) // 16 + 1) * 16
     base = MODELS[args.model]
     moe = base["n_experts"] > 0
-    cfg = dict(base, batch=args.batch, kv_kind=kv_kind, max_seq=max_seq)
+    cfg = dict(base, batch=args.batch, kv_kind=kv_kind, max_seq=max_seq,
+               hot_window=args.hot_window if kv_kind == 2 else 0)
     ctx = nexus_amd.Context(0)
     print(f"[bench] device {ctx.device_name()}; building {args.model}-shaped model "
           f"(batch {args.batch}, ctx {args.ctx}, kv {args.kv})", file=sys.stderr, flush=True)
@@ -308,8 +338,10 @@ def main() -> int:
     micro = gemv_microbench(ctx, args.batch) if not moe else None
     nxf = nxf_verify_bench(ctx, not args.no_cpu)
     pre = prefill_bench(ctx, base) if not moe else None
+    tier = tiering_bench(ctx, base) if base["head_dim"] == 128 else None
     ctx.close()
-    kv_name = "fp16" if kv_kind == 0 else "TurboQuant 3.5-bit"
+    kv_name = ["fp16", "TurboQuant 3.5-bit", f"tiered (last {args.hot_window} positions fp16, older pages "
+               "TurboQuant 3.5-bit)"][kv_kind]
     if moe:
         workload = (f"mixtral-8x7b-shape int4-g32 greedy decode (top-2 of 8 experts), batch {args.batch}, "
                     f"ctx {args.ctx} {kv_name} paged KV")
@@ -358,9 +390,12 @@ def main() -> int:
     line["sampling"] = sampling
     if pre is not None:
         line["prefill"] = pre
+    if tier is not None:
+        line["tiering"] = tier
     if not args.no_cpu:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind)
+        line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind,
+                                            args.hot_window if kv_kind == 2 else 0)
     print(json.dumps(line), flush=True)
     return 0
 

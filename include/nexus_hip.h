@@ -228,12 +228,17 @@ typedef struct {
     int n_experts, top_k;   /* n_experts == 0: dense SwiGLU */
     int max_seq;            /* per sequence, multiple of 16 */
     int batch;              /* sequences decoded together (1..8) */
-    int kv_kind;            /* 0 = fp16 pages, 1 = TurboQuant pages (head_dim 128) */
+    int kv_kind;            /* 0 = fp16 pages, 1 = TurboQuant pages (head_dim 128),
+                               2 = tiered: the last hot_window positions fp16 (a ring of
+                               hot_window / 16 + 1 pages per sequence), older pages
+                               compressed to TurboQuant on the device as they leave
+                               the window (head_dim 128) */
     float rope_theta;
     float eps;
     uint64_t seed;
     float norm_sigma;       /* RMSNorm weights: 0 = all 1.0, else 1 + N(0, norm_sigma)
                                seeded per tensor (synthetic models) */
+    int hot_window;         /* kv_kind 2: positions kept fp16, a positive multiple of 16 */
 } nx_model_config;
 
 typedef struct nx_model nx_model;
@@ -263,6 +268,14 @@ nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float
  * (n_outlier channels per head scaled x10); the pending token of every
  * sequence becomes a seeded start token. */
 nx_status nx_model_fill_context(nx_model* m, int ctx, int n_outlier);
+/* The stored form of position pos of sequence b in layer `layer`, all kv
+ * heads, K (kv 0) or V (kv 1): form 0 = fp16 [hkv][head_dim] (2 * hkv *
+ * head_dim bytes), form 1 = TurboQuant [hkv] x (32 bytes of 4-bit codes, 24
+ * of 3-bit codes, fp16 norm) (58 * hkv bytes); *form tells which (tiered
+ * pages: 1 before the window, 0 in it).  The per-position read-back of
+ * PagedKVCache::get_vectors (kv/paged_attention.cpp:161-230), as stored
+ * rather than decompressed; cap = bytes available at out. */
+nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* form, void* out, size_t cap);
 /* The pending (next input) token of every sequence, [batch]. */
 nx_status nx_model_pending(nx_model* m, int32_t* tokens);
 /* Engine::generate's loop (engine.cpp:155-173) of `steps` decode_step calls

@@ -61,6 +61,24 @@ __device__ inline float ld_coh(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The part of sequence b's context a launch covers.  Tiered pages
+// (hot_window > 0): the compressed pages [0, cold) (range 1) or the fp16
+// window [cold, ctx) (range 2, read from page cold / 16 of the block table
+// on), cold = 16 floor((ctx - hot_window) / 16), at least 0.
+__device__ inline void attn_range(const AttnArgs& a, int b, int& ctx, int& pg0) {
+    ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    pg0 = 0;
+    if (a.hot_window > 0) {
+        const int cold = kPage * max(0, (ctx - a.hot_window) / kPage);
+        if (a.range == 1) {
+            ctx = cold;
+        } else {
+            pg0 = cold / kPage;
+            ctx -= cold;
+        }
+    }
+}
+
 // Cross-wavefront merge of the block: lds holds one record per wavefront
 // (O[G][HD], M[G], L[G]); every wavefront has written its own before the
 // barrier.  The rescale factors exp(m_w - M) are computed once per (wavefront,
@@ -303,6 +321,7 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
         v[u] = sx < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(rs, (sx * REC + 4 * c) * 4, 0, kSc1)
                            : f4v{0.f, 0.f, 0.f, 0.f};
     }
+    __shared__ float mlh[2 * G];  // the merged (M, L) of each head
     for (int hh = wave; hh < G; hh += kAttnWaves) {
         const bool ok = lane < nsplit;
         const int sl = ok ? lane : nsplit - 1;
@@ -312,6 +331,10 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
         const float e = (ok && M != -__builtin_inff()) ? __expf(m - M) : 0.0f;
         const float L = wave_sum(e * l);
         wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : 0.0f;
+        if (lane == 0) {
+            mlh[2 * hh] = M;
+            mlh[2 * hh + 1] = L;
+        }
     }
     f4v acc = {0.f, 0.f, 0.f, 0.f};
     __syncthreads();
@@ -345,13 +368,24 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
         }
     }
     uint16_t* out = a.out16 + ((size_t)b * a.hq + (size_t)kvh * G) * HD;
+    // record mode (tiered pages): the normalized O in fp32 and (M, L) per
+    // head, for the merge with the other part of the context
+    float* ro = a.rec_o ? a.rec_o + ((size_t)b * a.hq + (size_t)kvh * G) * HD : nullptr;
+    if (ro && tid < 2 * G) a.rec_ml[((size_t)b * a.hq + (size_t)kvh * G) * 2 + tid] = mlh[tid];
     if constexpr (TQ) {
         static_assert(HD == 128, "TurboQuant vectors are 128 long");
         __shared__ float ov[G * HD];
         if (tid < NC) *reinterpret_cast<float4*>(&ov[4 * tid]) = r;
         lds_fwht<G>(ov);
-        for (int idx = tid; idx < G * HD; idx += kAttnThreads)
-            out[idx] = f2h_bits(ov[idx] * kTqScale * a.vsign[idx % HD]);
+        for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
+            const float y = ov[idx] * kTqScale * a.vsign[idx % HD];
+            if (ro)
+                ro[idx] = y;
+            else
+                out[idx] = f2h_bits(y);
+        }
+    } else if (ro) {
+        if (tid < NC) *reinterpret_cast<float4*>(ro + 4 * tid) = r;
     } else if (tid < NC) {
         *reinterpret_cast<uint2*>(out + 4 * tid) =
             make_uint2((uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16),
@@ -374,12 +408,13 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
 
     // The context length and this wavefront's block-table entries (page
     // p0 + wave + 4i in lane i) are requested together: one round trip.
-    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    int ctx, pg0;
+    attn_range(a, b, ctx, pg0);
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
-    const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
-                            ? a.block_table[(size_t)b * a.max_blocks + my_page]
+    const int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
+                            ? a.block_table[(size_t)b * a.max_blocks + pg0 + my_page]
                             : 0;
     // q as the B operand (column = head t, k = 8g + j of each 32-dim step).
     // Columns t >= G repeat head G - 1 (loads without a branch, so all of q
@@ -671,12 +706,13 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsp
     __shared__ float qrot[G * HD];
     __shared__ uint32_t cbk[24];
 
-    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+    int ctx, pg0;
+    attn_range(a, b, ctx, pg0);
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
-    const int bt_lane = (lane < npw_max && my_page < a.max_blocks)
-                            ? a.block_table[(size_t)b * a.max_blocks + my_page]
+    const int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
+                            ? a.block_table[(size_t)b * a.max_blocks + pg0 + my_page]
                             : 0;
     const int npages = (ctx + kPage - 1) / kPage;
     const int p1 = min(p0 + pps, npages);
@@ -781,11 +817,10 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsp
 
 // ----------------------------------------------------- TurboQuant encode --
 // One wavefront per vector; lane l holds coordinates l and l + 64.
-__device__ inline void tq_encode_wave(const float* __restrict__ x, const float* __restrict__ sign,
+__device__ inline void tq_encode_vals(float x0, float x1, const float* __restrict__ sign,
                                       uint8_t* __restrict__ c4, uint8_t* __restrict__ c3,
                                       uint16_t* __restrict__ norm, uint8_t* lds_codes) {
     const int lane = threadIdx.x & 63;
-    const float x0 = x[lane], x1 = x[lane + 64];
     const float a0 = x0 * x0;
     const float a1 = x1 * x1;
     float w = a0 + a1;
@@ -838,6 +873,14 @@ __device__ inline void tq_encode_wave(const float* __restrict__ x, const float* 
         c3[lane] = (uint8_t)(bits >> (8 * r));
     }
     if (lane == 0) *norm = f2h_bits(n);
+}
+
+// One vector of 128 from memory: lane l takes entries l and l + 64.
+__device__ inline void tq_encode_wave(const float* __restrict__ x, const float* __restrict__ sign,
+                                      uint8_t* __restrict__ c4, uint8_t* __restrict__ c3,
+                                      uint16_t* __restrict__ norm, uint8_t* lds_codes) {
+    const int lane = threadIdx.x & 63;
+    tq_encode_vals(x[lane], x[lane + 64], sign, c4, c3, norm, lds_codes);
 }
 
 __global__ __launch_bounds__(256) void k_tq_encode(const float* x, int nvec, const float* signs,
@@ -961,7 +1004,115 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     }
 }
 
+// Tiered pages, the page that leaves the fp16 window this step: when the
+// position p just written completes page q = (p - H + 1) / 16 - 1 beyond
+// the window (p - H + 1 a positive multiple of 16), its fp16 K and V (hot
+// page hot_bt[q]) are encoded into the TurboQuant page tq_bt[q].  Block
+// (b, kv * hkv + h), one wavefront: the 16 vectors of one head and kind.
+// Every other step the blocks leave at once.
+__global__ __launch_bounds__(64) void k_tq_compress(const int32_t* pos, int hot_window, int hkv,
+                                                    const int32_t* hot_bt, const int32_t* tq_bt, int max_blocks,
+                                                    const uint16_t* kpool, const uint16_t* vpool, const float* ksign,
+                                                    const float* vsign, uint8_t* kc4, uint8_t* kc3, uint16_t* kn,
+                                                    uint8_t* vc4, uint8_t* vc3, uint16_t* vn) {
+    __shared__ uint8_t codes[128];
+    const int b = blockIdx.x, kv = blockIdx.y / hkv, h = blockIdx.y % hkv, lane = threadIdx.x;
+    const int done = pos[b] - hot_window + 1;
+    if (done < kPage || done % kPage) return;
+    const int q = done / kPage - 1;
+    const size_t hot = (size_t)hot_bt[(size_t)b * max_blocks + q] * hkv + h;
+    const size_t dst0 = ((size_t)tq_bt[(size_t)b * max_blocks + q] * hkv + h) * kPage;
+    for (int slot = 0; slot < kPage; ++slot) {
+        // the previous slot's reads of codes[] come before this slot's writes
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float x0, x1;
+        if (kv == 0) {  // K pages are token-major [16][128]
+            const uint16_t* src = kpool + (hot * kPage + slot) * kTqD;
+            x0 = h2f_bits(src[lane]);
+            x1 = h2f_bits(src[lane + 64]);
+        } else {        // V pages are dimension-major [128][16]
+            const uint16_t* src = vpool + hot * kPage * kTqD;
+            x0 = h2f_bits(src[(size_t)lane * kPage + slot]);
+            x1 = h2f_bits(src[(size_t)(lane + 64) * kPage + slot]);
+        }
+        const size_t dst = dst0 + slot;
+        if (kv == 0)
+            tq_encode_vals(x0, x1, ksign, kc4 + dst * 32, kc3 + dst * 24, kn + dst, codes);
+        else
+            tq_encode_vals(x0, x1, vsign, vc4 + dst * 32, vc3 + dst * 24, vn + dst, codes);
+    }
+}
+
+// Attention over tiered pages, the last step: the normalized outputs of the
+// compressed part (oa, (Ma, La)) and of the fp16 window (ob, (Mb, Lb)) of
+// each (sequence, head) combined with weights L exp(M - max M).
+__global__ __launch_bounds__(128) void k_attn_merge2(const float* oa, const float* mla, const float* ob,
+                                                     const float* mlb, uint16_t* out, int hd) {
+    const size_t bh = blockIdx.x;
+    const float Ma = mla[2 * bh], La = mla[2 * bh + 1], Mb = mlb[2 * bh], Lb = mlb[2 * bh + 1];
+    const float M = fmaxf(La > 0.0f ? Ma : -__builtin_inff(), Lb > 0.0f ? Mb : -__builtin_inff());
+    const float wa = La > 0.0f ? La * __expf(Ma - M) : 0.0f, wb = Lb > 0.0f ? Lb * __expf(Mb - M) : 0.0f;
+    const float den = wa + wb;
+    for (int d = threadIdx.x; d < hd; d += 128) {
+        const float va = wa > 0.0f ? oa[bh * hd + d] : 0.0f, vb = wb > 0.0f ? ob[bh * hd + d] : 0.0f;
+        out[bh * hd + d] = f2h_bits(den > 0.0f ? (wa * va + wb * vb) / den : 0.0f);
+    }
+}
+
+// Context fill of tiered pages: positions [cold, ctx) of raw [ctx][hkv][hd]
+// (fp32) as fp16 into the window's pages of sequence b.
+__global__ __launch_bounds__(256) void k_put_hot(const float* raw, int ctx, int cold, int hkv, int hd, int b,
+                                                 const int32_t* hot_bt, int max_blocks, uint16_t* kpool,
+                                                 uint16_t* vpool, int kv) {
+    const long n = (long)(ctx - cold) * hkv * hd;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const int p = cold + (int)(i / (hkv * hd)), h = (int)(i / hd % hkv), d = (int)(i % hd);
+        const size_t page = ((size_t)hot_bt[(size_t)b * max_blocks + p / kPage] * hkv + h) * kPage * hd;
+        const uint16_t v = f2h_bits(raw[((size_t)p * hkv + h) * hd + d]);
+        if (kv == 0)
+            kpool[page + (size_t)(p % kPage) * hd + d] = v;
+        else
+            vpool[page + (size_t)d * kPage + p % kPage] = v;
+    }
+}
+
+// x = fp32(fp16(x)), RNE (the values the fp16 window holds).
+__global__ __launch_bounds__(256) void k_round_f16(float* x, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        x[i] = h2f_bits(f2h_bits(x[i]));
+}
+
 }  // namespace
+
+hipError_t tq_compress_launch(const int32_t* pos, int hot_window, int batch, int hkv, const int32_t* hot_bt,
+                              const int32_t* tq_bt, int max_blocks, const uint16_t* kpool, const uint16_t* vpool,
+                              const float* ksign, const float* vsign, uint8_t* kc4, uint8_t* kc3, uint16_t* kn,
+                              uint8_t* vc4, uint8_t* vc3, uint16_t* vn, hipStream_t st) {
+    hipLaunchKernelGGL(k_tq_compress, dim3(batch, 2 * hkv), dim3(64), 0, st, pos, hot_window, hkv, hot_bt, tq_bt,
+                       max_blocks, kpool, vpool, ksign, vsign, kc4, kc3, kn, vc4, vc3, vn);
+    return hipGetLastError();
+}
+
+hipError_t attn_merge2_launch(const float* oa, const float* mla, const float* ob, const float* mlb, uint16_t* out,
+                              int batch, int hq, int hd, hipStream_t st) {
+    hipLaunchKernelGGL(k_attn_merge2, dim3(batch * hq), dim3(128), 0, st, oa, mla, ob, mlb, out, hd);
+    return hipGetLastError();
+}
+
+hipError_t put_hot_launch(const float* raw, int ctx, int cold, int hkv, int hd, int b, const int32_t* hot_bt,
+                          int max_blocks, uint16_t* kpool, uint16_t* vpool, int kv, hipStream_t st) {
+    if (ctx <= cold) return hipSuccess;
+    hipLaunchKernelGGL(k_put_hot, dim3(256), dim3(256), 0, st, raw, ctx, cold, hkv, hd, b, hot_bt, max_blocks, kpool,
+                       vpool, kv);
+    return hipGetLastError();
+}
+
+hipError_t round_f16_launch(float* x, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_round_f16, dim3(1024), dim3(256), 0, st, x, n);
+    return hipGetLastError();
+}
 
 hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st) {
     if (P < 1 || p0 < 0 || !a.block_table) return hipErrorInvalidValue;

@@ -80,6 +80,14 @@ struct nx_model {
     uint16_t* moe_act = nullptr;
     float* moe_y = nullptr;
     float* attn_part = nullptr;
+    // tiered pages: the fp16 window's ring of hot_pages pages per sequence
+    // (hot_bt[b][p] = b * hot_pages + p % hot_pages, the same max_blocks
+    // stride as block_table) and the two attention records (compressed
+    // part, window) before their merge
+    int hot_pages = 0;
+    int32_t* hot_bt = nullptr;
+    float* rec_o[2] = {nullptr, nullptr};
+    float* rec_ml[2] = {nullptr, nullptr};
     unsigned* attn_counts = nullptr;  // split-completion counters of the fp16 attention
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
@@ -194,6 +202,75 @@ nx_status enqueue_sample(nx_model* m, int b0, int nb) {
     return NX_OK;
 }
 
+// Attention of layer ly for every sequence (q in m->q, output m->att16).
+// Tiered pages: the TurboQuant kernel over the compressed pages and the
+// fp16 kernel over the window, each leaving a normalized record, and their
+// merge.
+hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
+    const nx_model_config& c = m->c;
+    nx::AttnArgs at{};
+    at.q = m->q;
+    at.kpool = ly.kpool;
+    at.vpool = ly.vpool;
+    at.kc4 = ly.kc4;
+    at.kc3 = ly.kc3;
+    at.vc4 = ly.vc4;
+    at.vc3 = ly.vc3;
+    at.kn = ly.kn;
+    at.vn = ly.vn;
+    at.ksign = ly.ksign;
+    at.vsign = ly.vsign;
+    at.block_table = m->block_table;
+    at.ctx_lens = nullptr;
+    at.pos = m->pos;
+    at.out16 = m->att16;
+    at.batch = c.batch;
+    at.hq = c.n_heads;
+    at.hkv = c.n_kv_heads;
+    at.hd = c.head_dim;
+    at.max_blocks = m->max_blocks;
+    at.max_ctx = c.max_seq;
+    at.part = m->attn_part;
+    at.counts = m->attn_counts;
+    if (c.kv_kind == 0) return nx::attn_f16_launch(at, st);
+    if (c.kv_kind == 1) return nx::attn_tq_launch(at, st);
+    at.hot_window = c.hot_window;
+    at.range = 1;
+    at.rec_o = m->rec_o[0];
+    at.rec_ml = m->rec_ml[0];
+    hipError_t e = nx::attn_tq_launch(at, st);
+    if (e != hipSuccess) return e;
+    at.range = 2;
+    at.block_table = m->hot_bt;
+    at.max_ctx = m->hot_pages * nx::kPage;
+    at.rec_o = m->rec_o[1];
+    at.rec_ml = m->rec_ml[1];
+    e = nx::attn_f16_launch(at, st);
+    if (e != hipSuccess) return e;
+    return nx::attn_merge2_launch(m->rec_o[0], m->rec_ml[0], m->rec_o[1], m->rec_ml[1], m->att16, c.batch,
+                                  c.n_heads, c.head_dim, st);
+}
+
+// KV bytes one attention pass reads for sequences at hpos (TurboQuant: 58
+// bytes per vector; tiered: TurboQuant before the window, fp16 in it).
+double kv_bytes(const nx_model* m) {
+    const nx_model_config& c = m->c;
+    const double f16 = 2.0 * c.n_kv_heads * c.head_dim * 2, tq = 2.0 * c.n_kv_heads * 58;
+    double kv = 0.0;
+    for (int b = 0; b < c.batch; ++b) {
+        const int ctx = m->hpos[b] + 1;
+        if (c.kv_kind == 0) {
+            kv += ctx * f16;
+        } else if (c.kv_kind == 1) {
+            kv += ctx * tq;
+        } else {
+            const int cold = nx::kPage * std::max(0, (ctx - c.hot_window) / nx::kPage);
+            kv += cold * tq + (ctx - cold) * f16;
+        }
+    }
+    return kv;
+}
+
 // One decode step for every sequence, enqueued on the context stream.
 nx_status enqueue_step(nx_model* m) {
     const nx_model_config& c = m->c;
@@ -223,9 +300,9 @@ nx_status enqueue_step(nx_model* m) {
         a.pos = m->pos;
         a.cos_t = m->rope_cos;
         a.sin_t = m->rope_sin;
-        a.block_table = m->block_table;
+        a.block_table = c.kv_kind == 2 ? m->hot_bt : m->block_table;
         a.max_blocks = m->max_blocks;
-        if (c.kv_kind == 0) {
+        if (c.kv_kind != 1) {
             a.kpool = ly.kpool;
             a.vpool = ly.vpool;
         } else {
@@ -236,32 +313,12 @@ nx_status enqueue_step(nx_model* m) {
             NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr, ly.kc4,
                                               ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table, m->pos,
                                               m->max_blocks, st));
+        if (c.kv_kind == 2)  // the page that left the fp16 window, if any, into TurboQuant
+            NX_LAUNCH(m, nx::tq_compress_launch(m->pos, c.hot_window, B, c.n_kv_heads, m->hot_bt, m->block_table,
+                                                m->max_blocks, ly.kpool, ly.vpool, ly.ksign, ly.vsign, ly.kc4,
+                                                ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, st));
         // attention
-        nx::AttnArgs at{};
-        at.q = m->q;
-        at.kpool = ly.kpool;
-        at.vpool = ly.vpool;
-        at.kc4 = ly.kc4;
-        at.kc3 = ly.kc3;
-        at.vc4 = ly.vc4;
-        at.vc3 = ly.vc3;
-        at.kn = ly.kn;
-        at.vn = ly.vn;
-        at.ksign = ly.ksign;
-        at.vsign = ly.vsign;
-        at.block_table = m->block_table;
-        at.ctx_lens = nullptr;
-        at.pos = m->pos;
-        at.out16 = m->att16;
-        at.batch = B;
-        at.hq = c.n_heads;
-        at.hkv = c.n_kv_heads;
-        at.hd = c.head_dim;
-        at.max_blocks = m->max_blocks;
-        at.max_ctx = c.max_seq;
-        at.part = m->attn_part;
-        at.counts = m->attn_counts;
-        NX_LAUNCH(m, c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st));
+        NX_LAUNCH(m, attention_launch(m, ly, st));
         // output projection + residual
         nx::GemvArgs o{};
         o.W = ly.wo;
@@ -441,6 +498,7 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     m->Fp = m->Gf * 32;
     m->max_blocks = c.max_seq / nx::kPage;
     m->n_blocks = m->max_blocks * B;
+    m->hot_pages = c.kv_kind == 2 ? c.hot_window / nx::kPage + 1 : 0;
     m->out_stride = c.max_seq;
     m->layers.resize(L);
     m->hpos.assign(B, -1);
@@ -475,7 +533,13 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         if (c.kv_kind == 0) {
             NX_TRY(dalloc(m, &ly.kpool, pool_elems));
             NX_TRY(dalloc(m, &ly.vpool, pool_elems));
-        } else {
+        }
+        if (c.kv_kind == 2) {
+            const size_t hot_elems = (size_t)B * m->hot_pages * c.n_kv_heads * nx::kPage * c.head_dim;
+            NX_TRY(dalloc(m, &ly.kpool, hot_elems));
+            NX_TRY(dalloc(m, &ly.vpool, hot_elems));
+        }
+        if (c.kv_kind != 0) {
             NX_TRY(dalloc(m, &ly.kc4, pool_vecs * 32));
             NX_TRY(dalloc(m, &ly.kc3, pool_vecs * 24));
             NX_TRY(dalloc(m, &ly.vc4, pool_vecs * 32));
@@ -542,6 +606,18 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         NX_TRY(dalloc(m, &m->moe_y, (size_t)B * c.top_k * d));
     }
     NX_TRY(dalloc(m, &m->attn_counts, nx::attn_count_words(B, c.n_kv_heads)));
+    if (c.kv_kind == 2) {
+        std::vector<int32_t> ring((size_t)B * m->max_blocks);
+        for (int b = 0; b < B; ++b)
+            for (int p = 0; p < m->max_blocks; ++p) ring[(size_t)b * m->max_blocks + p] = b * m->hot_pages + p % m->hot_pages;
+        NX_TRY(dalloc(m, &m->hot_bt, ring.size()));
+        NX_HIP(m->ctx, hipMemcpyAsync(m->hot_bt, ring.data(), ring.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
+        for (int i = 0; i < 2; ++i) {
+            NX_TRY(dalloc(m, &m->rec_o[i], (size_t)B * m->qdim));
+            NX_TRY(dalloc(m, &m->rec_ml[i], (size_t)B * c.n_heads * 2));
+        }
+        NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    }
     NX_TRY(dalloc(m, &m->attn_part,
                   nx::attn_workspace_bytes(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq) / 4 + 1));
     {
@@ -559,13 +635,15 @@ nx_status create_impl(nx_model* m, bool synthetic) {
 nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.n_layers < 1 || c.d_model < 32 || c.n_heads < 1 || c.n_kv_heads < 1 || c.n_heads % c.n_kv_heads ||
         c.ffn < 2 || c.vocab < 2 || c.max_seq < nx::kPage || c.max_seq % nx::kPage || c.batch < 1 || c.batch > 8 ||
-        (c.kv_kind != 0 && c.kv_kind != 1) || c.eps <= 0.0f || c.rope_theta <= 0.0f ||
+        c.kv_kind < 0 || c.kv_kind > 2 || c.eps <= 0.0f || c.rope_theta <= 0.0f ||
         !(c.norm_sigma >= 0.0f && c.norm_sigma < 1e3f))
         return fail(ctx, NX_ERR_INVALID, "nx_model_create: invalid configuration");
     const int G = c.n_heads / c.n_kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return fail(ctx, NX_ERR_UNSUPPORTED, "hq/hkv must be 1, 2, 4 or 8");
     if (c.head_dim != 64 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
-    if (c.kv_kind == 1 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
+    if (c.kv_kind != 0 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
+    if (c.kv_kind == 2 && (c.hot_window < nx::kPage || c.hot_window % nx::kPage || c.hot_window >= c.max_seq))
+        return fail(ctx, NX_ERR_INVALID, "hot_window must be a positive multiple of 16 below max_seq");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
     if (c.max_seq > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the attention limit");
     if (c.d_model > 14336 || c.ffn > 14336 || c.n_heads * c.head_dim > 14336)
@@ -833,7 +911,8 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
     int32_t* och = nullptr;
     NX_TRY(dalloc(m, &och, (size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1)));
     float* raw = nullptr;
-    if (c.kv_kind == 1) NX_TRY(dalloc(m, &raw, (size_t)ctx_len * hkv * hd));
+    if (c.kv_kind != 0) NX_TRY(dalloc(m, &raw, (size_t)ctx_len * hkv * hd));
+    const int cold = c.kv_kind == 2 ? nx::kPage * std::max(0, (ctx_len - c.hot_window) / nx::kPage) : ctx_len;
     std::vector<int32_t> ho((size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
@@ -848,13 +927,20 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
             NX_LAUNCH(m, nx::gen_ctx_f16_launch(ly.kpool, ly.vpool, m->block_table, m->max_blocks, B, ctx_len, hkv, hd, L,
                                                 c.seed, k1, och, n_outlier, st));
         } else {
+            // tiered: the values rounded to fp16 (what the window holds), the
+            // pages before cold encoded, the rest into the window's ring
             for (int b = 0; b < B; ++b)
                 for (int kv = 0; kv < 2; ++kv) {
                     NX_LAUNCH(m, nx::gen_ctx_raw_launch(raw, ctx_len, hkv, hd, L, b, kv, c.seed, k1,
                                                         och + (size_t)kv * hkv * n_outlier, n_outlier, st));
-                    NX_LAUNCH(m, nx::tq_encode_ctx_launch(raw, ctx_len, hkv, kv ? ly.vsign : ly.ksign, nullptr, nullptr,
-                                                          kv ? ly.vc4 : ly.kc4, kv ? ly.vc3 : ly.kc3, kv ? ly.vn : ly.kn,
-                                                          m->block_table, m->max_blocks, b, st));
+                    if (c.kv_kind == 2) NX_LAUNCH(m, nx::round_f16_launch(raw, (size_t)ctx_len * hkv * hd, st));
+                    if (cold > 0)
+                        NX_LAUNCH(m, nx::tq_encode_ctx_launch(raw, cold, hkv, kv ? ly.vsign : ly.ksign, nullptr, nullptr,
+                                                              kv ? ly.vc4 : ly.kc4, kv ? ly.vc3 : ly.kc3,
+                                                              kv ? ly.vn : ly.kn, m->block_table, m->max_blocks, b, st));
+                    if (c.kv_kind == 2)
+                        NX_LAUNCH(m, nx::put_hot_launch(raw, ctx_len, cold, hkv, hd, b, m->hot_bt, m->max_blocks,
+                                                        ly.kpool, ly.vpool, kv, st));
                 }
         }
         NX_HIP(m->ctx, hipStreamSynchronize(st));
@@ -878,6 +964,48 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
                 break;
             }
     }
+    return NX_OK;
+}
+
+nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* form, void* out, size_t cap) {
+    if (!m || !form || !out) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    if (layer < 0 || layer >= c.n_layers || b < 0 || b >= c.batch || kv < 0 || kv > 1 || pos < 0 ||
+        pos > m->hpos[(size_t)b])
+        return fail(m->ctx, NX_ERR_INVALID, "nx_model_kv_read: no such position");
+    const int hkv = c.n_kv_heads, hd = c.head_dim, page = pos / nx::kPage, slot = pos % nx::kPage;
+    const int ctx_len = m->hpos[(size_t)b] + 1;
+    const int cold = c.kv_kind == 0   ? 0
+                     : c.kv_kind == 1 ? ctx_len
+                                      : nx::kPage * std::max(0, (ctx_len - c.hot_window) / nx::kPage);
+    *form = pos < cold ? 1 : 0;
+    const size_t need = *form ? (size_t)58 * hkv : (size_t)2 * hkv * hd;
+    if (cap < need) return fail(m->ctx, NX_ERR_INVALID, "nx_model_kv_read: %zu bytes needed", need);
+    const Layer& ly = m->layers[layer];
+    hipStream_t st = m->ctx->stream;
+    uint8_t* dst = static_cast<uint8_t*>(out);
+    int32_t blk = 0;
+    const int32_t* bt = *form || c.kv_kind == 0 ? m->block_table : m->hot_bt;
+    NX_HIP(m->ctx, hipMemcpyAsync(&blk, bt + (size_t)b * m->max_blocks + page, 4, hipMemcpyDeviceToHost, st));
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    for (int h = 0; h < hkv; ++h) {
+        if (*form) {
+            const size_t vi = ((size_t)blk * hkv + h) * nx::kPage + slot;
+            uint8_t* o = dst + (size_t)58 * h;
+            NX_HIP(m->ctx, hipMemcpyAsync(o, (kv ? ly.vc4 : ly.kc4) + vi * 32, 32, hipMemcpyDeviceToHost, st));
+            NX_HIP(m->ctx, hipMemcpyAsync(o + 32, (kv ? ly.vc3 : ly.kc3) + vi * 24, 24, hipMemcpyDeviceToHost, st));
+            NX_HIP(m->ctx, hipMemcpyAsync(o + 56, (kv ? ly.vn : ly.kn) + vi, 2, hipMemcpyDeviceToHost, st));
+        } else {
+            // K pages are token-major [16][hd], V pages dimension-major [hd][16]
+            const uint16_t* pg = (kv ? ly.vpool : ly.kpool) + ((size_t)blk * hkv + h) * nx::kPage * hd;
+            uint16_t* o = reinterpret_cast<uint16_t*>(dst) + (size_t)h * hd;
+            if (kv)
+                NX_HIP(m->ctx, hipMemcpy2DAsync(o, 2, pg + slot, 2 * nx::kPage, 2, hd, hipMemcpyDeviceToHost, st));
+            else
+                NX_HIP(m->ctx, hipMemcpyAsync(o, pg + (size_t)slot * hd, 2 * (size_t)hd, hipMemcpyDeviceToHost, st));
+        }
+    }
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
     return NX_OK;
 }
 
@@ -934,7 +1062,7 @@ nx_status nx_model_position(nx_model* m, int b, int* p) {
 nx_status nx_model_step_bytes(nx_model* m, double* bytes) {
     if (!m || !bytes) return NX_ERR_INVALID;
     const nx_model_config& c = m->c;
-    const int d = c.d_model, F = c.ffn, E = c.n_experts, B = c.batch;
+    const int d = c.d_model, F = c.ffn, E = c.n_experts;
     double w = (double)qbytes(c.vocab, d);  // lm_head
     for (int L = 0; L < c.n_layers; ++L) {
         w += (double)qbytes(m->nqkv, d) + (double)qbytes(d, m->qdim);
@@ -949,10 +1077,7 @@ nx_status nx_model_step_bytes(nx_model* m, double* bytes) {
             w += (double)qbytes(E, d) + active * ((double)qbytes(2 * (size_t)F, d) + (double)qbytes(d, F));
         }
     }
-    double kv = 0.0;
-    const double per_tok = c.kv_kind == 0 ? 2.0 * c.n_kv_heads * c.head_dim * 2 : 2.0 * c.n_kv_heads * 58;
-    for (int b = 0; b < B; ++b) kv += (double)(m->hpos[b] + 1) * per_tok;
-    *bytes = w + kv * c.n_layers;
+    *bytes = w + kv_bytes(m) * c.n_layers;
     return NX_OK;
 }
 
@@ -1041,33 +1166,7 @@ nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double
         if (m->hpos[b] < 0) return fail(m->ctx, NX_ERR_STATE, "no context to attend over");
     hipStream_t st = m->ctx->stream;
     // launch i attends over layer i % n_layers (a separate cache per layer)
-    auto launch = [&](int i) {
-        const Layer& ly = m->layers[i % c.n_layers];
-        nx::AttnArgs at{};
-        at.q = m->q;
-        at.kpool = ly.kpool;
-        at.vpool = ly.vpool;
-        at.kc4 = ly.kc4;
-        at.kc3 = ly.kc3;
-        at.vc4 = ly.vc4;
-        at.vc3 = ly.vc3;
-        at.kn = ly.kn;
-        at.vn = ly.vn;
-        at.ksign = ly.ksign;
-        at.vsign = ly.vsign;
-        at.block_table = m->block_table;
-        at.pos = m->pos;
-        at.out16 = m->att16;
-        at.batch = c.batch;
-        at.hq = c.n_heads;
-        at.hkv = c.n_kv_heads;
-        at.hd = c.head_dim;
-        at.max_blocks = m->max_blocks;
-        at.max_ctx = c.max_seq;
-        at.part = m->attn_part;
-        at.counts = m->attn_counts;
-        return c.kv_kind == 0 ? nx::attn_f16_launch(at, st) : nx::attn_tq_launch(at, st);
-    };
+    auto launch = [&](int i) { return attention_launch(m, m->layers[i % c.n_layers], st); };
     for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
     for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch(i));
@@ -1076,12 +1175,7 @@ nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double
     float ms = 0.0f;
     NX_HIP(m->ctx, hipEventElapsedTime(&ms, m->ctx->ev0, m->ctx->ev1));
     *avg_ms = (double)ms / iters;
-    if (bytes) {
-        const double per_tok = c.kv_kind == 0 ? 2.0 * c.n_kv_heads * c.head_dim * 2 : 2.0 * c.n_kv_heads * 58;
-        double kv = 0.0;
-        for (int b = 0; b < c.batch; ++b) kv += (double)(m->hpos[b] + 1) * per_tok;
-        *bytes = kv;
-    }
+    if (bytes) *bytes = kv_bytes(m);
     return NX_OK;
 }
 

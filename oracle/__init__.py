@@ -31,7 +31,7 @@ class Cfg(C.Structure):
         ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int),
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
-        ("seed", C.c_uint64), ("norm_sigma", C.c_float),
+        ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
     ]
 
 
@@ -93,6 +93,13 @@ def _load() -> C.CDLL:
         "nxo_attn_decode_paged_tq": (None, [_f32p, _u8p, _u8p, _u16p, _u8p, _u8p, _u16p, _f32p,
                                             _f32p, _f32p, _f32p, _i32p, C.c_int, _i32p, C.c_int,
                                             C.c_int, C.c_int, _f32p]),
+        "nxo_tiered_append": (None, [_f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, _f32p, _u16p, _u16p,
+                                     _u8p, _u8p, _u16p, _u8p, _u8p, _u16p, _i32p, C.c_int, C.c_int,
+                                     C.c_int]),
+        "nxo_tiered_cold": (C.c_int, [C.c_int, C.c_int]),
+        "nxo_attn_decode_tiered": (None, [_f32p, _u16p, _u16p, _u8p, _u8p, _u16p, _u8p, _u8p, _u16p,
+                                          _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int, _i32p, C.c_int,
+                                          C.c_int, C.c_int, C.c_int, _f32p]),
         "nxo_moe_route": (None, [_f32p, C.c_int, C.c_int, _i32p, _f32p]),
         "nxo_model_create": (C.c_void_p, [C.POINTER(Cfg)]),
         "nxo_model_free": (None, [C.c_void_p]),
@@ -101,6 +108,7 @@ def _load() -> C.CDLL:
                                            C.POINTER(C.c_double)]),
         "nxo_model_generate": (None, [C.c_void_p, _i32p, C.c_int, C.c_int, _i32p, _f32p]),
         "nxo_model_fill_context": (None, [C.c_void_p, C.c_int, C.c_int]),
+        "nxo_model_kv_read": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _u8p]),
         "nxo_model_position": (C.c_int, [C.c_void_p, C.c_int]),
         "nxo_num_threads": (C.c_int, []),
         "nxo_set_num_threads": (None, [C.c_int]),
@@ -272,6 +280,13 @@ class Model:
 
     def fill_context(self, ctx: int, n_outlier: int = 0):
         lib.nxo_model_fill_context(self.h, ctx, n_outlier)
+
+    def kv_read(self, layer: int, b: int, pos: int, kv: int, form: int) -> np.ndarray:
+        """Stored bytes of one position, all kv heads (nxo_model_kv_read)."""
+        out = np.zeros(max(58, 2 * self.cfg.head_dim) * self.cfg.n_kv_heads, np.uint8)
+        n = lib.nxo_model_kv_read(self.h, layer, b, pos, kv, form, out)
+        assert n > 0, "the oracle model does not hold that form"
+        return out[:n]
 
     def position(self, b: int = 0) -> int:
         return lib.nxo_model_position(self.h, b)

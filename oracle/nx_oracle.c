@@ -567,6 +567,63 @@ void nxo_attn_decode_paged_tq(const float* q,
     }
 }
 
+/* Tiered pages: see nx_oracle.h. */
+void nxo_tiered_append(const float* k, const float* v, int hkv, const float* ksigns, const float* vsigns,
+                       const float* b4, const float* b3, uint16_t* kpool, uint16_t* vpool, uint8_t* kc4,
+                       uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                       const int32_t* block_table, int max_blocks, int b, int pos) {
+    const size_t n = (size_t)hkv * NXO_TQ_D;
+    float* r = (float*)malloc(sizeof(float) * 2 * n);
+    for (size_t i = 0; i < n; ++i) {
+        r[i] = round_f16(k[i]);
+        r[n + i] = round_f16(v[i]);
+    }
+    nxo_kv_append_f16(r, r + n, kpool, vpool, block_table, max_blocks, b, pos, hkv, NXO_TQ_D);
+    nxo_tq_append(r, r + n, hkv, ksigns, vsigns, b4, b3, kc4, kc3, kn, vc4, vc3, vn, block_table, max_blocks,
+                  b, pos);
+    free(r);
+}
+
+int nxo_tiered_cold(int ctx, int hot_window) {
+    const int c = ctx - hot_window;
+    return c > 0 ? NXO_PAGE * (c / NXO_PAGE) : 0;
+}
+
+void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                            const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                            const uint16_t* vn, const float* ksigns, const float* vsigns, const float* c4,
+                            const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
+                            int hot_window, int B, int hq, int hkv, float* out) {
+    const int hd = NXO_TQ_D;
+    const int grp = hq / hkv;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int b = 0; b < B; ++b) {
+        for (int kvh = 0; kvh < hkv; ++kvh) {
+            const int ctx = ctx_lens[b], cold = nxo_tiered_cold(ctx, hot_window);
+            const int32_t* bt = block_table + (size_t)b * max_blocks;
+            const size_t rows = (size_t)(ctx > 0 ? ctx : 1);
+            float* K = (float*)malloc(sizeof(float) * rows * hd);
+            float* V = (float*)malloc(sizeof(float) * rows * hd);
+            float* scores = (float*)malloc(sizeof(float) * rows);
+            gather_f16(kpool, bt, ctx, hkv, kvh, hd, 0, K);
+            gather_f16(vpool, bt, ctx, hkv, kvh, hd, 1, V);
+            for (int t = 0; t < cold; ++t) {
+                const size_t vi = ((size_t)bt[t / NXO_PAGE] * hkv + kvh) * NXO_PAGE + t % NXO_PAGE;
+                nxo_tq_decode(kc4 + vi * 32, kc3 + vi * 24, kn + vi, 1, ksigns, c4, c3, K + (size_t)t * hd);
+                nxo_tq_decode(vc4 + vi * 32, vc3 + vi * 24, vn + vi, 1, vsigns, c4, c3, V + (size_t)t * hd);
+            }
+            for (int j = 0; j < grp; ++j) {
+                const int h = kvh * grp + j;
+                attend_head(q + ((size_t)b * hq + h) * hd, K, V, (size_t)hd, ctx, hd,
+                            out + ((size_t)b * hq + h) * hd, scores);
+            }
+            free(K);
+            free(V);
+            free(scores);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ MoE -- */
 void nxo_moe_route(const float* logits, int E, int k, int32_t* ids, float* weights) {
     float p[256];
@@ -721,10 +778,11 @@ nxo_model* nxo_model_create(const nxo_cfg* cfg) {
                 make_qmat(&ly->ew2[e], d, c->ffn, seed, NXO_TID_EXPERT(L, e, 2), 0.02);
             }
         }
-        if (c->kv_kind == 0) {
+        if (c->kv_kind != 1) {
             ly->kpool = (uint16_t*)calloc(pool_elems, 2);
             ly->vpool = (uint16_t*)calloc(pool_elems, 2);
-        } else {
+        }
+        if (c->kv_kind != 0) {
             ly->kc4 = (uint8_t*)calloc(pool_vecs, 32);
             ly->kc3 = (uint8_t*)calloc(pool_vecs, 24);
             ly->vc4 = (uint8_t*)calloc(pool_vecs, 32);
@@ -782,6 +840,29 @@ void nxo_model_free(nxo_model* m) {
 
 int nxo_model_position(const nxo_model* m, int b) { return m->pos[b]; }
 const int32_t* nxo_model_block_table(const nxo_model* m) { return m->block_table; }
+int nxo_model_kv_read(const nxo_model* m, int layer, int b, int pos, int kv, int form, uint8_t* out) {
+    const nxo_cfg* c = &m->c;
+    const int hkv = c->n_kv_heads, hd = c->head_dim;
+    const layer_t* ly = &m->layers[layer];
+    const int blk = m->block_table[(size_t)b * m->max_blocks + pos / NXO_PAGE], slot = pos % NXO_PAGE;
+    if (form == 0 && !ly->kpool) return 0;
+    if (form == 1 && !ly->kc4) return 0;
+    for (int h = 0; h < hkv; ++h) {
+        if (form == 1) {
+            const size_t vi = ((size_t)blk * hkv + h) * NXO_PAGE + slot;
+            memcpy(out + (size_t)58 * h, (kv ? ly->vc4 : ly->kc4) + vi * 32, 32);
+            memcpy(out + (size_t)58 * h + 32, (kv ? ly->vc3 : ly->kc3) + vi * 24, 24);
+            memcpy(out + (size_t)58 * h + 56, (kv ? ly->vn : ly->kn) + vi, 2);
+        } else {
+            const uint16_t* pg = (kv ? ly->vpool : ly->kpool) + ((size_t)blk * hkv + h) * NXO_PAGE * hd;
+            for (int d = 0; d < hd; ++d) {
+                const uint16_t v = kv ? pg[(size_t)d * NXO_PAGE + slot] : pg[(size_t)slot * hd + d];
+                memcpy(out + ((size_t)h * hd + d) * 2, &v, 2);
+            }
+        }
+    }
+    return form == 1 ? 58 * hkv : 2 * hkv * hd;
+}
 int nxo_model_max_blocks(const nxo_model* m) { return m->max_blocks; }
 
 /* x (fp32) -> fp16-rounded RMSNorm output with weights w (NULL = 1.0). */
@@ -855,6 +936,10 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
             if (c->kv_kind == 0)
                 nxo_kv_append_f16(kb, vb, ly->kpool, ly->vpool, m->block_table, m->max_blocks, b,
                                   m->pos[b], hkv, hd);
+            else if (c->kv_kind == 2)
+                nxo_tiered_append(kb, vb, hkv, ly->ksign, ly->vsign, m->b4, m->b3, ly->kpool, ly->vpool,
+                                  ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn, m->block_table,
+                                  m->max_blocks, b, m->pos[b]);
             else
                 nxo_tq_append(kb, vb, hkv, ly->ksign, ly->vsign, m->b4, m->b3, ly->kc4, ly->kc3,
                               ly->kn, ly->vc4, ly->vc3, ly->vn, m->block_table, m->max_blocks, b,
@@ -863,6 +948,10 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
         if (c->kv_kind == 0)
             nxo_attn_decode_paged_f16(m->q, ly->kpool, ly->vpool, m->block_table, m->max_blocks,
                                       ctx, B, hq, hkv, hd, m->att);
+        else if (c->kv_kind == 2)
+            nxo_attn_decode_tiered(m->q, ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
+                                   ly->vn, ly->ksign, ly->vsign, m->c4, m->c3, m->block_table, m->max_blocks,
+                                   ctx, c->hot_window, B, hq, hkv, m->att);
         else
             nxo_attn_decode_paged_tq(m->q, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn,
                                      ly->ksign, ly->vsign, m->c4, m->c3, m->block_table,
@@ -955,6 +1044,10 @@ void nxo_model_fill_context(nxo_model* m, int ctx, int n_outlier) {
                 if (c->kv_kind == 0)
                     nxo_kv_append_f16(kv, kv + (size_t)hkv * hd, ly->kpool, ly->vpool, m->block_table,
                                       m->max_blocks, b, p, hkv, hd);
+                else if (c->kv_kind == 2)
+                    nxo_tiered_append(kv, kv + (size_t)hkv * hd, hkv, ly->ksign, ly->vsign, m->b4, m->b3,
+                                      ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
+                                      ly->vn, m->block_table, m->max_blocks, b, p);
                 else
                     nxo_tq_append(kv, kv + (size_t)hkv * hd, hkv, ly->ksign, ly->vsign, m->b4, m->b3,
                                   ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn, m->block_table,

@@ -157,6 +157,27 @@ void nxo_attn_decode_paged_tq(const float* q,
                               const float* c4, const float* c3,
                               const int32_t* block_table, int max_blocks,
                               const int32_t* ctx_lens, int B, int hq, int hkv, float* out);
+/* Tiered pages (kv_kind 2), after the reference's PagedKVCache
+ * (kv/paged_attention.cpp): positions are written as fp16 (Hot,
+ * insert_kv :81-128) and a page is compressed to TurboQuant once it lies
+ * wholly outside the window of the last hot_window positions (the Hot ->
+ * Warm step of compress_tier :244-291, run per page as it leaves the
+ * window).  The restatement keeps both forms of every position: append
+ * writes the fp16 page and the TurboQuant codes of the fp16 values (the
+ * codes a later compression of that page produces), and attention reads
+ * position t < cold from the codes, t >= cold from fp16, cold =
+ * 16 floor((ctx - hot_window) / 16) clamped at 0, in one softmax (the
+ * mixed-tier gather of get_vectors :161-230). */
+void nxo_tiered_append(const float* k, const float* v, int hkv, const float* ksigns, const float* vsigns,
+                       const float* b4, const float* b3, uint16_t* kpool, uint16_t* vpool, uint8_t* kc4,
+                       uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                       const int32_t* block_table, int max_blocks, int b, int pos);
+int nxo_tiered_cold(int ctx, int hot_window);
+void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                            const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                            const uint16_t* vn, const float* ksigns, const float* vsigns, const float* c4,
+                            const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
+                            int hot_window, int B, int hq, int hkv, float* out);
 
 /* ------------------------------------------------------------------ MoE -- */
 /* model/hybrid_model.cpp:1662-1694: softmax over E (max-subtract, expf,
@@ -177,11 +198,14 @@ typedef struct {
     int n_experts, top_k;          /* n_experts == 0: dense SwiGLU FFN */
     int max_seq;                   /* per sequence, multiple of 16 */
     int batch;                     /* sequences */
-    int kv_kind;                   /* 0 = fp16 pages, 1 = TurboQuant pages */
+    int kv_kind;                   /* 0 = fp16 pages, 1 = TurboQuant pages, 2 = tiered:
+                                      the last hot_window positions (and the partly
+                                      filled page) fp16, older pages TurboQuant */
     float rope_theta;
     float eps;
     uint64_t seed;
     float norm_sigma;              /* RMSNorm weights: 0 = 1.0, else 1 + N(0, norm_sigma) */
+    int hot_window;                /* kv_kind 2: tokens kept fp16, a multiple of 16 */
 } nxo_cfg;
 
 typedef struct nxo_model nxo_model;
@@ -202,6 +226,11 @@ void nxo_model_fill_context(nxo_model* m, int ctx, int n_outlier);
 int nxo_model_position(const nxo_model* m, int b);
 /* Accessors used by the tests (host copies of the model's tensors). */
 const int32_t* nxo_model_block_table(const nxo_model* m);
+/* The stored form of position pos (all kv heads) of layer `layer`, K (kv 0)
+ * or V (kv 1): form 0 = fp16 [hkv][hd], form 1 = TurboQuant [hkv] x (32 B
+ * 4-bit codes, 24 B 3-bit codes, fp16 norm); the model must hold that form
+ * (tiered models hold both).  Returns the bytes written, 0 if absent. */
+int nxo_model_kv_read(const nxo_model* m, int layer, int b, int pos, int kv, int form, uint8_t* out);
 int nxo_model_max_blocks(const nxo_model* m);
 /* Time one forward step split into layers and the lm_head (seconds). */
 void nxo_model_forward_timed(nxo_model* m, const int32_t* tokens, float* logits,

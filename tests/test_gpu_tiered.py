@@ -1,0 +1,101 @@
+"""Tiered pages on the GPU (kv_kind 2): the last hot_window positions in
+fp16, older pages compressed to TurboQuant on the device as they leave the
+window (the Hot -> Warm step of PagedKVCache::compress_tier,
+kv/paged_attention.cpp:244-291, run per page), attention over both tiers
+in one softmax (the mixed-tier gather of get_vectors, :161-230).  Checked
+against the oracle's restatement: greedy tokens, logits, and the stored
+bytes of every compressed page bit-exact."""
+import numpy as np
+import pytest
+
+import nexus_amd
+import oracle
+from conftest import rel_err
+from test_gpu_model import TINY, assert_greedy_parity, run_both, top2_margin
+
+pytestmark = pytest.mark.gpu
+
+TQ_TINY = dict(TINY, n_heads=4, n_kv_heads=2, head_dim=128, d_model=512)
+
+
+@pytest.mark.parametrize("batch,H", [(1, 16), (2, 48)])
+def test_tiered_greedy_parity(ctx, batch, H):
+    """A 12-token prompt and 100 greedy tokens: pages leave the window and
+    are compressed every 16 steps from position H + 15 on."""
+    cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, seed=0x7E1 + H)
+    got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
+    assert_greedy_parity(got, want, margins)
+
+
+def _oracle_steps(om, start, steps):
+    tok, want, margins = start, [], []
+    for _ in range(steps):
+        logits = om.forward(tok)
+        tok = logits.argmax(axis=1).astype(np.int32)
+        want.append(tok)
+        margins.append(top2_margin(logits))
+    return np.stack(want, 1), np.stack(margins, 1), logits
+
+
+def test_tiered_filled_context_and_compressor(ctx):
+    """A 300-position context with a 64-position window (pages 0..13
+    compressed by the fill, 14..18 in the window), then 40 decode steps, in
+    which pages 14, 15 and 16 leave the window and the device compressor
+    encodes them.  Every stored position of the fill is bit-exact against
+    the oracle (codes before the window, fp16 in it), so are the pages the
+    compressor wrote, and the decode gives the oracle's tokens."""
+    cfg = dict(TQ_TINY, batch=2, max_seq=512, kv_kind=2, hot_window=64, seed=0x71E2)
+    ctx_len, steps = 300, 40
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(ctx_len, 4)
+    om = oracle.Model(**cfg)
+    om.fill_context(ctx_len, 4)
+
+    def check(positions, form_want):
+        for L in range(cfg["n_layers"]):
+            for b in range(2):
+                for kv in range(2):
+                    for p in positions:
+                        form, got = gm.kv_read(L, b, p, kv)
+                        assert form == form_want, (L, b, p, kv)
+                        want = om.kv_read(L, b, p, kv, form)
+                        assert np.array_equal(got, want), (L, b, p, kv, form)
+
+    check(list(range(0, 224, 7)) + [223], 1)
+    check(range(224, 300), 0)
+    start = gm.pending()
+    got = gm.decode(steps)
+    glog = gm.logits()
+    check(range(224, 272), 1)  # compressed on the device during the decode
+    check(range(272, 300), 0)
+    gm.close()
+    want, margins, logits = _oracle_steps(om, start, steps)
+    om.close()
+    assert_greedy_parity(got, want, margins)
+    if np.array_equal(got, want):
+        assert rel_err(glog, logits) < 1e-3
+
+
+def test_tiered_window_covering_context_matches_fp16_pages(ctx):
+    """A window larger than the context keeps every position in fp16: the
+    tiered path (an empty compressed part, the fp16 kernel's record and the
+    merge) gives the fp16-page model's logits within 1e-3 and its tokens."""
+    base = dict(TQ_TINY, batch=2, max_seq=512, seed=0xF16)
+    ctx_len, steps = 200, 12
+    out = {}
+    for kind, extra in ((0, {}), (2, {"hot_window": 480})):
+        m = nexus_amd.Model(ctx, **dict(base, kv_kind=kind, **extra))
+        m.fill_context(ctx_len, 0)
+        toks = m.decode(steps)
+        out[kind] = (toks, m.logits())
+        m.close()
+    assert np.array_equal(out[0][0], out[2][0])
+    assert rel_err(out[2][1], out[0][1]) < 1e-3
+
+
+def test_tiered_config_rejected(ctx):
+    for H in (0, 24, 128):
+        with pytest.raises(RuntimeError):
+            nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=2, hot_window=H))
+    with pytest.raises(RuntimeError):
+        nexus_amd.Model(ctx, **dict(TINY, kv_kind=2, hot_window=32))  # head_dim 64

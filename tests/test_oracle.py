@@ -446,6 +446,61 @@ def test_tq_attention_close_to_fp16_attention():
     assert rel_err(out[0], want) < 0.25
 
 
+def test_tiered_cold_boundary():
+    """Pages wholly before the window of the last H positions are cold:
+    cold = 16 floor((ctx - H) / 16), 0 while ctx <= H + 15."""
+    for ctx, H, want in [(1, 16, 0), (16, 16, 0), (31, 16, 0), (32, 16, 16), (47, 16, 16), (48, 16, 32),
+                         (300, 64, 224), (4096, 4096, 0), (32768, 4096, 28672), (32767, 4096, 28656)]:
+        assert L.nxo_tiered_cold(ctx, H) == want, (ctx, H)
+
+
+@pytest.mark.parametrize("ctx,H", [(100, 32), (40, 16), (20, 48), (16, 16)])
+def test_tiered_attention_vs_fp64(ctx, H):
+    """Tiered pages against an independent float64 restatement: positions
+    before cold read as the TurboQuant round trip of their fp16 values,
+    the rest as fp16, one softmax over all.  A cold boundary one page off
+    (the planted mistake below) moves the result well past the bound."""
+    rng = np.random.default_rng(ctx + H)
+    hq, hkv, B = 4, 2, 2
+    K = rng.normal(0, 1, (B, ctx, hkv, 128)).astype(np.float32)
+    V = rng.normal(0, 1, (B, ctx, hkv, 128)).astype(np.float32)
+    q = rng.normal(0, 0.4, (B, hq, 128)).astype(np.float32)
+    ks, vs = oracle.tq_signs(3, 1), oracle.tq_signs(3, 2)
+    c4, b4 = oracle.codebook(4)
+    c3, b3 = oracle.codebook(3)
+    max_blocks = (ctx + 15) // 16 + 1
+    bt = rng.permutation(B * max_blocks).astype(np.int32).reshape(B, max_blocks)
+    nv = B * max_blocks * hkv * 16
+    kp, vp = np.zeros(nv * 128, np.uint16), np.zeros(nv * 128, np.uint16)
+    kc4, kc3, kn = np.zeros((nv, 32), np.uint8), np.zeros((nv, 24), np.uint8), np.zeros(nv, np.uint16)
+    vc4, vc3, vn = np.zeros_like(kc4), np.zeros_like(kc3), np.zeros_like(kn)
+    for b in range(B):
+        for p in range(ctx):
+            L.nxo_tiered_append(np.ascontiguousarray(K[b, p]), np.ascontiguousarray(V[b, p]), hkv, ks, vs, b4,
+                                b3, kp, vp, kc4, kc3, kn, vc4, vc3, vn, bt, max_blocks, b, p)
+    out = np.empty_like(q)
+    L.nxo_attn_decode_tiered(q, kp, vp, kc4, kc3, kn, vc4, vc3, vn, ks, vs, c4, c3, bt, max_blocks,
+                             np.full(B, ctx, np.int32), H, B, hq, hkv, out)
+
+    def want_for(cold):
+        Kf = K.astype(np.float16).astype(np.float64)
+        Vf = V.astype(np.float16).astype(np.float64)
+        for b in range(B):
+            for h in range(hkv):
+                if cold:
+                    rk = oracle.tq_decode(*oracle.tq_encode(K[b, :cold, h].astype(np.float16).astype(np.float32), ks)[:3], ks)
+                    rv = oracle.tq_decode(*oracle.tq_encode(V[b, :cold, h].astype(np.float16).astype(np.float32), vs)[:3], vs)
+                    Kf[b, :cold, h], Vf[b, :cold, h] = rk, rv
+        return np.stack([_attn_fp64(q[b].astype(np.float64), Kf[b], Vf[b], hq, hkv, 128) for b in range(B)])
+
+    cold = max(0, (ctx - H) // 16 * 16)
+    want = want_for(cold)
+    e = rel_err(out, want)
+    assert e < 1e-5, e
+    if cold + 16 <= ctx:
+        assert rel_err(want_for(cold + 16), want) > 1e-3
+
+
 # -------------------------------------------------------------------- MoE --
 def test_moe_route_golden():
     g = gold("moe_route.npz")
