@@ -237,6 +237,8 @@ def main() -> int:
     ap.add_argument("--hot-window", type=int, default=4096,
                     help="tiered pages: positions kept fp16 (older pages TurboQuant)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode measurement (no GEMV, NXF, prefill or tiering lines)")
     ap.add_argument("--profile-kernel", choices=["ffn", "attention", "xxh32"],
                     help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -335,10 +337,11 @@ def main() -> int:
     ffn_gbs = ffn_bytes / (ffn_ms * 1e-3) / 1e9
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     model.close()
-    micro = gemv_microbench(ctx, args.batch) if not moe else None
-    nxf = nxf_verify_bench(ctx, not args.no_cpu)
-    pre = prefill_bench(ctx, base) if not moe else None
-    tier = tiering_bench(ctx, base) if base["head_dim"] == 128 else None
+    full = not args.decode_only
+    micro = gemv_microbench(ctx, args.batch) if full and not moe else None
+    nxf = nxf_verify_bench(ctx, not args.no_cpu) if full else None
+    pre = prefill_bench(ctx, base) if full and not moe else None
+    tier = tiering_bench(ctx, base) if full and base["head_dim"] == 128 else None
     ctx.close()
     kv_name = ["fp16", "TurboQuant 3.5-bit", f"tiered (last {args.hot_window} positions fp16, older pages "
                "TurboQuant 3.5-bit)"][kv_kind]
@@ -386,7 +389,8 @@ def main() -> int:
     }
     if micro is not None:
         line["gemv_microbench"] = micro
-    line["nxf_verify"] = nxf
+    if nxf is not None:
+        line["nxf_verify"] = nxf
     line["sampling"] = sampling
     if pre is not None:
         line["prefill"] = pre

@@ -61,16 +61,18 @@ __device__ inline float ld_coh(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The part of sequence b's context a launch covers.  Tiered pages
-// (hot_window > 0): the compressed pages [0, cold) (range 1) or the fp16
-// window [cold, ctx) (range 2, read from page cold / 16 of the block table
-// on), cold = 16 floor((ctx - hot_window) / 16), at least 0.
-__device__ inline void attn_range(const AttnArgs& a, int b, int& ctx, int& pg0) {
+// The part of sequence b's context a block covers: all of it (range 0), or
+// with tiered pages the compressed pages [0, cold) (range 1) or the fp16
+// window [cold, ctx) (range 2, read from page cold / 16 of the hot table
+// on), cold = 16 floor((ctx - 1 - hot_window) / 16), at least 0: the pages
+// compressed before this step (the page that leaves the window at this step
+// is compressed by the same launch and read here as fp16).
+__device__ inline void attn_range(const AttnArgs& a, int b, int range, int& ctx, int& pg0) {
     ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     pg0 = 0;
-    if (a.hot_window > 0) {
-        const int cold = kPage * max(0, (ctx - a.hot_window) / kPage);
-        if (a.range == 1) {
+    if (range != 0) {
+        const int cold = kPage * max(0, (ctx - 1 - a.hot_window) / kPage);
+        if (range == 1) {
             ctx = cold;
         } else {
             pg0 = cold / kPage;
@@ -291,10 +293,12 @@ constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
 // s = t / NC (mod NG), NG = 256 / NC; it requests all of them at once
 // (16-byte buffer loads with the sc1 bit, skipped past nsplit, where the
 // weight is zero), and the NG partial sums meet in LDS.
-// TQ: the merged value sums are in the rotated domain; they are rotated
-// back (o = D_v H o~ / sqrt(128), an FWHT in LDS) before the fp16 output.
+// TQ: the value sums of records [0, ntq) are in the rotated domain (all of
+// them for TurboQuant pages, the compressed part for tiered pages); their
+// merged sum is rotated back (o = D_v H o~ / sqrt(128), an FWHT in LDS) and
+// added to the merged sum of the fp16 records [ntq, nsplit).
 template <int G, int HD, bool TQ = false>
-__device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b) {
+__device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     constexpr int NC = G * HD / 4, NG = kAttnThreads / NC;
     constexpr int KMAX = (kMaxSplits + NG - 1) / NG, U = KMAX < 16 ? KMAX : 16;
@@ -321,7 +325,6 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
         v[u] = sx < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(rs, (sx * REC + 4 * c) * 4, 0, kSc1)
                            : f4v{0.f, 0.f, 0.f, 0.f};
     }
-    __shared__ float mlh[2 * G];  // the merged (M, L) of each head
     for (int hh = wave; hh < G; hh += kAttnWaves) {
         const bool ok = lane < nsplit;
         const int sl = ok ? lane : nsplit - 1;
@@ -331,19 +334,21 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
         const float e = (ok && M != -__builtin_inff()) ? __expf(m - M) : 0.0f;
         const float L = wave_sum(e * l);
         wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : 0.0f;
-        if (lane == 0) {
-            mlh[2 * hh] = M;
-            mlh[2 * hh + 1] = L;
-        }
     }
-    f4v acc = {0.f, 0.f, 0.f, 0.f};
+    f4v acc = {0.f, 0.f, 0.f, 0.f}, accp = {0.f, 0.f, 0.f, 0.f};  // rotated, plain records
     __syncthreads();
     for (int s0 = sg;;) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int sx = s0 + u * NG;
             const float w = wgt[h * kMaxSplits + min(sx, kMaxSplits - 1)] * (sx < nsplit ? 1.0f : 0.0f);
-            acc += w * v[u];
+            if constexpr (TQ) {
+                const float wr = sx < ntq ? w : 0.0f;
+                acc += wr * v[u];
+                accp += (w - wr) * v[u];
+            } else {
+                acc += w * v[u];
+            }
         }
         s0 += NG * U;
         if (s0 >= nsplit) break;
@@ -354,38 +359,36 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
                                : f4v{0.f, 0.f, 0.f, 0.f};
         }
     }
+    auto group_sum = [&]() {
+        float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid < NC) {
+            r = acc4[tid];
+            for (int gi = 1; gi < NG; ++gi) {
+                const float4 q = acc4[gi * NC + tid];
+                r.x += q.x;
+                r.y += q.y;
+                r.z += q.z;
+                r.w += q.w;
+            }
+        }
+        return r;
+    };
     acc4[tid] = make_float4(acc.x, acc.y, acc.z, acc.w);
     __syncthreads();
-    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < NC) {
-        r = acc4[tid];
-        for (int gi = 1; gi < NG; ++gi) {
-            const float4 q = acc4[gi * NC + tid];
-            r.x += q.x;
-            r.y += q.y;
-            r.z += q.z;
-            r.w += q.w;
-        }
-    }
+    const float4 r = group_sum();
     uint16_t* out = a.out16 + ((size_t)b * a.hq + (size_t)kvh * G) * HD;
-    // record mode (tiered pages): the normalized O in fp32 and (M, L) per
-    // head, for the merge with the other part of the context
-    float* ro = a.rec_o ? a.rec_o + ((size_t)b * a.hq + (size_t)kvh * G) * HD : nullptr;
-    if (ro && tid < 2 * G) a.rec_ml[((size_t)b * a.hq + (size_t)kvh * G) * 2 + tid] = mlh[tid];
     if constexpr (TQ) {
         static_assert(HD == 128, "TurboQuant vectors are 128 long");
-        __shared__ float ov[G * HD];
+        __shared__ float ov[G * HD], ovp[G * HD];
         if (tid < NC) *reinterpret_cast<float4*>(&ov[4 * tid]) = r;
+        __syncthreads();
+        acc4[tid] = make_float4(accp.x, accp.y, accp.z, accp.w);
+        __syncthreads();
+        const float4 rp = group_sum();
+        if (tid < NC) *reinterpret_cast<float4*>(&ovp[4 * tid]) = rp;
         lds_fwht<G>(ov);
-        for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
-            const float y = ov[idx] * kTqScale * a.vsign[idx % HD];
-            if (ro)
-                ro[idx] = y;
-            else
-                out[idx] = f2h_bits(y);
-        }
-    } else if (ro) {
-        if (tid < NC) *reinterpret_cast<float4*>(ro + 4 * tid) = r;
+        for (int idx = tid; idx < G * HD; idx += kAttnThreads)
+            out[idx] = f2h_bits(ov[idx] * kTqScale * a.vsign[idx % HD] + ovp[idx]);
     } else if (tid < NC) {
         *reinterpret_cast<uint2*>(out + 4 * tid) =
             make_uint2((uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16),
@@ -399,8 +402,13 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int kvh, int b)
 // The block stores its record, counts itself in a.counts for its (sequence,
 // kv head), and the last of the nsplit blocks merges the records
 // (merge_last) and resets the counter to zero for the next launch.
-template <int G, int HD, bool PIPE>
-__device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b) {
+// range, slot, nrec, ntq: the part of the context (attn_range), this
+// block's record among the nrec records of its (sequence, kv head), and the
+// rotated records among them (tiered pages: the TurboQuant blocks' [0, ntq),
+// merged by merge_last<G, 128, true> when TIER).
+template <int G, int HD, bool PIPE, bool TIER = false>
+__device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b,
+                                    int range = 0, int slot = -1, int nrec = 0, int ntq = 0) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, t = lane & 15;
@@ -408,13 +416,17 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
 
     // The context length and this wavefront's block-table entries (page
     // p0 + wave + 4i in lane i) are requested together: one round trip.
+    if (slot < 0) {
+        slot = split;
+        nrec = nsplit;
+    }
     int ctx, pg0;
-    attn_range(a, b, ctx, pg0);
+    attn_range(a, b, range, ctx, pg0);
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
     const int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
-                            ? a.block_table[(size_t)b * a.max_blocks + pg0 + my_page]
+                            ? (range == 2 ? a.hot_table : a.block_table)[(size_t)b * a.max_blocks + pg0 + my_page]
                             : 0;
     // q as the B operand (column = head t, k = 8g + j of each 32-dim step).
     // Columns t >= G repeat head G - 1 (loads without a branch, so all of q
@@ -486,8 +498,8 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
         my[MO + t] = m;
         my[LO + t] = lsum;
     }
-    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    merge_waves_store<G, HD, true>(parts + (size_t)split * REC, lds);
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nrec * REC;
+    merge_waves_store<G, HD, true>(parts + (size_t)slot * REC, lds);
     // every thread's record stores are complete before the block counts itself
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -495,11 +507,11 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
     if (threadIdx.x == 0) {
         unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
         const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = prev == (unsigned)nsplit - 1u;
+        last = prev == (unsigned)nrec - 1u;
         if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (last) merge_last<G, HD>(a, nsplit, kvh, b);
+    if (last) merge_last<G, HD, TIER>(a, nrec, ntq, kvh, b);
 }
 
 // PIPE: more than one page pair per wavefront (pps > 8), two pairs in
@@ -697,17 +709,22 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
 // of the (sequence, kv head) merges the records and rotates the value sums
 // back (merge_last<G, 128, true>).
 template <int G, bool PIPE>
-__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
+__device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b,
+                                   int range = 0, int slot = -1, int nrec = 0, int ntq = 0) {
     constexpr int HD = 128, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
     __shared__ float qrot[G * HD];
     __shared__ uint32_t cbk[24];
 
+    if (slot < 0) {
+        slot = split;
+        nrec = nsplit;
+        ntq = nsplit;  // every record rotated
+    }
     int ctx, pg0;
-    attn_range(a, b, ctx, pg0);
+    attn_range(a, b, range, ctx, pg0);
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
@@ -798,21 +815,26 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsp
         my[MO + t] = m;
         my[LO + t] = lsum;
     }
-    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    merge_waves_store<G, HD, true>(parts + (size_t)split * REC, lds);
+    float* parts = a.part + ((size_t)b * a.hkv + kvh) * nrec * REC;
+    merge_waves_store<G, HD, true>(parts + (size_t)slot * REC, lds);
     // as attn_f16_run: the record is stored before the block counts itself;
-    // the last of the nsplit blocks merges, rotates back and resets the counter
+    // the last of the nrec blocks merges, rotates back and resets the counter
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __shared__ int last;
     if (threadIdx.x == 0) {
         unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
         const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = prev == (unsigned)nsplit - 1u;
+        last = prev == (unsigned)nrec - 1u;
         if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (last) merge_last<G, HD, true>(a, nsplit, kvh, b);
+    if (last) merge_last<G, HD, true>(a, nrec, ntq, kvh, b);
+}
+
+template <int G, bool PIPE>
+__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
+    attn_tq_run<G, PIPE>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // ----------------------------------------------------- TurboQuant encode --
@@ -1004,61 +1026,62 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     }
 }
 
-// Tiered pages, the page that leaves the fp16 window this step: when the
-// position p just written completes page q = (p - H + 1) / 16 - 1 beyond
-// the window (p - H + 1 a positive multiple of 16), its fp16 K and V (hot
-// page hot_bt[q]) are encoded into the TurboQuant page tq_bt[q].  Block
-// (b, kv * hkv + h), one wavefront: the 16 vectors of one head and kind.
-// Every other step the blocks leave at once.
-__global__ __launch_bounds__(64) void k_tq_compress(const int32_t* pos, int hot_window, int hkv,
-                                                    const int32_t* hot_bt, const int32_t* tq_bt, int max_blocks,
-                                                    const uint16_t* kpool, const uint16_t* vpool, const float* ksign,
-                                                    const float* vsign, uint8_t* kc4, uint8_t* kc3, uint16_t* kn,
-                                                    uint8_t* vc4, uint8_t* vc3, uint16_t* vn) {
+// Tiered pages, the page that leaves the fp16 window at this step: when
+// the position p being written completes page q = (p - H + 1) / 16 - 1
+// outside the window (p - H + 1 a positive multiple of 16), its fp16 K or V
+// (ring page hot_table[q]) is encoded into the TurboQuant page
+// block_table[q]: block `part` of the four of each kind encodes slots
+// 4 part .. 4 part + 3 on its first wavefront.  On the other steps the block
+// leaves at once.  The attention blocks of the same launch
+// read page q as fp16 and the TurboQuant pages before it only.
+constexpr int kCompressParts = 4;
+__device__ inline void tq_compress_block(const AttnArgs& a, int kv, int part, int h, int b) {
     __shared__ uint8_t codes[128];
-    const int b = blockIdx.x, kv = blockIdx.y / hkv, h = blockIdx.y % hkv, lane = threadIdx.x;
-    const int done = pos[b] - hot_window + 1;
-    if (done < kPage || done % kPage) return;
+    const int lane = threadIdx.x & 63;
+    const int done = a.pos[b] - a.hot_window + 1;
+    if (threadIdx.x >= kWave || done < kPage || done % kPage) return;
     const int q = done / kPage - 1;
-    const size_t hot = (size_t)hot_bt[(size_t)b * max_blocks + q] * hkv + h;
-    const size_t dst0 = ((size_t)tq_bt[(size_t)b * max_blocks + q] * hkv + h) * kPage;
-    for (int slot = 0; slot < kPage; ++slot) {
+    const size_t hot = (size_t)a.hot_table[(size_t)b * a.max_blocks + q] * a.hkv + h;
+    const size_t dst0 = ((size_t)a.block_table[(size_t)b * a.max_blocks + q] * a.hkv + h) * kPage;
+    // the TurboQuant pools, written only here
+    uint8_t* c4 = const_cast<uint8_t*>(kv ? a.vc4 : a.kc4);
+    uint8_t* c3 = const_cast<uint8_t*>(kv ? a.vc3 : a.kc3);
+    uint16_t* nr = const_cast<uint16_t*>(kv ? a.vn : a.kn);
+    const float* sign = kv ? a.vsign : a.ksign;
+    for (int slot = part * (kPage / kCompressParts); slot < (part + 1) * (kPage / kCompressParts); ++slot) {
         // the previous slot's reads of codes[] come before this slot's writes
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float x0, x1;
         if (kv == 0) {  // K pages are token-major [16][128]
-            const uint16_t* src = kpool + (hot * kPage + slot) * kTqD;
+            const uint16_t* src = a.kpool + (hot * kPage + slot) * kTqD;
             x0 = h2f_bits(src[lane]);
             x1 = h2f_bits(src[lane + 64]);
         } else {        // V pages are dimension-major [128][16]
-            const uint16_t* src = vpool + hot * kPage * kTqD;
+            const uint16_t* src = a.vpool + hot * kPage * kTqD;
             x0 = h2f_bits(src[(size_t)lane * kPage + slot]);
             x1 = h2f_bits(src[(size_t)(lane + 64) * kPage + slot]);
         }
         const size_t dst = dst0 + slot;
-        if (kv == 0)
-            tq_encode_vals(x0, x1, ksign, kc4 + dst * 32, kc3 + dst * 24, kn + dst, codes);
-        else
-            tq_encode_vals(x0, x1, vsign, vc4 + dst * 32, vc3 + dst * 24, vn + dst, codes);
+        tq_encode_vals(x0, x1, sign, c4 + dst * 32, c3 + dst * 24, nr + dst, codes);
     }
 }
 
-// Attention over tiered pages, the last step: the normalized outputs of the
-// compressed part (oa, (Ma, La)) and of the fp16 window (ob, (Mb, Lb)) of
-// each (sequence, head) combined with weights L exp(M - max M).
-__global__ __launch_bounds__(128) void k_attn_merge2(const float* oa, const float* mla, const float* ob,
-                                                     const float* mlb, uint16_t* out, int hd) {
-    const size_t bh = blockIdx.x;
-    const float Ma = mla[2 * bh], La = mla[2 * bh + 1], Mb = mlb[2 * bh], Lb = mlb[2 * bh + 1];
-    const float M = fmaxf(La > 0.0f ? Ma : -__builtin_inff(), Lb > 0.0f ? Mb : -__builtin_inff());
-    const float wa = La > 0.0f ? La * __expf(Ma - M) : 0.0f, wb = Lb > 0.0f ? Lb * __expf(Mb - M) : 0.0f;
-    const float den = wa + wb;
-    for (int d = threadIdx.x; d < hd; d += 128) {
-        const float va = wa > 0.0f ? oa[bh * hd + d] : 0.0f, vb = wb > 0.0f ? ob[bh * hd + d] : 0.0f;
-        out[bh * hd + d] = f2h_bits(den > 0.0f ? (wa * va + wb * vb) / den : 0.0f);
-    }
+// Tiered pages in one launch: blocks x < ntq are TurboQuant splits of the
+// compressed pages, the next nf fp16 splits of the window (the last of these
+// ntq + nf blocks of a (sequence, kv head) merges both kinds of record), and
+// the last 2 kCompressParts compress the page leaving the window (K, V).
+template <int G, bool PT, bool PF>
+__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tiered(AttnArgs a, int ntq, int ppt, int nf, int ppf) {
+    const int x = blockIdx.x;
+    if (x < ntq)
+        attn_tq_run<G, PT>(a, ntq, ppt, x, blockIdx.y, blockIdx.z, 1, x, ntq + nf, ntq);
+    else if (x < ntq + nf)
+        attn_f16_run<G, 128, PF, true>(a, nf, ppf, x - ntq, blockIdx.y, blockIdx.z, 2, x, ntq + nf, ntq);
+    else
+        tq_compress_block(a, (x - ntq - nf) / kCompressParts, (x - ntq - nf) % kCompressParts, blockIdx.y,
+                          blockIdx.z);
 }
 
 // Context fill of tiered pages: positions [cold, ctx) of raw [ctx][hkv][hd]
@@ -1085,21 +1108,6 @@ __global__ __launch_bounds__(256) void k_round_f16(float* x, size_t n) {
 }
 
 }  // namespace
-
-hipError_t tq_compress_launch(const int32_t* pos, int hot_window, int batch, int hkv, const int32_t* hot_bt,
-                              const int32_t* tq_bt, int max_blocks, const uint16_t* kpool, const uint16_t* vpool,
-                              const float* ksign, const float* vsign, uint8_t* kc4, uint8_t* kc3, uint16_t* kn,
-                              uint8_t* vc4, uint8_t* vc3, uint16_t* vn, hipStream_t st) {
-    hipLaunchKernelGGL(k_tq_compress, dim3(batch, 2 * hkv), dim3(64), 0, st, pos, hot_window, hkv, hot_bt, tq_bt,
-                       max_blocks, kpool, vpool, ksign, vsign, kc4, kc3, kn, vc4, vc3, vn);
-    return hipGetLastError();
-}
-
-hipError_t attn_merge2_launch(const float* oa, const float* mla, const float* ob, const float* mlb, uint16_t* out,
-                              int batch, int hq, int hd, hipStream_t st) {
-    hipLaunchKernelGGL(k_attn_merge2, dim3(batch * hq), dim3(128), 0, st, oa, mla, ob, mlb, out, hd);
-    return hipGetLastError();
-}
 
 hipError_t put_hot_launch(const float* raw, int ctx, int cold, int hkv, int hd, int b, const int32_t* hot_bt,
                           int max_blocks, uint16_t* kpool, uint16_t* vpool, int kv, hipStream_t st) {
@@ -1220,6 +1228,59 @@ hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st) {
     NX_ATTN_CASE(4)
     NX_ATTN_CASE(8)
 #undef NX_ATTN_CASE
+    return hipErrorInvalidValue;
+}
+
+// Tiered split plan: about one block per CU over all (kv head, sequence)
+// pairs, shared between the compressed pages (TurboQuant, at most
+// (max_ctx - hot_window) / 16 + 1 pages) and the window (hot_window / 16 + 1
+// pages) in proportion to their cost, a TurboQuant page taking about 0.8 of
+// an fp16 page's time.
+struct TierPlan {
+    int ntq, ppt, nf, ppf;
+};
+TierPlan plan_tiered(int max_ctx, int hot_window, int hkv, int batch) {
+    const int pt = max(1, (max_ctx - hot_window) / kPage + 1), pf = hot_window / kPage + 2;
+    const int S = min(max(2, (device_cus() + hkv * batch - 1) / (hkv * batch)), kMaxSplits);
+    const double ct = 0.8 * pt, cf = pf;
+    const int nt0 = min(max(1, (int)(S * ct / (ct + cf) + 0.5)), S - 1);
+    TierPlan p;
+    p.ppt = min(max((pt + nt0 - 1) / nt0, 1), kPagesPerSplitMax);
+    p.ntq = (pt + p.ppt - 1) / p.ppt;
+    const int nf0 = max(1, S - p.ntq);
+    p.ppf = min(max((pf + nf0 - 1) / nf0, 1), kPagesPerSplitMax);
+    p.nf = (pf + p.ppf - 1) / p.ppf;
+    return p;
+}
+
+size_t attn_tiered_workspace_bytes(int batch, int hq, int hkv) {
+    return sizeof(float) * (size_t)batch * hkv * kMaxSplits * rec_floats(hq / hkv, 128);
+}
+
+hipError_t attn_tiered_launch(const AttnArgs& a, hipStream_t st) {
+    if (!a.counts || !a.part || a.hd != 128 || a.hot_window < kPage) return hipErrorInvalidValue;
+    const TierPlan p = plan_tiered(a.max_ctx, a.hot_window, a.hkv, a.batch);
+    if (p.ntq + p.nf > kMaxSplits) return hipErrorInvalidValue;
+    const dim3 grid(p.ntq + p.nf + 2 * kCompressParts, a.hkv, a.batch);
+    const int G = a.hq / a.hkv;
+    const bool pt = p.ppt > kPagesPerSplitMin, pf = p.ppf > kPagesPerSplitMin;
+#define NX_TIER_CASE(GG, PT, PF)                                                                  \
+    if (G == GG && pt == PT && pf == PF) {                                                        \
+        hipLaunchKernelGGL((k_attn_tiered<GG, PT, PF>), grid, dim3(kAttnThreads), 0, st, a, p.ntq, \
+                           p.ppt, p.nf, p.ppf);                                                   \
+        return hipGetLastError();                                                                 \
+    }
+#define NX_TIER_G(GG)               \
+    NX_TIER_CASE(GG, true, true)    \
+    NX_TIER_CASE(GG, true, false)   \
+    NX_TIER_CASE(GG, false, true)   \
+    NX_TIER_CASE(GG, false, false)
+    NX_TIER_G(1)
+    NX_TIER_G(2)
+    NX_TIER_G(4)
+    NX_TIER_G(8)
+#undef NX_TIER_G
+#undef NX_TIER_CASE
     return hipErrorInvalidValue;
 }
 

@@ -97,14 +97,13 @@ struct AttnArgs {
     // counts[(b * hkv + kvh) * kAttnCountStride]; zero before a launch, and
     // the launch leaves them at zero
     unsigned* counts;
-    // tiered pages: hot_window > 0 selects range 1 (the compressed pages
-    // [0, cold)) or range 2 (the fp16 window [cold, ctx), its pages from
-    // entry cold / 16 of the block table on), cold = 16 floor((ctx -
-    // hot_window) / 16); rec_o (non-null) receives the normalized O fp32
-    // [batch][hq][hd] and rec_ml (M, L) [batch][hq][2] instead of out16
-    int hot_window, range;
-    float* rec_o;
-    float* rec_ml;
+    // tiered pages (attn_tiered_launch): positions [0, cold) are read from
+    // the TurboQuant pages through block_table, [cold, ctx) from the fp16
+    // pages through hot_table (entries from cold / 16 on), cold = 16
+    // floor((ctx - 1 - hot_window) / 16) clamped at 0; the same launch
+    // compresses the page that leaves the window at this step
+    int hot_window;
+    const int32_t* hot_table;
 };
 constexpr int kAttnCountStride = 64;  // counters 256 bytes apart
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
@@ -122,16 +121,12 @@ hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st);
 // one sequence at positions p0 + t, block_table = that sequence's row,
 // out16 [P][hq][hd]; row t attends to positions <= p0 + t.  No workspace.
 hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st);
-// Tiered pages (hot fp16 window of hot_window tokens, older pages in
-// TurboQuant): encode the page that left the window this step (see the
-// kernel); merge the two attention parts into out16; fill the window's
-// pages from raw fp32 [ctx][hkv][hd]; round fp32 values through fp16.
-hipError_t tq_compress_launch(const int32_t* pos, int hot_window, int batch, int hkv, const int32_t* hot_bt,
-                              const int32_t* tq_bt, int max_blocks, const uint16_t* kpool, const uint16_t* vpool,
-                              const float* ksign, const float* vsign, uint8_t* kc4, uint8_t* kc3, uint16_t* kn,
-                              uint8_t* vc4, uint8_t* vc3, uint16_t* vn, hipStream_t st);
-hipError_t attn_merge2_launch(const float* oa, const float* mla, const float* ob, const float* mlb, uint16_t* out,
-                              int batch, int hq, int hd, hipStream_t st);
+// Attention over tiered pages in one launch, which also compresses the page
+// leaving the window (max_ctx bounds ctx_lens).
+hipError_t attn_tiered_launch(const AttnArgs& a, hipStream_t st);
+size_t attn_tiered_workspace_bytes(int batch, int hq, int hkv);
+// Tiered pages: fill the window's pages from raw fp32 [ctx][hkv][hd]; round
+// fp32 values through fp16.
 hipError_t put_hot_launch(const float* raw, int ctx, int cold, int hkv, int hd, int b, const int32_t* hot_bt,
                           int max_blocks, uint16_t* kpool, uint16_t* vpool, int kv, hipStream_t st);
 hipError_t round_f16_launch(float* x, size_t n, hipStream_t st);

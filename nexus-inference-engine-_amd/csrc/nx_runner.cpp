@@ -82,12 +82,9 @@ struct nx_model {
     float* attn_part = nullptr;
     // tiered pages: the fp16 window's ring of hot_pages pages per sequence
     // (hot_bt[b][p] = b * hot_pages + p % hot_pages, the same max_blocks
-    // stride as block_table) and the two attention records (compressed
-    // part, window) before their merge
+    // stride as block_table)
     int hot_pages = 0;
     int32_t* hot_bt = nullptr;
-    float* rec_o[2] = {nullptr, nullptr};
-    float* rec_ml[2] = {nullptr, nullptr};
     unsigned* attn_counts = nullptr;  // split-completion counters of the fp16 attention
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
@@ -203,9 +200,9 @@ nx_status enqueue_sample(nx_model* m, int b0, int nb) {
 }
 
 // Attention of layer ly for every sequence (q in m->q, output m->att16).
-// Tiered pages: the TurboQuant kernel over the compressed pages and the
-// fp16 kernel over the window, each leaving a normalized record, and their
-// merge.
+// Tiered pages: one launch whose blocks read either the compressed pages
+// (TurboQuant) or the fp16 window, merged by the last block, and compress the
+// page that leaves the window at this step.
 hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
     const nx_model_config& c = m->c;
     nx::AttnArgs at{};
@@ -235,20 +232,8 @@ hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
     if (c.kv_kind == 0) return nx::attn_f16_launch(at, st);
     if (c.kv_kind == 1) return nx::attn_tq_launch(at, st);
     at.hot_window = c.hot_window;
-    at.range = 1;
-    at.rec_o = m->rec_o[0];
-    at.rec_ml = m->rec_ml[0];
-    hipError_t e = nx::attn_tq_launch(at, st);
-    if (e != hipSuccess) return e;
-    at.range = 2;
-    at.block_table = m->hot_bt;
-    at.max_ctx = m->hot_pages * nx::kPage;
-    at.rec_o = m->rec_o[1];
-    at.rec_ml = m->rec_ml[1];
-    e = nx::attn_f16_launch(at, st);
-    if (e != hipSuccess) return e;
-    return nx::attn_merge2_launch(m->rec_o[0], m->rec_ml[0], m->rec_o[1], m->rec_ml[1], m->att16, c.batch,
-                                  c.n_heads, c.head_dim, st);
+    at.hot_table = m->hot_bt;
+    return nx::attn_tiered_launch(at, st);
 }
 
 // KV bytes one attention pass reads for sequences at hpos (TurboQuant: 58
@@ -264,7 +249,7 @@ double kv_bytes(const nx_model* m) {
         } else if (c.kv_kind == 1) {
             kv += ctx * tq;
         } else {
-            const int cold = nx::kPage * std::max(0, (ctx - c.hot_window) / nx::kPage);
+            const int cold = nx::kPage * std::max(0, (ctx - 1 - c.hot_window) / nx::kPage);  // attention's boundary
             kv += cold * tq + (ctx - cold) * f16;
         }
     }
@@ -313,10 +298,6 @@ nx_status enqueue_step(nx_model* m) {
             NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr, ly.kc4,
                                               ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table, m->pos,
                                               m->max_blocks, st));
-        if (c.kv_kind == 2)  // the page that left the fp16 window, if any, into TurboQuant
-            NX_LAUNCH(m, nx::tq_compress_launch(m->pos, c.hot_window, B, c.n_kv_heads, m->hot_bt, m->block_table,
-                                                m->max_blocks, ly.kpool, ly.vpool, ly.ksign, ly.vsign, ly.kc4,
-                                                ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, st));
         // attention
         NX_LAUNCH(m, attention_launch(m, ly, st));
         // output projection + residual
@@ -612,14 +593,13 @@ nx_status create_impl(nx_model* m, bool synthetic) {
             for (int p = 0; p < m->max_blocks; ++p) ring[(size_t)b * m->max_blocks + p] = b * m->hot_pages + p % m->hot_pages;
         NX_TRY(dalloc(m, &m->hot_bt, ring.size()));
         NX_HIP(m->ctx, hipMemcpyAsync(m->hot_bt, ring.data(), ring.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
-        for (int i = 0; i < 2; ++i) {
-            NX_TRY(dalloc(m, &m->rec_o[i], (size_t)B * m->qdim));
-            NX_TRY(dalloc(m, &m->rec_ml[i], (size_t)B * c.n_heads * 2));
-        }
         NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     }
     NX_TRY(dalloc(m, &m->attn_part,
-                  nx::attn_workspace_bytes(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq) / 4 + 1));
+                  std::max(nx::attn_workspace_bytes(B, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq),
+                           c.kv_kind == 2 ? nx::attn_tiered_workspace_bytes(B, c.n_heads, c.n_kv_heads) : 0) /
+                          4 +
+                      1));
     {
         std::vector<int32_t> minus1(B, -1);
         NX_HIP(m->ctx, hipMemcpyAsync(m->pos, minus1.data(), (size_t)B * 4, hipMemcpyHostToDevice, m->ctx->stream));
@@ -644,6 +624,8 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.kv_kind != 0 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
     if (c.kv_kind == 2 && (c.hot_window < nx::kPage || c.hot_window % nx::kPage || c.hot_window >= c.max_seq))
         return fail(ctx, NX_ERR_INVALID, "hot_window must be a positive multiple of 16 below max_seq");
+    if (c.kv_kind == 2 && c.max_seq > nx::attn_max_ctx() / 2)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the tiered attention limit");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
     if (c.max_seq > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the attention limit");
     if (c.d_model > 14336 || c.ffn > 14336 || c.n_heads * c.head_dim > 14336)

@@ -585,7 +585,7 @@ void nxo_tiered_append(const float* k, const float* v, int hkv, const float* ksi
 }
 
 int nxo_tiered_cold(int ctx, int hot_window) {
-    const int c = ctx - hot_window;
+    const int c = ctx - 1 - hot_window;
     return c > 0 ? NXO_PAGE * (c / NXO_PAGE) : 0;
 }
 

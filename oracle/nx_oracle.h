@@ -165,9 +165,11 @@ void nxo_attn_decode_paged_tq(const float* q,
  * window).  The restatement keeps both forms of every position: append
  * writes the fp16 page and the TurboQuant codes of the fp16 values (the
  * codes a later compression of that page produces), and attention reads
- * position t < cold from the codes, t >= cold from fp16, cold =
- * 16 floor((ctx - hot_window) / 16) clamped at 0, in one softmax (the
- * mixed-tier gather of get_vectors :161-230). */
+ * position t < cold from the codes, t >= cold from fp16, in one softmax
+ * (the mixed-tier gather of get_vectors :161-230).  cold = 16 floor((ctx -
+ * 1 - hot_window) / 16) clamped at 0: the pages compressed before the step
+ * that attends over ctx positions (a page is compressed by the step whose
+ * position completes it outside the window, after that step's attention). */
 void nxo_tiered_append(const float* k, const float* v, int hkv, const float* ksigns, const float* vsigns,
                        const float* b4, const float* b3, uint16_t* kpool, uint16_t* vpool, uint8_t* kc4,
                        uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,

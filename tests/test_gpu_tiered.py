@@ -18,13 +18,22 @@ pytestmark = pytest.mark.gpu
 TQ_TINY = dict(TINY, n_heads=4, n_kv_heads=2, head_dim=128, d_model=512)
 
 
+# Positions produced by the decode are compressed from K and V that the GPU
+# and the oracle compute with different fp32 summation orders, so their fp16
+# values can differ in the last bit and a TurboQuant code can land one level
+# apart; one such code moves a logit by up to about 1e-2.  Tokens may differ
+# only where the oracle's top-two margin is below this bound (the
+# compressor's codes for identical inputs are checked bit-exact below).
+TQ_TIE = 2e-2
+
+
 @pytest.mark.parametrize("batch,H", [(1, 16), (2, 48)])
 def test_tiered_greedy_parity(ctx, batch, H):
     """A 12-token prompt and 100 greedy tokens: pages leave the window and
     are compressed every 16 steps from position H + 15 on."""
     cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, seed=0x7E1 + H)
     got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
-    assert_greedy_parity(got, want, margins)
+    assert_greedy_parity(got, want, margins, tie=TQ_TIE)
 
 
 def _oracle_steps(om, start, steps):

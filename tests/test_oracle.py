@@ -447,14 +447,15 @@ def test_tq_attention_close_to_fp16_attention():
 
 
 def test_tiered_cold_boundary():
-    """Pages wholly before the window of the last H positions are cold:
-    cold = 16 floor((ctx - H) / 16), 0 while ctx <= H + 15."""
-    for ctx, H, want in [(1, 16, 0), (16, 16, 0), (31, 16, 0), (32, 16, 16), (47, 16, 16), (48, 16, 32),
-                         (300, 64, 224), (4096, 4096, 0), (32768, 4096, 28672), (32767, 4096, 28656)]:
+    """Attention over ctx positions reads as compressed the pages wholly
+    before the window of the H positions preceding the current one:
+    cold = 16 floor((ctx - 1 - H) / 16), 0 while ctx <= H + 16."""
+    for ctx, H, want in [(1, 16, 0), (16, 16, 0), (32, 16, 0), (33, 16, 16), (48, 16, 16), (49, 16, 32),
+                         (300, 64, 224), (4096, 4096, 0), (32768, 4096, 28656), (32769, 4096, 28672)]:
         assert L.nxo_tiered_cold(ctx, H) == want, (ctx, H)
 
 
-@pytest.mark.parametrize("ctx,H", [(100, 32), (40, 16), (20, 48), (16, 16)])
+@pytest.mark.parametrize("ctx,H", [(100, 32), (41, 16), (20, 48), (16, 16)])
 def test_tiered_attention_vs_fp64(ctx, H):
     """Tiered pages against an independent float64 restatement: positions
     before cold read as the TurboQuant round trip of their fp16 values,
@@ -493,7 +494,7 @@ def test_tiered_attention_vs_fp64(ctx, H):
                     Kf[b, :cold, h], Vf[b, :cold, h] = rk, rv
         return np.stack([_attn_fp64(q[b].astype(np.float64), Kf[b], Vf[b], hq, hkv, 128) for b in range(B)])
 
-    cold = max(0, (ctx - H) // 16 * 16)
+    cold = max(0, (ctx - 1 - H) // 16 * 16)
     want = want_for(cold)
     e = rel_err(out, want)
     assert e < 1e-5, e
