@@ -85,6 +85,35 @@ def test_tiered_filled_context_and_compressor(ctx):
         assert rel_err(glog, logits) < 1e-3
 
 
+@pytest.mark.parametrize("hq,hkv,H,ctx_len", [(8, 2, 128, 700), (8, 1, 32, 1000), (4, 4, 256, 260)])
+def test_tiered_filled_context_group_sizes(ctx, hq, hkv, H, ctx_len):
+    """Query groups of 4 and 8 heads, a single kv head, windows of 32 to 256
+    positions and a context just past the first compressed page: 20 decode
+    steps from a filled context give the oracle's tokens (and logits within
+    1e-3 when the tokens agree); the compressed pages stay bit-exact."""
+    cfg = dict(TINY, n_heads=hq, n_kv_heads=hkv, head_dim=128, d_model=hq * 128, max_seq=1024 + 64, batch=1,
+               kv_kind=2, hot_window=H, seed=0x6000 + hq * 16 + hkv + H)
+    steps = 20
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(ctx_len, 4)
+    om = oracle.Model(**cfg)
+    om.fill_context(ctx_len, 4)
+    start = gm.pending()
+    got = gm.decode(steps)
+    glog = gm.logits()
+    cold = 16 * max(0, (ctx_len - H) // 16)
+    for p in list(range(0, cold, 37)) + ([cold - 1] if cold else []):
+        for kv in range(2):
+            form, g = gm.kv_read(cfg["n_layers"] - 1, 0, p, kv)
+            assert form == 1 and np.array_equal(g, om.kv_read(cfg["n_layers"] - 1, 0, p, kv, 1)), (p, kv)
+    gm.close()
+    want, margins, logits = _oracle_steps(om, start, steps)
+    om.close()
+    assert_greedy_parity(got, want, margins)
+    if np.array_equal(got, want):
+        assert rel_err(glog, logits) < 1e-3
+
+
 def test_tiered_window_covering_context_matches_fp16_pages(ctx):
     """A window larger than the context keeps every position in fp16: the
     tiered path (an empty compressed part, the fp16 kernel's record and the
