@@ -23,7 +23,7 @@ Also reported:
   prefill       batched prefill of a 2048-token prompt on a fresh model of
                 the same shape (dense models), wall clock around the call;
                 its dominant kernel, the gate/up int4-g32 GEMM of a
-                512-token chunk, against the 2.5 PFLOP/s dense fp16 peak.
+                2048-token chunk, against the 2.5 PFLOP/s dense fp16 peak.
 
 Other workloads: --model mixtral-8x7b (top-2 of 8 experts of 14336, vocab
 32000; the roofline kernel is then the routed gate/up expert GEMV), --kv tq
@@ -188,7 +188,7 @@ def tiering_bench(ctx, base: dict, ctx_len: int = 32768, hot_window: int = 4096,
 
 def prefill_bench(ctx, base: dict, P: int = 2048) -> dict:
     """Batched prefill throughput of a P-token prompt (fresh model, positions
-    from 0) and the TFLOP/s of its gate/up GEMM at the 512-token chunk."""
+    from 0) and the TFLOP/s of its gate/up GEMM at the 2048-token chunk."""
     import ctypes as C
 
     import numpy as np
@@ -210,7 +210,7 @@ def prefill_bench(ctx, base: dict, P: int = 2048) -> dict:
     qkv = (base["n_heads"] + 2 * base["n_kv_heads"]) * base["head_dim"]
     w_flops = 2.0 * P * L * d * (qkv + base["n_heads"] * base["head_dim"] + 3 * F)
     att_flops = 4.0 * L * base["n_heads"] * base["head_dim"] * P * (P + 1) / 2
-    M, N, K = 512, 2 * F, d
+    M, N, K = 2048, 2 * F, d
     G = (K + 31) // 32
     bx, bw, bs, by = ctx.alloc(M * K * 2), ctx.alloc(N * G * 16), ctx.alloc(N * G * 2), ctx.alloc(M * N * 4)
     ms = C.c_double()

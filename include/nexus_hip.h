@@ -251,7 +251,7 @@ nx_status nx_model_destroy(nx_model* m);
  * pending as the next input and written to next_tokens [batch] (optional). */
 nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens);
 /* Prefill mode: 1 (default) = batched -- for dense models with fp16 pages
- * each sequence's prompt goes through every layer in chunks of up to 512
+ * each sequence's prompt goes through every layer in chunks of up to 2048
  * tokens as int4-g32 GEMMs on the matrix cores, with causal attention over
  * the pages; 0 = one decode step per prompt token (the reference's
  * HybridModel::prefill loop, hybrid_model.cpp:604-644).  MoE and

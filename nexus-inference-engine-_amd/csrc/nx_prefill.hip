@@ -31,12 +31,15 @@ namespace {
 typedef _Float16 ph8_t __attribute__((ext_vector_type(8)));
 typedef float pf4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kPfBM = 128, kPfBN = 64, kPfBK = 128, kPfThreads = 256;
+constexpr int kPfBM = 128, kPfThreads = 256;
 constexpr int kPfXcds = 8;  // blocks are dealt to the XCDs round-robin by block index
-constexpr int kPfGPS = kPfBK / 32;          // groups per stage
-constexpr int kPfAStride = kPfBK + 8;       // fp16 per LDS row of X: rows 4 banks apart, 16 rows read conflict-free
-constexpr int kPfAChunks = kPfBM * kPfBK / 8 / kPfThreads;  // 16-byte chunks of X per thread per stage
-static_assert(kPfBN * kPfGPS <= kPfThreads, "one code group and one scale per thread");
+// Tile shapes: BN weight rows x BM tokens per block, BK k per stage; the
+// four wavefronts form WM x (4 / WM) sub-tiles.  When 128 x 128 tiles give
+// at least kPfWideTiles blocks (two per CU), each wavefront takes 32 rows and
+// all 128 tokens, so it dequantizes each weight fragment once for 8 token
+// fragments; smaller products keep 64-row tiles (2 x 2 wavefronts) for
+// enough blocks.
+constexpr long kPfWideTiles = 512;
 
 // Code dword (8 nibbles, low nibble = even k) -> fp16 (q - 8) in the k order
 // (0 2 4 6 1 3 5 7): each nibble byte joined with 0x64 is the fp16 1024 + q.
@@ -57,8 +60,14 @@ __device__ inline float lane_xor1(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
 }
 
-template <int EPI>
+template <int EPI, int kPfBN, int kPfBK, int WM>
 __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
+    constexpr int kPfGPS = kPfBK / 32;     // groups per stage
+    constexpr int kPfAStride = kPfBK + 8;  // fp16 per LDS row of X: rows 4 banks apart, 16 rows read conflict-free
+    constexpr int kPfAChunks = kPfBM * kPfBK / 8 / kPfThreads;  // 16-byte chunks of X per thread per stage
+    constexpr int WN = 4 / WM, RM = kPfBM / WM, RN = kPfBN / WN, NI = RM / 16, NJ = RN / 16;
+    static_assert(kPfBN * kPfGPS <= kPfThreads, "one code group and one scale per thread");
+    static_assert(WM * WN == 4 && NI * 16 == RM && NJ * 16 == RN, "wavefront sub-tiles");
     __shared__ __align__(16) uint16_t As[2][kPfBM * kPfAStride];
     __shared__ __align__(16) uint32_t Bs[2][kPfBN * kPfGPS * 4];  // [row][group][4 dwords]
     __shared__ uint16_t Ss[2][kPfBN * kPfGPS];                    // [row][group]
@@ -73,7 +82,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
     const int nb0 = xcd * ntn / kPfXcds, nn = (xcd + 1) * ntn / kPfXcds - nb0;
     if (nn <= 0 || local >= nn * ntm) return;  // the block count is rounded up to 8 x the largest share
     const int n0 = (nb0 + local % nn) * kPfBN, m0 = (local / nn) * kPfBM;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % WM, wn = wave / WM;
     const int M = a.M, N = a.N, K = a.K, G = a.G;
     const int nstage = (G + kPfGPS - 1) / kPfGPS;
 
@@ -110,11 +119,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
         }
     };
 
-    pf4_t acc[4][2], acl[4][2];  // (q - 8) s_hi x and (q - 8) s_lo 2^10 x
+    pf4_t acc[NI][NJ], acl[NI][NJ];  // (q - 8) s_hi x and (q - 8) s_lo 2^10 x
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = acl[i][j] = pf4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = acl[i][j] = pf4_t{0.f, 0.f, 0.f, 0.f};
 
     load(0);
     store(0);
@@ -124,21 +133,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
         if (s + 1 < nstage) load(s + 1);
 #pragma unroll
         for (int g = 0; g < kPfGPS; ++g) {
-            ph8_t af[4];
+            ph8_t af[NI];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
                 af[i] = __builtin_bit_cast(
-                    ph8_t, *reinterpret_cast<const uint4*>(&As[buf][(64 * wm + 16 * i + c) * kPfAStride + 32 * g + 8 * kq]));
+                    ph8_t, *reinterpret_cast<const uint4*>(&As[buf][(RM * wm + 16 * i + c) * kPfAStride + 32 * g + 8 * kq]));
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = 32 * wn + 16 * j + c;
+            for (int j = 0; j < NJ; ++j) {
+                const int row = RN * wn + 16 * j + c;
                 const ph8_t w = pf_codes_to_h8(Bs[buf][(row * kPfGPS + g) * 4 + kq]);
                 const uint16_t sb = Ss[buf][row * kPfGPS + g];
                 const _Float16 shi = __builtin_bit_cast(_Float16, (uint16_t)(sb & 0xFFF0u));
                 const _Float16 slo = (__builtin_bit_cast(_Float16, sb) - shi) * (_Float16)1024.0f;
                 const ph8_t wh = w * shi, wl = w * slo;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < NI; ++i) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], wh, acc[i][j], 0, 0, 0);
                     acl[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], wl, acl[i][j], 0, 0, 0);
                 }
@@ -148,16 +157,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
         __syncthreads();
     }
 
-    // tile (i, j): lane (c, kq) holds weight row n0 + 32 wn + 16 j + c for
-    // tokens m0 + 64 wm + 16 i + 4 kq + r, r < 4
+    // tile (i, j): lane (c, kq) holds weight row n0 + RN wn + 16 j + c for
+    // tokens m0 + RM wm + 16 i + 4 kq + r, r < 4
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + 32 * wn + 16 * j + c;
+    for (int j = 0; j < NJ; ++j) {
+        const int n = n0 + RN * wn + 16 * j + c;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 64 * wm + 16 * i + 4 * kq + r;
+                const int m = m0 + RM * wm + 16 * i + 4 * kq + r;
                 const float v = fmaf(acl[i][j][r], 0.0009765625f, acc[i][j][r]);
                 if (EPI == PF_SWIGLU) {
                     const float u = lane_xor1(v);  // the up row n + 1 sits in lane c + 1
@@ -223,17 +232,27 @@ hipError_t pf_gemm_launch(int epi, const PfGemmArgs& a, hipStream_t st) {
     if (a.M < 1 || a.N < 1 || a.K < 8 || a.K % 8 || a.ldx % 8 || (reinterpret_cast<uintptr_t>(a.x) & 15) ||
         a.G != (a.K + 31) / 32 || (epi == PF_SWIGLU && a.N % 2))
         return hipErrorInvalidValue;
-    const long ntn = (a.N + kPfBN - 1) / kPfBN, ntm = (a.M + kPfBM - 1) / kPfBM;
+    const bool wide = (long)((a.N + 127) / 128) * ((a.M + kPfBM - 1) / kPfBM) >= kPfWideTiles;
+    const long BN = wide ? 128 : 64;
+    const long ntn = (a.N + BN - 1) / BN, ntm = (a.M + kPfBM - 1) / kPfBM;
     const long share = (ntn + kPfXcds - 1) / kPfXcds;  // largest column-tile share of an XCD
     const long blocks = (long)kPfXcds * share * ntm;
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     const dim3 grid((unsigned)blocks);
+#define NX_PF_CASE(E)                                                                                   \
+    case E:                                                                                             \
+        if (wide)                                                                                       \
+            hipLaunchKernelGGL((k_pf_gemm<E, 128, 64, 1>), grid, dim3(kPfThreads), 0, st, a);          \
+        else                                                                                            \
+            hipLaunchKernelGGL((k_pf_gemm<E, 64, 128, 2>), grid, dim3(kPfThreads), 0, st, a);          \
+        break;
     switch (epi) {
-        case PF_F32: hipLaunchKernelGGL(k_pf_gemm<PF_F32>, grid, dim3(kPfThreads), 0, st, a); break;
-        case PF_ACC: hipLaunchKernelGGL(k_pf_gemm<PF_ACC>, grid, dim3(kPfThreads), 0, st, a); break;
-        case PF_SWIGLU: hipLaunchKernelGGL(k_pf_gemm<PF_SWIGLU>, grid, dim3(kPfThreads), 0, st, a); break;
+        NX_PF_CASE(PF_F32)
+        NX_PF_CASE(PF_ACC)
+        NX_PF_CASE(PF_SWIGLU)
         default: return hipErrorInvalidValue;
     }
+#undef NX_PF_CASE
     return hipGetLastError();
 }
 

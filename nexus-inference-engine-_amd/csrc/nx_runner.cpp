@@ -665,7 +665,7 @@ nx_status nx_model_destroy(nx_model* m) {
 
 namespace {
 
-constexpr int kPrefillChunk = 512;  // prompt tokens per pass through the layers
+constexpr int kPrefillChunk = 2048;  // prompt tokens per pass through the layers (each weight read once per pass)
 
 // Device scratch of one prefill call, released on every exit path.
 struct PrefillScratch {

@@ -46,6 +46,18 @@ def test_gemm_accumulates(ctx):
     assert rel_err(got, want) < 1e-3
 
 
+@pytest.mark.parametrize("M,N,K,acc", [(1024, 8192, 512, False), (2048, 4096, 256, True), (1000, 8200, 688, False)])
+def test_gemm_wide_tiles_matches_oracle(ctx, M, N, K, acc):
+    """Products with enough 128 x 128 tiles for two blocks per CU take the
+    wide tile shape (one wavefront per 32 weight rows and all 128 tokens):
+    exact tiles, ragged M and N, a last group of 16 k, the accumulating
+    epilogue."""
+    got, want = _gemm_case(ctx, M, N, K, seed=M + N + K, accumulate=acc)
+    e = rel_err(got, want)
+    print(f"M={M} N={N} K={K} rel_err={e:.2e}")
+    assert e < 1e-3
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 28672, 4096), (64, 4096, 14336)])
 def test_gemm_8b_shapes(ctx, M, N, K):
     """The 8B gate/up and down shapes with 64 tokens."""
@@ -106,11 +118,11 @@ def test_batched_prefill_matches_token_steps(ctx, P):
 
 
 def test_batched_prefill_two_chunks_matches_oracle(ctx):
-    """A 600-token prompt (two chunks of the batched path, the second
+    """A 2100-token prompt (two chunks of the batched path, the second
     attending to pages of the first) and 8 greedy tokens against the
     oracle's token-by-token run; RMSNorm weights not 1."""
-    cfg = dict(TINY, max_seq=1024, seed=0x600, norm_sigma=0.1)
-    script = [("prompt", oracle.prompt_tokens(cfg["seed"], 1, 600, cfg["vocab"])), ("decode", 7)]
+    cfg = dict(TINY, max_seq=2304, seed=0x600, norm_sigma=0.1)
+    script = [("prompt", oracle.prompt_tokens(cfg["seed"], 1, 2100, cfg["vocab"])), ("decode", 7)]
     want, margins = oracle_script(cfg, script)
     got, _, _ = gpu_script(ctx, cfg, script, True)
     assert_greedy_parity(got, want, margins)
