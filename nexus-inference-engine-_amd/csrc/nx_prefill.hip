@@ -171,7 +171,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
                 if (EPI == PF_SWIGLU) {
                     const float u = lane_xor1(v);  // the up row n + 1 sits in lane c + 1
                     if ((c & 1) == 0 && m < M && n + 1 < N)
-                        a.act16[(size_t)m * a.lda + (n >> 1)] = f2h_bits(v / (1.0f + expf(-v)) * u);
+                        // hardware exp and reciprocal (a few ulp in fp32, below the fp16
+                        // rounding of the stored activation)
+                        a.act16[(size_t)m * a.lda + (n >> 1)] =
+                            f2h_bits(v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)) * u);
                 } else if (m < M && n < N) {
                     float* y = a.y32 + (size_t)m * a.ldy + n;
                     *y = EPI == PF_ACC ? *y + v : v;
