@@ -1000,15 +1000,21 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     f4_t o[HD / 16];
 #pragma unroll
     for (int nt = 0; nt < HD / 16; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
-    for (int pa = 0; pa < npages; pa += 2) {
-        const int pb = pa + 1;
-        const int na = min(max(lastpos + 1 - kPage * pa, 0), kPage);
-        const int nb = min(max(lastpos + 1 - kPage * pb, 0), kPage);
-        const int blka = a.block_table[pa];
-        const int blkb = pb < npages ? a.block_table[pb] : blka;
-        PairRaw<HD> r;
-        load_pair<HD>(r, a, blka, na, blkb, nb, kvh, lane);
-        pair_update<HD, true>(r, qh, ql, scale, na, nb, m, lsum, o, lane, kPage * pa, kPage * pb, qpos);
+    // page pairs with the next pair in flight: it is requested unconditionally
+    // (pages past the walk re-read its last page with no valid tokens), so
+    // the wait for the current pair leaves the next one outstanding
+    auto blk_of = [&](int p) { return a.block_table[min(p, npages - 1)]; };
+    auto valid_of = [&](int p) { return p < npages ? min(max(lastpos + 1 - kPage * p, 0), kPage) : 0; };
+    PairRaw<HD> ra, rb;
+    load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
+    for (int pa = 0; pa < npages; pa += 4) {
+        load_pair<HD>(rb, a, blk_of(pa + 2), valid_of(pa + 2), blk_of(pa + 3), valid_of(pa + 3), kvh, lane);
+        pair_update<HD, true>(ra, qh, ql, scale, valid_of(pa), valid_of(pa + 1), m, lsum, o, lane, kPage * pa,
+                              kPage * (pa + 1), qpos);
+        if (pa + 2 >= npages) break;
+        load_pair<HD>(ra, a, blk_of(pa + 4), valid_of(pa + 4), blk_of(pa + 5), valid_of(pa + 5), kvh, lane);
+        pair_update<HD, true>(rb, qh, ql, scale, valid_of(pa + 2), valid_of(pa + 3), m, lsum, o, lane,
+                              kPage * (pa + 2), kPage * (pa + 3), qpos);
     }
     // the query's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);
