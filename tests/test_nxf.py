@@ -226,6 +226,32 @@ def test_model_save_load_round_trip(ctx, tmp_path, moe):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kv_kind,hot", [(1, 0), (2, 32)])
+def test_loaded_model_with_turboquant_and_tiered_pages(ctx, tmp_path, kv_kind, hot):
+    """The run configuration of a load selects the page kind: a model saved
+    as NXF and loaded with TurboQuant or tiered pages (a 32-position window,
+    pages compressed during the 60 decode steps) decodes exactly as the
+    synthetic model it was saved from."""
+    cfg = dict(TINY, n_heads=4, n_kv_heads=2, head_dim=128, d_model=512, kv_kind=kv_kind, hot_window=hot)
+    p = tmp_path / "tq.nxf"
+    prompt = oracle.prompt_tokens(cfg["seed"], 1, 8, cfg["vocab"])
+    a = nexus_amd.Model(ctx, **cfg)
+    a.save_nxf(p)
+    first_a = a.prefill(prompt)
+    toks_a = a.decode(60)
+    log_a = a.logits()
+    a.close()
+    b = nexus_amd.Model.load_nxf(ctx, p, batch=1, max_seq=cfg["max_seq"], kv_kind=kv_kind, seed=cfg["seed"],
+                                 hot_window=hot)
+    first_b = b.prefill(prompt)
+    toks_b = b.decode(60)
+    log_b = b.logits()
+    b.close()
+    assert (first_a == first_b).all() and (toks_a == toks_b).all()
+    assert np.array_equal(log_a, log_b)
+
+
+@pytest.mark.gpu
 def test_loaded_model_matches_oracle_with_norm_weights(ctx, tmp_path):
     """The RMSNorm weights travel through the file into the fused kernels:
     greedy tokens of the loaded model equal the oracle's for the same
