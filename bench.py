@@ -24,13 +24,20 @@ Also reported:
                 the same shape (dense models), wall clock around the call;
                 its dominant kernel, the gate/up int4-g32 GEMM of a
                 2048-token chunk, against the 2.5 PFLOP/s dense fp16 peak.
+  sampling      decode steps with temperature / top-k / top-p sampling
+                inside the step graph, and the oracle sampler's time.
+  tiering       one layer of the same shape at a 32768-token context with
+                fp16, TurboQuant and tiered pages (last 4096 positions
+                fp16): attention time and KV bytes, one-layer step time.
 
 Other workloads: --model mixtral-8x7b (top-2 of 8 experts of 14336, vocab
 32000; the roofline kernel is then the routed gate/up expert GEMV), --kv tq
-(TurboQuant pages), --batch, --ctx.
+(TurboQuant pages), --kv tiered [--hot-window H], --batch, --ctx.
+--decode-only leaves out the GEMV, NXF, prefill and tiering lines.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
-                       [--model llama-8b|mixtral-8x7b] [--kv fp16|tq --ctx C] [--no-cpu]
+                       [--model llama-8b|mixtral-8x7b] [--kv fp16|tq|tiered --ctx C]
+                       [--hot-window H] [--no-cpu] [--decode-only]
 """
 from __future__ import annotations
 
