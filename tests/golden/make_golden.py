@@ -13,6 +13,8 @@ compiled in place from the reference sources:
   kv_fp16.npz        HybridKVCache::f32_to_f16 / f16_to_f32 (model/hybrid_model.h:123-140)
   paged_gather.npz   PagedKVCache::insert_kv + get_keys/get_values (kv/paged_attention.cpp:81-230)
   moe_route.npz      MoERouter::route              (model/moe_router.cpp:55-113), identity gate
+  nxf_ref_files.npz  NXFWriter                     (format/nxf_writer.cpp:93-338): the files of the
+                     NXF format tests, payload regions zeroed, chunk offsets in tensor order
 
 Usage: python tests/golden/make_golden.py
 """
@@ -20,6 +22,7 @@ from __future__ import annotations
 
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 import numpy as np
@@ -129,7 +132,39 @@ def main() -> None:
     for i in range(16):
         R.ref_moe_route(E, topk, E, gate, np.ascontiguousarray(hidden[i]), ids[i], w[i])
     np.savez_compressed(HERE / "moe_route.npz", logits=hidden, ids=ids, weights=w, k=topk)
+
+    write_nxf_files()
     print("golden vectors written to", HERE)
+
+
+def write_nxf_files() -> None:
+    """The reference writer's files for the NXF format cases, with every
+    chunk's payload zeroed (the tests regenerate the payload from the case's
+    tensors) and the file offset of every chunk in tensor order, so the GPU
+    tests can rebuild the reference's exact bytes without the checker."""
+    sys.path.insert(0, str(HERE.parent))
+    sys.path.insert(0, str(ROOT / "nexus-inference-engine-_amd"))
+    from nexus_amd.nxf import NXFReader
+    from nxf_cases import NXF_CASES, REF_TEST_MANIFEST, ref_write
+    out = {}
+    with tempfile.TemporaryDirectory() as td:
+        for case, make in NXF_CASES.items():
+            tensors = make()
+            p = Path(td) / f"{case}.nxf"
+            ref_write(p, REF_TEST_MANIFEST, tensors)
+            data = np.frombuffer(p.read_bytes(), np.uint8).copy()
+            offs = []
+            with NXFReader.open(p) as r:
+                for name, _, _, chunks in tensors:
+                    t = r.get_tensor(name)
+                    for j, (b, _, _) in enumerate(chunks):
+                        off = t.chunks[j].file_offset
+                        assert data[off:off + len(b)].tobytes() == b
+                        data[off:off + len(b)] = 0
+                        offs.append(off)
+            out[f"{case}_masked"] = data
+            out[f"{case}_offsets"] = np.array(offs, np.int64)
+    np.savez_compressed(HERE / "nxf_ref_files.npz", **out)
 
 
 if __name__ == "__main__":

