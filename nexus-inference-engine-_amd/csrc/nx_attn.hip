@@ -31,11 +31,12 @@ struct SplitPlan {
     int nsplit, pps;  // splits per (sequence, kv head), pages per split
 };
 
-// A split is 8 pages (two per wavefront, all in flight at once) until
-// kMaxSplits splits per (sequence, kv head) are reached; longer contexts get
-// more pages per split.  A wavefront keeps its block-table entries one per
-// lane, which bounds a split at 4 * 64 pages: contexts up to
-// kMaxSplits * 256 pages (attn_max_ctx() tokens).
+// A split is kPagesPerSplitMin = 16 pages (two per wavefront of the
+// 8-wavefront block, all in flight at once) until kMaxSplits splits per
+// (sequence, kv head) are reached; longer contexts get more pages per split.
+// A wavefront keeps its block-table entries one per lane, which bounds a
+// split at kAttnWaves * 64 pages: contexts up to kMaxSplits * 512 pages
+// (attn_max_ctx() tokens).
 constexpr int kPagesPerSplitMin = 2 * kAttnWaves;
 constexpr int kPagesPerSplitMax = kAttnWaves * kWave;
 
@@ -396,8 +397,8 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
     }
 }
 
-// One split of one (kv head, sequence): 8 pages (more for very long
-// contexts) shared by the block's four wavefronts, two pages per wavefront
+// One split of one (kv head, sequence): pps pages (16 at the fixed plan)
+// shared by the block's kAttnWaves wavefronts, two pages per wavefront
 // step.  PIPE: more than one page pair per wavefront, two pairs in flight.
 // The block stores its record, counts itself in a.counts for its (sequence,
 // kv head), and the last of the nsplit blocks merges the records
@@ -415,7 +416,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
     __shared__ __align__(16) float lds[kAttnWaves * REC];
 
     // The context length and this wavefront's block-table entries (page
-    // p0 + wave + 4i in lane i) are requested together: one round trip.
+    // p0 + wave + kAttnWaves * i in lane i) are requested together: one round trip.
     if (slot < 0) {
         slot = split;
         nrec = nsplit;
@@ -455,7 +456,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
 
     const int npages = (ctx + kPage - 1) / kPage;
     const int p1 = min(p0 + pps, npages);
-    // pages of this wavefront: p0 + wave + 4i for i < npw, taken in pairs
+    // pages of this wavefront: p0 + wave + kAttnWaves * i for i < npw, taken in pairs
     const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
     auto valid_of = [&](int i) { return i < npw ? min(ctx - (p0 + wave + kAttnWaves * i) * kPage, kPage) : 0; };
     auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
@@ -1041,37 +1042,38 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
 // leaves at once.  The attention blocks of the same launch
 // read page q as fp16 and the TurboQuant pages before it only.
 constexpr int kCompressParts = 4;
+constexpr int kCompressWaves = kPage / kCompressParts;  // one slot per wavefront
+static_assert(kCompressWaves <= kAttnWaves, "a compressing block holds one wavefront per slot of its part");
+// Block `part` of the K (kv 0) or V (kv 1) compression: wavefront w encodes
+// slot part * kCompressWaves + w of the page that left the window.  Each
+// wavefront packs its codes through its own row of LDS scratch; a single row
+// shared by the block would let one wavefront overwrite the codes another
+// is still packing.
 __device__ inline void tq_compress_block(const AttnArgs& a, int kv, int part, int h, int b) {
-    __shared__ uint8_t codes[128];
-    const int lane = threadIdx.x & 63;
+    __shared__ uint8_t codes[kCompressWaves][128];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int done = a.pos[b] - a.hot_window + 1;
-    if (threadIdx.x >= kWave || done < kPage || done % kPage) return;
+    if (w >= kCompressWaves || done < kPage || done % kPage) return;
     const int q = done / kPage - 1;
+    const int slot = part * kCompressWaves + w;
     const size_t hot = (size_t)a.hot_table[(size_t)b * a.max_blocks + q] * a.hkv + h;
-    const size_t dst0 = ((size_t)a.block_table[(size_t)b * a.max_blocks + q] * a.hkv + h) * kPage;
+    const size_t dst = ((size_t)a.block_table[(size_t)b * a.max_blocks + q] * a.hkv + h) * kPage + slot;
     // the TurboQuant pools, written only here
     uint8_t* c4 = const_cast<uint8_t*>(kv ? a.vc4 : a.kc4);
     uint8_t* c3 = const_cast<uint8_t*>(kv ? a.vc3 : a.kc3);
     uint16_t* nr = const_cast<uint16_t*>(kv ? a.vn : a.kn);
     const float* sign = kv ? a.vsign : a.ksign;
-    for (int slot = part * (kPage / kCompressParts); slot < (part + 1) * (kPage / kCompressParts); ++slot) {
-        // the previous slot's reads of codes[] come before this slot's writes
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float x0, x1;
-        if (kv == 0) {  // K pages are token-major [16][128]
-            const uint16_t* src = a.kpool + (hot * kPage + slot) * kTqD;
-            x0 = h2f_bits(src[lane]);
-            x1 = h2f_bits(src[lane + 64]);
-        } else {        // V pages are dimension-major [128][16]
-            const uint16_t* src = a.vpool + hot * kPage * kTqD;
-            x0 = h2f_bits(src[(size_t)lane * kPage + slot]);
-            x1 = h2f_bits(src[(size_t)(lane + 64) * kPage + slot]);
-        }
-        const size_t dst = dst0 + slot;
-        tq_encode_vals(x0, x1, sign, c4 + dst * 32, c3 + dst * 24, nr + dst, codes);
+    float x0, x1;
+    if (kv == 0) {  // K pages are token-major [16][128]
+        const uint16_t* src = a.kpool + (hot * kPage + slot) * kTqD;
+        x0 = h2f_bits(src[lane]);
+        x1 = h2f_bits(src[lane + 64]);
+    } else {        // V pages are dimension-major [128][16]
+        const uint16_t* src = a.vpool + hot * kPage * kTqD;
+        x0 = h2f_bits(src[(size_t)lane * kPage + slot]);
+        x1 = h2f_bits(src[(size_t)(lane + 64) * kPage + slot]);
     }
+    tq_encode_vals(x0, x1, sign, c4 + dst * 32, c3 + dst * 24, nr + dst, codes[w]);
 }
 
 // Tiered pages in one launch: blocks x < ntq are TurboQuant splits of the

@@ -19,6 +19,7 @@
 #include <cerrno>
 #include <cmath>
 #include <cstdarg>
+#include <cstddef>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -151,91 +152,201 @@ std::string manifest_json(const nx_nxf_manifest& m) {
     return s;
 }
 
-struct JsonCursor {
-    const char* p;
-    const char* end;
-    void ws() {
-        while (p < end && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
+// A manifest value: the NXF manifest holds only strings and numbers.
+struct JsonValue {
+    bool is_str = false;
+    std::string str;
+    double num = 0.0;
+};
+
+// Tokenizer of one flat JSON object, {"key": value, ...} with string or
+// number values, into (key, value) pairs in file order.  Standard JSON
+// (RFC 8259) for those two kinds; nested objects, arrays, literals and
+// trailing commas are rejected.
+class FlatJson {
+  public:
+    FlatJson(const char* data, size_t len) : s_(data), n_(len) {}
+
+    bool parse(std::vector<std::pair<std::string, JsonValue>>& out) {
+        skip_ws();
+        if (!eat('{')) return false;
+        skip_ws();
+        if (eat('}')) return at_end();
+        for (;;) {
+            std::pair<std::string, JsonValue> kv;
+            skip_ws();
+            if (!string(kv.first)) return false;
+            skip_ws();
+            if (!eat(':')) return false;
+            skip_ws();
+            if (i_ < n_ && s_[i_] == '"') {
+                kv.second.is_str = true;
+                if (!string(kv.second.str)) return false;
+            } else if (!number(kv.second.num)) {
+                return false;
+            }
+            out.push_back(std::move(kv));
+            skip_ws();
+            if (eat('}')) return at_end();
+            if (!eat(',')) return false;
+        }
     }
-    bool str(std::string& out) {
-        out.clear();
-        if (p >= end || *p != '"') return false;
-        for (++p; p < end && *p != '"'; ++p) {
-            if (*p == '\\' && p + 1 < end) {
-                ++p;
-                out += *p == 'n' ? '\n' : *p == 't' ? '\t' : *p;  // \" \\ \/ and the rest verbatim
-            } else {
-                out += *p;
+
+  private:
+    const char* s_;
+    size_t n_, i_ = 0;
+
+    void skip_ws() {
+        while (i_ < n_ && (s_[i_] == ' ' || s_[i_] == '\t' || s_[i_] == '\n' || s_[i_] == '\r')) ++i_;
+    }
+    bool eat(char c) {
+        if (i_ < n_ && s_[i_] == c) {
+            ++i_;
+            return true;
+        }
+        return false;
+    }
+    bool at_end() {
+        skip_ws();
+        return i_ == n_ || (i_ + 1 == n_ && s_[i_] == '\0');
+    }
+    static int hex(char c) {
+        if (c >= '0' && c <= '9') return c - '0';
+        if (c >= 'a' && c <= 'f') return c - 'a' + 10;
+        if (c >= 'A' && c <= 'F') return c - 'A' + 10;
+        return -1;
+    }
+    // "..." with the JSON escapes; \uXXXX below 0x80 becomes that byte,
+    // other code points are written as UTF-8.
+    bool string(std::string& out) {
+        if (!eat('"')) return false;
+        while (i_ < n_) {
+            const char c = s_[i_++];
+            if (c == '"') return true;
+            if ((unsigned char)c < 0x20) return false;
+            if (c != '\\') {
+                out += c;
+                continue;
+            }
+            if (i_ >= n_) return false;
+            const char e = s_[i_++];
+            switch (e) {
+                case '"': case '\\': case '/': out += e; break;
+                case 'b': out += '\b'; break;
+                case 'f': out += '\f'; break;
+                case 'n': out += '\n'; break;
+                case 'r': out += '\r'; break;
+                case 't': out += '\t'; break;
+                case 'u': {
+                    if (i_ + 4 > n_) return false;
+                    unsigned cp = 0;
+                    for (int k = 0; k < 4; ++k) {
+                        const int h = hex(s_[i_ + k]);
+                        if (h < 0) return false;
+                        cp = cp * 16 + (unsigned)h;
+                    }
+                    i_ += 4;
+                    if (cp < 0x80) {
+                        out += (char)cp;
+                    } else if (cp < 0x800) {
+                        out += (char)(0xC0 | (cp >> 6));
+                        out += (char)(0x80 | (cp & 0x3F));
+                    } else {
+                        out += (char)(0xE0 | (cp >> 12));
+                        out += (char)(0x80 | ((cp >> 6) & 0x3F));
+                        out += (char)(0x80 | (cp & 0x3F));
+                    }
+                    break;
+                }
+                default: return false;
             }
         }
-        if (p >= end) return false;
-        ++p;
-        return true;
+        return false;
     }
-    bool num(double& v) {
-        char buf[64];
-        size_t i = 0;
-        while (p < end && i + 1 < sizeof(buf) &&
-               (*p == '-' || *p == '+' || *p == '.' || *p == 'e' || *p == 'E' || (*p >= '0' && *p <= '9')))
-            buf[i++] = *p++;
-        buf[i] = 0;
-        if (i == 0) return false;
-        v = strtod(buf, nullptr);
+    // -?(0|[1-9][0-9]*)(.[0-9]+)?([eE][+-]?[0-9]+)?, converted by strtod
+    bool number(double& v) {
+        const size_t b = i_;
+        auto digits = [&]() {
+            const size_t d = i_;
+            while (i_ < n_ && s_[i_] >= '0' && s_[i_] <= '9') ++i_;
+            return i_ > d;
+        };
+        eat('-');
+        if (eat('0')) {
+        } else if (!digits()) {
+            return false;
+        }
+        if (eat('.') && !digits()) return false;
+        if (i_ < n_ && (s_[i_] == 'e' || s_[i_] == 'E')) {
+            ++i_;
+            if (!eat('+')) eat('-');
+            if (!digits()) return false;
+        }
+        const std::string text(s_ + b, i_ - b);
+        v = strtod(text.c_str(), nullptr);
         return true;
     }
 };
 
-void copy_str(char* dst, size_t n, const std::string& s) {
-    const size_t k = std::min(n - 1, s.size());
-    memcpy(dst, s.data(), k);
-    dst[k] = 0;
+// The manifest fields (nxf.h:73-96) and the range each must lie in.
+enum class FieldKind { Text, U32, U8, F32 };
+struct ManifestField {
+    const char* key;
+    FieldKind kind;
+    size_t offset;
+    size_t size;  // Text: capacity including the terminator
+};
+#define NX_MF(field, kind) {#field, FieldKind::kind, offsetof(nx_nxf_manifest, field), sizeof(nx_nxf_manifest::field)}
+const ManifestField kManifestFields[] = {
+    NX_MF(architecture, Text), NX_MF(name, Text), NX_MF(num_layers, U32), NX_MF(hidden_dim, U32),
+    NX_MF(num_heads, U32), NX_MF(num_kv_heads, U32), NX_MF(head_dim, U32), NX_MF(vocab_size, U32),
+    NX_MF(max_seq_len, U32), NX_MF(rope_theta, F32), NX_MF(rms_norm_eps, F32), NX_MF(num_experts, U32),
+    NX_MF(num_active_experts, U32), NX_MF(default_codec, U8), NX_MF(default_group_size, U8),
+};
+#undef NX_MF
+
+// Store one value into its field: text into a string field (truncated to
+// the field), a number into a numeric field.  Integer fields take integral
+// values in [0, 2^32 - 1] (bytes: [0, 255]); floats any finite value that
+// rounds to a finite float.  Anything else rejects the manifest.
+bool assign_field(nx_nxf_manifest& m, const ManifestField& f, const JsonValue& v) {
+    char* dst = reinterpret_cast<char*>(&m) + f.offset;
+    if (f.kind == FieldKind::Text) {
+        if (!v.is_str) return false;
+        const size_t k = std::min(f.size - 1, v.str.size());
+        memcpy(dst, v.str.data(), k);
+        dst[k] = 0;
+        return true;
+    }
+    if (v.is_str || !std::isfinite(v.num)) return false;
+    if (f.kind == FieldKind::F32) {
+        const float x = (float)v.num;
+        if (!std::isfinite(x)) return false;
+        memcpy(dst, &x, sizeof(x));
+        return true;
+    }
+    const double hi = f.kind == FieldKind::U8 ? 255.0 : 4294967295.0;
+    if (v.num < 0.0 || v.num > hi || v.num != std::floor(v.num)) return false;
+    if (f.kind == FieldKind::U8) {
+        const uint8_t x = (uint8_t)v.num;
+        memcpy(dst, &x, 1);
+    } else {
+        const uint32_t x = (uint32_t)v.num;
+        memcpy(dst, &x, 4);
+    }
+    return true;
 }
 
+// Manifest JSON -> struct.  Keys outside the format are ignored (as the
+// reference reader does); a known key with the wrong kind or an
+// out-of-range value fails the open.
 bool parse_manifest(const char* data, size_t len, nx_nxf_manifest& m) {
-    JsonCursor c{data, data + len};
-    c.ws();
-    if (c.p >= c.end || *c.p != '{') return false;
-    ++c.p;
-    std::string key, sval;
-    for (;;) {
-        c.ws();
-        if (c.p >= c.end) return false;
-        if (*c.p == '}') return true;
-        if (*c.p == ',') {
-            ++c.p;
-            c.ws();
-            if (c.p < c.end && *c.p == '}') return true;
-        }
-        if (!c.str(key)) return false;
-        c.ws();
-        if (c.p >= c.end || *c.p != ':') return false;
-        ++c.p;
-        c.ws();
-        if (c.p >= c.end) return false;
-        if (*c.p == '"') {
-            if (!c.str(sval)) return false;
-            if (key == "architecture") copy_str(m.architecture, sizeof(m.architecture), sval);
-            else if (key == "name") copy_str(m.name, sizeof(m.name), sval);
-            else if (key == "default_codec") m.default_codec = (uint8_t)atoi(sval.c_str());
-        } else {
-            double v = 0.0;
-            if (!c.num(v)) return false;
-            const uint32_t u = (uint32_t)v;
-            if (key == "num_layers") m.num_layers = u;
-            else if (key == "hidden_dim") m.hidden_dim = u;
-            else if (key == "num_heads") m.num_heads = u;
-            else if (key == "num_kv_heads") m.num_kv_heads = u;
-            else if (key == "head_dim") m.head_dim = u;
-            else if (key == "vocab_size") m.vocab_size = u;
-            else if (key == "max_seq_len") m.max_seq_len = u;
-            else if (key == "rope_theta") m.rope_theta = (float)v;
-            else if (key == "rms_norm_eps") m.rms_norm_eps = (float)v;
-            else if (key == "num_experts") m.num_experts = u;
-            else if (key == "num_active_experts") m.num_active_experts = u;
-            else if (key == "default_codec") m.default_codec = (uint8_t)u;
-            else if (key == "default_group_size") m.default_group_size = (uint8_t)u;
-        }
-    }
+    std::vector<std::pair<std::string, JsonValue>> kvs;
+    if (!FlatJson(data, len).parse(kvs)) return false;
+    for (const auto& kv : kvs)
+        for (const ManifestField& f : kManifestFields)
+            if (kv.first == f.key && !assign_field(m, f, kv.second)) return false;
+    return true;
 }
 
 // ---------------------------------------------------------------- index --

@@ -152,6 +152,50 @@ def test_gpu_xxh32_rejects_bad_ranges(ctx):
     ctx.free(buf)
 
 
+def _with_manifest(tmp_path, text: str):
+    """The reference writer's test file with its manifest replaced by
+    `text` (appended at the end of the file, header offsets updated)."""
+    data = bytearray(ref_file_bytes("reference_test"))
+    body = text.encode()
+    off = len(data)
+    data += body
+    data[8:16] = off.to_bytes(8, "little")          # manifest_offset
+    data[16:24] = len(body).to_bytes(8, "little")   # manifest_size
+    data[48:56] = len(data).to_bytes(8, "little")   # total_file_size
+    p = tmp_path / "m.nxf"
+    p.write_bytes(bytes(data))
+    return p
+
+
+MANIFEST_OK = ('{"architecture": "llama", "name": "a\\"b\\\\c\\/d\\u0041\\u00e9", "num_layers": 2, '
+               '"hidden_dim": 128, "rope_theta": 1e4, "rms_norm_eps": 1E-5, "unknown": "x", "other": -3.5, '
+               '"default_codec": 255, "max_seq_len": 4294967295}')
+
+
+def test_manifest_parser_accepts_standard_json(tmp_path):
+    """Escapes (\\", \\\\, \\/, \\u), exponents, unknown keys of either kind and
+    the limits of the integer fields are read as JSON defines them."""
+    with NXFReader.open(_with_manifest(tmp_path, MANIFEST_OK)) as r:
+        m = r.manifest()
+    assert m.name == 'a"b\\c/dAé' and m.architecture == "llama"
+    assert (m.num_layers, m.hidden_dim, m.default_codec, m.max_seq_len) == (2, 128, 255, 4294967295)
+    assert m.rope_theta == 10000.0 and abs(m.rms_norm_eps - 1e-5) < 1e-12
+
+
+@pytest.mark.parametrize("bad", [
+    '{"num_layers": -1}', '{"num_layers": 4294967296}', '{"num_layers": 2.5}', '{"default_codec": 256}',
+    '{"default_codec": "1"}', '{"num_layers": "2"}', '{"name": 3}', '{"rope_theta": 1e39}',
+    '{"num_layers": 2,}', '{"num_layers": 2', '{"a": {"b": 1}}', '{"a": [1]}', '{"a": true}',
+    '{"num_layers": 01}', '{"num_layers": .5}', '{"name": "x\\q"}', '{"num_layers": 2} x'])
+def test_manifest_parser_rejects(tmp_path, bad):
+    """Values outside a field's range (negative, 2^32 and above, fractions,
+    bytes above 255, floats that overflow), a value of the wrong kind, and
+    text that is not a flat JSON object of strings and numbers fail the
+    open instead of being cast."""
+    with pytest.raises(NxError):
+        NXFReader.open(_with_manifest(tmp_path, bad))
+
+
 @needs_ref
 @pytest.mark.parametrize("case", list(NXF_CASES))
 def test_nxf_fixture_is_the_reference_writers_file(tmp_path, case):
