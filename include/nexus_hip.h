@@ -166,6 +166,23 @@ nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q_f32, nx_buf kpool, nx_b
                                    nx_buf block_table, nx_buf ctx_lens_i32, nx_buf out_f16,
                                    int batch, int hq, int hkv, int head_dim, int max_blocks,
                                    int num_blocks);
+/* nx_attn_decode_paged_f16 for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments and result;
+ * the split records and counters live in a static device array of the
+ * library (4 MiB of records + 16384 counters per device, held until the
+ * process ends), so the call allocates nothing and does not synchronize:
+ * it may be captured.  The context length and block-table checks run in the
+ * kernel instead of on the host: a sequence whose length exceeds
+ * max_blocks * 16 or whose table names a block outside [0, num_blocks) gets
+ * NaN output rows (its pages are not read).  NX_ERR_UNSUPPORTED when the
+ * split plan of (batch, hq, hkv, head_dim, max_blocks) needs more records or
+ * counters than the array holds.  Every call on one device shares the array:
+ * calls that overlap on one device (two streams, two contexts) race. */
+nx_status nx_attn_decode_paged_f16_noalloc(nx_ctx* ctx, nx_buf q_f32, nx_buf kpool, nx_buf vpool,
+                                           nx_buf block_table, nx_buf ctx_lens_i32, nx_buf out_f16,
+                                           int batch, int hq, int hkv, int head_dim, int max_blocks,
+                                           int num_blocks);
 /* TurboQuant codebooks (Lloyd-Max for N(0,1/128), kv/turbo_quant.cpp:172-219)
  * as computed by this library on the host: c4[16], b4[15], c3[8], b3[7]. */
 nx_status nx_tq_codebooks(float* c4, float* b4, float* c3, float* b3);

@@ -163,6 +163,14 @@ nx_status nx_init(nx_ctx** out, int device) {
         delete ctx;
         return NX_ERR_HIP;
     }
+    // the no-allocation attention's scratch: its address on this device
+    // (hipSetDevice above made it current)
+    if (nx::attn_noalloc_scratch(&ctx->na_scratch) != hipSuccess || !ctx->na_scratch) {
+        g_init_error = "hipGetSymbolAddress of the attention scratch failed";
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return NX_ERR_HIP;
+    }
     nx::tq_codebook(128, 4, ctx->c4, ctx->b4);
     nx::tq_codebook(128, 3, ctx->c3, ctx->b3);
     nx::tq_set_codebooks(ctx->c4, ctx->b4, ctx->c3, ctx->b3);
@@ -584,6 +592,62 @@ nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf v
     a.max_ctx = max_ctx;
     a.part = static_cast<float*>(ctx->attn_ws);
     return launched(ctx, nx::attn_f16_launch(a, ctx->stream), "attn_f16");
+}
+
+// The fp16 paged attention with its split records and counters in the
+// library's static scratch (g_attn_scratch in nx_attn.hip, whose device
+// address nx_init took): no allocation, no host synchronization, so it may be
+// captured into a graph.  Its kernels check the context lengths and table
+// entries themselves (check_blocks); a sequence that fails gets NaN rows.
+nx_status nx_attn_decode_paged_f16_noalloc(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf vpool, nx_buf bt,
+                                           nx_buf lens, nx_buf out, int batch, int hq, int hkv, int hd,
+                                           int max_blocks, int num_blocks) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || (hd != 64 && hd != 128) || max_blocks <= 0 ||
+        num_blocks <= 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_attn_decode_paged_f16_noalloc: bad shape");
+    const int G = hq / hkv;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "nx_attn_decode_paged_f16_noalloc: hq/hkv = %d", G);
+    NX_NEED(ctx, q, (size_t)batch * hq * hd * 4, "q");
+    const size_t pool = (size_t)num_blocks * hkv * nx::kPage * hd * 2;
+    NX_NEED(ctx, kpool, pool, "kpool");
+    NX_NEED(ctx, vpool, pool, "vpool");
+    NX_NEED(ctx, out, (size_t)batch * hq * hd * 2, "out");
+    NX_NEED(ctx, bt, (size_t)batch * max_blocks * 4, "block_table");
+    NX_NEED(ctx, lens, (size_t)batch * 4, "ctx_lens");
+    const int max_ctx = max_blocks * nx::kPage;
+    if (max_ctx > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_blocks above the attention limit");
+    const size_t rec = nx::attn_f16_workspace_bytes(batch, hq, hkv, hd, max_ctx);
+    const size_t words = nx::attn_count_words(batch, hkv);
+    if (rec > nx::kNoAllocRecordBytes || words > nx::kNoAllocCountWords)
+        return fail(ctx, NX_ERR_UNSUPPORTED,
+                    "nx_attn_decode_paged_f16_noalloc: needs %zu bytes of split records and %zu counters; "
+                    "the static scratch holds %zu and %zu",
+                    rec, words, nx::kNoAllocRecordBytes, nx::kNoAllocCountWords);
+    char* base = static_cast<char*>(ctx->na_scratch);
+    unsigned* counts = reinterpret_cast<unsigned*>(base + nx::kNoAllocRecordBytes);
+    // counters start at zero (a launch that completes leaves them at zero;
+    // cleared here by a kernel, not a memset, so the call can be captured)
+    hipError_t e = nx::zero_u32_launch(counts, words, ctx->stream);
+    if (e != hipSuccess) return launched(ctx, e, "attn_noalloc zero counters");
+    nx::AttnArgs a{};
+    a.counts = counts;
+    a.part = reinterpret_cast<float*>(base);
+    a.q = dptr<const float>(q);
+    a.kpool = dptr<const uint16_t>(kpool);
+    a.vpool = dptr<const uint16_t>(vpool);
+    a.block_table = dptr<const int32_t>(bt);
+    a.ctx_lens = dptr<const int32_t>(lens);
+    a.out16 = dptr<uint16_t>(out);
+    a.batch = batch;
+    a.hq = hq;
+    a.hkv = hkv;
+    a.hd = hd;
+    a.max_blocks = max_blocks;
+    a.max_ctx = max_ctx;
+    a.check_blocks = num_blocks;
+    return launched(ctx, nx::attn_f16_launch(a, ctx->stream), "attn_f16_noalloc");
 }
 
 nx_status nx_tq_codebooks(float* c4, float* b4, float* c3, float* b3) {

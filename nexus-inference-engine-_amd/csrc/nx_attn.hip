@@ -334,7 +334,9 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
         const float M = wave_max(m);
         const float e = (ok && M != -__builtin_inff()) ? __expf(m - M) : 0.0f;
         const float L = wave_sum(e * l);
-        wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : 0.0f;
+        // a NaN denominator (NaN scores, or a sequence the kernel's table
+        // check rejected) stays NaN in the output rather than becoming zero
+        wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : (L == L ? 0.0f : L);
     }
     f4v acc = {0.f, 0.f, 0.f, 0.f}, accp = {0.f, 0.f, 0.f, 0.f};  // rotated, plain records
     __syncthreads();
@@ -423,12 +425,24 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
     }
     int ctx, pg0;
     attn_range(a, b, range, ctx, pg0);
+    bool bad = false;
+    if (a.check_blocks > 0 && (ctx < 0 || ctx > a.max_blocks * kPage)) {
+        bad = true;
+        ctx = min(max(ctx, 0), a.max_blocks * kPage);
+    }
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
-    const int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
-                            ? (range == 2 ? a.hot_table : a.block_table)[(size_t)b * a.max_blocks + pg0 + my_page]
-                            : 0;
+    int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
+                      ? (range == 2 ? a.hot_table : a.block_table)[(size_t)b * a.max_blocks + pg0 + my_page]
+                      : 0;
+    if (a.check_blocks > 0) {
+        // entries of pages inside the context must name a block of the pool
+        const bool used = lane < npw_max && my_page * kPage < ctx;
+        const bool inval = used && (bt_lane < 0 || bt_lane >= a.check_blocks);
+        bad = bad || __any(inval);
+        bt_lane = inval ? 0 : bt_lane;
+    }
     // q as the B operand (column = head t, k = 8g + j of each 32-dim step).
     // Columns t >= G repeat head G - 1 (loads without a branch, so all of q
     // is requested at once); their scores and output rows are never used.
@@ -497,7 +511,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
             if (4 * g + i < G) my[(4 * g + i) * HD + 16 * nt + t] = o[nt][i];
     if (g == 0 && t < G) {
         my[MO + t] = m;
-        my[LO + t] = lsum;
+        my[LO + t] = bad ? __builtin_nanf("") : lsum;
     }
     float* parts = a.part + ((size_t)b * a.hkv + kvh) * nrec * REC;
     merge_waves_store<G, HD, true>(parts + (size_t)slot * REC, lds);
@@ -1185,6 +1199,26 @@ SplitPlan plan_splits_f16(int max_ctx, int hkv, int batch) {
     const SplitPlan base = plan_splits(max_ctx);
     if ((long)base.nsplit * hkv * batch <= device_cus()) return base;
     return plan_splits_tq(max_ctx, hkv, batch);
+}
+
+// Scratch of nx_attn_decode_paged_f16_noalloc (records, then counters).
+// In host code the name is only a stand-in: the device address comes from
+// attn_noalloc_scratch.
+static __device__ __align__(256) unsigned char g_attn_scratch[kNoAllocRecordBytes + 4 * kNoAllocCountWords];
+
+hipError_t attn_noalloc_scratch(void** out) {
+    return hipGetSymbolAddress(out, HIP_SYMBOL(g_attn_scratch));
+}
+
+__global__ __launch_bounds__(256) void k_zero_u32(unsigned* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
+
+hipError_t zero_u32_launch(unsigned* p, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_zero_u32, dim3(blocks), dim3(256), 0, st, p, n);
+    return hipGetLastError();
 }
 
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {

@@ -24,6 +24,9 @@ struct nx_ctx {
     size_t attn_ws_bytes = 0;
     unsigned* attn_counts = nullptr;  // split-completion counters (zero between launches)
     size_t attn_count_words = 0;
+    // device address of the static scratch array of
+    // nx_attn_decode_paged_f16_noalloc on this context's device
+    void* na_scratch = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     // scratch rows of nx_sample (grow-only)
     float* smp_ws = nullptr;

@@ -104,8 +104,22 @@ struct AttnArgs {
     // compresses the page that leaves the window at this step
     int hot_window;
     const int32_t* hot_table;
+    // > 0 (fp16 pages, standalone): the kernel itself checks each sequence's
+    // context length against max_blocks * 16 and the block-table entries of
+    // its pages against [0, check_blocks); an entry outside reads block 0
+    // instead and the sequence's output rows become NaN (no host check)
+    int check_blocks;
 };
 constexpr int kAttnCountStride = 64;  // counters 256 bytes apart
+// Split records and counters of nx_attn_decode_paged_f16_noalloc: a
+// file-scope device array of kNoAllocRecordBytes of records followed by
+// kNoAllocCountWords counters, one copy per device.
+constexpr size_t kNoAllocRecordBytes = (size_t)4 << 20;
+constexpr size_t kNoAllocCountWords = 16384;
+// Device address of that array on the current device (hipGetSymbolAddress).
+hipError_t attn_noalloc_scratch(void** out);
+// Zero n words at p (a kernel, so it may be captured into a graph).
+hipError_t zero_u32_launch(unsigned* p, size_t n, hipStream_t st);
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx);
 // Workspace of attn_f16_launch for exactly this (batch, max_ctx): the split
 // plan it launches, which has fewer splits than attn_workspace_bytes assumes

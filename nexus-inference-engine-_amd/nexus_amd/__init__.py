@@ -106,6 +106,7 @@ _SIGS = {
     "nx_residual_add": (_I, [_P, _B, _B, _B, _I]),
     "nx_kv_append_f16": (_I, [_P, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I]),
     "nx_attn_decode_paged_f16": (_I, [_P, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I, _I]),
+    "nx_attn_decode_paged_f16_noalloc": (_I, [_P, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I, _I, _I]),
     "nx_tq_codebooks": (_I, [_P, _P, _P, _P]),
     "nx_tq_encode": (_I, [_P, _B, _B, _B, _B, _B, _I]),
     "nx_tq_append": (_I, [_P, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I]),
