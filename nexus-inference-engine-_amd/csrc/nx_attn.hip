@@ -16,16 +16,22 @@
 // (q~ = H D q), scores are n_t * <q~, c[code_t]> / sqrt(128 * 128), V is summed
 // in the rotated domain and rotated back (D H o~ / sqrt(128)) by the merging
 // block.
-#include "nx_common.h"
-#include "nx_kernels.h"
+#include "nx_attn_dev.h"
 
 namespace nx {
 
 namespace {
 
-constexpr int kAttnWaves = 8;
-constexpr int kAttnThreads = kAttnWaves * kWave;
-constexpr int kMaxSplits = 64;  // splits per (sequence, kv head)
+using namespace at;
+
+#ifdef NX_LAYER_TRACE
+__device__ unsigned long long g_attn_trace[1024 * 8];
+#define NX_ATRACE(i) \
+    if (threadIdx.x == 0) g_attn_trace[(blockIdx.x + gridDim.x * blockIdx.y) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define NX_ATRACE(i)
+#endif
+
 
 struct SplitPlan {
     int nsplit, pps;  // splits per (sequence, kv head), pages per split
@@ -49,216 +55,6 @@ SplitPlan plan_splits(int max_ctx) {
     return {nsplit, pps};
 }
 
-// Split partial record, float offsets: O[G][HD] at 0, M[G], L[G], padded to 16 bytes.
-__host__ __device__ constexpr int rec_floats(int G, int HD) { return (G * HD + 2 * G + 3) / 4 * 4; }
-
-
-// Agent-scope (coherent across XCDs) store and load of a split record word,
-// for records handed to the block that merges them within the same launch.
-__device__ inline void st_coh(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float ld_coh(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The part of sequence b's context a block covers: all of it (range 0), or
-// with tiered pages the compressed pages [0, cold) (range 1) or the fp16
-// window [cold, ctx) (range 2, read from page cold / 16 of the hot table
-// on), cold = 16 floor((ctx - 1 - hot_window) / 16), at least 0: the pages
-// compressed before this step (the page that leaves the window at this step
-// is compressed by the same launch and read here as fp16).
-__device__ inline void attn_range(const AttnArgs& a, int b, int range, int& ctx, int& pg0) {
-    ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
-    pg0 = 0;
-    if (range != 0) {
-        const int cold = kPage * max(0, (ctx - 1 - a.hot_window) / kPage);
-        if (range == 1) {
-            ctx = cold;
-        } else {
-            pg0 = cold / kPage;
-            ctx -= cold;
-        }
-    }
-}
-
-// Cross-wavefront merge of the block: lds holds one record per wavefront
-// (O[G][HD], M[G], L[G]); every wavefront has written its own before the
-// barrier.  The rescale factors exp(m_w - M) are computed once per (wavefront,
-// head) by the first G * kAttnWaves lanes of wavefront 0 (max and sum over
-// groups of kAttnWaves lanes), then every thread sums its O elements over the
-// wavefronts.  The merged split record goes to `part` (COH: agent-scope
-// stores).
-template <int G, int HD, bool COH = false>
-__device__ inline void merge_waves_store(float* __restrict__ part, const float* lds) {
-    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    static_assert(G * kAttnWaves <= kWave, "one lane of wavefront 0 per (wavefront, head)");
-    __shared__ float fw[kAttnWaves * G];
-    __syncthreads();
-    const int t = threadIdx.x;
-    if (t < kWave) {
-        const bool act = t < G * kAttnWaves;
-        const int h = act ? t / kAttnWaves : 0, w = t % kAttnWaves;
-        const float m = act ? lds[w * REC + MO + h] : -__builtin_inff();
-        float M = m;
-#pragma unroll
-        for (int o = 1; o < kAttnWaves; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, kWave));
-        const float f = (M == -__builtin_inff()) ? 0.0f : __expf(m - M);
-        float L = act ? f * lds[w * REC + LO + h] : 0.0f;
-#pragma unroll
-        for (int o = 1; o < kAttnWaves; o <<= 1) L += __shfl_xor(L, o, kWave);
-        if (act) {
-            fw[w * G + h] = f;
-            if (w == 0) {
-                if (COH) {
-                    st_coh(part + MO + h, M);
-                    st_coh(part + LO + h, L);
-                } else {
-                    part[MO + h] = M;
-                    part[LO + h] = L;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    for (int idx = t; idx < G * HD; idx += kAttnThreads) {
-        const int h = idx / HD;
-        float acc = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) acc = fmaf(lds[w * REC + idx], fw[w * G + h], acc);
-        if (COH)
-            st_coh(part + idx, acc);
-        else
-            part[idx] = acc;
-    }
-}
-
-// ------------------------------------------------------------ fp16 pages --
-// q.K^T and P.V run on the matrix cores (v_mfma_f32_16x16x32_f16, wave64):
-//   A operand (16 x 32): lane l holds row l%16, k = 8(l/16) .. +7
-//   B operand (32 x 16): lane l holds column l%16, k = 8(l/16) .. +7
-//   C (16 x 16 fp32):    lane l holds column l%16, rows 4(l/16) .. +3
-// Scores S = K q^T per page: M = the page's 16 tokens, N = query heads (G of
-// 16 columns used), K = head dims.  A K page row is read straight into the A
-// operand (16 bytes per lane per k-step).  q enters as fp16 hi + lo parts
-// (q = hi + lo to 2^-22), so the two products give the fp32 score; K is exact
-// fp16 and the products accumulate in fp32.
-// Values O = P V per page pair: M = heads, N = 16 dims per tile, K = the 32
-// tokens of two pages.  The token order of that K dimension is chosen so the
-// probabilities a lane needs are exactly the 8 scores it holds in the S
-// layout (k = 8g + j: page a token 4g + j for j < 4, page b token 4g + j - 4),
-// and V pages are stored dimension-major ([hd][16] per page), so the B
-// operand is two 8-byte reads per lane.  P enters as fp16 hi + lo as well.
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-
-__device__ inline h8_t as_h8(uint4 v) { return __builtin_bit_cast(h8_t, v); }
-
-template <int HD>
-struct PairRaw {
-    uint4 k[2][HD / 32];  // K of pages a, b: A operand per k-step
-    uint2 v[HD / 16][2];  // V of pages a, b: tokens 4g..4g+3 of dim 16 nt + l%16
-    uint2 vmask[2];       // per page: bits of the V words that hold valid tokens
-};
-
-// Load pages a and b of a pair; na / nb = valid tokens of each (0 = none).
-// Every load is issued unconditionally, because a branch or a select around a
-// load makes the compiler wait for that load at once and the page would
-// arrive one round trip per tile: page b with no valid token re-reads page a
-// (blka must be a valid block), K rows of tokens past the valid count are
-// left as loaded (their scores are masked in pair_update), and the V words
-// of those tokens are cleared with masks.
-template <int HD>
-__device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, int na, int blkb,
-                                 int nb, int kvh, int lane) {
-    const int g = lane >> 4, t = lane & 15;
-    const int pb = nb > 0 ? blkb : blka;
-#pragma unroll
-    for (int pg = 0; pg < 2; ++pg) {
-        const int blk = pg ? pb : blka, n = pg ? nb : na;
-        const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
-#pragma unroll
-        for (int s = 0; s < HD / 32; ++s)
-            r.k[pg][s] = *reinterpret_cast<const uint4*>(a.kpool + base + (size_t)t * HD + 32 * s + 8 * g);
-        // tokens 4g .. 4g+3 of the V words: the first `valid` are kept
-        // (applied in pair_update, so that nothing here waits for the data)
-        const int valid = min(max(n - 4 * g, 0), 4);
-        r.vmask[pg] = make_uint2((uint32_t)(0xFFFFFFFFull >> (16 * (2 - min(valid, 2)))),
-                                 (uint32_t)(0xFFFFFFFFull >> (16 * (2 - max(valid - 2, 0)))));
-#pragma unroll
-        for (int nt = 0; nt < HD / 16; ++nt)
-            r.v[nt][pg] = *reinterpret_cast<const uint2*>(a.vpool + base + (size_t)(16 * nt + t) * kPage + 4 * g);
-    }
-    // keep the V loads ahead of the first product (the scheduler would sink
-    // them below the wait for K, costing a second round trip)
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// Fold one page pair into the wavefront's state: m (running max of head l%16),
-// lsum (this lane's share of the softmax denominator), O (C layout, rows =
-// heads 4(l/16) + i, columns = dims 16 nt + l%16).
-// CAUSAL (prefill): the columns are query tokens instead of heads; token
-// 4(l/16) + i of page a (b) is at position pos_a (pos_b) + 4(l/16) + i and
-// is masked for the query at position qpos (this lane's column) when later.
-template <int HD, bool CAUSAL = false>
-__device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 32],
-                                   const h8_t (&ql)[HD / 32], float scale, int na, int nb, float& m,
-                                   float& lsum, f4_t (&o)[HD / 16], int lane, int pos_a = 0, int pos_b = 0,
-                                   int qpos = 0) {
-    const int g = lane >> 4;
-    f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < HD / 32; ++s) {
-        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), qh[s], sa, 0, 0, 0);
-        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), ql[s], sa, 0, 0, 0);
-        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), qh[s], sb, 0, 0, 0);
-        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), ql[s], sb, 0, 0, 0);
-    }
-    float p[8];
-    float mloc = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const bool va = 4 * g + i < na && (!CAUSAL || pos_a + 4 * g + i <= qpos);
-        const bool vb = 4 * g + i < nb && (!CAUSAL || pos_b + 4 * g + i <= qpos);
-        p[i] = va ? sa[i] * scale : -__builtin_inff();
-        p[4 + i] = vb ? sb[i] * scale : -__builtin_inff();
-        mloc = fmaxf(mloc, fmaxf(p[i], p[4 + i]));
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mn = fmaxf(m, mloc);
-    const bool none = mn == -__builtin_inff();
-    const float corr = none ? 1.0f : __expf(m - mn);
-    float ps = 0.0f;
-    h8_t ph, pl;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float e = none ? 0.0f : __expf(p[j] - mn);
-        ps += e;
-        ph[j] = (_Float16)e;
-        pl[j] = (_Float16)(e - (float)ph[j]);
-    }
-    lsum = lsum * corr + ps;
-    m = mn;
-    // rows of O in this lane are heads 4g + i; their rescale factors live in
-    // the lanes whose column is that head
-    float c[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = __shfl(corr, 4 * g + i, 64);
-#pragma unroll
-    for (int nt = 0; nt < HD / 16; ++nt) {
-        f4_t acc = o[nt];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] *= c[i];
-        const h8_t vb = as_h8(make_uint4(r.v[nt][0].x & r.vmask[0].x, r.v[nt][0].y & r.vmask[0].y,
-                                         r.v[nt][1].x & r.vmask[1].x, r.v[nt][1].y & r.vmask[1].y));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, acc, 0, 0, 0);
-        o[nt] = acc;
-    }
-}
-
-
 // ------------------------------------------------- TurboQuant constants --
 __constant__ float c_tq_c4[16];
 __constant__ float c_tq_b4[15];
@@ -266,142 +62,10 @@ __constant__ float c_tq_c3[8];
 __constant__ float c_tq_b3[7];
 __constant__ float c_tq_cb[24];  // c_tq_c4 then c_tq_c3
 
-// In-LDS FWHT of G vectors of 128 (canonical butterfly network).
-template <int G>
-__device__ inline void lds_fwht(float* v) {
-    for (int h = 1; h < 128; h <<= 1) {
-        __syncthreads();
-        for (int t = threadIdx.x; t < G * 64; t += kAttnThreads) {
-            const int g = t >> 6, k = t & 63;
-            const int j = ((k / h) * 2 * h) + (k % h);
-            const float x = v[g * 128 + j], y = v[g * 128 + j + h];
-            v[g * 128 + j] = x + y;
-            v[g * 128 + j + h] = x - y;
-        }
-    }
-    __syncthreads();
-}
-
-constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
-
-// Run by the last split block of a (sequence, kv head) to finish: merges the
-// nsplit records of its G query heads and writes the fp16 output.  The
-// records were stored by other blocks with agent-scope stores, each complete
-// before its block counted itself, so they are read with agent-scope (sc1)
-// loads.  Wavefront w computes the weights exp(m_s - M) / L of heads
-// w, w + 4, ... with lane s holding split s (nsplit <= 64).  Thread t then
-// owns float4 column t % NC of O (NC = G * HD / 4) for the splits
-// s = t / NC (mod NG), NG = 256 / NC; it requests all of them at once
-// (16-byte buffer loads with the sc1 bit, skipped past nsplit, where the
-// weight is zero), and the NG partial sums meet in LDS.
-// TQ: the value sums of records [0, ntq) are in the rotated domain (all of
-// them for TurboQuant pages, the compressed part for tiered pages); their
-// merged sum is rotated back (o = D_v H o~ / sqrt(128), an FWHT in LDS) and
-// added to the merged sum of the fp16 records [ntq, nsplit).
-template <int G, int HD, bool TQ = false>
-__device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kvh, int b) {
-    constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    constexpr int NC = G * HD / 4, NG = kAttnThreads / NC;
-    constexpr int KMAX = (kMaxSplits + NG - 1) / NG, U = KMAX < 16 ? KMAX : 16;
-    constexpr int kSc1 = 16;  // cache-policy bit of the agent-scope load
-    static_assert(kMaxSplits <= kWave, "one split per lane");
-    static_assert(NC * NG == kAttnThreads, "float4 columns tile the block");
-    __shared__ float wgt[G * kMaxSplits];
-    __shared__ float4 acc4[kAttnThreads];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
-    const int c = tid % NC, sg = tid / NC, h = 4 * c / HD;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(parts), 0, nsplit * REC * 4, 0x00020000);
-    typedef float f4v __attribute__((ext_vector_type(4)));
-    // the first batch of O columns is requested together with the split
-    // maxima and denominators: one round trip for both
-    // (s is uniform within a wavefront, as NC is a multiple of 64 or NG
-    // divides the wavefront evenly; every load is consumed only after all
-    // of them are issued)
-    f4v v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int sx = sg + u * NG;
-        v[u] = sx < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(rs, (sx * REC + 4 * c) * 4, 0, kSc1)
-                           : f4v{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int hh = wave; hh < G; hh += kAttnWaves) {
-        const bool ok = lane < nsplit;
-        const int sl = ok ? lane : nsplit - 1;
-        const float m = ld_coh(parts + (size_t)sl * REC + MO + hh);
-        const float l = ld_coh(parts + (size_t)sl * REC + LO + hh);
-        const float M = wave_max(m);
-        const float e = (ok && M != -__builtin_inff()) ? __expf(m - M) : 0.0f;
-        const float L = wave_sum(e * l);
-        // a NaN denominator (NaN scores, or a sequence the kernel's table
-        // check rejected) stays NaN in the output rather than becoming zero
-        wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : (L == L ? 0.0f : L);
-    }
-    f4v acc = {0.f, 0.f, 0.f, 0.f}, accp = {0.f, 0.f, 0.f, 0.f};  // rotated, plain records
-    __syncthreads();
-    for (int s0 = sg;;) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int sx = s0 + u * NG;
-            const float w = wgt[h * kMaxSplits + min(sx, kMaxSplits - 1)] * (sx < nsplit ? 1.0f : 0.0f);
-            if constexpr (TQ) {
-                const float wr = sx < ntq ? w : 0.0f;
-                acc += wr * v[u];
-                accp += (w - wr) * v[u];
-            } else {
-                acc += w * v[u];
-            }
-        }
-        s0 += NG * U;
-        if (s0 >= nsplit) break;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int sx = s0 + u * NG;
-            v[u] = sx < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(rs, (sx * REC + 4 * c) * 4, 0, kSc1)
-                               : f4v{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    auto group_sum = [&]() {
-        float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (tid < NC) {
-            r = acc4[tid];
-            for (int gi = 1; gi < NG; ++gi) {
-                const float4 q = acc4[gi * NC + tid];
-                r.x += q.x;
-                r.y += q.y;
-                r.z += q.z;
-                r.w += q.w;
-            }
-        }
-        return r;
-    };
-    acc4[tid] = make_float4(acc.x, acc.y, acc.z, acc.w);
-    __syncthreads();
-    const float4 r = group_sum();
-    uint16_t* out = a.out16 + ((size_t)b * a.hq + (size_t)kvh * G) * HD;
-    if constexpr (TQ) {
-        static_assert(HD == 128, "TurboQuant vectors are 128 long");
-        __shared__ float ov[G * HD], ovp[G * HD];
-        if (tid < NC) *reinterpret_cast<float4*>(&ov[4 * tid]) = r;
-        __syncthreads();
-        acc4[tid] = make_float4(accp.x, accp.y, accp.z, accp.w);
-        __syncthreads();
-        const float4 rp = group_sum();
-        if (tid < NC) *reinterpret_cast<float4*>(&ovp[4 * tid]) = rp;
-        lds_fwht<G>(ov);
-        for (int idx = tid; idx < G * HD; idx += kAttnThreads)
-            out[idx] = f2h_bits(ov[idx] * kTqScale * a.vsign[idx % HD] + ovp[idx]);
-    } else if (tid < NC) {
-        *reinterpret_cast<uint2*>(out + 4 * tid) =
-            make_uint2((uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16),
-                       (uint32_t)f2h_bits(r.z) | ((uint32_t)f2h_bits(r.w) << 16));
-    }
-}
-
-// One split of one (kv head, sequence): pps pages (16 at the fixed plan)
-// shared by the block's kAttnWaves wavefronts, two pages per wavefront
-// step.  PIPE: more than one page pair per wavefront, two pairs in flight.
+// One split of one (kv head, sequence): the pages s, s + nsplit, ... of
+// split s, shared by the block's kAttnWaves wavefronts, two pages per
+// wavefront step.  PIPE: more than one page pair per wavefront (the launcher
+// decides from the longest context), two pairs in flight.
 // The block stores its record, counts itself in a.counts for its (sequence,
 // kv head), and the last of the nsplit blocks merges the records
 // (merge_last) and resets the counter to zero for the next launch.
@@ -410,12 +74,13 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
 // rotated records among them (tiered pages: the TurboQuant blocks' [0, ntq),
 // merged by merge_last<G, 128, true> when TIER).
 template <int G, int HD, bool PIPE, bool TIER = false>
-__device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b,
+__device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, int kvh, int b,
                                     int range = 0, int slot = -1, int nrec = 0, int ntq = 0) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
+    NX_ATRACE(0);
 
     // The context length and this wavefront's block-table entries (page
     // p0 + wave + kAttnWaves * i in lane i) are requested together: one round trip.
@@ -430,15 +95,21 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
         bad = true;
         ctx = min(max(ctx, 0), a.max_blocks * kPage);
     }
-    const int p0 = split * pps;
-    const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
-    const int my_page = p0 + wave + kAttnWaves * lane;
-    int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
+    // Pages are dealt to the splits round-robin and to a split's wavefronts
+    // in turn: wavefront w of split s takes pages s + nsplit (w + 8 i), so
+    // the pages a block reads do not depend on the context length (every
+    // block-table entry is requested before the length arrives) and a
+    // context of any length spreads over all the splits.  Lane i holds the
+    // entry of page i.
+    const int stride = nsplit * kAttnWaves;
+    const int first = split + nsplit * wave;
+    const int my_page = first + stride * lane;
+    int bt_lane = (pg0 + my_page < a.max_blocks)
                       ? (range == 2 ? a.hot_table : a.block_table)[(size_t)b * a.max_blocks + pg0 + my_page]
                       : 0;
     if (a.check_blocks > 0) {
         // entries of pages inside the context must name a block of the pool
-        const bool used = lane < npw_max && my_page * kPage < ctx;
+        const bool used = my_page * kPage < ctx;
         const bool inval = used && (bt_lane < 0 || bt_lane >= a.check_blocks);
         bad = bad || __any(inval);
         bt_lane = inval ? 0 : bt_lane;
@@ -467,12 +138,12 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
         }
     }
     const float scale = 1.0f / sqrtf((float)HD);
+    NX_ATRACE(1);
 
     const int npages = (ctx + kPage - 1) / kPage;
-    const int p1 = min(p0 + pps, npages);
-    // pages of this wavefront: p0 + wave + kAttnWaves * i for i < npw, taken in pairs
-    const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
-    auto valid_of = [&](int i) { return i < npw ? min(ctx - (p0 + wave + kAttnWaves * i) * kPage, kPage) : 0; };
+    // pages of this wavefront: first + stride * i for i < npw, taken in pairs
+    const int npw = first < npages ? (npages - first + stride - 1) / stride : 0;
+    auto valid_of = [&](int i) { return i < npw ? min(ctx - (first + stride * i) * kPage, kPage) : 0; };
     auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
     float m = -__builtin_inff(), lsum = 0.0f;
     f4_t o[HD / 16];
@@ -499,6 +170,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
             pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
         }
     }
+    NX_ATRACE(2);
     // the head's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
@@ -518,6 +190,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
     // every thread's record stores are complete before the block counts itself
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    NX_ATRACE(3);
     __shared__ int last;
     if (threadIdx.x == 0) {
         unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
@@ -526,15 +199,17 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int pps, int 
         if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+    NX_ATRACE(4);
     if (last) merge_last<G, HD, TIER>(a, nrec, ntq, kvh, b);
+    if (last) NX_ATRACE(5);
+    NX_ATRACE(6);
 }
 
-// PIPE: more than one page pair per wavefront (pps > 8), two pairs in
-// flight; otherwise the single pair is loaded up front and the kernel fits
-// two blocks per CU.
+// PIPE: more than one page pair per wavefront, two pairs in flight;
+// otherwise the single pair is loaded up front.
 template <int G, int HD, bool PIPE>
-__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int nsplit, int pps) {
-    attn_f16_run<G, HD, PIPE>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
+__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int nsplit) {
+    attn_f16_run<G, HD, PIPE>(a, nsplit, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // ------------------------------------------------------ TurboQuant pages --
@@ -836,6 +511,7 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     // the last of the nrec blocks merges, rotates back and resets the counter
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    NX_ATRACE(3);
     __shared__ int last;
     if (threadIdx.x == 0) {
         unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
@@ -1100,7 +776,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tiered(AttnArgs a, int
     if (x < ntq)
         attn_tq_run<G, PT>(a, ntq, ppt, x, blockIdx.y, blockIdx.z, 1, x, ntq + nf, ntq);
     else if (x < ntq + nf)
-        attn_f16_run<G, 128, PF, true>(a, nf, ppf, x - ntq, blockIdx.y, blockIdx.z, 2, x, ntq + nf, ntq);
+        attn_f16_run<G, 128, PF, true>(a, nf, x - ntq, blockIdx.y, blockIdx.z, 2, x, ntq + nf, ntq);
     else
         tq_compress_block(a, (x - ntq - nf) / kCompressParts, (x - ntq - nf) % kCompressParts, blockIdx.y,
                           blockIdx.z);
@@ -1165,10 +841,11 @@ hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st)
     return hipErrorInvalidValue;
 }
 
+SplitPlan plan_splits_f16(int max_ctx, int hkv, int batch);
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
-    const SplitPlan sp = plan_splits(max_ctx);
+    const int nsplit = max(plan_splits(max_ctx).nsplit, plan_splits_f16(max_ctx, hkv, batch).nsplit);
     const int G = hq / hkv;
-    return sizeof(float) * (size_t)batch * hkv * sp.nsplit * rec_floats(G, hd);
+    return sizeof(float) * (size_t)batch * hkv * nsplit * rec_floats(G, hd);
 }
 
 int attn_max_ctx() { return kMaxSplits * kPagesPerSplitMax * kPage; }
@@ -1192,13 +869,18 @@ SplitPlan plan_splits_tq(int max_ctx, int hkv, int batch) {
     return {nsplit, pps};
 }
 
-// fp16 splits: plan_splits, unless its grid would exceed one block per CU
-// (batched decode); then the TurboQuant plan's larger splits, so a single
-// round of blocks streams with two pairs in flight per wavefront.
+// fp16 splits: as many as fill the CUs with one block each over all (kv
+// head, sequence) pairs, at most kMaxSplits and at most one per page of the
+// longest context.  Pages are dealt round-robin (attn_f16_run), so pps is
+// the most pages any split takes; more than two per wavefront (pps >
+// kPagesPerSplitMin) selects the pipelined kernel.
 SplitPlan plan_splits_f16(int max_ctx, int hkv, int batch) {
-    const SplitPlan base = plan_splits(max_ctx);
-    if ((long)base.nsplit * hkv * batch <= device_cus()) return base;
-    return plan_splits_tq(max_ctx, hkv, batch);
+    const int pages = max((max_ctx + kPage - 1) / kPage, 1);
+    const int want = max(device_cus() / max(hkv * batch, 1), 1);
+    // a wavefront holds the block-table entries of its pages one per lane
+    const int least = (pages + kPagesPerSplitMax - 1) / kPagesPerSplitMax;
+    const int nsplit = min(max(min(want, pages), least), kMaxSplits);
+    return {nsplit, (pages + nsplit - 1) / nsplit};
 }
 
 // Scratch of nx_attn_decode_paged_f16_noalloc (records, then counters).
@@ -1221,6 +903,12 @@ hipError_t zero_u32_launch(unsigned* p, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
+#ifdef NX_LAYER_TRACE
+extern "C" int nx_debug_attn_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_attn_trace), sizeof(unsigned long long) * 1024 * 8);
+}
+#endif
+
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     if (!a.counts || !a.part) return hipErrorInvalidValue;
     const SplitPlan sp = plan_splits_f16(a.max_ctx, a.hkv, a.batch);
@@ -1231,10 +919,10 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     if (G == GG && a.hd == HH) {                                                                  \
         if (pipe)                                                                                 \
             hipLaunchKernelGGL((k_attn_f16<GG, HH, true>), grid, dim3(kAttnThreads), 0, st, a,     \
-                               sp.nsplit, sp.pps);                                                \
+                               sp.nsplit);                                                        \
         else                                                                                      \
             hipLaunchKernelGGL((k_attn_f16<GG, HH, false>), grid, dim3(kAttnThreads), 0, st, a,    \
-                               sp.nsplit, sp.pps);                                                \
+                               sp.nsplit);                                                        \
         return hipGetLastError();                                                                 \
     }
     NX_ATTN_CASE(1, 64)

@@ -120,6 +120,7 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
     if (XVEC) {
         uint32_t X[kMfmaEPT][4];
         float V[XS == X_RMSNORM ? kMfmaEPT : 1][8];
+        float NW[XS == X_RMSNORM ? kMfmaEPT : 1][8];
 #pragma unroll
         for (int j = 0; j < kMfmaEPT; ++j) {
             const int e = min(tid + j * kMfmaThreads, ne - 1);
@@ -134,6 +135,11 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
                 const float4 u = src[0], w = src[1];
                 V[j][0] = u.x; V[j][1] = u.y; V[j][2] = u.z; V[j][3] = u.w;
                 V[j][4] = w.x; V[j][5] = w.y; V[j][6] = w.z; V[j][7] = w.w;
+                // the norm weights with the values (without weights: h again, unused)
+                const float4* ws = reinterpret_cast<const float4*>(a.norm_w ? a.norm_w + kb : a.h32 + xo);
+                const float4 wu = ws[0], ww = ws[1];
+                NW[j][0] = wu.x; NW[j][1] = wu.y; NW[j][2] = wu.z; NW[j][3] = wu.w;
+                NW[j][4] = ww.x; NW[j][5] = ww.y; NW[j][6] = ww.z; NW[j][7] = ww.w;
             }
         }
         if (XS == X_RMSNORM && NORM) {
@@ -173,8 +179,8 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
                 for (int h = 0; h < 4; ++h) {
                     const int k = kb + 2 * h;
                     const float t0 = V[j][2 * h] * inv[b], t1 = V[j][2 * h + 1] * inv[b];
-                    const uint32_t lo = k < K ? f2h_bits(a.norm_w ? t0 * a.norm_w[k] : t0) : 0u;
-                    const uint32_t hi = k + 1 < K ? f2h_bits(a.norm_w ? t1 * a.norm_w[k + 1] : t1) : 0u;
+                    const uint32_t lo = k < K ? f2h_bits(a.norm_w ? t0 * NW[j][2 * h] : t0) : 0u;
+                    const uint32_t hi = k + 1 < K ? f2h_bits(a.norm_w ? t1 * NW[j][2 * h + 1] : t1) : 0u;
                     X[j][h] = lo | (hi << 16);
                 }
             } else if (kb >= K) {
@@ -559,6 +565,12 @@ hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+#ifdef NX_LAYER_TRACE
+extern "C" int nx_debug_gemv_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(gv::g_gemv_trace), sizeof(unsigned long long) * 64 * 256 * 8);
+}
+#endif
 
 hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st) {
     if (a.batch < 1 || a.batch > 8) return hipErrorInvalidValue;

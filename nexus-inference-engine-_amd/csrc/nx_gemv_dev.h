@@ -9,6 +9,16 @@
 namespace nx {
 namespace gv {
 
+#ifdef NX_LAYER_TRACE
+// phase timestamps of the batch-1 GEMV, per (epilogue, groups per lane) kind
+__device__ unsigned long long g_gemv_trace[64 * 256 * 8];
+#define NX_GTRACE(key, i) \
+    if (threadIdx.x == 0 && blockIdx.x < 256) \
+        g_gemv_trace[((key) * 256 + blockIdx.x) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define NX_GTRACE(key, i)
+#endif
+
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockThreads = kWavesPerBlock * kWave;
 
@@ -385,7 +395,9 @@ __device__ inline void put_chunk(int c, const uint32_t (&X)[4], uint32_t* sp, fl
     if ((c & 3) == 0) s8[c >> 2] = 8.0f * s;
 }
 
-__device__ inline void norm_chunk(const float (&v)[8], const float* __restrict__ w, int k0, int K,
+// fp16((v * inv) * w) of one 8-element chunk at k0; the weights w were
+// loaded with the chunk (has_w false: weights of one).
+__device__ inline void norm_chunk(const float (&v)[8], const float (&w)[8], bool has_w, int k0, int K,
                                   float inv, uint32_t (&X)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -393,11 +405,11 @@ __device__ inline void norm_chunk(const float (&v)[8], const float* __restrict__
         const int k = k0 + 2 * j;
         if (k < K) {
             const float t = v[2 * j] * inv;
-            lo = f2h_bits(w ? t * w[k] : t);
+            lo = f2h_bits(has_w ? t * w[2 * j] : t);
         }
         if (k + 1 < K) {
             const float t = v[2 * j + 1] * inv;
-            hi = f2h_bits(w ? t * w[k + 1] : t);
+            hi = f2h_bits(has_w ? t * w[2 * j + 1] : t);
         }
         X[j] = lo | (hi << 16);
     }
@@ -412,10 +424,13 @@ __device__ inline void norm_chunk(const float (&v)[8], const float* __restrict__
 // Loads complete in issue order, so waiting for the row then does not wait
 // for the weights, and a wavefront's first tile can be reduced as soon as it
 // arrives.  For X_RMSNORM the block reduces sum(h^2) once and converts from
-// the registers.  stage_finish ends with a barrier.
+// the registers; the norm weights of a chunk are requested with it (loads
+// issued later, inside the conversion, would wait for every tile in
+// flight).  stage_finish ends with a barrier.
 template <int CPT, int XS>
 struct StageRegs {
     float v[XS == X_RMSNORM ? CPT : 1][8];
+    float w[XS == X_RMSNORM ? CPT : 1][8];
     uint32_t X[XS == X_F16 ? CPT : 1][4];
 };
 
@@ -425,12 +440,16 @@ __device__ inline void stage_issue(const GemvArgs& a, int b, StageRegs<CPT, XS>&
     if (XVEC) {
         // K % 8 == 0 and an aligned row (checked by the launcher)
         const int nvalid = K / 8;
+        // without norm weights the loads read h again (values unused)
+        const float* wsrc = a.norm_w ? a.norm_w : a.h32 + (size_t)b * a.ldx;
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            if (XS == X_F16)
+            if (XS == X_F16) {
                 load_x8_u(a.x16 + (size_t)b * a.ldx, tid + j * NT, nvalid, r.X[j]);
-            else
+            } else {
                 load_h8_u(a.h32 + (size_t)b * a.ldx, tid + j * NT, nvalid, r.v[j]);
+                load_h8_u(wsrc, tid + j * NT, nvalid, r.w[j]);
+            }
         }
         return;
     }
@@ -443,9 +462,14 @@ __device__ inline void stage_issue(const GemvArgs& a, int b, StageRegs<CPT, XS>&
     } else {
         const float* h = a.h32 + (size_t)b * a.ldx;
         const bool vec = (reinterpret_cast<uintptr_t>(h) & 15u) == 0 && (a.ldx & 3) == 0;
+        const float* w = a.norm_w ? a.norm_w : h;
+        const bool wvec = vec && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
 #pragma unroll
         for (int j = 0; j < CPT; ++j)
-            if (tid + j * NT < nch) load_h8(h, 8 * (tid + j * NT), K, vec, r.v[j]);
+            if (tid + j * NT < nch) {
+                load_h8(h, 8 * (tid + j * NT), K, vec, r.v[j]);
+                load_h8(w, 8 * (tid + j * NT), K, wvec, r.w[j]);
+            }
     }
 }
 
@@ -475,7 +499,7 @@ __device__ inline void stage_finish(const GemvArgs& a, StageRegs<CPT, XS>& r, ui
             const int c = tid + j * NT;
             if (c < nch) {
                 uint32_t X[4];
-                norm_chunk(r.v[j], a.norm_w, 8 * c, K, inv, X);
+                norm_chunk(r.v[j], r.w[j], a.norm_w != nullptr, 8 * c, K, inv, X);
                 put_chunk(c, X, sp, s8);
             }
         }
@@ -510,14 +534,21 @@ __device__ inline void load_pairs_lds(XPairs<GPL>& xp, const uint32_t* sp, const
 
 // Row range of wavefront `w` for batch 1: rows are dealt in pairs (a pair is
 // never split, so the RoPE and SwiGLU epilogues see both rows), `base` pairs
-// per wavefront plus one more for the first `extra` wavefronts.
+// per wavefront plus `extra` more spread over the blocks of `wpb`
+// wavefronts (the first extra % nb blocks take one more), so every CU
+// streams about the same number of rows; a block's extra pairs go to its
+// first wavefronts.  Wavefronts of one block hold consecutive ranges.
 struct RowSplit {
     int base, extra;
+    int nb = 1, wpb = 1;  // blocks and wavefronts per block of the grid
 };
 
 __device__ inline void wave_rows(const RowSplit& rs, int w, int N, int& r0, int& r1) {
-    const int u0 = w * rs.base + min(w, rs.extra);
-    const int nu = rs.base + (w < rs.extra ? 1 : 0);
+    const int blk = w / rs.wpb, j = w % rs.wpb;
+    const int eb = rs.extra / rs.nb, er = rs.extra % rs.nb;
+    const int here = eb + (blk < er ? 1 : 0);  // extra pairs of this block
+    const int u0 = w * rs.base + blk * eb + min(blk, er) + min(j, here);
+    const int nu = rs.base + (j < here ? 1 : 0);
     r0 = min(2 * u0, N);
     r1 = min(2 * (u0 + nu), N);
 }
@@ -575,6 +606,8 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     __shared__ __align__(16) uint32_t sp[kWave * GPL * 16];
     __shared__ float s8[kWave * GPL];
     __shared__ float red[WPB];
+    [[maybe_unused]] constexpr int TKEY = EPI * 8 + (GPL & 7);
+    NX_GTRACE(TKEY, 0);
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = block * WPB + (threadIdx.x >> 6);
     int r0, r1;
@@ -591,6 +624,7 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     // ahead of every weight tile, so x arrives after one round trip instead
     // of behind the first tiles of all the other wavefronts.
     if (WPB > kWavesPerBlock) __syncthreads();
+    NX_GTRACE(TKEY, 1);
     Tile<GPL, R> t[DEPTH];
     if (!XFIRST) {
 #pragma unroll
@@ -607,7 +641,9 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
         }
         if (a.kpool) qblk = a.block_table[qp / kPage];
     }
+    NX_GTRACE(TKEY, 2);
     stage_finish<CPT, XS, NT>(a, sr, sp, s8, red);  // block barrier: every wavefront takes part
+    NX_GTRACE(TKEY, 3);
     // XFIRST: the first tiles are requested only once x is staged (x then
     // arrives without weight traffic queued beside it)
     if (XFIRST) {
@@ -642,9 +678,11 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
                     }
                 }
                 if (lane == 0) epilogue<EPI, R>(a, 0, r0 + (i + j) * R, r1, res, best_v, best_i, &pre);
+                if (i + j == 0) NX_GTRACE(TKEY, 4);
             }
         }
     }
+    NX_GTRACE(TKEY, 5);
     if (EPI == E_LOGITS) {
         // one atomic per block: the wavefronts' maxima meet in LDS first
         __shared__ unsigned long long bk[WPB];
@@ -669,12 +707,12 @@ constexpr int kB1WavesPerCU = 8;
 // such grids (routed experts) divide the CUs.  Returns the number of blocks.
 inline int b1_plan(int N, int R, int waves_per_cu, RowSplit& rs, int wpb = kWavesPerBlock, int share = 1) {
     const int units = (N + 1) / 2;
-    const int min_units = (R + 1) / 2;
+    const int min_units = (R + 1) / 2;  // at least one full tile per wavefront
     int waves = device_cus() * waves_per_cu / (share > 0 ? share : 1);
     const int maxw = (units + min_units - 1) / min_units;
     if (waves > maxw) waves = maxw;
     waves = (waves + wpb - 1) / wpb * wpb;
-    rs = RowSplit{units / waves, units % waves};
+    rs = RowSplit{units / waves, units % waves, waves / wpb, wpb};
     return waves / wpb;
 }
 

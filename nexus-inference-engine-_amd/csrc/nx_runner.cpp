@@ -96,6 +96,15 @@ struct nx_model {
     float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
     int top_k = 0;
     float* smp_scratch = nullptr;  // [batch][vocab], allocated when sampling is first set
+    // fused attention block (batch 1, fp16 pages): QKV, attention and wo of a
+    // layer in one launch (nx_layer.hip); counters per layer, the step count
+    // the embedding kernel keeps, and the error word of a timed-out wait
+    bool fused_ok = false;         // the shape and device allow it
+    bool fused = false;            // in use
+    nx::LayerArgs lplan{};
+    unsigned* lsync = nullptr;     // [n_layers][hkv + 1][kAttnCountStride]
+    unsigned* lstate = nullptr;    // [0] epoch, [64] error word
+    unsigned* h_err = nullptr;     // pinned host copy of the error word
 };
 
 namespace {
@@ -199,11 +208,56 @@ nx_status enqueue_sample(nx_model* m, int b0, int nb) {
     return NX_OK;
 }
 
-// Attention of layer ly for every sequence (q in m->q, output m->att16).
-// Tiered pages: one launch whose blocks read either the compressed pages
-// (TurboQuant) or the fp16 window, merged by the last block, and compress the
-// page that leaves the window at this step.
-hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
+// Arguments of the batch-1 QKV GEMV (RMSNorm of h, RoPE, page write) and of
+// the wo GEMV (attention output, residual add into h) of layer L.
+nx::GemvArgs qkv_args(const nx_model* m, const Layer& ly) {
+    const nx_model_config& c = m->c;
+    nx::GemvArgs a{};
+    a.W = ly.wqkv;
+    a.S = ly.sqkv;
+    a.N = m->nqkv;
+    a.K = c.d_model;
+    a.G = m->Gd;
+    a.batch = c.batch;
+    a.h32 = m->h;
+    a.ldx = c.d_model;
+    a.eps = c.eps;
+    a.norm_w = ly.norm_attn;
+    a.q32 = m->q;
+    a.qdim = m->qdim;
+    a.kvdim = m->kvdim;
+    a.hd = c.head_dim;
+    a.hkv = c.n_kv_heads;
+    a.pos = m->pos;
+    a.cos_t = m->rope_cos;
+    a.sin_t = m->rope_sin;
+    a.block_table = c.kv_kind == 2 ? m->hot_bt : m->block_table;
+    a.max_blocks = m->max_blocks;
+    if (c.kv_kind != 1) {
+        a.kpool = ly.kpool;
+        a.vpool = ly.vpool;
+    } else {
+        a.kv_tmp = m->kv_tmp;
+    }
+    return a;
+}
+
+nx::GemvArgs wo_args(const nx_model* m, const Layer& ly) {
+    nx::GemvArgs o{};
+    o.W = ly.wo;
+    o.S = ly.so;
+    o.N = m->c.d_model;
+    o.K = m->qdim;
+    o.G = m->Gq;
+    o.batch = m->c.batch;
+    o.x16 = m->att16;
+    o.ldx = m->qdim;
+    o.y32 = m->h;
+    o.ldy = m->c.d_model;
+    return o;
+}
+
+nx::AttnArgs attn_args(const nx_model* m, const Layer& ly) {
     const nx_model_config& c = m->c;
     nx::AttnArgs at{};
     at.q = m->q;
@@ -229,6 +283,16 @@ hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
     at.max_ctx = c.max_seq;
     at.part = m->attn_part;
     at.counts = m->attn_counts;
+    return at;
+}
+
+// Attention of layer ly for every sequence (q in m->q, output m->att16).
+// Tiered pages: one launch whose blocks read either the compressed pages
+// (TurboQuant) or the fp16 window, merged by the last block, and compress the
+// page that leaves the window at this step.
+hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
+    const nx_model_config& c = m->c;
+    nx::AttnArgs at = attn_args(m, ly);
     if (c.kv_kind == 0) return nx::attn_f16_launch(at, st);
     if (c.kv_kind == 1) return nx::attn_tq_launch(at, st);
     at.hot_window = c.hot_window;
@@ -256,63 +320,63 @@ double kv_bytes(const nx_model* m) {
     return kv;
 }
 
+// QKV, attention and wo of layer L as one launch (batch 1, fp16 pages).
+hipError_t fused_attention_launch(nx_model* m, int L, hipStream_t st) {
+    const Layer& ly = m->layers[L];
+    nx::LayerArgs a = m->lplan;
+    a.qkv = qkv_args(m, ly);
+    a.wo = wo_args(m, ly);
+    a.at = attn_args(m, ly);
+    a.sync = m->lsync + (size_t)L * (m->c.n_kv_heads + 1) * nx::kAttnCountStride;
+    a.epoch = m->lstate;
+    a.err = m->lstate + 64;
+    return nx::attn_block_b1_launch(a, st);
+}
+
+// Zero the fused block's counters, step count and error word (stream
+// ordered: before the next step that uses them).
+nx_status reset_fused_state(nx_model* m) {
+    if (!m->lsync) return NX_OK;
+    const size_t words = (size_t)m->c.n_layers * (m->c.n_kv_heads + 1) * nx::kAttnCountStride;
+    NX_HIP(m->ctx, hipMemsetAsync(m->lsync, 0, words * 4, m->ctx->stream));
+    NX_HIP(m->ctx, hipMemsetAsync(m->lstate, 0, 128 * 4, m->ctx->stream));
+    return NX_OK;
+}
+
+// After a synchronized run of steps: a wait of the fused block that timed
+// out (a block was not resident, or a hand-off never came) leaves the error
+// word set; the outputs of those steps are not to be used.
+nx_status check_fused_state(nx_model* m) {
+    if (!m->fused) return NX_OK;
+    NX_HIP(m->ctx, hipMemcpyAsync(m->h_err, m->lstate + 64, 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    if (*m->h_err == 0u) return NX_OK;
+    NX_TRY(reset_fused_state(m));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return fail(m->ctx, NX_ERR_TIMEOUT, "fused attention block: a wait between blocks timed out; the step's outputs are invalid");
+}
+
 // One decode step for every sequence, enqueued on the context stream.
 nx_status enqueue_step(nx_model* m) {
     const nx_model_config& c = m->c;
     hipStream_t st = m->ctx->stream;
     const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts;
     NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d,
-                                  c.vocab, B, st));
+                                  c.vocab, B, st, m->fused ? m->lstate : nullptr));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
-        // RMSNorm + QKV + RoPE + paged KV append
-        nx::GemvArgs a{};
-        a.W = ly.wqkv;
-        a.S = ly.sqkv;
-        a.N = m->nqkv;
-        a.K = d;
-        a.G = m->Gd;
-        a.batch = B;
-        a.h32 = m->h;
-        a.ldx = d;
-        a.eps = c.eps;
-        a.norm_w = ly.norm_attn;
-        a.q32 = m->q;
-        a.qdim = m->qdim;
-        a.kvdim = m->kvdim;
-        a.hd = c.head_dim;
-        a.hkv = c.n_kv_heads;
-        a.pos = m->pos;
-        a.cos_t = m->rope_cos;
-        a.sin_t = m->rope_sin;
-        a.block_table = c.kv_kind == 2 ? m->hot_bt : m->block_table;
-        a.max_blocks = m->max_blocks;
-        if (c.kv_kind != 1) {
-            a.kpool = ly.kpool;
-            a.vpool = ly.vpool;
+        if (m->fused) {
+            NX_LAUNCH(m, fused_attention_launch(m, L, st));
         } else {
-            a.kv_tmp = m->kv_tmp;
+            // RMSNorm + QKV + RoPE + paged KV append, attention, wo + residual
+            NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_QKV, qkv_args(m, ly), st));
+            if (c.kv_kind == 1)
+                NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr,
+                                                  ly.kc4, ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table,
+                                                  m->pos, m->max_blocks, st));
+            NX_LAUNCH(m, attention_launch(m, ly, st));
+            NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, wo_args(m, ly), st));
         }
-        NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_QKV, a, st));
-        if (c.kv_kind == 1)
-            NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr, ly.kc4,
-                                              ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table, m->pos,
-                                              m->max_blocks, st));
-        // attention
-        NX_LAUNCH(m, attention_launch(m, ly, st));
-        // output projection + residual
-        nx::GemvArgs o{};
-        o.W = ly.wo;
-        o.S = ly.so;
-        o.N = d;
-        o.K = m->qdim;
-        o.G = m->Gq;
-        o.batch = B;
-        o.x16 = m->att16;
-        o.ldx = m->qdim;
-        o.y32 = m->h;
-        o.ldy = d;
-        NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, o, st));
         if (E == 0) {
             // RMSNorm + gate/up + SwiGLU, then down + residual
             nx::GemvArgs f{};
@@ -461,6 +525,7 @@ nx_status free_model(nx_model* m) {
     for (void* p : m->allocs) (void)hipFree(p);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
     if (m->h_out) (void)hipHostFree(m->h_out);
+    if (m->h_err) (void)hipHostFree(m->h_err);
     delete m;
     return NX_OK;
 }
@@ -607,6 +672,14 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     }
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_stage, sizeof(int32_t) * B, hipHostMallocDefault));
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_out, sizeof(int32_t) * (size_t)B * m->out_stride, hipHostMallocDefault));
+    // the fused attention block where the shape allows it (on by default)
+    if (B == 1 && c.kv_kind == 0 &&
+        nx::attn_block_b1_plan(d, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq, m->lplan)) {
+        NX_TRY(dalloc(m, &m->lsync, (size_t)c.n_layers * (c.n_kv_heads + 1) * nx::kAttnCountStride));
+        NX_TRY(dalloc(m, &m->lstate, 128));
+        NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_err, sizeof(unsigned), hipHostMallocDefault));
+        m->fused_ok = true;
+    }
     if (synthetic) NX_TRY(generate_weights(m));
     NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     return NX_OK;
@@ -836,6 +909,22 @@ nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float
     return NX_OK;
 }
 
+nx_status nx_model_set_fused(nx_model* m, int on) {
+    if (!m || (on != 0 && on != 1)) return NX_ERR_INVALID;
+    if (on && !m->fused_ok) return fail(m->ctx, NX_ERR_UNSUPPORTED, "the fused attention block does not run this model");
+    if ((bool)on == m->fused) return NX_OK;
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->exec_multi) (void)hipGraphExecDestroy(m->exec_multi);
+    m->exec = nullptr;
+    m->exec_multi = nullptr;
+    m->fused = on != 0;
+    // counters and step count restart together
+    NX_TRY(reset_fused_state(m));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return NX_OK;
+}
+
 nx_status nx_model_set_prefill(nx_model* m, int batched) {
     if (!m || (batched != 0 && batched != 1)) return NX_ERR_INVALID;
     m->prefill_batched = batched;
@@ -875,6 +964,7 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
     std::vector<unsigned long long> best(B);
     NX_HIP(m->ctx, hipMemcpyAsync(best.data(), m->best, (size_t)B * 8, hipMemcpyDeviceToHost, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
+    NX_TRY(check_fused_state(m));
     for (int b = 0; b < B; ++b) {
         m->hpos[b] += P;
         if (next_tokens) next_tokens[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)(best[b] & 0xFFFFFFFFull));
@@ -1020,6 +1110,7 @@ nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
     if (out_tokens)
         NX_HIP(m->ctx, hipMemcpyAsync(m->h_out, m->out_tokens, (size_t)B * m->out_stride * 4, hipMemcpyDeviceToHost, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
+    NX_TRY(check_fused_state(m));
     for (int b = 0; b < B; ++b) {
         m->hpos[b] += steps;
         if (out_tokens)
