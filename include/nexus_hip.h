@@ -106,6 +106,17 @@ nx_status nx_synchronize(nx_ctx* ctx);
  * updated in place instead of re-instantiated. */
 nx_status nx_token_begin(nx_ctx* ctx);
 nx_status nx_token_end(nx_ctx* ctx);
+/* ComputeDispatch::flush_token / resume_token (compute_dispatch.h:120-123,
+ * compute_dispatch.cpp:816-833; called around the CPU parts of a decode step,
+ * hybrid_model.cpp:820-1241): flush launches the ops captured so far in the
+ * token batch and waits, so their results can be read; resume captures the
+ * following ops into a new segment, launched by the next flush or by
+ * nx_token_end.  Each segment keeps its own graph, updated in place from
+ * token to token.  A flush after a flush, or a resume without a flush, is a
+ * no-op (as in the reference); either outside nx_token_begin/end is
+ * NX_ERR_STATE. */
+nx_status nx_token_flush(nx_ctx* ctx);
+nx_status nx_token_resume(nx_ctx* ctx);
 
 /* ------------------------------------------------------------------ ops -- */
 /* int4-g32 GEMV: y[b][n] = sum_k x[b][k] * (q[n][k] - 8) * s[n][k/32], fp32
@@ -222,6 +233,21 @@ nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits_f32, nx_buf ids_i32, nx_b
 nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, nx_buf w2,
                             nx_buf s2, nx_buf ids_i32, nx_buf weights_f32, nx_buf out_f32, int d,
                             int F, int E, int k, int batch, int accumulate);
+/* GEMM C[M][N] = A[M][K] B[K][N], all fp32 row-major, on the matrix cores
+ * (fp32 products and sums).  ComputeDispatch::gemm (compute_dispatch.h:42,
+ * the dense-weight path of hybrid_model.cpp:121; compute::gemm_f32). */
+nx_status nx_gemm_f32(nx_ctx* ctx, nx_buf A, nx_buf B, nx_buf C, int M, int N, int K);
+/* SwiGLU FFN of int4-g32 weights: y[b] (+)= W2 (fp16(silu(W1 x_b) * W3 x_b))
+ * for batch rows of x fp16 [batch][d]; w13 [2F][d] holds W1 / W3 rows
+ * interleaved (row 2f = W1 row f, 2f+1 = W3 row f), s13 their scales, w2
+ * [d][F] and s2; y fp32 [batch][d].  The four dispatches of
+ * ComputeDispatch::gpu_ffn_fused (compute_dispatch.h:254,
+ * compute_dispatch.cpp:682-727) as two launches (the SwiGLU is the gate/up
+ * GEMV's epilogue); the intermediate activations stay on the device in a
+ * workspace of the context (grown outside capture, or reserved with
+ * nx_reserve_workspace). */
+nx_status nx_ffn_int4_g32(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, nx_buf w2, nx_buf s2, nx_buf y_f32,
+                          int d, int F, int batch, int accumulate);
 /* Greedy sampling: first maximum of logits fp32 [batch][V]
  * (hybrid_model.cpp:2027-2038). */
 nx_status nx_argmax(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int batch);
@@ -235,6 +261,57 @@ nx_status nx_argmax(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int b
  * the top-k and top-p orders keep the lower index. */
 nx_status nx_sample(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int batch, float temperature, int top_k,
                     float top_p, uint64_t seed);
+
+/* -------------------------------------------------- set-up and residency -- */
+/* The persistent activation buffers of a decode step
+ * (ComputeDispatch::GPUBufferPool, compute_dispatch.h:137-155): device
+ * buffers of the context, zero-filled, `batch` rows each, freed with
+ * nx_free or nx_destroy.  GEMV inputs are fp16 here (norm, attn_out,
+ * ffn_act); the reference keeps them fp32. */
+typedef struct {
+    nx_buf hidden;    /* fp32 [batch][hidden] */
+    nx_buf residual;  /* fp32 [batch][hidden] */
+    nx_buf norm;      /* fp16 [batch][hidden] (the reference's norm_buf) */
+    nx_buf q;         /* fp32 [batch][max_q] */
+    nx_buf k, v;      /* fp32 [batch][max_kv] */
+    nx_buf attn_out;  /* fp16 [batch][max_q] */
+    nx_buf ffn_gate;  /* fp32 [batch][max_ffn] */
+    nx_buf ffn_up;    /* fp32 [batch][max_ffn] */
+    nx_buf ffn_act;   /* fp16 [batch][max_ffn rounded up to 8] SwiGLU output */
+    nx_buf ffn_out;   /* fp32 [batch][hidden] */
+    nx_buf logits;    /* fp32 [batch][vocab] */
+    nx_buf token;     /* int32 [batch] */
+} nx_gpu_pool;
+/* ComputeDispatch::init_gpu_pool (compute_dispatch.h:163,
+ * hybrid_model.cpp:540). */
+nx_status nx_init_gpu_pool(nx_ctx* ctx, int hidden, int max_q, int max_kv, int max_ffn, int vocab, int batch,
+                           nx_gpu_pool* out);
+/* ComputeDispatch::init_kv_cache (compute_dispatch.h:170,
+ * compute_dispatch.cpp:357-385; hybrid_model.cpp:550): the GPU-resident KV
+ * cache as fp16 pages of 16 tokens for the paged entry points --
+ * kpools[l] / vpools[l] (num_layers buffers each, zero-filled) of
+ * num_blocks = batch * max_blocks pages of n_kv_heads x 16 x head_dim, and a
+ * block table int32 [batch][max_blocks] mapping sequence b's page p to block
+ * b * max_blocks + p (max_blocks = ceil(max_seq / 16)).  The reference
+ * keeps fp32 K/V contiguous per layer. */
+nx_status nx_init_kv_cache(nx_ctx* ctx, int num_layers, int max_seq, int n_kv_heads, int head_dim, int batch,
+                           nx_buf* kpools, nx_buf* vpools, nx_buf* block_table, int* max_blocks, int* num_blocks);
+/* ComputeDispatch::pre_allocate_activation_buffer (compute_dispatch.h:281,
+ * compute_dispatch.cpp:862-870; hybrid_model.cpp:519): grows every
+ * workspace the entry points keep per context -- FFN activations, sampler
+ * rows, attention split records and counters -- to what calls up to these
+ * sizes need, so those calls allocate nothing (and may be captured).  A size
+ * of 0 skips its workspace.  The reference reserves staging bytes; this
+ * library takes the shapes the bytes come from. */
+nx_status nx_reserve_workspace(nx_ctx* ctx, int batch, int max_ffn, int vocab, int n_heads, int n_kv_heads,
+                               int head_dim, int max_ctx);
+/* ComputeDispatch::preload_all_buffers (compute_dispatch.h:285,
+ * compute_dispatch.cpp:872-887; hybrid_model.cpp:581, :639): the reference
+ * touches every cached weight buffer to fault its pages into RAM.  Device
+ * memory is resident once allocated, so this waits for every upload on the
+ * context's stream to finish and reports the number of cached weight
+ * buffers (n_buffers may be NULL). */
+nx_status nx_preload_all_buffers(nx_ctx* ctx, size_t* n_buffers);
 
 /* ----------------------------------------------------------- the runner -- */
 /* A resident decoder driven by this library: the counterpart of

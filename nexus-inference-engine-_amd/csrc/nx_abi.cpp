@@ -59,6 +59,7 @@ nx_status launched(nx_ctx* ctx, hipError_t e, const char* what) {
     if (e != hipSuccess) return nx::hip_fail(ctx, e, what);
     return NX_OK;
 }
+nx_status ensure_smp_ws(nx_ctx* ctx, size_t floats);
 }  // namespace
 
 // ------------------------------------------------------------------ draw --
@@ -188,6 +189,9 @@ nx_status nx_destroy(nx_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->token_exec) (void)hipGraphExecDestroy(ctx->token_exec);
+    for (hipGraphExec_t e : ctx->seg_exec)
+        if (e) (void)hipGraphExecDestroy(e);
+    if (ctx->ffn_ws) (void)hipFree(ctx->ffn_ws);
     for (auto& kv : ctx->bufs) (void)hipFree(reinterpret_cast<void*>(kv.first));
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
     if (ctx->attn_counts) (void)hipFree(ctx->attn_counts);
@@ -317,42 +321,77 @@ nx_status nx_synchronize(nx_ctx* ctx) {
 // ----------------------------------------------------------------- batching --
 nx_status nx_token_begin(nx_ctx* ctx) {
     if (!ctx) return NX_ERR_INVALID;
-    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "token batch already open");
+    if (ctx->capturing || ctx->token_flushed) return fail(ctx, NX_ERR_STATE, "token batch already open");
     NX_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     ctx->capturing = true;
+    ctx->token_seg = 0;
+    return NX_OK;
+}
+
+// End the capture of the current segment of the token batch, launch its
+// graph and wait.  Segment s keeps its own instantiated graph, updated in
+// place while the captured sequence keeps its shape.
+static nx_status run_segment(nx_ctx* ctx) {
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    NX_HIP(ctx, hipStreamEndCapture(ctx->stream, &g));
+    const int seg = ctx->token_seg;
+    if (seg > 0 && (int)ctx->seg_exec.size() < seg) ctx->seg_exec.resize(seg, nullptr);
+    hipGraphExec_t& ex = seg == 0 ? ctx->token_exec : ctx->seg_exec[seg - 1];
+    bool ok = false;
+    if (ex) {
+        hipGraphNode_t err_node = nullptr;
+        hipGraphExecUpdateResult res;
+        if (hipGraphExecUpdate(ex, g, &err_node, &res) == hipSuccess && res == hipGraphExecUpdateSuccess)
+            ok = true;
+        else {
+            (void)hipGetLastError();
+            (void)hipGraphExecDestroy(ex);
+            ex = nullptr;
+        }
+    }
+    if (!ok) {
+        hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            ex = nullptr;
+            return nx::hip_fail(ctx, e, "hipGraphInstantiate");
+        }
+    }
+    (void)hipGraphDestroy(g);
+    NX_HIP(ctx, hipGraphLaunch(ex, ctx->stream));
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return NX_OK;
 }
 
 nx_status nx_token_end(nx_ctx* ctx) {
     if (!ctx) return NX_ERR_INVALID;
+    if (ctx->token_flushed) {  // flushed and not resumed: nothing is pending
+        ctx->token_flushed = false;
+        return NX_OK;
+    }
     if (!ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_token_end without nx_token_begin");
-    ctx->capturing = false;
-    hipGraph_t g = nullptr;
-    NX_HIP(ctx, hipStreamEndCapture(ctx->stream, &g));
-    bool ok = false;
-    if (ctx->token_exec) {
-        hipGraphNode_t err_node = nullptr;
-        hipGraphExecUpdateResult res;
-        if (hipGraphExecUpdate(ctx->token_exec, g, &err_node, &res) == hipSuccess &&
-            res == hipGraphExecUpdateSuccess)
-            ok = true;
-        else {
-            (void)hipGetLastError();
-            (void)hipGraphExecDestroy(ctx->token_exec);
-            ctx->token_exec = nullptr;
-        }
-    }
-    if (!ok) {
-        hipError_t e = hipGraphInstantiate(&ctx->token_exec, g, nullptr, nullptr, 0);
-        if (e != hipSuccess) {
-            (void)hipGraphDestroy(g);
-            ctx->token_exec = nullptr;
-            return nx::hip_fail(ctx, e, "hipGraphInstantiate");
-        }
-    }
-    (void)hipGraphDestroy(g);
-    NX_HIP(ctx, hipGraphLaunch(ctx->token_exec, ctx->stream));
-    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return run_segment(ctx);
+}
+
+nx_status nx_token_flush(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->token_flushed) return NX_OK;  // already flushed (as the reference: a no-op)
+    if (!ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_token_flush outside a token batch");
+    nx_status s = run_segment(ctx);
+    if (s != NX_OK) return s;
+    ctx->token_flushed = true;
+    return NX_OK;
+}
+
+nx_status nx_token_resume(nx_ctx* ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return NX_OK;  // not flushed: batching continues (a no-op)
+    if (!ctx->token_flushed) return fail(ctx, NX_ERR_STATE, "nx_token_resume outside a token batch");
+    NX_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->token_flushed = false;
+    ctx->capturing = true;
+    ++ctx->token_seg;
     return NX_OK;
 }
 
@@ -883,16 +922,8 @@ nx_status nx_sample(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch, fl
         return fail(ctx, NX_ERR_UNSUPPORTED, "nx_sample: top_p < 1 needs top_k in (0, 1024]");
     NX_NEED(ctx, logits, (size_t)batch * V * 4, "logits");
     NX_NEED(ctx, out, (size_t)batch * 4, "out");
-    const size_t need = (size_t)batch * V;
-    if (need > ctx->smp_ws_floats) {
-        if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_sample: scratch must grow outside capture");
-        NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        if (ctx->smp_ws) (void)hipFree(ctx->smp_ws);
-        ctx->smp_ws = nullptr;
-        ctx->smp_ws_floats = 0;
-        NX_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->smp_ws), need * sizeof(float)));
-        ctx->smp_ws_floats = need;
-    }
+    nx_status ws = ensure_smp_ws(ctx, (size_t)batch * V);
+    if (ws != NX_OK) return ws;
     nx::SampleArgs a{};
     a.scratch = ctx->smp_ws;
     a.logits = dptr<const float>(logits);
@@ -935,3 +966,184 @@ nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x, const nx_buf* wq, const nx_buf* sc
 }
 
 }  // extern "C"
+
+// ------------------------------------------------- dispatch-layer entries --
+// The remaining ComputeDispatch members the runner calls
+// (hybrid_model.cpp:121, :512-581, :639, :820-1241).
+
+nx_status nx_gemm_f32(nx_ctx* ctx, nx_buf A, nx_buf B, nx_buf C, int M, int N, int K) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (M <= 0 || N <= 0 || K <= 0 || M > 4194240)
+        return fail(ctx, NX_ERR_INVALID, "nx_gemm_f32: bad shape M=%d N=%d K=%d", M, N, K);
+    NX_NEED(ctx, A, (size_t)M * K * 4, "A");
+    NX_NEED(ctx, B, (size_t)K * N * 4, "B");
+    NX_NEED(ctx, C, (size_t)M * N * 4, "C");
+    return launched(ctx, nx::gemm_f32_launch(dptr<const float>(A), dptr<const float>(B), dptr<float>(C), M, N, K,
+                                             ctx->stream),
+                    "gemm_f32");
+}
+
+namespace {
+// Grow-only fp16 activation workspace of nx_ffn_int4_g32.
+nx_status ensure_ffn_ws(nx_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->ffn_ws_bytes) return NX_OK;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "FFN workspace must grow outside capture");
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->ffn_ws) (void)hipFree(ctx->ffn_ws);
+    ctx->ffn_ws = nullptr;
+    ctx->ffn_ws_bytes = 0;
+    NX_HIP(ctx, hipMalloc(&ctx->ffn_ws, bytes));
+    ctx->ffn_ws_bytes = bytes;
+    return NX_OK;
+}
+
+nx_status ensure_smp_ws(nx_ctx* ctx, size_t floats) {
+    if (floats <= ctx->smp_ws_floats) return NX_OK;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "sampler scratch must grow outside capture");
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->smp_ws) (void)hipFree(ctx->smp_ws);
+    ctx->smp_ws = nullptr;
+    ctx->smp_ws_floats = 0;
+    NX_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->smp_ws), floats * sizeof(float)));
+    ctx->smp_ws_floats = floats;
+    return NX_OK;
+}
+
+size_t ffn_lda(int F) { return (size_t)(F + 7) / 8 * 8; }
+}  // namespace
+
+nx_status nx_ffn_int4_g32(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_buf w2, nx_buf s2, nx_buf y, int d,
+                          int F, int batch, int accumulate) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (d <= 0 || F <= 0 || batch < 1 || batch > 8)
+        return fail(ctx, NX_ERR_INVALID, "nx_ffn_int4_g32: bad shape d=%d F=%d batch=%d", d, F, batch);
+    const int Gd = (d + 31) / 32, Gf = (F + 31) / 32;
+    if (Gd > 7 * 64 || Gf > 7 * 64) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_ffn_int4_g32: d or F above 14336");
+    NX_NEED(ctx, x, (size_t)batch * d * 2, "x");
+    NX_NEED(ctx, w13, (size_t)2 * F * Gd * 16, "w13");
+    NX_NEED(ctx, s13, (size_t)2 * F * Gd * 2, "s13");
+    NX_NEED(ctx, w2, (size_t)d * Gf * 16, "w2");
+    NX_NEED(ctx, s2, (size_t)d * Gf * 2, "s2");
+    NX_NEED(ctx, y, (size_t)batch * d * 4, "y");
+    const size_t lda = ffn_lda(F);
+    nx_status s = ensure_ffn_ws(ctx, (size_t)batch * lda * 2);
+    if (s != NX_OK) return s;
+    uint16_t* act = static_cast<uint16_t*>(ctx->ffn_ws);
+    nx::GemvArgs f{};
+    f.W = dptr<const uint8_t>(w13);
+    f.S = dptr<const uint16_t>(s13);
+    f.N = 2 * F;
+    f.K = d;
+    f.G = Gd;
+    f.batch = batch;
+    f.x16 = dptr<const uint16_t>(x);
+    f.ldx = d;
+    f.act16 = act;
+    f.lda = (int)lda;
+    s = launched(ctx, nx::gemv_launch(nx::X_F16, nx::E_SWIGLU, f, ctx->stream), "ffn gate/up");
+    if (s != NX_OK) return s;
+    nx::GemvArgs dn{};
+    dn.W = dptr<const uint8_t>(w2);
+    dn.S = dptr<const uint16_t>(s2);
+    dn.N = d;
+    dn.K = F;
+    dn.G = Gf;
+    dn.batch = batch;
+    dn.x16 = act;
+    dn.ldx = (int)lda;
+    dn.y32 = dptr<float>(y);
+    dn.ldy = d;
+    return launched(ctx, nx::gemv_launch(nx::X_F16, accumulate ? nx::E_ACC : nx::E_F32, dn, ctx->stream), "ffn down");
+}
+
+nx_status nx_init_gpu_pool(nx_ctx* ctx, int hidden, int max_q, int max_kv, int max_ffn, int vocab, int batch,
+                           nx_gpu_pool* out) {
+    if (!ctx || !out) return NX_ERR_INVALID;
+    if (hidden <= 0 || max_q <= 0 || max_kv <= 0 || max_ffn <= 0 || vocab <= 0 || batch < 1 || batch > 8)
+        return fail(ctx, NX_ERR_INVALID, "nx_init_gpu_pool: bad sizes");
+    const size_t B = (size_t)batch;
+    struct Want {
+        nx_buf* dst;
+        size_t bytes;
+    } want[] = {
+        {&out->hidden, B * hidden * 4},  {&out->residual, B * hidden * 4}, {&out->norm, B * hidden * 2},
+        {&out->q, B * max_q * 4},        {&out->k, B * max_kv * 4},        {&out->v, B * max_kv * 4},
+        {&out->attn_out, B * max_q * 2}, {&out->ffn_gate, B * max_ffn * 4}, {&out->ffn_up, B * max_ffn * 4},
+        {&out->ffn_act, B * ffn_lda(max_ffn) * 2}, {&out->ffn_out, B * hidden * 4},
+        {&out->logits, B * vocab * 4},   {&out->token, B * 4},
+    };
+    const int n = (int)(sizeof(want) / sizeof(want[0]));
+    for (int i = 0; i < n; ++i) {
+        nx_status s = nx_alloc(ctx, want[i].bytes, want[i].dst);
+        if (s != NX_OK) {
+            for (int j = 0; j < i; ++j) (void)nx_free(ctx, *want[j].dst);
+            return s;
+        }
+    }
+    return NX_OK;
+}
+
+nx_status nx_init_kv_cache(nx_ctx* ctx, int num_layers, int max_seq, int n_kv_heads, int head_dim, int batch,
+                           nx_buf* kpools, nx_buf* vpools, nx_buf* block_table, int* max_blocks, int* num_blocks) {
+    if (!ctx || !kpools || !vpools || !block_table) return NX_ERR_INVALID;
+    if (num_layers < 1 || max_seq < 1 || n_kv_heads < 1 || (head_dim != 64 && head_dim != 128) || batch < 1 ||
+        batch > 8)
+        return fail(ctx, NX_ERR_INVALID, "nx_init_kv_cache: bad shape");
+    const int mb = (max_seq + nx::kPage - 1) / nx::kPage, nb = batch * mb;
+    const size_t pool = (size_t)nb * n_kv_heads * nx::kPage * head_dim * 2;
+    std::vector<int32_t> bt((size_t)batch * mb);
+    for (int b = 0; b < batch; ++b)
+        for (int p = 0; p < mb; ++p) bt[(size_t)b * mb + p] = b * mb + p;
+    nx_status s = nx_alloc(ctx, bt.size() * 4, block_table);
+    if (s != NX_OK) return s;
+    s = nx_upload(ctx, *block_table, 0, bt.data(), bt.size() * 4);
+    int done = 0;
+    for (; s == NX_OK && done < num_layers; ++done) {
+        s = nx_alloc(ctx, pool, &kpools[done]);
+        if (s != NX_OK) break;
+        s = nx_alloc(ctx, pool, &vpools[done]);
+        if (s != NX_OK) {
+            (void)nx_free(ctx, kpools[done]);
+            break;
+        }
+    }
+    if (s != NX_OK) {
+        for (int j = 0; j < done; ++j) {
+            (void)nx_free(ctx, kpools[j]);
+            (void)nx_free(ctx, vpools[j]);
+        }
+        (void)nx_free(ctx, *block_table);
+        return s;
+    }
+    if (max_blocks) *max_blocks = mb;
+    if (num_blocks) *num_blocks = nb;
+    return NX_OK;
+}
+
+nx_status nx_reserve_workspace(nx_ctx* ctx, int batch, int max_ffn, int vocab, int n_heads, int n_kv_heads,
+                               int head_dim, int max_ctx) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (batch < 1 || batch > 8 || max_ffn < 0 || vocab < 0 || n_heads < 0 || n_kv_heads < 0 || head_dim < 0 ||
+        max_ctx < 0)
+        return fail(ctx, NX_ERR_INVALID, "nx_reserve_workspace: bad sizes");
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_reserve_workspace inside a token batch");
+    nx_status s = NX_OK;
+    if (max_ffn > 0) s = ensure_ffn_ws(ctx, (size_t)batch * ffn_lda(max_ffn) * 2);
+    if (s == NX_OK && vocab > 0) s = ensure_smp_ws(ctx, (size_t)batch * vocab);
+    if (s == NX_OK && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_ctx > 0) {
+        if (n_heads % n_kv_heads) return fail(ctx, NX_ERR_INVALID, "nx_reserve_workspace: n_heads % n_kv_heads");
+        if (max_ctx > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_ctx above the attention limit");
+        s = ensure_attn_ws(ctx, nx::attn_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, max_ctx));
+        if (s == NX_OK) s = ensure_attn_counts(ctx, nx::attn_count_words(batch, n_kv_heads));
+    }
+    if (s == NX_OK) NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return s;
+}
+
+nx_status nx_preload_all_buffers(nx_ctx* ctx, size_t* n_buffers) {
+    if (!ctx) return NX_ERR_INVALID;
+    if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_preload_all_buffers inside a token batch");
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (n_buffers) *n_buffers = ctx->wcache.size();
+    return NX_OK;
+}

@@ -579,6 +579,7 @@ hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st) {
             case E_F16: return launch_gpl<X_F16, E_F16>(a, st);
             case E_F32: return launch_gpl<X_F16, E_F32>(a, st);
             case E_ACC: return launch_gpl<X_F16, E_ACC>(a, st);
+            case E_SWIGLU: return launch_gpl<X_F16, E_SWIGLU>(a, st);
             default: return hipErrorInvalidValue;
         }
     }

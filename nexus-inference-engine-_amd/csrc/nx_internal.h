@@ -8,6 +8,7 @@
 #include <map>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/nexus_hip.h"
 
@@ -19,6 +20,14 @@ struct nx_ctx {
     std::string err;
     bool capturing = false;
     hipGraphExec_t token_exec = nullptr;
+    // token batch split by flush / resume: the graph of each segment after
+    // the first is kept per segment (segment 0 uses token_exec)
+    bool token_flushed = false;
+    int token_seg = 0;
+    std::vector<hipGraphExec_t> seg_exec;
+    // intermediate SwiGLU activations of nx_ffn_int4_g32 (grow-only, fp16)
+    void* ffn_ws = nullptr;
+    size_t ffn_ws_bytes = 0;
     // workspace of the standalone attention entry points
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;

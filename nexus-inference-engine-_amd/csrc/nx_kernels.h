@@ -340,6 +340,9 @@ struct LayerArgs {
 bool attn_block_b1_plan(int d, int hq, int hkv, int hd, int max_ctx, LayerArgs& plan);
 hipError_t attn_block_b1_launch(const LayerArgs& a, hipStream_t st);
 
+// fp32 GEMM C[M][N] = A[M][K] B[K][N], row-major, on the matrix cores (nx_gemm.hip).
+hipError_t gemm_f32_launch(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t st);
+
 // XXH32 (seed 0) of byte ranges of one device buffer: range i is
 // [off, off + len) (off a multiple of 16); its hash goes to out[slot].
 struct HashRange {

@@ -73,6 +73,12 @@ class NxfTensor(C.Structure):
 
 
 _B = C.c_uint64  # nx_buf
+
+
+class GpuPool(C.Structure):
+    """nx_gpu_pool (ComputeDispatch::GPUBufferPool, compute_dispatch.h:137-155)."""
+    _fields_ = [(n, C.c_uint64) for n in ("hidden", "residual", "norm", "q", "k", "v", "attn_out", "ffn_gate",
+                                          "ffn_up", "ffn_act", "ffn_out", "logits", "token")]
 _P = C.c_void_p
 _I = C.c_int
 _F = C.c_float
@@ -94,6 +100,15 @@ _SIGS = {
     "nx_synchronize": (_I, [_P]),
     "nx_token_begin": (_I, [_P]),
     "nx_token_end": (_I, [_P]),
+    "nx_token_flush": (_I, [_P]),
+    "nx_token_resume": (_I, [_P]),
+    "nx_gemm_f32": (_I, [_P, _B, _B, _B, _I, _I, _I]),
+    "nx_ffn_int4_g32": (_I, [_P, _B, _B, _B, _B, _B, _B, _I, _I, _I, _I]),
+    "nx_init_gpu_pool": (_I, [_P, _I, _I, _I, _I, _I, _I, C.POINTER(GpuPool)]),
+    "nx_init_kv_cache": (_I, [_P, _I, _I, _I, _I, _I, C.POINTER(_B), C.POINTER(_B), C.POINTER(_B),
+                              C.POINTER(_I), C.POINTER(_I)]),
+    "nx_reserve_workspace": (_I, [_P, _I, _I, _I, _I, _I, _I, _I]),
+    "nx_preload_all_buffers": (_I, [_P, C.POINTER(C.c_size_t)]),
     "nx_gemv_int4_g32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I]),
     "nx_gemv_int4_g32_f32": (_I, [_P, _B, _B, _B, _B, _I, _I, _I, _I]),
     "nx_unpack_int4": (_I, [_P, _B, _B, C.c_size_t]),
