@@ -253,9 +253,10 @@ nx_status nx_ffn_int4_g32(nx_ctx* ctx, nx_buf x_f16, nx_buf w13, nx_buf s13, nx_
 nx_status nx_argmax(nx_ctx* ctx, nx_buf logits_f32, nx_buf out_i32, int V, int batch);
 /* HybridModel::Impl::sample_token (hybrid_model.cpp:2023-2099) on the device
  * for each of `batch` rows of logits: temperature <= 0 is the greedy argmax;
- * otherwise softmax of logits / T, top-k (0 = off, else at most 1024),
- * top-p (< 1 needs top-k), renormalize, and the first index whose running
- * sum reaches u * sum.  u comes from a fresh MT19937 seeded with `seed` at
+ * otherwise softmax of logits / T, top-k (0 or >= V = off), top-p over what
+ * top-k keeps (1 = off; the entry whose running sum in descending order
+ * first exceeds top_p is kept), renormalize, and the first index whose
+ * running sum reaches u * sum.  u comes from a fresh MT19937 seeded with `seed` at
  * every call, as in the reference (std::uniform_real_distribution<float>
  * as libstdc++ computes it); seed 0 draws from std::random_device.  Ties in
  * the top-k and top-p orders keep the lower index. */

@@ -917,9 +917,6 @@ nx_status nx_sample(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch, fl
     if (temperature <= 0.0f) return nx_argmax(ctx, logits, out, V, batch);
     if (V <= 0 || batch < 1) return fail(ctx, NX_ERR_INVALID, "nx_sample: bad shape");
     if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f) return fail(ctx, NX_ERR_INVALID, "nx_sample: bad parameters");
-    if (top_k > 1024 && top_k < V) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_sample: top_k above 1024");
-    if ((top_k == 0 || top_k >= V) && top_p < 1.0f)
-        return fail(ctx, NX_ERR_UNSUPPORTED, "nx_sample: top_p < 1 needs top_k in (0, 1024]");
     NX_NEED(ctx, logits, (size_t)batch * V * 4, "logits");
     NX_NEED(ctx, out, (size_t)batch * 4, "out");
     nx_status ws = ensure_smp_ws(ctx, (size_t)batch * V);

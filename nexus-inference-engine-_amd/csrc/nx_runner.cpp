@@ -892,9 +892,6 @@ nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float
     const int V = m->c.vocab;
     if (temperature > 0.0f) {
         if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f) return fail(m->ctx, NX_ERR_INVALID, "sampling: bad parameters");
-        if (top_k > 1024 && top_k < V) return fail(m->ctx, NX_ERR_UNSUPPORTED, "sampling: top_k above 1024");
-        if ((top_k == 0 || top_k >= V) && top_p < 1.0f)
-            return fail(m->ctx, NX_ERR_UNSUPPORTED, "sampling: top_p < 1 needs top_k in (0, 1024]");
     }
     if (temperature > 0.0f && !m->smp_scratch) NX_TRY(dalloc(m, &m->smp_scratch, (size_t)m->c.batch * V));
     m->temperature = temperature > 0.0f ? temperature : 0.0f;

@@ -17,10 +17,13 @@
 //    lane takes the running sum in that order; the renormalization and the
 //    draw's scan run over the survivors in index order in one lane, the
 //    reference's own summation order.
-//  - no top-k (k == 0 or k >= V) with top_p = 1: the draw's scan runs over
-//    the vocabulary in wavefront, iteration and lane order with fp32
-//    partial sums in a fixed order.  No top-k with top_p < 1 is refused by
-//    the launcher.
+//  - otherwise (no top-k, or k above 1024; with or without top-p): every
+//    entry is a candidate.  A radix selection by counts finds the k-th
+//    largest p, a radix selection by probability mass (exact 40-bit
+//    fixed-point sums) finds where the running sum in descending order
+//    first exceeds top_p; ties at either value keep the lowest indices.
+//    The draw's scan runs over the kept entries in wavefront, iteration and
+//    lane order with fp32 partial sums in a fixed order.
 // The softmax denominator is a fixed-order block sum; the reference's is a
 // sequential fp32 sum, so probabilities agree to rounding.
 #include "nx_common.h"
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
         }
     }
 
-    if (a.top_k > 0 && a.top_k < V) {
+    if (a.top_k > 0 && a.top_k < V && a.top_k <= kSmpMaxK) {
         // candidates: the entries with e >= exp(-D) for the smallest D whose
         // count is at least k (they hold the top k: p orders as e), if that
         // count fits in LDS; otherwise a radix selection over all of p finds
@@ -387,20 +390,179 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
         }
         __syncthreads();
     } else {
-        // all V kept: running sums per wavefront (64-lane scans, iterations
+        // Every entry is a candidate: no top-k, or top-k above the candidate
+        // list (kSmpMaxK), each with or without top-p.  A top-k cut keeps the
+        // entries above the k-th largest p and, of the entries equal to it,
+        // the lowest indices (radix selection of the k-th value by counts).
+        // A top-p cut keeps, in descending order of p (ties by index), the
+        // entries up to the first whose running sum exceeds top_p (radix
+        // selection of that value by probability mass; the masses are summed
+        // as 40-bit fixed-point integers, exact and independent of order,
+        // where the reference adds fp32 in its sorted order).  The kept
+        // entries are renormalized and drawn from in vocabulary order.
+        const bool use_k = a.top_k > 0 && a.top_k < V;
+        const bool use_p = a.top_p < 1.0f;
+        // --- top-k: the k-th largest p (bits kb) and how many of its ties to keep
+        uint32_t kb = 0;
+        int kneed = 0;
+        if (use_k) {
+            uint32_t prefix = 0, pmask = 0;
+            int need = a.top_k;
+            for (int sh = 24; sh >= 0; sh -= 8) {
+                for (int j2 = tid; j2 < 256; j2 += kSmpThreads) hist[j2] = 0;
+                __syncthreads();
+                smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+                    const uint32_t bits = __builtin_bit_cast(uint32_t, ev / sum_e);
+                    if (ok && (bits & pmask) == prefix) atomicAdd(&hist[(bits >> sh) & 0xFF], 1);
+                });
+                __syncthreads();
+                if (tid == 0) {
+                    int bin = 255, above = 0;
+                    for (; bin > 0; --bin) {
+                        if (above + hist[bin] >= need) break;
+                        above += hist[bin];
+                    }
+                    wi[0][0] = bin;
+                    wi[0][1] = above;
+                }
+                __syncthreads();
+                prefix |= (uint32_t)wi[0][0] << sh;
+                pmask |= 0xFFu << sh;
+                need -= wi[0][1];
+                __syncthreads();
+            }
+            kb = prefix;
+            kneed = need;
+        }
+        // tie ranks in vocabulary order: each wavefront's count of ties, then
+        // the exclusive prefix over the wavefronts (ranks[w])
+        auto wave_base = [&](int cnt, int* base) {
+            cnt = smp_wave_sum(cnt);
+            if (l == 0) base[w] = cnt;
+            __syncthreads();
+            if (tid == 0) {
+                int acc = 0;
+                for (int q = 0; q < kSmpWaves; ++q) {
+                    const int c = base[q];
+                    base[q] = acc;
+                    acc += c;
+                }
+                base[kSmpWaves] = acc;
+            }
+            __syncthreads();
+            return base[w];
+        };
+        int ktb = 0;
+        if (use_k) {
+            int cnt = 0;
+            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+                cnt += ok && __builtin_bit_cast(uint32_t, ev / sum_e) == kb;
+            });
+            ktb = wave_base(cnt, wi[1]);
+        }
+        // keep-by-k of the 64 entries of one step (krun: ties of kb before them)
+        auto kept_k = [&](bool ok, uint32_t bits, int& krun) {
+            const bool tie = ok && use_k && bits == kb;
+            const unsigned long long tm = __ballot(tie);
+            const bool keep = ok && (!use_k || bits > kb || (tie && krun + popc_below(tm, l) < kneed));
+            krun += __popcll(tm);
+            return keep;
+        };
+        // --- top-p over the entries top-k keeps: the value pb at which the
+        // running mass first exceeds top_p, the mass above it, and how many
+        // of its ties to keep
+        __shared__ unsigned long long hmass[256];
+        __shared__ int pinfo[1];
+        bool pcut = false;
+        uint32_t pb = 0;
+        int pneed = 0;
+        if (use_p) {
+            const unsigned long long tp = (unsigned long long)((double)a.top_p * 1099511627776.0);
+            uint32_t prefix = 0, pmask = 0;
+            unsigned long long above = 0;
+            bool cut = true;
+            for (int sh = 24; sh >= 0 && cut; sh -= 8) {
+                for (int j2 = tid; j2 < 256; j2 += kSmpThreads) hmass[j2] = 0ull;
+                __syncthreads();
+                int krun = ktb;
+                smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+                    const float pv = ev / sum_e;
+                    const uint32_t bits = __builtin_bit_cast(uint32_t, pv);
+                    const bool keep = kept_k(ok, bits, krun);
+                    if (keep && (bits & pmask) == prefix)
+                        atomicAdd(&hmass[(bits >> sh) & 0xFF], (unsigned long long)(pv * 1099511627776.0f));
+                });
+                __syncthreads();
+                if (tid == 0) {
+                    int bin = 255;
+                    unsigned long long ab = above;
+                    for (; bin >= 0; --bin) {
+                        if (ab + hmass[bin] > tp) break;
+                        ab += hmass[bin];
+                    }
+                    pinfo[0] = bin;  // -1: the kept mass never exceeds top_p
+                    // mass above the crossing bin, carried in LDS as two words
+                    wi[0][1] = (int)(uint32_t)(ab & 0xFFFFFFFFull);
+                    wi[0][2] = (int)(uint32_t)(ab >> 32);
+                }
+                __syncthreads();
+                const int bin = pinfo[0];
+                if (bin < 0) {
+                    cut = false;
+                } else {
+                    prefix |= (uint32_t)bin << sh;
+                    pmask |= 0xFFu << sh;
+                    above = (unsigned long long)(uint32_t)wi[0][1] | ((unsigned long long)(uint32_t)wi[0][2] << 32);
+                }
+                __syncthreads();
+            }
+            if (cut) {
+                pcut = true;
+                pb = prefix;
+                const unsigned long long unit =
+                    (unsigned long long)(__builtin_bit_cast(float, pb) * 1099511627776.0f);
+                // smallest m >= 1 with above + m * unit > tp
+                pneed = unit > 0 ? (int)min((tp - above) / unit + 1ull, (unsigned long long)V) : V;
+            }
+        }
+        int ptb = 0;
+        if (pcut) {
+            int cnt = 0, krun = ktb;
+            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+                const uint32_t bits = __builtin_bit_cast(uint32_t, ev / sum_e);
+                const bool keep = kept_k(ok, bits, krun);
+                cnt += keep && bits == pb;
+            });
+            ptb = wave_base(cnt, wi[2]);
+        }
+        // the kept p of one step's entry (krun, prun: ties before the step)
+        auto kept_p = [&](bool ok, float ev, int& krun, int& prun) {
+            const float pv = ev / sum_e;
+            const uint32_t bits = __builtin_bit_cast(uint32_t, pv);
+            const bool keep = kept_k(ok, bits, krun);
+            const bool tie = keep && pcut && bits == pb;
+            const unsigned long long tm = __ballot(tie);
+            const bool kp = keep && (!pcut || bits > pb || (tie && prun + popc_below(tm, l) < pneed));
+            prun += __popcll(tm);
+            return kp ? pv : 0.0f;
+        };
+        // --- the draw: running sums per wavefront (64-lane scans, iterations
         // in order), wavefronts in order
         float run = 0.0f;
-        smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
-            const float x = smp_wave_scan(ok ? ev / sum_e : 0.0f);
-            run = run + __shfl(x, 63, 64);
-        });
+        {
+            int krun = ktb, prun = ptb;
+            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int, bool ok, float ev) {
+                const float x = smp_wave_scan(kept_p(ok, ev, krun, prun));
+                run = run + __shfl(x, 63, 64);
+            });
+        }
         if (l == 0) wf[w] = run;
         __syncthreads();
         if (tid == 0) {
             float acc = 0.0f;
-            for (int j = 0; j < kSmpWaves; ++j) {
-                const float t = wf[j];
-                wf[j] = acc;
+            for (int j2 = 0; j2 < kSmpWaves; ++j2) {
+                const float t = wf[j2];
+                wf[j2] = acc;
                 acc = acc + t;
             }
             wf[kSmpWaves] = acc;
@@ -411,10 +573,10 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
         const float r = u * wf[kSmpWaves];
         if (r > 0.0f && base < r && next >= r) {  // this wavefront holds the crossing (exactly one does)
             float rr = 0.0f;
-            int tok = -1, lastnz = -1;
+            int tok = -1, lastnz = -1, krun = ktb, prun = ptb;
             smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int i0, bool ok, float ev) {
+                const float p = kept_p(ok, ev, krun, prun);  // every step: the tie counts advance
                 if (tok >= 0) return;  // uniform: found in an earlier step
-                const float p = ok ? ev / sum_e : 0.0f;
                 const float x = smp_wave_scan(p);
                 const float it = __shfl(x, 63, 64);
                 const unsigned long long nz = __ballot(p > 0.0f);
@@ -440,8 +602,7 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
 }  // namespace
 
 hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st) {
-    if (a.V < 1 || batch < 1 || a.temperature <= 0.0f || a.top_k < 0 || (a.top_k > kSmpMaxK && a.top_k < a.V) ||
-        !(a.top_p > 0.0f) || ((a.top_k == 0 || a.top_k >= a.V) && a.top_p < 1.0f) ||
+    if (a.V < 1 || batch < 1 || a.temperature <= 0.0f || a.top_k < 0 || !(a.top_p > 0.0f) || a.top_p > 1.0f ||
         (a.u_fixed < 0.0f && !a.u && !a.pos) || !a.scratch)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_sample, dim3(batch), dim3(kSmpThreads), 0, st, a);
