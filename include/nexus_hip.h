@@ -363,6 +363,46 @@ nx_status nx_model_set_prefill(nx_model* m, int batched);
  * fused form whose in-launch hand-off times out makes nx_model_decode /
  * nx_model_prefill return NX_ERR_TIMEOUT. */
 nx_status nx_model_set_fused(nx_model* m, int on);
+/* The configuration the model was created with. */
+nx_status nx_model_get_config(nx_model* m, nx_model_config* out);
+/* The context the model runs on. */
+nx_ctx* nx_model_context(nx_model* m);
+
+/* Sequence slots.  Each of the `batch` slots holds one sequence (active) or
+ * none (free).  nx_model_prefill and nx_model_fill_context make every slot
+ * active; nx_model_decode advances the active slots only (a free slot's
+ * output tokens are -1, and the step computes nothing it keeps).  The
+ * reference serves one request per Engine::generate
+ * (nexus/src/core/engine.cpp:124-184); these let sequences of different
+ * prompt lengths join and leave a batch between decode calls.
+ * nx_model_admit: sequence `slot` starts over with prompt[P] (any P below
+ * max_seq): the prompt is prefilled into that slot alone -- batched GEMMs
+ * where the model allows it, otherwise one step per prompt token during
+ * which the other active sequences are held (they compute a position they
+ * have not reached and keep their state) -- and its first generated token
+ * is written to next_token (optional).  nx_model_retire frees a slot. */
+nx_status nx_model_admit(nx_model* m, int slot, const int32_t* prompt, int P, int32_t* next_token);
+nx_status nx_model_retire(nx_model* m, int slot);
+nx_status nx_model_slot_active(nx_model* m, int slot, int* active);
+
+/* Request scheduler over a model's slots (the serving loop of
+ * Engine::generate, engine.cpp:124-184, for many requests): requests wait
+ * in arrival order and are admitted into free slots; active slots decode in
+ * chunks of up to 8 steps; a request completes after max_new tokens (its
+ * first is the token after the prompt) or once it emits `stop` (-1: none),
+ * and its slot goes to the next waiting request.  Creating a scheduler
+ * frees every slot of the model. */
+typedef struct nx_sched nx_sched;
+nx_status nx_sched_create(nx_model* m, nx_sched** out);
+nx_status nx_sched_destroy(nx_sched* s);
+nx_status nx_sched_submit(nx_sched* s, const int32_t* prompt, int P, int max_new, int stop, int* id);
+/* One round: admit what fits, decode one chunk, retire what completed. */
+nx_status nx_sched_step(nx_sched* s, int* n_active, int* n_waiting);
+/* Rounds until no request is waiting or active. */
+nx_status nx_sched_run(nx_sched* s);
+/* The tokens of request id so far (up to cap into out), their number and
+ * whether the request is complete. */
+nx_status nx_sched_result(nx_sched* s, int id, int32_t* out, int cap, int* n, int* done);
 /* Sampling of the decode loop (SamplingParams, core/config.h:60-66):
  * temperature <= 0 = greedy (the default); otherwise every step samples
  * with nx_sample's rules inside the step graph.  seed != 0: the draw of

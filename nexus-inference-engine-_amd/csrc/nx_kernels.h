@@ -210,9 +210,17 @@ void tq_set_codebooks(const float* c4, const float* b4, const float* c3, const f
 // when that index is in [0, out_stride).
 // epoch (optional): a step counter the embedding kernel increments once per
 // launch; the fused attention block counts its hand-offs against it.
+// feed (optional, [batch]): what each sequence slot consumes at this step --
+// kFeedDecode its pending token (recorded as output), a token id >= 0 (a
+// prompt token, not recorded), kFeedPark (a free slot: token 0 at position
+// 0) or kFeedHold (a paused sequence: token 0 at position fpos[b], one it
+// has not reached, so nothing it holds is overwritten).  Both parked and
+// held slots leave pos[b] at that position, for the host to restore.
+constexpr int kFeedDecode = -1, kFeedPark = -2, kFeedHold = -3;
 hipError_t embed_launch(unsigned long long* best, int32_t* pos, const int32_t* base,
                         int32_t* out_tokens, int out_stride, const uint16_t* embed, float* h,
-                        int d, int vocab, int batch, hipStream_t st, unsigned* epoch = nullptr);
+                        int d, int vocab, int batch, hipStream_t st, unsigned* epoch = nullptr,
+                        const int32_t* feed = nullptr, const int32_t* fpos = nullptr);
 // Record the pending tokens (decoded from best) at out_tokens[b][pos[b] - base[b]].
 hipError_t finish_tokens_launch(const unsigned long long* best, const int32_t* pos,
                                 const int32_t* base, int32_t* out_tokens, int out_stride,

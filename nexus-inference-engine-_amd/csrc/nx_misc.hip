@@ -207,20 +207,32 @@ __global__ void k_gen_ctx_raw(float* dst, int ctx, int hkv, int hd, uint64_t key
 __global__ __launch_bounds__(256) void k_embed(unsigned long long* best, int32_t* pos,
                                                const int32_t* base, int32_t* out_tokens,
                                                int out_stride, const uint16_t* embed, float* h,
-                                               int d, int vocab, unsigned* epoch) {
+                                               int d, int vocab, unsigned* epoch, const int32_t* feed,
+                                               const int32_t* fpos) {
     __shared__ int tok_s;
     const int b = blockIdx.x;
     if (b == 0 && threadIdx.x == 0 && epoch) *epoch += 1u;
     if (threadIdx.x == 0) {
-        const unsigned long long k = best[b];
-        int tok = (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+        const int f = feed ? feed[b] : kFeedDecode;
+        int tok, p;
+        if (f == kFeedPark) {  // a free slot: token 0 at position 0 of its own pages
+            tok = 0;
+            p = 0;
+        } else if (f == kFeedHold) {  // a paused sequence: a position it has not reached yet
+            tok = 0;
+            p = fpos[b];
+        } else {
+            const unsigned long long k = best[b];
+            tok = f >= 0 ? f : (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+            p = pos[b] + 1;
+            const int idx = p - base[b] - 1;
+            if (f == kFeedDecode && out_tokens && idx >= 0 && idx < out_stride)
+                out_tokens[(size_t)b * out_stride + idx] = tok;
+        }
         if (tok < 0 || tok >= vocab) tok = 0;  // never index outside the table
         tok_s = tok;
         best[b] = 0ull;
-        const int p = pos[b] + 1;
         pos[b] = p;
-        const int idx = p - base[b] - 1;
-        if (out_tokens && idx >= 0 && idx < out_stride) out_tokens[(size_t)b * out_stride + idx] = tok;
     }
     __syncthreads();
     const int tok = tok_s;
@@ -574,9 +586,10 @@ hipError_t gen_ctx_raw_launch(float* dst, int ctx, int hkv, int hd, int L, int b
 
 hipError_t embed_launch(unsigned long long* best, int32_t* pos, const int32_t* base,
                         int32_t* out_tokens, int out_stride, const uint16_t* embed, float* h,
-                        int d, int vocab, int batch, hipStream_t st, unsigned* epoch) {
+                        int d, int vocab, int batch, hipStream_t st, unsigned* epoch, const int32_t* feed,
+                        const int32_t* fpos) {
     hipLaunchKernelGGL(k_embed, dim3(batch), dim3(256), 0, st, best, pos, base, out_tokens,
-                       out_stride, embed, h, d, vocab, epoch);
+                       out_stride, embed, h, d, vocab, epoch, feed, fpos);
     return hipGetLastError();
 }
 

@@ -105,6 +105,13 @@ struct nx_model {
     unsigned* lsync = nullptr;     // [n_layers][hkv + 1][kAttnCountStride]
     unsigned* lstate = nullptr;    // [0] epoch, [64] error word
     unsigned* h_err = nullptr;     // pinned host copy of the error word
+    // per-slot serving state: a slot holds one sequence (active) or none
+    // (free: parked at position 0 by the step graph); feed / fpos tell the
+    // embedding kernel what each slot consumes at a step (kFeed*)
+    std::vector<char> active;
+    int32_t* feed = nullptr;     // device [batch]
+    int32_t* fpos = nullptr;     // device [batch]
+    int32_t* h_feed = nullptr;   // pinned host [2 * batch]: feed then fpos
 };
 
 namespace {
@@ -356,13 +363,35 @@ nx_status check_fused_state(nx_model* m) {
     return fail(m->ctx, NX_ERR_TIMEOUT, "fused attention block: a wait between blocks timed out; the step's outputs are invalid");
 }
 
+// What each slot consumes at the following steps: feed[b] (a kFeed* mode or
+// a token id) and fpos[b] (the position of a held slot); stream ordered.
+nx_status upload_feed(nx_model* m, const int32_t* feed, const int32_t* fpos) {
+    const int B = m->c.batch;
+    for (int b = 0; b < B; ++b) {
+        m->h_feed[b] = feed[b];
+        m->h_feed[B + b] = fpos ? fpos[b] : 0;
+    }
+    NX_HIP(m->ctx, hipMemcpyAsync(m->feed, m->h_feed, (size_t)B * 4, hipMemcpyHostToDevice, m->ctx->stream));
+    NX_HIP(m->ctx, hipMemcpyAsync(m->fpos, m->h_feed + B, (size_t)B * 4, hipMemcpyHostToDevice, m->ctx->stream));
+    // the pinned staging is rewritten by the next call
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return NX_OK;
+}
+
+// Active slots decode, free slots are parked.
+nx_status feed_decode(nx_model* m) {
+    std::vector<int32_t> f((size_t)m->c.batch);
+    for (int b = 0; b < m->c.batch; ++b) f[(size_t)b] = m->active[(size_t)b] ? nx::kFeedDecode : nx::kFeedPark;
+    return upload_feed(m, f.data(), nullptr);
+}
+
 // One decode step for every sequence, enqueued on the context stream.
 nx_status enqueue_step(nx_model* m) {
     const nx_model_config& c = m->c;
     hipStream_t st = m->ctx->stream;
     const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts;
     NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d,
-                                  c.vocab, B, st, m->fused ? m->lstate : nullptr));
+                                  c.vocab, B, st, m->fused ? m->lstate : nullptr, m->feed, m->fpos));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
         if (m->fused) {
@@ -526,6 +555,7 @@ nx_status free_model(nx_model* m) {
     if (m->h_stage) (void)hipHostFree(m->h_stage);
     if (m->h_out) (void)hipHostFree(m->h_out);
     if (m->h_err) (void)hipHostFree(m->h_err);
+    if (m->h_feed) (void)hipHostFree(m->h_feed);
     delete m;
     return NX_OK;
 }
@@ -670,6 +700,11 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         NX_HIP(m->ctx, hipMemcpyAsync(m->pos, minus1.data(), (size_t)B * 4, hipMemcpyHostToDevice, m->ctx->stream));
         NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     }
+    NX_TRY(dalloc(m, &m->feed, (size_t)B));
+    NX_TRY(dalloc(m, &m->fpos, (size_t)B));
+    NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_feed, sizeof(int32_t) * 2 * B, hipHostMallocDefault));
+    m->active.assign((size_t)B, 1);
+    NX_TRY(feed_decode(m));
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_stage, sizeof(int32_t) * B, hipHostMallocDefault));
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_out, sizeof(int32_t) * (size_t)B * m->out_stride, hipHostMallocDefault));
     // the fused attention block where the shape allows it (on by default)
@@ -938,12 +973,14 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
             if (prompt[(size_t)b * P + i] < 0 || prompt[(size_t)b * P + i] >= c.vocab)
                 return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
     }
+    for (int b = 0; b < B; ++b) m->active[(size_t)b] = 1;
     if (m->prefill_batched && c.n_experts == 0 && c.kv_kind == 0) {
         for (int b = 0; b < B; ++b) NX_TRY(prefill_batched(m, b, prompt + (size_t)b * P, P));
         if (next_tokens) NX_TRY(nx_model_pending(m, next_tokens));
         return NX_OK;
     }
     NX_TRY(ensure_graph(m));
+    NX_TRY(feed_decode(m));
     hipStream_t st = m->ctx->stream;
     // token-major copy of the prompt: prompt_dev[i][b]
     std::vector<int32_t> tm((size_t)P * B);
@@ -1022,7 +1059,10 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
     NX_HIP(m->ctx, hipMemcpyAsync(m->prompt, start.data(), (size_t)B * 4, hipMemcpyHostToDevice, st));
     NX_LAUNCH(m, nx::set_tokens_launch(m->best, m->prompt, B, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
-    for (int b = 0; b < B; ++b) m->hpos[b] = ctx_len - 1;
+    for (int b = 0; b < B; ++b) {
+        m->hpos[b] = ctx_len - 1;
+        m->active[(size_t)b] = 1;
+    }
     // the scratch buffers are released with the model; drop them now
     for (void* ptr : {static_cast<void*>(och), static_cast<void*>(raw)}) {
         if (!ptr) continue;
@@ -1091,14 +1131,19 @@ nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
     if (!m || steps < 1) return NX_ERR_INVALID;
     const nx_model_config& c = m->c;
     const int B = c.batch;
+    int nact = 0;
     for (int b = 0; b < B; ++b) {
+        if (!m->active[b]) continue;
+        ++nact;
         if (m->hpos[b] < 0) return fail(m->ctx, NX_ERR_STATE, "decode before prefill or fill_context");
         if (m->hpos[b] + steps >= c.max_seq) return fail(m->ctx, NX_ERR_CAPACITY, "decode exceeds max_seq");
     }
+    if (nact == 0) return fail(m->ctx, NX_ERR_STATE, "decode with no active sequence");
     if (steps > m->out_stride) return fail(m->ctx, NX_ERR_CAPACITY, "too many steps for one call");
     NX_TRY(ensure_graph(m));
+    NX_TRY(feed_decode(m));
     hipStream_t st = m->ctx->stream;
-    for (int b = 0; b < B; ++b) m->h_stage[b] = m->hpos[b] + 1;
+    for (int b = 0; b < B; ++b) m->h_stage[b] = m->active[b] ? m->hpos[b] + 1 : 1 << 30;
     NX_HIP(m->ctx, hipMemcpyAsync(m->base, m->h_stage, (size_t)B * 4, hipMemcpyHostToDevice, st));
     int s = 0;
     for (; s + kStepsPerGraph <= steps; s += kStepsPerGraph) NX_HIP(m->ctx, hipGraphLaunch(m->exec_multi, st));
@@ -1109,9 +1154,97 @@ nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
     NX_HIP(m->ctx, hipStreamSynchronize(st));
     NX_TRY(check_fused_state(m));
     for (int b = 0; b < B; ++b) {
-        m->hpos[b] += steps;
-        if (out_tokens)
+        if (m->active[b]) m->hpos[b] += steps;
+        if (!out_tokens) continue;
+        if (m->active[b])
             std::memcpy(out_tokens + (size_t)b * steps, m->h_out + (size_t)b * m->out_stride, (size_t)steps * 4);
+        else
+            std::fill(out_tokens + (size_t)b * steps, out_tokens + (size_t)(b + 1) * steps, -1);
+    }
+    return NX_OK;
+}
+
+nx_status nx_model_get_config(nx_model* m, nx_model_config* out) {
+    if (!m || !out) return NX_ERR_INVALID;
+    *out = m->c;
+    return NX_OK;
+}
+
+nx_ctx* nx_model_context(nx_model* m) { return m ? m->ctx : nullptr; }
+
+nx_status nx_model_retire(nx_model* m, int slot) {
+    if (!m || slot < 0 || slot >= m->c.batch) return NX_ERR_INVALID;
+    m->active[(size_t)slot] = 0;
+    return NX_OK;
+}
+
+nx_status nx_model_slot_active(nx_model* m, int slot, int* active) {
+    if (!m || !active || slot < 0 || slot >= m->c.batch) return NX_ERR_INVALID;
+    *active = m->active[(size_t)slot] ? 1 : 0;
+    return NX_OK;
+}
+
+nx_status nx_model_admit(nx_model* m, int slot, const int32_t* prompt, int P, int32_t* next_token) {
+    if (!m || !prompt || P < 1 || slot < 0 || slot >= m->c.batch) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    const int B = c.batch;
+    if (P >= c.max_seq) return fail(m->ctx, NX_ERR_CAPACITY, "admit: prompt of %d exceeds max_seq", P);
+    for (int i = 0; i < P; ++i)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab) return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
+    hipStream_t st = m->ctx->stream;
+    // the slot starts over: position -1, its pages are overwritten from position 0
+    m->active[(size_t)slot] = 0;
+    m->hpos[(size_t)slot] = -1;
+    const int32_t minus1 = -1;
+    NX_HIP(m->ctx, hipMemcpyAsync(m->pos + slot, &minus1, 4, hipMemcpyHostToDevice, st));
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    if (m->prefill_batched && c.n_experts == 0 && c.kv_kind == 0) {
+        // the slot's prompt alone through the batched prefill
+        NX_TRY(prefill_batched(m, slot, prompt, P));
+    } else {
+        // one step per prompt token for this slot; the other active sequences
+        // are held (each step writes a position they have not reached, and
+        // their pending tokens are put back), free slots are parked
+        std::vector<int32_t> feed((size_t)B), fpos((size_t)B, 0);
+        for (int b = 0; b < B; ++b) {
+            const bool hold = b != slot && m->active[(size_t)b] && m->hpos[(size_t)b] >= 0;
+            if (hold && m->hpos[(size_t)b] + 1 >= c.max_seq)
+                return fail(m->ctx, NX_ERR_CAPACITY, "admit: sequence in slot %d is at max_seq", b);
+            feed[(size_t)b] = hold ? nx::kFeedHold : nx::kFeedPark;
+            fpos[(size_t)b] = hold ? m->hpos[(size_t)b] + 1 : 0;
+        }
+        NX_TRY(ensure_graph(m));
+        std::vector<unsigned long long> saved((size_t)B);
+        NX_HIP(m->ctx, hipMemcpyAsync(saved.data(), m->best, (size_t)B * 8, hipMemcpyDeviceToHost, st));
+        for (int b = 0; b < B; ++b) m->h_stage[b] = 1 << 30;  // nothing is recorded
+        NX_HIP(m->ctx, hipMemcpyAsync(m->base, m->h_stage, (size_t)B * 4, hipMemcpyHostToDevice, st));
+        for (int i = 0; i < P; ++i) {
+            feed[(size_t)slot] = prompt[i];
+            NX_TRY(upload_feed(m, feed.data(), fpos.data()));
+            NX_HIP(m->ctx, hipGraphLaunch(m->exec, st));
+        }
+        // held and parked slots go back to where they were
+        std::vector<unsigned long long> best((size_t)B);
+        NX_HIP(m->ctx, hipMemcpyAsync(best.data(), m->best, (size_t)B * 8, hipMemcpyDeviceToHost, st));
+        NX_HIP(m->ctx, hipStreamSynchronize(st));
+        NX_TRY(check_fused_state(m));
+        std::vector<int32_t> pos((size_t)B);
+        for (int b = 0; b < B; ++b) {
+            pos[(size_t)b] = b == slot ? P - 1 : m->hpos[(size_t)b];
+            if (b != slot) best[(size_t)b] = saved[(size_t)b];
+        }
+        NX_HIP(m->ctx, hipMemcpyAsync(m->pos, pos.data(), (size_t)B * 4, hipMemcpyHostToDevice, st));
+        NX_HIP(m->ctx, hipMemcpyAsync(m->best, best.data(), (size_t)B * 8, hipMemcpyHostToDevice, st));
+        NX_HIP(m->ctx, hipStreamSynchronize(st));
+        m->hpos[(size_t)slot] = P - 1;
+    }
+    m->active[(size_t)slot] = 1;
+    NX_TRY(feed_decode(m));
+    if (next_token) {
+        unsigned long long k = 0;
+        NX_HIP(m->ctx, hipMemcpyAsync(&k, m->best + slot, 8, hipMemcpyDeviceToHost, st));
+        NX_HIP(m->ctx, hipStreamSynchronize(st));
+        *next_token = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
     }
     return NX_OK;
 }

@@ -137,6 +137,17 @@ _SIGS = {
     "nx_model_prefill": (_I, [_P, _P, _I, _P]),
     "nx_model_set_prefill": (_I, [_P, _I]),
     "nx_model_set_fused": (_I, [_P, _I]),
+    "nx_model_get_config": (_I, [_P, C.POINTER(ModelConfig)]),
+    "nx_model_context": (_P, [_P]),
+    "nx_model_admit": (_I, [_P, _I, _P, _I, C.POINTER(C.c_int32)]),
+    "nx_model_retire": (_I, [_P, _I]),
+    "nx_model_slot_active": (_I, [_P, _I, C.POINTER(_I)]),
+    "nx_sched_create": (_I, [_P, C.POINTER(_P)]),
+    "nx_sched_destroy": (_I, [_P]),
+    "nx_sched_submit": (_I, [_P, _P, _I, _I, _I, C.POINTER(_I)]),
+    "nx_sched_step": (_I, [_P, C.POINTER(_I), C.POINTER(_I)]),
+    "nx_sched_run": (_I, [_P]),
+    "nx_sched_result": (_I, [_P, _I, _P, _I, C.POINTER(_I), C.POINTER(_I)]),
     "nx_model_fill_context": (_I, [_P, _I, _I]),
     "nx_model_kv_read": (_I, [_P, _I, _I, _I, _I, C.POINTER(C.c_int), _P, C.c_size_t]),
     "nx_model_pending": (_I, [_P, _P]),
@@ -384,6 +395,23 @@ class Model:
     def decode_untimed(self, steps: int):
         self.ctx.check(self.ctx.L.nx_model_decode(self.h, steps, None), "nx_model_decode")
 
+    def admit(self, slot: int, prompt) -> int:
+        """Sequence `slot` starts over with this prompt (nx_model_admit);
+        returns its first generated token."""
+        p = np.ascontiguousarray(prompt, np.int32).reshape(-1)
+        nxt = C.c_int32()
+        self.ctx.check(self.ctx.L.nx_model_admit(self.h, slot, p.ctypes.data, p.size, C.byref(nxt)),
+                       "nx_model_admit")
+        return int(nxt.value)
+
+    def retire(self, slot: int):
+        self.ctx.check(self.ctx.L.nx_model_retire(self.h, slot), "nx_model_retire")
+
+    def slot_active(self, slot: int) -> bool:
+        a = C.c_int()
+        self.ctx.check(self.ctx.L.nx_model_slot_active(self.h, slot, C.byref(a)), "nx_model_slot_active")
+        return bool(a.value)
+
     def logits(self) -> np.ndarray:
         out = np.empty((self.cfg.batch, self.cfg.vocab), np.float32)
         self.ctx.check(self.ctx.L.nx_model_logits(self.h, out.ctypes.data), "nx_model_logits")
@@ -410,3 +438,43 @@ class Model:
         self.ctx.check(self.ctx.L.nx_model_time_attention(self.h, iters, C.byref(ms), C.byref(nb)),
                        "nx_model_time_attention")
         return ms.value, nb.value
+
+
+class Scheduler:
+    """nx_sched: requests admitted into a model's free slots in arrival
+    order, decoded together, retired when complete."""
+
+    def __init__(self, model: Model):
+        self.model = model
+        self.L = model.ctx.L
+        h = C.c_void_p()
+        model.ctx.check(self.L.nx_sched_create(model.h, C.byref(h)), "nx_sched_create")
+        self.h = h
+
+    def submit(self, prompt, max_new: int, stop: int = -1) -> int:
+        p = np.ascontiguousarray(prompt, np.int32).reshape(-1)
+        rid = C.c_int()
+        self.model.ctx.check(self.L.nx_sched_submit(self.h, p.ctypes.data, p.size, max_new, stop, C.byref(rid)),
+                             "nx_sched_submit")
+        return int(rid.value)
+
+    def step(self):
+        a, w = C.c_int(), C.c_int()
+        self.model.ctx.check(self.L.nx_sched_step(self.h, C.byref(a), C.byref(w)), "nx_sched_step")
+        return int(a.value), int(w.value)
+
+    def run(self):
+        self.model.ctx.check(self.L.nx_sched_run(self.h), "nx_sched_run")
+
+    def result(self, rid: int):
+        n, done = C.c_int(), C.c_int()
+        self.model.ctx.check(self.L.nx_sched_result(self.h, rid, None, 0, C.byref(n), C.byref(done)), "result")
+        out = np.empty(n.value, np.int32)
+        self.model.ctx.check(self.L.nx_sched_result(self.h, rid, out.ctypes.data, n.value, C.byref(n),
+                                                    C.byref(done)), "nx_sched_result")
+        return out, bool(done.value)
+
+    def close(self):
+        if self.h:
+            self.L.nx_sched_destroy(self.h)
+            self.h = None

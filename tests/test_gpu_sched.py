@@ -1,0 +1,105 @@
+"""Sequences joining and leaving a batch (nx_model_admit / nx_model_retire)
+and the request scheduler (nx_sched) on the GPU: every sequence's greedy
+tokens equal the oracle's for that sequence decoded alone, whatever its
+prompt length, the slot it lands in and what the other slots do meanwhile."""
+import numpy as np
+import pytest
+
+import nexus_amd
+import oracle
+from test_gpu_model import TINY, assert_greedy_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def standalone(cfg, prompt, n):
+    om = oracle.Model(**dict(cfg, batch=1))
+    want, margins = om.generate(np.asarray(prompt, np.int32)[None, :], n)
+    om.close()
+    return want[0], margins[0]
+
+
+def prompts(cfg, lens):
+    return [oracle.prompt_tokens(cfg["seed"] + 17 * i + 1, 1, n, cfg["vocab"])[0] for i, n in enumerate(lens)]
+
+
+CFGS = {
+    "dense": dict(TINY, batch=3, max_seq=128, seed=0x5C01),
+    "dense-steps": dict(TINY, batch=3, max_seq=128, seed=0x5C02),
+    "moe": dict(TINY, batch=3, max_seq=128, n_experts=4, top_k=2, seed=0x5C03),
+    "turboquant": dict(TINY, batch=3, max_seq=128, n_heads=4, n_kv_heads=1, head_dim=128, d_model=512,
+                       kv_kind=1, seed=0x5C04),
+}
+
+
+@pytest.mark.parametrize("kind", sorted(CFGS))
+def test_admit_and_retire_mid_decode(ctx, kind):
+    """A joins slot 0; after 6 steps B joins slot 1; after 5 more A leaves
+    and C joins slot 0; slot 2 stays free throughout.  Dense models prefill
+    an admitted prompt as a batched GEMM pass ("dense-steps" turns that off),
+    the others one step per prompt token while the other sequences are held."""
+    cfg = CFGS[kind]
+    print(f"[case] {kind}", flush=True)
+    A, B, C = prompts(cfg, [5, 9, 3])
+    gm = nexus_amd.Model(ctx, **cfg)
+    if kind == "dense-steps":
+        gm.set_prefill(False)
+    for s in range(3):
+        gm.retire(s)
+    got = {"A": [gm.admit(0, A)], "B": [], "C": []}
+    out = gm.decode(6)
+    got["A"] += out[0].tolist()
+    assert (out[1] == -1).all() and (out[2] == -1).all()
+    got["B"].append(gm.admit(1, B))
+    out = gm.decode(5)
+    got["A"] += out[0].tolist()
+    got["B"] += out[1].tolist()
+    gm.retire(0)
+    assert not gm.slot_active(0) and gm.slot_active(1)
+    got["C"].append(gm.admit(0, C))
+    out = gm.decode(7)
+    got["B"] += out[1].tolist()
+    got["C"] += out[0].tolist()
+    assert (out[2] == -1).all()
+    gm.close()
+    for name, p in (("A", A), ("B", B), ("C", C)):
+        want, margins = standalone(cfg, p, len(got[name]))
+        assert_greedy_parity(np.array([got[name]]), want[None, :], margins[None, :])
+
+
+def test_scheduler_serves_requests_in_two_slots(ctx):
+    """Five requests of different prompt lengths and token counts through two
+    slots, one of them stopping at a token it emits; each request's tokens
+    equal the oracle's for it alone."""
+    cfg = dict(TINY, batch=2, max_seq=128, seed=0x5C05)
+    lens, counts = [4, 11, 6, 2, 9], [7, 3, 10, 5, 6]
+    ps = prompts(cfg, lens)
+    wants = [standalone(cfg, p, n) for p, n in zip(ps, counts)]
+    stop = int(wants[2][0][2])  # request 2 stops at the third token it emits (first occurrence)
+    first = int(np.nonzero(wants[2][0] == stop)[0][0])
+    gm = nexus_amd.Model(ctx, **cfg)
+    sched = nexus_amd.Scheduler(gm)
+    ids = [sched.submit(p, n, stop if i == 2 else -1) for i, (p, n) in enumerate(zip(ps, counts))]
+    sched.run()
+    for i, rid in enumerate(ids):
+        out, done = sched.result(rid)
+        assert done
+        want, margins = wants[i]
+        n = first + 1 if i == 2 else counts[i]
+        assert len(out) == n, (i, len(out), n)
+        assert_greedy_parity(out[None, :], want[None, :n], margins[None, :n])
+    sched.close()
+    gm.close()
+
+
+def test_scheduler_rejects_what_cannot_fit(ctx):
+    cfg = dict(TINY, batch=2, max_seq=32, seed=0x5C06)
+    gm = nexus_amd.Model(ctx, **cfg)
+    sched = nexus_amd.Scheduler(gm)
+    with pytest.raises(nexus_amd.NxError) as e:
+        sched.submit(np.zeros(20, np.int32), 20)
+    assert e.value.code == 7
+    with pytest.raises(nexus_amd.NxError):
+        sched.submit(np.array([cfg["vocab"]], np.int32), 2)
+    sched.close()
+    gm.close()
