@@ -65,7 +65,7 @@ MIXTRAL = dict(LLAMA8B, vocab=32000, n_experts=8, top_k=2, rope_theta=1000000.0)
 MODELS = {"llama-8b": LLAMA8B, "mixtral-8x7b": MIXTRAL}
 
 
-def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window: int = 0) -> dict:
+def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window: int = 0, reps: int = 3) -> dict:
     """Time the oracle's decode step on a bounded sample and scale to a token."""
     import numpy as np
 
@@ -77,7 +77,7 @@ def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window:
     m.fill_context(ctx_len, 4 if kv_kind else 0)
     tok = np.zeros(batch, np.int32)
     m.forward_timed(tok)  # warm caches
-    reps, tl, th = 3, 0.0, 0.0
+    tl, th = 0.0, 0.0
     for _ in range(reps):
         _, a, b = m.forward_timed(tok)
         tl += a
@@ -89,6 +89,114 @@ def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window:
             "cores": int(oracle.lib.nxo_num_threads()), "kind": "port",
             "sample": (f"oracle decode step of one {shape} layer at ctx {ctx_len} ({reps} reps) "
                        f"+ lm_head rows 1/{vocab_frac}, scaled to {base['n_layers']} layers + full lm_head")}
+
+
+TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=688, vocab=4096,
+            n_experts=0, top_k=0, batch=1, kv_kind=0, rope_theta=10000.0, eps=1e-5, seed=0x5EED)
+
+
+def seeded_prompt(seed: int, batch: int, P: int, vocab: int):
+    """Uniform token ids in [4, vocab) from a seeded generator."""
+    import numpy as np
+    return np.random.default_rng(seed).integers(4, vocab, (batch, P), dtype=np.int32)
+
+
+def cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def with_threads(n: int, fn):
+    """fn() with the oracle's OpenMP pool at n threads (0: all), restored after."""
+    import oracle
+    before = int(oracle.lib.nxo_num_threads())
+    if n > 0:
+        oracle.lib.nxo_set_num_threads(n)
+    try:
+        return fn()
+    finally:
+        oracle.lib.nxo_set_num_threads(before)
+
+
+def cpu_baselines(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window: int) -> dict:
+    """The oracle on the host at all cores and at one core: the main
+    workload (bounded sample, scaled to a token), the tiny model's full
+    greedy decode (config 1) and the five GEMV shapes at batch 1 and 8
+    (config 2, one product each)."""
+    import numpy as np
+
+    import oracle
+    allc = int(oracle.lib.nxo_num_threads())
+    out = {"cpu_model": cpu_model_name(), "cores_all": allc}
+    out["decode_1core"] = with_threads(1, lambda: cpu_baseline(base, ctx_len, batch, kv_kind, hot_window, reps=1))
+
+    def tiny():
+        m = oracle.Model(**dict(TINY, max_seq=128))
+        prompt = seeded_prompt(TINY["seed"], 1, 16, TINY["vocab"])
+        t0 = time.perf_counter()
+        m.generate(prompt, 64)
+        dt = time.perf_counter() - t0
+        m.close()
+        return round(64 / dt, 2)
+    out["tiny_decode"] = {"workload": "tiny Llama (2 layers, d 256), 16-token prompt + 64 greedy tokens",
+                          "unit": "tok/s", "all_cores": with_threads(0, tiny), "one_core": with_threads(1, tiny)}
+    rng = np.random.default_rng(0)
+    gem = []
+    for N, K in GEMV_SHAPES:
+        G = (K + 31) // 32
+        codes = rng.integers(0, 256, (N, G * 16), dtype=np.uint8)
+        scales = np.full((N, G), 0x2000, np.uint16)  # fp16 2^-7
+        row = {"shape": f"{N}x{K}"}
+        for B in (1, 8):
+            x = rng.standard_normal((B, K)).astype(np.float32)
+            nbytes = N * K * 0.5625 + B * (2 * K + 2 * N)
+            for tag, n in (("all", 0), ("1core", 1)):
+                def one():
+                    t0 = time.perf_counter()
+                    oracle.gemv(codes, scales, x, N, K)
+                    return time.perf_counter() - t0
+                dt = with_threads(n, one)
+                row[f"b{B}_{tag}_us"] = round(dt * 1e6, 1)
+                row[f"b{B}_{tag}_GBps"] = round(nbytes / dt / 1e9, 2)
+        gem.append(row)
+    out["gemv"] = gem
+    return out
+
+
+def decode_line(ctx, base: dict, name: str, batch: int, kv_kind: int, ctx_len: int, steps: int,
+                prompt: bool = False) -> dict:
+    """Greedy decode rate of one more workload: its model built on the
+    device, its context filled with seeded K/V (or, with `prompt`, a seeded
+    prompt of ctx_len tokens prefilled), 2 untimed steps, then `steps` timed
+    (device synchronized on both sides); bytes per step are the algorithmic
+    weight and KV bytes."""
+    import nexus_amd
+    max_seq = ((ctx_len + steps + 32) // 16 + 1) * 16
+    m = nexus_amd.Model(ctx, **dict(base, batch=batch, kv_kind=kv_kind, max_seq=max_seq))
+    if prompt:
+        m.prefill(seeded_prompt(base["seed"], batch, ctx_len, base["vocab"]))
+    else:
+        m.fill_context(ctx_len, 4 if kv_kind else 0)
+    m.decode_untimed(2)
+    b0 = m.step_bytes()
+    ctx.sync()
+    t0 = time.perf_counter()
+    m.decode_untimed(steps)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    b1 = m.step_bytes()
+    m.close()
+    sb = 0.5 * (b0 + b1)
+    return {"workload": name, "batch": batch, "ctx": ctx_len, "steps": steps,
+            "tok_s": round(steps * batch / dt, 2), "ms_per_step": round(dt * 1e3 / steps, 4),
+            "GB_per_step": round(sb / 1e9, 4), "hbm_GBps_end_to_end": round(sb / (dt / steps) / 1e9, 1),
+            "roofline_end_to_end_frac": round(sb / (dt / steps) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
 def measured_traffic(kind: str):
@@ -107,9 +215,12 @@ GEMV_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256
 
 def gemv_microbench(ctx, batch: int = 1, iters: int = 200) -> list:
     """Standalone int4-g32 GEMV (fp16 x, fp16 y) on the five 8B projection
-    shapes; bytes = N*K*0.5625 + batch*(2K + 2N), HIP-event timed.  Each
-    shape rotates over enough weight copies (>= 768 MB in total) that every
-    launch reads its weights from HBM, not from the 256 MB last-level cache."""
+    shapes; bytes = N*K*0.5625 + batch*(2K + 2N).  The launches are captured
+    as one graph and timed with HIP events around its replay, so `us` is a
+    launch's share of a graph (what a decode step pays per launch, the
+    kernel boundary included).  Each shape rotates over enough weight copies
+    (>= 768 MB in total) that every launch reads its weights from HBM, not
+    from the 256 MB last-level cache."""
     import ctypes as C
     out = []
     for N, K in GEMV_SHAPES:
@@ -350,7 +461,18 @@ def main() -> int:
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     model.close()
     full = not args.decode_only
-    micro = gemv_microbench(ctx, args.batch) if full and not moe else None
+    micro = (gemv_microbench(ctx, 1) + gemv_microbench(ctx, 8)) if full and not moe else None
+    # the other decode workloads, when the default one is measured
+    others = None
+    if full and args.model == "llama-8b" and args.batch == 1 and kv_kind == 0 and args.ctx == 4096:
+        print("[bench] other decode workloads", file=sys.stderr, flush=True)
+        others = [
+            decode_line(ctx, TINY, "tiny llama (2 layers, d 256), 16-token prompt", 1, 0, 16, 64, prompt=True),
+            decode_line(ctx, LLAMA8B, "llama-3.1-8b-shape, fp16 paged KV", 8, 0, 4096, 128),
+            decode_line(ctx, LLAMA8B, "llama-3.1-8b-shape, TurboQuant 3.5-bit paged KV", 1, 1, 32768, 64),
+            decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 1, 0, 4096, 128),
+            decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 8, 0, 4096, 128),
+        ]
     nxf = nxf_verify_bench(ctx, not args.no_cpu) if full else None
     pre = prefill_bench(ctx, base) if full and not moe else None
     tier = tiering_bench(ctx, base) if full and base["head_dim"] == 128 else None
@@ -401,6 +523,8 @@ def main() -> int:
     }
     if micro is not None:
         line["gemv_microbench"] = micro
+    if others is not None:
+        line["decode_workloads"] = others
     if nxf is not None:
         line["nxf_verify"] = nxf
     line["sampling"] = sampling
@@ -410,8 +534,11 @@ def main() -> int:
         line["tiering"] = tier
     if not args.no_cpu:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind,
-                                            args.hot_window if kv_kind == 2 else 0)
+        hw = args.hot_window if kv_kind == 2 else 0
+        line["cpu_baseline"] = cpu_baseline(base, args.ctx, args.batch, kv_kind, hw)
+        line["cpu_baseline"]["cpu_model"] = cpu_model_name()
+        if full:
+            line["cpu_baselines"] = cpu_baselines(base, args.ctx, args.batch, kv_kind, hw)
     print(json.dumps(line), flush=True)
     return 0
 

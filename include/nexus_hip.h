@@ -447,10 +447,12 @@ nx_status nx_model_step_bytes(nx_model* m, double* bytes);
  * least one step must have run; NX_ERR_STATE otherwise), bytes = the active
  * experts' gate/up weights plus the gathered inputs and outputs. */
 nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double* bytes);
-/* Same for standalone nx_gemv_int4_g32 launches of shape N x K, batch:
- * launch i uses weight copy i % ncopies (wq[], scales_f16[]), so with enough
- * copies every launch streams its weights from HBM rather than from the
- * last-level cache. */
+/* Average device time (ms) per launch of nx_gemv_int4_g32 of shape N x K,
+ * batch: `iters` launches captured as one graph, one warm replay, then one
+ * replay between HIP events (so the figure includes the kernel boundary a
+ * decode step's graph pays per launch).  Launch i uses weight copy
+ * i % ncopies (wq[], scales_f16[]), so with enough copies every launch
+ * streams its weights from HBM rather than from the last-level cache. */
 nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x_f16, const nx_buf* wq, const nx_buf* scales_f16,
                        int ncopies, nx_buf y_f16, int N, int K, int batch, int iters,
                        double* avg_ms);

@@ -949,15 +949,33 @@ nx_status nx_time_gemv(nx_ctx* ctx, nx_buf x, const nx_buf* wq, const nx_buf* sc
         nx_status s = nx_gemv_int4_g32(ctx, x, wq[c], sc[c], y, N, K, batch);
         if (s != NX_OK) return s;
     }
-    NX_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
-    for (int i = 0; i < iters; ++i) {
-        nx_status s = nx_gemv_int4_g32(ctx, x, wq[i % ncopies], sc[i % ncopies], y, N, K, batch);
-        if (s != NX_OK) return s;
+    // the launches as one graph, as a decode step runs them: the average
+    // includes the kernel boundary a step pays per launch, not the host's
+    // per-launch submission cost
+    NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    NX_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    nx_status s = NX_OK;
+    for (int i = 0; i < iters && s == NX_OK; ++i)
+        s = nx_gemv_int4_g32(ctx, x, wq[i % ncopies], sc[i % ncopies], y, N, K, batch);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (s != NX_OK || e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return s != NX_OK ? s : nx::hip_fail(ctx, e, "hipStreamEndCapture");
     }
-    NX_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));
-    NX_HIP(ctx, hipEventSynchronize(ctx->ev1));
+    hipGraphExec_t ge = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ei != hipSuccess) return nx::hip_fail(ctx, ei, "hipGraphInstantiate");
     float ms = 0.0f;
-    NX_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+    hipError_t er = hipGraphLaunch(ge, ctx->stream);  // warm
+    if (er == hipSuccess) er = hipEventRecord(ctx->ev0, ctx->stream);
+    if (er == hipSuccess) er = hipGraphLaunch(ge, ctx->stream);
+    if (er == hipSuccess) er = hipEventRecord(ctx->ev1, ctx->stream);
+    if (er == hipSuccess) er = hipEventSynchronize(ctx->ev1);
+    if (er == hipSuccess) er = hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+    (void)hipGraphExecDestroy(ge);
+    if (er != hipSuccess) return nx::hip_fail(ctx, er, "timing graph");
     *avg_ms = (double)ms / iters;
     return NX_OK;
 }
