@@ -30,6 +30,7 @@
 // with a running argmax.  The input is either fp16 x or the fused RMSNorm of
 // an fp32 hidden state, computed once per block into LDS.
 #include <algorithm>
+#include <type_traits>
 
 #include "nx_gemv_dev.h"
 
@@ -64,23 +65,39 @@ __global__ __launch_bounds__(WPB * kWave, 1) void k_gemv_b1(GemvArgs a, RowSplit
 // ---------------------------------------------------------- batch 2..8 --
 // The weights of 16 rows meet the batch's x on the matrix cores
 // (v_mfma_f32_16x16x32_f16, one 32-element group per product):
-//   A (16 x 32): lane l holds row l%16, k = 8(l/16) .. +7 of the group: its 4
-//      code bytes, split into low and high nibbles, give the fp16 values
-//      (q - 8) in the k order (0 2 4 6 1 3 5 7); a byte joined with 0x64 is
-//      1024 + q, exact in fp16;
+//   A (16 x 32): lane l holds row l%16, k = 8(l/16) .. +7 of the group: its
+//      code dword gives the fp16 values (q - 8) in the k order
+//      (0 4 1 5 2 6 3 7): a low nibble ORed into 0x6400 is 1024 + q and a high
+//      nibble 1024 + 16 q, both exact in fp16 (codes_to_h8);
 //   B (32 x 16): lane l holds batch column l%16 with the same k order (x is
 //      staged in LDS in that order; columns past the batch are never stored);
 //   C (16 x 16 fp32): lane l holds column l%16, rows 4(l/16) .. +3.
 // Each product is a group sum (exact int4 x fp16 products, fp32 sums), which
 // is scaled by its row's group scale and accumulated in fp32, as in the
-// batch-1 kernel.  A block of 8 wavefronts takes whole 16-row tiles and splits
-// each 4096-wide K stage among its wavefronts (16 groups each); x is staged in
-// LDS per stage (K = 14336 takes four stages, one tile per block), the
-// wavefronts' partial tiles meet in LDS, and the tile's epilogue runs in
-// wavefront (tile % 8).  Every load before a wait is unconditional (clamped
-// rows, groups and stage entries), so the compiler's waits count exactly.
+// batch-1 kernel.  A block of 8 wavefronts takes whole 16-row tiles; K up to
+// 4096 is staged in LDS once, and the wavefronts stream (tile, 16-group pass)
+// items.  Longer K with fp16 x (the down projection) streams the same way
+// with each wavefront owning an eighth of K and loading its x straight from
+// memory with the weights (x is small and stays in the L2).  The
+// wavefronts' partial tiles meet in LDS.  Every load before a wait is
+// unconditional (clamped rows, groups and stage entries), so the compiler's
+// waits count exactly.
 typedef _Float16 mh8_t __attribute__((ext_vector_type(8)));
 typedef float mf4_t __attribute__((ext_vector_type(4)));
+
+#ifdef NX_LAYER_TRACE
+// phase timestamps of the batch-2..8 GEMV per (epilogue, input) kind, block
+// (< 256) and phase: entry, x staged, first item computed, first tile done,
+// items done, exit
+__device__ unsigned long long g_mfma_trace[16 * 256 * 8];
+#define NX_MTRACE_K(key, i) \
+    if (threadIdx.x == 0 && blockIdx.x < 256 && blockIdx.y == 0 && (key) >= 0) \
+        g_mfma_trace[((key) * 256 + blockIdx.x) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
+#define NX_MTRACE(i) NX_MTRACE_K(EPI * 2 + XS, i)
+#else
+#define NX_MTRACE_K(key, i)
+#define NX_MTRACE(i)
+#endif
 
 constexpr int kMfmaWaves = 8;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
@@ -90,21 +107,145 @@ constexpr int kMfmaGC = kMfmaKC / 32;              // groups per stage
 constexpr int kMfmaGW = kMfmaGC / kMfmaWaves;      // groups per wavefront per stage
 constexpr int kMfmaEPT = kMfmaGC * 4 * kMfmaCols / kMfmaThreads;  // stage entries per thread
 
-__device__ inline mh8_t codes_to_h8(uint32_t w) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu, k64 = 0x64646464u;
-    const uint4 r = make_uint4(__builtin_amdgcn_perm(k64, lo, 0x04010400u), __builtin_amdgcn_perm(k64, lo, 0x04030402u),
-                               __builtin_amdgcn_perm(k64, hi, 0x04010400u), __builtin_amdgcn_perm(k64, hi, 0x04030402u));
-    return __builtin_bit_cast(mh8_t, r) - (_Float16)1032.0f;
+typedef _Float16 mh2_t __attribute__((ext_vector_type(2)));
+
+// The 8 codes of a dword as fp16 (q - 8) in the k order (0 4 1 5 2 6 3 7):
+// byte i holds k = 2i (low nibble) and 2i + 1 (high nibble).  (w & 0x000F000F)
+// | 0x64006400 is the pair (1024 + q0, 1024 + q4); with mask 0x00F000F0 it is
+// (1024 + 16 q1, 1024 + 16 q5); w >> 8 gives k 2, 6 and 3, 7 the same way.
+// Then q - 8 = t - 1032 or t / 16 - 72, exact (one rounding of an exact
+// value) -- four v_and_or_b32, one shift, two packed adds, two packed fmas.
+// (w & mask) | bits in one instruction (the compiler splits it in two when
+// both constants are literals); mask in a VGPR, bits in an SGPR.
+__device__ inline uint32_t and_or(uint32_t w, uint32_t mask, uint32_t bits) {
+    uint32_t d;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(w), "v"(mask), "s"(bits));
+    return d;
 }
 
-// Eight consecutive fp16 inputs (as 4 dwords) in the k order (0 2 4 6 1 3 5 7).
+__device__ inline mh8_t codes_to_h8(uint32_t w) {
+    const uint32_t m = 0x64006400u, w8 = w >> 8;
+    const mh2_t a = __builtin_bit_cast(mh2_t, and_or(w, 0x000F000Fu, m));
+    const mh2_t b = __builtin_bit_cast(mh2_t, and_or(w, 0x00F000F0u, m));
+    const mh2_t c = __builtin_bit_cast(mh2_t, and_or(w8, 0x000F000Fu, m));
+    const mh2_t d = __builtin_bit_cast(mh2_t, and_or(w8, 0x00F000F0u, m));
+    const mh2_t off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const mh2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f}, off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const mh2_t r0 = a + off, r1 = __builtin_elementwise_fma(b, sixteenth, off16);
+    const mh2_t r2 = c + off, r3 = __builtin_elementwise_fma(d, sixteenth, off16);
+    return mh8_t{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+}
+
+// Eight consecutive fp16 inputs (as 4 dwords) in the k order (0 4 1 5 2 6 3 7).
 __device__ inline uint4 perm_x8(const uint32_t (&X)[4]) {
-    return make_uint4(__builtin_amdgcn_perm(X[1], X[0], 0x05040100u), __builtin_amdgcn_perm(X[3], X[2], 0x05040100u),
-                      __builtin_amdgcn_perm(X[1], X[0], 0x07060302u), __builtin_amdgcn_perm(X[3], X[2], 0x07060302u));
+    return make_uint4(__builtin_amdgcn_perm(X[2], X[0], 0x05040100u), __builtin_amdgcn_perm(X[2], X[0], 0x07060302u),
+                      __builtin_amdgcn_perm(X[3], X[1], 0x05040100u), __builtin_amdgcn_perm(X[3], X[1], 0x07060302u));
+}
+
+// The x values of a thread's stage entries, held between the requests and
+// their use (XVEC staging).
+template <int XS>
+struct StageRegs {
+    uint32_t X[kMfmaEPT][4];
+    float V[XS == X_RMSNORM ? kMfmaEPT : 1][8];
+    float NW[XS == X_RMSNORM ? kMfmaEPT : 1][8];
+};
+
+// XVEC staging, first half: request the thread's entries (all before any
+// use).  The norm weights are requested only when there are any.
+template <int XS>
+__device__ inline void stage_issue(const GemvArgs& a, int k0, int gc, StageRegs<XS>& r, int xrow) {
+    const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
+    const bool has_w = a.norm_w != nullptr;
+#pragma unroll
+    for (int j = 0; j < kMfmaEPT; ++j) {
+        const int e = min(tid + j * kMfmaThreads, ne - 1);
+        const int b = min(e % kMfmaCols, nb - 1), q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
+        const int kb = min(k0 + 32 * g + 8 * q, K - 8);
+        const size_t xo = (size_t)(xrow >= 0 ? xrow : b) * a.ldx + kb;
+        if (XS == X_F16) {
+            const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + xo);
+            r.X[j][0] = v.x; r.X[j][1] = v.y; r.X[j][2] = v.z; r.X[j][3] = v.w;
+        } else {
+            const float4* src = reinterpret_cast<const float4*>(a.h32 + xo);
+            const float4 u = src[0], w = src[1];
+            r.V[j][0] = u.x; r.V[j][1] = u.y; r.V[j][2] = u.z; r.V[j][3] = u.w;
+            r.V[j][4] = w.x; r.V[j][5] = w.y; r.V[j][6] = w.z; r.V[j][7] = w.w;
+        }
+    }
+    if (XS == X_RMSNORM && has_w) {
+#pragma unroll
+        for (int j = 0; j < kMfmaEPT; ++j) {
+            const int e = min(tid + j * kMfmaThreads, ne - 1);
+            const int q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
+            const int kb = min(k0 + 32 * g + 8 * q, K - 8);
+            const float4* ws = reinterpret_cast<const float4*>(a.norm_w + kb);
+            const float4 wu = ws[0], ww = ws[1];
+            r.NW[j][0] = wu.x; r.NW[j][1] = wu.y; r.NW[j][2] = wu.z; r.NW[j][3] = wu.w;
+            r.NW[j][4] = ww.x; r.NW[j][5] = ww.y; r.NW[j][6] = ww.z; r.NW[j][7] = ww.w;
+        }
+    }
+}
+
+// XVEC staging, second half: (NORM: 1/rms per batch row from the staged
+// values, reduced through LDS in red) convert and store the entries.
+template <int XS, bool NORM>
+__device__ inline void stage_finish(const GemvArgs& a, int k0, int gc, StageRegs<XS>& r, uint4* xs, float* inv,
+                                    float (*red)[kMfmaCols], [[maybe_unused]] int tkey = -1) {
+    const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
+    const bool has_w = a.norm_w != nullptr;
+    NX_MTRACE_K(tkey, 6);
+    if (XS == X_RMSNORM && NORM) {
+        // a thread's entries all belong to batch row tid % kMfmaCols
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMfmaEPT; ++j) {
+            const int e = tid + j * kMfmaThreads;
+            const int kb = k0 + 32 * (e / (4 * kMfmaCols)) + 8 * ((e / kMfmaCols) & 3);
+            if (e < ne && kb < K)
+#pragma unroll
+                for (int h = 0; h < 8; ++h) ss = fmaf(r.V[j][h], r.V[j][h], ss);
+        }
+        // lanes with the same tid % kMfmaCols: a stride-8 sum within the wavefront
+        ss += __shfl_xor(ss, 8, kWave);
+        ss += __shfl_xor(ss, 16, kWave);
+        ss += __shfl_xor(ss, 32, kWave);
+        const int lane = tid & (kWave - 1), wave = tid >> 6;
+        if (lane < kMfmaCols) red[wave][lane] = ss;
+        __syncthreads();
+        if (tid < kMfmaCols) {
+            float t = 0.0f;
+            for (int w = 0; w < kMfmaWaves; ++w) t += red[w][tid];
+            inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
+        }
+        __syncthreads();
+        NX_MTRACE_K(tkey, 7);
+    }
+#pragma unroll
+    for (int j = 0; j < kMfmaEPT; ++j) {
+        const int e = tid + j * kMfmaThreads;
+        if (e >= ne) break;
+        const int b = e % kMfmaCols, q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
+        const int kb = k0 + 32 * g + 8 * q;
+        if (b >= nb) continue;
+        if (XS == X_RMSNORM) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int k = kb + 2 * h;
+                const float t0 = r.V[j][2 * h] * inv[b], t1 = r.V[j][2 * h + 1] * inv[b];
+                const uint32_t lo = k < K ? f2h_bits(has_w ? t0 * r.NW[j][2 * h] : t0) : 0u;
+                const uint32_t hi = k + 1 < K ? f2h_bits(has_w ? t1 * r.NW[j][2 * h + 1] : t1) : 0u;
+                r.X[j][h] = lo | (hi << 16);
+            }
+        } else if (kb >= K) {
+            r.X[j][0] = r.X[j][1] = r.X[j][2] = r.X[j][3] = 0u;
+        }
+        xs[e] = perm_x8(r.X[j]);
+    }
 }
 
 // Stage x[b][k0 .. k0 + 32 gc) of every batch row into LDS: entry
-// (g * 4 + q) * kMfmaCols + b holds x[b][k0 + 32g + 8q + (0 2 4 6 1 3 5 7)].
+// (g * 4 + q) * kMfmaCols + b holds x[b][k0 + 32g + 8q + (0 4 1 5 2 6 3 7)].
 // XVEC: K % 8 == 0 and 16-byte aligned rows, one 16-byte load per entry (X_F16)
 // or two (X_RMSNORM); all loads of a thread are issued before any is used.
 // X_RMSNORM needs inv[b] = 1 / sqrt(mean(h_b^2) + eps).
@@ -113,81 +254,12 @@ __device__ inline uint4 perm_x8(const uint32_t (&X)[4]) {
 // through LDS in red), so the input costs one round trip.
 template <int XS, bool XVEC, bool NORM = false>
 __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs, float* inv,
-                                    float (*red)[kMfmaCols] = nullptr, int xrow = -1) {
-    // xrow >= 0: the x row of this thread's batch row (routed experts gather
-    // their tokens); a thread's entries all belong to batch row tid % 8
+                                    float (*red)[kMfmaCols] = nullptr, int xrow = -1, int tkey = -1) {
     const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
     if (XVEC) {
-        uint32_t X[kMfmaEPT][4];
-        float V[XS == X_RMSNORM ? kMfmaEPT : 1][8];
-        float NW[XS == X_RMSNORM ? kMfmaEPT : 1][8];
-#pragma unroll
-        for (int j = 0; j < kMfmaEPT; ++j) {
-            const int e = min(tid + j * kMfmaThreads, ne - 1);
-            const int b = min(e % kMfmaCols, nb - 1), q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
-            const int kb = min(k0 + 32 * g + 8 * q, K - 8);
-            const size_t xo = (size_t)(xrow >= 0 ? xrow : b) * a.ldx + kb;
-            if (XS == X_F16) {
-                const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + xo);
-                X[j][0] = v.x; X[j][1] = v.y; X[j][2] = v.z; X[j][3] = v.w;
-            } else {
-                const float4* src = reinterpret_cast<const float4*>(a.h32 + xo);
-                const float4 u = src[0], w = src[1];
-                V[j][0] = u.x; V[j][1] = u.y; V[j][2] = u.z; V[j][3] = u.w;
-                V[j][4] = w.x; V[j][5] = w.y; V[j][6] = w.z; V[j][7] = w.w;
-                // the norm weights with the values (without weights: h again, unused)
-                const float4* ws = reinterpret_cast<const float4*>(a.norm_w ? a.norm_w + kb : a.h32 + xo);
-                const float4 wu = ws[0], ww = ws[1];
-                NW[j][0] = wu.x; NW[j][1] = wu.y; NW[j][2] = wu.z; NW[j][3] = wu.w;
-                NW[j][4] = ww.x; NW[j][5] = ww.y; NW[j][6] = ww.z; NW[j][7] = ww.w;
-            }
-        }
-        if (XS == X_RMSNORM && NORM) {
-            // a thread's entries all belong to batch row tid % kMfmaCols
-            float ss = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kMfmaEPT; ++j) {
-                const int e = tid + j * kMfmaThreads;
-                const int kb = k0 + 32 * (e / (4 * kMfmaCols)) + 8 * ((e / kMfmaCols) & 3);
-                if (e < ne && kb < K)
-#pragma unroll
-                    for (int h = 0; h < 8; ++h) ss = fmaf(V[j][h], V[j][h], ss);
-            }
-            // lanes with the same tid % kMfmaCols: a stride-8 sum within the wavefront
-            ss += __shfl_xor(ss, 8, kWave);
-            ss += __shfl_xor(ss, 16, kWave);
-            ss += __shfl_xor(ss, 32, kWave);
-            const int lane = tid & (kWave - 1), wave = tid >> 6;
-            if (lane < kMfmaCols) red[wave][lane] = ss;
-            __syncthreads();
-            if (tid < kMfmaCols) {
-                float t = 0.0f;
-                for (int w = 0; w < kMfmaWaves; ++w) t += red[w][tid];
-                inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
-            }
-            __syncthreads();
-        }
-#pragma unroll
-        for (int j = 0; j < kMfmaEPT; ++j) {
-            const int e = tid + j * kMfmaThreads;
-            if (e >= ne) break;
-            const int b = e % kMfmaCols, q = (e / kMfmaCols) & 3, g = e / (4 * kMfmaCols);
-            const int kb = k0 + 32 * g + 8 * q;
-            if (b >= nb) continue;
-            if (XS == X_RMSNORM) {
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    const int k = kb + 2 * h;
-                    const float t0 = V[j][2 * h] * inv[b], t1 = V[j][2 * h + 1] * inv[b];
-                    const uint32_t lo = k < K ? f2h_bits(a.norm_w ? t0 * NW[j][2 * h] : t0) : 0u;
-                    const uint32_t hi = k + 1 < K ? f2h_bits(a.norm_w ? t1 * NW[j][2 * h + 1] : t1) : 0u;
-                    X[j][h] = lo | (hi << 16);
-                }
-            } else if (kb >= K) {
-                X[j][0] = X[j][1] = X[j][2] = X[j][3] = 0u;
-            }
-            xs[e] = perm_x8(X[j]);
-        }
+        StageRegs<XS> r;
+        stage_issue<XS>(a, k0, gc, r, xrow);
+        stage_finish<XS, NORM>(a, k0, gc, r, xs, inv, red, tkey);
         return;
     }
     for (int e = tid; e < ne; e += kMfmaThreads) {
@@ -226,17 +298,23 @@ __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs
 // needs quarter kq of every group in lane row kq, which a 4 x 4 exchange
 // across the four 16-lane rows provides (quad_transpose).  SALIGN: G % 4 == 0,
 // so the scales of 4 consecutive groups are one 8-byte load.
+// XG: the wavefront's x of the item's groups too (x loaded from memory with
+// the weights instead of staged in LDS), lane (c, kq) holding quarter kq of
+// each group for batch row c % 8.
+template <bool XG = false>
 struct MfmaRegs {
     uint4 code[kMfmaGW / 4];
     uint32_t sc[kMfmaGW / 2];  // fp16 scale pairs (groups 2u, 2u+1) of the lane's weight row
+    uint4 x[XG ? kMfmaGW : 1];
 };
 
 // keep = 0: a request with no use (past the block's last tile); every lane
 // then reads the first 16 bytes of row min(row0, N-1) of the stage, one cache
-// line.
-template <bool SALIGN>
-__device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs, int ge, MfmaRegs& r,
-                                 int keep = 1) {
+// line.  FULL: groups gs .. gs + 15 all exist (no clamping).  XG: x of the
+// same groups from row offset xoff.
+template <bool SALIGN, bool FULL, bool XG>
+__device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs, int ge, MfmaRegs<XG>& r,
+                                 int keep = 1, size_t xoff = 0) {
     const int lane = threadIdx.x & (kWave - 1), c = lane & 15, kq = lane >> 4;
     const int G = a.G;
     const int gl = ge - 1;  // last group of the stage (ge == stage groups when the wavefront has none)
@@ -245,7 +323,8 @@ __device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs,
     if (SALIGN) {
 #pragma unroll
         for (int u4 = 0; u4 < kMfmaGW / 4; ++u4) {
-            const uint2 v = *reinterpret_cast<const uint2*>(srow + min(gs + 4 * u4, gl & ~3) * keep);
+            const int g = FULL ? gs + 4 * u4 : min(gs + 4 * u4, gl & ~3);
+            const uint2 v = *reinterpret_cast<const uint2*>(srow + g * keep);
             r.sc[2 * u4] = v.x;
             r.sc[2 * u4 + 1] = v.y;
         }
@@ -257,8 +336,15 @@ __device__ inline void mfma_load(const GemvArgs& a, int row0, int gbase, int gs,
     }
     const uint8_t* wrow = a.W + row * G * 16 + (size_t)gbase * 16;
 #pragma unroll
-    for (int u4 = 0; u4 < kMfmaGW / 4; ++u4)
-        r.code[u4] = *reinterpret_cast<const uint4*>(wrow + (size_t)(min(gs + 4 * u4 + kq, gl) * keep) * 16);
+    for (int u4 = 0; u4 < kMfmaGW / 4; ++u4) {
+        const int g = FULL ? gs + 4 * u4 + kq : min(gs + 4 * u4 + kq, gl);
+        r.code[u4] = *reinterpret_cast<const uint4*>(wrow + (size_t)(g * keep) * 16);
+    }
+    if constexpr (XG) {
+#pragma unroll
+        for (int u = 0; u < kMfmaGW; ++u)
+            r.x[u] = *reinterpret_cast<const uint4*>(a.x16 + xoff + 32 * min(gs + u, gl) + 8 * kq);
+    }
 }
 
 // 4 x 4 exchange across the 16-lane rows: on entry lane row r holds the four
@@ -279,17 +365,29 @@ __device__ inline void quad_transpose(const uint4& q, uint32_t (&o)[4]) {
 }
 
 // The A operands (x of the batch) of the wavefront's groups, from LDS.
+template <bool FULL>
 __device__ inline void mfma_load_x(const uint4* xs, int gs, int ge, uint4 (&xv)[kMfmaGW]) {
     const int lane = threadIdx.x & (kWave - 1), c = lane & 15, kq = lane >> 4;
     const int gl = ge - 1;
 #pragma unroll
-    for (int u = 0; u < kMfmaGW; ++u) xv[u] = xs[(min(gs + u, gl) * 4 + kq) * kMfmaCols + (c & (kMfmaCols - 1))];
+    for (int u = 0; u < kMfmaGW; ++u)
+        xv[u] = xs[((FULL ? gs + u : min(gs + u, gl)) * 4 + kq) * kMfmaCols + (c & (kMfmaCols - 1))];
+}
+
+// The A operands from an XG item's registers, in the MFMA's k order.
+__device__ inline void mfma_perm_x(const uint4 (&x)[kMfmaGW], uint4 (&xv)[kMfmaGW]) {
+#pragma unroll
+    for (int u = 0; u < kMfmaGW; ++u) {
+        const uint32_t X[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+        xv[u] = perm_x8(X);
+    }
 }
 
 // Group sums of the wavefront's share, scaled and accumulated into acc
-// (fully unrolled, so the register arrays stay in registers; groups past ge
-// repeat a valid group with weight zero).
-__device__ inline void mfma_compute(const MfmaRegs& r, const uint4 (&xv)[kMfmaGW], int gs, int ge, mf4_t& acc) {
+// (fully unrolled, so the register arrays stay in registers; unless FULL,
+// groups past ge repeat a valid group with weight zero).
+template <bool FULL, bool XG>
+__device__ inline void mfma_compute(const MfmaRegs<XG>& r, const uint4 (&xv)[kMfmaGW], int gs, int ge, mf4_t& acc) {
     uint32_t code[kMfmaGW];
 #pragma unroll
     for (int u4 = 0; u4 < kMfmaGW / 4; ++u4) {
@@ -300,24 +398,26 @@ __device__ inline void mfma_compute(const MfmaRegs& r, const uint4 (&xv)[kMfmaGW
     }
 #pragma unroll
     for (int u = 0; u < kMfmaGW; ++u) {
-        const float on = gs + u < ge ? 1.0f : 0.0f;
         const mf4_t z = {0.f, 0.f, 0.f, 0.f};
         const mf4_t cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8_t, xv[u]),
                                                                codes_to_h8(code[u]), z, 0, 0, 0);
         const uint32_t pr = r.sc[u >> 1];
-        const float sv = h2f_bits((uint16_t)((u & 1) ? (pr >> 16) : (pr & 0xFFFFu))) * on;
+        float sv = h2f_bits((uint16_t)((u & 1) ? (pr >> 16) : (pr & 0xFFFFu)));
+        if (!FULL) sv *= gs + u < ge ? 1.0f : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(cg[i], sv, acc[i]);
     }
 }
 
-template <int XS, int EPI, bool XVEC, bool SALIGN, bool MOE = false>
+// FULL: K <= 4096 and every wavefront's K slice is whole passes of 16 groups.
+template <int XS, int EPI, bool XVEC, bool SALIGN, bool MOE, bool FULL>
 __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, int nb, int ks) {
     __shared__ __align__(16) uint4 xs[kMfmaGC * 4 * kMfmaCols];
     __shared__ __align__(16) float part[2][kMfmaWaves * 16 * kMfmaCols];  // [wave][weight row][batch row]
     __shared__ float inv[kMfmaCols];
     __shared__ float red[kMfmaWaves][kMfmaCols];
     __shared__ unsigned long long bk[kMfmaThreads];
+    NX_MTRACE(0);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
     const int N = args.N, K = args.K;
@@ -342,35 +442,41 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
         yrow = pl[8 + min(c, kMoePlanMaxSlots - 1)];
     }
     const int nstage = (K + kMfmaKC - 1) / kMfmaKC;
-    if (XS == X_RMSNORM && XVEC && nstage == 1) {
-        mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red, xrow);
-    } else if (XS == X_RMSNORM) {
-        // sum of h^2 per batch row over all of K
-        float ss[kMfmaCols];
+    // the input: staged in LDS for one stage (and RMSNorm's 1/rms per batch
+    // row); run by the streaming loop after its first weight requests
+    auto stage_input = [&]() {
+        if (XS == X_RMSNORM && XVEC && nstage == 1) {
+            mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red, xrow, EPI * 2 + XS);
+        } else if (XS == X_RMSNORM) {
+            // sum of h^2 per batch row over all of K
+            float ss[kMfmaCols];
 #pragma unroll
-        for (int b = 0; b < kMfmaCols; ++b) ss[b] = 0.0f;
-        for (int k = tid; k < K; k += kMfmaThreads)
+            for (int b = 0; b < kMfmaCols; ++b) ss[b] = 0.0f;
+            for (int k = tid; k < K; k += kMfmaThreads)
 #pragma unroll
-            for (int b = 0; b < kMfmaCols; ++b)
-                if (b < a.batch) {
-                    const float v = a.h32[(size_t)b * a.ldx + k];
-                    ss[b] = fmaf(v, v, ss[b]);
-                }
+                for (int b = 0; b < kMfmaCols; ++b)
+                    if (b < a.batch) {
+                        const float v = a.h32[(size_t)b * a.ldx + k];
+                        ss[b] = fmaf(v, v, ss[b]);
+                    }
 #pragma unroll
-        for (int b = 0; b < kMfmaCols; ++b) {
-            const float t = wave_sum(ss[b]);
-            if (lane == 0) red[wave][b] = t;
+            for (int b = 0; b < kMfmaCols; ++b) {
+                const float t = wave_sum(ss[b]);
+                if (lane == 0) red[wave][b] = t;
+            }
+            __syncthreads();
+            if (tid < kMfmaCols) {
+                float t = 0.0f;
+                for (int w = 0; w < kMfmaWaves; ++w) t += red[w][tid];
+                inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        if (tid < kMfmaCols) {
-            float t = 0.0f;
-            for (int w = 0; w < kMfmaWaves; ++w) t += red[w][tid];
-            inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
-        }
-        __syncthreads();
-    }
-    if (nstage == 1 && !(XS == X_RMSNORM && XVEC)) mfma_stage_x<XS, XVEC>(a, 0, (K + 31) / 32, xs, inv, nullptr, xrow);
-    if (nstage == 1) __syncthreads();  // x staged
+        if (nstage == 1 && !(XS == X_RMSNORM && XVEC))
+            mfma_stage_x<XS, XVEC>(a, 0, (K + 31) / 32, xs, inv, nullptr, xrow);
+        if (nstage == 1) __syncthreads();  // x staged
+        NX_MTRACE(1);
+    };
     float best_v = -__builtin_inff();
     int best_i = -1;
     const int gs = wave * kMfmaGW;
@@ -390,34 +496,48 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             epilogue<EPI, 4>(a, yrow, row0 + 4 * kq, N, res, best_v, best_i);
         }
     };
-    if (nstage == 1) {
-        // A tile is split over ks wavefronts along K (ks = 1 for large N).
-        // Wavefront (tsub, kslice) = (wave / ks, wave % ks) takes tiles
-        // t0 + tsub + (8 / ks) i and, of each, the groups of its K slice in
-        // passes of 16; it streams these (tile, pass) items with the next
-        // item requested before the current one is computed.  Only at a
-        // tile's end do the wavefronts meet: partial sums go to LDS and, after
-        // the barrier, wavefront kslice 0 of each tile adds them and runs the
-        // epilogue.  (A barrier per pass made every wavefront wait for the
-        // others' prefetched data, which a CU returns in request order.)
-        // The item loop takes whole pairs with no exit inside, so each
-        // request it carries across the back edge is consumed in the next
-        // pass and the compiler's waits stay exact.
+    // fp16 x with K beyond one LDS stage: x straight from memory (XG)
+    constexpr bool kXG = XS == X_F16 && XVEC && SALIGN && !FULL;
+    // A tile is split over ks wavefronts along K (ks = 1 for large N).
+    // Wavefront (tsub, kslice) = (wave / ks, wave % ks) takes tiles
+    // t0 + tsub + (8 / ks) i and, of each, the groups of its K slice in
+    // passes of 16; it streams these (tile, pass) items with the next item
+    // requested before the current one is computed.  Only at a tile's end do
+    // the wavefronts meet: partial sums go to LDS and, after the barrier,
+    // wavefront kslice 0 of each tile adds them and runs the epilogue.  (A
+    // barrier per pass made every wavefront wait for the others' prefetched
+    // data, which a CU returns in request order.)  The item loop takes whole
+    // pairs with no exit inside, so each request it carries across the back
+    // edge is consumed in the next pass and the compiler's waits stay exact.
+    // XG (several stages, ks = 8): K slices of ceil(G / 8) groups, x of the
+    // item's groups loaded with its weights.
+    auto stream = [&](auto xg_tag) {
+        constexpr bool XG = decltype(xg_tag)::value;
         const int G = a.G, wpt = kMfmaWaves / ks, kslice = wave % ks, tsub = wave / ks;
-        const int gps = ((G + ks - 1) / ks + kMfmaGW - 1) / kMfmaGW * kMfmaGW, npass = gps / kMfmaGW;
+        const int gps = XG ? (G + ks - 1) / ks : ((G + ks - 1) / ks + kMfmaGW - 1) / kMfmaGW * kMfmaGW;
+        const int npass = (gps + kMfmaGW - 1) / kMfmaGW, send = min(G, (kslice + 1) * gps);
         const int iters = (tpb + wpt - 1) / wpt, nitem = iters * npass;
+        const size_t xoff = XG ? (size_t)(xrow >= 0 ? xrow : min(c & (kMfmaCols - 1), a.batch - 1)) * a.ldx : 0;
         auto item_tile = [&](int j) { return t0 + tsub + wpt * (j / npass); };
         auto item_gs = [&](int j) { return kslice * gps + kMfmaGW * (j % npass); };
-        auto load_item = [&](int j, MfmaRegs& r) {
+        auto load_item = [&](int j, MfmaRegs<XG>& r) {
             const int gs = item_gs(j), keep = j < nitem && item_tile(j) < t0 + nt ? 1 : 0;
-            mfma_load<SALIGN>(a, item_tile(j) * 16, 0, gs, min(G, gs + kMfmaGW), r, keep);
+            mfma_load<SALIGN, FULL, XG>(a, item_tile(j) * 16, 0, gs, min(send, gs + kMfmaGW), r, keep, xoff);
         };
         auto tile_end = [&](int j, const mf4_t& acc) {
             const int slot = (j / npass) & 1, t = item_tile(j);
             if (kq < 2)
                 *reinterpret_cast<float4*>(&part[slot][(wave * 16 + c) * kMfmaCols + 4 * kq]) =
                     make_float4(acc[0], acc[1], acc[2], acc[3]);
-            __syncthreads();
+            // ks = 1: the wavefront holds whole tiles and reads back only its
+            // own slot (LDS operations of one wavefront complete in order)
+            if (ks == 1) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            } else {
+                __syncthreads();
+            }
             if (kslice == 0 && c < a.batch && t < t0 + nt) {
                 float res[4] = {0.f, 0.f, 0.f, 0.f};
                 for (int s2 = 0; s2 < ks; ++s2)
@@ -428,31 +548,90 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             }
         };
         mf4_t acc = {0.f, 0.f, 0.f, 0.f};
-        auto step = [&](int j, const MfmaRegs& r) {
-            const int gs = item_gs(j), ge = min(G, gs + kMfmaGW);
+        MfmaRegs<XG> ra, rb;
+        if constexpr (!XG && XVEC) {
+            // the input's requests go first, the first two items' right
+            // behind them (a CU returns data in request order, so x is not
+            // held up), and only then is the input used
+            StageRegs<XS> sr;
+            stage_issue<XS>(a, 0, (K + 31) / 32, sr, xrow);
+            load_item(0, ra);
+            load_item(1, rb);
+            __builtin_amdgcn_sched_barrier(0);
+            stage_finish<XS, XS == X_RMSNORM>(a, 0, (K + 31) / 32, sr, xs, inv, red, EPI * 2 + XS);
+            __syncthreads();  // x staged
+            NX_MTRACE(1);
+        } else {
+            stage_input();
+            load_item(0, ra);
+            if constexpr (!XG) load_item(1, rb);
+        }
+        // one pass per tile (ks = 8 at K = 4096): the wavefront's x is the
+        // same for every item, read from LDS once
+        uint4 xh[kMfmaGW];
+        const bool xhold = !XG && FULL && npass == 1;
+        if (xhold) mfma_load_x<FULL>(xs, min(kslice * gps, G - 1), min(send, kslice * gps + kMfmaGW), xh);
+        auto step = [&](int j, const MfmaRegs<XG>& r) {
+            const int gs = item_gs(j), ge = min(send, gs + kMfmaGW);
             uint4 xv[kMfmaGW];
-            mfma_load_x(xs, min(gs, G - 1), ge, xv);
-            mfma_compute(r, xv, gs, ge, acc);
+            if constexpr (XG) {
+                mfma_perm_x(r.x, xv);
+            } else if (xhold) {
+#pragma unroll
+                for (int u = 0; u < kMfmaGW; ++u) xv[u] = xh[u];
+            } else {
+                mfma_load_x<FULL>(xs, min(gs, G - 1), ge, xv);
+            }
+            mfma_compute<FULL, XG>(r, xv, gs, ge, acc);
+            if (j == 0) NX_MTRACE(2);
             if (j % npass == npass - 1) {
                 tile_end(j, acc);
+                if (j == npass - 1) NX_MTRACE(3);
                 acc = mf4_t{0.f, 0.f, 0.f, 0.f};
             }
         };
-        MfmaRegs ra, rb;
-        load_item(0, ra);
+        if constexpr (XG) {
+            // two items in flight (an XG item holds its x too)
+            int j = 0;
+            for (; j + 1 < nitem; j += 2) {
+                load_item(j + 1, rb);
+                __builtin_amdgcn_sched_barrier(0);
+                step(j, ra);
+                load_item(j + 2, ra);
+                __builtin_amdgcn_sched_barrier(0);
+                step(j + 1, rb);
+            }
+            if (j < nitem) step(j, ra);
+            return;
+        }
+        // three items in flight: item j + 2 is requested before item j is
+        // used (loads past the last item read a valid line and are unused)
+        MfmaRegs<XG> rc;
         int j = 0;
-        for (; j + 1 < nitem; j += 2) {
-            load_item(j + 1, rb);
-            // the next item's requests stay ahead of this item's first use (the
+        for (; j + 2 < nitem; j += 3) {
+            load_item(j + 2, rc);
+            // the next items' requests stay ahead of this item's first use (the
             // scheduler would otherwise hoist the use, which then waits for all)
             __builtin_amdgcn_sched_barrier(0);
             step(j, ra);
-            load_item(j + 2, ra);
+            load_item(j + 3, ra);
             __builtin_amdgcn_sched_barrier(0);
             step(j + 1, rb);
+            load_item(j + 4, rb);
+            __builtin_amdgcn_sched_barrier(0);
+            step(j + 2, rc);
         }
         if (j < nitem) step(j, ra);
+        if (j + 1 < nitem) step(j + 1, rb);
+    };
+    if (nstage == 1) {
+        stream(std::integral_constant<bool, false>{});
+        NX_MTRACE(4);
+    } else if constexpr (kXG) {
+        stream(std::integral_constant<bool, true>{});
+        NX_MTRACE(4);
     } else {
+        stage_input();
         // K in several stages: x restaged per stage
         for (int t = 0; t < nt; ++t) {
             const int row0 = (t0 + t) * 16;
@@ -460,14 +639,14 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             for (int st = 0; st < nstage; ++st) {
                 const int k0 = st * kMfmaKC, gc = (min(kMfmaKC, K - k0) + 31) / 32;
                 const int ge = min(gc, gs + kMfmaGW);
-                MfmaRegs rg;
-                mfma_load<SALIGN>(a, row0, k0 / 32, gs, ge, rg);
+                MfmaRegs<false> rg;
+                mfma_load<SALIGN, false, false>(a, row0, k0 / 32, gs, ge, rg);
                 __syncthreads();  // the previous stage's readers are done
                 mfma_stage_x<XS, XVEC>(a, k0, gc, xs, inv, nullptr, xrow);
                 __syncthreads();
                 uint4 xv[kMfmaGW];
-                mfma_load_x(xs, gs, ge, xv);
-                mfma_compute(rg, xv, gs, ge, acc);
+                mfma_load_x<false>(xs, gs, ge, xv);
+                mfma_compute<false, false>(rg, xv, gs, ge, acc);
             }
             finish(t, row0, acc);
         }
@@ -485,6 +664,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             if (m) atomicMax(&a.best[tid], m);
         }
     }
+    NX_MTRACE(5);
 }
 
 // Batch 1: a persistent grid of WPB wavefronts per CU in one block each
@@ -510,30 +690,35 @@ hipError_t launch_b1(const GemvArgs& a, hipStream_t st, int ny = 1) {
 
 // Batch 2..8 on the matrix cores.  One stage (K <= 4096): ks wavefronts per
 // tile, the fewest that still give every wavefront of one block per CU a
-// tile, and enough tiles per block for one round of blocks.  Several stages:
-// one tile per block.
+// tile, and enough tiles per block for one round of blocks.  Longer K with
+// fp16 x (whole groups, aligned): the same streaming with ks = 8, x from
+// memory.  Otherwise several LDS stages, one tile per block.
 // MOE: ny grid rows of routed experts share the CUs.
 template <int XS, int EPI, bool MOE = false>
 hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
     const int ntile = (a.N + 15) / 16, cus = device_cus();
-    int blocks = ntile, ks = 1;
-    if (a.K <= kMfmaKC) {
-        // one round: the grid rows (experts) share the CUs, a block's tiles
-        // are an even share of its row's
-        blocks = std::max(1, std::min(ntile, (cus + ny - 1) / ny));
-        const int per_block = (ntile + blocks - 1) / blocks;
-        ks = per_block <= 1 ? 8 : per_block <= 2 ? 4 : per_block <= 4 ? 2 : 1;
-    }
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       a.ldx % (XS == X_F16 ? 8 : 4) == 0;
     const bool salign = a.G % 4 == 0;
-#define NX_MFMA(XV, SA) \
-    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA, MOE>), dim3(blocks, ny), dim3(kMfmaThreads), 0, st, a, blocks, ks)
-    if (xvec && salign) NX_MFMA(true, true);
-    else if (xvec) NX_MFMA(true, false);
-    else if (salign) NX_MFMA(false, true);
-    else NX_MFMA(false, false);
+    const bool xg = XS == X_F16 && a.K > kMfmaKC && a.K % 32 == 0 && xvec && salign;
+    int blocks = ntile, ks = 1;
+    if (a.K <= kMfmaKC || xg) {
+        // one round: the grid rows (experts) share the CUs, a block's tiles
+        // are an even share of its row's
+        blocks = std::max(1, std::min(ntile, (cus + ny - 1) / ny));
+        const int per_block = (ntile + blocks - 1) / blocks;
+        ks = xg || per_block <= 1 ? 8 : per_block <= 2 ? 4 : per_block <= 4 ? 2 : 1;
+    }
+    const bool full = a.K <= kMfmaKC && xvec && salign && a.G % (kMfmaGW * ks) == 0;
+#define NX_MFMA(XV, SA, FL)                                                                                   \
+    hipLaunchKernelGGL((k_gemv_mfma<XS, EPI, XV, SA, MOE, FL>), dim3(blocks, ny), dim3(kMfmaThreads), 0, st, a, \
+                       blocks, ks)
+    if (full) NX_MFMA(true, true, true);
+    else if (xvec && salign) NX_MFMA(true, true, false);
+    else if (xvec) NX_MFMA(true, false, false);
+    else if (salign) NX_MFMA(false, true, false);
+    else NX_MFMA(false, false, false);
 #undef NX_MFMA
     return hipGetLastError();
 }
@@ -569,6 +754,9 @@ hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
 #ifdef NX_LAYER_TRACE
 extern "C" int nx_debug_gemv_trace(unsigned long long* out) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(gv::g_gemv_trace), sizeof(unsigned long long) * 64 * 256 * 8);
+}
+extern "C" int nx_debug_mfma_trace(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_mfma_trace), sizeof(unsigned long long) * 16 * 256 * 8);
 }
 #endif
 
