@@ -130,8 +130,15 @@ template <int HD>
 struct PairRaw {
     uint4 k[2][HD / 32];  // K of pages a, b: A operand per k-step
     uint2 v[HD / 16][2];  // V of pages a, b: tokens 4g..4g+3 of dim 16 nt + l%16
-    uint2 vmask[2];       // per page: bits of the V words that hold valid tokens
 };
+
+// Bits of a lane's V words (tokens 4g .. 4g+3, fp16 each) that hold the first
+// n tokens of the page.
+__device__ inline uint2 vmask_of(int n, int g) {
+    const int valid = min(max(n - 4 * g, 0), 4);
+    return make_uint2((uint32_t)(0xFFFFFFFFull >> (16 * (2 - min(valid, 2)))),
+                      (uint32_t)(0xFFFFFFFFull >> (16 * (2 - max(valid - 2, 0)))));
+}
 
 // Load pages a and b of a pair; na / nb = valid tokens of each (0 = none).
 // Every load is issued unconditionally, because a branch or a select around a
@@ -139,7 +146,7 @@ struct PairRaw {
 // arrive one round trip per tile: page b with no valid token re-reads page a
 // (blka must be a valid block), K rows of tokens past the valid count are
 // left as loaded (their scores are masked in pair_update), and the V words
-// of those tokens are cleared with masks.
+// of those tokens are cleared with masks (vmask_of, in pair_update).
 template <int HD>
 __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, int na, int blkb,
                                  int nb, int kvh, int lane) {
@@ -147,16 +154,11 @@ __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, in
     const int pb = nb > 0 ? blkb : blka;
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
-        const int blk = pg ? pb : blka, n = pg ? nb : na;
+        const int blk = pg ? pb : blka;
         const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
 #pragma unroll
         for (int s = 0; s < HD / 32; ++s)
             r.k[pg][s] = *reinterpret_cast<const uint4*>(a.kpool + base + (size_t)t * HD + 32 * s + 8 * g);
-        // tokens 4g .. 4g+3 of the V words: the first `valid` are kept
-        // (applied in pair_update, so that nothing here waits for the data)
-        const int valid = min(max(n - 4 * g, 0), 4);
-        r.vmask[pg] = make_uint2((uint32_t)(0xFFFFFFFFull >> (16 * (2 - min(valid, 2)))),
-                                 (uint32_t)(0xFFFFFFFFull >> (16 * (2 - max(valid - 2, 0)))));
 #pragma unroll
         for (int nt = 0; nt < HD / 16; ++nt)
             r.v[nt][pg] = *reinterpret_cast<const uint2*>(a.vpool + base + (size_t)(16 * nt + t) * kPage + 4 * g);
@@ -212,6 +214,9 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
     }
     lsum = lsum * corr + ps;
     m = mn;
+    // V words of tokens past the valid counts are cleared (they may hold
+    // anything, and their zero weights must not meet a NaN)
+    const uint2 ma = vmask_of(na, g), mb = vmask_of(nb, g);
     // rows of O in this lane are heads 4g + i; their rescale factors live in
     // the lanes whose column is that head
     float c[4];
@@ -222,8 +227,8 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
         f4_t acc = o[nt];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= c[i];
-        const h8_t vb = as_h8(make_uint4(r.v[nt][0].x & r.vmask[0].x, r.v[nt][0].y & r.vmask[0].y,
-                                         r.v[nt][1].x & r.vmask[1].x, r.v[nt][1].y & r.vmask[1].y));
+        const h8_t vb = as_h8(make_uint4(r.v[nt][0].x & ma.x, r.v[nt][0].y & ma.y, r.v[nt][1].x & mb.x,
+                                         r.v[nt][1].y & mb.y));
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, acc, 0, 0, 0);
         o[nt] = acc;

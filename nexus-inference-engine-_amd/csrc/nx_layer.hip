@@ -123,10 +123,7 @@ __device__ inline void load_page_a(PairRaw<HD>& r, const AttnArgs& a, int blka, 
         r.k[0][s] = *reinterpret_cast<const uint4*>(a.kpool + base + (size_t)t * HD + 32 * s + 8 * g);
         r.k[1][s] = make_uint4(0u, 0u, 0u, 0u);
     }
-    const int valid = min(max(na - 4 * g, 0), 4);
-    r.vmask[0] = make_uint2((uint32_t)(0xFFFFFFFFull >> (16 * (2 - min(valid, 2)))),
-                            (uint32_t)(0xFFFFFFFFull >> (16 * (2 - max(valid - 2, 0)))));
-    r.vmask[1] = make_uint2(0u, 0u);
+    (void)na;
 #pragma unroll
     for (int nt = 0; nt < HD / 16; ++nt) {
         r.v[nt][0] = *reinterpret_cast<const uint2*>(a.vpool + base + (size_t)(16 * nt + t) * kPage + 4 * g);
