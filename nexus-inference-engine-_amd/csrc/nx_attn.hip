@@ -61,6 +61,7 @@ __constant__ float c_tq_b4[15];
 __constant__ float c_tq_c3[8];
 __constant__ float c_tq_b3[7];
 __constant__ float c_tq_cb[24];  // c_tq_c4 then c_tq_c3
+constexpr int kTqTbl4 = 256, kTqTbl = kTqTbl4 + 64;  // LDS pair tables of the attention
 
 // One split of one (kv head, sequence): the pages s, s + nsplit, ... of
 // split s, shared by the block's kAttnWaves wavefronts, two pages per
@@ -227,8 +228,17 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int ns
 //   P.V (B = V: column n = l%16, k = the pair's tokens 8g + j, j < 4 from page
 //     a, j >= 4 from page b): tile nt holds code nt of chunk n of each token,
 //     so output column n of tile nt is dimension 8n + nt.
-// Codebook values enter as fp16 hi + lo (one LDS word holds both halves), q~
-// and P as hi + lo; three products give fp32-accurate sums.  The V norm is
+// Codebook values enter the scores as fp16 hi + lo, q~ as hi + lo: three
+// products per step give fp32-accurate scores (their errors would pass through
+// exp).  P enters as hi + lo and the codebook values of V as fp16 (rounded to
+// nearest: at most 2^-12 relative per value, an error that stays linear in the
+// output): two products per tile.  Codes are looked up in LDS pair tables:
+// entry f of the 4-bit table (256 entries) holds the fp16 hi pair and lo pair
+// of (c4[f & 15], c4[f >> 4]), of the 3-bit table (64 entries, from entry
+// 256) those of (c3[f & 7], c3[f >> 3]), so one 8-byte lookup gives two
+// score operand values (fewer instructions than a lookup per code, which
+// needs two perms per pair, for more bank conflicts); the low 16 bits of
+// entry c are hi(c4[c]) (hi(c3[c])) for the value operand.  The V norm is
 // folded into P, the K norm and the scale into the scores.
 struct TqPair {
     uint2 k4[2], k3[2];           // pages a, b: 4-bit chunks (2g, 2g+1) of token l%16; the 8 bytes holding its 3-bit chunks (2g, 2g+1)
@@ -252,7 +262,7 @@ struct TqLane {
         stride = b4 ? 32 : 24;
         shift = b4 ? 0 : (3 * j) & 3;
         bits = b4 ? 4 : 3;
-        cbo = b4 ? 0 : 16;
+        cbo = b4 ? 0 : kTqTbl4;
     }
 };
 
@@ -281,30 +291,22 @@ __device__ inline void tq_load_pair(TqPair& r, const AttnArgs& a, const TqLane& 
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// fp16 hi and lo operands of 8 codes (width `bits`, from bit 0 of w) through
-// the LDS codebook (cbk[cbo + code] = hi | lo << 16).
-__device__ inline void tq_dequant8(uint32_t w, int bits, int cbo, const uint32_t* cbk, h8_t& hi, h8_t& lo) {
-    uint32_t e[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = cbk[cbo + __builtin_amdgcn_ubfe(w, bits * i, bits)];
-    uint4 h, l;
-    h.x = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
-    l.x = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
-    h.y = __builtin_amdgcn_perm(e[3], e[2], 0x05040100u);
-    l.y = __builtin_amdgcn_perm(e[3], e[2], 0x07060302u);
-    h.z = __builtin_amdgcn_perm(e[5], e[4], 0x05040100u);
-    l.z = __builtin_amdgcn_perm(e[5], e[4], 0x07060302u);
-    h.w = __builtin_amdgcn_perm(e[7], e[6], 0x05040100u);
-    l.w = __builtin_amdgcn_perm(e[7], e[6], 0x07060302u);
-    hi = as_h8(h);
-    lo = as_h8(l);
+// fp16 hi and lo operands of 8 codes (width `bits`, from bit 0 of w): four
+// pair-table lookups, codes 2i and 2i + 1 in dword i.
+__device__ inline void tq_dequant8(uint32_t w, int bits, const uint2* tbl, h8_t& hi, h8_t& lo) {
+    const int pb = 2 * bits;
+    const uint2* t = tbl + (bits == 4 ? 0 : kTqTbl4);
+    const uint2 e0 = t[__builtin_amdgcn_ubfe(w, 0, pb)], e1 = t[__builtin_amdgcn_ubfe(w, pb, pb)];
+    const uint2 e2 = t[__builtin_amdgcn_ubfe(w, 2 * pb, pb)], e3 = t[__builtin_amdgcn_ubfe(w, 3 * pb, pb)];
+    hi = as_h8(make_uint4(e0.x, e1.x, e2.x, e3.x));
+    lo = as_h8(make_uint4(e0.y, e1.y, e2.y, e3.y));
 }
 
 // Fold one page pair into the wavefront's state (as pair_update: m and lsum
 // of head l%16, O in the C layout with rows = heads 4(l/16) + i, tile nt
 // column n = dimension 8n + nt).  na / nb: valid tokens of the two pages.
 __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h8_t (&qh)[4], const h8_t (&ql)[4],
-                                      const uint32_t* cbk, float scale, int na, int nb, float& m, float& lsum,
+                                      const uint2* cbk, float scale, int na, int nb, float& m, float& lsum,
                                       f4_t (&o)[8], int lane) {
     const int g = lane >> 4;
     const int sh3 = 8 * ((6 * g) & 3);
@@ -317,7 +319,7 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             h8_t kh, kl;
-            tq_dequant8(chunk[s], s < 2 ? 4 : 3, s < 2 ? 0 : 16, cbk, kh, kl);
+            tq_dequant8(chunk[s], s < 2 ? 4 : 3, cbk, kh, kl);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], acc, 0, 0, 0);
@@ -373,22 +375,16 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
     for (int nt = 0; nt < 8; ++nt) {
         uint32_t e[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = cbk[ln.cbo + __builtin_amdgcn_ubfe(vw[j], ln.bits * nt, ln.bits)];
-        uint4 h, l;
-        h.x = __builtin_amdgcn_perm(e[1], e[0], 0x05040100u);
-        l.x = __builtin_amdgcn_perm(e[1], e[0], 0x07060302u);
-        h.y = __builtin_amdgcn_perm(e[3], e[2], 0x05040100u);
-        l.y = __builtin_amdgcn_perm(e[3], e[2], 0x07060302u);
-        h.z = __builtin_amdgcn_perm(e[5], e[4], 0x05040100u);
-        l.z = __builtin_amdgcn_perm(e[5], e[4], 0x07060302u);
-        h.w = __builtin_amdgcn_perm(e[7], e[6], 0x05040100u);
-        l.w = __builtin_amdgcn_perm(e[7], e[6], 0x07060302u);
+        for (int j = 0; j < 8; ++j) e[j] = cbk[ln.cbo + __builtin_amdgcn_ubfe(vw[j], ln.bits * nt, ln.bits)].x;
+        const uint4 h = make_uint4(__builtin_amdgcn_perm(e[1], e[0], 0x05040100u),
+                                   __builtin_amdgcn_perm(e[3], e[2], 0x05040100u),
+                                   __builtin_amdgcn_perm(e[5], e[4], 0x05040100u),
+                                   __builtin_amdgcn_perm(e[7], e[6], 0x05040100u));
         f4_t acc = o[nt];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= c[i];
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, as_h8(h), acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, as_h8(h), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, as_h8(l), acc, 0, 0, 0);
         o[nt] = acc;
     }
 }
@@ -406,8 +402,9 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
     __shared__ float qrot[G * HD];
-    __shared__ uint32_t cbk[24];
+    __shared__ uint2 cbk[kTqTbl];
 
+    NX_ATRACE(0);
     if (slot < 0) {
         slot = split;
         nrec = nsplit;
@@ -428,31 +425,41 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
     const TqLane ln(a, t);
 
-    // q, the K signs and the codebook first (one clamped load per value and
-    // thread), then the first pair of pages: all in flight before q is rotated
-    constexpr int QPT = (G * HD + kAttnThreads - 1) / kAttnThreads;
-    float qv[QPT], sv[QPT];
-#pragma unroll
-    for (int u = 0; u < QPT; ++u) {
-        const int idx = min((int)threadIdx.x + u * kAttnThreads, G * HD - 1);
-        qv[u] = a.q[((size_t)b * a.hq + kvh * G) * HD + idx];
-        sv[u] = a.ksign[idx % HD];
-    }
-    const float cbv = c_tq_cb[min((int)threadIdx.x, 23)];
-    TqPair ra, rb;
-    tq_load_pair(ra, a, ln, blk_of(0), blk_of(1), valid_of(1), kvh, lane);
+    // q and the K signs (wavefront w: head min(w, G - 1), lane l: dimensions
+    // l and l + 64), the codebook, then the first pair of pages: all in
+    // flight before q is rotated
+    const float* qsrc = a.q + ((size_t)b * a.hq + kvh * G + min(wave, G - 1)) * HD;
+    const float q0 = qsrc[lane], q1 = qsrc[lane + 64];
+    const float s0 = a.ksign[lane], s1 = a.ksign[lane + 64];
+    // pair-table entry of this thread (threads < kTqTbl)
+    const int te = min((int)threadIdx.x, kTqTbl - 1);
+    const float cb0 = te < kTqTbl4 ? c_tq_cb[te & 15] : c_tq_cb[16 + ((te - kTqTbl4) & 7)];
+    const float cb1 = te < kTqTbl4 ? c_tq_cb[te >> 4] : c_tq_cb[16 + ((te - kTqTbl4) >> 3)];
+    // page pair p (pages 2p, 2p + 1 of the wavefront); pairs past the
+    // wavefront's pages re-read its first page and are not processed
+    auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
+    auto load_p = [&](TqPair& r, int p) {
+        tq_load_pair(r, a, ln, blk_or0(2 * p), blk_or0(2 * p + 1), valid_of(2 * p + 1), kvh, lane);
+    };
+    TqPair r0, r1, r2;
+    load_p(r0, 0);
+    if constexpr (PIPE) load_p(r1, 1);
 
-    if (threadIdx.x < 24) {
-        const _Float16 hi = (_Float16)cbv;
-        const _Float16 lo = (_Float16)(cbv - (float)hi);
-        cbk[threadIdx.x] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+    if (threadIdx.x < kTqTbl) {
+        const _Float16 h0 = (_Float16)cb0, h1 = (_Float16)cb1;
+        const _Float16 l0 = (_Float16)(cb0 - (float)h0), l1 = (_Float16)(cb1 - (float)h1);
+        cbk[threadIdx.x] = make_uint2(
+            (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+            (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16));
     }
-#pragma unroll
-    for (int u = 0; u < QPT; ++u) {
-        const int idx = threadIdx.x + u * kAttnThreads;
-        if (idx < G * HD) qrot[idx] = sv[u] * qv[u];
+    // q~ = H D q of head w in wavefront w
+    if (wave < G) {
+        float u0 = s0 * q0, u1 = s1 * q1;
+        wave_fwht128(u0, u1);
+        qrot[wave * HD + lane] = u0;
+        qrot[wave * HD + lane + 64] = u1;
     }
-    lds_fwht<G>(qrot);
+    __syncthreads();
 
     // q~ as the B operand: column = head t (columns past G repeat head G-1),
     // k-step s in the dimension order of the K operand
@@ -471,26 +478,33 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
         }
     }
     const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
+    NX_ATRACE(1);
 
     float m = -__builtin_inff(), lsum = 0.0f;
     f4_t o[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    auto upd = [&](const TqPair& r, int p) {
+        tq_pair_update(r, ln, qh, ql, cbk, scale, valid_of(2 * p), valid_of(2 * p + 1), m, lsum, o, lane);
+    };
     if constexpr (PIPE) {
-        // the next pair is requested unconditionally (a pair past the
-        // wavefront's pages re-reads its first page and is not processed), so
-        // the wait for the current pair leaves the next one in flight
-        auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
-        for (int i = 0; i < npw; i += 4) {
-            tq_load_pair(rb, a, ln, blk_or0(i + 2), blk_or0(i + 3), valid_of(i + 3), kvh, lane);
-            tq_pair_update(ra, ln, qh, ql, cbk, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
-            if (i + 2 >= npw) break;
-            tq_load_pair(ra, a, ln, blk_or0(i + 4), blk_or0(i + 5), valid_of(i + 5), kvh, lane);
-            tq_pair_update(rb, ln, qh, ql, cbk, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
+        // three register sets in rotation: pair p + 2 is requested before
+        // pair p is used, so two pairs stay in flight
+        const int np = (npw + 1) / 2;
+        for (int p = 0; p < np; p += 3) {
+            load_p(r2, p + 2);
+            upd(r0, p);
+            if (p + 1 >= np) break;
+            load_p(r0, p + 3);
+            upd(r1, p + 1);
+            if (p + 2 >= np) break;
+            load_p(r1, p + 4);
+            upd(r2, p + 2);
         }
     } else {
-        if (npw > 0) tq_pair_update(ra, ln, qh, ql, cbk, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
+        if (npw > 0) upd(r0, 0);
     }
+    NX_ATRACE(2);
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     // wavefront record: rows h = 4g + i < G of O (column t of tile nt is
@@ -520,7 +534,10 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
         if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+    NX_ATRACE(4);
     if (last) merge_last<G, HD, true>(a, nrec, ntq, kvh, b);
+    if (last) NX_ATRACE(5);
+    NX_ATRACE(6);
 }
 
 template <int G, bool PIPE>

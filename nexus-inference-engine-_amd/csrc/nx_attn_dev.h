@@ -236,20 +236,26 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
 }
 
 
-// In-LDS FWHT of G vectors of 128 (canonical butterfly network).
-template <int G>
-__device__ inline void lds_fwht(float* v) {
-    for (int h = 1; h < 128; h <<= 1) {
-        __syncthreads();
-        for (int t = threadIdx.x; t < G * 64; t += kAttnThreads) {
-            const int g = t >> 6, k = t & 63;
-            const int j = ((k / h) * 2 * h) + (k % h);
-            const float x = v[g * 128 + j], y = v[g * 128 + j + h];
-            v[g * 128 + j] = x + y;
-            v[g * 128 + j + h] = x - y;
+// FWHT of one vector of 128 held by a wavefront, lane l holding elements l
+// (u0) and l + 64 (u1): the canonical butterfly network, stages h = 1, 2,
+// .., 64 each taking (x_j, x_{j+h}) -> (x_j + x_{j+h}, x_j - x_{j+h}) for the
+// j with bit h clear (h <= 32 across lanes, h = 64 inside the lane).  On
+// return element l is u0 and element l + 64 is u1.
+__device__ inline void wave_fwht128(float& u0, float& u1) {
+    const int lane = threadIdx.x & 63;
+    for (int h = 1; h < 64; h <<= 1) {
+        const float p0 = __shfl_xor(u0, h, 64), p1 = __shfl_xor(u1, h, 64);
+        if (lane & h) {
+            u0 = p0 - u0;
+            u1 = p1 - u1;
+        } else {
+            u0 = u0 + p0;
+            u1 = u1 + p1;
         }
     }
-    __syncthreads();
+    const float a = u0 + u1, b = u0 - u1;
+    u0 = a;
+    u1 = b;
 }
 
 constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
@@ -361,9 +367,14 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
         __syncthreads();
         const float4 rp = group_sum();
         if (tid < NC) *reinterpret_cast<float4*>(&ovp[4 * tid]) = rp;
-        lds_fwht<G>(ov);
-        for (int idx = tid; idx < G * HD; idx += kAttnThreads)
-            out[idx] = f2h_bits(ov[idx] * kTqScale * a.vsign[idx % HD] + ovp[idx]);
+        __syncthreads();
+        // head w rotated back in wavefront w
+        for (int hh = wave; hh < G; hh += kAttnWaves) {
+            float u0 = ov[hh * HD + lane], u1 = ov[hh * HD + lane + 64];
+            wave_fwht128(u0, u1);
+            out[hh * HD + lane] = f2h_bits(u0 * kTqScale * a.vsign[lane] + ovp[hh * HD + lane]);
+            out[hh * HD + lane + 64] = f2h_bits(u1 * kTqScale * a.vsign[lane + 64] + ovp[hh * HD + lane + 64]);
+        }
     } else if (tid < NC) {
         const uint32_t w0 = (uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16);
         const uint32_t w1 = (uint32_t)f2h_bits(r.z) | ((uint32_t)f2h_bits(r.w) << 16);
