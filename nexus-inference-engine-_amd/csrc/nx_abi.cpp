@@ -196,6 +196,7 @@ nx_status nx_destroy(nx_ctx* ctx) {
     if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
     if (ctx->attn_counts) (void)hipFree(ctx->attn_counts);
     if (ctx->smp_ws) (void)hipFree(ctx->smp_ws);
+    if (ctx->gemv_ws) (void)hipFree(ctx->gemv_ws);
     (void)hipEventDestroy(ctx->ev0);
     (void)hipEventDestroy(ctx->ev1);
     (void)hipStreamDestroy(ctx->stream);
@@ -396,6 +397,27 @@ nx_status nx_token_resume(nx_ctx* ctx) {
 }
 
 // ---------------------------------------------------------------------- ops --
+// The K-part workspace of a batched GEMV (nx::gemv_kparts), grown outside
+// capture; under capture without room it stays null and the GEMV runs in
+// one launch.
+static nx_status gemv_kpart_ws(nx_ctx* ctx, int N, int K, int batch, float** out) {
+    *out = nullptr;
+    const int kp = nx::gemv_kparts(K, batch);
+    if (kp == 0) return NX_OK;
+    const size_t need = (size_t)kp * batch * N;
+    if (need > ctx->gemv_ws_floats) {
+        if (ctx->capturing) return NX_OK;
+        NX_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->gemv_ws) (void)hipFree(ctx->gemv_ws);
+        ctx->gemv_ws = nullptr;
+        ctx->gemv_ws_floats = 0;
+        NX_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->gemv_ws), need * sizeof(float)));
+        ctx->gemv_ws_floats = need;
+    }
+    *out = ctx->gemv_ws;
+    return NX_OK;
+}
+
 static nx_status gemv_common(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
                              int batch, int out_bytes, const char* name, nx::GemvArgs& a) {
     if (!ctx) return NX_ERR_INVALID;
@@ -417,7 +439,7 @@ static nx_status gemv_common(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf
     a.x16 = dptr<const uint16_t>(x);
     a.ldx = K;
     a.ldy = N;
-    return NX_OK;
+    return gemv_kpart_ws(ctx, N, K, batch, &a.kpart);
 }
 
 nx_status nx_gemv_int4_g32(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf y, int N, int K,
@@ -1068,6 +1090,8 @@ nx_status nx_ffn_int4_g32(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_buf 
     dn.ldx = (int)lda;
     dn.y32 = dptr<float>(y);
     dn.ldy = d;
+    s = gemv_kpart_ws(ctx, d, F, batch, &dn.kpart);
+    if (s != NX_OK) return s;
     return launched(ctx, nx::gemv_launch(nx::X_F16, accumulate ? nx::E_ACC : nx::E_F32, dn, ctx->stream), "ffn down");
 }
 
@@ -1144,6 +1168,10 @@ nx_status nx_reserve_workspace(nx_ctx* ctx, int batch, int max_ffn, int vocab, i
     if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_reserve_workspace inside a token batch");
     nx_status s = NX_OK;
     if (max_ffn > 0) s = ensure_ffn_ws(ctx, (size_t)batch * ffn_lda(max_ffn) * 2);
+    if (s == NX_OK && max_ffn > 0 && n_heads > 0 && head_dim > 0) {
+        float* unused = nullptr;  // the down projection's K parts (d = n_heads * head_dim)
+        s = gemv_kpart_ws(ctx, n_heads * head_dim, max_ffn, batch, &unused);
+    }
     if (s == NX_OK && vocab > 0) s = ensure_smp_ws(ctx, (size_t)batch * vocab);
     if (s == NX_OK && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_ctx > 0) {
         if (n_heads % n_kv_heads) return fail(ctx, NX_ERR_INVALID, "nx_reserve_workspace: n_heads % n_kv_heads");

@@ -421,11 +421,21 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
     const int N = args.N, K = args.K;
+    // E_PART: block x is row group x / kparts over K part x % kparts, groups
+    // [gbase0, gbase0 + Gx); otherwise all of K
+    int bx = blockIdx.x, gq = 0, gbase0 = 0, Gx = args.G;
+    if constexpr (EPI == E_PART) {
+        gq = blockIdx.x % args.kparts;
+        bx = blockIdx.x / args.kparts;
+        const int gpp = ((args.G + args.kparts - 1) / args.kparts + kMfmaGW - 1) / kMfmaGW * kMfmaGW;
+        gbase0 = gq * gpp;
+        Gx = min(args.G, gbase0 + gpp) - gbase0;
+    }
     // the nb blocks of a grid row share the tiles evenly: block x takes
     // [x ntile / nb, (x + 1) ntile / nb), at most tpb tiles
     const int ntile = (N + 15) / 16, tpb = (ntile + nb - 1) / nb;
-    const int t0 = (int)((long)blockIdx.x * ntile / nb), nt = (int)((long)(blockIdx.x + 1) * ntile / nb) - t0;
-    if (nt <= 0) return;
+    const int t0 = (int)((long)bx * ntile / nb), nt = (int)((long)(bx + 1) * ntile / nb) - t0;
+    if (nt <= 0 || Gx <= 0) return;
     static_assert(!MOE || XS == X_F16, "routed experts take fp16 x");
     GemvArgs a = args;
     // routed experts: grid row y's expert and its token slots; x row of this
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
         xrow = pl[(args.moe_xslot ? 8 : 16) + min(tid % kMfmaCols, a.batch - 1)];
         yrow = pl[8 + min(c, kMoePlanMaxSlots - 1)];
     }
-    const int nstage = (K + kMfmaKC - 1) / kMfmaKC;
+    const int nstage = EPI == E_PART ? 1 : (K + kMfmaKC - 1) / kMfmaKC;
     // the input: staged in LDS for one stage (and RMSNorm's 1/rms per batch
     // row); run by the streaming loop after its first weight requests
     auto stage_input = [&]() {
@@ -513,7 +523,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     // item's groups loaded with its weights.
     auto stream = [&](auto xg_tag) {
         constexpr bool XG = decltype(xg_tag)::value;
-        const int G = a.G, wpt = kMfmaWaves / ks, kslice = wave % ks, tsub = wave / ks;
+        const int G = Gx, wpt = kMfmaWaves / ks, kslice = wave % ks, tsub = wave / ks;
         const int gps = XG ? (G + ks - 1) / ks : ((G + ks - 1) / ks + kMfmaGW - 1) / kMfmaGW * kMfmaGW;
         const int npass = (gps + kMfmaGW - 1) / kMfmaGW, send = min(G, (kslice + 1) * gps);
         const int iters = (tpb + wpt - 1) / wpt, nitem = iters * npass;
@@ -522,7 +532,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
         auto item_gs = [&](int j) { return kslice * gps + kMfmaGW * (j % npass); };
         auto load_item = [&](int j, MfmaRegs<XG>& r) {
             const int gs = item_gs(j), keep = j < nitem && item_tile(j) < t0 + nt ? 1 : 0;
-            mfma_load<SALIGN, FULL, XG>(a, item_tile(j) * 16, 0, gs, min(send, gs + kMfmaGW), r, keep, xoff);
+            mfma_load<SALIGN, FULL, XG>(a, item_tile(j) * 16, gbase0, gs, min(send, gs + kMfmaGW), r, keep, xoff);
         };
         auto tile_end = [&](int j, const mf4_t& acc) {
             const int slot = (j / npass) & 1, t = item_tile(j);
@@ -544,7 +554,14 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         res[i] += part[slot][((tsub * ks + s2) * 16 + 4 * kq + i) * kMfmaCols + c];
-                epilogue<EPI, 4>(a, yrow, t * 16 + 4 * kq, N, res, best_v, best_i);
+                if constexpr (EPI == E_PART) {
+                    float* dst = a.kpart + ((size_t)gq * a.batch + c) * N + t * 16 + 4 * kq;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (t * 16 + 4 * kq + i < N) dst[i] = res[i];
+                } else {
+                    epilogue<EPI, 4>(a, yrow, t * 16 + 4 * kq, N, res, best_v, best_i);
+                }
             }
         };
         mf4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -554,11 +571,11 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             // behind them (a CU returns data in request order, so x is not
             // held up), and only then is the input used
             StageRegs<XS> sr;
-            stage_issue<XS>(a, 0, (K + 31) / 32, sr, xrow);
+            stage_issue<XS>(a, 32 * gbase0, Gx, sr, xrow);
             load_item(0, ra);
             load_item(1, rb);
             __builtin_amdgcn_sched_barrier(0);
-            stage_finish<XS, XS == X_RMSNORM>(a, 0, (K + 31) / 32, sr, xs, inv, red, EPI * 2 + XS);
+            stage_finish<XS, XS == X_RMSNORM>(a, 32 * gbase0, Gx, sr, xs, inv, red, EPI * 2 + XS);
             __syncthreads();  // x staged
             NX_MTRACE(1);
         } else {
@@ -688,6 +705,21 @@ hipError_t launch_b1(const GemvArgs& a, hipStream_t st, int ny = 1) {
     return hipGetLastError();
 }
 
+// Sum of the K parts of a split GEMV in part order, then the epilogue
+// (E_ACC: y32 += sum, E_F32: y32 = sum, E_F16: y16 = fp16(sum)).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemv_ksum(const float* __restrict__ part, int kparts, int B, int N,
+                                                   float* y32, uint16_t* y16, int ldy) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= B * N) return;
+    const int b = i / N, n = i - b * N;
+    float s = 0.0f;
+    for (int q = 0; q < kparts; ++q) s += part[((size_t)q * B + b) * N + n];
+    if (EPI == E_ACC) y32[(size_t)b * ldy + n] += s;
+    else if (EPI == E_F32) y32[(size_t)b * ldy + n] = s;
+    else y16[(size_t)b * ldy + n] = f2h_bits(s);
+}
+
 // Batch 2..8 on the matrix cores.  One stage (K <= 4096): ks wavefronts per
 // tile, the fewest that still give every wavefront of one block per CU a
 // tile, and enough tiles per block for one round of blocks.  Longer K with
@@ -701,6 +733,27 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       a.ldx % (XS == X_F16 ? 8 : 4) == 0;
     const bool salign = a.G % 4 == 0;
+    if constexpr (XS == X_F16 && !MOE && (EPI == E_F16 || EPI == E_F32 || EPI == E_ACC)) {
+        // K split over gemv_kparts(K) groups of blocks: each stages its part
+        // of x once for its tiles (a block holding all of K would read all of
+        // x for 16 rows); the part sums meet in a second launch
+        const int kp = gemv_kparts(a.K, a.batch);
+        if (kp > 0 && a.kpart && xvec && salign) {
+            GemvArgs p = a;
+            p.kparts = kp;
+            const int rg = std::max(1, std::min(ntile, cus / kp));
+            const int per_block = (ntile + rg - 1) / rg;
+            const int ksp = per_block <= 1 ? 8 : per_block <= 2 ? 4 : per_block <= 4 ? 2 : 1;
+            hipLaunchKernelGGL((k_gemv_mfma<X_F16, E_PART, true, true, false, false>), dim3(rg * kp),
+                               dim3(kMfmaThreads), 0, st, p, rg, ksp);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            const int n = a.batch * a.N;
+            hipLaunchKernelGGL((k_gemv_ksum<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, a.kpart, kp, a.batch,
+                               a.N, a.y32, a.y16, a.ldy);
+            return hipGetLastError();
+        }
+    }
     const bool xg = XS == X_F16 && a.K > kMfmaKC && a.K % 32 == 0 && xvec && salign;
     int blocks = ntile, ks = 1;
     if (a.K <= kMfmaKC || xg) {

@@ -40,6 +40,10 @@ struct nx_ctx {
     // scratch rows of nx_sample (grow-only)
     float* smp_ws = nullptr;
     size_t smp_ws_floats = 0;
+    // K-part sums of batched GEMVs with K beyond 4096 (grow-only; without
+    // room, under capture, one launch streams all of K)
+    float* gemv_ws = nullptr;
+    size_t gemv_ws_floats = 0;
     float c4[16], b4[15], c3[8], b3[7];
 };
 

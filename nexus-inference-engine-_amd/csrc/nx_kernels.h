@@ -23,6 +23,7 @@ enum Epi : int {
     E_QKV = 3,      // RoPE on q/k rows; q -> q32; k,v -> fp16 pages (or fp32 kv_tmp)
     E_SWIGLU = 4,   // rows (2j, 2j+1) = (gate j, up j) -> act16[b][j] = fp16(silu(g)*u)
     E_LOGITS = 5,   // y32[b][n] = y and running argmax into best[b]
+    E_PART = 6,     // kpart[part][b][n] = partial sum over the block's K part
 };
 
 // Row pairs per wavefront of a batch-1 GEMV: base pairs each, one more for
@@ -70,7 +71,17 @@ struct GemvArgs {
     const int32_t* moe_plan;
     size_t moe_wstride, moe_sstride;
     int moe_xslot;
+    // Batch 2..8 with fp16 x and K beyond 4096 (the down projection): K is
+    // split over gemv_kparts(K) groups of blocks, which write partial sums
+    // [part][batch][N] here; a second launch adds them in part order and
+    // runs the epilogue.  nullptr: one launch streams all of K per block.
+    float* kpart;
+    int kparts;  // set by the launcher
 };
+
+// Parts of a K-split batch-2..8 GEMV (0: none); the workspace is
+// gemv_kparts(K) * batch * N floats.
+inline int gemv_kparts(int K, int batch) { return batch >= 2 && K > 4096 && K % 32 == 0 ? (K + 4095) / 4096 : 0; }
 
 // Routing plan of one active expert (int32 words): [0] expert id (-1: no
 // expert for this grid row), [1] its number of token slots n (<= 8),

@@ -68,6 +68,7 @@ struct nx_model {
     float* q = nullptr;
     uint16_t* att16 = nullptr;
     uint16_t* act16 = nullptr;
+    float* kpart = nullptr;  // K-part sums of the batched down projection
     float* logits = nullptr;
     float* kv_tmp = nullptr;
     uint16_t* xn16 = nullptr;
@@ -433,6 +434,7 @@ nx_status enqueue_step(nx_model* m) {
             dn.ldx = m->Fp;
             dn.y32 = m->h;
             dn.ldy = d;
+            dn.kpart = m->kpart;
             NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, dn, st));
         } else {
             nx::MoeArgs ma{};
@@ -668,6 +670,7 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     NX_TRY(dalloc(m, &m->q, (size_t)B * m->qdim));
     NX_TRY(dalloc(m, &m->att16, (size_t)B * m->qdim));
     NX_TRY(dalloc(m, &m->act16, (size_t)B * m->Fp));
+    if (nx::gemv_kparts(c.ffn, B) > 0) NX_TRY(dalloc(m, &m->kpart, (size_t)nx::gemv_kparts(c.ffn, B) * B * d));
     NX_TRY(dalloc(m, &m->logits, (size_t)B * c.vocab));
     NX_TRY(dalloc(m, &m->kv_tmp, (size_t)B * 2 * m->kvdim));
     NX_TRY(dalloc(m, &m->xn16, (size_t)B * d));
