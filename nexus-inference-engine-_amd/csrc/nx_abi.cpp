@@ -900,10 +900,12 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
         ++r;
     }
     for (; r < rows; ++r) plan[(size_t)r * nx::kMoePlanInts] = -1;
-    // workspace: plan | act16[batch*k][Fp] | y32[batch*k][d]
+    // workspace: plan | act16[batch*k][Fp] | y32[batch*k][d] | K-part sums
+    // of the down projection [kparts][batch*k][d]
     const size_t off_act = (plan.size() * 4 + 255) / 256 * 256;
     const size_t off_y = (off_act + (size_t)batch * k * Fp * 2 + 255) / 256 * 256;
-    const size_t total = off_y + (size_t)batch * k * d * 4;
+    const size_t off_kp = (off_y + (size_t)batch * k * d * 4 + 255) / 256 * 256;
+    const size_t total = off_kp + (size_t)nx::gemv_kparts(F, batch) * batch * k * d * 4;
     nx_status s = ensure_attn_ws(ctx, total);
     if (s != NX_OK) return s;
     char* ws = static_cast<char*>(ctx->attn_ws);
@@ -925,6 +927,7 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
     a.weights = dptr<const float>(w);
     a.act16 = reinterpret_cast<uint16_t*>(ws + off_act);
     a.y32 = reinterpret_cast<float*>(ws + off_y);
+    a.kpart = nx::gemv_kparts(F, batch) > 0 ? reinterpret_cast<float*>(ws + off_kp) : nullptr;
     a.out = dptr<float>(out);
     a.accumulate = accumulate;
     hipError_t e = nx::moe_gate_up_launch(a, ctx->stream);

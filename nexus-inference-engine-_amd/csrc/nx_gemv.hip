@@ -555,7 +555,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
                     for (int i = 0; i < 4; ++i)
                         res[i] += part[slot][((tsub * ks + s2) * 16 + 4 * kq + i) * kMfmaCols + c];
                 if constexpr (EPI == E_PART) {
-                    float* dst = a.kpart + ((size_t)gq * a.batch + c) * N + t * 16 + 4 * kq;
+                    // routed experts: the partial row of the lane's token slot
+                    float* dst = a.kpart + ((size_t)gq * a.kpart_rows + (MOE ? yrow : c)) * N + t * 16 + 4 * kq;
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         if (t * 16 + 4 * kq + i < N) dst[i] = res[i];
@@ -733,21 +734,23 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       a.ldx % (XS == X_F16 ? 8 : 4) == 0;
     const bool salign = a.G % 4 == 0;
-    if constexpr (XS == X_F16 && !MOE && (EPI == E_F16 || EPI == E_F32 || EPI == E_ACC)) {
+    if constexpr (XS == X_F16 && (MOE ? EPI == E_F32 : (EPI == E_F16 || EPI == E_F32 || EPI == E_ACC))) {
         // K split over gemv_kparts(K) groups of blocks: each stages its part
         // of x once for its tiles (a block holding all of K would read all of
-        // x for 16 rows); the part sums meet in a second launch
+        // x for 16 rows); the part sums meet in a second launch (routed
+        // experts: in the combine)
         const int kp = gemv_kparts(a.K, a.batch);
         if (kp > 0 && a.kpart && xvec && salign) {
             GemvArgs p = a;
             p.kparts = kp;
-            const int rg = std::max(1, std::min(ntile, cus / kp));
+            if (!MOE) p.kpart_rows = a.batch;
+            const int rg = std::max(1, std::min(ntile, cus / (kp * ny)));
             const int per_block = (ntile + rg - 1) / rg;
             const int ksp = per_block <= 1 ? 8 : per_block <= 2 ? 4 : per_block <= 4 ? 2 : 1;
-            hipLaunchKernelGGL((k_gemv_mfma<X_F16, E_PART, true, true, false, false>), dim3(rg * kp),
+            hipLaunchKernelGGL((k_gemv_mfma<X_F16, E_PART, true, true, MOE, false>), dim3(rg * kp, ny),
                                dim3(kMfmaThreads), 0, st, p, rg, ksp);
             const hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
+            if (e != hipSuccess || MOE) return e;
             const int n = a.batch * a.N;
             hipLaunchKernelGGL((k_gemv_ksum<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, a.kpart, kp, a.batch,
                                a.N, a.y32, a.y16, a.ldy);
@@ -866,6 +869,10 @@ hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
     a.moe_wstride = (size_t)N * G * 16;
     a.moe_sstride = (size_t)N * G;
     a.moe_xslot = GATEUP ? 0 : 1;
+    if (!GATEUP && moe_down_split(m)) {
+        a.kpart = m.kpart;
+        a.kpart_rows = m.batch * m.k;
+    }
     const int ny = moe_plan_rows(m.E, m.batch, m.k);
     constexpr int EPI = GATEUP ? E_SWIGLU : E_F32;
     const int gpl = (G + kWave - 1) / kWave;
@@ -883,6 +890,14 @@ hipError_t moe_launch(const MoeFfnArgs& m, hipStream_t st) {
 }
 
 }  // namespace
+
+// The conditions of launch_mfma's K split for the routed down projection
+// (x = act16 rows of Fp elements, G = F / 32 groups).
+bool moe_down_split(const MoeFfnArgs& m) {
+    const int Fp = (m.F + 31) / 32 * 32, G = (m.F + 31) / 32;
+    return m.kpart && gemv_kparts(m.F, m.batch) > 0 && m.F % 8 == 0 && Fp % 8 == 0 && G % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(m.act16) & 15u) == 0;
+}
 
 hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st) { return moe_launch<true>(a, st); }
 hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st) { return moe_launch<false>(a, st); }

@@ -76,7 +76,8 @@ struct GemvArgs {
     // [part][batch][N] here; a second launch adds them in part order and
     // runs the epilogue.  nullptr: one launch streams all of K per block.
     float* kpart;
-    int kparts;  // set by the launcher
+    int kparts;      // set by the launcher
+    int kpart_rows;  // rows of one part: batch, or batch * k slots for routed experts
 };
 
 // Parts of a K-split batch-2..8 GEMV (0: none); the workspace is
@@ -282,7 +283,13 @@ struct MoeFfnArgs {
     float* y32;                 // [batch*k][d]
     float* out;                 // [batch][d]
     int accumulate;
+    // batch >= 2: the down projection's K-part sums [gemv_kparts(F, batch)]
+    // [batch*k][d], added by the combine (nullptr: y32 holds the sums)
+    float* kpart;
 };
+// Whether the routed down projection writes K-part sums (a.kpart) for the
+// combine to add; decided once here for both launches.
+bool moe_down_split(const MoeFfnArgs& a);
 hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st);

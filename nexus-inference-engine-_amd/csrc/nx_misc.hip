@@ -481,13 +481,25 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     if (tid == 0) build_lists(a, sid, scnt);
 }
 
-__global__ void k_moe_combine(const float* y32, const float* weights, float* out, int d, int k,
-                              int batch, int accumulate) {
+// kparts > 0: slot s's down projection is the sum, in part order, of the K
+// parts kpart[q][s] instead of y32[s].
+__global__ void k_moe_combine(const float* y32, const float* kpart, int kparts, const float* weights, float* out,
+                              int d, int k, int batch, int accumulate) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= batch * d) return;
     const int b = t / d, i = t % d;
     float acc = 0.0f;
-    for (int j = 0; j < k; ++j) acc += weights[(size_t)b * k + j] * y32[((size_t)b * k + j) * d + i];
+    for (int j = 0; j < k; ++j) {
+        const size_t s = (size_t)b * k + j;
+        float y;
+        if (kparts > 0) {
+            y = 0.0f;
+            for (int q = 0; q < kparts; ++q) y += kpart[((size_t)q * batch * k + s) * d + i];
+        } else {
+            y = y32[s * d + i];
+        }
+        acc += weights[s] * y;
+    }
     out[t] = accumulate ? out[t] + acc : acc;
 }
 
@@ -630,7 +642,8 @@ hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st) {
 
 hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st) {
     const size_t n = (size_t)a.batch * a.d;
-    hipLaunchKernelGGL(k_moe_combine, grid1(n, 256), dim3(256), 0, st, a.y32, a.weights, a.out,
+    const int kparts = moe_down_split(a) ? gemv_kparts(a.F, a.batch) : 0;
+    hipLaunchKernelGGL(k_moe_combine, grid1(n, 256), dim3(256), 0, st, a.y32, a.kpart, kparts, a.weights, a.out,
                        a.d, a.k, a.batch, a.accumulate);
     return hipGetLastError();
 }

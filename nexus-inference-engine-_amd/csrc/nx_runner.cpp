@@ -80,6 +80,7 @@ struct nx_model {
     unsigned* moe_counter = nullptr;  // arrival counter of the MoE routing launch (zero between launches)
     uint16_t* moe_act = nullptr;
     float* moe_y = nullptr;
+    float* moe_kpart = nullptr;  // K-part sums of the batched routed down projection
     float* attn_part = nullptr;
     // tiered pages: the fp16 window's ring of hot_pages pages per sequence
     // (hot_bt[b][p] = b * hot_pages + p % hot_pages, the same max_blocks
@@ -490,6 +491,7 @@ nx_status enqueue_step(nx_model* m) {
             mf.weights = m->moe_w;
             mf.act16 = m->moe_act;
             mf.y32 = m->moe_y;
+            mf.kpart = m->moe_kpart;
             mf.out = m->h;
             mf.accumulate = 1;
             NX_LAUNCH(m, nx::moe_gate_up_launch(mf, st));
@@ -683,6 +685,8 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         NX_TRY(dalloc(m, &m->moe_counter, 64));
         NX_TRY(dalloc(m, &m->moe_act, (size_t)B * c.top_k * m->Fp));
         NX_TRY(dalloc(m, &m->moe_y, (size_t)B * c.top_k * d));
+        if (nx::gemv_kparts(F, B) > 0)
+            NX_TRY(dalloc(m, &m->moe_kpart, (size_t)nx::gemv_kparts(F, B) * B * c.top_k * d));
     }
     NX_TRY(dalloc(m, &m->attn_counts, nx::attn_count_words(B, c.n_kv_heads)));
     if (c.kv_kind == 2) {
