@@ -360,8 +360,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode measurement (no GEMV, NXF, prefill or tiering lines)")
-    ap.add_argument("--profile-kernel", choices=["ffn", "attention", "xxh32"],
-                    help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-kernel", choices=["ffn", "attention", "xxh32", "gemv"],
+                    help="only launch one kernel 64 times over the layers (for rocprofv3 --pmc); gemv: "
+                         "the standalone GEMV microbench of --gemv-shape at --batch")
+    ap.add_argument("--gemv-shape", default="14336x4096", help="N x K of --profile-kernel gemv")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched prefill measurement (for rocprofv3)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -387,6 +389,14 @@ def main() -> int:
     if args.prefill_only:
         ctx = nexus_amd.Context(0)
         print(json.dumps({"prefill": prefill_bench(ctx, MODELS[args.model])}))
+        ctx.close()
+        return 0
+    if args.profile_kernel == "gemv":
+        global GEMV_SHAPES
+        GEMV_SHAPES = [tuple(int(v) for v in args.gemv_shape.split("x"))]
+        ctx = nexus_amd.Context(0)
+        for r in gemv_microbench(ctx, args.batch, iters=20):
+            print(json.dumps(r))
         ctx.close()
         return 0
     if args.profile_kernel == "xxh32":
