@@ -664,6 +664,65 @@ __global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batc
         tq_encode_wave(src, vsign, vc4 + dst * 32, vc3 + dst * 24, vn + dst, codes[wave]);
 }
 
+// A prompt chunk's K and V rows [n][2][hkv*128] (positions p0 + t) into the
+// sequence's pages, one wavefront per vector (the encoder of k_tq_append).
+__global__ __launch_bounds__(256) void k_tq_encode_rows(const float* kvrows, int n, int p0, int hkv,
+                                                        const float* ksign, const float* vsign, uint8_t* kc4,
+                                                        uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3,
+                                                        uint16_t* vn, const int32_t* bt) {
+    __shared__ uint8_t codes[4][128];
+    const int wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * 4 + wave;  // (t, kv, h)
+    if (v >= n * 2 * hkv) return;
+    const int t = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv, p = p0 + t;
+    const size_t dst = ((size_t)bt[p / kPage] * hkv + h) * kPage + p % kPage;
+    const float* src = kvrows + ((size_t)t * 2 + kv) * hkv * 128 + (size_t)h * 128;
+    if (kv == 0)
+        tq_encode_wave(src, ksign, kc4 + dst * 32, kc3 + dst * 24, kn + dst, codes[wave]);
+    else
+        tq_encode_wave(src, vsign, vc4 + dst * 32, vc3 + dst * 24, vn + dst, codes[wave]);
+}
+
+// TurboQuant vectors of positions < npos of one sequence back to fp16 pages
+// of the same blocks, one wavefront per vector: u_i = codebook value of code
+// i (4-bit for i < 64, 3-bit after), the FWHT, then ((u_i / sqrt(128)) *
+// sign_i) * norm -- the decoder's arithmetic in its order -- rounded to fp16.
+// K also as its fp16 remainder (klo = K - fp16(K)), for scores to fp32
+// accuracy.
+__global__ __launch_bounds__(256) void k_tq_decode_pages(const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn,
+                                                         const uint8_t* vc4, const uint8_t* vc3, const uint16_t* vn,
+                                                         const float* ksign, const float* vsign, const int32_t* bt,
+                                                         int npos, int hkv, uint16_t* kpool, uint16_t* vpool,
+                                                         uint16_t* klo) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * 4 + wave;  // (p, kv, h)
+    if (v >= npos * 2 * hkv) return;
+    const int p = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv;
+    const size_t blk = (size_t)bt[p / kPage], vec = (blk * hkv + h) * kPage + p % kPage;
+    const uint8_t* c4 = (kv ? vc4 : kc4) + vec * 32;
+    const uint8_t* c3 = (kv ? vc3 : kc3) + vec * 24;
+    const float* sign = kv ? vsign : ksign;
+    const int q4 = (c4[lane >> 1] >> (4 * (lane & 1))) & 15;
+    const int bit = 3 * lane, byte = bit >> 3;
+    const int q3 = ((c3[byte] | (c3[min(byte + 1, 23)] << 8)) >> (bit & 7)) & 7;
+    float u0 = c_tq_cb[q4], u1 = c_tq_cb[16 + q3];
+    wave_fwht128(u0, u1);
+    const float nrm = h2f_bits((kv ? vn : kn)[vec]);
+    const float x0 = ((u0 * kTqScale) * sign[lane]) * nrm, x1 = ((u1 * kTqScale) * sign[lane + 64]) * nrm;
+    const uint16_t o0 = f2h_bits(x0), o1 = f2h_bits(x1);
+    const size_t page = (blk * hkv + h) * kPage * 128;
+    const int slot = p % kPage;
+    if (kv) {  // V pages are dimension-major [128][16]
+        vpool[page + (size_t)lane * kPage + slot] = o0;
+        vpool[page + (size_t)(lane + 64) * kPage + slot] = o1;
+    } else {   // K pages are token-major [16][128]
+        kpool[page + (size_t)slot * 128 + lane] = o0;
+        kpool[page + (size_t)slot * 128 + lane + 64] = o1;
+        klo[page + (size_t)slot * 128 + lane] = f2h_bits(x0 - h2f_bits(o0));
+        klo[page + (size_t)slot * 128 + lane + 64] = f2h_bits(x1 - h2f_bits(o1));
+    }
+}
+
 // Causal prefill attention over fp16 pages: query rows t < P of one sequence
 // (positions p0 + t) attend to the positions <= their own.  A wavefront takes
 // 16 consecutive queries of one head as the columns of the decode layout
@@ -673,7 +732,9 @@ __global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batc
 // query's position; the scores get the causal mask per (token, query).
 // Blocks are numbered from the last query tile down, so the longest walks
 // start first.
-template <int G, int HD>
+// KLO: K pages are fp16 hi (kpool) + lo (kpool_lo), a third product per step
+// (prefill over TurboQuant pages decoded for it).
+template <int G, int HD, bool KLO = false>
 __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int P) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, t = lane & 15;
     const int kvh = blockIdx.y, h = kvh * G + w;
@@ -714,15 +775,32 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     auto blk_of = [&](int p) { return a.block_table[min(p, npages - 1)]; };
     auto valid_of = [&](int p) { return p < npages ? min(max(lastpos + 1 - kPage * p, 0), kPage) : 0; };
     PairRaw<HD> ra, rb;
+    PairKlo<HD> la, lb;
+    // K lo of a pair (KLO), the same addresses in kpool_lo
+    auto load_lo = [&](PairKlo<HD>& r, int pa_, int pb_) {
+        if constexpr (KLO) {
+#pragma unroll
+            for (int pg = 0; pg < 2; ++pg) {
+                const int blk = pg ? (valid_of(pb_) > 0 ? blk_of(pb_) : blk_of(pa_)) : blk_of(pa_);
+                const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
+#pragma unroll
+                for (int s = 0; s < HD / 32; ++s)
+                    r.k[pg][s] = *reinterpret_cast<const uint4*>(a.kpool_lo + base + (size_t)t * HD + 32 * s + 8 * g);
+            }
+        }
+    };
+    load_lo(la, 0, 1);
     load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
     for (int pa = 0; pa < npages; pa += 4) {
+        load_lo(lb, pa + 2, pa + 3);
         load_pair<HD>(rb, a, blk_of(pa + 2), valid_of(pa + 2), blk_of(pa + 3), valid_of(pa + 3), kvh, lane);
-        pair_update<HD, true>(ra, qh, ql, scale, valid_of(pa), valid_of(pa + 1), m, lsum, o, lane, kPage * pa,
-                              kPage * (pa + 1), qpos);
+        pair_update<HD, true, KLO>(ra, qh, ql, scale, valid_of(pa), valid_of(pa + 1), m, lsum, o, lane, kPage * pa,
+                                   kPage * (pa + 1), qpos, &la);
         if (pa + 2 >= npages) break;
+        load_lo(la, pa + 4, pa + 5);
         load_pair<HD>(ra, a, blk_of(pa + 4), valid_of(pa + 4), blk_of(pa + 5), valid_of(pa + 5), kvh, lane);
-        pair_update<HD, true>(rb, qh, ql, scale, valid_of(pa + 2), valid_of(pa + 3), m, lsum, o, lane,
-                              kPage * (pa + 2), kPage * (pa + 3), qpos);
+        pair_update<HD, true, KLO>(rb, qh, ql, scale, valid_of(pa + 2), valid_of(pa + 3), m, lsum, o, lane,
+                                   kPage * (pa + 2), kPage * (pa + 3), qpos, &lb);
     }
     // the query's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);
@@ -837,15 +915,28 @@ hipError_t round_f16_launch(float* x, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
+// K hi + lo pages (kpool_lo) for head_dim 128 and at most 4 query heads per
+// kv head (with 8, the kernel's two wavefronts per SIMD cannot hold the lo
+// operands).
+template <int G, int HD>
+hipError_t attn_prefill_case(const AttnArgs& a, int p0, int P, dim3 grid, hipStream_t st) {
+    if constexpr (HD == 128 && G <= 4) {
+        if (a.kpool_lo) {
+            hipLaunchKernelGGL((k_attn_prefill<G, HD, true>), grid, dim3(64 * G), 0, st, a, p0, P);
+            return hipGetLastError();
+        }
+    }
+    if (a.kpool_lo) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_attn_prefill<G, HD>), grid, dim3(64 * G), 0, st, a, p0, P);
+    return hipGetLastError();
+}
+
 hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st) {
     if (P < 1 || p0 < 0 || !a.block_table) return hipErrorInvalidValue;
     const dim3 grid((P + 15) / 16, a.hkv);
     const int G = a.hq / a.hkv;
-#define NX_PF_ATTN_CASE(GG, HH)                                                                       \
-    if (G == GG && a.hd == HH) {                                                                      \
-        hipLaunchKernelGGL((k_attn_prefill<GG, HH>), grid, dim3(64 * GG), 0, st, a, p0, P);           \
-        return hipGetLastError();                                                                     \
-    }
+#define NX_PF_ATTN_CASE(GG, HH) \
+    if (G == GG && a.hd == HH) return attn_prefill_case<GG, HH>(a, p0, P, grid, st);
     NX_PF_ATTN_CASE(1, 64)
     NX_PF_ATTN_CASE(2, 64)
     NX_PF_ATTN_CASE(4, 64)
@@ -1061,6 +1152,27 @@ hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* s
     if (nvec <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_tq_encode_ctx, dim3((nvec + 3) / 4), dim3(256), 0, st, x, ctx, hkv, signs,
                        c4, c3, norms, block_table, max_blocks, b);
+    return hipGetLastError();
+}
+
+hipError_t tq_encode_rows_launch(const float* kvrows, int n, int p0, int hkv, const float* ksign, const float* vsign,
+                                 uint8_t* kc4, uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                                 const int32_t* bt, hipStream_t st) {
+    const int nvec = n * 2 * hkv;
+    if (nvec <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tq_encode_rows, dim3((nvec + 3) / 4), dim3(256), 0, st, kvrows, n, p0, hkv, ksign, vsign, kc4,
+                       kc3, kn, vc4, vc3, vn, bt);
+    return hipGetLastError();
+}
+
+hipError_t tq_decode_pages_launch(const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4,
+                                  const uint8_t* vc3, const uint16_t* vn, const float* ksign, const float* vsign,
+                                  const int32_t* bt, int npos, int hkv, uint16_t* kpool, uint16_t* vpool,
+                                  uint16_t* klo, hipStream_t st) {
+    const int nvec = npos * 2 * hkv;
+    if (nvec <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tq_decode_pages, dim3((nvec + 3) / 4), dim3(256), 0, st, kc4, kc3, kn, vc4, vc3, vn, ksign,
+                       vsign, bt, npos, hkv, kpool, vpool, klo);
     return hipGetLastError();
 }
 

@@ -132,6 +132,12 @@ struct PairRaw {
     uint2 v[HD / 16][2];  // V of pages a, b: tokens 4g..4g+3 of dim 16 nt + l%16
 };
 
+// The low fp16 parts (K - fp16(K)) of a pair's K, same layout as PairRaw::k.
+template <int HD>
+struct PairKlo {
+    uint4 k[2][HD / 32];
+};
+
 // Bits of a lane's V words (tokens 4g .. 4g+3, fp16 each) that hold the first
 // n tokens of the page.
 __device__ inline uint2 vmask_of(int n, int g) {
@@ -174,11 +180,12 @@ __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, in
 // CAUSAL (prefill): the columns are query tokens instead of heads; token
 // 4(l/16) + i of page a (b) is at position pos_a (pos_b) + 4(l/16) + i and
 // is masked for the query at position qpos (this lane's column) when later.
-template <int HD, bool CAUSAL = false>
+// KLO: K is fp16 hi + lo (kl), a third product K_lo q_hi per step.
+template <int HD, bool CAUSAL = false, bool KLO = false>
 __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 32],
                                    const h8_t (&ql)[HD / 32], float scale, int na, int nb, float& m,
                                    float& lsum, f4_t (&o)[HD / 16], int lane, int pos_a = 0, int pos_b = 0,
-                                   int qpos = 0) {
+                                   int qpos = 0, const PairKlo<HD>* kl = nullptr) {
     const int g = lane >> 4;
     f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -187,6 +194,10 @@ __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 3
         sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), ql[s], sa, 0, 0, 0);
         sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), qh[s], sb, 0, 0, 0);
         sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), ql[s], sb, 0, 0, 0);
+        if constexpr (KLO) {
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kl->k[0][s]), qh[s], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kl->k[1][s]), qh[s], sb, 0, 0, 0);
+        }
     }
     float p[8];
     float mloc = -__builtin_inff();

@@ -99,6 +99,7 @@ struct AttnArgs {
     const float* q;            // [batch][hq][hd]
     const uint16_t* kpool;     // fp16 pages
     const uint16_t* vpool;
+    const uint16_t* kpool_lo;  // prefill over decoded TurboQuant pages: K - fp16(K), or nullptr
     // TurboQuant pages (head_dim 128)
     const uint8_t *kc4, *kc3, *vc4, *vc3;
     const uint16_t *kn, *vn;
@@ -209,6 +210,18 @@ hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* s
                                 uint16_t* norms, const int32_t* block_table, int max_blocks,
                                 int b, hipStream_t st);
 // Append one token per sequence from kv_tmp [batch][2][hkv*128].
+// Encode the K and V rows [n][2][hkv*128] of positions p0 .. p0 + n - 1 of
+// one sequence (block table bt of that sequence) into its pages.
+hipError_t tq_encode_rows_launch(const float* kvrows, int n, int p0, int hkv, const float* ksign, const float* vsign,
+                                 uint8_t* kc4, uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                                 const int32_t* bt, hipStream_t st);
+// Decode positions 0 .. npos - 1 of one sequence's TurboQuant pages into fp16
+// pages of the same blocks (K token-major, V dimension-major), K also as its
+// fp16 remainder klo (same layout).
+hipError_t tq_decode_pages_launch(const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4,
+                                  const uint8_t* vc3, const uint16_t* vn, const float* ksign, const float* vsign,
+                                  const int32_t* bt, int npos, int hkv, uint16_t* kpool, uint16_t* vpool,
+                                  uint16_t* klo, hipStream_t st);
 hipError_t tq_append_launch(const float* kv_tmp, int batch, int hkv, const float* ksign,
                             const float* vsign, const float* b4, const float* b3, uint8_t* kc4,
                             uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
@@ -313,7 +326,7 @@ hipError_t pf_embed_launch(const int32_t* tokens, int P, const uint16_t* embed, 
                            hipStream_t st);
 hipError_t pf_rope_kv_launch(const float* qkv, int ld, int P, int p0, int qdim, int kvdim, int hd, int hkv,
                              const float* cos_t, const float* sin_t, const int32_t* bt, uint16_t* kpool,
-                             uint16_t* vpool, float* q32, hipStream_t st);
+                             uint16_t* vpool, float* q32, hipStream_t st, float* kvrows = nullptr);
 
 // Sampling (nx_sample.hip): sample_token of hybrid_model.cpp:2023-2099 per
 // sequence; the draw is u_fixed when >= 0, else u[b], else a counter-based

@@ -195,9 +195,12 @@ __global__ __launch_bounds__(256) void k_pf_embed(const int32_t* tokens, const u
 // RoPE of the q and k rows of token t at position p0 + t (the rotation of
 // the decode QKV epilogue), q to q32 [P][qdim], k and v (fp16, RNE) into
 // the pages of the sequence (block table row bt).
+// kvrows != nullptr (TurboQuant pages): K and V rows go there as fp32
+// [P][2][kvdim] for the encoder instead of into fp16 pages.
 __global__ __launch_bounds__(256) void k_pf_rope_kv(const float* qkv, int ld, int P, int p0, int qdim, int kvdim,
                                                     int hd, int hkv, const float* cos_t, const float* sin_t,
-                                                    const int32_t* bt, uint16_t* kpool, uint16_t* vpool, float* q32) {
+                                                    const int32_t* bt, uint16_t* kpool, uint16_t* vpool, float* q32,
+                                                    float* kvrows) {
     const int npair = (qdim + 2 * kvdim) / 2;
     const long idx = (long)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (long)P * npair) return;
@@ -217,6 +220,11 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(const float* qkv, int ld, in
         return;
     }
     const int kv = row < qdim + kvdim ? 0 : 1, j = row - qdim - kv * kvdim, kvh = j / hd, dd = j % hd;
+    if (kvrows) {
+        kvrows[((size_t)t * 2 + kv) * kvdim + j] = v0;
+        kvrows[((size_t)t * 2 + kv) * kvdim + j + 1] = v1;
+        return;
+    }
     const size_t page = ((size_t)bt[p / kPage] * hkv + kvh) * kPage * hd;
     if (kv) {  // V pages are dimension-major [hd][16]
         vpool[page + (size_t)dd * kPage + p % kPage] = f2h_bits(v0);
@@ -267,10 +275,10 @@ hipError_t pf_embed_launch(const int32_t* tokens, int P, const uint16_t* embed, 
 
 hipError_t pf_rope_kv_launch(const float* qkv, int ld, int P, int p0, int qdim, int kvdim, int hd, int hkv,
                              const float* cos_t, const float* sin_t, const int32_t* bt, uint16_t* kpool,
-                             uint16_t* vpool, float* q32, hipStream_t st) {
+                             uint16_t* vpool, float* q32, hipStream_t st, float* kvrows) {
     const long n = (long)P * ((qdim + 2 * kvdim) / 2);
     hipLaunchKernelGGL(k_pf_rope_kv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, qkv, ld, P, p0, qdim, kvdim,
-                       hd, hkv, cos_t, sin_t, bt, kpool, vpool, q32);
+                       hd, hkv, cos_t, sin_t, bt, kpool, vpool, q32, kvrows);
     return hipGetLastError();
 }
 

@@ -804,7 +804,19 @@ struct PrefillScratch {
 // wavefront), output projection and FFN GEMMs with the residual accumulated
 // in place.  Then the final RMSNorm,
 // lm_head and argmax of the last token leave its greedy successor pending,
-// as after P decode steps.  Dense models with fp16 pages.
+// as after P decode steps.  Dense models.  TurboQuant pages (kv_kind 1):
+// the chunk's K and V rows are encoded into the pages, and the attention runs
+// over the sequence's pages decoded to fp16 (positions up to the chunk's
+// last), so every query sees the stored (quantized) K and V of the positions
+// before it and of its own, as the decode steps would.
+// Models the batched prefill takes: dense, fp16 pages or TurboQuant pages
+// (the latter with at most 4 query heads per kv head).
+bool batched_prefill_ok(const nx_model* m) {
+    const nx_model_config& c = m->c;
+    return m->prefill_batched && c.n_experts == 0 &&
+           (c.kv_kind == 0 || (c.kv_kind == 1 && c.n_heads <= 4 * c.n_kv_heads));
+}
+
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
     const nx_model_config& c = m->c;
     nx_ctx* ctx = m->ctx;
@@ -821,6 +833,15 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
         sc.get(&x16, (size_t)C * d) != hipSuccess || sc.get(&att, (size_t)C * m->qdim) != hipSuccess ||
         sc.get(&act, (size_t)C * m->Fp) != hipSuccess)
         return fail(ctx, NX_ERR_OOM, "prefill: scratch for %d tokens", C);
+    const bool tq = c.kv_kind == 1;
+    float* kvrows = nullptr;
+    uint16_t *k16 = nullptr, *k16lo = nullptr, *v16 = nullptr;  // decoded pages (every block of the pool)
+    if (tq) {
+        const size_t pool = (size_t)m->n_blocks * hkv * nx::kPage * hd;
+        if (sc.get(&kvrows, (size_t)C * 2 * m->kvdim) != hipSuccess || sc.get(&k16, pool) != hipSuccess ||
+            sc.get(&k16lo, pool) != hipSuccess || sc.get(&v16, pool) != hipSuccess)
+            return fail(ctx, NX_ERR_OOM, "prefill: decoded pages");
+    }
     int last = 0;
     for (int done = 0; done < P; done += C) {
         const int n = std::min(C, P - done), pb = p0 + done;
@@ -841,12 +862,20 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             g.y32 = qkv;
             g.ldy = m->nqkv;
             NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_F32, g, st));
+            const int32_t* bt = m->block_table + (size_t)b * MB;
             NX_LAUNCH(m, nx::pf_rope_kv_launch(qkv, m->nqkv, n, pb, m->qdim, m->kvdim, hd, hkv, m->rope_cos, m->rope_sin,
-                                               m->block_table + (size_t)b * MB, ly.kpool, ly.vpool, q, st));
+                                               bt, ly.kpool, ly.vpool, q, st, kvrows));
+            if (tq) {
+                NX_LAUNCH(m, nx::tq_encode_rows_launch(kvrows, n, pb, hkv, ly.ksign, ly.vsign, ly.kc4, ly.kc3, ly.kn,
+                                                       ly.vc4, ly.vc3, ly.vn, bt, st));
+                NX_LAUNCH(m, nx::tq_decode_pages_launch(ly.kc4, ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, ly.ksign,
+                                                        ly.vsign, bt, pb + n, hkv, k16, v16, k16lo, st));
+            }
             nx::AttnArgs at{};
             at.q = q;
-            at.kpool = ly.kpool;
-            at.vpool = ly.vpool;
+            at.kpool = tq ? k16 : ly.kpool;
+            at.vpool = tq ? v16 : ly.vpool;
+            at.kpool_lo = tq ? k16lo : nullptr;
             at.block_table = m->block_table + (size_t)b * MB;
             at.out16 = att;
             at.batch = 1;
@@ -981,7 +1010,7 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
                 return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
     }
     for (int b = 0; b < B; ++b) m->active[(size_t)b] = 1;
-    if (m->prefill_batched && c.n_experts == 0 && c.kv_kind == 0) {
+    if (batched_prefill_ok(m)) {
         for (int b = 0; b < B; ++b) NX_TRY(prefill_batched(m, b, prompt + (size_t)b * P, P));
         if (next_tokens) NX_TRY(nx_model_pending(m, next_tokens));
         return NX_OK;
@@ -1205,7 +1234,7 @@ nx_status nx_model_admit(nx_model* m, int slot, const int32_t* prompt, int P, in
     const int32_t minus1 = -1;
     NX_HIP(m->ctx, hipMemcpyAsync(m->pos + slot, &minus1, 4, hipMemcpyHostToDevice, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
-    if (m->prefill_batched && c.n_experts == 0 && c.kv_kind == 0) {
+    if (batched_prefill_ok(m)) {
         // the slot's prompt alone through the batched prefill
         NX_TRY(prefill_batched(m, slot, prompt, P));
     } else {
