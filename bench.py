@@ -326,7 +326,9 @@ def prefill_bench(ctx, base: dict, P: int = 2048) -> dict:
     m.close()
     d, F, L = base["d_model"], base["ffn"], base["n_layers"]
     qkv = (base["n_heads"] + 2 * base["n_kv_heads"]) * base["head_dim"]
-    w_flops = 2.0 * P * L * d * (qkv + base["n_heads"] * base["head_dim"] + 3 * F)
+    # routed experts: each token runs top_k experts' FFNs and the router
+    experts = base["top_k"] if base["n_experts"] > 0 else 1
+    w_flops = 2.0 * P * L * d * (qkv + base["n_heads"] * base["head_dim"] + 3 * F * experts + base["n_experts"])
     att_flops = 4.0 * L * base["n_heads"] * base["head_dim"] * P * (P + 1) / 2
     M, N, K = 2048, 2 * F, d
     G = (K + 31) // 32
@@ -484,7 +486,7 @@ def main() -> int:
             decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 8, 0, 4096, 128),
         ]
     nxf = nxf_verify_bench(ctx, not args.no_cpu) if full else None
-    pre = prefill_bench(ctx, base) if full and not moe else None
+    pre = prefill_bench(ctx, base) if full else None
     tier = tiering_bench(ctx, base) if full and base["head_dim"] == 128 else None
     ctx.close()
     kv_name = ["fp16", "TurboQuant 3.5-bit", f"tiered (last {args.hot_window} positions fp16, older pages "

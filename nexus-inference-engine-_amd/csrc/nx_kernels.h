@@ -300,6 +300,16 @@ struct MoeFfnArgs {
     // [batch*k][d], added by the combine (nullptr: y32 holds the sums)
     float* kpart;
 };
+// Batched prefill of MoE layers: routing of n tokens from their logits
+// [n][E] (as decode routes them), token slots grouped by expert (counts:
+// cnt[E] then offsets[E]; row_tok[row] = token, slot_row[t * k + j] = row);
+// gathering fp16 rows; the weighted combine h[t] += sum_j w yg[row].
+hipError_t pf_route_launch(const float* logits, int n, int E, int k, int32_t* ids, float* w, int32_t* row_tok,
+                           int32_t* slot_row, int32_t* counts, hipStream_t st);
+hipError_t pf_gather_launch(const uint16_t* x16, const int32_t* row_tok, int rows, int d, uint16_t* xg,
+                            hipStream_t st);
+hipError_t pf_moe_combine_launch(const float* yg, const int32_t* slot_row, const float* w, int n, int k, int d,
+                                 float* h, hipStream_t st);
 // Whether the routed down projection writes K-part sums (a.kpart) for the
 // combine to add; decided once here for both launches.
 bool moe_down_split(const MoeFfnArgs& a);

@@ -505,6 +505,67 @@ __global__ void k_moe_combine(const float* y32, const float* kpart, int kparts, 
 
 inline dim3 grid1(size_t n, int threads) { return dim3((unsigned)((n + threads - 1) / threads)); }
 
+// Prefill routing of n tokens (logits [n][E]): each token routed as a decode
+// step routes it (route_row), then the token slots (t, j) grouped by expert
+// in (t, j) order: expert e's rows are off[e] .. off[e] + cnt[e] - 1 of the
+// gathered buffers, row r holding token row_tok[r]; slot_row[t * k + j] is
+// the row of slot (t, j).  counts: cnt[E] then off[E].  One block.
+constexpr int kPfRouteThreads = 256;
+__global__ __launch_bounds__(kPfRouteThreads) void k_pf_route(const float* logits, int n, int E, int k, int32_t* ids,
+                                                              float* w, int32_t* row_tok, int32_t* slot_row,
+                                                              int32_t* counts) {
+    __shared__ float p[kPfRouteThreads][64];
+    __shared__ int sid[kPfRouteThreads][8];
+    __shared__ float sw[kPfRouteThreads][8];
+    __shared__ int cnt[64], off[64];
+    const int tid = threadIdx.x;
+    for (int t = tid; t < n; t += kPfRouteThreads) {
+        route_row(logits + (size_t)t * E, E, k, sid[tid], sw[tid], p[tid]);
+        for (int j = 0; j < k; ++j) {
+            ids[(size_t)t * k + j] = sid[tid][j];
+            w[(size_t)t * k + j] = sw[tid][j];
+        }
+    }
+    __syncthreads();
+    if (tid != 0) return;
+    for (int e = 0; e < E; ++e) cnt[e] = 0;
+    for (int s = 0; s < n * k; ++s) cnt[ids[s]] += 1;
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+        off[e] = acc;
+        acc += cnt[e];
+        counts[e] = cnt[e];
+        counts[E + e] = off[e];
+        cnt[e] = 0;
+    }
+    for (int s = 0; s < n * k; ++s) {
+        const int e = ids[s], r = off[e] + cnt[e];
+        cnt[e] += 1;
+        row_tok[r] = s / k;
+        slot_row[s] = r;
+    }
+}
+
+// xg[r] = x16[row_tok[r]] (fp16 rows of d, d % 8 == 0), 8 elements a thread.
+__global__ __launch_bounds__(256) void k_pf_gather(const uint16_t* x16, const int32_t* row_tok, int rows, int d,
+                                                   uint16_t* xg) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x, per = d / 8;
+    if (i >= (long)rows * per) return;
+    const int r = (int)(i / per), c = (int)(i % per);
+    reinterpret_cast<uint4*>(xg + (size_t)r * d)[c] = reinterpret_cast<const uint4*>(x16 + (size_t)row_tok[r] * d)[c];
+}
+
+// h[t] += sum_j w[t][j] * yg[slot_row[t * k + j]] (the decode combine's order).
+__global__ void k_pf_moe_combine(const float* yg, const int32_t* slot_row, const float* w, int n, int k, int d,
+                                 float* h) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n * d) return;
+    const int t = (int)(i / d), c = (int)(i % d);
+    float acc = 0.0f;
+    for (int j = 0; j < k; ++j) acc += w[(size_t)t * k + j] * yg[(size_t)slot_row[(size_t)t * k + j] * d + c];
+    h[i] = h[i] + acc;
+}
+
 }  // namespace
 
 hipError_t rmsnorm_launch(const float* x, const float* w, uint16_t* out, int dim, float eps,
@@ -637,6 +698,27 @@ hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st) {
     if (a.batch > 64 || a.E > 64 || a.k > 8) return hipErrorInvalidValue;
     if (a.plan && a.batch > kMoePlanMaxSlots) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t pf_route_launch(const float* logits, int n, int E, int k, int32_t* ids, float* w, int32_t* row_tok,
+                           int32_t* slot_row, int32_t* counts, hipStream_t st) {
+    if (n < 1 || E < 1 || E > 64 || k < 1 || k > 8 || k > E) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_route, dim3(1), dim3(kPfRouteThreads), 0, st, logits, n, E, k, ids, w, row_tok, slot_row,
+                       counts);
+    return hipGetLastError();
+}
+
+hipError_t pf_gather_launch(const uint16_t* x16, const int32_t* row_tok, int rows, int d, uint16_t* xg,
+                            hipStream_t st) {
+    if (d % 8 || rows < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_gather, grid1((size_t)rows * (d / 8), 256), dim3(256), 0, st, x16, row_tok, rows, d, xg);
+    return hipGetLastError();
+}
+
+hipError_t pf_moe_combine_launch(const float* yg, const int32_t* slot_row, const float* w, int n, int k, int d,
+                                 float* h, hipStream_t st) {
+    hipLaunchKernelGGL(k_pf_moe_combine, grid1((size_t)n * d, 256), dim3(256), 0, st, yg, slot_row, w, n, k, d, h);
     return hipGetLastError();
 }
 

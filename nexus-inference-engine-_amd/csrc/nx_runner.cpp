@@ -809,12 +809,11 @@ struct PrefillScratch {
 // over the sequence's pages decoded to fp16 (positions up to the chunk's
 // last), so every query sees the stored (quantized) K and V of the positions
 // before it and of its own, as the decode steps would.
-// Models the batched prefill takes: dense, fp16 pages or TurboQuant pages
-// (the latter with at most 4 query heads per kv head).
+// Models the batched prefill takes: dense or MoE, fp16 pages or TurboQuant
+// pages (the latter with at most 4 query heads per kv head).
 bool batched_prefill_ok(const nx_model* m) {
     const nx_model_config& c = m->c;
-    return m->prefill_batched && c.n_experts == 0 &&
-           (c.kv_kind == 0 || (c.kv_kind == 1 && c.n_heads <= 4 * c.n_kv_heads));
+    return m->prefill_batched && (c.kv_kind == 0 || (c.kv_kind == 1 && c.n_heads <= 4 * c.n_kv_heads));
 }
 
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
@@ -833,6 +832,19 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
         sc.get(&x16, (size_t)C * d) != hipSuccess || sc.get(&att, (size_t)C * m->qdim) != hipSuccess ||
         sc.get(&act, (size_t)C * m->Fp) != hipSuccess)
         return fail(ctx, NX_ERR_OOM, "prefill: scratch for %d tokens", C);
+    // MoE layers: router logits, routing, token slots grouped by expert
+    // (gathered x rows, their activations and outputs)
+    const int E = c.n_experts, kx = c.top_k, S = C * std::max(kx, 1);
+    float *rlog = nullptr, *rw = nullptr, *yg = nullptr;
+    int32_t *rid = nullptr, *row_tok = nullptr, *slot_row = nullptr, *counts = nullptr;
+    uint16_t *xg = nullptr, *actg = nullptr;
+    if (E > 0 && (sc.get(&rlog, (size_t)C * E) != hipSuccess || sc.get(&rw, (size_t)S) != hipSuccess ||
+                  sc.get(&rid, (size_t)S) != hipSuccess || sc.get(&row_tok, (size_t)S) != hipSuccess ||
+                  sc.get(&slot_row, (size_t)S) != hipSuccess || sc.get(&counts, (size_t)2 * E) != hipSuccess ||
+                  sc.get(&xg, (size_t)S * d) != hipSuccess || sc.get(&actg, (size_t)S * m->Fp) != hipSuccess ||
+                  sc.get(&yg, (size_t)S * d) != hipSuccess))
+        return fail(ctx, NX_ERR_OOM, "prefill: expert scratch for %d tokens", C);
+    std::vector<int32_t> hcounts((size_t)2 * std::max(E, 1));
     const bool tq = c.kv_kind == 1;
     float* kvrows = nullptr;
     uint16_t *k16 = nullptr, *k16lo = nullptr, *v16 = nullptr;  // decoded pages (every block of the pool)
@@ -898,6 +910,57 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             o.ldy = d;
             NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_ACC, o, st));
             NX_LAUNCH(m, nx::rmsnorm_launch(h, ly.norm_ffn, x16, d, c.eps, n, st));
+            if (E > 0) {
+                // router GEMM, routing as the decode step routes, then each
+                // active expert's gate/up and down GEMMs over its gathered
+                // token rows, and the weighted combine into h
+                nx::PfGemmArgs r{};
+                r.x = x16;
+                r.ldx = d;
+                r.W = ly.wr;
+                r.S = ly.sr;
+                r.M = n;
+                r.N = E;
+                r.K = d;
+                r.G = m->Gd;
+                r.y32 = rlog;
+                r.ldy = E;
+                NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_F32, r, st));
+                NX_LAUNCH(m, nx::pf_route_launch(rlog, n, E, kx, rid, rw, row_tok, slot_row, counts, st));
+                NX_LAUNCH(m, nx::pf_gather_launch(x16, row_tok, n * kx, d, xg, st));
+                NX_HIP(ctx, hipMemcpyAsync(hcounts.data(), counts, (size_t)2 * E * 4, hipMemcpyDeviceToHost, st));
+                NX_HIP(ctx, hipStreamSynchronize(st));
+                for (int e = 0; e < E; ++e) {
+                    const int ne = hcounts[(size_t)e], oe = hcounts[(size_t)E + e];
+                    if (ne == 0) continue;
+                    nx::PfGemmArgs f{};
+                    f.x = xg + (size_t)oe * d;
+                    f.ldx = d;
+                    f.W = ly.w13 + (size_t)e * 2 * F * m->Gd * 16;
+                    f.S = ly.s13 + (size_t)e * 2 * F * m->Gd;
+                    f.M = ne;
+                    f.N = 2 * F;
+                    f.K = d;
+                    f.G = m->Gd;
+                    f.act16 = actg + (size_t)oe * m->Fp;
+                    f.lda = m->Fp;
+                    NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_SWIGLU, f, st));
+                    nx::PfGemmArgs dn{};
+                    dn.x = actg + (size_t)oe * m->Fp;
+                    dn.ldx = m->Fp;
+                    dn.W = ly.w2 + (size_t)e * d * m->Gf * 16;
+                    dn.S = ly.s2 + (size_t)e * d * m->Gf;
+                    dn.M = ne;
+                    dn.N = d;
+                    dn.K = F;
+                    dn.G = m->Gf;
+                    dn.y32 = yg + (size_t)oe * d;
+                    dn.ldy = d;
+                    NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_F32, dn, st));
+                }
+                NX_LAUNCH(m, nx::pf_moe_combine_launch(yg, slot_row, rw, n, kx, d, h, st));
+                continue;
+            }
             nx::PfGemmArgs f{};
             f.x = x16;
             f.ldx = d;
