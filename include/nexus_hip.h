@@ -335,6 +335,14 @@ typedef struct {
     float norm_sigma;       /* RMSNorm weights: 0 = all 1.0, else 1 + N(0, norm_sigma)
                                seeded per tensor (synthetic models) */
     int hot_window;         /* kv_kind 2: positions kept fp16, a positive multiple of 16 */
+    int warm_window;        /* kv_kind 2: 0 = two tiers (fp16, TurboQuant); else a positive
+                               multiple of 16: the positions before the window kept TurboQuant
+                               (Warm, a ring of warm_window / 16 + 1 pages per sequence), older
+                               pages re-encoded on the device to the Cool form (3-bit codes on
+                               every coordinate, 50 bytes per vector) as they leave that range:
+                               the Hot -> Warm -> Cool tiers of PagedKVCache
+                               (kv/paged_attention.h:18-24, compress_tier
+                               kv/paged_attention.cpp:244-291) as a per-page policy */
 } nx_model_config;
 
 typedef struct nx_model nx_model;
@@ -417,8 +425,10 @@ nx_status nx_model_fill_context(nx_model* m, int ctx, int n_outlier);
 /* The stored form of position pos of sequence b in layer `layer`, all kv
  * heads, K (kv 0) or V (kv 1): form 0 = fp16 [hkv][head_dim] (2 * hkv *
  * head_dim bytes), form 1 = TurboQuant [hkv] x (32 bytes of 4-bit codes, 24
- * of 3-bit codes, fp16 norm) (58 * hkv bytes); *form tells which (tiered
- * pages: 1 before the window, 0 in it).  The per-position read-back of
+ * of 3-bit codes, fp16 norm) (58 * hkv bytes), form 2 = Cool [hkv] x (48
+ * bytes of 3-bit codes, fp16 norm) (50 * hkv bytes); *form tells which
+ * (tiered pages: 1 before the window, 0 in it, 2 before the Warm range with
+ * three tiers).  The per-position read-back of
  * PagedKVCache::get_vectors (kv/paged_attention.cpp:161-230), as stored
  * rather than decompressed; cap = bytes available at out. */
 nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* form, void* out, size_t cap);

@@ -240,8 +240,12 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int ns
 // needs two perms per pair, for more bank conflicts); the low 16 bits of
 // entry c are hi(c4[c]) (hi(c3[c])) for the value operand.  The V norm is
 // folded into P, the K norm and the scale into the scores.
+// Cool pages (COOL) hold 48-byte records, 3-bit codes on every dimension:
+// chunk n (dimensions 8n .. 8n+7) at byte 3n, so dimensions 0..63 form a
+// 24-byte half laid out as the 3-bit part above, 64..127 a second one.  The
+// same operand layouts apply, every chunk decoded through the 3-bit table.
 struct TqPair {
-    uint2 k4[2], k3[2];           // pages a, b: 4-bit chunks (2g, 2g+1) of token l%16; the 8 bytes holding its 3-bit chunks (2g, 2g+1)
+    uint2 k4[2], k3[2];           // pages a, b: 4-bit chunks (2g, 2g+1) of token l%16 (Cool: the 8 bytes holding its chunks 2g, 2g+1); the 8 bytes holding its 3-bit chunks (2g, 2g+1) (Cool: chunks 8+2g, 9+2g)
     uint32_t v0[2][4], v1[2][4];  // pages a, b, tokens 4g + j: the dwords holding chunk l%16
     uint2 kn[2], vn[2];           // pages a, b: fp16 norms of tokens 4g .. 4g+3
 };
@@ -254,7 +258,16 @@ struct TqPair {
 struct TqLane {
     const uint8_t* vb;
     int d1, stride, shift, bits, cbo;
-    __device__ TqLane(const AttnArgs& a, int n) {
+    __device__ TqLane(const AttnArgs& a, int n, bool cool = false) {
+        if (cool) {  // chunk n: 3 bytes at byte 3n of a 48-byte record
+            vb = a.vcc + 4 * ((3 * n) >> 2);
+            d1 = 4 * (((3 * n + 2) >> 2) - ((3 * n) >> 2));
+            stride = 48;
+            shift = (3 * n) & 3;
+            bits = 3;
+            cbo = kTqTbl4;
+            return;
+        }
         const bool b4 = n < 8;
         const int j = n - 8;
         vb = (b4 ? a.vc4 : a.vc3) + (b4 ? 4 * n : 4 * ((3 * j) >> 2));
@@ -269,24 +282,30 @@ struct TqLane {
 // Every load is unconditional (see load_pair): page b with no valid token
 // re-reads page a (blka is a valid block); tokens past the valid counts are
 // masked when the pair is processed.
+template <bool COOL = false>
 __device__ inline void tq_load_pair(TqPair& r, const AttnArgs& a, const TqLane& ln, int blka, int blkb,
                                     int nb, int kvh, int lane) {
     const int t = lane & 15, g = lane >> 4;
-    const int o3 = 4 * ((3 * g) >> 1);  // dword holding byte 6g of the 3-bit part
+    const int o3 = 4 * ((3 * g) >> 1);  // dword holding byte 6g of a 3-bit part
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
         const int blk = pg && nb > 0 ? blkb : blka;
         const size_t rec = ((size_t)blk * a.hkv + kvh) * kPage;
-        r.k4[pg] = *reinterpret_cast<const uint2*>(a.kc4 + (rec + t) * 32 + 8 * g);
-        r.k3[pg] = *reinterpret_cast<const uint2*>(a.kc3 + (rec + t) * 24 + o3);
+        if constexpr (COOL) {
+            r.k4[pg] = *reinterpret_cast<const uint2*>(a.kcc + (rec + t) * 48 + o3);
+            r.k3[pg] = *reinterpret_cast<const uint2*>(a.kcc + (rec + t) * 48 + 24 + o3);
+        } else {
+            r.k4[pg] = *reinterpret_cast<const uint2*>(a.kc4 + (rec + t) * 32 + 8 * g);
+            r.k3[pg] = *reinterpret_cast<const uint2*>(a.kc3 + (rec + t) * 24 + o3);
+        }
         const uint8_t* vb = ln.vb + (rec + 4 * g) * (size_t)ln.stride;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             r.v0[pg][j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride);
             r.v1[pg][j] = *reinterpret_cast<const uint32_t*>(vb + j * ln.stride + ln.d1);
         }
-        r.kn[pg] = *reinterpret_cast<const uint2*>(a.kn + rec + 4 * g);
-        r.vn[pg] = *reinterpret_cast<const uint2*>(a.vn + rec + 4 * g);
+        r.kn[pg] = *reinterpret_cast<const uint2*>((COOL ? a.kcn : a.kn) + rec + 4 * g);
+        r.vn[pg] = *reinterpret_cast<const uint2*>((COOL ? a.vcn : a.vn) + rec + 4 * g);
     }
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -305,6 +324,7 @@ __device__ inline void tq_dequant8(uint32_t w, int bits, const uint2* tbl, h8_t&
 // Fold one page pair into the wavefront's state (as pair_update: m and lsum
 // of head l%16, O in the C layout with rows = heads 4(l/16) + i, tile nt
 // column n = dimension 8n + nt).  na / nb: valid tokens of the two pages.
+template <bool COOL = false>
 __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h8_t (&qh)[4], const h8_t (&ql)[4],
                                       const uint2* cbk, float scale, int na, int nb, float& m, float& lsum,
                                       f4_t (&o)[8], int lane) {
@@ -314,12 +334,17 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
         const uint64_t w3 = ((uint64_t)r.k3[pg].y << 32 | r.k3[pg].x) >> sh3;
-        const uint32_t chunk[4] = {r.k4[pg].x, r.k4[pg].y, (uint32_t)w3 & 0xFFFFFFu, (uint32_t)(w3 >> 24) & 0xFFFFFFu};
+        uint32_t chunk[4] = {r.k4[pg].x, r.k4[pg].y, (uint32_t)w3 & 0xFFFFFFu, (uint32_t)(w3 >> 24) & 0xFFFFFFu};
+        if constexpr (COOL) {
+            const uint64_t wa = ((uint64_t)r.k4[pg].y << 32 | r.k4[pg].x) >> sh3;
+            chunk[0] = (uint32_t)wa & 0xFFFFFFu;
+            chunk[1] = (uint32_t)(wa >> 24) & 0xFFFFFFu;
+        }
         f4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             h8_t kh, kl;
-            tq_dequant8(chunk[s], s < 2 ? 4 : 3, cbk, kh, kl);
+            tq_dequant8(chunk[s], COOL || s >= 2 ? 3 : 4, cbk, kh, kl);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], acc, 0, 0, 0);
@@ -394,7 +419,7 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
 // than one), q rotated once per block (q~ = H D q in LDS); the last block
 // of the (sequence, kv head) merges the records and rotates the value sums
 // back (merge_last<G, 128, true>).
-template <int G, bool PIPE>
+template <int G, bool PIPE, bool COOL = false>
 __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b,
                                    int range = 0, int slot = -1, int nrec = 0, int ntq = 0) {
     constexpr int HD = 128, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
@@ -416,14 +441,14 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
     const int bt_lane = (lane < npw_max && pg0 + my_page < a.max_blocks)
-                            ? a.block_table[(size_t)b * a.max_blocks + pg0 + my_page]
+                            ? (COOL ? a.cool_table : a.block_table)[(size_t)b * a.max_blocks + pg0 + my_page]
                             : 0;
     const int npages = (ctx + kPage - 1) / kPage;
     const int p1 = min(p0 + pps, npages);
     const int npw = p1 > p0 + wave ? (p1 - p0 - wave + kAttnWaves - 1) / kAttnWaves : 0;
     auto valid_of = [&](int i) { return i < npw ? min(ctx - (p0 + wave + kAttnWaves * i) * kPage, kPage) : 0; };
     auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
-    const TqLane ln(a, t);
+    const TqLane ln(a, t, COOL);
 
     // q and the K signs (wavefront w: head min(w, G - 1), lane l: dimensions
     // l and l + 64), the codebook, then the first pair of pages: all in
@@ -439,7 +464,7 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     // wavefront's pages re-read its first page and are not processed
     auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
     auto load_p = [&](TqPair& r, int p) {
-        tq_load_pair(r, a, ln, blk_or0(2 * p), blk_or0(2 * p + 1), valid_of(2 * p + 1), kvh, lane);
+        tq_load_pair<COOL>(r, a, ln, blk_or0(2 * p), blk_or0(2 * p + 1), valid_of(2 * p + 1), kvh, lane);
     };
     TqPair r0, r1, r2;
     load_p(r0, 0);
@@ -485,7 +510,7 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
     auto upd = [&](const TqPair& r, int p) {
-        tq_pair_update(r, ln, qh, ql, cbk, scale, valid_of(2 * p), valid_of(2 * p + 1), m, lsum, o, lane);
+        tq_pair_update<COOL>(r, ln, qh, ql, cbk, scale, valid_of(2 * p), valid_of(2 * p + 1), m, lsum, o, lane);
     };
     if constexpr (PIPE) {
         // three register sets in rotation: pair p + 2 is requested before
@@ -547,9 +572,11 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsp
 
 // ----------------------------------------------------- TurboQuant encode --
 // One wavefront per vector; lane l holds coordinates l and l + 64.
-__device__ inline void tq_encode_vals(float x0, float x1, const float* __restrict__ sign,
-                                      uint8_t* __restrict__ c4, uint8_t* __restrict__ c3,
-                                      uint16_t* __restrict__ norm, uint8_t* lds_codes) {
+// Norm, rotation and codes (the oracle's arithmetic in its order): returns
+// n = |x|; q0, q1 = the codes of coordinates l and l + 64, the first from the
+// 16-level boundaries (Cool: the 8-level ones), the second from the 8-level.
+template <bool COOL>
+__device__ inline float tq_codes_lane(float x0, float x1, const float* __restrict__ sign, int& q0, int& q1) {
     const int lane = threadIdx.x & 63;
     const float a0 = x0 * x0;
     const float a1 = x1 * x1;
@@ -566,43 +593,81 @@ __device__ inline void tq_encode_vals(float x0, float x1, const float* __restric
         u0 = (sign[lane] * x0) * inv;
         u1 = (sign[lane + 64] * x1) * inv;
     }
-    // FWHT: stages h = 1 .. 32 across lanes, h = 64 inside the lane.
-    for (int h = 1; h < 64; h <<= 1) {
-        const float p0 = __shfl_xor(u0, h, 64);
-        const float p1 = __shfl_xor(u1, h, 64);
-        if (lane & h) {
-            u0 = p0 - u0;
-            u1 = p1 - u1;
-        } else {
-            u0 = u0 + p0;
-            u1 = u1 + p1;
-        }
-    }
-    {
-        const float t0 = u0 + u1, t1 = u0 - u1;
-        u0 = t0;
-        u1 = t1;
-    }
+    wave_fwht128(u0, u1);
     const float y0 = u0 * kTqScale, y1 = u1 * kTqScale;
-    int q0 = 0, q1 = 0;
+    q0 = 0;
+    q1 = 0;
+    if constexpr (COOL) {
 #pragma unroll
-    for (int j = 0; j < 15; ++j) q0 += (y0 < c_tq_b4[j]) ? 0 : 1;
+        for (int j = 0; j < 7; ++j) q0 += (y0 < c_tq_b3[j]) ? 0 : 1;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 15; ++j) q0 += (y0 < c_tq_b4[j]) ? 0 : 1;
+    }
 #pragma unroll
     for (int j = 0; j < 7; ++j) q1 += (y1 < c_tq_b3[j]) ? 0 : 1;
+    return n;
+}
+
+// Pack and store one vector's codes (a wavefront, through its own LDS row):
+// TurboQuant: 64 x 4 bits LSB-first at ca (32 B), 64 x 3 bits at cb (24 B);
+// Cool: 128 x 3 bits at ca (48 B).  Then the fp16 norm.
+template <bool COOL>
+__device__ inline void tq_store_codes(int q0, int q1, float n, uint8_t* __restrict__ ca, uint8_t* __restrict__ cb,
+                                      uint16_t* __restrict__ norm, uint8_t* lds_codes) {
+    const int lane = threadIdx.x & 63;
     lds_codes[lane] = (uint8_t)q0;
     lds_codes[lane + 64] = (uint8_t)q1;
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < 32) c4[lane] = (uint8_t)(lds_codes[2 * lane] | (lds_codes[2 * lane + 1] << 4));
-    if (lane < 24) {
-        const int g = lane / 3, r = lane % 3;
-        uint32_t bits = 0;
+    if constexpr (COOL) {
+        if (lane < 48) {
+            const int g = lane / 3, r = lane % 3;
+            uint32_t bits = 0;
 #pragma unroll
-        for (int m = 0; m < 8; ++m) bits |= (uint32_t)lds_codes[64 + 8 * g + m] << (3 * m);
-        c3[lane] = (uint8_t)(bits >> (8 * r));
+            for (int m = 0; m < 8; ++m) bits |= (uint32_t)lds_codes[8 * g + m] << (3 * m);
+            ca[lane] = (uint8_t)(bits >> (8 * r));
+        }
+    } else {
+        if (lane < 32) ca[lane] = (uint8_t)(lds_codes[2 * lane] | (lds_codes[2 * lane + 1] << 4));
+        if (lane < 24) {
+            const int g = lane / 3, r = lane % 3;
+            uint32_t bits = 0;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) bits |= (uint32_t)lds_codes[64 + 8 * g + m] << (3 * m);
+            cb[lane] = (uint8_t)(bits >> (8 * r));
+        }
     }
     if (lane == 0) *norm = f2h_bits(n);
+}
+
+__device__ inline void tq_encode_vals(float x0, float x1, const float* __restrict__ sign,
+                                      uint8_t* __restrict__ c4, uint8_t* __restrict__ c3,
+                                      uint16_t* __restrict__ norm, uint8_t* lds_codes) {
+    int q0, q1;
+    const float n = tq_codes_lane<false>(x0, x1, sign, q0, q1);
+    tq_store_codes<false>(q0, q1, n, c4, c3, norm, lds_codes);
+}
+
+// Codes of coordinates l and l + 64 of a stored TurboQuant vector.
+__device__ inline void tq_load_codes_lane(const uint8_t* c4, const uint8_t* c3, int& q0, int& q1) {
+    const int lane = threadIdx.x & 63;
+    q0 = (c4[lane >> 1] >> (4 * (lane & 1))) & 15;
+    const int bit = 3 * lane, byte = bit >> 3;
+    q1 = ((c3[byte] | (c3[min(byte + 1, 23)] << 8)) >> (bit & 7)) & 7;
+}
+
+// Decoded coordinates l and l + 64 of a TurboQuant vector from its codes:
+// u = codebook values, the FWHT, then ((u / sqrt(128)) * sign) * norm.
+__device__ inline void tq_values_lane(int q0, int q1, uint16_t norm, const float* __restrict__ sign, float& x0,
+                                      float& x1) {
+    const int lane = threadIdx.x & 63;
+    float u0 = c_tq_cb[q0], u1 = c_tq_cb[16 + q1];
+    wave_fwht128(u0, u1);
+    const float nrm = h2f_bits(norm);
+    x0 = ((u0 * kTqScale) * sign[lane]) * nrm;
+    x1 = ((u1 * kTqScale) * sign[lane + 64]) * nrm;
 }
 
 // One vector of 128 from memory: lane l takes entries l and l + 64.
@@ -625,15 +690,15 @@ __global__ __launch_bounds__(256) void k_tq_encode(const float* x, int nvec, con
                    norms + dst, codes[wave]);
 }
 
-// Context rows [ctx][hkv][128] of sequence b -> pages.
+// Context rows [p0, ctx) of x [ctx][hkv][128] of sequence b -> pages.
 __global__ __launch_bounds__(256) void k_tq_encode_ctx(const float* x, int ctx, int hkv,
                                                        const float* signs, uint8_t* c4,
                                                        uint8_t* c3, uint16_t* norms,
                                                        const int32_t* block_table, int max_blocks,
-                                                       int b) {
+                                                       int b, int p0) {
     __shared__ uint8_t codes[4][128];
     const int wave = threadIdx.x >> 6;
-    const int v = blockIdx.x * 4 + wave;
+    const int v = p0 * hkv + blockIdx.x * 4 + wave;
     if (v >= ctx * hkv) return;
     const int t = v / hkv, h = v % hkv;
     const int blk = block_table[(size_t)b * max_blocks + t / kPage];
@@ -699,16 +764,10 @@ __global__ __launch_bounds__(256) void k_tq_decode_pages(const uint8_t* kc4, con
     if (v >= npos * 2 * hkv) return;
     const int p = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv;
     const size_t blk = (size_t)bt[p / kPage], vec = (blk * hkv + h) * kPage + p % kPage;
-    const uint8_t* c4 = (kv ? vc4 : kc4) + vec * 32;
-    const uint8_t* c3 = (kv ? vc3 : kc3) + vec * 24;
-    const float* sign = kv ? vsign : ksign;
-    const int q4 = (c4[lane >> 1] >> (4 * (lane & 1))) & 15;
-    const int bit = 3 * lane, byte = bit >> 3;
-    const int q3 = ((c3[byte] | (c3[min(byte + 1, 23)] << 8)) >> (bit & 7)) & 7;
-    float u0 = c_tq_cb[q4], u1 = c_tq_cb[16 + q3];
-    wave_fwht128(u0, u1);
-    const float nrm = h2f_bits((kv ? vn : kn)[vec]);
-    const float x0 = ((u0 * kTqScale) * sign[lane]) * nrm, x1 = ((u1 * kTqScale) * sign[lane + 64]) * nrm;
+    int q0, q1;
+    tq_load_codes_lane((kv ? vc4 : kc4) + vec * 32, (kv ? vc3 : kc3) + vec * 24, q0, q1);
+    float x0, x1;
+    tq_values_lane(q0, q1, (kv ? vn : kn)[vec], kv ? vsign : ksign, x0, x1);
     const uint16_t o0 = f2h_bits(x0), o1 = f2h_bits(x1);
     const size_t page = (blk * hkv + h) * kPage * 128;
     const int slot = p % kPage;
@@ -861,6 +920,37 @@ __device__ inline void tq_compress_block(const AttnArgs& a, int kv, int part, in
     tq_encode_vals(x0, x1, sign, c4 + dst * 32, c3 + dst * 24, nr + dst, codes[w]);
 }
 
+// Three tiers, the page that leaves the Warm range at this step: when the
+// position p being written completes page q = (p - H - W + 1) / 16 - 1
+// outside the last H + W positions, its TurboQuant vectors (block_table[q])
+// are decoded to fp32 and encoded Cool into cool_table[q] -- the Warm ->
+// Cool step of compress_tier (kv/paged_attention.cpp:262-285), per page.
+// Block `part` of the four of each kind takes slots 4 part .. 4 part + 3,
+// one per wavefront.  The TurboQuant page is only read here, and the Warm
+// splits of the same launch still read page q in that form; the Hot -> Warm
+// compressor of the launch writes page q + W / 16, a different block of the
+// Warm ring.
+__device__ inline void cool_compress_block(const AttnArgs& a, int kv, int part, int h, int b) {
+    __shared__ uint8_t codes[kCompressWaves][128];
+    const int w = threadIdx.x >> 6;
+    const int done = a.pos[b] - a.hot_window - a.warm_window + 1;
+    if (w >= kCompressWaves || done < kPage || done % kPage) return;
+    const int q = done / kPage - 1;
+    const int slot = part * kCompressWaves + w;
+    const size_t src = ((size_t)a.block_table[(size_t)b * a.max_blocks + q] * a.hkv + h) * kPage + slot;
+    const size_t dst = ((size_t)a.cool_table[(size_t)b * a.max_blocks + q] * a.hkv + h) * kPage + slot;
+    const float* sign = kv ? a.vsign : a.ksign;
+    int q0, q1;
+    tq_load_codes_lane((kv ? a.vc4 : a.kc4) + src * 32, (kv ? a.vc3 : a.kc3) + src * 24, q0, q1);
+    float x0, x1;
+    tq_values_lane(q0, q1, (kv ? a.vn : a.kn)[src], sign, x0, x1);
+    // the Cool pools, written only here and by the context fill
+    uint8_t* cc = const_cast<uint8_t*>(kv ? a.vcc : a.kcc);
+    uint16_t* cn = const_cast<uint16_t*>(kv ? a.vcn : a.kcn);
+    const float n = tq_codes_lane<true>(x0, x1, sign, q0, q1);
+    tq_store_codes<true>(q0, q1, n, cc + dst * 48, nullptr, cn + dst, codes[w]);
+}
+
 // Tiered pages in one launch: blocks x < ntq are TurboQuant splits of the
 // compressed pages, the next nf fp16 splits of the window (the last of these
 // ntq + nf blocks of a (sequence, kv head) merges both kinds of record), and
@@ -875,6 +965,59 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tiered(AttnArgs a, int
     else
         tq_compress_block(a, (x - ntq - nf) / kCompressParts, (x - ntq - nf) % kCompressParts, blockIdx.y,
                           blockIdx.z);
+}
+
+// Split plan of three tiers: nc Cool splits of ppc pages, nw TurboQuant
+// splits of ppw pages, nf fp16 splits of ppf pages.
+struct TierPlan3 {
+    int nc, ppc, nw, ppw, nf, ppf;
+};
+
+// Three tiers in one launch: blocks x < nc are Cool splits, the next nw
+// TurboQuant splits, the next nf fp16 splits (the last of these nc + nw + nf
+// blocks of a (sequence, kv head) merges the three kinds of record, the
+// first nc + nw in the rotated domain); then 2 kCompressParts blocks
+// compress the page leaving the fp16 window (K, V) and 2 kCompressParts the
+// page leaving the Warm range.
+template <int G, bool PC, bool PW, bool PF>
+__global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tiered3(AttnArgs a, TierPlan3 p) {
+    const int x = blockIdx.x, nrot = p.nc + p.nw, nrec = nrot + p.nf;
+    if (x < p.nc) {
+        attn_tq_run<G, PC, true>(a, p.nc, p.ppc, x, blockIdx.y, blockIdx.z, 3, x, nrec, nrot);
+    } else if (x < nrot) {
+        attn_tq_run<G, PW>(a, p.nw, p.ppw, x - p.nc, blockIdx.y, blockIdx.z, 1, x, nrec, nrot);
+    } else if (x < nrec) {
+        attn_f16_run<G, 128, PF, true>(a, p.nf, x - nrot, blockIdx.y, blockIdx.z, 2, x, nrec, nrot);
+    } else {
+        const int c = x - nrec;
+        if (c < 2 * kCompressParts)
+            tq_compress_block(a, c / kCompressParts, c % kCompressParts, blockIdx.y, blockIdx.z);
+        else
+            cool_compress_block(a, (c - 2 * kCompressParts) / kCompressParts, c % kCompressParts, blockIdx.y,
+                                blockIdx.z);
+    }
+}
+
+// Context fill of Cool pages: positions [0, n) of x [ctx][hkv][128] (fp32,
+// the fp16 values) of sequence b, one wavefront per vector, encoded
+// TurboQuant, decoded, and encoded Cool (what the per-page compressors give
+// a position that passed through both steps) into cool_table's pages.
+__global__ __launch_bounds__(256) void k_cool_encode_ctx(const float* x, int n, int hkv, const float* signs,
+                                                         uint8_t* cc, uint16_t* cn, const int32_t* cool_table,
+                                                         int max_blocks, int b) {
+    __shared__ uint8_t codes[4][128];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int v = blockIdx.x * 4 + wave;
+    if (v >= n * hkv) return;
+    const int t = v / hkv, h = v % hkv;
+    const size_t dst = ((size_t)cool_table[(size_t)b * max_blocks + t / kPage] * hkv + h) * kPage + t % kPage;
+    const float* src = x + (size_t)v * 128;
+    int q0, q1;
+    const float nw = tq_codes_lane<false>(src[lane], src[lane + 64], signs, q0, q1);
+    float x0, x1;
+    tq_values_lane(q0, q1, f2h_bits(nw), signs, x0, x1);
+    const float nc = tq_codes_lane<true>(x0, x1, signs, q0, q1);
+    tq_store_codes<true>(q0, q1, nc, cc + dst * 48, nullptr, cn + dst, codes[wave]);
 }
 
 // Context fill of tiered pages: positions [cold, ctx) of raw [ctx][hkv][hd]
@@ -1095,8 +1238,56 @@ size_t attn_tiered_workspace_bytes(int batch, int hq, int hkv) {
     return sizeof(float) * (size_t)batch * hkv * kMaxSplits * rec_floats(hq / hkv, 128);
 }
 
+// Three tiers: the Cool pages (at most (max_ctx - H - W) / 16 + 1), the Warm
+// range (W / 16 + 1 pages) and the window (H / 16 + 2 pages) share about one
+// block per CU over all (kv head, sequence) pairs in proportion to their
+// cost (a TurboQuant or Cool page taking about 0.8 of an fp16 page's time).
+TierPlan3 plan_tiered3(int max_ctx, int hot_window, int warm_window, int hkv, int batch) {
+    const int pc = max(1, (max_ctx - hot_window - warm_window) / kPage + 1);
+    const int pw = warm_window / kPage + 1, pf = hot_window / kPage + 2;
+    const int S = min(max(3, (device_cus() + hkv * batch - 1) / (hkv * batch)), kMaxSplits);
+    const double cc = 0.8 * pc, cw = 0.8 * pw, cf = pf, tot = cc + cw + cf;
+    auto part = [&](int pages, double cost, int avail, int& n, int& pp) {
+        const int n0 = min(max(1, (int)(S * cost / tot + 0.5)), max(avail, 1));
+        pp = min(max((pages + n0 - 1) / n0, 1), kPagesPerSplitMax);
+        n = (pages + pp - 1) / pp;
+    };
+    TierPlan3 p;
+    part(pc, cc, S - 2, p.nc, p.ppc);
+    part(pw, cw, S - p.nc - 1, p.nw, p.ppw);
+    part(pf, cf, S - p.nc - p.nw, p.nf, p.ppf);
+    return p;
+}
+
+hipError_t attn_tiered3_launch(const AttnArgs& a, hipStream_t st) {
+    if (!a.cool_table || !a.kcc || !a.vcc || !a.kcn || !a.vcn || a.warm_window % kPage) return hipErrorInvalidValue;
+    const TierPlan3 p = plan_tiered3(a.max_ctx, a.hot_window, a.warm_window, a.hkv, a.batch);
+    if (p.nc + p.nw + p.nf > kMaxSplits) return hipErrorInvalidValue;
+    const dim3 grid(p.nc + p.nw + p.nf + 4 * kCompressParts, a.hkv, a.batch);
+    const int G = a.hq / a.hkv;
+    const bool pc = p.ppc > kPagesPerSplitMin, pw = p.ppw > kPagesPerSplitMin, pf = p.ppf > kPagesPerSplitMin;
+#define NX_TIER3_CASE(GG, PC, PW, PF)                                                                     \
+    if (G == GG && pc == PC && pw == PW && pf == PF) {                                                    \
+        hipLaunchKernelGGL((k_attn_tiered3<GG, PC, PW, PF>), grid, dim3(kAttnThreads), 0, st, a, p);      \
+        return hipGetLastError();                                                                         \
+    }
+#define NX_TIER3_PW(GG, PC, PW) NX_TIER3_CASE(GG, PC, PW, true) NX_TIER3_CASE(GG, PC, PW, false)
+#define NX_TIER3_PC(GG, PC) NX_TIER3_PW(GG, PC, true) NX_TIER3_PW(GG, PC, false)
+#define NX_TIER3_G(GG) NX_TIER3_PC(GG, true) NX_TIER3_PC(GG, false)
+    NX_TIER3_G(1)
+    NX_TIER3_G(2)
+    NX_TIER3_G(4)
+    NX_TIER3_G(8)
+#undef NX_TIER3_G
+#undef NX_TIER3_PC
+#undef NX_TIER3_PW
+#undef NX_TIER3_CASE
+    return hipErrorInvalidValue;
+}
+
 hipError_t attn_tiered_launch(const AttnArgs& a, hipStream_t st) {
     if (!a.counts || !a.part || a.hd != 128 || a.hot_window < kPage) return hipErrorInvalidValue;
+    if (a.warm_window > 0) return attn_tiered3_launch(a, st);
     const TierPlan p = plan_tiered(a.max_ctx, a.hot_window, a.hkv, a.batch);
     if (p.ntq + p.nf > kMaxSplits) return hipErrorInvalidValue;
     const dim3 grid(p.ntq + p.nf + 2 * kCompressParts, a.hkv, a.batch);
@@ -1145,13 +1336,22 @@ hipError_t tq_encode_launch(const float* x, int nvec, const float* signs, const 
 hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* signs,
                                 const float* b4, const float* b3, uint8_t* c4, uint8_t* c3,
                                 uint16_t* norms, const int32_t* block_table, int max_blocks, int b,
-                                hipStream_t st) {
+                                hipStream_t st, int p0) {
     (void)b4;
     (void)b3;
-    const int nvec = ctx * hkv;
+    const int nvec = (ctx - p0) * hkv;
     if (nvec <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_tq_encode_ctx, dim3((nvec + 3) / 4), dim3(256), 0, st, x, ctx, hkv, signs,
-                       c4, c3, norms, block_table, max_blocks, b);
+                       c4, c3, norms, block_table, max_blocks, b, p0);
+    return hipGetLastError();
+}
+
+hipError_t cool_encode_ctx_launch(const float* x, int n, int hkv, const float* signs, uint8_t* cc, uint16_t* cn,
+                                  const int32_t* cool_table, int max_blocks, int b, hipStream_t st) {
+    const int nvec = n * hkv;
+    if (nvec <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_cool_encode_ctx, dim3((nvec + 3) / 4), dim3(256), 0, st, x, n, hkv, signs, cc, cn,
+                       cool_table, max_blocks, b);
     return hipGetLastError();
 }
 

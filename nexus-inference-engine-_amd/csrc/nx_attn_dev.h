@@ -35,19 +35,25 @@ __device__ inline void st_coh_u16(uint16_t* p, uint16_t v) {
 }
 
 // The part of sequence b's context a block covers: all of it (range 0), or
-// with tiered pages the compressed pages [0, cold) (range 1) or the fp16
-// window [cold, ctx) (range 2, read from page cold / 16 of the hot table
-// on), cold = 16 floor((ctx - 1 - hot_window) / 16), at least 0: the pages
-// compressed before this step (the page that leaves the window at this step
-// is compressed by the same launch and read here as fp16).
+// with tiered pages the TurboQuant pages [cool, cold) (range 1, from page
+// cool / 16 on), the fp16 window [cold, ctx) (range 2, read from page cold /
+// 16 of the hot table on) or the Cool pages [0, cool) (range 3).  cold = 16
+// floor((ctx - 1 - hot_window) / 16), at least 0: the pages compressed
+// before this step (the page that leaves the window at this step is
+// compressed by the same launch and read here as fp16); cool likewise with
+// hot_window + warm_window, 0 without a Cool tier (warm_window 0).
 __device__ inline void attn_range(const AttnArgs& a, int b, int range, int& ctx, int& pg0) {
     ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     pg0 = 0;
     if (range != 0) {
         const int cold = kPage * max(0, (ctx - 1 - a.hot_window) / kPage);
-        if (range == 1) {
-            ctx = cold;
-        } else {
+        const int cool = a.warm_window > 0 ? kPage * max(0, (ctx - 1 - a.hot_window - a.warm_window) / kPage) : 0;
+        if (range == 1) {  // Warm: [cool, cold)
+            pg0 = cool / kPage;
+            ctx = cold - cool;
+        } else if (range == 3) {  // Cool: [0, cool)
+            ctx = cool;
+        } else {  // fp16: [cold, ctx)
             pg0 = cold / kPage;
             ctx -= cold;
         }

@@ -123,6 +123,16 @@ struct AttnArgs {
     // compresses the page that leaves the window at this step
     int hot_window;
     const int32_t* hot_table;
+    // three tiers (warm_window > 0): positions [0, cool) are read from the
+    // Cool pages through cool_table (3-bit codes on all 128 coordinates,
+    // [blocks][hkv][16][48], fp16 norms [blocks][hkv][16]), [cool, cold) from
+    // the TurboQuant (Warm) pages through block_table; cool = 16 floor((ctx -
+    // 1 - hot_window - warm_window) / 16) clamped at 0.  The same launch
+    // re-encodes the page that leaves the Warm range into the Cool pages.
+    int warm_window;
+    const int32_t* cool_table;
+    const uint8_t *kcc, *vcc;
+    const uint16_t *kcn, *vcn;
     // > 0 (fp16 pages, standalone): the kernel itself checks each sequence's
     // context length against max_blocks * 16 and the block-table entries of
     // its pages against [0, check_blocks); an entry outside reads block 0
@@ -155,7 +165,8 @@ hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st);
 // out16 [P][hq][hd]; row t attends to positions <= p0 + t.  No workspace.
 hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st);
 // Attention over tiered pages in one launch, which also compresses the page
-// leaving the window (max_ctx bounds ctx_lens).
+// leaving the window (max_ctx bounds ctx_lens) and, with three tiers
+// (warm_window > 0), re-encodes Cool the page leaving the Warm range.
 hipError_t attn_tiered_launch(const AttnArgs& a, hipStream_t st);
 size_t attn_tiered_workspace_bytes(int batch, int hq, int hkv);
 // Tiered pages: fill the window's pages from raw fp32 [ctx][hkv][hd]; round
@@ -208,7 +219,12 @@ hipError_t tq_encode_launch(const float* x, int nvec, const float* signs, const 
 hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* signs,
                                 const float* b4, const float* b3, uint8_t* c4, uint8_t* c3,
                                 uint16_t* norms, const int32_t* block_table, int max_blocks,
-                                int b, hipStream_t st);
+                                int b, hipStream_t st, int p0 = 0);
+// Context fill of Cool pages: positions [0, n) of x [.][hkv][128] of
+// sequence b encoded TurboQuant, decoded and encoded Cool (48-byte codes,
+// fp16 norms) into the pages of cool_table.
+hipError_t cool_encode_ctx_launch(const float* x, int n, int hkv, const float* signs, uint8_t* cc, uint16_t* cn,
+                                  const int32_t* cool_table, int max_blocks, int b, hipStream_t st);
 // Append one token per sequence from kv_tmp [batch][2][hkv*128].
 // Encode the K and V rows [n][2][hkv*128] of positions p0 .. p0 + n - 1 of
 // one sequence (block table bt of that sequence) into its pages.

@@ -38,6 +38,8 @@ struct Layer {
     uint16_t *kpool = nullptr, *vpool = nullptr;
     uint8_t *kc4 = nullptr, *kc3 = nullptr, *vc4 = nullptr, *vc3 = nullptr;
     uint16_t *kn = nullptr, *vn = nullptr;
+    uint8_t *kcc = nullptr, *vcc = nullptr;    // Cool pages [blocks][hkv][16][48] (three tiers)
+    uint16_t *kcn = nullptr, *vcn = nullptr;
     float *ksign = nullptr, *vsign = nullptr;
     int32_t* moe_count = nullptr;  // [E]
     float* norm_attn = nullptr;    // RMSNorm weights [d]; nullptr = 1.0
@@ -87,6 +89,12 @@ struct nx_model {
     // stride as block_table)
     int hot_pages = 0;
     int32_t* hot_bt = nullptr;
+    // three tiers (warm_window > 0): block_table is the TurboQuant (Warm)
+    // range's ring of warm_pages pages per sequence (block_table[b][p] = b *
+    // warm_pages + p % warm_pages), cool_bt the Cool pages (a seeded
+    // permutation of the pool, max_blocks per sequence)
+    int warm_pages = 0;
+    int32_t* cool_bt = nullptr;
     unsigned* attn_counts = nullptr;  // split-completion counters of the fp16 attention
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
@@ -306,25 +314,39 @@ hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
     if (c.kv_kind == 1) return nx::attn_tq_launch(at, st);
     at.hot_window = c.hot_window;
     at.hot_table = m->hot_bt;
+    at.warm_window = c.warm_window;
+    at.cool_table = m->cool_bt;
+    at.kcc = ly.kcc;
+    at.vcc = ly.vcc;
+    at.kcn = ly.kcn;
+    at.vcn = ly.vcn;
     return nx::attn_tiered_launch(at, st);
 }
 
+// Tier boundaries of a sequence whose next attention covers ctx positions:
+// [0, cool) Cool, [cool, cold) TurboQuant, [cold, ctx) fp16.
+void tier_bounds(const nx_model_config& c, int ctx, int& cool, int& cold) {
+    if (c.kv_kind != 2) {
+        cool = 0;
+        cold = c.kv_kind == 1 ? ctx : 0;
+        return;
+    }
+    cold = nx::kPage * std::max(0, (ctx - 1 - c.hot_window) / nx::kPage);
+    cool = c.warm_window > 0 ? nx::kPage * std::max(0, (ctx - 1 - c.hot_window - c.warm_window) / nx::kPage) : 0;
+}
+
 // KV bytes one attention pass reads for sequences at hpos (TurboQuant: 58
-// bytes per vector; tiered: TurboQuant before the window, fp16 in it).
+// bytes per vector, Cool 50; tiered: Cool, then TurboQuant before the
+// window, fp16 in it).
 double kv_bytes(const nx_model* m) {
     const nx_model_config& c = m->c;
-    const double f16 = 2.0 * c.n_kv_heads * c.head_dim * 2, tq = 2.0 * c.n_kv_heads * 58;
+    const double f16 = 2.0 * c.n_kv_heads * c.head_dim * 2, tq = 2.0 * c.n_kv_heads * 58, cl = 2.0 * c.n_kv_heads * 50;
     double kv = 0.0;
     for (int b = 0; b < c.batch; ++b) {
         const int ctx = m->hpos[b] + 1;
-        if (c.kv_kind == 0) {
-            kv += ctx * f16;
-        } else if (c.kv_kind == 1) {
-            kv += ctx * tq;
-        } else {
-            const int cold = nx::kPage * std::max(0, (ctx - 1 - c.hot_window) / nx::kPage);  // attention's boundary
-            kv += cold * tq + (ctx - cold) * f16;
-        }
+        int cool = 0, cold = 0;
+        tier_bounds(c, ctx, cool, cold);  // the attention's boundaries
+        kv += cool * cl + (cold - cool) * tq + (ctx - cold) * f16;
     }
     return kv;
 }
@@ -579,6 +601,7 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     m->max_blocks = c.max_seq / nx::kPage;
     m->n_blocks = m->max_blocks * B;
     m->hot_pages = c.kv_kind == 2 ? c.hot_window / nx::kPage + 1 : 0;
+    m->warm_pages = c.kv_kind == 2 && c.warm_window > 0 ? c.warm_window / nx::kPage + 1 : 0;
     m->out_stride = c.max_seq;
     m->layers.resize(L);
     m->hpos.assign(B, -1);
@@ -620,12 +643,21 @@ nx_status create_impl(nx_model* m, bool synthetic) {
             NX_TRY(dalloc(m, &ly.vpool, hot_elems));
         }
         if (c.kv_kind != 0) {
-            NX_TRY(dalloc(m, &ly.kc4, pool_vecs * 32));
-            NX_TRY(dalloc(m, &ly.kc3, pool_vecs * 24));
-            NX_TRY(dalloc(m, &ly.vc4, pool_vecs * 32));
-            NX_TRY(dalloc(m, &ly.vc3, pool_vecs * 24));
-            NX_TRY(dalloc(m, &ly.kn, pool_vecs));
-            NX_TRY(dalloc(m, &ly.vn, pool_vecs));
+            // three tiers: the TurboQuant pool holds only the Warm ring
+            const size_t tq_vecs =
+                m->warm_pages > 0 ? (size_t)B * m->warm_pages * c.n_kv_heads * nx::kPage : pool_vecs;
+            NX_TRY(dalloc(m, &ly.kc4, tq_vecs * 32));
+            NX_TRY(dalloc(m, &ly.kc3, tq_vecs * 24));
+            NX_TRY(dalloc(m, &ly.vc4, tq_vecs * 32));
+            NX_TRY(dalloc(m, &ly.vc3, tq_vecs * 24));
+            NX_TRY(dalloc(m, &ly.kn, tq_vecs));
+            NX_TRY(dalloc(m, &ly.vn, tq_vecs));
+        }
+        if (m->warm_pages > 0) {
+            NX_TRY(dalloc(m, &ly.kcc, pool_vecs * 48));
+            NX_TRY(dalloc(m, &ly.vcc, pool_vecs * 48));
+            NX_TRY(dalloc(m, &ly.kcn, pool_vecs));
+            NX_TRY(dalloc(m, &ly.vcn, pool_vecs));
         }
         NX_TRY(dalloc(m, &ly.ksign, 128));
         NX_TRY(dalloc(m, &ly.vsign, 128));
@@ -656,9 +688,18 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     }
     // block table: a seeded permutation of the pool, max_blocks per sequence
+    // (three tiers: the Cool table; the block table is the Warm ring)
     {
         std::vector<int32_t> perm;
         host_shuffle(perm, m->n_blocks, c.seed, nx::kTidShuffle);
+        if (m->warm_pages > 0) {
+            NX_TRY(dalloc(m, &m->cool_bt, perm.size()));
+            NX_HIP(m->ctx, hipMemcpyAsync(m->cool_bt, perm.data(), perm.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
+            NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+            for (int b = 0; b < B; ++b)
+                for (int p = 0; p < m->max_blocks; ++p)
+                    perm[(size_t)b * m->max_blocks + p] = b * m->warm_pages + p % m->warm_pages;
+        }
         NX_TRY(dalloc(m, &m->block_table, perm.size()));
         NX_HIP(m->ctx, hipMemcpyAsync(m->block_table, perm.data(), perm.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
         NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
@@ -739,6 +780,8 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.kv_kind != 0 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
     if (c.kv_kind == 2 && (c.hot_window < nx::kPage || c.hot_window % nx::kPage || c.hot_window >= c.max_seq))
         return fail(ctx, NX_ERR_INVALID, "hot_window must be a positive multiple of 16 below max_seq");
+    if (c.warm_window < 0 || c.warm_window % nx::kPage || (c.warm_window > 0 && c.kv_kind != 2))
+        return fail(ctx, NX_ERR_INVALID, "warm_window must be 0 or (tiered pages) a positive multiple of 16");
     if (c.kv_kind == 2 && c.max_seq > nx::attn_max_ctx() / 2)
         return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the tiered attention limit");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
@@ -1117,7 +1160,8 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
     NX_TRY(dalloc(m, &och, (size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1)));
     float* raw = nullptr;
     if (c.kv_kind != 0) NX_TRY(dalloc(m, &raw, (size_t)ctx_len * hkv * hd));
-    const int cold = c.kv_kind == 2 ? nx::kPage * std::max(0, (ctx_len - c.hot_window) / nx::kPage) : ctx_len;
+    int cool = 0, cold = 0;
+    tier_bounds(c, ctx_len + 1, cool, cold);  // the boundaries of the first decode step
     std::vector<int32_t> ho((size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
@@ -1133,16 +1177,22 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
                                                 c.seed, k1, och, n_outlier, st));
         } else {
             // tiered: the values rounded to fp16 (what the window holds), the
-            // pages before cold encoded, the rest into the window's ring
+            // pages before cool encoded Cool, those in [cool, cold) encoded,
+            // the rest into the window's ring
             for (int b = 0; b < B; ++b)
                 for (int kv = 0; kv < 2; ++kv) {
                     NX_LAUNCH(m, nx::gen_ctx_raw_launch(raw, ctx_len, hkv, hd, L, b, kv, c.seed, k1,
                                                         och + (size_t)kv * hkv * n_outlier, n_outlier, st));
                     if (c.kv_kind == 2) NX_LAUNCH(m, nx::round_f16_launch(raw, (size_t)ctx_len * hkv * hd, st));
-                    if (cold > 0)
+                    if (cool > 0)
+                        NX_LAUNCH(m, nx::cool_encode_ctx_launch(raw, cool, hkv, kv ? ly.vsign : ly.ksign,
+                                                                kv ? ly.vcc : ly.kcc, kv ? ly.vcn : ly.kcn, m->cool_bt,
+                                                                m->max_blocks, b, st));
+                    if (cold > cool)
                         NX_LAUNCH(m, nx::tq_encode_ctx_launch(raw, cold, hkv, kv ? ly.vsign : ly.ksign, nullptr, nullptr,
                                                               kv ? ly.vc4 : ly.kc4, kv ? ly.vc3 : ly.kc3,
-                                                              kv ? ly.vn : ly.kn, m->block_table, m->max_blocks, b, st));
+                                                              kv ? ly.vn : ly.kn, m->block_table, m->max_blocks, b, st,
+                                                              cool));
                     if (c.kv_kind == 2)
                         NX_LAUNCH(m, nx::put_hot_launch(raw, ctx_len, cold, hkv, hd, b, m->hot_bt, m->max_blocks,
                                                         ly.kpool, ly.vpool, kv, st));
@@ -1182,22 +1232,25 @@ nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* 
         pos > m->hpos[(size_t)b])
         return fail(m->ctx, NX_ERR_INVALID, "nx_model_kv_read: no such position");
     const int hkv = c.n_kv_heads, hd = c.head_dim, page = pos / nx::kPage, slot = pos % nx::kPage;
-    const int ctx_len = m->hpos[(size_t)b] + 1;
-    const int cold = c.kv_kind == 0   ? 0
-                     : c.kv_kind == 1 ? ctx_len
-                                      : nx::kPage * std::max(0, (ctx_len - c.hot_window) / nx::kPage);
-    *form = pos < cold ? 1 : 0;
-    const size_t need = *form ? (size_t)58 * hkv : (size_t)2 * hkv * hd;
+    int cool = 0, cold = 0;
+    tier_bounds(c, m->hpos[(size_t)b] + 2, cool, cold);  // the boundaries of the next decode step
+    *form = pos < cool ? 2 : pos < cold ? 1 : 0;
+    const size_t need = *form == 2 ? (size_t)50 * hkv : *form ? (size_t)58 * hkv : (size_t)2 * hkv * hd;
     if (cap < need) return fail(m->ctx, NX_ERR_INVALID, "nx_model_kv_read: %zu bytes needed", need);
     const Layer& ly = m->layers[layer];
     hipStream_t st = m->ctx->stream;
     uint8_t* dst = static_cast<uint8_t*>(out);
     int32_t blk = 0;
-    const int32_t* bt = *form || c.kv_kind == 0 ? m->block_table : m->hot_bt;
+    const int32_t* bt = *form == 2 ? m->cool_bt : *form || c.kv_kind == 0 ? m->block_table : m->hot_bt;
     NX_HIP(m->ctx, hipMemcpyAsync(&blk, bt + (size_t)b * m->max_blocks + page, 4, hipMemcpyDeviceToHost, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
     for (int h = 0; h < hkv; ++h) {
-        if (*form) {
+        if (*form == 2) {
+            const size_t vi = ((size_t)blk * hkv + h) * nx::kPage + slot;
+            uint8_t* o = dst + (size_t)50 * h;
+            NX_HIP(m->ctx, hipMemcpyAsync(o, (kv ? ly.vcc : ly.kcc) + vi * 48, 48, hipMemcpyDeviceToHost, st));
+            NX_HIP(m->ctx, hipMemcpyAsync(o + 48, (kv ? ly.vcn : ly.kcn) + vi, 2, hipMemcpyDeviceToHost, st));
+        } else if (*form) {
             const size_t vi = ((size_t)blk * hkv + h) * nx::kPage + slot;
             uint8_t* o = dst + (size_t)58 * h;
             NX_HIP(m->ctx, hipMemcpyAsync(o, (kv ? ly.vc4 : ly.kc4) + vi * 32, 32, hipMemcpyDeviceToHost, st));

@@ -32,6 +32,7 @@ class Cfg(C.Structure):
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
+        ("warm_window", C.c_int),
     ]
 
 
@@ -97,6 +98,16 @@ def _load() -> C.CDLL:
                                      _u8p, _u8p, _u16p, _u8p, _u8p, _u16p, _i32p, C.c_int, C.c_int,
                                      C.c_int]),
         "nxo_tiered_cold": (C.c_int, [C.c_int, C.c_int]),
+        "nxo_tiered_cool": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+        "nxo_cool_encode": (None, [_f32p, C.c_int, _f32p, _f32p, _u8p, _u16p]),
+        "nxo_cool_decode": (None, [_u8p, _u16p, C.c_int, _f32p, _f32p, _f32p]),
+        "nxo_tq_to_cool": (None, [_u8p, _u8p, _u16p, C.c_int, _f32p, _f32p, _f32p, _f32p, _u8p, _u16p]),
+        "nxo_tiered_append_cool": (None, [C.c_int, _f32p, _f32p, _f32p, _f32p, _f32p, _u8p, _u8p, _u16p, _u8p,
+                                          _u8p, _u16p, _u8p, _u16p, _u8p, _u16p, _i32p, C.c_int, C.c_int,
+                                          C.c_int]),
+        "nxo_attn_decode_tiered_cool": (None, [_f32p, _u16p, _u16p, _u8p, _u8p, _u16p, _u8p, _u8p, _u16p, _u8p,
+                                               _u16p, _u8p, _u16p, _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int,
+                                               _i32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p]),
         "nxo_attn_decode_tiered": (None, [_f32p, _u16p, _u16p, _u8p, _u8p, _u16p, _u8p, _u8p, _u16p,
                                           _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int, _i32p, C.c_int,
                                           C.c_int, C.c_int, C.c_int, _f32p]),
@@ -239,6 +250,38 @@ def tq_decode(k4, k3, nr, signs) -> np.ndarray:
     return out
 
 
+def cool_encode(x: np.ndarray, signs: np.ndarray):
+    """[n][128] fp32 -> Cool form (codes [n][48], norms u16 [n])."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, 128)
+    n = x.shape[0]
+    _, b3 = codebook(3)
+    cc = np.empty((n, 48), np.uint8)
+    nr = np.empty(n, np.uint16)
+    lib.nxo_cool_encode(x, n, np.ascontiguousarray(signs, np.float32), b3, cc, nr)
+    return cc, nr
+
+
+def cool_decode(cc, nr, signs) -> np.ndarray:
+    n = cc.shape[0]
+    c3, _ = codebook(3)
+    out = np.empty((n, 128), np.float32)
+    lib.nxo_cool_decode(np.ascontiguousarray(cc), np.ascontiguousarray(nr), n,
+                        np.ascontiguousarray(signs, np.float32), c3, out)
+    return out
+
+
+def tq_to_cool(k4, k3, nr, signs):
+    """TurboQuant (Warm) vectors -> Cool form (codes [n][48], norms u16 [n])."""
+    n = k4.shape[0]
+    c4, _ = codebook(4)
+    c3, b3 = codebook(3)
+    cc = np.empty((n, 48), np.uint8)
+    cn = np.empty(n, np.uint16)
+    lib.nxo_tq_to_cool(np.ascontiguousarray(k4), np.ascontiguousarray(k3), np.ascontiguousarray(nr), n,
+                       np.ascontiguousarray(signs, np.float32), c4, c3, b3, cc, cn)
+    return cc, cn
+
+
 def f16_to_f32(bits: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(bits, np.uint16).view(np.float16).astype(np.float32)
 
@@ -283,7 +326,7 @@ class Model:
 
     def kv_read(self, layer: int, b: int, pos: int, kv: int, form: int) -> np.ndarray:
         """Stored bytes of one position, all kv heads (nxo_model_kv_read)."""
-        out = np.zeros(max(58, 2 * self.cfg.head_dim) * self.cfg.n_kv_heads, np.uint8)
+        out = np.zeros(max(58, 2 * self.cfg.head_dim) * self.cfg.n_kv_heads, np.uint8)  # every form fits
         n = lib.nxo_model_kv_read(self.h, layer, b, pos, kv, form, out)
         assert n > 0, "the oracle model does not hold that form"
         return out[:n]

@@ -473,25 +473,35 @@ void nxo_fwht128(float* u) {
 
 static const float kTqScale = 0.08838834764831845f; /* float(1/sqrt(128)) */
 
+/* y = H D (x / n) / sqrt(128) of one vector; returns n (y = 0 when n <= 1e-12). */
+static float tq_rotate(const float* xv, const float* signs, float* y) {
+    const float nrm = sqrtf(nxo_tq_sumsq(xv));
+    if (nrm > 1e-12f) {
+        const float inv = 1.0f / nrm;
+        for (int i = 0; i < NXO_TQ_D; ++i) y[i] = (signs[i] * xv[i]) * inv;
+    } else {
+        for (int i = 0; i < NXO_TQ_D; ++i) y[i] = 0.0f;
+    }
+    nxo_fwht128(y);
+    for (int i = 0; i < NXO_TQ_D; ++i) y[i] = y[i] * kTqScale;
+    return nrm;
+}
+
+/* o = ((H u / sqrt(128)) * D) * n: the inverse rotation of codebook values u (overwritten). */
+static void tq_unrotate(float* u, uint16_t norm, const float* signs, float* o) {
+    nxo_fwht128(u);
+    const float nrm = nxo_f16_to_f32(norm);
+    for (int i = 0; i < NXO_TQ_D; ++i) o[i] = ((u[i] * kTqScale) * signs[i]) * nrm;
+}
+
 void nxo_tq_encode(const float* x, int n, const float* signs, const float* b4, const float* b3,
                    uint8_t* codes4, uint8_t* codes3, uint16_t* norms, uint8_t* codes_unpacked) {
     for (int v = 0; v < n; ++v) {
-        const float* xv = x + (size_t)v * NXO_TQ_D;
-        const float nrm = sqrtf(nxo_tq_sumsq(xv));
-        norms[v] = nxo_f32_to_f16(nrm);
-        float u[NXO_TQ_D];
-        if (nrm > 1e-12f) {
-            const float inv = 1.0f / nrm;
-            for (int i = 0; i < NXO_TQ_D; ++i) u[i] = (signs[i] * xv[i]) * inv;
-        } else {
-            for (int i = 0; i < NXO_TQ_D; ++i) u[i] = 0.0f;
-        }
-        nxo_fwht128(u);
+        float y[NXO_TQ_D];
+        norms[v] = nxo_f32_to_f16(tq_rotate(x + (size_t)v * NXO_TQ_D, signs, y));
         uint8_t c[NXO_TQ_D];
-        for (int i = 0; i < NXO_TQ_D; ++i) {
-            const float y = u[i] * kTqScale;
-            c[i] = (i < 64) ? nxo_tq_encode_scalar(y, b4, 16) : nxo_tq_encode_scalar(y, b3, 8);
-        }
+        for (int i = 0; i < NXO_TQ_D; ++i)
+            c[i] = (i < 64) ? nxo_tq_encode_scalar(y[i], b4, 16) : nxo_tq_encode_scalar(y[i], b3, 8);
         nxo_pack_codes(codes4 + (size_t)v * 32, c, 64, 4);
         nxo_pack_codes(codes3 + (size_t)v * 24, c + 64, 64, 3);
         if (codes_unpacked) memcpy(codes_unpacked + (size_t)v * NXO_TQ_D, c, NXO_TQ_D);
@@ -506,10 +516,38 @@ void nxo_tq_decode(const uint8_t* codes4, const uint8_t* codes3, const uint16_t*
         nxo_unpack_codes(c + 64, codes3 + (size_t)v * 24, 64, 3);
         float u[NXO_TQ_D];
         for (int i = 0; i < NXO_TQ_D; ++i) u[i] = (i < 64) ? c4[c[i]] : c3[c[i]];
-        nxo_fwht128(u);
-        const float nrm = nxo_f16_to_f32(norms[v]);
-        float* o = out + (size_t)v * NXO_TQ_D;
-        for (int i = 0; i < NXO_TQ_D; ++i) o[i] = ((u[i] * kTqScale) * signs[i]) * nrm;
+        tq_unrotate(u, norms[v], signs, out + (size_t)v * NXO_TQ_D);
+    }
+}
+
+void nxo_cool_encode(const float* x, int n, const float* signs, const float* b3, uint8_t* codes,
+                     uint16_t* norms) {
+    for (int v = 0; v < n; ++v) {
+        float y[NXO_TQ_D];
+        norms[v] = nxo_f32_to_f16(tq_rotate(x + (size_t)v * NXO_TQ_D, signs, y));
+        uint8_t c[NXO_TQ_D];
+        for (int i = 0; i < NXO_TQ_D; ++i) c[i] = nxo_tq_encode_scalar(y[i], b3, 8);
+        nxo_pack_codes(codes + (size_t)v * NXO_COOL_CODES, c, NXO_TQ_D, 3);
+    }
+}
+
+void nxo_cool_decode(const uint8_t* codes, const uint16_t* norms, int n, const float* signs, const float* c3,
+                     float* out) {
+    for (int v = 0; v < n; ++v) {
+        uint8_t c[NXO_TQ_D];
+        nxo_unpack_codes(c, codes + (size_t)v * NXO_COOL_CODES, NXO_TQ_D, 3);
+        float u[NXO_TQ_D];
+        for (int i = 0; i < NXO_TQ_D; ++i) u[i] = c3[c[i]];
+        tq_unrotate(u, norms[v], signs, out + (size_t)v * NXO_TQ_D);
+    }
+}
+
+void nxo_tq_to_cool(const uint8_t* codes4, const uint8_t* codes3, const uint16_t* norms, int n, const float* signs,
+                    const float* c4, const float* c3, const float* b3, uint8_t* cool, uint16_t* cool_norms) {
+    for (int v = 0; v < n; ++v) {
+        float x[NXO_TQ_D];
+        nxo_tq_decode(codes4 + (size_t)v * 32, codes3 + (size_t)v * 24, norms + v, 1, signs, c4, c3, x);
+        nxo_cool_encode(x, 1, signs, b3, cool + (size_t)v * NXO_COOL_CODES, cool_norms + v);
     }
 }
 
@@ -589,17 +627,39 @@ int nxo_tiered_cold(int ctx, int hot_window) {
     return c > 0 ? NXO_PAGE * (c / NXO_PAGE) : 0;
 }
 
-void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
-                            const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
-                            const uint16_t* vn, const float* ksigns, const float* vsigns, const float* c4,
-                            const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
-                            int hot_window, int B, int hq, int hkv, float* out) {
+int nxo_tiered_cool(int ctx, int hot_window, int warm_window) {
+    if (warm_window <= 0) return 0;
+    return nxo_tiered_cold(ctx, hot_window + warm_window);
+}
+
+void nxo_tiered_append_cool(int hkv, const float* ksigns, const float* vsigns, const float* c4, const float* c3,
+                            const float* b3, const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn,
+                            const uint8_t* vc4, const uint8_t* vc3, const uint16_t* vn, uint8_t* kcc,
+                            uint16_t* kcn, uint8_t* vcc, uint16_t* vcn, const int32_t* block_table, int max_blocks,
+                            int b, int pos) {
+    const int blk = block_table[(size_t)b * max_blocks + pos / NXO_PAGE];
+    for (int h = 0; h < hkv; ++h) {
+        const size_t vi = ((size_t)blk * hkv + h) * NXO_PAGE + pos % NXO_PAGE;
+        nxo_tq_to_cool(kc4 + vi * 32, kc3 + vi * 24, kn + vi, 1, ksigns, c4, c3, b3, kcc + vi * NXO_COOL_CODES,
+                       kcn + vi);
+        nxo_tq_to_cool(vc4 + vi * 32, vc3 + vi * 24, vn + vi, 1, vsigns, c4, c3, b3, vcc + vi * NXO_COOL_CODES,
+                       vcn + vi);
+    }
+}
+
+void nxo_attn_decode_tiered_cool(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                                 const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                                 const uint16_t* vn, const uint8_t* kcc, const uint16_t* kcn, const uint8_t* vcc,
+                                 const uint16_t* vcn, const float* ksigns, const float* vsigns, const float* c4,
+                                 const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
+                                 int hot_window, int warm_window, int B, int hq, int hkv, float* out) {
     const int hd = NXO_TQ_D;
     const int grp = hq / hkv;
 #pragma omp parallel for collapse(2) schedule(dynamic)
     for (int b = 0; b < B; ++b) {
         for (int kvh = 0; kvh < hkv; ++kvh) {
             const int ctx = ctx_lens[b], cold = nxo_tiered_cold(ctx, hot_window);
+            const int cool = nxo_tiered_cool(ctx, hot_window, warm_window);
             const int32_t* bt = block_table + (size_t)b * max_blocks;
             const size_t rows = (size_t)(ctx > 0 ? ctx : 1);
             float* K = (float*)malloc(sizeof(float) * rows * hd);
@@ -609,8 +669,13 @@ void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_
             gather_f16(vpool, bt, ctx, hkv, kvh, hd, 1, V);
             for (int t = 0; t < cold; ++t) {
                 const size_t vi = ((size_t)bt[t / NXO_PAGE] * hkv + kvh) * NXO_PAGE + t % NXO_PAGE;
-                nxo_tq_decode(kc4 + vi * 32, kc3 + vi * 24, kn + vi, 1, ksigns, c4, c3, K + (size_t)t * hd);
-                nxo_tq_decode(vc4 + vi * 32, vc3 + vi * 24, vn + vi, 1, vsigns, c4, c3, V + (size_t)t * hd);
+                if (t < cool) {
+                    nxo_cool_decode(kcc + vi * NXO_COOL_CODES, kcn + vi, 1, ksigns, c3, K + (size_t)t * hd);
+                    nxo_cool_decode(vcc + vi * NXO_COOL_CODES, vcn + vi, 1, vsigns, c3, V + (size_t)t * hd);
+                } else {
+                    nxo_tq_decode(kc4 + vi * 32, kc3 + vi * 24, kn + vi, 1, ksigns, c4, c3, K + (size_t)t * hd);
+                    nxo_tq_decode(vc4 + vi * 32, vc3 + vi * 24, vn + vi, 1, vsigns, c4, c3, V + (size_t)t * hd);
+                }
             }
             for (int j = 0; j < grp; ++j) {
                 const int h = kvh * grp + j;
@@ -622,6 +687,15 @@ void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_
             free(scores);
         }
     }
+}
+
+void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                            const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                            const uint16_t* vn, const float* ksigns, const float* vsigns, const float* c4,
+                            const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
+                            int hot_window, int B, int hq, int hkv, float* out) {
+    nxo_attn_decode_tiered_cool(q, kpool, vpool, kc4, kc3, kn, vc4, vc3, vn, NULL, NULL, NULL, NULL, ksigns, vsigns,
+                                c4, c3, block_table, max_blocks, ctx_lens, hot_window, 0, B, hq, hkv, out);
 }
 
 /* ------------------------------------------------------------------ MoE -- */
@@ -671,6 +745,8 @@ typedef struct {
     uint16_t *kpool, *vpool;                 /* fp16 pages */
     uint8_t *kc4, *kc3, *vc4, *vc3;          /* TurboQuant pages */
     uint16_t *kn, *vn;
+    uint8_t *kcc, *vcc;                      /* Cool codes (tiered with warm_window > 0) */
+    uint16_t *kcn, *vcn;
     float ksign[NXO_TQ_D], vsign[NXO_TQ_D];
     float *norm_attn, *norm_ffn;             /* RMSNorm weights, NULL = 1.0 */
 } layer_t;
@@ -790,6 +866,12 @@ nxo_model* nxo_model_create(const nxo_cfg* cfg) {
             ly->kn = (uint16_t*)calloc(pool_vecs, 2);
             ly->vn = (uint16_t*)calloc(pool_vecs, 2);
         }
+        if (c->kv_kind == 2 && c->warm_window > 0) {
+            ly->kcc = (uint8_t*)calloc(pool_vecs, NXO_COOL_CODES);
+            ly->vcc = (uint8_t*)calloc(pool_vecs, NXO_COOL_CODES);
+            ly->kcn = (uint16_t*)calloc(pool_vecs, 2);
+            ly->vcn = (uint16_t*)calloc(pool_vecs, 2);
+        }
         nxo_tq_signs(ly->ksign, seed, NXO_TID_LAYER(L, NXO_TQ_KSIGN));
         nxo_tq_signs(ly->vsign, seed, NXO_TID_LAYER(L, NXO_TQ_VSIGN));
     }
@@ -827,6 +909,7 @@ void nxo_model_free(nxo_model* m) {
         }
         free(ly->kpool); free(ly->vpool);
         free(ly->kc4); free(ly->kc3); free(ly->vc4); free(ly->vc3); free(ly->kn); free(ly->vn);
+        free(ly->kcc); free(ly->vcc); free(ly->kcn); free(ly->vcn);
         free(ly->norm_attn); free(ly->norm_ffn);
     }
     free(m->norm_final);
@@ -847,8 +930,14 @@ int nxo_model_kv_read(const nxo_model* m, int layer, int b, int pos, int kv, int
     const int blk = m->block_table[(size_t)b * m->max_blocks + pos / NXO_PAGE], slot = pos % NXO_PAGE;
     if (form == 0 && !ly->kpool) return 0;
     if (form == 1 && !ly->kc4) return 0;
+    if (form == 2 && !ly->kcc) return 0;
     for (int h = 0; h < hkv; ++h) {
-        if (form == 1) {
+        if (form == 2) {
+            const size_t vi = ((size_t)blk * hkv + h) * NXO_PAGE + slot;
+            memcpy(out + (size_t)(NXO_COOL_CODES + 2) * h, (kv ? ly->vcc : ly->kcc) + vi * NXO_COOL_CODES,
+                   NXO_COOL_CODES);
+            memcpy(out + (size_t)(NXO_COOL_CODES + 2) * h + NXO_COOL_CODES, (kv ? ly->vcn : ly->kcn) + vi, 2);
+        } else if (form == 1) {
             const size_t vi = ((size_t)blk * hkv + h) * NXO_PAGE + slot;
             memcpy(out + (size_t)58 * h, (kv ? ly->vc4 : ly->kc4) + vi * 32, 32);
             memcpy(out + (size_t)58 * h + 32, (kv ? ly->vc3 : ly->kc3) + vi * 24, 24);
@@ -861,9 +950,21 @@ int nxo_model_kv_read(const nxo_model* m, int layer, int b, int pos, int kv, int
             }
         }
     }
-    return form == 1 ? 58 * hkv : 2 * hkv * hd;
+    return form == 2 ? (NXO_COOL_CODES + 2) * hkv : form == 1 ? 58 * hkv : 2 * hkv * hd;
 }
 int nxo_model_max_blocks(const nxo_model* m) { return m->max_blocks; }
+
+/* Tiered append of one position: fp16 and Warm forms, and the Cool form
+ * (from the Warm codes) when the model has a Cool tier. */
+static void tiered_append(nxo_model* m, layer_t* ly, const float* k, const float* v, int b, int pos) {
+    const int hkv = m->c.n_kv_heads;
+    nxo_tiered_append(k, v, hkv, ly->ksign, ly->vsign, m->b4, m->b3, ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn,
+                      ly->vc4, ly->vc3, ly->vn, m->block_table, m->max_blocks, b, pos);
+    if (ly->kcc)
+        nxo_tiered_append_cool(hkv, ly->ksign, ly->vsign, m->c4, m->c3, m->b3, ly->kc4, ly->kc3, ly->kn, ly->vc4,
+                               ly->vc3, ly->vn, ly->kcc, ly->kcn, ly->vcc, ly->vcn, m->block_table, m->max_blocks, b,
+                               pos);
+}
 
 /* x (fp32) -> fp16-rounded RMSNorm output with weights w (NULL = 1.0). */
 static void norm_to_f16(const float* x, const float* w, int d, float eps, float* out) {
@@ -937,9 +1038,7 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
                 nxo_kv_append_f16(kb, vb, ly->kpool, ly->vpool, m->block_table, m->max_blocks, b,
                                   m->pos[b], hkv, hd);
             else if (c->kv_kind == 2)
-                nxo_tiered_append(kb, vb, hkv, ly->ksign, ly->vsign, m->b4, m->b3, ly->kpool, ly->vpool,
-                                  ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn, m->block_table,
-                                  m->max_blocks, b, m->pos[b]);
+                tiered_append(m, ly, kb, vb, b, m->pos[b]);
             else
                 nxo_tq_append(kb, vb, hkv, ly->ksign, ly->vsign, m->b4, m->b3, ly->kc4, ly->kc3,
                               ly->kn, ly->vc4, ly->vc3, ly->vn, m->block_table, m->max_blocks, b,
@@ -949,9 +1048,10 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
             nxo_attn_decode_paged_f16(m->q, ly->kpool, ly->vpool, m->block_table, m->max_blocks,
                                       ctx, B, hq, hkv, hd, m->att);
         else if (c->kv_kind == 2)
-            nxo_attn_decode_tiered(m->q, ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
-                                   ly->vn, ly->ksign, ly->vsign, m->c4, m->c3, m->block_table, m->max_blocks,
-                                   ctx, c->hot_window, B, hq, hkv, m->att);
+            nxo_attn_decode_tiered_cool(m->q, ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
+                                        ly->vn, ly->kcc, ly->kcn, ly->vcc, ly->vcn, ly->ksign, ly->vsign, m->c4,
+                                        m->c3, m->block_table, m->max_blocks, ctx, c->hot_window, c->warm_window,
+                                        B, hq, hkv, m->att);
         else
             nxo_attn_decode_paged_tq(m->q, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn,
                                      ly->ksign, ly->vsign, m->c4, m->c3, m->block_table,
@@ -1045,9 +1145,7 @@ void nxo_model_fill_context(nxo_model* m, int ctx, int n_outlier) {
                     nxo_kv_append_f16(kv, kv + (size_t)hkv * hd, ly->kpool, ly->vpool, m->block_table,
                                       m->max_blocks, b, p, hkv, hd);
                 else if (c->kv_kind == 2)
-                    nxo_tiered_append(kv, kv + (size_t)hkv * hd, hkv, ly->ksign, ly->vsign, m->b4, m->b3,
-                                      ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
-                                      ly->vn, m->block_table, m->max_blocks, b, p);
+                    tiered_append(m, ly, kv, kv + (size_t)hkv * hd, b, p);
                 else
                     nxo_tq_append(kv, kv + (size_t)hkv * hd, hkv, ly->ksign, ly->vsign, m->b4, m->b3,
                                   ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn, m->block_table,

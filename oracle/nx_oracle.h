@@ -141,6 +141,20 @@ void nxo_tq_encode(const float* x, int n, const float* signs, const float* b4, c
 /* x_hat = n * D * H(c[code]) / sqrt(128)  (inverse of the rotation above). */
 void nxo_tq_decode(const uint8_t* codes4, const uint8_t* codes3, const uint16_t* norms, int n,
                    const float* signs, const float* c4, const float* c3, float* out);
+/* Cool vector format, the reference's Cool quantizer (TurboQuantKV(head_dim,
+ * 3, 42), kv/paged_attention.cpp:31-32: 3-bit codes on every coordinate) in
+ * the build's rotation and norm: y as above, every coordinate coded with the
+ * 8-level codebook; codes = 128 x 3 bits LSB-first (48 B; coordinates 0..63
+ * fill bytes 0..23), norm = fp16(n).  50 bytes per vector. */
+#define NXO_COOL_CODES 48
+void nxo_cool_encode(const float* x, int n, const float* signs, const float* b3, uint8_t* codes,
+                     uint16_t* norms);
+void nxo_cool_decode(const uint8_t* codes, const uint16_t* norms, int n, const float* signs, const float* c3,
+                     float* out);
+/* Warm -> Cool, the step of compress_tier (kv/paged_attention.cpp:262-285):
+ * the TurboQuant vector decoded to fp32 (nxo_tq_decode), then encoded Cool. */
+void nxo_tq_to_cool(const uint8_t* codes4, const uint8_t* codes3, const uint16_t* norms, int n, const float* signs,
+                    const float* c4, const float* c3, const float* b3, uint8_t* cool, uint16_t* cool_norms);
 /* TQ page pool: codes4 [blocks][hkv][16][32], codes3 [blocks][hkv][16][24],
  * norms [blocks][hkv][16] fp16. */
 void nxo_tq_append(const float* k, const float* v, int hkv,
@@ -175,6 +189,26 @@ void nxo_tiered_append(const float* k, const float* v, int hkv, const float* ksi
                        uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
                        const int32_t* block_table, int max_blocks, int b, int pos);
 int nxo_tiered_cold(int ctx, int hot_window);
+/* Three tiers (warm_window > 0): pages also leave the Warm range [cool,
+ * cold) once they lie wholly outside the last hot_window + warm_window
+ * positions, and are then read in the Cool form, the Warm codes decoded and
+ * encoded Cool (the Warm -> Cool step of compress_tier, per page).  cool =
+ * nxo_tiered_cold(ctx, hot_window + warm_window), 0 when warm_window is 0.
+ * append_cool writes the Cool form of position pos from its Warm codes
+ * (pools [blocks][hkv][16][48] and [blocks][hkv][16] fp16 norms); the
+ * attention reads t < cool Cool, cool <= t < cold Warm, the rest fp16. */
+int nxo_tiered_cool(int ctx, int hot_window, int warm_window);
+void nxo_tiered_append_cool(int hkv, const float* ksigns, const float* vsigns, const float* c4, const float* c3,
+                            const float* b3, const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn,
+                            const uint8_t* vc4, const uint8_t* vc3, const uint16_t* vn, uint8_t* kcc,
+                            uint16_t* kcn, uint8_t* vcc, uint16_t* vcn, const int32_t* block_table, int max_blocks,
+                            int b, int pos);
+void nxo_attn_decode_tiered_cool(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                                 const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                                 const uint16_t* vn, const uint8_t* kcc, const uint16_t* kcn, const uint8_t* vcc,
+                                 const uint16_t* vcn, const float* ksigns, const float* vsigns, const float* c4,
+                                 const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
+                                 int hot_window, int warm_window, int B, int hq, int hkv, float* out);
 void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
                             const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
                             const uint16_t* vn, const float* ksigns, const float* vsigns, const float* c4,
@@ -208,6 +242,8 @@ typedef struct {
     uint64_t seed;
     float norm_sigma;              /* RMSNorm weights: 0 = 1.0, else 1 + N(0, norm_sigma) */
     int hot_window;                /* kv_kind 2: tokens kept fp16, a multiple of 16 */
+    int warm_window;               /* kv_kind 2: 0 = two tiers; else the positions before the
+                                      fp16 window kept Warm (a multiple of 16), older pages Cool */
 } nxo_cfg;
 
 typedef struct nxo_model nxo_model;
@@ -230,7 +266,8 @@ int nxo_model_position(const nxo_model* m, int b);
 const int32_t* nxo_model_block_table(const nxo_model* m);
 /* The stored form of position pos (all kv heads) of layer `layer`, K (kv 0)
  * or V (kv 1): form 0 = fp16 [hkv][hd], form 1 = TurboQuant [hkv] x (32 B
- * 4-bit codes, 24 B 3-bit codes, fp16 norm); the model must hold that form
+ * 4-bit codes, 24 B 3-bit codes, fp16 norm), form 2 = Cool [hkv] x (48 B
+ * 3-bit codes, fp16 norm); the model must hold that form
  * (tiered models hold both).  Returns the bytes written, 0 if absent. */
 int nxo_model_kv_read(const nxo_model* m, int layer, int b, int pos, int kv, int form, uint8_t* out);
 int nxo_model_max_blocks(const nxo_model* m);

@@ -145,6 +145,53 @@ def test_tiered_pipelined_batch8(ctx):
     _filled_parity(ctx, cfg, 4000, 20, n_outlier=4, tie=TQ_TIE, check_pages=pages)
 
 
+def test_8b_three_tier_32k_one_layer(ctx):
+    """One 8B-shaped layer at 32760 positions with three tiers (last 4096
+    fp16, the 4096 before them TurboQuant, older pages Cool): all three
+    split loops are pipelined; at the 8th step position 32767 completes
+    page 1791 outside the window and page (32767 - 8192 + 1) / 16 - 1 = 1535
+    outside the Warm range, and the device re-encodes page 1535 Cool,
+    bit-exact with the oracle."""
+    cfg = dict(LLAMA8B, n_layers=1, kv_kind=2, hot_window=4096, warm_window=4096, max_seq=32768 + 256,
+               seed=0x3C8E)
+    ctx_len, steps = 32760, 10
+
+    def pages(gm, om):
+        for p in list(range(1535 * 16, 1536 * 16)) + [0, 12345, 24559]:
+            for kv in range(2):
+                form, g = gm.kv_read(0, 0, p, kv)
+                assert form == 2, (p, kv)
+                assert np.array_equal(g, om.kv_read(0, 0, p, kv, 2)), (p, kv)
+        for p in (1791 * 16, 1791 * 16 + 15, 24576, 28671):
+            form, g = gm.kv_read(0, 0, p, 0)
+            assert form == 1 and np.array_equal(g, om.kv_read(0, 0, p, 0, 1)), p
+
+    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+
+
+def test_three_tier_pipelined_batch8(ctx):
+    """Batch 8, 8 kv heads, 4608 positions of capacity, a 512-position
+    window and a 512-position Warm range: the split plan pipelines the Cool,
+    TurboQuant and fp16 loops; 20 steps from 4000 filled positions cross one
+    compression of each kind per sequence (at the 16th step)."""
+    cfg = dict(LLAMA8B, n_layers=2, d_model=512, n_heads=16, n_kv_heads=8, ffn=688, vocab=4096, batch=8,
+               max_seq=4608, kv_kind=2, hot_window=512, warm_window=512, seed=0x3CB8)
+
+    def pages(gm, om):
+        # position 4015 completes page 218 outside the window and page
+        # (4015 - 1024 + 1) / 16 - 1 = 186 outside the Warm range
+        for b in (0, 7):
+            for p in range(186 * 16, 187 * 16, 5):
+                for kv in range(2):
+                    form, g = gm.kv_read(1, b, p, kv)
+                    assert form == 2 and np.array_equal(g, om.kv_read(1, b, p, kv, 2)), (b, p, kv)
+            for p in range(218 * 16, 219 * 16, 5):
+                form, g = gm.kv_read(1, b, p, 1)
+                assert form == 1 and np.array_equal(g, om.kv_read(1, b, p, 1, 1)), (b, p)
+
+    _filled_parity(ctx, cfg, 4000, 20, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+
+
 # ------------------------------------------------------------ Mixtral shape --
 @pytest.mark.parametrize("batch", [1, 8])
 def test_mixtral_one_layer_parity(ctx, batch):

@@ -2,9 +2,12 @@
 fp16, older pages compressed to TurboQuant on the device as they leave the
 window (the Hot -> Warm step of PagedKVCache::compress_tier,
 kv/paged_attention.cpp:244-291, run per page), attention over both tiers
-in one softmax (the mixed-tier gather of get_vectors, :161-230).  Checked
-against the oracle's restatement: greedy tokens, logits, and the stored
-bytes of every compressed page bit-exact."""
+in one softmax (the mixed-tier gather of get_vectors, :161-230).  With a
+warm_window, pages that also leave the Warm range are re-encoded Cool
+(3-bit codes on every coordinate; the Warm -> Cool step of compress_tier)
+and attention reads three tiers.  Checked against the oracle's
+restatement: greedy tokens, logits, and the stored bytes of every
+compressed page bit-exact."""
 import numpy as np
 import pytest
 
@@ -137,3 +140,112 @@ def test_tiered_config_rejected(ctx):
             nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=2, hot_window=H))
     with pytest.raises(RuntimeError):
         nexus_amd.Model(ctx, **dict(TINY, kv_kind=2, hot_window=32))  # head_dim 64
+
+
+# ------------------------------------------------------------- three tiers --
+@pytest.mark.parametrize("batch,H,W", [(1, 16, 16), (2, 32, 48)])
+def test_three_tier_greedy_parity(ctx, batch, H, W):
+    """A 12-token prompt and 100 greedy tokens: pages leave the fp16 window
+    from position H + 15 on and the Warm range from H + W + 15 on, both
+    compressions on the device in the attention launch."""
+    cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, warm_window=W, seed=0x3C1 + H + W)
+    got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
+    assert_greedy_parity(got, want, margins, tie=TQ_TIE)
+
+
+def _check_forms(gm, om, n_layers, batch, ranges):
+    for L in range(n_layers):
+        for b in range(batch):
+            for kv in range(2):
+                for positions, form_want in ranges:
+                    for p in positions:
+                        form, got = gm.kv_read(L, b, p, kv)
+                        assert form == form_want, (L, b, p, kv, form)
+                        want = om.kv_read(L, b, p, kv, form)
+                        assert np.array_equal(got, want), (L, b, p, kv, form)
+
+
+def test_three_tier_filled_context_and_compressors(ctx):
+    """300 filled positions with a 64-position window and a 32-position Warm
+    range: the fill writes pages 0..11 Cool, 12..13 TurboQuant, 14..18
+    fp16.  In 40 decode steps pages 14, 15, 16 leave the window and pages
+    12, 13, 14 leave the Warm range (page 14 both: the Warm codes the
+    device wrote are re-encoded 32 steps later).  Every Cool, TurboQuant and
+    fp16 position is bit-exact against the oracle, before and after."""
+    cfg = dict(TQ_TINY, batch=2, max_seq=512, kv_kind=2, hot_window=64, warm_window=32, seed=0x3C2)
+    ctx_len, steps = 300, 40
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(ctx_len, 4)
+    om = oracle.Model(**cfg)
+    om.fill_context(ctx_len, 4)
+    n_layers = cfg["n_layers"]
+    _check_forms(gm, om, n_layers, 2, [(list(range(0, 192, 5)) + [191], 2), (range(192, 224, 3), 1),
+                                       (range(224, 300, 4), 0)])
+    start = gm.pending()
+    got = gm.decode(steps)
+    glog = gm.logits()
+    _check_forms(gm, om, n_layers, 2, [(range(192, 240), 2), (range(240, 272), 1), (range(272, 300), 0)])
+    gm.close()
+    want, margins, logits = _oracle_steps(om, start, steps)
+    om.close()
+    assert_greedy_parity(got, want, margins)
+    if np.array_equal(got, want):
+        assert rel_err(glog, logits) < 1e-3
+
+
+@pytest.mark.parametrize("hq,hkv,H,W,ctx_len", [(8, 2, 128, 64, 700), (8, 1, 32, 32, 1000), (4, 4, 256, 16, 400)])
+def test_three_tier_group_sizes(ctx, hq, hkv, H, W, ctx_len):
+    """Query groups of 2 to 8 heads, a single kv head, several window and
+    Warm sizes: 20 decode steps from a filled context give the oracle's
+    tokens (logits within 1e-3 when the tokens agree); Cool pages stay
+    bit-exact."""
+    cfg = dict(TINY, n_heads=hq, n_kv_heads=hkv, head_dim=128, d_model=hq * 128, max_seq=1024 + 64, batch=1,
+               kv_kind=2, hot_window=H, warm_window=W, seed=0x6100 + hq * 16 + hkv + H + W)
+    steps = 20
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(ctx_len, 4)
+    om = oracle.Model(**cfg)
+    om.fill_context(ctx_len, 4)
+    start = gm.pending()
+    got = gm.decode(steps)
+    glog = gm.logits()
+    cool = 16 * max(0, (ctx_len + steps - H - W) // 16)
+    for p in list(range(0, cool, 37)) + ([cool - 1] if cool else []):
+        for kv in range(2):
+            form, g = gm.kv_read(cfg["n_layers"] - 1, 0, p, kv)
+            assert form == 2 and np.array_equal(g, om.kv_read(cfg["n_layers"] - 1, 0, p, kv, 2)), (p, kv)
+    gm.close()
+    want, margins, logits = _oracle_steps(om, start, steps)
+    om.close()
+    assert_greedy_parity(got, want, margins)
+    if np.array_equal(got, want):
+        assert rel_err(glog, logits) < 1e-3
+
+
+def test_three_tier_empty_cool_range_matches_two_tiers(ctx):
+    """A Warm range that covers the whole compressed part (no page ever
+    reaches Cool): the three-tier launch (an empty Cool range, its extra
+    records and compressor blocks) gives the two-tier model's tokens and
+    logits within 1e-3."""
+    base = dict(TQ_TINY, batch=2, max_seq=512, kv_kind=2, hot_window=32, seed=0x3C3)
+    ctx_len, steps = 200, 12
+    out = {}
+    for W in (0, 448):
+        m = nexus_amd.Model(ctx, **dict(base, warm_window=W))
+        m.fill_context(ctx_len, 4)
+        toks = m.decode(steps)
+        out[W] = (toks, m.logits())
+        form, _ = m.kv_read(0, 0, 0, 0)
+        assert form == 1
+        m.close()
+    assert np.array_equal(out[0][0], out[448][0])
+    assert rel_err(out[448][1], out[0][1]) < 1e-3
+
+
+def test_three_tier_config_rejected(ctx):
+    for W in (-16, 8, 24):
+        with pytest.raises(RuntimeError):
+            nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=2, hot_window=32, warm_window=W))
+    for kind in (0, 1):
+        with pytest.raises(RuntimeError):
+            nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=kind, warm_window=32))

@@ -502,6 +502,151 @@ def test_tiered_attention_vs_fp64(ctx, H):
         assert rel_err(want_for(cold + 16), want) > 1e-3
 
 
+# ------------------------------------------------------------ Cool tier --
+def _unpack3_lsb(cc):
+    """[n][48] bytes -> [n][128] 3-bit codes, LSB-first (numpy's bit order)."""
+    bits = np.unpackbits(cc, axis=1, bitorder="little").reshape(cc.shape[0], 128, 3)
+    return (bits[:, :, 0] | (bits[:, :, 1] << 1) | (bits[:, :, 2] << 2)).astype(np.uint8)
+
+
+def _rotated(x, signs):
+    from scipy.linalg import hadamard
+    H = hadamard(128).astype(np.float64) / np.sqrt(128)
+    x = x.astype(np.float64)
+    n = np.linalg.norm(x, axis=1, keepdims=True)
+    return (H @ (signs.astype(np.float64) * x / n).T).T, n[:, 0]
+
+
+def test_cool_codes_vs_hadamard_fp64():
+    """Cool codes: every coordinate of y = H D x / (|x| sqrt(128)) coded by
+    the 8-level boundaries (first j with y < b_j), packed 3 bits LSB-first
+    in 48 bytes; norm fp16(|x|).  Checked against an fp64 restatement with
+    scipy's Hadamard matrix and numpy's bit unpacking; codes may differ only
+    where y lies within 1e-5 of a boundary."""
+    rng = np.random.default_rng(21)
+    x = rng.normal(0, 1, (300, 128)).astype(np.float32)
+    x[:, [3, 77]] *= 10.0
+    signs = oracle.tq_signs(7, 0x208)
+    cc, nr = oracle.cool_encode(x, signs)
+    y, n = _rotated(x, signs)
+    _, b3 = oracle.codebook(3)
+    want = np.searchsorted(b3.astype(np.float64), y, side="right").astype(np.uint8)
+    got = _unpack3_lsb(cc)
+    near = np.min(np.abs(y[..., None] - b3.astype(np.float64)), axis=-1) < 1e-5
+    assert np.array_equal(got[~near], want[~near])
+    assert (got == want).mean() > 0.999
+    assert np.array_equal(nr, oracle.f16_bits(n.astype(np.float32)))
+    # the first 64 coordinates fill bytes 0..23 exactly (two 24-byte halves)
+    lo = np.unpackbits(cc[:, :24], axis=1, bitorder="little").reshape(-1, 64, 3)
+    assert np.array_equal(lo[:, :, 0] | (lo[:, :, 1] << 1) | (lo[:, :, 2] << 2), got[:, :64])
+
+
+def test_cool_roundtrip_distortion():
+    """3-bit codes on every coordinate: the Gaussian 8-level Lloyd-Max
+    distortion 0.03454 per unit variance (the 3.5-bit form sits at 0.022)."""
+    rng = np.random.default_rng(22)
+    x = rng.normal(0, 1, (2000, 128)).astype(np.float32)
+    signs = oracle.tq_signs(7, 0x209)
+    cc, nr = oracle.cool_encode(x, signs)
+    xh = oracle.cool_decode(cc, nr, signs)
+    err = np.sum((xh - x) ** 2, 1) / np.sum(x**2, 1)
+    assert 0.030 < err.mean() < 0.039
+    z = np.zeros((1, 128), np.float32)
+    zc, zn = oracle.cool_encode(z, signs)
+    assert zn[0] == 0 and np.all(oracle.cool_decode(zc, zn, signs) == 0)
+
+
+def test_tq_to_cool_is_nearest_code_of_warm_values():
+    """Warm -> Cool decodes the 3.5-bit vector and encodes it Cool.  The
+    rotation is orthonormal, so in exact arithmetic the Cool coordinates are
+    the Warm codebook values over their norm, c / |c|: the Cool codes equal
+    the 8-level codes of c / |c| (away from boundaries), and the Cool norm is
+    the Warm norm times |c|."""
+    rng = np.random.default_rng(23)
+    x = rng.normal(0, 1, (400, 128)).astype(np.float32)
+    signs = oracle.tq_signs(7, 0x20A)
+    k4, k3, nr, cu = oracle.tq_encode(x, signs)
+    cc, cn = oracle.tq_to_cool(k4, k3, nr, signs)
+    c4, _ = oracle.codebook(4)
+    c3, b3 = oracle.codebook(3)
+    cv = np.where(np.arange(128) < 64, c4[np.minimum(cu, 15)], c3[np.minimum(cu, 7)]).astype(np.float64)
+    cnorm = np.linalg.norm(cv, axis=1)
+    y = cv / cnorm[:, None]
+    want = np.searchsorted(b3.astype(np.float64), y, side="right").astype(np.uint8)
+    got = _unpack3_lsb(cc)
+    near = np.min(np.abs(y[..., None] - b3.astype(np.float64)), axis=-1) < 1e-5
+    assert np.array_equal(got[~near], want[~near])
+    wn = oracle.f16_to_f32(nr).astype(np.float64) * cnorm * np.sqrt(128) * 0.08838834764831845
+    assert np.allclose(oracle.f16_to_f32(cn), wn, rtol=2e-3)
+
+
+def test_tiered_cool_boundary():
+    """cool = 16 floor((ctx - 1 - H - W) / 16) clamped at 0; no Cool tier
+    when W is 0."""
+    for ctx, H, W, want in [(1, 16, 16, 0), (48, 16, 16, 0), (49, 16, 16, 16), (300, 64, 32, 192),
+                            (32768, 4096, 4096, 24560), (32769, 4096, 4096, 24576), (5000, 16, 0, 0)]:
+        assert L.nxo_tiered_cool(ctx, H, W) == want, (ctx, H, W)
+        assert L.nxo_tiered_cool(ctx, H, W) <= L.nxo_tiered_cold(ctx, H)
+
+
+@pytest.mark.parametrize("ctx,H,W", [(130, 32, 16), (90, 16, 48), (40, 16, 16), (70, 48, 32)])
+def test_tiered_cool_attention_vs_fp64(ctx, H, W):
+    """Three tiers against an independent float64 restatement: positions
+    before cool read as the Cool round trip of the Warm round trip of their
+    fp16 values, [cool, cold) as the Warm round trip, the rest fp16, one
+    softmax over all.  Moving the Cool boundary by one page (the planted
+    mistake) moves the result past the bound."""
+    rng = np.random.default_rng(ctx * 3 + H + W)
+    hq, hkv, B = 4, 2, 2
+    K = rng.normal(0, 1, (B, ctx, hkv, 128)).astype(np.float32)
+    V = rng.normal(0, 1, (B, ctx, hkv, 128)).astype(np.float32)
+    q = rng.normal(0, 0.4, (B, hq, 128)).astype(np.float32)
+    ks, vs = oracle.tq_signs(4, 1), oracle.tq_signs(4, 2)
+    c4, b4 = oracle.codebook(4)
+    c3, b3 = oracle.codebook(3)
+    max_blocks = (ctx + 15) // 16 + 1
+    bt = rng.permutation(B * max_blocks).astype(np.int32).reshape(B, max_blocks)
+    nv = B * max_blocks * hkv * 16
+    kp, vp = np.zeros(nv * 128, np.uint16), np.zeros(nv * 128, np.uint16)
+    kc4, kc3, kn = np.zeros((nv, 32), np.uint8), np.zeros((nv, 24), np.uint8), np.zeros(nv, np.uint16)
+    vc4, vc3, vn = np.zeros_like(kc4), np.zeros_like(kc3), np.zeros_like(kn)
+    kcc, kcn = np.zeros((nv, 48), np.uint8), np.zeros(nv, np.uint16)
+    vcc, vcn = np.zeros_like(kcc), np.zeros_like(kcn)
+    for b in range(B):
+        for p in range(ctx):
+            L.nxo_tiered_append(np.ascontiguousarray(K[b, p]), np.ascontiguousarray(V[b, p]), hkv, ks, vs, b4,
+                                b3, kp, vp, kc4, kc3, kn, vc4, vc3, vn, bt, max_blocks, b, p)
+            L.nxo_tiered_append_cool(hkv, ks, vs, c4, c3, b3, kc4, kc3, kn, vc4, vc3, vn, kcc, kcn, vcc, vcn, bt,
+                                     max_blocks, b, p)
+    out = np.empty_like(q)
+    L.nxo_attn_decode_tiered_cool(q, kp, vp, kc4, kc3, kn, vc4, vc3, vn, kcc, kcn, vcc, vcn, ks, vs, c4, c3, bt,
+                                  max_blocks, np.full(B, ctx, np.int32), H, W, B, hq, hkv, out)
+
+    def want_for(cool, cold):
+        Kf = K.astype(np.float16).astype(np.float64)
+        Vf = V.astype(np.float16).astype(np.float64)
+        for b in range(B):
+            for h in range(hkv):
+                for X, Xf, s in ((K, Kf, ks), (V, Vf, vs)):
+                    if not cold:
+                        continue
+                    warm = oracle.tq_encode(X[b, :cold, h].astype(np.float16).astype(np.float32), s)[:3]
+                    Xf[b, :cold, h] = oracle.tq_decode(*warm, s)
+                    if cool:
+                        cc, cn = oracle.tq_to_cool(warm[0][:cool], warm[1][:cool], warm[2][:cool], s)
+                        Xf[b, :cool, h] = oracle.cool_decode(cc, cn, s)
+        return np.stack([_attn_fp64(q[b].astype(np.float64), Kf[b], Vf[b], hq, hkv, 128) for b in range(B)])
+
+    cold = max(0, (ctx - 1 - H) // 16 * 16)
+    cool = max(0, (ctx - 1 - H - W) // 16 * 16)
+    assert cool == L.nxo_tiered_cool(ctx, H, W) and cold == L.nxo_tiered_cold(ctx, H)
+    want = want_for(cool, cold)
+    e = rel_err(out, want)
+    assert e < 1e-5, e
+    if cool + 16 <= cold:
+        assert rel_err(want_for(cool + 16, cold), want) > 1e-3
+
+
 # -------------------------------------------------------------------- MoE --
 def test_moe_route_golden():
     g = gold("moe_route.npz")
