@@ -343,6 +343,12 @@ typedef struct {
                                the Hot -> Warm -> Cool tiers of PagedKVCache
                                (kv/paged_attention.h:18-24, compress_tier
                                kv/paged_attention.cpp:244-291) as a per-page policy */
+    int cool_window;        /* kv_kind 2 with a warm_window: 0 = keep every Cool page; else a
+                               positive multiple of 16: the positions kept Cool (a ring of
+                               cool_window / 16 + 1 pages per sequence), older pages evicted --
+                               the Cold tier of evict_cold_pages (kv/paged_attention.cpp:295-310):
+                               attention reads an evicted position as the zero key and value
+                               get_vectors gathers for a page it does not hold (:172, :219) */
 } nx_model_config;
 
 typedef struct nx_model nx_model;
@@ -428,7 +434,7 @@ nx_status nx_model_fill_context(nx_model* m, int ctx, int n_outlier);
  * of 3-bit codes, fp16 norm) (58 * hkv bytes), form 2 = Cool [hkv] x (48
  * bytes of 3-bit codes, fp16 norm) (50 * hkv bytes); *form tells which
  * (tiered pages: 1 before the window, 0 in it, 2 before the Warm range with
- * three tiers).  The per-position read-back of
+ * three tiers, 3 = evicted, no bytes).  The per-position read-back of
  * PagedKVCache::get_vectors (kv/paged_attention.cpp:161-230), as stored
  * rather than decompressed; cap = bytes available at out. */
 nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* form, void* out, size_t cap);

@@ -998,16 +998,16 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tiered3(AttnArgs a, Ti
     }
 }
 
-// Context fill of Cool pages: positions [0, n) of x [ctx][hkv][128] (fp32,
+// Context fill of Cool pages: positions [p0, n) of x [ctx][hkv][128] (fp32,
 // the fp16 values) of sequence b, one wavefront per vector, encoded
 // TurboQuant, decoded, and encoded Cool (what the per-page compressors give
 // a position that passed through both steps) into cool_table's pages.
-__global__ __launch_bounds__(256) void k_cool_encode_ctx(const float* x, int n, int hkv, const float* signs,
+__global__ __launch_bounds__(256) void k_cool_encode_ctx(const float* x, int p0, int n, int hkv, const float* signs,
                                                          uint8_t* cc, uint16_t* cn, const int32_t* cool_table,
                                                          int max_blocks, int b) {
     __shared__ uint8_t codes[4][128];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int v = blockIdx.x * 4 + wave;
+    const int v = p0 * hkv + blockIdx.x * 4 + wave;
     if (v >= n * hkv) return;
     const int t = v / hkv, h = v % hkv;
     const size_t dst = ((size_t)cool_table[(size_t)b * max_blocks + t / kPage] * hkv + h) * kPage + t % kPage;
@@ -1238,12 +1238,14 @@ size_t attn_tiered_workspace_bytes(int batch, int hq, int hkv) {
     return sizeof(float) * (size_t)batch * hkv * kMaxSplits * rec_floats(hq / hkv, 128);
 }
 
-// Three tiers: the Cool pages (at most (max_ctx - H - W) / 16 + 1), the Warm
-// range (W / 16 + 1 pages) and the window (H / 16 + 2 pages) share about one
-// block per CU over all (kv head, sequence) pairs in proportion to their
-// cost (a TurboQuant or Cool page taking about 0.8 of an fp16 page's time).
-TierPlan3 plan_tiered3(int max_ctx, int hot_window, int warm_window, int hkv, int batch) {
-    const int pc = max(1, (max_ctx - hot_window - warm_window) / kPage + 1);
+// Three tiers: the Cool pages (at most (max_ctx - H - W) / 16 + 1, or C / 16
+// + 1 with a Cool window C), the Warm range (W / 16 + 1 pages) and the
+// window (H / 16 + 2 pages) share about one block per CU over all (kv head,
+// sequence) pairs in proportion to their cost (a TurboQuant or Cool page
+// taking about 0.8 of an fp16 page's time).
+TierPlan3 plan_tiered3(int max_ctx, int hot_window, int warm_window, int cool_window, int hkv, int batch) {
+    int pc = max(1, (max_ctx - hot_window - warm_window) / kPage + 1);
+    if (cool_window > 0) pc = min(pc, cool_window / kPage + 1);
     const int pw = warm_window / kPage + 1, pf = hot_window / kPage + 2;
     const int S = min(max(3, (device_cus() + hkv * batch - 1) / (hkv * batch)), kMaxSplits);
     const double cc = 0.8 * pc, cw = 0.8 * pw, cf = pf, tot = cc + cw + cf;
@@ -1260,8 +1262,10 @@ TierPlan3 plan_tiered3(int max_ctx, int hot_window, int warm_window, int hkv, in
 }
 
 hipError_t attn_tiered3_launch(const AttnArgs& a, hipStream_t st) {
-    if (!a.cool_table || !a.kcc || !a.vcc || !a.kcn || !a.vcn || a.warm_window % kPage) return hipErrorInvalidValue;
-    const TierPlan3 p = plan_tiered3(a.max_ctx, a.hot_window, a.warm_window, a.hkv, a.batch);
+    if (!a.cool_table || !a.kcc || !a.vcc || !a.kcn || !a.vcn || a.warm_window % kPage || a.cool_window < 0 ||
+        a.cool_window % kPage)
+        return hipErrorInvalidValue;
+    const TierPlan3 p = plan_tiered3(a.max_ctx, a.hot_window, a.warm_window, a.cool_window, a.hkv, a.batch);
     if (p.nc + p.nw + p.nf > kMaxSplits) return hipErrorInvalidValue;
     const dim3 grid(p.nc + p.nw + p.nf + 4 * kCompressParts, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
@@ -1346,11 +1350,11 @@ hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* s
     return hipGetLastError();
 }
 
-hipError_t cool_encode_ctx_launch(const float* x, int n, int hkv, const float* signs, uint8_t* cc, uint16_t* cn,
-                                  const int32_t* cool_table, int max_blocks, int b, hipStream_t st) {
-    const int nvec = n * hkv;
+hipError_t cool_encode_ctx_launch(const float* x, int p0, int n, int hkv, const float* signs, uint8_t* cc,
+                                  uint16_t* cn, const int32_t* cool_table, int max_blocks, int b, hipStream_t st) {
+    const int nvec = (n - p0) * hkv;
     if (nvec <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_cool_encode_ctx, dim3((nvec + 3) / 4), dim3(256), 0, st, x, n, hkv, signs, cc, cn,
+    hipLaunchKernelGGL(k_cool_encode_ctx, dim3((nvec + 3) / 4), dim3(256), 0, st, x, p0, n, hkv, signs, cc, cn,
                        cool_table, max_blocks, b);
     return hipGetLastError();
 }

@@ -37,11 +37,12 @@ __device__ inline void st_coh_u16(uint16_t* p, uint16_t v) {
 // The part of sequence b's context a block covers: all of it (range 0), or
 // with tiered pages the TurboQuant pages [cool, cold) (range 1, from page
 // cool / 16 on), the fp16 window [cold, ctx) (range 2, read from page cold /
-// 16 of the hot table on) or the Cool pages [0, cool) (range 3).  cold = 16
+// 16 of the hot table on) or the Cool pages [evict, cool) (range 3).  cold = 16
 // floor((ctx - 1 - hot_window) / 16), at least 0: the pages compressed
 // before this step (the page that leaves the window at this step is
 // compressed by the same launch and read here as fp16); cool likewise with
-// hot_window + warm_window, 0 without a Cool tier (warm_window 0).
+// hot_window + warm_window, 0 without a Cool tier (warm_window 0), evict
+// with hot_window + warm_window + cool_window, 0 without eviction.
 __device__ inline void attn_range(const AttnArgs& a, int b, int range, int& ctx, int& pg0) {
     ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
     pg0 = 0;
@@ -51,8 +52,12 @@ __device__ inline void attn_range(const AttnArgs& a, int b, int range, int& ctx,
         if (range == 1) {  // Warm: [cool, cold)
             pg0 = cool / kPage;
             ctx = cold - cool;
-        } else if (range == 3) {  // Cool: [0, cool)
-            ctx = cool;
+        } else if (range == 3) {  // Cool: [evict, cool)
+            const int evict =
+                a.cool_window > 0 ? kPage * max(0, (ctx - 1 - a.hot_window - a.warm_window - a.cool_window) / kPage)
+                                  : 0;
+            pg0 = evict / kPage;
+            ctx = max(cool - evict, 0);
         } else {  // fp16: [cold, ctx)
             pg0 = cold / kPage;
             ctx -= cold;
@@ -306,6 +311,15 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
     const int c = tid % NC, sg = tid / NC, h = 4 * c / HD;
+    // evicted positions (three tiers with a Cool window): zero keys and
+    // values, each a score of 0 in the softmax and nothing in the sum
+    float nev = 0.0f;
+    if constexpr (TQ) {
+        if (a.cool_window > 0 && a.warm_window > 0) {
+            const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.pos[b] + 1;
+            nev = (float)(kPage * max(0, (ctx - 1 - a.hot_window - a.warm_window - a.cool_window) / kPage));
+        }
+    }
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(parts), 0, nsplit * REC * 4, 0x00020000);
     typedef float f4v __attribute__((ext_vector_type(4)));
@@ -326,9 +340,9 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
         const int sl = ok ? lane : nsplit - 1;
         const float m = ld_coh(parts + (size_t)sl * REC + MO + hh);
         const float l = ld_coh(parts + (size_t)sl * REC + LO + hh);
-        const float M = wave_max(m);
+        const float M = nev > 0.0f ? fmaxf(wave_max(m), 0.0f) : wave_max(m);
         const float e = (ok && M != -__builtin_inff()) ? __expf(m - M) : 0.0f;
-        const float L = wave_sum(e * l);
+        const float L = wave_sum(e * l) + (nev > 0.0f ? nev * __expf(-M) : 0.0f);
         // a NaN denominator (NaN scores, or a sequence the kernel's table
         // check rejected) stays NaN in the output rather than becoming zero
         wgt[hh * kMaxSplits + lane] = L > 0.0f ? e / L : (L == L ? 0.0f : L);

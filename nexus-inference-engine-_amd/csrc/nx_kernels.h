@@ -130,6 +130,11 @@ struct AttnArgs {
     // 1 - hot_window - warm_window) / 16) clamped at 0.  The same launch
     // re-encodes the page that leaves the Warm range into the Cool pages.
     int warm_window;
+    // Cold (cool_window > 0 with three tiers): positions [0, evict) are
+    // evicted, evict = 16 floor((ctx - 1 - hot_window - warm_window -
+    // cool_window) / 16) clamped at 0; they enter the softmax as zero keys
+    // and values (score 0), and the Cool range is [evict, cool)
+    int cool_window;
     const int32_t* cool_table;
     const uint8_t *kcc, *vcc;
     const uint16_t *kcn, *vcn;
@@ -220,11 +225,11 @@ hipError_t tq_encode_ctx_launch(const float* x, int ctx, int hkv, const float* s
                                 const float* b4, const float* b3, uint8_t* c4, uint8_t* c3,
                                 uint16_t* norms, const int32_t* block_table, int max_blocks,
                                 int b, hipStream_t st, int p0 = 0);
-// Context fill of Cool pages: positions [0, n) of x [.][hkv][128] of
+// Context fill of Cool pages: positions [p0, n) of x [.][hkv][128] of
 // sequence b encoded TurboQuant, decoded and encoded Cool (48-byte codes,
 // fp16 norms) into the pages of cool_table.
-hipError_t cool_encode_ctx_launch(const float* x, int n, int hkv, const float* signs, uint8_t* cc, uint16_t* cn,
-                                  const int32_t* cool_table, int max_blocks, int b, hipStream_t st);
+hipError_t cool_encode_ctx_launch(const float* x, int p0, int n, int hkv, const float* signs, uint8_t* cc,
+                                  uint16_t* cn, const int32_t* cool_table, int max_blocks, int b, hipStream_t st);
 // Append one token per sequence from kv_tmp [batch][2][hkv*128].
 // Encode the K and V rows [n][2][hkv*128] of positions p0 .. p0 + n - 1 of
 // one sequence (block table bt of that sequence) into its pages.

@@ -95,6 +95,9 @@ struct nx_model {
     // permutation of the pool, max_blocks per sequence)
     int warm_pages = 0;
     int32_t* cool_bt = nullptr;
+    // with a Cool window (cool_window > 0), cool_bt is the Cool range's ring of
+    // cool_pages pages per sequence and older pages are evicted
+    int cool_pages = 0;
     unsigned* attn_counts = nullptr;  // split-completion counters of the fp16 attention
     int32_t* h_stage = nullptr;  // pinned host staging [batch]
     int32_t* h_out = nullptr;    // pinned host [batch][out_stride]
@@ -315,6 +318,7 @@ hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
     at.hot_window = c.hot_window;
     at.hot_table = m->hot_bt;
     at.warm_window = c.warm_window;
+    at.cool_window = c.cool_window;
     at.cool_table = m->cool_bt;
     at.kcc = ly.kcc;
     at.vcc = ly.vcc;
@@ -324,29 +328,33 @@ hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
 }
 
 // Tier boundaries of a sequence whose next attention covers ctx positions:
-// [0, cool) Cool, [cool, cold) TurboQuant, [cold, ctx) fp16.
-void tier_bounds(const nx_model_config& c, int ctx, int& cool, int& cold) {
+// [0, evict) evicted, [evict, cool) Cool, [cool, cold) TurboQuant, [cold,
+// ctx) fp16.
+void tier_bounds(const nx_model_config& c, int ctx, int& cool, int& cold, int& evict) {
+    evict = 0;
     if (c.kv_kind != 2) {
         cool = 0;
         cold = c.kv_kind == 1 ? ctx : 0;
         return;
     }
-    cold = nx::kPage * std::max(0, (ctx - 1 - c.hot_window) / nx::kPage);
-    cool = c.warm_window > 0 ? nx::kPage * std::max(0, (ctx - 1 - c.hot_window - c.warm_window) / nx::kPage) : 0;
+    auto edge = [&](int w) { return nx::kPage * std::max(0, (ctx - 1 - w) / nx::kPage); };
+    cold = edge(c.hot_window);
+    cool = c.warm_window > 0 ? edge(c.hot_window + c.warm_window) : 0;
+    if (c.warm_window > 0 && c.cool_window > 0) evict = edge(c.hot_window + c.warm_window + c.cool_window);
 }
 
 // KV bytes one attention pass reads for sequences at hpos (TurboQuant: 58
 // bytes per vector, Cool 50; tiered: Cool, then TurboQuant before the
-// window, fp16 in it).
+// window, fp16 in it; evicted positions are read from no memory).
 double kv_bytes(const nx_model* m) {
     const nx_model_config& c = m->c;
     const double f16 = 2.0 * c.n_kv_heads * c.head_dim * 2, tq = 2.0 * c.n_kv_heads * 58, cl = 2.0 * c.n_kv_heads * 50;
     double kv = 0.0;
     for (int b = 0; b < c.batch; ++b) {
         const int ctx = m->hpos[b] + 1;
-        int cool = 0, cold = 0;
-        tier_bounds(c, ctx, cool, cold);  // the attention's boundaries
-        kv += cool * cl + (cold - cool) * tq + (ctx - cold) * f16;
+        int cool = 0, cold = 0, evict = 0;
+        tier_bounds(c, ctx, cool, cold, evict);  // the attention's boundaries
+        kv += (cool - evict) * cl + (cold - cool) * tq + (ctx - cold) * f16;
     }
     return kv;
 }
@@ -602,6 +610,7 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     m->n_blocks = m->max_blocks * B;
     m->hot_pages = c.kv_kind == 2 ? c.hot_window / nx::kPage + 1 : 0;
     m->warm_pages = c.kv_kind == 2 && c.warm_window > 0 ? c.warm_window / nx::kPage + 1 : 0;
+    m->cool_pages = m->warm_pages > 0 && c.cool_window > 0 ? c.cool_window / nx::kPage + 1 : 0;
     m->out_stride = c.max_seq;
     m->layers.resize(L);
     m->hpos.assign(B, -1);
@@ -654,10 +663,13 @@ nx_status create_impl(nx_model* m, bool synthetic) {
             NX_TRY(dalloc(m, &ly.vn, tq_vecs));
         }
         if (m->warm_pages > 0) {
-            NX_TRY(dalloc(m, &ly.kcc, pool_vecs * 48));
-            NX_TRY(dalloc(m, &ly.vcc, pool_vecs * 48));
-            NX_TRY(dalloc(m, &ly.kcn, pool_vecs));
-            NX_TRY(dalloc(m, &ly.vcn, pool_vecs));
+            // with a Cool window the Cool pool holds only the Cool ring
+            const size_t cool_vecs =
+                m->cool_pages > 0 ? (size_t)B * m->cool_pages * c.n_kv_heads * nx::kPage : pool_vecs;
+            NX_TRY(dalloc(m, &ly.kcc, cool_vecs * 48));
+            NX_TRY(dalloc(m, &ly.vcc, cool_vecs * 48));
+            NX_TRY(dalloc(m, &ly.kcn, cool_vecs));
+            NX_TRY(dalloc(m, &ly.vcn, cool_vecs));
         }
         NX_TRY(dalloc(m, &ly.ksign, 128));
         NX_TRY(dalloc(m, &ly.vsign, 128));
@@ -693,8 +705,13 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         std::vector<int32_t> perm;
         host_shuffle(perm, m->n_blocks, c.seed, nx::kTidShuffle);
         if (m->warm_pages > 0) {
-            NX_TRY(dalloc(m, &m->cool_bt, perm.size()));
-            NX_HIP(m->ctx, hipMemcpyAsync(m->cool_bt, perm.data(), perm.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
+            std::vector<int32_t> cool = perm;
+            if (m->cool_pages > 0)
+                for (int b = 0; b < B; ++b)
+                    for (int p = 0; p < m->max_blocks; ++p)
+                        cool[(size_t)b * m->max_blocks + p] = b * m->cool_pages + p % m->cool_pages;
+            NX_TRY(dalloc(m, &m->cool_bt, cool.size()));
+            NX_HIP(m->ctx, hipMemcpyAsync(m->cool_bt, cool.data(), cool.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
             NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
             for (int b = 0; b < B; ++b)
                 for (int p = 0; p < m->max_blocks; ++p)
@@ -782,6 +799,8 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
         return fail(ctx, NX_ERR_INVALID, "hot_window must be a positive multiple of 16 below max_seq");
     if (c.warm_window < 0 || c.warm_window % nx::kPage || (c.warm_window > 0 && c.kv_kind != 2))
         return fail(ctx, NX_ERR_INVALID, "warm_window must be 0 or (tiered pages) a positive multiple of 16");
+    if (c.cool_window < 0 || c.cool_window % nx::kPage || (c.cool_window > 0 && c.warm_window == 0))
+        return fail(ctx, NX_ERR_INVALID, "cool_window must be 0 or (with a warm_window) a positive multiple of 16");
     if (c.kv_kind == 2 && c.max_seq > nx::attn_max_ctx() / 2)
         return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the tiered attention limit");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
@@ -1160,8 +1179,8 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
     NX_TRY(dalloc(m, &och, (size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1)));
     float* raw = nullptr;
     if (c.kv_kind != 0) NX_TRY(dalloc(m, &raw, (size_t)ctx_len * hkv * hd));
-    int cool = 0, cold = 0;
-    tier_bounds(c, ctx_len + 1, cool, cold);  // the boundaries of the first decode step
+    int cool = 0, cold = 0, evict = 0;
+    tier_bounds(c, ctx_len + 1, cool, cold, evict);  // the boundaries of the first decode step
     std::vector<int32_t> ho((size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
@@ -1177,15 +1196,15 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
                                                 c.seed, k1, och, n_outlier, st));
         } else {
             // tiered: the values rounded to fp16 (what the window holds), the
-            // pages before cool encoded Cool, those in [cool, cold) encoded,
-            // the rest into the window's ring
+            // pages in [evict, cool) encoded Cool, those in [cool, cold)
+            // encoded, the rest into the window's ring
             for (int b = 0; b < B; ++b)
                 for (int kv = 0; kv < 2; ++kv) {
                     NX_LAUNCH(m, nx::gen_ctx_raw_launch(raw, ctx_len, hkv, hd, L, b, kv, c.seed, k1,
                                                         och + (size_t)kv * hkv * n_outlier, n_outlier, st));
                     if (c.kv_kind == 2) NX_LAUNCH(m, nx::round_f16_launch(raw, (size_t)ctx_len * hkv * hd, st));
-                    if (cool > 0)
-                        NX_LAUNCH(m, nx::cool_encode_ctx_launch(raw, cool, hkv, kv ? ly.vsign : ly.ksign,
+                    if (cool > evict)
+                        NX_LAUNCH(m, nx::cool_encode_ctx_launch(raw, evict, cool, hkv, kv ? ly.vsign : ly.ksign,
                                                                 kv ? ly.vcc : ly.kcc, kv ? ly.vcn : ly.kcn, m->cool_bt,
                                                                 m->max_blocks, b, st));
                     if (cold > cool)
@@ -1232,9 +1251,10 @@ nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* 
         pos > m->hpos[(size_t)b])
         return fail(m->ctx, NX_ERR_INVALID, "nx_model_kv_read: no such position");
     const int hkv = c.n_kv_heads, hd = c.head_dim, page = pos / nx::kPage, slot = pos % nx::kPage;
-    int cool = 0, cold = 0;
-    tier_bounds(c, m->hpos[(size_t)b] + 2, cool, cold);  // the boundaries of the next decode step
-    *form = pos < cool ? 2 : pos < cold ? 1 : 0;
+    int cool = 0, cold = 0, evict = 0;
+    tier_bounds(c, m->hpos[(size_t)b] + 2, cool, cold, evict);  // the boundaries of the next decode step
+    *form = pos < evict ? 3 : pos < cool ? 2 : pos < cold ? 1 : 0;
+    if (*form == 3) return NX_OK;  // evicted: nothing stored
     const size_t need = *form == 2 ? (size_t)50 * hkv : *form ? (size_t)58 * hkv : (size_t)2 * hkv * hd;
     if (cap < need) return fail(m->ctx, NX_ERR_INVALID, "nx_model_kv_read: %zu bytes needed", need);
     const Layer& ly = m->layers[layer];

@@ -43,7 +43,7 @@ class ModelConfig(C.Structure):
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
-        ("warm_window", C.c_int),
+        ("warm_window", C.c_int), ("cool_window", C.c_int),
     ]
 
 
@@ -313,14 +313,14 @@ class Model:
 
     @classmethod
     def load_nxf(cls, ctx: Context, path, batch=1, max_seq=128, kv_kind=0, seed=0x5EED,
-                 hot_window=0, warm_window=0) -> "Model":
+                 hot_window=0, warm_window=0, cool_window=0) -> "Model":
         """A model from an NXF file (nx_model_load_nxf): dimensions from the
         file, every chunk verified on the GPU; batch, max_seq, kv_kind,
-        hot_window, warm_window and seed are the caller's."""
+        hot_window, warm_window, cool_window and seed are the caller's."""
         self = cls.__new__(cls)
         self.ctx = ctx
         run = ModelConfig(batch=batch, max_seq=max_seq, kv_kind=kv_kind, seed=seed, hot_window=hot_window,
-                          warm_window=warm_window)
+                          warm_window=warm_window, cool_window=cool_window)
         h = C.c_void_p()
         ctx.check(ctx.L.nx_model_load_nxf(ctx.h, str(path).encode(), C.byref(run), C.byref(h)),
                   "nx_model_load_nxf")
@@ -337,7 +337,7 @@ class Model:
             n_kv_heads=m.num_kv_heads, head_dim=m.head_dim, ffn=w1.shape[-1], vocab=m.vocab_size,
             n_experts=m.num_experts, top_k=m.num_active_experts, max_seq=max_seq, batch=batch,
             kv_kind=kv_kind, rope_theta=m.rope_theta, eps=m.rms_norm_eps, seed=seed,
-            hot_window=hot_window, warm_window=warm_window)
+            hot_window=hot_window, warm_window=warm_window, cool_window=cool_window)
         return self
 
     def save_nxf(self, path):
@@ -375,13 +375,14 @@ class Model:
 
     def kv_read(self, layer: int, b: int, pos: int, kv: int):
         """(form, stored bytes) of one position, all kv heads (nx_model_kv_read):
-        form 0 fp16, form 1 TurboQuant (58 bytes per head), form 2 Cool (50)."""
+        form 0 fp16, form 1 TurboQuant (58 bytes per head), form 2 Cool (50),
+        form 3 evicted (no bytes)."""
         cap = max(58, 2 * self.cfg.head_dim) * self.cfg.n_kv_heads
         out = np.zeros(cap, np.uint8)
         form = C.c_int()
         self.ctx.check(self.ctx.L.nx_model_kv_read(self.h, layer, b, pos, kv, C.byref(form), out.ctypes.data, cap),
                        "nx_model_kv_read")
-        n = {0: 2 * self.cfg.head_dim, 1: 58, 2: 50}[form.value] * self.cfg.n_kv_heads
+        n = {0: 2 * self.cfg.head_dim, 1: 58, 2: 50, 3: 0}[form.value] * self.cfg.n_kv_heads
         return form.value, out[:n]
 
     def pending(self) -> np.ndarray:

@@ -32,7 +32,7 @@ class Cfg(C.Structure):
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
-        ("warm_window", C.c_int),
+        ("warm_window", C.c_int), ("cool_window", C.c_int),
     ]
 
 
@@ -99,6 +99,11 @@ def _load() -> C.CDLL:
                                      C.c_int]),
         "nxo_tiered_cold": (C.c_int, [C.c_int, C.c_int]),
         "nxo_tiered_cool": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+        "nxo_tiered_evict": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
+        "nxo_attn_decode_tiered_evict": (None, [_f32p, _u16p, _u16p, _u8p, _u8p, _u16p, _u8p, _u8p, _u16p, _u8p,
+                                                _u16p, _u8p, _u16p, _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int,
+                                                _i32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                                _f32p]),
         "nxo_cool_encode": (None, [_f32p, C.c_int, _f32p, _f32p, _u8p, _u16p]),
         "nxo_cool_decode": (None, [_u8p, _u16p, C.c_int, _f32p, _f32p, _f32p]),
         "nxo_tq_to_cool": (None, [_u8p, _u8p, _u16p, C.c_int, _f32p, _f32p, _f32p, _f32p, _u8p, _u16p]),

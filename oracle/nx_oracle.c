@@ -632,6 +632,11 @@ int nxo_tiered_cool(int ctx, int hot_window, int warm_window) {
     return nxo_tiered_cold(ctx, hot_window + warm_window);
 }
 
+int nxo_tiered_evict(int ctx, int hot_window, int warm_window, int cool_window) {
+    if (warm_window <= 0 || cool_window <= 0) return 0;
+    return nxo_tiered_cold(ctx, hot_window + warm_window + cool_window);
+}
+
 void nxo_tiered_append_cool(int hkv, const float* ksigns, const float* vsigns, const float* c4, const float* c3,
                             const float* b3, const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn,
                             const uint8_t* vc4, const uint8_t* vc3, const uint16_t* vn, uint8_t* kcc,
@@ -653,6 +658,17 @@ void nxo_attn_decode_tiered_cool(const float* q, const uint16_t* kpool, const ui
                                  const uint16_t* vcn, const float* ksigns, const float* vsigns, const float* c4,
                                  const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
                                  int hot_window, int warm_window, int B, int hq, int hkv, float* out) {
+    nxo_attn_decode_tiered_evict(q, kpool, vpool, kc4, kc3, kn, vc4, vc3, vn, kcc, kcn, vcc, vcn, ksigns, vsigns, c4,
+                                 c3, block_table, max_blocks, ctx_lens, hot_window, warm_window, 0, B, hq, hkv, out);
+}
+
+void nxo_attn_decode_tiered_evict(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                                  const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                                  const uint16_t* vn, const uint8_t* kcc, const uint16_t* kcn, const uint8_t* vcc,
+                                  const uint16_t* vcn, const float* ksigns, const float* vsigns, const float* c4,
+                                  const float* c3, const int32_t* block_table, int max_blocks,
+                                  const int32_t* ctx_lens, int hot_window, int warm_window, int cool_window, int B,
+                                  int hq, int hkv, float* out) {
     const int hd = NXO_TQ_D;
     const int grp = hq / hkv;
 #pragma omp parallel for collapse(2) schedule(dynamic)
@@ -660,6 +676,7 @@ void nxo_attn_decode_tiered_cool(const float* q, const uint16_t* kpool, const ui
         for (int kvh = 0; kvh < hkv; ++kvh) {
             const int ctx = ctx_lens[b], cold = nxo_tiered_cold(ctx, hot_window);
             const int cool = nxo_tiered_cool(ctx, hot_window, warm_window);
+            const int evict = nxo_tiered_evict(ctx, hot_window, warm_window, cool_window);
             const int32_t* bt = block_table + (size_t)b * max_blocks;
             const size_t rows = (size_t)(ctx > 0 ? ctx : 1);
             float* K = (float*)malloc(sizeof(float) * rows * hd);
@@ -669,7 +686,10 @@ void nxo_attn_decode_tiered_cool(const float* q, const uint16_t* kpool, const ui
             gather_f16(vpool, bt, ctx, hkv, kvh, hd, 1, V);
             for (int t = 0; t < cold; ++t) {
                 const size_t vi = ((size_t)bt[t / NXO_PAGE] * hkv + kvh) * NXO_PAGE + t % NXO_PAGE;
-                if (t < cool) {
+                if (t < evict) {  /* evicted: the zero vectors get_vectors gathers */
+                    memset(K + (size_t)t * hd, 0, sizeof(float) * hd);
+                    memset(V + (size_t)t * hd, 0, sizeof(float) * hd);
+                } else if (t < cool) {
                     nxo_cool_decode(kcc + vi * NXO_COOL_CODES, kcn + vi, 1, ksigns, c3, K + (size_t)t * hd);
                     nxo_cool_decode(vcc + vi * NXO_COOL_CODES, vcn + vi, 1, vsigns, c3, V + (size_t)t * hd);
                 } else {
@@ -1048,10 +1068,10 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
             nxo_attn_decode_paged_f16(m->q, ly->kpool, ly->vpool, m->block_table, m->max_blocks,
                                       ctx, B, hq, hkv, hd, m->att);
         else if (c->kv_kind == 2)
-            nxo_attn_decode_tiered_cool(m->q, ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
-                                        ly->vn, ly->kcc, ly->kcn, ly->vcc, ly->vcn, ly->ksign, ly->vsign, m->c4,
-                                        m->c3, m->block_table, m->max_blocks, ctx, c->hot_window, c->warm_window,
-                                        B, hq, hkv, m->att);
+            nxo_attn_decode_tiered_evict(m->q, ly->kpool, ly->vpool, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3,
+                                         ly->vn, ly->kcc, ly->kcn, ly->vcc, ly->vcn, ly->ksign, ly->vsign, m->c4,
+                                         m->c3, m->block_table, m->max_blocks, ctx, c->hot_window, c->warm_window,
+                                         c->cool_window, B, hq, hkv, m->att);
         else
             nxo_attn_decode_paged_tq(m->q, ly->kc4, ly->kc3, ly->kn, ly->vc4, ly->vc3, ly->vn,
                                      ly->ksign, ly->vsign, m->c4, m->c3, m->block_table,

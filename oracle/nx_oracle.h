@@ -198,6 +198,13 @@ int nxo_tiered_cold(int ctx, int hot_window);
  * (pools [blocks][hkv][16][48] and [blocks][hkv][16] fp16 norms); the
  * attention reads t < cool Cool, cool <= t < cold Warm, the rest fp16. */
 int nxo_tiered_cool(int ctx, int hot_window, int warm_window);
+/* Cold (evicted) pages, after evict_cold_pages (kv/paged_attention.cpp:
+ * 295-310): with warm_window and cool_window > 0, pages wholly outside the
+ * last hot_window + warm_window + cool_window positions are dropped, and
+ * get_vectors gathers zero vectors for them (:172, :219), so attention
+ * scores them 0 with value 0 in its softmax.  evict = nxo_tiered_cold(ctx,
+ * hot_window + warm_window + cool_window), 0 when either window is 0. */
+int nxo_tiered_evict(int ctx, int hot_window, int warm_window, int cool_window);
 void nxo_tiered_append_cool(int hkv, const float* ksigns, const float* vsigns, const float* c4, const float* c3,
                             const float* b3, const uint8_t* kc4, const uint8_t* kc3, const uint16_t* kn,
                             const uint8_t* vc4, const uint8_t* vc3, const uint16_t* vn, uint8_t* kcc,
@@ -209,6 +216,14 @@ void nxo_attn_decode_tiered_cool(const float* q, const uint16_t* kpool, const ui
                                  const uint16_t* vcn, const float* ksigns, const float* vsigns, const float* c4,
                                  const float* c3, const int32_t* block_table, int max_blocks, const int32_t* ctx_lens,
                                  int hot_window, int warm_window, int B, int hq, int hkv, float* out);
+/* As above with positions t < evict (nxo_tiered_evict) read as zero K and V. */
+void nxo_attn_decode_tiered_evict(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
+                                  const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
+                                  const uint16_t* vn, const uint8_t* kcc, const uint16_t* kcn, const uint8_t* vcc,
+                                  const uint16_t* vcn, const float* ksigns, const float* vsigns, const float* c4,
+                                  const float* c3, const int32_t* block_table, int max_blocks,
+                                  const int32_t* ctx_lens, int hot_window, int warm_window, int cool_window, int B,
+                                  int hq, int hkv, float* out);
 void nxo_attn_decode_tiered(const float* q, const uint16_t* kpool, const uint16_t* vpool, const uint8_t* kc4,
                             const uint8_t* kc3, const uint16_t* kn, const uint8_t* vc4, const uint8_t* vc3,
                             const uint16_t* vn, const float* ksigns, const float* vsigns, const float* c4,
@@ -244,6 +259,8 @@ typedef struct {
     int hot_window;                /* kv_kind 2: tokens kept fp16, a multiple of 16 */
     int warm_window;               /* kv_kind 2: 0 = two tiers; else the positions before the
                                       fp16 window kept Warm (a multiple of 16), older pages Cool */
+    int cool_window;               /* kv_kind 2 with warm_window: 0 = keep every Cool page; else
+                                      the positions kept Cool (a multiple of 16), older pages evicted */
 } nxo_cfg;
 
 typedef struct nxo_model nxo_model;

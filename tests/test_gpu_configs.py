@@ -169,6 +169,27 @@ def test_8b_three_tier_32k_one_layer(ctx):
     _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tie=TQ_TIE, check_pages=pages)
 
 
+def test_8b_evicting_tiers_32k_one_layer(ctx):
+    """One 8B-shaped layer at 32760 positions: last 4096 fp16, 4096
+    TurboQuant, 8192 Cool in a ring of 513 pages, older pages evicted (16368
+    positions read as zero keys and values).  At the 8th step page 1535
+    moves to the Cool ring (bit-exact) and page 1023 is evicted."""
+    cfg = dict(LLAMA8B, n_layers=1, kv_kind=2, hot_window=4096, warm_window=4096, cool_window=8192,
+               max_seq=32768 + 256, seed=0xE78E)
+    ctx_len, steps = 32760, 10
+
+    def pages(gm, om):
+        for p in (0, 9999, 1023 * 16, 1023 * 16 + 15):
+            form, g = gm.kv_read(0, 0, p, 0)
+            assert form == 3 and g.size == 0, p
+        for p in list(range(1535 * 16, 1536 * 16)) + [1024 * 16, 20000]:
+            for kv in range(2):
+                form, g = gm.kv_read(0, 0, p, kv)
+                assert form == 2 and np.array_equal(g, om.kv_read(0, 0, p, kv, 2)), (p, kv)
+
+    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+
+
 def test_three_tier_pipelined_batch8(ctx):
     """Batch 8, 8 kv heads, 4608 positions of capacity, a 512-position
     window and a 512-position Warm range: the split plan pipelines the Cool,

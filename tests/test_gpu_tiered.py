@@ -249,3 +249,59 @@ def test_three_tier_config_rejected(ctx):
     for kind in (0, 1):
         with pytest.raises(RuntimeError):
             nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=kind, warm_window=32))
+
+
+# ----------------------------------------------------------- Cold eviction --
+@pytest.mark.parametrize("batch,H,W,C", [(1, 16, 16, 32), (2, 32, 16, 16)])
+def test_evicting_tiers_greedy_parity(ctx, batch, H, W, C):
+    """A 12-token prompt and 100 greedy tokens with a Cool window: from
+    position H + W + C + 15 on, pages leave the Cool range and are evicted
+    (read as zero keys and values, as get_vectors gathers a page it no longer
+    holds); the Cool pages live in a ring of C / 16 + 1 pages."""
+    cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, warm_window=W, cool_window=C,
+               seed=0xE71 + H + W + C)
+    got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
+    assert_greedy_parity(got, want, margins, tie=TQ_TIE)
+
+
+def test_evicting_tiers_filled_context(ctx):
+    """300 filled positions, window 64, Warm 32, Cool 64: the fill evicts
+    pages 0..7 and writes 8..11 Cool (into the ring), 12..13 TurboQuant;
+    40 decode steps evict pages 8..10 and move 12..14 to the Cool ring.
+    Stored pages stay bit-exact against the oracle, tokens agree."""
+    cfg = dict(TQ_TINY, batch=2, max_seq=512, kv_kind=2, hot_window=64, warm_window=32, cool_window=64,
+               seed=0xE72)
+    ctx_len, steps = 300, 40
+    gm = nexus_amd.Model(ctx, **cfg)
+    gm.fill_context(ctx_len, 4)
+    om = oracle.Model(**cfg)
+    om.fill_context(ctx_len, 4)
+    n_layers = cfg["n_layers"]
+
+    def evicted(positions):
+        for b in range(2):
+            for p in positions:
+                form, got = gm.kv_read(n_layers - 1, b, p, 0)
+                assert form == 3 and got.size == 0, (b, p, form)
+
+    evicted(range(0, 128, 9))
+    _check_forms(gm, om, n_layers, 2, [(range(128, 192, 3), 2), (range(192, 224, 3), 1), (range(224, 300, 4), 0)])
+    start = gm.pending()
+    got = gm.decode(steps)
+    glog = gm.logits()
+    evicted([0, 127, 128, 175])
+    _check_forms(gm, om, n_layers, 2, [(range(176, 240), 2), (range(240, 272), 1), (range(272, 300), 0)])
+    gm.close()
+    want, margins, logits = _oracle_steps(om, start, steps)
+    om.close()
+    assert_greedy_parity(got, want, margins)
+    if np.array_equal(got, want):
+        assert rel_err(glog, logits) < 1e-3
+
+
+def test_evicting_tiers_config_rejected(ctx):
+    for C in (-16, 8):
+        with pytest.raises(RuntimeError):
+            nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=2, hot_window=32, warm_window=16, cool_window=C))
+    with pytest.raises(RuntimeError):  # a Cool window needs a Warm range
+        nexus_amd.Model(ctx, **dict(TQ_TINY, kv_kind=2, hot_window=32, cool_window=32))

@@ -647,6 +647,63 @@ def test_tiered_cool_attention_vs_fp64(ctx, H, W):
         assert rel_err(want_for(cool + 16, cold), want) > 1e-3
 
 
+def test_tiered_evict_boundary():
+    """evict = 16 floor((ctx - 1 - H - W - C) / 16) clamped at 0; nothing is
+    evicted without a Warm range or with C = 0."""
+    for ctx, H, W, C, want in [(49, 16, 16, 16, 0), (65, 16, 16, 16, 16), (300, 64, 32, 64, 128),
+                               (32769, 4096, 4096, 8192, 16384), (5000, 16, 0, 16, 0), (5000, 16, 16, 0, 0)]:
+        assert L.nxo_tiered_evict(ctx, H, W, C) == want, (ctx, H, W, C)
+        assert L.nxo_tiered_evict(ctx, H, W, C) <= L.nxo_tiered_cool(ctx, H, W)
+
+
+@pytest.mark.parametrize("ctx,H,W,C", [(130, 16, 16, 32), (100, 32, 16, 16)])
+def test_tiered_evict_attention_vs_fp64(ctx, H, W, C):
+    """Evicted positions read as zero vectors (get_vectors zero-fills a
+    page it does not find): against an fp64 restatement in which positions
+    before evict have zero K and V -- they still take softmax weight
+    exp(0 - max) each.  Dropping them from the softmax instead (the planted
+    mistake) moves the result past the bound."""
+    rng = np.random.default_rng(ctx + 7 * H + W + C)
+    hq, hkv, B = 4, 1, 1
+    K = rng.normal(0, 1, (B, ctx, hkv, 128)).astype(np.float32)
+    V = rng.normal(0, 1, (B, ctx, hkv, 128)).astype(np.float32)
+    q = rng.normal(0, 0.4, (B, hq, 128)).astype(np.float32)
+    ks, vs = oracle.tq_signs(5, 1), oracle.tq_signs(5, 2)
+    c4, b4 = oracle.codebook(4)
+    c3, b3 = oracle.codebook(3)
+    max_blocks = (ctx + 15) // 16 + 1
+    bt = np.arange(max_blocks, dtype=np.int32).reshape(1, max_blocks)
+    nv = max_blocks * hkv * 16
+    kp, vp = np.zeros(nv * 128, np.uint16), np.zeros(nv * 128, np.uint16)
+    kc4, kc3, kn = np.zeros((nv, 32), np.uint8), np.zeros((nv, 24), np.uint8), np.zeros(nv, np.uint16)
+    vc4, vc3, vn = np.zeros_like(kc4), np.zeros_like(kc3), np.zeros_like(kn)
+    kcc, kcn = np.zeros((nv, 48), np.uint8), np.zeros(nv, np.uint16)
+    vcc, vcn = np.zeros_like(kcc), np.zeros_like(kcn)
+    for p in range(ctx):
+        L.nxo_tiered_append(np.ascontiguousarray(K[0, p]), np.ascontiguousarray(V[0, p]), hkv, ks, vs, b4, b3, kp,
+                            vp, kc4, kc3, kn, vc4, vc3, vn, bt, max_blocks, 0, p)
+        L.nxo_tiered_append_cool(hkv, ks, vs, c4, c3, b3, kc4, kc3, kn, vc4, vc3, vn, kcc, kcn, vcc, vcn, bt,
+                                 max_blocks, 0, p)
+    out = np.empty_like(q)
+    L.nxo_attn_decode_tiered_evict(q, kp, vp, kc4, kc3, kn, vc4, vc3, vn, kcc, kcn, vcc, vcn, ks, vs, c4, c3, bt,
+                                   max_blocks, np.full(B, ctx, np.int32), H, W, C, B, hq, hkv, out)
+    ev = L.nxo_tiered_evict(ctx, H, W, C)
+    cool, cold = L.nxo_tiered_cool(ctx, H, W), L.nxo_tiered_cold(ctx, H)
+    assert 0 < ev < cool < cold
+    Kf = K[0].astype(np.float16).astype(np.float64)
+    Vf = V[0].astype(np.float16).astype(np.float64)
+    for X, Xf, s in ((K[0], Kf, ks), (V[0], Vf, vs)):
+        warm = oracle.tq_encode(X[:cold, 0].astype(np.float16).astype(np.float32), s)[:3]
+        Xf[:cold, 0] = oracle.tq_decode(*warm, s)
+        cc, cn = oracle.tq_to_cool(warm[0][:cool], warm[1][:cool], warm[2][:cool], s)
+        Xf[:cool, 0] = oracle.cool_decode(cc, cn, s)
+        Xf[:ev] = 0.0
+    want = _attn_fp64(q[0].astype(np.float64), Kf, Vf, hq, hkv, 128)
+    assert rel_err(out[0], want) < 1e-5
+    dropped = _attn_fp64(q[0].astype(np.float64), Kf[ev:], Vf[ev:], hq, hkv, 128)
+    assert rel_err(dropped, want) > 1e-3
+
+
 # -------------------------------------------------------------------- MoE --
 def test_moe_route_golden():
     g = gold("moe_route.npz")
