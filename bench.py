@@ -277,16 +277,23 @@ def nxf_verify_bench(ctx, cpu: bool, nbytes: int = 4 << 30, chunk: int = 64 << 1
 PEAK_MFMA_TFLOPS = 2500.0  # dense fp16 matrix-core peak
 
 
-def tiering_bench(ctx, base: dict, ctx_len: int = 32768, hot_window: int = 4096, steps: int = 64) -> dict:
+def tiering_bench(ctx, base: dict, ctx_len: int = 32768, hot_window: int = 4096, steps: int = 64,
+                  warm_window: int = 4096, cool_window: int = 8192) -> dict:
     """One layer of the model's shape at a long context, with fp16,
-    TurboQuant and tiered pages: the attention pass (KV bytes it reads, its
-    time) and the time of a one-layer decode step (for tiered pages it
-    includes the device compressor, which encodes a page every 16 steps)."""
+    TurboQuant and tiered pages (two tiers; three: Warm range warm_window;
+    evicting: also a Cool window, older pages evicted): the attention pass
+    (KV bytes it reads, its time), the time of a one-layer decode step (for
+    tiered pages it includes the device compressors, which encode a page
+    every 16 steps) and the KV bytes one layer holds for the sequence at the
+    end (resident_bytes: pages that hold data, by tier)."""
     import nexus_amd
-    out = {"ctx": ctx_len, "hot_window": hot_window}
-    for name, kind in (("fp16", 0), ("tq", 1), ("tiered", 2)):
+    out = {"ctx": ctx_len, "hot_window": hot_window, "warm_window": warm_window, "cool_window": cool_window}
+    hkv = base["n_kv_heads"]
+    per = {"f16": 2 * hkv * base["head_dim"] * 2, "tq": 2 * hkv * 58, "cool": 2 * hkv * 50}
+    for name, kind, W, C in (("fp16", 0, 0, 0), ("tq", 1, 0, 0), ("tiered", 2, 0, 0), ("three_tier", 2, warm_window, 0),
+                             ("evicting", 2, warm_window, cool_window)):
         cfg = dict(base, n_layers=1, vocab=1024, batch=1, kv_kind=kind, max_seq=ctx_len + 16 * (steps // 16 + 2),
-                   hot_window=hot_window if kind == 2 else 0)
+                   hot_window=hot_window if kind == 2 else 0, warm_window=W, cool_window=C)
         m = nexus_amd.Model(ctx, **cfg)
         m.fill_context(ctx_len, 4 if kind else 0)
         m.decode_untimed(2)
@@ -298,8 +305,19 @@ def tiering_bench(ctx, base: dict, ctx_len: int = 32768, hot_window: int = 4096,
         ms, nb = m.time_attention(200)
         m.close()
         gbs = nb / (ms * 1e-3) / 1e9
+        n = ctx_len + 2 + steps  # positions held after the run
+        if kind == 0:
+            res = n * per["f16"]
+        elif kind == 1:
+            res = n * per["tq"]
+        else:
+            cold = 16 * max(0, (n - hot_window) // 16)
+            cool = 16 * max(0, (n - hot_window - W) // 16) if W else 0
+            evict = 16 * max(0, (n - hot_window - W - C) // 16) if C else 0
+            res = (n - cold) * per["f16"] + (cold - cool) * per["tq"] + (cool - evict) * per["cool"]
         out[name] = {"attention_us": round(ms * 1e3, 2), "kv_bytes": int(nb), "GBps": round(gbs, 1),
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "step_ms_1layer": round(step_ms, 4)}
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "step_ms_1layer": round(step_ms, 4),
+                     "resident_bytes": int(res)}
     out["kv_bytes_vs_fp16"] = round(out["tiered"]["kv_bytes"] / out["fp16"]["kv_bytes"], 4)
     return out
 

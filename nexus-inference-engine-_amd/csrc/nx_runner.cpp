@@ -1181,6 +1181,7 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
     if (c.kv_kind != 0) NX_TRY(dalloc(m, &raw, (size_t)ctx_len * hkv * hd));
     int cool = 0, cold = 0, evict = 0;
     tier_bounds(c, ctx_len + 1, cool, cold, evict);  // the boundaries of the first decode step
+    cold = std::min(cold, ctx_len);  // TurboQuant pages: every filled position (raw holds ctx_len rows)
     std::vector<int32_t> ho((size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
