@@ -446,6 +446,64 @@ def test_tq_attention_close_to_fp16_attention():
     assert rel_err(out[0], want) < 0.25
 
 
+def _tq_decode_fp64(k4, k3, nr, signs):
+    """Independent float64 decode: unpack LSB-first with numpy, codebook
+    values, scipy's Hadamard matrix, x = n * D * H c / sqrt(128)."""
+    from scipy.linalg import hadamard
+    c4, _ = oracle.codebook(4)
+    c3, _ = oracle.codebook(3)
+    b4 = np.unpackbits(k4, axis=1, bitorder="little").reshape(-1, 64, 4)
+    q4 = b4[..., 0] | (b4[..., 1] << 1) | (b4[..., 2] << 2) | (b4[..., 3] << 3)
+    b3 = np.unpackbits(k3, axis=1, bitorder="little").reshape(-1, 64, 3)
+    q3 = b3[..., 0] | (b3[..., 1] << 1) | (b3[..., 2] << 2)
+    cv = np.concatenate([c4[q4], c3[q3]], axis=1).astype(np.float64)
+    H = hadamard(128).astype(np.float64) / np.sqrt(128)
+    n = oracle.f16_to_f32(nr).astype(np.float64)
+    return (cv @ H) * signs.astype(np.float64) * n[:, None]
+
+
+def test_tq_paged_attention_vs_fp64_decode():
+    """nxo_attn_decode_paged_tq as a whole: two kv heads, two sequences of
+    ragged length, a shuffled block table; against float64 attention over
+    an independent float64 decode of the stored codes, within 1e-5.  Reading
+    V with the K signs (the planted mistake) moves the restatement far past
+    the bound."""
+    rng = np.random.default_rng(31)
+    hq, hkv, B = 8, 2, 2
+    lens = [45, 70]
+    max_blocks = 5
+    bt = rng.permutation(B * max_blocks).astype(np.int32).reshape(B, max_blocks)
+    ks, vs = oracle.tq_signs(6, 1), oracle.tq_signs(6, 2)
+    c4, b4 = oracle.codebook(4)
+    c3, b3 = oracle.codebook(3)
+    nv = B * max_blocks * hkv * 16
+    kc4, kc3, kn = np.zeros((nv, 32), np.uint8), np.zeros((nv, 24), np.uint8), np.zeros(nv, np.uint16)
+    vc4, vc3, vn = np.zeros_like(kc4), np.zeros_like(kc3), np.zeros_like(kn)
+    Ks = [rng.normal(0, 1, (n, hkv, 128)).astype(np.float32) for n in lens]
+    Vs = [rng.normal(0, 1, (n, hkv, 128)).astype(np.float32) for n in lens]
+    for b in range(B):
+        for p in range(lens[b]):
+            L.nxo_tq_append(np.ascontiguousarray(Ks[b][p]), np.ascontiguousarray(Vs[b][p]), hkv, ks, vs, b4, b3,
+                            kc4, kc3, kn, vc4, vc3, vn, bt, max_blocks, b, p)
+    q = rng.normal(0, 0.5, (B, hq, 128)).astype(np.float32)
+    out = np.empty_like(q)
+    L.nxo_attn_decode_paged_tq(q, kc4, kc3, kn, vc4, vc3, vn, ks, vs, c4, c3, bt, max_blocks,
+                               np.array(lens, np.int32), B, hq, hkv, out)
+
+    def want_for(vsign):
+        res = []
+        for b in range(B):
+            idx = np.array([[(bt[b, p // 16] * hkv + h) * 16 + p % 16 for h in range(hkv)] for p in range(lens[b])])
+            K = _tq_decode_fp64(kc4[idx.ravel()], kc3[idx.ravel()], kn[idx.ravel()], ks).reshape(lens[b], hkv, 128)
+            V = _tq_decode_fp64(vc4[idx.ravel()], vc3[idx.ravel()], vn[idx.ravel()], vsign).reshape(lens[b], hkv, 128)
+            res.append(_attn_fp64(q[b].astype(np.float64), K, V, hq, hkv, 128))
+        return np.stack(res)
+
+    want = want_for(vs)
+    assert rel_err(out, want) < 1e-5
+    assert rel_err(want_for(ks), want) > 1e-2
+
+
 def test_tiered_cold_boundary():
     """Attention over ctx positions reads as compressed the pages wholly
     before the window of the H positions preceding the current one:
