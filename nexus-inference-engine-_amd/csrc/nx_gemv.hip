@@ -721,6 +721,70 @@ __global__ __launch_bounds__(256) void k_gemv_ksum(const float* __restrict__ par
     else y16[(size_t)b * ldy + n] = f2h_bits(s);
 }
 
+// The same sum, then (post_x16) the RMSNorm of each finished row: one block
+// of kNormRowThreads per batch row, 16-byte chunks (N % 4 == 0, N <=
+// 4 * kNormRowThreads * kNormRowChunks), every element summed exactly as
+// k_gemv_ksum sums it.
+constexpr int kNormRowThreads = 1024, kNormRowChunks = 4;
+template <int EPI>
+__global__ __launch_bounds__(kNormRowThreads) void k_gemv_ksum_norm(const float* __restrict__ part, int kparts,
+                                                                     int B, int N, float* y32, const float* w,
+                                                                     uint16_t* x16, float eps) {
+    __shared__ float red[kNormRowThreads / 64];
+    const int b = blockIdx.x, t = threadIdx.x, nc = N / 4;
+    float4 v[kNormRowChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNormRowChunks; ++j) {
+        const int c = t + j * kNormRowThreads;
+        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c >= nc) continue;
+        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < kparts; ++q) {
+            const float4 p = reinterpret_cast<const float4*>(part + ((size_t)q * B + b) * N)[c];
+            s.x += p.x;
+            s.y += p.y;
+            s.z += p.z;
+            s.w += p.w;
+        }
+        float4* yp = reinterpret_cast<float4*>(y32 + (size_t)b * N) + c;
+        if (EPI == E_ACC) {
+            const float4 y = *yp;
+            s.x = y.x + s.x;
+            s.y = y.y + s.y;
+            s.z = y.z + s.z;
+            s.w = y.w + s.w;
+        }
+        *yp = s;
+        v[j] = s;
+        ss += s.x * s.x + s.y * s.y + s.z * s.z + s.w * s.w;
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormRowThreads / 64; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)N + eps);
+    uint2* ob = reinterpret_cast<uint2*>(x16 + (size_t)b * N);
+#pragma unroll
+    for (int j = 0; j < kNormRowChunks; ++j) {
+        const int c = t + j * kNormRowThreads;
+        if (c >= nc) break;
+        const float4 wv = w ? reinterpret_cast<const float4*>(w)[c] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const uint32_t lo = (uint32_t)f2h_bits(v[j].x * inv * wv.x) | ((uint32_t)f2h_bits(v[j].y * inv * wv.y) << 16);
+        const uint32_t hi = (uint32_t)f2h_bits(v[j].z * inv * wv.z) | ((uint32_t)f2h_bits(v[j].w * inv * wv.w) << 16);
+        ob[c] = make_uint2(lo, hi);
+    }
+}
+
+// RMSNorm of the rows a GEMV just wrote (post_x16), where its launch did not.
+hipError_t post_norm_launch(const GemvArgs& a, hipStream_t st) {
+    if (!a.post_x16) return hipSuccess;
+    if (a.ldy != a.N || !a.y32) return hipErrorInvalidValue;
+    return rmsnorm_launch(a.y32, a.post_norm_w, a.post_x16, a.N, a.post_eps, a.batch, st);
+}
+
 // Batch 2..8 on the matrix cores.  One stage (K <= 4096): ks wavefronts per
 // tile, the fewest that still give every wavefront of one block per CU a
 // tile, and enough tiles per block for one round of blocks.  Longer K with
@@ -751,10 +815,21 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
                                dim3(kMfmaThreads), 0, st, p, rg, ksp);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess || MOE) return e;
+            if constexpr (EPI == E_ACC || EPI == E_F32) {
+                const bool vec = a.N % 4 == 0 && a.N <= 4 * kNormRowThreads * kNormRowChunks && a.ldy == a.N &&
+                                 ((reinterpret_cast<uintptr_t>(a.y32) | reinterpret_cast<uintptr_t>(a.post_norm_w) |
+                                   reinterpret_cast<uintptr_t>(a.post_x16)) & 15u) == 0;
+                if (a.post_x16 && vec) {
+                    hipLaunchKernelGGL((k_gemv_ksum_norm<EPI>), dim3(a.batch), dim3(kNormRowThreads), 0, st,
+                                       a.kpart, kp, a.batch, a.N, a.y32, a.post_norm_w, a.post_x16, a.post_eps);
+                    return hipGetLastError();
+                }
+            }
             const int n = a.batch * a.N;
             hipLaunchKernelGGL((k_gemv_ksum<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, a.kpart, kp, a.batch,
                                a.N, a.y32, a.y16, a.ldy);
-            return hipGetLastError();
+            const hipError_t e2 = hipGetLastError();
+            return e2 != hipSuccess ? e2 : post_norm_launch(a, st);
         }
     }
     const bool xg = XS == X_F16 && a.K > kMfmaKC && a.K % 32 == 0 && xvec && salign;
@@ -776,7 +851,8 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
     else if (salign) NX_MFMA(false, true, false);
     else NX_MFMA(false, false, false);
 #undef NX_MFMA
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess || MOE ? e : post_norm_launch(a, st);
 }
 
 // Tile shapes per groups-per-lane (K <= 64 * 32 * GPL), chosen by measuring
@@ -786,20 +862,29 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
 // rows in a ring of 3 otherwise.  K = 14336 without paired rows: one row per
 // tile with x in registers.  Paired epilogues at GPL >= 4 keep x in LDS.
 template <int XS, int EPI>
-hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
+hipError_t launch_b1_gpl(const GemvArgs& a, hipStream_t st) {
     const int gpl = (a.G + kWave - 1) / kWave;
     constexpr bool kPairs = EPI == E_QKV || EPI == E_SWIGLU;
+    if (gpl <= 1) return launch_b1<1, 4, 2, false, XS, EPI>(a, st);
+    if (gpl <= 2) {
+        if constexpr (EPI == E_QKV) return launch_b1<2, 4, 1, false, XS, EPI>(a, st);
+        if constexpr (EPI == E_SWIGLU || EPI == E_LOGITS) return launch_b1<2, 2, 2, false, XS, EPI>(a, st);
+        return launch_b1<2, 1, 3, false, XS, EPI>(a, st);
+    }
+    if (gpl <= 4) return launch_b1<4, 2, 2, true, XS, EPI>(a, st);
+    if (gpl > 7) return hipErrorInvalidValue;
+    if constexpr (kPairs) return launch_b1<7, 2, 2, true, XS, EPI>(a, st);
+    return launch_b1<7, 1, 1, false, XS, EPI>(a, st);
+}
+
+// Batch 1 on the row kernels, batch 2..8 on the matrix cores; then the
+// post-GEMV RMSNorm where the launch asks for one.
+template <int XS, int EPI>
+hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
+    const int gpl = (a.G + kWave - 1) / kWave;
     if (a.batch == 1) {
-        if (gpl <= 1) return launch_b1<1, 4, 2, false, XS, EPI>(a, st);
-        if (gpl <= 2) {
-            if constexpr (EPI == E_QKV) return launch_b1<2, 4, 1, false, XS, EPI>(a, st);
-            if constexpr (EPI == E_SWIGLU || EPI == E_LOGITS) return launch_b1<2, 2, 2, false, XS, EPI>(a, st);
-            return launch_b1<2, 1, 3, false, XS, EPI>(a, st);
-        }
-        if (gpl <= 4) return launch_b1<4, 2, 2, true, XS, EPI>(a, st);
-        if (gpl > 7) return hipErrorInvalidValue;
-        if constexpr (kPairs) return launch_b1<7, 2, 2, true, XS, EPI>(a, st);
-        return launch_b1<7, 1, 1, false, XS, EPI>(a, st);
+        const hipError_t e = launch_b1_gpl<XS, EPI>(a, st);
+        return e != hipSuccess ? e : post_norm_launch(a, st);
     }
     if (gpl > 7) return hipErrorInvalidValue;
     return launch_mfma<XS, EPI>(a, st);
@@ -824,6 +909,8 @@ hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st) {
             case E_F32: return launch_gpl<X_F16, E_F32>(a, st);
             case E_ACC: return launch_gpl<X_F16, E_ACC>(a, st);
             case E_SWIGLU: return launch_gpl<X_F16, E_SWIGLU>(a, st);
+            case E_QKV: return launch_gpl<X_F16, E_QKV>(a, st);
+            case E_LOGITS: return launch_gpl<X_F16, E_LOGITS>(a, st);
             default: return hipErrorInvalidValue;
         }
     }

@@ -78,6 +78,13 @@ struct GemvArgs {
     float* kpart;
     int kparts;      // set by the launcher
     int kpart_rows;  // rows of one part: batch, or batch * k slots for routed experts
+    // Optional (E_ACC / E_F32, ldy == N): also write post_x16 [batch][N] =
+    // fp16(RMSNorm(y32 row) * post_norm_w) of the rows just written, the
+    // input of the next RMSNorm-input GEMV.  The K-split path does it in its
+    // part-sum launch; the others in a launch of their own.
+    const float* post_norm_w;  // nullptr = ones
+    uint16_t* post_x16;
+    float post_eps;
 };
 
 // Parts of a K-split batch-2..8 GEMV (0: none); the workspace is

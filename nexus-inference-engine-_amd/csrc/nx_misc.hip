@@ -33,6 +33,46 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* w,
     }
 }
 
+// One row per block of 1024 threads, 16-byte loads: every x and weight
+// chunk of the row is requested at once (thread t holds chunks t, t + 1024,
+// ..., at most kNormChunks), one reduction, the normalized row from
+// registers.  Rows of up to 16384 with dim % 4 == 0 and 16-byte aligned
+// pointers.
+constexpr int kNormThreads = 1024, kNormChunks = 4;
+__global__ __launch_bounds__(kNormThreads) void k_rmsnorm_vec(const float* x, const float* w, uint16_t* out,
+                                                              int dim, float eps) {
+    __shared__ float red[kNormThreads / 64];
+    const int nc = dim / 4, t = threadIdx.x;
+    const float4* xb = reinterpret_cast<const float4*>(x + (size_t)blockIdx.x * dim);
+    const float4* wb = reinterpret_cast<const float4*>(w);
+    float4 v[kNormChunks], wv[kNormChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) {
+        const int c = t + j * kNormThreads;
+        v[j] = c < nc ? xb[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[j] = w && c < nc ? wb[c] : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)dim + eps);
+    uint2* ob = reinterpret_cast<uint2*>(out + (size_t)blockIdx.x * dim);
+#pragma unroll
+    for (int j = 0; j < kNormChunks; ++j) {
+        const int c = t + j * kNormThreads;
+        if (c >= nc) break;
+        const uint32_t lo = (uint32_t)f2h_bits(v[j].x * inv * wv[j].x) | ((uint32_t)f2h_bits(v[j].y * inv * wv[j].y) << 16);
+        const uint32_t hi = (uint32_t)f2h_bits(v[j].z * inv * wv[j].z) | ((uint32_t)f2h_bits(v[j].w * inv * wv[j].w) << 16);
+        ob[c] = make_uint2(lo, hi);
+    }
+}
+
 __global__ void k_rope(float* x, const int32_t* pos, const float* cos_t, const float* sin_t,
                        int heads, int hd, int batch) {
     const int half = hd / 2;
@@ -570,7 +610,13 @@ __global__ void k_pf_moe_combine(const float* yg, const int32_t* slot_row, const
 
 hipError_t rmsnorm_launch(const float* x, const float* w, uint16_t* out, int dim, float eps,
                           int batch, hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(batch), dim3(256), 0, st, x, w, out, dim, eps);
+    const bool vec = dim % 4 == 0 && dim <= 4 * kNormThreads * kNormChunks &&
+                     ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                       reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_rmsnorm_vec, dim3(batch), dim3(kNormThreads), 0, st, x, w, out, dim, eps);
+    else
+        hipLaunchKernelGGL(k_rmsnorm, dim3(batch), dim3(256), 0, st, x, w, out, dim, eps);
     return hipGetLastError();
 }
 

@@ -105,6 +105,7 @@ struct nx_model {
     hipGraphExec_t exec_multi = nullptr;  // kStepsPerGraph decode steps
     std::vector<int> hpos;       // host mirror of pos (last processed position)
     int prefill_batched = 1;     // batched (GEMM) prefill where the model allows it
+    int prenorm = 1;             // batch 2-8: RMSNorm as its own launch before the GEMVs that take it
     // sampling (temperature <= 0: greedy argmax of the lm_head epilogue)
     float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
     int top_k = 0;
@@ -417,6 +418,29 @@ nx_status feed_decode(nx_model* m) {
     return upload_feed(m, f.data(), nullptr);
 }
 
+// Batch 2-8 with pre-normalized GEMV inputs (m->prenorm): RMSNorm(h) is
+// written once per token as fp16 (m->xn16) and the GEMVs that take it stage
+// that, instead of every block of the matrix-core GEMV reading and reducing
+// the whole fp32 h.
+bool prenorm_on(const nx_model* m) { return m->prenorm && m->c.batch > 1; }
+
+// A GEMV whose input is RMSNorm(h32) with weights norm_w: at batch 1 the
+// kernel normalizes h itself while it stages it; with prenorm_on the input
+// is m->xn16, written by a small launch here, or already (xn_ready) by the
+// launch before, which normalized the rows it finished.
+hipError_t norm_gemv_launch(nx_model* m, int epi, nx::GemvArgs a, hipStream_t st, bool xn_ready = false) {
+    if (!prenorm_on(m)) return nx::gemv_launch(nx::X_RMSNORM, epi, a, st);
+    if (!xn_ready) {
+        const hipError_t e = nx::rmsnorm_launch(a.h32, a.norm_w, m->xn16, a.K, a.eps, a.batch, st);
+        if (e != hipSuccess) return e;
+    }
+    a.x16 = m->xn16;
+    a.ldx = a.K;
+    a.h32 = nullptr;
+    a.norm_w = nullptr;
+    return nx::gemv_launch(nx::X_F16, epi, a, st);
+}
+
 // One decode step for every sequence, enqueued on the context stream.
 nx_status enqueue_step(nx_model* m) {
     const nx_model_config& c = m->c;
@@ -424,13 +448,14 @@ nx_status enqueue_step(nx_model* m) {
     const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts;
     NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d,
                                   c.vocab, B, st, m->fused ? m->lstate : nullptr, m->feed, m->fpos));
+    bool xn_ready = false;  // m->xn16 holds RMSNorm(h) for the next RMSNorm-input GEMV
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
         if (m->fused) {
             NX_LAUNCH(m, fused_attention_launch(m, L, st));
         } else {
             // RMSNorm + QKV + RoPE + paged KV append, attention, wo + residual
-            NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_QKV, qkv_args(m, ly), st));
+            NX_LAUNCH(m, norm_gemv_launch(m, nx::E_QKV, qkv_args(m, ly), st, xn_ready));
             if (c.kv_kind == 1)
                 NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr,
                                                   ly.kc4, ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table,
@@ -453,7 +478,7 @@ nx_status enqueue_step(nx_model* m) {
             f.norm_w = ly.norm_ffn;
             f.act16 = m->act16;
             f.lda = m->Fp;
-            NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_SWIGLU, f, st));
+            NX_LAUNCH(m, norm_gemv_launch(m, nx::E_SWIGLU, f, st));
             nx::GemvArgs dn{};
             dn.W = ly.w2;
             dn.S = ly.s2;
@@ -466,7 +491,14 @@ nx_status enqueue_step(nx_model* m) {
             dn.y32 = m->h;
             dn.ldy = d;
             dn.kpart = m->kpart;
+            if (prenorm_on(m)) {
+                // the new h rows normalized for the next layer's QKV (or the lm_head)
+                dn.post_norm_w = L + 1 < c.n_layers ? m->layers[(size_t)L + 1].norm_attn : m->norm_final;
+                dn.post_x16 = m->xn16;
+                dn.post_eps = c.eps;
+            }
             NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, dn, st));
+            xn_ready = prenorm_on(m);
         } else {
             nx::MoeArgs ma{};
             ma.logits = m->router_logits;
@@ -527,6 +559,7 @@ nx_status enqueue_step(nx_model* m) {
             NX_LAUNCH(m, nx::moe_gate_up_launch(mf, st));
             NX_LAUNCH(m, nx::moe_down_launch(mf, st));
             NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+            xn_ready = false;
         }
     }
     // final RMSNorm + lm_head + greedy argmax
@@ -544,7 +577,7 @@ nx_status enqueue_step(nx_model* m) {
     lm.y32 = m->logits;
     lm.ldy = c.vocab;
     lm.best = m->best;
-    NX_LAUNCH(m, nx::gemv_launch(nx::X_RMSNORM, nx::E_LOGITS, lm, st));
+    NX_LAUNCH(m, norm_gemv_launch(m, nx::E_LOGITS, lm, st, xn_ready));
     if (m->temperature > 0.0f) NX_TRY(enqueue_sample(m, 0, B));
     return NX_OK;
 }
