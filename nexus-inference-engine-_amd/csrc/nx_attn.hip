@@ -82,6 +82,8 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
     NX_ATRACE(0);
+    attn_args_early(a);
+    asm volatile("" ::"s"(a.kpool), "s"(a.vpool), "s"(nsplit));
 
     // The context length and this wavefront's block-table entries (page
     // p0 + wave + kAttnWaves * i in lane i) are requested together: one round trip.
@@ -430,6 +432,9 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     __shared__ uint2 cbk[kTqTbl];
 
     NX_ATRACE(0);
+    attn_args_early(a);
+    asm volatile("" ::"s"(a.kc4), "s"(a.kc3), "s"(a.vc4), "s"(a.vc3), "s"(a.kn), "s"(a.vn), "s"(a.ksign),
+                 "s"(a.vsign), "s"(nsplit), "s"(pps));
     if (slot < 0) {
         slot = split;
         nrec = nsplit;

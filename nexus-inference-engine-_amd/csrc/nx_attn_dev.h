@@ -34,6 +34,14 @@ __device__ inline void st_coh_u16(uint16_t* p, uint16_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The arguments a split block reads first, requested together from the
+// argument segment (the compiler would otherwise fetch them in several
+// dependent rounds as each is first needed).
+__device__ inline void attn_args_early(const AttnArgs& a) {
+    asm volatile("" ::"s"(a.q), "s"(a.block_table), "s"(a.ctx_lens), "s"(a.pos), "s"(a.hq), "s"(a.hkv),
+                 "s"(a.max_blocks), "s"(a.hot_window), "s"(a.check_blocks));
+}
+
 // The part of sequence b's context a block covers: all of it (range 0), or
 // with tiered pages the TurboQuant pages [cool, cold) (range 1, from page
 // cool / 16 on), the fp16 window [cold, ctx) (range 2, read from page cold /

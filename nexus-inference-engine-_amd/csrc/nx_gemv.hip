@@ -418,6 +418,15 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     __shared__ float red[kMfmaWaves][kMfmaCols];
     __shared__ unsigned long long bk[kMfmaThreads];
     NX_MTRACE(0);
+    // The arguments the prologue uses, requested together: the compiler
+    // would otherwise fetch them from the argument segment in several
+    // dependent rounds as each is first needed.
+    asm volatile("" ::"s"(args.W), "s"(args.S), "s"(args.x16), "s"(args.h32), "s"(args.N), "s"(args.K),
+                 "s"(args.G), "s"(args.batch), "s"(args.ldx), "s"(args.kparts), "s"(args.moe_plan), "s"(nb),
+                 "s"(ks));
+    if constexpr (EPI == E_SWIGLU) asm volatile("" ::"s"(args.act16), "s"(args.lda));
+    if constexpr (EPI == E_ACC || EPI == E_F32) asm volatile("" ::"s"(args.y32), "s"(args.ldy));
+    if constexpr (EPI == E_PART) asm volatile("" ::"s"(args.kpart), "s"(args.kpart_rows));
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
     const int N = args.N, K = args.K;
@@ -434,7 +443,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     // the nb blocks of a grid row share the tiles evenly: block x takes
     // [x ntile / nb, (x + 1) ntile / nb), at most tpb tiles
     const int ntile = (N + 15) / 16, tpb = (ntile + nb - 1) / nb;
-    const int t0 = (int)((long)bx * ntile / nb), nt = (int)((long)(bx + 1) * ntile / nb) - t0;
+    // (bx + 1) * ntile < 2^31: ntile <= 8192 tiles, nb <= 65536 blocks
+    const int t0 = (int)((unsigned)(bx * ntile) / (unsigned)nb), nt = (int)((unsigned)((bx + 1) * ntile) / (unsigned)nb) - t0;
     if (nt <= 0 || Gx <= 0) return;
     static_assert(!MOE || XS == X_F16, "routed experts take fp16 x");
     GemvArgs a = args;
@@ -793,6 +803,7 @@ hipError_t post_norm_launch(const GemvArgs& a, hipStream_t st) {
 // MOE: ny grid rows of routed experts share the CUs.
 template <int XS, int EPI, bool MOE = false>
 hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
+    if (a.N > (1 << 24)) return hipErrorInvalidValue;  // the kernel's 32-bit tile arithmetic
     const int ntile = (a.N + 15) / 16, cus = device_cus();
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
@@ -803,7 +814,7 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
         // of x once for its tiles (a block holding all of K would read all of
         // x for 16 rows); the part sums meet in a second launch (routed
         // experts: in the combine)
-        const int kp = gemv_kparts(a.K, a.batch);
+        const int kp = a.want_kparts > 0 && a.batch >= 2 && a.K % 32 == 0 ? a.want_kparts : gemv_kparts(a.K, a.batch);
         if (kp > 0 && a.kpart && xvec && salign) {
             GemvArgs p = a;
             p.kparts = kp;

@@ -85,6 +85,9 @@ struct GemvArgs {
     const float* post_norm_w;  // nullptr = ones
     uint16_t* post_x16;
     float post_eps;
+    // > 0: K parts of the batch 2..8 split (instead of gemv_kparts(K)),
+    // when kpart holds want_kparts * batch * N floats
+    int want_kparts;
 };
 
 // Parts of a K-split batch-2..8 GEMV (0: none); the workspace is

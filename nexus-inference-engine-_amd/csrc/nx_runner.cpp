@@ -106,6 +106,7 @@ struct nx_model {
     std::vector<int> hpos;       // host mirror of pos (last processed position)
     int prefill_batched = 1;     // batched (GEMM) prefill where the model allows it
     int prenorm = 1;             // batch 2-8: RMSNorm as its own launch before the GEMVs that take it
+    int wo_kparts = 2;           // batch 2-8: K parts of wo (0: one launch over all of K)
     // sampling (temperature <= 0: greedy argmax of the lm_head epilogue)
     float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
     int top_k = 0;
@@ -461,7 +462,19 @@ nx_status enqueue_step(nx_model* m) {
                                                   ly.kc4, ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table,
                                                   m->pos, m->max_blocks, st));
             NX_LAUNCH(m, attention_launch(m, ly, st));
-            NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, wo_args(m, ly), st));
+            nx::GemvArgs wo = wo_args(m, ly);
+            if (prenorm_on(m) && m->kpart && m->wo_kparts > 0 && m->wo_kparts <= nx::gemv_kparts(c.ffn, B)) {
+                // K split, the part-sum launch normalizes the new h for gate/up
+                wo.kpart = m->kpart;
+                wo.want_kparts = m->wo_kparts;
+                if (E == 0) {
+                    wo.post_norm_w = ly.norm_ffn;
+                    wo.post_x16 = m->xn16;
+                    wo.post_eps = c.eps;
+                }
+            }
+            NX_LAUNCH(m, nx::gemv_launch(nx::X_F16, nx::E_ACC, wo, st));
+            xn_ready = wo.post_x16 != nullptr;
         }
         if (E == 0) {
             // RMSNorm + gate/up + SwiGLU, then down + residual
@@ -478,7 +491,7 @@ nx_status enqueue_step(nx_model* m) {
             f.norm_w = ly.norm_ffn;
             f.act16 = m->act16;
             f.lda = m->Fp;
-            NX_LAUNCH(m, norm_gemv_launch(m, nx::E_SWIGLU, f, st));
+            NX_LAUNCH(m, norm_gemv_launch(m, nx::E_SWIGLU, f, st, xn_ready));
             nx::GemvArgs dn{};
             dn.W = ly.w2;
             dn.S = ly.s2;
