@@ -408,7 +408,8 @@ __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
 // router rows are requested together up front.  Each block publishes its
 // logits with agent-scope stores, waits for them, and counts itself in
 // *counter; the last block resets the counter and routes every sequence
-// (k_moe_route's routing) from the published logits.
+// (k_moe_route's routing) from the published logits.  With one sequence the
+// block routes from its own logits in LDS at once.
 constexpr int kNrThreads = 1024;
 constexpr int kNrWaves = kNrThreads / kWave;
 constexpr int kNrMaxD = 4096;
@@ -425,6 +426,9 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     __shared__ float sw[8 * 8];
     __shared__ int scnt[kNrMaxE];
     __shared__ int last;
+    // the arguments the prologue uses, requested in one round
+    asm volatile("" ::"s"(a.h), "s"(a.wr), "s"(a.sr), "s"(a.d), "s"(a.batch), "s"(a.E), "s"(a.norm_w),
+                 "s"(a.xn16), "s"(a.eps));
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6, b = blockIdx.x;
     const int d = a.d, B = a.batch, E = a.E, G = d / 32;
     const float* hb = a.h + (size_t)b * d;
@@ -490,25 +494,25 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
             }
         }
         acc = wave_sum(acc);
-        if (lane == 0)
+        if (lane == 0) {
             __hip_atomic_store(a.logits + (size_t)b * E + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // this block's logits are stored before it counts itself
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        int l = 1;
-        if (B > 1) {
-            const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            l = prev == (unsigned)B - 1u;
-            if (l) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lg[b * E + e] = acc;  // batch 1: the routing reads them here
         }
-        last = l;
     }
-    __syncthreads();
-    if (!last) return;
-    for (int idx = tid; idx < B * E; idx += kNrThreads)
-        lg[idx] = __hip_atomic_load(a.logits + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (B > 1) {
+        // this block's logits are stored before it counts itself
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = prev == (unsigned)B - 1u;
+            if (last) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        for (int idx = tid; idx < B * E; idx += kNrThreads)
+            lg[idx] = __hip_atomic_load(a.logits + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
     if (tid < B) {
         route_row(lg + tid * E, E, a.k, sid + tid * a.k, sw + tid * a.k, sp[tid]);
