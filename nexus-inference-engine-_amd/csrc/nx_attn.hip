@@ -416,12 +416,74 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
     }
 }
 
+template <bool COOL>
+__device__ inline float tq_codes_lane(float x0, float x1, const float* __restrict__ sign, int& q0, int& q1);
+template <bool COOL>
+__device__ inline void tq_store_codes(int q0, int q1, float n, uint8_t* __restrict__ ca, uint8_t* __restrict__ cb,
+                                      uint16_t* __restrict__ norm, uint8_t* lds_codes);
+
+// The token being written at this step (a.kv_cur: its fp32 K and V), in
+// wavefront 0 of one extra block of the launch that reads no page: encode K
+// and V into the TurboQuant pages at position pos[b] (what a separate
+// append launch would store) and form the token's softmax record from its
+// codes -- score n_k * scale * sum_i c[code_i] q~_i for each head, value
+// n_v * c[code_i] in the rotated domain -- in the layouts of the page loop
+// (m and l of head l%16, l on the lanes of group 0; O rows 4(l/16) + i,
+// column t of tile nt = dimension 8t + nt).  The page splits stop before
+// this position.
+template <int G>
+__device__ inline void tq_current_record(const AttnArgs& a, int b, int kvh, const float* qrot, float scale, float& m,
+                                         float& lsum, f4_t (&o)[8]) {
+    constexpr int HD = 128;
+    __shared__ float scratch[64 + 128];  // packing rows of the K and V codes, then the value
+    const int lane = threadIdx.x & 63, g = lane >> 4, t = lane & 15;
+    const int p = a.pos[b];
+    const float* kx = a.kv_cur + (size_t)b * 2 * a.hkv * HD + (size_t)kvh * HD;
+    const float* vx = kx + (size_t)a.hkv * HD;
+    const size_t dst = ((size_t)a.block_table[(size_t)b * a.max_blocks + p / kPage] * a.hkv + kvh) * kPage + p % kPage;
+    // the TurboQuant pools, written here for the later steps
+    uint8_t* codes = reinterpret_cast<uint8_t*>(scratch);
+    int kq0, kq1, vq0, vq1;
+    const float nk = tq_codes_lane<false>(kx[lane], kx[lane + 64], a.ksign, kq0, kq1);
+    tq_store_codes<false>(kq0, kq1, nk, const_cast<uint8_t*>(a.kc4) + dst * 32, const_cast<uint8_t*>(a.kc3) + dst * 24,
+                          const_cast<uint16_t*>(a.kn) + dst, codes);
+    const float nv = tq_codes_lane<false>(vx[lane], vx[lane + 64], a.vsign, vq0, vq1);
+    tq_store_codes<false>(vq0, vq1, nv, const_cast<uint8_t*>(a.vc4) + dst * 32, const_cast<uint8_t*>(a.vc3) + dst * 24,
+                          const_cast<uint16_t*>(a.vn) + dst, codes + 128);
+    // scores of the G heads (the norms as stored, fp16)
+    const float k0 = c_tq_cb[kq0], k1 = c_tq_cb[16 + kq1];
+    const float kscale = h2f_bits(f2h_bits(nk)) * scale;
+    float s[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) s[h] = wave_sum(k0 * qrot[h * HD + lane] + k1 * qrot[h * HD + lane + 64]) * kscale;
+    // the value in the rotated domain, redistributed to the C layout (column
+    // t of tile nt is dimension 8t + nt)
+    float* v = scratch + 64;
+    v[lane] = c_tq_cb[vq0];
+    v[lane + 64] = c_tq_cb[16 + vq1];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float vscale = h2f_bits(f2h_bits(nv));
+    float st = s[0];
+#pragma unroll
+    for (int h = 1; h < G; ++h) st = t == h ? s[h] : st;
+    m = st;
+    lsum = g == 0 ? 1.0f : 0.0f;  // exp(st - m); the record's sum over the lane groups
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[nt][i] = vscale * v[8 * t + nt];
+}
+
 // One split of one (kv head, sequence) over TurboQuant pages: the page
 // schedule of attn_f16_run (pairs, two in flight when a wavefront has more
 // than one), q rotated once per block (q~ = H D q in LDS); the last block
 // of the (sequence, kv head) merges the records and rotates the value sums
 // back (merge_last<G, 128, true>).
-template <int G, bool PIPE, bool COOL = false>
+// CUR: the extra block of a launch with kv_cur (the position being written,
+// no pages; tq_current_record).
+template <int G, bool PIPE, bool COOL = false, bool CUR = false>
 __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int split, int kvh, int b,
                                    int range = 0, int slot = -1, int nrec = 0, int ntq = 0) {
     constexpr int HD = 128, REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
@@ -442,6 +504,8 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     }
     int ctx, pg0;
     attn_range(a, b, range, ctx, pg0);
+    const bool cur = range == 0 && a.kv_cur != nullptr;  // the current position comes from kv_cur
+    if (cur) ctx -= 1;
     const int p0 = split * pps;
     const int npw_max = (pps - wave + kAttnWaves - 1) / kAttnWaves;
     const int my_page = p0 + wave + kAttnWaves * lane;
@@ -517,7 +581,9 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     auto upd = [&](const TqPair& r, int p) {
         tq_pair_update<COOL>(r, ln, qh, ql, cbk, scale, valid_of(2 * p), valid_of(2 * p + 1), m, lsum, o, lane);
     };
-    if constexpr (PIPE) {
+    if constexpr (CUR) {
+        if (wave == 0) tq_current_record<G>(a, b, kvh, qrot, scale, m, lsum, o);
+    } else if constexpr (PIPE) {
         // three register sets in rotation: pair p + 2 is requested before
         // pair p is used, so two pairs stay in flight
         const int np = (npw + 1) / 2;
@@ -570,9 +636,15 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     NX_ATRACE(6);
 }
 
+// With kv_cur the last block of each (sequence, kv head) takes the position
+// being written (its own instantiation, so the page loop's registers are
+// not shared with it).
 template <int G, bool PIPE>
 __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_tq(AttnArgs a, int nsplit, int pps) {
-    attn_tq_run<G, PIPE>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
+    if (a.kv_cur && (int)blockIdx.x == nsplit - 1)
+        attn_tq_run<G, false, false, true>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
+    else
+        attn_tq_run<G, PIPE>(a, nsplit, pps, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // ----------------------------------------------------- TurboQuant encode --
@@ -1099,7 +1171,8 @@ hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st)
 
 SplitPlan plan_splits_f16(int max_ctx, int hkv, int batch);
 size_t attn_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx) {
-    const int nsplit = max(plan_splits(max_ctx).nsplit, plan_splits_f16(max_ctx, hkv, batch).nsplit);
+    // TurboQuant pages in the decode step: one more record (the position being written)
+    const int nsplit = max(min(plan_splits(max_ctx).nsplit + 1, kMaxSplits), plan_splits_f16(max_ctx, hkv, batch).nsplit);
     const int G = hq / hkv;
     return sizeof(float) * (size_t)batch * hkv * nsplit * rec_floats(G, hd);
 }
@@ -1114,11 +1187,13 @@ size_t attn_f16_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx)
 
 // TurboQuant splits: about one block per CU over all (kv head, sequence)
 // pairs (the pipelined kernel holds one 8-wavefront block per CU), never
-// more splits than plan_splits (which sizes the workspace).
-SplitPlan plan_splits_tq(int max_ctx, int hkv, int batch) {
+// more splits than plan_splits (which sizes the workspace); `extra` blocks
+// per pair that read no pages (the position being written) count against
+// the CUs too.
+SplitPlan plan_splits_tq(int max_ctx, int hkv, int batch, int extra = 0) {
     const SplitPlan base = plan_splits(max_ctx);
     const int pages = (max_ctx + kPage - 1) / kPage;
-    const int want = (device_cus() + hkv * batch - 1) / (hkv * batch);
+    const int want = (device_cus() + hkv * batch - 1) / (hkv * batch) - extra;
     int nsplit = min(base.nsplit, max(want, 1));
     const int pps = min(max((pages + nsplit - 1) / nsplit, 1), kPagesPerSplitMax);
     nsplit = max((pages + pps - 1) / pps, 1);
@@ -1195,7 +1270,16 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
 
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st) {
     if (!a.counts || !a.part) return hipErrorInvalidValue;
-    const SplitPlan sp = plan_splits_tq(a.max_ctx, a.hkv, a.batch);
+    SplitPlan sp = plan_splits_tq(a.max_ctx, a.hkv, a.batch, a.kv_cur ? 1 : 0);
+    if (a.kv_cur && sp.nsplit >= kMaxSplits) {
+        // room for the current position's block among the records
+        const int pages = (a.max_ctx + kPage - 1) / kPage;
+        sp.pps = (pages + kMaxSplits - 2) / (kMaxSplits - 1);
+        sp.nsplit = (pages + sp.pps - 1) / sp.pps;
+        if (sp.pps > kPagesPerSplitMax) return hipErrorInvalidValue;
+    }
+    // with kv_cur, one more block: the position being written (no pages)
+    if (a.kv_cur) sp.nsplit += 1;
     const dim3 grid(sp.nsplit, a.hkv, a.batch);
     const int G = a.hq / a.hkv;
     if (a.hd != 128) return hipErrorInvalidValue;

@@ -148,6 +148,11 @@ struct AttnArgs {
     const int32_t* cool_table;
     const uint8_t *kcc, *vcc;
     const uint16_t *kcn, *vcn;
+    // TurboQuant pages in the decode step (attn_tq_launch): the fp32 K and V
+    // of the token being written ([batch][2][hkv * 128]); the launch encodes
+    // them into the pages at pos[b] and attends over them with the pages
+    // before (nullptr: the pages already hold every position)
+    const float* kv_cur;
     // > 0 (fp16 pages, standalone): the kernel itself checks each sequence's
     // context length against max_blocks * 16 and the block-table entries of
     // its pages against [0, check_blocks); an entry outside reads block 0

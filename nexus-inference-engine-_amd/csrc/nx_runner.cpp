@@ -309,14 +309,19 @@ nx::AttnArgs attn_args(const nx_model* m, const Layer& ly) {
 }
 
 // Attention of layer ly for every sequence (q in m->q, output m->att16).
+// TurboQuant pages: the launch also appends this step's K and V (kv_tmp),
+// unless `append` is false (the pages already hold every position).
 // Tiered pages: one launch whose blocks read either the compressed pages
 // (TurboQuant) or the fp16 window, merged by the last block, and compress the
 // page that leaves the window at this step.
-hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st) {
+hipError_t attention_launch(nx_model* m, const Layer& ly, hipStream_t st, bool append = true) {
     const nx_model_config& c = m->c;
     nx::AttnArgs at = attn_args(m, ly);
     if (c.kv_kind == 0) return nx::attn_f16_launch(at, st);
-    if (c.kv_kind == 1) return nx::attn_tq_launch(at, st);
+    if (c.kv_kind == 1) {
+        if (append) at.kv_cur = m->kv_tmp;  // the launch also encodes this step's K and V into the pages
+        return nx::attn_tq_launch(at, st);
+    }
     at.hot_window = c.hot_window;
     at.hot_table = m->hot_bt;
     at.warm_window = c.warm_window;
@@ -457,10 +462,6 @@ nx_status enqueue_step(nx_model* m) {
         } else {
             // RMSNorm + QKV + RoPE + paged KV append, attention, wo + residual
             NX_LAUNCH(m, norm_gemv_launch(m, nx::E_QKV, qkv_args(m, ly), st, xn_ready));
-            if (c.kv_kind == 1)
-                NX_LAUNCH(m, nx::tq_append_launch(m->kv_tmp, B, c.n_kv_heads, ly.ksign, ly.vsign, nullptr, nullptr,
-                                                  ly.kc4, ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, m->block_table,
-                                                  m->pos, m->max_blocks, st));
             NX_LAUNCH(m, attention_launch(m, ly, st));
             nx::GemvArgs wo = wo_args(m, ly);
             if (prenorm_on(m) && m->kpart && m->wo_kparts > 0 && m->wo_kparts <= nx::gemv_kparts(c.ffn, B)) {
@@ -1587,8 +1588,9 @@ nx_status nx_model_time_attention(nx_model* m, int iters, double* avg_ms, double
     for (int b = 0; b < c.batch; ++b)
         if (m->hpos[b] < 0) return fail(m->ctx, NX_ERR_STATE, "no context to attend over");
     hipStream_t st = m->ctx->stream;
-    // launch i attends over layer i % n_layers (a separate cache per layer)
-    auto launch = [&](int i) { return attention_launch(m, m->layers[i % c.n_layers], st); };
+    // launch i attends over layer i % n_layers (a separate cache per layer),
+    // whose pages already hold every position (TurboQuant pages: no append)
+    auto launch = [&](int i) { return attention_launch(m, m->layers[i % c.n_layers], st, false); };
     for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
     for (int i = 0; i < iters; ++i) NX_LAUNCH(m, launch(i));
