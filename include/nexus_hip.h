@@ -349,6 +349,13 @@ typedef struct {
                                the Cold tier of evict_cold_pages (kv/paged_attention.cpp:295-310):
                                attention reads an evicted position as the zero key and value
                                get_vectors gathers for a page it does not hold (:172, :219) */
+    int kv_blocks;          /* 0 = every sequence holds a full-length page table (batch *
+                               max_seq / 16 pages); else the pages of one shared pool, taken
+                               as sequences grow and given back when a slot retires or starts
+                               over (the page table of PagedKVCache, kv/paged_attention.cpp:
+                               59-77, whose pages are created on first insert); a step that
+                               needs more than are free fails with NX_ERR_CAPACITY before it
+                               runs.  Not with a cool_window (every table is then a ring). */
 } nx_model_config;
 
 typedef struct nx_model nx_model;
@@ -438,6 +445,10 @@ nx_status nx_model_fill_context(nx_model* m, int ctx, int n_outlier);
  * PagedKVCache::get_vectors (kv/paged_attention.cpp:161-230), as stored
  * rather than decompressed; cap = bytes available at out. */
 nx_status nx_model_kv_read(nx_model* m, int layer, int b, int pos, int kv, int* form, void* out, size_t cap);
+/* Pages of the model's KV pool (per layer) and how many are free: with a
+ * shared pool (kv_blocks) its free list, else batch * max_seq / 16 less the
+ * pages the sequences' positions cover.  Either pointer may be NULL. */
+nx_status nx_model_kv_pages(nx_model* m, int* total, int* free_pages);
 /* The pending (next input) token of every sequence, [batch]. */
 nx_status nx_model_pending(nx_model* m, int32_t* tokens);
 /* Engine::generate's loop (engine.cpp:155-173) of `steps` decode_step calls

@@ -95,6 +95,16 @@ struct nx_model {
     // permutation of the pool, max_blocks per sequence)
     int warm_pages = 0;
     int32_t* cool_bt = nullptr;
+    // shared page pool (kv_blocks > 0): the sequence-length table (block_table,
+    // or cool_bt with three tiers) takes pages on demand from a free list of
+    // kv_blocks pages and gives them back when the slot retires or starts
+    // over; entries without a page name the spare page pool_trash, which
+    // parked and held slots may write and nothing reads
+    int pool_trash = -1;
+    int32_t* long_table = nullptr;
+    std::vector<int32_t> h_table;            // host copy of long_table
+    std::vector<std::vector<int32_t>> owned;  // pages of each slot, in position order
+    std::vector<int32_t> free_pages;
     // with a Cool window (cool_window > 0), cool_bt is the Cool range's ring of
     // cool_pages pages per sequence and older pages are evicted
     int cool_pages = 0;
@@ -364,6 +374,50 @@ double kv_bytes(const nx_model* m) {
         kv += (cool - evict) * cl + (cold - cool) * tq + (ctx - cold) * f16;
     }
     return kv;
+}
+
+// Shared page pool: pages for positions up to last_pos of every slot that
+// `want` names (slot -> last position, -1 = none), all or nothing; the
+// table rows that changed are uploaded before anything reads them.
+nx_status pool_ensure(nx_model* m, const std::vector<int>& want) {
+    if (m->c.kv_blocks <= 0) return NX_OK;
+    size_t need = 0;
+    for (size_t b = 0; b < want.size(); ++b) {
+        const size_t n = want[b] >= 0 ? (size_t)(want[b] / nx::kPage + 1) : 0;
+        if (n > m->owned[b].size()) need += n - m->owned[b].size();
+    }
+    if (need > m->free_pages.size())
+        return fail(m->ctx, NX_ERR_CAPACITY, "kv page pool: %zu pages needed, %zu free", need, m->free_pages.size());
+    for (size_t b = 0; b < want.size(); ++b) {
+        if (want[b] < 0) continue;
+        const size_t n = (size_t)(want[b] / nx::kPage + 1), first = m->owned[b].size();
+        if (n <= first) continue;
+        for (size_t i = first; i < n; ++i) {
+            const int32_t blk = m->free_pages.back();
+            m->free_pages.pop_back();
+            m->owned[b].push_back(blk);
+            m->h_table[b * m->max_blocks + i] = blk;
+        }
+        const size_t off = b * m->max_blocks + first;
+        NX_HIP(m->ctx, hipMemcpyAsync(m->long_table + off, m->h_table.data() + off, (n - first) * 4,
+                                      hipMemcpyHostToDevice, m->ctx->stream));
+    }
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return NX_OK;
+}
+
+// The pages of slot b back to the free list (its rows name the spare page).
+nx_status pool_release(nx_model* m, int b) {
+    if (m->c.kv_blocks <= 0 || m->owned[(size_t)b].empty()) return NX_OK;
+    std::vector<int32_t>& own = m->owned[(size_t)b];
+    for (size_t i = own.size(); i-- > 0;) m->free_pages.push_back(own[i]);
+    const size_t off = (size_t)b * m->max_blocks;
+    std::fill(m->h_table.begin() + off, m->h_table.begin() + off + own.size(), m->pool_trash);
+    NX_HIP(m->ctx, hipMemcpyAsync(m->long_table + off, m->h_table.data() + off, own.size() * 4, hipMemcpyHostToDevice,
+                                  m->ctx->stream));
+    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    own.clear();
+    return NX_OK;
 }
 
 // QKV, attention and wo of layer L as one launch (batch 1, fp16 pages).
@@ -654,7 +708,7 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     m->Gf = (F + 31) / 32;
     m->Fp = m->Gf * 32;
     m->max_blocks = c.max_seq / nx::kPage;
-    m->n_blocks = m->max_blocks * B;
+    m->n_blocks = c.kv_blocks > 0 ? c.kv_blocks + 1 : m->max_blocks * B;
     m->hot_pages = c.kv_kind == 2 ? c.hot_window / nx::kPage + 1 : 0;
     m->warm_pages = c.kv_kind == 2 && c.warm_window > 0 ? c.warm_window / nx::kPage + 1 : 0;
     m->cool_pages = m->warm_pages > 0 && c.cool_window > 0 ? c.cool_window / nx::kPage + 1 : 0;
@@ -747,10 +801,22 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     }
     // block table: a seeded permutation of the pool, max_blocks per sequence
-    // (three tiers: the Cool table; the block table is the Warm ring)
+    // (three tiers: the Cool table; the block table is the Warm ring); with a
+    // shared pool every entry starts at the spare page and the free list is the
+    // seeded permutation of the others
     {
         std::vector<int32_t> perm;
         host_shuffle(perm, m->n_blocks, c.seed, nx::kTidShuffle);
+        if (c.kv_blocks > 0) {
+            m->pool_trash = c.kv_blocks;
+            m->free_pages.clear();
+            for (int32_t blk : perm)
+                if (blk != m->pool_trash) m->free_pages.push_back(blk);
+            std::reverse(m->free_pages.begin(), m->free_pages.end());  // taken from the back
+            m->owned.assign((size_t)B, {});
+            perm.assign((size_t)B * m->max_blocks, m->pool_trash);
+            m->h_table = perm;
+        }
         if (m->warm_pages > 0) {
             std::vector<int32_t> cool = perm;
             if (m->cool_pages > 0)
@@ -767,6 +833,7 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         NX_TRY(dalloc(m, &m->block_table, perm.size()));
         NX_HIP(m->ctx, hipMemcpyAsync(m->block_table, perm.data(), perm.size() * 4, hipMemcpyHostToDevice, m->ctx->stream));
         NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+        if (c.kv_blocks > 0) m->long_table = m->warm_pages > 0 ? m->cool_bt : m->block_table;
     }
     NX_TRY(dalloc(m, &m->pos, B));
     NX_TRY(dalloc(m, &m->base, B));
@@ -848,6 +915,10 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
         return fail(ctx, NX_ERR_INVALID, "warm_window must be 0 or (tiered pages) a positive multiple of 16");
     if (c.cool_window < 0 || c.cool_window % nx::kPage || (c.cool_window > 0 && c.warm_window == 0))
         return fail(ctx, NX_ERR_INVALID, "cool_window must be 0 or (with a warm_window) a positive multiple of 16");
+    if (c.kv_blocks < 0 || c.kv_blocks > (1 << 24))
+        return fail(ctx, NX_ERR_INVALID, "kv_blocks must be 0 (a full-length table per sequence) or a page count");
+    if (c.kv_blocks > 0 && c.cool_window > 0)
+        return fail(ctx, NX_ERR_INVALID, "kv_blocks: with a cool_window every table is a per-sequence ring");
     if (c.kv_kind == 2 && c.max_seq > nx::attn_max_ctx() / 2)
         return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the tiered attention limit");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
@@ -1181,6 +1252,11 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
             if (prompt[(size_t)b * P + i] < 0 || prompt[(size_t)b * P + i] >= c.vocab)
                 return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
     }
+    {
+        std::vector<int> want((size_t)B);
+        for (int b = 0; b < B; ++b) want[(size_t)b] = m->hpos[(size_t)b] + P;
+        NX_TRY(pool_ensure(m, want));
+    }
     for (int b = 0; b < B; ++b) m->active[(size_t)b] = 1;
     if (batched_prefill_ok(m)) {
         for (int b = 0; b < B; ++b) NX_TRY(prefill_batched(m, b, prompt + (size_t)b * P, P));
@@ -1221,6 +1297,10 @@ nx_status nx_model_fill_context(nx_model* m, int ctx_len, int n_outlier) {
     if (n_outlier < 0 || n_outlier > 16 || n_outlier > c.head_dim) return fail(m->ctx, NX_ERR_INVALID, "n_outlier out of range");
     hipStream_t st = m->ctx->stream;
     const int hkv = c.n_kv_heads, hd = c.head_dim, B = c.batch;
+    // every sequence starts over with ctx_len positions (a shared pool: its
+    // pages for them)
+    for (int b = 0; b < B; ++b) NX_TRY(pool_release(m, b));
+    NX_TRY(pool_ensure(m, std::vector<int>((size_t)B, ctx_len - 1)));
     const float k1 = nx::normal_k(1.0);
     int32_t* och = nullptr;
     NX_TRY(dalloc(m, &och, (size_t)2 * hkv * (n_outlier > 0 ? n_outlier : 1)));
@@ -1360,6 +1440,12 @@ nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
     }
     if (nact == 0) return fail(m->ctx, NX_ERR_STATE, "decode with no active sequence");
     if (steps > m->out_stride) return fail(m->ctx, NX_ERR_CAPACITY, "too many steps for one call");
+    {
+        std::vector<int> want((size_t)B, -1);
+        for (int b = 0; b < B; ++b)
+            if (m->active[(size_t)b]) want[(size_t)b] = m->hpos[(size_t)b] + steps;
+        NX_TRY(pool_ensure(m, want));
+    }
     NX_TRY(ensure_graph(m));
     NX_TRY(feed_decode(m));
     hipStream_t st = m->ctx->stream;
@@ -1395,6 +1481,19 @@ nx_ctx* nx_model_context(nx_model* m) { return m ? m->ctx : nullptr; }
 nx_status nx_model_retire(nx_model* m, int slot) {
     if (!m || slot < 0 || slot >= m->c.batch) return NX_ERR_INVALID;
     m->active[(size_t)slot] = 0;
+    return pool_release(m, slot);
+}
+
+nx_status nx_model_kv_pages(nx_model* m, int* total, int* free_pages) {
+    if (!m) return NX_ERR_INVALID;
+    const bool shared = m->c.kv_blocks > 0;
+    if (total) *total = shared ? m->c.kv_blocks : m->max_blocks * m->c.batch;
+    if (free_pages) {
+        int used = 0;
+        if (!shared)
+            for (int b = 0; b < m->c.batch; ++b) used += m->hpos[(size_t)b] >= 0 ? m->hpos[(size_t)b] / nx::kPage + 1 : 0;
+        *free_pages = shared ? (int)m->free_pages.size() : m->max_blocks * m->c.batch - used;
+    }
     return NX_OK;
 }
 
@@ -1412,9 +1511,16 @@ nx_status nx_model_admit(nx_model* m, int slot, const int32_t* prompt, int P, in
     for (int i = 0; i < P; ++i)
         if (prompt[i] < 0 || prompt[i] >= c.vocab) return fail(m->ctx, NX_ERR_INVALID, "prompt token out of vocabulary");
     hipStream_t st = m->ctx->stream;
-    // the slot starts over: position -1, its pages are overwritten from position 0
+    // the slot starts over: position -1, its pages are overwritten from
+    // position 0 (a shared pool: its pages go back, the prompt's are taken)
     m->active[(size_t)slot] = 0;
     m->hpos[(size_t)slot] = -1;
+    NX_TRY(pool_release(m, slot));
+    {
+        std::vector<int> want((size_t)B, -1);
+        want[(size_t)slot] = P - 1;
+        NX_TRY(pool_ensure(m, want));
+    }
     const int32_t minus1 = -1;
     NX_HIP(m->ctx, hipMemcpyAsync(m->pos + slot, &minus1, 4, hipMemcpyHostToDevice, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));

@@ -1,11 +1,14 @@
 // Request scheduler over the runner's sequence slots: the serving loop of
 // Engine::generate (nexus/src/core/engine.cpp:124-184) -- prefill a prompt,
 // decode up to max_tokens tokens, stop early -- for many requests at once.
-// Requests wait in arrival order; whenever a slot is free the next one is
-// admitted into it (its prompt prefilled alone, whatever its length, while
-// the other slots keep their sequences), then every active slot decodes in
-// chunks of steps, and a request that has its tokens (or emitted its stop
-// token) is retired, freeing the slot for the next one.
+// Requests wait in arrival order; whenever a slot is free and the KV page
+// pool can hold the request to its last position (pages reserved per
+// request: a model with a shared pool, kv_blocks, holds fewer pages than
+// batch * max_seq / 16), the next one is admitted into it (its prompt
+// prefilled alone, whatever its length, while the other slots keep their
+// sequences), then every active slot decodes in chunks of steps, and a
+// request that has its tokens (or emitted its stop token) is retired,
+// freeing the slot and its pages for the next one.
 #include <algorithm>
 #include <deque>
 #include <map>
@@ -20,6 +23,7 @@ namespace {
 struct Request {
     std::vector<int32_t> prompt;
     int max_new = 0, stop = -1;
+    int pages = 0;  // KV pages to its last position: (P + max_new - 2) / 16 + 1
     std::vector<int32_t> out;
     int slot = -1;
     bool done = false;
@@ -35,6 +39,7 @@ struct nx_sched {
     nx_model* m = nullptr;
     nx_ctx* ctx = nullptr;
     int batch = 0, max_seq = 0, vocab = 0;
+    int pool_pages = 0, reserved = 0;  // pages of the model's pool, reserved by active requests
     std::deque<int> waiting;
     std::vector<int> slot_req;  // request id per slot, -1 = free
     std::map<int, Request> reqs;
@@ -67,6 +72,11 @@ nx_status nx_sched_create(nx_model* m, nx_sched** out) {
     sc->vocab = c.vocab;
     sc->slot_req.assign((size_t)c.batch, -1);
     for (int b = 0; b < c.batch; ++b) (void)nx_model_retire(m, b);
+    s = nx_model_kv_pages(m, &sc->pool_pages, nullptr);
+    if (s != NX_OK) {
+        delete sc;
+        return s;
+    }
     *out = sc;
     return NX_OK;
 }
@@ -88,6 +98,9 @@ nx_status nx_sched_submit(nx_sched* s, const int32_t* prompt, int P, int max_new
     r.prompt.assign(prompt, prompt + P);
     r.max_new = max_new;
     r.stop = stop;
+    r.pages = (P + max_new - 2) / 16 + 1;
+    if (r.pages > s->pool_pages)
+        return fail(s->ctx, NX_ERR_CAPACITY, "request of %d pages exceeds the KV pool of %d", r.pages, s->pool_pages);
     const int rid = s->next_id++;
     s->reqs.emplace(rid, std::move(r));
     s->waiting.push_back(rid);
@@ -101,8 +114,9 @@ nx_status nx_sched_step(nx_sched* s, int* n_active, int* n_waiting) {
     for (int b = 0; b < s->batch && !s->waiting.empty(); ++b) {
         if (s->slot_req[(size_t)b] >= 0) continue;
         const int rid = s->waiting.front();
-        s->waiting.pop_front();
         Request& r = s->reqs[rid];
+        if (s->reserved + r.pages > s->pool_pages) break;  // in arrival order: wait for pages
+        s->waiting.pop_front();
         int32_t first = 0;
         nx_status st = nx_model_admit(s->m, b, r.prompt.data(), (int)r.prompt.size(), &first);
         if (st != NX_OK) return st;
@@ -112,6 +126,7 @@ nx_status nx_sched_step(nx_sched* s, int* n_active, int* n_waiting) {
             r.slot = -1;
         } else {
             s->slot_req[(size_t)b] = rid;
+            s->reserved += r.pages;
         }
     }
     // one chunk of decode steps for the active slots
@@ -134,6 +149,7 @@ nx_status nx_sched_step(nx_sched* s, int* n_active, int* n_waiting) {
             if (take(r, tok.data() + (size_t)b * need, need)) {
                 (void)nx_model_retire(s->m, b);
                 s->slot_req[(size_t)b] = -1;
+                s->reserved -= r.pages;
                 r.slot = -1;
             }
         }

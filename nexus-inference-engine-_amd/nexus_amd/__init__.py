@@ -43,7 +43,7 @@ class ModelConfig(C.Structure):
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
-        ("warm_window", C.c_int), ("cool_window", C.c_int),
+        ("warm_window", C.c_int), ("cool_window", C.c_int), ("kv_blocks", C.c_int),
     ]
 
 
@@ -151,6 +151,7 @@ _SIGS = {
     "nx_sched_result": (_I, [_P, _I, _P, _I, C.POINTER(_I), C.POINTER(_I)]),
     "nx_model_fill_context": (_I, [_P, _I, _I]),
     "nx_model_kv_read": (_I, [_P, _I, _I, _I, _I, C.POINTER(C.c_int), _P, C.c_size_t]),
+    "nx_model_kv_pages": (_I, [_P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "nx_model_pending": (_I, [_P, _P]),
     "nx_model_decode": (_I, [_P, _I, _P]),
     "nx_model_logits": (_I, [_P, _P]),
@@ -384,6 +385,12 @@ class Model:
                        "nx_model_kv_read")
         n = {0: 2 * self.cfg.head_dim, 1: 58, 2: 50, 3: 0}[form.value] * self.cfg.n_kv_heads
         return form.value, out[:n]
+
+    def kv_pages(self):
+        """(pages of the KV pool, free pages) (nx_model_kv_pages)."""
+        total, free = C.c_int(), C.c_int()
+        self.ctx.check(self.ctx.L.nx_model_kv_pages(self.h, C.byref(total), C.byref(free)), "nx_model_kv_pages")
+        return total.value, free.value
 
     def pending(self) -> np.ndarray:
         t = np.empty(self.cfg.batch, np.int32)

@@ -32,7 +32,7 @@ class Cfg(C.Structure):
         ("n_experts", C.c_int), ("top_k", C.c_int), ("max_seq", C.c_int), ("batch", C.c_int),
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
-        ("warm_window", C.c_int), ("cool_window", C.c_int),
+        ("warm_window", C.c_int), ("cool_window", C.c_int), ("kv_blocks", C.c_int),
     ]
 
 

@@ -261,6 +261,8 @@ typedef struct {
                                       fp16 window kept Warm (a multiple of 16), older pages Cool */
     int cool_window;               /* kv_kind 2 with warm_window: 0 = keep every Cool page; else
                                       the positions kept Cool (a multiple of 16), older pages evicted */
+    int kv_blocks;                 /* the GPU runner's shared page pool; which physical page holds a
+                                      position changes no result, so the restatement ignores it */
 } nxo_cfg;
 
 typedef struct nxo_model nxo_model;

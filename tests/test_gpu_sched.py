@@ -29,6 +29,12 @@ CFGS = {
     "moe": dict(TINY, batch=3, max_seq=128, n_experts=4, top_k=2, seed=0x5C03),
     "turboquant": dict(TINY, batch=3, max_seq=128, n_heads=4, n_kv_heads=1, head_dim=128, d_model=512,
                        kv_kind=1, seed=0x5C04),
+    # a shared pool of 4 pages (the three slots would hold 24): C takes A's page
+    "dense-pool": dict(TINY, batch=3, max_seq=128, seed=0x5C07, kv_blocks=4),
+    "turboquant-pool": dict(TINY, batch=3, max_seq=128, n_heads=4, n_kv_heads=1, head_dim=128, d_model=512,
+                            kv_kind=1, seed=0x5C08, kv_blocks=4),
+    "tiered-pool": dict(TINY, batch=3, max_seq=128, n_heads=4, n_kv_heads=1, head_dim=128, d_model=512,
+                        kv_kind=2, hot_window=16, seed=0x5C09, kv_blocks=4),
 }
 
 
@@ -61,6 +67,12 @@ def test_admit_and_retire_mid_decode(ctx, kind):
     got["B"] += out[1].tolist()
     got["C"] += out[0].tolist()
     assert (out[2] == -1).all()
+    if "kv_blocks" in cfg:
+        # B holds positions 0..20 (two pages), C 0..9 (one)
+        assert gm.kv_pages() == (4, 1)
+        gm.retire(0)
+        gm.retire(1)
+        assert gm.kv_pages() == (4, 4)
     gm.close()
     for name, p in (("A", A), ("B", B), ("C", C)):
         want, margins = standalone(cfg, p, len(got[name]))
@@ -102,4 +114,51 @@ def test_scheduler_rejects_what_cannot_fit(ctx):
     with pytest.raises(nexus_amd.NxError):
         sched.submit(np.array([cfg["vocab"]], np.int32), 2)
     sched.close()
+    gm.close()
+
+
+def test_scheduler_waits_for_pool_pages(ctx):
+    """A shared pool of 8 pages under three slots: requests are admitted in
+    arrival order only while their pages to the last position fit (A 4 + B 2,
+    then C 4 waits for A), every request's tokens equal the oracle's for it
+    alone, and the pool is whole again at the end."""
+    cfg = dict(TINY, batch=3, max_seq=128, seed=0x5C0A, kv_blocks=8)
+    lens, counts = [20, 5, 30, 9, 14], [40, 20, 30, 12, 50]  # pages 4, 2, 4, 2, 4
+    ps = prompts(cfg, lens)
+    wants = [standalone(cfg, p, n) for p, n in zip(ps, counts)]
+    gm = nexus_amd.Model(ctx, **cfg)
+    sched = nexus_amd.Scheduler(gm)
+    ids = [sched.submit(p, n) for p, n in zip(ps, counts)]
+    sched.step()
+    assert gm.slot_active(0) and gm.slot_active(1) and not gm.slot_active(2)  # C waits for pages
+    sched.run()
+    for i, rid in enumerate(ids):
+        out, done = sched.result(rid)
+        assert done and len(out) == counts[i]
+        want, margins = wants[i]
+        assert_greedy_parity(out[None, :], want[None, :], margins[None, :])
+    assert gm.kv_pages() == (8, 8)
+    with pytest.raises(nexus_amd.NxError) as e:  # 9 pages: more than the pool
+        sched.submit(np.zeros(100, np.int32), 40)
+    assert e.value.code == 7
+    sched.close()
+    gm.close()
+
+
+def test_pool_exhaustion_fails_before_the_step(ctx):
+    """One sequence in a pool of 3 pages: decode to position 47 works and
+    matches the oracle; the next step needs a fourth page and fails with
+    NX_ERR_CAPACITY without running."""
+    cfg = dict(TINY, batch=1, max_seq=128, seed=0x5C0B, kv_blocks=3)
+    prompt = prompts(cfg, [10])[0]
+    want, margins = standalone(cfg, prompt, 39)
+    gm = nexus_amd.Model(ctx, **cfg)
+    first = gm.prefill(np.asarray(prompt, np.int32)[None, :])
+    got = np.concatenate([first, gm.decode(38)[0]])  # positions 10..47
+    assert gm.kv_pages() == (3, 0)
+    assert_greedy_parity(got[None, :], want[None, :], margins[None, :])
+    with pytest.raises(nexus_amd.NxError) as e:
+        gm.decode(1)
+    assert e.value.code == 7
+    assert gm.position(0) == 47
     gm.close()
