@@ -30,9 +30,13 @@ def assert_greedy_parity(got, want, margins, tie=TIE_MARGIN):
         diff = np.nonzero(got[b] != want[b])[0]
         if diff.size:
             i = int(diff[0])
+            print(f"[parity] sequence {b}: diverged at token {i} of {want.shape[1]}, oracle margin "
+                  f"{margins[b, i]:.3g}", flush=True)
             assert margins[b, i] < tie, (
                 f"sequence {b}: token {i} differs ({got[b, i]} vs {want[b, i]}) "
                 f"at oracle margin {margins[b, i]:.3g}")
+        else:
+            print(f"[parity] sequence {b}: {want.shape[1]} tokens identical", flush=True)
 
 
 def top2_margin(logits):
