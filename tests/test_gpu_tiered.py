@@ -143,12 +143,15 @@ def test_tiered_config_rejected(ctx):
 
 
 # ------------------------------------------------------------- three tiers --
-@pytest.mark.parametrize("batch,H,W", [(1, 16, 16), (2, 32, 48)])
-def test_three_tier_greedy_parity(ctx, batch, H, W):
+@pytest.mark.parametrize("batch,H,W,pool", [(1, 16, 16, 0), (2, 32, 48, 0), (2, 16, 16, 15)])
+def test_three_tier_greedy_parity(ctx, batch, H, W, pool):
     """A 12-token prompt and 100 greedy tokens: pages leave the fp16 window
     from position H + 15 on and the Warm range from H + W + 15 on, both
-    compressions on the device in the attention launch."""
-    cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, warm_window=W, seed=0x3C1 + H + W)
+    compressions on the device in the attention launch.  pool > 0: the Cool
+    table draws from a shared pool of that many pages (two sequences of 7
+    pages each)."""
+    cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, warm_window=W, seed=0x3C1 + H + W + pool,
+               kv_blocks=pool)
     got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
     assert_greedy_parity(got, want, margins, tie=TQ_TIE)
 
