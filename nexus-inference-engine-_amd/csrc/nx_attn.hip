@@ -239,9 +239,10 @@ __global__ __launch_bounds__(kAttnThreads, 1) void k_attn_f16(AttnArgs a, int ns
 // of (c4[f & 15], c4[f >> 4]), of the 3-bit table (64 entries, from entry
 // 256) those of (c3[f & 7], c3[f >> 3]), so one 8-byte lookup gives two
 // score operand values (fewer instructions than a lookup per code, which
-// needs two perms per pair, for more bank conflicts); the low 16 bits of
-// entry c are hi(c4[c]) (hi(c3[c])) for the value operand.  The V norm is
-// folded into P, the K norm and the scale into the scores.
+// needs two perms per pair, for more bank conflicts); for the value operand
+// the low 32 bits of the entry of two adjacent codes of a token, the hi
+// values of both, feed two tiles.  The V norm is folded into P, the K norm
+// and the scale into the scores.
 // Cool pages (COOL) hold 48-byte records, 3-bit codes on every dimension:
 // chunk n (dimensions 8n .. 8n+7) at byte 3n, so dimensions 0..63 form a
 // 24-byte half laid out as the 3-bit part above, 64..127 a second one.  The
@@ -398,21 +399,32 @@ __device__ inline void tq_pair_update(const TqPair& r, const TqLane& ln, const h
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         vw[j] = __builtin_amdgcn_alignbyte(r.v1[j >> 2][j & 3], r.v0[j >> 2][j & 3], ln.shift);
+    // tiles nt and nt + 1 from one pair-table lookup per token: codes nt and
+    // nt + 1 of a chunk are adjacent, and the low 32 bits of their pair's entry
+    // are (hi(c[code nt]), hi(c[code nt + 1]))
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int nt = 0; nt < 8; nt += 2) {
         uint32_t e[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = cbk[ln.cbo + __builtin_amdgcn_ubfe(vw[j], ln.bits * nt, ln.bits)].x;
-        const uint4 h = make_uint4(__builtin_amdgcn_perm(e[1], e[0], 0x05040100u),
-                                   __builtin_amdgcn_perm(e[3], e[2], 0x05040100u),
-                                   __builtin_amdgcn_perm(e[5], e[4], 0x05040100u),
-                                   __builtin_amdgcn_perm(e[7], e[6], 0x05040100u));
-        f4_t acc = o[nt];
+        for (int j = 0; j < 8; ++j) e[j] = cbk[ln.cbo + __builtin_amdgcn_ubfe(vw[j], ln.bits * nt, 2 * ln.bits)].x;
+        const uint4 h0 = make_uint4(__builtin_amdgcn_perm(e[1], e[0], 0x05040100u),
+                                    __builtin_amdgcn_perm(e[3], e[2], 0x05040100u),
+                                    __builtin_amdgcn_perm(e[5], e[4], 0x05040100u),
+                                    __builtin_amdgcn_perm(e[7], e[6], 0x05040100u));
+        const uint4 h1 = make_uint4(__builtin_amdgcn_perm(e[1], e[0], 0x07060302u),
+                                    __builtin_amdgcn_perm(e[3], e[2], 0x07060302u),
+                                    __builtin_amdgcn_perm(e[5], e[4], 0x07060302u),
+                                    __builtin_amdgcn_perm(e[7], e[6], 0x07060302u));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] *= c[i];
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, as_h8(h), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, as_h8(h), acc, 0, 0, 0);
-        o[nt] = acc;
+        for (int u = 0; u < 2; ++u) {
+            const uint4 h = u ? h1 : h0;
+            f4_t acc = o[nt + u];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] *= c[i];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, as_h8(h), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, as_h8(h), acc, 0, 0, 0);
+            o[nt + u] = acc;
+        }
     }
 }
 
