@@ -412,17 +412,29 @@ __device__ inline void mfma_compute(const MfmaRegs<XG>& r, const uint4 (&xv)[kMf
 #pragma unroll
         for (int j = 0; j < 4; ++j) code[4 * u4 + j] = o[j];
     }
-#pragma unroll
-    for (int u = 0; u < kMfmaGW; ++u) {
-        const mf4_t z = {0.f, 0.f, 0.f, 0.f};
-        const mf4_t cg = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8_t, xv[u]),
-                                                               codes_to_h8(code[u]), z, 0, 0, 0);
+    // group u's product is requested before group u - 1's is scaled and
+    // accumulated, so the conversion of u's codes, not wait states, covers
+    // the matrix core's latency
+    const mf4_t z = {0.f, 0.f, 0.f, 0.f};
+    auto product = [&](int u) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8_t, xv[u]), codes_to_h8(code[u]), z, 0,
+                                                      0, 0);
+    };
+    auto fold = [&](int u, const mf4_t& cg) {
         const uint32_t pr = r.sc[u >> 1];
         float sv = h2f_bits((uint16_t)((u & 1) ? (pr >> 16) : (pr & 0xFFFFu)));
         if (!FULL) sv *= gs + u < ge ? 1.0f : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(cg[i], sv, acc[i]);
+    };
+    mf4_t prev = product(0);
+#pragma unroll
+    for (int u = 1; u < kMfmaGW; ++u) {
+        const mf4_t cg = product(u);
+        fold(u - 1, prev);
+        prev = cg;
     }
+    fold(kMfmaGW - 1, prev);
 }
 
 // FULL: K <= 4096 and every wavefront's K slice is whole passes of 16 groups.
