@@ -120,7 +120,9 @@ nx_status nx_token_resume(nx_ctx* ctx);
 
 /* ------------------------------------------------------------------ ops -- */
 /* int4-g32 GEMV: y[b][n] = sum_k x[b][k] * (q[n][k] - 8) * s[n][k/32], fp32
- * accumulation, y stored fp16.  x fp16 [batch][K].  batch 1..8.
+ * accumulation, y stored fp16.  x fp16 [batch][K].  batch 1..8.  Any K and
+ * alignment work; batch 2..8 runs its fastest form when K % 256 == 0 (whole
+ * groups, a multiple of 8 per row) and the scales start 16-byte aligned.
  * Replaces ComputeDispatch::gemm_int4 (compute_dispatch.h:59,
  * compute_dispatch.cpp:142-176) -> MetalBackend::gemv_int4_nr8
  * (metal_backend.mm:607-642), and gemv_int4 (compute_dispatch.h:47) whose
