@@ -66,7 +66,11 @@ def _gemv_case(ctx, N, K, B, codes, scales, seed):
 
 @pytest.mark.parametrize("N,K,B", [(64, 96, 1), (256, 256, 1), (1376, 256, 1), (256, 688, 1),
                                    (256, 688, 3), (1024, 4096, 1), (4096, 4096, 2), (512, 14336, 1),
-                                   (300, 14336, 8), (130, 8192, 5)])
+                                   (300, 14336, 8), (130, 8192, 5),
+                                   # batch 2-8 scale-load forms: 16-byte loads clamped at the
+                                   # stage end (24 groups), 2-byte loads (12 groups, G % 8 != 0),
+                                   # several stages with G % 8 != 0 (132 groups)
+                                   (160, 768, 4), (200, 384, 4), (96, 4224, 6)])
 def test_gemv_parity(ctx, N, K, B):
     rng = np.random.default_rng(N + K + B)
     w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
