@@ -374,9 +374,6 @@ def main() -> int:
     ap.add_argument("--kv", choices=["fp16", "tq", "tiered"], default="fp16")
     ap.add_argument("--hot-window", type=int, default=4096,
                     help="tiered pages: positions kept fp16 (older pages TurboQuant)")
-    ap.add_argument("--layout", choices=["default", "separate"], default="default",
-                    help="separate: QKV, attention and wo as three launches per layer even where the "
-                         "fused attention block applies")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode measurement (no GEMV, NXF, prefill or tiering lines)")
@@ -436,8 +433,6 @@ def main() -> int:
     print(f"[bench] device {ctx.device_name()}; building {args.model}-shaped model "
           f"(batch {args.batch}, ctx {args.ctx}, kv {args.kv})", file=sys.stderr, flush=True)
     model = nexus_amd.Model(ctx, **cfg)
-    if args.layout == "separate":
-        model.set_fused(False)
     model.fill_context(args.ctx, 4 if kv_kind else 0)
     if args.profile_kernel:
         model.decode_untimed(1)

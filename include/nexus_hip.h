@@ -53,7 +53,7 @@ typedef int nx_status;
 #define NX_ERR_STATE 5        /* call out of order (e.g. token_end without begin) */
 #define NX_ERR_NO_DEVICE 6    /* no usable gfx950 device */
 #define NX_ERR_CAPACITY 7     /* sequence or cache capacity exhausted */
-#define NX_ERR_TIMEOUT 8      /* a hand-off between the blocks of one launch timed out; outputs invalid */
+#define NX_ERR_TIMEOUT 8      /* reserved: a wait inside a launch timed out (no entry point waits inside a launch) */
 
 typedef struct nx_ctx nx_ctx;
 typedef uint64_t nx_buf; /* 0 = none */
@@ -376,16 +376,6 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
  * HybridModel::prefill loop, hybrid_model.cpp:604-644).  MoE and
  * TurboQuant-page models always prefill one token per step. */
 nx_status nx_model_set_prefill(nx_model* m, int batched);
-/* Decode-step layout of the attention half of each layer: 0 (the default)
- * = QKV, paged attention and the output projection as one launch each (the
- * reference's per-op dispatch order, hybrid_model.cpp:1257-1443); 1 = the
- * three in one launch whose blocks hand their results to each other inside
- * the launch (batch 1, fp16 pages, head_dim 64 or 128, d_model and
- * n_heads * head_dim at most 4096, max_seq within the device's plan;
- * NX_ERR_UNSUPPORTED otherwise).  Both give the same tokens; a step of the
- * fused form whose in-launch hand-off times out makes nx_model_decode /
- * nx_model_prefill return NX_ERR_TIMEOUT. */
-nx_status nx_model_set_fused(nx_model* m, int on);
 /* The configuration the model was created with. */
 nx_status nx_model_get_config(nx_model* m, nx_model_config* out);
 /* The context the model runs on. */
@@ -424,7 +414,9 @@ nx_status nx_sched_step(nx_sched* s, int* n_active, int* n_waiting);
 /* Rounds until no request is waiting or active. */
 nx_status nx_sched_run(nx_sched* s);
 /* The tokens of request id so far (up to cap into out), their number and
- * whether the request is complete. */
+ * whether the request is complete.  A request whose admission failed (the
+ * nx_sched_step that tried it returned the error) is complete with no tokens,
+ * and this call returns that admission's status. */
 nx_status nx_sched_result(nx_sched* s, int id, int32_t* out, int cap, int* n, int* done);
 /* Sampling of the decode loop (SamplingParams, core/config.h:60-66):
  * temperature <= 0 = greedy (the default); otherwise every step samples

@@ -24,13 +24,6 @@ namespace {
 
 using namespace at;
 
-#ifdef NX_LAYER_TRACE
-__device__ unsigned long long g_attn_trace[1024 * 8];
-#define NX_ATRACE(i) \
-    if (threadIdx.x == 0) g_attn_trace[(blockIdx.x + gridDim.x * blockIdx.y) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
-#else
-#define NX_ATRACE(i)
-#endif
 
 
 struct SplitPlan {
@@ -81,7 +74,6 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
-    NX_ATRACE(0);
     attn_args_early(a);
     asm volatile("" ::"s"(a.kpool), "s"(a.vpool), "s"(nsplit));
 
@@ -141,7 +133,6 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
         }
     }
     const float scale = 1.0f / sqrtf((float)HD);
-    NX_ATRACE(1);
 
     const int npages = (ctx + kPage - 1) / kPage;
     // pages of this wavefront: first + stride * i for i < npw, taken in pairs
@@ -173,7 +164,6 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
             pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
         }
     }
-    NX_ATRACE(2);
     // the head's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
@@ -193,7 +183,6 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
     // every thread's record stores are complete before the block counts itself
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    NX_ATRACE(3);
     __shared__ int last;
     if (threadIdx.x == 0) {
         unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
@@ -202,10 +191,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
         if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    NX_ATRACE(4);
     if (last) merge_last<G, HD, TIER>(a, nrec, ntq, kvh, b);
-    if (last) NX_ATRACE(5);
-    NX_ATRACE(6);
 }
 
 // PIPE: more than one page pair per wavefront, two pairs in flight;
@@ -505,7 +491,6 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     __shared__ float qrot[G * HD];
     __shared__ uint2 cbk[kTqTbl];
 
-    NX_ATRACE(0);
     attn_args_early(a);
     asm volatile("" ::"s"(a.kc4), "s"(a.kc3), "s"(a.vc4), "s"(a.vc3), "s"(a.kn), "s"(a.vn), "s"(a.ksign),
                  "s"(a.vsign), "s"(nsplit), "s"(pps));
@@ -584,7 +569,6 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
         }
     }
     const float scale = kTqScale / sqrtf((float)HD);  // rotation normalisation and 1/sqrt(hd)
-    NX_ATRACE(1);
 
     float m = -__builtin_inff(), lsum = 0.0f;
     f4_t o[8];
@@ -612,7 +596,6 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     } else {
         if (npw > 0) upd(r0, 0);
     }
-    NX_ATRACE(2);
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     // wavefront record: rows h = 4g + i < G of O (column t of tile nt is
@@ -633,7 +616,6 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     // the last of the nrec blocks merges, rotates back and resets the counter
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    NX_ATRACE(3);
     __shared__ int last;
     if (threadIdx.x == 0) {
         unsigned* cnt = a.counts + ((size_t)b * a.hkv + kvh) * kAttnCountStride;
@@ -642,10 +624,7 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
         if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    NX_ATRACE(4);
     if (last) merge_last<G, HD, true>(a, nrec, ntq, kvh, b);
-    if (last) NX_ATRACE(5);
-    NX_ATRACE(6);
 }
 
 // With kv_cur the last block of each (sequence, kv head) takes the position
@@ -1246,11 +1225,6 @@ hipError_t zero_u32_launch(unsigned* p, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
-#ifdef NX_LAYER_TRACE
-extern "C" int nx_debug_attn_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_attn_trace), sizeof(unsigned long long) * 1024 * 8);
-}
-#endif
 
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     if (!a.counts || !a.part) return hipErrorInvalidValue;

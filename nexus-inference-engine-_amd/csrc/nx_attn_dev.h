@@ -1,8 +1,7 @@
-// Device building blocks of paged decode attention shared by the split
-// kernels (nx_attn.hip) and the fused attention block (nx_layer.hip): split
-// records and their merge, the fp16 page-pair product on the matrix cores,
-// and the agent-scope (cross-XCD coherent) accesses used for hand-offs
-// between blocks of one launch.
+// Device building blocks of the paged decode attention kernels (nx_attn.hip):
+// split records and their merge, the fp16 page-pair product on the matrix
+// cores, and the agent-scope (cross-XCD coherent) accesses used for the
+// hand-off of split records to the merging block of the same launch.
 #pragma once
 
 #include "nx_common.h"
@@ -27,13 +26,6 @@ __device__ inline void st_coh(float* p, float v) {
 __device__ inline float ld_coh(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline void st_coh_u32(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void st_coh_u16(uint16_t* p, uint16_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // The arguments a split block reads first, requested together from the
 // argument segment (the compiler would otherwise fetch them in several
 // dependent rounds as each is first needed).
@@ -304,9 +296,7 @@ constexpr float kTqScale = 0.08838834764831845f;  // float(1/sqrt(128))
 // them for TurboQuant pages, the compressed part for tiered pages); their
 // merged sum is rotated back (o = D_v H o~ / sqrt(128), an FWHT in LDS) and
 // added to the merged sum of the fp16 records [ntq, nsplit).
-// COH_OUT: the output is stored with agent-scope stores (read by other
-// blocks of the same launch).
-template <int G, int HD, bool TQ = false, bool COH_OUT = false>
+template <int G, int HD, bool TQ = false>
 __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kvh, int b) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
     constexpr int NC = G * HD / 4, NG = kAttnThreads / NC;
@@ -417,13 +407,7 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
     } else if (tid < NC) {
         const uint32_t w0 = (uint32_t)f2h_bits(r.x) | ((uint32_t)f2h_bits(r.y) << 16);
         const uint32_t w1 = (uint32_t)f2h_bits(r.z) | ((uint32_t)f2h_bits(r.w) << 16);
-        if constexpr (COH_OUT) {  // read by other blocks of the same launch
-            uint32_t* o32 = reinterpret_cast<uint32_t*>(out + 4 * tid);
-            st_coh_u32(o32, w0);
-            st_coh_u32(o32 + 1, w1);
-        } else {
-            *reinterpret_cast<uint2*>(out + 4 * tid) = make_uint2(w0, w1);
-        }
+        *reinterpret_cast<uint2*>(out + 4 * tid) = make_uint2(w0, w1);
     }
 }
 

@@ -85,19 +85,6 @@ __global__ __launch_bounds__(WPB * kWave, 1) void k_gemv_b1(GemvArgs a, RowSplit
 typedef _Float16 mh8_t __attribute__((ext_vector_type(8)));
 typedef float mf4_t __attribute__((ext_vector_type(4)));
 
-#ifdef NX_LAYER_TRACE
-// phase timestamps of the batch-2..8 GEMV per (epilogue, input) kind, block
-// (< 256) and phase: entry, x staged, first item computed, first tile done,
-// items done, exit
-__device__ unsigned long long g_mfma_trace[16 * 256 * 8];
-#define NX_MTRACE_K(key, i) \
-    if (threadIdx.x == 0 && blockIdx.x < 256 && blockIdx.y == 0 && (key) >= 0) \
-        g_mfma_trace[((key) * 256 + blockIdx.x) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
-#define NX_MTRACE(i) NX_MTRACE_K(EPI * 2 + XS, i)
-#else
-#define NX_MTRACE_K(key, i)
-#define NX_MTRACE(i)
-#endif
 
 constexpr int kMfmaWaves = 8;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
@@ -191,10 +178,9 @@ __device__ inline void stage_issue(const GemvArgs& a, int k0, int gc, StageRegs<
 // values, reduced through LDS in red) convert and store the entries.
 template <int XS, bool NORM>
 __device__ inline void stage_finish(const GemvArgs& a, int k0, int gc, StageRegs<XS>& r, uint4* xs, float* inv,
-                                    float (*red)[kMfmaCols], [[maybe_unused]] int tkey = -1) {
+                                    float (*red)[kMfmaCols]) {
     const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
     const bool has_w = a.norm_w != nullptr;
-    NX_MTRACE_K(tkey, 6);
     if (XS == X_RMSNORM && NORM) {
         // a thread's entries all belong to batch row tid % kMfmaCols
         float ss = 0.0f;
@@ -219,7 +205,6 @@ __device__ inline void stage_finish(const GemvArgs& a, int k0, int gc, StageRegs
             inv[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
         }
         __syncthreads();
-        NX_MTRACE_K(tkey, 7);
     }
 #pragma unroll
     for (int j = 0; j < kMfmaEPT; ++j) {
@@ -254,12 +239,12 @@ __device__ inline void stage_finish(const GemvArgs& a, int k0, int gc, StageRegs
 // through LDS in red), so the input costs one round trip.
 template <int XS, bool XVEC, bool NORM = false>
 __device__ inline void mfma_stage_x(const GemvArgs& a, int k0, int gc, uint4* xs, float* inv,
-                                    float (*red)[kMfmaCols] = nullptr, int xrow = -1, int tkey = -1) {
+                                    float (*red)[kMfmaCols] = nullptr, int xrow = -1) {
     const int tid = threadIdx.x, K = a.K, ne = gc * 4 * kMfmaCols, nb = a.batch;
     if (XVEC) {
         StageRegs<XS> r;
         stage_issue<XS>(a, k0, gc, r, xrow);
-        stage_finish<XS, NORM>(a, k0, gc, r, xs, inv, red, tkey);
+        stage_finish<XS, NORM>(a, k0, gc, r, xs, inv, red);
         return;
     }
     for (int e = tid; e < ne; e += kMfmaThreads) {
@@ -445,7 +430,6 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     __shared__ float inv[kMfmaCols];
     __shared__ float red[kMfmaWaves][kMfmaCols];
     __shared__ unsigned long long bk[kMfmaThreads];
-    NX_MTRACE(0);
     // The arguments the prologue uses, requested together: the compiler
     // would otherwise fetch them from the argument segment in several
     // dependent rounds as each is first needed.
@@ -471,8 +455,12 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     // the nb blocks of a grid row share the tiles evenly: block x takes
     // [x ntile / nb, (x + 1) ntile / nb), at most tpb tiles
     const int ntile = (N + 15) / 16, tpb = (ntile + nb - 1) / nb;
-    // (bx + 1) * ntile < 2^31: ntile <= 8192 tiles, nb <= 65536 blocks
-    const int t0 = (int)((unsigned)(bx * ntile) / (unsigned)nb), nt = (int)((unsigned)((bx + 1) * ntile) / (unsigned)nb) - t0;
+    // 32-bit tile arithmetic: either a block per tile (nb == ntile, the
+    // several-stage path) or nb at most the launcher's block count of one
+    // round (<= 2^10) with ntile <= 2^20 (N <= 2^24), so (bx + 1) * ntile < 2^30
+    const bool one = nb == ntile;
+    const int t0 = one ? bx : (int)((unsigned)(bx * ntile) / (unsigned)nb);
+    const int nt = one ? 1 : (int)((unsigned)((bx + 1) * ntile) / (unsigned)nb) - t0;
     if (nt <= 0 || Gx <= 0) return;
     static_assert(!MOE || XS == X_F16, "routed experts take fp16 x");
     GemvArgs a = args;
@@ -494,7 +482,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     // row); run by the streaming loop after its first weight requests
     auto stage_input = [&]() {
         if (XS == X_RMSNORM && XVEC && nstage == 1) {
-            mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red, xrow, EPI * 2 + XS);
+            mfma_stage_x<XS, XVEC, true>(a, 0, (K + 31) / 32, xs, inv, red, xrow);
         } else if (XS == X_RMSNORM) {
             // sum of h^2 per batch row over all of K
             float ss[kMfmaCols];
@@ -523,7 +511,6 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
         if (nstage == 1 && !(XS == X_RMSNORM && XVEC))
             mfma_stage_x<XS, XVEC>(a, 0, (K + 31) / 32, xs, inv, nullptr, xrow);
         if (nstage == 1) __syncthreads();  // x staged
-        NX_MTRACE(1);
     };
     float best_v = -__builtin_inff();
     int best_i = -1;
@@ -614,9 +601,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             load_item(0, ra);
             load_item(1, rb);
             __builtin_amdgcn_sched_barrier(0);
-            stage_finish<XS, XS == X_RMSNORM>(a, 32 * gbase0, Gx, sr, xs, inv, red, EPI * 2 + XS);
+            stage_finish<XS, XS == X_RMSNORM>(a, 32 * gbase0, Gx, sr, xs, inv, red);
             __syncthreads();  // x staged
-            NX_MTRACE(1);
         } else {
             stage_input();
             load_item(0, ra);
@@ -639,10 +625,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
                 mfma_load_x<FULL>(xs, min(gs, G - 1), ge, xv);
             }
             mfma_compute<FULL, XG>(r, xv, gs, ge, acc);
-            if (j == 0) NX_MTRACE(2);
             if (j % npass == npass - 1) {
                 tile_end(j, acc);
-                if (j == npass - 1) NX_MTRACE(3);
                 acc = mf4_t{0.f, 0.f, 0.f, 0.f};
             }
         };
@@ -682,10 +666,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     };
     if (nstage == 1) {
         stream(std::integral_constant<bool, false>{});
-        NX_MTRACE(4);
     } else if constexpr (kXG) {
         stream(std::integral_constant<bool, true>{});
-        NX_MTRACE(4);
     } else {
         stage_input();
         // K in several stages: x restaged per stage
@@ -720,7 +702,6 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
             if (m) atomicMax(&a.best[tid], m);
         }
     }
-    NX_MTRACE(5);
 }
 
 // Batch 1: a persistent grid of WPB wavefronts per CU in one block each
@@ -831,8 +812,10 @@ hipError_t post_norm_launch(const GemvArgs& a, hipStream_t st) {
 // MOE: ny grid rows of routed experts share the CUs.
 template <int XS, int EPI, bool MOE = false>
 hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
-    if (a.N > (1 << 24)) return hipErrorInvalidValue;  // the kernel's 32-bit tile arithmetic
+    // the kernel's 32-bit tile arithmetic: N <= 2^24, and a grid of one
+    // round has at most 2^10 blocks per row (or one block per tile)
     const int ntile = (a.N + 15) / 16, cus = device_cus();
+    if (a.N > (1 << 24) || cus > (1 << 10)) return hipErrorInvalidValue;
     const void* x = XS == X_F16 ? static_cast<const void*>(a.x16) : static_cast<const void*>(a.h32);
     const bool xvec = a.K % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       a.ldx % (XS == X_F16 ? 8 : 4) == 0;
@@ -932,14 +915,6 @@ hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
 
 }  // namespace
 
-#ifdef NX_LAYER_TRACE
-extern "C" int nx_debug_gemv_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(gv::g_gemv_trace), sizeof(unsigned long long) * 64 * 256 * 8);
-}
-extern "C" int nx_debug_mfma_trace(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_mfma_trace), sizeof(unsigned long long) * 16 * 256 * 8);
-}
-#endif
 
 hipError_t gemv_launch(int xsrc, int epi, const GemvArgs& a, hipStream_t st) {
     if (a.batch < 1 || a.batch > 8) return hipErrorInvalidValue;

@@ -9,15 +9,6 @@
 namespace nx {
 namespace gv {
 
-#ifdef NX_LAYER_TRACE
-// phase timestamps of the batch-1 GEMV, per (epilogue, groups per lane) kind
-__device__ unsigned long long g_gemv_trace[64 * 256 * 8];
-#define NX_GTRACE(key, i) \
-    if (threadIdx.x == 0 && blockIdx.x < 256) \
-        g_gemv_trace[((key) * 256 + blockIdx.x) * 8 + (i)] = __builtin_amdgcn_s_memrealtime()
-#else
-#define NX_GTRACE(key, i)
-#endif
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockThreads = kWavesPerBlock * kWave;
@@ -606,8 +597,6 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     __shared__ __align__(16) uint32_t sp[kWave * GPL * 16];
     __shared__ float s8[kWave * GPL];
     __shared__ float red[WPB];
-    [[maybe_unused]] constexpr int TKEY = EPI * 8 + (GPL & 7);
-    NX_GTRACE(TKEY, 0);
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = block * WPB + (threadIdx.x >> 6);
     int r0, r1;
@@ -624,7 +613,6 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     // ahead of every weight tile, so x arrives after one round trip instead
     // of behind the first tiles of all the other wavefronts.
     if (WPB > kWavesPerBlock) __syncthreads();
-    NX_GTRACE(TKEY, 1);
     Tile<GPL, R> t[DEPTH];
     if (!XFIRST) {
 #pragma unroll
@@ -641,9 +629,7 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
         }
         if (a.kpool) qblk = a.block_table[qp / kPage];
     }
-    NX_GTRACE(TKEY, 2);
     stage_finish<CPT, XS, NT>(a, sr, sp, s8, red);  // block barrier: every wavefront takes part
-    NX_GTRACE(TKEY, 3);
     // XFIRST: the first tiles are requested only once x is staged (x then
     // arrives without weight traffic queued beside it)
     if (XFIRST) {
@@ -678,11 +664,9 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
                     }
                 }
                 if (lane == 0) epilogue<EPI, R>(a, 0, r0 + (i + j) * R, r1, res, best_v, best_i, &pre);
-                if (i + j == 0) NX_GTRACE(TKEY, 4);
             }
         }
     }
-    NX_GTRACE(TKEY, 5);
     if (EPI == E_LOGITS) {
         // one atomic per block: the wavefronts' maxima meet in LDS first
         __shared__ unsigned long long bk[WPB];

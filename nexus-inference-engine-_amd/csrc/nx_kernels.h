@@ -26,12 +26,6 @@ enum Epi : int {
     E_PART = 6,     // kpart[part][b][n] = partial sum over the block's K part
 };
 
-// Row pairs per wavefront of a batch-1 GEMV: base pairs each, one more for
-// the first `extra` wavefronts.
-struct gv_rowsplit_t {
-    int base, extra;
-};
-
 struct GemvArgs {
     const uint8_t* W;       // [N][G*16]
     const uint16_t* S;      // [N][G]
@@ -269,8 +263,6 @@ void tq_set_codebooks(const float* c4, const float* b4, const float* c3, const f
 // h[b] = fp32(embed[tok]).
 // The token consumed at new position p is recorded at out_tokens[b][p - base[b] - 1]
 // when that index is in [0, out_stride).
-// epoch (optional): a step counter the embedding kernel increments once per
-// launch; the fused attention block counts its hand-offs against it.
 // feed (optional, [batch]): what each sequence slot consumes at this step --
 // kFeedDecode its pending token (recorded as output), a token id >= 0 (a
 // prompt token, not recorded), kFeedPark (a free slot: token 0 at position
@@ -280,8 +272,8 @@ void tq_set_codebooks(const float* c4, const float* b4, const float* c3, const f
 constexpr int kFeedDecode = -1, kFeedPark = -2, kFeedHold = -3;
 hipError_t embed_launch(unsigned long long* best, int32_t* pos, const int32_t* base,
                         int32_t* out_tokens, int out_stride, const uint16_t* embed, float* h,
-                        int d, int vocab, int batch, hipStream_t st, unsigned* epoch = nullptr,
-                        const int32_t* feed = nullptr, const int32_t* fpos = nullptr);
+                        int d, int vocab, int batch, hipStream_t st, const int32_t* feed = nullptr,
+                        const int32_t* fpos = nullptr);
 // Record the pending tokens (decoded from best) at out_tokens[b][pos[b] - base[b]].
 hipError_t finish_tokens_launch(const unsigned long long* best, const int32_t* pos,
                                 const int32_t* base, int32_t* out_tokens, int out_stride,
@@ -396,34 +388,6 @@ hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st);
 // The reference's draw for a seed: std::uniform_real_distribution<float>(0, 1)
 // of the first output of std::mt19937(seed) (seed 0: std::random_device).
 float sample_draw(uint64_t seed);
-
-// ------------------------------------------------ fused attention block --
-// One decoder layer's attention half at batch 1 over fp16 pages in one
-// launch of one block per CU (nx_layer.hip): RMSNorm + QKV GEMV + RoPE + page
-// write, paged attention (round-robin page splits, last-block merge) and the
-// output projection with the residual add.  Every block requests its QKV
-// rows, its KV pages and its wo rows at the start; blocks hand q / k / v and
-// the attention output to each other through agent-scope stores and
-// counters.  Counters count up across steps: a wait for n arrivals per step
-// waits for n * epoch, epoch being the step count the embedding kernel keeps.
-struct LayerArgs {
-    GemvArgs qkv;             // X_RMSNORM -> E_QKV (N = qdim + 2 kvdim rows, batch 1)
-    GemvArgs wo;              // x16 = the attention output, y32 = h (residual add)
-    AttnArgs at;              // q, pages, block table, pos, out16, part, counts
-    unsigned* sync;           // this layer's counters, kAttnCountStride words apart:
-                              // [g] kv head g's QKV rows written, [hkv] heads merged
-    const unsigned* epoch;
-    unsigned* err;            // set to 1 by a wait that times out
-    int nsplit;               // attention splits per kv head (blocks [0, nsplit * hkv))
-    int qkv_pairs;            // QKV row pairs per block (<= 16)
-    gv_rowsplit_t wo_rows;    // wo row pairs per wavefront (base, extra); at most one
-    int qkv_expect[32];       // blocks writing rows of each kv head
-};
-// Whether the fused attention block runs this shape on this device (batch 1,
-// fp16 pages, hq/hkv in {1,2,4,8}, head_dim 64 or 128, d_model and hq*hd at
-// most 4096, contexts up to max_ctx), and its plan.
-bool attn_block_b1_plan(int d, int hq, int hkv, int hd, int max_ctx, LayerArgs& plan);
-hipError_t attn_block_b1_launch(const LayerArgs& a, hipStream_t st);
 
 // fp32 GEMM C[M][N] = A[M][K] B[K][N], row-major, on the matrix cores (nx_gemm.hip).
 hipError_t gemm_f32_launch(const float* A, const float* B, float* C, int M, int N, int K, hipStream_t st);

@@ -247,11 +247,9 @@ __global__ void k_gen_ctx_raw(float* dst, int ctx, int hkv, int hd, uint64_t key
 __global__ __launch_bounds__(256) void k_embed(unsigned long long* best, int32_t* pos,
                                                const int32_t* base, int32_t* out_tokens,
                                                int out_stride, const uint16_t* embed, float* h,
-                                               int d, int vocab, unsigned* epoch, const int32_t* feed,
-                                               const int32_t* fpos) {
+                                               int d, int vocab, const int32_t* feed, const int32_t* fpos) {
     __shared__ int tok_s;
     const int b = blockIdx.x;
-    if (b == 0 && threadIdx.x == 0 && epoch) *epoch += 1u;
     if (threadIdx.x == 0) {
         const int f = feed ? feed[b] : kFeedDecode;
         int tok, p;
@@ -709,10 +707,10 @@ hipError_t gen_ctx_raw_launch(float* dst, int ctx, int hkv, int hd, int L, int b
 
 hipError_t embed_launch(unsigned long long* best, int32_t* pos, const int32_t* base,
                         int32_t* out_tokens, int out_stride, const uint16_t* embed, float* h,
-                        int d, int vocab, int batch, hipStream_t st, unsigned* epoch, const int32_t* feed,
+                        int d, int vocab, int batch, hipStream_t st, const int32_t* feed,
                         const int32_t* fpos) {
     hipLaunchKernelGGL(k_embed, dim3(batch), dim3(256), 0, st, best, pos, base, out_tokens,
-                       out_stride, embed, h, d, vocab, epoch, feed, fpos);
+                       out_stride, embed, h, d, vocab, feed, fpos);
     return hipGetLastError();
 }
 

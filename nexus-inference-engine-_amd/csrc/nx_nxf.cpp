@@ -161,8 +161,12 @@ struct JsonValue {
 
 // Tokenizer of one flat JSON object, {"key": value, ...} with string or
 // number values, into (key, value) pairs in file order.  Standard JSON
-// (RFC 8259) for those two kinds; nested objects, arrays, literals and
-// trailing commas are rejected.
+// (RFC 8259) for those two kinds, with the reference reader's leniencies
+// (format/nxf_reader.cpp:75-180) where files of the reference writer need
+// them: raw control bytes inside strings (its escaper, nxf_writer.cpp:76-89,
+// writes \r and the other control bytes unescaped) and anything after the
+// closing brace.  Nested objects, arrays, literals and trailing commas are
+// rejected.
 class FlatJson {
   public:
     FlatJson(const char* data, size_t len) : s_(data), n_(len) {}
@@ -206,10 +210,8 @@ class FlatJson {
         }
         return false;
     }
-    bool at_end() {
-        skip_ws();
-        return i_ == n_ || (i_ + 1 == n_ && s_[i_] == '\0');
-    }
+    // the object is complete at its closing brace; what follows is ignored
+    bool at_end() { return true; }
     static int hex(char c) {
         if (c >= '0' && c <= '9') return c - '0';
         if (c >= 'a' && c <= 'f') return c - 'a' + 10;
@@ -223,8 +225,7 @@ class FlatJson {
         while (i_ < n_) {
             const char c = s_[i_++];
             if (c == '"') return true;
-            if ((unsigned char)c < 0x20) return false;
-            if (c != '\\') {
+            if (c != '\\') {  // raw bytes, control bytes included, are taken as they are
                 out += c;
                 continue;
             }
@@ -306,9 +307,10 @@ const ManifestField kManifestFields[] = {
 #undef NX_MF
 
 // Store one value into its field: text into a string field (truncated to
-// the field), a number into a numeric field.  Integer fields take integral
-// values in [0, 2^32 - 1] (bytes: [0, 255]); floats any finite value that
-// rounds to a finite float.  Anything else rejects the manifest.
+// the field), a number into a numeric field (default_codec also as quoted
+// text).  Integer fields take integral values in [0, 2^32 - 1] (bytes:
+// [0, 255]); floats any finite value that rounds to a finite float.
+// Anything else rejects the manifest.
 bool assign_field(nx_nxf_manifest& m, const ManifestField& f, const JsonValue& v) {
     char* dst = reinterpret_cast<char*>(&m) + f.offset;
     if (f.kind == FieldKind::Text) {
@@ -318,20 +320,34 @@ bool assign_field(nx_nxf_manifest& m, const ManifestField& f, const JsonValue& v
         dst[k] = 0;
         return true;
     }
-    if (v.is_str || !std::isfinite(v.num)) return false;
+    double num = v.num;
+    if (v.is_str) {
+        // a quoted default_codec is read as the reference reader reads it
+        // (atoi of the text, format/nxf_reader.cpp:162): leading spaces, an
+        // optional sign and the digits that follow; no digits read as 0
+        if (strcmp(f.key, "default_codec") != 0) return false;
+        const char* t = v.str.c_str();
+        while (*t == ' ' || (*t >= '\t' && *t <= '\r')) ++t;
+        const bool neg = *t == '-';
+        if (*t == '-' || *t == '+') ++t;
+        num = 0.0;
+        for (int k = 0; *t >= '0' && *t <= '9' && k < 12; ++t, ++k) num = num * 10.0 + (*t - '0');
+        if (neg) num = -num;
+    }
+    if (!std::isfinite(num)) return false;
     if (f.kind == FieldKind::F32) {
-        const float x = (float)v.num;
+        const float x = (float)num;
         if (!std::isfinite(x)) return false;
         memcpy(dst, &x, sizeof(x));
         return true;
     }
     const double hi = f.kind == FieldKind::U8 ? 255.0 : 4294967295.0;
-    if (v.num < 0.0 || v.num > hi || v.num != std::floor(v.num)) return false;
+    if (num < 0.0 || num > hi || num != std::floor(num)) return false;
     if (f.kind == FieldKind::U8) {
-        const uint8_t x = (uint8_t)v.num;
+        const uint8_t x = (uint8_t)num;
         memcpy(dst, &x, 1);
     } else {
-        const uint32_t x = (uint32_t)v.num;
+        const uint32_t x = (uint32_t)num;
         memcpy(dst, &x, 4);
     }
     return true;

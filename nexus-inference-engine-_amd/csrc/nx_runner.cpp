@@ -121,15 +121,6 @@ struct nx_model {
     float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
     int top_k = 0;
     float* smp_scratch = nullptr;  // [batch][vocab], allocated when sampling is first set
-    // fused attention block (batch 1, fp16 pages): QKV, attention and wo of a
-    // layer in one launch (nx_layer.hip); counters per layer, the step count
-    // the embedding kernel keeps, and the error word of a timed-out wait
-    bool fused_ok = false;         // the shape and device allow it
-    bool fused = false;            // in use
-    nx::LayerArgs lplan{};
-    unsigned* lsync = nullptr;     // [n_layers][hkv + 1][kAttnCountStride]
-    unsigned* lstate = nullptr;    // [0] epoch, [64] error word
-    unsigned* h_err = nullptr;     // pinned host copy of the error word
     // per-slot serving state: a slot holds one sequence (active) or none
     // (free: parked at position 0 by the step graph); feed / fpos tell the
     // embedding kernel what each slot consumes at a step (kFeed*)
@@ -420,42 +411,6 @@ nx_status pool_release(nx_model* m, int b) {
     return NX_OK;
 }
 
-// QKV, attention and wo of layer L as one launch (batch 1, fp16 pages).
-hipError_t fused_attention_launch(nx_model* m, int L, hipStream_t st) {
-    const Layer& ly = m->layers[L];
-    nx::LayerArgs a = m->lplan;
-    a.qkv = qkv_args(m, ly);
-    a.wo = wo_args(m, ly);
-    a.at = attn_args(m, ly);
-    a.sync = m->lsync + (size_t)L * (m->c.n_kv_heads + 1) * nx::kAttnCountStride;
-    a.epoch = m->lstate;
-    a.err = m->lstate + 64;
-    return nx::attn_block_b1_launch(a, st);
-}
-
-// Zero the fused block's counters, step count and error word (stream
-// ordered: before the next step that uses them).
-nx_status reset_fused_state(nx_model* m) {
-    if (!m->lsync) return NX_OK;
-    const size_t words = (size_t)m->c.n_layers * (m->c.n_kv_heads + 1) * nx::kAttnCountStride;
-    NX_HIP(m->ctx, hipMemsetAsync(m->lsync, 0, words * 4, m->ctx->stream));
-    NX_HIP(m->ctx, hipMemsetAsync(m->lstate, 0, 128 * 4, m->ctx->stream));
-    return NX_OK;
-}
-
-// After a synchronized run of steps: a wait of the fused block that timed
-// out (a block was not resident, or a hand-off never came) leaves the error
-// word set; the outputs of those steps are not to be used.
-nx_status check_fused_state(nx_model* m) {
-    if (!m->fused) return NX_OK;
-    NX_HIP(m->ctx, hipMemcpyAsync(m->h_err, m->lstate + 64, 4, hipMemcpyDeviceToHost, m->ctx->stream));
-    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
-    if (*m->h_err == 0u) return NX_OK;
-    NX_TRY(reset_fused_state(m));
-    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
-    return fail(m->ctx, NX_ERR_TIMEOUT, "fused attention block: a wait between blocks timed out; the step's outputs are invalid");
-}
-
 // What each slot consumes at the following steps: feed[b] (a kFeed* mode or
 // a token id) and fpos[b] (the position of a held slot); stream ordered.
 nx_status upload_feed(nx_model* m, const int32_t* feed, const int32_t* fpos) {
@@ -507,13 +462,11 @@ nx_status enqueue_step(nx_model* m) {
     hipStream_t st = m->ctx->stream;
     const int B = c.batch, d = c.d_model, F = c.ffn, E = c.n_experts;
     NX_LAUNCH(m, nx::embed_launch(m->best, m->pos, m->base, m->out_tokens, m->out_stride, m->embed, m->h, d,
-                                  c.vocab, B, st, m->fused ? m->lstate : nullptr, m->feed, m->fpos));
+                                  c.vocab, B, st, m->feed, m->fpos));
     bool xn_ready = false;  // m->xn16 holds RMSNorm(h) for the next RMSNorm-input GEMV
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
-        if (m->fused) {
-            NX_LAUNCH(m, fused_attention_launch(m, L, st));
-        } else {
+        {
             // RMSNorm + QKV + RoPE + paged KV append, attention, wo + residual
             NX_LAUNCH(m, norm_gemv_launch(m, nx::E_QKV, qkv_args(m, ly), st, xn_ready));
             NX_LAUNCH(m, attention_launch(m, ly, st));
@@ -689,7 +642,6 @@ nx_status free_model(nx_model* m) {
     for (void* p : m->allocs) (void)hipFree(p);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
     if (m->h_out) (void)hipHostFree(m->h_out);
-    if (m->h_err) (void)hipHostFree(m->h_err);
     if (m->h_feed) (void)hipHostFree(m->h_feed);
     delete m;
     return NX_OK;
@@ -886,14 +838,6 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     NX_TRY(feed_decode(m));
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_stage, sizeof(int32_t) * B, hipHostMallocDefault));
     NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_out, sizeof(int32_t) * (size_t)B * m->out_stride, hipHostMallocDefault));
-    // the fused attention block where the shape allows it (on by default)
-    if (B == 1 && c.kv_kind == 0 &&
-        nx::attn_block_b1_plan(d, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq, m->lplan)) {
-        NX_TRY(dalloc(m, &m->lsync, (size_t)c.n_layers * (c.n_kv_heads + 1) * nx::kAttnCountStride));
-        NX_TRY(dalloc(m, &m->lstate, 128));
-        NX_HIP(m->ctx, hipHostMalloc((void**)&m->h_err, sizeof(unsigned), hipHostMallocDefault));
-        m->fused_ok = true;
-    }
     if (synthetic) NX_TRY(generate_weights(m));
     NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     return NX_OK;
@@ -1220,22 +1164,6 @@ nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float
     return NX_OK;
 }
 
-nx_status nx_model_set_fused(nx_model* m, int on) {
-    if (!m || (on != 0 && on != 1)) return NX_ERR_INVALID;
-    if (on && !m->fused_ok) return fail(m->ctx, NX_ERR_UNSUPPORTED, "the fused attention block does not run this model");
-    if ((bool)on == m->fused) return NX_OK;
-    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
-    if (m->exec) (void)hipGraphExecDestroy(m->exec);
-    if (m->exec_multi) (void)hipGraphExecDestroy(m->exec_multi);
-    m->exec = nullptr;
-    m->exec_multi = nullptr;
-    m->fused = on != 0;
-    // counters and step count restart together
-    NX_TRY(reset_fused_state(m));
-    NX_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
-    return NX_OK;
-}
-
 nx_status nx_model_set_prefill(nx_model* m, int batched) {
     if (!m || (batched != 0 && batched != 1)) return NX_ERR_INVALID;
     m->prefill_batched = batched;
@@ -1282,7 +1210,6 @@ nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* n
     std::vector<unsigned long long> best(B);
     NX_HIP(m->ctx, hipMemcpyAsync(best.data(), m->best, (size_t)B * 8, hipMemcpyDeviceToHost, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
-    NX_TRY(check_fused_state(m));
     for (int b = 0; b < B; ++b) {
         m->hpos[b] += P;
         if (next_tokens) next_tokens[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)(best[b] & 0xFFFFFFFFull));
@@ -1458,7 +1385,6 @@ nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens) {
     if (out_tokens)
         NX_HIP(m->ctx, hipMemcpyAsync(m->h_out, m->out_tokens, (size_t)B * m->out_stride * 4, hipMemcpyDeviceToHost, st));
     NX_HIP(m->ctx, hipStreamSynchronize(st));
-    NX_TRY(check_fused_state(m));
     for (int b = 0; b < B; ++b) {
         if (m->active[b]) m->hpos[b] += steps;
         if (!out_tokens) continue;
@@ -1553,8 +1479,7 @@ nx_status nx_model_admit(nx_model* m, int slot, const int32_t* prompt, int P, in
         std::vector<unsigned long long> best((size_t)B);
         NX_HIP(m->ctx, hipMemcpyAsync(best.data(), m->best, (size_t)B * 8, hipMemcpyDeviceToHost, st));
         NX_HIP(m->ctx, hipStreamSynchronize(st));
-        NX_TRY(check_fused_state(m));
-        std::vector<int32_t> pos((size_t)B);
+            std::vector<int32_t> pos((size_t)B);
         for (int b = 0; b < B; ++b) {
             pos[(size_t)b] = b == slot ? P - 1 : m->hpos[(size_t)b];
             if (b != slot) best[(size_t)b] = saved[(size_t)b];

@@ -27,6 +27,7 @@ struct Request {
     std::vector<int32_t> out;
     int slot = -1;
     bool done = false;
+    nx_status err = NX_OK;  // a failed admission: the request is done with this status
 };
 
 // Steps per decode call of the scheduler: at most this many, fewer when an
@@ -116,10 +117,17 @@ nx_status nx_sched_step(nx_sched* s, int* n_active, int* n_waiting) {
         const int rid = s->waiting.front();
         Request& r = s->reqs[rid];
         if (s->reserved + r.pages > s->pool_pages) break;  // in arrival order: wait for pages
-        s->waiting.pop_front();
         int32_t first = 0;
         nx_status st = nx_model_admit(s->m, b, r.prompt.data(), (int)r.prompt.size(), &first);
-        if (st != NX_OK) return st;
+        // the request leaves the queue either way: admitted, or done with the
+        // admission's status (nx_model_admit leaves the slot free on failure;
+        // a retry could fail the same way forever in nx_sched_run)
+        s->waiting.pop_front();
+        if (st != NX_OK) {
+            r.done = true;
+            r.err = st;
+            return st;
+        }
         r.slot = b;
         if (take(r, &first, 1)) {
             (void)nx_model_retire(s->m, b);
@@ -179,5 +187,6 @@ nx_status nx_sched_result(nx_sched* s, int id, int32_t* out, int cap, int* n, in
     *n = (int)r.out.size();
     *done = r.done ? 1 : 0;
     if (out) std::copy(r.out.begin(), r.out.begin() + std::min(cap, (int)r.out.size()), out);
+    if (r.err != NX_OK) return fail(s->ctx, r.err, "request %d failed at admission", id);
     return NX_OK;
 }

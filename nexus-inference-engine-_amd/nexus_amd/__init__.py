@@ -137,7 +137,6 @@ _SIGS = {
     "nx_model_destroy": (_I, [_P]),
     "nx_model_prefill": (_I, [_P, _P, _I, _P]),
     "nx_model_set_prefill": (_I, [_P, _I]),
-    "nx_model_set_fused": (_I, [_P, _I]),
     "nx_model_get_config": (_I, [_P, C.POINTER(ModelConfig)]),
     "nx_model_context": (_P, [_P]),
     "nx_model_admit": (_I, [_P, _I, _P, _I, C.POINTER(C.c_int32)]),
@@ -361,10 +360,6 @@ class Model:
         """SamplingParams of the decode loop; temperature <= 0 is greedy."""
         self.ctx.check(self.ctx.L.nx_model_set_sampling(self.h, temperature, top_k, top_p, seed),
                        "nx_model_set_sampling")
-
-    def set_fused(self, on: bool):
-        """QKV, attention and wo of each layer in one launch (batch 1, fp16 pages)."""
-        self.ctx.check(self.ctx.L.nx_model_set_fused(self.h, int(on)), "nx_model_set_fused")
 
     def set_prefill(self, batched: bool):
         """Batched GEMM prefill (default) or one decode step per prompt token."""

@@ -145,13 +145,13 @@ def write_nxf_files() -> None:
     sys.path.insert(0, str(HERE.parent))
     sys.path.insert(0, str(ROOT / "nexus-inference-engine-_amd"))
     from nexus_amd.nxf import NXFReader
-    from nxf_cases import NXF_CASES, REF_TEST_MANIFEST, ref_write
+    from nxf_cases import CASE_MANIFEST, NXF_CASES, ref_write
     out = {}
     with tempfile.TemporaryDirectory() as td:
         for case, make in NXF_CASES.items():
             tensors = make()
             p = Path(td) / f"{case}.nxf"
-            ref_write(p, REF_TEST_MANIFEST, tensors)
+            ref_write(p, CASE_MANIFEST[case], tensors)
             data = np.frombuffer(p.read_bytes(), np.uint8).copy()
             offs = []
             with NXFReader.open(p) as r:

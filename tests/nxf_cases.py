@@ -43,13 +43,20 @@ def ragged_tensors(seed=7):
     return t
 
 
-NXF_CASES = {"reference_test": ref_test_tensors, "ragged": ragged_tensors}
+NXF_CASES = {"reference_test": ref_test_tensors, "ragged": ragged_tensors,
+             "control_name": ref_test_tensors}
+# The manifest of each case: the reference test's, except that "control_name"
+# names the model with control bytes, which the reference's JSON escaper
+# (format/nxf_writer.cpp:76-89) writes raw (only ", \\, \\n and \\t are escaped).
+CONTROL_NAME = "ctl\r\x01\x1f\x7f\n\tend"
+CASE_MANIFEST = {"reference_test": REF_TEST_MANIFEST, "ragged": REF_TEST_MANIFEST,
+                 "control_name": dict(REF_TEST_MANIFEST, name=CONTROL_NAME)}
 GOLDEN = Path(__file__).resolve().parent / "golden" / "nxf_ref_files.npz"
 
 
 def ref_file_bytes(case: str) -> bytes:
     """The bytes the reference's NXFWriter writes for a case of NXF_CASES
-    with REF_TEST_MANIFEST, rebuilt from the fixture golden/nxf_ref_files.npz
+    with its CASE_MANIFEST, rebuilt from the fixture golden/nxf_ref_files.npz
     (the reference writer's file with the payload regions zeroed, and each
     chunk's offset): the case's chunk bytes are put back at those offsets."""
     with np.load(GOLDEN) as z:

@@ -162,3 +162,37 @@ def test_pool_exhaustion_fails_before_the_step(ctx):
     assert e.value.code == 7
     assert gm.position(0) == 47
     gm.close()
+
+
+def test_scheduler_admission_failure_completes_the_request(ctx):
+    """A request whose admission fails leaves the queue as complete with the
+    admission's status instead of being dropped: here the pool's pages were
+    taken by a sequence admitted into slot 1 directly (not through the
+    scheduler), so admitting the request into slot 0 runs out of pages.  The
+    step reports NX_ERR_CAPACITY, the request's result carries it, slot 0
+    stays free, and the next request is served (tokens equal to the oracle's
+    for it alone) once the pages are back."""
+    cfg = dict(TINY, batch=2, max_seq=128, seed=0x5C0C, kv_blocks=8)
+    p_long, p_req, p_next = prompts(cfg, [90, 40, 12])  # pages 6 (admitted directly), 3 at admission, 1
+    gm = nexus_amd.Model(ctx, **cfg)
+    sched = nexus_amd.Scheduler(gm)
+    gm.admit(1, p_long)
+    assert gm.kv_pages() == (8, 2)
+    rid = sched.submit(p_req, 20)
+    with pytest.raises(nexus_amd.NxError) as e:
+        sched.step()
+    assert e.value.code == 7
+    with pytest.raises(nexus_amd.NxError) as e:
+        sched.result(rid)
+    assert e.value.code == 7
+    assert not gm.slot_active(0)
+    gm.retire(1)
+    assert gm.kv_pages() == (8, 8)
+    rid2 = sched.submit(p_next, 10)
+    sched.run()  # the failed request is not tried again
+    out, done = sched.result(rid2)
+    want, margins = standalone(cfg, p_next, 10)
+    assert done and len(out) == 10
+    assert_greedy_parity(out[None, :], want[None, :], margins[None, :])
+    sched.close()
+    gm.close()

@@ -14,8 +14,8 @@ import nexus_amd
 import oracle
 from nexus_amd import NxError
 from nexus_amd.nxf import NXFReader
-from nxf_cases import (NXF_CASES, REF_TEST_MANIFEST, our_summary, our_write, ragged_tensors, ref_chunk,
-                       ref_file_bytes, ref_summary, ref_test_tensors, ref_write)
+from nxf_cases import (CASE_MANIFEST, CONTROL_NAME, NXF_CASES, REF_TEST_MANIFEST, our_summary, our_write,
+                       ragged_tensors, ref_chunk, ref_file_bytes, ref_summary, ref_test_tensors, ref_write)
 
 needs_ref = pytest.mark.skipif(oracle.ref() is None, reason="reference checker oracle/_ref not built")
 
@@ -182,11 +182,34 @@ def test_manifest_parser_accepts_standard_json(tmp_path):
     assert m.rope_theta == 10000.0 and abs(m.rms_norm_eps - 1e-5) < 1e-12
 
 
+def test_manifest_parser_takes_what_the_reference_reader_takes(tmp_path):
+    """Raw control bytes inside a string (the reference writer leaves \\r and
+    other control bytes unescaped), default_codec as quoted text (read as
+    atoi reads it, format/nxf_reader.cpp:162) and bytes after the closing
+    brace are accepted, as the reference reader accepts them."""
+    text = '{"name": "a\rb\x01c\x1f", "default_codec": " 3", "num_layers": 2} trailing \x00 bytes'
+    with NXFReader.open(_with_manifest(tmp_path, text)) as r:
+        m = r.manifest()
+    assert m.name == "a\rb\x01c\x1f" and m.default_codec == 3 and m.num_layers == 2
+    with NXFReader.open(_with_manifest(tmp_path, '{"default_codec": "x"}')) as r:
+        assert r.manifest().default_codec == 0  # no digits: atoi gives 0
+
+
+def test_reader_reads_the_control_name_fixture(tmp_path):
+    """The reference writer's file whose model name holds raw control bytes
+    (the fixture of case control_name) opens with that name."""
+    p = tmp_path / "c.nxf"
+    p.write_bytes(ref_file_bytes("control_name"))
+    with NXFReader.open(p) as r:
+        m = r.manifest()
+    assert m.name == CONTROL_NAME and m.num_layers == 2
+
+
 @pytest.mark.parametrize("bad", [
     '{"num_layers": -1}', '{"num_layers": 4294967296}', '{"num_layers": 2.5}', '{"default_codec": 256}',
-    '{"default_codec": "1"}', '{"num_layers": "2"}', '{"name": 3}', '{"rope_theta": 1e39}',
-    '{"num_layers": 2,}', '{"num_layers": 2', '{"a": {"b": 1}}', '{"a": [1]}', '{"a": true}',
-    '{"num_layers": 01}', '{"num_layers": .5}', '{"name": "x\\q"}', '{"num_layers": 2} x'])
+    '{"default_codec": "256"}', '{"default_codec": "-1"}', '{"num_layers": "2"}', '{"name": 3}',
+    '{"rope_theta": 1e39}', '{"num_layers": 2,}', '{"num_layers": 2', '{"a": {"b": 1}}', '{"a": [1]}',
+    '{"a": true}', '{"num_layers": 01}', '{"num_layers": .5}', '{"name": "x\\q"}'])
 def test_manifest_parser_rejects(tmp_path, bad):
     """Values outside a field's range (negative, 2^32 and above, fractions,
     bytes above 255, floats that overflow), a value of the wrong kind, and
@@ -203,7 +226,7 @@ def test_nxf_fixture_is_the_reference_writers_file(tmp_path, case):
     payload put back) is byte for byte the file the reference's NXFWriter
     writes for the case now."""
     p = tmp_path / "ref.nxf"
-    ref_write(p, REF_TEST_MANIFEST, NXF_CASES[case]())
+    ref_write(p, CASE_MANIFEST[case], NXF_CASES[case]())
     assert p.read_bytes() == ref_file_bytes(case)
 
 
@@ -214,7 +237,7 @@ def test_writer_output_is_byte_identical_to_reference_writer(ctx, tmp_path, case
     (the fixture of its file) and by this library's writer (checksums
     computed on the GPU) give byte-identical files."""
     b = tmp_path / "ours.nxf"
-    our_write(ctx, b, REF_TEST_MANIFEST, NXF_CASES[case]())
+    our_write(ctx, b, CASE_MANIFEST[case], NXF_CASES[case]())
     assert b.read_bytes() == ref_file_bytes(case)
 
 

@@ -105,7 +105,10 @@ def test_oracle_sampler_matches_float64_restatement(V, T, top_k, top_p):
         if margin > tol_fp32_sequential(V, kept):
             assert got == want, (rep, got, want, margin)
             checked += 1
-    assert checked >= 8
+    # the inputs are seeded, so every case checks a fixed number of its 40
+    # draws (19 to 40 of them)
+    print(f"oracle == float64 on {checked} of 40 draws")
+    assert checked >= 15
 
 
 def test_oracle_sampler_limits():
@@ -128,7 +131,7 @@ def test_gpu_sampler_matches_oracle(ctx, V, T, top_k, top_p):
     reference's fp32 arithmetic) wherever it is farther than that one's."""
     rng = np.random.default_rng(V * 3 + top_k)
     B = 16
-    checked = 0
+    checked = checked_o = 0
     for seed in (7, 1234, 99991):
         logits = (rng.standard_normal((B, V)) * 3).astype(np.float32)
         bl, bo = ctx.upload(logits), ctx.alloc(B * 4)
@@ -145,7 +148,11 @@ def test_gpu_sampler_matches_oracle(ctx, V, T, top_k, top_p):
                 checked += 1
             if margin > tol_fp32_sequential(V, kept):
                 assert got[b] == want, (seed, b, got[b], want, margin)
-    assert checked >= 16
+                checked_o += 1
+    # seeded inputs: each case checks a fixed number of its 48 rows against
+    # float64 (24 to 48) and against the oracle (6 to 48)
+    print(f"GPU == float64 on {checked} of {3 * B} rows, GPU == oracle on {checked_o}")
+    assert checked >= 20 and checked_o >= 5
 
 
 @pytest.mark.gpu
