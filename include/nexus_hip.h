@@ -222,7 +222,8 @@ nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q_f32, nx_buf kc4, nx_buf 
                                   nx_buf block_table, nx_buf ctx_lens_i32, nx_buf out_f16,
                                   int batch, int hq, int hkv, int max_blocks, int num_blocks);
 /* MoE routing: softmax over E logits fp32 [batch][E], top-k by probability
- * (ties: lower id), renormalized weights.  hybrid_model.cpp:1656-1694. */
+ * (ties: lower id), renormalized weights.  hybrid_model.cpp:1656-1694.
+ * E <= 256, k <= min(16, E), batch <= 64. */
 nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits_f32, nx_buf ids_i32, nx_buf weights_f32,
                             int E, int k, int batch);
 /* Expert SwiGLU FFN for routed tokens: out[b] (+)= sum_j w[b][j] *
@@ -358,6 +359,10 @@ typedef struct {
                                59-77, whose pages are created on first insert); a step that
                                needs more than are free fails with NX_ERR_CAPACITY before it
                                runs.  Not with a cool_window (every table is then a ring). */
+    int qk_norm;            /* 1: per-head RMSNorm of q and k after the QKV projection (every
+                               head_dim slice normalized with the layer's head_dim-long
+                               attn_q_norm / attn_k_norm weights, hybrid_model.cpp:1325-1349),
+                               applied before RoPE; 0: none */
 } nx_model_config;
 
 typedef struct nx_model nx_model;
@@ -451,6 +456,13 @@ nx_status nx_model_pending(nx_model* m, int32_t* tokens);
  * whole step is one HIP graph launch; nothing is copied to the host between
  * steps. */
 nx_status nx_model_decode(nx_model* m, int steps, int32_t* out_tokens);
+/* The same steps with the input token of every step given instead of fed
+ * back (teacher forcing): active sequence b consumes tokens[b][s] at step s
+ * (tokens [batch][steps]), and logits [batch][steps][V] (optional) receive
+ * the fp32 logits each step produced.  Positions advance by steps; the
+ * pending token afterwards is the last step's greedy token.  One graph
+ * launch per step, with the step's tokens uploaded before it. */
+nx_status nx_model_decode_forced(nx_model* m, const int32_t* tokens, int steps, float* logits);
 /* Logits fp32 [batch][V] of the last step. */
 nx_status nx_model_logits(nx_model* m, float* out);
 /* Current position of sequence b. */

@@ -827,7 +827,7 @@ nx_status nx_attn_decode_paged_tq(nx_ctx* ctx, nx_buf q, nx_buf kc4, nx_buf kc3,
 
 nx_status nx_moe_route_topk(nx_ctx* ctx, nx_buf logits, nx_buf ids, nx_buf w, int E, int k, int batch) {
     if (!ctx) return NX_ERR_INVALID;
-    if (E < 1 || E > 64 || k < 1 || k > 8 || k > E || batch < 1 || batch > 64)
+    if (E < 1 || E > nx::kMoeMaxExperts || k < 1 || k > nx::kMoeMaxTopK || k > E || batch < 1 || batch > 64)
         return fail(ctx, NX_ERR_INVALID, "nx_moe_route_topk: bad shape E=%d k=%d batch=%d", E, k, batch);
     NX_NEED(ctx, logits, (size_t)batch * E * 4, "logits");
     NX_NEED(ctx, ids, (size_t)batch * k * 4, "ids");
@@ -853,7 +853,8 @@ nx_status nx_moe_expert_ffn(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_bu
                             int accumulate) {
     if (!ctx) return NX_ERR_INVALID;
     if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_moe_expert_ffn validates expert ids on the host; not capturable");
-    if (d <= 0 || F <= 0 || E < 1 || E > 64 || k < 1 || k > 8 || k > E || batch < 1 || batch > 8)
+    if (d <= 0 || F <= 0 || E < 1 || E > nx::kMoeMaxExperts || k < 1 || k > nx::kMoeMaxTopK || k > E || batch < 1 ||
+        batch > nx::kMoeMaxBatch)
         return fail(ctx, NX_ERR_INVALID, "nx_moe_expert_ffn: bad shape");
     const int Gd = (d + 31) / 32, Gf = (F + 31) / 32;
     if (Gd > 448 || Gf > 448) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_moe_expert_ffn: K above 14336");

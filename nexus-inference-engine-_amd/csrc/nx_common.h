@@ -47,7 +47,7 @@ inline float normal_k(double sigma) {
 constexpr uint32_t kTidEmbed = 1u, kTidLmHead = 2u, kTidFinalNorm = 3u, kTidStart = 5u, kTidShuffle = 7u;
 NX_HD uint32_t tid_layer(int L, int kind) { return 0x100u * ((uint32_t)L + 1u) + (uint32_t)kind; }
 enum { W_Q = 0, W_K = 1, W_V = 2, W_O = 3, W_GATE = 4, W_UP = 5, W_DOWN = 6, W_ROUTER = 7,
-       TQ_KSIGN = 8, TQ_VSIGN = 9, N_ATTN = 10, N_FFN = 11 };
+       TQ_KSIGN = 8, TQ_VSIGN = 9, N_ATTN = 10, N_FFN = 11, N_QNORM = 12, N_KNORM = 13 };
 NX_HD uint32_t tid_expert(int L, int e, int w) {
     return 0x01000000u + 0x1000u * (uint32_t)L + 4u * (uint32_t)e + (uint32_t)w;
 }

@@ -260,7 +260,7 @@ __device__ inline void epilogue(const GemvArgs& a, int b, int n0, int nlim, cons
             const int row = n0 + r;
             if (row >= nlim) break;
             float v0 = res[r], v1 = res[r + 1];
-            if (row < a.qdim + a.kvdim) {
+            if (row < a.qdim + a.kvdim && a.cos_t) {  // no tables: the projection alone
                 const int i = (row % a.hd) >> 1;
                 const float c = have ? pre->c[r / 2] : a.cos_t[(size_t)p * half + i];
                 const float s = have ? pre->s[r / 2] : a.sin_t[(size_t)p * half + i];
@@ -622,7 +622,7 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     int qblk = 0;
     if (EPI == E_QKV && rope_pre) {
         const int row = r0 + 2 * lane;
-        if (row < r1 && row < a.qdim + a.kvdim) {
+        if (row < r1 && row < a.qdim + a.kvdim && a.cos_t) {
             const int i = (row % a.hd) >> 1;
             qc = a.cos_t[(size_t)qp * (a.hd >> 1) + i];
             qs = a.sin_t[(size_t)qp * (a.hd >> 1) + i];

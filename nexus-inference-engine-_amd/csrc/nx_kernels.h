@@ -20,7 +20,7 @@ enum Epi : int {
     E_F16 = 0,      // y16[b][n] = y
     E_F32 = 1,      // y32[b][n] = y
     E_ACC = 2,      // y32[b][n] += y   (residual add)
-    E_QKV = 3,      // RoPE on q/k rows; q -> q32; k,v -> fp16 pages (or fp32 kv_tmp)
+    E_QKV = 3,      // RoPE on q/k rows (none without cos_t); q -> q32; k,v -> fp16 pages (or fp32 kv_tmp)
     E_SWIGLU = 4,   // rows (2j, 2j+1) = (gate j, up j) -> act16[b][j] = fp16(silu(g)*u)
     E_LOGITS = 5,   // y32[b][n] = y and running argmax into best[b]
     E_PART = 6,     // kpart[part][b][n] = partial sum over the block's K part
@@ -45,7 +45,7 @@ struct GemvArgs {
     float* q32;             // [batch][qdim]
     int qdim, kvdim, hd, hkv;
     const int32_t* pos;     // [batch] position of the token being processed
-    const float* cos_t;     // [max_pos][hd/2]
+    const float* cos_t;     // [max_pos][hd/2]; nullptr: no RoPE (the projection alone)
     const float* sin_t;
     uint16_t* kpool;        // fp16 pages (kv_kind 0)
     uint16_t* vpool;
@@ -93,6 +93,12 @@ inline int gemv_kparts(int K, int batch) { return batch >= 2 && K > 4096 && K % 
 // [8 + i] slot i (= b * k + j), [16 + i] token b of slot i, for i < n.
 constexpr int kMoePlanInts = 32;
 constexpr int kMoePlanMaxSlots = 8;
+// Routing limits: experts per layer, experts per token (the reference's
+// default is 10 when the manifest names none, hybrid_model.cpp:1648), and
+// sequences per step.
+constexpr int kMoeMaxExperts = 256;
+constexpr int kMoeMaxTopK = 16;
+constexpr int kMoeMaxBatch = 8;
 // Plan rows a step needs: the most experts that can be active at once.
 __host__ __device__ inline int moe_plan_rows(int E, int batch, int k) { return E < batch * k ? E : batch * k; }
 
@@ -197,6 +203,30 @@ hipError_t rope_launch(float* x, const int32_t* pos, const float* cos_t, const f
 hipError_t swiglu_launch(const float* g, const float* u, uint16_t* out, int n, int batch,
                          hipStream_t st);
 hipError_t residual_add_launch(const float* a, const float* b, float* out, int n, hipStream_t st);
+// Per-head Q/K RMSNorm (hybrid_model.cpp:1325-1349) + RoPE + the paged
+// write of K/V for one decode step: q [batch][hq * hd] in q32 and k, v
+// [batch][2][hkv * hd] in kv_tmp hold the raw projection; every head_dim
+// slice of q and k is normalized with the head_dim weights (nullptr: 1.0),
+// then rotated at pos[b]; q goes back to q32, k and v to the fp16 pages at
+// block_table[b][pos / 16] (kpool == nullptr: k back to kv_tmp, for the
+// TurboQuant attention's append).  head_dim <= 256.
+struct QknArgs {
+    float* q32;
+    float* kv_tmp;
+    const float *qn, *kn;
+    const float *cos_t, *sin_t;
+    const int32_t* pos;
+    const int32_t* block_table;
+    int max_blocks;
+    uint16_t *kpool, *vpool;
+    int hq, hkv, hd;
+    float eps;
+};
+hipError_t qk_norm_rope_launch(const QknArgs& a, int batch, hipStream_t st);
+// The same normalization alone, in place, over `rows` rows: q heads at
+// q + r * ldq, k heads at k + r * ldk (the batched prefill's QKV rows).
+hipError_t head_rmsnorm_launch(float* q, int ldq, float* k, int ldk, int rows, int hq, int hkv, int hd,
+                               const float* qn, const float* kn, float eps, hipStream_t st);
 hipError_t kv_append_f16_launch(const float* k, const float* v, uint16_t* kpool, uint16_t* vpool,
                                 const int32_t* block_table, const int32_t* pos, int batch,
                                 int hkv, int hd, int max_blocks, hipStream_t st);

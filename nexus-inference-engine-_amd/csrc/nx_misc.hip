@@ -89,6 +89,94 @@ __global__ void k_rope(float* x, const int32_t* pos, const float* cos_t, const f
     v[2 * i + 1] = a * s + bb * c;
 }
 
+// Per-head Q/K RMSNorm (HybridModel, hybrid_model.cpp:1325-1349: every
+// head_dim slice of q and of k through rmsnorm with the head_dim-long
+// weights), then RoPE and the page write of one decode step.  Block (head,
+// sequence), one wavefront: heads [0, hq) of q, [hq, hq + hkv) of k, then
+// hkv heads of v (written to the pages unchanged).  Lane l holds the RoPE
+// pairs j = l and l + 64 (elements 2j, 2j + 1), hd <= 256.  The arithmetic
+// is the oracle's: ((x * inv) * w), then the rotation.
+__global__ __launch_bounds__(64) void k_qk_norm_rope(QknArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const int hd = a.hd, half = hd >> 1, qdim = a.hq * hd, kvdim = a.hkv * hd;
+    const int kind = h < a.hq ? 0 : h < a.hq + a.hkv ? 1 : 2;  // q, k, v
+    const int hh = kind == 0 ? h : kind == 1 ? h - a.hq : h - a.hq - a.hkv;
+    float* x = kind == 0 ? a.q32 + (size_t)b * qdim + (size_t)hh * hd
+                         : a.kv_tmp + ((size_t)b * 2 + (kind == 2 ? 1 : 0)) * kvdim + (size_t)hh * hd;
+    const int p = a.pos[b];
+    float v0[2], v1[2];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = lane + 64 * u;
+        v0[u] = j < half ? x[2 * j] : 0.0f;
+        v1[u] = j < half ? x[2 * j + 1] : 0.0f;
+        ss += v0[u] * v0[u] + v1[u] * v1[u];
+    }
+    if (kind != 2) {
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+        const float* w = kind == 0 ? a.qn : a.kn;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int j = lane + 64 * u;
+            if (j >= half) continue;
+            float x0 = v0[u] * inv, x1 = v1[u] * inv;
+            if (w) {
+                x0 = x0 * w[2 * j];
+                x1 = x1 * w[2 * j + 1];
+            }
+            const float c = a.cos_t[(size_t)p * half + j], s = a.sin_t[(size_t)p * half + j];
+            v0[u] = x0 * c - x1 * s;
+            v1[u] = x0 * s + x1 * c;
+        }
+    }
+    const size_t page = a.kpool ? ((size_t)a.block_table[(size_t)b * a.max_blocks + p / kPage] * a.hkv + hh) *
+                                      kPage * hd
+                                : 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int j = lane + 64 * u;
+        if (j >= half) continue;
+        if (kind == 0 || (kind == 1 && !a.kpool)) {
+            x[2 * j] = v0[u];
+            x[2 * j + 1] = v1[u];
+        } else if (kind == 1) {  // K pages are token-major [16][hd]
+            a.kpool[page + (size_t)(p % kPage) * hd + 2 * j] = f2h_bits(v0[u]);
+            a.kpool[page + (size_t)(p % kPage) * hd + 2 * j + 1] = f2h_bits(v1[u]);
+        } else if (a.kpool) {    // V pages are dimension-major [hd][16]
+            a.vpool[page + (size_t)(2 * j) * kPage + p % kPage] = f2h_bits(v0[u]);
+            a.vpool[page + (size_t)(2 * j + 1) * kPage + p % kPage] = f2h_bits(v1[u]);
+        }
+    }
+}
+
+// The normalization alone, in place: block (head, row), heads [0, hq) of
+// q + row * ldq, [hq, hq + hkv) of k + row * ldk; lane l holds elements l,
+// l + 64, ... (hd <= 256).
+__global__ __launch_bounds__(64) void k_head_rmsnorm(float* q, int ldq, float* k, int ldk, int hq, int hd,
+                                                     const float* qn, const float* kn, float eps) {
+    const int h = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+    const bool isq = h < hq;
+    float* x = isq ? q + (size_t)row * ldq + (size_t)h * hd : k + (size_t)row * ldk + (size_t)(h - hq) * hd;
+    const float* w = isq ? qn : kn;
+    float v[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = lane + 64 * u;
+        v[u] = i < hd ? x[i] : 0.0f;
+        ss += v[u] * v[u];
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = lane + 64 * u;
+        if (i < hd) x[i] = w ? (v[u] * inv) * w[i] : v[u] * inv;
+    }
+}
+
 __global__ void k_swiglu(const float* g, const float* u, uint16_t* out, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -320,29 +408,38 @@ __global__ void k_set_tokens(unsigned long long* best, const int32_t* tokens, in
 
 // Routing of one sequence (hybrid_model.cpp:1656-1694): softmax over the E
 // logits, the k largest probabilities (ties: lower id), weights renormalized
-// over the chosen k.
-// ids, w: the k outputs; p: E floats of scratch (all in LDS).
-__device__ inline void route_row(const float* lg, int E, int k, int* ids, float* w, float* p) {
+// over the chosen k.  A probability is recomputed where it is compared
+// (expf(l - max) / sum, the same value every time) instead of being kept, so
+// any E up to kMoeMaxExperts needs only the taken bitmask as scratch.
+// ids, w: the k outputs; taken: kMoeMaxExperts / 32 words of scratch.
+__device__ inline void route_row(const float* lg, int E, int k, int* ids, float* w, uint32_t* taken) {
     float mx = lg[0];
     for (int e = 1; e < E; ++e) mx = fmaxf(mx, lg[e]);
     float sum = 0.0f;
-    for (int e = 0; e < E; ++e) {
-        p[e] = expf(lg[e] - mx);
-        sum += p[e];
-    }
-    if (sum > 0.0f)
-        for (int e = 0; e < E; ++e) p[e] = p[e] / sum;
-    unsigned long long taken = 0ull;
+    for (int e = 0; e < E; ++e) sum += expf(lg[e] - mx);
+    auto prob = [&](int e) {
+        const float x = expf(lg[e] - mx);
+        return sum > 0.0f ? x / sum : x;
+    };
+    for (int i = 0; i < (E + 31) / 32; ++i) taken[i] = 0u;
     float active = 0.0f;
     for (int j = 0; j < k; ++j) {
         int best = -1;
-        for (int e = 0; e < E; ++e)
-            if (!((taken >> e) & 1ull) && (best < 0 || p[e] > p[best])) best = e;
-        taken |= 1ull << best;
+        float bp = 0.0f;
+        for (int e = 0; e < E; ++e) {
+            if ((taken[e >> 5] >> (e & 31)) & 1u) continue;
+            const float pe = prob(e);
+            if (best < 0 || pe > bp) {
+                best = e;
+                bp = pe;
+            }
+        }
+        taken[best >> 5] |= 1u << (best & 31);
         ids[j] = best;
-        active += p[best];
+        w[j] = bp;
+        active += bp;
     }
-    for (int j = 0; j < k; ++j) w[j] = active > 0.0f ? p[ids[j]] / active : 1.0f / (float)k;
+    for (int j = 0; j < k; ++j) w[j] = active > 0.0f ? w[j] / active : 1.0f / (float)k;
 }
 
 // Per-expert slot lists in (b, j) order and the routing plan (the active
@@ -383,12 +480,12 @@ __device__ inline void build_lists(const MoeArgs& a, const int32_t* ids, int* cn
 // per-expert token lists and the routing plan.
 __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
     const int b = threadIdx.x;
-    __shared__ int32_t sid[64 * 8];
-    __shared__ float sp[64][64];
-    __shared__ int scnt[64];
-    __shared__ float sw[64 * 8];
+    __shared__ int32_t sid[64 * kMoeMaxTopK];
+    __shared__ uint32_t tk[64][kMoeMaxExperts / 32];
+    __shared__ int scnt[kMoeMaxExperts];
+    __shared__ float sw[64 * kMoeMaxTopK];
     if (b < a.batch) {
-        route_row(a.logits + (size_t)b * a.E, a.E, a.k, sid + b * a.k, sw + b * a.k, sp[b]);
+        route_row(a.logits + (size_t)b * a.E, a.E, a.k, sid + b * a.k, sw + b * a.k, tk[b]);
         for (int j = 0; j < a.k; ++j) {
             a.ids[(size_t)b * a.k + j] = sid[b * a.k + j];
             a.weights[(size_t)b * a.k + j] = sw[b * a.k + j];
@@ -418,10 +515,10 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     __shared__ __align__(16) uint16_t xs[kNrMaxD];  // pair-major: [pair m of the group][group g]
     __shared__ float red[kNrWaves];
     __shared__ float inv_s;
-    __shared__ float lg[8 * kNrMaxE];
-    __shared__ int32_t sid[8 * 8];
-    __shared__ float sp[8][kNrMaxE];
-    __shared__ float sw[8 * 8];
+    __shared__ float lg[kMoeMaxBatch * kNrMaxE];
+    __shared__ int32_t sid[kMoeMaxBatch * kMoeMaxTopK];
+    __shared__ uint32_t tk[kMoeMaxBatch][kMoeMaxExperts / 32];
+    __shared__ float sw[kMoeMaxBatch * kMoeMaxTopK];
     __shared__ int scnt[kNrMaxE];
     __shared__ int last;
     // the arguments the prologue uses, requested in one round
@@ -513,7 +610,7 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     }
     __syncthreads();
     if (tid < B) {
-        route_row(lg + tid * E, E, a.k, sid + tid * a.k, sw + tid * a.k, sp[tid]);
+        route_row(lg + tid * E, E, a.k, sid + tid * a.k, sw + tid * a.k, tk[tid]);
         for (int j = 0; j < a.k; ++j) {
             a.ids[(size_t)tid * a.k + j] = sid[tid * a.k + j];
             a.weights[(size_t)tid * a.k + j] = sw[tid * a.k + j];
@@ -556,13 +653,13 @@ constexpr int kPfRouteThreads = 256;
 __global__ __launch_bounds__(kPfRouteThreads) void k_pf_route(const float* logits, int n, int E, int k, int32_t* ids,
                                                               float* w, int32_t* row_tok, int32_t* slot_row,
                                                               int32_t* counts) {
-    __shared__ float p[kPfRouteThreads][64];
-    __shared__ int sid[kPfRouteThreads][8];
-    __shared__ float sw[kPfRouteThreads][8];
-    __shared__ int cnt[64], off[64];
+    __shared__ uint32_t tk[kPfRouteThreads][kMoeMaxExperts / 32];
+    __shared__ int sid[kPfRouteThreads][kMoeMaxTopK];
+    __shared__ float sw[kPfRouteThreads][kMoeMaxTopK];
+    __shared__ int cnt[kMoeMaxExperts], off[kMoeMaxExperts];
     const int tid = threadIdx.x;
     for (int t = tid; t < n; t += kPfRouteThreads) {
-        route_row(logits + (size_t)t * E, E, k, sid[tid], sw[tid], p[tid]);
+        route_row(logits + (size_t)t * E, E, k, sid[tid], sw[tid], tk[tid]);
         for (int j = 0; j < k; ++j) {
             ids[(size_t)t * k + j] = sid[tid][j];
             w[(size_t)t * k + j] = sw[tid][j];
@@ -627,6 +724,22 @@ hipError_t rope_launch(float* x, const int32_t* pos, const float* cos_t, const f
     const size_t n = (size_t)batch * heads * (hd / 2);
     hipLaunchKernelGGL(k_rope, grid1(n, 256), dim3(256), 0, st, x, pos, cos_t, sin_t, heads, hd,
                        batch);
+    return hipGetLastError();
+}
+
+hipError_t qk_norm_rope_launch(const QknArgs& a, int batch, hipStream_t st) {
+    if (a.hd < 2 || a.hd > 256 || a.hd % 2 || a.hq < 1 || a.hkv < 1 || batch < 1 || !a.q32 || !a.kv_tmp ||
+        !a.cos_t || !a.sin_t || !a.pos || (a.kpool && (!a.vpool || !a.block_table)))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_qk_norm_rope, dim3(a.hq + 2 * a.hkv, batch), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t head_rmsnorm_launch(float* q, int ldq, float* k, int ldk, int rows, int hq, int hkv, int hd,
+                               const float* qn, const float* kn, float eps, hipStream_t st) {
+    if (hd < 1 || hd > 256 || hq < 1 || hkv < 1 || rows < 0) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_head_rmsnorm, dim3(hq + hkv, rows), dim3(64), 0, st, q, ldq, k, ldk, hq, hd, qn, kn, eps);
     return hipGetLastError();
 }
 
@@ -730,7 +843,8 @@ hipError_t set_tokens_launch(unsigned long long* best, const int32_t* tokens, in
 
 bool moe_norm_route_fits(int d, int E, int k, int batch) {
     // whole 32-element groups, so the router's last group reads no x past its row
-    return batch >= 1 && batch <= 8 && E >= 1 && E <= kNrMaxE && k >= 1 && k <= 8 && k <= E && d >= 32 &&
+    return batch >= 1 && batch <= kMoeMaxBatch && E >= 1 && E <= kNrMaxE && k >= 1 && k <= kMoeMaxTopK && k <= E &&
+           d >= 32 &&
            d % 32 == 0 && d <= kNrMaxD;
 }
 
@@ -743,7 +857,8 @@ hipError_t moe_norm_route_launch(const MoeArgs& a, hipStream_t st) {
 }
 
 hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st) {
-    if (a.batch > 64 || a.E > 64 || a.k > 8) return hipErrorInvalidValue;
+    if (a.batch < 1 || a.batch > 64 || a.E < 1 || a.E > kMoeMaxExperts || a.k < 1 || a.k > kMoeMaxTopK || a.k > a.E)
+        return hipErrorInvalidValue;
     if (a.plan && a.batch > kMoePlanMaxSlots) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
@@ -751,7 +866,7 @@ hipError_t moe_route_launch(const MoeArgs& a, hipStream_t st) {
 
 hipError_t pf_route_launch(const float* logits, int n, int E, int k, int32_t* ids, float* w, int32_t* row_tok,
                            int32_t* slot_row, int32_t* counts, hipStream_t st) {
-    if (n < 1 || E < 1 || E > 64 || k < 1 || k > 8 || k > E) return hipErrorInvalidValue;
+    if (n < 1 || E < 1 || E > kMoeMaxExperts || k < 1 || k > kMoeMaxTopK || k > E) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pf_route, dim3(1), dim3(kPfRouteThreads), 0, st, logits, n, E, k, ids, w, row_tok, slot_row,
                        counts);
     return hipGetLastError();

@@ -44,6 +44,8 @@ struct Layer {
     int32_t* moe_count = nullptr;  // [E]
     float* norm_attn = nullptr;    // RMSNorm weights [d]; nullptr = 1.0
     float* norm_ffn = nullptr;
+    float* qnorm = nullptr;        // per-head Q/K RMSNorm weights [hd] (qk_norm); nullptr = 1.0
+    float* knorm = nullptr;
 };
 
 size_t qbytes(size_t N, int K) { return N * (size_t)((K + 31) / 32) * 18; }
@@ -174,22 +176,25 @@ nx_status generate_weights(nx_model* m) {
     const int d = c.d_model, F = c.ffn, E = c.n_experts;
     NX_LAUNCH(m, nx::gen_f16_launch(m->embed, (size_t)c.vocab * d, seed, nx::kTidEmbed, k02, st));
     NX_LAUNCH(m, nx::gen_quant_launch(m->lm_w, m->lm_s, c.vocab, d, seed, nx::kTidLmHead, k02, 0, 1, st));
-    // RMSNorm weights 1 + N(0, norm_sigma), generated on the host
-    auto gen_norm = [&](float* dst, uint32_t tid) -> nx_status {
+    // RMSNorm weights 1 + N(0, norm_sigma), generated on the host (n = d, or
+    // head_dim for the Q/K norms)
+    auto gen_norm = [&](float* dst, uint32_t tid, int n) -> nx_status {
         if (!dst) return NX_OK;
-        std::vector<float> w((size_t)d);
+        std::vector<float> w((size_t)n);
         const uint64_t key = nx::stream_key(seed, tid);
         const float kn = nx::normal_k((double)c.norm_sigma);
-        for (int i = 0; i < d; ++i) w[(size_t)i] = 1.0f + nx::normal_from(nx::rand_at(key, (uint64_t)i), kn);
+        for (int i = 0; i < n; ++i) w[(size_t)i] = 1.0f + nx::normal_from(nx::rand_at(key, (uint64_t)i), kn);
         NX_HIP(m->ctx, hipMemcpyAsync(dst, w.data(), w.size() * 4, hipMemcpyHostToDevice, st));
         NX_HIP(m->ctx, hipStreamSynchronize(st));  // w is released on return
         return NX_OK;
     };
-    NX_TRY(gen_norm(m->norm_final, nx::kTidFinalNorm));
+    NX_TRY(gen_norm(m->norm_final, nx::kTidFinalNorm, d));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[L];
-        NX_TRY(gen_norm(ly.norm_attn, nx::tid_layer(L, nx::N_ATTN)));
-        NX_TRY(gen_norm(ly.norm_ffn, nx::tid_layer(L, nx::N_FFN)));
+        NX_TRY(gen_norm(ly.norm_attn, nx::tid_layer(L, nx::N_ATTN), d));
+        NX_TRY(gen_norm(ly.norm_ffn, nx::tid_layer(L, nx::N_FFN), d));
+        NX_TRY(gen_norm(ly.qnorm, nx::tid_layer(L, nx::N_QNORM), c.head_dim));
+        NX_TRY(gen_norm(ly.knorm, nx::tid_layer(L, nx::N_KNORM), c.head_dim));
         NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->qdim, d, seed, nx::tid_layer(L, nx::W_Q), k02, 0, 1, st));
         NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->kvdim, d, seed, nx::tid_layer(L, nx::W_K), k02, m->qdim, 1, st));
         NX_LAUNCH(m, nx::gen_quant_launch(ly.wqkv, ly.sqkv, m->kvdim, d, seed, nx::tid_layer(L, nx::W_V), k02,
@@ -256,13 +261,44 @@ nx::GemvArgs qkv_args(const nx_model* m, const Layer& ly) {
     a.sin_t = m->rope_sin;
     a.block_table = c.kv_kind == 2 ? m->hot_bt : m->block_table;
     a.max_blocks = m->max_blocks;
-    if (c.kv_kind != 1) {
+    if (c.kv_kind != 1 && !c.qk_norm) {
         a.kpool = ly.kpool;
         a.vpool = ly.vpool;
     } else {
         a.kv_tmp = m->kv_tmp;
     }
+    if (c.qk_norm) {
+        // the projection only: q to q32, k and v to kv_tmp, no RoPE; the
+        // Q/K norm launch then normalizes, rotates and writes the pages
+        a.cos_t = nullptr;
+        a.sin_t = nullptr;
+    }
     return a;
+}
+
+// Per-head Q/K RMSNorm + RoPE + the page write of K/V (qk_norm models),
+// after the QKV GEMV of layer ly left q in q32 and k, v in kv_tmp.
+hipError_t qk_norm_launch(nx_model* m, const Layer& ly, hipStream_t st) {
+    const nx_model_config& c = m->c;
+    nx::QknArgs a{};
+    a.q32 = m->q;
+    a.kv_tmp = m->kv_tmp;
+    a.qn = ly.qnorm;
+    a.kn = ly.knorm;
+    a.cos_t = m->rope_cos;
+    a.sin_t = m->rope_sin;
+    a.pos = m->pos;
+    a.block_table = c.kv_kind == 2 ? m->hot_bt : m->block_table;
+    a.max_blocks = m->max_blocks;
+    if (c.kv_kind != 1) {  // TurboQuant pages: the attention launch appends from kv_tmp
+        a.kpool = ly.kpool;
+        a.vpool = ly.vpool;
+    }
+    a.hq = c.n_heads;
+    a.hkv = c.n_kv_heads;
+    a.hd = c.head_dim;
+    a.eps = c.eps;
+    return nx::qk_norm_rope_launch(a, c.batch, st);
 }
 
 nx::GemvArgs wo_args(const nx_model* m, const Layer& ly) {
@@ -469,6 +505,7 @@ nx_status enqueue_step(nx_model* m) {
         {
             // RMSNorm + QKV + RoPE + paged KV append, attention, wo + residual
             NX_LAUNCH(m, norm_gemv_launch(m, nx::E_QKV, qkv_args(m, ly), st, xn_ready));
+            if (c.qk_norm) NX_LAUNCH(m, qk_norm_launch(m, ly, st));
             NX_LAUNCH(m, attention_launch(m, ly, st));
             nx::GemvArgs wo = wo_args(m, ly);
             if (prenorm_on(m) && m->kpart && m->wo_kparts > 0 && m->wo_kparts <= nx::gemv_kparts(c.ffn, B)) {
@@ -689,6 +726,10 @@ nx_status create_impl(nx_model* m, bool synthetic) {
         if (norms) {
             NX_TRY(dalloc(m, &ly.norm_attn, (size_t)d));
             NX_TRY(dalloc(m, &ly.norm_ffn, (size_t)d));
+            if (c.qk_norm) {
+                NX_TRY(dalloc(m, &ly.qnorm, (size_t)c.head_dim));
+                NX_TRY(dalloc(m, &ly.knorm, (size_t)c.head_dim));
+            }
         }
         if (E > 0) {
             NX_TRY(dalloc(m, &ly.wr, (size_t)E * m->Gd * 16));
@@ -847,7 +888,7 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.n_layers < 1 || c.d_model < 32 || c.n_heads < 1 || c.n_kv_heads < 1 || c.n_heads % c.n_kv_heads ||
         c.ffn < 2 || c.vocab < 2 || c.max_seq < nx::kPage || c.max_seq % nx::kPage || c.batch < 1 || c.batch > 8 ||
         c.kv_kind < 0 || c.kv_kind > 2 || c.eps <= 0.0f || c.rope_theta <= 0.0f ||
-        !(c.norm_sigma >= 0.0f && c.norm_sigma < 1e3f))
+        !(c.norm_sigma >= 0.0f && c.norm_sigma < 1e3f) || (c.qk_norm != 0 && c.qk_norm != 1))
         return fail(ctx, NX_ERR_INVALID, "nx_model_create: invalid configuration");
     const int G = c.n_heads / c.n_kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return fail(ctx, NX_ERR_UNSUPPORTED, "hq/hkv must be 1, 2, 4 or 8");
@@ -869,8 +910,9 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
     if (c.max_seq > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the attention limit");
     if (c.d_model > 14336 || c.ffn > 14336 || c.n_heads * c.head_dim > 14336)
         return fail(ctx, NX_ERR_UNSUPPORTED, "GEMV K above 14336");
-    if (c.n_experts < 0 || c.n_experts > 64 || (c.n_experts > 0 && (c.top_k < 1 || c.top_k > 8 || c.top_k > c.n_experts)))
-        return fail(ctx, NX_ERR_INVALID, "invalid expert configuration");
+    if (c.n_experts < 0 || c.n_experts > nx::kMoeMaxExperts ||
+        (c.n_experts > 0 && (c.top_k < 1 || c.top_k > nx::kMoeMaxTopK || c.top_k > c.n_experts)))
+        return fail(ctx, NX_ERR_INVALID, "invalid expert configuration (experts <= 256, 1 <= top_k <= min(16, experts))");
     return NX_OK;
 }
 
@@ -998,6 +1040,9 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             g.y32 = qkv;
             g.ldy = m->nqkv;
             NX_LAUNCH(m, nx::pf_gemm_launch(nx::PF_F32, g, st));
+            if (c.qk_norm)  // per-head Q/K RMSNorm of the chunk's rows, before RoPE
+                NX_LAUNCH(m, nx::head_rmsnorm_launch(qkv, m->nqkv, qkv + m->qdim, m->nqkv, n, hq, hkv, hd, ly.qnorm,
+                                                     ly.knorm, c.eps, st));
             const int32_t* bt = m->block_table + (size_t)b * MB;
             NX_LAUNCH(m, nx::pf_rope_kv_launch(qkv, m->nqkv, n, pb, m->qdim, m->kvdim, hd, hkv, m->rope_cos, m->rope_sin,
                                                bt, ly.kpool, ly.vpool, q, st, kvrows));
@@ -1500,6 +1545,49 @@ nx_status nx_model_admit(nx_model* m, int slot, const int32_t* prompt, int P, in
     return NX_OK;
 }
 
+nx_status nx_model_decode_forced(nx_model* m, const int32_t* tokens, int steps, float* logits) {
+    if (!m || !tokens || steps < 1) return NX_ERR_INVALID;
+    const nx_model_config& c = m->c;
+    const int B = c.batch;
+    int nact = 0;
+    for (int b = 0; b < B; ++b) {
+        if (!m->active[(size_t)b]) continue;
+        ++nact;
+        if (m->hpos[(size_t)b] < 0) return fail(m->ctx, NX_ERR_STATE, "decode before prefill or fill_context");
+        if (m->hpos[(size_t)b] + steps >= c.max_seq) return fail(m->ctx, NX_ERR_CAPACITY, "decode exceeds max_seq");
+        for (int s = 0; s < steps; ++s) {
+            const int32_t t = tokens[(size_t)b * steps + s];
+            if (t < 0 || t >= c.vocab) return fail(m->ctx, NX_ERR_INVALID, "forced token out of vocabulary");
+        }
+    }
+    if (nact == 0) return fail(m->ctx, NX_ERR_STATE, "decode with no active sequence");
+    {
+        std::vector<int> want((size_t)B, -1);
+        for (int b = 0; b < B; ++b)
+            if (m->active[(size_t)b]) want[(size_t)b] = m->hpos[(size_t)b] + steps;
+        NX_TRY(pool_ensure(m, want));
+    }
+    NX_TRY(ensure_graph(m));
+    hipStream_t st = m->ctx->stream;
+    for (int b = 0; b < B; ++b) m->h_stage[b] = 1 << 30;  // nothing is recorded
+    NX_HIP(m->ctx, hipMemcpyAsync(m->base, m->h_stage, (size_t)B * 4, hipMemcpyHostToDevice, st));
+    std::vector<int32_t> feed((size_t)B);
+    const size_t V = (size_t)c.vocab;
+    for (int s = 0; s < steps; ++s) {
+        for (int b = 0; b < B; ++b) feed[(size_t)b] = m->active[(size_t)b] ? tokens[(size_t)b * steps + s] : nx::kFeedPark;
+        NX_TRY(upload_feed(m, feed.data(), nullptr));
+        NX_HIP(m->ctx, hipGraphLaunch(m->exec, st));
+        if (logits)
+            for (int b = 0; b < B; ++b)
+                NX_HIP(m->ctx, hipMemcpyAsync(logits + ((size_t)b * steps + s) * V, m->logits + (size_t)b * V, V * 4,
+                                              hipMemcpyDeviceToHost, st));
+    }
+    NX_HIP(m->ctx, hipStreamSynchronize(st));
+    for (int b = 0; b < B; ++b)
+        if (m->active[(size_t)b]) m->hpos[(size_t)b] += steps;
+    return feed_decode(m);
+}
+
 nx_status nx_model_logits(nx_model* m, float* out) {
     if (!m || !out) return NX_ERR_INVALID;
     NX_HIP(m->ctx, hipMemcpyAsync(out, m->logits, (size_t)m->c.batch * m->c.vocab * 4, hipMemcpyDeviceToHost, m->ctx->stream));
@@ -1673,18 +1761,22 @@ std::vector<NxfTensorSpec> nxf_specs(nx_model* m) {
                   RowMap mp) {
         t.push_back({name, std::move(shape), NX_DTYPE_I4, rows, G * 16, G * 2, w, sc, mp});
     };
-    auto f32 = [&](const std::string& name, float* w) {
-        t.push_back({name, {(int64_t)d}, NX_DTYPE_F32, 1, d * 4, 0, reinterpret_cast<uint8_t*>(w), nullptr, plain(1)});
+    auto f32 = [&](const std::string& name, float* w, size_t n) {
+        t.push_back({name, {(int64_t)n}, NX_DTYPE_F32, 1, n * 4, 0, reinterpret_cast<uint8_t*>(w), nullptr, plain(1)});
     };
     t.push_back({"tok_embeddings.weight", {(int64_t)d, (int64_t)V}, NX_DTYPE_F16, V, d * 2, 0,
                  reinterpret_cast<uint8_t*>(m->embed), nullptr, plain(V)});
-    f32("norm.weight", m->norm_final);
+    f32("norm.weight", m->norm_final, d);
     i4("output.weight", {(int64_t)d, (int64_t)V}, V, Gd, m->lm_w, m->lm_s, plain(V));
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = m->layers[(size_t)L];
         const std::string p = "layers." + std::to_string(L) + ".";
-        f32(p + "attention_norm.weight", ly.norm_attn);
-        f32(p + "ffn_norm.weight", ly.norm_ffn);
+        f32(p + "attention_norm.weight", ly.norm_attn, d);
+        f32(p + "ffn_norm.weight", ly.norm_ffn, d);
+        if (c.qk_norm) {  // the Q/K norms of hybrid_model.cpp:1952-1953, head_dim long
+            f32(p + "attn_q_norm.weight", ly.qnorm, (size_t)c.head_dim);
+            f32(p + "attn_k_norm.weight", ly.knorm, (size_t)c.head_dim);
+        }
         i4(p + "attention.wq.weight", {(int64_t)d, (int64_t)qd}, qd, Gd, ly.wqkv, ly.sqkv, plain(qd, 0));
         i4(p + "attention.wk.weight", {(int64_t)d, (int64_t)kvd}, kvd, Gd, ly.wqkv, ly.sqkv, plain(kvd, qd));
         i4(p + "attention.wv.weight", {(int64_t)d, (int64_t)kvd}, kvd, Gd, ly.wqkv, ly.sqkv, plain(kvd, qd + kvd));
@@ -1830,7 +1922,10 @@ nx_status nx_model_load_nxf(nx_ctx* ctx, const char* path, const nx_model_config
         c.head_dim = (int)man.head_dim;
         c.vocab = (int)man.vocab_size;
         c.n_experts = (int)man.num_experts;
-        c.top_k = (int)man.num_active_experts;
+        // no count in the manifest: ten experts per token, as the reference
+        // runs it (hybrid_model.cpp:1648, capped at the expert count, :1675)
+        c.top_k = c.n_experts > 0 && man.num_active_experts == 0 ? std::min(10, c.n_experts)
+                                                                   : (int)man.num_active_experts;
         c.rope_theta = man.rope_theta;
         c.eps = man.rms_norm_eps;
         c.norm_sigma = 0.0f;
@@ -1843,6 +1938,16 @@ nx_status nx_model_load_nxf(nx_ctx* ctx, const char* path, const nx_model_config
             break;
         }
         c.ffn = (int)info.shape[info.ndim - 1];
+        // per-head Q/K norms where the file has them (hybrid_model.cpp:1952-1953
+        // loads each when present); both or neither
+        int tq = -1, tk = -1;
+        nx_nxf_find(r, "layers.0.attn_q_norm.weight", &tq);
+        nx_nxf_find(r, "layers.0.attn_k_norm.weight", &tk);
+        if ((tq < 0) != (tk < 0)) {
+            s = fail(ctx, NX_ERR_UNSUPPORTED, "nxf '%s': a Q norm without a K norm (or the reverse)", path);
+            break;
+        }
+        c.qk_norm = tq >= 0 ? 1 : 0;
         if ((s = check_config(ctx, c)) != NX_OK) break;
         m = new nx_model();
         m->ctx = ctx;

@@ -44,6 +44,7 @@ class ModelConfig(C.Structure):
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
         ("warm_window", C.c_int), ("cool_window", C.c_int), ("kv_blocks", C.c_int),
+        ("qk_norm", C.c_int),
     ]
 
 
@@ -153,6 +154,7 @@ _SIGS = {
     "nx_model_kv_pages": (_I, [_P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "nx_model_pending": (_I, [_P, _P]),
     "nx_model_decode": (_I, [_P, _I, _P]),
+    "nx_model_decode_forced": (_I, [_P, _P, _I, _P]),
     "nx_model_logits": (_I, [_P, _P]),
     "nx_model_position": (_I, [_P, _I, C.POINTER(_I)]),
     "nx_model_step_bytes": (_I, [_P, C.POINTER(C.c_double)]),
@@ -331,13 +333,16 @@ class Model:
         m = r.manifest()
         w1 = r.get_tensor("layers.0.feed_forward.experts.w1.weight" if m.num_experts
                           else "layers.0.feed_forward.w1.weight")
+        qk = any(t.name == "layers.0.attn_q_norm.weight" for t in r.tensors())
         r.close()
         self.cfg = ModelConfig(
             n_layers=m.num_layers, d_model=m.hidden_dim, n_heads=m.num_heads,
             n_kv_heads=m.num_kv_heads, head_dim=m.head_dim, ffn=w1.shape[-1], vocab=m.vocab_size,
-            n_experts=m.num_experts, top_k=m.num_active_experts, max_seq=max_seq, batch=batch,
+            n_experts=m.num_experts,
+            top_k=(min(10, m.num_experts) if m.num_experts and not m.num_active_experts else m.num_active_experts),
+            max_seq=max_seq, batch=batch,
             kv_kind=kv_kind, rope_theta=m.rope_theta, eps=m.rms_norm_eps, seed=seed,
-            hot_window=hot_window, warm_window=warm_window, cool_window=cool_window)
+            hot_window=hot_window, warm_window=warm_window, cool_window=cool_window, qk_norm=int(qk))
         return self
 
     def save_nxf(self, path):
@@ -395,6 +400,17 @@ class Model:
     def decode(self, steps: int) -> np.ndarray:
         out = np.empty((self.cfg.batch, steps), np.int32)
         self.ctx.check(self.ctx.L.nx_model_decode(self.h, steps, out.ctypes.data), "nx_model_decode")
+        return out
+
+    def decode_forced(self, tokens) -> np.ndarray:
+        """Teacher-forced steps (nx_model_decode_forced): sequence b consumes
+        tokens[b][s] at step s; returns the logits [batch][steps][vocab]."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        if t.ndim != 2 or t.shape[0] != self.cfg.batch:
+            raise ValueError("tokens must be [batch][steps]")
+        out = np.empty((self.cfg.batch, t.shape[1], self.cfg.vocab), np.float32)
+        self.ctx.check(self.ctx.L.nx_model_decode_forced(self.h, t.ctypes.data, t.shape[1], out.ctypes.data),
+                       "nx_model_decode_forced")
         return out
 
     def decode_untimed(self, steps: int):

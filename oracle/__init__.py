@@ -33,6 +33,7 @@ class Cfg(C.Structure):
         ("kv_kind", C.c_int), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("seed", C.c_uint64), ("norm_sigma", C.c_float), ("hot_window", C.c_int),
         ("warm_window", C.c_int), ("cool_window", C.c_int), ("kv_blocks", C.c_int),
+        ("qk_norm", C.c_int),
     ]
 
 
@@ -72,6 +73,7 @@ def _load() -> C.CDLL:
         "nxo_sample": (C.c_int, [_f32p, C.c_int, C.c_float, C.c_int, C.c_float, C.c_float]),
         "nxo_rope_table": (None, [C.c_int, C.c_int, C.c_double, _f32p, _f32p]),
         "nxo_rope": (None, [_f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]),
+        "nxo_head_rmsnorm": (None, [_f32p, C.c_int, C.c_int, C.c_void_p, C.c_float]),
         "nxo_swiglu": (None, [_f32p, _f32p, C.c_int, _f32p]),
         "nxo_argmax": (C.c_int, [_f32p, C.c_int]),
         "nxo_kv_append_f16": (None, [_f32p, _f32p, _u16p, _u16p, _i32p, C.c_int, C.c_int,

@@ -264,6 +264,10 @@ void nxo_rope(float* x, int n_heads, int hd, int pos, const float* cos_tab, cons
     }
 }
 
+void nxo_head_rmsnorm(float* x, int n_heads, int hd, const float* w, float eps) {
+    for (int h = 0; h < n_heads; ++h) nxo_rmsnorm(x + (size_t)h * hd, w, hd, eps, x + (size_t)h * hd);
+}
+
 void nxo_swiglu(const float* g, const float* u, int n, float* out) {
     for (int i = 0; i < n; ++i) out[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
 }
@@ -769,6 +773,7 @@ typedef struct {
     uint16_t *kcn, *vcn;
     float ksign[NXO_TQ_D], vsign[NXO_TQ_D];
     float *norm_attn, *norm_ffn;             /* RMSNorm weights, NULL = 1.0 */
+    float *qnorm, *knorm;                    /* per-head Q/K RMSNorm weights [hd] (qk_norm), NULL = 1.0 */
 } layer_t;
 
 struct nxo_model {
@@ -858,6 +863,10 @@ nxo_model* nxo_model_create(const nxo_cfg* cfg) {
         make_qmat(&ly->wo, d, m->qdim, seed, NXO_TID_LAYER(L, NXO_W_O), 0.02);
         ly->norm_attn = make_norm(d, seed, NXO_TID_LAYER(L, NXO_N_ATTN), c->norm_sigma);
         ly->norm_ffn = make_norm(d, seed, NXO_TID_LAYER(L, NXO_N_FFN), c->norm_sigma);
+        if (c->qk_norm) {
+            ly->qnorm = make_norm(hd, seed, NXO_TID_LAYER(L, NXO_N_QNORM), c->norm_sigma);
+            ly->knorm = make_norm(hd, seed, NXO_TID_LAYER(L, NXO_N_KNORM), c->norm_sigma);
+        }
         if (c->n_experts == 0) {
             make_qmat(&ly->w1, c->ffn, d, seed, NXO_TID_LAYER(L, NXO_W_GATE), 0.02);
             make_qmat(&ly->w3, c->ffn, d, seed, NXO_TID_LAYER(L, NXO_W_UP), 0.02);
@@ -931,6 +940,7 @@ void nxo_model_free(nxo_model* m) {
         free(ly->kc4); free(ly->kc3); free(ly->vc4); free(ly->vc3); free(ly->kn); free(ly->vn);
         free(ly->kcc); free(ly->vcc); free(ly->kcn); free(ly->vcn);
         free(ly->norm_attn); free(ly->norm_ffn);
+        free(ly->qnorm); free(ly->knorm);
     }
     free(m->norm_final);
     free(m->layers);
@@ -1052,6 +1062,10 @@ static void forward_impl(nxo_model* m, const int32_t* tokens, float* logits, dou
             float* qb = m->q + (size_t)b * m->qdim;
             float* kb = m->k + (size_t)b * m->kvdim;
             float* vb = m->v + (size_t)b * m->kvdim;
+            if (c->qk_norm) {  /* model/hybrid_model.cpp:1325-1349, before RoPE */
+                nxo_head_rmsnorm(qb, hq, hd, ly->qnorm, c->eps);
+                nxo_head_rmsnorm(kb, hkv, hd, ly->knorm, c->eps);
+            }
             nxo_rope(qb, hq, hd, m->pos[b], m->rope_cos, m->rope_sin);
             nxo_rope(kb, hkv, hd, m->pos[b], m->rope_cos, m->rope_sin);
             if (c->kv_kind == 0)

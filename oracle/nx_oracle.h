@@ -86,6 +86,10 @@ void nxo_rmsnorm(const float* x, const float* w, int d, float eps, float* out);
  * (a,b) -> (a*c - b*s, a*s + b*c). */
 void nxo_rope_table(int max_pos, int hd, double theta, float* cos_tab, float* sin_tab);
 void nxo_rope(float* x, int n_heads, int hd, int pos, const float* cos_tab, const float* sin_tab);
+/* The Q/K norm of model/hybrid_model.cpp:1325-1349: every hd-long slice of
+ * x[n_heads * hd] through nxo_rmsnorm with the same hd weights (NULL = 1.0),
+ * in place. */
+void nxo_head_rmsnorm(float* x, int n_heads, int hd, const float* w, float eps);
 /* model/hybrid_model.cpp:1627-1630: out = g / (1 + expf(-g)) * u */
 void nxo_swiglu(const float* g, const float* u, int n, float* out);
 /* model/hybrid_model.cpp:2027-2038: first maximum wins (strict >). */
@@ -263,6 +267,9 @@ typedef struct {
                                       the positions kept Cool (a multiple of 16), older pages evicted */
     int kv_blocks;                 /* the GPU runner's shared page pool; which physical page holds a
                                       position changes no result, so the restatement ignores it */
+    int qk_norm;                   /* 1: per-head RMSNorm of q and k after the projection, before
+                                      RoPE, with head_dim-long weights per layer (attn_q_norm /
+                                      attn_k_norm, model/hybrid_model.cpp:1325-1349) */
 } nxo_cfg;
 
 typedef struct nxo_model nxo_model;
@@ -331,7 +338,7 @@ uint32_t nxo_xxh32(const void* data, size_t len, uint32_t seed);
 #define NXO_TID_LAYER(L, kind) (0x100u * ((uint32_t)(L) + 1u) + (uint32_t)(kind))
 enum { NXO_W_Q = 0, NXO_W_K = 1, NXO_W_V = 2, NXO_W_O = 3, NXO_W_GATE = 4, NXO_W_UP = 5,
        NXO_W_DOWN = 6, NXO_W_ROUTER = 7, NXO_TQ_KSIGN = 8, NXO_TQ_VSIGN = 9, NXO_N_ATTN = 10,
-       NXO_N_FFN = 11 };
+       NXO_N_FFN = 11, NXO_N_QNORM = 12, NXO_N_KNORM = 13 };
 /* expert e of layer L: NXO_TID_EXPERT(L, e, 0=gate,1=up,2=down) */
 #define NXO_TID_EXPERT(L, e, w) (0x01000000u + 0x1000u * (uint32_t)(L) + 4u * (uint32_t)(e) + (uint32_t)(w))
 /* synthetic context of sequence b, layer L, kv = 0 (K) / 1 (V) */

@@ -12,19 +12,21 @@ oracle on identical seeded inputs:
 - the 8B shape at batch 8: a full layer plus lm_head against the oracle, and
   the 32-layer decode's determinism and range.
 
-Greedy tokens must equal the oracle's (a step whose oracle top-two margin is
-a numerical tie may pick the other token, after which the sequences
-diverge); logits within 1e-3 when the tokens agree.  TurboQuant codes of the
-pages compressed during the decode must be bit-exact."""
+Every decode is teacher-forced: the GPU model and the oracle consume the
+oracle's greedy tokens, and at every step the logits must agree within
+1e-3 (pages the decode itself compresses: TQ_TOL) and the greedy token must
+be the oracle's wherever the oracle's top-two margin is not a numerical
+tie.  TurboQuant codes of the pages compressed during the decode must be
+bit-exact."""
 import numpy as np
 import pytest
 
 import nexus_amd
 import oracle
-from conftest import f16, rel_err
+from conftest import check_forced, f16, forced_logits, rel_err
 from test_gpu_kernels import _tq_pools, up
-from test_gpu_model import LLAMA8B, TIE_MARGIN, assert_greedy_parity, top2_margin
-from test_gpu_tiered import TQ_TIE
+from test_gpu_model import LLAMA8B, TIE_MARGIN
+from test_gpu_tiered import TQ_TIE, TQ_TOL
 
 pytestmark = pytest.mark.gpu
 L = oracle.lib
@@ -38,39 +40,23 @@ def _start_tokens(cfg):
     return np.array([L.nxo_rand_u64(cfg["seed"], 5, b) % cfg["vocab"] for b in range(cfg["batch"])], np.int32)
 
 
-def _oracle_steps(om, start, steps):
-    tok, want, margins = start, [], []
-    logits = None
-    for _ in range(steps):
-        logits = om.forward(tok)
-        tok = logits.argmax(axis=1).astype(np.int32)
-        want.append(tok)
-        margins.append(top2_margin(logits))
-    return np.stack(want, 1), np.stack(margins, 1), logits
-
-
-def _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=0, tie=TIE_MARGIN, check_pages=None):
-    """Fill ctx_len positions on both sides, decode `steps` greedy tokens,
-    compare tokens and last logits; check_pages(gm, om) runs before close."""
+def _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=0, tol=1e-3, tie=TIE_MARGIN, check_pages=None):
+    """Fill ctx_len positions on both sides and run `steps` teacher-forced
+    decode steps (check_forced); check_pages(gm, om) runs before close."""
+    label = f"ctx {ctx_len} batch {cfg['batch']} kv_kind {cfg['kv_kind']} seed {cfg['seed']:#x}"
     print(f"[case] {cfg} ctx {ctx_len} steps {steps}", flush=True)
     gm = nexus_amd.Model(ctx, **cfg)
     gm.fill_context(ctx_len, n_outlier)
     start = gm.pending()
-    got = gm.decode(steps)
-    glog = gm.logits()
     om = oracle.Model(**cfg)
     om.fill_context(ctx_len, n_outlier)
     assert np.array_equal(start, _start_tokens(cfg))
-    want, margins, logits = _oracle_steps(om, start, steps)
+    glog, olog = forced_logits(gm, om, start, steps)
     if check_pages is not None:
         check_pages(gm, om)
     gm.close()
     om.close()
-    print("min oracle top1-top2 margin", float(margins.min()), flush=True)
-    assert_greedy_parity(got, want, margins, tie=tie)
-    if np.array_equal(got, want):
-        assert rel_err(glog, logits) < 1e-3
-    return got, want
+    check_forced(glog, olog, tol, tie, label)
 
 
 # ------------------------------------------------- 8B @ 32K TurboQuant pages --
@@ -102,9 +88,10 @@ def test_tq_attention_parity_pipelined(ctx, lens):
 
 def test_8b_turboquant_32k_one_layer(ctx):
     """One 8B-shaped layer plus lm_head over 32768 TurboQuant positions
-    (4 outlier channels per head x10), three greedy steps."""
+    (4 outlier channels per head x10), 64 teacher-forced decode steps (the
+    steps of the 32K workload), each appending its position to the pages."""
     cfg = dict(LLAMA8B, n_layers=1, kv_kind=1, max_seq=32768 + 256, seed=0x32C4)
-    _filled_parity(ctx, cfg, 32768, 3, n_outlier=4)
+    _filled_parity(ctx, cfg, 32768, 64, n_outlier=4, tol=TQ_TOL, tie=TQ_TIE)
 
 
 def test_8b_tiered_32k_one_layer(ctx):
@@ -122,7 +109,7 @@ def test_8b_tiered_32k_one_layer(ctx):
                 assert form == 1, (p, kv)
                 assert np.array_equal(g, om.kv_read(0, 0, p, kv, 1)), (p, kv)
 
-    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tol=TQ_TOL, tie=TQ_TIE, check_pages=pages)
 
 
 def test_tiered_pipelined_batch8(ctx):
@@ -142,7 +129,7 @@ def test_tiered_pipelined_batch8(ctx):
                     form, g = gm.kv_read(1, b, p, kv)
                     assert form == 1 and np.array_equal(g, om.kv_read(1, b, p, kv, 1)), (b, p, kv)
 
-    _filled_parity(ctx, cfg, 4000, 20, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+    _filled_parity(ctx, cfg, 4000, 20, n_outlier=4, tol=TQ_TOL, tie=TQ_TIE, check_pages=pages)
 
 
 def test_8b_three_tier_32k_one_layer(ctx):
@@ -166,7 +153,7 @@ def test_8b_three_tier_32k_one_layer(ctx):
             form, g = gm.kv_read(0, 0, p, 0)
             assert form == 1 and np.array_equal(g, om.kv_read(0, 0, p, 0, 1)), p
 
-    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tol=TQ_TOL, tie=TQ_TIE, check_pages=pages)
 
 
 def test_8b_evicting_tiers_32k_one_layer(ctx):
@@ -187,7 +174,7 @@ def test_8b_evicting_tiers_32k_one_layer(ctx):
                 form, g = gm.kv_read(0, 0, p, kv)
                 assert form == 2 and np.array_equal(g, om.kv_read(0, 0, p, kv, 2)), (p, kv)
 
-    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+    _filled_parity(ctx, cfg, ctx_len, steps, n_outlier=4, tol=TQ_TOL, tie=TQ_TIE, check_pages=pages)
 
 
 def test_three_tier_pipelined_batch8(ctx):
@@ -210,7 +197,7 @@ def test_three_tier_pipelined_batch8(ctx):
                 form, g = gm.kv_read(1, b, p, 1)
                 assert form == 1 and np.array_equal(g, om.kv_read(1, b, p, 1, 1)), (b, p)
 
-    _filled_parity(ctx, cfg, 4000, 20, n_outlier=4, tie=TQ_TIE, check_pages=pages)
+    _filled_parity(ctx, cfg, 4000, 20, n_outlier=4, tol=TQ_TOL, tie=TQ_TIE, check_pages=pages)
 
 
 # ------------------------------------------------------------ Mixtral shape --
@@ -289,3 +276,46 @@ def test_8b_decode_properties_batch8(ctx):
         gm.close()
     assert np.array_equal(runs[0][0], runs[1][0])
     assert np.array_equal(runs[0][1], runs[1][1])
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_mixtral_decode_properties(ctx, batch):
+    """The 32-layer Mixtral shape (8 experts of 14336, top-2, all resident)
+    over 4096 positions: deterministic across two models, tokens in range,
+    finite logits, and the step's algorithmic bytes between the closed forms
+    for top-2 and for every expert active in each layer."""
+    cfg = dict(MIXTRAL, batch=batch)
+    d, F, E, V, qkv = 4096, 14336, 8, 32000, 4096 + 2 * 1024
+    qb = lambda n, k: n * ((k + 31) // 32) * 18  # int4-g32 codes + fp16 scales
+    shared = qb(V, d) + 32 * (qb(qkv, d) + qb(d, 4096) + qb(E, d))
+    expert = qb(2 * F, d) + qb(d, F)
+    kv = batch * 32 * 4096 * 2 * 8 * 128 * 2
+    runs = []
+    for _ in range(2):
+        print(f"[case] mixtral 32 layers batch {batch} ctx 4096", flush=True)
+        gm = nexus_amd.Model(ctx, **cfg)
+        gm.fill_context(4096, 0)
+        toks = gm.decode(4)
+        lg = gm.logits()
+        nb = gm.step_bytes()
+        assert shared + 32 * 2 * expert + kv - 1e7 <= nb <= shared + 32 * E * expert + kv + 1e8, nb
+        assert toks.min() >= 0 and toks.max() < V
+        assert np.all(np.isfinite(lg))
+        runs.append((toks, lg))
+        gm.close()
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
+
+
+@pytest.mark.parametrize("batch,kv_kind", [(1, 0), (8, 0), (1, 1)])
+def test_8b_one_layer_qk_norm(ctx, batch, kv_kind):
+    """One 8B-shaped layer with per-head Q/K RMSNorm (the attn_q_norm /
+    attn_k_norm of Qwen3- and Gemma-style models, hybrid_model.cpp:1325-1349,
+    weights 1 + N(0, 0.1)) at 512 positions: the batch-1 streaming and
+    batch-8 matrix-core QKV GEMVs write the projection alone, the Q/K norm
+    launch normalizes, rotates and writes the pages (TurboQuant pages: the
+    attention launch appends), four teacher-forced steps."""
+    cfg = dict(LLAMA8B, n_layers=1, max_seq=1024, batch=batch, kv_kind=kv_kind, qk_norm=1, norm_sigma=0.1,
+               seed=0x9C8B + batch + 16 * kv_kind)
+    _filled_parity(ctx, cfg, 512, 4, n_outlier=4 if kv_kind else 0, tol=TQ_TOL if kv_kind else 1e-3,
+                   tie=TQ_TIE if kv_kind else TIE_MARGIN)

@@ -356,6 +356,22 @@ def test_moe_route(ctx):
         assert np.allclose(w[b], ow, rtol=2e-6, atol=0)
 
 
+@pytest.mark.parametrize("B,E,k", [(8, 256, 16), (3, 64, 10), (64, 128, 2)])
+def test_moe_route_wide(ctx, B, E, k):
+    """Routing over up to 256 experts, top-16 and 64 sequences: ids equal the
+    oracle's, weights within 2e-6."""
+    rng = np.random.default_rng(E * 7 + k)
+    logits = (rng.normal(0, 1, (B, E)) * 2).astype(np.float32)
+    ib, wb = ctx.alloc(B * k * 4), ctx.alloc(B * k * 4)
+    ctx.check(ctx.L.nx_moe_route_topk(ctx.h, up(ctx, logits), ib, wb, E, k, B), "route")
+    ids, w = ctx.download(ib, (B, k), np.int32), ctx.download(wb, (B, k), np.float32)
+    for b in range(B):
+        oi, ow = np.empty(k, np.int32), np.empty(k, np.float32)
+        L.nxo_moe_route(np.ascontiguousarray(logits[b]), E, k, oi, ow)
+        assert np.array_equal(ids[b], oi)
+        assert np.allclose(w[b], ow, rtol=2e-6, atol=0)
+
+
 def test_moe_expert_ffn(ctx):
     rng = np.random.default_rng(10)
     d, F, E, k, B = 256, 688, 4, 2, 3

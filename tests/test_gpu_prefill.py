@@ -70,18 +70,21 @@ def oracle_script(cfg, script):
     ("prompt", [B][P]) and ("decode", n) entries: a prompt is run token by
     token and yields its last token's successor; decode steps feed back."""
     om = oracle.Model(**cfg)
-    toks, margins, pending = [], [], None
+    toks, margins, pending, plog = [], [], None, []
     for kind, v in script:
         steps = [v[:, i].copy() for i in range(v.shape[1])] if kind == "prompt" else [None] * v
         for j, t in enumerate(steps):
             lg = om.forward(np.ascontiguousarray(pending if t is None else t, np.int32))
             if kind == "prompt" and j < len(steps) - 1:
                 continue
+            if kind == "prompt":
+                plog.append(lg)
             pending = np.argmax(lg, axis=1).astype(np.int32)
             part = np.sort(lg, axis=1)
             toks.append(pending.copy())
             margins.append(part[:, -1] - part[:, -2])
     om.close()
+    oracle_script.prompt_logits = plog  # logits after each prompt of the last script
     return np.stack(toks, 1), np.stack(margins, 1)
 
 
@@ -131,8 +134,9 @@ def test_batched_prefill_matches_token_steps(ctx, P, kind):
     tb, lb, pb = gpu_script(ctx, cfg, script, False)
     assert pa == pb == P + 10
     e = rel_err(la[0], lb[0])
-    print(f"P={P} {kind} logits rel_err={e:.2e}")
-    assert e < LOGIT_TOL[kind]
+    eo = max(rel_err(x[0], oracle_script.prompt_logits[0]) for x in (la, lb))
+    print(f"P={P} {kind} logits rel_err={e:.2e}, against the oracle {eo:.2e}")
+    assert e < LOGIT_TOL[kind] and eo < LOGIT_TOL[kind]
     assert_greedy_parity(ta, want, margins)
     assert_greedy_parity(tb, want, margins)
 
@@ -145,7 +149,10 @@ def test_batched_prefill_two_chunks_matches_oracle(ctx, kind):
     cfg = dict(KINDS[kind], max_seq=2304, seed=0x600, norm_sigma=0.1)
     script = [("prompt", oracle.prompt_tokens(cfg["seed"], 1, 2100, cfg["vocab"])), ("decode", 7)]
     want, margins = oracle_script(cfg, script)
-    got, _, _ = gpu_script(ctx, cfg, script, True)
+    got, lg, _ = gpu_script(ctx, cfg, script, True)
+    e = rel_err(lg[0], oracle_script.prompt_logits[0])
+    print(f"{kind} 2100-token prompt: logits rel_err against the oracle {e:.2e}")
+    assert e < LOGIT_TOL[kind]
     assert_greedy_parity(got, want, margins)
 
 
@@ -166,6 +173,12 @@ def test_batched_prefill_batch2_and_after_decode(ctx, kind):
         e = rel_err(x, y)
         print(f"{kind} logits rel_err={e:.2e}")
         assert e < LOGIT_TOL[kind]
+    # against the oracle: after the first prompt, and after the second where
+    # the tokens decoded between them were the oracle's
+    plog = oracle_script.prompt_logits
+    assert rel_err(la[0], plog[0]) < LOGIT_TOL[kind]
+    if np.array_equal(ta[:, :4], want[:, :4]):
+        assert rel_err(la[1], plog[1]) < LOGIT_TOL[kind]
 
 
 @pytest.mark.parametrize("kv_kind", [0, 1])

@@ -6,28 +6,22 @@ in one softmax (the mixed-tier gather of get_vectors, :161-230).  With a
 warm_window, pages that also leave the Warm range are re-encoded Cool
 (3-bit codes on every coordinate; the Warm -> Cool step of compress_tier)
 and attention reads three tiers.  Checked against the oracle's
-restatement: greedy tokens, logits, and the stored bytes of every
-compressed page bit-exact."""
+restatement: greedy tokens, teacher-forced logits of every step, and the
+stored bytes of every compressed page bit-exact."""
 import numpy as np
 import pytest
 
 import nexus_amd
 import oracle
-from conftest import rel_err
-from test_gpu_model import TINY, assert_greedy_parity, run_both, top2_margin
+from conftest import TQ_DECODE_TIE, TQ_DECODE_TOL, TQ_TIE, TQ_TOL, check_forced, forced_logits, rel_err
+from test_gpu_model import TINY, assert_greedy_parity, run_both, run_forced, top2_margin
 
 pytestmark = pytest.mark.gpu
 
 TQ_TINY = dict(TINY, n_heads=4, n_kv_heads=2, head_dim=128, d_model=512)
 
 
-# Positions produced by the decode are compressed from K and V that the GPU
-# and the oracle compute with different fp32 summation orders, so their fp16
-# values can differ in the last bit and a TurboQuant code can land one level
-# apart; one such code moves a logit by up to about 1e-2.  Tokens may differ
-# only where the oracle's top-two margin is below this bound (the
-# compressor's codes for identical inputs are checked bit-exact below).
-TQ_TIE = 2e-2
+
 
 
 @pytest.mark.parametrize("batch,H", [(1, 16), (2, 48)])
@@ -36,17 +30,8 @@ def test_tiered_greedy_parity(ctx, batch, H):
     are compressed every 16 steps from position H + 15 on."""
     cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, seed=0x7E1 + H)
     got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
-    assert_greedy_parity(got, want, margins, tie=TQ_TIE)
-
-
-def _oracle_steps(om, start, steps):
-    tok, want, margins = start, [], []
-    for _ in range(steps):
-        logits = om.forward(tok)
-        tok = logits.argmax(axis=1).astype(np.int32)
-        want.append(tok)
-        margins.append(top2_margin(logits))
-    return np.stack(want, 1), np.stack(margins, 1), logits
+    assert_greedy_parity(got, want, margins, tie=TQ_DECODE_TIE)
+    run_forced(ctx, cfg, 12, 100, tol=TQ_DECODE_TOL, tie=TQ_DECODE_TIE)
 
 
 def test_tiered_filled_context_and_compressor(ctx):
@@ -76,16 +61,12 @@ def test_tiered_filled_context_and_compressor(ctx):
     check(list(range(0, 224, 7)) + [223], 1)
     check(range(224, 300), 0)
     start = gm.pending()
-    got = gm.decode(steps)
-    glog = gm.logits()
+    glog, olog = forced_logits(gm, om, start, steps)
     check(range(224, 272), 1)  # compressed on the device during the decode
     check(range(272, 300), 0)
     gm.close()
-    want, margins, logits = _oracle_steps(om, start, steps)
     om.close()
-    assert_greedy_parity(got, want, margins)
-    if np.array_equal(got, want):
-        assert rel_err(glog, logits) < 1e-3
+    check_forced(glog, olog, TQ_TOL, TQ_TIE, f"seed {cfg['seed']:#x}")
 
 
 @pytest.mark.parametrize("hq,hkv,H,ctx_len", [(8, 2, 128, 700), (8, 1, 32, 1000), (4, 4, 256, 260)])
@@ -102,19 +83,15 @@ def test_tiered_filled_context_group_sizes(ctx, hq, hkv, H, ctx_len):
     om = oracle.Model(**cfg)
     om.fill_context(ctx_len, 4)
     start = gm.pending()
-    got = gm.decode(steps)
-    glog = gm.logits()
+    glog, olog = forced_logits(gm, om, start, steps)
     cold = 16 * max(0, (ctx_len - H) // 16)
     for p in list(range(0, cold, 37)) + ([cold - 1] if cold else []):
         for kv in range(2):
             form, g = gm.kv_read(cfg["n_layers"] - 1, 0, p, kv)
             assert form == 1 and np.array_equal(g, om.kv_read(cfg["n_layers"] - 1, 0, p, kv, 1)), (p, kv)
     gm.close()
-    want, margins, logits = _oracle_steps(om, start, steps)
     om.close()
-    assert_greedy_parity(got, want, margins)
-    if np.array_equal(got, want):
-        assert rel_err(glog, logits) < 1e-3
+    check_forced(glog, olog, TQ_TOL, TQ_TIE, f"seed {cfg['seed']:#x}")
 
 
 def test_tiered_window_covering_context_matches_fp16_pages(ctx):
@@ -153,7 +130,8 @@ def test_three_tier_greedy_parity(ctx, batch, H, W, pool):
     cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, warm_window=W, seed=0x3C1 + H + W + pool,
                kv_blocks=pool)
     got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
-    assert_greedy_parity(got, want, margins, tie=TQ_TIE)
+    assert_greedy_parity(got, want, margins, tie=TQ_DECODE_TIE)
+    run_forced(ctx, cfg, 12, 100, tol=TQ_DECODE_TOL, tie=TQ_DECODE_TIE)
 
 
 def _check_forms(gm, om, n_layers, batch, ranges):
@@ -185,15 +163,11 @@ def test_three_tier_filled_context_and_compressors(ctx):
     _check_forms(gm, om, n_layers, 2, [(list(range(0, 192, 5)) + [191], 2), (range(192, 224, 3), 1),
                                        (range(224, 300, 4), 0)])
     start = gm.pending()
-    got = gm.decode(steps)
-    glog = gm.logits()
+    glog, olog = forced_logits(gm, om, start, steps)
     _check_forms(gm, om, n_layers, 2, [(range(192, 240), 2), (range(240, 272), 1), (range(272, 300), 0)])
     gm.close()
-    want, margins, logits = _oracle_steps(om, start, steps)
     om.close()
-    assert_greedy_parity(got, want, margins)
-    if np.array_equal(got, want):
-        assert rel_err(glog, logits) < 1e-3
+    check_forced(glog, olog, TQ_TOL, TQ_TIE, f"seed {cfg['seed']:#x}")
 
 
 @pytest.mark.parametrize("hq,hkv,H,W,ctx_len", [(8, 2, 128, 64, 700), (8, 1, 32, 32, 1000), (4, 4, 256, 16, 400)])
@@ -210,19 +184,15 @@ def test_three_tier_group_sizes(ctx, hq, hkv, H, W, ctx_len):
     om = oracle.Model(**cfg)
     om.fill_context(ctx_len, 4)
     start = gm.pending()
-    got = gm.decode(steps)
-    glog = gm.logits()
+    glog, olog = forced_logits(gm, om, start, steps)
     cool = 16 * max(0, (ctx_len + steps - H - W) // 16)
     for p in list(range(0, cool, 37)) + ([cool - 1] if cool else []):
         for kv in range(2):
             form, g = gm.kv_read(cfg["n_layers"] - 1, 0, p, kv)
             assert form == 2 and np.array_equal(g, om.kv_read(cfg["n_layers"] - 1, 0, p, kv, 2)), (p, kv)
     gm.close()
-    want, margins, logits = _oracle_steps(om, start, steps)
     om.close()
-    assert_greedy_parity(got, want, margins)
-    if np.array_equal(got, want):
-        assert rel_err(glog, logits) < 1e-3
+    check_forced(glog, olog, TQ_TOL, TQ_TIE, f"seed {cfg['seed']:#x}")
 
 
 def test_three_tier_empty_cool_range_matches_two_tiers(ctx):
@@ -264,7 +234,8 @@ def test_evicting_tiers_greedy_parity(ctx, batch, H, W, C):
     cfg = dict(TQ_TINY, batch=batch, kv_kind=2, hot_window=H, warm_window=W, cool_window=C,
                seed=0xE71 + H + W + C)
     got, want, margins = run_both(ctx, cfg, P=12, n_new=100)
-    assert_greedy_parity(got, want, margins, tie=TQ_TIE)
+    assert_greedy_parity(got, want, margins, tie=TQ_DECODE_TIE)
+    run_forced(ctx, cfg, 12, 100, tol=TQ_DECODE_TOL, tie=TQ_DECODE_TIE)
 
 
 def test_evicting_tiers_filled_context(ctx):
@@ -290,16 +261,12 @@ def test_evicting_tiers_filled_context(ctx):
     evicted(range(0, 128, 9))
     _check_forms(gm, om, n_layers, 2, [(range(128, 192, 3), 2), (range(192, 224, 3), 1), (range(224, 300, 4), 0)])
     start = gm.pending()
-    got = gm.decode(steps)
-    glog = gm.logits()
+    glog, olog = forced_logits(gm, om, start, steps)
     evicted([0, 127, 128, 175])
     _check_forms(gm, om, n_layers, 2, [(range(176, 240), 2), (range(240, 272), 1), (range(272, 300), 0)])
     gm.close()
-    want, margins, logits = _oracle_steps(om, start, steps)
     om.close()
-    assert_greedy_parity(got, want, margins)
-    if np.array_equal(got, want):
-        assert rel_err(glog, logits) < 1e-3
+    check_forced(glog, olog, TQ_TOL, TQ_TIE, f"seed {cfg['seed']:#x}")
 
 
 def test_evicting_tiers_config_rejected(ctx):

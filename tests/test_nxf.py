@@ -345,6 +345,63 @@ def test_loaded_model_matches_oracle_with_norm_weights(ctx, tmp_path):
 
 
 @pytest.mark.gpu
+def test_qk_norm_weights_round_trip(ctx, tmp_path):
+    """A model with per-head Q/K norms writes layers.L.attn_q_norm.weight and
+    attn_k_norm.weight (head_dim long, the names hybrid_model.cpp:1952-1953
+    loads); loading the file turns the norms on and decodes the original
+    model's tokens and logits exactly."""
+    cfg = dict(TINY, qk_norm=1, norm_sigma=0.1, seed=0x9C10)
+    p = tmp_path / "qk.nxf"
+    prompt = oracle.prompt_tokens(cfg["seed"], 1, 9, cfg["vocab"])
+    a = nexus_amd.Model(ctx, **cfg)
+    a.save_nxf(p)
+    ta = a.prefill(prompt)
+    toks_a, log_a = a.decode(10), a.logits()
+    a.close()
+    with NXFReader.open(p) as r:
+        t = r.get_tensor("layers.1.attn_k_norm.weight")
+        assert t is not None and list(t.shape) == [cfg["head_dim"]]
+    b = nexus_amd.Model.load_nxf(ctx, p, batch=1, max_seq=cfg["max_seq"], seed=cfg["seed"])
+    assert b.cfg.qk_norm == 1
+    tb = b.prefill(prompt)
+    toks_b, log_b = b.decode(10), b.logits()
+    b.close()
+    assert (ta == tb).all() and (toks_a == toks_b).all() and np.array_equal(log_a, log_b)
+
+
+@pytest.mark.gpu
+def test_load_without_expert_count_routes_ten(ctx, tmp_path):
+    """A MoE file whose manifest gives no active-expert count
+    (num_active_experts 0) runs ten experts per token, as the reference does
+    (hybrid_model.cpp:1648): the loaded model decodes as the top-10 model it
+    was saved from."""
+    import re
+    cfg = dict(TINY, n_experts=16, top_k=10, seed=0xA10)
+    p = tmp_path / "moe.nxf"
+    prompt = oracle.prompt_tokens(cfg["seed"], 1, 6, cfg["vocab"])
+    a = nexus_amd.Model(ctx, **cfg)
+    a.save_nxf(p)
+    ta = a.prefill(prompt)
+    toks_a, log_a = a.decode(8), a.logits()
+    a.close()
+    data = bytearray(p.read_bytes())
+    off = int.from_bytes(data[8:16], "little")
+    size = int.from_bytes(data[16:24], "little")
+    text = data[off:off + size].decode()
+    new = re.sub(r'"num_active_experts":\s*10', lambda m: m.group(0)[:-2] + " 0", text)
+    assert new != text and len(new) == len(text)
+    data[off:off + size] = new.encode()
+    p.write_bytes(bytes(data))
+    with NXFReader.open(p) as r:
+        assert r.manifest().num_active_experts == 0
+    b = nexus_amd.Model.load_nxf(ctx, p, batch=1, max_seq=cfg["max_seq"], seed=cfg["seed"])
+    tb = b.prefill(prompt)
+    toks_b, log_b = b.decode(8), b.logits()
+    b.close()
+    assert (ta == tb).all() and (toks_a == toks_b).all() and np.array_equal(log_a, log_b)
+
+
+@pytest.mark.gpu
 def test_model_load_rejects_a_corrupt_file(ctx, tmp_path):
     """A flipped byte inside layer 1's wo codes fails the load with a
     checksum error naming that tensor; nothing is returned."""

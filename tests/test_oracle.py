@@ -158,6 +158,32 @@ def test_rmsnorm_vs_fp64():
     assert rel_err(out, want) < 1e-6
 
 
+def test_head_rmsnorm_vs_fp64():
+    """The Q/K norm (hybrid_model.cpp:1325-1349): every head_dim slice is
+    normalized by its own RMS with the shared head_dim weights.  Heads of
+    scales 1e-2 .. 1e2 make a norm over the whole vector (or over the wrong
+    slice) fail; with unit weights each head's RMS is sqrt(m / (m + eps)), m
+    its mean square."""
+    heads, hd, eps = 5, 128, 1e-5
+    rng = np.random.default_rng(12)
+    x = (rng.normal(0, 1, (heads, hd)) * (10.0 ** np.arange(-2, 3))[:, None]).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    y = x.reshape(-1).copy()
+    L.nxo_head_rmsnorm(y, heads, hd, w.ctypes.data, eps)
+    xd = x.astype(np.float64)
+    ms = np.mean(xd ** 2, axis=1, keepdims=True)
+    want = xd / np.sqrt(ms + eps) * w
+    assert rel_err(y.reshape(heads, hd), want) < 1e-6
+    for h in range(heads):  # per head, not only overall
+        assert rel_err(y.reshape(heads, hd)[h], want[h]) < 1e-6
+    whole = xd / np.sqrt(np.mean(xd ** 2) + eps) * w
+    assert rel_err(y.reshape(heads, hd), whole) > 0.5
+    u = x.reshape(-1).copy()
+    L.nxo_head_rmsnorm(u, heads, hd, None, eps)
+    rms = np.sqrt(np.mean(u.reshape(heads, hd).astype(np.float64) ** 2, axis=1))
+    assert np.allclose(rms, np.sqrt(ms[:, 0] / (ms[:, 0] + eps)), rtol=1e-6, atol=0)
+
+
 def test_rope_is_complex_rotation():
     hd, heads, pos, theta = 64, 3, 37, 10000.0
     cos = np.empty((128, hd // 2), np.float32)
@@ -772,6 +798,33 @@ def test_moe_route_golden():
         L.nxo_moe_route(np.ascontiguousarray(g["logits"][i]), g["logits"].shape[1], k, ids, w)
         assert np.array_equal(ids, g["ids"][i])
         assert np.allclose(w, g["weights"][i], rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("E,k", [(64, 10), (256, 16), (160, 7)])
+def test_moe_route_wide(E, k):
+    """Routing over up to 256 experts and top-16 (the reference's default
+    is top-10, hybrid_model.cpp:1648): against the reference MoERouter built
+    from its sources (identity gate, so the logits are the hidden state) and
+    against a float64 softmax with the k largest by value (ties by id)."""
+    rng = np.random.default_rng(E + k)
+    R = oracle.ref()
+    for rep in range(6):
+        lg = (rng.standard_normal(E) * (0.5 + rep)).astype(np.float32)
+        ids = np.empty(k, np.int32)
+        w = np.empty(k, np.float32)
+        L.nxo_moe_route(lg, E, k, ids, w)
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        order = np.lexsort((np.arange(E), -p))[:k]
+        assert np.array_equal(ids, order)
+        assert np.allclose(w, p[order] / p[order].sum(), rtol=2e-6, atol=0)
+        if R is not None:
+            rid = np.empty(k, np.int32)
+            rw = np.empty(k, np.float32)
+            gate = np.eye(E, dtype=np.float32)
+            assert R.ref_moe_route(E, k, E, gate, lg, rid, rw) == k
+            assert np.array_equal(ids, rid)
+            assert np.allclose(w, rw, rtol=1e-6, atol=0)
 
 
 def test_moe_route_ties_pick_lower_id():
