@@ -120,9 +120,10 @@ nx_status nx_token_resume(nx_ctx* ctx);
 
 /* ------------------------------------------------------------------ ops -- */
 /* int4-g32 GEMV: y[b][n] = sum_k x[b][k] * (q[n][k] - 8) * s[n][k/32], fp32
- * accumulation, y stored fp16.  x fp16 [batch][K].  batch 1..8.  Any K and
- * alignment work; batch 2..8 runs its fastest form when K % 256 == 0 (whole
- * groups, a multiple of 8 per row) and the scales start 16-byte aligned.
+ * accumulation, y stored fp16.  x fp16 [batch][K].  batch 1..8, K up to
+ * 28672 (NX_ERR_UNSUPPORTED above).  Any K and alignment work; batch 2..8
+ * runs its fastest form when K % 256 == 0 (whole groups, a multiple of 8 per
+ * row) and the scales start 16-byte aligned.
  * Replaces ComputeDispatch::gemm_int4 (compute_dispatch.h:59,
  * compute_dispatch.cpp:142-176) -> MetalBackend::gemv_int4_nr8
  * (metal_backend.mm:607-642), and gemv_int4 (compute_dispatch.h:47) whose
@@ -243,7 +244,7 @@ nx_status nx_gemm_f32(nx_ctx* ctx, nx_buf A, nx_buf B, nx_buf C, int M, int N, i
 /* SwiGLU FFN of int4-g32 weights: y[b] (+)= W2 (fp16(silu(W1 x_b) * W3 x_b))
  * for batch rows of x fp16 [batch][d]; w13 [2F][d] holds W1 / W3 rows
  * interleaved (row 2f = W1 row f, 2f+1 = W3 row f), s13 their scales, w2
- * [d][F] and s2; y fp32 [batch][d].  The four dispatches of
+ * [d][F] and s2; y fp32 [batch][d]; d up to 14336, F up to 28672.  The four dispatches of
  * ComputeDispatch::gpu_ffn_fused (compute_dispatch.h:254,
  * compute_dispatch.cpp:682-727) as two launches (the SwiGLU is the gate/up
  * GEMV's epilogue); the intermediate activations stay on the device in a

@@ -424,7 +424,7 @@ static nx_status gemv_common(nx_ctx* ctx, nx_buf x, nx_buf wq, nx_buf sc, nx_buf
     if (N <= 0 || K <= 0 || batch < 1 || batch > 8)
         return fail(ctx, NX_ERR_INVALID, "%s: bad shape N=%d K=%d batch=%d", name, N, K, batch);
     const int G = (K + 31) / 32;
-    if (G > 7 * 64) return fail(ctx, NX_ERR_UNSUPPORTED, "%s: K=%d above 14336", name, K);
+    if (G > 14 * 64) return fail(ctx, NX_ERR_UNSUPPORTED, "%s: K=%d above 28672", name, K);
     NX_NEED(ctx, x, (size_t)batch * K * 2, "x");
     NX_NEED(ctx, wq, (size_t)N * G * 16, "weights");
     NX_NEED(ctx, sc, (size_t)N * G * 2, "scales");
@@ -618,7 +618,7 @@ nx_status nx_attn_decode_paged_f16(nx_ctx* ctx, nx_buf q, nx_buf kpool, nx_buf v
                                    int max_blocks, int num_blocks) {
     if (!ctx) return NX_ERR_INVALID;
     if (ctx->capturing) return fail(ctx, NX_ERR_STATE, "nx_attn_decode_paged_f16 validates the block table on the host; not capturable");
-    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || (hd != 64 && hd != 128) || max_blocks <= 0 ||
+    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || (hd != 64 && hd != 128 && hd != 256) || max_blocks <= 0 ||
         num_blocks <= 0)
         return fail(ctx, NX_ERR_INVALID, "nx_attn_decode_paged_f16: bad shape");
     const int G = hq / hkv;
@@ -664,7 +664,7 @@ nx_status nx_attn_decode_paged_f16_noalloc(nx_ctx* ctx, nx_buf q, nx_buf kpool, 
                                            nx_buf lens, nx_buf out, int batch, int hq, int hkv, int hd,
                                            int max_blocks, int num_blocks) {
     if (!ctx) return NX_ERR_INVALID;
-    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || (hd != 64 && hd != 128) || max_blocks <= 0 ||
+    if (batch < 1 || hkv <= 0 || hq <= 0 || hq % hkv || (hd != 64 && hd != 128 && hd != 256) || max_blocks <= 0 ||
         num_blocks <= 0)
         return fail(ctx, NX_ERR_INVALID, "nx_attn_decode_paged_f16_noalloc: bad shape");
     const int G = hq / hkv;
@@ -1059,7 +1059,7 @@ nx_status nx_ffn_int4_g32(nx_ctx* ctx, nx_buf x, nx_buf w13, nx_buf s13, nx_buf 
     if (d <= 0 || F <= 0 || batch < 1 || batch > 8)
         return fail(ctx, NX_ERR_INVALID, "nx_ffn_int4_g32: bad shape d=%d F=%d batch=%d", d, F, batch);
     const int Gd = (d + 31) / 32, Gf = (F + 31) / 32;
-    if (Gd > 7 * 64 || Gf > 7 * 64) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_ffn_int4_g32: d or F above 14336");
+    if (Gd > 7 * 64 || Gf > 14 * 64) return fail(ctx, NX_ERR_UNSUPPORTED, "nx_ffn_int4_g32: d above 14336 or F above 28672");
     NX_NEED(ctx, x, (size_t)batch * d * 2, "x");
     NX_NEED(ctx, w13, (size_t)2 * F * Gd * 16, "w13");
     NX_NEED(ctx, s13, (size_t)2 * F * Gd * 2, "s13");

@@ -143,7 +143,15 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
     f4_t o[HD / 16];
 #pragma unroll
     for (int nt = 0; nt < HD / 16; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
-    if constexpr (PIPE) {
+    if constexpr (PIPE && HD > 128) {
+        // 256-long heads: one pair in flight (a second pair's K and V would
+        // not fit the registers of two wavefronts per SIMD)
+        PairRaw<HD> ra;
+        for (int i = 0; i < npw; i += 2) {
+            load_pair<HD>(ra, a, blk_of(i), valid_of(i), blk_of(i + 1), valid_of(i + 1), kvh, lane);
+            pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
+        }
+    } else if constexpr (PIPE) {
         // every pair is requested unconditionally (a pair past the
         // wavefront's pages re-reads its first page and is not processed), so
         // the wait for the current pair leaves the next one in flight
@@ -1250,6 +1258,10 @@ hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st) {
     NX_ATTN_CASE(2, 128)
     NX_ATTN_CASE(4, 128)
     NX_ATTN_CASE(8, 128)
+    NX_ATTN_CASE(1, 256)
+    NX_ATTN_CASE(2, 256)
+    NX_ATTN_CASE(4, 256)
+    NX_ATTN_CASE(8, 256)
 #undef NX_ATTN_CASE
     return hipErrorInvalidValue;
 }

@@ -826,7 +826,7 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
         // of x once for its tiles (a block holding all of K would read all of
         // x for 16 rows); the part sums meet in a second launch (routed
         // experts: in the combine)
-        const int kp = a.want_kparts > 0 && a.batch >= 2 && a.K % 32 == 0 ? a.want_kparts : gemv_kparts(a.K, a.batch);
+        const int kp = gemv_parts_for(a.K, a.batch, a.want_kparts);
         if (kp > 0 && a.kpart && xvec && salign) {
             GemvArgs p = a;
             p.kparts = kp;
@@ -884,7 +884,7 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
 // the RoPE and SwiGLU epilogues need) in a ring of 2, lm_head in a ring of
 // 3, single rows in a ring of 3 otherwise.  K = 14336 without paired rows:
 // one row per tile with x in registers.  Paired epilogues at GPL >= 4 keep x
-// in LDS.  (Measured at batch 1 against these: QKV in one 4-row tile per
+// in LDS (at GPL 7 one pair in flight per wavefront: two spilled).  (Measured at batch 1 against these: QKV in one 4-row tile per
 // wavefront (192 blocks) or a ring of 3, wo in pairs or a ring of 4, gate/up
 // in a ring of 3 or with 16 wavefronts per CU, down in a ring of 2 with x in
 // LDS: all slower.)
@@ -899,8 +899,15 @@ hipError_t launch_b1_gpl(const GemvArgs& a, hipStream_t st) {
         return launch_b1<2, 1, 3, false, XS, EPI>(a, st);
     }
     if (gpl <= 4) return launch_b1<4, 2, 2, true, XS, EPI>(a, st);
-    if (gpl > 7) return hipErrorInvalidValue;
-    if constexpr (kPairs) return launch_b1<7, 2, 2, true, XS, EPI>(a, st);
+    if (gpl > 7) {
+        // K up to 28672 (a 70B-class down projection): single rows in a ring
+        // of 2 with x in LDS (57 KB); fp16 inputs with a plain, fp32 or
+        // residual epilogue only
+        if constexpr (XS == X_F16 && (EPI == E_F16 || EPI == E_F32 || EPI == E_ACC))
+            if (gpl <= 14) return launch_b1<14, 1, 2, true, XS, EPI>(a, st);
+        return hipErrorInvalidValue;
+    }
+    if constexpr (kPairs) return launch_b1<7, 2, 1, true, XS, EPI>(a, st);
     return launch_b1<7, 1, 1, false, XS, EPI>(a, st);
 }
 
@@ -913,7 +920,7 @@ hipError_t launch_gpl(const GemvArgs& a, hipStream_t st) {
         const hipError_t e = launch_b1_gpl<XS, EPI>(a, st);
         return e != hipSuccess ? e : post_norm_launch(a, st);
     }
-    if (gpl > 7) return hipErrorInvalidValue;
+    if (gpl > 14) return hipErrorInvalidValue;
     return launch_mfma<XS, EPI>(a, st);
 }
 

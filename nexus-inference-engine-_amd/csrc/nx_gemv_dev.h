@@ -545,10 +545,14 @@ __device__ inline void wave_rows(const RowSplit& rs, int w, int N, int& r0, int&
 }
 
 // Tile product with x read from the LDS pair layout (used where holding x in
-// registers would cost GPL * 17 VGPRs and limit occupancy).
+// registers would cost GPL * 17 VGPRs and limit occupancy).  The layout's
+// groups from G to kWave * GPL hold zeros (zero_pairs_lds), so every lane
+// reads its groups without a branch (a branch around the reads made the
+// compiler keep every group's pairs live at once and spill).
 template <int GPL, int R>
 __device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, const float* s8,
                                     int G, int lane, float (&res)[R]) {
+    (void)G;
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -556,8 +560,7 @@ __device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, c
     for (int i = 0; i < GPL; ++i) {
         const int g = lane + kWave * i;
         uint32_t P[16];
-        float sx = 0.0f;
-        if (g < G) {
+        {
             const uint4* src = reinterpret_cast<const uint4*>(sp + g * 16);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -567,11 +570,8 @@ __device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, c
                 P[4 * q + 2] = v.z;
                 P[4 * q + 3] = v.w;
             }
-            sx = s8[g];
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) P[j] = 0u;
         }
+        const float sx = s8[g];
 #pragma unroll
         for (int r = 0; r < R; ++r)
             acc[r] = fmaf(group_dot(t.w[r][i], P, sx), h2f_bits(t.s[r][i]), acc[r]);
@@ -581,6 +581,15 @@ __device__ inline void tile_dot_lds(const Tile<GPL, R>& t, const uint32_t* sp, c
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) res[r] = wave_sum(acc[r]);
+}
+
+// Zeros in the pair layout's groups [G, GPL * kWave) and their sums (the
+// groups no staged chunk writes), for tile_dot_lds; the caller's barrier
+// orders them before the reads.
+template <int GPL, int NT>
+__device__ inline void zero_pairs_lds(uint32_t* sp, float* s8, int G) {
+    for (int i = G * 16 + (int)threadIdx.x; i < GPL * kWave * 16; i += NT) sp[i] = 0u;
+    for (int g = G + (int)threadIdx.x; g < GPL * kWave; g += NT) s8[g] = 0.0f;
 }
 
 // Batch 1, persistent: every wavefront streams its own contiguous row range
@@ -629,6 +638,7 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
         }
         if (a.kpool) qblk = a.block_table[qp / kPage];
     }
+    if constexpr (XLDS) zero_pairs_lds<GPL, NT>(sp, s8, a.G);
     stage_finish<CPT, XS, NT>(a, sr, sp, s8, red);  // block barrier: every wavefront takes part
     // XFIRST: the first tiles are requested only once x is staged (x then
     // arrives without weight traffic queued beside it)

@@ -87,6 +87,12 @@ struct GemvArgs {
 // Parts of a K-split batch-2..8 GEMV (0: none); the workspace is
 // gemv_kparts(K) * batch * N floats.
 inline int gemv_kparts(int K, int batch) { return batch >= 2 && K > 4096 && K % 32 == 0 ? (K + 4095) / 4096 : 0; }
+// The parts a batch 2..8 GEMV with want_kparts = want splits K into (a part
+// stages at most 4096 k in LDS); its workspace is that many * batch * N floats.
+inline int gemv_parts_for(int K, int batch, int want) {
+    const int base = gemv_kparts(K, batch);
+    return want > 0 && batch >= 2 && K % 32 == 0 ? (want > base ? want : base) : base;
+}
 
 // Routing plan of one active expert (int32 words): [0] expert id (-1: no
 // expert for this grid row), [1] its number of token slots n (<= 8),

@@ -72,7 +72,8 @@ struct nx_model {
     float* q = nullptr;
     uint16_t* att16 = nullptr;
     uint16_t* act16 = nullptr;
-    float* kpart = nullptr;  // K-part sums of the batched down projection
+    float* kpart = nullptr;  // K-part sums of the batched down projection and wo ([kparts_max][batch][d])
+    int kparts_max = 0;
     float* logits = nullptr;
     float* kv_tmp = nullptr;
     uint16_t* xn16 = nullptr;
@@ -508,7 +509,8 @@ nx_status enqueue_step(nx_model* m) {
             if (c.qk_norm) NX_LAUNCH(m, qk_norm_launch(m, ly, st));
             NX_LAUNCH(m, attention_launch(m, ly, st));
             nx::GemvArgs wo = wo_args(m, ly);
-            if (prenorm_on(m) && m->kpart && m->wo_kparts > 0 && m->wo_kparts <= nx::gemv_kparts(c.ffn, B)) {
+            if (prenorm_on(m) && m->kpart && m->wo_kparts > 0 &&
+                nx::gemv_parts_for(m->qdim, B, m->wo_kparts) <= m->kparts_max) {
                 // K split, the part-sum launch normalizes the new h for gate/up
                 wo.kpart = m->kpart;
                 wo.want_kparts = m->wo_kparts;
@@ -837,7 +839,9 @@ nx_status create_impl(nx_model* m, bool synthetic) {
     NX_TRY(dalloc(m, &m->q, (size_t)B * m->qdim));
     NX_TRY(dalloc(m, &m->att16, (size_t)B * m->qdim));
     NX_TRY(dalloc(m, &m->act16, (size_t)B * m->Fp));
-    if (nx::gemv_kparts(c.ffn, B) > 0) NX_TRY(dalloc(m, &m->kpart, (size_t)nx::gemv_kparts(c.ffn, B) * B * d));
+    // K-part sums of the batch 2-8 down projection and of wo (both N = d)
+    m->kparts_max = std::max(nx::gemv_kparts(c.ffn, B), nx::gemv_parts_for(m->qdim, B, m->wo_kparts));
+    if (m->kparts_max > 0) NX_TRY(dalloc(m, &m->kpart, (size_t)m->kparts_max * B * d));
     NX_TRY(dalloc(m, &m->logits, (size_t)B * c.vocab));
     NX_TRY(dalloc(m, &m->kv_tmp, (size_t)B * 2 * m->kvdim));
     NX_TRY(dalloc(m, &m->xn16, (size_t)B * d));
@@ -892,7 +896,8 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
         return fail(ctx, NX_ERR_INVALID, "nx_model_create: invalid configuration");
     const int G = c.n_heads / c.n_kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return fail(ctx, NX_ERR_UNSUPPORTED, "hq/hkv must be 1, 2, 4 or 8");
-    if (c.head_dim != 64 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+        return fail(ctx, NX_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
     if (c.kv_kind != 0 && c.head_dim != 128) return fail(ctx, NX_ERR_UNSUPPORTED, "TurboQuant pages need head_dim 128");
     if (c.kv_kind == 2 && (c.hot_window < nx::kPage || c.hot_window % nx::kPage || c.hot_window >= c.max_seq))
         return fail(ctx, NX_ERR_INVALID, "hot_window must be a positive multiple of 16 below max_seq");
@@ -908,8 +913,11 @@ nx_status check_config(nx_ctx* ctx, const nx_model_config& c) {
         return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the tiered attention limit");
     if (c.d_model % 32 || (c.n_heads * c.head_dim) % 32) return fail(ctx, NX_ERR_UNSUPPORTED, "d_model and hq*hd must be multiples of 32");
     if (c.max_seq > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_seq above the attention limit");
-    if (c.d_model > 14336 || c.ffn > 14336 || c.n_heads * c.head_dim > 14336)
-        return fail(ctx, NX_ERR_UNSUPPORTED, "GEMV K above 14336");
+    // GEMV K: RMSNorm inputs (QKV, gate/up, lm_head: d_model) up to 14336,
+    // fp16 inputs (wo: hq * hd, the dense down projection: ffn) up to 28672;
+    // routed experts' down projection up to 14336
+    if (c.d_model > 14336 || c.n_heads * c.head_dim > 28672 || c.ffn > (c.n_experts > 0 ? 14336 : 28672))
+        return fail(ctx, NX_ERR_UNSUPPORTED, "GEMV K above its limit (d_model 14336, hq*hd 28672, ffn 28672)");
     if (c.n_experts < 0 || c.n_experts > nx::kMoeMaxExperts ||
         (c.n_experts > 0 && (c.top_k < 1 || c.top_k > nx::kMoeMaxTopK || c.top_k > c.n_experts)))
         return fail(ctx, NX_ERR_INVALID, "invalid expert configuration (experts <= 256, 1 <= top_k <= min(16, experts))");
@@ -979,7 +987,10 @@ struct PrefillScratch {
 // pages (the latter with at most 4 query heads per kv head).
 bool batched_prefill_ok(const nx_model* m) {
     const nx_model_config& c = m->c;
-    return m->prefill_batched && (c.kv_kind == 0 || (c.kv_kind == 1 && c.n_heads <= 4 * c.n_kv_heads));
+    // (256-long heads prefill one step per token: the causal prefill
+    // attention holds heads of at most 128)
+    return m->prefill_batched && c.head_dim <= 128 &&
+           (c.kv_kind == 0 || (c.kv_kind == 1 && c.n_heads <= 4 * c.n_kv_heads));
 }
 
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {

@@ -94,6 +94,20 @@ def test_gemv_parity_8b_shapes(ctx, N, K, B):
     assert rel_err(y32, want) < 1e-5
 
 
+# 70B-class projections (d 8192, FFN 28672): the down projection's K = 28672
+# runs the batch-1 kernel with x in LDS and the batch-8 matrix-core kernel's
+# K split; gate/up (N = 28672, K = 8192) the ordinary forms.  Plus K = 28672
+# with a ragged row count at batch 3 and a K that is not a multiple of 256.
+@pytest.mark.parametrize("N,K,B", [(8192, 28672, 1), (8192, 28672, 8), (28672, 8192, 1), (28672, 8192, 8),
+                                   (300, 28672, 3), (200, 20000, 1)])
+def test_gemv_parity_70b_shapes(ctx, N, K, B):
+    codes, scales = oracle.gen_quant_rows(0, N, K, 0x70B, N % 97 + K % 89, 0.02)
+    y16, y32, y2, want = _gemv_case(ctx, N, K, B, codes, scales, N + K + B)
+    assert rel_err(y16, want) < TOL
+    assert rel_err(y32, want) < 1e-5
+    assert rel_err(y2, 2 * want) < 1e-5
+
+
 def test_gemv_rejects_bad_shapes(ctx):
     xb, wb, sb, yb = ctx.alloc(64), ctx.alloc(64), ctx.alloc(64), ctx.alloc(64)
     with pytest.raises(nexus_amd.NxError):
@@ -102,6 +116,12 @@ def test_gemv_rejects_bad_shapes(ctx):
         ctx.gemv(xb, wb, sb, yb, 1, 32, 9)  # batch above 8
     with pytest.raises(nexus_amd.NxError):
         ctx.gemv(xb, wb, sb, 12345, 1, 32, 1)  # unknown buffer
+    big = [ctx.alloc(1 << 20) for _ in range(4)]
+    with pytest.raises(nexus_amd.NxError) as e:
+        ctx.gemv(big[0], big[1], big[2], big[3], 1, 28704, 1)  # K above 28672
+    assert e.value.code == 4
+    for b in big:
+        ctx.free(b)
 
 
 # ------------------------------------------------------------ elementwise --
@@ -184,7 +204,11 @@ def _pools(rng, B, hkv, hd, lens, seed=7):
 
 @pytest.mark.parametrize("hq,hkv,hd,lens", [
     (4, 2, 64, [1]), (4, 2, 64, [17]), (4, 2, 64, [16, 100]), (32, 8, 128, [4096]),
-    (32, 8, 128, [1, 15, 300]), (8, 8, 128, [33]), (32, 4, 128, [64, 129]), (32, 8, 128, [4096] * 8)])
+    (32, 8, 128, [1, 15, 300]), (8, 8, 128, [33]), (32, 4, 128, [64, 129]), (32, 8, 128, [4096] * 8),
+    # 256-long heads: one page pair (short contexts) and the one-pair loop
+    # (20000 positions, 20 pages per split), query groups of 1 to 8
+    (8, 2, 256, [1]), (16, 4, 256, [300, 17]), (16, 2, 256, [33]), (4, 4, 256, [70]),
+    (8, 1, 256, [20000]), (32, 8, 256, [4096] * 2)])
 def test_attention_f16_parity(ctx, hq, hkv, hd, lens):
     rng = np.random.default_rng(hq + hd + sum(lens))
     B = len(lens)

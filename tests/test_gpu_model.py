@@ -124,6 +124,31 @@ def test_wide_moe_parity(ctx, E, k, batch):
     run_forced(ctx, cfg, 7, 16)
 
 
+@pytest.mark.parametrize("batch,qk", [(1, 0), (3, 1)])
+def test_head_dim_256_parity(ctx, batch, qk):
+    """256-long heads (the Gemma-style width the reference's Q/K-norm code
+    defaults to, hybrid_model.cpp:1328): RoPE, the page layout, the split
+    attention and its merge over 256 dimensions, with and without the Q/K
+    norm, against the oracle (tokens and teacher-forced logits)."""
+    cfg = dict(TINY, n_heads=4, n_kv_heads=2, head_dim=256, d_model=512, batch=batch, qk_norm=qk, norm_sigma=0.1,
+               seed=0x2560 + batch)
+    got, want, margins = run_both(ctx, cfg, P=9, n_new=20)
+    assert_greedy_parity(got, want, margins)
+    run_forced(ctx, cfg, 9, 20)
+
+
+def test_wide_ffn_and_heads_parity(ctx):
+    """An FFN of 16384 and 64 query heads of 256 (hq * hd = 16384): the down
+    projection and wo take K beyond 14336 (the batch-1 kernel with x in LDS,
+    the matrix cores at batch 2), against the oracle."""
+    for batch in (1, 2):
+        cfg = dict(TINY, d_model=512, n_heads=64, n_kv_heads=8, head_dim=256, ffn=16384, batch=batch,
+                   seed=0x7A0B + batch)
+        got, want, margins = run_both(ctx, cfg, P=5, n_new=8)
+        assert_greedy_parity(got, want, margins)
+        run_forced(ctx, cfg, 5, 8)
+
+
 QK = dict(qk_norm=1, norm_sigma=0.1)
 
 

@@ -252,7 +252,7 @@ def _paged_setup(rng, B, hkv, hd, max_blocks, ctx_lens):
     return bt, kpool, vpool, raw
 
 
-@pytest.mark.parametrize("hq,hkv,hd", [(4, 2, 64), (8, 2, 128)])
+@pytest.mark.parametrize("hq,hkv,hd", [(4, 2, 64), (8, 2, 128), (8, 2, 256)])
 def test_paged_attention_vs_fp64(hq, hkv, hd):
     rng = np.random.default_rng(hq * hd)
     B, max_blocks = 3, 4
