@@ -65,30 +65,49 @@ MIXTRAL = dict(LLAMA8B, vocab=32000, n_experts=8, top_k=2, rope_theta=1000000.0)
 MODELS = {"llama-8b": LLAMA8B, "mixtral-8x7b": MIXTRAL}
 
 
-def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window: int = 0, reps: int = 3) -> dict:
-    """Time the oracle's decode step on a bounded sample and scale to a token."""
+def cpu_baseline(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window: int = 0, reps: int = 3,
+                 plans=None) -> dict:
+    """Time the oracle's decode step on a bounded sample and scale to a step:
+    decode steps of one layer of the shape plus 1/8 of the lm_head rows,
+    scaled to every layer and the whole lm_head.  plans: list of (threads,
+    steps, seconds) -- at `threads` OpenMP threads (0: all), `steps` decode
+    steps, fewer once `seconds` of sampled work have passed (0: no limit);
+    the model is built once and the result is one baseline per plan (a
+    single one at the current thread count and `reps` steps by default)."""
     import numpy as np
 
     import oracle
+    single = plans is None
+    plans = plans or [(0, reps, 0.0)]
     vocab_frac = 8
     cfg = dict(base, n_layers=1, vocab=base["vocab"] // vocab_frac, batch=batch, kv_kind=kv_kind,
-               max_seq=((ctx_len + 16) // 16 + 1) * 16, hot_window=hot_window)
+               max_seq=((ctx_len + sum(p[1] + 1 for p in plans) + 16) // 16 + 1) * 16, hot_window=hot_window)
     m = oracle.Model(**cfg)
     m.fill_context(ctx_len, 4 if kv_kind else 0)
     tok = np.zeros(batch, np.int32)
-    m.forward_timed(tok)  # warm caches
-    tl, th = 0.0, 0.0
-    for _ in range(reps):
-        _, a, b = m.forward_timed(tok)
-        tl += a
-        th += b
-    m.close()
-    t_token = base["n_layers"] * tl / reps + vocab_frac * th / reps
     shape = "8B-shaped" if base["n_experts"] == 0 else "Mixtral-shaped (top-2 of 8 experts)"
-    return {"value": round(batch / t_token, 4), "unit": "tok/s",
-            "cores": int(oracle.lib.nxo_num_threads()), "kind": "port",
-            "sample": (f"oracle decode step of one {shape} layer at ctx {ctx_len} ({reps} reps) "
-                       f"+ lm_head rows 1/{vocab_frac}, scaled to {base['n_layers']} layers + full lm_head")}
+    kv = ["fp16", "TurboQuant", "tiered"][kv_kind]
+
+    def run(steps, budget):
+        m.forward_timed(tok)  # warm caches
+        tl, th, n = 0.0, 0.0, 0
+        while n < steps:
+            _, a, b = m.forward_timed(tok)
+            tl += a
+            th += b
+            n += 1
+            if budget and tl + th > budget:
+                break
+        t_step = base["n_layers"] * tl / n + vocab_frac * th / n
+        return {"value": round(batch / t_step, 4), "unit": "tok/s",
+                "cores": int(oracle.lib.nxo_num_threads()), "kind": "port",
+                "sample": (f"{n} oracle decode steps of one {shape} layer at batch {batch}, ctx {ctx_len} {kv} "
+                           f"pages + lm_head rows 1/{vocab_frac}, scaled to {base['n_layers']} layers + full lm_head")}
+    try:
+        out = [with_threads(t, lambda: run(st, bud)) for t, st, bud in plans]
+    finally:
+        m.close()
+    return out[0] if single else out
 
 
 TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=688, vocab=4096,
@@ -170,12 +189,14 @@ def cpu_baselines(base: dict, ctx_len: int, batch: int, kv_kind: int, hot_window
 
 
 def decode_line(ctx, base: dict, name: str, batch: int, kv_kind: int, ctx_len: int, steps: int,
-                prompt: bool = False) -> dict:
+                prompt: bool = False, cpu: bool = False) -> dict:
     """Greedy decode rate of one more workload: its model built on the
     device, its context filled with seeded K/V (or, with `prompt`, a seeded
     prompt of ctx_len tokens prefilled), 2 untimed steps, then `steps` timed
     (device synchronized on both sides); bytes per step are the algorithmic
-    weight and KV bytes."""
+    weight and KV bytes.  cpu: the oracle's rate on the same workload (8
+    sampled decode steps at all host cores, up to 8 within 10 s at one core;
+    cpu_baseline) and its effective GB/s by the same byte count."""
     import nexus_amd
     max_seq = ((ctx_len + steps + 32) // 16 + 1) * 16
     m = nexus_amd.Model(ctx, **dict(base, batch=batch, kv_kind=kv_kind, max_seq=max_seq))
@@ -193,19 +214,29 @@ def decode_line(ctx, base: dict, name: str, batch: int, kv_kind: int, ctx_len: i
     b1 = m.step_bytes()
     m.close()
     sb = 0.5 * (b0 + b1)
-    return {"workload": name, "batch": batch, "ctx": ctx_len, "steps": steps,
+    line = {"workload": name, "batch": batch, "ctx": ctx_len, "steps": steps,
             "tok_s": round(steps * batch / dt, 2), "ms_per_step": round(dt * 1e3 / steps, 4),
             "GB_per_step": round(sb / 1e9, 4), "hbm_GBps_end_to_end": round(sb / (dt / steps) / 1e9, 1),
             "roofline_end_to_end_frac": round(sb / (dt / steps) / 1e9 / PEAK_HBM_GBS, 4)}
+    if cpu:
+        cbs = cpu_baseline(base, ctx_len, batch, kv_kind, plans=[(0, 8, 0.0), (1, 8, 10.0)])
+        for key, cb in zip(("cpu_baseline", "cpu_baseline_1core"), cbs):
+            cb["effective_GBps"] = round(sb * cb["value"] / batch / 1e9, 3)
+            line[key] = cb
+    return line
 
 
-def measured_traffic(kind: str):
-    """HBM bytes per launch of `kind` ("ffn" / "attention") from the committed
-    rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE, calibrated on a copy
-    kernel); None when no summary is present."""
+def measured_traffic(kind: str, nbytes: float):
+    """HBM bytes per launch of `kind` ("ffn" / "attention" / "attention_tq")
+    from the committed rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE,
+    calibrated on a copy kernel); None when no summary is present or it was
+    taken on a launch of other algorithmic bytes than `nbytes`."""
     try:
         with open(ROOT / "profiles" / "traffic.json") as f:
-            return int(json.load(f)["kernels"][kind]["traffic_bytes"])
+            k = json.load(f)["kernels"][kind]
+        if abs(k["algorithmic_bytes"] - nbytes) > 1e-3 * nbytes:
+            return None
+        return int(k["traffic_bytes"])
     except (OSError, KeyError, ValueError):
         return None
 
@@ -434,14 +465,18 @@ def main() -> int:
           f"(batch {args.batch}, ctx {args.ctx}, kv {args.kv})", file=sys.stderr, flush=True)
     model = nexus_amd.Model(ctx, **cfg)
     model.fill_context(args.ctx, 4 if kv_kind else 0)
+    model.decode_untimed(1)
     if args.profile_kernel:
-        model.decode_untimed(1)
         ms, nb = (model.time_ffn_gemv if args.profile_kernel == "ffn" else model.time_attention)(64)
         print(json.dumps({"kernel": args.profile_kernel, "avg_us": round(ms * 1e3, 3),
                           "bytes": int(nb), "launches": 64 + base["n_layers"]}))
         model.close()
         ctx.close()
         return 0
+    # the dominant kernel and the attention timed over the filled context
+    # (the launches the committed PMC summary of --profile-kernel counts)
+    ffn_ms, ffn_bytes = model.time_ffn_gemv(200)
+    att_ms, att_bytes = model.time_attention(200)
     if args.warmup > 0:
         model.decode_untimed(args.warmup)
     bytes_start = model.step_bytes()
@@ -480,8 +515,6 @@ def main() -> int:
         for _ in range(10):
             oracle.lib.nxo_sample(lg, base["vocab"], 0.7, 40, 0.9, 0.5)
         sampling["cpu_ms_per_sample"] = round((time.perf_counter() - t0) * 100, 3)
-    ffn_ms, ffn_bytes = model.time_ffn_gemv(200)
-    att_ms, att_bytes = model.time_attention(200)
     ffn_gbs = ffn_bytes / (ffn_ms * 1e-3) / 1e9
     att_gbs = att_bytes / (att_ms * 1e-3) / 1e9
     model.close()
@@ -491,12 +524,13 @@ def main() -> int:
     others = None
     if full and args.model == "llama-8b" and args.batch == 1 and kv_kind == 0 and args.ctx == 4096:
         print("[bench] other decode workloads", file=sys.stderr, flush=True)
+        cpu = not args.no_cpu
         others = [
             decode_line(ctx, TINY, "tiny llama (2 layers, d 256), 16-token prompt", 1, 0, 16, 64, prompt=True),
-            decode_line(ctx, LLAMA8B, "llama-3.1-8b-shape, fp16 paged KV", 8, 0, 4096, 128),
-            decode_line(ctx, LLAMA8B, "llama-3.1-8b-shape, TurboQuant 3.5-bit paged KV", 1, 1, 32768, 64),
-            decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 1, 0, 4096, 128),
-            decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 8, 0, 4096, 128),
+            decode_line(ctx, LLAMA8B, "llama-3.1-8b-shape, fp16 paged KV", 8, 0, 4096, 128, cpu=cpu),
+            decode_line(ctx, LLAMA8B, "llama-3.1-8b-shape, TurboQuant 3.5-bit paged KV", 1, 1, 32768, 64, cpu=cpu),
+            decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 1, 0, 4096, 128, cpu=cpu),
+            decode_line(ctx, MIXTRAL, "mixtral-8x7b-shape (top-2 of 8), fp16 paged KV", 8, 0, 4096, 128, cpu=cpu),
         ]
     nxf = nxf_verify_bench(ctx, not args.no_cpu) if full else None
     pre = prefill_bench(ctx, base) if full else None
@@ -536,13 +570,15 @@ def main() -> int:
         "roofline": {
             "kernel": ffn_kernel,
             "bound": "hbm", "achieved": round(ffn_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": None if moe else measured_traffic("ffn"),
+            "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic("ffn", ffn_bytes) if args.batch == 1 else None,
             "avg_us": round(ffn_ms * 1e3, 3), "bytes": int(ffn_bytes),
         },
         "attention": {
             "kernel": "paged decode attention, one layer", "achieved": round(att_gbs, 1),
             "frac": round(att_gbs / PEAK_HBM_GBS, 4), "avg_us": round(att_ms * 1e3, 3),
-            "bytes": int(att_bytes), "traffic": measured_traffic("attention") if kv_kind == 0 else None,
+            "bytes": int(att_bytes), "traffic": ({0: measured_traffic("attention", att_bytes),
+                         1: measured_traffic("attention_tq", att_bytes)}.get(kv_kind)
+                        if args.batch == 1 and args.model == "llama-8b" else None),
         },
         "roofline_end_to_end_frac": round(step_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
     }
