@@ -377,6 +377,15 @@ hipError_t pf_moe_combine_launch(const float* yg, const int32_t* slot_row, const
 // Whether the routed down projection writes K-part sums (a.kpart) for the
 // combine to add; decided once here for both launches.
 bool moe_down_split(const MoeFfnArgs& a);
+// Batch 1 (nx_moe.hip): the routing folded into the gate/up launch (every
+// block normalizes h = m.h with m.norm_w, computes the router logits and the
+// routing; block (0, 0) writes ids, weights, counts, slot lists and the
+// plan), and the down projection with the weighted combine into f.out (h +=
+// sum_j w_j y_j, top-k 1 or 2; f.weights and ids from the gate/up launch).
+bool moe_b1_fused_fits(int d, int F, int E, int k);
+bool moe_b1_down_combine_fits(int F, int k);
+hipError_t moe_b1_gate_up_launch(const MoeArgs& m, const MoeFfnArgs& f, hipStream_t st);
+hipError_t moe_b1_down_combine_launch(const MoeFfnArgs& f, const int32_t* ids, hipStream_t st);
 hipError_t moe_gate_up_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_down_launch(const MoeFfnArgs& a, hipStream_t st);
 hipError_t moe_combine_launch(const MoeFfnArgs& a, hipStream_t st);

@@ -570,7 +570,16 @@ nx_status enqueue_step(nx_model* m) {
             ma.expert_count = ly.moe_count;
             ma.expert_slots = m->moe_slots;
             ma.plan = m->moe_plan;
-            if (nx::moe_norm_route_fits(d, E, c.top_k, B)) {
+            const bool fused_b1 = B == 1 && nx::moe_b1_fused_fits(d, F, E, c.top_k);
+            if (fused_b1) {
+                // batch 1: the routing runs in the gate/up launch below
+                ma.h = m->h;
+                ma.eps = c.eps;
+                ma.norm_w = ly.norm_ffn;
+                ma.d = d;
+                ma.wr = ly.wr;
+                ma.sr = ly.sr;
+            } else if (nx::moe_norm_route_fits(d, E, c.top_k, B)) {
                 // RMSNorm, router and routing in one launch
                 ma.h = m->h;
                 ma.eps = c.eps;
@@ -616,9 +625,19 @@ nx_status enqueue_step(nx_model* m) {
             mf.kpart = m->moe_kpart;
             mf.out = m->h;
             mf.accumulate = 1;
-            NX_LAUNCH(m, nx::moe_gate_up_launch(mf, st));
-            NX_LAUNCH(m, nx::moe_down_launch(mf, st));
-            NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+            if (fused_b1) {
+                NX_LAUNCH(m, nx::moe_b1_gate_up_launch(ma, mf, st));
+                if (nx::moe_b1_down_combine_fits(F, c.top_k)) {
+                    NX_LAUNCH(m, nx::moe_b1_down_combine_launch(mf, m->moe_ids, st));
+                } else {
+                    NX_LAUNCH(m, nx::moe_down_launch(mf, st));
+                    NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+                }
+            } else {
+                NX_LAUNCH(m, nx::moe_gate_up_launch(mf, st));
+                NX_LAUNCH(m, nx::moe_down_launch(mf, st));
+                NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+            }
             xn_ready = false;
         }
     }
@@ -1676,6 +1695,7 @@ nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double*
             slots += cnt[e];
         }
         if (active == 0) return fail(m->ctx, NX_ERR_STATE, "no routed step to time (decode once first)");
+        const bool fused_b1 = c.batch == 1 && nx::moe_b1_fused_fits(c.d_model, c.ffn, E, c.top_k);
         launch = [&](int i) {
             const Layer& ly = m->layers[i % c.n_layers];
             nx::MoeFfnArgs mf{};
@@ -1696,9 +1716,33 @@ nx_status nx_model_time_ffn_gemv(nx_model* m, int iters, double* avg_ms, double*
             mf.y32 = m->moe_y;
             mf.out = m->h;
             mf.accumulate = 1;
+            if (fused_b1) {
+                // the launch of the decode step: routing of h with layer i's
+                // router, then the chosen experts' gate/up
+                nx::MoeArgs ma{};
+                ma.logits = m->router_logits;
+                ma.E = E;
+                ma.k = c.top_k;
+                ma.batch = 1;
+                ma.ids = m->moe_ids;
+                ma.weights = m->moe_w;
+                ma.expert_count = ly.moe_count;
+                ma.expert_slots = m->moe_slots;
+                ma.plan = m->moe_plan;
+                ma.h = m->h;
+                ma.norm_w = ly.norm_ffn;
+                ma.eps = c.eps;
+                ma.d = c.d_model;
+                ma.wr = ly.wr;
+                ma.sr = ly.sr;
+                return nx::moe_b1_gate_up_launch(ma, mf, st);
+            }
             return nx::moe_gate_up_launch(mf, st);
         };
         nbytes = active * (double)qbytes(2 * (size_t)c.ffn, c.d_model) + (double)slots * (2.0 * c.d_model + 2.0 * c.ffn);
+        if (fused_b1)  // every block reads h (fp32) and the router once from HBM
+            nbytes = c.top_k * (double)qbytes(2 * (size_t)c.ffn, c.d_model) + (double)qbytes((size_t)E, c.d_model) +
+                     4.0 * c.d_model + 2.0 * c.top_k * c.ffn;
     }
     for (int i = 0; i < c.n_layers; ++i) NX_LAUNCH(m, launch(i));
     NX_HIP(m->ctx, hipEventRecord(m->ctx->ev0, st));
