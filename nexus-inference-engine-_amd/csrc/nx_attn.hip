@@ -112,33 +112,37 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
     // q as the B operand (column = head t, k = 8g + j of each 32-dim step).
     // Columns t >= G repeat head G - 1 (loads without a branch, so all of q
     // is requested at once); their scores and output rows are never used.
-    h8_t qh[HD / 32], ql[HD / 32];
-    {
-        const float* qsrc = a.q + ((size_t)b * a.hq + kvh * G + min(t, G - 1)) * HD + 8 * g;
-        float4 x[HD / 32][2];
+    const float* qsrc = a.q + ((size_t)b * a.hq + kvh * G + min(t, G - 1)) * HD + 8 * g;
+    float4 qx[HD / 32][2];
 #pragma unroll
-        for (int s = 0; s < HD / 32; ++s) {
-            x[s][0] = *reinterpret_cast<const float4*>(qsrc + 32 * s);
-            x[s][1] = *reinterpret_cast<const float4*>(qsrc + 32 * s + 4);
-        }
-#pragma unroll
-        for (int s = 0; s < HD / 32; ++s) {
-            const float v[8] = {x[s][0].x, x[s][0].y, x[s][0].z, x[s][0].w,
-                                x[s][1].x, x[s][1].y, x[s][1].z, x[s][1].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                qh[s][j] = (_Float16)v[j];
-                ql[s][j] = (_Float16)(v[j] - (float)qh[s][j]);
-            }
-        }
+    for (int s = 0; s < HD / 32; ++s) {
+        qx[s][0] = *reinterpret_cast<const float4*>(qsrc + 32 * s);
+        qx[s][1] = *reinterpret_cast<const float4*>(qsrc + 32 * s + 4);
     }
-    const float scale = 1.0f / sqrtf((float)HD);
-
     const int npages = (ctx + kPage - 1) / kPage;
     // pages of this wavefront: first + stride * i for i < npw, taken in pairs
     const int npw = first < npages ? (npages - first + stride - 1) / stride : 0;
     auto valid_of = [&](int i) { return i < npw ? min(ctx - (first + stride * i) * kPage, kPage) : 0; };
     auto blk_of = [&](int i) { return __builtin_amdgcn_readlane(bt_lane, min(i, kWave - 1)); };
+    // a pair past the wavefront's pages re-reads its first page and is not processed
+    auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
+    // the first page pair is requested before q is converted (its addresses
+    // need only the block table), so the pages do not wait for q's round trip
+    constexpr bool kEarly = !(PIPE && HD > 128);
+    PairRaw<HD> ra;
+    if constexpr (kEarly) load_pair<HD>(ra, a, blk_or0(0), valid_of(0), blk_or0(1), valid_of(1), kvh, lane);
+    h8_t qh[HD / 32], ql[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+        const float v[8] = {qx[s][0].x, qx[s][0].y, qx[s][0].z, qx[s][0].w,
+                            qx[s][1].x, qx[s][1].y, qx[s][1].z, qx[s][1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            qh[s][j] = (_Float16)v[j];
+            ql[s][j] = (_Float16)(v[j] - (float)qh[s][j]);
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
     float m = -__builtin_inff(), lsum = 0.0f;
     f4_t o[HD / 16];
 #pragma unroll
@@ -146,18 +150,14 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
     if constexpr (PIPE && HD > 128) {
         // 256-long heads: one pair in flight (a second pair's K and V would
         // not fit the registers of two wavefronts per SIMD)
-        PairRaw<HD> ra;
         for (int i = 0; i < npw; i += 2) {
             load_pair<HD>(ra, a, blk_of(i), valid_of(i), blk_of(i + 1), valid_of(i + 1), kvh, lane);
             pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
         }
     } else if constexpr (PIPE) {
-        // every pair is requested unconditionally (a pair past the
-        // wavefront's pages re-reads its first page and is not processed), so
-        // the wait for the current pair leaves the next one in flight
-        auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
-        PairRaw<HD> ra, rb;
-        load_pair<HD>(ra, a, blk_or0(0), valid_of(0), blk_or0(1), valid_of(1), kvh, lane);
+        // every pair is requested unconditionally, so the wait for the
+        // current pair leaves the next one in flight
+        PairRaw<HD> rb;
         for (int i = 0; i < npw; i += 4) {
             load_pair<HD>(rb, a, blk_or0(i + 2), valid_of(i + 2), blk_or0(i + 3), valid_of(i + 3), kvh, lane);
             pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
@@ -166,11 +166,7 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
             pair_update<HD>(rb, qh, ql, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
         }
     } else {
-        PairRaw<HD> ra;
-        if (npw > 0) {
-            load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
-            pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
-        }
+        if (npw > 0) pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
     }
     // the head's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);

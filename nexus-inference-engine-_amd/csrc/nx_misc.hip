@@ -444,36 +444,49 @@ __device__ inline void route_row(const float* lg, int E, int k, int* ids, float*
 
 // Per-expert slot lists in (b, j) order and the routing plan (the active
 // experts in ascending order; a token's k experts are distinct, so an expert
-// holds at most `batch` slots), from the chosen ids [batch][k].  One thread;
-// cnt: E ints of scratch (LDS).
-__device__ inline void build_lists(const MoeArgs& a, const int32_t* ids, int* cnt) {
-    for (int e = 0; e < a.E; ++e) cnt[e] = 0;
-    for (int bb = 0; bb < a.batch; ++bb)
-        for (int j = 0; j < a.k; ++j) {
-            const int e = ids[bb * a.k + j];
-            a.expert_slots[(size_t)e * a.batch * a.k + cnt[e]] = bb * a.k + j;
-            cnt[e] += 1;
-        }
-    for (int e = 0; e < a.E; ++e) a.expert_count[e] = cnt[e];
+// holds at most `batch` slots), from the chosen ids [batch][k] (LDS).  Run by
+// every thread of the block: thread e lists expert e's slots, wavefront 0
+// ranks the active experts (ballots over 64 experts at a time), then the
+// plan rows are written in parallel.  cnt, rank: E ints of LDS scratch.
+__device__ inline void build_lists(const MoeArgs& a, const int32_t* ids, int* cnt, int* rank) {
+    const int t = threadIdx.x, nt = blockDim.x, E = a.E, n = a.batch * a.k;
+    for (int e = t; e < E; e += nt) {
+        int c = 0;
+        for (int sl = 0; sl < n; ++sl)
+            if (ids[sl] == e) a.expert_slots[(size_t)e * n + c++] = sl;
+        cnt[e] = c;
+        a.expert_count[e] = c;
+    }
+    __syncthreads();
     if (!a.plan) return;
-    const int rows = moe_plan_rows(a.E, a.batch, a.k);
-    int r = 0;
-    for (int e = 0; e < a.E && r < rows; ++e) {
-        if (cnt[e] == 0) continue;
-        int32_t* pl = a.plan + (size_t)r * kMoePlanInts;
+    __shared__ int nact;
+    if (t < kWave) {
+        int base = 0;
+        for (int c0 = 0; c0 < E; c0 += kWave) {
+            const int e = c0 + t;
+            const bool act = e < E && cnt[e] > 0;
+            const unsigned long long bal = __ballot(act);
+            if (act) rank[e] = base + __popcll(bal & ((1ull << t) - 1ull));
+            base += __popcll(bal);
+        }
+        if (t == 0) nact = base;
+    }
+    __syncthreads();
+    const int rows = moe_plan_rows(E, a.batch, a.k);
+    for (int e = t; e < E; e += nt) {
+        if (cnt[e] == 0 || rank[e] >= rows) continue;
+        int32_t* pl = a.plan + (size_t)rank[e] * kMoePlanInts;
         pl[0] = e;
         pl[1] = cnt[e];
-        int n = 0;
-        for (int bb = 0; bb < a.batch; ++bb)
-            for (int j = 0; j < a.k; ++j)
-                if (ids[bb * a.k + j] == e) {
-                    pl[8 + n] = bb * a.k + j;
-                    pl[16 + n] = bb;
-                    ++n;
-                }
-        ++r;
+        int c = 0;
+        for (int sl = 0; sl < n; ++sl)
+            if (ids[sl] == e) {
+                pl[8 + c] = sl;
+                pl[16 + c] = sl / a.k;
+                ++c;
+            }
     }
-    for (; r < rows; ++r) a.plan[(size_t)r * kMoePlanInts] = -1;
+    for (int r = nact + t; r < rows; r += nt) a.plan[(size_t)r * kMoePlanInts] = -1;
 }
 
 // Single block: thread b routes sequence b; thread 0 then builds the
@@ -482,7 +495,7 @@ __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
     const int b = threadIdx.x;
     __shared__ int32_t sid[64 * kMoeMaxTopK];
     __shared__ uint32_t tk[64][kMoeMaxExperts / 32];
-    __shared__ int scnt[kMoeMaxExperts];
+    __shared__ int scnt[kMoeMaxExperts], srank[kMoeMaxExperts];
     __shared__ float sw[64 * kMoeMaxTopK];
     if (b < a.batch) {
         route_row(a.logits + (size_t)b * a.E, a.E, a.k, sid + b * a.k, sw + b * a.k, tk[b]);
@@ -492,7 +505,7 @@ __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) build_lists(a, sid, scnt);
+    build_lists(a, sid, scnt, srank);
 }
 
 // The MoE block's input and routing in one launch (batch <= 8, E <= 16,
@@ -519,7 +532,7 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     __shared__ int32_t sid[kMoeMaxBatch * kMoeMaxTopK];
     __shared__ uint32_t tk[kMoeMaxBatch][kMoeMaxExperts / 32];
     __shared__ float sw[kMoeMaxBatch * kMoeMaxTopK];
-    __shared__ int scnt[kNrMaxE];
+    __shared__ int scnt[kNrMaxE], srank[kNrMaxE];
     __shared__ int last;
     // the arguments the prologue uses, requested in one round
     asm volatile("" ::"s"(a.h), "s"(a.wr), "s"(a.sr), "s"(a.d), "s"(a.batch), "s"(a.E), "s"(a.norm_w),
@@ -617,7 +630,7 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
         }
     }
     __syncthreads();
-    if (tid == 0) build_lists(a, sid, scnt);
+    build_lists(a, sid, scnt, srank);
 }
 
 // kparts > 0: slot s's down projection is the sum, in part order, of the K
