@@ -377,6 +377,11 @@ hipError_t pf_moe_combine_launch(const float* yg, const int32_t* slot_row, const
 // Whether the routed down projection writes K-part sums (a.kpart) for the
 // combine to add; decided once here for both launches.
 bool moe_down_split(const MoeFfnArgs& a);
+// The combine (a.out += sum_j w_j y_j, accumulate set), then the RMSNorm of
+// each new row with weights w (nullptr = ones) into x16 [batch][d]: the next
+// RMSNorm-input GEMV's input, with no launch of its own.
+bool moe_combine_norm_fits(const MoeFfnArgs& a);
+hipError_t moe_combine_norm_launch(const MoeFfnArgs& a, const float* w, uint16_t* x16, float eps, hipStream_t st);
 // Batch 1 (nx_moe.hip): the routing folded into the gate/up launch (every
 // block normalizes h = m.h with m.norm_w, computes the router logits and the
 // routing; block (0, 0) writes ids, weights, counts, slot lists and the

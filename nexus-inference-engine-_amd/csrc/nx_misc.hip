@@ -4,6 +4,7 @@
 // routing.  None of these is on the HBM-heavy path; they favour simplicity.
 #include "nx_common.h"
 #include "nx_kernels.h"
+#include "nx_route_dev.h"
 
 namespace nx {
 
@@ -489,22 +490,18 @@ __device__ inline void build_lists(const MoeArgs& a, const int32_t* ids, int* cn
     for (int r = nact + t; r < rows; r += nt) a.plan[(size_t)r * kMoePlanInts] = -1;
 }
 
-// Single block: thread b routes sequence b; thread 0 then builds the
+// Single wavefront: sequences routed in turn (route_wave), then the
 // per-expert token lists and the routing plan.
 __global__ __launch_bounds__(64) void k_moe_route(MoeArgs a) {
-    const int b = threadIdx.x;
     __shared__ int32_t sid[64 * kMoeMaxTopK];
-    __shared__ uint32_t tk[64][kMoeMaxExperts / 32];
     __shared__ int scnt[kMoeMaxExperts], srank[kMoeMaxExperts];
     __shared__ float sw[64 * kMoeMaxTopK];
-    if (b < a.batch) {
-        route_row(a.logits + (size_t)b * a.E, a.E, a.k, sid + b * a.k, sw + b * a.k, tk[b]);
-        for (int j = 0; j < a.k; ++j) {
-            a.ids[(size_t)b * a.k + j] = sid[b * a.k + j];
-            a.weights[(size_t)b * a.k + j] = sw[b * a.k + j];
-        }
-    }
+    for (int b = 0; b < a.batch; ++b) route_wave(a.logits + (size_t)b * a.E, a.E, a.k, sid + b * a.k, sw + b * a.k);
     __syncthreads();
+    for (int s = threadIdx.x; s < a.batch * a.k; s += 64) {
+        a.ids[s] = sid[s];
+        a.weights[s] = sw[s];
+    }
     build_lists(a, sid, scnt, srank);
 }
 
@@ -530,7 +527,6 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     __shared__ float inv_s;
     __shared__ float lg[kMoeMaxBatch * kNrMaxE];
     __shared__ int32_t sid[kMoeMaxBatch * kMoeMaxTopK];
-    __shared__ uint32_t tk[kMoeMaxBatch][kMoeMaxExperts / 32];
     __shared__ float sw[kMoeMaxBatch * kMoeMaxTopK];
     __shared__ int scnt[kNrMaxE], srank[kNrMaxE];
     __shared__ int last;
@@ -622,14 +618,12 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
             lg[idx] = __hip_atomic_load(a.logits + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (tid < B) {
-        route_row(lg + tid * E, E, a.k, sid + tid * a.k, sw + tid * a.k, tk[tid]);
-        for (int j = 0; j < a.k; ++j) {
-            a.ids[(size_t)tid * a.k + j] = sid[tid * a.k + j];
-            a.weights[(size_t)tid * a.k + j] = sw[tid * a.k + j];
-        }
-    }
+    if (wave < B) route_wave(lg + wave * E, E, a.k, sid + wave * a.k, sw + wave * a.k);
     __syncthreads();
+    if (tid < B * a.k) {
+        a.ids[tid] = sid[tid];
+        a.weights[tid] = sw[tid];
+    }
     build_lists(a, sid, scnt, srank);
 }
 
@@ -653,6 +647,72 @@ __global__ void k_moe_combine(const float* y32, const float* kpart, int kparts, 
         acc += weights[s] * y;
     }
     out[t] = accumulate ? out[t] + acc : acc;
+}
+
+// The combine of k_moe_combine (accumulate into h, the same sums in the same
+// order), then the RMSNorm of each finished row with weights w (nullptr =
+// ones) into x16, the input of the next RMSNorm-input GEMV: one block per
+// sequence, 16-byte chunks (d % 4 == 0, d <= 4 * kCnThreads * kCnChunks).
+constexpr int kCnThreads = 1024, kCnChunks = 4;
+__global__ __launch_bounds__(kCnThreads) void k_moe_combine_norm(const float* y32, const float* kpart, int kparts,
+                                                                 const float* weights, float* h, int d, int k,
+                                                                 int batch, const float* w, uint16_t* x16,
+                                                                 float eps) {
+    __shared__ float red[kCnThreads / 64];
+    const int b = blockIdx.x, t = threadIdx.x, nc = d / 4;
+    float4 v[kCnChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int jc = 0; jc < kCnChunks; ++jc) {
+        const int c = t + jc * kCnThreads;
+        v[jc] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c >= nc) continue;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < k; ++j) {
+            const size_t sl = (size_t)b * k + j;
+            float4 y;
+            if (kparts > 0) {
+                y = make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int q = 0; q < kparts; ++q) {
+                    const float4 p = reinterpret_cast<const float4*>(kpart + ((size_t)q * batch * k + sl) * d)[c];
+                    y.x += p.x;
+                    y.y += p.y;
+                    y.z += p.z;
+                    y.w += p.w;
+                }
+            } else {
+                y = reinterpret_cast<const float4*>(y32 + sl * d)[c];
+            }
+            const float ws = weights[sl];
+            acc.x += ws * y.x;
+            acc.y += ws * y.y;
+            acc.z += ws * y.z;
+            acc.w += ws * y.w;
+        }
+        float4* hp = reinterpret_cast<float4*>(h + (size_t)b * d) + c;
+        const float4 o = *hp;
+        const float4 r = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
+        *hp = r;
+        v[jc] = r;
+        ss += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCnThreads / 64; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+    uint2* ob = reinterpret_cast<uint2*>(x16 + (size_t)b * d);
+#pragma unroll
+    for (int jc = 0; jc < kCnChunks; ++jc) {
+        const int c = t + jc * kCnThreads;
+        if (c >= nc) break;
+        const float4 wv = w ? reinterpret_cast<const float4*>(w)[c] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const uint32_t lo = (uint32_t)f2h_bits(v[jc].x * inv * wv.x) | ((uint32_t)f2h_bits(v[jc].y * inv * wv.y) << 16);
+        const uint32_t hi = (uint32_t)f2h_bits(v[jc].z * inv * wv.z) | ((uint32_t)f2h_bits(v[jc].w * inv * wv.w) << 16);
+        ob[c] = make_uint2(lo, hi);
+    }
 }
 
 inline dim3 grid1(size_t n, int threads) { return dim3((unsigned)((n + threads - 1) / threads)); }
@@ -895,6 +955,20 @@ hipError_t pf_gather_launch(const uint16_t* x16, const int32_t* row_tok, int row
 hipError_t pf_moe_combine_launch(const float* yg, const int32_t* slot_row, const float* w, int n, int k, int d,
                                  float* h, hipStream_t st) {
     hipLaunchKernelGGL(k_pf_moe_combine, grid1((size_t)n * d, 256), dim3(256), 0, st, yg, slot_row, w, n, k, d, h);
+    return hipGetLastError();
+}
+
+bool moe_combine_norm_fits(const MoeFfnArgs& a) {
+    return a.accumulate && a.d % 4 == 0 && a.d <= 4 * kCnThreads * kCnChunks &&
+           (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0 && (reinterpret_cast<uintptr_t>(a.y32) & 15u) == 0 &&
+           (!a.kpart || (reinterpret_cast<uintptr_t>(a.kpart) & 15u) == 0);
+}
+
+hipError_t moe_combine_norm_launch(const MoeFfnArgs& a, const float* w, uint16_t* x16, float eps, hipStream_t st) {
+    if (!moe_combine_norm_fits(a) || !x16) return hipErrorInvalidValue;
+    const int kparts = moe_down_split(a) ? gemv_kparts(a.F, a.batch) : 0;
+    hipLaunchKernelGGL(k_moe_combine_norm, dim3(a.batch), dim3(kCnThreads), 0, st, a.y32, a.kpart, kparts, a.weights,
+                       a.out, a.d, a.k, a.batch, w, x16, eps);
     return hipGetLastError();
 }
 

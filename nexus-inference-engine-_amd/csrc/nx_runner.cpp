@@ -633,12 +633,20 @@ nx_status enqueue_step(nx_model* m) {
                     NX_LAUNCH(m, nx::moe_down_launch(mf, st));
                     NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
                 }
+                xn_ready = false;
             } else {
                 NX_LAUNCH(m, nx::moe_gate_up_launch(mf, st));
                 NX_LAUNCH(m, nx::moe_down_launch(mf, st));
-                NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+                if (prenorm_on(m) && nx::moe_combine_norm_fits(mf)) {
+                    // the new h rows normalized for the next layer's QKV (or the lm_head)
+                    const float* nw = L + 1 < c.n_layers ? m->layers[(size_t)L + 1].norm_attn : m->norm_final;
+                    NX_LAUNCH(m, nx::moe_combine_norm_launch(mf, nw, m->xn16, c.eps, st));
+                    xn_ready = true;
+                } else {
+                    NX_LAUNCH(m, nx::moe_combine_launch(mf, st));
+                    xn_ready = false;
+                }
             }
-            xn_ready = false;
         }
     }
     // final RMSNorm + lm_head + greedy argmax
