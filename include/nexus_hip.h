@@ -71,6 +71,10 @@ nx_status nx_device_name(nx_ctx* ctx, char* buf, size_t n);
 const char* nx_last_error(nx_ctx* ctx);
 /* Message of the last nx_init failure (no context exists then). */
 const char* nx_init_error(void);
+/* SHA-1 of the sources the library was built from (csrc/ and include/, as
+ * the Makefile concatenates them).  No counterpart in the reference: lets a
+ * binding refuse a library that is older than the sources beside it. */
+const char* nx_source_hash(void);
 
 /* --------------------------------------------------------------- memory -- */
 /* MetalBackend::alloc_shared_buffer / free_buffer (metal_backend.mm:760-768, :859-864).

@@ -8,6 +8,7 @@ no gfx950 device is present, the constructors raise.
 from __future__ import annotations
 
 import ctypes as C
+import hashlib
 import os
 import subprocess
 from pathlib import Path
@@ -91,6 +92,7 @@ _SIGS = {
     "nx_device_name": (_I, [_P, C.c_char_p, C.c_size_t]),
     "nx_last_error": (C.c_char_p, [_P]),
     "nx_init_error": (C.c_char_p, []),
+    "nx_source_hash": (C.c_char_p, []),
     "nx_alloc": (_I, [_P, C.c_size_t, C.POINTER(_B)]),
     "nx_free": (_I, [_P, _B]),
     "nx_upload": (_I, [_P, _B, C.c_size_t, _P, C.c_size_t]),
@@ -193,8 +195,24 @@ _SIGS = {
 _lib = None
 
 
+_DEFAULT_LIB = LIB_PATH
+
+
+def source_hash() -> str:
+    """SHA-1 of the library's sources as the Makefile computes it: the
+    contents of csrc/*.hip, *.cpp, *.h and ../include/*.h concatenated in the
+    byte order of their paths relative to the package root."""
+    rel = [f"csrc/{p.name}" for p in (ROOT / "csrc").iterdir() if p.suffix in (".hip", ".cpp", ".h")]
+    rel += [f"../include/{p.name}" for p in (ROOT.parent / "include").glob("*.h")]
+    h = hashlib.sha1()
+    for r in sorted(rel):
+        h.update((ROOT / r).read_bytes())
+    return h.hexdigest()
+
+
 def lib() -> C.CDLL:
-    """Load libnexus_hip.so (raises if it has not been built)."""
+    """Load libnexus_hip.so (raises if it has not been built, or if the
+    in-tree library was built from other sources than the tree holds)."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
@@ -206,6 +224,11 @@ def lib() -> C.CDLL:
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        if LIB_PATH == _DEFAULT_LIB:
+            built, tree = L.nx_source_hash().decode(), source_hash()
+            if built != tree:
+                raise RuntimeError(f"{LIB_PATH} was built from other sources (sha1 {built}) than the tree "
+                                   f"holds ({tree}): rebuild it with `make -C {ROOT}`")
         _lib = L
     return _lib
 

@@ -61,3 +61,11 @@ def test_null_arguments_are_rejected():
     assert L.nx_destroy(None) == 1
     assert L.nx_gemv_int4_g32(None, 0, 0, 0, 0, 1, 32, 1) == 1
     assert L.nx_tq_codebooks(None, None, None, None) == 1
+
+
+def test_library_built_from_these_sources():
+    """The in-tree library reports the SHA-1 of the sources it was built
+    from, and the binding refuses one built from other sources."""
+    L = nexus_amd.lib()
+    assert L.nx_source_hash().decode() == nexus_amd.source_hash()
+    assert re.fullmatch(r"[0-9a-f]{40}", nexus_amd.source_hash())
