@@ -143,6 +143,20 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
         }
     }
     const float scale = 1.0f / sqrtf((float)HD);
+    // 256-long heads: q's operands go to LDS (every wavefront writes the same
+    // values, then reads its own), read per k-step by pair_update
+    constexpr bool QL = HD > 128;
+    __shared__ __align__(16) uint4 qlds[QL ? G * 4 * (HD / 32) * 2 : 1];
+    const uint4* qls = nullptr;
+    if constexpr (QL) {
+        if (t < G)
+#pragma unroll
+            for (int s = 0; s < HD / 32; ++s) {
+                qlds[((t * 4 + g) * (HD / 32) + s) * 2] = __builtin_bit_cast(uint4, qh[s]);
+                qlds[((t * 4 + g) * (HD / 32) + s) * 2 + 1] = __builtin_bit_cast(uint4, ql[s]);
+            }
+        qls = qlds + (min(t, G - 1) * 4 + g) * (HD / 32) * 2;
+    }
     float m = -__builtin_inff(), lsum = 0.0f;
     f4_t o[HD / 16];
 #pragma unroll
@@ -152,7 +166,8 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
         // not fit the registers of two wavefronts per SIMD)
         for (int i = 0; i < npw; i += 2) {
             load_pair<HD>(ra, a, blk_of(i), valid_of(i), blk_of(i + 1), valid_of(i + 1), kvh, lane);
-            pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
+            pair_update<HD, false, false, QL>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane, 0,
+                                              0, 0, nullptr, qls);
         }
     } else if constexpr (PIPE) {
         // every pair is requested unconditionally, so the wait for the
@@ -166,7 +181,9 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
             pair_update<HD>(rb, qh, ql, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
         }
     } else {
-        if (npw > 0) pair_update<HD>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane);
+        if (npw > 0)
+            pair_update<HD, false, false, QL>(ra, qh, ql, scale, valid_of(0), valid_of(1), m, lsum, o, lane, 0, 0, 0,
+                                              nullptr, qls);
     }
     // the head's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);

@@ -192,22 +192,33 @@ __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, in
 // 4(l/16) + i of page a (b) is at position pos_a (pos_b) + 4(l/16) + i and
 // is masked for the query at position qpos (this lane's column) when later.
 // KLO: K is fp16 hi + lo (kl), a third product K_lo q_hi per step.
-template <int HD, bool CAUSAL = false, bool KLO = false>
+// QL (256-long heads): q's hi and lo operands are read from LDS per k-step
+// (qls[2s], qls[2s + 1]) instead of qh / ql, so they take no registers across
+// the page pair (a pair's K and V take 128 VGPRs there).
+template <int HD, bool CAUSAL = false, bool KLO = false, bool QL = false>
 __device__ inline void pair_update(const PairRaw<HD>& r, const h8_t (&qh)[HD / 32],
                                    const h8_t (&ql)[HD / 32], float scale, int na, int nb, float& m,
                                    float& lsum, f4_t (&o)[HD / 16], int lane, int pos_a = 0, int pos_b = 0,
-                                   int qpos = 0, const PairKlo<HD>* kl = nullptr) {
+                                   int qpos = 0, const PairKlo<HD>* kl = nullptr, const uint4* qls = nullptr) {
     const int g = lane >> 4;
     f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < HD / 32; ++s) {
-        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), qh[s], sa, 0, 0, 0);
-        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), ql[s], sa, 0, 0, 0);
-        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), qh[s], sb, 0, 0, 0);
-        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), ql[s], sb, 0, 0, 0);
+        h8_t qhs, qls_;
+        if constexpr (QL) {
+            qhs = as_h8(qls[2 * s]);
+            qls_ = as_h8(qls[2 * s + 1]);
+        } else {
+            qhs = qh[s];
+            qls_ = ql[s];
+        }
+        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), qhs, sa, 0, 0, 0);
+        sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[0][s]), qls_, sa, 0, 0, 0);
+        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), qhs, sb, 0, 0, 0);
+        sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(r.k[1][s]), qls_, sb, 0, 0, 0);
         if constexpr (KLO) {
-            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kl->k[0][s]), qh[s], sa, 0, 0, 0);
-            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kl->k[1][s]), qh[s], sb, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kl->k[0][s]), qhs, sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kl->k[1][s]), qhs, sb, 0, 0, 0);
         }
     }
     float p[8];
