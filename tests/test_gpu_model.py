@@ -124,6 +124,20 @@ def test_wide_moe_parity(ctx, E, k, batch):
     run_forced(ctx, cfg, 7, 16)
 
 
+@pytest.mark.parametrize("d,F,k", [(8192, 1024, 1), (2048, 7168, 2), (512, 14336, 3)])
+def test_moe_batch1_routed_shapes(ctx, d, F, k):
+    """Batch-1 routed experts at the widths whose kernels no other test
+    reaches: d_model 8192 (the routing gate/up launch with x in LDS), an FFN
+    of 7168 and 14336 (the down projection with the combine at 4 and 7
+    groups per lane), top-1 (one slot per output row) and top-3 (the
+    separate down projection and combine after the routing gate/up launch);
+    greedy tokens and teacher-forced logits against the oracle."""
+    cfg = dict(TINY, n_layers=1, d_model=d, ffn=F, n_experts=4, top_k=k, vocab=2048, seed=0xB100 + k)
+    got, want, margins = run_both(ctx, cfg, P=5, n_new=8)
+    assert_greedy_parity(got, want, margins)
+    run_forced(ctx, cfg, 5, 8)
+
+
 @pytest.mark.parametrize("batch,qk", [(1, 0), (3, 1)])
 def test_head_dim_256_parity(ctx, batch, qk):
     """256-long heads (the Gemma-style width the reference's Q/K-norm code
