@@ -183,7 +183,8 @@ size_t attn_f16_workspace_bytes(int batch, int hq, int hkv, int hd, int max_ctx)
 inline size_t attn_count_words(int batch, int hkv) { return (size_t)batch * hkv * kAttnCountStride; }
 // Longest context the attention kernels accept.
 int attn_max_ctx();
-// Each enqueues two launches: the split kernel and the merge of its records.
+// One launch each: the split blocks, the last of each (sequence, kv head)
+// merging the records.
 hipError_t attn_f16_launch(const AttnArgs& a, hipStream_t st);
 hipError_t attn_tq_launch(const AttnArgs& a, hipStream_t st);
 // Causal prefill attention over fp16 pages: q rows t < P ([P][hq][hd]) of
