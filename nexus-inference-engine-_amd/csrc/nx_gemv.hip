@@ -9,9 +9,10 @@
 // HBM stream: one 16-byte load (one group = 32 codes) plus one 2-byte scale
 // per lane per row, coalesced into 1 KiB per wave instruction.  R rows form a
 // tile whose R*GPL loads are in flight together.  At batch 1 the grid is
-// persistent (one block of 8 wavefronts per CU), each wavefront streams a
-// contiguous row range with the next tile requested before the current one
-// is reduced, and the first tiles are requested right after the input.  The
+// persistent (one block of 8 wavefronts per CU), the tiles are dealt to the
+// wavefronts in turn (the grid streams one window of the matrix at a time),
+// each wavefront requests its next tile before the current one is reduced,
+// and the first tiles are requested right after the input.  The
 // loads up to the first wait are straight-line code, so the wait for the
 // input counts the tile loads behind it instead of waiting for all of them.
 //
@@ -743,40 +744,58 @@ __global__ __launch_bounds__(256) void k_gemv_ksum(const float* __restrict__ par
 // The same sum, then (post_x16) the RMSNorm of each finished row: one block
 // of kNormRowThreads per batch row, 16-byte chunks (N % 4 == 0, N <=
 // 4 * kNormRowThreads * kNormRowChunks), every element summed exactly as
-// k_gemv_ksum sums it.
-constexpr int kNormRowThreads = 1024, kNormRowChunks = 4;
-template <int EPI>
-__global__ __launch_bounds__(kNormRowThreads) void k_gemv_ksum_norm(const float* __restrict__ part, int kparts,
-                                                                     int B, int N, float* y32, const float* w,
-                                                                     uint16_t* x16, float eps) {
+// k_gemv_ksum sums it.  KP parts, CH chunks per thread: every load of a
+// thread (its parts, the residual, the norm weights) is requested before
+// any is used, so the launch waits for one round trip (loads of chunks
+// past the row re-read its last chunk and are not used).
+constexpr int kNormRowThreads = 1024, kNormRowChunks = 4, kNormMaxParts = 8;
+template <int EPI, int KP, int CH>
+__global__ __launch_bounds__(kNormRowThreads) void k_gemv_ksum_norm(const float* __restrict__ part, int B, int N,
+                                                                     float* y32, const float* w, uint16_t* x16,
+                                                                     float eps) {
     __shared__ float red[kNormRowThreads / 64];
     const int b = blockIdx.x, t = threadIdx.x, nc = N / 4;
-    float4 v[kNormRowChunks];
+    // chunks whose loads are in flight together (all of them unless that
+    // would not fit the registers of 1024 threads)
+    constexpr int CL = CH * (KP + 2) <= 24 ? CH : 1;
+    float4 v[CH], wv[CH];
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kNormRowChunks; ++j) {
-        const int c = t + j * kNormRowThreads;
-        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (c >= nc) continue;
-        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int q = 0; q < kparts; ++q) {
-            const float4 p = reinterpret_cast<const float4*>(part + ((size_t)q * B + b) * N)[c];
-            s.x += p.x;
-            s.y += p.y;
-            s.z += p.z;
-            s.w += p.w;
+    for (int j0 = 0; j0 < CH; j0 += CL) {
+        float4 pv[CL][KP], yv[CL];
+#pragma unroll
+        for (int i = 0; i < CL; ++i) {
+            const int c = min(t + (j0 + i) * kNormRowThreads, nc - 1);
+#pragma unroll
+            for (int q = 0; q < KP; ++q)
+                pv[i][q] = reinterpret_cast<const float4*>(part + ((size_t)q * B + b) * N)[c];
+            yv[i] = EPI == E_ACC ? reinterpret_cast<const float4*>(y32 + (size_t)b * N)[c]
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[j0 + i] = w ? reinterpret_cast<const float4*>(w)[c] : make_float4(1.f, 1.f, 1.f, 1.f);
         }
-        float4* yp = reinterpret_cast<float4*>(y32 + (size_t)b * N) + c;
-        if (EPI == E_ACC) {
-            const float4 y = *yp;
-            s.x = y.x + s.x;
-            s.y = y.y + s.y;
-            s.z = y.z + s.z;
-            s.w = y.w + s.w;
+#pragma unroll
+        for (int i = 0; i < CL; ++i) {
+            const int c = t + (j0 + i) * kNormRowThreads;
+            float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int q = 0; q < KP; ++q) {
+                s.x += pv[i][q].x;
+                s.y += pv[i][q].y;
+                s.z += pv[i][q].z;
+                s.w += pv[i][q].w;
+            }
+            if (EPI == E_ACC) {
+                s.x = yv[i].x + s.x;
+                s.y = yv[i].y + s.y;
+                s.z = yv[i].z + s.z;
+                s.w = yv[i].w + s.w;
+            }
+            v[j0 + i] = s;
+            if (c < nc) {
+                reinterpret_cast<float4*>(y32 + (size_t)b * N)[c] = s;
+                ss += s.x * s.x + s.y * s.y + s.z * s.z + s.w * s.w;
+            }
         }
-        *yp = s;
-        v[j] = s;
-        ss += s.x * s.x + s.y * s.y + s.z * s.z + s.w * s.w;
     }
     ss = wave_sum(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
@@ -787,13 +806,39 @@ __global__ __launch_bounds__(kNormRowThreads) void k_gemv_ksum_norm(const float*
     const float inv = 1.0f / sqrtf(tot / (float)N + eps);
     uint2* ob = reinterpret_cast<uint2*>(x16 + (size_t)b * N);
 #pragma unroll
-    for (int j = 0; j < kNormRowChunks; ++j) {
+    for (int j = 0; j < CH; ++j) {
         const int c = t + j * kNormRowThreads;
         if (c >= nc) break;
-        const float4 wv = w ? reinterpret_cast<const float4*>(w)[c] : make_float4(1.f, 1.f, 1.f, 1.f);
-        const uint32_t lo = (uint32_t)f2h_bits(v[j].x * inv * wv.x) | ((uint32_t)f2h_bits(v[j].y * inv * wv.y) << 16);
-        const uint32_t hi = (uint32_t)f2h_bits(v[j].z * inv * wv.z) | ((uint32_t)f2h_bits(v[j].w * inv * wv.w) << 16);
+        const uint32_t lo = (uint32_t)f2h_bits(v[j].x * inv * wv[j].x) | ((uint32_t)f2h_bits(v[j].y * inv * wv[j].y) << 16);
+        const uint32_t hi = (uint32_t)f2h_bits(v[j].z * inv * wv[j].z) | ((uint32_t)f2h_bits(v[j].w * inv * wv[j].w) << 16);
         ob[c] = make_uint2(lo, hi);
+    }
+}
+
+template <int EPI, int KP>
+hipError_t ksum_norm_launch_kp(const GemvArgs& a, hipStream_t st) {
+    if (a.N <= 4 * kNormRowThreads)
+        hipLaunchKernelGGL((k_gemv_ksum_norm<EPI, KP, 1>), dim3(a.batch), dim3(kNormRowThreads), 0, st, a.kpart,
+                           a.batch, a.N, a.y32, a.post_norm_w, a.post_x16, a.post_eps);
+    else
+        hipLaunchKernelGGL((k_gemv_ksum_norm<EPI, KP, kNormRowChunks>), dim3(a.batch), dim3(kNormRowThreads), 0, st,
+                           a.kpart, a.batch, a.N, a.y32, a.post_norm_w, a.post_x16, a.post_eps);
+    return hipGetLastError();
+}
+
+// The part sums + RMSNorm launch for kp parts (1 <= kp <= kNormMaxParts).
+template <int EPI>
+hipError_t ksum_norm_launch(const GemvArgs& a, int kp, hipStream_t st) {
+    switch (kp) {
+        case 1: return ksum_norm_launch_kp<EPI, 1>(a, st);
+        case 2: return ksum_norm_launch_kp<EPI, 2>(a, st);
+        case 3: return ksum_norm_launch_kp<EPI, 3>(a, st);
+        case 4: return ksum_norm_launch_kp<EPI, 4>(a, st);
+        case 5: return ksum_norm_launch_kp<EPI, 5>(a, st);
+        case 6: return ksum_norm_launch_kp<EPI, 6>(a, st);
+        case 7: return ksum_norm_launch_kp<EPI, 7>(a, st);
+        case 8: return ksum_norm_launch_kp<EPI, 8>(a, st);
+        default: return hipErrorInvalidValue;
     }
 }
 
@@ -842,11 +887,7 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
                 const bool vec = a.N % 4 == 0 && a.N <= 4 * kNormRowThreads * kNormRowChunks && a.ldy == a.N &&
                                  ((reinterpret_cast<uintptr_t>(a.y32) | reinterpret_cast<uintptr_t>(a.post_norm_w) |
                                    reinterpret_cast<uintptr_t>(a.post_x16)) & 15u) == 0;
-                if (a.post_x16 && vec) {
-                    hipLaunchKernelGGL((k_gemv_ksum_norm<EPI>), dim3(a.batch), dim3(kNormRowThreads), 0, st,
-                                       a.kpart, kp, a.batch, a.N, a.y32, a.post_norm_w, a.post_x16, a.post_eps);
-                    return hipGetLastError();
-                }
+                if (a.post_x16 && vec && kp <= kNormMaxParts) return ksum_norm_launch<EPI>(a, kp, st);
             }
             const int n = a.batch * a.N;
             hipLaunchKernelGGL((k_gemv_ksum<EPI>), dim3((n + 255) / 256), dim3(256), 0, st, a.kpart, kp, a.batch,

@@ -75,9 +75,11 @@ __global__ __launch_bounds__(kMoeThreads, 1) void k_moe_b1_gate_up(GemvArgs a, R
     asm volatile("" ::"s"(a.h32), "s"(a.norm_w), "s"(m.wr), "s"(m.sr), "s"(m.E), "s"(a.G), "s"(a.K));
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
     const int E = m.E, G = a.G;
-    int r0, r1;
-    wave_rows(rs, blockIdx.x * WPB + wave, a.N, r0, r1);
-    const int nt = r1 > r0 ? (r1 - r0 + R - 1) / R : 0;
+    // the grid row's tiles dealt to its wavefronts in turn (as the dense
+    // batch-1 GEMV deals them)
+    const int NW = rs.nb * rs.wpb, T = (a.N + R - 1) / R, wid = blockIdx.x * WPB + wave;
+    const int nt = wid < T ? (T - wid + NW - 1) / NW : 0;
+    auto trow = [&](int k) { return (wid + min(k, max(nt - 1, 0)) * NW) * R; };
     // h with its norm weights, and this wavefront's first router row
     StageRegs<CPT, X_RMSNORM> sr;
     stage_issue<CPT, X_RMSNORM, NT, XVEC>(a, 0, sr);
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(kMoeThreads, 1) void k_moe_b1_gate_up(GemvArgs a, R
     g.act16 += (size_t)slot * a.lda;
     Tile<GPL, R> t[DEPTH];
 #pragma unroll
-    for (int j = 0; j < DEPTH; ++j) load_tile_u<GPL, R>(t[j], g.W, g.S, G, r0, r1, r0 + j * R, lane);
+    for (int j = 0; j < DEPTH; ++j) load_tile_u<GPL, R>(t[j], g.W, g.S, G, 0, a.N, trow(j), lane);
     float best_v = 0.0f;
     int best_i = 0;
     float res[R];
@@ -131,8 +133,8 @@ __global__ __launch_bounds__(kMoeThreads, 1) void k_moe_b1_gate_up(GemvArgs a, R
                 tile_dot_lds<GPL, R>(t[j], sp, s8, G, lane, res);
             else
                 tile_dot<GPL, R>(t[j], xp, res);
-            load_tile_u<GPL, R>(t[j], g.W, g.S, G, r0, r1, r0 + (i + j + DEPTH) * R, lane);
-            if (lane == 0) epilogue<E_SWIGLU, R>(g, 0, r0 + (i + j) * R, r1, res, best_v, best_i);
+            load_tile_u<GPL, R>(t[j], g.W, g.S, G, 0, a.N, trow(i + j + DEPTH), lane);
+            if (lane == 0) epilogue<E_SWIGLU, R>(g, 0, trow(i + j), a.N, res, best_v, best_i);
         }
     }
 }
