@@ -593,13 +593,15 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     __shared__ float s8[kWave * GPL];
     __shared__ float red[WPB];
     const int lane = threadIdx.x & (kWave - 1);
-    const int wid = block * WPB + (threadIdx.x >> 6);
     // Tiles of R rows are dealt to the grid's NW wavefronts in turn: the k-th
     // tile of wavefront w holds rows (w + k NW) R .., so at any moment the
     // grid streams one contiguous window of the matrix (contiguous row
     // ranges per wavefront, 2048 separate streams, were 7% slower on the
-    // 28672 x 4096 gate/up).  Requests past the wavefront's last tile
+    // 28672 x 4096 gate/up).  Wavefront j of block b deals as w = j nb + b,
+    // so a last partial round spreads over every block (CU) rather than
+    // filling the first ones.  Requests past the wavefront's last tile
     // re-read that tile.
+    const int wid = (threadIdx.x >> 6) * rs.nb + block;
     const int NW = rs.nb * rs.wpb, T = (a.N + R - 1) / R;
     const int nt = wid < T ? (T - wid + NW - 1) / NW : 0;
     auto trow = [&](int k) { return (wid + min(k, max(nt - 1, 0)) * NW) * R; };

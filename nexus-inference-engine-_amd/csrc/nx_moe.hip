@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kMoeThreads, 1) void k_moe_b1_gate_up(GemvArgs a, R
     const int E = m.E, G = a.G;
     // the grid row's tiles dealt to its wavefronts in turn (as the dense
     // batch-1 GEMV deals them)
-    const int NW = rs.nb * rs.wpb, T = (a.N + R - 1) / R, wid = blockIdx.x * WPB + wave;
+    const int NW = rs.nb * rs.wpb, T = (a.N + R - 1) / R, wid = wave * rs.nb + blockIdx.x;
     const int nt = wid < T ? (T - wid + NW - 1) / NW : 0;
     auto trow = [&](int k) { return (wid + min(k, max(nt - 1, 0)) * NW) * R; };
     // h with its norm weights, and this wavefront's first router row
