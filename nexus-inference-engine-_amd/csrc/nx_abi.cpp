@@ -945,10 +945,11 @@ nx_status nx_sample(nx_ctx* ctx, nx_buf logits, nx_buf out, int V, int batch, fl
     if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f) return fail(ctx, NX_ERR_INVALID, "nx_sample: bad parameters");
     NX_NEED(ctx, logits, (size_t)batch * V * 4, "logits");
     NX_NEED(ctx, out, (size_t)batch * 4, "out");
-    nx_status ws = ensure_smp_ws(ctx, (size_t)batch * V);
+    nx_status ws = ensure_smp_ws(ctx, (size_t)batch * ((size_t)V + nx::kSmpPartFloats));
     if (ws != NX_OK) return ws;
     nx::SampleArgs a{};
     a.scratch = ctx->smp_ws;
+    a.part = ctx->smp_ws + (size_t)batch * V;
     a.logits = dptr<const float>(logits);
     a.V = V;
     a.ldl = V;

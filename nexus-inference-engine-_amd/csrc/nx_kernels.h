@@ -434,7 +434,12 @@ struct SampleArgs {
     int32_t* out;
     unsigned long long* best;
     float* scratch;       // [batch][V] floats
+    float* part;          // [batch][kSmpPartFloats] floats
 };
+// Per-block partials of the sampler's first passes (max, sum, candidate
+// counts of each of kSmpBlocks blocks per sequence).
+constexpr int kSmpBlocks = 64;
+constexpr int kSmpPartFloats = kSmpBlocks * 10;
 hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st);
 // The reference's draw for a seed: std::uniform_real_distribution<float>(0, 1)
 // of the first output of std::mt19937(seed) (seed 0: std::random_device).

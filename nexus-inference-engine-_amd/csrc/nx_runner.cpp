@@ -123,7 +123,7 @@ struct nx_model {
     // sampling (temperature <= 0: greedy argmax of the lm_head epilogue)
     float temperature = 0.0f, top_p = 1.0f, u_fixed = -1.0f;
     int top_k = 0;
-    float* smp_scratch = nullptr;  // [batch][vocab], allocated when sampling is first set
+    float* smp_scratch = nullptr;  // [batch][vocab] then [batch][kSmpPartFloats], allocated when sampling is first set
     // per-slot serving state: a slot holds one sequence (active) or none
     // (free: parked at position 0 by the step graph); feed / fpos tell the
     // embedding kernel what each slot consumes at a step (kFeed*)
@@ -233,6 +233,7 @@ nx_status enqueue_sample(nx_model* m, int b0, int nb) {
     s.pos = m->pos + b0;
     s.best = m->best + b0;
     s.scratch = m->smp_scratch + (size_t)b0 * m->c.vocab;
+    s.part = m->smp_scratch + (size_t)m->c.batch * m->c.vocab + (size_t)b0 * nx::kSmpPartFloats;
     NX_LAUNCH(m, nx::sample_launch(s, nb, m->ctx->stream));
     return NX_OK;
 }
@@ -1234,7 +1235,8 @@ nx_status nx_model_set_sampling(nx_model* m, float temperature, int top_k, float
     if (temperature > 0.0f) {
         if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f) return fail(m->ctx, NX_ERR_INVALID, "sampling: bad parameters");
     }
-    if (temperature > 0.0f && !m->smp_scratch) NX_TRY(dalloc(m, &m->smp_scratch, (size_t)m->c.batch * V));
+    if (temperature > 0.0f && !m->smp_scratch)
+        NX_TRY(dalloc(m, &m->smp_scratch, (size_t)m->c.batch * ((size_t)V + nx::kSmpPartFloats)));
     m->temperature = temperature > 0.0f ? temperature : 0.0f;
     m->top_k = top_k;
     m->top_p = top_p;

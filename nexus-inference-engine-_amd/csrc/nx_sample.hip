@@ -3,12 +3,14 @@
 // top-k, top-p, renormalize, one uniform draw, the first vocabulary index
 // whose running sum reaches it -- so the logits never leave HBM.
 //
-// One block of 1024 threads per sequence.  Wavefront w owns the contiguous
-// vocabulary chunk [w C, (w + 1) C) and walks it 64 consecutive entries at a
-// time (coalesced), so wavefront order then iteration order then lane order
-// is vocabulary order; ballots keep that order where it matters.
-// e_i = expf((l_i - max) / T) is computed once into a scratch row; later
-// passes read p_i = e_i / sum.
+// Three launches: the maximum logit, then e_i = expf((l_i - max) / T) into a
+// scratch row with partial sums and candidate counts, each over 64 blocks
+// per sequence (k_sample_max, k_sample_exp); then one block of 1024 threads
+// per sequence (k_sample) for the selection and the draw.  In k_sample,
+// wavefront w owns the contiguous vocabulary chunk [w C, (w + 1) C) and
+// walks it 64 consecutive entries at a time (coalesced), so wavefront order
+// then iteration order then lane order is vocabulary order; ballots keep
+// that order where it matters.  Later passes read p_i = e_i / sum.
 //  - top-k (0 < k <= 1024, k < V): four 8-bit radix passes over the bits of
 //    p_i (positive floats order as their bits) find the k-th largest value;
 //    ties at that value keep the lowest indices (the reference's
@@ -24,8 +26,9 @@
 //    first exceeds top_p; ties at either value keep the lowest indices.
 //    The draw's scan runs over the kept entries in wavefront, iteration and
 //    lane order with fp32 partial sums in a fixed order.
-// The softmax denominator is a fixed-order block sum; the reference's is a
-// sequential fp32 sum, so probabilities agree to rounding.
+// The softmax denominator is a fixed-order sum (per block, then the blocks
+// in order); the reference's is a sequential fp32 sum, so probabilities
+// agree to rounding.
 #include "nx_common.h"
 #include "nx_kernels.h"
 
@@ -112,6 +115,87 @@ __device__ inline void smp_pass(int c0, int c1, Load load, Use use) {
     }
 }
 
+// The first two passes over the vocabulary, spread over kSmpBlocks blocks
+// per sequence (on the one block of k_sample they took 50 of its 85 us):
+// block p = 4 w + q covers quarter q of k_sample wavefront w's chunk.
+// k_sample_max writes each block's maximum logit; k_sample_exp takes the
+// maximum of those (exact in any order), writes e_i = expf((l_i - max) / T)
+// into the scratch row and each block's sum of e (per thread in index
+// order, wavefront tree, wavefronts in order) and its counts at each
+// candidate threshold.  k_sample adds the sums in block order.
+constexpr int kSmpPThreads = 256, kSmpPWaves = kSmpPThreads / 64;
+static_assert(kSmpBlocks == 4 * kSmpWaves && kSmpBlocks == 64, "four blocks per k_sample wavefront chunk, one per lane");
+static_assert(kSmpPartFloats == kSmpBlocks * (2 + kSmpThr), "partials: max, sum, counts");
+__device__ inline void smp_block_range(int V, int p, int& c0, int& c1) {
+    const int C = ((V + kSmpWaves - 1) / kSmpWaves + 63) / 64 * 64, Q = C / 4;
+    c0 = min((p / 4) * C + (p % 4) * Q, V);
+    c1 = min(c0 + Q, V);
+}
+
+__global__ __launch_bounds__(kSmpPThreads) void k_sample_max(SampleArgs a) {
+    __shared__ float wm[kSmpPWaves];
+    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const float* lg = a.logits + (size_t)b * a.ldl;
+    int c0, c1;
+    smp_block_range(a.V, p, c0, c1);
+    float mx = -__builtin_inff();
+    for (int i = c0 + tid; i < c1; i += kSmpPThreads) mx = fmaxf(mx, lg[i]);
+    mx = smp_wave_max(mx);
+    if ((tid & 63) == 0) wm[tid >> 6] = mx;
+    __syncthreads();
+    if (tid == 0) {
+        float m = wm[0];
+        for (int j = 1; j < kSmpPWaves; ++j) m = fmaxf(m, wm[j]);
+        a.part[(size_t)b * kSmpPartFloats + p] = m;
+    }
+}
+
+__global__ __launch_bounds__(kSmpPThreads) void k_sample_exp(SampleArgs a) {
+    __shared__ float wm[kSmpPWaves];
+    __shared__ int wc[kSmpThr][kSmpPWaves];
+    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const float* lg = a.logits + (size_t)b * a.ldl;
+    float* e = a.scratch + (size_t)b * a.V;
+    float* pt = a.part + (size_t)b * kSmpPartFloats;
+    int c0, c1;
+    smp_block_range(a.V, p, c0, c1);
+    // the sequence's maximum: every wavefront takes it from the blocks' maxima
+    const float mx = smp_wave_max(pt[l]);
+    const float T = a.temperature;
+    float sum = 0.0f, thr[kSmpThr];
+    int cnt[kSmpThr];
+#pragma unroll
+    for (int j = 0; j < kSmpThr; ++j) {
+        thr[j] = expf(-c_smp_D[j]);
+        cnt[j] = 0;
+    }
+    for (int i = c0 + tid; i < c1; i += kSmpPThreads) {
+        const float v = expf((lg[i] - mx) / T);
+        e[i] = v;
+        sum += v;
+#pragma unroll
+        for (int j = 0; j < kSmpThr; ++j) cnt[j] += v >= thr[j];
+    }
+    sum = smp_wave_sum(sum);
+#pragma unroll
+    for (int j = 0; j < kSmpThr; ++j) {
+        const int c = smp_wave_sum(cnt[j]);
+        if (l == 0) wc[j][w] = c;
+    }
+    if (l == 0) wm[w] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        float s = 0.0f;
+        for (int j = 0; j < kSmpPWaves; ++j) s += wm[j];
+        pt[kSmpBlocks + p] = s;
+    }
+    if (tid < kSmpThr) {
+        int c = 0;
+        for (int j = 0; j < kSmpPWaves; ++j) c += wc[tid][j];
+        pt[2 * kSmpBlocks + kSmpThr * p + tid] = (float)c;  // exact: c <= V < 2^24
+    }
+}
+
 __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
     __shared__ float wf[kSmpWaves + 1];
     __shared__ int wi[4][kSmpWaves + 1];
@@ -122,54 +206,23 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
     __shared__ int ord[kSmpCand];
     __shared__ int tcnt[kSmpThr][kSmpWaves + 1];
     const int b = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63, V = a.V;
-    const float* lg = a.logits + (size_t)b * a.ldl;
-    float* e = a.scratch + (size_t)b * V;
+    const float* e = a.scratch + (size_t)b * V;
     const int C = ((V + kSmpWaves - 1) / kSmpWaves + 63) / 64 * 64;
     const int c0 = min(w * C, V), c1 = min(c0 + C, V);
-    const float T = a.temperature;
 
-    // max, then e and its sum: per lane in order, wavefront tree, wavefronts in order
-    float mx = -__builtin_inff();
-    smp_pass(c0, c1, [&](int i) { return lg[i]; }, [&](int, bool ok, float v) { mx = ok ? fmaxf(mx, v) : mx; });
-    mx = smp_wave_max(mx);
-    if (l == 0) wf[w] = mx;
-    __syncthreads();
-    if (tid == 0) {
-        float m = wf[0];
-        for (int j = 1; j < kSmpWaves; ++j) m = fmaxf(m, wf[j]);
-        wf[kSmpWaves] = m;
+    // the e row, its sum (the blocks' sums in block order) and per wavefront
+    // chunk the entries at or above each candidate threshold exp(-D), from
+    // k_sample_max / k_sample_exp
+    const float* pt = a.part + (size_t)b * kSmpPartFloats;
+    if (tid < kSmpThr * kSmpWaves) {
+        const int j = tid / kSmpWaves, ww = tid % kSmpWaves;
+        float c = 0.0f;
+        for (int q = 0; q < 4; ++q) c += pt[2 * kSmpBlocks + kSmpThr * (4 * ww + q) + j];
+        tcnt[j][ww] = (int)c;
     }
-    __syncthreads();
-    mx = wf[kSmpWaves];
-    __syncthreads();
-    // e, its sum, and per wavefront the entries at or above each candidate
-    // threshold exp(-D)
-    float part = 0.0f, thr[kSmpThr];
-    int cnt[kSmpThr];
-#pragma unroll
-    for (int j = 0; j < kSmpThr; ++j) {
-        thr[j] = expf(-c_smp_D[j]);
-        cnt[j] = 0;
-    }
-    smp_pass(c0, c1, [&](int i) { return lg[i]; }, [&](int i0, bool ok, float x) {
-        if (!ok) return;
-        const float v = expf((x - mx) / T);
-        e[i0 + l] = v;
-        part += v;
-#pragma unroll
-        for (int j = 0; j < kSmpThr; ++j) cnt[j] += v >= thr[j];
-    });
-#pragma unroll
-    for (int j = 0; j < kSmpThr; ++j) {
-        const int c = smp_wave_sum(cnt[j]);
-        if (l == 0) tcnt[j][w] = c;
-    }
-    part = smp_wave_sum(part);
-    if (l == 0) wf[w] = part;
-    __syncthreads();  // also makes the e row visible to the block
     if (tid == 0) {
         float acc = 0.0f;
-        for (int j = 0; j < kSmpWaves; ++j) acc += wf[j];
+        for (int j = 0; j < kSmpBlocks; ++j) acc += pt[kSmpBlocks + j];
         wf[kSmpWaves] = acc;
     }
     __syncthreads();
@@ -602,9 +655,11 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
 }  // namespace
 
 hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st) {
-    if (a.V < 1 || batch < 1 || a.temperature <= 0.0f || a.top_k < 0 || !(a.top_p > 0.0f) || a.top_p > 1.0f ||
-        (a.u_fixed < 0.0f && !a.u && !a.pos) || !a.scratch)
+    if (a.V < 1 || a.V >= (1 << 24) || batch < 1 || a.temperature <= 0.0f || a.top_k < 0 || !(a.top_p > 0.0f) ||
+        a.top_p > 1.0f || (a.u_fixed < 0.0f && !a.u && !a.pos) || !a.scratch || !a.part)
         return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sample_max, dim3(kSmpBlocks, batch), dim3(kSmpPThreads), 0, st, a);
+    hipLaunchKernelGGL(k_sample_exp, dim3(kSmpBlocks, batch), dim3(kSmpPThreads), 0, st, a);
     hipLaunchKernelGGL(k_sample, dim3(batch), dim3(kSmpThreads), 0, st, a);
     return hipGetLastError();
 }
