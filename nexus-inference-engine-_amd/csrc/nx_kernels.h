@@ -437,9 +437,11 @@ struct SampleArgs {
     float* part;          // [batch][kSmpPartFloats] floats
 };
 // Per-block partials of the sampler's first passes (max, sum, candidate
-// counts of each of kSmpBlocks blocks per sequence).
-constexpr int kSmpBlocks = 64;
-constexpr int kSmpPartFloats = kSmpBlocks * 10;
+// counts of each of kSmpBlocks blocks per sequence), then the top-k
+// candidates (kSmpCandMax probabilities, then as many indices).
+constexpr int kSmpBlocks = 64, kSmpCandMax = 4096;
+constexpr int kSmpCandOff = kSmpBlocks * 10;
+constexpr int kSmpPartFloats = kSmpCandOff + 2 * kSmpCandMax;
 hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st);
 // The reference's draw for a seed: std::uniform_real_distribution<float>(0, 1)
 // of the first output of std::mt19937(seed) (seed 0: std::random_device).

@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kSmpThreads = 1024;
 constexpr int kSmpMaxK = 1024;
-constexpr int kSmpCand = 4096;  // top-k candidates held in LDS
+constexpr int kSmpCand = kSmpCandMax;  // top-k candidates held in LDS
 constexpr int kSmpThr = 8;      // candidate thresholds e >= exp(-D)
 __constant__ float c_smp_D[kSmpThr] = {24.0f, 16.0f, 12.0f, 8.0f, 5.0f, 3.0f, 2.0f, 1.0f};
 
@@ -125,7 +125,7 @@ __device__ inline void smp_pass(int c0, int c1, Load load, Use use) {
 // candidate threshold.  k_sample adds the sums in block order.
 constexpr int kSmpPThreads = 256, kSmpPWaves = kSmpPThreads / 64;
 static_assert(kSmpBlocks == 4 * kSmpWaves && kSmpBlocks == 64, "four blocks per k_sample wavefront chunk, one per lane");
-static_assert(kSmpPartFloats == kSmpBlocks * (2 + kSmpThr), "partials: max, sum, counts");
+static_assert(kSmpCandOff == kSmpBlocks * (2 + kSmpThr), "partials: max, sum, counts");
 __device__ inline void smp_block_range(int V, int p, int& c0, int& c1) {
     const int C = ((V + kSmpWaves - 1) / kSmpWaves + 63) / 64 * 64, Q = C / 4;
     c0 = min((p / 4) * C + (p % 4) * Q, V);
@@ -196,6 +196,71 @@ __global__ __launch_bounds__(kSmpPThreads) void k_sample_exp(SampleArgs a) {
     }
 }
 
+// Top-k (k <= kSmpMaxK) with a candidate threshold that fits kSmpCand: the
+// threshold pick of k_sample (the smallest D whose count of e >= exp(-D) is
+// at least k), then block p writes the entries of its range at or above it,
+// in index order, at the sum of the earlier blocks' counts -- the candidate
+// list k_sample would gather with one pass over the row on one CU.
+__global__ __launch_bounds__(kSmpPThreads) void k_sample_gather(SampleArgs a) {
+    __shared__ int wsum[kSmpPWaves];
+    __shared__ int pk[2];
+    __shared__ float sm;
+    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    if (!(a.top_k > 0 && a.top_k < a.V && a.top_k <= kSmpMaxK)) return;
+    const float* e = a.scratch + (size_t)b * a.V;
+    float* pt = a.part + (size_t)b * kSmpPartFloats;
+    if (w == 0) {
+        // lane q: block q's counts; totals in a fixed order (exact integers)
+        int pick = -1, base = 0;
+        for (int j = 0; j < kSmpThr; ++j) {
+            const int c = (int)pt[2 * kSmpBlocks + kSmpThr * l + j];
+            const int tot = smp_wave_sum(c);
+            if (tot >= a.top_k) {
+                pick = tot <= kSmpCand ? j : -2;
+                base = smp_wave_sum(l < p ? c : 0);
+            }
+        }
+        if (l == 0) {
+            pk[0] = pick;
+            pk[1] = base;
+        }
+    }
+    if (tid == 0) {
+        float acc = 0.0f;
+        for (int j = 0; j < kSmpBlocks; ++j) acc += pt[kSmpBlocks + j];
+        sm = acc;
+    }
+    __syncthreads();
+    const int pick = pk[0];
+    if (pick < 0) return;
+    int base = pk[1];
+    const float sum_e = sm, th = expf(-c_smp_D[pick]);
+    float* cp = pt + kSmpCandOff;
+    int* ci = reinterpret_cast<int*>(cp + kSmpCandMax);
+    int c0, c1;
+    smp_block_range(a.V, p, c0, c1);
+    for (int i0 = c0; i0 < c1; i0 += kSmpPThreads) {
+        const int i = i0 + tid;
+        const float ev = i < c1 ? e[i] : 0.0f;
+        const bool keep = i < c1 && ev >= th;
+        const unsigned long long km = __ballot(keep);
+        if (l == 0) wsum[w] = __popcll(km);
+        __syncthreads();
+        int before = 0, all = 0;
+        for (int j = 0; j < kSmpPWaves; ++j) {
+            before += j < w ? wsum[j] : 0;
+            all += wsum[j];
+        }
+        if (keep) {
+            const int at = base + before + popc_below(km, l);
+            cp[at] = ev / sum_e;
+            ci[at] = i;
+        }
+        base += all;
+        __syncthreads();
+    }
+}
+
 __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
     __shared__ float wf[kSmpWaves + 1];
     __shared__ int wi[4][kSmpWaves + 1];
@@ -263,19 +328,14 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
         int n = 0;
         const int pick = wi[0][3];
         if (pick >= 0) {
-            const float th = expf(-c_smp_D[pick]);
-            int orun = tcnt[pick][w];
-            smp_pass(c0, c1, [&](int i) { return e[i]; }, [&](int i0, bool ok, float ev) {
-                const bool keep = ok && ev >= th;
-                const unsigned long long km = __ballot(keep);
-                if (keep) {
-                    const int at = orun + popc_below(km, l);
-                    cand_p[at] = ev / sum_e;
-                    cand_i[at] = i0 + l;
-                }
-                orun += __popcll(km);
-            });
+            // the candidates gathered by k_sample_gather, in index order
             n = tcnt[pick][kSmpWaves];
+            const float* cp = a.part + (size_t)b * kSmpPartFloats + kSmpCandOff;
+            const int* ci = reinterpret_cast<const int*>(cp + kSmpCandMax);
+            for (int j = tid; j < n; j += kSmpThreads) {
+                cand_p[j] = cp[j];
+                cand_i[j] = ci[j];
+            }
         } else {
         // the k-th largest p: radix select over its bits, 8 at a time
         uint32_t prefix = 0, pmask = 0;
@@ -660,6 +720,8 @@ hipError_t sample_launch(const SampleArgs& a, int batch, hipStream_t st) {
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_sample_max, dim3(kSmpBlocks, batch), dim3(kSmpPThreads), 0, st, a);
     hipLaunchKernelGGL(k_sample_exp, dim3(kSmpBlocks, batch), dim3(kSmpPThreads), 0, st, a);
+    if (a.top_k > 0 && a.top_k < a.V && a.top_k <= kSmpMaxK)
+        hipLaunchKernelGGL(k_sample_gather, dim3(kSmpBlocks, batch), dim3(kSmpPThreads), 0, st, a);
     hipLaunchKernelGGL(k_sample, dim3(batch), dim3(kSmpThreads), 0, st, a);
     return hipGetLastError();
 }
