@@ -1177,7 +1177,7 @@ nx_status nx_reserve_workspace(nx_ctx* ctx, int batch, int max_ffn, int vocab, i
         float* unused = nullptr;  // the down projection's K parts (d = n_heads * head_dim)
         s = gemv_kpart_ws(ctx, n_heads * head_dim, max_ffn, batch, &unused);
     }
-    if (s == NX_OK && vocab > 0) s = ensure_smp_ws(ctx, (size_t)batch * vocab);
+    if (s == NX_OK && vocab > 0) s = ensure_smp_ws(ctx, (size_t)batch * ((size_t)vocab + nx::kSmpPartFloats));
     if (s == NX_OK && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_ctx > 0) {
         if (n_heads % n_kv_heads) return fail(ctx, NX_ERR_INVALID, "nx_reserve_workspace: n_heads % n_kv_heads");
         if (max_ctx > nx::attn_max_ctx()) return fail(ctx, NX_ERR_UNSUPPORTED, "max_ctx above the attention limit");
