@@ -922,22 +922,24 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st, int ny = 1) {
 // Tile shapes per groups-per-lane (K <= 64 * 32 * GPL), chosen by measuring
 // the 8B decode shapes on cold weights; batch 1 runs one block of 8
 // wavefronts per CU.  K = 4096: QKV and gate/up in 2-row tiles (a pair, as
-// the RoPE and SwiGLU epilogues need) in a ring of 2, lm_head in a ring of
-// 3, 2-row tiles in a ring of 1 otherwise (wo: one tile per wavefront).
+// the RoPE and SwiGLU epilogues need), in a ring of 1 (QKV: 1.5 tiles per
+// wavefront) and of 2; lm_head in a ring of 3; 2-row tiles in a ring of 1
+// otherwise (wo: one tile per wavefront).
 // K = 14336 without paired rows: one row per tile with x in registers.
 // Paired epilogues at GPL >= 4 keep x in LDS (at GPL 7 one pair in flight
 // per wavefront: two spilled).  (Measured at batch 1 against these: QKV in
-// one 4-row tile per wavefront (192 blocks), a ring of 1 or of 3; wo as
-// single rows in a ring of 3 or 1; gate/up in a ring of 1 or 3, or with 12
-// or 16 wavefronts per CU; down in a ring of 2 (x in registers or in LDS)
-// or as 2-row tiles: all slower.)
+// 4-row tiles, a ring of 2 or of 3; wo as single rows in a ring of 3 or 1;
+// gate/up in a ring of 1 or 3, in 4-row tiles, or with 12 or 16 wavefronts
+// per CU; down in a ring of 2 (x in registers or in LDS) or as 2-row tiles:
+// all slower; lm_head in a ring of 1 or 2, or in 4-row tiles: the same.)
 template <int XS, int EPI>
 hipError_t launch_b1_gpl(const GemvArgs& a, hipStream_t st) {
     const int gpl = (a.G + kWave - 1) / kWave;
     constexpr bool kPairs = EPI == E_QKV || EPI == E_SWIGLU;
     if (gpl <= 1) return launch_b1<1, 4, 2, false, XS, EPI>(a, st);
     if (gpl <= 2) {
-        if constexpr (EPI == E_QKV || EPI == E_SWIGLU) return launch_b1<2, 2, 2, false, XS, EPI>(a, st);
+        if constexpr (EPI == E_QKV) return launch_b1<2, 2, 1, false, XS, EPI>(a, st);
+        if constexpr (EPI == E_SWIGLU) return launch_b1<2, 2, 2, false, XS, EPI>(a, st);
         if constexpr (EPI == E_LOGITS) return launch_b1<2, 2, 3, false, XS, EPI>(a, st);
         return launch_b1<2, 2, 1, false, XS, EPI>(a, st);
     }
