@@ -71,7 +71,7 @@ template <int G, int HD, bool PIPE, bool TIER = false>
 __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, int kvh, int b,
                                     int range = 0, int slot = -1, int nrec = 0, int ntq = 0) {
     constexpr int REC = rec_floats(G, HD), MO = G * HD, LO = G * HD + G;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, t = lane & 15;
     __shared__ __align__(16) float lds[kAttnWaves * REC];
     attn_args_early(a);
@@ -771,7 +771,7 @@ __global__ __launch_bounds__(256) void k_tq_encode(const float* x, int nvec, con
                                                    uint8_t* c4, uint8_t* c3, uint16_t* norms,
                                                    const int32_t* idx) {
     __shared__ uint8_t codes[4][128];
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int v = blockIdx.x * 4 + wave;
     if (v >= nvec) return;
     const int dst = idx ? idx[v] : v;
@@ -786,7 +786,7 @@ __global__ __launch_bounds__(256) void k_tq_encode_ctx(const float* x, int ctx, 
                                                        const int32_t* block_table, int max_blocks,
                                                        int b, int p0) {
     __shared__ uint8_t codes[4][128];
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int v = p0 * hkv + blockIdx.x * 4 + wave;
     if (v >= ctx * hkv) return;
     const int t = v / hkv, h = v % hkv;
@@ -804,7 +804,7 @@ __global__ __launch_bounds__(256) void k_tq_append(const float* kv_tmp, int batc
                                                    const int32_t* block_table, const int32_t* pos,
                                                    int max_blocks) {
     __shared__ uint8_t codes[4][128];
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int v = blockIdx.x * 4 + wave;  // (b, kv, h)
     if (v >= batch * 2 * hkv) return;
     const int b = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv;
@@ -825,7 +825,7 @@ __global__ __launch_bounds__(256) void k_tq_encode_rows(const float* kvrows, int
                                                         uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3,
                                                         uint16_t* vn, const int32_t* bt) {
     __shared__ uint8_t codes[4][128];
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int v = blockIdx.x * 4 + wave;  // (t, kv, h)
     if (v >= n * 2 * hkv) return;
     const int t = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv, p = p0 + t;
@@ -848,7 +848,7 @@ __global__ __launch_bounds__(256) void k_tq_decode_pages(const uint8_t* kc4, con
                                                          const float* ksign, const float* vsign, const int32_t* bt,
                                                          int npos, int hkv, uint16_t* kpool, uint16_t* vpool,
                                                          uint16_t* klo) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int v = blockIdx.x * 4 + wave;  // (p, kv, h)
     if (v >= npos * 2 * hkv) return;
     const int p = v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv;
@@ -884,7 +884,7 @@ __global__ __launch_bounds__(256) void k_tq_decode_pages(const uint8_t* kc4, con
 // (prefill over TurboQuant pages decoded for it).
 template <int G, int HD, bool KLO = false>
 __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int P) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, t = lane & 15;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = lane >> 4, t = lane & 15;
     const int kvh = blockIdx.y, h = kvh * G + w;
     const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16;
     const int lastpos = p0 + min(q0 + 15, P - 1);
@@ -984,7 +984,7 @@ static_assert(kCompressWaves <= kAttnWaves, "a compressing block holds one wavef
 // is still packing.
 __device__ inline void tq_compress_block(const AttnArgs& a, int kv, int part, int h, int b) {
     __shared__ uint8_t codes[kCompressWaves][128];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int done = a.pos[b] - a.hot_window + 1;
     if (w >= kCompressWaves || done < kPage || done % kPage) return;
     const int q = done / kPage - 1;
@@ -1021,7 +1021,7 @@ __device__ inline void tq_compress_block(const AttnArgs& a, int kv, int part, in
 // Warm ring.
 __device__ inline void cool_compress_block(const AttnArgs& a, int kv, int part, int h, int b) {
     __shared__ uint8_t codes[kCompressWaves][128];
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int done = a.pos[b] - a.hot_window - a.warm_window + 1;
     if (w >= kCompressWaves || done < kPage || done % kPage) return;
     const int q = done / kPage - 1;
@@ -1095,7 +1095,7 @@ __global__ __launch_bounds__(256) void k_cool_encode_ctx(const float* x, int p0,
                                                          uint8_t* cc, uint16_t* cn, const int32_t* cool_table,
                                                          int max_blocks, int b) {
     __shared__ uint8_t codes[4][128];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int v = p0 * hkv + blockIdx.x * 4 + wave;
     if (v >= n * hkv) return;
     const int t = v / hkv, h = v % hkv;

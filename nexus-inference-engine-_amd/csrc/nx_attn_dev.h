@@ -317,7 +317,7 @@ __device__ inline void merge_last(const AttnArgs& a, int nsplit, int ntq, int kv
     static_assert(NC * NG == kAttnThreads, "float4 columns tile the block");
     __shared__ float wgt[G * kMaxSplits];
     __shared__ float4 acc4[kAttnThreads];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float* parts = a.part + ((size_t)b * a.hkv + kvh) * nsplit * REC;
     const int c = tid % NC, sg = tid / NC, h = 4 * c / HD;
     // evicted positions (three tiers with a Cool window): zero keys and

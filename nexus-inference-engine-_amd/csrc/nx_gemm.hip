@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const float* __restrict__ A, c
                                                   float* __restrict__ C, int M, int N, int K) {
     __shared__ float As[kGT][kGK + 1];
     __shared__ float Bs[kGK][kGT + 4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m0 = blockIdx.y * kGT, n0 = blockIdx.x * kGT;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     gf4 acc[2][2];

@@ -197,7 +197,7 @@ __device__ inline void stage_finish(const GemvArgs& a, int k0, int gc, StageRegs
         ss += __shfl_xor(ss, 8, kWave);
         ss += __shfl_xor(ss, 16, kWave);
         ss += __shfl_xor(ss, 32, kWave);
-        const int lane = tid & (kWave - 1), wave = tid >> 6;
+        const int lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (lane < kMfmaCols) red[wave][lane] = ss;
         __syncthreads();
         if (tid < kMfmaCols) {
@@ -440,7 +440,8 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void k_gemv_mfma(GemvArgs args, in
     if constexpr (EPI == E_SWIGLU) asm volatile("" ::"s"(args.act16), "s"(args.lda));
     if constexpr (EPI == E_ACC || EPI == E_F32) asm volatile("" ::"s"(args.y32), "s"(args.ldy));
     if constexpr (EPI == E_PART) asm volatile("" ::"s"(args.kpart), "s"(args.kpart_rows));
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, kq = lane >> 4;
     const int N = args.N, K = args.K;
     // E_PART: block x is row group x / kparts over K part x % kparts, groups

@@ -601,7 +601,7 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     // so a last partial round spreads over every block (CU) rather than
     // filling the first ones.  Requests past the wavefront's last tile
     // re-read that tile.
-    const int wid = (threadIdx.x >> 6) * rs.nb + block;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * rs.nb + block;
     const int NW = rs.nb * rs.wpb, T = (a.N + R - 1) / R;
     const int nt = wid < T ? (T - wid + NW - 1) / NW : 0;
     auto trow = [&](int k) { return (wid + min(k, max(nt - 1, 0)) * NW) * R; };

@@ -12,7 +12,7 @@ namespace {
 
 __device__ inline float block_sum256(float v, float* red) {
     v = wave_sum(v);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (lane == 0) red[wave] = v;
     __syncthreads();
     const float t = red[0] + red[1] + red[2] + red[3];
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(kNrThreads) void k_moe_norm_route(MoeArgs a) {
     // the arguments the prologue uses, requested in one round
     asm volatile("" ::"s"(a.h), "s"(a.wr), "s"(a.sr), "s"(a.d), "s"(a.batch), "s"(a.E), "s"(a.norm_w),
                  "s"(a.xn16), "s"(a.eps));
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6, b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6), b = blockIdx.x;
     const int d = a.d, B = a.batch, E = a.E, G = d / 32;
     const float* hb = a.h + (size_t)b * d;
     float hv[PER];

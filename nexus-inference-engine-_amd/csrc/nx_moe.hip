@@ -73,7 +73,7 @@ __global__ __launch_bounds__(kMoeThreads, 1) void k_moe_b1_gate_up(GemvArgs a, R
     __shared__ int sel[kMoeMaxTopK];
     __shared__ float sw[kMoeMaxTopK];
     asm volatile("" ::"s"(a.h32), "s"(a.norm_w), "s"(m.wr), "s"(m.sr), "s"(m.E), "s"(a.G), "s"(a.K));
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int E = m.E, G = a.G;
     // the grid row's tiles dealt to its wavefronts in turn (as the dense
     // batch-1 GEMV deals them)
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kMoeThreads, 1) void k_moe_b1_down_combine(GemvArgs
     __shared__ float s8[KS * kWave * GPL];
     __shared__ float ys[KS * kDcRows];
     asm volatile("" ::"s"(a.x16), "s"(a.W), "s"(a.S), "s"(ids), "s"(wts), "s"(a.G), "s"(a.K), "s"(a.N));
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slot = wave / WG, wj = wave % WG;
     const int n0 = blockIdx.x * rows_per_block, n1 = min(n0 + rows_per_block, a.N);
     // this wavefront's rows: a contiguous share of the block's

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gemm(PfGemmArgs a) {
     __shared__ __align__(16) uint16_t As[2][kPfBM * kPfAStride];
     __shared__ __align__(16) uint32_t Bs[2][kPfBN * kPfGPS * 4];  // [row][group][4 dwords]
     __shared__ uint16_t Ss[2][kPfBN * kPfGPS];                    // [row][group]
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, kq = lane >> 4;
     // XCD-aware tile order: the blocks of XCD x (block index % 8 == x) take
     // the column tiles [x nt / 8, (x + 1) nt / 8), all of one row tile before

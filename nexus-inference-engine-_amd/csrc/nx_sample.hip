@@ -71,7 +71,7 @@ __device__ inline int popc_below(unsigned long long m, int l) {
 // prefix; *incl the inclusive one, *total the sum.
 template <class T>
 __device__ inline T smp_block_scan(T v, T* wsum, T* incl, T* total) {
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
     T x = v;
     for (int o = 1; o < 64; o <<= 1) {
         const T y = __shfl_up(x, o, 64);
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kSmpPThreads) void k_sample_max(SampleArgs a) {
 __global__ __launch_bounds__(kSmpPThreads) void k_sample_exp(SampleArgs a) {
     __shared__ float wm[kSmpPWaves];
     __shared__ int wc[kSmpThr][kSmpPWaves];
-    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
     const float* lg = a.logits + (size_t)b * a.ldl;
     float* e = a.scratch + (size_t)b * a.V;
     float* pt = a.part + (size_t)b * kSmpPartFloats;
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kSmpPThreads) void k_sample_gather(SampleArgs a) {
     __shared__ int wsum[kSmpPWaves];
     __shared__ int pk[2];
     __shared__ float sm;
-    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int p = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
     if (!(a.top_k > 0 && a.top_k < a.V && a.top_k <= kSmpMaxK)) return;
     const float* e = a.scratch + (size_t)b * a.V;
     float* pt = a.part + (size_t)b * kSmpPartFloats;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
     __shared__ int cand_i[kSmpCand];
     __shared__ int ord[kSmpCand];
     __shared__ int tcnt[kSmpThr][kSmpWaves + 1];
-    const int b = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63, V = a.V;
+    const int b = blockIdx.x, tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, V = a.V;
     const float* e = a.scratch + (size_t)b * V;
     const int C = ((V + kSmpWaves - 1) / kSmpWaves + 63) / 64 * 64;
     const int c0 = min(w * C, V), c1 = min(c0 + C, V);
