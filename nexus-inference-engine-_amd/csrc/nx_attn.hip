@@ -882,10 +882,12 @@ __global__ __launch_bounds__(256) void k_tq_decode_pages(const uint8_t* kc4, con
 // start first.
 // KLO: K pages are fp16 hi (kpool) + lo (kpool_lo), a third product per step
 // (prefill over TurboQuant pages decoded for it).
+// hsub blocks share a kv head (grid row y = kvh * hsub + sub), each taking G
+// of its G * hsub query heads, sub * G + w.
 template <int G, int HD, bool KLO = false>
-__global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int P) {
+__global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int P, int hsub) {
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = lane >> 4, t = lane & 15;
-    const int kvh = blockIdx.y, h = kvh * G + w;
+    const int kvh = (int)blockIdx.y / hsub, h = kvh * G * hsub + ((int)blockIdx.y - kvh * hsub) * G + w;
     const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16;
     const int lastpos = p0 + min(q0 + 15, P - 1);
     const int npages = lastpos / kPage + 1;
@@ -1147,19 +1149,23 @@ hipError_t round_f16_launch(float* x, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
-// K hi + lo pages (kpool_lo) for head_dim 128 and at most 4 query heads per
-// kv head (with 8, the kernel's two wavefronts per SIMD cannot hold the lo
-// operands).
+// K hi + lo pages (kpool_lo) for head_dim 128: at most 4 query heads per
+// block (with 8, the kernel's two wavefronts per SIMD cannot hold the lo
+// operands), so 8 heads per kv head take two blocks of 4 that read the same
+// pages (the second block's reads meet the first's in the L2).
 template <int G, int HD>
 hipError_t attn_prefill_case(const AttnArgs& a, int p0, int P, dim3 grid, hipStream_t st) {
-    if constexpr (HD == 128 && G <= 4) {
+    if constexpr (HD == 128) {
         if (a.kpool_lo) {
-            hipLaunchKernelGGL((k_attn_prefill<G, HD, true>), grid, dim3(64 * G), 0, st, a, p0, P);
+            constexpr int GB = G <= 4 ? G : 4, HS = G / GB;
+            static_assert(GB * HS == G, "query heads per kv head split into blocks of at most 4");
+            hipLaunchKernelGGL((k_attn_prefill<GB, HD, true>), dim3(grid.x, grid.y * HS), dim3(64 * GB), 0, st, a,
+                               p0, P, HS);
             return hipGetLastError();
         }
     }
     if (a.kpool_lo) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_attn_prefill<G, HD>), grid, dim3(64 * G), 0, st, a, p0, P);
+    hipLaunchKernelGGL((k_attn_prefill<G, HD>), grid, dim3(64 * G), 0, st, a, p0, P, 1);
     return hipGetLastError();
 }
 

@@ -1012,13 +1012,12 @@ struct PrefillScratch {
 // last), so every query sees the stored (quantized) K and V of the positions
 // before it and of its own, as the decode steps would.
 // Models the batched prefill takes: dense or MoE, fp16 pages or TurboQuant
-// pages (the latter with at most 4 query heads per kv head).
+// pages.
 bool batched_prefill_ok(const nx_model* m) {
     const nx_model_config& c = m->c;
     // (256-long heads prefill one step per token: the causal prefill
     // attention holds heads of at most 128)
-    return m->prefill_batched && c.head_dim <= 128 &&
-           (c.kv_kind == 0 || (c.kv_kind == 1 && c.n_heads <= 4 * c.n_kv_heads));
+    return m->prefill_batched && c.head_dim <= 128 && (c.kv_kind == 0 || c.kv_kind == 1);
 }
 
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {

@@ -141,6 +141,26 @@ def test_batched_prefill_matches_token_steps(ctx, P, kind):
     assert_greedy_parity(tb, want, margins)
 
 
+def test_batched_prefill_turboquant_8_heads_per_kv(ctx):
+    """TurboQuant pages with 8 query heads per kv head (two kv heads; the
+    causal attention runs as two blocks of 4 heads per kv head over the same
+    decoded pages): batched and one-step prefill logits within the
+    TurboQuant bound of each other and of the oracle, and both give the
+    oracle's greedy tokens (ties aside)."""
+    cfg = dict(TQ, n_heads=16, n_kv_heads=2, seed=0x7A8)
+    script = [("prompt", oracle.prompt_tokens(cfg["seed"], 1, 40, cfg["vocab"])), ("decode", 7)]
+    want, margins = oracle_script(cfg, script)
+    ta, la, pa = gpu_script(ctx, cfg, script, True)
+    tb, lb, pb = gpu_script(ctx, cfg, script, False)
+    assert pa == pb == 40 + 6
+    e = rel_err(la[0], lb[0])
+    eo = max(rel_err(x[0], oracle_script.prompt_logits[0]) for x in (la, lb))
+    print(f"G=8 turboquant logits rel_err={e:.2e}, against the oracle {eo:.2e}")
+    assert e < LOGIT_TOL["turboquant"] and eo < LOGIT_TOL["turboquant"]
+    assert_greedy_parity(ta, want, margins)
+    assert_greedy_parity(tb, want, margins)
+
+
 @pytest.mark.parametrize("kind", sorted(KINDS))
 def test_batched_prefill_two_chunks_matches_oracle(ctx, kind):
     """A 2100-token prompt (two chunks of the batched path, the second
