@@ -376,15 +376,17 @@ typedef struct nx_model nx_model;
 nx_status nx_model_create(nx_ctx* ctx, const nx_model_config* cfg, nx_model** out);
 nx_status nx_model_destroy(nx_model* m);
 /* HybridModel::prefill (hybrid_model.cpp:604-644): run prompt [batch][P]
- * token by token; afterwards the greedy token of the last prompt position is
- * pending as the next input and written to next_tokens [batch] (optional). */
+ * (batched or token by token, nx_model_set_prefill); afterwards the greedy
+ * token of the last prompt position is pending as the next input and written
+ * to next_tokens [batch] (optional). */
 nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens);
-/* Prefill mode: 1 (default) = batched -- for dense models with fp16 pages
- * each sequence's prompt goes through every layer in chunks of up to 2048
- * tokens as int4-g32 GEMMs on the matrix cores, with causal attention over
- * the pages; 0 = one decode step per prompt token (the reference's
- * HybridModel::prefill loop, hybrid_model.cpp:604-644).  MoE and
- * TurboQuant-page models always prefill one token per step. */
+/* Prefill mode: 1 (default) = batched -- for dense and MoE models with fp16
+ * or TurboQuant pages and heads of at most 128, each sequence's prompt goes
+ * through every layer in chunks of up to 2048 tokens as int4-g32 GEMMs on
+ * the matrix cores (routed experts over their gathered tokens), with causal
+ * attention over the pages; 0 = one decode step per prompt token (the
+ * reference's HybridModel::prefill loop, hybrid_model.cpp:604-644).  Tiered
+ * pages and 256-long heads always prefill one token per step. */
 nx_status nx_model_set_prefill(nx_model* m, int batched);
 /* The configuration the model was created with. */
 nx_status nx_model_get_config(nx_model* m, nx_model_config* out);
