@@ -884,18 +884,27 @@ __global__ __launch_bounds__(256) void k_tq_decode_pages(const uint8_t* kc4, con
 // (prefill over TurboQuant pages decoded for it).
 // hsub blocks share a kv head (grid row y = kvh * hsub + sub), each taking G
 // of its G * hsub query heads, sub * G + w.
-template <int G, int HD, bool KLO = false>
+// TIER (tiered pages, with KLO): query tiles are page-aligned positions (the
+// first tile starts p0 % 16 queries before the prompt), so a tile's queries
+// share one cold boundary; pages before it come from the decoded TurboQuant
+// pools, the rest from the fp16 pages kpool_win / vpool_win (K lo zero).
+template <int G, int HD, bool KLO = false, bool TIER = false>
 __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int P, int hsub) {
+    static_assert(!TIER || KLO, "tiered prefill reads decoded TurboQuant pages as hi + lo");
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = lane >> 4, t = lane & 15;
     const int kvh = (int)blockIdx.y / hsub, h = kvh * G * hsub + ((int)blockIdx.y - kvh * hsub) * G + w;
-    const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16;
+    const int qoff = TIER ? p0 % kPage : 0;
+    const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * 16 - qoff;
+    const int qi = min(max(q0 + t, 0), P - 1);  // this lane's query (clamped into the prompt)
     const int lastpos = p0 + min(q0 + 15, P - 1);
     const int npages = lastpos / kPage + 1;
+    // the tile's cold boundary in pages (positions p0 + q0 .. + 15 share it)
+    const int bnd = TIER ? max(0, (p0 + q0 - a.hot_window) / kPage) : 0;
     // q as the B operand: column t = query q0 + t (clamped: columns past the
     // prompt repeat its last query and are not written), k = 8g + j
     h8_t qh[HD / 32], ql[HD / 32];
     {
-        const float* qsrc = a.q + ((size_t)min(q0 + t, P - 1) * a.hq + h) * HD + 8 * g;
+        const float* qsrc = a.q + ((size_t)qi * a.hq + h) * HD + 8 * g;
         float4 x[HD / 32][2];
 #pragma unroll
         for (int s = 0; s < HD / 32; ++s) {
@@ -914,7 +923,7 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
         }
     }
     const float scale = 1.0f / sqrtf((float)HD);
-    const int qpos = p0 + min(q0 + t, P - 1);
+    const int qpos = p0 + qi;
     float m = -__builtin_inff(), lsum = 0.0f;
     f4_t o[HD / 16];
 #pragma unroll
@@ -926,29 +935,41 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     auto valid_of = [&](int p) { return p < npages ? min(max(lastpos + 1 - kPage * p, 0), kPage) : 0; };
     PairRaw<HD> ra, rb;
     PairKlo<HD> la, lb;
-    // K lo of a pair (KLO), the same addresses in kpool_lo
+    // K lo of a pair (KLO), the same addresses in kpool_lo (TIER: pages from
+    // the boundary on read the zero page)
     auto load_lo = [&](PairKlo<HD>& r, int pa_, int pb_) {
         if constexpr (KLO) {
 #pragma unroll
             for (int pg = 0; pg < 2; ++pg) {
-                const int blk = pg ? (valid_of(pb_) > 0 ? blk_of(pb_) : blk_of(pa_)) : blk_of(pa_);
-                const size_t base = ((size_t)blk * a.hkv + kvh) * kPage * HD;
+                const int pp = pg && valid_of(pb_) > 0 ? pb_ : pa_;
+                const size_t base = ((size_t)blk_of(pp) * a.hkv + kvh) * kPage * HD;
+                const uint16_t* lo = TIER && pp >= bnd ? a.lo_zero : a.kpool_lo + base;
 #pragma unroll
                 for (int s = 0; s < HD / 32; ++s)
-                    r.k[pg][s] = *reinterpret_cast<const uint4*>(a.kpool_lo + base + (size_t)t * HD + 32 * s + 8 * g);
+                    r.k[pg][s] = *reinterpret_cast<const uint4*>(lo + (size_t)t * HD + 32 * s + 8 * g);
             }
         }
     };
+    auto load_p = [&](PairRaw<HD>& r, int pa_, int pb_) {
+        if constexpr (TIER) {
+            const bool wa = pa_ >= bnd, wb = pb_ >= bnd;
+            load_pair_from<HD>(r, wa ? a.kpool_win : a.kpool, wa ? a.vpool_win : a.vpool, blk_of(pa_),
+                               wb ? a.kpool_win : a.kpool, wb ? a.vpool_win : a.vpool, blk_of(pb_), valid_of(pb_),
+                               a.hkv, kvh, lane);
+        } else {
+            load_pair<HD>(r, a, blk_of(pa_), valid_of(pa_), blk_of(pb_), valid_of(pb_), kvh, lane);
+        }
+    };
     load_lo(la, 0, 1);
-    load_pair<HD>(ra, a, blk_of(0), valid_of(0), blk_of(1), valid_of(1), kvh, lane);
+    load_p(ra, 0, 1);
     for (int pa = 0; pa < npages; pa += 4) {
         load_lo(lb, pa + 2, pa + 3);
-        load_pair<HD>(rb, a, blk_of(pa + 2), valid_of(pa + 2), blk_of(pa + 3), valid_of(pa + 3), kvh, lane);
+        load_p(rb, pa + 2, pa + 3);
         pair_update<HD, true, KLO>(ra, qh, ql, scale, valid_of(pa), valid_of(pa + 1), m, lsum, o, lane, kPage * pa,
                                    kPage * (pa + 1), qpos, &la);
         if (pa + 2 >= npages) break;
         load_lo(la, pa + 4, pa + 5);
-        load_pair<HD>(ra, a, blk_of(pa + 4), valid_of(pa + 4), blk_of(pa + 5), valid_of(pa + 5), kvh, lane);
+        load_p(ra, pa + 4, pa + 5);
         pair_update<HD, true, KLO>(rb, qh, ql, scale, valid_of(pa + 2), valid_of(pa + 3), m, lsum, o, lane,
                                    kPage * (pa + 2), kPage * (pa + 3), qpos, &lb);
     }
@@ -960,7 +981,7 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     for (int i = 0; i < 4; ++i) {
         const float L = __shfl(lsum, 4 * g + i, 64);
         const int q = q0 + 4 * g + i;
-        if (q < P) {
+        if (q >= 0 && q < P) {
             uint16_t* out = a.out16 + ((size_t)q * a.hq + h) * HD + t;
 #pragma unroll
             for (int nt = 0; nt < HD / 16; ++nt) out[16 * nt] = f2h_bits(o[nt][i] / L);
@@ -1134,6 +1155,59 @@ __global__ __launch_bounds__(256) void k_round_f16(float* x, size_t n) {
         x[i] = h2f_bits(f2h_bits(x[i]));
 }
 
+// Batched prefill over tiered pages (pf_tier_rows_launch): one wavefront per
+// (position t in [lo, pe), K or V, kv head), lane l holding coordinates l
+// and l + 64 of the fp16 value -- from the window's ring page before pb,
+// from the chunk's row (rounded) after.  ring = 0: the value goes to the
+// fp16 page of the block table (vk / vv) and, below tq_hi, is encoded into
+// the TurboQuant page; ring = 1 (lo >= pb): it goes to the ring page.  (The
+// ring is written in a launch of its own: a long chunk's last pages share
+// ring slots with the pages before pb that the first launch reads.)
+__global__ __launch_bounds__(256) void k_pf_tier_rows(const float* kvrows, int pb, int lo, int pe, int tq_hi,
+                                                      int ring, int hkv, int b, const int32_t* bt,
+                                                      const int32_t* hot_bt, int max_blocks, uint16_t* ring_k,
+                                                      uint16_t* ring_v, uint16_t* vk, uint16_t* vv,
+                                                      const float* ksign, const float* vsign, uint8_t* kc4,
+                                                      uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3,
+                                                      uint16_t* vn) {
+    constexpr int HD = kTqD;
+    __shared__ uint8_t codes[4][128];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int v = blockIdx.x * 4 + wave;  // ((t - lo), kv, h)
+    const int t = lo + v / (2 * hkv), kv = (v / hkv) % 2, h = v % hkv;
+    if (t >= pe) return;
+    const int slot = t % kPage;
+    // K pages are token-major [16][128], V pages dimension-major [128][16]
+    auto at = [&](int d) { return kv ? (size_t)d * kPage + slot : (size_t)slot * HD + d; };
+    uint16_t* const rp = kv ? ring_v : ring_k;
+    const size_t rpage = ((size_t)hot_bt[(size_t)b * max_blocks + t / kPage] * hkv + h) * kPage * HD;
+    uint16_t x0, x1;
+    if (ring) {
+        const float* r = kvrows + ((size_t)(t - pb) * 2 + kv) * hkv * HD + (size_t)h * HD;
+        rp[rpage + at(lane)] = f2h_bits(r[lane]);
+        rp[rpage + at(lane + 64)] = f2h_bits(r[lane + 64]);
+        return;
+    }
+    if (t < pb) {
+        x0 = rp[rpage + at(lane)];
+        x1 = rp[rpage + at(lane + 64)];
+    } else {
+        const float* r = kvrows + ((size_t)(t - pb) * 2 + kv) * hkv * HD + (size_t)h * HD;
+        x0 = f2h_bits(r[lane]);
+        x1 = f2h_bits(r[lane + 64]);
+    }
+    const int blk = bt[(size_t)b * max_blocks + t / kPage];
+    uint16_t* const vp = kv ? vv : vk;
+    const size_t vpage = ((size_t)blk * hkv + h) * kPage * HD;
+    vp[vpage + at(lane)] = x0;
+    vp[vpage + at(lane + 64)] = x1;
+    if (t < tq_hi) {
+        const size_t dst = ((size_t)blk * hkv + h) * kPage + slot;
+        tq_encode_vals(h2f_bits(x0), h2f_bits(x1), kv ? vsign : ksign, (kv ? vc4 : kc4) + dst * 32,
+                       (kv ? vc3 : kc3) + dst * 24, (kv ? vn : kn) + dst, codes[wave]);
+    }
+}
+
 }  // namespace
 
 hipError_t put_hot_launch(const float* raw, int ctx, int cold, int hkv, int hd, int b, const int32_t* hot_bt,
@@ -1142,6 +1216,26 @@ hipError_t put_hot_launch(const float* raw, int ctx, int cold, int hkv, int hd, 
     hipLaunchKernelGGL(k_put_hot, dim3(256), dim3(256), 0, st, raw, ctx, cold, hkv, hd, b, hot_bt, max_blocks, kpool,
                        vpool, kv);
     return hipGetLastError();
+}
+
+hipError_t pf_tier_rows_launch(const float* kvrows, int pb, int lo, int pe, int tq_hi, int ring_lo, int hkv, int b,
+                               const int32_t* bt, const int32_t* hot_bt, int max_blocks, uint16_t* ring_k,
+                               uint16_t* ring_v, uint16_t* vk, uint16_t* vv, const float* ksign, const float* vsign,
+                               uint8_t* kc4, uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                               hipStream_t st) {
+    // the ring holds the positions before pb that are not yet TurboQuant
+    if (lo < 0 || lo > pb || pb > pe || tq_hi < lo || tq_hi > pe || ring_lo < pb || hkv < 1) return hipErrorInvalidValue;
+    for (int ring = 0; ring < 2; ++ring) {
+        const int from = ring ? ring_lo : lo;
+        const long nvec = (long)(pe - from) * 2 * hkv;
+        if (nvec <= 0) continue;
+        hipLaunchKernelGGL(k_pf_tier_rows, dim3((unsigned)((nvec + 3) / 4)), dim3(256), 0, st, kvrows, pb, from, pe,
+                           tq_hi, ring, hkv, b, bt, hot_bt, max_blocks, ring_k, ring_v, vk, vv, ksign, vsign, kc4, kc3,
+                           kn, vc4, vc3, vn);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t round_f16_launch(float* x, size_t n, hipStream_t st) {
@@ -1159,12 +1253,21 @@ hipError_t attn_prefill_case(const AttnArgs& a, int p0, int P, dim3 grid, hipStr
         if (a.kpool_lo) {
             constexpr int GB = G <= 4 ? G : 4, HS = G / GB;
             static_assert(GB * HS == G, "query heads per kv head split into blocks of at most 4");
+            if (a.kpool_win) {
+                // tiered pages: page-aligned query tiles, one more when the
+                // prompt starts inside a page
+                if (!a.vpool_win || !a.lo_zero || a.hot_window < kPage || a.hot_window % kPage)
+                    return hipErrorInvalidValue;
+                hipLaunchKernelGGL((k_attn_prefill<GB, HD, true, true>), dim3((P + p0 % kPage + 15) / 16, grid.y * HS),
+                                   dim3(64 * GB), 0, st, a, p0, P, HS);
+                return hipGetLastError();
+            }
             hipLaunchKernelGGL((k_attn_prefill<GB, HD, true>), dim3(grid.x, grid.y * HS), dim3(64 * GB), 0, st, a,
                                p0, P, HS);
             return hipGetLastError();
         }
     }
-    if (a.kpool_lo) return hipErrorInvalidValue;
+    if (a.kpool_lo || a.kpool_win) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_attn_prefill<G, HD>), grid, dim3(64 * G), 0, st, a, p0, P, 1);
     return hipGetLastError();
 }

@@ -185,6 +185,32 @@ __device__ inline void load_pair(PairRaw<HD>& r, const AttnArgs& a, int blka, in
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// load_pair with each page's pools given (ka / va for page a, kb / vb for
+// page b; wavefront-uniform choices): the tiered prefill reads a query
+// tile's pages before its cold boundary from the decoded TurboQuant pages
+// and the others from fp16 pages.  Page b with no valid token re-reads page a.
+template <int HD>
+__device__ inline void load_pair_from(PairRaw<HD>& r, const uint16_t* ka, const uint16_t* va, int blka,
+                                      const uint16_t* kb, const uint16_t* vb, int blkb, int nb, int hkv, int kvh,
+                                      int lane) {
+    const int g = lane >> 4, t = lane & 15;
+    const bool dup = nb <= 0;
+#pragma unroll
+    for (int pg = 0; pg < 2; ++pg) {
+        const int blk = pg && !dup ? blkb : blka;
+        const uint16_t* kp = pg && !dup ? kb : ka;
+        const uint16_t* vp = pg && !dup ? vb : va;
+        const size_t base = ((size_t)blk * hkv + kvh) * kPage * HD;
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)
+            r.k[pg][s] = *reinterpret_cast<const uint4*>(kp + base + (size_t)t * HD + 32 * s + 8 * g);
+#pragma unroll
+        for (int nt = 0; nt < HD / 16; ++nt)
+            r.v[nt][pg] = *reinterpret_cast<const uint2*>(vp + base + (size_t)(16 * nt + t) * kPage + 4 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // Fold one page pair into the wavefront's state: m (running max of head l%16),
 // lsum (this lane's share of the softmax denominator), O (C layout, rows =
 // heads 4(l/16) + i, columns = dims 16 nt + l%16).

@@ -116,6 +116,13 @@ struct AttnArgs {
     const uint16_t* kpool;     // fp16 pages
     const uint16_t* vpool;
     const uint16_t* kpool_lo;  // prefill over decoded TurboQuant pages: K - fp16(K), or nullptr
+    // prefill over tiered pages: fp16 pages (through block_table) of the
+    // positions from the first query tile's cold boundary on; a tile of 16
+    // queries (page-aligned positions) reads the pages before its cold
+    // boundary (16 floor((position - hot_window) / 16), clamped at 0) from
+    // kpool / vpool / kpool_lo (the decoded TurboQuant pages) and the rest
+    // from these, with K lo read from lo_zero (one page of zeros)
+    const uint16_t *kpool_win, *vpool_win, *lo_zero;
     // TurboQuant pages (head_dim 128)
     const uint8_t *kc4, *kc3, *vc4, *vc3;
     const uint16_t *kn, *vn;
@@ -282,6 +289,18 @@ hipError_t cool_encode_ctx_launch(const float* x, int p0, int n, int hkv, const 
 hipError_t tq_encode_rows_launch(const float* kvrows, int n, int p0, int hkv, const float* ksign, const float* vsign,
                                  uint8_t* kc4, uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
                                  const int32_t* bt, hipStream_t st);
+// Batched prefill over tiered pages, one layer and chunk of sequence b: the
+// fp16 K and V of positions [lo, pe) -- the window's ring pages (hot_bt)
+// before pb, the chunk's rows kvrows [pe - pb][2][hkv*128] rounded to fp16
+// from pb on -- into the fp16 pages vk / vv (block table bt), into the
+// TurboQuant pages for positions below tq_hi (encoded from those fp16 values,
+// as the decode step's compression encodes a page leaving the window), and
+// into the ring for positions from ring_lo (>= pb) on.
+hipError_t pf_tier_rows_launch(const float* kvrows, int pb, int lo, int pe, int tq_hi, int ring_lo, int hkv, int b,
+                               const int32_t* bt, const int32_t* hot_bt, int max_blocks, uint16_t* ring_k,
+                               uint16_t* ring_v, uint16_t* vk, uint16_t* vv, const float* ksign, const float* vsign,
+                               uint8_t* kc4, uint8_t* kc3, uint16_t* kn, uint8_t* vc4, uint8_t* vc3, uint16_t* vn,
+                               hipStream_t st);
 // Decode positions 0 .. npos - 1 of one sequence's TurboQuant pages into fp16
 // pages of the same blocks (K token-major, V dimension-major), K also as its
 // fp16 remainder klo (same layout).

@@ -1010,14 +1010,24 @@ struct PrefillScratch {
 // the chunk's K and V rows are encoded into the pages, and the attention runs
 // over the sequence's pages decoded to fp16 (positions up to the chunk's
 // last), so every query sees the stored (quantized) K and V of the positions
-// before it and of its own, as the decode steps would.
-// Models the batched prefill takes: dense or MoE, fp16 pages or TurboQuant
-// pages.
+// before it and of its own, as the decode steps would.  Tiered pages
+// (kv_kind 2, two tiers): per layer and chunk, the positions not yet
+// TurboQuant (the window's ring before the chunk, the chunk's rows rounded
+// to fp16) go to fp16 pages of the block table, those the decode steps up
+// to the chunk's last position would have compressed are encoded into the
+// TurboQuant pages, the window's last pages into the ring; the attention
+// reads each page-aligned query tile's pages before its cold boundary from
+// the decoded TurboQuant pages and the rest as fp16, as the decode step at
+// that position would.
+// Models the batched prefill takes: dense or MoE, fp16, TurboQuant or
+// two-tier tiered pages.
 bool batched_prefill_ok(const nx_model* m) {
     const nx_model_config& c = m->c;
     // (256-long heads prefill one step per token: the causal prefill
-    // attention holds heads of at most 128)
-    return m->prefill_batched && c.head_dim <= 128 && (c.kv_kind == 0 || c.kv_kind == 1);
+    // attention holds heads of at most 128; so do tiered pages with a Warm
+    // range, whose TurboQuant pages are a ring of their own)
+    return m->prefill_batched && c.head_dim <= 128 &&
+           (c.kv_kind == 0 || c.kv_kind == 1 || (c.kv_kind == 2 && c.warm_window == 0));
 }
 
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
@@ -1049,15 +1059,25 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
                   sc.get(&yg, (size_t)S * d) != hipSuccess))
         return fail(ctx, NX_ERR_OOM, "prefill: expert scratch for %d tokens", C);
     std::vector<int32_t> hcounts((size_t)2 * std::max(E, 1));
-    const bool tq = c.kv_kind == 1;
+    const bool tq = c.kv_kind == 1, tier = c.kv_kind == 2;
     float* kvrows = nullptr;
     uint16_t *k16 = nullptr, *k16lo = nullptr, *v16 = nullptr;  // decoded pages (every block of the pool)
-    if (tq) {
+    uint16_t *wk = nullptr, *wv = nullptr, *zlo = nullptr;      // tiered: fp16 pages, a page of zeros
+    if (tq || tier) {
         const size_t pool = (size_t)m->n_blocks * hkv * nx::kPage * hd;
         if (sc.get(&kvrows, (size_t)C * 2 * m->kvdim) != hipSuccess || sc.get(&k16, pool) != hipSuccess ||
             sc.get(&k16lo, pool) != hipSuccess || sc.get(&v16, pool) != hipSuccess)
             return fail(ctx, NX_ERR_OOM, "prefill: decoded pages");
+        if (tier) {
+            if (sc.get(&wk, pool) != hipSuccess || sc.get(&wv, pool) != hipSuccess ||
+                sc.get(&zlo, (size_t)nx::kPage * hd) != hipSuccess)
+                return fail(ctx, NX_ERR_OOM, "prefill: fp16 pages");
+            NX_HIP(ctx, hipMemsetAsync(zlo, 0, (size_t)nx::kPage * hd * sizeof(uint16_t), st));
+        }
     }
+    // tiered pages: positions that are TurboQuant once the positions before p
+    // are written (the pages the decode steps have compressed by then)
+    auto tq_upto = [&](int p) { return p >= c.hot_window ? nx::kPage * ((p - c.hot_window) / nx::kPage) : 0; };
     int last = 0;
     for (int done = 0; done < P; done += C) {
         const int n = std::min(C, P - done), pb = p0 + done;
@@ -1084,6 +1104,16 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             const int32_t* bt = m->block_table + (size_t)b * MB;
             NX_LAUNCH(m, nx::pf_rope_kv_launch(qkv, m->nqkv, n, pb, m->qdim, m->kvdim, hd, hkv, m->rope_cos, m->rope_sin,
                                                bt, ly.kpool, ly.vpool, q, st, kvrows));
+            if (tier) {
+                const int pe = pb + n, lo = tq_upto(pb), tq_hi = tq_upto(pe);
+                // the ring's pages at the chunk's end: the last hot_pages
+                const int ring_lo = std::max(pb, nx::kPage * ((pe - 1) / nx::kPage - m->hot_pages + 1));
+                NX_LAUNCH(m, nx::pf_tier_rows_launch(kvrows, pb, lo, pe, tq_hi, ring_lo, hkv, b, m->block_table, m->hot_bt,
+                                                     MB, ly.kpool, ly.vpool, wk, wv, ly.ksign, ly.vsign, ly.kc4, ly.kc3,
+                                                     ly.kn, ly.vc4, ly.vc3, ly.vn, st));
+                NX_LAUNCH(m, nx::tq_decode_pages_launch(ly.kc4, ly.kc3, ly.kn, ly.vc4, ly.vc3, ly.vn, ly.ksign,
+                                                        ly.vsign, bt, tq_hi, hkv, k16, v16, k16lo, st));
+            }
             if (tq) {
                 NX_LAUNCH(m, nx::tq_encode_rows_launch(kvrows, n, pb, hkv, ly.ksign, ly.vsign, ly.kc4, ly.kc3, ly.kn,
                                                        ly.vc4, ly.vc3, ly.vn, bt, st));
@@ -1092,9 +1122,15 @@ nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {
             }
             nx::AttnArgs at{};
             at.q = q;
-            at.kpool = tq ? k16 : ly.kpool;
-            at.vpool = tq ? v16 : ly.vpool;
-            at.kpool_lo = tq ? k16lo : nullptr;
+            at.kpool = tq || tier ? k16 : ly.kpool;
+            at.vpool = tq || tier ? v16 : ly.vpool;
+            at.kpool_lo = tq || tier ? k16lo : nullptr;
+            if (tier) {
+                at.kpool_win = wk;
+                at.vpool_win = wv;
+                at.lo_zero = zlo;
+                at.hot_window = c.hot_window;
+            }
             at.block_table = m->block_table + (size_t)b * MB;
             at.out16 = att;
             at.batch = 1;
