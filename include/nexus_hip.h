@@ -381,13 +381,12 @@ nx_status nx_model_destroy(nx_model* m);
  * to next_tokens [batch] (optional). */
 nx_status nx_model_prefill(nx_model* m, const int32_t* prompt, int P, int32_t* next_tokens);
 /* Prefill mode: 1 (default) = batched -- for dense and MoE models with fp16,
- * TurboQuant or tiered pages and heads of at most 128, each sequence's prompt goes
+ * TurboQuant or tiered pages, each sequence's prompt goes
  * through every layer in chunks of up to 2048 tokens as int4-g32 GEMMs on
  * the matrix cores (routed experts over their gathered tokens), with causal
  * attention over the pages; 0 = one decode step per prompt token (the
  * reference's HybridModel::prefill loop, hybrid_model.cpp:604-644).  Tiered
- * pages with a Warm range and 256-long heads always prefill one token per
- * step. */
+ * pages with a Warm range always prefill one token per step. */
 nx_status nx_model_set_prefill(nx_model* m, int batched);
 /* The configuration the model was created with. */
 nx_status nx_model_get_config(nx_model* m, nx_model_config* out);

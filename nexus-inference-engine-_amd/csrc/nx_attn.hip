@@ -928,50 +928,72 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(AttnArgs a, int p0, int
     f4_t o[HD / 16];
 #pragma unroll
     for (int nt = 0; nt < HD / 16; ++nt) o[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
-    // page pairs with the next pair in flight: it is requested unconditionally
-    // (pages past the walk re-read its last page with no valid tokens), so
-    // the wait for the current pair leaves the next one outstanding
-    auto blk_of = [&](int p) { return a.block_table[min(p, npages - 1)]; };
-    auto valid_of = [&](int p) { return p < npages ? min(max(lastpos + 1 - kPage * p, 0), kPage) : 0; };
-    PairRaw<HD> ra, rb;
-    PairKlo<HD> la, lb;
-    // K lo of a pair (KLO), the same addresses in kpool_lo (TIER: pages from
-    // the boundary on read the zero page)
-    auto load_lo = [&](PairKlo<HD>& r, int pa_, int pb_) {
-        if constexpr (KLO) {
+    if constexpr (HD > 128) {
+        // 256-long heads: each lane's q operands go to its own LDS slots and
+        // are read per k-step (registers hold one page pair, its products
+        // and O), one pair in flight
+        static_assert(!KLO, "256-long heads have fp16 pages only");
+        __shared__ __align__(16) uint4 qlds[G * kWave * (HD / 32) * 2];
+        uint4* qls = qlds + ((size_t)w * kWave + lane) * (HD / 32) * 2;
 #pragma unroll
-            for (int pg = 0; pg < 2; ++pg) {
-                const int pp = pg && valid_of(pb_) > 0 ? pb_ : pa_;
-                const size_t base = ((size_t)blk_of(pp) * a.hkv + kvh) * kPage * HD;
-                const uint16_t* lo = TIER && pp >= bnd ? a.lo_zero : a.kpool_lo + base;
+        for (int s = 0; s < HD / 32; ++s) {
+            qls[2 * s] = __builtin_bit_cast(uint4, qh[s]);
+            qls[2 * s + 1] = __builtin_bit_cast(uint4, ql[s]);
+        }
+        auto blk1 = [&](int p) { return a.block_table[min(p, npages - 1)]; };
+        auto valid1 = [&](int p) { return p < npages ? min(max(lastpos + 1 - kPage * p, 0), kPage) : 0; };
+        PairRaw<HD> r1;
+        for (int pa = 0; pa < npages; pa += 2) {
+            load_pair<HD>(r1, a, blk1(pa), valid1(pa), blk1(pa + 1), valid1(pa + 1), kvh, lane);
+            pair_update<HD, true, false, true>(r1, qh, ql, scale, valid1(pa), valid1(pa + 1), m, lsum, o, lane,
+                                               kPage * pa, kPage * (pa + 1), qpos, nullptr, qls);
+        }
+    } else {
+        // page pairs with the next pair in flight: it is requested unconditionally
+        // (pages past the walk re-read its last page with no valid tokens), so
+        // the wait for the current pair leaves the next one outstanding
+        auto blk_of = [&](int p) { return a.block_table[min(p, npages - 1)]; };
+        auto valid_of = [&](int p) { return p < npages ? min(max(lastpos + 1 - kPage * p, 0), kPage) : 0; };
+        PairRaw<HD> ra, rb;
+        PairKlo<HD> la, lb;
+        // K lo of a pair (KLO), the same addresses in kpool_lo (TIER: pages from
+        // the boundary on read the zero page)
+        auto load_lo = [&](PairKlo<HD>& r, int pa_, int pb_) {
+            if constexpr (KLO) {
 #pragma unroll
-                for (int s = 0; s < HD / 32; ++s)
-                    r.k[pg][s] = *reinterpret_cast<const uint4*>(lo + (size_t)t * HD + 32 * s + 8 * g);
+                for (int pg = 0; pg < 2; ++pg) {
+                    const int pp = pg && valid_of(pb_) > 0 ? pb_ : pa_;
+                    const size_t base = ((size_t)blk_of(pp) * a.hkv + kvh) * kPage * HD;
+                    const uint16_t* lo = TIER && pp >= bnd ? a.lo_zero : a.kpool_lo + base;
+#pragma unroll
+                    for (int s = 0; s < HD / 32; ++s)
+                        r.k[pg][s] = *reinterpret_cast<const uint4*>(lo + (size_t)t * HD + 32 * s + 8 * g);
+                }
             }
+        };
+        auto load_p = [&](PairRaw<HD>& r, int pa_, int pb_) {
+            if constexpr (TIER) {
+                const bool wa = pa_ >= bnd, wb = pb_ >= bnd;
+                load_pair_from<HD>(r, wa ? a.kpool_win : a.kpool, wa ? a.vpool_win : a.vpool, blk_of(pa_),
+                                   wb ? a.kpool_win : a.kpool, wb ? a.vpool_win : a.vpool, blk_of(pb_), valid_of(pb_),
+                                   a.hkv, kvh, lane);
+            } else {
+                load_pair<HD>(r, a, blk_of(pa_), valid_of(pa_), blk_of(pb_), valid_of(pb_), kvh, lane);
+            }
+        };
+        load_lo(la, 0, 1);
+        load_p(ra, 0, 1);
+        for (int pa = 0; pa < npages; pa += 4) {
+            load_lo(lb, pa + 2, pa + 3);
+            load_p(rb, pa + 2, pa + 3);
+            pair_update<HD, true, KLO>(ra, qh, ql, scale, valid_of(pa), valid_of(pa + 1), m, lsum, o, lane, kPage * pa,
+                                       kPage * (pa + 1), qpos, &la);
+            if (pa + 2 >= npages) break;
+            load_lo(la, pa + 4, pa + 5);
+            load_p(ra, pa + 4, pa + 5);
+            pair_update<HD, true, KLO>(rb, qh, ql, scale, valid_of(pa + 2), valid_of(pa + 3), m, lsum, o, lane,
+                                       kPage * (pa + 2), kPage * (pa + 3), qpos, &lb);
         }
-    };
-    auto load_p = [&](PairRaw<HD>& r, int pa_, int pb_) {
-        if constexpr (TIER) {
-            const bool wa = pa_ >= bnd, wb = pb_ >= bnd;
-            load_pair_from<HD>(r, wa ? a.kpool_win : a.kpool, wa ? a.vpool_win : a.vpool, blk_of(pa_),
-                               wb ? a.kpool_win : a.kpool, wb ? a.vpool_win : a.vpool, blk_of(pb_), valid_of(pb_),
-                               a.hkv, kvh, lane);
-        } else {
-            load_pair<HD>(r, a, blk_of(pa_), valid_of(pa_), blk_of(pb_), valid_of(pb_), kvh, lane);
-        }
-    };
-    load_lo(la, 0, 1);
-    load_p(ra, 0, 1);
-    for (int pa = 0; pa < npages; pa += 4) {
-        load_lo(lb, pa + 2, pa + 3);
-        load_p(rb, pa + 2, pa + 3);
-        pair_update<HD, true, KLO>(ra, qh, ql, scale, valid_of(pa), valid_of(pa + 1), m, lsum, o, lane, kPage * pa,
-                                   kPage * (pa + 1), qpos, &la);
-        if (pa + 2 >= npages) break;
-        load_lo(la, pa + 4, pa + 5);
-        load_p(ra, pa + 4, pa + 5);
-        pair_update<HD, true, KLO>(rb, qh, ql, scale, valid_of(pa + 2), valid_of(pa + 3), m, lsum, o, lane,
-                                   kPage * (pa + 2), kPage * (pa + 3), qpos, &lb);
     }
     // the query's denominator: sum of the four lanes that share its column
     lsum += __shfl_xor(lsum, 16, 64);
@@ -1286,6 +1308,10 @@ hipError_t attn_prefill_launch(const AttnArgs& a, int p0, int P, hipStream_t st)
     NX_PF_ATTN_CASE(2, 128)
     NX_PF_ATTN_CASE(4, 128)
     NX_PF_ATTN_CASE(8, 128)
+    NX_PF_ATTN_CASE(1, 256)
+    NX_PF_ATTN_CASE(2, 256)
+    NX_PF_ATTN_CASE(4, 256)
+    NX_PF_ATTN_CASE(8, 256)
 #undef NX_PF_ATTN_CASE
     return hipErrorInvalidValue;
 }

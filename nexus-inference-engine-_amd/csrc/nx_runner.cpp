@@ -1023,11 +1023,9 @@ struct PrefillScratch {
 // two-tier tiered pages.
 bool batched_prefill_ok(const nx_model* m) {
     const nx_model_config& c = m->c;
-    // (256-long heads prefill one step per token: the causal prefill
-    // attention holds heads of at most 128; so do tiered pages with a Warm
-    // range, whose TurboQuant pages are a ring of their own)
-    return m->prefill_batched && c.head_dim <= 128 &&
-           (c.kv_kind == 0 || c.kv_kind == 1 || (c.kv_kind == 2 && c.warm_window == 0));
+    // (tiered pages with a Warm range, whose TurboQuant pages are a ring of
+    // their own, prefill one step per token)
+    return m->prefill_batched && (c.kv_kind == 0 || c.kv_kind == 1 || (c.kv_kind == 2 && c.warm_window == 0));
 }
 
 nx_status prefill_batched(nx_model* m, int b, const int32_t* tokens, int P) {

@@ -171,7 +171,9 @@ QK = dict(qk_norm=1, norm_sigma=0.1)
     ("moe", {"n_experts": 4, "top_k": 2}, True),
     ("turboquant", {"n_heads": 4, "n_kv_heads": 1, "head_dim": 128, "d_model": 512, "kv_kind": 1}, True),
     ("tiered", {"n_heads": 4, "n_kv_heads": 2, "head_dim": 128, "d_model": 512, "kv_kind": 2, "hot_window": 16},
-     False),
+     True),
+    ("tiered-steps", {"n_heads": 4, "n_kv_heads": 2, "head_dim": 128, "d_model": 512, "kv_kind": 2,
+                      "hot_window": 16}, False),
     ("hd128-batch8", {"n_heads": 8, "n_kv_heads": 2, "head_dim": 128, "d_model": 512, "batch": 8}, True)])
 def test_qk_norm_parity(ctx, name, extra, batched):
     """Per-head Q/K RMSNorm (attn_q_norm / attn_k_norm, hybrid_model.cpp:

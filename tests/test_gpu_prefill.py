@@ -110,7 +110,9 @@ MOE = dict(TINY, n_experts=4, top_k=2)
 # after its first, so prompts of 40 tokens and more read TurboQuant pages;
 # two kv heads
 TIERED = dict(TQ, n_kv_heads=2, kv_kind=2, hot_window=16)
-KINDS = {"fp16": TINY, "turboquant": TQ, "moe": MOE, "tiered": TIERED}
+# 256-long heads: the causal attention reads q's operands from LDS
+HD256 = dict(TINY, n_heads=4, n_kv_heads=2, head_dim=256, d_model=512)
+KINDS = {"fp16": TINY, "turboquant": TQ, "moe": MOE, "tiered": TIERED, "hd256": HD256}
 # Logits of the two prefill paths: fp16 pages agree to rounding (1e-3).
 # TurboQuant pages quantize K and V, which reach the encoder through GEMM
 # (batched) or GEMV (one step per token) summation orders: a value at a
@@ -121,7 +123,7 @@ KINDS = {"fp16": TINY, "turboquant": TQ, "moe": MOE, "tiered": TIERED}
 # O(1), the stored pages are compared with the oracle's code by code in
 # test_batched_prefill_turboquant_pages_match_oracle, and the greedy tokens
 # with the oracle's in the tests here.
-LOGIT_TOL = {"fp16": 1e-3, "turboquant": 2e-2, "moe": 1e-3, "tiered": 2e-2}
+LOGIT_TOL = {"fp16": 1e-3, "turboquant": 2e-2, "moe": 1e-3, "tiered": 2e-2, "hd256": 1e-3}
 
 
 @pytest.mark.parametrize("kind", sorted(KINDS))
