@@ -274,6 +274,63 @@ def test_batched_prefill_turboquant_pages_match_oracle(ctx):
     om.close()
 
 
+def test_batched_prefill_tiered_pages_match_oracle(ctx):
+    """The tiered pages the batched prefill leaves (57 prompt tokens, a
+    16-position window, prompts at 0 and then at 57 after three decode
+    steps): the positions the decode steps would have compressed read back as
+    TurboQuant (at least 97% of their code bytes equal to the oracle's after
+    its token-by-token run, as in the TurboQuant test, norms within 1e-3),
+    the window's positions as fp16 from the ring: each position's vector
+    within 1e-2 of the oracle's, relative to its largest element (an RMSNorm
+    input that rounds one fp16 step apart moves some elements by up to 5e-4
+    on either prefill path; a stale or misplaced position differs by O(1))."""
+    cfg = dict(TIERED, max_seq=256, seed=0x7A2)
+    H = cfg["hot_window"]
+    p1 = oracle.prompt_tokens(cfg["seed"], 1, 57, cfg["vocab"])
+    p2 = oracle.prompt_tokens(cfg["seed"] + 1, 1, 30, cfg["vocab"])
+    gm = nexus_amd.Model(ctx, **cfg)
+    om = oracle.Model(**cfg)
+    gm.prefill(p1)
+    for i in range(p1.shape[1]):
+        lg = om.forward(np.ascontiguousarray(p1[:, i], np.int32))
+    # three decode steps fed the oracle's tokens on both sides, then a second
+    # prompt starting inside a page
+    fed = []
+    for _ in range(3):
+        t = lg.argmax(axis=1).astype(np.int32)
+        fed.append(t)
+        lg = om.forward(t)
+    gm.decode_forced(np.stack(fed, 1))
+    gm.prefill(p2)
+    for i in range(p2.shape[1]):
+        om.forward(np.ascontiguousarray(p2[:, i], np.int32))
+    end = 57 + 3 + 30
+    cold = 16 * ((end - H) // 16)  # TurboQuant below, the window's ring from here
+    for L in range(cfg["n_layers"]):
+        same = total = 0
+        for p in range(end):
+            for kv in (0, 1):
+                form, g = gm.kv_read(L, 0, p, kv)
+                if p < cold:
+                    w = om.kv_read(L, 0, p, kv, 1)
+                    assert form == 1 and g.size == w.size, (L, p, kv, form)
+                    for h in range(cfg["n_kv_heads"]):
+                        gh, wh = g[58 * h:58 * h + 58], w[58 * h:58 * h + 58]
+                        same += int(np.sum(gh[:56] == wh[:56]))
+                        total += 56
+                        gn, wn = float(gh[56:58].view(np.float16)[0]), float(wh[56:58].view(np.float16)[0])
+                        assert abs(gn - wn) <= 1e-3 * abs(wn), (L, p, kv, h)
+                else:
+                    w = om.kv_read(L, 0, p, kv, 0)
+                    assert form == 0 and g.size == w.size, (L, p, kv, form)
+                    gv, wv = g.view(np.float16).astype(np.float32), w.view(np.float16).astype(np.float32)
+                    assert rel_err(gv, wv) < 1e-2, (L, p, kv)
+        print(f"layer {L}: {same}/{total} TurboQuant code bytes equal")
+        assert same >= 0.97 * total
+    gm.close()
+    om.close()
+
+
 def test_batched_prefill_mixtral_layer_shape(ctx):
     """Two layers of the Mixtral shape (d 4096, 32/8 heads of 128, 8 experts
     of FFN 14336, top-2, vocab 32000), a 96-token prompt: the batched prefill
