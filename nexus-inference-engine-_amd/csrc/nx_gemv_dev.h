@@ -599,8 +599,8 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
     // ranges per wavefront, 2048 separate streams, were 7% slower on the
     // 28672 x 4096 gate/up).  Wavefront j of block b deals as w = j nb + b,
     // so a last partial round spreads over every block (CU) rather than
-    // filling the first ones.  Requests past the wavefront's last tile
-    // re-read that tile.
+    // filling the first ones.  Requests of a deeper ring past the
+    // wavefront's last tile re-read that tile.
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * rs.nb + block;
     const int NW = rs.nb * rs.wpb, T = (a.N + R - 1) / R;
     const int nt = wid < T ? (T - wid + NW - 1) / NW : 0;
@@ -656,7 +656,14 @@ __device__ inline void gemv_b1_run(const GemvArgs& a, const RowSplit& rs, int bl
                     tile_dot_lds<GPL, R>(t[j], sp, s8, a.G, lane, res);
                 else
                     tile_dot<GPL, R>(t[j], xp, res);
-                load_tile_u<GPL, R>(t[j], a.W, a.S, a.G, 0, a.N, trow(i + j + DEPTH), lane);
+                // the slot's next tile.  With a ring of one (QKV, wo and the
+                // down projection: one or two tiles per wavefront) nothing is
+                // requested past the wavefront's last tile: re-reading it was
+                // a second round trip before the wavefront could end (8B
+                // decode 690 -> 700 tok/s).  Deeper rings keep the request
+                // unconditional (the condition made gate/up slower).
+                if (DEPTH > 1 || i + j + DEPTH < nt)
+                    load_tile_u<GPL, R>(t[j], a.W, a.S, a.G, 0, a.N, trow(i + j + DEPTH), lane);
                 RopePre pre{};
                 if (EPI == E_QKV && rope_pre) {
                     const int u0 = (i + j) * PPT;  // the lane of the tile's first pair
