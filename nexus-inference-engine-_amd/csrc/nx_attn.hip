@@ -170,14 +170,19 @@ __device__ inline void attn_f16_run(const AttnArgs& a, int nsplit, int split, in
                                               0, 0, nullptr, qls);
         }
     } else if constexpr (PIPE) {
-        // every pair is requested unconditionally, so the wait for the
-        // current pair leaves the next one in flight
+        // the next pair is requested before the current one is used, so the
+        // wait for the current pair leaves the next one in flight; nothing is
+        // requested past the wavefront's last pair (a re-read of its first
+        // page there was a round trip before the record: batch-8 attention
+        // 31.5 -> 30.5 us)
         PairRaw<HD> rb;
         for (int i = 0; i < npw; i += 4) {
-            load_pair<HD>(rb, a, blk_or0(i + 2), valid_of(i + 2), blk_or0(i + 3), valid_of(i + 3), kvh, lane);
+            if (i + 2 < npw)
+                load_pair<HD>(rb, a, blk_or0(i + 2), valid_of(i + 2), blk_or0(i + 3), valid_of(i + 3), kvh, lane);
             pair_update<HD>(ra, qh, ql, scale, valid_of(i), valid_of(i + 1), m, lsum, o, lane);
             if (i + 2 >= npw) break;
-            load_pair<HD>(ra, a, blk_or0(i + 4), valid_of(i + 4), blk_or0(i + 5), valid_of(i + 5), kvh, lane);
+            if (i + 4 < npw)
+                load_pair<HD>(ra, a, blk_or0(i + 4), valid_of(i + 4), blk_or0(i + 5), valid_of(i + 5), kvh, lane);
             pair_update<HD>(rb, qh, ql, scale, valid_of(i + 2), valid_of(i + 3), m, lsum, o, lane);
         }
     } else {
@@ -548,10 +553,13 @@ __device__ inline void attn_tq_run(const AttnArgs& a, int nsplit, int pps, int s
     const float cb0 = te < kTqTbl4 ? c_tq_cb[te & 15] : c_tq_cb[16 + ((te - kTqTbl4) & 7)];
     const float cb1 = te < kTqTbl4 ? c_tq_cb[te >> 4] : c_tq_cb[16 + ((te - kTqTbl4) >> 3)];
     // page pair p (pages 2p, 2p + 1 of the wavefront); pairs past the
-    // wavefront's pages re-read its first page and are not processed
+    // wavefront's pages are not requested (the first pair always is: a
+    // wavefront with no pages re-reads its first page and processes nothing;
+    // re-reading it for every pair past the last cost 32K attention 0.5 us)
     auto blk_or0 = [&](int i) { return i < npw ? blk_of(i) : blk_of(0); };
     auto load_p = [&](TqPair& r, int p) {
-        tq_load_pair<COOL>(r, a, ln, blk_or0(2 * p), blk_or0(2 * p + 1), valid_of(2 * p + 1), kvh, lane);
+        if (p == 0 || 2 * p < npw)
+            tq_load_pair<COOL>(r, a, ln, blk_or0(2 * p), blk_or0(2 * p + 1), valid_of(2 * p + 1), kvh, lane);
     };
     TqPair r0, r1, r2;
     load_p(r0, 0);
