@@ -294,9 +294,9 @@ struct TqLane {
     }
 };
 
-// Every load is unconditional (see load_pair): page b with no valid token
-// re-reads page a (blka is a valid block); tokens past the valid counts are
-// masked when the pair is processed.
+// A page's loads have no per-lane condition (see load_pair): page b with no
+// valid token re-reads page a (blka is a valid block); tokens past the valid
+// counts are masked when the pair is processed.
 template <bool COOL = false>
 __device__ inline void tq_load_pair(TqPair& r, const AttnArgs& a, const TqLane& ln, int blka, int blkb,
                                     int nb, int kvh, int lane) {
