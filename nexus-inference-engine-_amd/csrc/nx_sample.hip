@@ -310,19 +310,24 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
         // count is at least k (they hold the top k: p orders as e), if that
         // count fits in LDS; otherwise a radix selection over all of p finds
         // exactly k
-        if (tid == 0) {
-            int pick = -1;
-            for (int j = 0; j < kSmpThr; ++j) {
-                int tot = 0;
+        if (w == 0) {
+            // lane j < kSmpThr: threshold j's exclusive prefix over the
+            // wavefronts and its total; D decreases with j, so the pick is
+            // the last threshold whose count reaches k (-2 if that count
+            // does not fit the candidate list, -1 if none reaches k)
+            int tot = 0;
+            if (l < kSmpThr) {
                 for (int q = 0; q < kSmpWaves; ++q) {
-                    const int c = tcnt[j][q];
-                    tcnt[j][q] = tot;  // exclusive prefix over wavefronts
+                    const int c = tcnt[l][q];
+                    tcnt[l][q] = tot;
                     tot += c;
                 }
-                tcnt[j][kSmpWaves] = tot;
-                if (tot >= a.top_k) pick = tot <= kSmpCand ? j : -2;  // D decreasing: the last fitting one
+                tcnt[l][kSmpWaves] = tot;
             }
-            wi[0][3] = pick;
+            const unsigned long long ok = __ballot(l < kSmpThr && tot >= a.top_k);
+            const int jm = ok ? 63 - __clzll(ok) : 0;
+            const int tj = __shfl(tot, jm, kWave);
+            if (l == 0) wi[0][3] = ok ? (tj <= kSmpCand ? jm : -2) : -1;
         }
         __syncthreads();
         int n = 0;
@@ -438,20 +443,38 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
                     }
                     __syncthreads();
                 }
-            if (tid == 0) {
+            // top-p: the running sum in sorted order by one wavefront (lane
+            // j holds entry j, read in order), then the entries past the cut
+            // are cleared by the block
+            if (w == 0) {
                 int cut = kk;
                 if (a.top_p < 1.0f) {
-                    float cum = 0.0f;
-                    for (int j = 0; j < kk; ++j) {
-                        cum += cand_p[ord[j]];
-                        if (cum > a.top_p) {
-                            cut = j + 1;
-                            break;
+                    if (kk <= kWave) {
+                        const float pv = l < kk ? cand_p[ord[l]] : 0.0f;
+                        float cum = 0.0f;
+                        for (int j = 0; j < kk; ++j) {
+                            cum += readlane_f(pv, j);
+                            if (cum > a.top_p) {
+                                cut = j + 1;
+                                break;
+                            }
+                        }
+                    } else {
+                        float cum = 0.0f;
+                        for (int j = 0; j < kk; ++j) {
+                            cum += cand_p[ord[j]];
+                            if (cum > a.top_p) {
+                                cut = j + 1;
+                                break;
+                            }
                         }
                     }
                 }
-                for (int j = cut; j < n; ++j) cand_p[ord[j]] = 0.0f;
+                if (l == 0) wi[0][0] = cut;
             }
+            __syncthreads();
+            const int cut = wi[0][0];
+            for (int j = cut + tid; j < n; j += kSmpThreads) cand_p[ord[j]] = 0.0f;
             __syncthreads();
         }
         // the kept entries (at most k) in index order, compacted in parallel
@@ -482,9 +505,15 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
                 }
         }
         __syncthreads();
-        if (tid == 0) {
+        // renormalization and draw by one wavefront, in index order (lane j
+        // holds kept entry j when there are at most 64, read in order)
+        if (w == 0) {
+            const bool lanes = ktot <= kWave;
+            const float pv = lanes && l < ktot ? cand_p[l] : 0.0f;
+            const int iv = lanes && l < ktot ? cand_i[l] : 0;
+            auto p_at = [&](int j) { return lanes ? readlane_f(pv, j) : cand_p[j]; };
             float sm = 0.0f;
-            for (int j = 0; j < ktot; ++j) sm += cand_p[j];
+            for (int j = 0; j < ktot; ++j) sm += p_at(j);
             int tok = V - 1;
             const float r = u * sm;
             if (sm <= 0.0f || r <= 0.0f) {
@@ -492,14 +521,14 @@ __global__ __launch_bounds__(kSmpThreads) void k_sample(SampleArgs a) {
             } else {
                 float cum = 0.0f;
                 for (int j = 0; j < ktot; ++j) {
-                    cum += cand_p[j];
+                    cum += p_at(j);
                     if (cum >= r) {
-                        tok = cand_i[j];
+                        tok = lanes ? __builtin_amdgcn_readlane(iv, j) : cand_i[j];
                         break;
                     }
                 }
             }
-            sel = tok;
+            if (l == 0) sel = tok;
         }
         __syncthreads();
     } else {
